@@ -1,0 +1,199 @@
+/*
+ * twilight_hip.h - C ABI of the MI355X (gfx950) sparse-decode KV path.
+ *
+ * One shared library, libtwilight_hip.so, built by hipcc for gfx950 and loaded
+ * with ctypes exactly as the reference loads its natives (raw pointers,
+ * int64 sizes, an opaque stream, an int status).  No torch types cross this
+ * boundary.  Every entry point:
+ *   - returns TW_OK (0) or a nonzero TW_E* status; the Python layer maps
+ *     TW_EINVAL / TW_ERANGE to ValueError and the rest to RuntimeError;
+ *   - enqueues work on `stream` (a hipStream_t, NULL = legacy default stream)
+ *     and never synchronizes it, unless the comment says otherwise;
+ *   - takes caller-allocated outputs.  Entry points that need scratch take a
+ *     `workspace` pointer whose size is given by the matching *_workspace_size
+ *     query; its arrival counters must be zero before the first call (the
+ *     library leaves them zero after every call, so a workspace is reusable,
+ *     but two calls sharing one workspace must not overlap in time).
+ *
+ * dtype codes: TW_DTYPE_F16, TW_DTYPE_BF16, TW_DTYPE_F32 (key/value/metadata
+ * storage); queries for scoring are always fp32, as in the reference.
+ *
+ * Reference paths below are relative to source/headinfer/headinfer/ unless
+ * they start with scripts/.
+ */
+#ifndef TWILIGHT_HIP_H
+#define TWILIGHT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum tw_status {
+  TW_OK = 0,
+  TW_EINVAL = 1,      /* bad shape, dtype, pointer or flag */
+  TW_ERANGE = 2,      /* an index is outside its source (gather natives) */
+  TW_ENOMEM = 3,      /* workspace too small */
+  TW_EHIP = 4,        /* HIP runtime error; see tw_last_hip_error() */
+  TW_EUNSUPPORTED = 5 /* valid request this build does not implement */
+};
+
+enum tw_dtype { TW_DTYPE_F16 = 0, TW_DTYPE_BF16 = 1, TW_DTYPE_F32 = 2 };
+
+/* Human-readable status text; never NULL. */
+const char* tw_status_string(int status);
+/* The hipError_t recorded by the most recent TW_EHIP return (0 if none). */
+int tw_last_hip_error(void);
+/* Library version, (major << 16) | minor. */
+int tw_version(void);
+
+/* ------------------------------------------------------------------------
+ * a2 + a3: prompt metadata, one launch for n_entries KV heads.
+ * Replaces QuestTopKOffloadedCache._build_metadata
+ * (quest_offload_cache.py:276-289: per-page amin/amax over rows
+ * [sink + p*bs, sink + (p+1)*bs), complete pages only) and the Twilight
+ * override (twilight_offload_cache.py:925-936) calling affine_int4_pack
+ * (twilight_offload_cache.py:25-37).
+ *   keys      [n_entries][key_entry_stride] elements, row t of entry e at
+ *             keys + e*key_entry_stride + t*D; rows 0..T-1 are read.
+ *   page_min/page_max (nullable together) [n_entries][page_entry_stride]
+ *             elements, page p at + p*D; pages = T > sink ? (T-sink)/bs : 0.
+ *   packed/scale/minimum (nullable together): packed u8 [..][T][D/2] with
+ *             quant_entry_stride rows per entry (row t at + t*D/2), scale and
+ *             minimum [..][quant_entry_stride] in the key dtype.
+ * min/max use the IEEE total order (-0 < +0); a NaN anywhere in the reduced
+ * set yields the dtype's canonical NaN.  INT4 codes: low nibble = channel 2j,
+ * a NaN code is stored as 0.  D must be even and <= 1024.
+ * ---------------------------------------------------------------------- */
+int tw_build_page_metadata(const void* keys, int64_t key_entry_stride, int n_entries, int T, int D,
+                           int dtype, int sink, int block_size, void* page_min, void* page_max,
+                           int64_t page_entry_stride, void* packed, void* scale, void* minimum,
+                           int64_t quant_entry_stride, void* stream);
+
+/* a4: affine_int4_dequantize (twilight_offload_cache.py:40-47):
+ * out[n][d] = f32(code)*f32(scale[n]) + f32(minimum[n]) (mul, then add). */
+int tw_int4_dequantize(const void* packed, const void* scale, const void* minimum, int dtype,
+                       int64_t N, int D, float* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * a6: fused_quest_score (twilight_fused_quest.py:35-46 / _score :12-32).
+ *   q [G][R][D] fp32; page_min/page_max: group g page p at
+ *   + g*page_group_stride + p*D; out [G][R][P] fp32.
+ * score = sum_d f32(q_d > 0 ? max_d : min_d) * q_d in the reference order:
+ * 32 accumulators (d mod 32) filled chunk by chunk, then an adjacent-pair
+ * tree; no fused multiply-add.  Bit-exact for D = 128; the same order
+ * generalises to any D <= 256.
+ * ---------------------------------------------------------------------- */
+int tw_quest_score(const float* q, const void* page_min, const void* page_max, int dtype, int G,
+                   int R, int P, int D, int64_t page_group_stride, float* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * a5: torch.topk(scores, k, sorted=False).indices.sort()
+ * (quest_offload_cache.py:373-374, twilight_offload_cache.py:1153).
+ * scores [rows][P] fp32 (row stride score_row_stride) -> out [rows][k] int64
+ * ascending page ids.  Ties go to the lowest index, NaN ranks highest, -0
+ * equals +0.  1 <= k <= P.
+ * ---------------------------------------------------------------------- */
+int tw_topk_sorted(const float* scores, int rows, int P, int64_t score_row_stride, int k,
+                   int64_t* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused Quest selection for one decoder layer: score + top-k + GQA row
+ * plan, one launch.  Covers prepare_layer_selection
+ * (quest_offload_cache.py:299-401) followed by _selected_positions
+ * (:403-511) for the G entries of a layer, and the Twilight stage-1 B0
+ * selection (twilight_offload_cache.py:1128-1166).
+ *   q [G][R][D] fp32; metadata as in tw_quest_score; P pages scored.
+ *   scores (nullable) [G][R][P] fp32 output; when NULL the workspace holds
+ *   them.
+ *   sel_pages (nullable) [G][R][k] int32 ascending page ids.
+ *   Row plan (nullable rows): for group g, rows[g*rows_stride + i] lists
+ *   token positions  [0,sink_end) ++ (sink + p*bs + [0,bs)) for every page p
+ *   selected by any of the R heads, ascending ++ [recent_start, length),
+ *   then, if append_position >= 0, append_position itself.  row_masks
+ *   (nullable) gets the bitmask of heads that see each row (pages: heads
+ *   that selected them; all other rows: all heads).  row_counts[g] gets the
+ *   number of rows.
+ *   Window: sink_end = min(sink, length); recent_start = max(sink_end,
+ *   length - max(0, recent - 1))  (quest_offload_cache.py:330-332).
+ * R <= 8 when rows/row_masks are requested.
+ * ---------------------------------------------------------------------- */
+size_t tw_quest_select_workspace_size(int G, int R, int P);
+int tw_quest_select(const float* q, const void* page_min, const void* page_max, int dtype, int G,
+                    int R, int P, int D, int64_t page_group_stride, int k, float* scores,
+                    int32_t* sel_pages, int32_t* rows, uint8_t* row_masks, int32_t* row_counts,
+                    int64_t rows_stride, int sink, int recent, int block_size, int length,
+                    int append_position, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * a22: sparse GQA decode attention, split-K over selected rows, one query
+ * token per group.  Replaces _flash_attention_varlen_forward
+ * (mp.py:21-52) on the decode paths that call it (GQA group branch
+ * mp.py:239-279, layer-flat branch :283-321, per-head reference :424-452).
+ *
+ * Group g (G = B * Hk sequences x KV heads) attends with its R query heads
+ *   q[g][r][0..D)                       (dtype, contiguous [G][R][D])
+ * over its rows.  Two row modes:
+ *   rows != NULL (indexed): row i of group g is position rows[g*rows_stride+i]
+ *     of entry g, i.e. k_base + (g*entry_stride_rows + pos) * D, for
+ *     i < row_counts[g]; optional row_masks drop heads per row.
+ *   rows == NULL (varlen): cu_seqlens_k[B+1] (int32, device) delimits
+ *     sequence b = g / Hk; row i of group g is
+ *     k_base + (cu_seqlens_k[b] + i) * (Hk*D) + (g % Hk) * D.
+ *     window_left >= 0 keeps only the last window_left+1 keys
+ *     (flash-attn window_size=(w,w) at q_len 1).
+ * cur_k/cur_v (nullable, [G][D]): one extra key/value appended after the
+ * rows of each group (the decode token).
+ * softmax_scale multiplies q.k; out [G][R][D] in dtype.  k_base/v_base may
+ * point at HBM or at mapped pinned host memory.  max_rows bounds every
+ * group's row count and sizes the grid.
+ * ---------------------------------------------------------------------- */
+size_t tw_decode_attention_workspace_size(int G, int R, int D, int max_rows);
+int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G,
+                        int R, int D, const int32_t* rows, const uint8_t* row_masks,
+                        const int32_t* row_counts, int64_t rows_stride, int64_t entry_stride_rows,
+                        const int32_t* cu_seqlens_k, int Hk, int window_left, int max_rows,
+                        const void* cur_k, const void* cur_v, float softmax_scale, void* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * a14-a16 / a18: head-wise K/V row gather into the attention layout.
+ * Replaces the CPU index_select + H2D of update / update_layer_flat_ragged /
+ * update_layer_gqa_group_ragged (quest_offload_cache.py:576-624,816-936;
+ * twilight_offload_cache.py:2973-3101) and the mapped-host assembly kernel
+ * launch_resident_zero_copy (resident_zero_copy.cu:44-65).
+ *   src_k/src_v: row r at + r*D (HBM, or the device alias of mapped pinned
+ *   host memory returned by tw_host_device_pointer).
+ *   src_rows [n] int64 source rows (absolute, i.e. entry*Lmax + pos);
+ *   dst_rows (nullable) [n] int64 destination rows (NULL: dst row = i).
+ *   Rows outside [0, src_row_limit) are not read; the call then still
+ *   completes and sets *error_flag (device int32, nullable) to 1.
+ * Bit-exact copies.
+ * ---------------------------------------------------------------------- */
+int tw_gather_rows(const void* src_k, const void* src_v, int64_t src_row_limit,
+                   const int64_t* src_rows, const int64_t* dst_rows, int64_t n, int D,
+                   int elem_bytes, void* dst_k, void* dst_v, int32_t* error_flag, void* stream);
+
+/* Device address of pinned host memory allocated by hipHostMalloc (torch
+ * pin_memory=True); replaces cudaHostGetDevicePointer in
+ * resident_zero_copy.py:149-163. */
+int tw_host_device_pointer(void* host_ptr, void** device_ptr);
+
+/* ------------------------------------------------------------------------
+ * a20/a21: per-step append of the decode token.  Replaces _schedule_d2h
+ * (quest_offload_cache.py:230-274) and the token-batched new-KV D2H
+ * (twilight_offload_cache.py:551-794).  For each of n_entries entries,
+ * row `position` of entry (first_entry + i) in dst_k/dst_v ([E][Lmax][D],
+ * HBM or mapped pinned host) receives new_k[i]/new_v[i] ([n][D]).
+ * ---------------------------------------------------------------------- */
+int tw_append_kv(const void* new_k, const void* new_v, int n_entries, int D, int elem_bytes,
+                 void* dst_k, void* dst_v, int64_t entry_stride_rows, int first_entry,
+                 int64_t position, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TWILIGHT_HIP_H */

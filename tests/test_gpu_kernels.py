@@ -1,0 +1,316 @@
+"""GPU parity of the first-layer kernels against the CPU oracle.
+
+Bit-exact: page metadata, INT4 pack, Quest scores (reference order), top-k
+page ids (ties -> lowest index), the fused row plan, row gather (HBM and
+zero-copy pinned host) and append.  Attention: within 2e-3 abs + 1e-2 rel of
+a float64 reference.  All calls go through the C ABI via headinfer.kernels.
+"""
+
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import TORCH_DT, from_bits, minmax_pages, randn, same_bits, to_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def K():
+    from headinfer import kernels
+
+    return kernels
+
+
+# ------------------------------------------------------------ metadata
+META_CASES = [
+    ("f16", 4103, 128, 64, 16),
+    ("bf16", 4103, 128, 64, 16),
+    ("f32", 1030, 128, 64, 16),
+    ("bf16", 16, 4, 1, 1),
+    ("f16", 63, 128, 64, 16),
+    ("bf16", 200, 256, 5, 7),
+    ("f16", 100, 6, 3, 4),
+]
+
+
+@pytest.mark.parametrize("dtype,T,D,sink,bs", META_CASES)
+def test_page_metadata_bit_exact(K, dev, dtype, T, D, sink, bs):
+    _say(f"[metadata] {dtype} T={T} D={D} sink={sink} bs={bs}")
+    keys = randn((T, D), dtype, seed=T + D)
+    keys[min(3, T - 1)] = 0.5  # constant row (scale clamps; fp16 scale underflows)
+    if T > 10:
+        keys[7, 1] = float("nan")
+        keys[9, :] = -0.0
+        keys[9, 2] = 0.0
+    P = (T - sink) // bs if T > sink else 0
+    kd = keys.to(dev)
+    pmin = torch.empty((max(P, 1), D), dtype=keys.dtype, device=dev)
+    pmax = torch.empty_like(pmin)
+    packed = torch.empty((T, D // 2), dtype=torch.uint8, device=dev)
+    scale = torch.empty((T,), dtype=keys.dtype, device=dev)
+    minimum = torch.empty_like(scale)
+    K.build_page_metadata(kd, sink=sink, block_size=bs, page_min=pmin, page_max=pmax, packed=packed, scale=scale,
+                          minimum=minimum)
+    torch.cuda.synchronize()
+    omin, omax, opk, osc, omn = oracle.build_page_metadata(to_bits(keys), dtype, sink, bs)
+    assert np.array_equal(packed.cpu().numpy(), opk)
+    assert same_bits(scale, from_bits(osc, dtype))
+    assert same_bits(minimum, from_bits(omn, dtype))
+    if P:
+        assert same_bits(pmin[:P], from_bits(omin, dtype))
+        assert same_bits(pmax[:P], from_bits(omax, dtype))
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+def test_int4_round_trip_bound(K, dev, dtype):
+    """scripts/test_twilight_offload_cache_v1.py:82-89 on the GPU path."""
+    keys = randn((17, 128), dtype, seed=7)
+    packed, scale, minimum = K.affine_int4_pack(keys.to(dev))
+    restored = K.affine_int4_dequantize(packed, scale, minimum)
+    assert packed.shape == (17, 64) and restored.shape == (17, 128)
+    err = (restored.cpu() - keys.float()).abs().amax(dim=-1)
+    assert torch.isfinite(restored).all()
+    assert torch.all(err <= scale.cpu().float() / 2 + 1e-6)
+    odq = oracle.int4_dequantize(packed.cpu().numpy(), to_bits(scale), to_bits(minimum), dtype)
+    assert np.array_equal(restored.cpu().numpy().view(np.uint32), odq.view(np.uint32))
+
+
+# --------------------------------------------------------- Quest score
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("pages", [17, 186, 465, 1000, 2025, 2048])
+def test_quest_score_and_topk_bit_exact(K, dev, dtype, pages):
+    """Cases of scripts/test_twilight_fused_quest_v1.py:11-25 (seed 20260911)."""
+    _say(f"[quest] {dtype} pages={pages}")
+    g = torch.Generator().manual_seed(20260911 + pages)
+    for kind in ("bf16", "fp32", "exponents"):
+        q = torch.randn((8, 3, 128), generator=g)
+        if kind == "bf16":
+            q = q.bfloat16().float()
+        if kind == "exponents":
+            q = q * torch.exp2(torch.randint(-12, 12, q.shape, generator=g).float())
+        lo, hi = minmax_pages(dtype, 8, pages, 128, seed=pages * 3 + len(kind))
+        got = K.fused_quest_score(q.to(dev), lo.to(dev), hi.to(dev))
+        ref = oracle.quest_score(q.numpy(), to_bits(lo), to_bits(hi), dtype)
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32)), kind
+        k = min(pages, 512)
+        idx = K.topk_sorted(got, k)
+        assert np.array_equal(idx.cpu().numpy(), oracle.topk_sorted(ref, k)), kind
+
+
+@pytest.mark.parametrize("value", [0.0, 1.0, -1.0])
+def test_quest_score_tie_cases(K, dev, value):
+    """scripts/test_twilight_fused_quest_v1.py:26-34: constant q, lo=-2, hi=1."""
+    q = torch.full((8, 3, 128), value)
+    lo = torch.full((8, 513, 128), -2.0, dtype=torch.bfloat16)
+    hi = torch.ones_like(lo)
+    got = K.fused_quest_score(q.to(dev), lo.to(dev), hi.to(dev))
+    ref = oracle.quest_score(q.numpy(), to_bits(lo), to_bits(hi), "bf16")
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    idx = K.topk_sorted(got, 512)
+    assert np.array_equal(idx.cpu().numpy(), np.broadcast_to(np.arange(512), (8, 3, 512)))
+
+
+def test_topk_ties_nan_negzero(K, dev):
+    g = torch.Generator().manual_seed(5)
+    s = torch.randint(-3, 4, (16, 1000), generator=g).float()
+    s[0, 10] = float("nan")
+    s[1, :] = 0.0
+    s[1, ::3] = -0.0
+    s[2, :] = float("-inf")
+    s[3, 500:] = float("inf")
+    for k in (1, 7, 64, 999, 1000):
+        got = K.topk_sorted(s.to(dev), k)
+        assert np.array_equal(got.cpu().numpy(), oracle.topk_sorted(s.numpy(), k)), k
+
+
+# ------------------------------------------------------ fused selection
+@pytest.mark.parametrize(
+    "dtype,G,R,L,sink,recent,bs,frac",
+    [
+        ("f16", 8, 4, 4096, 64, 256, 16, 0.0625),   # 4K-context layer, k = 16 pages
+        ("f16", 8, 4, 32768, 64, 256, 16, 0.0625),  # 32K-context layer, k = 128 pages
+        ("bf16", 4, 7, 20000, 64, 256, 16, 0.05),
+        ("bf16", 2, 3, 16, 1, 2, 1, 0.5),
+        ("f32", 3, 8, 1000, 10, 20, 8, 0.2),
+    ],
+)
+def test_quest_select_row_plan(K, dev, dtype, G, R, L, sink, recent, bs, frac):
+    _say(f"[quest_select] {dtype} G={G} R={R} L={L}")
+    D = 128 if L > 16 else 4
+    cand, k = oracle.quest_budget(L, sink, recent, bs, frac, (L - sink) // bs)
+    P = cand
+    lo, hi = minmax_pages(dtype, G, P, D, seed=L)
+    q = randn((G, R, D), "f32", seed=L + 1)
+    stride = L + 1
+    rows = torch.full((G, stride), -7, dtype=torch.int32, device=dev)
+    masks = torch.zeros((G, stride), dtype=torch.uint8, device=dev)
+    counts = torch.zeros((G,), dtype=torch.int32, device=dev)
+    sel = torch.empty((G, R, k), dtype=torch.int32, device=dev)
+    scores = torch.empty((G, R, P), dtype=torch.float32, device=dev)
+    for it in range(2):  # twice: the arrival counters must be reset by the kernel
+        K.quest_select(q.to(dev), lo.to(dev), hi.to(dev), k, scores=scores, sel_pages=sel, rows=rows,
+                       row_masks=masks, row_counts=counts, sink=sink, recent=recent, block_size=bs, length=L,
+                       append_position=L)
+        torch.cuda.synchronize()
+    ref_scores = oracle.quest_score(q.numpy(), to_bits(lo), to_bits(hi), dtype)
+    assert np.array_equal(scores.cpu().numpy().view(np.uint32), ref_scores.view(np.uint32))
+    ref_sel = oracle.topk_sorted(ref_scores, k)
+    assert np.array_equal(sel.cpu().numpy(), ref_sel)
+    for g in range(G):
+        r_rows, r_masks = oracle.quest_row_plan(ref_sel[g], P, sink, recent, bs, L, L)
+        n = int(counts[g])
+        assert n == len(r_rows)
+        assert np.array_equal(rows[g, :n].cpu().numpy(), r_rows)
+        assert np.array_equal(masks[g, :n].cpu().numpy(), r_masks)
+
+
+# ------------------------------------------------------------ attention
+def _attn_ref(q, kc, vc, rows, masks, cur_k, cur_v, scale):
+    out = []
+    for g in range(q.shape[0]):
+        keys = kc[g][rows[g]].float().numpy()
+        vals = vc[g][rows[g]].float().numpy()
+        m = masks[g] if masks is not None else None
+        if cur_k is not None:
+            keys = np.concatenate([keys, cur_k[g : g + 1].float().numpy()])
+            vals = np.concatenate([vals, cur_v[g : g + 1].float().numpy()])
+            if m is not None:
+                m = np.concatenate([m, np.array([255], np.uint8)])
+        out.append(oracle.decode_attention(q[g].float().numpy(), keys, vals, scale, m))
+    return np.stack(out)
+
+
+def _close(got, ref, atol=2e-3, rtol=1e-2):
+    got = got.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref)
+    ok = err <= atol + rtol * np.abs(ref)
+    assert ok.all(), f"max abs err {err.max():.3e}"
+
+
+@pytest.mark.parametrize(
+    "dtype,G,R,D,L,n_rows,masked,cur",
+    [
+        ("f16", 8, 4, 128, 32768, 2368, True, True),
+        ("bf16", 8, 4, 128, 32768, 8512, False, True),
+        ("bf16", 4, 7, 128, 5000, 700, True, True),
+        ("f16", 2, 1, 64, 3000, 333, False, False),
+        ("f32", 3, 8, 128, 2000, 1000, True, True),
+        ("bf16", 2, 3, 4, 32, 9, True, True),
+        ("f16", 2, 2, 256, 1000, 129, False, True),
+    ],
+)
+def test_decode_attention_rows(K, dev, dtype, G, R, D, L, n_rows, masked, cur):
+    _say(f"[attention rows] {dtype} G={G} R={R} D={D} rows={n_rows}")
+    g0 = torch.Generator().manual_seed(L + n_rows)
+    kc = randn((G, L, D), dtype, seed=1)
+    vc = randn((G, L, D), dtype, seed=2)
+    q = randn((G, R, D), dtype, seed=3)
+    rows = torch.stack([torch.randperm(L, generator=g0)[:n_rows].sort().values for _ in range(G)]).to(torch.int32)
+    counts = torch.tensor([n_rows - 5 * g if n_rows > 5 * G else n_rows for g in range(G)], dtype=torch.int32)
+    masks = None
+    if masked:
+        masks = torch.randint(0, 1 << R, (G, n_rows), generator=g0).to(torch.uint8)
+        masks[:, -1] = (1 << R) - 1  # each head sees at least one row
+    ck = randn((G, D), dtype, seed=4) if cur else None
+    cv = randn((G, D), dtype, seed=5) if cur else None
+    scale = 1.0 / math.sqrt(D)
+    out = K.decode_attention_rows(q.to(dev), kc.to(dev), vc.to(dev), rows.to(dev), counts.to(dev), n_rows,
+                                  row_masks=None if masks is None else masks.to(dev),
+                                  cur_k=None if ck is None else ck.to(dev), cur_v=None if cv is None else cv.to(dev))
+    torch.cuda.synchronize()
+    ref_rows = [rows[g, : int(counts[g])].long().numpy() for g in range(G)]
+    ref_masks = None if masks is None else [masks[g, : int(counts[g])].numpy() for g in range(G)]
+    ref = _attn_ref(q, kc, vc, ref_rows, ref_masks, ck, cv, scale)
+    _close(out, ref)
+
+
+@pytest.mark.parametrize("dtype,B,Hk,R,D", [("bf16", 8, 1, 4, 128), ("f16", 3, 2, 3, 128), ("bf16", 5, 1, 1, 4)])
+def test_decode_attention_varlen(K, dev, dtype, B, Hk, R, D):
+    _say(f"[attention varlen] {dtype} B={B} Hk={Hk} R={R} D={D}")
+    g0 = torch.Generator().manual_seed(B * 100 + D)
+    lens = torch.randint(1, 3000 if D > 4 else 40, (B,), generator=g0)
+    cu = torch.zeros(B + 1, dtype=torch.int32)
+    cu[1:] = lens.cumsum(0)
+    total = int(cu[-1])
+    k = randn((total, Hk, D), dtype, seed=11)
+    v = randn((total, Hk, D), dtype, seed=12)
+    q = randn((B, Hk * R, D), dtype, seed=13)
+    for window in (-1, 100):
+        out = K.decode_attention_varlen(q.to(dev), k.to(dev), v.to(dev), cu.to(dev), int(lens.max()),
+                                        window_left=window)
+        torch.cuda.synchronize()
+        ref = np.zeros((B, Hk * R, D))
+        for b in range(B):
+            s0, s1 = int(cu[b]), int(cu[b + 1])
+            if window >= 0:
+                s0 = max(s0, s1 - (window + 1))
+            for h in range(Hk):
+                ref[b, h * R:(h + 1) * R] = oracle.decode_attention(
+                    q[b, h * R:(h + 1) * R].float().numpy(), k[s0:s1, h].float().numpy(),
+                    v[s0:s1, h].float().numpy(), 1.0 / math.sqrt(D))
+        _close(out, ref)
+
+
+# ------------------------------------------------------- rows movement
+@pytest.mark.parametrize("host", [False, True])
+def test_gather_rows_bit_exact(K, dev, host):
+    _say(f"[gather] host={host}")
+    g0 = torch.Generator().manual_seed(123)
+    rows_total, D = 10000, 128
+    k = randn((rows_total, D), "bf16", seed=21)
+    v = randn((rows_total, D), "bf16", seed=22)
+    if host:
+        k, v = k.pin_memory(), v.pin_memory()
+    else:
+        k, v = k.to(dev), v.to(dev)
+    for n in (0, 1, 8192):
+        src = torch.randint(rows_total, (n,), generator=g0)
+        dk = torch.empty((n, D), dtype=torch.bfloat16, device=dev)
+        dv = torch.empty_like(dk)
+        flag = torch.zeros((), dtype=torch.int32, device=dev)
+        K.gather_rows(k, v, src.to(dev), dk, dv, error_flag=flag)
+        torch.cuda.synchronize()
+        assert int(flag) == 0
+        assert same_bits(dk, k.cpu()[src]) and same_bits(dv, v.cpu()[src])
+    # scatter into a direct layout with gaps, plus one invalid source row
+    src = torch.tensor([5, 9999, 0, 10000, -1, 77])
+    dst = torch.tensor([0, 1, 3, 4, 5, 6])
+    dk = torch.zeros((8, D), dtype=torch.bfloat16, device=dev)
+    dv = torch.zeros_like(dk)
+    flag = torch.zeros((), dtype=torch.int32, device=dev)
+    K.gather_rows(k, v, src.to(dev), dk, dv, dst.to(dev), error_flag=flag)
+    torch.cuda.synchronize()
+    assert int(flag) == 1
+    kc = k.cpu()
+    for s, d in ((5, 0), (9999, 1), (0, 3), (77, 6)):
+        assert same_bits(dk[d], kc[s])
+    assert (dk[[2, 4, 5, 7]].float() == 0).all()
+
+
+@pytest.mark.parametrize("host", [False, True])
+def test_append_kv(K, dev, host):
+    E, Lmax, D = 6, 40, 128
+    dk = torch.zeros((E, Lmax, D), dtype=torch.float16)
+    dv = torch.zeros_like(dk)
+    if host:
+        dk, dv = dk.pin_memory(), dv.pin_memory()
+    else:
+        dk, dv = dk.to(dev), dv.to(dev)
+    nk = randn((3, D), "f16", seed=31).to(dev)
+    nv = randn((3, D), "f16", seed=32).to(dev)
+    K.append_kv(nk, nv, dk, dv, first_entry=2, position=17)
+    torch.cuda.synchronize()
+    assert same_bits(dk[2:5, 17], nk.cpu()) and same_bits(dv[2:5, 17], nv.cpu())
+    assert float(dk.cpu().float().abs().sum()) == float(nk.cpu().float().abs().sum())

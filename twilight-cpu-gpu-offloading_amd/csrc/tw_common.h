@@ -1,0 +1,207 @@
+// Shared device helpers for the sparse-decode KV path on CDNA4 (gfx950).
+//
+// Every kernel in this library is written for 64-lane wavefronts.  Arithmetic
+// whose rounding is part of the parity contract (page scores, INT4 scale and
+// codes, QK estimates) uses the explicit IEEE intrinsics below and the whole
+// library is compiled with -ffp-contract=off, so no multiply/add pair is ever
+// fused behind our back.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/twilight_hip.h"
+
+namespace tw {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- dtypes
+// Storage types: 16-bit formats are carried as raw uint16_t bit patterns so the
+// conversions below (and therefore every rounding step) are explicit.
+struct F16 {
+  using storage = uint16_t;
+  static constexpr int code = TW_DTYPE_F16;
+};
+struct BF16 {
+  using storage = uint16_t;
+  static constexpr int code = TW_DTYPE_BF16;
+};
+struct F32 {
+  using storage = float;
+  static constexpr int code = TW_DTYPE_F32;
+};
+
+__device__ __forceinline__ float u32_as_f32(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f32_as_u32(float f) { return __float_as_uint(f); }
+
+// Exact widening conversions.
+__device__ __forceinline__ float to_f32(F16, uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ float to_f32(BF16, uint16_t h) {
+  return u32_as_f32(static_cast<uint32_t>(h) << 16);
+}
+__device__ __forceinline__ float to_f32(F32, float f) { return f; }
+
+// Round-to-nearest-even narrowing conversions (NaN -> canonical quiet NaN).
+__device__ __forceinline__ uint16_t from_f32(F16, float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+__device__ __forceinline__ uint16_t from_f32(BF16, float f) {
+  uint32_t u = f32_as_u32(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>(((u >> 16) & 0x8000u) | 0x7fc0u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ float from_f32(F32, float f) { return f; }
+
+// Round a float to the storage precision and back (the "compute in the key
+// dtype" step of a 16-bit subtraction).
+template <typename DT>
+__device__ __forceinline__ float round_to(float f) {
+  return to_f32(DT{}, from_f32(DT{}, f));
+}
+
+// ------------------------------------------------------- total orders
+// Orderable keys: unsigned comparison of the key equals numeric comparison of
+// the value, with -0 < +0.  Used for order-independent min/max reductions.
+__device__ __forceinline__ uint32_t order_key16(uint16_t h) {
+  return (h & 0x8000u) ? static_cast<uint32_t>(static_cast<uint16_t>(~h)) : static_cast<uint32_t>(h | 0x8000u);
+}
+__device__ __forceinline__ uint16_t from_order_key16(uint32_t k) {
+  return (k & 0x8000u) ? static_cast<uint16_t>(k & 0x7fffu) : static_cast<uint16_t>(~k);
+}
+__device__ __forceinline__ uint32_t order_key32(uint32_t u) {
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ uint32_t from_order_key32(uint32_t k) {
+  return (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+}
+
+__device__ __forceinline__ bool is_nan(F16, uint16_t h) { return (h & 0x7fffu) > 0x7c00u; }
+__device__ __forceinline__ bool is_nan(BF16, uint16_t h) { return (h & 0x7fffu) > 0x7f80u; }
+__device__ __forceinline__ bool is_nan(F32, float f) { return (f32_as_u32(f) & 0x7fffffffu) > 0x7f800000u; }
+
+__device__ __forceinline__ uint16_t canonical_nan(F16) { return 0x7e00u; }
+__device__ __forceinline__ uint16_t canonical_nan(BF16) { return 0x7fc0u; }
+__device__ __forceinline__ float canonical_nan(F32) { return u32_as_f32(0x7fc00000u); }
+
+__device__ __forceinline__ uint32_t order_key(F16, uint16_t h) { return order_key16(h); }
+__device__ __forceinline__ uint32_t order_key(BF16, uint16_t h) { return order_key16(h); }
+__device__ __forceinline__ uint32_t order_key(F32, float f) { return order_key32(f32_as_u32(f)); }
+__device__ __forceinline__ uint16_t from_order_key(F16, uint32_t k) { return from_order_key16(k); }
+__device__ __forceinline__ uint16_t from_order_key(BF16, uint32_t k) { return from_order_key16(k); }
+__device__ __forceinline__ float from_order_key(F32, uint32_t k) { return u32_as_f32(from_order_key32(k)); }
+
+// Selection key for scores: NaN ranks above everything, -0 equals +0.
+__device__ __forceinline__ uint32_t score_key(float s) {
+  uint32_t u = f32_as_u32(s);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;
+  if (u == 0x80000000u) u = 0u;
+  return order_key32(u);
+}
+
+// ------------------------------------------------------- wave helpers
+__device__ __forceinline__ int lane_id() {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+}
+__device__ __forceinline__ uint64_t lanemask_lt() {
+  const int l = lane_id();
+  return (l == 0) ? 0ull : (~0ull >> (64 - l));
+}
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t w = __shfl_xor(v, o);
+    v = v > w ? v : w;
+  }
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t w = __shfl_xor(v, o);
+    v = v < w ? v : w;
+  }
+  return v;
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Inclusive suffix sum over lanes: result in lane l is sum of v over lanes >= l.
+__device__ __forceinline__ uint32_t wave_suffix_sum_u32(uint32_t v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    uint32_t w = __shfl_down(v, o);
+    if (l + o < 64) v += w;
+  }
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_suffix_sum_u64(uint64_t v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    uint64_t w = __shfl_down(v, o);
+    if (l + o < 64) v += w;
+  }
+  return v;
+}
+// Inclusive prefix sum over lanes.
+__device__ __forceinline__ int wave_prefix_sum_i32(int v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int w = __shfl_up(v, o);
+    if (l >= o) v += w;
+  }
+  return v;
+}
+
+// Index of the lowest set lane in a non-empty ballot.
+__device__ __forceinline__ int first_lane(uint64_t ballot) { return __ffsll(static_cast<long long>(ballot)) - 1; }
+
+// ------------------------------------------------ cross-block handoff
+// "Last block" pattern: every block publishes its results, then bumps a
+// per-group arrival counter; the block that arrives last consumes all
+// results and resets the counter so the next launch starts from zero (no
+// memset node, so the sequence is graph-capture safe).  No block ever waits
+// on another, so there is no forward-progress assumption.
+__device__ __forceinline__ bool arrive_last(unsigned int* counter, unsigned int expected, int* s_flag) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned int prev = atomicAdd(counter, 1u);
+    const bool last = (prev + 1u == expected);
+    if (last) atomicExch(counter, 0u);
+    *s_flag = last ? 1 : 0;
+  }
+  __syncthreads();
+  const bool last = *s_flag != 0;
+  if (last) __threadfence();
+  return last;
+}
+
+}  // namespace tw
+
+// Host-side launch bookkeeping shared by the C-ABI entry points.
+namespace tw_host {
+int record_hip_error(hipError_t err);
+int check_launch();
+}  // namespace tw_host

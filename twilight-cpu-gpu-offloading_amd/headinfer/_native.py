@@ -1,0 +1,111 @@
+"""ctypes bindings of the package's native libraries.
+
+``libtwilight_hip.so`` (gfx950 HIP kernels) and ``libtwilight_host.so`` (host
+natives) are loaded the way the reference loads its natives: ``ctypes.CDLL``
+with explicit argtypes, raw pointers and an int status
+(cpu_kv_gather.py:17-18, resident_zero_copy.py:41-42).  Unlike the reference
+nothing is compiled at import time: the libraries are built in-tree ahead of
+time (``build_native.py``).  A missing library is an error, never a fallback.
+
+torch is imported first on purpose: the HIP runtime torch ships has the same
+soname as /opt/rocm's, so the kernels run on torch's runtime and can take
+torch's stream handles directly.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_DIR = Path(__file__).resolve().parent / "_lib"
+HIP_LIB = LIB_DIR / "libtwilight_hip.so"
+HOST_LIB = LIB_DIR / "libtwilight_host.so"
+
+TW_OK, TW_EINVAL, TW_ERANGE, TW_ENOMEM, TW_EHIP, TW_EUNSUPPORTED = range(6)
+DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+_hip = None
+_host = None
+
+vp = ctypes.c_void_p
+i32 = ctypes.c_int
+i64 = ctypes.c_int64
+f32 = ctypes.c_float
+szt = ctypes.c_size_t
+
+_HIP_SIGNATURES = {
+    "tw_status_string": (ctypes.c_char_p, [i32]),
+    "tw_last_hip_error": (i32, []),
+    "tw_version": (i32, []),
+    "tw_build_page_metadata": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i64, vp, vp, vp, i64, vp]),
+    "tw_int4_dequantize": (i32, [vp, vp, vp, i32, i64, i32, vp, vp]),
+    "tw_quest_score": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp]),
+    "tw_topk_sorted": (i32, [vp, i32, i32, i64, i32, vp, vp]),
+    "tw_quest_select_workspace_size": (szt, [i32, i32, i32]),
+    "tw_quest_select": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, i32, vp, vp, vp, vp, vp, i64, i32, i32, i32,
+                              i32, i32, vp, szt, vp]),
+    "tw_decode_attention_workspace_size": (szt, [i32, i32, i32, i32]),
+    "tw_decode_attention": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i64, vp, i32, i32, i32, vp, vp,
+                                  f32, vp, vp, szt, vp]),
+    "tw_gather_rows": (i32, [vp, vp, i64, vp, vp, i64, i32, i32, vp, vp, vp, vp]),
+    "tw_host_device_pointer": (i32, [vp, ctypes.POINTER(ctypes.c_void_p)]),
+    "tw_append_kv": (i32, [vp, vp, i32, i32, i32, vp, vp, i64, i32, i64, vp]),
+}
+
+_HOST_SIGNATURES = {
+    "tw_host_gather_kv": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, i32]),
+    "tw_host_token_union": (i64, [ctypes.POINTER(ctypes.c_void_p), vp, i32, i64, vp, vp]),
+}
+
+
+def _load(path: Path, signatures: dict) -> ctypes.CDLL:
+    if not path.exists():
+        raise RuntimeError(
+            f"{path.name} is not built; run `python build_native.py` in {path.parent.parent.parent} "
+            "(or __graft_entry__.build()) first"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (res, args) in signatures.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def hip() -> ctypes.CDLL:
+    """The gfx950 kernel library (loaded once)."""
+    global _hip
+    if _hip is None:
+        _hip = _load(HIP_LIB, _HIP_SIGNATURES)
+    return _hip
+
+
+def host() -> ctypes.CDLL:
+    """The host natives library (loaded once)."""
+    global _host
+    if _host is None:
+        _host = _load(HOST_LIB, _HOST_SIGNATURES)
+    return _host
+
+
+def check(status: int, what: str) -> None:
+    """Map a C ABI status to the reference's exception types."""
+    if status == TW_OK:
+        return
+    text = hip().tw_status_string(status).decode()
+    if status in (TW_EINVAL, TW_ERANGE):
+        raise ValueError(f"{what}: {text}")
+    if status == TW_EHIP:
+        raise RuntimeError(f"{what}: {text} (hipError {hip().tw_last_hip_error()})")
+    raise RuntimeError(f"{what}: {text}")
+
+
+def stream_handle(device: torch.device | None = None) -> int:
+    """The hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,465 @@
+"""Tensor-level wrappers of the gfx950 kernels (the C ABI in
+include/twilight_hip.h).
+
+Every wrapper validates shapes, dtypes, devices and contiguity the way the
+reference's Triton wrappers do (e.g. twilight_fused_quest.py:35-46,
+twilight_fused_qk.py:80-101), enqueues on torch's current stream and never
+synchronizes.  There is no CPU path: tensors must live on a ROCm device (or,
+for the zero-copy host path, in pinned host memory).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _native
+from ._native import check, hip, ptr, stream_handle
+
+_KEY_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _native.DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}") from None
+
+
+def _require_device(*tensors: Optional[torch.Tensor], what: str) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"{what} requires ROCm device tensors (got {t.device})")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError(f"{what} requires tensors on one device")
+    if device is None:
+        raise ValueError(f"{what}: no device tensor given")
+    return device
+
+
+def _require_contiguous(*tensors: Optional[torch.Tensor], what: str) -> None:
+    for t in tensors:
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{what} requires contiguous tensors")
+
+
+class _Workspace:
+    """Per-device, per-purpose scratch buffers.  Allocated zeroed once; the
+    kernels return their arrival counters to zero after every launch."""
+
+    def __init__(self) -> None:
+        self._buffers: dict[tuple, torch.Tensor] = {}
+
+    def get(self, device: torch.device, name: str, nbytes: int) -> torch.Tensor:
+        key = (device, name)
+        buf = self._buffers.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 1 << 16)
+            if buf is not None:
+                size = max(size, 2 * buf.numel())
+            # Enqueue the replacement after any pending use of the old buffer.
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            self._buffers[key] = buf
+        return buf
+
+
+WORKSPACE = _Workspace()
+
+
+# --------------------------------------------------------------- metadata
+def build_page_metadata(
+    keys: torch.Tensor,
+    *,
+    sink: int,
+    block_size: int,
+    page_min: Optional[torch.Tensor] = None,
+    page_max: Optional[torch.Tensor] = None,
+    packed: Optional[torch.Tensor] = None,
+    scale: Optional[torch.Tensor] = None,
+    minimum: Optional[torch.Tensor] = None,
+) -> None:
+    """Prompt metadata of n entries in one launch (a2 + a3).
+
+    keys: [E, T, D] (or [T, D]); page_min/page_max: [E, >=P, D];
+    packed: [E, >=T, D/2] uint8; scale/minimum: [E, >=T].  Any of the two
+    output groups may be omitted."""
+    if keys.ndim == 2:
+        keys = keys.unsqueeze(0)
+    if keys.ndim != 3 or keys.dtype not in _KEY_DTYPES:
+        raise ValueError("keys must be [entries, tokens, dim] fp16/bf16/fp32")
+    E, T, D = keys.shape
+    if D % 2:
+        raise ValueError("head_dim must be even")
+    if keys.stride(2) != 1 or keys.stride(1) != D:
+        raise ValueError("keys rows must be contiguous")
+    dev = _require_device(keys, page_min, page_max, packed, scale, minimum, what="build_page_metadata")
+    pages = (T - sink) // block_size if T > sink else 0
+    pe = 0
+    if page_min is not None:
+        if page_max is None or page_min.shape != page_max.shape or page_min.dtype != keys.dtype:
+            raise ValueError("page_min/page_max must match each other and the key dtype")
+        if page_min.ndim == 2:
+            page_min, page_max = page_min.unsqueeze(0), page_max.unsqueeze(0)
+        if page_min.shape[0] != E or page_min.shape[1] < pages or page_min.shape[2] != D:
+            raise ValueError("page metadata buffers are too small")
+        if page_min.stride(2) != 1 or page_min.stride(1) != D or page_max.stride() != page_min.stride():
+            raise ValueError("page metadata buffers must be row-contiguous")
+        pe = page_min.stride(0)
+    qe = 0
+    if packed is not None:
+        if scale is None or minimum is None or scale.dtype != keys.dtype or minimum.dtype != keys.dtype:
+            raise ValueError("INT4 outputs must be given together in the key dtype")
+        if packed.ndim == 2:
+            packed, scale, minimum = packed.unsqueeze(0), scale.unsqueeze(0), minimum.unsqueeze(0)
+        if packed.dtype != torch.uint8 or packed.shape[0] != E or packed.shape[1] < T or packed.shape[2] != D // 2:
+            raise ValueError("packed buffer has the wrong shape")
+        if packed.stride(2) != 1 or packed.stride(1) != D // 2:
+            raise ValueError("packed rows must be contiguous")
+        if packed.stride(0) % (D // 2):
+            raise ValueError("packed entry stride must be a whole number of rows")
+        qe = packed.stride(0) // (D // 2)
+        if scale.stride(-1) != 1 or minimum.stride(-1) != 1 or scale.stride(0) != qe or minimum.stride(0) != qe:
+            raise ValueError("scale/minimum must share the packed entry stride")
+    elif scale is not None or minimum is not None:
+        raise ValueError("INT4 outputs must be given together")
+    if page_min is None and packed is None:
+        return
+    with torch.cuda.device(dev):
+        check(hip().tw_build_page_metadata(ptr(keys), keys.stride(0), E, T, D, _dt(keys), sink, block_size,
+                                           ptr(page_min), ptr(page_max), pe, ptr(packed), ptr(scale), ptr(minimum),
+                                           qe, stream_handle(dev)), "build_page_metadata")
+
+
+def affine_int4_pack(keys: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Per-token affine INT4 (twilight_offload_cache.py:25-37) on the GPU."""
+    if keys.ndim != 2 or keys.shape[-1] % 2:
+        raise ValueError("keys must be [tokens, even head_dim]")
+    T, D = keys.shape
+    keys = keys.contiguous()
+    packed = torch.empty((T, D // 2), dtype=torch.uint8, device=keys.device)
+    scale = torch.empty((T,), dtype=keys.dtype, device=keys.device)
+    minimum = torch.empty((T,), dtype=keys.dtype, device=keys.device)
+    build_page_metadata(keys, sink=T, block_size=1, packed=packed, scale=scale, minimum=minimum)
+    return packed, scale, minimum
+
+
+def affine_int4_dequantize(packed: torch.Tensor, scale: torch.Tensor, minimum: torch.Tensor) -> torch.Tensor:
+    """twilight_offload_cache.py:40-47 on the GPU; returns fp32 [..., D]."""
+    if packed.dtype != torch.uint8 or scale.shape != packed.shape[:-1] or minimum.shape != scale.shape:
+        raise ValueError("incompatible packed/scale/minimum")
+    if scale.dtype != minimum.dtype:
+        raise ValueError("scale and minimum dtypes differ")
+    dev = _require_device(packed, scale, minimum, what="affine_int4_dequantize")
+    packed, scale, minimum = packed.contiguous(), scale.contiguous(), minimum.contiguous()
+    D = packed.shape[-1] * 2
+    N = scale.numel()
+    out = torch.empty((*packed.shape[:-1], D), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check(hip().tw_int4_dequantize(ptr(packed), ptr(scale), ptr(minimum), _dt(scale), N, D, ptr(out),
+                                       stream_handle(dev)), "affine_int4_dequantize")
+    return out
+
+
+# ------------------------------------------------------------------ Quest
+def _check_score_inputs(q, page_min, page_max, what):
+    if q.ndim != 3 or q.dtype != torch.float32:
+        raise ValueError(f"{what}: q must be [G, R, D] fp32")
+    if page_min.dtype not in _KEY_DTYPES or page_max.dtype != page_min.dtype:
+        raise ValueError(f"{what}: unsupported metadata dtypes")
+    if page_min.ndim != 3 or page_min.shape != page_max.shape or page_min.shape[0] != q.shape[0] \
+            or page_min.shape[2] != q.shape[2]:
+        raise ValueError(f"{what}: metadata must be [G, P, D] matching q")
+    if page_min.stride(2) != 1 or page_min.stride(1) != q.shape[2] or page_max.stride() != page_min.stride():
+        raise ValueError(f"{what}: metadata rows must be contiguous")
+    if not q.is_contiguous():
+        raise ValueError(f"{what}: q must be contiguous")
+    if q.shape[2] % 2 or q.shape[2] > 256:
+        raise ValueError(f"{what}: head_dim must be even and <= 256")
+
+
+def fused_quest_score(q: torch.Tensor, page_min: torch.Tensor, page_max: torch.Tensor) -> torch.Tensor:
+    """Quest upper-bound page score in the reference's explicit order
+    (twilight_fused_quest.py:35-46).  q [G,R,D] fp32, lo/hi [G,P,D]."""
+    _check_score_inputs(q, page_min, page_max, "fused_quest_score")
+    dev = _require_device(q, page_min, page_max, what="fused_quest_score")
+    G, R, D = q.shape
+    P = page_min.shape[1]
+    out = torch.empty((G, R, P), dtype=torch.float32, device=dev)
+    if P == 0:
+        return out
+    with torch.cuda.device(dev):
+        check(hip().tw_quest_score(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
+                                   page_min.stride(0), ptr(out), stream_handle(dev)), "fused_quest_score")
+    return out
+
+
+def topk_sorted(scores: torch.Tensor, k: int) -> torch.Tensor:
+    """torch.topk(scores, k, sorted=False).indices.sort().values with ties to
+    the lowest index (quest_offload_cache.py:373-374).  int64 [..., k]."""
+    if scores.dtype != torch.float32:
+        raise ValueError("scores must be fp32")
+    dev = _require_device(scores, what="topk_sorted")
+    P = scores.shape[-1]
+    if not 1 <= k <= P:
+        raise ValueError("k must be in [1, P]")
+    flat = scores.reshape(-1, P)
+    if flat.stride(1) != 1:
+        flat = flat.contiguous()
+    out = torch.empty((flat.shape[0], k), dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        check(hip().tw_topk_sorted(ptr(flat), flat.shape[0], P, flat.stride(0), k, ptr(out), stream_handle(dev)),
+              "topk_sorted")
+    return out.view(*scores.shape[:-1], k)
+
+
+def quest_select(
+    q: torch.Tensor,
+    page_min: torch.Tensor,
+    page_max: torch.Tensor,
+    k: int,
+    *,
+    scores: Optional[torch.Tensor] = None,
+    sel_pages: Optional[torch.Tensor] = None,
+    rows: Optional[torch.Tensor] = None,
+    row_masks: Optional[torch.Tensor] = None,
+    row_counts: Optional[torch.Tensor] = None,
+    sink: int = 0,
+    recent: int = 1,
+    block_size: int = 1,
+    length: int = 0,
+    append_position: int = -1,
+) -> None:
+    """Fused score + top-k + row plan for one layer (one launch).
+
+    page_min/page_max: [G, P, D] views (P pages are scored).  Outputs are
+    caller-allocated: scores [G,R,P] fp32, sel_pages [G,R,k] int32, rows/row_masks
+    [G, stride] int32/uint8, row_counts [G] int32."""
+    _check_score_inputs(q, page_min, page_max, "quest_select")
+    dev = _require_device(q, page_min, page_max, scores, sel_pages, rows, row_masks, row_counts,
+                          what="quest_select")
+    G, R, D = q.shape
+    P = page_min.shape[1]
+    if not 1 <= k <= P:
+        raise ValueError("k must be in [1, P]")
+    for t, dt, shape in ((scores, torch.float32, (G, R, P)), (sel_pages, torch.int32, (G, R, k)),
+                         (row_counts, torch.int32, (G,))):
+        if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
+            raise ValueError("quest_select output has the wrong dtype/shape")
+    stride = 0
+    if rows is not None:
+        if rows.dtype != torch.int32 or rows.ndim != 2 or rows.shape[0] != G or rows.stride(1) != 1:
+            raise ValueError("rows must be [G, stride] int32")
+        stride = rows.stride(0)
+        if row_masks is not None and (row_masks.dtype != torch.uint8 or row_masks.shape != rows.shape
+                                      or row_masks.stride() != rows.stride()):
+            raise ValueError("row_masks must match rows")
+    nbytes = hip().tw_quest_select_workspace_size(G, R, P)
+    ws = WORKSPACE.get(dev, "quest_select", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_quest_select(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
+                                    page_min.stride(0), k, ptr(scores), ptr(sel_pages), ptr(rows), ptr(row_masks),
+                                    ptr(row_counts), stride, sink, recent, block_size, length, append_position,
+                                    ptr(ws), ws.numel(), stream_handle(dev)), "quest_select")
+
+
+# --------------------------------------------------------------- attention
+def decode_attention_rows(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    rows: torch.Tensor,
+    row_counts: torch.Tensor,
+    max_rows: int,
+    *,
+    row_masks: Optional[torch.Tensor] = None,
+    cur_k: Optional[torch.Tensor] = None,
+    cur_v: Optional[torch.Tensor] = None,
+    softmax_scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Sparse GQA decode attention reading K/V rows by position straight from
+    the cache.  q [G,R,D]; k_cache/v_cache [G, Lmax, D] (the layer's entries,
+    HBM or mapped pinned host); rows [G, stride] int32 positions; row_counts
+    [G] int32; cur_k/cur_v [G, D] extra decode token.  Returns [G,R,D]."""
+    if q.ndim != 3 or q.dtype not in _KEY_DTYPES:
+        raise ValueError("q must be [G, R, D]")
+    G, R, D = q.shape
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or k_cache.shape != v_cache.shape:
+        raise ValueError("K/V cache must match q's dtype and each other")
+    if k_cache.ndim != 3 or k_cache.shape[0] != G or k_cache.shape[2] != D or k_cache.stride() != v_cache.stride():
+        raise ValueError("K/V cache must be [G, Lmax, D]")
+    if k_cache.stride(2) != 1 or k_cache.stride(1) != D or k_cache.stride(0) % D:
+        raise ValueError("K/V cache rows must be contiguous")
+    if rows.dtype != torch.int32 or rows.ndim != 2 or rows.shape[0] != G or rows.stride(1) != 1:
+        raise ValueError("rows must be [G, stride] int32")
+    if row_counts.dtype != torch.int32 or tuple(row_counts.shape) != (G,):
+        raise ValueError("row_counts must be [G] int32")
+    if (cur_k is None) != (cur_v is None):
+        raise ValueError("cur_k and cur_v go together")
+    if cur_k is not None and (cur_k.shape != (G, D) or cur_k.dtype != q.dtype or not cur_k.is_contiguous()
+                              or not cur_v.is_contiguous() or cur_v.shape != cur_k.shape):
+        raise ValueError("cur_k/cur_v must be contiguous [G, D] in q's dtype")
+    dev = _require_device(q, rows, row_counts, row_masks, cur_k, cur_v, what="decode_attention")
+    _require_contiguous(q, what="decode_attention")
+    if out is None:
+        out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
+    ws = WORKSPACE.get(dev, "decode_attention", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_decode_attention(ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D, ptr(rows),
+                                        ptr(row_masks), ptr(row_counts), rows.stride(0), k_cache.stride(0) // D,
+                                        None, 0, -1, max_rows, ptr(cur_k), ptr(cur_v), scale, ptr(out), ptr(ws),
+                                        ws.numel(), stream_handle(dev)), "decode_attention")
+    return out
+
+
+def decode_attention_varlen(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    max_seqlen_k: int,
+    *,
+    softmax_scale: Optional[float] = None,
+    window_left: int = -1,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Varlen decode attention with one query token per sequence (the
+    flash_attn_varlen_func call of mp.py:40-52 at max_seqlen_q == 1).
+    q [B, Hq, D], k/v [total_k, Hk, D], cu_seqlens_k [B+1] int32."""
+    if q.ndim != 3 or k.ndim != 3 or v.shape != k.shape:
+        raise ValueError("expected q [B, Hq, D] and k/v [total_k, Hk, D]")
+    B, Hq, D = q.shape
+    Hk = k.shape[1]
+    if k.shape[2] != D or Hq % Hk:
+        raise ValueError("head_dim mismatch or Hq not a multiple of Hk")
+    if q.dtype not in _KEY_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q/k/v dtypes must match (fp16/bf16/fp32)")
+    if cu_seqlens_k.dtype != torch.int32 or tuple(cu_seqlens_k.shape) != (B + 1,):
+        raise ValueError("cu_seqlens_k must be [B+1] int32")
+    dev = _require_device(q, k, v, cu_seqlens_k, what="decode_attention_varlen")
+    _require_contiguous(q, k, v, cu_seqlens_k, what="decode_attention_varlen")
+    R = Hq // Hk
+    G = B * Hk
+    if out is None:
+        out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    max_rows = int(max_seqlen_k)
+    if window_left >= 0:
+        max_rows = min(max_rows, window_left + 1)
+    nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
+    ws = WORKSPACE.get(dev, "decode_attention", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_decode_attention(ptr(q), k.data_ptr(), v.data_ptr(), _dt(q), G, R, D, None, None, None, 0, 0,
+                                        ptr(cu_seqlens_k), Hk, int(window_left), max_rows, None, None, scale,
+                                        ptr(out), ptr(ws), ws.numel(), stream_handle(dev)), "decode_attention_varlen")
+    return out
+
+
+# ------------------------------------------------------------ row movement
+def host_device_pointer(t: torch.Tensor) -> int:
+    """Device address of a pinned host tensor's data (zero-copy access)."""
+    if t.is_cuda or not t.is_pinned():
+        raise ValueError("zero-copy source must be pinned host memory")
+    out = _native.ctypes.c_void_p()
+    check(hip().tw_host_device_pointer(t.data_ptr(), _native.ctypes.byref(out)), "host_device_pointer")
+    return int(out.value)
+
+
+def gather_rows(
+    src_k: torch.Tensor,
+    src_v: torch.Tensor,
+    src_rows: torch.Tensor,
+    dst_k: torch.Tensor,
+    dst_v: torch.Tensor,
+    dst_rows: Optional[torch.Tensor] = None,
+    *,
+    error_flag: Optional[torch.Tensor] = None,
+    device: Optional[torch.device] = None,
+) -> None:
+    """dst[dst_rows[i]] = src[src_rows[i]] for K and V (bit-exact).
+
+    src_k/src_v: [rows, D] on the device, or pinned host tensors (read
+    zero-copy through their mapped device address).  src_rows/dst_rows: int64
+    device tensors.  Out-of-range source rows are skipped and flagged in
+    error_flag (int32 device scalar)."""
+    if src_k.shape != src_v.shape or src_k.dtype != src_v.dtype or src_k.ndim != 2:
+        raise ValueError("src_k/src_v must be matching [rows, D]")
+    if dst_k.dtype != src_k.dtype or dst_v.dtype != src_k.dtype or dst_k.shape[-1] != src_k.shape[-1]:
+        raise ValueError("destination must match the source dtype and row width")
+    _require_contiguous(src_k, src_v, dst_k, dst_v, src_rows, dst_rows, what="gather_rows")
+    if src_rows.dtype != torch.int64 or (dst_rows is not None and (dst_rows.dtype != torch.int64
+                                                                   or dst_rows.shape != src_rows.shape)):
+        raise ValueError("row indices must be int64")
+    dev = _require_device(dst_k, dst_v, src_rows, dst_rows, error_flag, what="gather_rows")
+    if src_k.is_cuda:
+        sk, sv = src_k.data_ptr(), src_v.data_ptr()
+    else:
+        sk, sv = host_device_pointer(src_k), host_device_pointer(src_v)
+    D = src_k.shape[1]
+    with torch.cuda.device(dev):
+        check(hip().tw_gather_rows(sk, sv, src_k.shape[0], ptr(src_rows), ptr(dst_rows), src_rows.numel(), D,
+                                   src_k.element_size(), ptr(dst_k), ptr(dst_v), ptr(error_flag),
+                                   stream_handle(dev)), "gather_rows")
+
+
+def append_kv(
+    new_k: torch.Tensor,
+    new_v: torch.Tensor,
+    dst_k: torch.Tensor,
+    dst_v: torch.Tensor,
+    *,
+    first_entry: int,
+    position: int,
+    device: Optional[torch.device] = None,
+) -> None:
+    """Write the decode token of n entries into row `position` of
+    dst[first_entry + i] (dst: [E, Lmax, D], HBM or pinned host)."""
+    if new_k.ndim != 2 or new_k.shape != new_v.shape or new_k.dtype != new_v.dtype:
+        raise ValueError("new K/V must be matching [n, D]")
+    if dst_k.ndim != 3 or dst_k.shape != dst_v.shape or dst_k.shape[2] != new_k.shape[1] or dst_k.dtype != new_k.dtype:
+        raise ValueError("destination must be [E, Lmax, D] matching the new rows")
+    _require_contiguous(new_k, new_v, dst_k, dst_v, what="append_kv")
+    n, D = new_k.shape
+    if first_entry < 0 or first_entry + n > dst_k.shape[0] or not 0 <= position < dst_k.shape[1]:
+        raise ValueError("append target outside the cache")
+    dev = _require_device(new_k, new_v, what="append_kv")
+    if dst_k.is_cuda:
+        dk, dv = dst_k.data_ptr(), dst_v.data_ptr()
+    else:
+        dk, dv = host_device_pointer(dst_k), host_device_pointer(dst_v)
+    with torch.cuda.device(dev):
+        check(hip().tw_append_kv(ptr(new_k), ptr(new_v), n, D, new_k.element_size(), dk, dv, dst_k.shape[1],
+                                 first_entry, position, stream_handle(dev)), "append_kv")
+
+
+def host_gather_kv(k: torch.Tensor, v: torch.Tensor, rows: torch.Tensor, out_k: torch.Tensor, out_v: torch.Tensor,
+                   threads: Optional[int] = None) -> None:
+    """Host (CPU) row gather into staging, e.g. pinned memory for an async
+    H2D copy (the reference's CpuKVGather, cpu_kv_gather.py:21-36)."""
+    tensors = (k, v, rows, out_k, out_v)
+    if any(t.device.type != "cpu" or not t.is_contiguous() for t in tensors):
+        raise ValueError("CPU contiguous tensors required")
+    if k.ndim != 2 or k.shape != v.shape or k.dtype != v.dtype:
+        raise ValueError("invalid source layout")
+    if rows.ndim != 1 or rows.dtype != torch.int64:
+        raise ValueError("int64 row indices required")
+    if out_k.shape != (rows.numel(), k.shape[1]) or out_k.shape != out_v.shape:
+        raise ValueError("invalid output layout")
+    if out_k.dtype != k.dtype or out_v.dtype != k.dtype:
+        raise ValueError("dtype mismatch")
+    if rows.numel() == 0:
+        return
+    rc = _native.host().tw_host_gather_kv(k.data_ptr(), v.data_ptr(), out_k.data_ptr(), out_v.data_ptr(),
+                                          rows.data_ptr(), rows.numel(), k.shape[0], k.shape[1] * k.element_size(),
+                                          int(threads or torch.get_num_threads()))
+    if rc:
+        raise ValueError("row index out of bounds")
