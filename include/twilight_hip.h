@@ -100,30 +100,37 @@ int tw_topk_sorted(const float* scores, int rows, int P, int64_t score_row_strid
                    int64_t* out, void* stream);
 
 /* ------------------------------------------------------------------------
- * Fused Quest selection for one decoder layer: score + top-k + GQA row
- * plan, one launch.  Covers prepare_layer_selection
- * (quest_offload_cache.py:299-401) followed by _selected_positions
- * (:403-511) for the G entries of a layer, and the Twilight stage-1 B0
- * selection (twilight_offload_cache.py:1128-1166).
- *   q [G][R][D] fp32; metadata as in tw_quest_score; P pages scored.
- *   scores (nullable) [G][R][P] fp32 output; when NULL the workspace holds
- *   them.
- *   sel_pages (nullable) [G][R][k] int32 ascending page ids.
- *   Row plan (nullable rows): for group g, rows[g*rows_stride + i] lists
- *   token positions  [0,sink_end) ++ (sink + p*bs + [0,bs)) for every page p
- *   selected by any of the R heads, ascending ++ [recent_start, length),
- *   then, if append_position >= 0, append_position itself.  row_masks
- *   (nullable) gets the bitmask of heads that see each row (pages: heads
- *   that selected them; all other rows: all heads).  row_counts[g] gets the
- *   number of rows.
+ * Quest selection for one decoder layer: score, top-k and the GQA union
+ * plan, two launches (score kernel, then one selection block per query
+ * head; the last block of each KV group builds the group's plan).  Covers
+ * prepare_layer_selection (quest_offload_cache.py:299-401) followed by
+ * _selected_positions (:403-511) for the G entries of a layer, and the
+ * Twilight stage-1 B0 selection (twilight_offload_cache.py:1128-1166).
+ *   q [G][R][D] fp32; metadata as in tw_quest_score; P <= 8192 pages scored.
+ *   scores (nullable) [G][R][P] fp32 copy of the scores.
+ *   sel_pages (nullable) [G][R][k] int32 ascending page ids per head
+ *   (torch.topk(sorted=False) then sort, quest_offload_cache.py:373-374;
+ *   ties to the lowest page, NaN highest, -0 == +0).
+ *   Union plan (nullable): plan_pages[g*plan_stride + u], u < plan_counts[g],
+ *   the ascending pages selected by any of the R heads of group g, and
+ *   plan_masks the bitmask of heads that selected each.  plan_stride >=
+ *   min(P, R*k).
+ *   Row plan (nullable): for group g, rows[g*rows_stride + i] lists token
+ *   positions [0,sink_end) ++ (sink + p*bs + [0,bs)) for every union page p
+ *   ascending ++ [recent_start, length), then, if append_position >= 0,
+ *   append_position itself.  row_masks gets the heads that see each row
+ *   (pages: heads that selected them; all other rows: all heads),
+ *   row_counts[g] the number of rows.
  *   Window: sink_end = min(sink, length); recent_start = max(sink_end,
  *   length - max(0, recent - 1))  (quest_offload_cache.py:330-332).
- * R <= 8 when rows/row_masks are requested.
+ * R <= 8 when a plan is requested.  workspace: tw_quest_select_workspace_size
+ * bytes, zero before the first call (the library leaves its counters zero).
  * ---------------------------------------------------------------------- */
 size_t tw_quest_select_workspace_size(int G, int R, int P);
 int tw_quest_select(const float* q, const void* page_min, const void* page_max, int dtype, int G,
                     int R, int P, int D, int64_t page_group_stride, int k, float* scores,
-                    int32_t* sel_pages, int32_t* rows, uint8_t* row_masks, int32_t* row_counts,
+                    int32_t* sel_pages, int32_t* plan_pages, uint8_t* plan_masks, int32_t* plan_counts,
+                    int64_t plan_stride, int32_t* rows, uint8_t* row_masks, int32_t* row_counts,
                     int64_t rows_stride, int sink, int recent, int block_size, int length,
                     int append_position, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -151,6 +158,19 @@ int tw_quest_select(const float* q, const void* page_min, const void* page_max, 
  * group's row count and sizes the grid.
  * ---------------------------------------------------------------------- */
 size_t tw_decode_attention_workspace_size(int G, int R, int D, int max_rows);
+/* The same attention over a union plan from tw_quest_select: group g's rows
+ * are [0, sink_end) ++ the plan's pages expanded to block_size rows each
+ * (heads per plan_masks, nullable = all) ++ [recent_start, length) ++
+ * append_position (if >= 0), read by position from the group's entry
+ * (k_base + (g*entry_stride_rows + pos)*D).  max_rows bounds every group's
+ * row count (sink_end + max_pages*block_size + recent rows + 1) and sizes
+ * the grid and the workspace (tw_decode_attention_workspace_size). */
+int tw_decode_attention_pages(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
+                              int D, const int32_t* plan_pages, const uint8_t* plan_masks,
+                              const int32_t* plan_counts, int64_t plan_stride, int max_rows,
+                              int64_t entry_stride_rows, int sink, int recent, int block_size, int length,
+                              int append_position, float softmax_scale, void* out, void* workspace,
+                              size_t workspace_bytes, void* stream);
 int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G,
                         int R, int D, const int32_t* rows, const uint8_t* row_masks,
                         const int32_t* row_counts, int64_t rows_stride, int64_t entry_stride_rows,

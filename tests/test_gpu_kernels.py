@@ -135,6 +135,33 @@ def test_topk_ties_nan_negzero(K, dev):
         assert np.array_equal(got.cpu().numpy(), oracle.topk_sorted(s.numpy(), k)), k
 
 
+@pytest.mark.parametrize("P", [5, 1000, 2028, 2048, 4076, 8169, 8192])
+def test_topk_distributions(K, dev, P):
+    """Score shapes that exercise every selection pass: heavy outliers that
+    stretch the linear range, clusters of equal values at the boundary (more
+    than a block of equal candidates), tiny ranges, and mixed signs."""
+    _say(f"[topk dist] P={P}")
+    g = torch.Generator().manual_seed(P)
+    rows = []
+    rows.append(torch.randn(P, generator=g))
+    out = torch.randn(P, generator=g)
+    out[torch.randperm(P, generator=g)[: max(1, P // 100)]] *= 1e4  # planted outliers
+    rows.append(out)
+    rows.append(torch.randint(0, 3, (P,), generator=g).float())  # large equal clusters
+    rows.append(1.0 + torch.randn(P, generator=g) * 1e-6)  # range of a few ulps
+    rows.append(torch.randn(P, generator=g) * torch.exp2(torch.randint(-60, 60, (P,), generator=g).float()))
+    rows.append(torch.full((P,), 2.5).index_put_((torch.tensor([P // 2]),), torch.tensor(3.0)))
+    s = torch.stack(rows)
+    for k in sorted({1, min(P, 7), min(P, 128), max(1, P // 2), min(P, 300), P}):
+        got = K.topk_sorted(s.to(dev), k)
+        assert np.array_equal(got.cpu().numpy(), oracle.topk_sorted(s.numpy(), k)), k
+        # the contiguous vector-load path (P % 4 == 0, aligned rows) and the scalar path both run
+        wide = torch.zeros((s.shape[0], P + 3))
+        wide[:, :P] = s
+        got2 = K.topk_sorted(wide.to(dev)[:, :P], k)
+        assert np.array_equal(got2.cpu().numpy(), oracle.topk_sorted(s.numpy(), k)), ("strided", k)
+
+
 # ------------------------------------------------------ fused selection
 @pytest.mark.parametrize(
     "dtype,G,R,L,sink,recent,bs,frac",
@@ -159,10 +186,14 @@ def test_quest_select_row_plan(K, dev, dtype, G, R, L, sink, recent, bs, frac):
     counts = torch.zeros((G,), dtype=torch.int32, device=dev)
     sel = torch.empty((G, R, k), dtype=torch.int32, device=dev)
     scores = torch.empty((G, R, P), dtype=torch.float32, device=dev)
-    for it in range(2):  # twice: the arrival counters must be reset by the kernel
-        K.quest_select(q.to(dev), lo.to(dev), hi.to(dev), k, scores=scores, sel_pages=sel, rows=rows,
-                       row_masks=masks, row_counts=counts, sink=sink, recent=recent, block_size=bs, length=L,
-                       append_position=L)
+    pw = min(P, R * k)
+    ppages = torch.full((G, pw), -3, dtype=torch.int32, device=dev)
+    pmasks = torch.zeros((G, pw), dtype=torch.uint8, device=dev)
+    pcounts = torch.zeros((G,), dtype=torch.int32, device=dev)
+    for it in range(3):  # repeated: the arrival counters must be reset by the kernel
+        K.quest_select(q.to(dev), lo.to(dev), hi.to(dev), k, scores=scores, sel_pages=sel, plan_pages=ppages,
+                       plan_masks=pmasks, plan_counts=pcounts, rows=rows, row_masks=masks, row_counts=counts,
+                       sink=sink, recent=recent, block_size=bs, length=L, append_position=L)
         torch.cuda.synchronize()
     ref_scores = oracle.quest_score(q.numpy(), to_bits(lo), to_bits(hi), dtype)
     assert np.array_equal(scores.cpu().numpy().view(np.uint32), ref_scores.view(np.uint32))
@@ -174,6 +205,12 @@ def test_quest_select_row_plan(K, dev, dtype, G, R, L, sink, recent, bs, frac):
         assert n == len(r_rows)
         assert np.array_equal(rows[g, :n].cpu().numpy(), r_rows)
         assert np.array_equal(masks[g, :n].cpu().numpy(), r_masks)
+        # union plan: the pages any head selected, ascending, with the heads' bitmask
+        union = np.unique(ref_sel[g])
+        nu = int(pcounts[g])
+        assert nu == len(union) and np.array_equal(ppages[g, :nu].cpu().numpy(), union)
+        want = [sum(1 << r for r in range(R) if p in ref_sel[g, r]) for p in union]
+        assert np.array_equal(pmasks[g, :nu].cpu().numpy(), np.array(want, np.uint8))
 
 
 # ------------------------------------------------------------ attention
@@ -209,6 +246,7 @@ def _close(got, ref, atol=2e-3, rtol=1e-2):
         ("f32", 3, 8, 128, 2000, 1000, True, True),
         ("bf16", 2, 3, 4, 32, 9, True, True),
         ("f16", 2, 2, 256, 1000, 129, False, True),
+        ("bf16", 8, 4, 128, 32768, 6000, "sparse", True),
     ],
 )
 def test_decode_attention_rows(K, dev, dtype, G, R, D, L, n_rows, masked, cur):
@@ -220,7 +258,13 @@ def test_decode_attention_rows(K, dev, dtype, G, R, D, L, n_rows, masked, cur):
     rows = torch.stack([torch.randperm(L, generator=g0)[:n_rows].sort().values for _ in range(G)]).to(torch.int32)
     counts = torch.tensor([n_rows - 5 * g if n_rows > 5 * G else n_rows for g in range(G)], dtype=torch.int32)
     masks = None
-    if masked:
+    if masked == "sparse":
+        # each head sees about one row in 300: most blocks hold no visible row
+        # for some head, which must contribute nothing (not NaN) to the merge
+        masks = (torch.rand((G, n_rows, R), generator=g0) < 1 / 300).to(torch.uint8)
+        masks = (masks << torch.arange(R, dtype=torch.uint8)).sum(-1).to(torch.uint8)
+        masks[:, -1] = (1 << R) - 1
+    elif masked:
         masks = torch.randint(0, 1 << R, (G, n_rows), generator=g0).to(torch.uint8)
         masks[:, -1] = (1 << R) - 1  # each head sees at least one row
     ck = randn((G, D), dtype, seed=4) if cur else None
@@ -233,6 +277,55 @@ def test_decode_attention_rows(K, dev, dtype, G, R, D, L, n_rows, masked, cur):
     ref_rows = [rows[g, : int(counts[g])].long().numpy() for g in range(G)]
     ref_masks = None if masks is None else [masks[g, : int(counts[g])].numpy() for g in range(G)]
     ref = _attn_ref(q, kc, vc, ref_rows, ref_masks, ck, cv, scale)
+    _close(out, ref)
+
+
+@pytest.mark.parametrize(
+    "dtype,G,R,D,L,k,sink,recent,bs,masked",
+    [
+        ("f16", 8, 4, 128, 32768, 128, 64, 256, 16, True),   # the 32K Quest layer
+        ("bf16", 4, 7, 128, 20000, 60, 64, 256, 16, True),
+        ("bf16", 3, 2, 64, 3000, 20, 10, 30, 12, False),     # page size not a power of two
+        ("f32", 2, 3, 128, 1500, 8, 1, 2, 8, True),
+        ("f16", 2, 2, 6, 400, 5, 4, 9, 4, True),             # generic head dim
+    ],
+)
+def test_decode_attention_pages(K, dev, dtype, G, R, D, L, k, sink, recent, bs, masked):
+    """Attention over a union page plan == attention over its expanded rows."""
+    _say(f"[attention pages] {dtype} G={G} R={R} D={D} L={L} k={k}")
+    g0 = torch.Generator().manual_seed(L + k)
+    sink_end, recent_start, eligible = oracle.selection_window(L, sink, recent)
+    P = eligible // bs
+    Lmax = L + 1
+    kc = randn((G, Lmax, D), dtype, seed=41)
+    vc = randn((G, Lmax, D), dtype, seed=42)
+    q = randn((G, R, D), dtype, seed=43)
+    max_pages = min(P, R * k)
+    pages = torch.zeros((G, max_pages), dtype=torch.int32)
+    pm = torch.zeros((G, max_pages), dtype=torch.uint8)
+    counts = torch.zeros((G,), dtype=torch.int32)
+    for g in range(G):
+        n = int(torch.randint(1, max_pages + 1, (1,), generator=g0))
+        pages[g, :n] = torch.randperm(P, generator=g0)[:n].sort().values.to(torch.int32)
+        pm[g, :n] = torch.randint(1, 1 << R, (n,), generator=g0).to(torch.uint8)
+        counts[g] = n
+    out = K.decode_attention_pages(q.to(dev), kc.to(dev), vc.to(dev), pages.to(dev), counts.to(dev),
+                                   plan_masks=pm.to(dev) if masked else None, max_pages=max_pages, sink=sink,
+                                   recent=recent, block_size=bs, length=L, append_position=L)
+    torch.cuda.synchronize()
+    ref = np.zeros((G, R, D))
+    all_heads = (1 << R) - 1
+    for g in range(G):
+        n = int(counts[g])
+        pg = pages[g, :n].long()
+        rows = torch.cat([torch.arange(sink_end), (sink + pg[:, None] * bs + torch.arange(bs)).reshape(-1),
+                          torch.arange(recent_start, L), torch.tensor([L])])
+        m = None
+        if masked:
+            m = torch.cat([torch.full((sink_end,), all_heads), pm[g, :n].long().repeat_interleave(bs),
+                           torch.full((L - recent_start + 1,), all_heads)]).to(torch.uint8).numpy()
+        ref[g] = oracle.decode_attention(q[g].float().numpy(), kc[g, rows].float().numpy(),
+                                         vc[g, rows].float().numpy(), 1.0 / math.sqrt(D), m)
     _close(out, ref)
 
 

@@ -1,24 +1,29 @@
-// Sparse GQA decode attention over selected rows, split-K with a fused
-// last-block combine.
+// Sparse GQA decode attention over selected rows: split-K flash-decode with a
+// fused last-block combine.
 //
 // Reference call surface: _flash_attention_varlen_forward (mp.py:21-52) as
 // used by the GQA-group decode branch (mp.py:239-279: G sequences of one
 // query token x R heads against one KV head), the layer-flat branch
 // (mp.py:283-321) and the per-head reference path (mp.py:424-452).  The
-// reference semantics are softmax(q.k * scale) v over every key of the
-// sequence (causal with q_len 1 sees all keys), fp32 accumulation, output in
-// the input dtype.
+// semantics are softmax(q.k * scale) v over every key of the sequence (causal
+// with q_len 1 sees all keys), fp32 accumulation, output in the input dtype.
 //
-// Work split: block = (group g, chunk of rows).  Inside a block each of the 4
-// wavefronts takes 32 rows per iteration as 8 steps of 4 rows: LPR = D/8 lanes
-// share a row and each lane owns 8 consecutive channels, so a K or V row is a
-// 16-byte-per-lane coalesced load and the rows are read straight from the KV
-// cache by index (no gathered copy).  The R query heads of the group share
-// every K/V load.  Scores are reduced across the LPR lanes of a row with xor
-// shuffles; each wavefront keeps an online (max, sum, acc) per head; the four
-// wavefront partials are merged in LDS into one block partial; the last
-// block of the group (arrival counter, no waiting) merges all block partials
-// and writes the output.
+// The kernel is written for latency: a decode layer moves tens of MB, so it
+// completes in a handful of memory round trips and every round trip counts.
+//   round trip 1: row count, the wavefront's row indices (one per lane) and
+//                 masks, the group's queries -- all independent loads;
+//   round trip 2: the K and V rows (16 bytes per lane, 8 rows per lane in
+//                 flight), read straight from the cache by index;
+//   then the block partial (m, l, o) is published to the workspace with
+//   device-coherent stores, the block bumps the group's arrival counter, and
+//   the last block of the group loads every partial of the group in batched
+//   round trips and writes the output.
+// Every load is unconditional (clamped addresses, results masked) so the
+// compiler issues them back to back instead of one branch and wait per load.
+//
+// Work split: block = (group g, chunk of rows); 4 wavefronts; D/8 lanes share
+// a row and each lane owns 8 consecutive channels (one 16-byte load per row).
+// The R query heads of the group share every K/V load.
 #pragma clang fp contract(off)
 
 #include "tw_common.h"
@@ -28,7 +33,13 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
+constexpr int kMergeBatch = 64;
+constexpr int kMaxChunks = 128;
 constexpr float kLog2e = 1.4426950408889634f;
+
+// Row loads in flight per lane: fewer when the registers go to many heads or
+// to 32-bit values.
+constexpr int steps_for(int elem_bytes, int rmax) { return (elem_bytes == 2 && rmax <= 4) ? 8 : 4; }
 
 struct AttnArgs {
   const void* q;
@@ -47,20 +58,29 @@ struct AttnArgs {
   const void* cur_v;
   float scale_log2;
   void* out;
-  float* partials;          // [G][max_chunks][R][2 + D]
+  // Page-plan mode: group g's rows are [0, sink_end) ++ the union pages
+  // plan_pages[g][0 .. plan_counts[g]) expanded to bs rows each ++
+  // [recent_start, length) ++ append_position (if >= 0).
+  const int32_t* plan_pages;
+  const uint8_t* plan_masks;
+  const int32_t* plan_counts;
+  int64_t plan_stride;
+  int sink, recent, bs, length, append_position;
+  float* part_ml;           // [G][max_chunks][R][2]  (m, l)
+  float* part_o;            // [G][max_chunks][R][D]
   unsigned int* counters;   // [G]
   int max_chunks;
-  int iters;                // row iterations per block
+  int iters;                // row batches per block
   int max_rows;             // bound on every group's row count
 };
 
-template <typename S, int CPL>
-struct Chunk;
+// 8 consecutive channels of one row.
+template <typename S>
+struct Vec8;
 template <>
-struct Chunk<uint16_t, 8> {
+struct Vec8<uint16_t> {
   uint4 w;
   __device__ __forceinline__ void load(const uint16_t* p) { w = *reinterpret_cast<const uint4*>(p); }
-  __device__ __forceinline__ void zero() { w = make_uint4(0u, 0u, 0u, 0u); }
   template <typename DT>
   __device__ __forceinline__ void to_float(float (&f)[8]) const {
     const uint32_t a[4] = {w.x, w.y, w.z, w.w};
@@ -72,15 +92,11 @@ struct Chunk<uint16_t, 8> {
   }
 };
 template <>
-struct Chunk<float, 8> {
+struct Vec8<float> {
   float4 a, b;
   __device__ __forceinline__ void load(const float* p) {
     a = reinterpret_cast<const float4*>(p)[0];
     b = reinterpret_cast<const float4*>(p)[1];
-  }
-  __device__ __forceinline__ void zero() {
-    a = make_float4(0.f, 0.f, 0.f, 0.f);
-    b = a;
   }
   template <typename DT>
   __device__ __forceinline__ void to_float(float (&f)[8]) const {
@@ -89,82 +105,212 @@ struct Chunk<float, 8> {
   }
 };
 
-// Generic chunk for runtime D (one row per wavefront instruction, lane owns
-// channels 8*lane .. 8*lane+7, masked against D).
-template <typename S>
-struct GenericChunk {
-  S e[8];
-  __device__ __forceinline__ void load(const S* p, int c0, int D) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = (c0 + i < D) ? p[i] : S(0);
-  }
-  __device__ __forceinline__ void zero() {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = S(0);
-  }
-  template <typename DT>
-  __device__ __forceinline__ void to_float(float (&f)[8]) const {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = to_f32(DT{}, e[i]);
-  }
+// DPP lane permutations (GFX9 encodings) for sums inside lane groups.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+constexpr int kQuadXor1 = 0xb1;      // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4e;      // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+
+// Sum over each aligned group of N lanes (N = 1..64, power of two); every
+// lane of the group receives the sum.
+template <int N>
+__device__ __forceinline__ float row_group_sum(float x) {
+  if constexpr (N >= 2) x += dpp<kQuadXor1>(x);
+  if constexpr (N >= 4) x += dpp<kQuadXor2>(x);
+  if constexpr (N >= 8) x += dpp<kRowHalfMirror>(x);
+  if constexpr (N >= 16) x += dpp<kRowMirror>(x);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32);
+  return x;
+}
+
+// exp2(x - m), with a masked value (x = -inf) giving 0 even when m is -inf too.
+__device__ __forceinline__ float exp2_rel(float x, float m) {
+  return x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(x - m);
+}
+
+// Row sources: an explicit row list, a varlen sequence, or a page plan.
+constexpr int kModeRows = 0;
+constexpr int kModeVarlen = 1;
+constexpr int kModePages = 2;
+
+// Geometry of group g's rows (identical in every block of the group).
+struct GroupRows {
+  int n_list;        // rows from the list / sequence / plan
+  int n_rows;        // + the decode token
+  int64_t base;      // element offset of the group's row 0 (position 0)
+  int64_t stride;    // elements between positions
+  int win_start;     // varlen: first visible position
+  // page plan
+  int n_pages, sink_end, page_end, recent_start, recent_end;
 };
 
-template <typename DT, int DFIX, int RMAX, bool INDEXED>
-__global__ __launch_bounds__(kBlock) void decode_attn_kernel(AttnArgs a) {
-  using S = typename DT::storage;
-  constexpr bool kGeneric = (DFIX == 0);
-  constexpr int CPL = 8;
-  constexpr int LPR = kGeneric ? 64 : DFIX / CPL;   // lanes per row
-  constexpr int RPI = kWave / LPR;                   // rows per instruction
-  constexpr int NSTEP = (sizeof(S) == 2) ? 8 : 4;    // instructions per iteration
-  constexpr int RW = NSTEP * RPI;                    // rows per wavefront iteration
-  using ChunkT = typename std::conditional<kGeneric, GenericChunk<S>, Chunk<S, CPL>>::type;
-
-  const int D = kGeneric ? a.D : DFIX;
-  const int R = a.R;
-  const int g = blockIdx.x / a.max_chunks;
-  const int chunk = blockIdx.x - g * a.max_chunks;
-  const int wave = static_cast<int>(threadIdx.x) / kWave;
-  const int lane = lane_id();
-  const int rig = lane / LPR;            // row in instruction
-  const int c0 = (lane % LPR) * CPL;     // first channel of this lane
-
-  // ---- rows of this group ----
-  int n_list;
-  int64_t seg_base = 0;   // row offset of the group's first row
-  int64_t row_stride = D; // elements between consecutive rows
-  int64_t head_off = 0;
-  int win_start = 0;
-  if (INDEXED) {
-    n_list = a.counts[g];
-    n_list = n_list < 0 ? 0 : (n_list > a.max_rows ? a.max_rows : n_list);
-    seg_base = static_cast<int64_t>(g) * a.entry_stride;
+template <int MODE>
+__device__ __forceinline__ GroupRows group_rows(const AttnArgs& a, int g, int D) {
+  GroupRows gr;
+  gr.n_pages = gr.sink_end = gr.page_end = gr.recent_start = gr.recent_end = 0;
+  if (MODE == kModePages) {
+    int nu = a.plan_counts[g];
+    nu = nu < 0 ? 0 : (nu > a.plan_stride ? static_cast<int>(a.plan_stride) : nu);
+    const int sink_end = a.sink < a.length ? a.sink : a.length;
+    const int hist_recent = a.recent - 1 > 0 ? a.recent - 1 : 0;
+    const int recent_start = (a.length - hist_recent) > sink_end ? (a.length - hist_recent) : sink_end;
+    gr.n_pages = nu;
+    gr.sink_end = sink_end;
+    gr.page_end = sink_end + nu * a.bs;
+    gr.recent_start = recent_start;
+    gr.recent_end = gr.page_end + (a.length - recent_start);
+    const int n = gr.recent_end + (a.append_position >= 0 ? 1 : 0);
+    gr.n_list = n > a.max_rows ? a.max_rows : n;
+    gr.base = static_cast<int64_t>(g) * a.entry_stride * D;
+    gr.stride = D;
+    gr.win_start = 0;
+  } else if (MODE == kModeRows) {
+    int n = a.counts[g];
+    gr.n_list = n < 0 ? 0 : (n > a.max_rows ? a.max_rows : n);
+    gr.base = static_cast<int64_t>(g) * a.entry_stride * D;
+    gr.stride = D;
+    gr.win_start = 0;
   } else {
     const int b = g / a.Hk;
     const int h = g - b * a.Hk;
     const int s0 = a.cu_k[b];
     int n = a.cu_k[b + 1] - s0;
+    int ws = 0;
     if (a.window_left >= 0 && n > a.window_left + 1) {
-      win_start = n - (a.window_left + 1);
+      ws = n - (a.window_left + 1);
       n = a.window_left + 1;
     }
-    n_list = n < 0 ? 0 : (n > a.max_rows ? a.max_rows : n);
-    seg_base = s0;
-    row_stride = static_cast<int64_t>(a.Hk) * D;
-    head_off = static_cast<int64_t>(h) * D;
+    gr.n_list = n < 0 ? 0 : (n > a.max_rows ? a.max_rows : n);
+    gr.stride = static_cast<int64_t>(a.Hk) * D;
+    gr.base = static_cast<int64_t>(s0) * gr.stride + static_cast<int64_t>(h) * D;
+    gr.win_start = ws;
   }
-  const bool has_cur = a.cur_k != nullptr;
-  const int n_rows = n_list + (has_cur ? 1 : 0);
-  const int rows_per_block = kWaves * RW * a.iters;
-  const int n_chunks = (n_rows + rows_per_block - 1) / rows_per_block;
+  gr.n_rows = gr.n_list + (a.cur_k != nullptr ? 1 : 0);
+  return gr;
+}
+
+// Combine the chunk partials of group g (the calling block is the last one to
+// arrive) and write the output.  s_ml: LDS room for max_chunks * R * 2 floats.
+template <typename DT>
+__device__ void merge_partials(const AttnArgs& a, int g, int D, int n_chunks, float* s_ml) {
+  using S = typename DT::storage;
+  const int R = a.R;
+  const float* ml = a.part_ml + static_cast<int64_t>(g) * a.max_chunks * R * 2;
+  const float* po = a.part_o + static_cast<int64_t>(g) * a.max_chunks * R * D;
+  const int n_ml = n_chunks * R * 2;
+  {
+    // Up to 8 independent loads per thread in one batch.
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = static_cast<int>(threadIdx.x) + j * kBlock;
+      v[j] = fetch_f32(ml + (i < n_ml ? i : 0));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = static_cast<int>(threadIdx.x) + j * kBlock;
+      if (i < n_ml) s_ml[i] = v[j];
+    }
+    for (int i = static_cast<int>(threadIdx.x) + 8 * kBlock; i < n_ml; i += kBlock) s_ml[i] = fetch_f32(ml + i);
+  }
+  __syncthreads();
+  S* out = static_cast<S*>(a.out) + static_cast<int64_t>(g) * R * D;
+  const int half = D / 2;
+  for (int p = threadIdx.x; p < R * half; p += kBlock) {
+    const int r = p / half;
+    const int c = 2 * (p - r * half);
+    float M = -INFINITY;
+    for (int ch = 0; ch < n_chunks; ++ch) M = fmaxf(M, s_ml[(ch * R + r) * 2]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+    for (int cb = 0; cb < n_chunks; cb += kMergeBatch) {
+      float2 ov[kMergeBatch];
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        int ch = cb + j;
+        ch = ch < n_chunks ? ch : n_chunks - 1;
+        ov[j] = fetch_f32x2(po + (static_cast<int64_t>(ch) * R + r) * D + c);
+      }
+#pragma unroll
+      for (int j = 0; j < kMergeBatch; ++j) {
+        const int ch = cb + j;
+        if (ch < n_chunks) {
+          const float w = exp2_rel(s_ml[(ch * R + r) * 2], M);
+          L += w * s_ml[(ch * R + r) * 2 + 1];
+          o0 += w * ov[j].x;
+          o1 += w * ov[j].y;
+        }
+      }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    out[r * D + c] = from_f32(DT{}, o0 * inv);
+    out[r * D + c + 1] = from_f32(DT{}, o1 * inv);
+  }
+}
+
+// Block partial from the wavefront partials in LDS: either the final output
+// (single-chunk groups) or a partial for the merge.
+template <typename DT, int RMAX>
+__device__ void block_partial(const AttnArgs& a, int g, int chunk, int D, bool final_out, const float* s_m,
+                              const float* s_l, const float* s_o) {
+  using S = typename DT::storage;
+  const int R = a.R;
+  for (int idx = threadIdx.x; idx < R * D; idx += kBlock) {
+    const int r = idx / D;
+    const int c = idx - r * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w * RMAX + r]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = exp2_rel(s_m[w * RMAX + r], M);
+      L += f * s_l[w * RMAX + r];
+      O += f * s_o[(w * RMAX + r) * D + c];
+    }
+    if (final_out) {
+      S* out = static_cast<S*>(a.out) + static_cast<int64_t>(g) * R * D;
+      out[idx] = from_f32(DT{}, L > 0.0f ? O / L : 0.0f);
+    } else {
+      const int64_t pc = static_cast<int64_t>(g) * a.max_chunks + chunk;
+      publish_f32(a.part_o + pc * R * D + idx, O);
+      if (c == 0) publish_f32x2(a.part_ml + (pc * R + r) * 2, M, L);
+    }
+  }
+}
+
+template <typename DT, int D, int RMAX, int MODE>
+__global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(AttnArgs a) {
+  using S = typename DT::storage;
+  constexpr int CPL = 8;
+  constexpr int LPR = D / CPL;                       // lanes per row
+  constexpr int RPI = kWave / LPR;                   // rows per load instruction
+  constexpr int STEPS = steps_for(sizeof(S), RMAX);   // load instructions per batch
+  constexpr int RW = STEPS * RPI;                    // rows per wavefront batch
+  constexpr int RB = kWaves * RW;                    // rows per block batch
+  static_assert(RW <= kWave, "one index lane per row");
+
+  const int R = a.R;
+  const int g = blockIdx.x / a.max_chunks;
+  const int chunk = blockIdx.x - g * a.max_chunks;
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int rig = lane / LPR;
+  const int c0 = (lane % LPR) * CPL;
 
   __shared__ int s_flag;
-  __shared__ float s_m[kWaves][RMAX];
-  __shared__ float s_l[kWaves][RMAX];
-  extern __shared__ __align__(16) float s_o[];  // [kWaves][RMAX][D]
+  __shared__ float s_m[kWaves * RMAX];
+  __shared__ float s_l[kWaves * RMAX];
+  extern __shared__ __align__(16) float s_dyn[];   // [kWaves][RMAX][D] then merge scratch
 
-  if (n_rows == 0) {
-    // No keys at all: the output is defined as zeros (block 0 writes it).
+  const GroupRows gr = group_rows<MODE>(a, g, D);
+  const int rows_per_block = RB * a.iters;
+  const int n_chunks = (gr.n_rows + rows_per_block - 1) / rows_per_block;
+  if (gr.n_rows == 0) {
     if (chunk == 0) {
       S* o = static_cast<S*>(a.out) + static_cast<int64_t>(g) * R * D;
       for (int i = threadIdx.x; i < R * D; i += kBlock) o[i] = from_f32(DT{}, 0.0f);
@@ -173,17 +319,23 @@ __global__ __launch_bounds__(kBlock) void decode_attn_kernel(AttnArgs a) {
   }
   if (chunk >= n_chunks) return;
 
-  // ---- query registers: q[r][c0 .. c0+8) * scale * log2(e) ----
+  const S* kbase = static_cast<const S*>(a.k);
+  const S* vbase = static_cast<const S*>(a.v);
+  const S* ck = a.cur_k != nullptr ? static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D : nullptr;
+  const S* cv = a.cur_v != nullptr ? static_cast<const S*>(a.cur_v) + static_cast<int64_t>(g) * D : nullptr;
+
+  // ---- queries (scale * log2 e folded in); rows r >= R are zero ----
   float qv[RMAX][CPL];
   {
     const S* qg = static_cast<const S*>(a.q) + static_cast<int64_t>(g) * R * D;
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
+      Vec8<S> t;
+      t.load(qg + static_cast<int64_t>(r < R ? r : R - 1) * D + c0);
+      float f[CPL];
+      t.template to_float<DT>(f);
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int c = c0 + i;
-        qv[r][i] = (r < R && c < D) ? to_f32(DT{}, qg[static_cast<int64_t>(r) * D + c]) * a.scale_log2 : 0.0f;
-      }
+      for (int i = 0; i < CPL; ++i) qv[r][i] = (r < R) ? f[i] * a.scale_log2 : 0.0f;
     }
   }
 
@@ -196,65 +348,74 @@ __global__ __launch_bounds__(kBlock) void decode_attn_kernel(AttnArgs a) {
     for (int i = 0; i < CPL; ++i) o_acc[r][i] = 0.0f;
   }
 
-  const S* kbase = static_cast<const S*>(a.k);
-  const S* vbase = static_cast<const S*>(a.v);
-  const S* ck = has_cur ? static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D : nullptr;
-  const S* cv = has_cur ? static_cast<const S*>(a.cur_v) + static_cast<int64_t>(g) * D : nullptr;
+  // Row (or page) masks: when there are none, read a byte of the index list
+  // instead and force every head visible (keeps the load unconditional).
+  const int32_t* idx_src = MODE == kModePages ? a.plan_pages : a.rows;
+  const uint8_t* mask_in = MODE == kModePages ? a.plan_masks : a.masks;
+  const uint8_t* mask_src = mask_in != nullptr ? mask_in : reinterpret_cast<const uint8_t*>(idx_src);
+  const uint32_t mask_force = mask_in != nullptr ? 0u : 0xffu;
+  const int64_t list_base = static_cast<int64_t>(g) * (MODE == kModePages ? a.plan_stride : a.rows_stride);
+  const int last_list = MODE == kModePages ? (gr.n_pages > 0 ? gr.n_pages - 1 : 0)
+                                           : (gr.n_list > 0 ? gr.n_list - 1 : 0);
+  const bool bs_pow2 = (a.bs & (a.bs - 1)) == 0;
+  const int bs_shift = bs_pow2 && a.bs > 0 ? __ffs(a.bs) - 1 : 0;
+  // Readable stand-ins for rows that are dropped or not in the list.
+  const S* safe_k = gr.n_list > 0 ? kbase + gr.base : (ck != nullptr ? ck : kbase);
+  const S* safe_v = gr.n_list > 0 ? vbase + gr.base : (cv != nullptr ? cv : vbase);
+  const S* cur_k = ck != nullptr ? ck : safe_k;
+  const S* cur_v = cv != nullptr ? cv : safe_v;
 
-  const int block_row0 = chunk * rows_per_block;
   for (int it = 0; it < a.iters; ++it) {
-    const int wave_row0 = block_row0 + (it * kWaves + wave) * RW;
-    if (wave_row0 >= n_rows) break;
-    ChunkT kc[NSTEP], vc[NSTEP];
-    uint8_t hm[NSTEP];
-    bool valid[NSTEP];
+    const int row0 = chunk * rows_per_block + it * RB + wave * RW;
+    if (row0 >= gr.n_rows) break;
+    // ---- round trip 1: this lane's row indices and masks ----
+    int pos[STEPS];
+    uint32_t hm[STEPS];
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
-      const int i = wave_row0 + s * RPI + rig;
-      valid[s] = i < n_rows;
-      hm[s] = 0xffu;
-      const S* kp;
-      const S* vp;
-      if (!valid[s]) {
-        kp = nullptr;
-        vp = nullptr;
-      } else if (i >= n_list) {
-        kp = ck;
-        vp = cv;
+    for (int s = 0; s < STEPS; ++s) {
+      const int i = row0 + s * RPI + rig;
+      if (MODE == kModeRows) {
+        const int64_t at = list_base + (i < last_list ? i : last_list);
+        pos[s] = a.rows[at];
+        hm[s] = static_cast<uint32_t>(mask_src[at]) | mask_force;
+      } else if (MODE == kModePages) {
+        const int j = i - gr.sink_end;
+        int u = bs_pow2 ? (j >> bs_shift) : j / a.bs;
+        u = u < 0 ? 0 : (u > last_list ? last_list : u);
+        const int64_t at = list_base + u;
+        const int page = a.plan_pages[at];
+        const uint32_t pm = static_cast<uint32_t>(mask_src[at]) | mask_force;
+        const bool in_pages = i >= gr.sink_end && i < gr.page_end;
+        pos[s] = i < gr.sink_end ? i
+                 : in_pages      ? a.sink + page * a.bs + (j - u * a.bs)
+                 : i < gr.recent_end ? gr.recent_start + (i - gr.page_end)
+                                     : a.append_position;
+        hm[s] = in_pages ? pm : 0xffu;
       } else {
-        int64_t pos;
-        if (INDEXED) {
-          pos = a.rows[static_cast<int64_t>(g) * a.rows_stride + i];
-          if (a.masks != nullptr) hm[s] = a.masks[static_cast<int64_t>(g) * a.rows_stride + i];
-          // A position outside the entry is never read (row dropped).
-          if (pos < 0 || pos >= a.entry_stride) {
-            valid[s] = false;
-            pos = 0;
-          }
-        } else {
-          pos = win_start + i;
-        }
-        const int64_t off = (seg_base + pos) * row_stride + head_off;
-        kp = valid[s] ? kbase + off : nullptr;
-        vp = valid[s] ? vbase + off : nullptr;
-      }
-      if (valid[s]) {
-        if constexpr (kGeneric) {
-          kc[s].load(kp + c0, c0, D);
-          vc[s].load(vp + c0, c0, D);
-        } else {
-          kc[s].load(kp + c0);
-          vc[s].load(vp + c0);
-        }
-      } else {
-        kc[s].zero();
-        vc[s].zero();
+        pos[s] = gr.win_start + i;
+        hm[s] = 0xffu;
       }
     }
-    // scores (already in log2 units)
-    float sc[NSTEP][RMAX];
+    // ---- round trip 2: K/V rows ----
+    Vec8<S> kc[STEPS], vc[STEPS];
+    bool ok[STEPS];
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
+    for (int s = 0; s < STEPS; ++s) {
+      const int i = row0 + s * RPI + rig;
+      const bool in_list = i < gr.n_list && (MODE == kModeVarlen || (pos[s] >= 0 && pos[s] < a.entry_stride));
+      const bool cur = i == gr.n_list && i < gr.n_rows;
+      ok[s] = in_list || cur;
+      if (cur) hm[s] = 0xffu;
+      const int64_t off = gr.base + static_cast<int64_t>(in_list ? pos[s] : 0) * gr.stride;
+      const S* kp = cur ? cur_k : (in_list ? kbase + off : safe_k);
+      const S* vp = cur ? cur_v : (in_list ? vbase + off : safe_v);
+      kc[s].load(kp + c0);
+      vc[s].load(vp + c0);
+    }
+    // ---- scores in log2 units ----
+    float sc[STEPS][RMAX];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
       float kf[CPL];
       kc[s].template to_float<DT>(kf);
 #pragma unroll
@@ -266,21 +427,17 @@ __global__ __launch_bounds__(kBlock) void decode_attn_kernel(AttnArgs a) {
       }
     }
 #pragma unroll
-    for (int o = 1; o < LPR; o <<= 1) {
+    for (int s = 0; s < STEPS; ++s) {
 #pragma unroll
-      for (int s = 0; s < NSTEP; ++s) {
-#pragma unroll
-        for (int r = 0; r < RMAX; ++r) sc[s][r] += __shfl_xor(sc[s][r], o);
-      }
+      for (int r = 0; r < RMAX; ++r) sc[s][r] = row_group_sum<LPR>(sc[s][r]);
     }
-    // mask, running max
     float mnew[RMAX];
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int s = 0; s < NSTEP; ++s) {
-        const bool vis = valid[s] && r < R && ((hm[s] >> r) & 1u);
+      for (int s = 0; s < STEPS; ++s) {
+        const bool vis = ok[s] && r < R && ((hm[s] >> r) & 1u);
         sc[s][r] = vis ? sc[s][r] : -INFINITY;
         mx = fmaxf(mx, sc[s][r]);
       }
@@ -296,25 +453,20 @@ __global__ __launch_bounds__(kBlock) void decode_attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < CPL; ++i) o_acc[r][i] *= alpha;
     }
-    float lsum[RMAX];
 #pragma unroll
-    for (int r = 0; r < RMAX; ++r) lsum[r] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
+    for (int s = 0; s < STEPS; ++s) {
       float vf[CPL];
       vc[s].template to_float<DT>(vf);
 #pragma unroll
       for (int r = 0; r < RMAX; ++r) {
-        const float p = (sc[s][r] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sc[s][r] - m_run[r]);
-        lsum[r] += p;
+        const float p = exp2_rel(sc[s][r], m_run[r]);
+        l_run[r] += p;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) o_acc[r][i] = __builtin_fmaf(p, vf[i], o_acc[r][i]);
       }
     }
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r) l_run[r] += lsum[r];
   }
-  // Merge the row groups of the wavefront (same channels, different rows).
+  // ---- merge the row groups of the wavefront (same channels) ----
 #pragma unroll
   for (int r = 0; r < RMAX; ++r) {
 #pragma unroll
@@ -324,113 +476,259 @@ __global__ __launch_bounds__(kBlock) void decode_attn_kernel(AttnArgs a) {
       for (int i = 0; i < CPL; ++i) o_acc[r][i] += __shfl_xor(o_acc[r][i], o);
     }
   }
+  float* s_o = s_dyn;
   if (lane < LPR) {
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
-      if (r < R) {
-        if (lane == 0) {
-          s_m[wave][r] = m_run[r];
-          s_l[wave][r] = l_run[r];
-        }
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
-          const int c = c0 + i;
-          if (c < D) s_o[(wave * RMAX + r) * D + c] = o_acc[r][i];
-        }
+      if (lane == 0) {
+        s_m[wave * RMAX + r] = m_run[r];
+        s_l[wave * RMAX + r] = l_run[r];
       }
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) s_o[(wave * RMAX + r) * D + c0 + i] = o_acc[r][i];
     }
   }
   __syncthreads();
-  // Block partial: merge the wavefront partials (waves with no rows hold
-  // m = -inf, l = 0, acc = 0).
-  float* part = a.partials + (static_cast<int64_t>(g) * a.max_chunks + chunk) * R * (2 + D);
-  for (int idx = threadIdx.x; idx < R * D; idx += kBlock) {
-    const int r = idx / D;
-    const int c = idx - r * D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][r]);
-    float L = 0.0f, O = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = (s_m[w][r] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_m[w][r] - M);
-      L += f * s_l[w][r];
-      O += f * s_o[(w * RMAX + r) * D + c];
-    }
-    float* pr = part + r * (2 + D);
-    if (c == 0) {
-      pr[0] = M;
-      pr[1] = L;
-    }
-    pr[2 + c] = O;
-  }
+  block_partial<DT, RMAX>(a, g, chunk, D, n_chunks == 1, s_m, s_l, s_o);
+  if (n_chunks == 1) return;
   if (!arrive_last(a.counters + g, static_cast<unsigned int>(n_chunks), &s_flag)) return;
+  merge_partials<DT>(a, g, D, n_chunks, s_dyn + kWaves * RMAX * D);
+}
 
-  // ---- last block of the group: merge all chunk partials ----
-  const float* gp = a.partials + static_cast<int64_t>(g) * a.max_chunks * R * (2 + D);
-  S* out = static_cast<S*>(a.out) + static_cast<int64_t>(g) * R * D;
-  for (int idx = threadIdx.x; idx < R * D; idx += kBlock) {
-    const int r = idx / D;
-    const int c = idx - r * D;
-    float M = -INFINITY;
-    for (int ch = 0; ch < n_chunks; ++ch) M = fmaxf(M, gp[(ch * R + r) * (2 + D)]);
-    float L = 0.0f, O = 0.0f;
-    for (int ch = 0; ch < n_chunks; ++ch) {
-      const float* pr = gp + (ch * R + r) * (2 + D);
-      const float f = (pr[0] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(pr[0] - M);
-      L += f * pr[1];
-      O += f * pr[2 + c];
+// Generic head dimension (any even D <= 512): one row per wavefront step,
+// lane owns channels lane + 64 j.  Correctness path for unusual shapes.
+template <typename DT, int RMAX, int MODE>
+__global__ __launch_bounds__(kBlock) void decode_attn_generic(AttnArgs a) {
+  using S = typename DT::storage;
+  constexpr int JMAX = 8;  // D <= 512
+  const int R = a.R;
+  const int D = a.D;
+  const int g = blockIdx.x / a.max_chunks;
+  const int chunk = blockIdx.x - g * a.max_chunks;
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  __shared__ int s_flag;
+  __shared__ float s_m[kWaves * RMAX];
+  __shared__ float s_l[kWaves * RMAX];
+  extern __shared__ __align__(16) float s_dyn[];
+
+  const GroupRows gr = group_rows<MODE>(a, g, D);
+  const int rows_per_block = kWaves * 16 * a.iters;
+  const int n_chunks = (gr.n_rows + rows_per_block - 1) / rows_per_block;
+  if (gr.n_rows == 0) {
+    if (chunk == 0) {
+      S* o = static_cast<S*>(a.out) + static_cast<int64_t>(g) * R * D;
+      for (int i = threadIdx.x; i < R * D; i += kBlock) o[i] = from_f32(DT{}, 0.0f);
     }
-    out[idx] = from_f32(DT{}, L > 0.0f ? O / L : 0.0f);
+    return;
   }
+  if (chunk >= n_chunks) return;
+  const S* kbase = static_cast<const S*>(a.k);
+  const S* vbase = static_cast<const S*>(a.v);
+  const S* qg = static_cast<const S*>(a.q) + static_cast<int64_t>(g) * R * D;
+  float m_run[RMAX], l_run[RMAX], o_acc[RMAX][JMAX];
+#pragma unroll
+  for (int r = 0; r < RMAX; ++r) {
+    m_run[r] = -INFINITY;
+    l_run[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) o_acc[r][j] = 0.0f;
+  }
+  const int first = chunk * rows_per_block;
+  const int last = min(first + rows_per_block, gr.n_rows);
+  for (int i = first + wave; i < last; i += kWaves) {
+    const S* kp;
+    const S* vp;
+    uint32_t m = 0xffu;
+    bool ok = true;
+    if (i >= gr.n_list) {
+      kp = static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D;
+      vp = static_cast<const S*>(a.cur_v) + static_cast<int64_t>(g) * D;
+    } else {
+      int64_t pos;
+      if (MODE == kModeRows) {
+        const int64_t at = static_cast<int64_t>(g) * a.rows_stride + i;
+        pos = a.rows[at];
+        if (a.masks != nullptr) m = a.masks[at];
+        if (pos < 0 || pos >= a.entry_stride) ok = false;
+      } else if (MODE == kModePages) {
+        if (i < gr.sink_end) {
+          pos = i;
+        } else if (i < gr.page_end) {
+          const int j = i - gr.sink_end;
+          const int u = j / a.bs;
+          const int64_t at = static_cast<int64_t>(g) * a.plan_stride + u;
+          pos = a.sink + static_cast<int64_t>(a.plan_pages[at]) * a.bs + (j - u * a.bs);
+          if (a.plan_masks != nullptr) m = a.plan_masks[at];
+        } else if (i < gr.recent_end) {
+          pos = gr.recent_start + (i - gr.page_end);
+        } else {
+          pos = a.append_position;
+        }
+        if (pos < 0 || pos >= a.entry_stride) ok = false;
+      } else {
+        pos = gr.win_start + i;
+      }
+      if (!ok) continue;
+      kp = kbase + gr.base + pos * gr.stride;
+      vp = vbase + gr.base + pos * gr.stride;
+    }
+    float s[RMAX];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+      float acc = 0.0f;
+      if (r < R) {
+#pragma unroll
+        for (int j = 0; j < JMAX; ++j) {
+          const int c = lane + kWave * j;
+          if (c < D) acc = __builtin_fmaf(to_f32(DT{}, qg[r * D + c]) * a.scale_log2, to_f32(DT{}, kp[c]), acc);
+        }
+      }
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) acc += __shfl_xor(acc, o);
+      s[r] = (r < R && ((m >> r) & 1u)) ? acc : -INFINITY;
+    }
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+      const float mn = fmaxf(m_run[r], s[r]);
+      const float alpha = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run[r] - mn);
+      const float p = exp2_rel(s[r], mn);
+      m_run[r] = mn;
+      l_run[r] = l_run[r] * alpha + p;
+#pragma unroll
+      for (int j = 0; j < JMAX; ++j) {
+        const int c = lane + kWave * j;
+        const float vf = c < D ? to_f32(DT{}, vp[c]) : 0.0f;
+        o_acc[r][j] = o_acc[r][j] * alpha + p * vf;
+      }
+    }
+  }
+  float* s_o = s_dyn;
+#pragma unroll
+  for (int r = 0; r < RMAX; ++r) {
+    if (lane == 0) {
+      s_m[wave * RMAX + r] = m_run[r];
+      s_l[wave * RMAX + r] = l_run[r];
+    }
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) {
+      const int c = lane + kWave * j;
+      if (c < D) s_o[(wave * RMAX + r) * D + c] = o_acc[r][j];
+    }
+  }
+  __syncthreads();
+  block_partial<DT, RMAX>(a, g, chunk, D, n_chunks == 1, s_m, s_l, s_o);
+  if (n_chunks == 1) return;
+  if (!arrive_last(a.counters + g, static_cast<unsigned int>(n_chunks), &s_flag)) return;
+  merge_partials<DT>(a, g, D, n_chunks, s_dyn + kWaves * RMAX * D);
 }
 
-int rows_per_wave_iter(int dtype, int D) {
-  const bool generic = !(D == 64 || D == 128 || D == 256);
-  const int lpr = generic ? 64 : D / 8;
+bool fast_d(int D) { return D == 64 || D == 128 || D == 256; }
+
+int rmax_for(int R) { return R <= 1 ? 1 : (R <= 2 ? 2 : (R <= 4 ? 4 : 8)); }
+
+// Rows of one block batch.
+int rows_per_batch(int dtype, int D, int R) {
+  if (!fast_d(D)) return kWaves * 16;
+  const int lpr = D / 8;
   const int rpi = kWave / lpr;
-  const int nstep = dtype == TW_DTYPE_F32 ? 4 : 8;
-  return nstep * rpi;
+  return kWaves * steps_for(dtype == TW_DTYPE_F32 ? 4 : 2, rmax_for(R)) * rpi;
 }
 
-constexpr int kIters = 2;
+// Batches per block and chunks per group for a bound on the rows.  About
+// 1024 blocks fill the chip (3 resident blocks per CU); a group never has
+// more than kMaxChunks chunks, so the last block merges every partial in at
+// most two batched round trips.
+void plan_chunks(int dtype, int G, int R, int D, int max_rows_total, int* iters, int* chunks) {
+  const int rb = rows_per_batch(dtype, D, R);
+  int target = 1024 / (G > 0 ? G : 1);
+  target = target < 1 ? 1 : (target > kMaxChunks ? kMaxChunks : target);
+  int it = (max_rows_total + rb * target - 1) / (rb * target);
+  it = it < 1 ? 1 : it;
+  int ch = (max_rows_total + rb * it - 1) / (rb * it);
+  *iters = it;
+  *chunks = ch < 1 ? 1 : ch;
+}
 
-template <typename DT, int DFIX, bool INDEXED>
-int launch_r(const AttnArgs& a, hipStream_t stream) {
-  const size_t lds_o = static_cast<size_t>(kWaves) * 8 * a.D * sizeof(float);
+size_t dyn_lds_bytes(int R, int D, int chunks) {
+  return (static_cast<size_t>(kWaves) * rmax_for(R) * D + static_cast<size_t>(chunks) * R * 2) * sizeof(float);
+}
+
+template <typename DT, int D, int RMAX, int MODE>
+int launch_one(const AttnArgs& a, hipStream_t stream) {
+  const size_t lds = dyn_lds_bytes(a.R, a.D, a.max_chunks);
   const dim3 grid(a.G * a.max_chunks);
-  if (a.R <= 1) {
-    hipLaunchKernelGGL((decode_attn_kernel<DT, DFIX, 1, INDEXED>), grid, dim3(kBlock), lds_o, stream, a);
-  } else if (a.R <= 2) {
-    hipLaunchKernelGGL((decode_attn_kernel<DT, DFIX, 2, INDEXED>), grid, dim3(kBlock), lds_o, stream, a);
-  } else if (a.R <= 4) {
-    hipLaunchKernelGGL((decode_attn_kernel<DT, DFIX, 4, INDEXED>), grid, dim3(kBlock), lds_o, stream, a);
+  if constexpr (D > 0) {
+    auto kern = decode_attn_kernel<DT, D, RMAX, MODE>;
+    if (lds > 64 * 1024)
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds));
+    hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, stream, a);
   } else {
-    hipLaunchKernelGGL((decode_attn_kernel<DT, DFIX, 8, INDEXED>), grid, dim3(kBlock), lds_o, stream, a);
+    auto kern = decode_attn_generic<DT, RMAX, MODE>;
+    if (lds > 64 * 1024)
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds));
+    hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, stream, a);
   }
   return tw_host::check_launch();
 }
 
-template <typename DT, bool INDEXED>
+template <typename DT, int D, int MODE>
+int launch_r(const AttnArgs& a, hipStream_t stream) {
+  switch (rmax_for(a.R)) {
+    case 1: return launch_one<DT, D, 1, MODE>(a, stream);
+    case 2: return launch_one<DT, D, 2, MODE>(a, stream);
+    case 4: return launch_one<DT, D, 4, MODE>(a, stream);
+    default: return launch_one<DT, D, 8, MODE>(a, stream);
+  }
+}
+
+template <typename DT, int MODE>
 int launch_d(const AttnArgs& a, hipStream_t stream) {
   switch (a.D) {
-    case 64: return launch_r<DT, 64, INDEXED>(a, stream);
-    case 128: return launch_r<DT, 128, INDEXED>(a, stream);
-    case 256: return launch_r<DT, 256, INDEXED>(a, stream);
-    default: return launch_r<DT, 0, INDEXED>(a, stream);
+    case 64: return launch_r<DT, 64, MODE>(a, stream);
+    case 128: return launch_r<DT, 128, MODE>(a, stream);
+    case 256: return launch_r<DT, 256, MODE>(a, stream);
+    default: return launch_r<DT, 0, MODE>(a, stream);
   }
 }
 
 template <typename DT>
 int launch_mode(const AttnArgs& a, hipStream_t stream) {
-  return a.rows != nullptr ? launch_d<DT, true>(a, stream) : launch_d<DT, false>(a, stream);
+  if (a.plan_pages != nullptr) return launch_d<DT, kModePages>(a, stream);
+  return a.rows != nullptr ? launch_d<DT, kModeRows>(a, stream) : launch_d<DT, kModeVarlen>(a, stream);
+}
+
+int launch_dtype(int dtype, const AttnArgs& a, hipStream_t s) {
+  switch (dtype) {
+    case TW_DTYPE_F16: return launch_mode<F16>(a, s);
+    case TW_DTYPE_BF16: return launch_mode<BF16>(a, s);
+    default: return launch_mode<F32>(a, s);
+  }
 }
 
 size_t counter_bytes(int G) { return ((static_cast<size_t>(G) * 4 + 255) / 256) * 256; }
 
-int max_chunks_for(int dtype, int D, int max_rows_total) {
-  const int per_block = kWaves * rows_per_wave_iter(dtype, D) * kIters;
-  return (max_rows_total + per_block - 1) / per_block;
+// Workspace layout: counters | part_ml | part_o, sized for the largest chunk
+// count any dtype can produce for max_rows (+1 decode token).
+void workspace_layout(int G, int R, int D, int max_rows, size_t* ml_off, size_t* o_off, size_t* total) {
+  // The chunk count is not monotonic in the row bound (more rows can mean
+  // more batches per block and fewer chunks), so take the largest over both
+  // bounds a launch may use, with and without the decode token.
+  int chunks_max = 1;
+  for (int dt : {TW_DTYPE_F16, TW_DTYPE_F32}) {
+    for (int extra = 0; extra <= 1; ++extra) {
+      int it, ch;
+      plan_chunks(dt, G, R, D, max_rows + extra, &it, &ch);
+      chunks_max = ch > chunks_max ? ch : chunks_max;
+    }
+  }
+  const size_t chunks = static_cast<size_t>(chunks_max);
+  const size_t ml = static_cast<size_t>(G) * chunks * R * 2 * sizeof(float);
+  *ml_off = counter_bytes(G);
+  *o_off = *ml_off + ((ml + 255) / 256) * 256;
+  *total = *o_off + static_cast<size_t>(G) * chunks * R * D * sizeof(float);
 }
 
 }  // namespace
@@ -438,10 +736,9 @@ int max_chunks_for(int dtype, int D, int max_rows_total) {
 
 extern "C" size_t tw_decode_attention_workspace_size(int G, int R, int D, int max_rows) {
   if (G <= 0 || R <= 0 || D <= 0 || max_rows < 0) return 0;
-  // +1 row: the decode token; sized for the largest rows-per-block layout
-  // (fp32 has fewer rows per block than 16-bit types).
-  const int chunks = tw::max_chunks_for(TW_DTYPE_F32, D, max_rows + 1);
-  return tw::counter_bytes(G) + static_cast<size_t>(G) * (chunks > 0 ? chunks : 1) * R * (2 + D) * sizeof(float);
+  size_t ml, o, total;
+  tw::workspace_layout(G, R, D, max_rows, &ml, &o, &total);
+  return total;
 }
 
 extern "C" int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
@@ -450,26 +747,31 @@ extern "C" int tw_decode_attention(const void* q, const void* k_base, const void
                                    int Hk, int window_left, int max_rows, const void* cur_k, const void* cur_v,
                                    float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
                                    void* stream) {
-  if (q == nullptr || out == nullptr || G <= 0 || R <= 0 || R > 8 || D <= 0 || D > 512 || max_rows < 0)
+  if (q == nullptr || out == nullptr || G <= 0 || R <= 0 || R > 8 || D <= 0 || D > 512 || (D % 2) != 0 ||
+      max_rows < 0)
     return TW_EINVAL;
+  if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16 && dtype != TW_DTYPE_F32) return TW_EINVAL;
   if ((cur_k == nullptr) != (cur_v == nullptr)) return TW_EINVAL;
   if (max_rows > 0 && (k_base == nullptr || v_base == nullptr)) return TW_EINVAL;
   if (rows != nullptr) {
-    if (row_counts == nullptr || rows_stride < max_rows) return TW_EINVAL;
+    // rows_stride >= 1: every block may read entry 0 of its group's list.
+    if (row_counts == nullptr || rows_stride < max_rows || rows_stride < 1 || entry_stride_rows <= 0)
+      return TW_EINVAL;
   } else {
     if (row_masks != nullptr || cu_seqlens_k == nullptr || Hk <= 0 || (G % Hk) != 0) return TW_EINVAL;
   }
-  const bool fast = (D == 64 || D == 128 || D == 256);
   const int es = dtype == TW_DTYPE_F32 ? 4 : 2;
-  if (fast) {
+  if (tw::fast_d(D)) {
     const uintptr_t align = 16;
-    if ((reinterpret_cast<uintptr_t>(k_base) % align) || (reinterpret_cast<uintptr_t>(v_base) % align) ||
-        (cur_k && (reinterpret_cast<uintptr_t>(cur_k) % align)) || (cur_v && (reinterpret_cast<uintptr_t>(cur_v) % align)))
+    if ((reinterpret_cast<uintptr_t>(q) % align) || (reinterpret_cast<uintptr_t>(k_base) % align) ||
+        (reinterpret_cast<uintptr_t>(v_base) % align) || (cur_k && (reinterpret_cast<uintptr_t>(cur_k) % align)) ||
+        (cur_v && (reinterpret_cast<uintptr_t>(cur_v) % align)))
       return TW_EINVAL;
     if (rows == nullptr && ((static_cast<int64_t>(Hk) * D * es) % 16) != 0) return TW_EINVAL;
   }
-  if (workspace == nullptr || workspace_bytes < tw_decode_attention_workspace_size(G, R, D, max_rows))
-    return TW_ENOMEM;
+  size_t ml_off, o_off, total;
+  tw::workspace_layout(G, R, D, max_rows, &ml_off, &o_off, &total);
+  if (workspace == nullptr || workspace_bytes < total) return TW_ENOMEM;
   tw::AttnArgs a{};
   a.q = q;
   a.k = k_base;
@@ -490,16 +792,60 @@ extern "C" int tw_decode_attention(const void* q, const void* k_base, const void
   a.scale_log2 = softmax_scale * tw::kLog2e;
   a.out = out;
   a.counters = static_cast<unsigned int*>(workspace);
-  a.partials = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + tw::counter_bytes(G));
-  a.iters = tw::kIters;
+  a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ml_off);
+  a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
   a.max_rows = max_rows;
-  a.max_chunks = tw::max_chunks_for(dtype, D, max_rows + (cur_k != nullptr ? 1 : 0));
-  if (a.max_chunks <= 0) a.max_chunks = 1;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case TW_DTYPE_F16: return tw::launch_mode<tw::F16>(a, s);
-    case TW_DTYPE_BF16: return tw::launch_mode<tw::BF16>(a, s);
-    case TW_DTYPE_F32: return tw::launch_mode<tw::F32>(a, s);
-    default: return TW_EINVAL;
+  tw::plan_chunks(dtype, G, R, D, max_rows + (cur_k != nullptr ? 1 : 0), &a.iters, &a.max_chunks);
+  return tw::launch_dtype(dtype, a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tw_decode_attention_pages(const void* q, const void* k_base, const void* v_base, int dtype, int G,
+                                         int R, int D, const int32_t* plan_pages, const uint8_t* plan_masks,
+                                         const int32_t* plan_counts, int64_t plan_stride, int max_rows,
+                                         int64_t entry_stride_rows, int sink, int recent, int block_size,
+                                         int length, int append_position, float softmax_scale, void* out,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr || G <= 0 || R <= 0 || R > 8 ||
+      D <= 0 || D > 512 || (D % 2) != 0 || max_rows < 0)
+    return TW_EINVAL;
+  if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16 && dtype != TW_DTYPE_F32) return TW_EINVAL;
+  if (plan_pages == nullptr || plan_counts == nullptr || plan_stride < 1 || entry_stride_rows <= 0) return TW_EINVAL;
+  if (sink < 0 || recent <= 0 || block_size <= 0 || length < 0 || append_position >= entry_stride_rows)
+    return TW_EINVAL;
+  if (tw::fast_d(D)) {
+    const uintptr_t align = 16;
+    if ((reinterpret_cast<uintptr_t>(q) % align) || (reinterpret_cast<uintptr_t>(k_base) % align) ||
+        (reinterpret_cast<uintptr_t>(v_base) % align))
+      return TW_EINVAL;
   }
+  size_t ml_off, o_off, total;
+  tw::workspace_layout(G, R, D, max_rows, &ml_off, &o_off, &total);
+  if (workspace == nullptr || workspace_bytes < total) return TW_ENOMEM;
+  tw::AttnArgs a{};
+  a.q = q;
+  a.k = k_base;
+  a.v = v_base;
+  a.G = G;
+  a.R = R;
+  a.D = D;
+  a.entry_stride = entry_stride_rows;
+  a.plan_pages = plan_pages;
+  a.plan_masks = plan_masks;
+  a.plan_counts = plan_counts;
+  a.plan_stride = plan_stride;
+  a.sink = sink;
+  a.recent = recent;
+  a.bs = block_size;
+  a.length = length;
+  a.append_position = append_position;
+  a.Hk = 1;
+  a.window_left = -1;
+  a.scale_log2 = softmax_scale * tw::kLog2e;
+  a.out = out;
+  a.counters = static_cast<unsigned int*>(workspace);
+  a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ml_off);
+  a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
+  a.max_rows = max_rows;
+  tw::plan_chunks(dtype, G, R, D, max_rows, &a.iters, &a.max_chunks);
+  return tw::launch_dtype(dtype, a, static_cast<hipStream_t>(stream));
 }

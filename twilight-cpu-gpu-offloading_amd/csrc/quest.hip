@@ -1,27 +1,38 @@
 // Quest page selection: upper-bound page score, top-k pages per query head,
-// and the per-KV-group row plan consumed by the sparse decode attention.
+// and the per-KV-group union plan consumed by the sparse decode attention.
 //
 // Reference: fused_quest_score / _score (twilight_fused_quest.py:12-46),
 // QuestTopKOffloadedCache.prepare_layer_selection (quest_offload_cache.py:
 // 299-401) and the page -> token expansion of _selected_positions (:403-511).
 //
-// Score order (bit-exact with the reference for D = 128): 32 accumulators,
-// accumulator l adds the products of channels l, l+32, l+64, l+96 in that
-// order starting from +0; the 32 accumulators are then summed by an
-// adjacent-pair tree (the lane-0 result of shuffle-adds at offsets 1..16).
-// Each product is f32(q_d > 0 ? max_d : min_d) * q_d, never fused with the add.
+// Two kernels per layer:
 //
-// Work split: a block of 4 wavefronts scores a tile of 64 pages of one KV
-// group for all R query heads.  The tile is staged once in LDS with 16-byte
-// loads (padded row pitch, conflict-free column reads); wavefront w then
-// scores head w (w+4, ...) with lane = page, so the q > 0 choice of min or max
-// is wave-uniform and each lane reads exactly one value per channel.
+// 1. Scores.  A block of 4 wavefronts scores a tile of 64 pages of one KV
+//    group for all R query heads.  The tile is staged once in LDS with
+//    16-byte loads (padded row pitch, conflict-free column reads); wavefront
+//    w then scores head w (w+4, ...) with lane = page, so the q > 0 choice of
+//    min or max is wave-uniform.  Order (bit-exact with the reference for
+//    D = 128): 32 accumulators, accumulator l adds the products of channels
+//    l, l+32, l+64, l+96 in that order starting from +0; the 32 accumulators
+//    are then summed by an adjacent-pair tree (the lane-0 result of
+//    shuffle-adds at offsets 1..16).  Each product is
+//    f32(q_d > 0 ? max_d : min_d) * q_d, never fused with the add.
 //
-// Selection: the block that finishes a group last (arrival counter, no
-// waiting) runs one radix select per head -- 8-bit digits, LDS histogram,
-// suffix scan to find the k-th largest key -- and an ordered ballot
-// compaction that emits page ids ascending with ties to the lowest index.
-// It then builds the group's row plan from an LDS page-mask table.
+// 2. Selection.  One block of 256 threads per (group, head) row finds the k
+//    largest scores (order key: NaN highest, -0 == +0, ties to the lowest
+//    page).  Each thread holds a contiguous run of the row's keys in
+//    registers.  A pass histograms the remaining candidates into bins that
+//    are monotone in the key -- 2048 bins linear in the score value over the
+//    candidates' range when that range is finite, else the next 8-bit digit
+//    below the candidates' common key prefix -- finds the bin holding the
+//    k-th largest, takes every candidate above it and keeps the bin's keys
+//    as the next candidates.  At most 256 candidates are ranked exactly by
+//    (key desc, index asc); equal candidates are taken lowest index first.
+//    The winners are emitted in ascending page order.  The last block of a
+//    group (arrival counter, device-coherent handoff) ORs the R selections
+//    into a page mask and writes the union plan: the ascending union pages
+//    with the bitmask of heads that selected each, and optionally the
+//    expanded row plan (sink ++ union page rows ++ recent ++ decode row).
 #pragma clang fp contract(off)
 
 #include "tw_common.h"
@@ -31,9 +42,12 @@ namespace {
 
 constexpr int kTilePages = 64;
 constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
 constexpr int kMaxD = 256;
-constexpr int kMaxPlanPages = 16384;
+constexpr int kMaxSelPages = 8192;
+constexpr int kLinBins = 2048;
 
+// ------------------------------------------------------------------ scores
 __device__ __forceinline__ float lds_load(const uint8_t* p, F16) {
   return to_f32(F16{}, *reinterpret_cast<const uint16_t*>(p));
 }
@@ -58,18 +72,9 @@ struct ScoreArgs {
   const void* pmax;
   int64_t group_stride;    // elements
   int G, R, P, D;
-  float* scores;           // [G][R][P]
-};
-
-struct SelectArgs {
-  int k;
-  int32_t* sel_pages;      // nullable [G][R][k]
-  int32_t* rows;           // nullable [G][rows_stride]
-  uint8_t* row_masks;      // nullable
-  int32_t* row_counts;     // nullable [G]
-  int64_t rows_stride;
-  int sink, recent, bs, length, append_position;
-  unsigned int* counters;  // [G]
+  float* scores;           // [G][R][score_stride]
+  int64_t score_stride;
+  float* scores_out;       // nullable [G][R][P]
 };
 
 // Stage a tile of pages (min then max) into LDS with a padded pitch.
@@ -80,9 +85,8 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
   const int words = row_bytes / 4;  // D even -> row_bytes % 4 == 0
   const S* mn = static_cast<const S*>(a.pmin) + g * a.group_stride + static_cast<int64_t>(p0) * a.D;
   const S* mx = static_cast<const S*>(a.pmax) + g * a.group_stride + static_cast<int64_t>(p0) * a.D;
-  // Source rows are contiguous; copy dword by dword (pitch is dword aligned).
-  const int total = 2 * np * words;
-  const bool vec4 = (words % 4) == 0 && ((reinterpret_cast<uintptr_t>(mn) | reinterpret_cast<uintptr_t>(mx)) % 16) == 0;
+  const bool vec4 =
+      (words % 4) == 0 && ((reinterpret_cast<uintptr_t>(mn) | reinterpret_cast<uintptr_t>(mx)) % 16) == 0;
   if (vec4) {
     const int quads = words / 4;
     for (int i = threadIdx.x; i < 2 * np * quads; i += blockDim.x) {
@@ -98,6 +102,7 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
       dst[3] = v.w;
     }
   } else {
+    const int total = 2 * np * words;
     for (int i = threadIdx.x; i < total; i += blockDim.x) {
       const int which = i / (np * words);
       const int rem = i - which * np * words;
@@ -110,15 +115,29 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
 }
 
 template <typename DT, int DFIX>
-__device__ __forceinline__ void score_tile(const ScoreArgs& a, int g, int p0, int np, const uint8_t* lds,
-                                           int pitch) {
+__global__ __launch_bounds__(kBlock) void quest_score_kernel(ScoreArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
   using S = typename DT::storage;
+  const int tiles = (a.P + kTilePages - 1) / kTilePages;
+  const int g = blockIdx.x / tiles;
+  const int tile = blockIdx.x - g * tiles;
+  const int p0 = tile * kTilePages;
+  const int np = (a.P - p0) < kTilePages ? (a.P - p0) : kTilePages;
+  const int pitch = a.D * static_cast<int>(sizeof(S)) + 4;
+  // The group's queries go to LDS in the same round trip as the tile.
+  float* q_lds = reinterpret_cast<float*>(lds + 2 * kTilePages * pitch);
+  {
+    const float* qg = a.q + static_cast<int64_t>(g) * a.R * a.D;
+    for (int i = threadIdx.x; i < a.R * a.D; i += blockDim.x) q_lds[i] = qg[i];
+  }
+  stage_tile<DT>(a, g, p0, np, lds, pitch);
+  __syncthreads();
   const int es = static_cast<int>(sizeof(S));
   const int wave = wave_uniform(static_cast<int>(threadIdx.x) / kWave);
   const int lane = lane_id();
   const int D = DFIX > 0 ? DFIX : a.D;
-  for (int r = wave; r < a.R; r += kBlock / kWave) {
-    const float* qh = a.q + (static_cast<int64_t>(g) * a.R + r) * D;
+  for (int r = wave; r < a.R; r += kWaves) {
+    const float* qh = q_lds + r * D;
     float acc[32];
 #pragma unroll
     for (int l = 0; l < 32; ++l) acc[l] = 0.0f;
@@ -147,123 +166,295 @@ __device__ __forceinline__ void score_tile(const ScoreArgs& a, int g, int p0, in
       }
     }
     const float s = tree32(acc);
-    if (lane < np) a.scores[(static_cast<int64_t>(g) * a.R + r) * a.P + p0 + lane] = s;
+    if (lane < np) {
+      const int64_t row = static_cast<int64_t>(g) * a.R + r;
+      a.scores[row * a.score_stride + p0 + lane] = s;
+      if (a.scores_out != nullptr) a.scores_out[row * a.P + p0 + lane] = s;
+    }
   }
 }
 
-__device__ __forceinline__ void wave_lds_fence() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-}
+// --------------------------------------------------------------- selection
+struct SelectArgs {
+  const float* scores;     // row (g, r) at + (g*R + r)*score_stride
+  int64_t score_stride;
+  int vec_last4;           // vector loads: last readable float4 start of a row
+  int G, R, P, k;
+  int32_t* sel_ws;         // [G][R][k] (published; read by the union)
+  int32_t* sel_out;        // nullable [G][R][k]
+  int64_t* sel_out64;      // nullable [G][R][k]
+  bool want_union;
+  int32_t* plan_pages;     // nullable [G][plan_stride]
+  uint8_t* plan_masks;     // nullable
+  int32_t* plan_counts;    // nullable [G]
+  int64_t plan_stride;
+  int32_t* rows;           // nullable [G][rows_stride]
+  uint8_t* row_masks;      // nullable
+  int32_t* row_counts;     // nullable [G]
+  int64_t rows_stride;
+  int sink, recent, bs, length, append_position;
+  unsigned int* counters;  // [G]
+};
 
-// Radix select of the k largest values (score_key order, ties -> lowest
-// index) of vals[0..P); emit(slot, index) is called with ascending indices
-// and slot = rank in ascending-index order.  hist: 256 LDS words owned by the
-// calling wavefront.
-template <typename Emit>
-__device__ void wave_topk(const float* __restrict__ vals, int P, int k, uint32_t* hist, Emit emit) {
+struct SelShared {
+  uint32_t hist[kLinBins + 64];
+  uint32_t ckey[kBlock];
+  int32_t cidx[kBlock];
+  uint32_t selbits[kMaxSelPages / 32];
+  uint32_t red_max[kWaves];
+  uint32_t red_min[kWaves];
+  int scan[kWaves];
+  int bnd;
+  uint32_t bnd_above;
+  uint32_t bnd_count;
+  int flag;
+};
+
+__device__ __forceinline__ float key_value(uint32_t key) { return __uint_as_float(from_order_key32(key)); }
+
+// Exclusive prefix of v over the block's threads (thread order); *total gets
+// the block sum.  Two barriers, so consecutive calls never race on scan[].
+__device__ __forceinline__ int block_excl_scan(int v, int* scan, int* total) {
   const int lane = lane_id();
-  uint32_t prefix = 0u, mask = 0u;
-  uint32_t need = static_cast<uint32_t>(k);
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = lane; b < 256; b += kWave) hist[b] = 0u;
-    wave_lds_fence();
-    for (int i = lane; i < P; i += kWave) {
-      const uint32_t key = score_key(vals[i]);
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-    }
-    wave_lds_fence();
-    const uint32_t c0 = hist[4 * lane], c1 = hist[4 * lane + 1], c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
-    const uint32_t tot = c0 + c1 + c2 + c3;
-    const uint32_t incl = wave_suffix_sum_u32(tot);
-    const uint32_t above = incl - tot;
-    const bool has = above < need && need <= incl;
-    int bin = 0;
-    uint32_t new_above = above, bin_count = 0;
-    if (has) {
-      uint32_t acc = above;
-      if (need <= acc + c3) {
-        bin = 4 * lane + 3;
-        bin_count = c3;
-      } else if (acc += c3, need <= acc + c2) {
-        bin = 4 * lane + 2;
-        bin_count = c2;
-      } else if (acc += c2, need <= acc + c1) {
-        bin = 4 * lane + 1;
-        bin_count = c1;
-      } else {
-        acc += c1;
-        bin = 4 * lane;
-        bin_count = c0;
-      }
-      new_above = acc;
-    }
-    const int src = first_lane(__ballot(has));
-    bin = __shfl(bin, src);
-    new_above = __shfl(new_above, src);
-    bin_count = __shfl(bin_count, src);
-    need -= new_above;
-    prefix |= static_cast<uint32_t>(bin) << shift;
-    mask |= 255u << shift;
-    wave_lds_fence();
-    if (bin_count == need) break;
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int incl = wave_prefix_sum_i32(v);
+  if (lane == kWave - 1) scan[wave] = incl;
+  __syncthreads();
+  int before = 0, sum = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int t = scan[w];
+    before += w < wave ? t : 0;
+    sum += t;
   }
-  // Ordered compaction: indices ascending; keys strictly above the prefix are
-  // all taken, keys equal to it are taken lowest index first.
-  uint32_t out = 0u, eq_seen = 0u;
-  const uint64_t lt = lanemask_lt();
-  for (int base = 0; base < P; base += kWave) {
-    const int i = base + lane;
-    const bool valid = i < P;
-    const uint32_t mk = valid ? (score_key(vals[i]) & mask) : 0u;
-    const bool gt = valid && mk > prefix;
-    const bool eq = valid && mk == prefix;
-    const uint64_t eqb = __ballot(eq);
-    const uint32_t eq_rank = static_cast<uint32_t>(__popcll(eqb & lt));
-    const bool take = gt || (eq && eq_seen + eq_rank < need);
-    const uint64_t tb = __ballot(take);
-    if (take) emit(static_cast<int>(out + static_cast<uint32_t>(__popcll(tb & lt))), i);
-    out += static_cast<uint32_t>(__popcll(tb));
-    eq_seen += static_cast<uint32_t>(__popcll(eqb));
-  }
+  __syncthreads();
+  *total = sum;
+  return before + incl - v;
 }
 
-// Row plan of one group from the LDS page-mask table (byte per page).
-__device__ void build_row_plan(const SelectArgs& s, int g, int R, int P, const uint8_t* page_mask,
-                               int32_t* upage, uint8_t* umask, int* s_scan) {
+// Bin of a key in the current pass: linear in the value (2048 bins) or an
+// 8-bit digit of the key.  Both are monotone over the candidates.
+struct BinFn {
+  bool linear;
+  float vmin, scale;
+  int shift;
+  __device__ __forceinline__ int operator()(uint32_t key) const {
+    if (linear) {
+      const int b = static_cast<int>((key_value(key) - vmin) * scale);
+      return b < kLinBins - 1 ? b : kLinBins - 1;
+    }
+    return static_cast<int>((key >> shift) & 255u);
+  }
+};
+
+// Top-k of one row held as KPT contiguous keys per thread (indices
+// KPT*t .. KPT*t + KPT - 1).  emit(slot, index) is called once per selected
+// index, slot = rank in ascending index order.
+template <int KPT, typename Emit>
+__device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& sh, Emit emit) {
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid / kWave;
-  const uint8_t all = static_cast<uint8_t>((1u << R) - 1u);
-  // Ordered compaction of the union pages.
-  int total = 0;
-  for (int base = 0; base < P; base += kBlock) {
-    const int p = base + tid;
-    const uint8_t m = p < P ? page_mask[p] : 0;
-    const uint64_t b = __ballot(m != 0);
-    if (lane == 0) s_scan[wave] = __popcll(b);
-    __syncthreads();
-    int before = total;
-    for (int w = 0; w < wave; ++w) before += s_scan[w];
-    int chunk_total = 0;
-    for (int w = 0; w < kBlock / kWave; ++w) chunk_total += s_scan[w];
-    if (m != 0) {
-      const int slot = before + __popcll(b & lanemask_lt());
-      upage[slot] = p;
-      umask[slot] = m;
+  const int i0 = KPT * tid;
+  uint32_t cand = 0u, taken = 0u;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) cand |= (i0 + j < P) ? (1u << j) : 0u;
+  uint32_t need = static_cast<uint32_t>(k);
+  uint32_t ccount = static_cast<uint32_t>(P);
+  int mode = 0;  // 0: take every candidate, 1: exact rank, 2: equal keys by index
+  for (int level = 0;; ++level) {
+    if (ccount == need) break;
+    uint32_t cmax = 0u, cmin = 0xffffffffu;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool c = (cand >> j) & 1u;
+      cmax = (c && key[j] > cmax) ? key[j] : cmax;
+      cmin = (c && key[j] < cmin) ? key[j] : cmin;
     }
-    total += chunk_total;
+    cmax = wave_max_u32(cmax);
+    cmin = wave_min_u32(cmin);
+    if (lane == 0) {
+      sh.red_max[wave] = cmax;
+      sh.red_min[wave] = cmin;
+    }
     __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      cmax = sh.red_max[w] > cmax ? sh.red_max[w] : cmax;
+      cmin = sh.red_min[w] < cmin ? sh.red_min[w] : cmin;
+    }
+    if (cmax == cmin) {
+      mode = 2;
+      break;
+    }
+    if (ccount <= static_cast<uint32_t>(kBlock)) {
+      mode = 1;
+      break;
+    }
+    BinFn fn;
+    const float vmin = key_value(cmin);
+    const float vmax = key_value(cmax);
+    const float range = vmax - vmin;
+    fn.vmin = vmin;
+    fn.scale = static_cast<float>(kLinBins) / range;
+    // A few linear passes resolve real score distributions; after that (or
+    // for non-finite ranges) the digit passes bound the work at 4 more.
+    fn.linear = level < 3 && __builtin_isfinite(vmin) && __builtin_isfinite(vmax) && __builtin_isfinite(range) &&
+                range > 0.0f && __builtin_isfinite(fn.scale);
+    const int hi = 31 - __clz(static_cast<int>(cmax ^ cmin));
+    fn.shift = hi >= 7 ? hi - 7 : 0;
+    const int nb = fn.linear ? kLinBins : 256;
+    const int bpt = nb / kBlock;  // bins owned by a thread
+    for (int b = tid; b < (kLinBins + 64) / 4; b += kBlock)
+      reinterpret_cast<uint4*>(sh.hist)[b] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool c = (cand >> j) & 1u;
+      atomicAdd(&sh.hist[c ? fn(key[j]) : kLinBins], 1u);
+    }
+    __syncthreads();
+    uint32_t tot = 0u;
+    for (int b = 0; b < bpt; ++b) tot += sh.hist[bpt * tid + b];
+    // suffix sums over threads (bins descending)
+    const uint32_t wincl = wave_suffix_sum_u32(tot);
+    if (lane == 0) sh.scan[wave] = static_cast<int>(wincl);
+    __syncthreads();
+    uint32_t incl = wincl;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) incl += w > wave ? static_cast<uint32_t>(sh.scan[w]) : 0u;
+    if (incl - tot < need && need <= incl) {
+      uint32_t acc = incl - tot;
+      int bin = bpt * tid;
+      uint32_t cnt = 0u;
+      for (int b = bpt - 1; b >= 0; --b) {
+        const uint32_t c = sh.hist[bpt * tid + b];
+        if (need <= acc + c) {
+          bin = bpt * tid + b;
+          cnt = c;
+          break;
+        }
+        acc += c;
+      }
+      sh.bnd = bin;
+      sh.bnd_above = acc;
+      sh.bnd_count = cnt;
+    }
+    __syncthreads();
+    const int bnd = sh.bnd;
+    need -= sh.bnd_above;
+    ccount = sh.bnd_count;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool c = (cand >> j) & 1u;
+      const int b = fn(key[j]);
+      taken |= (c && b > bnd) ? (1u << j) : 0u;
+      cand &= (c && b == bnd) ? 0xffffffffu : ~(1u << j);
+    }
   }
-  const int nu = total;
+  int total;
+  if (mode == 1) {
+    // exact rank of at most kBlock candidates
+    const int mine = __popc(cand);
+    int slot = block_excl_scan(mine, sh.scan, &total);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      if ((cand >> j) & 1u) {
+        sh.ckey[slot] = key[j];
+        sh.cidx[slot] = i0 + j;
+        ++slot;
+      }
+    }
+    for (int w = tid; w < kMaxSelPages / 32; w += kBlock) sh.selbits[w] = 0u;
+    __syncthreads();
+    if (tid < static_cast<int>(ccount)) {
+      const uint32_t mk = sh.ckey[tid];
+      const int mi = sh.cidx[tid];
+      uint32_t rank = 0u;
+      for (int m = 0; m < static_cast<int>(ccount); ++m) {
+        const uint32_t km = sh.ckey[m];
+        const int im = sh.cidx[m];
+        rank += (km > mk || (km == mk && im < mi)) ? 1u : 0u;
+      }
+      if (rank < need) atomicOr(&sh.selbits[mi >> 5], 1u << (mi & 31));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int i = i0 + j;
+      const bool c = (cand >> j) & 1u;
+      taken |= (c && ((sh.selbits[(i >> 5) & (kMaxSelPages / 32 - 1)] >> (i & 31)) & 1u)) ? (1u << j) : 0u;
+    }
+  } else if (mode == 2) {
+    int before = block_excl_scan(__popc(cand), sh.scan, &total);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      if ((cand >> j) & 1u) {
+        taken |= (static_cast<uint32_t>(before) < need) ? (1u << j) : 0u;
+        ++before;
+      }
+    }
+  } else {
+    taken |= cand;
+  }
+  int slot = block_excl_scan(__popc(taken), sh.scan, &total);
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    if ((taken >> j) & 1u) emit(slot++, i0 + j);
+  }
+}
+
+// Union plan of group g: page_mask (LDS, byte per page, zero padded to a
+// multiple of 8) -> ascending union pages and their head masks, then the
+// optional row plan.  Thread t owns pages [8t, 8t + 8) of each 2048-page
+// stretch.
+__device__ void write_union_plan(const SelectArgs& s, int g, const uint8_t* page_mask, int32_t* upage,
+                                 uint8_t* umask, int* scan) {
+  const int tid = threadIdx.x;
+  const int P = s.P;
+  const uint8_t all = static_cast<uint8_t>((1u << s.R) - 1u);
+  int nu = 0;
+  for (int base = 0; base < P; base += kBlock * 8) {
+    const int p0 = base + 8 * tid;
+    uint2 w = make_uint2(0u, 0u);
+    if (p0 < P) w = reinterpret_cast<const uint2*>(page_mask)[p0 >> 3];
+    int cnt = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) cnt += (((w.x >> (8 * b)) & 255u) != 0u) + (((w.y >> (8 * b)) & 255u) != 0u);
+    int total;
+    int slot = nu + block_excl_scan(cnt, scan, &total);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const uint32_t m = ((b < 4 ? w.x : w.y) >> (8 * (b & 3))) & 255u;
+      if (m != 0u) {
+        upage[slot] = p0 + b;
+        umask[slot] = static_cast<uint8_t>(m);
+        ++slot;
+      }
+    }
+    nu += total;
+  }
+  __syncthreads();
+  if (s.plan_pages != nullptr) {
+    int32_t* pp = s.plan_pages + static_cast<int64_t>(g) * s.plan_stride;
+    uint8_t* pm = s.plan_masks != nullptr ? s.plan_masks + static_cast<int64_t>(g) * s.plan_stride : nullptr;
+    for (int i = tid; i < nu; i += kBlock) {
+      pp[i] = upage[i];
+      if (pm != nullptr) pm[i] = umask[i];
+    }
+  }
+  if (tid == 0 && s.plan_counts != nullptr) s.plan_counts[g] = nu;
   const int length = s.length;
+  const int bs = s.bs;
   const int sink_end = s.sink < length ? s.sink : length;
   const int hist_recent = s.recent - 1 > 0 ? s.recent - 1 : 0;
   const int recent_start = (length - hist_recent) > sink_end ? (length - hist_recent) : sink_end;
-  const int n_page_rows = nu * s.bs;
-  const int n_recent = length - recent_start;
-  const int count = sink_end + n_page_rows + n_recent + (s.append_position >= 0 ? 1 : 0);
+  const int page_end = sink_end + nu * bs;
+  const int recent_end = page_end + (length - recent_start);
+  const int count = recent_end + (s.append_position >= 0 ? 1 : 0);
   if (s.rows != nullptr) {
+    const bool pow2 = (bs & (bs - 1)) == 0;
+    const int sh = pow2 ? __ffs(bs) - 1 : 0;
     int32_t* rows = s.rows + static_cast<int64_t>(g) * s.rows_stride;
     uint8_t* masks = s.row_masks != nullptr ? s.row_masks + static_cast<int64_t>(g) * s.rows_stride : nullptr;
     for (int i = tid; i < count; i += kBlock) {
@@ -271,13 +462,13 @@ __device__ void build_row_plan(const SelectArgs& s, int g, int R, int P, const u
       uint8_t m = all;
       if (i < sink_end) {
         pos = i;
-      } else if (i < sink_end + n_page_rows) {
+      } else if (i < page_end) {
         const int j = i - sink_end;
-        const int u = j / s.bs;
-        pos = s.sink + upage[u] * s.bs + (j - u * s.bs);
+        const int u = pow2 ? (j >> sh) : j / bs;
+        pos = s.sink + upage[u] * bs + (j - u * bs);
         m = umask[u];
-      } else if (i < sink_end + n_page_rows + n_recent) {
-        pos = recent_start + (i - sink_end - n_page_rows);
+      } else if (i < recent_end) {
+        pos = recent_start + (i - page_end);
       } else {
         pos = s.append_position;
       }
@@ -288,100 +479,119 @@ __device__ void build_row_plan(const SelectArgs& s, int g, int R, int P, const u
   if (tid == 0 && s.row_counts != nullptr) s.row_counts[g] = count;
 }
 
-template <typename DT, int DFIX, bool FUSED>
-__global__ __launch_bounds__(kBlock) void quest_kernel(ScoreArgs a, SelectArgs s) {
-  extern __shared__ __align__(16) uint8_t lds[];
-  using S = typename DT::storage;
-  const int tiles = (a.P + kTilePages - 1) / kTilePages;
-  const int g = blockIdx.x / tiles;
-  const int tile = blockIdx.x - g * tiles;
-  const int p0 = tile * kTilePages;
-  const int np = (a.P - p0) < kTilePages ? (a.P - p0) : kTilePages;
-  const int pitch = a.D * static_cast<int>(sizeof(S)) + 4;
-  stage_tile<DT>(a, g, p0, np, lds, pitch);
-  __syncthreads();
-  score_tile<DT, DFIX>(a, g, p0, np, lds, pitch);
-  if (!FUSED) return;
-
-  __shared__ int s_flag;
-  if (!arrive_last(s.counters + g, static_cast<unsigned int>(tiles), &s_flag)) return;
-
-  // ---- last block of group g: top-k per head + row plan ----
-  __syncthreads();
-  const int wave = static_cast<int>(threadIdx.x) / kWave;
-  uint32_t* hist = reinterpret_cast<uint32_t*>(lds) + wave * 256;
-  const bool plan = s.rows != nullptr || s.row_counts != nullptr;
-  uint8_t* page_mask = lds + 4 * 256 * 4;  // after the 4 histograms
-  const int mask_bytes = ((a.P + 3) / 4) * 4;
-  if (plan) {
-    for (int i = threadIdx.x; i < mask_bytes / 4; i += kBlock) reinterpret_cast<uint32_t*>(page_mask)[i] = 0u;
-  }
-  __syncthreads();
-  for (int r = wave; r < a.R; r += kBlock / kWave) {
-    const float* vals = a.scores + (static_cast<int64_t>(g) * a.R + r) * a.P;
-    int32_t* out = s.sel_pages != nullptr ? s.sel_pages + (static_cast<int64_t>(g) * a.R + r) * s.k : nullptr;
-    const uint32_t bit = 1u << r;
-    wave_topk(vals, a.P, s.k, hist, [&](int slot, int idx) {
-      if (out != nullptr) out[slot] = idx;
-      if (plan) atomicOr(reinterpret_cast<uint32_t*>(page_mask) + (idx >> 2), bit << (8 * (idx & 3)));
-    });
-  }
-  __syncthreads();
-  if (!plan) return;
-  __shared__ int s_scan[kBlock / kWave];
-  int32_t* upage = reinterpret_cast<int32_t*>(page_mask + mask_bytes);
-  uint8_t* umask = reinterpret_cast<uint8_t*>(upage + a.P);
-  build_row_plan(s, g, a.R, a.P, page_mask, upage, umask, s_scan);
+__device__ __forceinline__ int32_t fetch_i32(const int32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_i32(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <typename Kern>
-size_t quest_lds_bytes(int P, int D, int es, bool fused) {
-  (void)sizeof(Kern*);
-  size_t tile = static_cast<size_t>(2 * kTilePages) * (static_cast<size_t>(D) * es + 4);
-  if (!fused) return tile;
-  const size_t mask_bytes = static_cast<size_t>((P + 3) / 4) * 4;
-  const size_t sel = 4 * 256 * 4 + mask_bytes + static_cast<size_t>(P) * 4 + static_cast<size_t>(P);
-  return tile > sel ? tile : sel;
+template <int KPT, bool VEC>
+__global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
+  __shared__ __align__(16) SelShared sh;
+  extern __shared__ __align__(16) uint8_t dyn[];  // union scratch
+  const int row = blockIdx.x;
+  const int g = row / s.R;
+  const int P = s.P;
+  const float* vals = s.scores + static_cast<int64_t>(row) * s.score_stride;
+  // ---- keys: one batched round trip ----
+  uint32_t key[KPT];
+  {
+    const int i0 = KPT * static_cast<int>(threadIdx.x);
+    if (VEC) {
+      // Rows are 16-byte aligned and readable up to vec_last4 + 3: a float4
+      // start clamped to vec_last4 stays inside the row.
+      const int last4 = s.vec_last4;
+#pragma unroll
+      for (int q4 = 0; q4 < KPT / 4; ++q4) {
+        int at = i0 + 4 * q4;
+        at = at < last4 ? at : last4;
+        const float4 v = *reinterpret_cast<const float4*>(vals + at);
+        key[4 * q4] = score_key(v.x);
+        key[4 * q4 + 1] = score_key(v.y);
+        key[4 * q4 + 2] = score_key(v.z);
+        key[4 * q4 + 3] = score_key(v.w);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const int i = i0 + j;
+        key[j] = score_key(vals[i < P ? i : P - 1]);
+      }
+    }
+  }
+  int32_t* ws_row = s.sel_ws != nullptr ? s.sel_ws + static_cast<int64_t>(row) * s.k : nullptr;
+  int32_t* out32 = s.sel_out != nullptr ? s.sel_out + static_cast<int64_t>(row) * s.k : nullptr;
+  int64_t* out64 = s.sel_out64 != nullptr ? s.sel_out64 + static_cast<int64_t>(row) * s.k : nullptr;
+  block_topk<KPT>(key, P, s.k, sh, [&](int slot, int idx) {
+    if (ws_row != nullptr) publish_i32(ws_row + slot, idx);
+    if (out32 != nullptr) out32[slot] = idx;
+    if (out64 != nullptr) out64[slot] = idx;
+  });
+  if (!s.want_union) return;
+  if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.flag)) return;
+
+  // ---- last block of group g: union of the R selections ----
+  const int mask_bytes = ((P + 7) / 8) * 8;
+  uint8_t* page_mask = dyn;
+  int32_t* upage = reinterpret_cast<int32_t*>(dyn + mask_bytes);
+  uint8_t* umask = reinterpret_cast<uint8_t*>(upage + P);
+  for (int i = threadIdx.x; i < mask_bytes / 4; i += kBlock) reinterpret_cast<uint32_t*>(page_mask)[i] = 0u;
+  __syncthreads();
+  const int32_t* sel_g = s.sel_ws + static_cast<int64_t>(g) * s.R * s.k;
+  const int n_sel = s.R * s.k;
+  for (int i = threadIdx.x; i < n_sel; i += kBlock) {
+    const int id = fetch_i32(sel_g + i);
+    const int hr = i / s.k;
+    atomicOr(reinterpret_cast<uint32_t*>(page_mask) + (id >> 2), (1u << hr) << (8 * (id & 3)));
+  }
+  __syncthreads();
+  write_union_plan(s, g, page_mask, upage, umask, sh.scan);
 }
 
-template <typename DT, bool FUSED>
-int launch_quest(const ScoreArgs& a, const SelectArgs& s, hipStream_t stream) {
-  const int tiles = (a.P + kTilePages - 1) / kTilePages;
-  const size_t lds = quest_lds_bytes<DT>(a.P, a.D, static_cast<int>(sizeof(typename DT::storage)), FUSED);
-  if (lds > 160 * 1024) return TW_EUNSUPPORTED;
-  dim3 grid(tiles * a.G);
-  if (a.D == 128) {
-    auto kern = quest_kernel<DT, 128, FUSED>;
-    if (lds > 64 * 1024) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, stream, a, s);
+size_t union_lds_bytes(int P) { return static_cast<size_t>((P + 7) / 8) * 8 + static_cast<size_t>(P) * 5 + 16; }
+
+template <int KPT>
+int launch_select_kpt(const SelectArgs& s, int n_rows, bool vec, hipStream_t stream) {
+  const size_t lds = s.want_union ? union_lds_bytes(s.P) : 0;
+  if (vec) {
+    hipLaunchKernelGGL((quest_select_kernel<KPT, true>), dim3(n_rows), dim3(kBlock), lds, stream, s);
   } else {
-    auto kern = quest_kernel<DT, 0, FUSED>;
-    if (lds > 64 * 1024) (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, stream, a, s);
+    hipLaunchKernelGGL((quest_select_kernel<KPT, false>), dim3(n_rows), dim3(kBlock), lds, stream, s);
   }
   return tw_host::check_launch();
 }
 
-template <bool FUSED>
-int dispatch_quest(int dtype, const ScoreArgs& a, const SelectArgs& s, hipStream_t stream) {
-  switch (dtype) {
-    case TW_DTYPE_F16: return launch_quest<F16, FUSED>(a, s, stream);
-    case TW_DTYPE_BF16: return launch_quest<BF16, FUSED>(a, s, stream);
-    case TW_DTYPE_F32: return launch_quest<F32, FUSED>(a, s, stream);
-    default: return TW_EINVAL;
-  }
+int launch_select(const SelectArgs& s, int n_rows, bool vec, hipStream_t stream) {
+  if (s.P <= 4 * kBlock) return launch_select_kpt<4>(s, n_rows, vec, stream);
+  if (s.P <= 8 * kBlock) return launch_select_kpt<8>(s, n_rows, vec, stream);
+  if (s.P <= 16 * kBlock) return launch_select_kpt<16>(s, n_rows, vec, stream);
+  return launch_select_kpt<32>(s, n_rows, vec, stream);
 }
 
-__global__ __launch_bounds__(kBlock) void topk_rows_kernel(const float* __restrict__ scores, int rows, int P,
-                                                           int64_t stride, int k, int64_t* __restrict__ out) {
-  __shared__ uint32_t hist[4 * 256];
-  const int wave = static_cast<int>(threadIdx.x) / kWave;
-  const int row = blockIdx.x * (kBlock / kWave) + wave;
-  if (row >= rows) return;
-  int64_t* o = out + static_cast<int64_t>(row) * k;
-  wave_topk(scores + row * stride, P, k, hist + wave * 256, [&](int slot, int idx) { o[slot] = idx; });
+template <typename DT>
+int launch_score(const ScoreArgs& a, hipStream_t stream) {
+  const int tiles = (a.P + kTilePages - 1) / kTilePages;
+  const size_t lds = static_cast<size_t>(2 * kTilePages) *
+                         (static_cast<size_t>(a.D) * sizeof(typename DT::storage) + 4) +
+                     static_cast<size_t>(a.R) * a.D * sizeof(float);
+  if (lds > 160 * 1024) return TW_EUNSUPPORTED;  // gfx950: 160 KB of LDS per CU
+  const dim3 grid(tiles * a.G);
+  auto kern = a.D == 128 ? quest_score_kernel<DT, 128> : quest_score_kernel<DT, 0>;
+  if (lds > 64 * 1024)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(lds));
+  hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, stream, a);
+  return tw_host::check_launch();
+}
+
+int dispatch_score(int dtype, const ScoreArgs& a, hipStream_t stream) {
+  switch (dtype) {
+    case TW_DTYPE_F16: return launch_score<F16>(a, stream);
+    case TW_DTYPE_BF16: return launch_score<BF16>(a, stream);
+    case TW_DTYPE_F32: return launch_score<F32>(a, stream);
+    default: return TW_EINVAL;
+  }
 }
 
 bool check_score_args(const float* q, const void* pmin, const void* pmax, int G, int R, int P, int D,
@@ -392,6 +602,9 @@ bool check_score_args(const float* q, const void* pmin, const void* pmax, int G,
   return true;
 }
 
+int64_t padded(int P) { return (static_cast<int64_t>(P) + 3) & ~static_cast<int64_t>(3); }
+size_t counter_bytes(int G) { return ((static_cast<size_t>(G) * 4 + 255) / 256) * 256; }
+
 }  // namespace
 }  // namespace tw
 
@@ -399,38 +612,56 @@ extern "C" int tw_quest_score(const float* q, const void* page_min, const void* 
                               int R, int P, int D, int64_t page_group_stride, float* out, void* stream) {
   if (!tw::check_score_args(q, page_min, page_max, G, R, P, D, page_group_stride) || out == nullptr)
     return TW_EINVAL;
-  tw::ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P, D, out};
-  tw::SelectArgs s{};
-  return tw::dispatch_quest<false>(dtype, a, s, static_cast<hipStream_t>(stream));
+  tw::ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P, D, out, P, nullptr};
+  return tw::dispatch_score(dtype, a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int tw_topk_sorted(const float* scores, int rows, int P, int64_t score_row_stride, int k,
                               int64_t* out, void* stream) {
   if (scores == nullptr || out == nullptr || rows < 0 || P <= 0 || k <= 0 || k > P) return TW_EINVAL;
   if (score_row_stride < P) return TW_EINVAL;
+  if (P > tw::kMaxSelPages) return TW_EUNSUPPORTED;
   if (rows == 0) return TW_OK;
-  const int blocks = (rows + 3) / 4;
-  hipLaunchKernelGGL(tw::topk_rows_kernel, dim3(blocks), dim3(tw::kBlock), 0, static_cast<hipStream_t>(stream),
-                     scores, rows, P, score_row_stride, k, out);
-  return tw_host::check_launch();
+  tw::SelectArgs s{};
+  s.scores = scores;
+  s.score_stride = score_row_stride;
+  s.G = rows;
+  s.R = 1;
+  s.P = P;
+  s.k = k;
+  s.sel_out64 = out;
+  s.want_union = false;
+  // Vector loads only where every row is 16-byte aligned and the last float4
+  // of a row ends exactly at its last score.
+  const bool vec = (score_row_stride % 4) == 0 && (P % 4) == 0 && (reinterpret_cast<uintptr_t>(scores) % 16) == 0;
+  s.vec_last4 = P - 4;
+  return tw::launch_select(s, rows, vec, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t tw_quest_select_workspace_size(int G, int R, int P) {
-  // arrival counters (one per group, 256-byte aligned) + scores [G][R][P]
-  const size_t counters = ((static_cast<size_t>(G) * 4 + 255) / 256) * 256;
-  return counters + static_cast<size_t>(G) * R * P * sizeof(float);
+  // arrival counters | scores [G][R][P rounded up to 4] | selections [G][R][<= P]
+  if (G <= 0 || R <= 0 || P <= 0) return 0;
+  return tw::counter_bytes(G) + static_cast<size_t>(G) * R * tw::padded(P) * sizeof(float) +
+         static_cast<size_t>(G) * R * P * sizeof(int32_t);
 }
 
 extern "C" int tw_quest_select(const float* q, const void* page_min, const void* page_max, int dtype, int G,
                                int R, int P, int D, int64_t page_group_stride, int k, float* scores,
-                               int32_t* sel_pages, int32_t* rows, uint8_t* row_masks, int32_t* row_counts,
+                               int32_t* sel_pages, int32_t* plan_pages, uint8_t* plan_masks, int32_t* plan_counts,
+                               int64_t plan_stride, int32_t* rows, uint8_t* row_masks, int32_t* row_counts,
                                int64_t rows_stride, int sink, int recent, int block_size, int length,
                                int append_position, void* workspace, size_t workspace_bytes, void* stream) {
   if (!tw::check_score_args(q, page_min, page_max, G, R, P, D, page_group_stride)) return TW_EINVAL;
   if (k <= 0 || k > P) return TW_EINVAL;
-  const bool plan = rows != nullptr || row_counts != nullptr;
-  if (plan) {
-    if (R > 8 || P > tw::kMaxPlanPages || sink < 0 || recent <= 0 || block_size <= 0 || length < 0) return TW_EINVAL;
+  if (P > tw::kMaxSelPages) return TW_EUNSUPPORTED;
+  const bool row_plan = rows != nullptr || row_counts != nullptr;
+  const bool page_plan = plan_pages != nullptr || plan_counts != nullptr;
+  if ((row_plan || page_plan) && R > 8) return TW_EINVAL;
+  if ((plan_masks != nullptr && plan_pages == nullptr) || (row_masks != nullptr && rows == nullptr)) return TW_EINVAL;
+  if (plan_pages != nullptr && plan_stride < (static_cast<int64_t>(R) * k < P ? static_cast<int64_t>(R) * k : P))
+    return TW_EINVAL;
+  if (row_plan) {
+    if (sink < 0 || recent <= 0 || block_size <= 0 || length < 0) return TW_EINVAL;
     // Pages must lie in the eligible window (between the sink and the recent
     // window, quest_offload_cache.py:330-334) so that page rows, sink rows
     // and recent rows are disjoint.
@@ -438,7 +669,6 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
     const int64_t hist_recent = recent - 1 > 0 ? recent - 1 : 0;
     const int64_t recent_start = (length - hist_recent) > sink_end ? (length - hist_recent) : sink_end;
     if (static_cast<int64_t>(sink) + static_cast<int64_t>(P) * block_size > recent_start) return TW_EINVAL;
-    if (row_masks != nullptr && rows == nullptr) return TW_EINVAL;
     if (rows != nullptr) {
       const int64_t union_pages = static_cast<int64_t>(R) * k < P ? static_cast<int64_t>(R) * k : P;
       const int64_t max_count = sink_end + union_pages * block_size + (length - recent_start) + 1;
@@ -446,12 +676,38 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
     }
   }
   if (workspace == nullptr || workspace_bytes < tw_quest_select_workspace_size(G, R, P)) return TW_ENOMEM;
-  const size_t counter_bytes = ((static_cast<size_t>(G) * 4 + 255) / 256) * 256;
-  unsigned int* counters = static_cast<unsigned int*>(workspace);
-  float* score_buf = scores != nullptr ? scores
-                                       : reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + counter_bytes);
-  tw::ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P, D, score_buf};
-  tw::SelectArgs s{k, sel_pages, rows, row_masks, row_counts, rows_stride, sink, recent, block_size, length,
-                   append_position, counters};
-  return tw::dispatch_quest<true>(dtype, a, s, static_cast<hipStream_t>(stream));
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  unsigned int* counters = reinterpret_cast<unsigned int*>(ws);
+  float* score_ws = reinterpret_cast<float*>(ws + tw::counter_bytes(G));
+  int32_t* sel_ws = reinterpret_cast<int32_t*>(score_ws + static_cast<int64_t>(G) * R * tw::padded(P));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  tw::ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P, D, score_ws, tw::padded(P), scores};
+  int rc = tw::dispatch_score(dtype, a, st);
+  if (rc != TW_OK) return rc;
+  tw::SelectArgs s{};
+  s.scores = score_ws;
+  s.score_stride = tw::padded(P);
+  s.vec_last4 = static_cast<int>(tw::padded(P)) - 4;
+  s.G = G;
+  s.R = R;
+  s.P = P;
+  s.k = k;
+  s.sel_ws = sel_ws;
+  s.sel_out = sel_pages;
+  s.want_union = row_plan || page_plan;
+  s.plan_pages = plan_pages;
+  s.plan_masks = plan_masks;
+  s.plan_counts = plan_counts;
+  s.plan_stride = plan_stride;
+  s.rows = rows;
+  s.row_masks = row_masks;
+  s.row_counts = row_counts;
+  s.rows_stride = rows_stride;
+  s.sink = sink;
+  s.recent = recent;
+  s.bs = block_size;
+  s.length = length;
+  s.append_position = append_position;
+  s.counters = counters;
+  return tw::launch_select(s, G * R, true, st);
 }

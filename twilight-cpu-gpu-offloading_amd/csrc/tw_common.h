@@ -178,24 +178,51 @@ __device__ __forceinline__ int wave_prefix_sum_i32(int v) {
 __device__ __forceinline__ int first_lane(uint64_t ballot) { return __ffsll(static_cast<long long>(ballot)) - 1; }
 
 // ------------------------------------------------ cross-block handoff
-// "Last block" pattern: every block publishes its results, then bumps a
-// per-group arrival counter; the block that arrives last consumes all
-// results and resets the counter so the next launch starts from zero (no
-// memset node, so the sequence is graph-capture safe).  No block ever waits
-// on another, so there is no forward-progress assumption.
+// Data handed from one block to another inside a launch goes through
+// device-coherent accesses: agent-scope relaxed atomic stores and loads,
+// which gfx950 issues with the device-coherence bit (write-through past the
+// XCD's non-coherent L2 on store, L2 bypass on load).  The "last block"
+// pattern then needs no cache maintenance: every block waits until its own
+// publishing stores have completed, bumps a per-group arrival counter, and
+// the block that arrives last reads every block's data.  An agent-scope
+// fence would instead write back and invalidate the whole L2 of the XCD,
+// which costs microseconds per block.  No block ever waits on another, so
+// there is no forward-progress assumption; the last block resets the
+// counter so the next launch starts from zero (no memset node, so the
+// sequence is graph-capture safe).
+__device__ __forceinline__ void publish_f32(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_f32x2(float* p, float a, float b) {
+  const uint64_t v = static_cast<uint64_t>(__float_as_uint(a)) | (static_cast<uint64_t>(__float_as_uint(b)) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float fetch_f32(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ float2 fetch_f32x2(const float* p) {
+  const uint64_t v =
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float(static_cast<uint32_t>(v)), __uint_as_float(static_cast<uint32_t>(v >> 32)));
+}
+
+// Returns true in every thread of the block that arrives last.  All of the
+// block's published data must have been written with publish_* before the
+// call.
 __device__ __forceinline__ bool arrive_last(unsigned int* counter, unsigned int expected, int* s_flag) {
-  __threadfence();
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's publishing stores are complete
+  __syncthreads();                // ... and so are every other wavefront's
   if (threadIdx.x == 0) {
-    const unsigned int prev = atomicAdd(counter, 1u);
+    const unsigned int prev =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = (prev + 1u == expected);
-    if (last) atomicExch(counter, 0u);
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *s_flag = last ? 1 : 0;
   }
   __syncthreads();
-  const bool last = *s_flag != 0;
-  if (last) __threadfence();
-  return last;
+  return *s_flag != 0;
 }
 
 }  // namespace tw

@@ -227,6 +227,9 @@ def quest_select(
     *,
     scores: Optional[torch.Tensor] = None,
     sel_pages: Optional[torch.Tensor] = None,
+    plan_pages: Optional[torch.Tensor] = None,
+    plan_masks: Optional[torch.Tensor] = None,
+    plan_counts: Optional[torch.Tensor] = None,
     rows: Optional[torch.Tensor] = None,
     row_masks: Optional[torch.Tensor] = None,
     row_counts: Optional[torch.Tensor] = None,
@@ -236,20 +239,22 @@ def quest_select(
     length: int = 0,
     append_position: int = -1,
 ) -> None:
-    """Fused score + top-k + row plan for one layer (one launch).
+    """Quest score + top-k + GQA union plan for one layer (two launches).
 
     page_min/page_max: [G, P, D] views (P pages are scored).  Outputs are
-    caller-allocated: scores [G,R,P] fp32, sel_pages [G,R,k] int32, rows/row_masks
-    [G, stride] int32/uint8, row_counts [G] int32."""
+    caller-allocated: scores [G,R,P] fp32, sel_pages [G,R,k] int32, the union
+    plan plan_pages/plan_masks [G, >=min(P, R*k)] int32/uint8 with
+    plan_counts [G] int32, the row plan rows/row_masks [G, stride]
+    int32/uint8 with row_counts [G] int32."""
     _check_score_inputs(q, page_min, page_max, "quest_select")
-    dev = _require_device(q, page_min, page_max, scores, sel_pages, rows, row_masks, row_counts,
-                          what="quest_select")
+    dev = _require_device(q, page_min, page_max, scores, sel_pages, plan_pages, plan_masks, plan_counts, rows,
+                          row_masks, row_counts, what="quest_select")
     G, R, D = q.shape
     P = page_min.shape[1]
     if not 1 <= k <= P:
         raise ValueError("k must be in [1, P]")
     for t, dt, shape in ((scores, torch.float32, (G, R, P)), (sel_pages, torch.int32, (G, R, k)),
-                         (row_counts, torch.int32, (G,))):
+                         (row_counts, torch.int32, (G,)), (plan_counts, torch.int32, (G,))):
         if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
             raise ValueError("quest_select output has the wrong dtype/shape")
     stride = 0
@@ -260,11 +265,21 @@ def quest_select(
         if row_masks is not None and (row_masks.dtype != torch.uint8 or row_masks.shape != rows.shape
                                       or row_masks.stride() != rows.stride()):
             raise ValueError("row_masks must match rows")
+    plan_stride = 0
+    if plan_pages is not None:
+        if plan_pages.dtype != torch.int32 or plan_pages.ndim != 2 or plan_pages.shape[0] != G \
+                or plan_pages.stride(1) != 1:
+            raise ValueError("plan_pages must be [G, stride] int32")
+        plan_stride = plan_pages.stride(0)
+        if plan_masks is not None and (plan_masks.dtype != torch.uint8 or plan_masks.shape != plan_pages.shape
+                                       or plan_masks.stride() != plan_pages.stride()):
+            raise ValueError("plan_masks must match plan_pages")
     nbytes = hip().tw_quest_select_workspace_size(G, R, P)
     ws = WORKSPACE.get(dev, "quest_select", nbytes)
     with torch.cuda.device(dev):
         check(hip().tw_quest_select(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
-                                    page_min.stride(0), k, ptr(scores), ptr(sel_pages), ptr(rows), ptr(row_masks),
+                                    page_min.stride(0), k, ptr(scores), ptr(sel_pages), ptr(plan_pages),
+                                    ptr(plan_masks), ptr(plan_counts), plan_stride, ptr(rows), ptr(row_masks),
                                     ptr(row_counts), stride, sink, recent, block_size, length, append_position,
                                     ptr(ws), ws.numel(), stream_handle(dev)), "quest_select")
 
@@ -318,6 +333,72 @@ def decode_attention_rows(
                                         ptr(row_masks), ptr(row_counts), rows.stride(0), k_cache.stride(0) // D,
                                         None, 0, -1, max_rows, ptr(cur_k), ptr(cur_v), scale, ptr(out), ptr(ws),
                                         ws.numel(), stream_handle(dev)), "decode_attention")
+    return out
+
+
+def plan_max_rows(max_pages: int, *, sink: int, recent: int, block_size: int, length: int,
+                  append_position: int = -1) -> int:
+    """Bound on the rows of a union plan of at most max_pages pages."""
+    sink_end = min(sink, length)
+    recent_start = max(sink_end, length - max(0, recent - 1))
+    return sink_end + max_pages * block_size + (length - recent_start) + (1 if append_position >= 0 else 0)
+
+
+def decode_attention_pages(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    plan_pages: torch.Tensor,
+    plan_counts: torch.Tensor,
+    *,
+    plan_masks: Optional[torch.Tensor] = None,
+    max_pages: int,
+    sink: int,
+    recent: int,
+    block_size: int,
+    length: int,
+    append_position: int = -1,
+    softmax_scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Sparse GQA decode attention over a union plan from quest_select: group
+    g sees [0, sink_end) ++ its union pages (heads per plan_masks) ++ the
+    recent window ++ append_position.  q [G,R,D]; k_cache/v_cache [G, Lmax, D].
+    Returns [G,R,D]."""
+    if q.ndim != 3 or q.dtype not in _KEY_DTYPES:
+        raise ValueError("q must be [G, R, D]")
+    G, R, D = q.shape
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or k_cache.shape != v_cache.shape:
+        raise ValueError("K/V cache must match q's dtype and each other")
+    if k_cache.ndim != 3 or k_cache.shape[0] != G or k_cache.shape[2] != D or k_cache.stride() != v_cache.stride():
+        raise ValueError("K/V cache must be [G, Lmax, D]")
+    if k_cache.stride(2) != 1 or k_cache.stride(1) != D or k_cache.stride(0) % D:
+        raise ValueError("K/V cache rows must be contiguous")
+    if plan_pages.dtype != torch.int32 or plan_pages.ndim != 2 or plan_pages.shape[0] != G \
+            or plan_pages.stride(1) != 1:
+        raise ValueError("plan_pages must be [G, stride] int32")
+    if plan_masks is not None and (plan_masks.dtype != torch.uint8 or plan_masks.shape != plan_pages.shape
+                                   or plan_masks.stride() != plan_pages.stride()):
+        raise ValueError("plan_masks must match plan_pages")
+    if plan_counts.dtype != torch.int32 or tuple(plan_counts.shape) != (G,):
+        raise ValueError("plan_counts must be [G] int32")
+    if not 0 <= max_pages <= plan_pages.shape[1]:
+        raise ValueError("max_pages must be within the plan width")
+    dev = _require_device(q, k_cache, v_cache, plan_pages, plan_masks, plan_counts, what="decode_attention_pages")
+    _require_contiguous(q, what="decode_attention_pages")
+    if out is None:
+        out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    max_rows = plan_max_rows(max_pages, sink=sink, recent=recent, block_size=block_size, length=length,
+                             append_position=append_position)
+    nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
+    ws = WORKSPACE.get(dev, "decode_attention", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_decode_attention_pages(ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D,
+                                              ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
+                                              plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink, recent,
+                                              block_size, length, append_position, scale, ptr(out), ptr(ws),
+                                              ws.numel(), stream_handle(dev)), "decode_attention_pages")
     return out
 
 
