@@ -10,14 +10,13 @@
 //
 // The kernel is written for latency: a decode layer moves tens of MB, so it
 // completes in a handful of memory round trips and every round trip counts.
-//   round trip 1: row count, the wavefront's row indices (one per lane) and
-//                 masks, the group's queries -- all independent loads;
+//   round trip 1: row count, the wavefront's row indices and masks, the
+//                 group's queries -- all independent loads;
 //   round trip 2: the K and V rows (16 bytes per lane, 8 rows per lane in
 //                 flight), read straight from the cache by index;
-//   then the block partial (m, l, o) is published to the workspace with
-//   device-coherent stores, the block bumps the group's arrival counter, and
-//   the last block of the group loads every partial of the group in batched
-//   round trips and writes the output.
+//   then the block's partial (m, l, o) goes to the workspace and a second,
+//   small launch merges the partials of every group that spans more than
+//   one block (one round trip: all chunks' loads are issued at once).
 // Every load is unconditional (clamped addresses, results masked) so the
 // compiler issues them back to back instead of one branch and wait per load.
 //
@@ -33,7 +32,6 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
-constexpr int kMergeBatch = 64;
 constexpr int kMaxChunks = 128;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -194,61 +192,75 @@ __device__ __forceinline__ GroupRows group_rows(const AttnArgs& a, int g, int D)
   return gr;
 }
 
-// Combine the chunk partials of group g (the calling block is the last one to
-// arrive) and write the output.  s_ml: LDS room for max_chunks * R * 2 floats.
-template <typename DT>
-__device__ void merge_partials(const AttnArgs& a, int g, int D, int n_chunks, float* s_ml) {
+// Split-K combine: one block per (group, head), thread t = channel t.  Runs
+// as its own launch after the partial kernel, so it reads the partials with
+// plain loads and issues every chunk's loads at once (one round trip); the
+// chunk weights exp2(m_c - M) and 1 / sum(w_c l_c) come from a block
+// reduction over the chunks' (m, l).  Groups that fit one chunk were written
+// by the partial kernel itself and are skipped.
+constexpr int kMergeBatch = 64;
+
+template <typename DT, int MODE>
+__global__ __launch_bounds__(512) void merge_kernel(AttnArgs a, int rows_per_block) {
   using S = typename DT::storage;
   const int R = a.R;
-  const float* ml = a.part_ml + static_cast<int64_t>(g) * a.max_chunks * R * 2;
-  const float* po = a.part_o + static_cast<int64_t>(g) * a.max_chunks * R * D;
-  const int n_ml = n_chunks * R * 2;
-  {
-    // Up to 8 independent loads per thread in one batch.
-    float v[8];
+  const int D = a.D;
+  const int g = blockIdx.x / R;
+  const int r = blockIdx.x - g * R;
+  const GroupRows gr = group_rows<MODE>(a, g, D);
+  const int n_chunks = (gr.n_rows + rows_per_block - 1) / rows_per_block;
+  if (n_chunks <= 1) return;
+  const int t = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = t / kWave;
+  const int n_waves = (blockDim.x + kWave - 1) / kWave;
+  __shared__ float s_red[8];
+  __shared__ float s_w[kMaxChunks];
+  const int64_t base = static_cast<int64_t>(g) * a.max_chunks;
+  const int ch_t = t < D ? t : D - 1;
+  float acc = 0.0f;
+  float L = 0.0f;
+  for (int cb = 0; cb < n_chunks; cb += kMergeBatch) {
+    float ov[kMergeBatch];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = static_cast<int>(threadIdx.x) + j * kBlock;
-      v[j] = fetch_f32(ml + (i < n_ml ? i : 0));
+    for (int j = 0; j < kMergeBatch; ++j) {
+      int c = cb + j;
+      c = c < n_chunks ? c : n_chunks - 1;
+      ov[j] = a.part_o[((base + c) * R + r) * D + ch_t];
+    }
+    if (cb == 0) {
+      // chunk weights: thread c holds chunk c's (m, l)
+      float m = -INFINITY, l = 0.0f;
+      for (int c = t; c < n_chunks; c += blockDim.x) {
+        const float2 v = *reinterpret_cast<const float2*>(a.part_ml + ((base + c) * R + r) * 2);
+        m = fmaxf(m, v.x);
+      }
+      m = wave_max_f32(m);
+      if (lane == 0) s_red[wave] = m;
+      __syncthreads();
+      float M = -INFINITY;
+      for (int w = 0; w < n_waves; ++w) M = fmaxf(M, s_red[w]);
+      __syncthreads();
+      for (int c = t; c < n_chunks; c += blockDim.x) {
+        const float2 v = *reinterpret_cast<const float2*>(a.part_ml + ((base + c) * R + r) * 2);
+        const float w = exp2_rel(v.x, M);
+        s_w[c] = w;
+        l += w * v.y;
+      }
+      l = wave_sum_f32(l);
+      if (lane == 0) s_red[wave] = l;
+      __syncthreads();
+      for (int w = 0; w < n_waves; ++w) L += s_red[w];
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = static_cast<int>(threadIdx.x) + j * kBlock;
-      if (i < n_ml) s_ml[i] = v[j];
+    for (int j = 0; j < kMergeBatch; ++j) {
+      const int c = cb + j;
+      acc += (c < n_chunks ? s_w[c] : 0.0f) * ov[j];
     }
-    for (int i = static_cast<int>(threadIdx.x) + 8 * kBlock; i < n_ml; i += kBlock) s_ml[i] = fetch_f32(ml + i);
   }
-  __syncthreads();
-  S* out = static_cast<S*>(a.out) + static_cast<int64_t>(g) * R * D;
-  const int half = D / 2;
-  for (int p = threadIdx.x; p < R * half; p += kBlock) {
-    const int r = p / half;
-    const int c = 2 * (p - r * half);
-    float M = -INFINITY;
-    for (int ch = 0; ch < n_chunks; ++ch) M = fmaxf(M, s_ml[(ch * R + r) * 2]);
-    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-    for (int cb = 0; cb < n_chunks; cb += kMergeBatch) {
-      float2 ov[kMergeBatch];
-#pragma unroll
-      for (int j = 0; j < kMergeBatch; ++j) {
-        int ch = cb + j;
-        ch = ch < n_chunks ? ch : n_chunks - 1;
-        ov[j] = fetch_f32x2(po + (static_cast<int64_t>(ch) * R + r) * D + c);
-      }
-#pragma unroll
-      for (int j = 0; j < kMergeBatch; ++j) {
-        const int ch = cb + j;
-        if (ch < n_chunks) {
-          const float w = exp2_rel(s_ml[(ch * R + r) * 2], M);
-          L += w * s_ml[(ch * R + r) * 2 + 1];
-          o0 += w * ov[j].x;
-          o1 += w * ov[j].y;
-        }
-      }
-    }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    out[r * D + c] = from_f32(DT{}, o0 * inv);
-    out[r * D + c + 1] = from_f32(DT{}, o1 * inv);
+  if (t < D) {
+    S* out = static_cast<S*>(a.out) + (static_cast<int64_t>(g) * R + r) * D;
+    out[t] = from_f32(DT{}, L > 0.0f ? acc / L : 0.0f);
   }
 }
 
@@ -277,8 +289,8 @@ __device__ void block_partial(const AttnArgs& a, int g, int chunk, int D, bool f
       out[idx] = from_f32(DT{}, L > 0.0f ? O / L : 0.0f);
     } else {
       const int64_t pc = static_cast<int64_t>(g) * a.max_chunks + chunk;
-      publish_f32(a.part_o + pc * R * D + idx, O);
-      if (c == 0) publish_f32x2(a.part_ml + (pc * R + r) * 2, M, L);
+      a.part_o[pc * R * D + idx] = O;
+      if (c == 0) *reinterpret_cast<float2*>(a.part_ml + (pc * R + r) * 2) = make_float2(M, L);
     }
   }
 }
@@ -302,7 +314,6 @@ __global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(
   const int rig = lane / LPR;
   const int c0 = (lane % LPR) * CPL;
 
-  __shared__ int s_flag;
   __shared__ float s_m[kWaves * RMAX];
   __shared__ float s_l[kWaves * RMAX];
   extern __shared__ __align__(16) float s_dyn[];   // [kWaves][RMAX][D] then merge scratch
@@ -490,9 +501,6 @@ __global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(
   }
   __syncthreads();
   block_partial<DT, RMAX>(a, g, chunk, D, n_chunks == 1, s_m, s_l, s_o);
-  if (n_chunks == 1) return;
-  if (!arrive_last(a.counters + g, static_cast<unsigned int>(n_chunks), &s_flag)) return;
-  merge_partials<DT>(a, g, D, n_chunks, s_dyn + kWaves * RMAX * D);
 }
 
 // Generic head dimension (any even D <= 512): one row per wavefront step,
@@ -507,7 +515,6 @@ __global__ __launch_bounds__(kBlock) void decode_attn_generic(AttnArgs a) {
   const int chunk = blockIdx.x - g * a.max_chunks;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
-  __shared__ int s_flag;
   __shared__ float s_m[kWaves * RMAX];
   __shared__ float s_l[kWaves * RMAX];
   extern __shared__ __align__(16) float s_dyn[];
@@ -618,9 +625,6 @@ __global__ __launch_bounds__(kBlock) void decode_attn_generic(AttnArgs a) {
   }
   __syncthreads();
   block_partial<DT, RMAX>(a, g, chunk, D, n_chunks == 1, s_m, s_l, s_o);
-  if (n_chunks == 1) return;
-  if (!arrive_last(a.counters + g, static_cast<unsigned int>(n_chunks), &s_flag)) return;
-  merge_partials<DT>(a, g, D, n_chunks, s_dyn + kWaves * RMAX * D);
 }
 
 bool fast_d(int D) { return D == 64 || D == 128 || D == 256; }
@@ -650,13 +654,11 @@ void plan_chunks(int dtype, int G, int R, int D, int max_rows_total, int* iters,
   *chunks = ch < 1 ? 1 : ch;
 }
 
-size_t dyn_lds_bytes(int R, int D, int chunks) {
-  return (static_cast<size_t>(kWaves) * rmax_for(R) * D + static_cast<size_t>(chunks) * R * 2) * sizeof(float);
-}
+size_t dyn_lds_bytes(int R, int D) { return static_cast<size_t>(kWaves) * rmax_for(R) * D * sizeof(float); }
 
 template <typename DT, int D, int RMAX, int MODE>
 int launch_one(const AttnArgs& a, hipStream_t stream) {
-  const size_t lds = dyn_lds_bytes(a.R, a.D, a.max_chunks);
+  const size_t lds = dyn_lds_bytes(a.R, a.D);
   const dim3 grid(a.G * a.max_chunks);
   if constexpr (D > 0) {
     auto kern = decode_attn_kernel<DT, D, RMAX, MODE>;
@@ -671,6 +673,11 @@ int launch_one(const AttnArgs& a, hipStream_t stream) {
                                 static_cast<int>(lds));
     hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, stream, a);
   }
+  int rc = tw_host::check_launch();
+  if (rc != TW_OK || a.max_chunks <= 1) return rc;
+  const int threads = ((a.D + kWave - 1) / kWave) * kWave;
+  hipLaunchKernelGGL((merge_kernel<DT, MODE>), dim3(a.G * a.R), dim3(threads), 0, stream, a,
+                     rows_per_batch(DT::code, a.D, a.R) * a.iters);
   return tw_host::check_launch();
 }
 

@@ -9,7 +9,7 @@
 //
 // 1. Scores.  A block of 4 wavefronts scores a tile of 64 pages of one KV
 //    group for all R query heads.  The tile is staged once in LDS with
-//    16-byte loads (padded row pitch, conflict-free column reads); wavefront
+//    16-byte loads (padded, 16-byte aligned row pitch); wavefront
 //    w then scores head w (w+4, ...) with lane = page, so the q > 0 choice of
 //    min or max is wave-uniform.  Order (bit-exact with the reference for
 //    D = 128): 32 accumulators, accumulator l adds the products of channels
@@ -56,6 +56,41 @@ __device__ __forceinline__ float lds_load(const uint8_t* p, BF16) {
 }
 __device__ __forceinline__ float lds_load(const uint8_t* p, F32) { return *reinterpret_cast<const float*>(p); }
 
+// x[i] = q[i] > 0 ? max[i] : min[i] for 8 consecutive channels of one page
+// (16-byte aligned LDS rows).
+__device__ __forceinline__ void select8(const uint8_t* mn, const uint8_t* mx, const float (&q)[8], float (&x)[8],
+                                        F16) {
+  const uint4 a = *reinterpret_cast<const uint4*>(mn);
+  const uint4 b = *reinterpret_cast<const uint4*>(mx);
+  const uint32_t lo[4] = {a.x, a.y, a.z, a.w}, hi[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t w = q[i] > 0.0f ? hi[i / 2] : lo[i / 2];
+    x[i] = to_f32(F16{}, static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xffffu)));
+  }
+}
+__device__ __forceinline__ void select8(const uint8_t* mn, const uint8_t* mx, const float (&q)[8], float (&x)[8],
+                                        BF16) {
+  const uint4 a = *reinterpret_cast<const uint4*>(mn);
+  const uint4 b = *reinterpret_cast<const uint4*>(mx);
+  const uint32_t lo[4] = {a.x, a.y, a.z, a.w}, hi[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t w = q[i] > 0.0f ? hi[i / 2] : lo[i / 2];
+    x[i] = to_f32(BF16{}, static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xffffu)));
+  }
+}
+__device__ __forceinline__ void select8(const uint8_t* mn, const uint8_t* mx, const float (&q)[8], float (&x)[8],
+                                        F32) {
+  float lo[8], hi[8];
+  *reinterpret_cast<float4*>(lo) = reinterpret_cast<const float4*>(mn)[0];
+  *reinterpret_cast<float4*>(lo + 4) = reinterpret_cast<const float4*>(mn)[1];
+  *reinterpret_cast<float4*>(hi) = reinterpret_cast<const float4*>(mx)[0];
+  *reinterpret_cast<float4*>(hi + 4) = reinterpret_cast<const float4*>(mx)[1];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = q[i] > 0.0f ? hi[i] : lo[i];
+}
+
 // Adjacent-pair tree over the 32 accumulators.
 __device__ __forceinline__ float tree32(float (&acc)[32]) {
 #pragma unroll
@@ -95,11 +130,7 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
       const int page = rem / quads;
       const int qd = rem - page * quads;
       const uint4 v = reinterpret_cast<const uint4*>(which ? mx : mn)[static_cast<int64_t>(page) * quads + qd];
-      uint32_t* dst = reinterpret_cast<uint32_t*>(lds + (which * kTilePages + page) * pitch) + qd * 4;
-      dst[0] = v.x;
-      dst[1] = v.y;
-      dst[2] = v.z;
-      dst[3] = v.w;
+      *reinterpret_cast<uint4*>(lds + (which * kTilePages + page) * pitch + qd * 16) = v;
     }
   } else {
     const int total = 2 * np * words;
@@ -123,7 +154,7 @@ __global__ __launch_bounds__(kBlock) void quest_score_kernel(ScoreArgs a) {
   const int tile = blockIdx.x - g * tiles;
   const int p0 = tile * kTilePages;
   const int np = (a.P - p0) < kTilePages ? (a.P - p0) : kTilePages;
-  const int pitch = a.D * static_cast<int>(sizeof(S)) + 4;
+  const int pitch = a.D * static_cast<int>(sizeof(S)) + 16;  // 16-byte aligned rows, padded
   // The group's queries go to LDS in the same round trip as the tile.
   float* q_lds = reinterpret_cast<float*>(lds + 2 * kTilePages * pitch);
   {
@@ -143,13 +174,20 @@ __global__ __launch_bounds__(kBlock) void quest_score_kernel(ScoreArgs a) {
     for (int l = 0; l < 32; ++l) acc[l] = 0.0f;
     const uint8_t* min_row = lds + lane * pitch;
     const uint8_t* max_row = lds + (kTilePages + lane) * pitch;
-    if (DFIX > 0) {
+    if constexpr (DFIX > 0) {
+      // 8 channels per step: 16-byte reads of both rows (independent of q,
+      // so they issue back to back), then the q > 0 choice on the data.
 #pragma unroll
-      for (int d = 0; d < DFIX; ++d) {
-        const float qd = qh[d];
-        const uint8_t* src = (qd > 0.0f) ? max_row : min_row;
-        const float x = lds_load(src + d * es, DT{});
-        acc[d & 31] = acc[d & 31] + x * qd;
+      for (int c = 0; c < DFIX / 8; ++c) {
+        float qv[8], x[8];
+        *reinterpret_cast<float4*>(qv) = *reinterpret_cast<const float4*>(qh + 8 * c);
+        *reinterpret_cast<float4*>(qv + 4) = *reinterpret_cast<const float4*>(qh + 8 * c + 4);
+        select8(min_row + 8 * c * es, max_row + 8 * c * es, qv, x, DT{});
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int d = 8 * c + i;
+          acc[d & 31] = acc[d & 31] + x[i] * qv[i];
+        }
       }
     } else {
       for (int c = 0; c * 32 < D; ++c) {
@@ -573,7 +611,7 @@ template <typename DT>
 int launch_score(const ScoreArgs& a, hipStream_t stream) {
   const int tiles = (a.P + kTilePages - 1) / kTilePages;
   const size_t lds = static_cast<size_t>(2 * kTilePages) *
-                         (static_cast<size_t>(a.D) * sizeof(typename DT::storage) + 4) +
+                         (static_cast<size_t>(a.D) * sizeof(typename DT::storage) + 16) +
                      static_cast<size_t>(a.R) * a.D * sizeof(float);
   if (lds > 160 * 1024) return TW_EUNSUPPORTED;  // gfx950: 160 KB of LDS per CU
   const dim3 grid(tiles * a.G);

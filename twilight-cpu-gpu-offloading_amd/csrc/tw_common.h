@@ -112,66 +112,77 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 }
 __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t w = __shfl_xor(v, o);
-    v = v > w ? v : w;
-  }
-  return v;
+// Wavefront reductions and scans on DPP lane permutations (a VALU operand
+// modifier, no LDS round trip): a butterfly inside each 16-lane row, then the
+// four row results combined through readlane.  GFX9 DPP encodings.
+constexpr int kDppQuadXor1 = 0xb1;       // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4e;       // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowShr1 = 0x111;       // row_shr:n = 0x110 + n
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, 0xf, 0xf, false));
 }
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t w = __shfl_xor(v, o);
-    v = v < w ? v : w;
-  }
-  return v;
+// Row shift with lanes that shift in from outside the row reading 0.
+template <int N>
+__device__ __forceinline__ uint32_t dpp_shr_zero(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), kDppRowShr1 - 1 + N, 0xf, 0xf, true));
 }
-__device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-__device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t x, int lane) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), lane));
 }
 
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_allreduce_u32(uint32_t v, Op op) {
+  v = op(v, dpp_u32<kDppQuadXor1>(v));
+  v = op(v, dpp_u32<kDppQuadXor2>(v));
+  v = op(v, dpp_u32<kDppRowHalfMirror>(v));
+  v = op(v, dpp_u32<kDppRowMirror>(v));
+  return op(op(readlane_u32(v, 0), readlane_u32(v, 16)), op(readlane_u32(v, 32), readlane_u32(v, 48)));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return wave_allreduce_u32(v, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  return wave_allreduce_u32(v, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  return static_cast<int>(
+      wave_allreduce_u32(static_cast<uint32_t>(v), [](uint32_t a, uint32_t b) { return a + b; }));
+}
+__device__ __forceinline__ float wave_max_f32(float v) {
+  return __uint_as_float(wave_allreduce_u32(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  return __uint_as_float(wave_allreduce_u32(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  }));
+}
+
+// Inclusive prefix sum over lanes (wraps modulo 2^32).
+__device__ __forceinline__ uint32_t wave_prefix_sum_u32(uint32_t v) {
+  v += dpp_shr_zero<1>(v);
+  v += dpp_shr_zero<2>(v);
+  v += dpp_shr_zero<4>(v);
+  v += dpp_shr_zero<8>(v);
+  const uint32_t t0 = readlane_u32(v, 15), t1 = readlane_u32(v, 31), t2 = readlane_u32(v, 47);
+  const int l = lane_id();
+  return v + (l >= 16 ? t0 : 0u) + (l >= 32 ? t1 : 0u) + (l >= 48 ? t2 : 0u);
+}
+__device__ __forceinline__ int wave_prefix_sum_i32(int v) {
+  return static_cast<int>(wave_prefix_sum_u32(static_cast<uint32_t>(v)));
+}
 // Inclusive suffix sum over lanes: result in lane l is sum of v over lanes >= l.
 __device__ __forceinline__ uint32_t wave_suffix_sum_u32(uint32_t v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    uint32_t w = __shfl_down(v, o);
-    if (l + o < 64) v += w;
-  }
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_suffix_sum_u64(uint64_t v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    uint64_t w = __shfl_down(v, o);
-    if (l + o < 64) v += w;
-  }
-  return v;
-}
-// Inclusive prefix sum over lanes.
-__device__ __forceinline__ int wave_prefix_sum_i32(int v) {
-  const int l = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int w = __shfl_up(v, o);
-    if (l >= o) v += w;
-  }
-  return v;
+  const uint32_t p = wave_prefix_sum_u32(v);
+  return readlane_u32(p, 63) - p + v;
 }
 
 // Index of the lowest set lane in a non-empty ballot.
