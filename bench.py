@@ -2,8 +2,9 @@
 
 Workload (default): one decode step of a Llama-3-8B-shaped model's
 sparse-decode KV path at 32K context with every KV head resident in HBM --
-32 layers x (fused Quest score + top-k + row plan, append of the decode
-token's K/V, sparse GQA decode attention over the selected rows).  Per layer:
+32 layers x (Quest score + top-k + GQA union plan, then the sparse GQA
+decode attention over sink ++ union pages ++ recent window ++ decode token,
+which also appends the decode token's K/V to the cache).  Per layer:
 8 KV heads, 4 query heads per KV head, head_dim 128, fp16, page size 16,
 sink 64, recent 256, a Quest budget of 128 pages (2048 tokens) per query
 head.  K carries 4 outlier channels (x8) and 16 planted relevant pages per
@@ -135,12 +136,13 @@ class QuestWorkload:
                                        self.plan_counts[layer], plan_masks=self.plan_masks[layer],
                                        max_pages=self.max_pages, sink=self.SINK, recent=self.RECENT,
                                        block_size=self.BS, length=self.L, append_position=self.L,
-                                       out=self.out[layer])
+                                       cur_k=self.cur_k[layer], cur_v=self.cur_v[layer], out=self.out[layer])
 
     def step(self) -> None:
+        """One decode step: per layer, Quest selection then attention with the
+        decode token's K/V appended to the cache in the same launch."""
         for layer in range(self.layers):
             self.select(layer)
-            self.append(layer)
             self.attend(layer)
 
     # algorithmic bytes ---------------------------------------------------
@@ -151,9 +153,10 @@ class QuestWorkload:
         fixed = min(self.SINK, self.L) + (self.RECENT - 1) + 1  # sink + recent + the decode token
         rows = (self.plan_counts.double().sum().item() * self.BS + G * fixed) / self.layers
         select = 2 * P * D * e * G + G * R * P * 4 * 2 + G * R * k * 4 + G * R * D * 4
-        attention = rows * 2 * D * e + 2 * G * R * D * e
-        append = 4 * G * D * e
-        return {"select": select, "attention": attention, "append": append, "rows_per_group": rows / G}
+        # K/V rows (the decode token's come from registers), q, out, and the
+        # append of the decode token (read + write)
+        attention = (rows - G) * 2 * D * e + 2 * G * R * D * e + 4 * G * D * e
+        return {"select": select, "attention": attention, "rows_per_group": rows / G}
 
 
 def graph_of(fn, warm: int = 2):
@@ -293,7 +296,6 @@ def main(argv=None) -> int:
     print("[bench] capturing graphs", file=sys.stderr, flush=True)
     g_step = graph_of(w.step)
     g_sel = graph_of(lambda: [w.select(i) for i in range(w.layers)])
-    g_app = graph_of(lambda: [w.append(i) for i in range(w.layers)])
     g_att = graph_of(lambda: [w.attend(i) for i in range(w.layers)])
 
     for _ in range(args.warmup):
@@ -309,10 +311,9 @@ def main(argv=None) -> int:
 
     reps = max(20, args.steps // 2)
     t_sel = time_graph(g_sel, reps) / w.layers
-    t_app = time_graph(g_app, reps) / w.layers
     t_att = time_graph(g_att, reps) / w.layers
     by = w.bytes_per_layer()
-    layer_bytes = by["select"] + by["attention"] + by["append"]
+    layer_bytes = by["select"] + by["attention"]
     layer_s = wall / w.layers
     value = layer_bytes / layer_s / 1e9
     kern = {
@@ -320,7 +321,6 @@ def main(argv=None) -> int:
                          "GBps": round(by["select"] / t_sel / 1e9, 1)},
         "decode_attention": {"us": round(t_att * 1e6, 2), "bytes": int(by["attention"]),
                              "GBps": round(by["attention"] / t_att / 1e9, 1)},
-        "append_kv": {"us": round(t_app * 1e6, 2), "bytes": int(by["append"])},
     }
     dom = "decode_attention" if t_att >= t_sel else "quest_select"
     ach = kern[dom]["GBps"]
@@ -338,8 +338,9 @@ def main(argv=None) -> int:
         "dtype": "f16",
         "data": "synthetic",
         "config": {
-            "workload": "quest-32k-hbm: Llama-3-8B-shaped sparse-decode KV path, 32 layers x (score+top-k+row "
-                        "plan, append, sparse GQA decode attention), all KV in HBM",
+            "workload": "quest-32k-hbm: Llama-3-8B-shaped sparse-decode KV path, 32 layers x (Quest score + "
+                        "top-k + GQA union plan, sparse GQA decode attention with the decode token's K/V "
+                        "append), all KV in HBM",
             "layers": w.layers, "context": w.L, "kv_heads": w.G, "q_per_kv": w.R, "head_dim": w.D,
             "page_size": w.BS, "budget_pages": w.k, "scored_pages": w.P, "sink": w.SINK, "recent": w.RECENT,
         },

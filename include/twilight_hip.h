@@ -160,17 +160,21 @@ int tw_quest_select(const float* q, const void* page_min, const void* page_max, 
 size_t tw_decode_attention_workspace_size(int G, int R, int D, int max_rows);
 /* The same attention over a union plan from tw_quest_select: group g's rows
  * are [0, sink_end) ++ the plan's pages expanded to block_size rows each
- * (heads per plan_masks, nullable = all) ++ [recent_start, length) ++
- * append_position (if >= 0), read by position from the group's entry
- * (k_base + (g*entry_stride_rows + pos)*D).  max_rows bounds every group's
- * row count (sink_end + max_pages*block_size + recent rows + 1) and sizes
- * the grid and the workspace (tw_decode_attention_workspace_size). */
+ * (heads per plan_masks, nullable = all) ++ [recent_start, length) ++ the
+ * decode token, read by position from the group's entry
+ * (k_base + (g*entry_stride_rows + pos)*D).  The decode token is the cache
+ * row append_position (if >= 0) or, when cur_k/cur_v ([G][D]) are given,
+ * cur_k/cur_v -- which the call then also writes to row append_position of
+ * every entry (the per-step append, quest_offload_cache.py:633-638, fused
+ * into the attention launch).  max_rows bounds every group's row count
+ * (sink_end + max_pages*block_size + recent rows + 1) and sizes the grid and
+ * the workspace (tw_decode_attention_workspace_size). */
 int tw_decode_attention_pages(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
                               int D, const int32_t* plan_pages, const uint8_t* plan_masks,
                               const int32_t* plan_counts, int64_t plan_stride, int max_rows,
                               int64_t entry_stride_rows, int sink, int recent, int block_size, int length,
-                              int append_position, float softmax_scale, void* out, void* workspace,
-                              size_t workspace_bytes, void* stream);
+                              int append_position, const void* cur_k, const void* cur_v, float softmax_scale,
+                              void* out, void* workspace, size_t workspace_bytes, void* stream);
 int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G,
                         int R, int D, const int32_t* rows, const uint8_t* row_masks,
                         const int32_t* row_counts, int64_t rows_stride, int64_t entry_stride_rows,

@@ -309,11 +309,21 @@ def test_decode_attention_pages(K, dev, dtype, G, R, D, L, k, sink, recent, bs, 
         pages[g, :n] = torch.randperm(P, generator=g0)[:n].sort().values.to(torch.int32)
         pm[g, :n] = torch.randint(1, 1 << R, (n,), generator=g0).to(torch.uint8)
         counts[g] = n
-    out = K.decode_attention_pages(q.to(dev), kc.to(dev), vc.to(dev), pages.to(dev), counts.to(dev),
+    kd, vd = kc.to(dev), vc.to(dev)
+    out = K.decode_attention_pages(q.to(dev), kd, vd, pages.to(dev), counts.to(dev),
                                    plan_masks=pm.to(dev) if masked else None, max_pages=max_pages, sink=sink,
                                    recent=recent, block_size=bs, length=L, append_position=L)
+    # the fused form: the decode token from cur_k/cur_v, appended to row L in the same launch
+    ck, cv = randn((G, D), dtype, seed=44), randn((G, D), dtype, seed=45)
+    out2 = K.decode_attention_pages(q.to(dev), kd, vd, pages.to(dev), counts.to(dev),
+                                    plan_masks=pm.to(dev) if masked else None, max_pages=max_pages, sink=sink,
+                                    recent=recent, block_size=bs, length=L, append_position=L,
+                                    cur_k=ck.to(dev), cur_v=cv.to(dev))
     torch.cuda.synchronize()
+    assert same_bits(kd[:, L], ck) and same_bits(vd[:, L], cv)
+    assert same_bits(kd[:, :L], kc[:, :L]) and same_bits(vd[:, :L], vc[:, :L])
     ref = np.zeros((G, R, D))
+    ref2 = np.zeros((G, R, D))
     all_heads = (1 << R) - 1
     for g in range(G):
         n = int(counts[g])
@@ -326,7 +336,11 @@ def test_decode_attention_pages(K, dev, dtype, G, R, D, L, k, sink, recent, bs, 
                            torch.full((L - recent_start + 1,), all_heads)]).to(torch.uint8).numpy()
         ref[g] = oracle.decode_attention(q[g].float().numpy(), kc[g, rows].float().numpy(),
                                          vc[g, rows].float().numpy(), 1.0 / math.sqrt(D), m)
+        kc[g, L], vc[g, L] = ck[g], cv[g]
+        ref2[g] = oracle.decode_attention(q[g].float().numpy(), kc[g, rows].float().numpy(),
+                                          vc[g, rows].float().numpy(), 1.0 / math.sqrt(D), m)
     _close(out, ref)
+    _close(out2, ref2)
 
 
 @pytest.mark.parametrize("dtype,B,Hk,R,D", [("bf16", 8, 1, 4, 128), ("f16", 3, 2, 3, 128), ("bf16", 5, 1, 1, 4)])

@@ -64,6 +64,10 @@ struct AttnArgs {
   const int32_t* plan_counts;
   int64_t plan_stride;
   int sink, recent, bs, length, append_position;
+  // Page-plan mode with cur_k/cur_v: the decode token is attended from
+  // cur_k/cur_v and also appended to the cache at append_position.
+  void* k_append;
+  void* v_append;
   float* part_ml;           // [G][max_chunks][R][2]  (m, l)
   float* part_o;            // [G][max_chunks][R][D]
   unsigned int* counters;   // [G]
@@ -162,8 +166,11 @@ __device__ __forceinline__ GroupRows group_rows(const AttnArgs& a, int g, int D)
     gr.page_end = sink_end + nu * a.bs;
     gr.recent_start = recent_start;
     gr.recent_end = gr.page_end + (a.length - recent_start);
-    const int n = gr.recent_end + (a.append_position >= 0 ? 1 : 0);
-    gr.n_list = n > a.max_rows ? a.max_rows : n;
+    // the decode token comes from the cache row append_position, or from
+    // cur_k/cur_v when they are given
+    const int n = gr.recent_end + (a.append_position >= 0 && a.cur_k == nullptr ? 1 : 0);
+    const int cap = a.max_rows - (a.cur_k != nullptr ? 1 : 0);  // max_rows counts the decode token
+    gr.n_list = n > cap ? (cap > 0 ? cap : 0) : n;
     gr.base = static_cast<int64_t>(g) * a.entry_stride * D;
     gr.stride = D;
     gr.win_start = 0;
@@ -192,15 +199,28 @@ __device__ __forceinline__ GroupRows group_rows(const AttnArgs& a, int g, int D)
   return gr;
 }
 
+// Append the decode token of group g to its cache entry (chunk 0's block).
+template <typename S>
+__device__ __forceinline__ void append_decode_token(const AttnArgs& a, int g, int D) {
+  if (a.k_append == nullptr) return;
+  const int64_t row = (static_cast<int64_t>(g) * a.entry_stride + a.append_position) * D;
+  const S* ck = static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D;
+  const S* cv = static_cast<const S*>(a.cur_v) + static_cast<int64_t>(g) * D;
+  S* dk = static_cast<S*>(a.k_append) + row;
+  S* dv = static_cast<S*>(a.v_append) + row;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    dk[i] = ck[i];
+    dv[i] = cv[i];
+  }
+}
+
 // Split-K combine: one block per (group, head), thread t = channel t.  Runs
 // as its own launch after the partial kernel, so it reads the partials with
 // plain loads and issues every chunk's loads at once (one round trip); the
 // chunk weights exp2(m_c - M) and 1 / sum(w_c l_c) come from a block
 // reduction over the chunks' (m, l).  Groups that fit one chunk were written
 // by the partial kernel itself and are skipped.
-constexpr int kMergeBatch = 64;
-
-template <typename DT, int MODE>
+template <typename DT, int MODE, int NB>
 __global__ __launch_bounds__(512) void merge_kernel(AttnArgs a, int rows_per_block) {
   using S = typename DT::storage;
   const int R = a.R;
@@ -215,49 +235,36 @@ __global__ __launch_bounds__(512) void merge_kernel(AttnArgs a, int rows_per_blo
   const int wave = t / kWave;
   const int n_waves = (blockDim.x + kWave - 1) / kWave;
   __shared__ float s_red[8];
-  __shared__ float s_w[kMaxChunks];
+  __shared__ float s_w[NB];
   const int64_t base = static_cast<int64_t>(g) * a.max_chunks;
   const int ch_t = t < D ? t : D - 1;
-  float acc = 0.0f;
-  float L = 0.0f;
-  for (int cb = 0; cb < n_chunks; cb += kMergeBatch) {
-    float ov[kMergeBatch];
+  // every load of the merge in one batch: o of all chunks for channel t, and
+  // (m, l) of chunk t
+  float ov[NB];
 #pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
-      int c = cb + j;
-      c = c < n_chunks ? c : n_chunks - 1;
-      ov[j] = a.part_o[((base + c) * R + r) * D + ch_t];
-    }
-    if (cb == 0) {
-      // chunk weights: thread c holds chunk c's (m, l)
-      float m = -INFINITY, l = 0.0f;
-      for (int c = t; c < n_chunks; c += blockDim.x) {
-        const float2 v = *reinterpret_cast<const float2*>(a.part_ml + ((base + c) * R + r) * 2);
-        m = fmaxf(m, v.x);
-      }
-      m = wave_max_f32(m);
-      if (lane == 0) s_red[wave] = m;
-      __syncthreads();
-      float M = -INFINITY;
-      for (int w = 0; w < n_waves; ++w) M = fmaxf(M, s_red[w]);
-      __syncthreads();
-      for (int c = t; c < n_chunks; c += blockDim.x) {
-        const float2 v = *reinterpret_cast<const float2*>(a.part_ml + ((base + c) * R + r) * 2);
-        const float w = exp2_rel(v.x, M);
-        s_w[c] = w;
-        l += w * v.y;
-      }
-      l = wave_sum_f32(l);
-      if (lane == 0) s_red[wave] = l;
-      __syncthreads();
-      for (int w = 0; w < n_waves; ++w) L += s_red[w];
-    }
-#pragma unroll
-    for (int j = 0; j < kMergeBatch; ++j) {
-      const int c = cb + j;
-      acc += (c < n_chunks ? s_w[c] : 0.0f) * ov[j];
-    }
+  for (int c = 0; c < NB; ++c) {
+    const int cc = c < n_chunks ? c : n_chunks - 1;
+    ov[c] = a.part_o[((base + cc) * R + r) * D + ch_t];
   }
+  const int ct = t < n_chunks ? t : n_chunks - 1;
+  const float2 mlv = *reinterpret_cast<const float2*>(a.part_ml + ((base + ct) * R + r) * 2);
+  const float m = t < n_chunks ? mlv.x : -INFINITY;
+  float mw = wave_max_f32(m);
+  if (lane == 0) s_red[wave] = mw;
+  __syncthreads();
+  float M = -INFINITY;
+  for (int w = 0; w < n_waves; ++w) M = fmaxf(M, s_red[w]);
+  __syncthreads();
+  const float w_t = t < n_chunks ? exp2_rel(m, M) : 0.0f;
+  if (t < NB) s_w[t] = w_t;
+  const float lw = wave_sum_f32(w_t * (t < n_chunks ? mlv.y : 0.0f));
+  if (lane == 0) s_red[wave] = lw;
+  __syncthreads();
+  float L = 0.0f;
+  for (int w = 0; w < n_waves; ++w) L += s_red[w];
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NB; ++c) acc += (c < n_chunks ? s_w[c] : 0.0f) * ov[c];
   if (t < D) {
     S* out = static_cast<S*>(a.out) + (static_cast<int64_t>(g) * R + r) * D;
     out[t] = from_f32(DT{}, L > 0.0f ? acc / L : 0.0f);
@@ -329,6 +336,7 @@ __global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(
     return;
   }
   if (chunk >= n_chunks) return;
+  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D);
 
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
@@ -530,6 +538,7 @@ __global__ __launch_bounds__(kBlock) void decode_attn_generic(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
+  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D);
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
   const S* qg = static_cast<const S*>(a.q) + static_cast<int64_t>(g) * R * D;
@@ -675,9 +684,15 @@ int launch_one(const AttnArgs& a, hipStream_t stream) {
   }
   int rc = tw_host::check_launch();
   if (rc != TW_OK || a.max_chunks <= 1) return rc;
-  const int threads = ((a.D + kWave - 1) / kWave) * kWave;
-  hipLaunchKernelGGL((merge_kernel<DT, MODE>), dim3(a.G * a.R), dim3(threads), 0, stream, a,
-                     rows_per_batch(DT::code, a.D, a.R) * a.iters);
+  // a block must cover every chunk with one (m, l) per thread
+  int threads = ((a.D + kWave - 1) / kWave) * kWave;
+  threads = threads < a.max_chunks ? ((a.max_chunks + kWave - 1) / kWave) * kWave : threads;
+  const int rpb = rows_per_batch(DT::code, a.D, a.R) * a.iters;
+  if (a.max_chunks <= 64) {
+    hipLaunchKernelGGL((merge_kernel<DT, MODE, 64>), dim3(a.G * a.R), dim3(threads), 0, stream, a, rpb);
+  } else {
+    hipLaunchKernelGGL((merge_kernel<DT, MODE, kMaxChunks>), dim3(a.G * a.R), dim3(threads), 0, stream, a, rpb);
+  }
   return tw_host::check_launch();
 }
 
@@ -810,8 +825,9 @@ extern "C" int tw_decode_attention_pages(const void* q, const void* k_base, cons
                                          int R, int D, const int32_t* plan_pages, const uint8_t* plan_masks,
                                          const int32_t* plan_counts, int64_t plan_stride, int max_rows,
                                          int64_t entry_stride_rows, int sink, int recent, int block_size,
-                                         int length, int append_position, float softmax_scale, void* out,
-                                         void* workspace, size_t workspace_bytes, void* stream) {
+                                         int length, int append_position, const void* cur_k, const void* cur_v,
+                                         float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
+                                         void* stream) {
   if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr || G <= 0 || R <= 0 || R > 8 ||
       D <= 0 || D > 512 || (D % 2) != 0 || max_rows < 0)
     return TW_EINVAL;
@@ -819,16 +835,24 @@ extern "C" int tw_decode_attention_pages(const void* q, const void* k_base, cons
   if (plan_pages == nullptr || plan_counts == nullptr || plan_stride < 1 || entry_stride_rows <= 0) return TW_EINVAL;
   if (sink < 0 || recent <= 0 || block_size <= 0 || length < 0 || append_position >= entry_stride_rows)
     return TW_EINVAL;
+  if ((cur_k == nullptr) != (cur_v == nullptr)) return TW_EINVAL;
   if (tw::fast_d(D)) {
     const uintptr_t align = 16;
     if ((reinterpret_cast<uintptr_t>(q) % align) || (reinterpret_cast<uintptr_t>(k_base) % align) ||
-        (reinterpret_cast<uintptr_t>(v_base) % align))
+        (reinterpret_cast<uintptr_t>(v_base) % align) || (reinterpret_cast<uintptr_t>(cur_k) % align) ||
+        (reinterpret_cast<uintptr_t>(cur_v) % align))
       return TW_EINVAL;
   }
   size_t ml_off, o_off, total;
   tw::workspace_layout(G, R, D, max_rows, &ml_off, &o_off, &total);
   if (workspace == nullptr || workspace_bytes < total) return TW_ENOMEM;
   tw::AttnArgs a{};
+  a.cur_k = cur_k;
+  a.cur_v = cur_v;
+  if (cur_k != nullptr && append_position >= 0) {
+    a.k_append = const_cast<void*>(k_base);
+    a.v_append = const_cast<void*>(v_base);
+  }
   a.q = q;
   a.k = k_base;
   a.v = v_base;

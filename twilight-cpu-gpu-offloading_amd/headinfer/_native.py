@@ -50,7 +50,7 @@ _HIP_SIGNATURES = {
     "tw_decode_attention": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i64, vp, i32, i32, i32, vp, vp,
                                   f32, vp, vp, szt, vp]),
     "tw_decode_attention_pages": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32, i32, i32,
-                                        i32, f32, vp, vp, szt, vp]),
+                                        i32, vp, vp, f32, vp, vp, szt, vp]),
     "tw_gather_rows": (i32, [vp, vp, i64, vp, vp, i64, i32, i32, vp, vp, vp, vp]),
     "tw_host_device_pointer": (i32, [vp, ctypes.POINTER(ctypes.c_void_p)]),
     "tw_append_kv": (i32, [vp, vp, i32, i32, i32, vp, vp, i64, i32, i64, vp]),

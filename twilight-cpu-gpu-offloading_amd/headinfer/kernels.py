@@ -358,13 +358,17 @@ def decode_attention_pages(
     block_size: int,
     length: int,
     append_position: int = -1,
+    cur_k: Optional[torch.Tensor] = None,
+    cur_v: Optional[torch.Tensor] = None,
     softmax_scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Sparse GQA decode attention over a union plan from quest_select: group
     g sees [0, sink_end) ++ its union pages (heads per plan_masks) ++ the
-    recent window ++ append_position.  q [G,R,D]; k_cache/v_cache [G, Lmax, D].
-    Returns [G,R,D]."""
+    recent window ++ the decode token.  q [G,R,D]; k_cache/v_cache [G, Lmax, D].
+    The decode token is cache row append_position, or cur_k/cur_v [G, D] when
+    given -- then they are also appended to row append_position of the cache
+    in the same launch.  Returns [G,R,D]."""
     if q.ndim != 3 or q.dtype not in _KEY_DTYPES:
         raise ValueError("q must be [G, R, D]")
     G, R, D = q.shape
@@ -384,21 +388,31 @@ def decode_attention_pages(
         raise ValueError("plan_counts must be [G] int32")
     if not 0 <= max_pages <= plan_pages.shape[1]:
         raise ValueError("max_pages must be within the plan width")
-    dev = _require_device(q, k_cache, v_cache, plan_pages, plan_masks, plan_counts, what="decode_attention_pages")
-    _require_contiguous(q, what="decode_attention_pages")
+    if (cur_k is None) != (cur_v is None):
+        raise ValueError("cur_k and cur_v go together")
+    if cur_k is not None and (cur_k.shape != (G, D) or cur_k.dtype != q.dtype or cur_v.shape != cur_k.shape
+                              or cur_v.dtype != q.dtype):
+        raise ValueError("cur_k/cur_v must be [G, D] in q's dtype")
+    if cur_k is not None and append_position >= k_cache.shape[1]:
+        raise ValueError("append_position outside the cache")
+    dev = _require_device(q, k_cache, v_cache, plan_pages, plan_masks, plan_counts, cur_k, cur_v,
+                          what="decode_attention_pages")
+    _require_contiguous(q, cur_k, cur_v, what="decode_attention_pages")
     if out is None:
         out = torch.empty_like(q)
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
     max_rows = plan_max_rows(max_pages, sink=sink, recent=recent, block_size=block_size, length=length,
-                             append_position=append_position)
+                             append_position=append_position if cur_k is None else -1)
+    max_rows += 0 if cur_k is None else 1
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
     with torch.cuda.device(dev):
         check(hip().tw_decode_attention_pages(ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D,
                                               ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
                                               plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink, recent,
-                                              block_size, length, append_position, scale, ptr(out), ptr(ws),
-                                              ws.numel(), stream_handle(dev)), "decode_attention_pages")
+                                              block_size, length, append_position, ptr(cur_k), ptr(cur_v), scale,
+                                              ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
+              "decode_attention_pages")
     return out
 
 
