@@ -135,6 +135,61 @@ int tw_quest_select(const float* q, const void* page_min, const void* page_max, 
                     int append_position, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Twilight stage 2, INT4 QK estimate over the B0 candidates of every head.
+ * Replaces fused_affine_int4_qk (twilight_fused_qk.py:12-55) with the
+ * 1/sqrt(D) scaling of prepare_layer_selection (twilight_offload_cache.py:
+ * 1197-1261).  The candidates of head r of group g are the b0_pages pages it
+ * chose in stage 1, ascending, each expanded to block_size positions
+ * sink + page*block_size + [0, block_size): candidate n = slot*block_size + i
+ * of the head's slot-th page.  They are read from the stage-1 union plan
+ * (plan_pages / plan_masks / plan_counts of tw_quest_select, k = b0_pages)
+ * so every INT4 row is loaded once for all R heads.
+ *   q [G][R][D] fp32 (16-byte aligned); packed[(g*quant_entry_stride + t)*
+ *   D/2 + d/2] (low nibble = even channel), scale/minimum [G][
+ *   quant_entry_stride] in dtype (tw_build_page_metadata's quantized keys);
+ *   quant_rows valid rows per entry (candidates beyond it are skipped).
+ *   logits [G][R][b0_pages*block_size] fp32 = qk_scale * (q . k~), k~_d =
+ *   code_d*scale + min, reduced as 8-channel sequential sums combined by an
+ *   adjacent-pair tree.  D in {64, 128, 256}; R <= 8.
+ * ---------------------------------------------------------------------- */
+int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t* packed, const void* scale,
+                   const void* minimum, int dtype, int64_t quant_entry_stride, int64_t quant_rows,
+                   const int32_t* plan_pages,
+                   const uint8_t* plan_masks, const int32_t* plan_counts, int64_t plan_stride, int b0_pages,
+                   int sink, int block_size, float qk_scale, float* logits, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Twilight stage 2, top-p budgets, token selection and the GQA union.
+ * Replaces the top-p of ExactTopPGraph (twilight_exact_top_p_graph.py:19-32;
+ * inline twilight_offload_cache.py:1274-1310), matched_budget_counts
+ * (twilight_offload_cache.py:50-86, per group, every head's capacity N) and
+ * the GPU GQA union (twilight_offload_cache.py:1517-1614).
+ *   logits [G][R][N] from tw_twilight_qk, N = b0_pages*block_size <= 8192;
+ *   sel_pages [G][R][b0_pages] the stage-1 pages (ascending) that map
+ *   candidate n of head r to position sink + sel_pages[n/bs]*bs + n%bs.
+ *   desired (nullable) [G][R]: the exact top-p count -- masses E_n =
+ *   floor(exp(l_n - max l) * 2^40) with a fixed fp32 exp polynomial, Z = sum
+ *   E_n, and the smallest c whose c largest logits (ties to the lower n)
+ *   carry at least ceil(round(top_p*2^24) * Z / 2^24).
+ *   budget_mode 0 (dynamic): each head keeps its desired candidates.
+ *   budget_mode 1 (matched): allocated = matched_budget_counts(desired,
+ *   target_total) per group, and each head keeps its top-allocated
+ *   candidates (ties to the lower n).  R <= target_total <= R*N.
+ *   allocated (nullable) [G][R] the kept counts.
+ *   rows[g*rows_stride + i] gets group g's ascending union of [0, sink_end),
+ *   the kept positions of its R heads and [recent_start, length), then
+ *   append_position if >= 0; row_counts[g] the count.  rows_stride >=
+ *   length + 1.  workspace: tw_twilight_select_workspace_size bytes, zero
+ *   before the first call (the library leaves its counters zero).
+ * ---------------------------------------------------------------------- */
+size_t tw_twilight_select_workspace_size(int G, int R, int N);
+int tw_twilight_select(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,
+                       float top_p, int budget_mode, int target_total, int32_t* desired, int32_t* allocated,
+                       int32_t* rows, int32_t* row_counts, int64_t rows_stride, int sink, int recent,
+                       int block_size, int length, int append_position, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * a22: sparse GQA decode attention, split-K over selected rows, one query
  * token per group.  Replaces _flash_attention_varlen_forward
  * (mp.py:21-52) on the decode paths that call it (GQA group branch

@@ -37,6 +37,13 @@ __all__ = [
     "quest_budget",
     "decode_attention",
     "host_gather",
+    "det_exp",
+    "int4_qk",
+    "top_p_count",
+    "top_p_threshold",
+    "mass",
+    "matched_budget_counts",
+    "twilight_layer",
 ]
 
 DTYPES = ("f16", "bf16", "f32")
@@ -68,6 +75,16 @@ def lib() -> ctypes.CDLL:
         L.or_topk_sorted.argtypes = [vp, i32, i32, i64, i32, vp]
         L.or_quest_row_plan.restype = i32
         L.or_quest_row_plan.argtypes = [vp, i32, i32, i32, i32, i32, i32, i32, i32, vp, vp]
+        L.or_det_exp.restype = ctypes.c_float
+        L.or_det_exp.argtypes = [ctypes.c_float]
+        L.or_int4_qk.restype = None
+        L.or_int4_qk.argtypes = [vp, i32, vp, vp, vp, i32, vp, i32, ctypes.c_float, vp]
+        L.or_top_p_count.restype = i32
+        L.or_top_p_count.argtypes = [vp, i32, ctypes.c_float, vp]
+        L.or_top_p_threshold.restype = ctypes.c_uint64
+        L.or_top_p_threshold.argtypes = [ctypes.c_uint64, ctypes.c_float]
+        L.or_mass.restype = ctypes.c_uint64
+        L.or_mass.argtypes = [ctypes.c_float, ctypes.c_float]
         _lib = L
     return _lib
 
@@ -234,3 +251,103 @@ def decode_attention(q: np.ndarray, keys: np.ndarray, values: np.ndarray, scale:
 def host_gather(src: np.ndarray, rows: np.ndarray) -> np.ndarray:
     """index_select of rows (quest_offload_cache.py:580-587)."""
     return src[np.asarray(rows, np.int64)]
+
+
+# ------------------------------------------------------------- Twilight
+def det_exp(x: float) -> float:
+    """The shared deterministic exp of x <= 0 (twilight_oracle.c)."""
+    return float(lib().or_det_exp(float(np.float32(x))))
+
+
+def int4_qk(q: np.ndarray, packed: np.ndarray, scale: np.ndarray, minimum: np.ndarray, dtype: str,
+            rows: np.ndarray, qk_scale: float) -> np.ndarray:
+    """INT4 QK estimate of one query head q [D] over candidate rows (a9)."""
+    q = np.ascontiguousarray(q, np.float32)
+    packed = np.ascontiguousarray(packed, np.uint8)
+    rows = np.ascontiguousarray(rows, np.int64)
+    out = np.zeros(rows.shape[0], np.float32)
+    lib().or_int4_qk(_ptr(q), q.shape[0], _ptr(packed), _ptr(np.ascontiguousarray(scale, _storage(dtype))),
+                     _ptr(np.ascontiguousarray(minimum, _storage(dtype))), _DT[dtype], _ptr(rows), rows.shape[0],
+                     float(np.float32(qk_scale)), _ptr(out))
+    return out
+
+
+def top_p_count(logits: np.ndarray, top_p: float) -> tuple[int, int]:
+    """(desired, Z) of the exact top-p count (a10)."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    z = ctypes.c_uint64()
+    d = lib().or_top_p_count(_ptr(lg), lg.shape[0], float(np.float32(top_p)), ctypes.byref(z))
+    return int(d), int(z.value)
+
+
+def top_p_threshold(z: int, top_p: float) -> int:
+    return int(lib().or_top_p_threshold(z, float(np.float32(top_p))))
+
+
+def mass(logit: float, lmax: float) -> int:
+    return int(lib().or_mass(float(np.float32(logit)), float(np.float32(lmax))))
+
+
+def matched_budget_counts(desired, target_total, capacities):
+    """Largest-remainder reallocation (twilight_offload_cache.py:50-86),
+    restated: each head keeps at least 1; the remaining target is split in
+    proportion to desired (float64), floors first, then +1 by (fractional
+    remainder desc, desired desc, index asc) until the target is met; any
+    excess is taken back from the heads with the smallest (desired, index)."""
+    n = len(desired)
+    if n == 0 or n != len(capacities):
+        raise ValueError("desired and capacities must be non-empty and aligned")
+    if min(desired) <= 0 or min(capacities) <= 0:
+        raise ValueError("desired counts and capacities must be positive")
+    if target_total < n or target_total > sum(capacities):
+        raise ValueError("target_total is infeasible")
+    remaining = target_total - n
+    total = float(sum(float(v) for v in desired))
+    raw = [remaining * float(v) / total for v in desired]
+    counts = [1 + min(capacities[i] - 1, math.floor(raw[i])) for i in range(n)]
+    while sum(counts) < target_total:
+        order = sorted((i for i in range(n) if counts[i] < capacities[i]),
+                       key=lambda i: (-(raw[i] - math.floor(raw[i])), -desired[i], i))
+        best = order[0]
+        counts[best] += 1
+        raw[best] = math.floor(raw[best])
+    while sum(counts) > target_total:
+        worst = min((i for i in range(n) if counts[i] > 1), key=lambda i: (desired[i], i))
+        counts[worst] -= 1
+    return counts
+
+
+def twilight_layer(q: np.ndarray, page_min: np.ndarray, page_max: np.ndarray, packed: np.ndarray,
+                   scale: np.ndarray, minimum: np.ndarray, dtype: str, *, length: int, sink: int, recent: int,
+                   block_size: int, b0_pages: int, top_p: float, budget_mode: str = "dynamic",
+                   fixed_pages: int = 0, qk_scale: float | None = None):
+    """Twilight selection of one KV group (prepare_layer_selection,
+    twilight_offload_cache.py:996-1614) in this build's defined orders.
+
+    q [R, D] fp32; page_min/page_max [P, D] (the P scored pages); packed
+    [T, D/2], scale/minimum [T] (storage of dtype).  Returns a dict with the
+    stage-1 pages [R, b0] (ascending), logits [R, N], desired [R], allocated
+    [R], selected positions per head (ascending) and the GQA union rows."""
+    R, D = q.shape
+    P = page_min.shape[0]
+    qk_scale = float(np.float32(1.0 / math.sqrt(D))) if qk_scale is None else qk_scale
+    sink_end, recent_start, _ = selection_window(length, sink, recent)
+    sc = quest_score(q[None], page_min[None], page_max[None], dtype)[0]
+    pages = topk_sorted(sc, b0_pages)  # [R, b0] ascending (candidate order)
+    offs = np.arange(block_size)
+    cand = (sink + pages[:, :, None] * block_size + offs).reshape(R, -1)  # [R, N]
+    logits = np.stack([int4_qk(q[r], packed, scale, minimum, dtype, cand[r], qk_scale) for r in range(R)])
+    N = cand.shape[1]
+    desired = np.array([top_p_count(logits[r], top_p)[0] for r in range(R)])
+    if budget_mode == "dynamic":
+        allocated = desired.copy()
+    else:
+        target = fixed_pages * block_size * R
+        allocated = np.array(matched_budget_counts(list(map(int, desired)), target, [N] * R))
+    selected = []
+    for r in range(R):
+        idx = topk_sorted(logits[r][None], int(allocated[r]))[0]
+        selected.append(np.sort(cand[r][idx]))
+    union = np.unique(np.concatenate([np.arange(sink_end), *selected, np.arange(recent_start, length)]))
+    return {"pages": pages, "candidates": cand, "logits": logits, "desired": desired, "allocated": allocated,
+            "selected": selected, "union": union}

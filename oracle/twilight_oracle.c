@@ -279,3 +279,105 @@ int or_quest_row_plan(const int64_t* sel, int R, int k, int P, int sink, int rec
   free(pm);
   return n;
 }
+
+/* ================================================================ Twilight */
+/* Deterministic exp of x <= 0, the one definition the GPU kernels share:
+ *   x < -28 -> 0 (e^-28 < 2^-40, below the top-p mass resolution);
+ *   t = x * log2(e) (fp32), n = round-half-even(t), f = t - n (exact),
+ *   2^f by its Taylor polynomial sum_k (ln 2)^k f^k / k! to degree 6 in
+ *   Horner form (separate multiply and add), scaled by 2^n exactly.
+ * Every step is one IEEE fp32 operation, so CPU and GPU agree bit for bit. */
+float or_det_exp(float x) {
+  if (!(x >= -28.0f)) return 0.0f;
+  const float t = x * 1.44269504088896341f;
+  const float n = rintf(t);
+  const float f = t - n;
+  float p = 1.54035303933816e-4f;
+  p = p * f + 1.33335581464284e-3f;
+  p = p * f + 9.61812910762848e-3f;
+  p = p * f + 5.55041086648216e-2f;
+  p = p * f + 2.40226506959101e-1f;
+  p = p * f + 6.93147180559945e-1f;
+  p = p * f + 1.0f;
+  return ldexpf(p, (int)n);
+}
+
+/* a9: INT4 QK estimate of one query head (twilight_fused_qk.py:12-55,
+ * twilight_offload_cache.py:1197-1261) in this build's defined order:
+ *   k_d = f32(code_d) * f32(scale) + f32(min)            (dequantize, :40-47)
+ *   acc_j = sum_{i<8} k_{8j+i} * q_{8j+i}, sequential from +0 (j = 0..D/8-1)
+ *   dot = adjacent-pair tree over the acc_j
+ *   logit = dot * qk_scale   (qk_scale = fp32(1/sqrt(D)))
+ * rows[n] selects the packed row of candidate n.  D in {64, 128, 256}. */
+void or_int4_qk(const float* q, int D, const uint8_t* packed, const void* scale, const void* minimum, int dt,
+                const int64_t* rows, int N, float qk_scale, float* out) {
+  float acc[64];
+  for (int n = 0; n < N; ++n) {
+    const int64_t t = rows[n];
+    const float s = load_f(scale, t, dt), m = load_f(minimum, t, dt);
+    const int chunks = D / 8;
+    for (int j = 0; j < chunks; ++j) {
+      float a = 0.0f;
+      for (int i = 0; i < 8; ++i) {
+        const int d = 8 * j + i;
+        const uint32_t b = packed[t * (D / 2) + d / 2];
+        const uint32_t code = (d & 1) ? (b >> 4) & 15u : b & 15u;
+        const float k = (float)code * s + m;
+        a = a + k * q[d];
+      }
+      acc[j] = a;
+    }
+    for (int w = 1; w < chunks; w <<= 1)
+      for (int j = 0; j < chunks; j += 2 * w) acc[j] = acc[j] + acc[j + w];
+    out[n] = acc[0] * qk_scale;
+  }
+}
+
+/* a10: top-p count (twilight_exact_top_p_graph.py:19-32; inline
+ * twilight_offload_cache.py:1274-1310) in this build's exact definition:
+ *   e_i = det_exp(l_i - max l), mass E_i = floor(e_i * 2^40) (int64),
+ *   Z = sum E_i, T = ceil(P24 * Z / 2^24) with P24 = round(top_p * 2^24),
+ *   desired = the smallest c >= 1 such that the c largest logits (ties to the
+ *   lowest index) carry mass >= T; at most N.
+ * All sums are exact integers, so the count does not depend on a summation
+ * order (the reference's fp32 argsort/softmax/cumsum order is unpinned).
+ * Returns desired; *z_out (nullable) gets Z. */
+typedef struct { uint32_t key; int32_t idx; } lk_t;
+static int cmp_lk(const void* a, const void* b) {
+  const lk_t* x = (const lk_t*)a;
+  const lk_t* y = (const lk_t*)b;
+  if (x->key != y->key) return x->key > y->key ? -1 : 1;
+  return x->idx < y->idx ? -1 : (x->idx > y->idx);
+}
+uint64_t or_top_p_threshold(uint64_t z, float top_p) {
+  const uint64_t p24 = (uint64_t)rintf(top_p * 16777216.0f);
+  const unsigned __int128 prod = (unsigned __int128)p24 * z;
+  return (uint64_t)((prod + ((1u << 24) - 1u)) >> 24);
+}
+uint64_t or_mass(float logit, float lmax) {
+  const float e = or_det_exp(logit - lmax);
+  return (uint64_t)(e * 1099511627776.0f); /* 2^40, exact scaling; truncation */
+}
+int or_top_p_count(const float* logits, int N, float top_p, uint64_t* z_out) {
+  if (N <= 0) return 0;
+  float lmax = logits[0];
+  for (int i = 1; i < N; ++i) lmax = logits[i] > lmax ? logits[i] : lmax;
+  lk_t* v = (lk_t*)malloc(sizeof(lk_t) * (size_t)N);
+  uint64_t z = 0;
+  for (int i = 0; i < N; ++i) {
+    v[i].key = score_key(logits[i]);
+    v[i].idx = i;
+    z += or_mass(logits[i], lmax);
+  }
+  const uint64_t T = or_top_p_threshold(z, top_p);
+  qsort(v, (size_t)N, sizeof(lk_t), cmp_lk);
+  int desired = N;
+  uint64_t cum = 0;
+  for (int c = 0; c < N; ++c) {
+    cum += or_mass(logits[v[c].idx], lmax);
+    if (cum >= T) { desired = c + 1; break; }
+  }
+  free(v);
+  if (z_out) *z_out = z;
+  return desired;
+}

@@ -1,0 +1,234 @@
+// Block-wide exact top-k over register-resident keys, shared by the Quest
+// page selection and the Twilight token selection.
+//
+// A block of 256 threads holds one row of scores as KPT contiguous order keys
+// per thread (score_key: NaN highest, -0 == +0).  A pass histograms the
+// remaining candidates into bins that are monotone in the key -- 2048 bins
+// linear in the score value over the candidates' range when that range is
+// finite, else the next 8-bit digit below the candidates' common key prefix
+// -- finds the bin holding the k-th largest, takes every candidate above it
+// and keeps the bin's keys as the next candidates.  At most 256 candidates
+// are ranked exactly by (key desc, index asc); equal candidates are taken
+// lowest index first.  The winners are reported in ascending index order.
+#pragma once
+
+#include "tw_common.h"
+
+namespace tw {
+namespace sel {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+constexpr int kMaxSelPages = 8192;  // longest row
+constexpr int kLinBins = 2048;
+
+struct SelShared {
+  uint32_t hist[kLinBins + 64];
+  uint32_t ckey[kBlock];
+  int32_t cidx[kBlock];
+  uint32_t selbits[kMaxSelPages / 32];
+  uint32_t red_max[kWaves];
+  uint32_t red_min[kWaves];
+  int scan[kWaves];
+  int bnd;
+  uint32_t bnd_above;
+  uint32_t bnd_count;
+  int flag;
+};
+
+__device__ __forceinline__ float key_value(uint32_t key) { return __uint_as_float(from_order_key32(key)); }
+
+// Exclusive prefix of v over the block's threads (thread order); *total gets
+// the block sum.  Two barriers, so consecutive calls never race on scan[].
+__device__ __forceinline__ int block_excl_scan(int v, int* scan, int* total) {
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int incl = wave_prefix_sum_i32(v);
+  if (lane == kWave - 1) scan[wave] = incl;
+  __syncthreads();
+  int before = 0, sum = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int t = scan[w];
+    before += w < wave ? t : 0;
+    sum += t;
+  }
+  __syncthreads();
+  *total = sum;
+  return before + incl - v;
+}
+
+// Bin of a key in the current pass: linear in the value (2048 bins) or an
+// 8-bit digit of the key.  Both are monotone over the candidates.
+struct BinFn {
+  bool linear;
+  float vmin, scale;
+  int shift;
+  __device__ __forceinline__ int operator()(uint32_t key) const {
+    if (linear) {
+      const int b = static_cast<int>((key_value(key) - vmin) * scale);
+      return b < kLinBins - 1 ? b : kLinBins - 1;
+    }
+    return static_cast<int>((key >> shift) & 255u);
+  }
+};
+
+// Top-k of one row held as KPT contiguous keys per thread (indices
+// KPT*t .. KPT*t + KPT - 1).  emit(slot, index) is called once per selected
+// index, slot = rank in ascending index order.
+template <int KPT, typename Emit>
+__device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& sh, Emit emit) {
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const int i0 = KPT * tid;
+  uint32_t cand = 0u, taken = 0u;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) cand |= (i0 + j < P) ? (1u << j) : 0u;
+  uint32_t need = static_cast<uint32_t>(k);
+  uint32_t ccount = static_cast<uint32_t>(P);
+  int mode = 0;  // 0: take every candidate, 1: exact rank, 2: equal keys by index
+  for (int level = 0;; ++level) {
+    if (ccount == need) break;
+    uint32_t cmax = 0u, cmin = 0xffffffffu;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool c = (cand >> j) & 1u;
+      cmax = (c && key[j] > cmax) ? key[j] : cmax;
+      cmin = (c && key[j] < cmin) ? key[j] : cmin;
+    }
+    cmax = wave_max_u32(cmax);
+    cmin = wave_min_u32(cmin);
+    if (lane == 0) {
+      sh.red_max[wave] = cmax;
+      sh.red_min[wave] = cmin;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      cmax = sh.red_max[w] > cmax ? sh.red_max[w] : cmax;
+      cmin = sh.red_min[w] < cmin ? sh.red_min[w] : cmin;
+    }
+    if (cmax == cmin) {
+      mode = 2;
+      break;
+    }
+    if (ccount <= static_cast<uint32_t>(kBlock)) {
+      mode = 1;
+      break;
+    }
+    BinFn fn;
+    const float vmin = key_value(cmin);
+    const float vmax = key_value(cmax);
+    const float range = vmax - vmin;
+    fn.vmin = vmin;
+    fn.scale = static_cast<float>(kLinBins) / range;
+    // A few linear passes resolve real score distributions; after that (or
+    // for non-finite ranges) the digit passes bound the work at 4 more.
+    fn.linear = level < 3 && __builtin_isfinite(vmin) && __builtin_isfinite(vmax) && __builtin_isfinite(range) &&
+                range > 0.0f && __builtin_isfinite(fn.scale);
+    const int hi = 31 - __clz(static_cast<int>(cmax ^ cmin));
+    fn.shift = hi >= 7 ? hi - 7 : 0;
+    const int nb = fn.linear ? kLinBins : 256;
+    const int bpt = nb / kBlock;  // bins owned by a thread
+    for (int b = tid; b < (kLinBins + 64) / 4; b += kBlock)
+      reinterpret_cast<uint4*>(sh.hist)[b] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool c = (cand >> j) & 1u;
+      atomicAdd(&sh.hist[c ? fn(key[j]) : kLinBins], 1u);
+    }
+    __syncthreads();
+    uint32_t tot = 0u;
+    for (int b = 0; b < bpt; ++b) tot += sh.hist[bpt * tid + b];
+    // suffix sums over threads (bins descending)
+    const uint32_t wincl = wave_suffix_sum_u32(tot);
+    if (lane == 0) sh.scan[wave] = static_cast<int>(wincl);
+    __syncthreads();
+    uint32_t incl = wincl;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) incl += w > wave ? static_cast<uint32_t>(sh.scan[w]) : 0u;
+    if (incl - tot < need && need <= incl) {
+      uint32_t acc = incl - tot;
+      int bin = bpt * tid;
+      uint32_t cnt = 0u;
+      for (int b = bpt - 1; b >= 0; --b) {
+        const uint32_t c = sh.hist[bpt * tid + b];
+        if (need <= acc + c) {
+          bin = bpt * tid + b;
+          cnt = c;
+          break;
+        }
+        acc += c;
+      }
+      sh.bnd = bin;
+      sh.bnd_above = acc;
+      sh.bnd_count = cnt;
+    }
+    __syncthreads();
+    const int bnd = sh.bnd;
+    need -= sh.bnd_above;
+    ccount = sh.bnd_count;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool c = (cand >> j) & 1u;
+      const int b = fn(key[j]);
+      taken |= (c && b > bnd) ? (1u << j) : 0u;
+      cand &= (c && b == bnd) ? 0xffffffffu : ~(1u << j);
+    }
+  }
+  int total;
+  if (mode == 1) {
+    // exact rank of at most kBlock candidates
+    const int mine = __popc(cand);
+    int slot = block_excl_scan(mine, sh.scan, &total);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      if ((cand >> j) & 1u) {
+        sh.ckey[slot] = key[j];
+        sh.cidx[slot] = i0 + j;
+        ++slot;
+      }
+    }
+    for (int w = tid; w < kMaxSelPages / 32; w += kBlock) sh.selbits[w] = 0u;
+    __syncthreads();
+    if (tid < static_cast<int>(ccount)) {
+      const uint32_t mk = sh.ckey[tid];
+      const int mi = sh.cidx[tid];
+      uint32_t rank = 0u;
+      for (int m = 0; m < static_cast<int>(ccount); ++m) {
+        const uint32_t km = sh.ckey[m];
+        const int im = sh.cidx[m];
+        rank += (km > mk || (km == mk && im < mi)) ? 1u : 0u;
+      }
+      if (rank < need) atomicOr(&sh.selbits[mi >> 5], 1u << (mi & 31));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int i = i0 + j;
+      const bool c = (cand >> j) & 1u;
+      taken |= (c && ((sh.selbits[(i >> 5) & (kMaxSelPages / 32 - 1)] >> (i & 31)) & 1u)) ? (1u << j) : 0u;
+    }
+  } else if (mode == 2) {
+    int before = block_excl_scan(__popc(cand), sh.scan, &total);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      if ((cand >> j) & 1u) {
+        taken |= (static_cast<uint32_t>(before) < need) ? (1u << j) : 0u;
+        ++before;
+      }
+    }
+  } else {
+    taken |= cand;
+  }
+  int slot = block_excl_scan(__popc(taken), sh.scan, &total);
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    if ((taken >> j) & 1u) emit(slot++, i0 + j);
+  }
+}
+
+}  // namespace sel
+}  // namespace tw

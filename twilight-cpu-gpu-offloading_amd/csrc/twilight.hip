@@ -1,0 +1,789 @@
+// Twilight stage 2: INT4 QK estimate over the Quest B0 candidates, softmax
+// top-p pruning (dynamic or matched budgets) and the per-KV-group token union.
+//
+// Reference: TwilightMatchedBudgetOffloadedCache.prepare_layer_selection
+// (twilight_offload_cache.py:996-1843): fused_affine_int4_qk
+// (twilight_fused_qk.py:12-55) and /sqrt(D) (:1197-1261), the top-p of
+// ExactTopPGraph (twilight_exact_top_p_graph.py:19-32, inline :1274-1310),
+// matched_budget_counts (:50-86) and the GPU GQA union (:1517-1614).
+//
+// Orders this build defines (the reference's are unpinned: cuBLAS / tl.sum
+// reductions, argsort ties, fp32 cumsum rounding):
+//   * logit = dot * qk_scale, dot = adjacent-pair tree over D/8 chunk sums,
+//     chunk sum = sum_{i<8} k_{8j+i} q_{8j+i} sequentially, k = code*scale+min;
+//   * candidate order = ascending token position (B0 pages ascending);
+//   * top-p: masses E_i = floor(det_exp(l_i - max l) * 2^40), exact integer
+//     sums; desired = smallest c whose c largest logits (ties to the lower
+//     candidate) carry >= ceil(P24 * Z / 2^24) of the total mass Z, with
+//     P24 = round(top_p * 2^24).  Sums of integers do not depend on the order
+//     they are taken in, so the GPU needs no sort: a mass-weighted histogram
+//     selection finds the boundary, as the top-k does for counts.
+#pragma clang fp contract(off)
+
+#include "select.h"
+
+namespace tw {
+namespace {
+
+using namespace sel;
+
+constexpr int kQkPagesPerBlock = 16;
+
+// ------------------------------------------------------------ INT4 QK
+struct QkArgs {
+  const float* q;             // [G][R][D]
+  const uint8_t* packed;      // entry g row t at + (g*qstride + t)*D/2
+  const void* scale;          // [G][qstride]
+  const void* minimum;
+  int64_t qstride;            // entry stride in rows
+  int64_t qrows;              // valid rows per entry
+  int G, R, D;
+  const int32_t* plan_pages;  // [G][plan_stride] union of the B0 pages, ascending
+  const uint8_t* plan_masks;  // heads that chose each page
+  const int32_t* plan_counts;
+  int64_t plan_stride;
+  int b0, sink, bs;
+  float qk_scale;
+  float* logits;              // [G][R][b0*bs]
+};
+
+template <typename DT, int DIM, int RMAX>
+__global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
+  using S = typename DT::storage;
+  constexpr int LPR = DIM / 8;        // lanes per row (8 channels = 4 code bytes each)
+  constexpr int RPI = kWave / LPR;    // rows per instruction
+  const int chunks = static_cast<int>((a.plan_stride + kQkPagesPerBlock - 1) / kQkPagesPerBlock);
+  const int g = blockIdx.x / chunks;
+  const int chunk = blockIdx.x - g * chunks;
+  int nu = a.plan_counts[g];
+  nu = nu < 0 ? 0 : (nu > a.plan_stride ? static_cast<int>(a.plan_stride) : nu);
+  const int u0 = chunk * kQkPagesPerBlock;
+  if (u0 >= nu) return;
+  const int np = (nu - u0) < kQkPagesPerBlock ? (nu - u0) : kQkPagesPerBlock;
+  const int R = a.R;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+
+  __shared__ int s_base[8];                    // candidate slots before page u0, per head
+  __shared__ int s_page[kQkPagesPerBlock];
+  __shared__ uint32_t s_mask[kQkPagesPerBlock];
+  __shared__ int s_slot[kQkPagesPerBlock][8];
+  if (tid < 8) s_base[tid] = 0;
+  __syncthreads();
+  // slot of a page for head r = number of earlier union pages head r chose
+  {
+    const uint8_t* pm = a.plan_masks + static_cast<int64_t>(g) * a.plan_stride;
+    int cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int u = tid; u < u0; u += kBlock) {
+      const uint32_t m = pm[u];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) cnt[r] += (m >> r) & 1u;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int w = wave_sum_i32(cnt[r]);
+      if (lane == 0 && w != 0) atomicAdd(&s_base[r], w);
+    }
+    if (tid < np) {
+      s_page[tid] = a.plan_pages[static_cast<int64_t>(g) * a.plan_stride + u0 + tid];
+      s_mask[tid] = pm[u0 + tid];
+    }
+  }
+  __syncthreads();
+  if (tid < 8) {
+    int run = s_base[tid];
+    for (int i = 0; i < np; ++i) {
+      s_slot[i][tid] = run;
+      run += (s_mask[i] >> tid) & 1u;
+    }
+  }
+  // queries of the group: 8 channels per lane, RMAX heads
+  const int c0 = (lane % LPR) * 8;
+  const int rig = lane / LPR;
+  float qv[RMAX][8];
+  {
+    const float* qg = a.q + static_cast<int64_t>(g) * R * DIM;
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+      const float* qr = qg + static_cast<int64_t>(r < R ? r : R - 1) * DIM + c0;
+      const float4 x = reinterpret_cast<const float4*>(qr)[0];
+      const float4 y = reinterpret_cast<const float4*>(qr)[1];
+      qv[r][0] = x.x; qv[r][1] = x.y; qv[r][2] = x.z; qv[r][3] = x.w;
+      qv[r][4] = y.x; qv[r][5] = y.y; qv[r][6] = y.z; qv[r][7] = y.w;
+    }
+  }
+  __syncthreads();
+  const int n_rows = np * a.bs;
+  const int64_t N = static_cast<int64_t>(a.b0) * a.bs;
+  const uint8_t* pk = a.packed + static_cast<int64_t>(g) * a.qstride * (DIM / 2);
+  const S* sc = static_cast<const S*>(a.scale) + static_cast<int64_t>(g) * a.qstride;
+  const S* mn = static_cast<const S*>(a.minimum) + static_cast<int64_t>(g) * a.qstride;
+  for (int row0 = wave * RPI; row0 < n_rows; row0 += kWaves * RPI) {
+    const int row = row0 + rig;
+    const bool ok = row < n_rows;
+    const int rr = ok ? row : n_rows - 1;
+    const int pi = rr / a.bs;
+    const int i = rr - pi * a.bs;
+    int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[pi]) * a.bs + i;
+    const bool in_range = t >= 0 && t < a.qrows;
+    t = in_range ? t : 0;
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(pk + t * (DIM / 2) + c0 / 2);
+    const float s = to_f32(DT{}, sc[t]);
+    const float m = to_f32(DT{}, mn[t]);
+    float k[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t code = (w >> (4 * j)) & 15u;  // byte j/2: low nibble = even channel
+      k[j] = static_cast<float>(code) * s + m;
+    }
+    const uint32_t pmask = s_mask[pi];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = acc + k[j] * qv[r][j];
+      // adjacent-pair tree over the LPR chunk sums of the row
+      acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                        kDppQuadXor1, 0xf, 0xf, false));
+      acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                        kDppQuadXor2, 0xf, 0xf, false));
+      if constexpr (LPR >= 8)
+        acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                          kDppRowHalfMirror, 0xf, 0xf, false));
+      if constexpr (LPR >= 16)
+        acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                          kDppRowMirror, 0xf, 0xf, false));
+      if constexpr (LPR >= 32) acc = acc + __shfl_xor(acc, 16);
+      const int slot = s_slot[pi][r < 8 ? r : 7];
+      if (ok && in_range && (lane % LPR) == 0 && r < R && ((pmask >> r) & 1u) && slot < a.b0) {
+        const int64_t n = static_cast<int64_t>(slot) * a.bs + i;
+        a.logits[(static_cast<int64_t>(g) * R + r) * N + n] = acc * a.qk_scale;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- top-p
+// Deterministic exp of x <= 0 (the definition the CPU oracle shares):
+// x < -28 -> 0; t = x*log2(e), n = rint(t), f = t - n, degree-6 Taylor
+// polynomial of 2^f in Horner form, scaled by 2^n.
+__device__ __forceinline__ float det_exp(float x) {
+  if (!(x >= -28.0f)) return 0.0f;
+  const float t = x * 1.44269504088896341f;
+  const float n = __builtin_rintf(t);
+  const float f = t - n;
+  float p = 1.54035303933816e-4f;
+  p = p * f + 1.33335581464284e-3f;
+  p = p * f + 9.61812910762848e-3f;
+  p = p * f + 5.55041086648216e-2f;
+  p = p * f + 2.40226506959101e-1f;
+  p = p * f + 6.93147180559945e-1f;
+  p = p * f + 1.0f;
+  return __builtin_ldexpf(p, static_cast<int>(n));
+}
+__device__ __forceinline__ uint64_t mass_of(float logit, float lmax) {
+  return static_cast<uint64_t>(det_exp(logit - lmax) * 1099511627776.0f);  // * 2^40, truncated
+}
+
+struct SelectArgs {
+  const float* logits;        // [G][R][N]
+  int G, R, N;
+  uint32_t p24;               // round(top_p * 2^24)
+  bool matched;
+  int target_total;           // matched: fixed_pages * bs * R
+  const int32_t* sel_pages;   // [G][R][b0] B0 pages per head, ascending
+  int b0;
+  int32_t* desired;           // [G][R]
+  int32_t* allocated;         // nullable [G][R]
+  uint32_t* selbits;          // [G][R][words_n] published selections
+  int words_n;
+  int32_t* rows;              // [G][rows_stride] the GQA union, ascending
+  int32_t* row_counts;        // [G]
+  int64_t rows_stride;
+  int sink, recent, bs, length, append_position;
+  unsigned int* counters;     // [G]
+};
+
+struct TopShared {
+  SelShared sel;
+  unsigned long long bin_mass[kLinBins + 64];
+  unsigned long long red64[kWaves];
+  unsigned long long cmass[kBlock];
+  float fred[kWaves];
+  int ires[4];
+  unsigned long long lres[2];
+};
+
+__device__ __forceinline__ uint64_t shfl_down_u64(uint64_t v, int o) {
+  const uint32_t lo = static_cast<uint32_t>(__shfl_down(static_cast<int>(v & 0xffffffffu), o));
+  const uint32_t hi = static_cast<uint32_t>(__shfl_down(static_cast<int>(v >> 32), o));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+// Inclusive suffix sum of 64-bit values over the lanes of a wavefront.
+__device__ __forceinline__ uint64_t wave_suffix_u64(uint64_t v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint64_t w = shfl_down_u64(v, o);
+    if (l + o < kWave) v += w;
+  }
+  return v;
+}
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, unsigned long long* red) {
+  const uint64_t s = wave_suffix_u64(v);  // lane 0 holds the wave sum
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  if (lane_id() == 0) red[wave] = s;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) t += red[w];
+  __syncthreads();
+  return t;
+}
+__device__ __forceinline__ float block_max_f32(float v, float* red) {
+  v = wave_max_f32(v);
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  if (lane_id() == 0) red[wave] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) t = fmaxf(t, red[w]);
+  __syncthreads();
+  return t;
+}
+
+// ceil(p24 * z / 2^24) without 128-bit arithmetic (p24 <= 2^24, z < 2^56).
+__device__ __forceinline__ uint64_t top_p_threshold(uint32_t p24, uint64_t z) {
+  // p24 * z = hi * 2^32 + lo with hi < 2^56 and lo < 2^57; (hi * 2^32) is a
+  // multiple of 2^24, so the ceiling only involves lo.
+  const uint64_t lo = static_cast<uint64_t>(p24) * (z & 0xffffffffu);
+  const uint64_t hi = static_cast<uint64_t>(p24) * (z >> 32);
+  return (hi << 8) + ((lo + ((1ull << 24) - 1)) >> 24);
+}
+
+// The smallest count c of top keys (key desc, index asc) whose masses sum to
+// >= need; marks them in *taken (bit j = key j of this thread).  Keys are
+// KPT contiguous per thread (indices KPT*t + j).
+template <int KPT>
+__device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)[KPT], int N, uint64_t need,
+                              TopShared& sh, uint32_t* taken_out) {
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const int i0 = KPT * tid;
+  uint32_t cand = 0u, taken = 0u;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) cand |= (i0 + j < N) ? (1u << j) : 0u;
+  int count = 0;  // keys taken so far (block-uniform)
+  int ccount = N;
+  for (int level = 0;; ++level) {
+    uint32_t cmax = 0u, cmin = 0xffffffffu;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool c = (cand >> j) & 1u;
+      cmax = (c && key[j] > cmax) ? key[j] : cmax;
+      cmin = (c && key[j] < cmin) ? key[j] : cmin;
+    }
+    cmax = wave_max_u32(cmax);
+    cmin = wave_min_u32(cmin);
+    if (lane == 0) {
+      sh.sel.red_max[wave] = cmax;
+      sh.sel.red_min[wave] = cmin;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      cmax = sh.sel.red_max[w] > cmax ? sh.sel.red_max[w] : cmax;
+      cmin = sh.sel.red_min[w] < cmin ? sh.sel.red_min[w] : cmin;
+    }
+    if (cmax == cmin) {
+      // equal keys carry equal masses: take ceil(need / m), lowest index first
+      uint64_t m = 0;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) m = ((cand >> j) & 1u) ? mass[j] : m;
+      if (lane == 0) sh.red64[wave] = 0;
+      __syncthreads();
+      if (m != 0) atomicMax(&sh.red64[wave], static_cast<unsigned long long>(m));
+      __syncthreads();
+      uint64_t mm = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) mm = sh.red64[w] > mm ? sh.red64[w] : mm;
+      const int needed = mm == 0 ? ccount : static_cast<int>((need + mm - 1) / mm);
+      int total;
+      int before = block_excl_scan(__popc(cand), sh.sel.scan, &total);
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        if ((cand >> j) & 1u) {
+          taken |= before < needed ? (1u << j) : 0u;
+          ++before;
+        }
+      }
+      count += needed < total ? needed : total;
+      break;
+    }
+    if (ccount <= kBlock) {
+      // exact: rank the candidates and walk their masses in rank order
+      int total;
+      int slot = block_excl_scan(__popc(cand), sh.sel.scan, &total);
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        if ((cand >> j) & 1u) {
+          sh.sel.ckey[slot] = key[j];
+          sh.sel.cidx[slot] = i0 + j;
+          sh.cmass[slot] = mass[j];
+          ++slot;
+        }
+      }
+      if (tid == 0) sh.ires[0] = total;  // default: every candidate
+      __syncthreads();
+      int my_rank = -1;
+      if (tid < total) {
+        const uint32_t mk = sh.sel.ckey[tid];
+        const int mi = sh.sel.cidx[tid];
+        uint64_t before = 0;
+        int rank = 0;
+        for (int m = 0; m < total; ++m) {
+          const uint32_t km = sh.sel.ckey[m];
+          const int im = sh.sel.cidx[m];
+          const bool ahead = km > mk || (km == mk && im < mi);
+          before += ahead ? sh.cmass[m] : 0ull;
+          rank += ahead ? 1 : 0;
+        }
+        my_rank = rank;
+        if (before < need && need <= before + sh.cmass[tid]) sh.ires[0] = rank + 1;
+      }
+      __syncthreads();
+      const int needed = sh.ires[0];
+      for (int w = tid; w < kMaxSelPages / 32; w += kBlock) sh.sel.selbits[w] = 0u;
+      __syncthreads();
+      if (tid < total && my_rank < needed) {
+        const int mi = sh.sel.cidx[tid];
+        atomicOr(&sh.sel.selbits[mi >> 5], 1u << (mi & 31));
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const int i = i0 + j;
+        const bool c = (cand >> j) & 1u;
+        taken |= (c && ((sh.sel.selbits[(i >> 5) & (kMaxSelPages / 32 - 1)] >> (i & 31)) & 1u)) ? (1u << j) : 0u;
+      }
+      count += needed;
+      break;
+    }
+    BinFn fn;
+    const float vmin = key_value(cmin);
+    const float vmax = key_value(cmax);
+    const float range = vmax - vmin;
+    fn.vmin = vmin;
+    fn.scale = static_cast<float>(kLinBins) / range;
+    fn.linear = level < 3 && __builtin_isfinite(vmin) && __builtin_isfinite(vmax) && __builtin_isfinite(range) &&
+                range > 0.0f && __builtin_isfinite(fn.scale);
+    const int hi = 31 - __clz(static_cast<int>(cmax ^ cmin));
+    fn.shift = hi >= 7 ? hi - 7 : 0;
+    const int nb = fn.linear ? kLinBins : 256;
+    const int bpt = nb / kBlock;
+    for (int b = tid; b < kLinBins + 64; b += kBlock) {
+      sh.sel.hist[b] = 0u;
+      sh.bin_mass[b] = 0ull;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool c = (cand >> j) & 1u;
+      const int b = c ? fn(key[j]) : kLinBins;
+      atomicAdd(&sh.sel.hist[b], 1u);
+      if (c && mass[j] != 0) atomicAdd(&sh.bin_mass[b], static_cast<unsigned long long>(mass[j]));
+    }
+    __syncthreads();
+    uint64_t tmass = 0;
+    uint32_t tcnt = 0;
+    for (int b = 0; b < bpt; ++b) {
+      tmass += sh.bin_mass[bpt * tid + b];
+      tcnt += sh.sel.hist[bpt * tid + b];
+    }
+    // suffix sums over threads (bins descending): masses and counts
+    const uint64_t wm = wave_suffix_u64(tmass);
+    const uint32_t wc = wave_suffix_sum_u32(tcnt);
+    if (lane == 0) {
+      sh.red64[wave] = wm;
+      sh.sel.scan[wave] = static_cast<int>(wc);
+    }
+    __syncthreads();
+    uint64_t incl = wm;
+    uint32_t incl_c = wc;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      incl += w > wave ? sh.red64[w] : 0ull;
+      incl_c += w > wave ? static_cast<uint32_t>(sh.sel.scan[w]) : 0u;
+    }
+    if (incl - tmass < need && need <= incl) {
+      uint64_t acc = incl - tmass;
+      uint32_t acc_c = incl_c - tcnt;
+      int bin = bpt * tid;
+      for (int b = bpt - 1; b >= 0; --b) {
+        const uint64_t mb = sh.bin_mass[bpt * tid + b];
+        if (need <= acc + mb) {
+          bin = bpt * tid + b;
+          break;
+        }
+        acc += mb;
+        acc_c += sh.sel.hist[bpt * tid + b];
+      }
+      sh.sel.bnd = bin;
+      sh.lres[0] = acc;
+      sh.sel.bnd_above = acc_c;
+      sh.sel.bnd_count = sh.sel.hist[bin];
+    }
+    __syncthreads();
+    const int bnd = sh.sel.bnd;
+    need -= sh.lres[0];
+    count += static_cast<int>(sh.sel.bnd_above);
+    ccount = static_cast<int>(sh.sel.bnd_count);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const bool c = (cand >> j) & 1u;
+      const int b = fn(key[j]);
+      taken |= (c && b > bnd) ? (1u << j) : 0u;
+      cand &= (c && b == bnd) ? 0xffffffffu : ~(1u << j);
+    }
+  }
+  *taken_out = taken;
+  return count;
+}
+
+// Matched budgets of one group (matched_budget_counts, twilight_offload_cache
+// .py:50-86): every head keeps one, the rest of target is split in proportion
+// to desired in float64, floors first, then +1 by (fractional remainder desc,
+// desired desc, index asc); any excess is taken from the heads with the
+// smallest (desired, index).  capacity: the candidate count of every head.
+__device__ void matched_counts(const int* desired, int R, int target, int capacity, int* counts) {
+  double raw[8];
+  double total = 0.0;
+  for (int i = 0; i < R; ++i) total = total + static_cast<double>(desired[i]);
+  const int remaining = target - R;
+  int sum = 0;
+  for (int i = 0; i < R; ++i) {
+    raw[i] = static_cast<double>(remaining) * static_cast<double>(desired[i]) / total;
+    const double fl = floor(raw[i]);
+    const int extra = fl < static_cast<double>(capacity - 1) ? static_cast<int>(fl) : capacity - 1;
+    counts[i] = 1 + extra;
+    sum += counts[i];
+  }
+  while (sum < target) {
+    int best = -1;
+    for (int i = 0; i < R; ++i) {
+      if (counts[i] >= capacity) continue;
+      if (best < 0) {
+        best = i;
+        continue;
+      }
+      const double fi = raw[i] - floor(raw[i]), fb = raw[best] - floor(raw[best]);
+      if (fi > fb || (fi == fb && desired[i] > desired[best])) best = i;
+    }
+    if (best < 0) break;
+    counts[best] += 1;
+    raw[best] = floor(raw[best]);
+    ++sum;
+  }
+  while (sum > target) {
+    int worst = -1;
+    for (int i = 0; i < R; ++i) {
+      if (counts[i] <= 1) continue;
+      if (worst < 0 || desired[i] < desired[worst]) worst = i;
+    }
+    if (worst < 0) break;
+    counts[worst] -= 1;
+    --sum;
+  }
+}
+
+// Bits of [a, b) within the 32-position word starting at lo.
+__device__ __forceinline__ uint32_t range_bits(int lo, int a, int b) {
+  const int s = a - lo < 0 ? 0 : (a - lo > 32 ? 32 : a - lo);
+  const int e = b - lo < 0 ? 0 : (b - lo > 32 ? 32 : b - lo);
+  const uint32_t below_e = e >= 32 ? 0xffffffffu : ((1u << e) - 1u);
+  const uint32_t below_s = s >= 32 ? 0xffffffffu : ((1u << s) - 1u);
+  return below_e & ~below_s;
+}
+
+// The last block of group g: token union of the R selections plus the sink
+// and recent windows, compacted ascending into the group's row list.
+__device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, int* scan) {
+  const int tid = threadIdx.x;
+  const int length = s.length;
+  const int sink_end = s.sink < length ? s.sink : length;
+  const int hist_recent = s.recent - 1 > 0 ? s.recent - 1 : 0;
+  const int recent_start = (length - hist_recent) > sink_end ? (length - hist_recent) : sink_end;
+  const int words = (length + 31) / 32;
+  for (int w = tid; w < words; w += kBlock) {
+    const int lo = 32 * w;
+    bits[w] = range_bits(lo, 0, sink_end) | range_bits(lo, recent_start, length);
+  }
+  __syncthreads();
+  const int n_words = s.words_n;
+  for (int r = 0; r < s.R; ++r) {
+    const uint32_t* sb = s.selbits + (static_cast<int64_t>(g) * s.R + r) * n_words;
+    const int32_t* pages = s.sel_pages + (static_cast<int64_t>(g) * s.R + r) * s.b0;
+    for (int w = tid; w < n_words; w += kBlock) {
+      uint32_t v = __hip_atomic_load(sb + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      while (v != 0u) {
+        const int b = __ffs(static_cast<int>(v)) - 1;
+        v &= v - 1u;
+        const int n = 32 * w + b;
+        const int pi = n / s.bs;
+        const int pos = s.sink + pages[pi] * s.bs + (n - pi * s.bs);
+        if (pos >= 0 && pos < length) atomicOr(&bits[pos >> 5], 1u << (pos & 31));
+      }
+    }
+  }
+  __syncthreads();
+  // compaction: thread t owns a contiguous run of words
+  const int wpt = (words + kBlock - 1) / kBlock;
+  const int w0 = tid * wpt;
+  int cnt = 0;
+  for (int w = w0; w < w0 + wpt && w < words; ++w) cnt += __popc(bits[w]);
+  int total;
+  int slot = block_excl_scan(cnt, scan, &total);
+  int32_t* rows = s.rows + static_cast<int64_t>(g) * s.rows_stride;
+  for (int w = w0; w < w0 + wpt && w < words; ++w) {
+    uint32_t v = bits[w];
+    while (v != 0u) {
+      const int b = __ffs(static_cast<int>(v)) - 1;
+      v &= v - 1u;
+      rows[slot++] = 32 * w + b;
+    }
+  }
+  const int count = total + (s.append_position >= 0 ? 1 : 0);
+  if (tid == 0) {
+    if (s.append_position >= 0) rows[total] = s.append_position;
+    s.row_counts[g] = count;
+  }
+}
+
+template <int KPT>
+__device__ __forceinline__ void load_logits(const float* row, int N, uint32_t (&key)[KPT], float& lmax,
+                                            float* fred) {
+  const int i0 = KPT * static_cast<int>(threadIdx.x);
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int i = i0 + j;
+    const float v = row[i < N ? i : N - 1];
+    key[j] = score_key(v);
+    mx = (i < N && v > mx) ? v : mx;
+  }
+  lmax = block_max_f32(mx, fred);
+}
+
+// Publish this row's selection bits (bit n = candidate n selected).
+template <int KPT>
+__device__ __forceinline__ void publish_selection(uint32_t* row_bits, int words, uint32_t taken, TopShared& sh) {
+  const int i0 = KPT * static_cast<int>(threadIdx.x);
+  for (int w = threadIdx.x; w < words; w += kBlock) sh.sel.selbits[w] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    if ((taken >> j) & 1u) atomicOr(&sh.sel.selbits[(i0 + j) >> 5], 1u << ((i0 + j) & 31));
+  }
+  __syncthreads();
+  for (int w = threadIdx.x; w < words; w += kBlock)
+    __hip_atomic_store(row_bits + w, sh.sel.selbits[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Stage A: the top-p count of every (group, head) row; in dynamic mode also
+// the selection and the group's token union.
+template <int KPT>
+__global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
+  __shared__ __align__(16) TopShared sh;
+  extern __shared__ __align__(16) uint32_t union_bits[];
+  const int row = blockIdx.x;
+  const int g = row / s.R;
+  const int N = s.N;
+  uint32_t key[KPT];
+  float lmax;
+  load_logits<KPT>(s.logits + static_cast<int64_t>(row) * N, N, key, lmax, sh.fred);
+  uint64_t mass[KPT];
+  uint64_t local = 0;
+  const int i0 = KPT * static_cast<int>(threadIdx.x);
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    mass[j] = (i0 + j < N) ? mass_of(key_value(key[j]), lmax) : 0ull;
+    local += mass[j];
+  }
+  const uint64_t z = block_sum_u64(local, sh.red64);
+  uint64_t need = top_p_threshold(s.p24, z);
+  if (need == 0) {
+    // no mass at all (non-finite logits): one key, the largest, as on the CPU
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) mass[j] = (i0 + j < N) ? 1ull : 0ull;
+    need = 1;
+  }
+  uint32_t taken;
+  int desired = block_top_mass<KPT>(key, mass, N, need, sh, &taken);
+  desired = desired < 1 ? 1 : (desired > N ? N : desired);
+  if (threadIdx.x == 0) s.desired[row] = desired;
+  if (s.matched) return;
+  if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = desired;
+  publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
+  if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
+  build_token_union(s, g, union_bits, sh.sel.scan);
+}
+
+// Stage B (matched budgets): allocation from the group's desired counts, the
+// top-allocated selection of each head and the group's token union.
+template <int KPT>
+__global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) {
+  __shared__ __align__(16) TopShared sh;
+  extern __shared__ __align__(16) uint32_t union_bits[];
+  const int row = blockIdx.x;
+  const int g = row / s.R;
+  const int r = row - g * s.R;
+  const int N = s.N;
+  if (threadIdx.x == 0) {
+    int d[8], c[8];
+    for (int i = 0; i < s.R; ++i) d[i] = s.desired[static_cast<int64_t>(g) * s.R + i];
+    matched_counts(d, s.R, s.target_total, N, c);
+    sh.ires[1] = c[r];
+  }
+  uint32_t key[KPT];
+  float lmax;
+  load_logits<KPT>(s.logits + static_cast<int64_t>(row) * N, N, key, lmax, sh.fred);  // (barriers inside)
+  int k = sh.ires[1];
+  k = k < 1 ? 1 : (k > N ? N : k);
+  if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = k;
+  const int i0 = KPT * static_cast<int>(threadIdx.x);
+  uint32_t taken = 0u;
+  block_topk<KPT>(key, N, k, sh.sel, [&](int, int idx) { taken |= 1u << (idx - i0); });
+  publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
+  if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
+  build_token_union(s, g, union_bits, sh.sel.scan);
+}
+
+// --------------------------------------------------------------- launch
+template <typename DT, int DIM>
+int launch_qk_r(const QkArgs& a, hipStream_t stream) {
+  const int chunks = static_cast<int>((a.plan_stride + kQkPagesPerBlock - 1) / kQkPagesPerBlock);
+  const dim3 grid(a.G * chunks);
+  if (a.R <= 4) {
+    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 4>), grid, dim3(kBlock), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 8>), grid, dim3(kBlock), 0, stream, a);
+  }
+  return tw_host::check_launch();
+}
+
+template <typename DT>
+int launch_qk(const QkArgs& a, hipStream_t stream) {
+  switch (a.D) {
+    case 64: return launch_qk_r<DT, 64>(a, stream);
+    case 128: return launch_qk_r<DT, 128>(a, stream);
+    case 256: return launch_qk_r<DT, 256>(a, stream);
+    default: return TW_EUNSUPPORTED;
+  }
+}
+
+template <int KPT>
+int launch_select_kpt(const SelectArgs& s, hipStream_t stream) {
+  const size_t lds = static_cast<size_t>((s.length + 31) / 32) * 4 + 16;
+  if (lds + sizeof(TopShared) > 160 * 1024) return TW_EUNSUPPORTED;
+  if (lds + sizeof(TopShared) > 64 * 1024) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(twilight_topp_kernel<KPT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess ||
+        hipFuncSetAttribute(reinterpret_cast<const void*>(twilight_matched_kernel<KPT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
+      return tw_host::check_launch();
+  }
+  const dim3 grid(s.G * s.R);
+  hipLaunchKernelGGL(twilight_topp_kernel<KPT>, grid, dim3(kBlock), lds, stream, s);
+  int rc = tw_host::check_launch();
+  if (rc != TW_OK || !s.matched) return rc;
+  hipLaunchKernelGGL(twilight_matched_kernel<KPT>, grid, dim3(kBlock), lds, stream, s);
+  return tw_host::check_launch();
+}
+
+int launch_select(const SelectArgs& s, hipStream_t stream) {
+  if (s.N <= 4 * kBlock) return launch_select_kpt<4>(s, stream);
+  if (s.N <= 8 * kBlock) return launch_select_kpt<8>(s, stream);
+  if (s.N <= 16 * kBlock) return launch_select_kpt<16>(s, stream);
+  return launch_select_kpt<32>(s, stream);
+}
+
+size_t counter_bytes(int G) { return ((static_cast<size_t>(G) * 4 + 255) / 256) * 256; }
+
+}  // namespace
+}  // namespace tw
+
+extern "C" int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t* packed, const void* scale,
+                              const void* minimum, int dtype, int64_t quant_entry_stride, int64_t quant_rows,
+                              const int32_t* plan_pages,
+                              const uint8_t* plan_masks, const int32_t* plan_counts, int64_t plan_stride,
+                              int b0_pages, int sink, int block_size, float qk_scale, float* logits, void* stream) {
+  if (q == nullptr || packed == nullptr || scale == nullptr || minimum == nullptr || plan_pages == nullptr ||
+      plan_masks == nullptr || plan_counts == nullptr || logits == nullptr)
+    return TW_EINVAL;
+  if (G <= 0 || R <= 0 || R > 8 || b0_pages <= 0 || sink < 0 || block_size <= 0 || plan_stride < 1 ||
+      quant_entry_stride <= 0 || quant_rows <= 0 || quant_rows > quant_entry_stride)
+    return TW_EINVAL;
+  if (D != 64 && D != 128 && D != 256) return TW_EUNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(q) % 16) || (reinterpret_cast<uintptr_t>(packed) % 4)) return TW_EINVAL;
+  tw::QkArgs a{q, packed, scale, minimum, quant_entry_stride, quant_rows, G, R, D, plan_pages, plan_masks, plan_counts,
+               plan_stride, b0_pages, sink, block_size, qk_scale, logits};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TW_DTYPE_F16: return tw::launch_qk<tw::F16>(a, s);
+    case TW_DTYPE_BF16: return tw::launch_qk<tw::BF16>(a, s);
+    case TW_DTYPE_F32: return tw::launch_qk<tw::F32>(a, s);
+    default: return TW_EINVAL;
+  }
+}
+
+extern "C" size_t tw_twilight_select_workspace_size(int G, int R, int N) {
+  if (G <= 0 || R <= 0 || N <= 0) return 0;
+  const size_t words = static_cast<size_t>((N + 31) / 32);
+  return tw::counter_bytes(G) + static_cast<size_t>(G) * R * words * 4 + static_cast<size_t>(G) * R * 4;
+}
+
+extern "C" int tw_twilight_select(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,
+                                  float top_p, int budget_mode, int target_total, int32_t* desired,
+                                  int32_t* allocated, int32_t* rows, int32_t* row_counts, int64_t rows_stride,
+                                  int sink, int recent, int block_size, int length, int append_position,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (logits == nullptr || sel_pages == nullptr || rows == nullptr || row_counts == nullptr) return TW_EINVAL;
+  if (G <= 0 || R <= 0 || R > 8 || N <= 0 || b0_pages <= 0 || N != b0_pages * block_size) return TW_EINVAL;
+  if (N > tw::sel::kMaxSelPages) return TW_EUNSUPPORTED;
+  if (!(top_p > 0.0f) || !(top_p <= 1.0f) || (budget_mode != 0 && budget_mode != 1)) return TW_EINVAL;
+  if (sink < 0 || recent <= 0 || block_size <= 0 || length < 0) return TW_EINVAL;
+  if (budget_mode == 1 && (target_total < R || target_total > static_cast<int64_t>(R) * N)) return TW_EINVAL;
+  // every union row fits: sink + recent + R*N selected + the decode row
+  if (rows_stride < static_cast<int64_t>(length) + 1) return TW_EINVAL;
+  if (workspace == nullptr || workspace_bytes < tw_twilight_select_workspace_size(G, R, N)) return TW_ENOMEM;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const int words = (N + 31) / 32;
+  tw::SelectArgs s{};
+  s.logits = logits;
+  s.G = G;
+  s.R = R;
+  s.N = N;
+  s.p24 = static_cast<uint32_t>(__builtin_rintf(top_p * 16777216.0f));
+  s.matched = budget_mode == 1;
+  s.target_total = target_total;
+  s.sel_pages = sel_pages;
+  s.b0 = b0_pages;
+  s.counters = reinterpret_cast<unsigned int*>(ws);
+  s.selbits = reinterpret_cast<uint32_t*>(ws + tw::counter_bytes(G));
+  s.words_n = words;
+  s.desired = desired != nullptr ? desired
+                                 : reinterpret_cast<int32_t*>(s.selbits + static_cast<int64_t>(G) * R * words);
+  s.allocated = allocated;
+  s.rows = rows;
+  s.row_counts = row_counts;
+  s.rows_stride = rows_stride;
+  s.sink = sink;
+  s.recent = recent;
+  s.bs = block_size;
+  s.length = length;
+  s.append_position = append_position;
+  return tw::launch_select(s, static_cast<hipStream_t>(stream));
+}

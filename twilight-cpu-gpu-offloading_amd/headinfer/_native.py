@@ -51,6 +51,10 @@ _HIP_SIGNATURES = {
                                   f32, vp, vp, szt, vp]),
     "tw_decode_attention_pages": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32, i32, i32,
                                         i32, vp, vp, f32, vp, vp, szt, vp]),
+    "tw_twilight_qk": (i32, [vp, i32, i32, i32, vp, vp, vp, i32, i64, i64, vp, vp, vp, i64, i32, i32, i32, f32, vp, vp]),
+    "tw_twilight_select_workspace_size": (szt, [i32, i32, i32]),
+    "tw_twilight_select": (i32, [vp, i32, i32, i32, vp, i32, f32, i32, i32, vp, vp, vp, vp, i64, i32, i32, i32, i32,
+                                 i32, vp, szt, vp]),
     "tw_gather_rows": (i32, [vp, vp, i64, vp, vp, i64, i32, i32, vp, vp, vp, vp]),
     "tw_host_device_pointer": (i32, [vp, ctypes.POINTER(ctypes.c_void_p)]),
     "tw_append_kv": (i32, [vp, vp, i32, i32, i32, vp, vp, i64, i32, i64, vp]),

@@ -284,6 +284,109 @@ def quest_select(
                                     ptr(ws), ws.numel(), stream_handle(dev)), "quest_select")
 
 
+# ---------------------------------------------------------------- Twilight
+def twilight_qk(
+    q: torch.Tensor,
+    packed: torch.Tensor,
+    scale: torch.Tensor,
+    minimum: torch.Tensor,
+    plan_pages: torch.Tensor,
+    plan_masks: torch.Tensor,
+    plan_counts: torch.Tensor,
+    b0_pages: int,
+    *,
+    sink: int,
+    block_size: int,
+    qk_scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """INT4 QK estimate of every head over its B0 candidates (one launch).
+
+    q [G,R,D] fp32; packed [G, >=T, D/2] uint8 with scale/minimum [G, >=T]
+    (build_page_metadata's INT4 outputs); the stage-1 union plan of
+    quest_select with k = b0_pages.  Returns logits [G, R, b0_pages*bs] fp32
+    in candidate order (each head's pages ascending, block_size rows each)."""
+    if q.ndim != 3 or q.dtype != torch.float32 or not q.is_contiguous():
+        raise ValueError("q must be contiguous [G, R, D] fp32")
+    G, R, D = q.shape
+    if packed.dtype != torch.uint8 or packed.ndim != 3 or packed.shape[0] != G or packed.shape[2] != D // 2:
+        raise ValueError("packed must be [G, T, D/2] uint8")
+    if packed.stride(2) != 1 or packed.stride(1) != D // 2 or packed.stride(0) % (D // 2):
+        raise ValueError("packed rows must be contiguous")
+    qe = packed.stride(0) // (D // 2)
+    if scale.dtype not in _KEY_DTYPES or minimum.dtype != scale.dtype or scale.ndim != 2:
+        raise ValueError("scale/minimum must be [G, T] in one key dtype")
+    if scale.stride(1) != 1 or minimum.stride(1) != 1 or scale.stride(0) != qe or minimum.stride(0) != qe:
+        raise ValueError("scale/minimum must share the packed entry stride")
+    if plan_pages.dtype != torch.int32 or plan_pages.ndim != 2 or plan_pages.shape[0] != G \
+            or plan_pages.stride(1) != 1 or plan_masks.stride() != plan_pages.stride() \
+            or plan_masks.dtype != torch.uint8 or plan_counts.dtype != torch.int32 or plan_counts.shape != (G,):
+        raise ValueError("plan_pages/plan_masks/plan_counts must be quest_select's union plan")
+    dev = _require_device(q, packed, scale, minimum, plan_pages, plan_masks, plan_counts, out, what="twilight_qk")
+    N = b0_pages * block_size
+    if out is None:
+        out = torch.empty((G, R, N), dtype=torch.float32, device=dev)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (G, R, N) or not out.is_contiguous():
+        raise ValueError("out must be contiguous [G, R, b0_pages*block_size] fp32")
+    qs = float(torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32)) if qk_scale is None else float(qk_scale)
+    with torch.cuda.device(dev):
+        check(hip().tw_twilight_qk(ptr(q), G, R, D, ptr(packed), ptr(scale), ptr(minimum), _dt(scale), qe,
+                                   packed.shape[1], ptr(plan_pages), ptr(plan_masks), ptr(plan_counts), plan_pages.stride(0),
+                                   b0_pages, sink, block_size, qs, ptr(out), stream_handle(dev)), "twilight_qk")
+    return out
+
+
+def twilight_select(
+    logits: torch.Tensor,
+    sel_pages: torch.Tensor,
+    *,
+    top_p: float,
+    budget_mode: str,
+    target_total: int = 0,
+    rows: torch.Tensor,
+    row_counts: torch.Tensor,
+    desired: Optional[torch.Tensor] = None,
+    allocated: Optional[torch.Tensor] = None,
+    sink: int,
+    recent: int,
+    block_size: int,
+    length: int,
+    append_position: int = -1,
+) -> None:
+    """Top-p counts, (matched) budgets, token selection and the GQA union row
+    list of one layer.  logits [G,R,N] from twilight_qk; sel_pages [G,R,b0]
+    the stage-1 pages; rows [G, >=length+1] int32 and row_counts [G] int32
+    receive the union (ascending, then append_position if >= 0); desired /
+    allocated [G,R] int32 (optional) the counts."""
+    if budget_mode not in ("dynamic", "matched"):
+        raise ValueError("budget_mode must be 'dynamic' or 'matched'")
+    if logits.dtype != torch.float32 or logits.ndim != 3 or not logits.is_contiguous():
+        raise ValueError("logits must be contiguous [G, R, N] fp32")
+    G, R, N = logits.shape
+    if sel_pages.dtype != torch.int32 or sel_pages.ndim != 3 or sel_pages.shape[:2] != (G, R) \
+            or not sel_pages.is_contiguous():
+        raise ValueError("sel_pages must be contiguous [G, R, b0] int32")
+    b0 = sel_pages.shape[2]
+    if b0 * block_size != N:
+        raise ValueError("logits must hold b0_pages * block_size candidates per head")
+    if rows.dtype != torch.int32 or rows.ndim != 2 or rows.shape[0] != G or rows.stride(1) != 1:
+        raise ValueError("rows must be [G, stride] int32")
+    if row_counts.dtype != torch.int32 or tuple(row_counts.shape) != (G,):
+        raise ValueError("row_counts must be [G] int32")
+    for t in (desired, allocated):
+        if t is not None and (t.dtype != torch.int32 or tuple(t.shape) != (G, R) or not t.is_contiguous()):
+            raise ValueError("desired/allocated must be contiguous [G, R] int32")
+    dev = _require_device(logits, sel_pages, rows, row_counts, desired, allocated, what="twilight_select")
+    nbytes = hip().tw_twilight_select_workspace_size(G, R, N)
+    ws = WORKSPACE.get(dev, "twilight_select", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_twilight_select(ptr(logits), G, R, N, ptr(sel_pages), b0, float(top_p),
+                                       1 if budget_mode == "matched" else 0, int(target_total), ptr(desired),
+                                       ptr(allocated), ptr(rows), ptr(row_counts), rows.stride(0), sink, recent,
+                                       block_size, length, append_position, ptr(ws), ws.numel(),
+                                       stream_handle(dev)), "twilight_select")
+
+
 # --------------------------------------------------------------- attention
 def decode_attention_rows(
     q: torch.Tensor,
