@@ -150,13 +150,26 @@ int tw_quest_select(const float* q, const void* page_min, const void* page_max, 
  *   quant_rows valid rows per entry (candidates beyond it are skipped).
  *   logits [G][R][b0_pages*block_size] fp32 = qk_scale * (q . k~), k~_d =
  *   code_d*scale + min, reduced as 8-channel sequential sums combined by an
- *   adjacent-pair tree.  D in {64, 128, 256}; R <= 8.
+ *   adjacent-pair tree.  D = 4 .. 256, a power of two (8 channels per lane
+ *   chunk, D channels when D < 8); R <= 8.
  * ---------------------------------------------------------------------- */
 int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t* packed, const void* scale,
                    const void* minimum, int dtype, int64_t quant_entry_stride, int64_t quant_rows,
                    const int32_t* plan_pages,
                    const uint8_t* plan_masks, const int32_t* plan_counts, int64_t plan_stride, int b0_pages,
                    int sink, int block_size, float qk_scale, float* logits, void* stream);
+
+/* INT4 QK at explicit positions: the fused_affine_int4_qk call surface
+ * (twilight_fused_qk.py:34-55).  q [G][R][D] fp32; positions [G][R][N] int64
+ * rows of entry g's INT4 keys (layout as in tw_twilight_qk; rows outside
+ * [0, quant_rows) give no output).  materialize = 0: out [G][R][N] =
+ * qk_scale * (q . k~) in tw_twilight_qk's order (qk_scale 1 reproduces the
+ * raw dot); materialize != 0: out [G][R][N][D] = k~ (16-byte aligned).
+ * D = 4 .. 256, a power of two. */
+int tw_int4_qk_positions(const float* q, int G, int R, int D, const uint8_t* packed, const void* scale,
+                         const void* minimum, int dtype, int64_t quant_entry_stride, int64_t quant_rows,
+                         const int64_t* positions, int N, float qk_scale, int materialize, float* out,
+                         void* stream);
 
 /* ------------------------------------------------------------------------
  * Twilight stage 2, top-p budgets, token selection and the GQA union.
@@ -176,6 +189,8 @@ int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t* packed, c
  *   target_total) per group, and each head keeps its top-allocated
  *   candidates (ties to the lower n).  R <= target_total <= R*N.
  *   allocated (nullable) [G][R] the kept counts.
+ *   head_bits (nullable) [G][R][ceil(N/32)]: bit n of head r's row is set
+ *   when the head keeps candidate n (its own selection before the union).
  *   rows[g*rows_stride + i] gets group g's ascending union of [0, sink_end),
  *   the kept positions of its R heads and [recent_start, length), then
  *   append_position if >= 0; row_counts[g] the count.  rows_stride >=
@@ -185,8 +200,8 @@ int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t* packed, c
 size_t tw_twilight_select_workspace_size(int G, int R, int N);
 int tw_twilight_select(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,
                        float top_p, int budget_mode, int target_total, int32_t* desired, int32_t* allocated,
-                       int32_t* rows, int32_t* row_counts, int64_t rows_stride, int sink, int recent,
-                       int block_size, int length, int append_position, void* workspace,
+                       uint32_t* head_bits, int32_t* rows, int32_t* row_counts, int64_t rows_stride, int sink,
+                       int recent, int block_size, int length, int append_position, void* workspace,
                        size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
@@ -254,6 +269,36 @@ int tw_decode_attention(const void* q, const void* k_base, const void* v_base, i
 int tw_gather_rows(const void* src_k, const void* src_v, int64_t src_row_limit,
                    const int64_t* src_rows, const int64_t* dst_rows, int64_t n, int D,
                    int elem_bytes, void* dst_k, void* dst_v, int32_t* error_flag, void* stream);
+
+/* Group-union gather of the GQA group path: replaces the per-layer union
+ * gather + H2D + current-token gap fill of update_layer_gqa_group_ragged
+ * (twilight_offload_cache.py:2936-3101,3290-3310).  Entry of group g starts
+ * at source row entry_row0 + g*entry_row_step (row = entry*Lmax + pos, the
+ * slab layout of slab_cache.py:36-73).  Group g's rows[g*rows_stride + i],
+ * i < row_counts[g] (device, clamped to max_count), then cur_k[g]/cur_v[g]
+ * ([G][D]), are written back to back into dst ([dst_capacity][D]); group g
+ * starts at sum_{h<g}(row_counts[h] + 1) and cu_seqlens[G+1] (int32,
+ * device) receives those offsets (the varlen cu_seqlens_k of the attention).
+ * Out-of-range rows are skipped and set *error_flag.  No host sync. */
+int tw_gather_union(const void* src_k, const void* src_v, int64_t src_row_limit, int64_t entry_row0,
+                    int64_t entry_row_step, const int32_t* rows, int64_t rows_stride, const int32_t* row_counts,
+                    int G, int max_count, const void* cur_k, const void* cur_v, int D, int elem_bytes,
+                    int64_t dst_capacity, void* dst_k, void* dst_v, int32_t* cu_seqlens, int32_t* error_flag,
+                    void* stream);
+
+/* Per-query-head gather of the Quest paths: replaces the per-head CPU
+ * index_select + H2D + current-token write of update (quest_offload_cache.py:
+ * 576-637) and the layer-flat ragged pack (:816-936).  Head r of group g sees
+ * [0, sink_end) ++ sel_pages[g][r][0..k) (ascending) expanded to block_size
+ * rows ++ [recent_start, length) and then cur_k[g]/cur_v[g]; its row t goes
+ * to dst row g*dst_g_stride + r*dst_r_stride + t*dst_t_stride (pack [1, Tmax,
+ * R, D]: strides (.., 1, R); flat segments: ((R*(len+1)), len+1, 1)).  The
+ * window is that of tw_quest_select.  All rows must land below dst_capacity. */
+int tw_gather_heads(const void* src_k, const void* src_v, int64_t src_row_limit, int64_t entry_row0,
+                    int64_t entry_row_step, const int32_t* sel_pages, int G, int R, int k, int sink, int recent,
+                    int block_size, int length, const void* cur_k, const void* cur_v, int D, int elem_bytes,
+                    int64_t dst_g_stride, int64_t dst_r_stride, int64_t dst_t_stride, int64_t dst_capacity,
+                    void* dst_k, void* dst_v, int32_t* error_flag, void* stream);
 
 /* Device address of pinned host memory allocated by hipHostMalloc (torch
  * pin_memory=True); replaces cudaHostGetDevicePointer in

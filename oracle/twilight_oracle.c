@@ -305,20 +305,21 @@ float or_det_exp(float x) {
 /* a9: INT4 QK estimate of one query head (twilight_fused_qk.py:12-55,
  * twilight_offload_cache.py:1197-1261) in this build's defined order:
  *   k_d = f32(code_d) * f32(scale) + f32(min)            (dequantize, :40-47)
- *   acc_j = sum_{i<8} k_{8j+i} * q_{8j+i}, sequential from +0 (j = 0..D/8-1)
+ *   acc_j = sum_{i<8} k_{8j+i} * q_{8j+i}, sequential from +0 (j = 0..ceil(D/8)-1,
+ *   the one chunk of D < 8 channels is partial)
  *   dot = adjacent-pair tree over the acc_j
  *   logit = dot * qk_scale   (qk_scale = fp32(1/sqrt(D)))
- * rows[n] selects the packed row of candidate n.  D in {64, 128, 256}. */
+ * rows[n] selects the packed row of candidate n.  D = 4 .. 256, a power of two. */
 void or_int4_qk(const float* q, int D, const uint8_t* packed, const void* scale, const void* minimum, int dt,
                 const int64_t* rows, int N, float qk_scale, float* out) {
   float acc[64];
   for (int n = 0; n < N; ++n) {
     const int64_t t = rows[n];
     const float s = load_f(scale, t, dt), m = load_f(minimum, t, dt);
-    const int chunks = D / 8;
+    const int chunks = (D + 7) / 8; /* the last chunk is partial when D < 8 */
     for (int j = 0; j < chunks; ++j) {
       float a = 0.0f;
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 8 && 8 * j + i < D; ++i) {
         const int d = 8 * j + i;
         const uint32_t b = packed[t * (D / 2) + d / 2];
         const uint32_t code = (d & 1) ? (b >> 4) & 15u : b & 15u;
@@ -328,7 +329,7 @@ void or_int4_qk(const float* q, int D, const uint8_t* packed, const void* scale,
       acc[j] = a;
     }
     for (int w = 1; w < chunks; w <<= 1)
-      for (int j = 0; j < chunks; j += 2 * w) acc[j] = acc[j] + acc[j + w];
+      for (int j = 0; j + w < chunks; j += 2 * w) acc[j] = acc[j] + acc[j + w];
     out[n] = acc[0] * qk_scale;
   }
 }

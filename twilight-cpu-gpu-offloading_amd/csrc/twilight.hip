@@ -47,11 +47,61 @@ struct QkArgs {
   float* logits;              // [G][R][b0*bs]
 };
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+// One INT4 row shared by LPR lanes, CPL channels (CPL/2 code bytes) each:
+// CPL = min(D, 8), so D = 4 .. 256 (a power of two) maps to 1 .. 32 lanes.
+template <int DIM>
+struct Int4Row {
+  static constexpr int CPL = DIM < 8 ? DIM : 8;
+  static constexpr int LPR = DIM / CPL;
+  static constexpr int RPI = kWave / LPR;  // rows per wavefront instruction
+  static_assert(CPL >= 2 && LPR * CPL == DIM && (LPR & (LPR - 1)) == 0, "unsupported head dim");
+
+  __device__ static __forceinline__ uint32_t codes(const uint8_t* row, int c0) {
+    if constexpr (CPL == 8) return *reinterpret_cast<const uint32_t*>(row + c0 / 2);
+    else if constexpr (CPL == 4) return *reinterpret_cast<const uint16_t*>(row + c0 / 2);
+    else return row[c0 / 2];
+  }
+  __device__ static __forceinline__ void query(const float* qr, float (&q)[8]) {
+    if constexpr (CPL == 8) {
+      const float4 x = reinterpret_cast<const float4*>(qr)[0];
+      const float4 y = reinterpret_cast<const float4*>(qr)[1];
+      q[0] = x.x; q[1] = x.y; q[2] = x.z; q[3] = x.w;
+      q[4] = y.x; q[5] = y.y; q[6] = y.z; q[7] = y.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) q[j] = j < CPL ? qr[j] : 0.0f;
+    }
+  }
+  // Sequential sum of the lane's CPL products, then the adjacent-pair tree
+  // over the row's LPR lane sums (every lane of the row gets the result).
+  __device__ static __forceinline__ float dot(const float (&k)[8], const float (&q)[8]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) acc = acc + k[j] * q[j];
+    if constexpr (LPR >= 2) acc = acc + dpp_f32<kDppQuadXor1>(acc);
+    if constexpr (LPR >= 4) acc = acc + dpp_f32<kDppQuadXor2>(acc);
+    if constexpr (LPR >= 8) acc = acc + dpp_f32<kDppRowHalfMirror>(acc);
+    if constexpr (LPR >= 16) acc = acc + dpp_f32<kDppRowMirror>(acc);
+    if constexpr (LPR >= 32) acc = acc + __shfl_xor(acc, 16);
+    return acc;
+  }
+  __device__ static __forceinline__ void dequant(uint32_t w, float s, float m, float (&k)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) k[j] = j < CPL ? static_cast<float>((w >> (4 * j)) & 15u) * s + m : 0.0f;
+  }
+};
+
 template <typename DT, int DIM, int RMAX>
 __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
   using S = typename DT::storage;
-  constexpr int LPR = DIM / 8;        // lanes per row (8 channels = 4 code bytes each)
-  constexpr int RPI = kWave / LPR;    // rows per instruction
+  using Row = Int4Row<DIM>;
+  constexpr int LPR = Row::LPR;
+  constexpr int RPI = Row::RPI;
   const int chunks = static_cast<int>((a.plan_stride + kQkPagesPerBlock - 1) / kQkPagesPerBlock);
   const int g = blockIdx.x / chunks;
   const int chunk = blockIdx.x - g * chunks;
@@ -98,20 +148,14 @@ __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
       run += (s_mask[i] >> tid) & 1u;
     }
   }
-  // queries of the group: 8 channels per lane, RMAX heads
-  const int c0 = (lane % LPR) * 8;
+  // queries of the group: CPL channels per lane, RMAX heads
+  const int c0 = (lane % LPR) * Row::CPL;
   const int rig = lane / LPR;
   float qv[RMAX][8];
   {
     const float* qg = a.q + static_cast<int64_t>(g) * R * DIM;
 #pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-      const float* qr = qg + static_cast<int64_t>(r < R ? r : R - 1) * DIM + c0;
-      const float4 x = reinterpret_cast<const float4*>(qr)[0];
-      const float4 y = reinterpret_cast<const float4*>(qr)[1];
-      qv[r][0] = x.x; qv[r][1] = x.y; qv[r][2] = x.z; qv[r][3] = x.w;
-      qv[r][4] = y.x; qv[r][5] = y.y; qv[r][6] = y.z; qv[r][7] = y.w;
-    }
+    for (int r = 0; r < RMAX; ++r) Row::query(qg + static_cast<int64_t>(r < R ? r : R - 1) * DIM + c0, qv[r]);
   }
   __syncthreads();
   const int n_rows = np * a.bs;
@@ -128,39 +172,64 @@ __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
     int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[pi]) * a.bs + i;
     const bool in_range = t >= 0 && t < a.qrows;
     t = in_range ? t : 0;
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(pk + t * (DIM / 2) + c0 / 2);
-    const float s = to_f32(DT{}, sc[t]);
-    const float m = to_f32(DT{}, mn[t]);
+    const uint32_t w = Row::codes(pk + t * (DIM / 2), c0);
     float k[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t code = (w >> (4 * j)) & 15u;  // byte j/2: low nibble = even channel
-      k[j] = static_cast<float>(code) * s + m;
-    }
+    Row::dequant(w, to_f32(DT{}, sc[t]), to_f32(DT{}, mn[t]), k);
     const uint32_t pmask = s_mask[pi];
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc = acc + k[j] * qv[r][j];
-      // adjacent-pair tree over the LPR chunk sums of the row
-      acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
-                                                                        kDppQuadXor1, 0xf, 0xf, false));
-      acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
-                                                                        kDppQuadXor2, 0xf, 0xf, false));
-      if constexpr (LPR >= 8)
-        acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
-                                                                          kDppRowHalfMirror, 0xf, 0xf, false));
-      if constexpr (LPR >= 16)
-        acc = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
-                                                                          kDppRowMirror, 0xf, 0xf, false));
-      if constexpr (LPR >= 32) acc = acc + __shfl_xor(acc, 16);
+      const float acc = Row::dot(k, qv[r]);
       const int slot = s_slot[pi][r < 8 ? r : 7];
       if (ok && in_range && (lane % LPR) == 0 && r < R && ((pmask >> r) & 1u) && slot < a.b0) {
         const int64_t n = static_cast<int64_t>(slot) * a.bs + i;
         a.logits[(static_cast<int64_t>(g) * R + r) * N + n] = acc * a.qk_scale;
       }
     }
+  }
+}
+
+// INT4 QK at explicit candidate positions, one query head per block row
+// (the fused_affine_int4_qk call surface): positions[g][r][n] index entry g's
+// INT4 rows.  Same dequantization and reduction order as twilight_qk_kernel;
+// with materialize, the dequantized fp32 rows are written instead.
+template <typename DT, int DIM>
+__global__ __launch_bounds__(kBlock) void int4_qk_positions_kernel(QkArgs a, const int64_t* positions, int N,
+                                                                   float* out, bool materialize) {
+  using S = typename DT::storage;
+  using Row = Int4Row<DIM>;
+  constexpr int LPR = Row::LPR;
+  constexpr int RPI = Row::RPI;
+  constexpr int ROWS = 64;  // candidates per block
+  const int tiles = (N + ROWS - 1) / ROWS;
+  const int row = blockIdx.x / tiles;  // g*R + r
+  const int tile = blockIdx.x - row * tiles;
+  const int g = row / a.R;
+  const int lane = lane_id();
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int c0 = (lane % LPR) * Row::CPL;
+  float qv[8];
+  Row::query(a.q + static_cast<int64_t>(row) * DIM + c0, qv);
+  const uint8_t* pk = a.packed + static_cast<int64_t>(g) * a.qstride * (DIM / 2);
+  const S* sc = static_cast<const S*>(a.scale) + static_cast<int64_t>(g) * a.qstride;
+  const S* mn = static_cast<const S*>(a.minimum) + static_cast<int64_t>(g) * a.qstride;
+  for (int i0 = tile * ROWS + wave * RPI; i0 < (tile + 1) * ROWS; i0 += kWaves * RPI) {
+    const int n = i0 + lane / LPR;
+    const bool ok = n < N && n < (tile + 1) * ROWS;
+    int64_t t = positions[static_cast<int64_t>(row) * N + (n < N ? n : N - 1)];
+    const bool in_range = t >= 0 && t < a.qrows;
+    t = in_range ? t : 0;
+    float k[8];
+    Row::dequant(Row::codes(pk + t * (DIM / 2), c0), to_f32(DT{}, sc[t]), to_f32(DT{}, mn[t]), k);
+    if (materialize) {
+      if (ok) {
+        float* o = out + (static_cast<int64_t>(row) * N + n) * DIM + c0;
+#pragma unroll
+        for (int j = 0; j < Row::CPL; ++j) o[j] = in_range ? k[j] : 0.0f;
+      }
+      continue;
+    }
+    const float acc = Row::dot(k, qv);
+    if (ok && in_range && (lane % LPR) == 0) out[static_cast<int64_t>(row) * N + n] = acc * a.qk_scale;
   }
 }
 
@@ -677,11 +746,39 @@ int launch_qk_r(const QkArgs& a, hipStream_t stream) {
 template <typename DT>
 int launch_qk(const QkArgs& a, hipStream_t stream) {
   switch (a.D) {
+    case 4: return launch_qk_r<DT, 4>(a, stream);
+    case 8: return launch_qk_r<DT, 8>(a, stream);
+    case 16: return launch_qk_r<DT, 16>(a, stream);
+    case 32: return launch_qk_r<DT, 32>(a, stream);
     case 64: return launch_qk_r<DT, 64>(a, stream);
     case 128: return launch_qk_r<DT, 128>(a, stream);
     case 256: return launch_qk_r<DT, 256>(a, stream);
     default: return TW_EUNSUPPORTED;
   }
+}
+
+template <typename DT, int DIM>
+void launch_qk_positions_d(const QkArgs& a, const int64_t* positions, int N, float* out, bool materialize,
+                           hipStream_t stream) {
+  const dim3 grid(a.G * a.R * ((N + 63) / 64));
+  hipLaunchKernelGGL((int4_qk_positions_kernel<DT, DIM>), grid, dim3(kBlock), 0, stream, a, positions, N, out,
+                     materialize);
+}
+
+template <typename DT>
+int launch_qk_positions(const QkArgs& a, const int64_t* positions, int N, float* out, bool materialize,
+                        hipStream_t stream) {
+  switch (a.D) {
+    case 4: launch_qk_positions_d<DT, 4>(a, positions, N, out, materialize, stream); break;
+    case 8: launch_qk_positions_d<DT, 8>(a, positions, N, out, materialize, stream); break;
+    case 16: launch_qk_positions_d<DT, 16>(a, positions, N, out, materialize, stream); break;
+    case 32: launch_qk_positions_d<DT, 32>(a, positions, N, out, materialize, stream); break;
+    case 64: launch_qk_positions_d<DT, 64>(a, positions, N, out, materialize, stream); break;
+    case 128: launch_qk_positions_d<DT, 128>(a, positions, N, out, materialize, stream); break;
+    case 256: launch_qk_positions_d<DT, 256>(a, positions, N, out, materialize, stream); break;
+    default: return TW_EUNSUPPORTED;
+  }
+  return tw_host::check_launch();
 }
 
 template <int KPT>
@@ -726,7 +823,7 @@ extern "C" int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t
   if (G <= 0 || R <= 0 || R > 8 || b0_pages <= 0 || sink < 0 || block_size <= 0 || plan_stride < 1 ||
       quant_entry_stride <= 0 || quant_rows <= 0 || quant_rows > quant_entry_stride)
     return TW_EINVAL;
-  if (D != 64 && D != 128 && D != 256) return TW_EUNSUPPORTED;
+  if (D < 4 || D > 256 || (D & (D - 1)) != 0) return TW_EUNSUPPORTED;
   if ((reinterpret_cast<uintptr_t>(q) % 16) || (reinterpret_cast<uintptr_t>(packed) % 4)) return TW_EINVAL;
   tw::QkArgs a{q, packed, scale, minimum, quant_entry_stride, quant_rows, G, R, D, plan_pages, plan_masks, plan_counts,
                plan_stride, b0_pages, sink, block_size, qk_scale, logits};
@@ -739,6 +836,28 @@ extern "C" int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t
   }
 }
 
+extern "C" int tw_int4_qk_positions(const float* q, int G, int R, int D, const uint8_t* packed, const void* scale,
+                                    const void* minimum, int dtype, int64_t quant_entry_stride, int64_t quant_rows,
+                                    const int64_t* positions, int N, float qk_scale, int materialize, float* out,
+                                    void* stream) {
+  if (q == nullptr || packed == nullptr || scale == nullptr || minimum == nullptr || out == nullptr) return TW_EINVAL;
+  if (G <= 0 || R <= 0 || N < 0 || quant_entry_stride <= 0 || quant_rows <= 0 || quant_rows > quant_entry_stride)
+    return TW_EINVAL;
+  if (N == 0) return TW_OK;
+  if (positions == nullptr) return TW_EINVAL;
+  if (D < 4 || D > 256 || (D & (D - 1)) != 0) return TW_EUNSUPPORTED;
+  if ((reinterpret_cast<uintptr_t>(q) % 16) || (reinterpret_cast<uintptr_t>(packed) % 4)) return TW_EINVAL;
+  tw::QkArgs a{q, packed, scale, minimum, quant_entry_stride, quant_rows, G, R, D, nullptr, nullptr, nullptr, 0,
+               0, 0, 1, qk_scale, nullptr};
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TW_DTYPE_F16: return tw::launch_qk_positions<tw::F16>(a, positions, N, out, materialize != 0, s);
+    case TW_DTYPE_BF16: return tw::launch_qk_positions<tw::BF16>(a, positions, N, out, materialize != 0, s);
+    case TW_DTYPE_F32: return tw::launch_qk_positions<tw::F32>(a, positions, N, out, materialize != 0, s);
+    default: return TW_EINVAL;
+  }
+}
+
 extern "C" size_t tw_twilight_select_workspace_size(int G, int R, int N) {
   if (G <= 0 || R <= 0 || N <= 0) return 0;
   const size_t words = static_cast<size_t>((N + 31) / 32);
@@ -747,9 +866,9 @@ extern "C" size_t tw_twilight_select_workspace_size(int G, int R, int N) {
 
 extern "C" int tw_twilight_select(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,
                                   float top_p, int budget_mode, int target_total, int32_t* desired,
-                                  int32_t* allocated, int32_t* rows, int32_t* row_counts, int64_t rows_stride,
-                                  int sink, int recent, int block_size, int length, int append_position,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
+                                  int32_t* allocated, uint32_t* head_bits, int32_t* rows, int32_t* row_counts,
+                                  int64_t rows_stride, int sink, int recent, int block_size, int length,
+                                  int append_position, void* workspace, size_t workspace_bytes, void* stream) {
   if (logits == nullptr || sel_pages == nullptr || rows == nullptr || row_counts == nullptr) return TW_EINVAL;
   if (G <= 0 || R <= 0 || R > 8 || N <= 0 || b0_pages <= 0 || N != b0_pages * block_size) return TW_EINVAL;
   if (N > tw::sel::kMaxSelPages) return TW_EUNSUPPORTED;
@@ -772,10 +891,11 @@ extern "C" int tw_twilight_select(const float* logits, int G, int R, int N, cons
   s.sel_pages = sel_pages;
   s.b0 = b0_pages;
   s.counters = reinterpret_cast<unsigned int*>(ws);
-  s.selbits = reinterpret_cast<uint32_t*>(ws + tw::counter_bytes(G));
+  s.selbits = head_bits != nullptr ? head_bits : reinterpret_cast<uint32_t*>(ws + tw::counter_bytes(G));
   s.words_n = words;
   s.desired = desired != nullptr ? desired
-                                 : reinterpret_cast<int32_t*>(s.selbits + static_cast<int64_t>(G) * R * words);
+                                 : reinterpret_cast<int32_t*>(ws + tw::counter_bytes(G) +
+                                                              static_cast<size_t>(G) * R * words * 4);
   s.allocated = allocated;
   s.rows = rows;
   s.row_counts = row_counts;

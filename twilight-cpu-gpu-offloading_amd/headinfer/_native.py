@@ -52,10 +52,15 @@ _HIP_SIGNATURES = {
     "tw_decode_attention_pages": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32, i32, i32,
                                         i32, vp, vp, f32, vp, vp, szt, vp]),
     "tw_twilight_qk": (i32, [vp, i32, i32, i32, vp, vp, vp, i32, i64, i64, vp, vp, vp, i64, i32, i32, i32, f32, vp, vp]),
+    "tw_int4_qk_positions": (i32, [vp, i32, i32, i32, vp, vp, vp, i32, i64, i64, vp, i32, f32, i32, vp, vp]),
     "tw_twilight_select_workspace_size": (szt, [i32, i32, i32]),
-    "tw_twilight_select": (i32, [vp, i32, i32, i32, vp, i32, f32, i32, i32, vp, vp, vp, vp, i64, i32, i32, i32, i32,
-                                 i32, vp, szt, vp]),
+    "tw_twilight_select": (i32, [vp, i32, i32, i32, vp, i32, f32, i32, i32, vp, vp, vp, vp, vp, i64, i32, i32, i32,
+                                 i32, i32, vp, szt, vp]),
     "tw_gather_rows": (i32, [vp, vp, i64, vp, vp, i64, i32, i32, vp, vp, vp, vp]),
+    "tw_gather_union": (i32, [vp, vp, i64, i64, i64, vp, i64, vp, i32, i32, vp, vp, i32, i32, i64, vp, vp, vp, vp,
+                              vp]),
+    "tw_gather_heads": (i32, [vp, vp, i64, i64, i64, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i64,
+                              i64, i64, i64, vp, vp, vp, vp]),
     "tw_host_device_pointer": (i32, [vp, ctypes.POINTER(ctypes.c_void_p)]),
     "tw_append_kv": (i32, [vp, vp, i32, i32, i32, vp, vp, i64, i32, i64, vp]),
 }

@@ -336,6 +336,33 @@ def twilight_qk(
     return out
 
 
+def fused_affine_int4_qk(q: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, minimum: torch.Tensor,
+                         positions: torch.Tensor, *, materialize: bool = False) -> torch.Tensor:
+    """FP32 q . k~ (or the dequantized k~ itself with materialize=True) at the
+    candidate positions (twilight_fused_qk.py:34-55).  q [G,R,D] fp32, packed
+    [G,H,D/2] uint8, scale/minimum [G,H], positions [G,R,N] int64 in [0, H)."""
+    if q.ndim != 3 or q.dtype != torch.float32:
+        raise ValueError("expected an FP32 [G, R, D] query")
+    g, r, d = q.shape
+    h = packed.shape[1] if packed.ndim == 3 else -1
+    n = positions.shape[-1]
+    if packed.shape != (g, h, d // 2) or d not in (4, 8, 16, 32, 64, 128, 256):
+        raise ValueError("packed must be [G, H, D/2] with a power-of-two head_dim in [4, 256]")
+    if scale.shape != (g, h) or minimum.shape != (g, h) or positions.shape != (g, r, n):
+        raise ValueError("incompatible affine INT4 metadata/positions")
+    if packed.dtype != torch.uint8 or positions.dtype != torch.int64 or scale.dtype not in _KEY_DTYPES \
+            or minimum.dtype != scale.dtype:
+        raise ValueError("expected uint8 packed K, int64 positions and fp16/bf16/fp32 scale/minimum")
+    _require_contiguous(q, packed, scale, minimum, positions, what="fused_affine_int4_qk")
+    dev = _require_device(q, packed, scale, minimum, positions, what="fused_affine_int4_qk")
+    out = torch.empty((g, r, n, d) if materialize else (g, r, n), device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        check(hip().tw_int4_qk_positions(ptr(q), g, r, d, ptr(packed), ptr(scale), ptr(minimum), _dt(scale), h, h,
+                                         ptr(positions), n, 1.0, int(bool(materialize)), ptr(out),
+                                         stream_handle(dev)), "fused_affine_int4_qk")
+    return out
+
+
 def twilight_select(
     logits: torch.Tensor,
     sel_pages: torch.Tensor,
@@ -347,6 +374,7 @@ def twilight_select(
     row_counts: torch.Tensor,
     desired: Optional[torch.Tensor] = None,
     allocated: Optional[torch.Tensor] = None,
+    head_bits: Optional[torch.Tensor] = None,
     sink: int,
     recent: int,
     block_size: int,
@@ -357,7 +385,8 @@ def twilight_select(
     list of one layer.  logits [G,R,N] from twilight_qk; sel_pages [G,R,b0]
     the stage-1 pages; rows [G, >=length+1] int32 and row_counts [G] int32
     receive the union (ascending, then append_position if >= 0); desired /
-    allocated [G,R] int32 (optional) the counts."""
+    allocated [G,R] int32 (optional) the counts; head_bits [G,R,ceil(N/32)]
+    int32 (optional) each head's kept candidates as a bitmap."""
     if budget_mode not in ("dynamic", "matched"):
         raise ValueError("budget_mode must be 'dynamic' or 'matched'")
     if logits.dtype != torch.float32 or logits.ndim != 3 or not logits.is_contiguous():
@@ -376,13 +405,17 @@ def twilight_select(
     for t in (desired, allocated):
         if t is not None and (t.dtype != torch.int32 or tuple(t.shape) != (G, R) or not t.is_contiguous()):
             raise ValueError("desired/allocated must be contiguous [G, R] int32")
-    dev = _require_device(logits, sel_pages, rows, row_counts, desired, allocated, what="twilight_select")
+    if head_bits is not None and (head_bits.dtype != torch.int32 or tuple(head_bits.shape) != (G, R, (N + 31) // 32)
+                                  or not head_bits.is_contiguous()):
+        raise ValueError("head_bits must be contiguous [G, R, ceil(N/32)] int32")
+    dev = _require_device(logits, sel_pages, rows, row_counts, desired, allocated, head_bits,
+                          what="twilight_select")
     nbytes = hip().tw_twilight_select_workspace_size(G, R, N)
     ws = WORKSPACE.get(dev, "twilight_select", nbytes)
     with torch.cuda.device(dev):
         check(hip().tw_twilight_select(ptr(logits), G, R, N, ptr(sel_pages), b0, float(top_p),
                                        1 if budget_mode == "matched" else 0, int(target_total), ptr(desired),
-                                       ptr(allocated), ptr(rows), ptr(row_counts), rows.stride(0), sink, recent,
+                                       ptr(allocated), ptr(head_bits), ptr(rows), ptr(row_counts), rows.stride(0), sink, recent,
                                        block_size, length, append_position, ptr(ws), ws.numel(),
                                        stream_handle(dev)), "twilight_select")
 
@@ -498,8 +531,10 @@ def decode_attention_pages(
         raise ValueError("cur_k/cur_v must be [G, D] in q's dtype")
     if cur_k is not None and append_position >= k_cache.shape[1]:
         raise ValueError("append_position outside the cache")
-    dev = _require_device(q, k_cache, v_cache, plan_pages, plan_masks, plan_counts, cur_k, cur_v,
-                          what="decode_attention_pages")
+    dev = _require_device(q, plan_pages, plan_masks, plan_counts, cur_k, cur_v, what="decode_attention_pages")
+    if k_cache.is_cuda and k_cache.device != dev:
+        raise ValueError("decode_attention_pages requires tensors on one device")
+    kp, vp = _slab_source(k_cache, v_cache)
     _require_contiguous(q, cur_k, cur_v, what="decode_attention_pages")
     if out is None:
         out = torch.empty_like(q)
@@ -510,7 +545,7 @@ def decode_attention_pages(
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
     with torch.cuda.device(dev):
-        check(hip().tw_decode_attention_pages(ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D,
+        check(hip().tw_decode_attention_pages(ptr(q), kp, vp, _dt(q), G, R, D,
                                               ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
                                               plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink, recent,
                                               block_size, length, append_position, ptr(cur_k), ptr(cur_v), scale,
@@ -563,13 +598,23 @@ def decode_attention_varlen(
 
 
 # ------------------------------------------------------------ row movement
+_DEVICE_ALIAS: dict[int, int] = {}
+
+
 def host_device_pointer(t: torch.Tensor) -> int:
-    """Device address of a pinned host tensor's data (zero-copy access)."""
+    """Device address of a pinned host tensor's data (zero-copy access).  The
+    mapping is looked up for the start of the tensor's pinned allocation (its
+    storage) and offset to the view."""
     if t.is_cuda or not t.is_pinned():
         raise ValueError("zero-copy source must be pinned host memory")
-    out = _native.ctypes.c_void_p()
-    check(hip().tw_host_device_pointer(t.data_ptr(), _native.ctypes.byref(out)), "host_device_pointer")
-    return int(out.value)
+    base = t.untyped_storage().data_ptr()
+    dev = _DEVICE_ALIAS.get(base)
+    if dev is None:
+        out = _native.ctypes.c_void_p()
+        check(hip().tw_host_device_pointer(base, _native.ctypes.byref(out)), "host_device_pointer")
+        dev = int(out.value)
+        _DEVICE_ALIAS[base] = dev
+    return dev + (t.data_ptr() - base)
 
 
 def gather_rows(
@@ -607,6 +652,109 @@ def gather_rows(
         check(hip().tw_gather_rows(sk, sv, src_k.shape[0], ptr(src_rows), ptr(dst_rows), src_rows.numel(), D,
                                    src_k.element_size(), ptr(dst_k), ptr(dst_v), ptr(error_flag),
                                    stream_handle(dev)), "gather_rows")
+
+
+def _slab_source(src_k: torch.Tensor, src_v: torch.Tensor) -> tuple[int, int]:
+    """Device addresses of a K/V source: HBM tensors, or pinned host tensors
+    read zero-copy through their mapped device address."""
+    if src_k.is_cuda != src_v.is_cuda:
+        raise ValueError("K and V sources must live in the same memory")
+    if src_k.is_cuda:
+        return src_k.data_ptr(), src_v.data_ptr()
+    return host_device_pointer(src_k), host_device_pointer(src_v)
+
+
+def gather_union(
+    src_k: torch.Tensor,
+    src_v: torch.Tensor,
+    rows: torch.Tensor,
+    row_counts: torch.Tensor,
+    cur_k: torch.Tensor,
+    cur_v: torch.Tensor,
+    dst_k: torch.Tensor,
+    dst_v: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    *,
+    entry_row0: int,
+    entry_row_step: int,
+    max_count: int,
+    error_flag: Optional[torch.Tensor] = None,
+) -> None:
+    """Pack each group's union rows, then its decode token, back to back
+    (the varlen K/V of the GQA group path) and write cu_seqlens [G+1].
+
+    src_k/src_v: the slab planes [rows, D] (HBM or pinned host); group g's
+    source rows are entry_row0 + g*entry_row_step + rows[g, i]; rows [G,
+    stride] int32 and row_counts [G] int32 on the device; cur_k/cur_v [G, D];
+    dst_k/dst_v [capacity, D]."""
+    if src_k.ndim != 2 or src_k.shape != src_v.shape or src_k.dtype != src_v.dtype:
+        raise ValueError("src_k/src_v must be matching [rows, D]")
+    D = src_k.shape[1]
+    G = rows.shape[0]
+    if rows.dtype != torch.int32 or rows.ndim != 2 or rows.stride(1) != 1 or row_counts.shape != (G,) \
+            or row_counts.dtype != torch.int32:
+        raise ValueError("rows must be [G, stride] int32 with row_counts [G] int32")
+    if cur_k.shape != (G, D) or cur_v.shape != (G, D) or cur_k.dtype != src_k.dtype or cur_v.dtype != src_k.dtype:
+        raise ValueError("cur_k/cur_v must be [G, D] in the cache dtype")
+    if dst_k.ndim != 2 or dst_k.shape != dst_v.shape or dst_k.shape[1] != D or dst_k.dtype != src_k.dtype:
+        raise ValueError("dst_k/dst_v must be [capacity, D] in the cache dtype")
+    if cu_seqlens.dtype != torch.int32 or cu_seqlens.shape != (G + 1,):
+        raise ValueError("cu_seqlens must be [G + 1] int32")
+    _require_contiguous(src_k, src_v, cur_k, cur_v, dst_k, dst_v, row_counts, cu_seqlens, what="gather_union")
+    dev = _require_device(rows, row_counts, cur_k, cur_v, dst_k, dst_v, cu_seqlens, error_flag,
+                          what="gather_union")
+    sk, sv = _slab_source(src_k, src_v)
+    with torch.cuda.device(dev):
+        check(hip().tw_gather_union(sk, sv, src_k.shape[0], entry_row0, entry_row_step, ptr(rows), rows.stride(0),
+                                    ptr(row_counts), G, max_count, ptr(cur_k), ptr(cur_v), D, src_k.element_size(),
+                                    dst_k.shape[0], ptr(dst_k), ptr(dst_v), ptr(cu_seqlens), ptr(error_flag),
+                                    stream_handle(dev)), "gather_union")
+
+
+def gather_heads(
+    src_k: torch.Tensor,
+    src_v: torch.Tensor,
+    sel_pages: Optional[torch.Tensor],
+    cur_k: torch.Tensor,
+    cur_v: torch.Tensor,
+    dst_k: torch.Tensor,
+    dst_v: torch.Tensor,
+    *,
+    entry_row0: int,
+    entry_row_step: int,
+    sink: int,
+    recent: int,
+    block_size: int,
+    length: int,
+    num_heads: int,
+    dst_strides: tuple[int, int, int],
+    error_flag: Optional[torch.Tensor] = None,
+) -> None:
+    """Per-query-head rows sink ++ own pages ++ recent ++ decode token into
+    dst rows g*sg + r*sr + t*st (dst_k/dst_v [capacity, D]).  sel_pages
+    [G, R, k] int32 device (None or k = 0: no pages)."""
+    if src_k.ndim != 2 or src_k.shape != src_v.shape or src_k.dtype != src_v.dtype:
+        raise ValueError("src_k/src_v must be matching [rows, D]")
+    D = src_k.shape[1]
+    G = cur_k.shape[0]
+    R = num_heads
+    k = 0 if sel_pages is None else sel_pages.shape[2]
+    if sel_pages is not None and (sel_pages.dtype != torch.int32 or sel_pages.shape[:2] != (G, R)
+                                  or not sel_pages.is_contiguous()):
+        raise ValueError("sel_pages must be contiguous [G, R, k] int32")
+    if cur_k.shape != (G, D) or cur_v.shape != (G, D) or cur_k.dtype != src_k.dtype or cur_v.dtype != src_k.dtype:
+        raise ValueError("cur_k/cur_v must be [G, D] in the cache dtype")
+    if dst_k.ndim != 2 or dst_k.shape != dst_v.shape or dst_k.shape[1] != D or dst_k.dtype != src_k.dtype:
+        raise ValueError("dst_k/dst_v must be [capacity, D] in the cache dtype")
+    _require_contiguous(src_k, src_v, cur_k, cur_v, dst_k, dst_v, what="gather_heads")
+    dev = _require_device(sel_pages, cur_k, cur_v, dst_k, dst_v, error_flag, what="gather_heads")
+    sk, sv = _slab_source(src_k, src_v)
+    sg, sr, st = dst_strides
+    with torch.cuda.device(dev):
+        check(hip().tw_gather_heads(sk, sv, src_k.shape[0], entry_row0, entry_row_step, ptr(sel_pages), G, R, k,
+                                    sink, recent, block_size, length, ptr(cur_k), ptr(cur_v), D,
+                                    src_k.element_size(), sg, sr, st, dst_k.shape[0], ptr(dst_k), ptr(dst_v),
+                                    ptr(error_flag), stream_handle(dev)), "gather_heads")
 
 
 def append_kv(
