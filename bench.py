@@ -352,7 +352,7 @@ def main(argv=None) -> int:
         "union_pages_per_group": round(w.plan_counts.double().mean().item(), 1),
         "kernels": kern,
         "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom},
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom), "kernel": dom},
         "parity": parity,
     }
     if not args.no_cpu_baseline:
@@ -360,6 +360,28 @@ def main(argv=None) -> int:
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0 if parity["ok"] else 1
+
+
+# rocprofv3 FETCH_SIZE / WRITE_SIZE of each kernel, calibrated against a copy
+# of known size and recorded with the commands that produced them.
+TRAFFIC_PROFILE = ROOT / "profiles" / "pmc_traffic_quest32k.md"
+TRAFFIC_KERNEL = {"decode_attention": "decode_attn_kernel", "quest_select": "quest_score_kernel"}
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of the named kernel from the committed PMC
+    summary, or None when it is absent."""
+    try:
+        text = TRAFFIC_PROFILE.read_text()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        if line.startswith("traffic_json:"):
+            table = json.loads(line.split(":", 1)[1])
+            for name, entry in table.items():
+                if TRAFFIC_KERNEL.get(kernel, kernel) in name:
+                    return int(entry["traffic_bytes"])
+    return None
 
 
 if __name__ == "__main__":
