@@ -50,7 +50,7 @@ int tw_last_hip_error(void);
 int tw_version(void);
 
 /* ------------------------------------------------------------------------
- * a2 + a3: prompt metadata, one launch for n_entries KV heads.
+ * Prompt metadata, one launch for n_entries KV heads.
  * Replaces QuestTopKOffloadedCache._build_metadata
  * (quest_offload_cache.py:276-289: per-page amin/amax over rows
  * [sink + p*bs, sink + (p+1)*bs), complete pages only) and the Twilight
@@ -72,13 +72,13 @@ int tw_build_page_metadata(const void* keys, int64_t key_entry_stride, int n_ent
                            int64_t page_entry_stride, void* packed, void* scale, void* minimum,
                            int64_t quant_entry_stride, void* stream);
 
-/* a4: affine_int4_dequantize (twilight_offload_cache.py:40-47):
+/* affine_int4_dequantize (twilight_offload_cache.py:40-47):
  * out[n][d] = f32(code)*f32(scale[n]) + f32(minimum[n]) (mul, then add). */
 int tw_int4_dequantize(const void* packed, const void* scale, const void* minimum, int dtype,
                        int64_t N, int D, float* out, void* stream);
 
 /* ------------------------------------------------------------------------
- * a6: fused_quest_score (twilight_fused_quest.py:35-46 / _score :12-32).
+ * fused_quest_score (twilight_fused_quest.py:35-46 / _score :12-32).
  *   q [G][R][D] fp32; page_min/page_max: group g page p at
  *   + g*page_group_stride + p*D; out [G][R][P] fp32.
  * score = sum_d f32(q_d > 0 ? max_d : min_d) * q_d in the reference order:
@@ -90,7 +90,7 @@ int tw_quest_score(const float* q, const void* page_min, const void* page_max, i
                    int R, int P, int D, int64_t page_group_stride, float* out, void* stream);
 
 /* ------------------------------------------------------------------------
- * a5: torch.topk(scores, k, sorted=False).indices.sort()
+ * torch.topk(scores, k, sorted=False).indices.sort()
  * (quest_offload_cache.py:373-374, twilight_offload_cache.py:1153).
  * scores [rows][P] fp32 (row stride score_row_stride) -> out [rows][k] int64
  * ascending page ids.  Ties go to the lowest index, NaN ranks highest, -0
@@ -164,7 +164,7 @@ int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t* packed, c
  * rows of entry g's INT4 keys (layout as in tw_twilight_qk; rows outside
  * [0, quant_rows) give no output).  materialize = 0: out [G][R][N] =
  * qk_scale * (q . k~) in tw_twilight_qk's order (qk_scale 1 reproduces the
- * raw dot); materialize != 0: out [G][R][N][D] = k~ (16-byte aligned).
+ * raw dot); materialize != 0: out [G][R][N][D] = k~.
  * D = 4 .. 256, a power of two. */
 int tw_int4_qk_positions(const float* q, int G, int R, int D, const uint8_t* packed, const void* scale,
                          const void* minimum, int dtype, int64_t quant_entry_stride, int64_t quant_rows,
@@ -205,7 +205,7 @@ int tw_twilight_select(const float* logits, int G, int R, int N, const int32_t* 
                        size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
- * a22: sparse GQA decode attention, split-K over selected rows, one query
+ * Sparse GQA decode attention, split-K over selected rows, one query
  * token per group.  Replaces _flash_attention_varlen_forward
  * (mp.py:21-52) on the decode paths that call it (GQA group branch
  * mp.py:239-279, layer-flat branch :283-321, per-head reference :424-452).
@@ -253,7 +253,7 @@ int tw_decode_attention(const void* q, const void* k_base, const void* v_base, i
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
- * a14-a16 / a18: head-wise K/V row gather into the attention layout.
+ * Head-wise K/V row gather into the attention layout.
  * Replaces the CPU index_select + H2D of update / update_layer_flat_ragged /
  * update_layer_gqa_group_ragged (quest_offload_cache.py:576-624,816-936;
  * twilight_offload_cache.py:2973-3101) and the mapped-host assembly kernel
@@ -306,7 +306,7 @@ int tw_gather_heads(const void* src_k, const void* src_v, int64_t src_row_limit,
 int tw_host_device_pointer(void* host_ptr, void** device_ptr);
 
 /* ------------------------------------------------------------------------
- * a20/a21: per-step append of the decode token.  Replaces _schedule_d2h
+ * Per-step append of the decode token.  Replaces _schedule_d2h
  * (quest_offload_cache.py:230-274) and the token-batched new-KV D2H
  * (twilight_offload_cache.py:551-794).  For each of n_entries entries,
  * row `position` of entry (first_entry + i) in dst_k/dst_v ([E][Lmax][D],

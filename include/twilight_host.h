@@ -14,7 +14,7 @@ extern "C" {
 
 enum tw_host_status { TW_HOST_OK = 0, TW_HOST_ERANGE = 1, TW_HOST_EINVAL = 2 };
 
-/* a19: row gather into (pinned) staging.
+/* Row gather into (pinned) staging.
  * Replaces gather_kv of cpu_kv_gather.cpp:3-16 and cpu_kv_run_gather.cpp:
  * 4-32 (bound by CpuKVGather / CpuKVRunGather, cpu_kv_gather.py:9-36,
  * cpu_kv_run_gather.py:8-17).  out_k[i] = k[rows[i]], out_v[i] = v[rows[i]],
@@ -24,7 +24,7 @@ enum tw_host_status { TW_HOST_OK = 0, TW_HOST_ERANGE = 1, TW_HOST_EINVAL = 2 };
 int tw_host_gather_kv(const void* k, const void* v, void* out_k, void* out_v, const int64_t* rows, int64_t n,
                       int64_t source_rows, int64_t row_bytes, int threads);
 
-/* a12 (CPU variant): sorted union of n_lists int64 position lists, all in
+/* CPU token union: sorted union of n_lists int64 position lists, all in
  * [0, length).  Replaces CpuTokenUnion.__call__ (cpu_token_union.py:13-23).
  * scratch: length bytes; out: room for length positions.  Returns the union
  * size, -1 on bad arguments, -2 if a position is outside [0, length). */

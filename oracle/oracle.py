@@ -261,7 +261,7 @@ def det_exp(x: float) -> float:
 
 def int4_qk(q: np.ndarray, packed: np.ndarray, scale: np.ndarray, minimum: np.ndarray, dtype: str,
             rows: np.ndarray, qk_scale: float) -> np.ndarray:
-    """INT4 QK estimate of one query head q [D] over candidate rows (a9)."""
+    """INT4 QK estimate of one query head q [D] over candidate rows."""
     q = np.ascontiguousarray(q, np.float32)
     packed = np.ascontiguousarray(packed, np.uint8)
     rows = np.ascontiguousarray(rows, np.int64)
@@ -273,7 +273,7 @@ def int4_qk(q: np.ndarray, packed: np.ndarray, scale: np.ndarray, minimum: np.nd
 
 
 def top_p_count(logits: np.ndarray, top_p: float) -> tuple[int, int]:
-    """(desired, Z) of the exact top-p count (a10)."""
+    """(desired, Z) of the exact top-p count."""
     lg = np.ascontiguousarray(logits, np.float32)
     z = ctypes.c_uint64()
     d = lib().or_top_p_count(_ptr(lg), lg.shape[0], float(np.float32(top_p)), ctypes.byref(z))

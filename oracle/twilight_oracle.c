@@ -124,7 +124,7 @@ static void minmax_bits(const void* base, int64_t start, int64_t stride, int64_t
   *mx = bmx;
 }
 
-/* ------------------------------------------------- a2 + a3: metadata */
+/* ------------------------------------------------------------ metadata */
 /* Page min/max (quest_offload_cache.py:276-289): pages = (T - sink) // bs
  * complete pages of rows [sink + p*bs, sink + (p+1)*bs).  INT4
  * (twilight_offload_cache.py:25-37) for every row.  Either output group may
@@ -173,7 +173,7 @@ int or_build_page_metadata(const void* keys, int T, int D, int dt, int sink, int
   return 0;
 }
 
-/* a4: affine_int4_dequantize (twilight_offload_cache.py:40-47). */
+/* affine_int4_dequantize (twilight_offload_cache.py:40-47). */
 void or_int4_dequantize(const uint8_t* packed, const void* scale, const void* minimum, int dt, int64_t N, int D,
                         float* out) {
   for (int64_t n = 0; n < N; ++n) {
@@ -187,7 +187,7 @@ void or_int4_dequantize(const uint8_t* packed, const void* scale, const void* mi
   }
 }
 
-/* ------------------------------------------------ a6: Quest page score */
+/* ------------------------------------------------ Quest page score */
 /* twilight_fused_quest.py:12-32: 32 lanes, lane l accumulates channels
  * l, l+32, l+64, l+96 (chunk order) starting from 0; then shuffle-adds at
  * offsets 1, 2, 4, 8, 16 and lane 0's value is the score.  Lane 0's value
@@ -222,7 +222,7 @@ void or_quest_score(const float* q, const void* page_min, const void* page_max, 
                                D, dt);
 }
 
-/* ------------------------------------------------ a5: top-k, sorted */
+/* ------------------------------------------------ top-k, sorted */
 /* torch.topk(sorted=False).indices.sort() (quest_offload_cache.py:373-374)
  * with ties to the lowest index, NaN ranked highest and -0 == +0. */
 static uint32_t score_key(float s) {
@@ -253,7 +253,7 @@ void or_topk_sorted(const float* scores, int rows, int P, int64_t stride, int k,
   free(tmp);
 }
 
-/* --------------------------------------- a7 + a12: GQA row plan */
+/* --------------------------------------------------- GQA row plan */
 /* Per group: [0, sink_end) ++ every page selected by any of the R heads
  * (ascending, each expanded to sink + p*bs + [0, bs), quest_offload_cache.py:
  * 484-490) ++ [recent_start, length) ++ append_position (if >= 0).  Window
@@ -302,7 +302,7 @@ float or_det_exp(float x) {
   return ldexpf(p, (int)n);
 }
 
-/* a9: INT4 QK estimate of one query head (twilight_fused_qk.py:12-55,
+/* INT4 QK estimate of one query head (twilight_fused_qk.py:12-55,
  * twilight_offload_cache.py:1197-1261) in this build's defined order:
  *   k_d = f32(code_d) * f32(scale) + f32(min)            (dequantize, :40-47)
  *   acc_j = sum_{i<8} k_{8j+i} * q_{8j+i}, sequential from +0 (j = 0..ceil(D/8)-1,
@@ -334,7 +334,7 @@ void or_int4_qk(const float* q, int D, const uint8_t* packed, const void* scale,
   }
 }
 
-/* a10: top-p count (twilight_exact_top_p_graph.py:19-32; inline
+/* Top-p count (twilight_exact_top_p_graph.py:19-32; inline
  * twilight_offload_cache.py:1274-1310) in this build's exact definition:
  *   e_i = det_exp(l_i - max l), mass E_i = floor(e_i * 2^40) (int64),
  *   Z = sum E_i, T = ceil(P24 * Z / 2^24) with P24 = round(top_p * 2^24),

@@ -25,6 +25,8 @@
 // The R query heads of the group share every K/V load.
 #pragma clang fp contract(off)
 
+#include <type_traits>
+
 #include "tw_common.h"
 
 namespace tw {
@@ -511,6 +513,342 @@ __global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(
   block_partial<DT, RMAX>(a, g, chunk, D, n_chunks == 1, s_m, s_l, s_o);
 }
 
+// ------------------------------------------------------------------ MFMA
+// 16-bit K/V: q.k on the matrix cores, p.v with packed dot2.
+//
+// q.k is a [16 heads x D] x [D x 16 rows] product per tile of 16 rows: four
+// (D/32) v_mfma_f32_16x16x32 steps, A = the group's queries (lane = head +
+// 16 * quarter), B = K^T (lane = row + 16 * quarter), each lane loading D/2
+// contiguous bytes of its row.  Quarter q, step s, element e is channel
+// q*D/4 + 8s + e in both operands.  The product lands as S[4*(lane/16)+v]
+// [lane%16] in register v, so lanes 0..15 hold heads 0..3 of the 16 rows
+// (16..31 heads 4..7).  Heads beyond R are zero rows of A.  The R <= 8 heads
+// of a GQA group pad the 16-row A operand; the padding costs matrix-core
+// cycles the kernel has to spare, and it takes the dot products, conversions
+// and cross-lane reductions of q.k off the vector ALU, which bounded the
+// all-VALU form.
+//
+// p.v stays on the vector ALU: V rows are read with 8 channels per lane
+// (D/8 lanes per row), p goes through LDS as the input dtype, and pairs of
+// rows are combined with v_dot2_f32_{f16,bf16} (p_a v_a + p_b v_b into an
+// fp32 accumulator), rounding p to the input dtype as flash-attention does.
+template <int D>
+struct MfmaGeom {
+  static constexpr int STEPS = D / 32;   // MFMA k-steps over the head dim
+  static constexpr int QC = D / 4;       // channels per quarter
+  static constexpr int LPR = D / 8;      // V lanes per row
+  static constexpr int RG = kWave / LPR; // V row groups
+  static constexpr int VR = 16 / RG;     // V rows per lane per 16-row tile
+};
+
+constexpr int mfma_tiles(int D, int rmax) {
+  return (D == 64 ? 4 : (D == 128 ? 2 : 1)) / ((rmax >= 8 && D != 256) ? 2 : 1);
+}
+
+template <typename DT>
+struct Half8;
+template <>
+struct Half8<F16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float dot2(uint32_t p, uint32_t v, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, p), __builtin_bit_cast(v2, v), acc, false);
+  }
+  static __device__ __forceinline__ void mfma(const uint4& a, const uint4& b, float (&c)[4]) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 acc = {c[0], c[1], c[2], c[3]};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), acc, 0, 0, 0);
+    c[0] = acc[0]; c[1] = acc[1]; c[2] = acc[2]; c[3] = acc[3];
+  }
+};
+template <>
+struct Half8<BF16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float dot2(uint32_t p, uint32_t v, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, p), __builtin_bit_cast(v2, v), acc, false);
+  }
+  static __device__ __forceinline__ void mfma(const uint4& a, const uint4& b, float (&c)[4]) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 acc = {c[0], c[1], c[2], c[3]};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8, a), __builtin_bit_cast(v8, b), acc, 0, 0, 0);
+    c[0] = acc[0]; c[1] = acc[1]; c[2] = acc[2]; c[3] = acc[3];
+  }
+};
+
+// Source row of list index i of a group: position, visible heads, and
+// whether it is a cache row, the decode token, or neither.
+struct RowRef {
+  int pos;
+  uint32_t hm;
+  bool in_list;
+  bool cur;
+};
+
+template <int MODE>
+__device__ __forceinline__ RowRef row_ref(const AttnArgs& a, const GroupRows& gr, int i, int64_t list_base,
+                                          int last_list, const uint8_t* mask_src, uint32_t mask_force,
+                                          bool bs_pow2, int bs_shift) {
+  RowRef r;
+  if (MODE == kModeRows) {
+    const int64_t at = list_base + (i < last_list ? i : last_list);
+    r.pos = a.rows[at];
+    r.hm = static_cast<uint32_t>(mask_src[at]) | mask_force;
+  } else if (MODE == kModePages) {
+    const int j = i - gr.sink_end;
+    int u = bs_pow2 ? (j >> bs_shift) : j / a.bs;
+    u = u < 0 ? 0 : (u > last_list ? last_list : u);
+    const int64_t at = list_base + u;
+    const int page = a.plan_pages[at];
+    const uint32_t pm = static_cast<uint32_t>(mask_src[at]) | mask_force;
+    const bool in_pages = i >= gr.sink_end && i < gr.page_end;
+    r.pos = i < gr.sink_end ? i
+            : in_pages      ? a.sink + page * a.bs + (j - u * a.bs)
+            : i < gr.recent_end ? gr.recent_start + (i - gr.page_end)
+                                : a.append_position;
+    r.hm = in_pages ? pm : 0xffu;
+  } else {
+    r.pos = gr.win_start + i;
+    r.hm = 0xffu;
+  }
+  r.in_list = i < gr.n_list && (MODE == kModeVarlen || (r.pos >= 0 && r.pos < a.entry_stride));
+  r.cur = i == gr.n_list && i < gr.n_rows;
+  if (r.cur) r.hm = 0xffu;
+  return r;
+}
+
+template <typename DT, int D, int RMAX, int MODE>
+__global__ __launch_bounds__(kBlock, 2) void decode_attn_mfma(AttnArgs a) {
+  using S = typename DT::storage;
+  using G = MfmaGeom<D>;
+  using H = Half8<DT>;
+  constexpr int TILES = mfma_tiles(D, RMAX);
+  constexpr int RW = 16 * TILES;             // rows per wavefront batch
+  constexpr int RB = kWaves * RW;            // rows per block batch
+  constexpr int HG = (RMAX + 3) / 4;         // 16-lane head groups of the q.k product
+  static_assert(RMAX <= 8, "at most 8 heads per group");
+
+  const int R = a.R;
+  const int g = blockIdx.x / a.max_chunks;
+  const int chunk = blockIdx.x - g * a.max_chunks;
+  const int wave = static_cast<int>(threadIdx.x) / kWave;
+  const int lane = lane_id();
+  const int krow = lane & 15;                // q.k: row of the tile / head of A
+  const int quarter = lane >> 4;
+  const int c0v = (lane % G::LPR) * 8;       // p.v: channels
+  const int rg = lane / G::LPR;              // p.v: row group
+
+  __shared__ float s_m[kWaves * RMAX];
+  __shared__ float s_l[kWaves * RMAX];
+  __shared__ __align__(16) S s_p[kWaves][RMAX][RW];   // p of the batch, per head
+  extern __shared__ __align__(16) float s_dyn[];
+
+  const GroupRows gr = group_rows<MODE>(a, g, D);
+  const int rows_per_block = RB * a.iters;
+  const int n_chunks = (gr.n_rows + rows_per_block - 1) / rows_per_block;
+  if (gr.n_rows == 0) {
+    if (chunk == 0) {
+      S* o = static_cast<S*>(a.out) + static_cast<int64_t>(g) * R * D;
+      for (int i = threadIdx.x; i < R * D; i += kBlock) o[i] = from_f32(DT{}, 0.0f);
+    }
+    return;
+  }
+  if (chunk >= n_chunks) return;
+  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D);
+
+  const S* kbase = static_cast<const S*>(a.k);
+  const S* vbase = static_cast<const S*>(a.v);
+  const S* ck = a.cur_k != nullptr ? static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D : nullptr;
+  const S* cv = a.cur_v != nullptr ? static_cast<const S*>(a.cur_v) + static_cast<int64_t>(g) * D : nullptr;
+
+  // ---- A operand: the group's queries, zero rows for heads >= R ----
+  uint4 qf[G::STEPS];
+  {
+    const S* qh = static_cast<const S*>(a.q) + (static_cast<int64_t>(g) * R + (krow < R ? krow : 0)) * D;
+#pragma unroll
+    for (int s = 0; s < G::STEPS; ++s) {
+      const uint4 t = *reinterpret_cast<const uint4*>(qh + quarter * G::QC + 8 * s);
+      qf[s] = krow < R ? t : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+
+  float m_run[RMAX];      // wave-uniform running max per head (log2 units)
+  float l_part[4];        // this lane's partial sum of p for heads 4*quarter + v
+  float o_acc[RMAX][8];   // p.v accumulators, channels c0v.., rows of group rg
+#pragma unroll
+  for (int h = 0; h < RMAX; ++h) {
+    m_run[h] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o_acc[h][i] = 0.0f;
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) l_part[v] = 0.0f;
+
+  const int32_t* idx_src = MODE == kModePages ? a.plan_pages : a.rows;
+  const uint8_t* mask_in = MODE == kModePages ? a.plan_masks : a.masks;
+  const uint8_t* mask_src = mask_in != nullptr ? mask_in : reinterpret_cast<const uint8_t*>(idx_src);
+  const uint32_t mask_force = mask_in != nullptr ? 0u : 0xffu;
+  const int64_t list_base = static_cast<int64_t>(g) * (MODE == kModePages ? a.plan_stride : a.rows_stride);
+  const int last_list = MODE == kModePages ? (gr.n_pages > 0 ? gr.n_pages - 1 : 0)
+                                           : (gr.n_list > 0 ? gr.n_list - 1 : 0);
+  const bool bs_pow2 = (a.bs & (a.bs - 1)) == 0;
+  const int bs_shift = bs_pow2 && a.bs > 0 ? __ffs(a.bs) - 1 : 0;
+  const S* safe_k = gr.n_list > 0 ? kbase + gr.base : (ck != nullptr ? ck : kbase);
+  const S* safe_v = gr.n_list > 0 ? vbase + gr.base : (cv != nullptr ? cv : vbase);
+  const S* cur_k = ck != nullptr ? ck : safe_k;
+  const S* cur_v = cv != nullptr ? cv : safe_v;
+
+  for (int it = 0; it < a.iters; ++it) {
+    const int row0 = chunk * rows_per_block + it * RB + wave * RW;
+    if (row0 >= gr.n_rows) break;
+    // ---- round trip 1: row indices (K rows and V rows of this lane) ----
+    RowRef kr[TILES], vr[TILES][G::VR];
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      kr[t] = row_ref<MODE>(a, gr, row0 + 16 * t + krow, list_base, last_list, mask_src, mask_force, bs_pow2,
+                            bs_shift);
+#pragma unroll
+      for (int j = 0; j < G::VR; ++j)
+        vr[t][j] = row_ref<MODE>(a, gr, row0 + 16 * t + rg * G::VR + j, list_base, last_list, mask_src,
+                                 mask_force, bs_pow2, bs_shift);
+    }
+    // ---- round trip 2: K fragments and V rows ----
+    uint4 kf[TILES][G::STEPS];
+    uint4 vf[TILES][G::VR];
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const S* kp = kr[t].cur ? cur_k
+                    : (kr[t].in_list ? kbase + gr.base + static_cast<int64_t>(kr[t].pos) * gr.stride : safe_k);
+#pragma unroll
+      for (int s = 0; s < G::STEPS; ++s)
+        kf[t][s] = *reinterpret_cast<const uint4*>(kp + quarter * G::QC + 8 * s);
+#pragma unroll
+      for (int j = 0; j < G::VR; ++j) {
+        const S* vp = vr[t][j].cur ? cur_v
+                      : (vr[t][j].in_list ? vbase + gr.base + static_cast<int64_t>(vr[t][j].pos) * gr.stride
+                                          : safe_v);
+        vf[t][j] = *reinterpret_cast<const uint4*>(vp + c0v);
+      }
+    }
+    // ---- q.k on the matrix cores ----
+    float sc[TILES][4];
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < G::STEPS; ++s) H::mfma(qf[s], kf[t][s], acc);
+      const bool ok = kr[t].in_list || kr[t].cur;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int h = 4 * quarter + v;
+        const bool vis = ok && h < R && ((kr[t].hm >> h) & 1u);
+        sc[t][v] = vis ? acc[v] * a.scale_log2 : -INFINITY;
+      }
+    }
+    // ---- batch max per head: over the tiles, then the 16 lanes of a row ----
+    float mx[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float x = sc[0][v];
+#pragma unroll
+      for (int t = 1; t < TILES; ++t) x = fmaxf(x, sc[t][v]);
+      x = fmaxf(x, dpp<kQuadXor1>(x));
+      x = fmaxf(x, dpp<kQuadXor2>(x));
+      x = fmaxf(x, dpp<kRowHalfMirror>(x));
+      x = fmaxf(x, dpp<kRowMirror>(x));
+      mx[v] = x;
+    }
+    float alpha[RMAX];
+#pragma unroll
+    for (int h = 0; h < RMAX; ++h) {
+      const float tile_max = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx[h & 3]), 16 * (h >> 2)));
+      const float mnew = fmaxf(m_run[h], tile_max);
+      alpha[h] = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run[h] - mnew);
+      m_run[h] = mnew;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o_acc[h][i] *= alpha[h];
+    }
+    // ---- p = exp2(s - m) in the input dtype through LDS ----
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int h = 4 * quarter + v;
+      // this lane's head for register v: 4*quarter + v (quarters >= HG are idle)
+      const float al = HG > 1 && quarter == 1 ? alpha[(4 + v) % RMAX] : alpha[v % RMAX];
+      const float m_lane = HG > 1 && quarter == 1 ? m_run[(4 + v) % RMAX] : m_run[v % RMAX];
+      float psum = 0.0f;
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        const float pv = exp2_rel(sc[t][v], m_lane);
+        psum += pv;
+        if (quarter < HG && h < RMAX) s_p[wave][h][16 * t + krow] = from_f32(DT{}, pv);
+      }
+      l_part[v] = l_part[v] * al + psum;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's p stores are done
+    __builtin_amdgcn_wave_barrier();
+    // ---- p.v: pairs of rows with v_dot2 ----
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+#pragma unroll
+      for (int j = 0; j < G::VR; j += 2) {
+        const uint32_t va[4] = {vf[t][j].x, vf[t][j].y, vf[t][j].z, vf[t][j].w};
+        const uint32_t vb[4] = {vf[t][j + 1].x, vf[t][j + 1].y, vf[t][j + 1].z, vf[t][j + 1].w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo[i] = __builtin_amdgcn_perm(vb[i], va[i], 0x05040100u);  // (a.ch 2i, b.ch 2i)
+          hi[i] = __builtin_amdgcn_perm(vb[i], va[i], 0x07060302u);  // (a.ch 2i+1, b.ch 2i+1)
+        }
+#pragma unroll
+        for (int h = 0; h < RMAX; ++h) {
+          const uint32_t pp = *reinterpret_cast<const uint32_t*>(&s_p[wave][h][16 * t + rg * G::VR + j]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            o_acc[h][2 * i] = H::dot2(pp, lo[i], o_acc[h][2 * i]);
+            o_acc[h][2 * i + 1] = H::dot2(pp, hi[i], o_acc[h][2 * i + 1]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // ---- the wavefront's (m, l, o): sum o over the row groups, l over rows ----
+#pragma unroll
+  for (int h = 0; h < RMAX; ++h) {
+#pragma unroll
+    for (int o = G::LPR; o < kWave; o <<= 1) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o_acc[h][i] += __shfl_xor(o_acc[h][i], o);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    float x = l_part[v];
+    x += dpp<kQuadXor1>(x);
+    x += dpp<kQuadXor2>(x);
+    x += dpp<kRowHalfMirror>(x);
+    x += dpp<kRowMirror>(x);
+    l_part[v] = x;
+  }
+  float* s_o = s_dyn;
+#pragma unroll
+  for (int h = 0; h < RMAX; ++h) {
+    const float lh = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_part[h & 3]), 16 * (h >> 2)));
+    if (lane == 0) {
+      s_m[wave * RMAX + h] = m_run[h];
+      s_l[wave * RMAX + h] = lh;
+    }
+    if (lane < G::LPR) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s_o[(wave * RMAX + h) * D + c0v + i] = o_acc[h][i];
+    }
+  }
+  __syncthreads();
+  block_partial<DT, RMAX>(a, g, chunk, D, n_chunks == 1, s_m, s_l, s_o);
+}
+
 // Generic head dimension (any even D <= 512): one row per wavefront step,
 // lane owns channels lane + 64 j.  Correctness path for unusual shapes.
 template <typename DT, int RMAX, int MODE>
@@ -641,8 +979,12 @@ bool fast_d(int D) { return D == 64 || D == 128 || D == 256; }
 int rmax_for(int R) { return R <= 1 ? 1 : (R <= 2 ? 2 : (R <= 4 ? 4 : 8)); }
 
 // Rows of one block batch.
+// The matrix-core kernel serves 16-bit K/V at D in {64, 128, 256}, R <= 8.
+bool use_mfma(int dtype, int D, int R) { return dtype != TW_DTYPE_F32 && fast_d(D) && R <= 8; }
+
 int rows_per_batch(int dtype, int D, int R) {
   if (!fast_d(D)) return kWaves * 16;
+  if (use_mfma(dtype, D, R)) return kWaves * 16 * mfma_tiles(D, rmax_for(R) < 4 ? 4 : rmax_for(R));
   const int lpr = D / 8;
   const int rpi = kWave / lpr;
   return kWaves * steps_for(dtype == TW_DTYPE_F32 ? 4 : 2, rmax_for(R)) * rpi;
@@ -667,9 +1009,17 @@ size_t dyn_lds_bytes(int R, int D) { return static_cast<size_t>(kWaves) * rmax_f
 
 template <typename DT, int D, int RMAX, int MODE>
 int launch_one(const AttnArgs& a, hipStream_t stream) {
-  const size_t lds = dyn_lds_bytes(a.R, a.D);
+  size_t lds = dyn_lds_bytes(a.R, a.D);
   const dim3 grid(a.G * a.max_chunks);
-  if constexpr (D > 0) {
+  if constexpr (D > 0 && !std::is_same<DT, F32>::value) {
+    constexpr int RM = RMAX < 4 ? 4 : RMAX;
+    lds = static_cast<size_t>(kWaves) * RM * D * sizeof(float);
+    auto kern = decode_attn_mfma<DT, D, RM, MODE>;
+    if (lds > 64 * 1024)
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(lds));
+    hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, stream, a);
+  } else if constexpr (D > 0) {
     auto kern = decode_attn_kernel<DT, D, RMAX, MODE>;
     if (lds > 64 * 1024)
       (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -85,7 +85,7 @@ def build_page_metadata(
     scale: Optional[torch.Tensor] = None,
     minimum: Optional[torch.Tensor] = None,
 ) -> None:
-    """Prompt metadata of n entries in one launch (a2 + a3).
+    """Prompt metadata of n entries in one launch (page min/max and INT4 keys).
 
     keys: [E, T, D] (or [T, D]); page_min/page_max: [E, >=P, D];
     packed: [E, >=T, D/2] uint8; scale/minimum: [E, >=T].  Any of the two
