@@ -273,6 +273,85 @@ __global__ __launch_bounds__(512) void merge_kernel(AttnArgs a, int rows_per_blo
   }
 }
 
+// Split-K combine for D in {64, 128, 256}: one block per (group, head), thread
+// t = (chunk lane t / (D/4), channel quad t % (D/4)).  Every chunk lane loads
+// its chunks' (m, l) and 16-byte o slices in one batch (at most 32 loads per
+// thread for D <= 128, one memory round trip), the block finds the max m,
+// weights its chunks by exp2(m_c - M) and the chunk lanes are summed in LDS.
+template <typename DT, int MODE, int D>
+__global__ __launch_bounds__(kBlock) void merge_vec_kernel(AttnArgs a, int rows_per_block) {
+  using S = typename DT::storage;
+  constexpr int NQ = D / 4;                        // channel quads
+  constexpr int NL = kBlock / NQ;                  // chunk lanes
+  constexpr int MAXJ = (kMaxChunks + NL - 1) / NL; // chunks per lane
+  const int R = a.R;
+  const int g = blockIdx.x / R;
+  const int r = blockIdx.x - g * R;
+  const GroupRows gr = group_rows<MODE>(a, g, D);
+  const int n_chunks = (gr.n_rows + rows_per_block - 1) / rows_per_block;
+  if (n_chunks <= 1) return;
+  const int t = threadIdx.x;
+  const int q = t % NQ;
+  const int cl = t / NQ;
+  const int wave = t / kWave;
+  __shared__ float s_red[kWaves];
+  __shared__ float4 s_o[NL][NQ];
+  __shared__ float s_l[NL];
+  const int64_t base = static_cast<int64_t>(g) * a.max_chunks;
+  float4 ov[MAXJ];
+  float mv[MAXJ], lv[MAXJ];
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const int c = cl + NL * j;
+    const int64_t pc = base + (c < n_chunks ? c : n_chunks - 1);
+    ov[j] = *reinterpret_cast<const float4*>(a.part_o + (pc * R + r) * D + 4 * q);
+    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (pc * R + r) * 2);
+    mv[j] = c < n_chunks ? ml.x : -INFINITY;
+    lv[j] = ml.y;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) m = fmaxf(m, mv[j]);
+  m = wave_max_f32(m);
+  if (lane_id() == 0) s_red[wave] = m;
+  __syncthreads();
+  float M = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_red[w]);
+  float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float l = 0.0f;
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const float w = exp2_rel(mv[j], M);
+    o.x += w * ov[j].x;
+    o.y += w * ov[j].y;
+    o.z += w * ov[j].z;
+    o.w += w * ov[j].w;
+    l += w * lv[j];
+  }
+  s_o[cl][q] = o;
+  if (q == 0) s_l[cl] = l;
+  __syncthreads();
+  if (cl == 0) {
+    float4 O = s_o[0][q];
+    float L = s_l[0];
+#pragma unroll
+    for (int k = 1; k < NL; ++k) {
+      O.x += s_o[k][q].x;
+      O.y += s_o[k][q].y;
+      O.z += s_o[k][q].z;
+      O.w += s_o[k][q].w;
+      L += s_l[k];
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    S* out = static_cast<S*>(a.out) + (static_cast<int64_t>(g) * R + r) * D + 4 * q;
+    out[0] = from_f32(DT{}, L > 0.0f ? O.x * inv : 0.0f);
+    out[1] = from_f32(DT{}, L > 0.0f ? O.y * inv : 0.0f);
+    out[2] = from_f32(DT{}, L > 0.0f ? O.z * inv : 0.0f);
+    out[3] = from_f32(DT{}, L > 0.0f ? O.w * inv : 0.0f);
+  }
+}
+
 // Block partial from the wavefront partials in LDS: either the final output
 // (single-chunk groups) or a partial for the merge.
 template <typename DT, int RMAX>
@@ -1038,6 +1117,10 @@ int launch_one(const AttnArgs& a, hipStream_t stream) {
   int threads = ((a.D + kWave - 1) / kWave) * kWave;
   threads = threads < a.max_chunks ? ((a.max_chunks + kWave - 1) / kWave) * kWave : threads;
   const int rpb = rows_per_batch(DT::code, a.D, a.R) * a.iters;
+  if constexpr (D == 64 || D == 128 || D == 256) {
+    hipLaunchKernelGGL((merge_vec_kernel<DT, MODE, D>), dim3(a.G * a.R), dim3(kBlock), 0, stream, a, rpb);
+    return tw_host::check_launch();
+  }
   if (a.max_chunks <= 64) {
     hipLaunchKernelGGL((merge_kernel<DT, MODE, 64>), dim3(a.G * a.R), dim3(threads), 0, stream, a, rpb);
   } else {
