@@ -48,7 +48,12 @@ def parse_args(argv=None):
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--workload", choices=("quest32k", "twilight32k", "offload64k"), default="quest32k",
+                    help="quest32k (default): 32K layer, KV in HBM; twilight32k: INT4 QK + top-p at 32K; "
+                         "offload64k: 64K layer with KV in pinned host memory (zero-copy vs DMA)")
+    ap.add_argument("--context", type=int, default=None, help="context length (workload default if omitted)")
+    ap.add_argument("--budget-mode", choices=("dynamic", "matched"), default="dynamic",
+                    help="Twilight budgets (twilight32k)")
     ap.add_argument("--budget-pages", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget (s)")
@@ -157,6 +162,198 @@ class QuestWorkload:
         # append of the decode token (read + write)
         attention = (rows - G) * 2 * D * e + 2 * G * R * D * e + 4 * G * D * e
         return {"select": select, "attention": attention, "rows_per_group": rows / G}
+
+
+class TwilightWorkload:
+    """Seeded synthetic inputs of the 32K Twilight layer: bf16 K/V in HBM,
+    per-token INT4 keys, Quest B0 = 4096 tokens (256 pages), top-p 0.95 with
+    dynamic budgets, page relevance Zipf(1.1) over permuted ranks added as
+    4 * w_p * u_g to the page's keys (u_g the normalised mean query)."""
+
+    G, R, D = 8, 4, 128
+    SINK, RECENT, BS = 64, 256, 16
+    B0_TOKENS, TOP_P, ALPHA, ZIPF = 4096, 0.95, 4.0, 1.1
+
+    def __init__(self, dev, layers: int, context: int, budget_mode: str = "dynamic", seed: int = 2):
+        import torch
+
+        from headinfer import kernels
+
+        self.dev, self.layers, self.L, self.mode = dev, layers, context, budget_mode
+        G, R, D, L = self.G, self.R, self.D, context
+        bf = torch.bfloat16
+        self.Lmax = L + 1
+        self.P_meta = (L - self.SINK) // self.BS
+        sink_end = min(self.SINK, L)
+        recent_start = max(sink_end, L - (self.RECENT - 1))
+        self.P = min((recent_start - sink_end) // self.BS, self.P_meta)
+        self.b0 = min(self.P, self.B0_TOKENS // self.BS)
+        self.N = self.b0 * self.BS
+        self.fixed = min(self.P, max(1, math.ceil(0.05 * (recent_start - sink_end) / self.BS)))
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        self.q = torch.randn((layers, G, R, D), generator=gen, device=dev).to(bf)
+        self.qf = self.q.float()
+        self.kc = torch.empty((layers, G, self.Lmax, D), dtype=bf, device=dev)
+        self.vc = torch.empty_like(self.kc)
+        self.cur_k = torch.randn((layers, G, D), generator=gen, device=dev).to(bf)
+        self.cur_v = torch.randn((layers, G, D), generator=gen, device=dev).to(bf)
+        self.pmin = torch.empty((layers, G, self.P_meta, D), dtype=bf, device=dev)
+        self.pmax = torch.empty_like(self.pmin)
+        self.packed = torch.empty((layers, G, self.Lmax, D // 2), dtype=torch.uint8, device=dev)
+        self.scale = torch.empty((layers, G, self.Lmax), dtype=bf, device=dev)
+        self.minimum = torch.empty_like(self.scale)
+        ranks = torch.arange(1, self.P + 1, device=dev, dtype=torch.float32)
+        for layer in range(layers):
+            k = torch.randn((G, self.Lmax, D), generator=gen, device=dev)
+            u = self.qf[layer].mean(dim=1)
+            u = u / u.norm(dim=-1, keepdim=True)
+            for g in range(G):
+                w = ranks[torch.randperm(self.P, generator=gen, device=dev)] ** (-self.ZIPF)
+                rows = self.SINK + torch.arange(self.P * self.BS, device=dev)
+                k[g, rows] += self.ALPHA * w.repeat_interleave(self.BS).unsqueeze(1) * u[g]
+            self.kc[layer].copy_(k.to(bf))
+            self.vc[layer].copy_(torch.randn((G, self.Lmax, D), generator=gen, device=dev).to(bf))
+            kernels.build_page_metadata(self.kc[layer, :, :L], sink=self.SINK, block_size=self.BS,
+                                        page_min=self.pmin[layer], page_max=self.pmax[layer],
+                                        packed=self.packed[layer], scale=self.scale[layer],
+                                        minimum=self.minimum[layer])
+        i32 = torch.int32
+        self.width = min(self.P, R * self.b0)
+        self.sel = torch.zeros((layers, G, R, self.b0), dtype=i32, device=dev)
+        self.plan_pages = torch.zeros((layers, G, self.width), dtype=i32, device=dev)
+        self.plan_masks = torch.zeros((layers, G, self.width), dtype=torch.uint8, device=dev)
+        self.plan_counts = torch.zeros((layers, G), dtype=i32, device=dev)
+        self.logits = torch.empty((layers, G, R, self.N), dtype=torch.float32, device=dev)
+        self.rows = torch.zeros((layers, G, self.Lmax), dtype=i32, device=dev)
+        self.row_counts = torch.zeros((layers, G), dtype=i32, device=dev)
+        self.desired = torch.zeros((layers, G, R), dtype=i32, device=dev)
+        self.max_rows = min(L, sink_end + R * self.N + (L - recent_start))
+        self.out = torch.empty_like(self.q)
+        torch.cuda.synchronize(dev)
+
+    def select(self, layer: int) -> None:
+        from headinfer import kernels
+
+        kernels.quest_select(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P], self.b0,
+                             sel_pages=self.sel[layer], plan_pages=self.plan_pages[layer],
+                             plan_masks=self.plan_masks[layer], plan_counts=self.plan_counts[layer])
+        kernels.twilight_qk(self.qf[layer], self.packed[layer], self.scale[layer], self.minimum[layer],
+                            self.plan_pages[layer], self.plan_masks[layer], self.plan_counts[layer], self.b0,
+                            sink=self.SINK, block_size=self.BS, out=self.logits[layer])
+        kernels.twilight_select(self.logits[layer], self.sel[layer], top_p=self.TOP_P, budget_mode=self.mode,
+                                target_total=self.fixed * self.BS * self.R, rows=self.rows[layer],
+                                row_counts=self.row_counts[layer], desired=self.desired[layer], sink=self.SINK,
+                                recent=self.RECENT, block_size=self.BS, length=self.L)
+
+    def attend(self, layer: int) -> None:
+        from headinfer import kernels
+
+        kernels.decode_attention_rows(self.q[layer], self.kc[layer], self.vc[layer], self.rows[layer],
+                                      self.row_counts[layer], self.max_rows, cur_k=self.cur_k[layer],
+                                      cur_v=self.cur_v[layer], out=self.out[layer])
+        kernels.append_kv(self.cur_k[layer], self.cur_v[layer], self.kc[layer], self.vc[layer], first_entry=0,
+                          position=self.L)
+
+    def step(self) -> None:
+        for layer in range(self.layers):
+            self.select(layer)
+            self.attend(layer)
+
+    def bytes_per_layer(self) -> dict:
+        G, R, D, P, N = self.G, self.R, self.D, self.P, self.N
+        e = 2
+        cand_rows = self.plan_counts.double().sum().item() * self.BS / self.layers   # union of the B0 candidates
+        rows = self.row_counts.double().sum().item() / self.layers                  # attended union rows
+        select = (2 * P * D * e * G + G * R * P * 4 * 2 + G * R * self.b0 * 4 + cand_rows * (D // 2 + 2 * e)
+                  + G * R * N * 4 * 2 + G * R * D * 4)
+        attention = rows * 2 * D * e + 2 * G * R * D * e + 4 * G * D * e
+        return {"select": select, "attention": attention, "rows_per_group": rows / G,
+                "candidate_rows_per_group": cand_rows / G}
+
+
+class OffloadWorkload(QuestWorkload):
+    """The 64K layer with every KV head in pinned host memory (page metadata
+    in HBM): Quest selection on the GPU, then the sparse attention reading the
+    selected pages either zero-copy over the host link (mapped pinned memory)
+    or after a host gather into pinned staging and one DMA copy."""
+
+    def __init__(self, dev, layers: int, context: int, budget_pages: int, seed: int = 3):
+        import torch
+
+        super().__init__(dev, layers, context, budget_pages, seed=seed)
+        hk = torch.empty(self.kc.shape, dtype=self.kc.dtype, pin_memory=True)
+        hv = torch.empty(self.vc.shape, dtype=self.vc.dtype, pin_memory=True)
+        hk.copy_(self.kc)
+        hv.copy_(self.vc)
+        self.hk, self.hv = hk, hv
+        del self.kc, self.vc
+        torch.cuda.empty_cache()
+        G, D = self.G, self.D
+        self.stage_k = torch.empty((G, self.max_rows, D), dtype=hk.dtype, pin_memory=True)
+        self.stage_v = torch.empty_like(self.stage_k)
+        self.dev_k = torch.empty((G, self.max_rows, D), dtype=hk.dtype, device=dev)
+        self.dev_v = torch.empty_like(self.dev_k)
+        self.rows_h = torch.zeros((G, self.max_rows), dtype=torch.int32, pin_memory=True)
+        self.rmask_h = torch.zeros((G, self.max_rows), dtype=torch.uint8, pin_memory=True)
+        self.counts_h = torch.zeros((G,), dtype=torch.int32, pin_memory=True)
+        self.rows_d = torch.zeros((G, self.max_rows), dtype=torch.int32, device=dev)
+        self.rmask_d = torch.zeros((G, self.max_rows), dtype=torch.uint8, device=dev)
+        self.counts_d = torch.zeros((G,), dtype=torch.int32, device=dev)
+
+    def attend(self, layer: int) -> None:
+        from headinfer import kernels
+
+        kernels.decode_attention_pages(self.q[layer], self.hk[layer], self.hv[layer], self.plan_pages[layer],
+                                       self.plan_counts[layer], plan_masks=self.plan_masks[layer],
+                                       max_pages=self.max_pages, sink=self.SINK, recent=self.RECENT,
+                                       block_size=self.BS, length=self.L, append_position=self.L,
+                                       cur_k=self.cur_k[layer], cur_v=self.cur_v[layer], out=self.out[layer])
+
+    def attend_dma(self, layer: int) -> int:
+        """The reference's host path: page ids to the host, CPU gather of each
+        group's union rows into pinned staging, one H2D copy per group and
+        plane, attention over the staged rows.  Returns the rows moved."""
+        import torch
+
+        from headinfer import kernels
+
+        counts = self.plan_counts[layer].cpu()
+        pages = self.plan_pages[layer].cpu()
+        masks = self.plan_masks[layer].cpu()
+        G, R, BS, L = self.G, self.R, self.BS, self.L
+        sink_end = min(self.SINK, L)
+        recent_start = max(sink_end, L - (self.RECENT - 1))
+        all_heads = (1 << R) - 1
+        moved = 0
+        for g in range(G):
+            nu = int(counts[g])
+            pg = pages[g, :nu].long()
+            pos = torch.cat([torch.arange(sink_end), (self.SINK + pg[:, None] * BS + torch.arange(BS)).reshape(-1),
+                             torch.arange(recent_start, L)])
+            n = pos.numel()
+            kernels.host_gather_kv(self.hk[layer, g], self.hv[layer, g], pos, self.stage_k[g, :n], self.stage_v[g, :n])
+            self.dev_k[g, :n].copy_(self.stage_k[g, :n], non_blocking=True)
+            self.dev_v[g, :n].copy_(self.stage_v[g, :n], non_blocking=True)
+            self.rows_h[g, :n] = torch.arange(n, dtype=torch.int32)
+            self.rmask_h[g, :n] = torch.cat([torch.full((sink_end,), all_heads),
+                                             masks[g, :nu].long().repeat_interleave(BS),
+                                             torch.full((L - recent_start,), all_heads)]).to(torch.uint8)
+            self.counts_h[g] = n
+            moved += n
+        self.rows_d.copy_(self.rows_h, non_blocking=True)
+        self.rmask_d.copy_(self.rmask_h, non_blocking=True)
+        self.counts_d.copy_(self.counts_h, non_blocking=True)
+        kernels.decode_attention_rows(self.q[layer], self.dev_k, self.dev_v, self.rows_d, self.counts_d,
+                                      self.max_rows, row_masks=self.rmask_d, cur_k=self.cur_k[layer],
+                                      cur_v=self.cur_v[layer], out=self.out[layer])
+        kernels.append_kv(self.cur_k[layer], self.cur_v[layer], self.hk[layer], self.hv[layer], first_entry=0,
+                          position=self.L)
+        return moved
+
+    def host_bytes_per_layer(self) -> float:
+        fixed = min(self.SINK, self.L) + (self.RECENT - 1)
+        rows = self.plan_counts.double().sum().item() * self.BS / self.layers + self.G * fixed
+        return rows * 2 * self.D * 2 + self.G * 2 * self.D * 2  # selected K/V rows read + decode token written
 
 
 def graph_of(fn, warm: int = 2):
@@ -278,6 +475,11 @@ def main(argv=None) -> int:
 
     _native.hip()  # fail loudly if the kernel library is missing
 
+    if args.workload == "twilight32k":
+        return run_twilight(args, dev)
+    if args.workload == "offload64k":
+        return run_offload(args, dev)
+    args.context = args.context or 32768
     print(f"[bench] building inputs: layers={args.layers} context={args.context}", file=sys.stderr, flush=True)
     w = QuestWorkload(dev, args.layers, args.context, args.budget_pages)
 
@@ -360,6 +562,203 @@ def main(argv=None) -> int:
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0 if parity["ok"] else 1
+
+
+def _timed_steps(step_graph, steps: int, warmup: int) -> tuple[float, float]:
+    """(wall seconds per replay, event seconds per replay) over `steps`."""
+    import torch
+
+    for _ in range(warmup):
+        step_graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step_graph.replay()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / max(1, steps)
+    return wall, time_graph(step_graph, steps)
+
+
+def _attention_check(q, keys, vals, rows, masks, cur_k, cur_v, out) -> float:
+    """Max abs error of out [R, D] against a float64 recomputation over the
+    given rows plus the decode token (None masks: every head sees every row)."""
+    import torch
+
+    R, D = q.shape
+    kk = torch.cat([keys[rows], cur_k[None]]).double()
+    vv = torch.cat([vals[rows], cur_v[None]]).double()
+    s = (kk @ q.double().T) / math.sqrt(D)
+    if masks is not None:
+        m = torch.cat([masks.long(), torch.tensor([(1 << R) - 1], device=masks.device)])
+        vis = ((m.unsqueeze(1) >> torch.arange(R, device=m.device)) & 1).bool()
+        s = s.masked_fill(~vis, float("-inf"))
+    ref = torch.softmax(s, dim=0).T @ vv
+    err = (out.double() - ref).abs()
+    ok = bool((err <= 2e-3 + 1e-2 * ref.abs()).all().item())
+    return float(err.max()) if ok else float("inf")
+
+
+def run_twilight(args, dev) -> int:
+    """Twilight at 32K: one decode step of 32 layers x (Quest B0 + INT4 QK +
+    top-p + GQA union, then sparse attention over the union and the append)."""
+    import torch
+
+    ctx = args.context or 32768
+    print(f"[bench] twilight inputs: layers={args.layers} context={ctx}", file=sys.stderr, flush=True)
+    w = TwilightWorkload(dev, args.layers, ctx, args.budget_mode)
+    w.step()
+    torch.cuda.synchronize()
+    # structure + attention of layer 0: union ascending, sink and recent present, within bounds
+    ok = True
+    err = 0.0
+    sink_end = min(w.SINK, w.L)
+    recent_start = max(sink_end, w.L - (w.RECENT - 1))
+    for g in range(w.G):
+        n = int(w.row_counts[0, g])
+        rows = w.rows[0, g, :n].long()
+        ok &= bool((rows[1:] > rows[:-1]).all()) and int(rows[0]) == 0 and int(rows[-1]) == w.L - 1
+        ok &= n >= sink_end + (w.L - recent_start) and bool((w.desired[0, g] >= 1).all())
+        e = _attention_check(w.q[0, g], w.kc[0, g, : w.L], w.vc[0, g, : w.L], rows, None, w.cur_k[0, g],
+                             w.cur_v[0, g], w.out[0, g])
+        ok &= e != float("inf")
+        err = max(err, e)
+    g_step = graph_of(w.step)
+    g_sel = graph_of(lambda: [w.select(i) for i in range(w.layers)])
+    g_att = graph_of(lambda: [w.attend(i) for i in range(w.layers)])
+    wall, _ = _timed_steps(g_step, args.steps, args.warmup)
+    reps = max(20, args.steps // 2)
+    t_sel = time_graph(g_sel, reps) / w.layers
+    t_att = time_graph(g_att, reps) / w.layers
+    by = w.bytes_per_layer()
+    layer_s = wall / w.layers
+    value = (by["select"] + by["attention"]) / layer_s / 1e9
+    kern = {"twilight_select": {"us": round(t_sel * 1e6, 2), "bytes": int(by["select"]),
+                                "GBps": round(by["select"] / t_sel / 1e9, 1)},
+            "decode_attention": {"us": round(t_att * 1e6, 2), "bytes": int(by["attention"]),
+                                 "GBps": round(by["attention"] / t_att / 1e9, 1)}}
+    dom = "decode_attention" if t_att >= t_sel else "twilight_select"
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "twilight-32k-hbm: Llama-3-8B-shaped layer x 32, Quest B0 4096 tokens, INT4 QK, "
+                               f"top-p {w.TOP_P} ({w.mode} budgets), union attention, KV in HBM",
+                   "layers": w.layers, "context": w.L, "kv_heads": w.G, "q_per_kv": w.R, "head_dim": w.D,
+                   "page_size": w.BS, "b0_pages": w.b0, "top_p": w.TOP_P, "budget_mode": w.mode},
+        "layer_us": round(layer_s * 1e6, 3),
+        "rows_per_group": round(by["rows_per_group"], 1),
+        "candidate_rows_per_group": round(by["candidate_rows_per_group"], 1),
+        "kernels": kern,
+        "roofline": {"bound": "hbm", "achieved": kern[dom]["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(kern[dom]["GBps"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom},
+        "parity": {"ok": ok, "attention_max_abs_err": err},
+    }
+    if not args.no_cpu_baseline:
+        from oracle.cpu_baseline import twilight_layer_step
+
+        threads = min(16, len(os.sched_getaffinity(0)))
+        torch.set_num_threads(threads)
+        L = w.L
+        cpu = [t.cpu() for t in (w.q[0], w.kc[0, :, :L], w.vc[0, :, :L], w.pmin[0, :, : w.P], w.pmax[0, :, : w.P],
+                                 w.packed[0], w.scale[0], w.minimum[0], w.cur_k[0], w.cur_v[0])]
+
+        def run():
+            twilight_layer_step(*cpu, length=L, b0_pages=w.b0, top_p=w.TOP_P, sink=w.SINK, recent=w.RECENT,
+                                block_size=w.BS)
+
+        run()
+        times = []
+        t0 = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t0 < args.cpu_seconds and len(times) < 100):
+            t1 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t1)
+        times.sort()
+        result["cpu_baseline"] = {"value": round(times[len(times) // 2] * 1e6, 1), "unit": "us/layer",
+                                  "cores": threads, "kind": "port",
+                                  "sample": f"median of {len(times)} single-layer steps (layer 0, 8 KV heads, torch "
+                                            "CPU: score, topk, INT4 dequant + matmul, argsort/softmax/cumsum top-p, "
+                                            "union, index_select, SDPA)"}
+    print(json.dumps(result), flush=True)
+    return 0 if ok else 1
+
+
+def run_offload(args, dev) -> int:
+    """64K layer with the KV in pinned host memory: the attention reads the
+    selected pages zero-copy over the host link; the reference's host-gather +
+    DMA path is timed beside it."""
+    import torch
+
+    ctx = args.context or 65536
+    print(f"[bench] offload inputs: layers={args.layers} context={ctx}", file=sys.stderr, flush=True)
+    w = OffloadWorkload(dev, args.layers, ctx, args.budget_pages)
+    w.step()
+    torch.cuda.synchronize()
+    ok = True
+    err = 0.0
+    sink_end = min(w.SINK, w.L)
+    recent_start = max(sink_end, w.L - (w.RECENT - 1))
+    for g in range(w.G):
+        nu = int(w.plan_counts[0, g])
+        pages = w.plan_pages[0, g, :nu].long().cpu()
+        pm = w.plan_masks[0, g, :nu].cpu()
+        rows = torch.cat([torch.arange(sink_end), (w.SINK + pages[:, None] * w.BS + torch.arange(w.BS)).reshape(-1),
+                          torch.arange(recent_start, w.L)])
+        masks = torch.cat([torch.full((sink_end,), (1 << w.R) - 1), pm.long().repeat_interleave(w.BS),
+                           torch.full((w.L - recent_start,), (1 << w.R) - 1)])
+        e = _attention_check(w.q[0, g].cpu(), w.hk[0, g], w.hv[0, g], rows, masks, w.cur_k[0, g].cpu(),
+                             w.cur_v[0, g].cpu(), w.out[0, g].cpu())
+        ok &= e != float("inf")
+        err = max(err, e)
+    g_step = graph_of(w.step)
+    steps = max(5, args.steps // 10)
+    wall, _ = _timed_steps(g_step, steps, min(args.warmup, 5))
+    layer_s = wall / w.layers
+    host_bytes = w.host_bytes_per_layer()
+    by = w.bytes_per_layer()
+    # the reference's host path for comparison: eager, a host sync per layer
+    w.step()
+    torch.cuda.synchronize()
+    dma_layers = min(w.layers, 8)
+    t0 = time.perf_counter()
+    for layer in range(dma_layers):
+        w.select(layer)
+        w.attend_dma(layer)
+    torch.cuda.synchronize()
+    dma_layer_s = (time.perf_counter() - t0) / dma_layers
+    # pinned host -> device copy rate of this box (the host link's practical peak)
+    big = torch.empty(1 << 30, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst.copy_(big, non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        dst.copy_(big, non_blocking=True)
+    e1.record()
+    torch.cuda.synchronize()
+    h2d_gbs = 3 * (1 << 30) / (e0.elapsed_time(e1) / 1e3) / 1e9
+    del big, dst
+    link = host_bytes / layer_s / 1e9
+    result = {
+        "metric": METRIC, "value": round((by["select"] + host_bytes) / layer_s / 1e9, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": steps, "warmup": min(args.warmup, 5), "ms_per_step": round(wall * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "offload-64k-host: Llama-3-8B-shaped layer x 32, KV in pinned host memory, page "
+                               "metadata in HBM, Quest selection, attention reading the selected pages zero-copy",
+                   "layers": w.layers, "context": w.L, "kv_heads": w.G, "q_per_kv": w.R, "head_dim": w.D,
+                   "page_size": w.BS, "budget_pages": w.k},
+        "layer_us": round(layer_s * 1e6, 3),
+        "host_link": {"bytes_per_layer": int(host_bytes), "zero_copy_GBps": round(link, 2),
+                      "pinned_h2d_copy_GBps": round(h2d_gbs, 2), "pcie_gen5_x16_GBps": 64.0,
+                      "frac_of_pcie": round(link / 64.0, 4), "frac_of_measured_copy": round(link / h2d_gbs, 4),
+                      "dma_path_layer_us": round(dma_layer_s * 1e6, 1),
+                      "dma_path_GBps": round(host_bytes / dma_layer_s / 1e9, 2)},
+        "rows_per_group": round(host_bytes / (2 * w.D * 2) / w.G, 1),
+        "parity": {"ok": ok, "attention_max_abs_err": err},
+    }
+    print(json.dumps(result), flush=True)
+    return 0 if ok else 1
 
 
 # rocprofv3 FETCH_SIZE / WRITE_SIZE of each kernel, calibrated against a copy

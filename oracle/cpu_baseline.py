@@ -55,3 +55,50 @@ def quest_layer_step(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
                                                vals.view(1, 1, -1, D).float(), is_causal=False, scale=scale)
             out[g, r] = o.view(D).to(q.dtype)
     return out, chosen.view(G, R, budget)
+
+
+def twilight_layer_step(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_min: torch.Tensor,
+                        page_max: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, minimum: torch.Tensor,
+                        cur_k: torch.Tensor, cur_v: torch.Tensor, *, length: int, b0_pages: int, top_p: float,
+                        sink: int, recent: int, block_size: int) -> torch.Tensor:
+    """One layer of the Twilight dynamic path on host tensors, in the
+    reference's op order (twilight_offload_cache.py:1128-1614): Quest B0 pages,
+    candidate expansion, INT4 dequantize + fp32 matmul / sqrt(D), argsort +
+    softmax + cumsum + searchsorted top-p, the per-group token union, then
+    index_select and SDPA over the union plus the decode token.
+
+    q [G,R,D]; k_cache/v_cache [G,>=L,D]; page metadata [G,P,D]; packed
+    [G,T,D/2] u8, scale/minimum [G,T]; cur_k/cur_v [G,D].  Returns [G,R,D]."""
+    G, R, D = q.shape
+    sink_end = min(sink, length)
+    recent_start = max(sink_end, length - max(0, recent - 1))
+    qf = q.float()
+    extrema = torch.where(qf.reshape(G * R, 1, D) > 0, page_max.repeat_interleave(R, 0),
+                          page_min.repeat_interleave(R, 0))
+    scores = (extrema.float() * qf.reshape(G * R, 1, D)).sum(dim=-1)
+    pages = torch.topk(scores, k=b0_pages, dim=-1, sorted=False).indices.view(G, R, b0_pages)
+    offsets = torch.arange(block_size)
+    cand = (sink + pages.unsqueeze(-1) * block_size + offsets).reshape(G, R, -1)   # [G,R,N]
+    out = torch.empty_like(q)
+    scale_qk = 1.0 / math.sqrt(D)
+    for g in range(G):
+        low = (packed[g] & 0x0F)
+        high = (packed[g] >> 4) & 0x0F
+        selected = [torch.arange(sink_end), torch.arange(recent_start, length)]
+        for r in range(R):
+            pos = cand[g, r]
+            codes = torch.stack((low[pos], high[pos]), dim=-1).flatten(-2).float()
+            k_hat = codes * scale[g, pos].float().unsqueeze(-1) + minimum[g, pos].float().unsqueeze(-1)
+            logits = (k_hat @ qf[g, r]) * scale_qk
+            order = torch.argsort(logits, descending=True)
+            cum = torch.cumsum(torch.softmax(logits[order], dim=0), dim=0)
+            desired = min(int(torch.searchsorted(cum, torch.tensor(top_p), right=False)) + 1, pos.numel())
+            selected.append(pos[order[:desired]])
+        union = torch.unique(torch.cat(selected), sorted=True)
+        keys = torch.cat((k_cache[g].index_select(0, union), cur_k[g:g + 1])).float()
+        vals = torch.cat((v_cache[g].index_select(0, union), cur_v[g:g + 1])).float()
+        o = F.scaled_dot_product_attention(qf[g].view(1, R, 1, D), keys.view(1, 1, -1, D).expand(1, R, -1, D),
+                                           vals.view(1, 1, -1, D).expand(1, R, -1, D), is_causal=False,
+                                           scale=scale_qk)
+        out[g] = o.view(R, D).to(q.dtype)
+    return out

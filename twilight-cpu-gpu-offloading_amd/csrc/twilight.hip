@@ -125,10 +125,19 @@ __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
   {
     const uint8_t* pm = a.plan_masks + static_cast<int64_t>(g) * a.plan_stride;
     int cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int u = tid; u < u0; u += kBlock) {
-      const uint32_t m = pm[u];
+    for (int ub = 0; ub < u0; ub += 4 * kBlock) {
+      uint32_t m4[4];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) cnt[r] += (m >> r) & 1u;
+      for (int j = 0; j < 4; ++j) {
+        const int u = ub + j * kBlock + tid;
+        m4[j] = pm[u < u0 ? u : 0];
+        m4[j] = u < u0 ? m4[j] : 0u;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) cnt[r] += (m4[j] >> r) & 1u;
+      }
     }
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -163,26 +172,44 @@ __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
   const uint8_t* pk = a.packed + static_cast<int64_t>(g) * a.qstride * (DIM / 2);
   const S* sc = static_cast<const S*>(a.scale) + static_cast<int64_t>(g) * a.qstride;
   const S* mn = static_cast<const S*>(a.minimum) + static_cast<int64_t>(g) * a.qstride;
-  for (int row0 = wave * RPI; row0 < n_rows; row0 += kWaves * RPI) {
-    const int row = row0 + rig;
-    const bool ok = row < n_rows;
-    const int rr = ok ? row : n_rows - 1;
-    const int pi = rr / a.bs;
-    const int i = rr - pi * a.bs;
-    int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[pi]) * a.bs + i;
-    const bool in_range = t >= 0 && t < a.qrows;
-    t = in_range ? t : 0;
-    const uint32_t w = Row::codes(pk + t * (DIM / 2), c0);
-    float k[8];
-    Row::dequant(w, to_f32(DT{}, sc[t]), to_f32(DT{}, mn[t]), k);
-    const uint32_t pmask = s_mask[pi];
+  // Rows in batches of QB wavefront steps: every load of a batch is issued
+  // before the first is used.
+  constexpr int QB = 8;
+  for (int base = wave * RPI; base < n_rows; base += kWaves * RPI * QB) {
+    uint32_t w[QB];
+    S sv[QB], mv[QB];
+    int pis[QB], is[QB];
+    bool oks[QB];
 #pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-      const float acc = Row::dot(k, qv[r]);
-      const int slot = s_slot[pi][r < 8 ? r : 7];
-      if (ok && in_range && (lane % LPR) == 0 && r < R && ((pmask >> r) & 1u) && slot < a.b0) {
-        const int64_t n = static_cast<int64_t>(slot) * a.bs + i;
-        a.logits[(static_cast<int64_t>(g) * R + r) * N + n] = acc * a.qk_scale;
+    for (int b = 0; b < QB; ++b) {
+      const int row = base + b * kWaves * RPI + rig;
+      const bool ok = row < n_rows;
+      const int rr = ok ? row : n_rows - 1;
+      const int pi = rr / a.bs;
+      const int i = rr - pi * a.bs;
+      int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[pi]) * a.bs + i;
+      const bool in_range = t >= 0 && t < a.qrows;
+      t = in_range ? t : 0;
+      w[b] = Row::codes(pk + t * (DIM / 2), c0);
+      sv[b] = sc[t];
+      mv[b] = mn[t];
+      pis[b] = pi;
+      is[b] = i;
+      oks[b] = ok && in_range;
+    }
+#pragma unroll
+    for (int b = 0; b < QB; ++b) {
+      float k[8];
+      Row::dequant(w[b], to_f32(DT{}, sv[b]), to_f32(DT{}, mv[b]), k);
+      const uint32_t pmask = s_mask[pis[b]];
+#pragma unroll
+      for (int r = 0; r < RMAX; ++r) {
+        const float acc = Row::dot(k, qv[r]);
+        const int slot = s_slot[pis[b]][r < 8 ? r : 7];
+        if (oks[b] && (lane % LPR) == 0 && r < R && ((pmask >> r) & 1u) && slot < a.b0) {
+          const int64_t n = static_cast<int64_t>(slot) * a.bs + is[b];
+          a.logits[(static_cast<int64_t>(g) * R + r) * N + n] = acc * a.qk_scale;
+        }
       }
     }
   }
@@ -591,19 +618,54 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
     bits[w] = range_bits(lo, 0, sink_end) | range_bits(lo, recent_start, length);
   }
   __syncthreads();
+  // Page by page: the bs candidates of head r's page pi are bits
+  // [pi*bs, pi*bs + bs) of its selection and positions sink + page*bs + [0, bs)
+  // of the union, so one page moves as one shifted bit field.  Four pages per
+  // thread are fetched before any is used (one round trip per 1024 pages).
   const int n_words = s.words_n;
-  for (int r = 0; r < s.R; ++r) {
-    const uint32_t* sb = s.selbits + (static_cast<int64_t>(g) * s.R + r) * n_words;
-    const int32_t* pages = s.sel_pages + (static_cast<int64_t>(g) * s.R + r) * s.b0;
-    for (int w = tid; w < n_words; w += kBlock) {
-      uint32_t v = __hip_atomic_load(sb + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      while (v != 0u) {
-        const int b = __ffs(static_cast<int>(v)) - 1;
-        v &= v - 1u;
-        const int n = 32 * w + b;
-        const int pi = n / s.bs;
-        const int pos = s.sink + pages[pi] * s.bs + (n - pi * s.bs);
-        if (pos >= 0 && pos < length) atomicOr(&bits[pos >> 5], 1u << (pos & 31));
+  const int bs = s.bs;
+  const int total_pages = s.R * s.b0;
+  for (int base = 0; base < total_pages; base += 4 * kBlock) {
+    int page[4], n0[4];
+    uint32_t lo[4], hi[4];
+    bool act[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = base + j * kBlock + tid;
+      act[j] = idx < total_pages;
+      const int ii = act[j] ? idx : 0;
+      const int r = ii / s.b0;
+      const int pi = ii - r * s.b0;
+      page[j] = s.sel_pages[(static_cast<int64_t>(g) * s.R + r) * s.b0 + pi];
+      n0[j] = pi * bs;
+      const uint32_t* sb = s.selbits + (static_cast<int64_t>(g) * s.R + r) * n_words;
+      const int w0 = n0[j] >> 5;
+      const int w1 = (n0[j] + (bs < 32 ? bs : 32) - 1) >> 5;
+      lo[j] = __hip_atomic_load(sb + w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      hi[j] = __hip_atomic_load(sb + (w1 < n_words ? w1 : w0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!act[j]) continue;
+      const int64_t pos0 = static_cast<int64_t>(s.sink) + static_cast<int64_t>(page[j]) * bs;
+      if (bs <= 32) {
+        const uint64_t both = (static_cast<uint64_t>(hi[j]) << 32) | lo[j];
+        const uint32_t m = static_cast<uint32_t>(both >> (n0[j] & 31)) &
+                           (bs == 32 ? 0xffffffffu : ((1u << bs) - 1u));
+        if (m == 0u || pos0 < 0 || pos0 + bs > length) continue;
+        const uint64_t field = static_cast<uint64_t>(m) << (pos0 & 31);
+        atomicOr(&bits[pos0 >> 5], static_cast<uint32_t>(field));
+        if (static_cast<uint32_t>(field >> 32) != 0u) atomicOr(&bits[(pos0 >> 5) + 1], static_cast<uint32_t>(field >> 32));
+      } else {
+        // pages wider than a word: bit by bit
+        const int r = (base + j * kBlock + tid) / s.b0;
+        const uint32_t* sb = s.selbits + (static_cast<int64_t>(g) * s.R + r) * n_words;
+        for (int i = 0; i < bs; ++i) {
+          const int n = n0[j] + i;
+          const uint32_t v = __hip_atomic_load(sb + (n >> 5), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const int64_t pos = pos0 + i;
+          if (((v >> (n & 31)) & 1u) && pos >= 0 && pos < length) atomicOr(&bits[pos >> 5], 1u << (pos & 31));
+        }
       }
     }
   }
