@@ -143,13 +143,10 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
   }
 }
 
+// Scores of one tile of kTilePages pages of group g for all R heads.
 template <typename DT, int DFIX>
-__global__ __launch_bounds__(kBlock) void quest_score_kernel(ScoreArgs a) {
-  extern __shared__ __align__(16) uint8_t lds[];
+__device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
   using S = typename DT::storage;
-  const int tiles = (a.P + kTilePages - 1) / kTilePages;
-  const int g = blockIdx.x / tiles;
-  const int tile = blockIdx.x - g * tiles;
   const int p0 = tile * kTilePages;
   const int np = (a.P - p0) < kTilePages ? (a.P - p0) : kTilePages;
   const int pitch = a.D * static_cast<int>(sizeof(S)) + 16;  // 16-byte aligned rows, padded
@@ -208,6 +205,14 @@ __global__ __launch_bounds__(kBlock) void quest_score_kernel(ScoreArgs a) {
       if (a.scores_out != nullptr) a.scores_out[row * a.P + p0 + lane] = s;
     }
   }
+}
+
+template <typename DT, int DFIX>
+__global__ __launch_bounds__(kBlock) void quest_score_kernel(ScoreArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tiles = (a.P + kTilePages - 1) / kTilePages;
+  const int g = blockIdx.x / tiles;
+  score_tile<DT, DFIX>(a, g, blockIdx.x - g * tiles, lds);
 }
 
 // --------------------------------------------------------------- selection
@@ -510,8 +515,6 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
   int32_t* sel_ws = reinterpret_cast<int32_t*>(score_ws + static_cast<int64_t>(G) * R * tw::padded(P));
   const hipStream_t st = static_cast<hipStream_t>(stream);
   tw::ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P, D, score_ws, tw::padded(P), scores};
-  int rc = tw::dispatch_score(dtype, a, st);
-  if (rc != TW_OK) return rc;
   tw::SelectArgs s{};
   s.scores = score_ws;
   s.score_stride = tw::padded(P);
@@ -537,5 +540,7 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
   s.length = length;
   s.append_position = append_position;
   s.counters = counters;
+  const int rc = tw::dispatch_score(dtype, a, st);
+  if (rc != TW_OK) return rc;
   return tw::launch_select(s, G * R, true, st);
 }

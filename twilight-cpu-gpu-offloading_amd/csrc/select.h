@@ -136,8 +136,7 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      const bool c = (cand >> j) & 1u;
-      atomicAdd(&sh.hist[c ? fn(key[j]) : kLinBins], 1u);
+      if ((cand >> j) & 1u) atomicAdd(&sh.hist[fn(key[j])], 1u);
     }
     __syncthreads();
     uint32_t tot = 0u;

@@ -486,10 +486,11 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      const bool c = (cand >> j) & 1u;
-      const int b = c ? fn(key[j]) : kLinBins;
-      atomicAdd(&sh.sel.hist[b], 1u);
-      if (c && mass[j] != 0) atomicAdd(&sh.bin_mass[b], static_cast<unsigned long long>(mass[j]));
+      if ((cand >> j) & 1u) {
+        const int b = fn(key[j]);
+        atomicAdd(&sh.sel.hist[b], 1u);
+        if (mass[j] != 0) atomicAdd(&sh.bin_mass[b], static_cast<unsigned long long>(mass[j]));
+      }
     }
     __syncthreads();
     uint64_t tmass = 0;
