@@ -7,12 +7,13 @@
 //
 // Two kernels per layer:
 //
-// 1. Scores.  A block of 4 wavefronts scores a tile of 64 pages of one KV
+// 1. Scores.  A block of 8 wavefronts scores a tile of 64 pages of one KV
 //    group for all R query heads.  The tile is staged once in LDS with
-//    16-byte loads (padded, 16-byte aligned row pitch); wavefront
-//    w then scores head w (w+4, ...) with lane = page, so the q > 0 choice of
-//    min or max is wave-uniform.  Order (bit-exact with the reference for
-//    D = 128): 32 accumulators, accumulator l adds the products of channels
+//    16-byte loads (padded, 16-byte aligned row pitch); wavefronts w and
+//    w+4 then score head w (w+4, ...) with lane = page, each summing half of
+//    the 32 accumulators, so the q > 0 choice of min or max is wave-uniform.
+//    Order (bit-exact with the reference for D = 128): 32 accumulators,
+//    accumulator l adds the products of channels
 //    l, l+32, l+64, l+96 in that order starting from +0; the 32 accumulators
 //    are then summed by an adjacent-pair tree (the lane-0 result of
 //    shuffle-adds at offsets 1..16).  Each product is
@@ -162,53 +163,75 @@ __device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
   const int wave = wave_uniform(static_cast<int>(threadIdx.x) / kWave);
   const int lane = lane_id();
   const int D = DFIX > 0 ? DFIX : a.D;
-  for (int r = wave; r < a.R; r += kWaves) {
-    const float* qh = q_lds + r * D;
-    float acc[32];
+  // Two wavefronts per head: half h sums accumulators 16h .. 16h+15 (channels
+  // d with d mod 32 in that range); the adjacent-pair tree over the 32
+  // accumulators is the sum of the two halves' 16-accumulator trees.
+  const int half = wave / 4;
+  const int hw = wave % 4;
+  __shared__ float s_half[4][kWave];
+  for (int r0 = 0; r0 < a.R; r0 += 4) {
+    const int r = r0 + hw;
+    float part = 0.0f;
+    if (r < a.R) {
+      const float* qh = q_lds + r * D;
+      float acc[16];
 #pragma unroll
-    for (int l = 0; l < 32; ++l) acc[l] = 0.0f;
-    const uint8_t* min_row = lds + lane * pitch;
-    const uint8_t* max_row = lds + (kTilePages + lane) * pitch;
-    if constexpr (DFIX > 0) {
-      // 8 channels per step: 16-byte reads of both rows (independent of q,
-      // so they issue back to back), then the q > 0 choice on the data.
+      for (int l = 0; l < 16; ++l) acc[l] = 0.0f;
+      const uint8_t* min_row = lds + lane * pitch;
+      const uint8_t* max_row = lds + (kTilePages + lane) * pitch;
+      if constexpr (DFIX > 0) {
+        // 8 channels per step: 16-byte reads of both rows, then the q > 0
+        // choice on the data.
 #pragma unroll
-      for (int c = 0; c < DFIX / 8; ++c) {
-        float qv[8], x[8];
-        *reinterpret_cast<float4*>(qv) = *reinterpret_cast<const float4*>(qh + 8 * c);
-        *reinterpret_cast<float4*>(qv + 4) = *reinterpret_cast<const float4*>(qh + 8 * c + 4);
-        select8(min_row + 8 * c * es, max_row + 8 * c * es, qv, x, DT{});
+        for (int c = 0; c < DFIX / 32; ++c) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int d = 8 * c + i;
-          acc[d & 31] = acc[d & 31] + x[i] * qv[i];
+          for (int e = 0; e < 2; ++e) {
+            const int d0 = 32 * c + 16 * half + 8 * e;
+            float qv[8], x[8];
+            *reinterpret_cast<float4*>(qv) = *reinterpret_cast<const float4*>(qh + d0);
+            *reinterpret_cast<float4*>(qv + 4) = *reinterpret_cast<const float4*>(qh + d0 + 4);
+            select8(min_row + d0 * es, max_row + d0 * es, qv, x, DT{});
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[8 * e + i] = acc[8 * e + i] + x[i] * qv[i];
+          }
         }
-      }
-    } else {
-      for (int c = 0; c * 32 < D; ++c) {
+      } else {
+        for (int c = 0; c * 32 < D; ++c) {
 #pragma unroll
-        for (int l = 0; l < 32; ++l) {
-          const int d = c * 32 + l;
-          if (d < D) {
-            const float qd = qh[d];
-            const uint8_t* src = (qd > 0.0f) ? max_row : min_row;
-            const float x = lds_load(src + d * es, DT{});
-            acc[l] = acc[l] + x * qd;
+          for (int l = 0; l < 16; ++l) {
+            const int d = c * 32 + 16 * half + l;
+            if (d < D) {
+              const float qd = qh[d];
+              const uint8_t* src = (qd > 0.0f) ? max_row : min_row;
+              const float x = lds_load(src + d * es, DT{});
+              acc[l] = acc[l] + x * qd;
+            }
           }
         }
       }
+#pragma unroll
+      for (int w = 1; w < 16; w <<= 1) {
+#pragma unroll
+        for (int l = 0; l < 16; l += 2 * w) acc[l] = acc[l] + acc[l + w];
+      }
+      part = acc[0];
     }
-    const float s = tree32(acc);
-    if (lane < np) {
+    if (half == 1) s_half[hw][lane] = part;
+    __syncthreads();
+    if (half == 0 && r < a.R && lane < np) {
+      const float sc = part + s_half[hw][lane];
       const int64_t row = static_cast<int64_t>(g) * a.R + r;
-      a.scores[row * a.score_stride + p0 + lane] = s;
-      if (a.scores_out != nullptr) a.scores_out[row * a.P + p0 + lane] = s;
+      a.scores[row * a.score_stride + p0 + lane] = sc;
+      if (a.scores_out != nullptr) a.scores_out[row * a.P + p0 + lane] = sc;
     }
+    __syncthreads();
   }
 }
 
+constexpr int kScoreBlock = 512;  // 8 wavefronts: two per head
+
 template <typename DT, int DFIX>
-__global__ __launch_bounds__(kBlock) void quest_score_kernel(ScoreArgs a) {
+__global__ __launch_bounds__(kScoreBlock) void quest_score_kernel(ScoreArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int tiles = (a.P + kTilePages - 1) / kTilePages;
   const int g = blockIdx.x / tiles;
@@ -414,7 +437,7 @@ int launch_score(const ScoreArgs& a, hipStream_t stream) {
   if (lds > 64 * 1024)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               static_cast<int>(lds));
-  hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, stream, a);
+  hipLaunchKernelGGL(kern, grid, dim3(kScoreBlock), lds, stream, a);
   return tw_host::check_launch();
 }
 
