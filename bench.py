@@ -15,7 +15,9 @@ last-level cache.
 A "step" is one replay of a HIP graph holding the 32 layers.  ``value`` is
 the algorithmic bytes of the step divided by its time (GB/s); ``layer_us`` is
 the step time divided by 32.  Per-kernel durations come from graphs holding
-only that kernel's 32 launches, timed with events on the launch stream.
+only that kernel's 32 launches (the attention's split-K kernel through the
+phase-1 entry point, its merge as the difference to the full call), timed
+with events on the launch stream.
 
 The CPU baseline times the oracle's torch-CPU port of the reference's op
 sequence for one layer (oracle/cpu_baseline.py) on a bounded sample.
@@ -134,14 +136,15 @@ class QuestWorkload:
         kernels.append_kv(self.cur_k[layer], self.cur_v[layer], self.kc[layer], self.vc[layer], first_entry=0,
                           position=self.L)
 
-    def attend(self, layer: int) -> None:
+    def attend(self, layer: int, phase: int = 3) -> None:
         from headinfer import kernels
 
         kernels.decode_attention_pages(self.q[layer], self.kc[layer], self.vc[layer], self.plan_pages[layer],
                                        self.plan_counts[layer], plan_masks=self.plan_masks[layer],
                                        max_pages=self.max_pages, sink=self.SINK, recent=self.RECENT,
                                        block_size=self.BS, length=self.L, append_position=self.L,
-                                       cur_k=self.cur_k[layer], cur_v=self.cur_v[layer], out=self.out[layer])
+                                       cur_k=self.cur_k[layer], cur_v=self.cur_v[layer], out=self.out[layer],
+                                       phase=phase)
 
     def step(self) -> None:
         """One decode step: per layer, Quest selection then attention with the
@@ -499,6 +502,8 @@ def main(argv=None) -> int:
     g_step = graph_of(w.step)
     g_sel = graph_of(lambda: [w.select(i) for i in range(w.layers)])
     g_att = graph_of(lambda: [w.attend(i) for i in range(w.layers)])
+    # the split-K kernel alone (phase 1; its partials are merged by phase 2)
+    g_att1 = graph_of(lambda: [w.attend(i, phase=1) for i in range(w.layers)])
 
     for _ in range(args.warmup):
         g_step.replay()
@@ -514,6 +519,9 @@ def main(argv=None) -> int:
     reps = max(20, args.steps // 2)
     t_sel = time_graph(g_sel, reps) / w.layers
     t_att = time_graph(g_att, reps) / w.layers
+    t_att1 = time_graph(g_att1, reps) / w.layers
+    w.step()  # leave a complete step's outputs after the phase-1 replays
+    torch.cuda.synchronize()
     by = w.bytes_per_layer()
     layer_bytes = by["select"] + by["attention"]
     layer_s = wall / w.layers
@@ -521,10 +529,14 @@ def main(argv=None) -> int:
     kern = {
         "quest_select": {"us": round(t_sel * 1e6, 2), "bytes": int(by["select"]),
                          "GBps": round(by["select"] / t_sel / 1e9, 1)},
-        "decode_attention": {"us": round(t_att * 1e6, 2), "bytes": int(by["attention"]),
-                             "GBps": round(by["attention"] / t_att / 1e9, 1)},
+        "decode_attention": {"us": round(t_att1 * 1e6, 2), "bytes": int(by["attention"]),
+                             "GBps": round(by["attention"] / t_att1 / 1e9, 1),
+                             "kernel": "decode_attn_mfma (split-K, fused decode-token append)"},
+        "attention_merge": {"us": round((t_att - t_att1) * 1e6, 2), "kernel": "merge_vec_kernel"},
     }
-    dom = "decode_attention" if t_att >= t_sel else "quest_select"
+    # the split-K attention is the longest single kernel of the layer (the
+    # selection entry is two launches: score and top-k + union)
+    dom = "decode_attention"
     ach = kern[dom]["GBps"]
     result = {
         "metric": METRIC,
@@ -625,6 +637,8 @@ def run_twilight(args, dev) -> int:
     g_step = graph_of(w.step)
     g_sel = graph_of(lambda: [w.select(i) for i in range(w.layers)])
     g_att = graph_of(lambda: [w.attend(i) for i in range(w.layers)])
+    # the split-K kernel alone (phase 1; its partials are merged by phase 2)
+    g_att1 = graph_of(lambda: [w.attend(i, phase=1) for i in range(w.layers)])
     wall, _ = _timed_steps(g_step, args.steps, args.warmup)
     reps = max(20, args.steps // 2)
     t_sel = time_graph(g_sel, reps) / w.layers
@@ -764,7 +778,7 @@ def run_offload(args, dev) -> int:
 # rocprofv3 FETCH_SIZE / WRITE_SIZE of each kernel, calibrated against a copy
 # of known size and recorded with the commands that produced them.
 TRAFFIC_PROFILE = ROOT / "profiles" / "pmc_traffic_quest32k.md"
-TRAFFIC_KERNEL = {"decode_attention": "decode_attn_kernel", "quest_select": "quest_score_kernel"}
+TRAFFIC_KERNEL = {"decode_attention": "decode_attn", "quest_select": "quest_score_kernel"}
 
 
 def measured_traffic(kernel: str):

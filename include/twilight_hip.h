@@ -245,6 +245,19 @@ int tw_decode_attention_pages(const void* q, const void* k_base, const void* v_b
                               int64_t entry_stride_rows, int sink, int recent, int block_size, int length,
                               int append_position, const void* cur_k, const void* cur_v, float softmax_scale,
                               void* out, void* workspace, size_t workspace_bytes, void* stream);
+/* tw_decode_attention_pages in two phases: phase 1 launches only the split-K
+ * kernel (groups that span one chunk get their final output; the others
+ * leave (m, l, o) partials in the workspace), phase 2 only the merge of those
+ * partials into out, phase 3 both (= tw_decode_attention_pages).  Phase 2
+ * takes the arguments and the workspace of the phase-1 call it completes.
+ * For callers that combine or time the two halves separately (e.g. partials
+ * combined across devices before the merge). */
+int tw_decode_attention_pages_phase(const void* q, const void* k_base, const void* v_base, int dtype, int G,
+                                    int R, int D, const int32_t* plan_pages, const uint8_t* plan_masks,
+                                    const int32_t* plan_counts, int64_t plan_stride, int max_rows,
+                                    int64_t entry_stride_rows, int sink, int recent, int block_size, int length,
+                                    int append_position, const void* cur_k, const void* cur_v, float softmax_scale,
+                                    void* out, void* workspace, size_t workspace_bytes, int phase, void* stream);
 int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G,
                         int R, int D, const int32_t* rows, const uint8_t* row_masks,
                         const int32_t* row_counts, int64_t rows_stride, int64_t entry_stride_rows,

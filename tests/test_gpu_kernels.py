@@ -421,3 +421,34 @@ def test_append_kv(K, dev, host):
     torch.cuda.synchronize()
     assert same_bits(dk[2:5, 17], nk.cpu()) and same_bits(dv[2:5, 17], nv.cpu())
     assert float(dk.cpu().float().abs().sum()) == float(nk.cpu().float().abs().sum())
+
+
+@pytest.mark.parametrize("dtype,G,R,D,L,k", [("f16", 8, 4, 128, 32768, 128), ("bf16", 3, 2, 64, 3000, 20)])
+def test_decode_attention_pages_phases(K, dev, dtype, G, R, D, L, k):
+    """Phase 1 (split-K partials) then phase 2 (merge) == the single call, bit for bit."""
+    _say(f"[attention phases] {dtype} G={G} L={L}")
+    g0 = torch.Generator().manual_seed(L + 7)
+    sink, recent, bs = 64, 256, 16
+    sink_end, recent_start, eligible = oracle.selection_window(L, sink, recent)
+    P = eligible // bs
+    mp = min(P, R * k)
+    pages = torch.zeros((G, mp), dtype=torch.int32)
+    pm = torch.zeros((G, mp), dtype=torch.uint8)
+    counts = torch.zeros((G,), dtype=torch.int32)
+    for g in range(G):
+        n = int(torch.randint(1, mp + 1, (1,), generator=g0))
+        pages[g, :n] = torch.randperm(P, generator=g0)[:n].sort().values.to(torch.int32)
+        pm[g, :n] = torch.randint(1, 1 << R, (n,), generator=g0).to(torch.uint8)
+        counts[g] = n
+    kc = randn((G, L + 1, D), dtype, seed=51).to(dev)
+    vc = randn((G, L + 1, D), dtype, seed=52).to(dev)
+    q = randn((G, R, D), dtype, seed=53).to(dev)
+    args = (q, kc, vc, pages.to(dev), counts.to(dev))
+    kw = dict(plan_masks=pm.to(dev), max_pages=mp, sink=sink, recent=recent, block_size=bs, length=L,
+              append_position=L)
+    full = K.decode_attention_pages(*args, **kw)
+    split = torch.empty_like(full)
+    K.decode_attention_pages(*args, **kw, out=split, phase=1)
+    K.decode_attention_pages(*args, **kw, out=split, phase=2)
+    torch.cuda.synchronize()
+    assert same_bits(full, split)

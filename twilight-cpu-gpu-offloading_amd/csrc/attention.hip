@@ -76,6 +76,7 @@ struct AttnArgs {
   int max_chunks;
   int iters;                // row batches per block
   int max_rows;             // bound on every group's row count
+  int phase;                // host side: 1 split-K partials, 2 merge, 3 (or 0) both
 };
 
 // 8 consecutive channels of one row.
@@ -1088,9 +1089,12 @@ size_t dyn_lds_bytes(int R, int D) { return static_cast<size_t>(kWaves) * rmax_f
 
 template <typename DT, int D, int RMAX, int MODE>
 int launch_one(const AttnArgs& a, hipStream_t stream) {
+  const int phase = a.phase == 0 ? 3 : a.phase;
   size_t lds = dyn_lds_bytes(a.R, a.D);
   const dim3 grid(a.G * a.max_chunks);
-  if constexpr (D > 0 && !std::is_same<DT, F32>::value) {
+  if (!(phase & 1)) {
+    // merge only: the partials of an earlier phase-1 launch with the same arguments
+  } else if constexpr (D > 0 && !std::is_same<DT, F32>::value) {
     constexpr int RM = RMAX < 4 ? 4 : RMAX;
     lds = static_cast<size_t>(kWaves) * RM * D * sizeof(float);
     auto kern = decode_attn_mfma<DT, D, RM, MODE>;
@@ -1112,7 +1116,7 @@ int launch_one(const AttnArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, stream, a);
   }
   int rc = tw_host::check_launch();
-  if (rc != TW_OK || a.max_chunks <= 1) return rc;
+  if (rc != TW_OK || !(phase & 2) || a.max_chunks <= 1) return rc;
   // a block must cover every chunk with one (m, l) per thread
   int threads = ((a.D + kWave - 1) / kWave) * kWave;
   threads = threads < a.max_chunks ? ((a.max_chunks + kWave - 1) / kWave) * kWave : threads;
@@ -1261,6 +1265,21 @@ extern "C" int tw_decode_attention_pages(const void* q, const void* k_base, cons
                                          int length, int append_position, const void* cur_k, const void* cur_v,
                                          float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
                                          void* stream) {
+  return tw_decode_attention_pages_phase(q, k_base, v_base, dtype, G, R, D, plan_pages, plan_masks, plan_counts,
+                                         plan_stride, max_rows, entry_stride_rows, sink, recent, block_size, length,
+                                         append_position, cur_k, cur_v, softmax_scale, out, workspace,
+                                         workspace_bytes, 3, stream);
+}
+
+extern "C" int tw_decode_attention_pages_phase(const void* q, const void* k_base, const void* v_base, int dtype,
+                                               int G, int R, int D, const int32_t* plan_pages,
+                                               const uint8_t* plan_masks, const int32_t* plan_counts,
+                                               int64_t plan_stride, int max_rows, int64_t entry_stride_rows,
+                                               int sink, int recent, int block_size, int length,
+                                               int append_position, const void* cur_k, const void* cur_v,
+                                               float softmax_scale, void* out, void* workspace,
+                                               size_t workspace_bytes, int phase, void* stream) {
+  if (phase < 1 || phase > 3) return TW_EINVAL;
   if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr || G <= 0 || R <= 0 || R > 8 ||
       D <= 0 || D > 512 || (D % 2) != 0 || max_rows < 0)
     return TW_EINVAL;
@@ -1310,6 +1329,7 @@ extern "C" int tw_decode_attention_pages(const void* q, const void* k_base, cons
   a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ml_off);
   a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
   a.max_rows = max_rows;
+  a.phase = phase;
   tw::plan_chunks(dtype, G, R, D, max_rows, &a.iters, &a.max_chunks);
   return tw::launch_dtype(dtype, a, static_cast<hipStream_t>(stream));
 }

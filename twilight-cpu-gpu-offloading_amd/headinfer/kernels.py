@@ -498,13 +498,17 @@ def decode_attention_pages(
     cur_v: Optional[torch.Tensor] = None,
     softmax_scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
+    phase: int = 3,
 ) -> torch.Tensor:
     """Sparse GQA decode attention over a union plan from quest_select: group
     g sees [0, sink_end) ++ its union pages (heads per plan_masks) ++ the
     recent window ++ the decode token.  q [G,R,D]; k_cache/v_cache [G, Lmax, D].
     The decode token is cache row append_position, or cur_k/cur_v [G, D] when
     given -- then they are also appended to row append_position of the cache
-    in the same launch.  Returns [G,R,D]."""
+    in the same launch.  phase 1 runs only the split-K kernel, phase 2 only
+    the merge of its partials (same arguments), 3 both.  Returns [G,R,D]."""
+    if phase not in (1, 2, 3):
+        raise ValueError("phase must be 1, 2 or 3")
     if q.ndim != 3 or q.dtype not in _KEY_DTYPES:
         raise ValueError("q must be [G, R, D]")
     G, R, D = q.shape
@@ -545,12 +549,12 @@ def decode_attention_pages(
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
     with torch.cuda.device(dev):
-        check(hip().tw_decode_attention_pages(ptr(q), kp, vp, _dt(q), G, R, D,
-                                              ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
-                                              plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink, recent,
-                                              block_size, length, append_position, ptr(cur_k), ptr(cur_v), scale,
-                                              ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
-              "decode_attention_pages")
+        check(hip().tw_decode_attention_pages_phase(ptr(q), kp, vp, _dt(q), G, R, D,
+                                                    ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
+                                                    plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink,
+                                                    recent, block_size, length, append_position, ptr(cur_k),
+                                                    ptr(cur_v), scale, ptr(out), ptr(ws), ws.numel(), int(phase),
+                                                    stream_handle(dev)), "decode_attention_pages")
     return out
 
 
