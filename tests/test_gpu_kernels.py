@@ -343,6 +343,88 @@ def test_decode_attention_pages(K, dev, dtype, G, R, D, L, k, sink, recent, bs, 
     _close(out2, ref2)
 
 
+@pytest.mark.parametrize(
+    "dtype,G,R,L,n_pages,decode,masked",
+    [
+        ("bf16", 2, 8, 700, 12, "cur_append", False),  # 8 heads, unmasked
+        ("f16", 3, 1, 500, 11, "cur_append", True),    # one head
+        ("f16", 2, 2, 900, 30, "cache_row", True),     # decode token read from cache row L
+        ("bf16", 2, 3, 1200, 40, "none", True),        # no decode token
+        ("f16", 2, 5, 1000, 25, "cur_only", True),     # decode token attended, not appended
+        ("bf16", 2, 4, 40, 0, "cur_append", False),    # context inside the sink window
+        ("f16", 2, 4, 300, 0, "cur_append", True),     # sink + recent only
+        ("f16", 3, 4, 70000, 1100, "cur_append", True),  # two batches per wavefront
+    ],
+)
+def test_decode_attention_page_tiles(K, dev, dtype, G, R, L, n_pages, decode, masked):
+    """16-row pages at D = 128 (the page-tile kernel): partial sink and recent
+    tiles, every decode-token form, R from 1 to 8, plan counts above the plan
+    width (clamped), against float64 over the expanded rows."""
+    _say(f"[attention page tiles] {dtype} G={G} R={R} L={L} pages={n_pages} decode={decode}")
+    D, sink, recent, bs = 128, 64, 256, 16
+    g0 = torch.Generator().manual_seed(L + R)
+    sink_end, recent_start, eligible = oracle.selection_window(L, sink, recent)
+    P = eligible // bs
+    width = max(1, n_pages)
+    Lmax = L + 2
+    kc = randn((G, Lmax, D), dtype, seed=61)
+    vc = randn((G, Lmax, D), dtype, seed=62)
+    q = randn((G, R, D), dtype, seed=63)
+    pages = torch.zeros((G, width), dtype=torch.int32)
+    pm = torch.zeros((G, width), dtype=torch.uint8)
+    counts = torch.zeros((G,), dtype=torch.int32)
+    for g in range(G):
+        n = min(n_pages, P) if g == 0 else int(torch.randint(0, min(n_pages, P) + 1, (1,), generator=g0))
+        if n:
+            pages[g, :n] = torch.randperm(P, generator=g0)[:n].sort().values.to(torch.int32)
+            pm[g, :n] = torch.randint(1, 1 << R, (n,), generator=g0).to(torch.uint8)
+        counts[g] = n
+    counts_dev = counts.clone()
+    if n_pages:
+        counts_dev[0] = width + 5  # beyond the plan width: the launch covers `width` pages
+    ck, cv = randn((G, D), dtype, seed=64), randn((G, D), dtype, seed=65)
+    kd, vd = kc.to(dev), vc.to(dev)
+    kw = dict(plan_masks=pm.to(dev) if masked else None, max_pages=width if n_pages else 0, sink=sink,
+              recent=recent, block_size=bs, length=L)
+    if decode == "cur_append":
+        kw.update(append_position=L, cur_k=ck.to(dev), cur_v=cv.to(dev))
+    elif decode == "cur_only":
+        kw.update(append_position=-1, cur_k=ck.to(dev), cur_v=cv.to(dev))
+    elif decode == "cache_row":
+        kw.update(append_position=L)
+    else:
+        kw.update(append_position=-1)
+    out = K.decode_attention_pages(q.to(dev), kd, vd, pages.to(dev), counts_dev.to(dev), **kw)
+    torch.cuda.synchronize()
+    if decode == "cur_append":
+        assert same_bits(kd[:, L], ck) and same_bits(vd[:, L], cv)
+    else:
+        assert same_bits(kd[:, L], kc[:, L]) and same_bits(vd[:, L], vc[:, L])
+    all_heads = (1 << R) - 1
+    ref = np.zeros((G, R, D))
+    for g in range(G):
+        n = int(counts[g])
+        pg = pages[g, :n].long()
+        keys = [kc[g, :sink_end], kc[g, (sink + pg[:, None] * bs + torch.arange(bs)).reshape(-1)],
+                kc[g, recent_start:L]]
+        vals = [vc[g, :sink_end], vc[g, (sink + pg[:, None] * bs + torch.arange(bs)).reshape(-1)],
+                vc[g, recent_start:L]]
+        m = [np.full(sink_end, all_heads), pm[g, :n].long().repeat_interleave(bs).numpy() if masked
+             else np.full(n * bs, all_heads), np.full(L - recent_start, all_heads)]
+        if decode.startswith("cur"):
+            keys.append(ck[g:g + 1])
+            vals.append(cv[g:g + 1])
+        elif decode == "cache_row":
+            keys.append(kc[g, L:L + 1])
+            vals.append(vc[g, L:L + 1])
+        if decode != "none":
+            m.append(np.array([all_heads]))
+        ref[g] = oracle.decode_attention(q[g].float().numpy(), torch.cat(keys).float().numpy(),
+                                         torch.cat(vals).float().numpy(), 1.0 / math.sqrt(D),
+                                         np.concatenate(m).astype(np.uint8))
+    _close(out, ref)
+
+
 @pytest.mark.parametrize("dtype,B,Hk,R,D", [("bf16", 8, 1, 4, 128), ("f16", 3, 2, 3, 128), ("bf16", 5, 1, 1, 4)])
 def test_decode_attention_varlen(K, dev, dtype, B, Hk, R, D):
     _say(f"[attention varlen] {dtype} B={B} Hk={Hk} R={R} D={D}")

@@ -77,6 +77,15 @@ struct AttnArgs {
   int iters;                // row batches per block
   int max_rows;             // bound on every group's row count
   int phase;                // host side: 1 split-K partials, 2 merge, 3 (or 0) both
+  // Page-tile kernel (16-row pages): window geometry computed on the host.
+  int t_sink_tiles;         // ceil(sink_end / 16)
+  int t_sink_end;
+  int t_recent_start;
+  int t_n_recent;           // recent rows: [recent_start, length)
+  int t_has_dec;            // a decode token follows the recent rows
+  int t_run;                // t_n_recent + t_has_dec
+  int t_run_tiles;          // ceil(t_run / 16)
+  int t_nu_cap;             // union pages the launch covers at most
 };
 
 // 8 consecutive channels of one row.
@@ -202,6 +211,16 @@ __device__ __forceinline__ GroupRows group_rows(const AttnArgs& a, int g, int D)
   return gr;
 }
 
+// Page-tile mode (decode_attn_tiles): chunks count 16-row tiles.
+constexpr int kModeTiles = 3;
+
+// Union pages of group g that a page-tile launch covers.
+__device__ __forceinline__ int tile_pages(const AttnArgs& a, int g) {
+  int nu = a.plan_counts[g];
+  nu = nu < 0 ? 0 : nu;
+  return nu > a.t_nu_cap ? a.t_nu_cap : nu;
+}
+
 // Append the decode token of group g to its cache entry (chunk 0's block).
 template <typename S>
 __device__ __forceinline__ void append_decode_token(const AttnArgs& a, int g, int D) {
@@ -288,8 +307,15 @@ __global__ __launch_bounds__(kBlock) void merge_vec_kernel(AttnArgs a, int rows_
   const int R = a.R;
   const int g = blockIdx.x / R;
   const int r = blockIdx.x - g * R;
-  const GroupRows gr = group_rows<MODE>(a, g, D);
-  const int n_chunks = (gr.n_rows + rows_per_block - 1) / rows_per_block;
+  // rows_per_block: rows of a chunk, or tiles of a chunk in page-tile mode
+  int n_chunks;
+  if constexpr (MODE == kModeTiles) {
+    const int nt = a.t_sink_tiles + tile_pages(a, g) + a.t_run_tiles;
+    n_chunks = (nt + rows_per_block - 1) / rows_per_block;
+  } else {
+    const GroupRows gr = group_rows<MODE>(a, g, D);
+    n_chunks = (gr.n_rows + rows_per_block - 1) / rows_per_block;
+  }
   if (n_chunks <= 1) return;
   const int t = threadIdx.x;
   const int q = t % NQ;
@@ -929,6 +955,320 @@ __global__ __launch_bounds__(kBlock, 2) void decode_attn_mfma(AttnArgs a) {
   block_partial<DT, RMAX>(a, g, chunk, D, n_chunks == 1, s_m, s_l, s_o);
 }
 
+// ---------------------------------------------------------------------------
+// Page-tile decode attention: page mode with 16-row pages, D = 128, 16-bit
+// K/V, R <= 8.  The group's rows are walked as 16-row tiles -- the sink
+// window in runs of 16 positions, one tile per union page (a page's rows are
+// contiguous in the entry), then the recent window followed by the decode
+// token.  Which source a tile has is wave-uniform, so a page id costs one
+// scalar load per tile and every lane addresses its rows as the tile's base
+// plus a lane offset.  The plan count and the wave's page slots are loaded in
+// the same round trip (slots are read speculatively, clamped to the plan
+// width), so K/V loads are the second and last dependent round trip.
+//
+// q.k: v_mfma_f32_16x16x32 with the heads as A rows (zero rows for heads >= R)
+// and the tile's 16 rows as B columns; lane (row, quarter) holds channels
+// 32 s + 8 quarter + [0, 8) of k-step s, so one K load instruction reads 64
+// contiguous bytes of each of 16 rows.  The result gives lane (row, quarter)
+// the scores of heads 4 quarter + [0, 4).
+// p.v: lane (c8, rg) owns channels 8 c8 + [0, 8) of rows 4 rg + [0, 4) of a
+// tile.  p goes through LDS as the input dtype, stored as (row 2i, row 2i+1)
+// pairs per head so that one 16-byte read gives a row pair's p for four
+// heads, and pairs of rows are combined with v_dot2_f32_{f16,bf16}.
+// One wavefront batch is TW tiles; a wave's first batch needs no rescale.
+constexpr int kTileRows = 16;
+constexpr int kTileD = 128;
+
+struct TileSrc {
+  int64_t pos0;  // position of the tile's row 0 in the entry (cache rows)
+  int cnt;       // rows of the tile that exist (0..16)
+  int dec;       // index of the decode token in the tile, or -1
+  uint32_t hm;   // heads that see the tile's cache rows
+};
+
+__device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, int t, int nu, int page, uint32_t pmask) {
+  TileSrc s;
+  s.dec = -1;
+  s.hm = 0xffu;
+  const int ts = a.t_sink_tiles;
+  if (t < ts) {
+    s.pos0 = static_cast<int64_t>(kTileRows) * t;
+    const int c = a.t_sink_end - kTileRows * t;
+    s.cnt = c < kTileRows ? c : kTileRows;
+  } else if (t < ts + nu) {
+    s.pos0 = a.sink + static_cast<int64_t>(page) * kTileRows;
+    s.hm = pmask;
+    s.cnt = (s.pos0 >= 0 && s.pos0 + kTileRows <= a.entry_stride) ? kTileRows : 0;
+  } else {
+    const int j0 = kTileRows * (t - ts - nu);
+    s.pos0 = static_cast<int64_t>(a.t_recent_start) + j0;
+    const int c = a.t_run - j0;
+    s.cnt = c < 0 ? 0 : (c < kTileRows ? c : kTileRows);
+    const int d = a.t_n_recent - j0;
+    s.dec = (a.t_has_dec && d >= 0 && d < kTileRows) ? d : -1;
+  }
+  if (s.cnt <= 0) {
+    s.cnt = 0;
+    s.pos0 = 0;
+  }
+  return s;
+}
+
+template <typename DT, int RMAX, int NW, int TW>
+__global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
+  using S = typename DT::storage;
+  using H = Half8<DT>;
+  constexpr int D = kTileD;
+  constexpr int NQ = RMAX > 4 ? 2 : 1;  // quarters of the q.k result that hold heads
+  constexpr int PW = RMAX / 4 > 0 ? RMAX / 4 : 1;  // 16-byte p reads per row pair
+  static_assert(RMAX == 4 || RMAX == 8, "4 or 8 head slots");
+
+  const int R = a.R;
+  const int g = blockIdx.x / a.max_chunks;
+  const int chunk = blockIdx.x - g * a.max_chunks;
+  const int wave = wave_uniform(static_cast<int>(threadIdx.x) / kWave);
+  const int lane = lane_id();
+  const int krow = lane & 15;
+  const int quarter = lane >> 4;
+  const int c8 = (lane & 15) * 8;
+  const int rg = lane >> 4;
+
+  __shared__ float s_m[NW][RMAX];
+  __shared__ float s_l[NW][RMAX];
+  __shared__ __align__(16) uint32_t s_p[NW][TW][8][RMAX];
+  __shared__ __align__(16) float s_o[NW][RMAX][D];
+
+  // ---- round trip 1: plan count, the first batch's page slots, q ----
+  const int64_t plan_base = static_cast<int64_t>(g) * a.plan_stride;
+  const int slot_last = static_cast<int>(a.plan_stride - 1);
+  const int per_chunk = NW * TW * a.iters;
+  int page[TW];
+  uint32_t pmask[TW];
+  auto load_slots = [&](int t0) {
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+      int u = t0 + tt - a.t_sink_tiles;
+      u = u < 0 ? 0 : (u > slot_last ? slot_last : u);
+      page[tt] = a.plan_pages[plan_base + u];
+      pmask[tt] = a.plan_masks != nullptr ? static_cast<uint32_t>(a.plan_masks[plan_base + u]) : 0xffu;
+    }
+  };
+  load_slots((chunk * a.iters * NW + wave) * TW);
+  uint4 qf[4];
+  {
+    const S* qh = static_cast<const S*>(a.q) + (static_cast<int64_t>(g) * R + (krow < R ? krow : 0)) * D + 8 * quarter;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint4 t = *reinterpret_cast<const uint4*>(qh + 32 * s);
+      qf[s] = krow < R ? t : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  const int nu = tile_pages(a, g);
+  const int n_tiles = a.t_sink_tiles + nu + a.t_run_tiles;
+  const int n_chunks = (n_tiles + per_chunk - 1) / per_chunk;
+  if (n_tiles == 0) {
+    if (chunk == 0) {
+      S* o = static_cast<S*>(a.out) + static_cast<int64_t>(g) * R * D;
+      for (int i = threadIdx.x; i < R * D; i += NW * kWave) o[i] = from_f32(DT{}, 0.0f);
+    }
+    return;
+  }
+  if (chunk >= n_chunks) return;
+  if (chunk == 0) append_decode_token<S>(a, g, D);
+
+  const S* kg = static_cast<const S*>(a.k) + static_cast<int64_t>(g) * a.entry_stride * D;
+  const S* vg = static_cast<const S*>(a.v) + static_cast<int64_t>(g) * a.entry_stride * D;
+  const int64_t dec_off = static_cast<int64_t>(a.append_position < 0 ? 0 : a.append_position) * D;
+  const S* kdec = a.cur_k != nullptr ? static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D : kg + dec_off;
+  const S* vdec = a.cur_v != nullptr ? static_cast<const S*>(a.cur_v) + static_cast<int64_t>(g) * D : vg + dec_off;
+
+  float m_run[RMAX];
+  float o_acc[RMAX][8];
+  float l_part[4];
+#pragma unroll
+  for (int h = 0; h < RMAX; ++h) {
+    m_run[h] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o_acc[h][i] = 0.0f;
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) l_part[v] = 0.0f;
+
+  for (int it = 0; it < a.iters; ++it) {
+    const int t0 = ((chunk * a.iters + it) * NW + wave) * TW;
+    if (it > 0) load_slots(t0);
+    if (t0 >= n_tiles) break;
+    // ---- round trip 2: K fragments and V rows of the batch ----
+    TileSrc ts[TW];
+    uint4 kf[TW][4];
+    uint4 vf[TW][4];
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+      ts[tt] = tile_src(a, t0 + tt, nu, page[tt], pmask[tt]);
+      const int64_t tb = ts[tt].pos0 * D;
+      const int kr = krow < ts[tt].cnt ? krow : 0;
+      const S* kp = krow == ts[tt].dec ? kdec : kg + tb + kr * D;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[tt][s] = *reinterpret_cast<const uint4*>(kp + 32 * s + 8 * quarter);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * rg + j;
+        const int vr = r < ts[tt].cnt ? r : 0;
+        const S* vp = r == ts[tt].dec ? vdec : vg + tb + vr * D;
+        vf[tt][j] = *reinterpret_cast<const uint4*>(vp + c8);
+      }
+    }
+    // ---- q.k on the matrix cores; scores in log2 units ----
+    float sc[TW][4];
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) H::mfma(qf[s], kf[tt][s], acc);
+      const bool ok = krow < ts[tt].cnt;
+      const uint32_t hm = krow == ts[tt].dec ? 0xffu : ts[tt].hm;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int h = 4 * quarter + v;
+        sc[tt][v] = (ok && h < R && ((hm >> h) & 1u)) ? acc[v] * a.scale_log2 : -INFINITY;
+      }
+    }
+    // ---- batch max per head: over the tiles, then the 16 rows of a quarter ----
+    float mx[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float x = sc[0][v];
+#pragma unroll
+      for (int tt = 1; tt < TW; ++tt) x = fmaxf(x, sc[tt][v]);
+      x = fmaxf(x, dpp<kQuadXor1>(x));
+      x = fmaxf(x, dpp<kQuadXor2>(x));
+      x = fmaxf(x, dpp<kRowHalfMirror>(x));
+      x = fmaxf(x, dpp<kRowMirror>(x));
+      mx[v] = x;
+    }
+    float alpha[RMAX];
+#pragma unroll
+    for (int h = 0; h < RMAX; ++h) {
+      const float bm = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx[h & 3]),
+                                                                           16 * (h >> 2)));
+      const float mnew = fmaxf(m_run[h], bm);
+      alpha[h] = (it == 0 || mnew == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m_run[h] - mnew);
+      m_run[h] = mnew;
+      if (it > 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o_acc[h][i] *= alpha[h];
+      }
+    }
+    // ---- p = exp2(s - m), rounded to the input dtype, into LDS ----
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int h = 4 * quarter + v;
+      const float al = NQ > 1 && quarter == 1 ? alpha[(4 + v) % RMAX] : alpha[v];
+      const float ml = NQ > 1 && quarter == 1 ? m_run[(4 + v) % RMAX] : m_run[v];
+      float psum = 0.0f;
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt) {
+        const float pv = exp2_rel(sc[tt][v], ml);
+        psum += pv;
+        if (quarter < NQ) {
+          S* sp = reinterpret_cast<S*>(&s_p[wave][tt][krow >> 1][h]);
+          sp[krow & 1] = from_f32(DT{}, pv);
+        }
+      }
+      l_part[v] = it == 0 ? psum : l_part[v] * al + psum;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's p stores are done
+    __builtin_amdgcn_wave_barrier();
+    // ---- p.v over row pairs ----
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp) {
+        const uint4 va = vf[tt][2 * jp];
+        const uint4 vb = vf[tt][2 * jp + 1];
+        const uint32_t wa[4] = {va.x, va.y, va.z, va.w};
+        const uint32_t wb[4] = {vb.x, vb.y, vb.z, vb.w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lo[i] = __builtin_amdgcn_perm(wb[i], wa[i], 0x05040100u);  // (row a ch 2i, row b ch 2i)
+          hi[i] = __builtin_amdgcn_perm(wb[i], wa[i], 0x07060302u);  // (row a ch 2i+1, row b ch 2i+1)
+        }
+        uint32_t pp[RMAX];
+#pragma unroll
+        for (int w = 0; w < PW; ++w) {
+          const uint4 t = *reinterpret_cast<const uint4*>(&s_p[wave][tt][2 * rg + jp][4 * w]);
+          pp[4 * w] = t.x;
+          pp[4 * w + 1] = t.y;
+          pp[4 * w + 2] = t.z;
+          pp[4 * w + 3] = t.w;
+        }
+#pragma unroll
+        for (int h = 0; h < RMAX; ++h) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            o_acc[h][2 * i] = H::dot2(pp[h], lo[i], o_acc[h][2 * i]);
+            o_acc[h][2 * i + 1] = H::dot2(pp[h], hi[i], o_acc[h][2 * i + 1]);
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // ---- the wavefront's (m, l, o): o over the 4 row groups, l over 16 rows ----
+#pragma unroll
+  for (int h = 0; h < RMAX; ++h) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float x = o_acc[h][i];
+      x += __shfl_xor(x, 16);
+      x += __shfl_xor(x, 32);
+      o_acc[h][i] = x;
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) l_part[v] = row_group_sum<16>(l_part[v]);
+#pragma unroll
+  for (int h = 0; h < RMAX; ++h) {
+    const float lh = __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_part[h & 3]), 16 * (h >> 2)));
+    if (lane == 0) {
+      s_m[wave][h] = m_run[h];
+      s_l[wave][h] = lh;
+    }
+    if (lane < 16) {
+      *reinterpret_cast<float4*>(&s_o[wave][h][c8]) = make_float4(o_acc[h][0], o_acc[h][1], o_acc[h][2], o_acc[h][3]);
+      *reinterpret_cast<float4*>(&s_o[wave][h][c8 + 4]) =
+          make_float4(o_acc[h][4], o_acc[h][5], o_acc[h][6], o_acc[h][7]);
+    }
+  }
+  __syncthreads();
+  // ---- block combine: the final output (one chunk) or a split-K partial ----
+  const bool final_out = n_chunks == 1;
+  for (int idx = threadIdx.x; idx < R * D; idx += NW * kWave) {
+    const int r = idx / D;
+    const int c = idx - r * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s_m[w][r]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = exp2_rel(s_m[w][r], M);
+      L += f * s_l[w][r];
+      O += f * s_o[w][r][c];
+    }
+    if (final_out) {
+      S* out = static_cast<S*>(a.out) + static_cast<int64_t>(g) * R * D;
+      out[idx] = from_f32(DT{}, L > 0.0f ? O / L : 0.0f);
+    } else {
+      const int64_t pc = static_cast<int64_t>(g) * a.max_chunks + chunk;
+      a.part_o[pc * R * D + idx] = O;
+      if (c == 0) *reinterpret_cast<float2*>(a.part_ml + (pc * R + r) * 2) = make_float2(M, L);
+    }
+  }
+}
+
 // Generic head dimension (any even D <= 512): one row per wavefront step,
 // lane owns channels lane + 64 j.  Correctness path for unusual shapes.
 template <typename DT, int RMAX, int MODE>
@@ -1085,6 +1425,50 @@ void plan_chunks(int dtype, int G, int R, int D, int max_rows_total, int* iters,
   *chunks = ch < 1 ? 1 : ch;
 }
 
+// Page-tile kernel shape: waves per block and tiles per wavefront batch.
+#ifndef TW_TILE_NW
+#define TW_TILE_NW 4
+#endif
+#ifndef TW_TILE_TW
+#define TW_TILE_TW 2
+#endif
+constexpr int kTileNW = TW_TILE_NW;
+constexpr int kTileTW = TW_TILE_TW;
+
+// Batches per block and chunks per group of the page-tile kernel for a bound
+// on the rows (decode token included).  The tile count is bounded by
+// max_rows / 16 + 3 (the sink and the recent run each round up once), and the
+// plan depends on max_rows only, so the workspace query and the launch agree.
+void plan_tile_chunks(int G, int max_rows_total, int* iters, int* chunks) {
+  const int mt = max_rows_total / kTileRows + 3;
+  const int tpb = kTileNW * kTileTW;
+  int target = 1024 / (G > 0 ? G : 1);
+  target = target < 1 ? 1 : (target > kMaxChunks ? kMaxChunks : target);
+  int it = (mt + tpb * target - 1) / (tpb * target);
+  it = it < 1 ? 1 : it;
+  const int ch = (mt + tpb * it - 1) / (tpb * it);
+  *iters = it;
+  *chunks = ch < 1 ? 1 : ch;
+}
+
+template <typename DT>
+int launch_tiles(const AttnArgs& a, hipStream_t stream) {
+  const int phase = a.phase == 0 ? 3 : a.phase;
+  if (phase & 1) {
+    const dim3 grid(a.G * a.max_chunks);
+    if (a.R <= 4)
+      hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW>), grid, dim3(kTileNW * kWave), 0, stream, a);
+    else
+      hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW>), grid, dim3(kTileNW * kWave), 0, stream, a);
+    const int rc = tw_host::check_launch();
+    if (rc != TW_OK) return rc;
+  }
+  if (!(phase & 2) || a.max_chunks <= 1) return TW_OK;
+  hipLaunchKernelGGL((merge_vec_kernel<DT, kModeTiles, kTileD>), dim3(a.G * a.R), dim3(kBlock), 0, stream, a,
+                     kTileNW * kTileTW * a.iters);
+  return tw_host::check_launch();
+}
+
 size_t dyn_lds_bytes(int R, int D) { return static_cast<size_t>(kWaves) * rmax_for(R) * D * sizeof(float); }
 
 template <typename DT, int D, int RMAX, int MODE>
@@ -1182,6 +1566,11 @@ void workspace_layout(int G, int R, int D, int max_rows, size_t* ml_off, size_t*
       plan_chunks(dt, G, R, D, max_rows + extra, &it, &ch);
       chunks_max = ch > chunks_max ? ch : chunks_max;
     }
+  }
+  {
+    int it, ch;
+    plan_tile_chunks(G, max_rows + 1, &it, &ch);
+    chunks_max = ch > chunks_max ? ch : chunks_max;
   }
   const size_t chunks = static_cast<size_t>(chunks_max);
   const size_t ml = static_cast<size_t>(G) * chunks * R * 2 * sizeof(float);
@@ -1330,6 +1719,33 @@ extern "C" int tw_decode_attention_pages_phase(const void* q, const void* k_base
   a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
   a.max_rows = max_rows;
   a.phase = phase;
+  // 16-row pages at D = 128 in a 16-bit dtype take the page-tile kernel
+  // (the sink, recent and decode rows must fit max_rows, as the plan bound
+  // promises); every other shape the row kernels.
+  const int sink_end = sink < length ? sink : length;
+  const int hist_recent = recent - 1 > 0 ? recent - 1 : 0;
+  const int recent_start = length - hist_recent > sink_end ? length - hist_recent : sink_end;
+  const int has_dec = (cur_k != nullptr || append_position >= 0) ? 1 : 0;
+  const int run = (length - recent_start) + has_dec;
+  if (dtype != TW_DTYPE_F32 && D == tw::kTileD && block_size == tw::kTileRows && length <= entry_stride_rows &&
+      max_rows >= sink_end + run) {
+    tw::plan_tile_chunks(G, max_rows, &a.iters, &a.max_chunks);
+    a.t_sink_tiles = (sink_end + tw::kTileRows - 1) / tw::kTileRows;
+    a.t_sink_end = sink_end;
+    a.t_recent_start = recent_start;
+    a.t_n_recent = length - recent_start;
+    a.t_has_dec = has_dec;
+    a.t_run = run;
+    a.t_run_tiles = (run + tw::kTileRows - 1) / tw::kTileRows;
+    const int64_t capacity = static_cast<int64_t>(a.max_chunks) * a.iters * tw::kTileNW * tw::kTileTW;
+    int64_t cap = (max_rows - sink_end - run) / tw::kTileRows;
+    const int64_t room = capacity - a.t_sink_tiles - a.t_run_tiles;
+    cap = cap < room ? cap : room;
+    cap = cap < plan_stride ? cap : plan_stride;
+    a.t_nu_cap = static_cast<int>(cap < 0 ? 0 : cap);
+    return dtype == TW_DTYPE_F16 ? tw::launch_tiles<tw::F16>(a, static_cast<hipStream_t>(stream))
+                                 : tw::launch_tiles<tw::BF16>(a, static_cast<hipStream_t>(stream));
+  }
   tw::plan_chunks(dtype, G, R, D, max_rows, &a.iters, &a.max_chunks);
   return tw::launch_dtype(dtype, a, static_cast<hipStream_t>(stream));
 }
