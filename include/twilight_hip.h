@@ -72,6 +72,23 @@ int tw_build_page_metadata(const void* keys, int64_t key_entry_stride, int n_ent
                            int64_t page_entry_stride, void* packed, void* scale, void* minimum,
                            int64_t quant_entry_stride, void* stream);
 
+/* Decode-time metadata update, one launch for n_entries KV heads, after row
+ * `position` of each entry was written (stream order after the append).
+ * Writes the INT4 code, scale and minimum of row `position` and, when the
+ * row completes page p = (position - sink) / bs (i.e. position >= sink and
+ * (position - sink + 1) % bs == 0), page p's min/max over rows
+ * [sink + p*bs, sink + (p+1)*bs).  Layouts as in tw_build_page_metadata;
+ * the keys may live in HBM or in mapped pinned host memory.  The outputs
+ * equal those of tw_build_page_metadata over position + 1 rows bit for bit.
+ * The reference builds page metadata and INT4 keys at prefill only
+ * (quest_offload_cache.py:528-537, twilight_offload_cache.py:925-936) and
+ * caps the candidate pages at the prompt's (quest_offload_cache.py:342-345);
+ * this entry point lets the selection cover pages completed during decode. */
+int tw_update_page_metadata(const void* keys, int64_t key_entry_stride, int n_entries, int position, int D,
+                            int dtype, int sink, int block_size, void* page_min, void* page_max,
+                            int64_t page_entry_stride, void* packed, void* scale, void* minimum,
+                            int64_t quant_entry_stride, void* stream);
+
 /* affine_int4_dequantize (twilight_offload_cache.py:40-47):
  * out[n][d] = f32(code)*f32(scale[n]) + f32(minimum[n]) (mul, then add). */
 int tw_int4_dequantize(const void* packed, const void* scale, const void* minimum, int dtype,

@@ -219,6 +219,55 @@ def test_quest_decode_layer_fast_path(H, dev, residency):
         assert _same(cache._key_cache[e, :T + 2], model.keys[e]) and _same(cache._value_cache[e, :T + 2], model.vals[e])
 
 
+@pytest.mark.parametrize("residency", ["hbm", "host"])
+def test_quest_decode_metadata_update(H, dev, residency):
+    """update_metadata_on_decode: pages completed during decode are scored
+    and selected.  Decode keys are planted along the queries, so the pages
+    they complete outrank the prompt's; the selection and the attention must
+    match the oracle's over metadata of all rows, and the cache's metadata
+    must equal a rebuild over the slab."""
+    G, R, D, T, sink, recent, bs, steps = 2, 4, 128, 200, 16, 8, 16, 48
+    dtype = "f16"
+    _say(f"[quest metadata update] {residency}")
+    cache = H["quest"].QuestTopKOffloadedCache(num_cache_entries=G, max_cache_len=T + steps, head_dim=D,
+                                               num_query_heads_per_kv=R, dtype=torch.float16, device=dev,
+                                               sink_tokens=sink, recent_tokens=recent, block_size=bs,
+                                               budget_pages=4, kv_residency=residency,
+                                               update_metadata_on_decode=True)
+    model = _Model(G, T, D, dtype, seed=71)
+    model.prefill(cache, dev)
+    g = torch.Generator().manual_seed(72)
+    qdir = torch.randn(G, D, generator=g)
+    qdir = qdir / qdir.norm(dim=1, keepdim=True)
+    new_pages_selected = 0
+    for step in range(steps):
+        L = T + step
+        q = (qdir[:, None, :] * 4 + 0.3 * torch.randn(G, R, D, generator=g)).to(torch.float16)
+        nk = (qdir * 6 + 0.5 * torch.randn(G, D, generator=g)).to(torch.float16)
+        nv = torch.randn(G, D, generator=g).to(torch.float16)
+        out = cache.decode_layer(queries=q.to(dev), key_states=nk.to(dev), value_states=nv.to(dev),
+                                 entries=list(range(G)))
+        ref = np.zeros((G, R, D))
+        for e in range(G):
+            full = _Model.__new__(_Model)
+            full.keys, full.prompt, full.dtype = model.keys, L, dtype
+            pos = _quest_positions(full, e, q[e].float().numpy(), L, sink, recent, bs, budget_pages=4)
+            new_pages_selected += sum(int((p >= T).sum()) for p in pos)
+            for r in range(R):
+                keys = torch.cat([model.keys[e][pos[r]], nk[e][None]]).float().numpy()
+                vals = torch.cat([model.vals[e][pos[r]], nv[e][None]]).float().numpy()
+                ref[e, r] = oracle.decode_attention(q[e, r:r + 1].float().numpy(), keys, vals, 1.0 / math.sqrt(D))[0]
+            model.append(e, nk[e], nv[e])
+        _close(out, ref)
+    assert new_pages_selected > 0, "no page completed during decode was ever selected"
+    torch.cuda.synchronize()
+    pages = (T + steps - sink) // bs
+    for e in range(G):
+        omin, omax, _, _, _ = oracle.build_page_metadata(to_bits(model.keys[e]), dtype, sink, bs, quant=False)
+        assert _same(cache._page_min[e, :pages], torch.from_numpy(omin.view(np.int16)).view(torch.float16))
+        assert _same(cache._page_max[e, :pages], torch.from_numpy(omax.view(np.int16)).view(torch.float16))
+
+
 # --------------------------------------------------------------- Twilight
 def _twilight_expected(model, e, q, length, cache):
     kb = to_bits(model.keys[e][:model.prompt])
@@ -275,6 +324,50 @@ def test_twilight_gqa_group_union(H, dev, residency, dtype, mode):
     torch.cuda.synchronize()
     for e in range(E):
         assert _same(cache._key_cache[e, :T + 2], model.keys[e])
+
+
+def test_twilight_decode_metadata_update(H, dev):
+    """Twilight with update_metadata_on_decode: decode rows get INT4 codes and
+    completed pages get min/max, so the union over pages completed during
+    decode equals the oracle's over metadata of all rows."""
+    G, R, D, T, steps = 2, 4, 128, 300, 40
+    dtype = "bf16"
+    _say("[twilight metadata update]")
+    cache = H["twilight"].TwilightMatchedBudgetOffloadedCache(
+        num_cache_entries=G, max_cache_len=T + steps, head_dim=D, num_query_heads_per_kv=R,
+        dtype=torch.bfloat16, device=dev, kv_residency="hbm", budget_mode="dynamic", sink_tokens=16,
+        recent_tokens=8, block_size=16, candidate_token_budget=64, top_p=0.9, layer_batched_selection=True,
+        gqa_groupwise_execution=True, gpu_compact_gqa_union=True, update_metadata_on_decode=True)
+    model = _Model(G, T, D, dtype, seed=81)
+    model.prefill(cache, dev)
+    g = torch.Generator().manual_seed(82)
+    qdir = torch.randn(G, D, generator=g)
+    qdir = qdir / qdir.norm(dim=1, keepdim=True)
+    entries = list(range(G))
+    late = 0
+    for step in range(steps):
+        L = T + step
+        qs = [(qdir[e] * 4 + 0.3 * torch.randn(R, D, generator=g)).to(torch.bfloat16)[None, :, None] for e in entries]
+        new = [((qdir[e] * 6 + 0.5 * torch.randn(D, generator=g)).to(torch.bfloat16),
+                torch.randn(D, generator=g).to(torch.bfloat16)) for e in entries]
+        cache.prepare_layer_selection(entries=entries, queries=[q.to(dev) for q in qs])
+        K, V, cu, max_k, lengths = cache.update_layer_gqa_group_ragged(
+            key_states=[k[None, None, None].to(dev) for k, _ in new],
+            value_states=[v[None, None, None].to(dev) for _, v in new],
+            queries=[q.to(dev) for q in qs], entries=entries)
+        cu_h = cu.cpu().numpy()
+        for gi, e in enumerate(entries):
+            full = _Model.__new__(_Model)
+            full.keys, full.prompt, full.dtype = model.keys, L, dtype
+            ref = _twilight_expected(full, e, qs[gi][0, :, 0].float().numpy(), L, cache)
+            u = np.asarray(ref["union"])
+            prompt_pages_end = 16 + ((T - 16) // 16) * 16  # rows of pages complete at prefill
+            late += int(((u >= prompt_pages_end) & (u < L - 7)).sum())  # pages completed during decode
+            s0, n = int(cu_h[gi]), len(ref["union"])
+            assert lengths[gi] == n + 1, (step, gi, lengths[gi], n)
+            assert _same(K[s0:s0 + n, 0], model.keys[e][ref["union"]])
+            model.append(e, *new[gi])
+    assert late > 0
 
 
 def test_twilight_per_head_update_and_flat(H, dev):

@@ -73,6 +73,43 @@ def test_page_metadata_bit_exact(K, dev, dtype, T, D, sink, bs):
         assert same_bits(pmax[:P], from_bits(omax, dtype))
 
 
+@pytest.mark.parametrize(
+    "dtype,D,sink,bs,host",
+    [("f16", 128, 64, 16, False), ("bf16", 128, 64, 16, True), ("f32", 64, 5, 7, False), ("bf16", 6, 3, 4, True)],
+)
+def test_update_page_metadata_matches_rebuild(K, dev, dtype, D, sink, bs, host):
+    """Prompt build, then one decode-time update per appended row (crossing
+    several page boundaries) == a rebuild over all rows, bit for bit."""
+    _say(f"[metadata update] {dtype} D={D} sink={sink} bs={bs} host={host}")
+    E = 3
+    T0 = sink + 5 * bs + 3
+    Lmax = T0 + 3 * bs + 2
+    keys = randn((E, Lmax, D), dtype, seed=D + bs)
+    keys[1, T0 + bs, 1] = float("nan")  # a NaN in a page completed during decode
+    keys[2, T0 + 2, :] = 0.25            # a constant decode row
+    kd = keys.to(dev)
+    slab = keys.clone().pin_memory() if host else kd
+    P = (Lmax - sink) // bs
+    pmin = torch.full((E, P, D), 7.0, dtype=keys.dtype, device=dev)
+    pmax = torch.full_like(pmin, 7.0)
+    packed = torch.zeros((E, Lmax, D // 2), dtype=torch.uint8, device=dev)
+    scale = torch.zeros((E, Lmax), dtype=keys.dtype, device=dev)
+    minimum = torch.zeros_like(scale)
+    K.build_page_metadata(kd[:, :T0], sink=sink, block_size=bs, page_min=pmin, page_max=pmax, packed=packed,
+                          scale=scale, minimum=minimum)
+    for pos in range(T0, Lmax):
+        for e0, n in ((0, 1), (1, E - 1)):
+            K.update_page_metadata(slab, first_entry=e0, n_entries=n, position=pos, sink=sink, block_size=bs,
+                                   page_min=pmin, page_max=pmax, packed=packed, scale=scale, minimum=minimum)
+    torch.cuda.synchronize()
+    for e in range(E):
+        omin, omax, opk, osc, omn = oracle.build_page_metadata(to_bits(keys[e]), dtype, sink, bs)
+        assert omin.shape[0] == P
+        assert same_bits(pmin[e], from_bits(omin, dtype)) and same_bits(pmax[e], from_bits(omax, dtype)), e
+        assert np.array_equal(packed[e].cpu().numpy(), opk), e
+        assert same_bits(scale[e], from_bits(osc, dtype)) and same_bits(minimum[e], from_bits(omn, dtype)), e
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
 def test_int4_round_trip_bound(K, dev, dtype):
     """scripts/test_twilight_offload_cache_v1.py:82-89 on the GPU path."""

@@ -176,6 +176,79 @@ __global__ __launch_bounds__(256) void build_metadata_kernel(
   }
 }
 
+// Decode-time update after row `position` of each entry was written: the
+// row's INT4 code and, when the row completes page p = (position - sink) / bs
+// (position - sink + 1 a multiple of bs), that page's min/max over its bs
+// rows.  One wavefront per entry, the same row routine as the prompt build,
+// so the result equals a rebuild over position + 1 rows bit for bit.
+template <typename DT>
+__global__ __launch_bounds__(256) void update_metadata_kernel(
+    const typename DT::storage* __restrict__ keys, int64_t key_entry_stride, int n_entries, int position, int D,
+    int sink, int bs, typename DT::storage* __restrict__ page_min, typename DT::storage* __restrict__ page_max,
+    int64_t page_entry_stride, uint8_t* __restrict__ packed, typename DT::storage* __restrict__ scale,
+    typename DT::storage* __restrict__ minimum, int64_t quant_entry_stride) {
+  using S = typename DT::storage;
+  const int e = blockIdx.x * (blockDim.x / kWave) + static_cast<int>(threadIdx.x) / kWave;
+  if (e >= n_entries) return;
+  const int lane = lane_id();
+  const int nchunk = (D + 127) / 128;
+  const S* kb = keys + static_cast<int64_t>(e) * key_entry_stride;
+  const bool quant = packed != nullptr;
+  const int64_t qrow = static_cast<int64_t>(e) * quant_entry_stride + position;
+  uint8_t* prow = quant ? packed + qrow * (D / 2) : nullptr;
+  S* srow = quant ? scale + qrow : nullptr;
+  S* mrow = quant ? minimum + qrow : nullptr;
+  uint32_t pmin[2 * kMaxPairChunks], pmax[2 * kMaxPairChunks], pnan = 0;
+#pragma unroll
+  for (int i = 0; i < 2 * kMaxPairChunks; ++i) {
+    pmin[i] = 0xffffffffu;
+    pmax[i] = 0u;
+  }
+  const bool completes = page_min != nullptr && position >= sink && (position - sink + 1) % bs == 0;
+  if (!completes) {
+    if (quant)
+      process_row<DT>(kb + static_cast<int64_t>(position) * D, D, nchunk, lane, false, pmin, pmax, pnan, prow,
+                      srow, mrow);
+    return;
+  }
+  const int page = (position - sink) / bs;
+  const int t0 = sink + page * bs;
+  for (int i = 0; i < bs; ++i) {
+    const int t = t0 + i;
+    const bool last = t == position;
+    process_row<DT>(kb + static_cast<int64_t>(t) * D, D, nchunk, lane, true, pmin, pmax, pnan,
+                    last ? prow : nullptr, last ? srow : nullptr, last ? mrow : nullptr);
+  }
+  S* mn_row = page_min + static_cast<int64_t>(e) * page_entry_stride + static_cast<int64_t>(page) * D;
+  S* mx_row = page_max + static_cast<int64_t>(e) * page_entry_stride + static_cast<int64_t>(page) * D;
+#pragma unroll
+  for (int c = 0; c < kMaxPairChunks; ++c) {
+    if (c >= nchunk) break;
+    const int d = 2 * lane + 128 * c;
+    if (d < D) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bool nan = (pnan >> (2 * c + h)) & 1u;
+        mn_row[d + h] = nan ? canonical_nan(DT{}) : from_order_key(DT{}, pmin[2 * c + h]);
+        mx_row[d + h] = nan ? canonical_nan(DT{}) : from_order_key(DT{}, pmax[2 * c + h]);
+      }
+    }
+  }
+}
+
+template <typename DT>
+int launch_update(const void* keys, int64_t key_entry_stride, int n_entries, int position, int D, int sink, int bs,
+                  void* page_min, void* page_max, int64_t page_entry_stride, void* packed, void* scale,
+                  void* minimum, int64_t quant_entry_stride, hipStream_t stream) {
+  using S = typename DT::storage;
+  hipLaunchKernelGGL(update_metadata_kernel<DT>, dim3((n_entries + 3) / 4), dim3(256), 0, stream,
+                     static_cast<const S*>(keys), key_entry_stride, n_entries, position, D, sink, bs,
+                     static_cast<S*>(page_min), static_cast<S*>(page_max), page_entry_stride,
+                     static_cast<uint8_t*>(packed), static_cast<S*>(scale), static_cast<S*>(minimum),
+                     quant_entry_stride);
+  return tw_host::check_launch();
+}
+
 template <typename DT>
 __global__ __launch_bounds__(256) void int4_dequant_kernel(const uint8_t* __restrict__ packed,
                                                            const typename DT::storage* __restrict__ scale,
@@ -252,6 +325,38 @@ extern "C" int tw_build_page_metadata(const void* keys, int64_t key_entry_stride
       return tw::launch_build<tw::F32>(keys, key_entry_stride, n_entries, T, D, sink, block_size, page_min,
                                        page_max, page_entry_stride, packed, scale, minimum,
                                        quant_entry_stride, s);
+    default:
+      return TW_EINVAL;
+  }
+}
+
+extern "C" int tw_update_page_metadata(const void* keys, int64_t key_entry_stride, int n_entries, int position,
+                                       int D, int dtype, int sink, int block_size, void* page_min, void* page_max,
+                                       int64_t page_entry_stride, void* packed, void* scale, void* minimum,
+                                       int64_t quant_entry_stride, void* stream) {
+  if (keys == nullptr || n_entries <= 0 || position < 0 || D <= 0 || (D % 2) != 0 || D > 1024) return TW_EINVAL;
+  if (sink < 0 || block_size <= 0) return TW_EINVAL;
+  if ((page_min == nullptr) != (page_max == nullptr)) return TW_EINVAL;
+  if (!((packed == nullptr) == (scale == nullptr) && (scale == nullptr) == (minimum == nullptr)))
+    return TW_EINVAL;
+  if (n_entries > 1 && key_entry_stride < static_cast<int64_t>(position + 1) * D) return TW_EINVAL;
+  if (packed != nullptr && n_entries > 1 && quant_entry_stride <= position) return TW_EINVAL;
+  if (page_min != nullptr && n_entries > 1 && position >= sink && (position - sink + 1) % block_size == 0 &&
+      page_entry_stride < static_cast<int64_t>((position - sink) / block_size + 1) * D)
+    return TW_EINVAL;
+  if (page_min == nullptr && packed == nullptr) return TW_OK;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TW_DTYPE_F16:
+      return tw::launch_update<tw::F16>(keys, key_entry_stride, n_entries, position, D, sink, block_size, page_min,
+                                        page_max, page_entry_stride, packed, scale, minimum, quant_entry_stride, s);
+    case TW_DTYPE_BF16:
+      return tw::launch_update<tw::BF16>(keys, key_entry_stride, n_entries, position, D, sink, block_size,
+                                         page_min, page_max, page_entry_stride, packed, scale, minimum,
+                                         quant_entry_stride, s);
+    case TW_DTYPE_F32:
+      return tw::launch_update<tw::F32>(keys, key_entry_stride, n_entries, position, D, sink, block_size, page_min,
+                                        page_max, page_entry_stride, packed, scale, minimum, quant_entry_stride, s);
     default:
       return TW_EINVAL;
   }

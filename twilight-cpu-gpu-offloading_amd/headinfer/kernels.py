@@ -137,6 +137,71 @@ def build_page_metadata(
                                            qe, stream_handle(dev)), "build_page_metadata")
 
 
+def update_page_metadata(
+    keys: torch.Tensor,
+    *,
+    first_entry: int,
+    n_entries: int,
+    position: int,
+    sink: int,
+    block_size: int,
+    page_min: Optional[torch.Tensor] = None,
+    page_max: Optional[torch.Tensor] = None,
+    packed: Optional[torch.Tensor] = None,
+    scale: Optional[torch.Tensor] = None,
+    minimum: Optional[torch.Tensor] = None,
+    device: Optional[torch.device] = None,
+) -> None:
+    """Decode-time metadata of entries [first_entry, first_entry + n_entries)
+    after row `position` was written: that row's INT4 code and, when the row
+    completes a page, the page's min/max (equal to a rebuild over
+    position + 1 rows).  keys: the K plane [E, Lmax, D] (HBM or pinned
+    host); page_min/page_max [E, P, D]; packed [E, T, D/2] with scale/minimum
+    [E, T], indexed by entry like keys."""
+    if keys.ndim != 3 or keys.dtype not in _KEY_DTYPES or keys.stride(2) != 1 or keys.stride(1) != keys.shape[2]:
+        raise ValueError("keys must be a row-contiguous [E, Lmax, D] plane")
+    E, Lmax, D = keys.shape
+    if n_entries <= 0 or first_entry < 0 or first_entry + n_entries > E or not 0 <= position < Lmax:
+        raise ValueError("update target outside the cache")
+    pe = qe = 0
+    pmin_p = pmax_p = pk_p = sc_p = mn_p = None
+    e0 = first_entry
+    if page_min is not None:
+        if page_max is None or page_min.shape != page_max.shape or page_min.dtype != keys.dtype \
+                or page_min.ndim != 3 or page_min.shape[0] != E or page_min.shape[2] != D \
+                or page_min.stride(2) != 1 or page_min.stride(1) != D or page_max.stride() != page_min.stride():
+            raise ValueError("page_min/page_max must be row-contiguous [E, P, D] in the key dtype")
+        completes = position >= sink and (position - sink + 1) % block_size == 0
+        if completes and (position - sink) // block_size >= page_min.shape[1]:
+            raise ValueError("page metadata buffers are too small")
+        pe = page_min.stride(0)
+        pmin_p, pmax_p = ptr(page_min[e0]), ptr(page_max[e0])
+    elif page_max is not None:
+        raise ValueError("page_min/page_max go together")
+    if packed is not None:
+        if scale is None or minimum is None or scale.dtype != keys.dtype or minimum.dtype != keys.dtype:
+            raise ValueError("INT4 outputs must be given together in the key dtype")
+        if packed.dtype != torch.uint8 or packed.ndim != 3 or packed.shape[0] != E or packed.shape[2] != D // 2 \
+                or packed.shape[1] <= position or packed.stride(2) != 1 or packed.stride(1) != D // 2 \
+                or packed.stride(0) % (D // 2):
+            raise ValueError("packed must be row-contiguous [E, > position, D/2] uint8")
+        qe = packed.stride(0) // (D // 2)
+        if scale.stride(-1) != 1 or minimum.stride(-1) != 1 or scale.stride(0) != qe or minimum.stride(0) != qe:
+            raise ValueError("scale/minimum must share the packed entry stride")
+        pk_p, sc_p, mn_p = ptr(packed[e0]), ptr(scale[e0]), ptr(minimum[e0])
+    elif scale is not None or minimum is not None:
+        raise ValueError("INT4 outputs must be given together")
+    if pmin_p is None and pk_p is None:
+        return
+    dev = _require_device(page_min, page_max, packed, scale, minimum, what="update_page_metadata")
+    kp = ptr(keys) if keys.is_cuda else host_device_pointer(keys)
+    kp += e0 * keys.stride(0) * keys.element_size()
+    with torch.cuda.device(dev):
+        check(hip().tw_update_page_metadata(kp, keys.stride(0), n_entries, position, D, _dt(keys), sink,
+                                            block_size, pmin_p, pmax_p, pe, pk_p, sc_p, mn_p, qe,
+                                            stream_handle(dev)), "update_page_metadata")
+
+
 def affine_int4_pack(keys: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Per-token affine INT4 (twilight_offload_cache.py:25-37) on the GPU."""
     if keys.ndim != 2 or keys.shape[-1] % 2:

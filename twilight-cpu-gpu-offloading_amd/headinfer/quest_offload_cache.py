@@ -87,6 +87,7 @@ class QuestTopKOffloadedCache(_CacheBase):
         per_head_varlen_attention_reference: bool = False,
         kv_residency: str = "host",
         budget_pages: Optional[int] = None,
+        update_metadata_on_decode: bool = False,
     ) -> None:
         super().__init__()
         device = torch.device(device)
@@ -137,6 +138,11 @@ class QuestTopKOffloadedCache(_CacheBase):
         self.sparse_gather_stabilized = bool(sparse_gather_stabilized)
         self.per_head_varlen_attention_reference = bool(per_head_varlen_attention_reference)
         self.kv_residency = kv_residency
+        # The reference builds page metadata at prefill only and caps the
+        # candidate pages at the prompt's; with this flag every decode append
+        # also writes the new row's metadata (pages completed during decode
+        # become candidates).
+        self.update_metadata_on_decode = bool(update_metadata_on_decode)
 
         self._bookkeeping = SequentialCacheState(num_cache_entries, max_cache_len)
         self._logical_lengths = self._bookkeeping.logical_lengths
@@ -291,6 +297,7 @@ class QuestTopKOffloadedCache(_CacheBase):
             "selection_interval": self.selection_interval,
             "layer_batched_selection": self.layer_batched_selection,
             "layer_flat_ragged_execution": self.layer_flat_ragged_execution,
+            "update_metadata_on_decode": self.update_metadata_on_decode,
             "logical_lengths": list(self._logical_lengths),
             "seen_tokens": self._seen_tokens,
             "prompt_length": self._prompt_length,
@@ -307,12 +314,40 @@ class QuestTopKOffloadedCache(_CacheBase):
         T = int(keys.shape[0])
         pages = (T - self.sink_tokens) // self.block_size if T > self.sink_tokens else 0
         if self._page_min is None:
-            shape = (self.geometry.num_entries, max(pages, 0), self.geometry.head_dim)
+            shape = (self.geometry.num_entries, self._metadata_page_capacity(pages), self.geometry.head_dim)
             self._page_min = torch.empty(shape, dtype=self.dtype, device=self.device)
             self._page_max = torch.empty(shape, dtype=self.dtype, device=self.device)
         if pages:
             kernels.build_page_metadata(keys.contiguous(), sink=self.sink_tokens, block_size=self.block_size,
                                         page_min=self._page_min[entry], page_max=self._page_max[entry])
+
+    def _metadata_page_capacity(self, prompt_pages: int) -> int:
+        if not self.update_metadata_on_decode:
+            return max(prompt_pages, 0)
+        return max(prompt_pages, (self.geometry.max_cache_len - self.sink_tokens) // self.block_size, 0)
+
+    def _update_decode_metadata(self, entries: Sequence[int], position: int) -> None:
+        """Metadata of the decode row `position` just appended to the entries
+        (stream-ordered after the append): the page it completes, if any."""
+        if not self.update_metadata_on_decode or self._page_min is None:
+            return
+        start = self._phase_start()
+        for e0, n in self._runs(entries):
+            kernels.update_page_metadata(self._key_cache, first_entry=e0, n_entries=n, position=position,
+                                         sink=self.sink_tokens, block_size=self.block_size,
+                                         page_min=self._page_min, page_max=self._page_max)
+        self._phase_end("metadata_update", start)
+
+    @staticmethod
+    def _runs(entries: Sequence[int]) -> list[tuple[int, int]]:
+        """Maximal runs of consecutive entries as (first, count)."""
+        runs: list[tuple[int, int]] = []
+        for e in entries:
+            if runs and runs[-1][0] + runs[-1][1] == e:
+                runs[-1] = (runs[-1][0], runs[-1][1] + 1)
+            else:
+                runs.append((e, 1))
+        return runs
 
     def _write_prompt(self, entry: int, key_states: torch.Tensor, value_states: torch.Tensor, start: int,
                       end: int) -> None:
@@ -539,6 +574,7 @@ class QuestTopKOffloadedCache(_CacheBase):
         self._phase_end("new_kv_append", start)
         if self.metrics_enabled:
             self.metrics["new_kv_append_bytes"] += 2 * cur_k.numel() * cur_k.element_size()
+        self._update_decode_metadata(entries, position)
 
     # ------------------------------------------------------ layer-flat ragged
     def _advance_layer(self, entries: Sequence[int], key_states: Sequence[torch.Tensor],
@@ -673,6 +709,7 @@ class QuestTopKOffloadedCache(_CacheBase):
             block_size=self.block_size, length=old_length, append_position=old_length,
             cur_k=key_states.contiguous(), cur_v=value_states.contiguous(), softmax_scale=softmax_scale, out=out)
         self._phase_end("attention", start)
+        self._update_decode_metadata(entries, old_length)
         for e in entries:
             self._last_query_head_lengths[e] = None
         return result

@@ -256,10 +256,12 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         E, D = self.geometry.num_entries, self.geometry.head_dim
         pages = (T - self.sink_tokens) // self.block_size if T > self.sink_tokens else 0
         if self._page_min is None:
-            self._page_min = torch.empty((E, max(pages, 0), D), dtype=self.dtype, device=self.device)
+            rows = max(T, self.geometry.max_cache_len) if self.update_metadata_on_decode else T
+            self._page_min = torch.empty((E, self._metadata_page_capacity(pages), D), dtype=self.dtype,
+                                         device=self.device)
             self._page_max = torch.empty_like(self._page_min)
-            self._packed = torch.empty((E, T, D // 2), dtype=torch.uint8, device=self.device)
-            self._qscale = torch.empty((E, T), dtype=self.dtype, device=self.device)
+            self._packed = torch.empty((E, rows, D // 2), dtype=torch.uint8, device=self.device)
+            self._qscale = torch.empty((E, rows), dtype=self.dtype, device=self.device)
             self._qmin = torch.empty_like(self._qscale)
         assert self._packed is not None and self._qscale is not None and self._qmin is not None
         kernels.build_page_metadata(keys, sink=self.sink_tokens, block_size=self.block_size,
@@ -267,6 +269,18 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
                                     page_max=self._page_max[entry] if pages else None,
                                     packed=self._packed[entry], scale=self._qscale[entry],
                                     minimum=self._qmin[entry])
+
+    def _update_decode_metadata(self, entries: Sequence[int], position: int) -> None:
+        """The decode row's INT4 code and the page it completes, if any."""
+        if not self.update_metadata_on_decode or self._page_min is None:
+            return
+        start = self._phase_start()
+        for e0, n in self._runs(entries):
+            kernels.update_page_metadata(self._key_cache, first_entry=e0, n_entries=n, position=position,
+                                         sink=self.sink_tokens, block_size=self.block_size,
+                                         page_min=self._page_min, page_max=self._page_max, packed=self._packed,
+                                         scale=self._qscale, minimum=self._qmin)
+        self._phase_end("metadata_update", start)
 
     # --------------------------------------------------------------- budgets
     def _twilight_budgets(self, old_length: int) -> tuple[int, int, int, int, int]:
