@@ -1,0 +1,126 @@
+"""mp_headinfer on the GPU: a patched Llama decodes through the offload caches.
+
+With a budget that selects every candidate page (Quest) or keeps every
+candidate (Twilight, top_p 1), the sparse path attends the sink window, every
+whole page before the recent window and the recent window -- all rows but
+the partial page between the last whole page and the recent window
+(quest_offload_cache.py:330-346).  The unpatched model attends the same rows
+through an explicit 4D mask, so the patched model's logits must match its.
+The unpatched model runs on the CPU in float32 with the same bf16-rounded weights (dense attention and its DynamicCache); the patched one
+runs in bf16 on the GPU, so the comparison allows bf16 activation rounding.
+Each decode entry point of the patch is covered: ``decode_layer`` (Quest and
+Twilight), the GQA-group ragged branch, the layer-flat ragged branch and the
+per-entry ``update`` branch.  Prompt and decode follow the reference runner:
+a random prompt, then decode steps with the fixed token id 1
+(run_ruler_partial_h2d_tpot_case_v1.py:1302-1322).
+"""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+T_PROMPT = 600
+DECODE_STEPS = 3
+
+
+def _say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+def _models(dev, seed=0):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    def cfg():
+        return LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=8,
+                           num_key_value_heads=2, head_dim=128, vocab_size=1000, max_position_embeddings=4096,
+                           rope_theta=500000.0)
+
+    torch.manual_seed(seed)
+    ref = LlamaForCausalLM(cfg())
+    with torch.no_grad():
+        for p in ref.parameters():
+            p.copy_(p.to(torch.bfloat16).float())
+    ref.config._attn_implementation = "eager"
+    ref = ref.float().eval()
+    gpu = LlamaForCausalLM(cfg())
+    gpu.load_state_dict(ref.state_dict())
+    gpu = gpu.to(device=dev, dtype=torch.bfloat16).eval()
+    return ref, gpu
+
+
+def _cache(kind, gpu):
+    from headinfer.quest_offload_cache import QuestTopKOffloadedCache
+    from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache
+
+    common = dict(max_cache_len=T_PROMPT + DECODE_STEPS + 2, sink_tokens=64, recent_tokens=256, block_size=16)
+    if kind == "quest":
+        return QuestTopKOffloadedCache.from_llama_model(gpu, kv_residency="hbm", budget_pages=1000, **common)
+    if kind == "quest_host_flat":
+        return QuestTopKOffloadedCache.from_llama_model(gpu, kv_residency="host", budget_pages=1000,
+                                                        layer_batched_selection=True,
+                                                        layer_flat_ragged_execution=True, **common)
+    if kind == "quest_per_entry":
+        return QuestTopKOffloadedCache.from_llama_model(gpu, kv_residency="hbm", budget_pages=1000,
+                                                        per_head_varlen_attention_reference=True, **common)
+    twilight = dict(candidate_token_budget=4096, top_p=1.0, budget_mode="dynamic", **common)
+    if kind == "twilight":
+        return TwilightMatchedBudgetOffloadedCache.from_llama_model(gpu, kv_residency="hbm", **twilight)
+    if kind == "twilight_groupwise":
+        return TwilightMatchedBudgetOffloadedCache.from_llama_model(
+            gpu, kv_residency="host", layer_batched_selection=True, gqa_groupwise_execution=True,
+            gpu_compact_gqa_union=True, **twilight)
+    raise ValueError(kind)
+
+
+def _sparse_mask(length: int, sink: int = 64, recent: int = 256, bs: int = 16) -> torch.Tensor:
+    """Additive [1, 1, 1, length + 1] mask of the decode token's visible rows
+    under a budget covering every candidate page."""
+    sink_end = min(sink, length)
+    recent_start = max(sink_end, length - max(0, recent - 1))
+    cand = (recent_start - sink_end) // bs
+    keep = torch.zeros(length + 1, dtype=torch.bool)
+    keep[:sink_end] = True
+    keep[sink:sink + cand * bs] = True
+    keep[recent_start:] = True
+    mask = torch.zeros((1, 1, 1, length + 1))
+    mask[..., ~keep] = torch.finfo(torch.float32).min
+    return mask
+
+
+def _check(got: torch.Tensor, ref: torch.Tensor, what: str) -> None:
+    got = got.float().cpu()
+    err = (got - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    assert err <= 0.03 * scale + 1e-3, f"{what}: max abs err {err:.4f} vs logit scale {scale:.4f}"
+
+
+@pytest.mark.parametrize("kind", ["quest", "quest_host_flat", "quest_per_entry", "twilight", "twilight_groupwise"])
+def test_patched_llama_matches_dense(dev, kind):
+    from headinfer import mp
+
+    _say(f"[model] {kind}")
+    ref, gpu = _models(dev)
+    mp.mp_headinfer(gpu)
+    cache = _cache(kind, gpu)
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, 1000, (1, T_PROMPT), generator=g)
+    with torch.no_grad():
+        out = gpu(input_ids=ids.to(dev), past_key_values=cache, use_cache=True, logits_to_keep=1)
+        r = ref(input_ids=ids, use_cache=True, logits_to_keep=1)
+        _check(out.logits[0, -1], r.logits[0, -1], "prefill")
+        past = r.past_key_values
+        tok = torch.ones((1, 1), dtype=torch.long)
+        for step in range(DECODE_STEPS):
+            out = gpu(input_ids=tok.to(dev), past_key_values=cache, use_cache=True)
+            r = ref(input_ids=tok, past_key_values=past, use_cache=True,
+                    attention_mask=_sparse_mask(T_PROMPT + step))
+            past = r.past_key_values
+            _check(out.logits[0, -1], r.logits[0, -1], f"decode step {step}")
+    torch.cuda.synchronize()
+    assert cache.get_seq_length() == T_PROMPT + DECODE_STEPS

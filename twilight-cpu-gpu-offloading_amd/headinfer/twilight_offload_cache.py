@@ -423,6 +423,45 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
             self.metrics["gather_bytes"] += 2 * (total - G) * D * cur_k.element_size()
         return self._flat_union_keys[:total], self._flat_union_values[:total], cu, max(lengths), lengths
 
+    # ------------------------------------------------------------ fast path
+    def decode_layer(self, *, queries: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
+                     entries: Sequence[int], softmax_scale: Optional[float] = None,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One decoder layer's Twilight decode with no host sync: both
+        selection stages and the GQA union on the device (Quest B0, INT4 QK,
+        top-p, union rows), then the split-K attention reading the union rows
+        and the decode token straight from the slab, then the append.
+
+        queries [G, R, D] in the cache dtype; key_states/value_states [G, D];
+        entries consecutive.  Returns [G, R, D]."""
+        G, R, D = queries.shape
+        if R != self.num_query_heads_per_kv or D != self.geometry.head_dim or len(entries) != G:
+            raise ValueError("queries must be [len(entries), num_query_heads_per_kv, head_dim]")
+        if key_states.shape != (G, D) or value_states.shape != (G, D):
+            raise ValueError("key_states/value_states must be [G, head_dim]")
+        if not self._consecutive(entries):
+            raise ValueError("decode_layer needs the consecutive entries of one layer")
+        for e in entries:
+            self._bookkeeping.advance(e, 1)
+            self._initialized[e] = True
+        self._seen_tokens = self._bookkeeping.seen_tokens
+        old_length = self._logical_lengths[entries[0]] - 1
+        self._wait_host_writes(entries)
+        state = self._select_layer(entries, queries.float().contiguous(), old_length)
+        self._trace_layer(state)
+        e0 = entries[0]
+        cur_k, cur_v = key_states.contiguous(), value_states.contiguous()
+        start = self._phase_start()
+        result = kernels.decode_attention_rows(queries.contiguous(), self._key_cache[e0:e0 + G],
+                                               self._value_cache[e0:e0 + G], state["rows"], state["counts"],
+                                               state["max_count"], cur_k=cur_k, cur_v=cur_v,
+                                               softmax_scale=softmax_scale, out=out)
+        self._phase_end("attention", start)
+        self._append(entries, cur_k, cur_v, old_length)
+        for e in entries:
+            self._last_query_head_lengths[e] = None
+        return result
+
     # ----------------------------------------------------- per-head selection
     def _head_positions(self, state: dict, g: int) -> list[torch.Tensor]:
         """Each head's own selected positions (sink ++ kept candidates ++
