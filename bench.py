@@ -50,9 +50,13 @@ def parse_args(argv=None):
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--workload", choices=("quest32k", "twilight32k", "offload64k"), default="quest32k",
+    ap.add_argument("--workload", choices=("quest32k", "twilight32k", "offload64k", "tpot32k"), default="quest32k",
                     help="quest32k (default): 32K layer, KV in HBM; twilight32k: INT4 QK + top-p at 32K; "
-                         "offload64k: 64K layer with KV in pinned host memory (zero-copy vs DMA)")
+                         "offload64k: 64K layer with KV in pinned host memory (zero-copy vs DMA); "
+                         "tpot32k: end-to-end p50 TPOT of a Llama-3-8B-shaped model at 32K context")
+    ap.add_argument("--decode-tokens", type=int, default=32, help="decode tokens per TPOT run (D1..Dn)")
+    ap.add_argument("--kv-residency", choices=("hbm", "host"), default="hbm",
+                    help="tpot32k: KV slab in HBM or in pinned host memory (read zero-copy)")
     ap.add_argument("--context", type=int, default=None, help="context length (workload default if omitted)")
     ap.add_argument("--budget-mode", choices=("dynamic", "matched"), default="dynamic",
                     help="Twilight budgets (twilight32k)")
@@ -482,6 +486,8 @@ def main(argv=None) -> int:
         return run_twilight(args, dev)
     if args.workload == "offload64k":
         return run_offload(args, dev)
+    if args.workload == "tpot32k":
+        return run_tpot(args, dev)
     args.context = args.context or 32768
     print(f"[bench] building inputs: layers={args.layers} context={args.context}", file=sys.stderr, flush=True)
     w = QuestWorkload(dev, args.layers, args.context, args.budget_pages)
@@ -531,7 +537,7 @@ def main(argv=None) -> int:
                          "GBps": round(by["select"] / t_sel / 1e9, 1)},
         "decode_attention": {"us": round(t_att1 * 1e6, 2), "bytes": int(by["attention"]),
                              "GBps": round(by["attention"] / t_att1 / 1e9, 1),
-                             "kernel": "decode_attn_mfma (split-K, fused decode-token append)"},
+                             "kernel": "decode_attn_tiles (split-K, fused decode-token append)"},
         "attention_merge": {"us": round((t_att - t_att1) * 1e6, 2), "kernel": "merge_vec_kernel"},
     }
     # the split-K attention is the longest single kernel of the layer (the
@@ -777,8 +783,96 @@ def run_offload(args, dev) -> int:
 
 # rocprofv3 FETCH_SIZE / WRITE_SIZE of each kernel, calibrated against a copy
 # of known size and recorded with the commands that produced them.
+def llama3_8b_config(layers: int = 32):
+    """Llama-3-8B shape: hidden 4096, FFN 14336, 32 query / 8 KV heads of 128,
+    vocab 128256, RoPE theta 500000."""
+    from transformers import LlamaConfig
+
+    return LlamaConfig(hidden_size=4096, intermediate_size=14336, num_hidden_layers=layers, num_attention_heads=32,
+                       num_key_value_heads=8, head_dim=128, vocab_size=128256, max_position_embeddings=131072,
+                       rope_theta=500000.0, rms_norm_eps=1e-5, tie_word_embeddings=False)
+
+
+def tpot_run(model, ids, dev, cache, decode_tokens: int) -> dict:
+    """Prefill `ids` into `cache` through the patched model, then decode
+    `decode_tokens` tokens of the fixed id 1; per-token synchronized wall time,
+    p50 and mean over D2..Dn (run_ruler_partial_h2d_tpot_case_v1.py:1302-1322,
+    1897-1906)."""
+    import torch
+
+    with torch.no_grad():
+        t0 = time.perf_counter()
+        model(input_ids=ids.to(dev), past_key_values=cache, use_cache=True, logits_to_keep=1)
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        tok = torch.ones((1, 1), dtype=torch.long, device=dev)
+        times = []
+        for _ in range(decode_tokens):
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            model(input_ids=tok, past_key_values=cache, use_cache=True)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t1)
+    steady = sorted(times[1:]) if len(times) > 1 else times
+    return {"tpot_p50_ms": round(steady[len(steady) // 2] * 1e3, 3),
+            "tpot_mean_ms": round(sum(steady) / len(steady) * 1e3, 3),
+            "d1_ms": round(times[0] * 1e3, 3), "prefill_s": round(prefill_s, 2), "decode_tokens": len(times)}
+
+
+def run_tpot(args, dev) -> int:
+    """End-to-end decode TPOT at 32K context: a Llama-3-8B-shaped model with
+    random-init bf16 weights, patched by mp_headinfer, KV in HBM through the
+    Quest cache (budget 128 pages = 2048 tokens per query head, sink 64,
+    recent 256, page 16).  A random 32K-token prompt is prefilled (dense
+    causal attention), then tokens of the fixed id 1 are decoded; TPOT is the
+    synchronized wall time per token, p50 over D2..Dn.  The same harness with
+    a budget covering every page is the dense-attention comparison."""
+    import torch
+
+    from headinfer import mp
+    from headinfer.quest_offload_cache import QuestTopKOffloadedCache
+    from transformers import LlamaForCausalLM
+
+    ctx = args.context or 32768
+    n_dec = max(2, args.decode_tokens)
+    residency = args.kv_residency
+    cfg = llama3_8b_config(args.layers)
+    print(f"[bench] tpot: Llama-3-8B-shaped x{args.layers} layers, random init, context {ctx}", file=sys.stderr,
+          flush=True)
+    torch.manual_seed(4)
+    with torch.device(dev):
+        model = LlamaForCausalLM._from_config(cfg, dtype=torch.bfloat16)
+    model.eval()
+    mp.mp_headinfer(model)
+    ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(5))
+    runs = {}
+    for label, pages in (("sparse", args.budget_pages), ("dense", 1 << 20)):
+        print(f"[bench] tpot {label}: prefill + {n_dec} decode tokens", file=sys.stderr, flush=True)
+        cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + n_dec + 8,
+                                                         kv_residency=residency, budget_pages=pages)
+        runs[label] = tpot_run(model, ids, dev, cache, n_dec)
+        del cache
+        torch.cuda.empty_cache()
+    sp = runs["sparse"]
+    result = {
+        "metric": METRIC, "value": sp["tpot_p50_ms"], "unit": "ms/token (p50 TPOT)", "n_gpus": 1,
+        "steps": n_dec, "warmup": 1, "ms_per_step": sp["tpot_p50_ms"], "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: random-init weights, random prompt ids, fixed decode token id 1",
+        "config": {"workload": f"tpot-{ctx // 1024}k-{residency}: Llama-3-8B-shaped decode (HF LlamaForCausalLM "
+                               "patched by mp_headinfer), Quest sparse attention, KV in "
+                               + ("HBM" if residency == "hbm" else "pinned host memory read zero-copy"),
+                   "layers": args.layers, "context": ctx, "kv_heads": 8, "q_per_kv": 4, "head_dim": 128,
+                   "page_size": 16, "budget_pages": args.budget_pages, "sink": 64, "recent": 256},
+        "tpot": runs,
+        "sparse_vs_dense_speedup": round(runs["dense"]["tpot_p50_ms"] / sp["tpot_p50_ms"], 3),
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 TRAFFIC_PROFILE = ROOT / "profiles" / "pmc_traffic_quest32k.md"
-TRAFFIC_KERNEL = {"decode_attention": "decode_attn", "quest_select": "quest_score_kernel"}
+TRAFFIC_KERNEL = {"decode_attention": "decode_attn_tiles", "quest_select": "quest_score_kernel"}
 
 
 def measured_traffic(kernel: str):
