@@ -89,6 +89,15 @@ int tw_update_page_metadata(const void* keys, int64_t key_entry_stride, int n_en
                             int64_t page_entry_stride, void* packed, void* scale, void* minimum,
                             int64_t quant_entry_stride, void* stream);
 
+/* Ragged tw_update_page_metadata: entry e's new row is positions[e] (int32,
+ * device).  Rows beyond max_position and pages at or beyond max_pages are
+ * skipped (the buffers' capacity), as are negative positions.  Otherwise the
+ * same outputs as tw_update_page_metadata entry by entry. */
+int tw_update_page_metadata_ragged(const void* keys, int64_t key_entry_stride, int n_entries, const int32_t* positions,
+                                   int max_position, int D, int dtype, int sink, int block_size, void* page_min,
+                                   void* page_max, int max_pages, int64_t page_entry_stride, void* packed,
+                                   void* scale, void* minimum, int64_t quant_entry_stride, void* stream);
+
 /* affine_int4_dequantize (twilight_offload_cache.py:40-47):
  * out[n][d] = f32(code)*f32(scale[n]) + f32(minimum[n]) (mul, then add). */
 int tw_int4_dequantize(const void* packed, const void* scale, const void* minimum, int dtype,
@@ -150,6 +159,24 @@ int tw_quest_select(const float* q, const void* page_min, const void* page_max, 
                     int64_t plan_stride, int32_t* rows, uint8_t* row_masks, int32_t* row_counts,
                     int64_t rows_stride, int sink, int recent, int block_size, int length,
                     int append_position, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Ragged groups: tw_quest_select's score, top-k and union plan for G groups
+ * of different lengths in one launch pair (e.g. the KV heads of several
+ * requests at one layer).  lengths [G] (int32, device) gives each group's
+ * tokens L_g; group g scores its candidate pages P_g = min(P_max,
+ * (recent_start_g - sink_end_g) / block_size) with the window of
+ * tw_quest_select, keeps k_g = min(k, P_g) pages per head (sel_pages slots
+ * k_g .. k-1 get -1) and writes the union plan of those.  Nothing depends on
+ * a host-side length, so a captured graph replays it as lengths advance.
+ * Same orders, ties and workspace (tw_quest_select_workspace_size(G, R,
+ * P_max)) as tw_quest_select; no row plan.  The reference is batch-1
+ * (slab_cache.py:5, quest_offload_cache.py:520-521); this batches its
+ * prepare_layer_selection (quest_offload_cache.py:299-401) over requests. */
+int tw_quest_select_ragged(const float* q, const void* page_min, const void* page_max, int dtype, int G, int R,
+                           int P_max, int D, int64_t page_group_stride, const int32_t* lengths, int k,
+                           int32_t* sel_pages, int32_t* plan_pages, uint8_t* plan_masks, int32_t* plan_counts,
+                           int64_t plan_stride, int sink, int recent, int block_size, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Twilight stage 2, INT4 QK estimate over the B0 candidates of every head.
@@ -275,6 +302,24 @@ int tw_decode_attention_pages_phase(const void* q, const void* k_base, const voi
                                     int64_t entry_stride_rows, int sink, int recent, int block_size, int length,
                                     int append_position, const void* cur_k, const void* cur_v, float softmax_scale,
                                     void* out, void* workspace, size_t workspace_bytes, int phase, void* stream);
+/* Ragged tw_decode_attention_pages: group g attends with the window of its
+ * own length lengths[g] (int32, device) -- [0, sink_end) ++ its union pages
+ * ++ [recent_start, L_g) ++ the decode token, which is cur_k/cur_v[g] (also
+ * written to row L_g of the entry when append != 0) or, without cur_k, the
+ * cache row L_g (append != 0) or none (append == 0).  16-bit K/V, D = 128,
+ * block_size = 16 (the page-tile kernel).  max_rows >= sink + recent bounds
+ * every group's rows with its union pages (plan pages beyond it are not
+ * attended); lengths[g] must be below entry_stride_rows (larger values are
+ * clamped).  Workspace as tw_decode_attention_workspace_size(G, R, D,
+ * max_rows).  Batches the reference's batch-1 GQA decode attention
+ * (mp.py:239-279) over requests. */
+int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
+                                     int D, const int32_t* plan_pages, const uint8_t* plan_masks,
+                                     const int32_t* plan_counts, int64_t plan_stride, int max_rows,
+                                     int64_t entry_stride_rows, int sink, int recent, int block_size,
+                                     const int32_t* lengths, int append, const void* cur_k, const void* cur_v,
+                                     float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
+                                     void* stream);
 int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G,
                         int R, int D, const int32_t* rows, const uint8_t* row_masks,
                         const int32_t* row_counts, int64_t rows_stride, int64_t entry_stride_rows,

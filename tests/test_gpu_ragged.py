@@ -1,0 +1,261 @@
+"""GPU parity of the ragged (multi-request) entry points.
+
+Groups of one launch have different lengths, read from a device array:
+quest_select_ragged must equal quest_select run group by group with each
+group's own length (bit-exact page ids and union plan), the ragged page-tile
+attention must match float64 attention over each group's own window, and the
+ragged metadata update must equal a rebuild.  A decode step made of these
+launches plus the device-side length increment is captured in a HIP graph
+and every replay is checked against the same step run eagerly.
+"""
+
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import from_bits, randn, same_bits, to_bits
+
+pytestmark = pytest.mark.gpu
+
+SINK, RECENT, BS, D = 64, 256, 16, 128
+
+
+def _say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def K():
+    from headinfer import kernels
+
+    return kernels
+
+
+def _metadata(keys, lengths, dtype, dev):
+    """Page min/max [G, P_max, D] of each group's complete pages over its own rows."""
+    G, Lmax, _ = keys.shape
+    P_max = (Lmax - SINK) // BS
+    pmin = torch.zeros((G, P_max, D), dtype=keys.dtype)
+    pmax = torch.zeros_like(pmin)
+    for g in range(G):
+        kb = to_bits(keys[g, :lengths[g]])
+        omin, omax, _, _, _ = oracle.build_page_metadata(kb, dtype, SINK, BS, quant=False)
+        if omin.shape[0]:
+            pmin[g, :omin.shape[0]] = from_bits(omin, dtype)
+            pmax[g, :omax.shape[0]] = from_bits(omax, dtype)
+    return pmin.to(dev), pmax.to(dev)
+
+
+def _cand(L):
+    sink_end, recent_start, eligible = oracle.selection_window(L, SINK, RECENT)
+    return eligible // BS
+
+
+LENGTHS = [40, 400, 1000, 5000, 20000, 33000]
+
+
+@pytest.mark.parametrize("dtype,R", [("bf16", 7), ("f16", 4)])
+def test_quest_select_ragged_matches_per_group(K, dev, dtype, R):
+    _say(f"[ragged select] {dtype} R={R}")
+    G, k = len(LENGTHS), 128
+    Lmax = max(LENGTHS) + 16
+    keys = randn((G, Lmax, D), dtype, seed=91)
+    q = randn((G, R, D), "f32", seed=92)
+    pmin, pmax = _metadata(keys, LENGTHS, dtype, dev)
+    P_max = pmin.shape[1]
+    lengths = torch.tensor(LENGTHS, dtype=torch.int32, device=dev)
+    width = min(P_max, R * k)
+    sel = torch.empty((G, R, k), dtype=torch.int32, device=dev)
+    pp = torch.empty((G, width), dtype=torch.int32, device=dev)
+    pm = torch.empty((G, width), dtype=torch.uint8, device=dev)
+    pc = torch.empty((G,), dtype=torch.int32, device=dev)
+    qd = q.to(dev)
+    K.quest_select_ragged(qd, pmin, pmax, lengths, k, sink=SINK, recent=RECENT, block_size=BS, sel_pages=sel,
+                          plan_pages=pp, plan_masks=pm, plan_counts=pc)
+    torch.cuda.synchronize()
+    for g, L in enumerate(LENGTHS):
+        P = _cand(L)
+        kg = min(k, P)
+        assert bool((sel[g, :, kg:] == -1).all()), g
+        if P == 0:
+            assert int(pc[g]) == 0
+            continue
+        w = min(P, R * kg)
+        s1 = torch.empty((1, R, kg), dtype=torch.int32, device=dev)
+        p1 = torch.empty((1, w), dtype=torch.int32, device=dev)
+        m1 = torch.empty((1, w), dtype=torch.uint8, device=dev)
+        c1 = torch.empty((1,), dtype=torch.int32, device=dev)
+        K.quest_select(qd[g:g + 1].contiguous(), pmin[g:g + 1, :P], pmax[g:g + 1, :P], kg, sel_pages=s1,
+                       plan_pages=p1, plan_masks=m1, plan_counts=c1)
+        torch.cuda.synchronize()
+        n = int(c1[0])
+        assert int(pc[g]) == n, g
+        assert torch.equal(sel[g, :, :kg].cpu(), s1[0].cpu()), g
+        assert torch.equal(pp[g, :n].cpu(), p1[0, :n].cpu()) and torch.equal(pm[g, :n].cpu(), m1[0, :n].cpu()), g
+
+
+def _rows(L, pages, masks, R, decode):
+    sink_end, recent_start, _ = oracle.selection_window(L, SINK, RECENT)
+    pg = pages.long()
+    rows = torch.cat([torch.arange(sink_end), (SINK + pg[:, None] * BS + torch.arange(BS)).reshape(-1),
+                      torch.arange(recent_start, L)])
+    all_heads = (1 << R) - 1
+    m = np.concatenate([np.full(sink_end, all_heads), masks.long().repeat_interleave(BS).numpy(),
+                        np.full(L - recent_start, all_heads)])
+    if decode != "none":
+        m = np.concatenate([m, [all_heads]])
+    return rows, m.astype(np.uint8)
+
+
+@pytest.mark.parametrize("decode", ["cur_append", "cache_row", "none"])
+@pytest.mark.parametrize("dtype,R", [("bf16", 7), ("f16", 4)])
+def test_decode_attention_pages_ragged(K, dev, dtype, R, decode):
+    _say(f"[ragged attention] {dtype} R={R} decode={decode}")
+    G, k = len(LENGTHS), 128
+    Lmax = max(LENGTHS) + 16
+    keys = randn((G, Lmax, D), dtype, seed=93)
+    vals = randn((G, Lmax, D), dtype, seed=94)
+    q = randn((G, R, D), dtype, seed=95)
+    ck, cv = randn((G, D), dtype, seed=96), randn((G, D), dtype, seed=97)
+    pmin, pmax = _metadata(keys, LENGTHS, dtype, dev)
+    lengths = torch.tensor(LENGTHS, dtype=torch.int32, device=dev)
+    width = min(pmin.shape[1], R * k)
+    pp = torch.empty((G, width), dtype=torch.int32, device=dev)
+    pm = torch.empty((G, width), dtype=torch.uint8, device=dev)
+    pc = torch.empty((G,), dtype=torch.int32, device=dev)
+    K.quest_select_ragged(q.float().to(dev), pmin, pmax, lengths, k, sink=SINK, recent=RECENT, block_size=BS,
+                          plan_pages=pp, plan_masks=pm, plan_counts=pc)
+    kd, vd = keys.to(dev), vals.to(dev)
+    kw = dict(plan_masks=pm, max_pages=width, sink=SINK, recent=RECENT, block_size=BS)
+    if decode == "cur_append":
+        kw.update(append=True, cur_k=ck.to(dev), cur_v=cv.to(dev))
+    else:
+        kw.update(append=decode == "cache_row")
+    out = K.decode_attention_pages_ragged(q.to(dev), kd, vd, pp, pc, lengths, **kw)
+    torch.cuda.synchronize()
+    ref = np.zeros((G, R, D))
+    for g, L in enumerate(LENGTHS):
+        n = int(pc[g])
+        rows, m = _rows(L, pp[g, :n].cpu(), pm[g, :n].cpu(), R, decode)
+        kk, vv = keys[g, rows], vals[g, rows]
+        if decode == "cur_append":
+            kk, vv = torch.cat([kk, ck[g:g + 1]]), torch.cat([vv, cv[g:g + 1]])
+            assert same_bits(kd[g, L], ck[g]) and same_bits(vd[g, L], cv[g]), g
+        elif decode == "cache_row":
+            kk, vv = torch.cat([kk, keys[g, L:L + 1]]), torch.cat([vv, vals[g, L:L + 1]])
+        ref[g] = oracle.decode_attention(q[g].float().numpy(), kk.float().numpy(), vv.float().numpy(),
+                                         1.0 / math.sqrt(D), m)
+    if decode != "cur_append":
+        assert same_bits(kd, keys.to(dev)) and same_bits(vd, vals.to(dev))
+    got = out.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref)
+    assert np.all(err <= 2e-3 + 1e-2 * np.abs(ref)), f"max abs err {err.max():.3e}"
+
+
+def test_update_page_metadata_ragged(K, dev):
+    _say("[ragged metadata update]")
+    dtype = "bf16"
+    E, Lmax = 4, 400
+    keys = randn((E, Lmax, D), dtype, seed=98)
+    starts = [100, 143, 200, 300]
+    kd = keys.to(dev)
+    P = (Lmax - SINK) // BS
+    pmin = torch.zeros((E, P, D), dtype=keys.dtype, device=dev)
+    pmax = torch.zeros_like(pmin)
+    packed = torch.zeros((E, Lmax, D // 2), dtype=torch.uint8, device=dev)
+    scale = torch.zeros((E, Lmax), dtype=keys.dtype, device=dev)
+    minimum = torch.zeros_like(scale)
+    for e, T in enumerate(starts):
+        K.build_page_metadata(kd[e, :T], sink=SINK, block_size=BS, page_min=pmin[e], page_max=pmax[e],
+                              packed=packed[e], scale=scale[e], minimum=minimum[e])
+    pos = torch.tensor(starts, dtype=torch.int32, device=dev)
+    steps = 40
+    for _ in range(steps):
+        K.update_page_metadata_ragged(kd, pos, first_entry=0, sink=SINK, block_size=BS, page_min=pmin,
+                                      page_max=pmax, packed=packed, scale=scale, minimum=minimum)
+        pos += 1
+    # a row beyond the buffers is skipped, not written
+    K.update_page_metadata_ragged(kd, torch.tensor([-1, Lmax, Lmax + 5, -7], dtype=torch.int32, device=dev),
+                                  first_entry=0, sink=SINK, block_size=BS, page_min=pmin, page_max=pmax,
+                                  packed=packed, scale=scale, minimum=minimum)
+    torch.cuda.synchronize()
+    for e, T in enumerate(starts):
+        n = T + steps
+        omin, omax, opk, osc, omn = oracle.build_page_metadata(to_bits(keys[e, :n]), dtype, SINK, BS)
+        p = omin.shape[0]
+        assert same_bits(pmin[e, :p], from_bits(omin, dtype)) and same_bits(pmax[e, :p], from_bits(omax, dtype)), e
+        assert bool((pmin[e, p:] == 0).all()), e
+        assert np.array_equal(packed[e, :n].cpu().numpy(), opk), e
+        assert same_bits(scale[e, :n], from_bits(osc, dtype)) and same_bits(minimum[e, :n], from_bits(omn, dtype))
+        assert bool((packed[e, n:] == 0).all()), e
+
+
+def test_ragged_step_graph_replays_match_eager(K, dev):
+    """select + attention (append) + metadata update + length increment,
+    captured once and replayed; each replay == the eager step, bit for bit."""
+    _say("[ragged graph]")
+    dtype, R, k = "bf16", 7, 32
+    lengths0 = [700, 1500, 2222, 3001]
+    G = len(lengths0)
+    steps = 5
+    Lmax = max(lengths0) + steps + 16
+    keys = randn((G, Lmax, D), dtype, seed=101)
+    vals = randn((G, Lmax, D), dtype, seed=102)
+    q = randn((G, R, D), dtype, seed=103)
+    ck, cv = randn((G, D), dtype, seed=104), randn((G, D), dtype, seed=105)
+    P_cap = (Lmax - SINK) // BS
+
+    def state():
+        pmin, pmax = _metadata(keys, lengths0, dtype, dev)
+        st = {"k": keys.to(dev), "v": vals.to(dev), "pmin": pmin, "pmax": pmax,
+              "len": torch.tensor(lengths0, dtype=torch.int32, device=dev),
+              "pp": torch.zeros((G, min(P_cap, R * k)), dtype=torch.int32, device=dev),
+              "pm": torch.zeros((G, min(P_cap, R * k)), dtype=torch.uint8, device=dev),
+              "pc": torch.zeros((G,), dtype=torch.int32, device=dev),
+              "out": torch.zeros((G, R, D), dtype=q.dtype, device=dev),
+              "q": q.to(dev), "qf": q.float().to(dev), "ck": ck.to(dev), "cv": cv.to(dev)}
+        return st
+
+    def step(st):
+        K.quest_select_ragged(st["qf"], st["pmin"], st["pmax"], st["len"], k, sink=SINK, recent=RECENT,
+                              block_size=BS, plan_pages=st["pp"], plan_masks=st["pm"], plan_counts=st["pc"])
+        K.decode_attention_pages_ragged(st["q"], st["k"], st["v"], st["pp"], st["pc"], st["len"],
+                                        plan_masks=st["pm"], max_pages=st["pp"].shape[1], sink=SINK, recent=RECENT,
+                                        block_size=BS, append=True, cur_k=st["ck"], cur_v=st["cv"], out=st["out"])
+        K.update_page_metadata_ragged(st["k"], st["len"], first_entry=0, sink=SINK, block_size=BS,
+                                      page_min=st["pmin"], page_max=st["pmax"])
+        st["len"].add_(1)
+
+    eager, graphed = state(), state()
+    step(graphed)  # warm-up (workspaces) outside the capture, then restore the graphed state
+    torch.cuda.synchronize()
+    ref_state = state()
+    for name in ("k", "v", "pmin", "pmax", "len"):
+        graphed[name].copy_(ref_state[name])
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step(graphed)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    # capture recorded but did not run the step: the graphed state is still at step 0
+    assert torch.equal(graphed["len"].cpu(), eager["len"].cpu())
+    for i in range(steps):
+        step(eager)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(graphed["len"].cpu(), eager["len"].cpu()), i
+        assert torch.equal(graphed["pc"].cpu(), eager["pc"].cpu()), i
+        assert same_bits(graphed["out"], eager["out"]), i
+        assert same_bits(graphed["k"], eager["k"]) and same_bits(graphed["pmin"], eager["pmin"]), i

@@ -86,6 +86,12 @@ struct AttnArgs {
   int t_run;                // t_n_recent + t_has_dec
   int t_run_tiles;          // ceil(t_run / 16)
   int t_nu_cap;             // union pages the launch covers at most
+  int t_per_chunk;          // tiles per chunk (waves x tiles per batch x batches)
+  // Ragged page-tile launches (nullable): group g has lengths[g] tokens, its
+  // window follows from it and the decode token is its row lengths[g]
+  // (appended there when ragged_append is set).
+  const int32_t* lengths;
+  int ragged_append;
 };
 
 // 8 consecutive channels of one row.
@@ -213,19 +219,61 @@ __device__ __forceinline__ GroupRows group_rows(const AttnArgs& a, int g, int D)
 
 // Page-tile mode (decode_attn_tiles): chunks count 16-row tiles.
 constexpr int kModeTiles = 3;
+constexpr int kTileRows = 16;
+
+// Window of group g in a page-tile launch: the host's (one length for every
+// group) or, for ragged launches, derived from lengths[g] the same way.
+struct TileWin {
+  int sink_tiles, sink_end, recent_start, n_recent, has_dec, run, run_tiles, nu_cap;
+  int append_position;  // the decode token's cache row, -1: none
+};
+
+__device__ __forceinline__ TileWin tile_window(const AttnArgs& a, int g) {
+  TileWin w;
+  if (a.lengths == nullptr) {
+    w.sink_tiles = a.t_sink_tiles;
+    w.sink_end = a.t_sink_end;
+    w.recent_start = a.t_recent_start;
+    w.n_recent = a.t_n_recent;
+    w.has_dec = a.t_has_dec;
+    w.run = a.t_run;
+    w.run_tiles = a.t_run_tiles;
+    w.nu_cap = a.t_nu_cap;
+    w.append_position = a.append_position;
+    return w;
+  }
+  const int lmax = static_cast<int>(a.entry_stride) - 1;  // the decode token's row stays in the entry
+  int L = a.lengths[g];
+  L = L < 0 ? 0 : (L > lmax ? lmax : L);
+  w.sink_end = a.sink < L ? a.sink : L;
+  const int hist_recent = a.recent - 1 > 0 ? a.recent - 1 : 0;
+  w.recent_start = (L - hist_recent) > w.sink_end ? (L - hist_recent) : w.sink_end;
+  w.n_recent = L - w.recent_start;
+  w.has_dec = (a.cur_k != nullptr || a.ragged_append) ? 1 : 0;
+  w.run = w.n_recent + w.has_dec;
+  w.sink_tiles = (w.sink_end + kTileRows - 1) / kTileRows;
+  w.run_tiles = (w.run + kTileRows - 1) / kTileRows;
+  w.append_position = a.ragged_append ? L : -1;
+  int cap = (a.max_rows - w.sink_end - w.run) / kTileRows;
+  const int room = a.max_chunks * a.t_per_chunk - w.sink_tiles - w.run_tiles;
+  cap = cap < room ? cap : room;
+  cap = cap < a.plan_stride ? cap : static_cast<int>(a.plan_stride);
+  w.nu_cap = cap < 0 ? 0 : cap;
+  return w;
+}
 
 // Union pages of group g that a page-tile launch covers.
-__device__ __forceinline__ int tile_pages(const AttnArgs& a, int g) {
+__device__ __forceinline__ int tile_pages(const AttnArgs& a, int g, const TileWin& w) {
   int nu = a.plan_counts[g];
   nu = nu < 0 ? 0 : nu;
-  return nu > a.t_nu_cap ? a.t_nu_cap : nu;
+  return nu > w.nu_cap ? w.nu_cap : nu;
 }
 
 // Append the decode token of group g to its cache entry (chunk 0's block).
 template <typename S>
-__device__ __forceinline__ void append_decode_token(const AttnArgs& a, int g, int D) {
-  if (a.k_append == nullptr) return;
-  const int64_t row = (static_cast<int64_t>(g) * a.entry_stride + a.append_position) * D;
+__device__ __forceinline__ void append_decode_token(const AttnArgs& a, int g, int D, int position) {
+  if (a.k_append == nullptr || position < 0) return;
+  const int64_t row = (static_cast<int64_t>(g) * a.entry_stride + position) * D;
   const S* ck = static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D;
   const S* cv = static_cast<const S*>(a.cur_v) + static_cast<int64_t>(g) * D;
   S* dk = static_cast<S*>(a.k_append) + row;
@@ -310,7 +358,8 @@ __global__ __launch_bounds__(kBlock) void merge_vec_kernel(AttnArgs a, int rows_
   // rows_per_block: rows of a chunk, or tiles of a chunk in page-tile mode
   int n_chunks;
   if constexpr (MODE == kModeTiles) {
-    const int nt = a.t_sink_tiles + tile_pages(a, g) + a.t_run_tiles;
+    const TileWin w = tile_window(a, g);
+    const int nt = w.sink_tiles + tile_pages(a, g, w) + w.run_tiles;
     n_chunks = (nt + rows_per_block - 1) / rows_per_block;
   } else {
     const GroupRows gr = group_rows<MODE>(a, g, D);
@@ -444,7 +493,7 @@ __global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(
     return;
   }
   if (chunk >= n_chunks) return;
-  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D);
+  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
 
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
@@ -760,7 +809,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_attn_mfma(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D);
+  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
 
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
@@ -976,7 +1025,6 @@ __global__ __launch_bounds__(kBlock, 2) void decode_attn_mfma(AttnArgs a) {
 // pairs per head so that one 16-byte read gives a row pair's p for four
 // heads, and pairs of rows are combined with v_dot2_f32_{f16,bf16}.
 // One wavefront batch is TW tiles; a wave's first batch needs no rescale.
-constexpr int kTileRows = 16;
 constexpr int kTileD = 128;
 
 struct TileSrc {
@@ -986,14 +1034,15 @@ struct TileSrc {
   uint32_t hm;   // heads that see the tile's cache rows
 };
 
-__device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, int t, int nu, int page, uint32_t pmask) {
+__device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w, int t, int nu, int page,
+                                            uint32_t pmask) {
   TileSrc s;
   s.dec = -1;
   s.hm = 0xffu;
-  const int ts = a.t_sink_tiles;
+  const int ts = w.sink_tiles;
   if (t < ts) {
     s.pos0 = static_cast<int64_t>(kTileRows) * t;
-    const int c = a.t_sink_end - kTileRows * t;
+    const int c = w.sink_end - kTileRows * t;
     s.cnt = c < kTileRows ? c : kTileRows;
   } else if (t < ts + nu) {
     s.pos0 = a.sink + static_cast<int64_t>(page) * kTileRows;
@@ -1001,11 +1050,11 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, int t, int nu, in
     s.cnt = (s.pos0 >= 0 && s.pos0 + kTileRows <= a.entry_stride) ? kTileRows : 0;
   } else {
     const int j0 = kTileRows * (t - ts - nu);
-    s.pos0 = static_cast<int64_t>(a.t_recent_start) + j0;
-    const int c = a.t_run - j0;
+    s.pos0 = static_cast<int64_t>(w.recent_start) + j0;
+    const int c = w.run - j0;
     s.cnt = c < 0 ? 0 : (c < kTileRows ? c : kTileRows);
-    const int d = a.t_n_recent - j0;
-    s.dec = (a.t_has_dec && d >= 0 && d < kTileRows) ? d : -1;
+    const int d = w.n_recent - j0;
+    s.dec = (w.has_dec && d >= 0 && d < kTileRows) ? d : -1;
   }
   if (s.cnt <= 0) {
     s.cnt = 0;
@@ -1063,8 +1112,9 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       qf[s] = krow < R ? t : make_uint4(0u, 0u, 0u, 0u);
     }
   }
-  const int nu = tile_pages(a, g);
-  const int n_tiles = a.t_sink_tiles + nu + a.t_run_tiles;
+  const TileWin win = tile_window(a, g);
+  const int nu = tile_pages(a, g, win);
+  const int n_tiles = win.sink_tiles + nu + win.run_tiles;
   const int n_chunks = (n_tiles + per_chunk - 1) / per_chunk;
   if (n_tiles == 0) {
     if (chunk == 0) {
@@ -1074,11 +1124,11 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if (chunk == 0) append_decode_token<S>(a, g, D);
+  if (chunk == 0) append_decode_token<S>(a, g, D, win.append_position);
 
   const S* kg = static_cast<const S*>(a.k) + static_cast<int64_t>(g) * a.entry_stride * D;
   const S* vg = static_cast<const S*>(a.v) + static_cast<int64_t>(g) * a.entry_stride * D;
-  const int64_t dec_off = static_cast<int64_t>(a.append_position < 0 ? 0 : a.append_position) * D;
+  const int64_t dec_off = static_cast<int64_t>(win.append_position < 0 ? 0 : win.append_position) * D;
   const S* kdec = a.cur_k != nullptr ? static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D : kg + dec_off;
   const S* vdec = a.cur_v != nullptr ? static_cast<const S*>(a.cur_v) + static_cast<int64_t>(g) * D : vg + dec_off;
 
@@ -1104,7 +1154,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     uint4 vf[TW][4];
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
-      ts[tt] = tile_src(a, t0 + tt, nu, page[tt], pmask[tt]);
+      ts[tt] = tile_src(a, win, t0 + tt, nu, page[tt], pmask[tt]);
       const int64_t tb = ts[tt].pos0 * D;
       const int kr = krow < ts[tt].cnt ? krow : 0;
       const S* kp = krow == ts[tt].dec ? kdec : kg + tb + kr * D;
@@ -1296,7 +1346,7 @@ __global__ __launch_bounds__(kBlock) void decode_attn_generic(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D);
+  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
   const S* qg = static_cast<const S*>(a.q) + static_cast<int64_t>(g) * R * D;
@@ -1737,7 +1787,8 @@ extern "C" int tw_decode_attention_pages_phase(const void* q, const void* k_base
     a.t_has_dec = has_dec;
     a.t_run = run;
     a.t_run_tiles = (run + tw::kTileRows - 1) / tw::kTileRows;
-    const int64_t capacity = static_cast<int64_t>(a.max_chunks) * a.iters * tw::kTileNW * tw::kTileTW;
+    a.t_per_chunk = a.iters * tw::kTileNW * tw::kTileTW;
+    const int64_t capacity = static_cast<int64_t>(a.max_chunks) * a.t_per_chunk;
     int64_t cap = (max_rows - sink_end - run) / tw::kTileRows;
     const int64_t room = capacity - a.t_sink_tiles - a.t_run_tiles;
     cap = cap < room ? cap : room;
@@ -1748,4 +1799,68 @@ extern "C" int tw_decode_attention_pages_phase(const void* q, const void* k_base
   }
   tw::plan_chunks(dtype, G, R, D, max_rows, &a.iters, &a.max_chunks);
   return tw::launch_dtype(dtype, a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const void* v_base, int dtype,
+                                                int G, int R, int D, const int32_t* plan_pages,
+                                                const uint8_t* plan_masks, const int32_t* plan_counts,
+                                                int64_t plan_stride, int max_rows, int64_t entry_stride_rows, int sink,
+                                                int recent, int block_size, const int32_t* lengths, int append,
+                                                const void* cur_k, const void* cur_v, float softmax_scale, void* out,
+                                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr || lengths == nullptr) return TW_EINVAL;
+  if (G <= 0 || R <= 0 || R > 8 || plan_pages == nullptr || plan_counts == nullptr || plan_stride < 1) return TW_EINVAL;
+  if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16) return TW_EUNSUPPORTED;
+  if (D != tw::kTileD || block_size != tw::kTileRows) return TW_EUNSUPPORTED;
+  if (sink < 0 || recent <= 0 || entry_stride_rows < 2 || entry_stride_rows > (1ll << 30)) return TW_EINVAL;
+  if (max_rows < sink + recent) return TW_EINVAL;  // every window's sink, recent and decode rows fit
+  if ((cur_k == nullptr) != (cur_v == nullptr)) return TW_EINVAL;
+  const uintptr_t align = 16;
+  if ((reinterpret_cast<uintptr_t>(q) % align) || (reinterpret_cast<uintptr_t>(k_base) % align) ||
+      (reinterpret_cast<uintptr_t>(v_base) % align) || (reinterpret_cast<uintptr_t>(cur_k) % align) ||
+      (reinterpret_cast<uintptr_t>(cur_v) % align))
+    return TW_EINVAL;
+  size_t ml_off, o_off, total;
+  tw::workspace_layout(G, R, D, max_rows, &ml_off, &o_off, &total);
+  if (workspace == nullptr || workspace_bytes < total) return TW_ENOMEM;
+  tw::AttnArgs a{};
+  a.q = q;
+  a.k = k_base;
+  a.v = v_base;
+  a.G = G;
+  a.R = R;
+  a.D = D;
+  a.entry_stride = entry_stride_rows;
+  a.plan_pages = plan_pages;
+  a.plan_masks = plan_masks;
+  a.plan_counts = plan_counts;
+  a.plan_stride = plan_stride;
+  a.sink = sink;
+  a.recent = recent;
+  a.bs = block_size;
+  a.length = 0;
+  a.append_position = -1;
+  a.cur_k = cur_k;
+  a.cur_v = cur_v;
+  if (cur_k != nullptr && append) {
+    a.k_append = const_cast<void*>(k_base);
+    a.v_append = const_cast<void*>(v_base);
+  }
+  a.lengths = lengths;
+  a.ragged_append = append ? 1 : 0;
+  a.Hk = 1;
+  a.window_left = -1;
+  a.scale_log2 = softmax_scale * tw::kLog2e;
+  a.out = out;
+  a.counters = static_cast<unsigned int*>(workspace);
+  a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ml_off);
+  a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
+  a.max_rows = max_rows;
+  a.phase = 3;
+  tw::plan_tile_chunks(G, max_rows, &a.iters, &a.max_chunks);
+  a.t_per_chunk = a.iters * tw::kTileNW * tw::kTileTW;
+  // page slots are read from tile ceil(sink / 16) on (every group past its sink window)
+  a.t_sink_tiles = (sink + tw::kTileRows - 1) / tw::kTileRows;
+  return dtype == TW_DTYPE_F16 ? tw::launch_tiles<tw::F16>(a, static_cast<hipStream_t>(stream))
+                               : tw::launch_tiles<tw::BF16>(a, static_cast<hipStream_t>(stream));
 }

@@ -183,13 +183,20 @@ __global__ __launch_bounds__(256) void build_metadata_kernel(
 // so the result equals a rebuild over position + 1 rows bit for bit.
 template <typename DT>
 __global__ __launch_bounds__(256) void update_metadata_kernel(
-    const typename DT::storage* __restrict__ keys, int64_t key_entry_stride, int n_entries, int position, int D,
+    const typename DT::storage* __restrict__ keys, int64_t key_entry_stride, int n_entries, int position_all,
+    const int32_t* __restrict__ positions, int max_position, int max_pages, int D,
     int sink, int bs, typename DT::storage* __restrict__ page_min, typename DT::storage* __restrict__ page_max,
     int64_t page_entry_stride, uint8_t* __restrict__ packed, typename DT::storage* __restrict__ scale,
     typename DT::storage* __restrict__ minimum, int64_t quant_entry_stride) {
   using S = typename DT::storage;
   const int e = blockIdx.x * (blockDim.x / kWave) + static_cast<int>(threadIdx.x) / kWave;
   if (e >= n_entries) return;
+  // ragged entries: each its own row; rows beyond the buffers are skipped
+  const int position = positions != nullptr ? positions[e] : position_all;
+  if (position < 0 || position > max_position) return;
+  if (page_min != nullptr && position >= sink && (position - sink + 1) % bs == 0 &&
+      (position - sink) / bs >= max_pages)
+    return;
   const int lane = lane_id();
   const int nchunk = (D + 127) / 128;
   const S* kb = keys + static_cast<int64_t>(e) * key_entry_stride;
@@ -237,16 +244,40 @@ __global__ __launch_bounds__(256) void update_metadata_kernel(
 }
 
 template <typename DT>
-int launch_update(const void* keys, int64_t key_entry_stride, int n_entries, int position, int D, int sink, int bs,
+int launch_update(const void* keys, int64_t key_entry_stride, int n_entries, int position,
+                  const int32_t* positions, int max_position, int max_pages, int D, int sink, int bs,
                   void* page_min, void* page_max, int64_t page_entry_stride, void* packed, void* scale,
                   void* minimum, int64_t quant_entry_stride, hipStream_t stream) {
   using S = typename DT::storage;
   hipLaunchKernelGGL(update_metadata_kernel<DT>, dim3((n_entries + 3) / 4), dim3(256), 0, stream,
-                     static_cast<const S*>(keys), key_entry_stride, n_entries, position, D, sink, bs,
+                     static_cast<const S*>(keys), key_entry_stride, n_entries, position, positions, max_position,
+                     max_pages, D, sink, bs,
                      static_cast<S*>(page_min), static_cast<S*>(page_max), page_entry_stride,
                      static_cast<uint8_t*>(packed), static_cast<S*>(scale), static_cast<S*>(minimum),
                      quant_entry_stride);
   return tw_host::check_launch();
+}
+
+int dispatch_update(int dtype, const void* keys, int64_t key_entry_stride, int n_entries, int position,
+                    const int32_t* positions, int max_position, int max_pages, int D, int sink, int bs,
+                    void* page_min, void* page_max, int64_t page_entry_stride, void* packed, void* scale,
+                    void* minimum, int64_t quant_entry_stride, hipStream_t s) {
+  switch (dtype) {
+    case TW_DTYPE_F16:
+      return launch_update<F16>(keys, key_entry_stride, n_entries, position, positions, max_position, max_pages, D,
+                                sink, bs, page_min, page_max, page_entry_stride, packed, scale, minimum,
+                                quant_entry_stride, s);
+    case TW_DTYPE_BF16:
+      return launch_update<BF16>(keys, key_entry_stride, n_entries, position, positions, max_position, max_pages, D,
+                                 sink, bs, page_min, page_max, page_entry_stride, packed, scale, minimum,
+                                 quant_entry_stride, s);
+    case TW_DTYPE_F32:
+      return launch_update<F32>(keys, key_entry_stride, n_entries, position, positions, max_position, max_pages, D,
+                                sink, bs, page_min, page_max, page_entry_stride, packed, scale, minimum,
+                                quant_entry_stride, s);
+    default:
+      return TW_EINVAL;
+  }
 }
 
 template <typename DT>
@@ -345,21 +376,32 @@ extern "C" int tw_update_page_metadata(const void* keys, int64_t key_entry_strid
       page_entry_stride < static_cast<int64_t>((position - sink) / block_size + 1) * D)
     return TW_EINVAL;
   if (page_min == nullptr && packed == nullptr) return TW_OK;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case TW_DTYPE_F16:
-      return tw::launch_update<tw::F16>(keys, key_entry_stride, n_entries, position, D, sink, block_size, page_min,
-                                        page_max, page_entry_stride, packed, scale, minimum, quant_entry_stride, s);
-    case TW_DTYPE_BF16:
-      return tw::launch_update<tw::BF16>(keys, key_entry_stride, n_entries, position, D, sink, block_size,
-                                         page_min, page_max, page_entry_stride, packed, scale, minimum,
-                                         quant_entry_stride, s);
-    case TW_DTYPE_F32:
-      return tw::launch_update<tw::F32>(keys, key_entry_stride, n_entries, position, D, sink, block_size, page_min,
-                                        page_max, page_entry_stride, packed, scale, minimum, quant_entry_stride, s);
-    default:
-      return TW_EINVAL;
-  }
+  const int big = 0x7fffffff;
+  return tw::dispatch_update(dtype, keys, key_entry_stride, n_entries, position, nullptr, big, big, D, sink,
+                             block_size, page_min, page_max, page_entry_stride, packed, scale, minimum,
+                             quant_entry_stride, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tw_update_page_metadata_ragged(const void* keys, int64_t key_entry_stride, int n_entries,
+                                              const int32_t* positions, int max_position, int D, int dtype, int sink,
+                                              int block_size, void* page_min, void* page_max, int max_pages,
+                                              int64_t page_entry_stride, void* packed, void* scale, void* minimum,
+                                              int64_t quant_entry_stride, void* stream) {
+  if (keys == nullptr || positions == nullptr || n_entries <= 0 || max_position < 0 || D <= 0 || (D % 2) != 0 ||
+      D > 1024)
+    return TW_EINVAL;
+  if (sink < 0 || block_size <= 0) return TW_EINVAL;
+  if ((page_min == nullptr) != (page_max == nullptr)) return TW_EINVAL;
+  if (!((packed == nullptr) == (scale == nullptr) && (scale == nullptr) == (minimum == nullptr)))
+    return TW_EINVAL;
+  if (n_entries > 1 && key_entry_stride < static_cast<int64_t>(max_position + 1) * D) return TW_EINVAL;
+  if (packed != nullptr && n_entries > 1 && quant_entry_stride <= max_position) return TW_EINVAL;
+  if (page_min != nullptr && (max_pages < 0 || (n_entries > 1 && page_entry_stride < static_cast<int64_t>(max_pages) * D)))
+    return TW_EINVAL;
+  if (page_min == nullptr && packed == nullptr) return TW_OK;
+  return tw::dispatch_update(dtype, keys, key_entry_stride, n_entries, 0, positions, max_position, max_pages, D,
+                             sink, block_size, page_min, page_max, page_entry_stride, packed, scale, minimum,
+                             quant_entry_stride, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int tw_int4_dequantize(const void* packed, const void* scale, const void* minimum, int dtype,

@@ -109,7 +109,22 @@ struct ScoreArgs {
   float* scores;           // [G][R][score_stride]
   int64_t score_stride;
   float* scores_out;       // nullable [G][R][P]
+  // Ragged groups (nullable): group g scores ragged_pages(lengths[g]) <= P pages.
+  const int32_t* lengths;
+  int sink, recent, bs;
 };
+
+// Candidate pages of a group with `length` tokens: the whole pages between
+// the sink and the recent window (quest_offload_cache.py:326-346), at most
+// P_max.
+__device__ __forceinline__ int ragged_pages(int length, int sink, int recent, int bs, int P_max) {
+  length = length < 0 ? 0 : length;
+  const int sink_end = sink < length ? sink : length;
+  const int hist_recent = recent - 1 > 0 ? recent - 1 : 0;
+  const int recent_start = (length - hist_recent) > sink_end ? (length - hist_recent) : sink_end;
+  const int cand = (recent_start - sink_end) / bs;
+  return cand < P_max ? cand : P_max;
+}
 
 // Stage a tile of pages (min then max) into LDS with a padded pitch.
 template <typename DT>
@@ -149,7 +164,9 @@ template <typename DT, int DFIX>
 __device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
   using S = typename DT::storage;
   const int p0 = tile * kTilePages;
-  const int np = (a.P - p0) < kTilePages ? (a.P - p0) : kTilePages;
+  const int P = a.lengths != nullptr ? ragged_pages(a.lengths[g], a.sink, a.recent, a.bs, a.P) : a.P;
+  if (p0 >= P) return;  // block-uniform
+  const int np = (P - p0) < kTilePages ? (P - p0) : kTilePages;
   const int pitch = a.D * static_cast<int>(sizeof(S)) + 16;  // 16-byte aligned rows, padded
   // The group's queries go to LDS in the same round trip as the tile.
   float* q_lds = reinterpret_cast<float*>(lds + 2 * kTilePages * pitch);
@@ -258,16 +275,18 @@ struct SelectArgs {
   int64_t rows_stride;
   int sink, recent, bs, length, append_position;
   unsigned int* counters;  // [G]
+  // Ragged groups (nullable): group g selects min(k, its candidate pages)
+  // among ragged_pages(lengths[g]) <= P; selection slots beyond that get -1.
+  const int32_t* lengths;
 };
 
 // Union plan of group g: page_mask (LDS, byte per page, zero padded to a
 // multiple of 8) -> ascending union pages and their head masks, then the
 // optional row plan.  Thread t owns pages [8t, 8t + 8) of each 2048-page
 // stretch.
-__device__ void write_union_plan(const SelectArgs& s, int g, const uint8_t* page_mask, int32_t* upage,
+__device__ void write_union_plan(const SelectArgs& s, int g, int P, const uint8_t* page_mask, int32_t* upage,
                                  uint8_t* umask, int* scan) {
   const int tid = threadIdx.x;
-  const int P = s.P;
   const uint8_t all = static_cast<uint8_t>((1u << s.R) - 1u);
   int nu = 0;
   for (int base = 0; base < P; base += kBlock * 8) {
@@ -348,7 +367,8 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
   extern __shared__ __align__(16) uint8_t dyn[];  // union scratch
   const int row = blockIdx.x;
   const int g = row / s.R;
-  const int P = s.P;
+  const int P = s.lengths != nullptr ? ragged_pages(s.lengths[g], s.sink, s.recent, s.bs, s.P) : s.P;
+  const int k = s.k < P ? s.k : P;
   const float* vals = s.scores + static_cast<int64_t>(row) * s.score_stride;
   // ---- keys: one batched round trip ----
   uint32_t key[KPT];
@@ -372,18 +392,24 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
 #pragma unroll
       for (int j = 0; j < KPT; ++j) {
         const int i = i0 + j;
-        key[j] = score_key(vals[i < P ? i : P - 1]);
+        key[j] = score_key(vals[i < P ? i : (P > 0 ? P - 1 : 0)]);
       }
     }
   }
   int32_t* ws_row = s.sel_ws != nullptr ? s.sel_ws + static_cast<int64_t>(row) * s.k : nullptr;
   int32_t* out32 = s.sel_out != nullptr ? s.sel_out + static_cast<int64_t>(row) * s.k : nullptr;
   int64_t* out64 = s.sel_out64 != nullptr ? s.sel_out64 + static_cast<int64_t>(row) * s.k : nullptr;
-  block_topk<KPT>(key, P, s.k, sh, [&](int slot, int idx) {
-    if (ws_row != nullptr) publish_i32(ws_row + slot, idx);
-    if (out32 != nullptr) out32[slot] = idx;
-    if (out64 != nullptr) out64[slot] = idx;
-  });
+  if (k > 0) {
+    block_topk<KPT>(key, P, k, sh, [&](int slot, int idx) {
+      if (ws_row != nullptr) publish_i32(ws_row + slot, idx);
+      if (out32 != nullptr) out32[slot] = idx;
+      if (out64 != nullptr) out64[slot] = idx;
+    });
+  }
+  for (int slot = k + static_cast<int>(threadIdx.x); slot < s.k; slot += kBlock) {
+    if (out32 != nullptr) out32[slot] = -1;
+    if (out64 != nullptr) out64[slot] = -1;
+  }
   if (!s.want_union) return;
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.flag)) return;
 
@@ -395,14 +421,14 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
   for (int i = threadIdx.x; i < mask_bytes / 4; i += kBlock) reinterpret_cast<uint32_t*>(page_mask)[i] = 0u;
   __syncthreads();
   const int32_t* sel_g = s.sel_ws + static_cast<int64_t>(g) * s.R * s.k;
-  const int n_sel = s.R * s.k;
+  const int n_sel = s.R * k;
   for (int i = threadIdx.x; i < n_sel; i += kBlock) {
-    const int id = fetch_i32(sel_g + i);
-    const int hr = i / s.k;
+    const int hr = i / k;
+    const int id = fetch_i32(sel_g + hr * s.k + (i - hr * k));
     atomicOr(reinterpret_cast<uint32_t*>(page_mask) + (id >> 2), (1u << hr) << (8 * (id & 3)));
   }
   __syncthreads();
-  write_union_plan(s, g, page_mask, upage, umask, sh.scan);
+  write_union_plan(s, g, P, page_mask, upage, umask, sh.scan);
 }
 
 size_t union_lds_bytes(int P) { return static_cast<size_t>((P + 7) / 8) * 8 + static_cast<size_t>(P) * 5 + 16; }
@@ -563,6 +589,55 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
   s.length = length;
   s.append_position = append_position;
   s.counters = counters;
+  const int rc = tw::dispatch_score(dtype, a, st);
+  if (rc != TW_OK) return rc;
+  return tw::launch_select(s, G * R, true, st);
+}
+
+extern "C" int tw_quest_select_ragged(const float* q, const void* page_min, const void* page_max, int dtype, int G,
+                                      int R, int P_max, int D, int64_t page_group_stride, const int32_t* lengths,
+                                      int k, int32_t* sel_pages, int32_t* plan_pages, uint8_t* plan_masks,
+                                      int32_t* plan_counts, int64_t plan_stride, int sink, int recent,
+                                      int block_size, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!tw::check_score_args(q, page_min, page_max, G, R, P_max, D, page_group_stride)) return TW_EINVAL;
+  if (lengths == nullptr || k <= 0 || k > P_max) return TW_EINVAL;
+  if (sink < 0 || recent <= 0 || block_size <= 0) return TW_EINVAL;
+  if (P_max > tw::kMaxSelPages) return TW_EUNSUPPORTED;
+  const bool page_plan = plan_pages != nullptr || plan_counts != nullptr;
+  if (page_plan && (R > 8 || plan_pages == nullptr || plan_counts == nullptr)) return TW_EINVAL;
+  if (plan_masks != nullptr && plan_pages == nullptr) return TW_EINVAL;
+  if (plan_pages != nullptr &&
+      plan_stride < (static_cast<int64_t>(R) * k < P_max ? static_cast<int64_t>(R) * k : P_max))
+    return TW_EINVAL;
+  if (workspace == nullptr || workspace_bytes < tw_quest_select_workspace_size(G, R, P_max)) return TW_ENOMEM;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  unsigned int* counters = reinterpret_cast<unsigned int*>(ws);
+  float* score_ws = reinterpret_cast<float*>(ws + tw::counter_bytes(G));
+  int32_t* sel_ws = reinterpret_cast<int32_t*>(score_ws + static_cast<int64_t>(G) * R * tw::padded(P_max));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  tw::ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P_max, D, score_ws, tw::padded(P_max), nullptr,
+                  lengths, sink, recent, block_size};
+  tw::SelectArgs s{};
+  s.scores = score_ws;
+  s.score_stride = tw::padded(P_max);
+  s.vec_last4 = static_cast<int>(tw::padded(P_max)) - 4;
+  s.G = G;
+  s.R = R;
+  s.P = P_max;
+  s.k = k;
+  s.sel_ws = sel_ws;
+  s.sel_out = sel_pages;
+  s.want_union = page_plan;
+  s.plan_pages = plan_pages;
+  s.plan_masks = plan_masks;
+  s.plan_counts = plan_counts;
+  s.plan_stride = plan_stride;
+  s.sink = sink;
+  s.recent = recent;
+  s.bs = block_size;
+  s.append_position = -1;
+  s.counters = counters;
+  s.lengths = lengths;
   const int rc = tw::dispatch_score(dtype, a, st);
   if (rc != TW_OK) return rc;
   return tw::launch_select(s, G * R, true, st);

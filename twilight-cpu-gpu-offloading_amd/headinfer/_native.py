@@ -41,6 +41,12 @@ _HIP_SIGNATURES = {
     "tw_version": (i32, []),
     "tw_build_page_metadata": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i64, vp, vp, vp, i64, vp]),
     "tw_update_page_metadata": (i32, [vp, i64, i32, i32, i32, i32, i32, i32, vp, vp, i64, vp, vp, vp, i64, vp]),
+    "tw_update_page_metadata_ragged": (i32, [vp, i64, i32, vp, i32, i32, i32, i32, i32, vp, vp, i32, i64, vp, vp,
+                                             vp, i64, vp]),
+    "tw_quest_select_ragged": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, i32, vp, vp, vp, vp, i64, i32, i32,
+                                     i32, vp, szt, vp]),
+    "tw_decode_attention_pages_ragged": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32,
+                                               i32, vp, i32, vp, vp, f32, vp, vp, szt, vp]),
     "tw_int4_dequantize": (i32, [vp, vp, vp, i32, i64, i32, vp, vp]),
     "tw_quest_score": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp]),
     "tw_topk_sorted": (i32, [vp, i32, i32, i64, i32, vp, vp]),

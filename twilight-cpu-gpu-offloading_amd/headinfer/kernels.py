@@ -202,6 +202,67 @@ def update_page_metadata(
                                             stream_handle(dev)), "update_page_metadata")
 
 
+def update_page_metadata_ragged(
+    keys: torch.Tensor,
+    positions: torch.Tensor,
+    *,
+    first_entry: int,
+    sink: int,
+    block_size: int,
+    page_min: Optional[torch.Tensor] = None,
+    page_max: Optional[torch.Tensor] = None,
+    packed: Optional[torch.Tensor] = None,
+    scale: Optional[torch.Tensor] = None,
+    minimum: Optional[torch.Tensor] = None,
+) -> None:
+    """update_page_metadata for entries [first_entry, first_entry + n) whose
+    new rows are positions [n] (int32, device); rows or pages beyond the
+    buffers are skipped."""
+    if keys.ndim != 3 or keys.dtype not in _KEY_DTYPES or keys.stride(2) != 1 or keys.stride(1) != keys.shape[2]:
+        raise ValueError("keys must be a row-contiguous [E, Lmax, D] plane")
+    E, Lmax, D = keys.shape
+    if positions.dtype != torch.int32 or positions.ndim != 1 or not positions.is_contiguous():
+        raise ValueError("positions must be contiguous [n] int32")
+    n = positions.shape[0]
+    if n <= 0 or first_entry < 0 or first_entry + n > E:
+        raise ValueError("update target outside the cache")
+    e0 = first_entry
+    max_position = Lmax - 1
+    pmin_p = pmax_p = pk_p = sc_p = mn_p = None
+    pe = qe = max_pages = 0
+    if page_min is not None:
+        if page_max is None or page_min.shape != page_max.shape or page_min.dtype != keys.dtype \
+                or page_min.ndim != 3 or page_min.shape[0] != E or page_min.shape[2] != D \
+                or page_min.stride(2) != 1 or page_min.stride(1) != D or page_max.stride() != page_min.stride():
+            raise ValueError("page_min/page_max must be row-contiguous [E, P, D] in the key dtype")
+        pe, max_pages = page_min.stride(0), page_min.shape[1]
+        pmin_p, pmax_p = ptr(page_min[e0]), ptr(page_max[e0])
+    elif page_max is not None:
+        raise ValueError("page_min/page_max go together")
+    if packed is not None:
+        if scale is None or minimum is None or scale.dtype != keys.dtype or minimum.dtype != keys.dtype:
+            raise ValueError("INT4 outputs must be given together in the key dtype")
+        if packed.dtype != torch.uint8 or packed.ndim != 3 or packed.shape[0] != E or packed.shape[2] != D // 2 \
+                or packed.stride(2) != 1 or packed.stride(1) != D // 2 or packed.stride(0) % (D // 2):
+            raise ValueError("packed must be row-contiguous [E, T, D/2] uint8")
+        qe = packed.stride(0) // (D // 2)
+        if scale.stride(-1) != 1 or minimum.stride(-1) != 1 or scale.stride(0) != qe or minimum.stride(0) != qe:
+            raise ValueError("scale/minimum must share the packed entry stride")
+        max_position = min(max_position, packed.shape[1] - 1)
+        pk_p, sc_p, mn_p = ptr(packed[e0]), ptr(scale[e0]), ptr(minimum[e0])
+    elif scale is not None or minimum is not None:
+        raise ValueError("INT4 outputs must be given together")
+    if pmin_p is None and pk_p is None:
+        return
+    dev = _require_device(positions, page_min, page_max, packed, scale, minimum, what="update_page_metadata_ragged")
+    kp = ptr(keys) if keys.is_cuda else host_device_pointer(keys)
+    kp += e0 * keys.stride(0) * keys.element_size()
+    with torch.cuda.device(dev):
+        check(hip().tw_update_page_metadata_ragged(kp, keys.stride(0), n, ptr(positions), max_position, D,
+                                                   _dt(keys), sink, block_size, pmin_p, pmax_p, max_pages, pe, pk_p,
+                                                   sc_p, mn_p, qe, stream_handle(dev)), "update_page_metadata_ragged")
+
+
 def affine_int4_pack(keys: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Per-token affine INT4 (twilight_offload_cache.py:25-37) on the GPU."""
     if keys.ndim != 2 or keys.shape[-1] % 2:
@@ -347,6 +408,55 @@ def quest_select(
                                     ptr(plan_masks), ptr(plan_counts), plan_stride, ptr(rows), ptr(row_masks),
                                     ptr(row_counts), stride, sink, recent, block_size, length, append_position,
                                     ptr(ws), ws.numel(), stream_handle(dev)), "quest_select")
+
+
+def quest_select_ragged(
+    q: torch.Tensor,
+    page_min: torch.Tensor,
+    page_max: torch.Tensor,
+    lengths: torch.Tensor,
+    k: int,
+    *,
+    sink: int,
+    recent: int,
+    block_size: int,
+    sel_pages: Optional[torch.Tensor] = None,
+    plan_pages: Optional[torch.Tensor] = None,
+    plan_masks: Optional[torch.Tensor] = None,
+    plan_counts: Optional[torch.Tensor] = None,
+) -> None:
+    """quest_select over G groups of different lengths (lengths [G] int32 on
+    the device): group g scores its own candidate pages (at most the P of
+    page_min [G, P, D]) and keeps min(k, its pages) per head; sel_pages slots
+    beyond that are -1.  Union plan as in quest_select."""
+    _check_score_inputs(q, page_min, page_max, "quest_select_ragged")
+    dev = _require_device(q, page_min, page_max, lengths, sel_pages, plan_pages, plan_masks, plan_counts,
+                          what="quest_select_ragged")
+    G, R, D = q.shape
+    P = page_min.shape[1]
+    if not 1 <= k <= P:
+        raise ValueError("k must be in [1, P]")
+    if lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,) or not lengths.is_contiguous():
+        raise ValueError("lengths must be contiguous [G] int32")
+    for t, dt, shape in ((sel_pages, torch.int32, (G, R, k)), (plan_counts, torch.int32, (G,))):
+        if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
+            raise ValueError("quest_select_ragged output has the wrong dtype/shape")
+    plan_stride = 0
+    if plan_pages is not None:
+        if plan_pages.dtype != torch.int32 or plan_pages.ndim != 2 or plan_pages.shape[0] != G \
+                or plan_pages.stride(1) != 1:
+            raise ValueError("plan_pages must be [G, stride] int32")
+        plan_stride = plan_pages.stride(0)
+        if plan_masks is not None and (plan_masks.dtype != torch.uint8 or plan_masks.shape != plan_pages.shape
+                                       or plan_masks.stride() != plan_pages.stride()):
+            raise ValueError("plan_masks must match plan_pages")
+    nbytes = hip().tw_quest_select_workspace_size(G, R, P)
+    ws = WORKSPACE.get(dev, "quest_select", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_quest_select_ragged(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
+                                           page_min.stride(0), ptr(lengths), k, ptr(sel_pages), ptr(plan_pages),
+                                           ptr(plan_masks), ptr(plan_counts), plan_stride, sink, recent, block_size,
+                                           ptr(ws), ws.numel(), stream_handle(dev)), "quest_select_ragged")
 
 
 # ---------------------------------------------------------------- Twilight
@@ -620,6 +730,76 @@ def decode_attention_pages(
                                                     recent, block_size, length, append_position, ptr(cur_k),
                                                     ptr(cur_v), scale, ptr(out), ptr(ws), ws.numel(), int(phase),
                                                     stream_handle(dev)), "decode_attention_pages")
+    return out
+
+
+def decode_attention_pages_ragged(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    plan_pages: torch.Tensor,
+    plan_counts: torch.Tensor,
+    lengths: torch.Tensor,
+    *,
+    plan_masks: Optional[torch.Tensor] = None,
+    max_pages: int,
+    sink: int,
+    recent: int,
+    block_size: int = 16,
+    append: bool = True,
+    cur_k: Optional[torch.Tensor] = None,
+    cur_v: Optional[torch.Tensor] = None,
+    softmax_scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """decode_attention_pages over G groups of different lengths (lengths [G]
+    int32 on the device): group g's window follows from its own length and
+    its decode token is cur_k/cur_v[g] (appended at row lengths[g] when
+    `append`), or the cache row lengths[g] (`append`, no cur_k), or none.
+    16-bit K/V, D = 128, block_size 16.  k_cache/v_cache [G, Lmax, D] (HBM or
+    pinned host).  Returns [G, R, D]."""
+    if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("q must be [G, R, D] fp16/bf16")
+    G, R, D = q.shape
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or k_cache.shape != v_cache.shape \
+            or k_cache.ndim != 3 or k_cache.shape[0] != G or k_cache.shape[2] != D \
+            or k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1 or k_cache.stride(1) != D \
+            or k_cache.stride(0) % D:
+        raise ValueError("K/V cache must be row-contiguous [G, Lmax, D] in q's dtype")
+    if plan_pages.dtype != torch.int32 or plan_pages.ndim != 2 or plan_pages.shape[0] != G \
+            or plan_pages.stride(1) != 1:
+        raise ValueError("plan_pages must be [G, stride] int32")
+    if plan_masks is not None and (plan_masks.dtype != torch.uint8 or plan_masks.shape != plan_pages.shape
+                                   or plan_masks.stride() != plan_pages.stride()):
+        raise ValueError("plan_masks must match plan_pages")
+    if plan_counts.dtype != torch.int32 or tuple(plan_counts.shape) != (G,):
+        raise ValueError("plan_counts must be [G] int32")
+    if lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,) or not lengths.is_contiguous():
+        raise ValueError("lengths must be contiguous [G] int32")
+    if not 0 <= max_pages <= plan_pages.shape[1]:
+        raise ValueError("max_pages must be within the plan width")
+    if (cur_k is None) != (cur_v is None):
+        raise ValueError("cur_k and cur_v go together")
+    if cur_k is not None and (cur_k.shape != (G, D) or cur_k.dtype != q.dtype or cur_v.shape != cur_k.shape
+                              or cur_v.dtype != q.dtype):
+        raise ValueError("cur_k/cur_v must be [G, D] in q's dtype")
+    dev = _require_device(q, plan_pages, plan_masks, plan_counts, lengths, cur_k, cur_v,
+                          what="decode_attention_pages_ragged")
+    kp, vp = _slab_source(k_cache, v_cache)
+    _require_contiguous(q, cur_k, cur_v, what="decode_attention_pages_ragged")
+    if out is None:
+        out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    max_rows = sink + max_pages * block_size + recent
+    nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
+    ws = WORKSPACE.get(dev, "decode_attention", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_decode_attention_pages_ragged(ptr(q), kp, vp, _dt(q), G, R, D, ptr(plan_pages),
+                                                     ptr(plan_masks), ptr(plan_counts), plan_pages.stride(0),
+                                                     max_rows, k_cache.stride(0) // D, sink, recent, block_size,
+                                                     ptr(lengths), int(bool(append)), ptr(cur_k), ptr(cur_v), scale,
+                                                     ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
+              "decode_attention_pages_ragged")
     return out
 
 
