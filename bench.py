@@ -50,10 +50,13 @@ def parse_args(argv=None):
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=32)
-    ap.add_argument("--workload", choices=("quest32k", "twilight32k", "offload64k", "tpot32k"), default="quest32k",
+    ap.add_argument("--workload", choices=("quest32k", "twilight32k", "offload64k", "tpot32k", "multireq"),
+                    default="quest32k",
                     help="quest32k (default): 32K layer, KV in HBM; twilight32k: INT4 QK + top-p at 32K; "
                          "offload64k: 64K layer with KV in pinned host memory (zero-copy vs DMA); "
-                         "tpot32k: end-to-end p50 TPOT of a Llama-3-8B-shaped model at 32K context")
+                         "tpot32k: end-to-end p50 TPOT of a Llama-3-8B-shaped model at 32K context; "
+                         "multireq: 8 requests of 16K-128K context, Qwen2.5-7B-like GQA, KV heads half in HBM "
+                         "and half in host memory, 256 decode steps with append and metadata update")
     ap.add_argument("--decode-tokens", type=int, default=32, help="decode tokens per TPOT run (D1..Dn)")
     ap.add_argument("--kv-residency", choices=("hbm", "host"), default="hbm",
                     help="tpot32k: KV slab in HBM or in pinned host memory (read zero-copy)")
@@ -488,6 +491,8 @@ def main(argv=None) -> int:
         return run_offload(args, dev)
     if args.workload == "tpot32k":
         return run_tpot(args, dev)
+    if args.workload == "multireq":
+        return run_multireq(args, dev)
     args.context = args.context or 32768
     print(f"[bench] building inputs: layers={args.layers} context={args.context}", file=sys.stderr, flush=True)
     w = QuestWorkload(dev, args.layers, args.context, args.budget_pages)
@@ -869,6 +874,221 @@ def run_tpot(args, dev) -> int:
     }
     print(json.dumps(result), flush=True)
     return 0
+
+
+class MultiRequestWorkload:
+    """Seeded inputs of the multi-request configuration: 8 requests with
+    contexts uniform in [16384, 131072] (rounded down to multiples of 16),
+    28 layers of a Qwen2.5-7B-like GQA attention (28 query heads, 4 KV heads,
+    head_dim 128, bf16), page 16, sink 64, recent 256, Quest budget 128 pages
+    per query head.  KV heads {0, 1} of every layer live in HBM, {2, 3} in
+    pinned host memory (read zero-copy).  Entries of one residency set are
+    ordered (layer, request, head), so a layer's 16 groups are consecutive;
+    every group carries its own length in one device array."""
+
+    LAYERS, HQ, HK, D = 28, 28, 4, 128
+    R = HQ // HK
+    REQUESTS, SINK, RECENT, BS, BUDGET = 8, 64, 256, 16, 128
+    STEPS = 256
+
+    def __init__(self, dev, layers: int, seed: int = 4):
+        import torch
+
+        from headinfer import kernels
+
+        self.dev, self.layers = dev, layers
+        self.kernels = kernels
+        g = torch.Generator().manual_seed(seed)
+        ctx = torch.randint(16384, 131072 + 1, (self.REQUESTS,), generator=g)
+        self.contexts = [int(c) // 16 * 16 for c in ctx]
+        self.Lmax = max(self.contexts) + self.STEPS + 16
+        self.HS = self.HK // 2                       # KV heads per residency set
+        self.G = self.REQUESTS * self.HS             # groups per layer and set
+        E = layers * self.G
+        self.P = min((self.Lmax - self.SINK) // self.BS, 8192)
+        self.width = min(self.P, self.R * self.BUDGET)
+        bf = torch.bfloat16
+        self.slab = {"hbm": torch.empty((2, E, self.Lmax, self.D), dtype=bf, device=dev),
+                     "host": torch.empty((2, E, self.Lmax, self.D), dtype=bf, pin_memory=True)}
+        self.pmin = {s: torch.zeros((E, self.P, self.D), dtype=bf, device=dev) for s in self.slab}
+        self.pmax = {s: torch.zeros((E, self.P, self.D), dtype=bf, device=dev) for s in self.slab}
+        lens = [c for c in self.contexts for _ in range(self.HS)]
+        self.lengths = torch.tensor(lens, dtype=torch.int32, device=dev)
+        self.lengths0 = list(lens)
+        tg = torch.Generator(device=dev).manual_seed(seed + 1)
+        for s in self.slab:
+            for layer in range(layers):
+                e0 = layer * self.G
+                kv = torch.randn((2, self.G, self.Lmax, self.D), generator=tg, device=dev, dtype=torch.float32).to(bf)
+                for gi, L in enumerate(lens):
+                    kernels.build_page_metadata(kv[0, gi, :L], sink=self.SINK, block_size=self.BS,
+                                                page_min=self.pmin[s][e0 + gi], page_max=self.pmax[s][e0 + gi])
+                self.slab[s][:, e0:e0 + self.G].copy_(kv)
+                del kv
+        torch.cuda.synchronize()
+        self.q = [{s: torch.randn((self.G, self.R, self.D), generator=tg, device=dev).to(bf) for s in self.slab}
+                  for _ in range(layers)]
+        self.qf = [{s: self.q[i][s].float() for s in self.slab} for i in range(layers)]
+        self.cur = [{s: torch.randn((2, self.G, self.D), generator=tg, device=dev).to(bf) for s in self.slab}
+                    for _ in range(layers)]
+        self.plan = [{s: (torch.zeros((self.G, self.width), dtype=torch.int32, device=dev),
+                          torch.zeros((self.G, self.width), dtype=torch.uint8, device=dev),
+                          torch.zeros((self.G,), dtype=torch.int32, device=dev)) for s in self.slab}
+                     for _ in range(layers)]
+        self.out = [{s: torch.empty((self.G, self.R, self.D), dtype=bf, device=dev) for s in self.slab}
+                    for _ in range(layers)]
+
+    def layer(self, i: int, s: str) -> None:
+        K = self.kernels
+        e0 = i * self.G
+        pp, pm, pc = self.plan[i][s]
+        K.quest_select_ragged(self.qf[i][s], self.pmin[s][e0:e0 + self.G], self.pmax[s][e0:e0 + self.G],
+                              self.lengths, self.BUDGET, sink=self.SINK, recent=self.RECENT, block_size=self.BS,
+                              plan_pages=pp, plan_masks=pm, plan_counts=pc)
+        K.decode_attention_pages_ragged(self.q[i][s], self.slab[s][0, e0:e0 + self.G], self.slab[s][1, e0:e0 + self.G],
+                                        pp, pc, self.lengths, plan_masks=pm, max_pages=self.width, sink=self.SINK,
+                                        recent=self.RECENT, block_size=self.BS, append=True,
+                                        cur_k=self.cur[i][s][0], cur_v=self.cur[i][s][1], out=self.out[i][s])
+        K.update_page_metadata_ragged(self.slab[s][0], self.lengths, first_entry=e0, sink=self.SINK,
+                                      block_size=self.BS, page_min=self.pmin[s], page_max=self.pmax[s])
+
+    def step(self) -> None:
+        for i in range(self.layers):
+            for s in ("hbm", "host"):
+                self.layer(i, s)
+        self.lengths.add_(1)
+
+    def bytes_per_step(self) -> dict:
+        """Algorithmic bytes of one step (current plans and lengths): page
+        metadata read (2 x D x 2 B per scored page), attended K/V rows
+        (2 x D x 2 B), the decode tokens' append; HBM and host link apart."""
+        lens = [L - 1 for L in self.lengths.tolist()]  # the lengths the last step ran with
+        pages = []
+        for L in lens:
+            sink_end = min(self.SINK, L)
+            recent_start = max(sink_end, L - (self.RECENT - 1))
+            pages.append(min(self.P, (recent_start - sink_end) // self.BS))
+        row = 2 * self.D * 2
+        out = {"hbm": 0.0, "host": 0.0, "rows": {"hbm": 0, "host": 0}}
+        for i in range(self.layers):
+            for s in ("hbm", "host"):
+                counts = self.plan[i][s][2].tolist()
+                rows = 0
+                for gi, L in enumerate(lens):
+                    sink_end = min(self.SINK, L)
+                    recent_start = max(sink_end, L - (self.RECENT - 1))
+                    rows += sink_end + counts[gi] * self.BS + (L - recent_start)
+                out["rows"][s] += rows
+                meta = sum(pages) * row
+                q_out = 2 * self.G * self.R * self.D * 2
+                out["hbm"] += meta + q_out + (rows * row if s == "hbm" else 0) + self.G * row
+                if s == "host":
+                    out["host"] += rows * row + self.G * row
+        return out
+
+
+def run_multireq(args, dev) -> int:
+    """Multi-request decode: 256 steps of 8 requests x 28 layers, each layer
+    one ragged Quest select + one ragged page-tile attention (decode-token
+    append fused) + one ragged metadata update per residency set, the step
+    captured once as a HIP graph whose replays advance every request's length
+    on the device.  1 eager warm-up step, 7 replayed warm-up steps and 248
+    timed steps make the 256."""
+    import torch
+
+    layers = args.layers if args.layers != 32 else MultiRequestWorkload.LAYERS
+    print(f"[bench] multireq inputs: {MultiRequestWorkload.REQUESTS} requests x {layers} layers", file=sys.stderr,
+          flush=True)
+    t0 = time.perf_counter()
+    w = MultiRequestWorkload(dev, layers)
+    setup_s = time.perf_counter() - t0
+    print(f"[bench] multireq contexts {w.contexts} (setup {setup_s:.1f} s)", file=sys.stderr, flush=True)
+    w.step()
+    torch.cuda.synchronize()
+    g_step = graph_of(w.step, warm=0)
+    warm, timed = 7, w.STEPS - 8
+    for _ in range(warm):
+        g_step.replay()
+    torch.cuda.synchronize()
+    print(f"[bench] multireq timing {timed} steps", file=sys.stderr, flush=True)
+    t1 = time.perf_counter()
+    for _ in range(timed):
+        g_step.replay()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t1) / timed
+    by = w.bytes_per_step()
+    ok, err = multireq_check(w)
+    hbm_gbs = by["hbm"] / step_s / 1e9
+    host_gbs = by["host"] / step_s / 1e9
+    result = {
+        "metric": METRIC, "value": round(w.REQUESTS / step_s, 1), "unit": "tokens/s (8 requests, sparse path)",
+        "n_gpus": 1, "steps": timed, "warmup": warm + 1, "ms_per_step": round(step_s * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "multireq: Qwen2.5-7B-like GQA (28 q / 4 kv heads, D 128) x 28 layers, 8 requests "
+                               "of 16K-128K context, KV heads {0,1} in HBM and {2,3} in pinned host memory, "
+                               "256 decode steps with append and page-metadata update, one graph per step",
+                   "layers": layers, "requests": w.REQUESTS, "contexts": w.contexts, "q_heads": w.HQ,
+                   "kv_heads": w.HK, "head_dim": w.D, "page_size": w.BS, "budget_pages": w.BUDGET,
+                   "sink": w.SINK, "recent": w.RECENT, "total_steps": w.STEPS},
+        "step_ms": round(step_s * 1e3, 3),
+        "layer_us": round(step_s / layers * 1e6, 2),
+        "hbm_bytes_per_step": int(by["hbm"]), "host_bytes_per_step": int(by["host"]),
+        "hbm_GBps": round(hbm_gbs, 1), "host_link_GBps": round(host_gbs, 2),
+        "host_link_frac_pcie_gen5_x16": round(host_gbs / 64.0, 4),
+        "rows_per_group": {s: round(by["rows"][s] / (w.G * layers), 1) for s in ("hbm", "host")},
+        "setup_s": round(setup_s, 1),
+        "parity": {"ok": ok, "attention_max_abs_err": err},
+    }
+    print(json.dumps(result), flush=True)
+    return 0 if ok else 1
+
+
+def multireq_check(w) -> tuple[bool, float]:
+    """After the run: layer 0's attention of the last step against float64
+    over each group's own rows (HBM and host sets, every group), and the
+    page metadata of layer 0's entries against a rebuild over their rows."""
+    import numpy as np
+    import torch
+
+    from headinfer import kernels
+
+    ok, err = True, 0.0
+    lens = [L - 1 for L in w.lengths.tolist()]
+    for s in ("hbm", "host"):
+        pp, pm, pc = (t.cpu() for t in w.plan[0][s])
+        kc = w.slab[s][0, :w.G].cpu() if s == "host" else w.slab[s][0, :w.G]
+        vc = w.slab[s][1, :w.G].cpu() if s == "host" else w.slab[s][1, :w.G]
+        q = w.q[0][s].cpu().double()
+        out = w.out[0][s].cpu().double()
+        for gi, L in enumerate(lens):
+            sink_end = min(w.SINK, L)
+            recent_start = max(sink_end, L - (w.RECENT - 1))
+            n = int(pc[gi])
+            pages = pp[gi, :n].long()
+            rows = torch.cat([torch.arange(sink_end), (w.SINK + pages[:, None] * w.BS + torch.arange(w.BS)).reshape(-1),
+                              torch.arange(recent_start, L + 1)])  # the decode token was appended at row L
+            kk = kc[gi][rows.to(kc.device)].cpu().double()
+            vv = vc[gi][rows.to(vc.device)].cpu().double()
+            masks = torch.cat([torch.full((sink_end,), 0xff), pm[gi, :n].long().repeat_interleave(w.BS),
+                               torch.full((L + 1 - recent_start,), 0xff)])
+            for r in range(w.R):
+                sc = (kk @ q[gi, r]) / math.sqrt(w.D)
+                sc = torch.where(((masks >> r) & 1).bool(), sc, torch.tensor(float("-inf"), dtype=sc.dtype))
+                p = torch.softmax(sc, dim=0)
+                ref = p @ vv
+                e = (out[gi, r] - ref).abs()
+                err = max(err, float(e.max()))
+                ok &= bool((e <= 2e-3 + 1e-2 * ref.abs()).all())
+        # metadata of layer 0's entries == a rebuild over each entry's rows
+        for gi, L in enumerate(lens):
+            keys = w.slab[s][0, gi, :L + 1].to(w.dev)
+            pages = (L + 1 - w.SINK) // w.BS
+            bmin = torch.empty((max(pages, 1), w.D), dtype=keys.dtype, device=w.dev)
+            bmax = torch.empty_like(bmin)
+            kernels.build_page_metadata(keys, sink=w.SINK, block_size=w.BS, page_min=bmin, page_max=bmax)
+            ok &= bool(torch.equal(bmin[:pages].view(torch.int16), w.pmin[s][gi, :pages].view(torch.int16)))
+            ok &= bool(torch.equal(bmax[:pages].view(torch.int16), w.pmax[s][gi, :pages].view(torch.int16)))
+    return ok, err
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "pmc_traffic_quest32k.md"
