@@ -798,12 +798,15 @@ def llama3_8b_config(layers: int = 32):
                        rope_theta=500000.0, rms_norm_eps=1e-5, tie_word_embeddings=False)
 
 
-def tpot_run(model, ids, dev, cache, decode_tokens: int) -> dict:
+def tpot_run(model, ids, dev, cache, decode_tokens: int, graph: bool = False) -> dict:
     """Prefill `ids` into `cache` through the patched model, then decode
-    `decode_tokens` tokens of the fixed id 1; per-token synchronized wall time,
-    p50 and mean over D2..Dn (run_ruler_partial_h2d_tpot_case_v1.py:1302-1322,
-    1897-1906)."""
+    `decode_tokens` tokens of the fixed id 1 -- through the HF forward, or
+    (graph) as replays of one captured decode graph (headinfer.graph_decode;
+    D1 includes its capture); per-token synchronized wall time, p50 and mean
+    over D2..Dn (run_ruler_partial_h2d_tpot_case_v1.py:1302-1322,1897-1906)."""
     import torch
+
+    from headinfer.graph_decode import GraphDecoder
 
     with torch.no_grad():
         t0 = time.perf_counter()
@@ -811,11 +814,15 @@ def tpot_run(model, ids, dev, cache, decode_tokens: int) -> dict:
         torch.cuda.synchronize()
         prefill_s = time.perf_counter() - t0
         tok = torch.ones((1, 1), dtype=torch.long, device=dev)
+        dec = GraphDecoder(model, cache, max_new_tokens=decode_tokens, fixed_token=1) if graph else None
         times = []
         for _ in range(decode_tokens):
             torch.cuda.synchronize()
             t1 = time.perf_counter()
-            model(input_ids=tok, past_key_values=cache, use_cache=True)
+            if dec is not None:
+                dec.step()
+            else:
+                model(input_ids=tok, past_key_values=cache, use_cache=True)
             torch.cuda.synchronize()
             times.append(time.perf_counter() - t1)
     steady = sorted(times[1:]) if len(times) > 1 else times
@@ -851,14 +858,16 @@ def run_tpot(args, dev) -> int:
     mp.mp_headinfer(model)
     ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(5))
     runs = {}
-    for label, pages in (("sparse", args.budget_pages), ("dense", 1 << 20)):
+    for label, pages, graph in (("sparse_graph", args.budget_pages, True), ("dense_graph", 1 << 20, True),
+                                ("sparse_hf_eager", args.budget_pages, False), ("dense_hf_eager", 1 << 20, False)):
         print(f"[bench] tpot {label}: prefill + {n_dec} decode tokens", file=sys.stderr, flush=True)
         cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + n_dec + 8,
-                                                         kv_residency=residency, budget_pages=pages)
-        runs[label] = tpot_run(model, ids, dev, cache, n_dec)
+                                                         kv_residency=residency, budget_pages=pages,
+                                                         update_metadata_on_decode=graph)
+        runs[label] = tpot_run(model, ids, dev, cache, n_dec, graph=graph)
         del cache
         torch.cuda.empty_cache()
-    sp = runs["sparse"]
+    sp = runs["sparse_graph"]
     result = {
         "metric": METRIC, "value": sp["tpot_p50_ms"], "unit": "ms/token (p50 TPOT)", "n_gpus": 1,
         "steps": n_dec, "warmup": 1, "ms_per_step": sp["tpot_p50_ms"], "higher_is_better": False,
@@ -870,7 +879,7 @@ def run_tpot(args, dev) -> int:
                    "layers": args.layers, "context": ctx, "kv_heads": 8, "q_per_kv": 4, "head_dim": 128,
                    "page_size": 16, "budget_pages": args.budget_pages, "sink": 64, "recent": 256},
         "tpot": runs,
-        "sparse_vs_dense_speedup": round(runs["dense"]["tpot_p50_ms"] / sp["tpot_p50_ms"], 3),
+        "sparse_vs_dense_speedup": round(runs["dense_graph"]["tpot_p50_ms"] / sp["tpot_p50_ms"], 3),
     }
     print(json.dumps(result), flush=True)
     return 0
