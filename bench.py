@@ -858,16 +858,25 @@ def run_tpot(args, dev) -> int:
     mp.mp_headinfer(model)
     ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(5))
     runs = {}
-    for label, pages, graph in (("sparse_graph", args.budget_pages, True), ("dense_graph", 1 << 20, True),
-                                ("sparse_hf_eager", args.budget_pages, False), ("dense_hf_eager", 1 << 20, False)):
+    variants = [("sparse_graph", args.budget_pages, True, False), ("dense_graph", 1 << 20, True, False),
+                ("sparse_hf_eager", args.budget_pages, False, False), ("dense_hf_eager", 1 << 20, False, False)]
+    if residency == "host":  # the HBM resident page cache (previous_token_resident_cache) serves host slabs
+        variants[1:1] = [("sparse_graph_resident", args.budget_pages, True, True)]
+        variants[4:4] = [("sparse_hf_eager_resident", args.budget_pages, False, True)]
+    for label, pages, graph, resident in variants:
         print(f"[bench] tpot {label}: prefill + {n_dec} decode tokens", file=sys.stderr, flush=True)
         cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + n_dec + 8,
                                                          kv_residency=residency, budget_pages=pages,
-                                                         update_metadata_on_decode=graph)
+                                                         update_metadata_on_decode=graph,
+                                                         previous_token_resident_cache=resident)
         runs[label] = tpot_run(model, ids, dev, cache, n_dec, graph=graph)
+        if resident:
+            st = cache.resident_stats()
+            runs[label]["resident_hit_ratio"] = round(st["resident_hit_pages"] / max(1, st["union_pages"]), 4)
         del cache
         torch.cuda.empty_cache()
-    sp = runs["sparse_graph"]
+    head = "sparse_graph_resident" if residency == "host" else "sparse_graph"
+    sp = runs[head]
     result = {
         "metric": METRIC, "value": sp["tpot_p50_ms"], "unit": "ms/token (p50 TPOT)", "n_gpus": 1,
         "steps": n_dec, "warmup": 1, "ms_per_step": sp["tpot_p50_ms"], "higher_is_better": False,
@@ -878,6 +887,7 @@ def run_tpot(args, dev) -> int:
                                + ("HBM" if residency == "hbm" else "pinned host memory read zero-copy"),
                    "layers": args.layers, "context": ctx, "kv_heads": 8, "q_per_kv": 4, "head_dim": 128,
                    "page_size": 16, "budget_pages": args.budget_pages, "sink": 64, "recent": 256},
+        "tpot_variant": head,
         "tpot": runs,
         "sparse_vs_dense_speedup": round(runs["dense_graph"]["tpot_p50_ms"] / sp["tpot_p50_ms"], 3),
     }

@@ -320,6 +320,31 @@ int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const vo
                                      const int32_t* lengths, int append, const void* cur_k, const void* cur_v,
                                      float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
                                      void* stream);
+/* Page-tile attention with a resident page cache in HBM, for slabs in host
+ * memory.  Replaces the previous-token resident cache of the Twilight cache
+ * (previous_token_resident_cache, twilight_offload_cache.py:2457-2608,
+ * 3323-3470; hit/miss mapping resident_gpu_mapping.py:14-144), which keeps
+ * the previous token's selected rows on the GPU and fetches only the misses
+ * from the host.  Here every group keeps the K/V pages of its last union in
+ * res_k/res_v [G][2][res_slots][16][D] (16-bit, HBM): a page the previous
+ * step stored is read from there instead of the slab, and every union page
+ * read (hit or miss) is stored into the buffer of this step's parity at its
+ * union index, with res_map[g][page] = (length << 32) | index (int64,
+ * [G][res_map_pages], initialised to -1).  res_stats [G][2] (nullable)
+ * accumulates (hit pages, union pages).  lengths (device, per group) or,
+ * when NULL, `length` for every group gives the window and the decode token
+ * row, which is appended there from cur_k/cur_v when append != 0 -- the
+ * semantics of tw_decode_attention_pages_ragged.  Union indexes at or above
+ * res_slots are read from the slab and not stored. */
+int tw_decode_attention_pages_resident(const void* q, const void* k_base, const void* v_base, int dtype, int G,
+                                       int R, int D, const int32_t* plan_pages, const uint8_t* plan_masks,
+                                       const int32_t* plan_counts, int64_t plan_stride, int max_rows,
+                                       int64_t entry_stride_rows, int sink, int recent, int block_size,
+                                       const int32_t* lengths, int length, int append, const void* cur_k,
+                                       const void* cur_v, float softmax_scale, void* res_k, void* res_v,
+                                       int64_t* res_map, int res_slots, int res_map_pages,
+                                       unsigned long long* res_stats, void* out, void* workspace,
+                                       size_t workspace_bytes, void* stream);
 int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G,
                         int R, int D, const int32_t* rows, const uint8_t* row_masks,
                         const int32_t* row_counts, int64_t rows_stride, int64_t entry_stride_rows,

@@ -467,3 +467,33 @@ def test_fused_affine_int4_qk(H, dev, dtype, D):
             want = oracle.int4_qk(q[g, r].numpy(), pk, s_, m_, dtype, pos[g, r].numpy(), 1.0)
             assert np.array_equal(got[g, r].cpu().numpy().view(np.uint32), want.view(np.uint32))
             assert np.array_equal(mat[g, r].cpu().numpy().view(np.uint32), deq[pos[g, r].numpy()].view(np.uint32))
+
+
+def test_quest_previous_token_resident_cache(H, dev):
+    """previous_token_resident_cache on a host slab: decode_layer outputs and
+    slab contents equal the plain cache's, and later steps hit the HBM
+    resident pages."""
+    G, R, D, T, steps = 4, 4, 128, 3000, 6
+    dtype = "f16"
+    _say("[quest resident cache]")
+    kw = dict(num_cache_entries=G, max_cache_len=T + steps + 2, head_dim=D, num_query_heads_per_kv=R,
+              dtype=torch.float16, device=dev, budget_pages=16, kv_residency="host")
+    plain = H["quest"].QuestTopKOffloadedCache(**kw)
+    res = H["quest"].QuestTopKOffloadedCache(previous_token_resident_cache=True, **kw)
+    model = _Model(G, T, D, dtype, seed=121)
+    model.prefill(plain, dev)
+    model.prefill(res, dev)
+    g = torch.Generator().manual_seed(122)
+    base = torch.randn(G, R, D, generator=g)
+    for step in range(steps):
+        q = (base + 0.1 * torch.randn(G, R, D, generator=g)).to(torch.float16).to(dev)
+        new = [model.new_token(D) for _ in range(G)]
+        nk = torch.stack([k for k, _ in new]).to(dev)
+        nv = torch.stack([v for _, v in new]).to(dev)
+        a = res.decode_layer(queries=q, key_states=nk, value_states=nv, entries=list(range(G)))
+        b = plain.decode_layer(queries=q, key_states=nk, value_states=nv, entries=list(range(G)))
+        torch.cuda.synchronize()
+        assert _same(a, b), step
+    assert _same(res._key_cache, plain._key_cache) and _same(res._value_cache, plain._value_cache)
+    st = res.resident_stats()
+    assert 0 < st["resident_hit_pages"] < st["union_pages"], st

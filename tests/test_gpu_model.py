@@ -126,22 +126,22 @@ def test_patched_llama_matches_dense(dev, kind):
     assert cache.get_seq_length() == T_PROMPT + DECODE_STEPS
 
 
-@pytest.mark.parametrize("residency", ["hbm", "host"])
-def test_graph_decoder_matches_eager(dev, residency):
+@pytest.mark.parametrize("residency,resident", [("hbm", False), ("host", False), ("host", True)])
+def test_graph_decoder_matches_eager(dev, residency, resident):
     """GraphDecoder (one captured graph per token over the ragged kernels)
     == the eager patched model, token by token, with the same cache policy."""
     from headinfer import mp
     from headinfer.graph_decode import GraphDecoder
     from headinfer.quest_offload_cache import QuestTopKOffloadedCache
 
-    _say(f"[graph decoder] {residency}")
+    _say(f"[graph decoder] {residency} resident={resident}")
     steps = 6
     _, gpu = _models(dev)
     mp.mp_headinfer(gpu)
     kw = dict(max_cache_len=T_PROMPT + steps + 2, sink_tokens=64, recent_tokens=256, block_size=16,
               kv_residency=residency, budget_pages=8, update_metadata_on_decode=True)
     eager_cache = QuestTopKOffloadedCache.from_llama_model(gpu, **kw)
-    graph_cache = QuestTopKOffloadedCache.from_llama_model(gpu, **kw)
+    graph_cache = QuestTopKOffloadedCache.from_llama_model(gpu, previous_token_resident_cache=resident, **kw)
     g = torch.Generator().manual_seed(3)
     ids = torch.randint(0, 1000, (1, T_PROMPT), generator=g).to(dev)
     tok = torch.ones((1, 1), dtype=torch.long, device=dev)

@@ -259,3 +259,60 @@ def test_ragged_step_graph_replays_match_eager(K, dev):
         assert torch.equal(graphed["pc"].cpu(), eager["pc"].cpu()), i
         assert same_bits(graphed["out"], eager["out"]), i
         assert same_bits(graphed["k"], eager["k"]) and same_bits(graphed["pmin"], eager["pmin"]), i
+
+
+@pytest.mark.parametrize("ragged", [True, False])
+def test_resident_page_cache_bit_exact(K, dev, ragged):
+    """Host slab, several decode steps with drifting queries: attention with
+    the HBM resident page cache == without it, bit for bit; the resident
+    buffer holds the slab's pages at their union indices; hits are counted."""
+    _say(f"[resident pages] ragged={ragged}")
+    dtype, R, k, steps = "bf16", 4, 16, 5
+    lengths0 = [3000, 3000, 3000] if not ragged else [2500, 3100, 4000]
+    G = len(lengths0)
+    Lmax = max(lengths0) + steps + 16
+    keys = randn((G, Lmax, D), dtype, seed=111)
+    vals = randn((G, Lmax, D), dtype, seed=112)
+    kh, vh = keys.clone().pin_memory(), vals.clone().pin_memory()      # resident-cache run (host slab)
+    kh2, vh2 = keys.clone().pin_memory(), vals.clone().pin_memory()    # plain run (host slab)
+    pmin, pmax = _metadata(keys, lengths0, dtype, dev)
+    P = pmin.shape[1]
+    width = min(P, R * k)
+    res = K.ResidentPages(G, width, P, D, keys.dtype, dev)
+    lengths = torch.tensor(lengths0, dtype=torch.int32, device=dev)
+    g = torch.Generator().manual_seed(113)
+    base = torch.randn((G, R, D), generator=g)
+    for step in range(steps):
+        q = (base + 0.15 * torch.randn((G, R, D), generator=g)).to(torch.bfloat16)
+        ck, cv = randn((G, D), dtype, seed=200 + step), randn((G, D), dtype, seed=300 + step)
+        pp = torch.zeros((G, width), dtype=torch.int32, device=dev)
+        pm = torch.zeros((G, width), dtype=torch.uint8, device=dev)
+        pc = torch.zeros((G,), dtype=torch.int32, device=dev)
+        K.quest_select_ragged(q.float().to(dev), pmin, pmax, lengths, k, sink=SINK, recent=RECENT, block_size=BS,
+                              plan_pages=pp, plan_masks=pm, plan_counts=pc)
+        kw = dict(plan_masks=pm, max_pages=width, sink=SINK, recent=RECENT, block_size=BS, append=True,
+                  cur_k=ck.to(dev), cur_v=cv.to(dev))
+        if ragged:
+            a = K.decode_attention_pages_resident(q.to(dev), kh, vh, pp, pc, res, lengths=lengths, **kw)
+            b = K.decode_attention_pages_ragged(q.to(dev), kh2, vh2, pp, pc, lengths, **kw)
+        else:
+            L = lengths0[0] + step
+            a = K.decode_attention_pages_resident(q.to(dev), kh, vh, pp, pc, res, length=L, **kw)
+            b = K.decode_attention_pages(q.to(dev), kh2, vh2, pp, pc, plan_masks=pm, max_pages=width, sink=SINK,
+                                         recent=RECENT, block_size=BS, length=L, append_position=L,
+                                         cur_k=ck.to(dev), cur_v=cv.to(dev))
+        torch.cuda.synchronize()
+        assert same_bits(a, b), step
+        # this step's buffer == the slab's union pages at their union indices
+        Ls = [L0 + step for L0 in lengths0]
+        for gi in range(G):
+            n = int(pc[gi])
+            pages = pp[gi, :n].long().cpu()
+            rows = (SINK + pages[:, None] * BS + torch.arange(BS)).reshape(-1)
+            par = Ls[gi] & 1
+            assert same_bits(res.k[gi, par, :n].reshape(-1, D), kh[gi][rows]), (step, gi)
+            assert same_bits(res.v[gi, par, :n].reshape(-1, D), vh[gi][rows]), (step, gi)
+        lengths += 1
+    assert same_bits(kh, kh2) and same_bits(vh, vh2)   # the appends landed alike
+    hits, union = res.stats.sum(dim=0).tolist()
+    assert union > 0 and 0 < hits < union, (hits, union)

@@ -92,6 +92,17 @@ struct AttnArgs {
   // (appended there when ragged_append is set).
   const int32_t* lengths;
   int ragged_append;
+  // Resident page cache (page-tile kernel, nullable): group g keeps the K/V
+  // of its union pages in HBM, res_k/res_v [G][2][res_slots][16][D] (two
+  // buffers alternating with the length's parity), and res_map [G]
+  // [res_map_pages] = (length << 32) | slot of the step that last stored
+  // each page.  res_stats [G][2] accumulates (hit pages, union pages).
+  void* res_k;
+  void* res_v;
+  int64_t* res_map;
+  int res_slots;
+  int res_map_pages;
+  unsigned long long* res_stats;
 };
 
 // 8 consecutive channels of one row.
@@ -226,6 +237,7 @@ constexpr int kTileRows = 16;
 struct TileWin {
   int sink_tiles, sink_end, recent_start, n_recent, has_dec, run, run_tiles, nu_cap;
   int append_position;  // the decode token's cache row, -1: none
+  int length;           // tokens before the decode token (the resident cache's epoch)
 };
 
 __device__ __forceinline__ TileWin tile_window(const AttnArgs& a, int g) {
@@ -240,6 +252,7 @@ __device__ __forceinline__ TileWin tile_window(const AttnArgs& a, int g) {
     w.run_tiles = a.t_run_tiles;
     w.nu_cap = a.t_nu_cap;
     w.append_position = a.append_position;
+    w.length = a.length;
     return w;
   }
   const int lmax = static_cast<int>(a.entry_stride) - 1;  // the decode token's row stays in the entry
@@ -254,6 +267,7 @@ __device__ __forceinline__ TileWin tile_window(const AttnArgs& a, int g) {
   w.sink_tiles = (w.sink_end + kTileRows - 1) / kTileRows;
   w.run_tiles = (w.run + kTileRows - 1) / kTileRows;
   w.append_position = a.ragged_append ? L : -1;
+  w.length = L;
   int cap = (a.max_rows - w.sink_end - w.run) / kTileRows;
   const int room = a.max_chunks * a.t_per_chunk - w.sink_tiles - w.run_tiles;
   cap = cap < room ? cap : room;
@@ -1032,6 +1046,8 @@ struct TileSrc {
   int cnt;       // rows of the tile that exist (0..16)
   int dec;       // index of the decode token in the tile, or -1
   uint32_t hm;   // heads that see the tile's cache rows
+  int u;         // union-plan index of a page tile, -1 for sink / recent tiles
+  int page;      // its page id
 };
 
 __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w, int t, int nu, int page,
@@ -1039,6 +1055,8 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
   TileSrc s;
   s.dec = -1;
   s.hm = 0xffu;
+  s.u = -1;
+  s.page = page;
   const int ts = w.sink_tiles;
   if (t < ts) {
     s.pos0 = static_cast<int64_t>(kTileRows) * t;
@@ -1048,6 +1066,7 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
     s.pos0 = a.sink + static_cast<int64_t>(page) * kTileRows;
     s.hm = pmask;
     s.cnt = (s.pos0 >= 0 && s.pos0 + kTileRows <= a.entry_stride) ? kTileRows : 0;
+    s.u = s.cnt > 0 ? t - ts : -1;
   } else {
     const int j0 = kTileRows * (t - ts - nu);
     s.pos0 = static_cast<int64_t>(w.recent_start) + j0;
@@ -1063,7 +1082,7 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
   return s;
 }
 
-template <typename DT, int RMAX, int NW, int TW>
+template <typename DT, int RMAX, int NW, int TW, bool RES>
 __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   using S = typename DT::storage;
   using H = Half8<DT>;
@@ -1131,6 +1150,11 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   const int64_t dec_off = static_cast<int64_t>(win.append_position < 0 ? 0 : win.append_position) * D;
   const S* kdec = a.cur_k != nullptr ? static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D : kg + dec_off;
   const S* vdec = a.cur_v != nullptr ? static_cast<const S*>(a.cur_v) + static_cast<int64_t>(g) * D : vg + dec_off;
+  // resident page cache buffers of this group, in rows: previous step's and this step's
+  constexpr bool res = RES;
+  const int64_t res_base = static_cast<int64_t>(g) * 2 * a.res_slots;
+  const int64_t res_prev = (res_base + static_cast<int64_t>((win.length - 1) & 1) * a.res_slots) * kTileRows;
+  const int64_t res_cur = (res_base + static_cast<int64_t>(win.length & 1) * a.res_slots) * kTileRows;
 
   float m_run[RMAX];
   float o_acc[RMAX][8];
@@ -1152,19 +1176,34 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     TileSrc ts[TW];
     uint4 kf[TW][4];
     uint4 vf[TW][4];
+    // resident page cache: a page stored by the previous step (epoch
+    // length - 1) is read from HBM instead of the slab
+    int hit_slot[TW];
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
       ts[tt] = tile_src(a, win, t0 + tt, nu, page[tt], pmask[tt]);
-      const int64_t tb = ts[tt].pos0 * D;
+      hit_slot[tt] = -1;
+      if (res && ts[tt].u >= 0 && ts[tt].page >= 0 && ts[tt].page < a.res_map_pages) {
+        const int64_t m = a.res_map[static_cast<int64_t>(g) * a.res_map_pages + ts[tt].page];
+        const int slot = static_cast<int>(m & 0xffffffffll);
+        if ((m >> 32) == static_cast<int64_t>(win.length) - 1 && slot >= 0 && slot < a.res_slots) hit_slot[tt] = slot;
+      }
+    }
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+      const bool hit = hit_slot[tt] >= 0;
+      const int64_t tb = hit ? (res_prev + static_cast<int64_t>(hit_slot[tt]) * kTileRows) * D : ts[tt].pos0 * D;
+      const S* kt = hit ? static_cast<const S*>(a.res_k) : kg;
+      const S* vt = hit ? static_cast<const S*>(a.res_v) : vg;
       const int kr = krow < ts[tt].cnt ? krow : 0;
-      const S* kp = krow == ts[tt].dec ? kdec : kg + tb + kr * D;
+      const S* kp = krow == ts[tt].dec ? kdec : kt + tb + kr * D;
 #pragma unroll
       for (int s = 0; s < 4; ++s) kf[tt][s] = *reinterpret_cast<const uint4*>(kp + 32 * s + 8 * quarter);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * rg + j;
         const int vr = r < ts[tt].cnt ? r : 0;
-        const S* vp = r == ts[tt].dec ? vdec : vg + tb + vr * D;
+        const S* vp = r == ts[tt].dec ? vdec : vt + tb + vr * D;
         vf[tt][j] = *reinterpret_cast<const uint4*>(vp + c8);
       }
     }
@@ -1259,6 +1298,30 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
           for (int i = 0; i < 4; ++i) {
             o_acc[h][2 * i] = H::dot2(pp[h], lo[i], o_acc[h][2 * i]);
             o_acc[h][2 * i + 1] = H::dot2(pp[h], hi[i], o_acc[h][2 * i + 1]);
+          }
+        }
+      }
+    }
+    // ---- resident page cache: every union page read goes to this step's buffer ----
+    if (res) {
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt) {
+        if (ts[tt].u < 0 || ts[tt].u >= a.res_slots) continue;
+        const int64_t db = (res_cur + static_cast<int64_t>(ts[tt].u) * kTileRows) * D;
+        S* dk = static_cast<S*>(a.res_k) + db;
+        S* dv = static_cast<S*>(a.res_v) + db;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          *reinterpret_cast<uint4*>(dk + krow * D + 32 * s + 8 * quarter) = kf[tt][s];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(dv + (4 * rg + j) * D + c8) = vf[tt][j];
+        if (lane == 0) {
+          if (ts[tt].page >= 0 && ts[tt].page < a.res_map_pages)
+            a.res_map[static_cast<int64_t>(g) * a.res_map_pages + ts[tt].page] =
+                (static_cast<int64_t>(win.length) << 32) | static_cast<int64_t>(ts[tt].u);
+          if (a.res_stats != nullptr) {
+            atomicAdd(a.res_stats + 2 * g + 1, 1ull);
+            if (hit_slot[tt] >= 0) atomicAdd(a.res_stats + 2 * g, 1ull);
           }
         }
       }
@@ -1506,10 +1569,17 @@ int launch_tiles(const AttnArgs& a, hipStream_t stream) {
   const int phase = a.phase == 0 ? 3 : a.phase;
   if (phase & 1) {
     const dim3 grid(a.G * a.max_chunks);
-    if (a.R <= 4)
-      hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW>), grid, dim3(kTileNW * kWave), 0, stream, a);
-    else
-      hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW>), grid, dim3(kTileNW * kWave), 0, stream, a);
+    const dim3 block(kTileNW * kWave);
+    if (a.res_map != nullptr) {
+      if (a.R <= 4)
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, true>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, true>), grid, block, 0, stream, a);
+    } else if (a.R <= 4) {
+      hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, false>), grid, block, 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, false>), grid, block, 0, stream, a);
+    }
     const int rc = tw_host::check_launch();
     if (rc != TW_OK) return rc;
   }
@@ -1801,29 +1871,38 @@ extern "C" int tw_decode_attention_pages_phase(const void* q, const void* k_base
   return tw::launch_dtype(dtype, a, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const void* v_base, int dtype,
-                                                int G, int R, int D, const int32_t* plan_pages,
-                                                const uint8_t* plan_masks, const int32_t* plan_counts,
-                                                int64_t plan_stride, int max_rows, int64_t entry_stride_rows, int sink,
-                                                int recent, int block_size, const int32_t* lengths, int append,
-                                                const void* cur_k, const void* cur_v, float softmax_scale, void* out,
-                                                void* workspace, size_t workspace_bytes, void* stream) {
-  if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr || lengths == nullptr) return TW_EINVAL;
+namespace tw {
+namespace {
+
+// Page-tile launch with per-group lengths from the device (lengths != NULL)
+// or one host length for every group, optionally with the resident page cache.
+int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R, int D,
+                       const int32_t* plan_pages, const uint8_t* plan_masks, const int32_t* plan_counts,
+                       int64_t plan_stride, int max_rows, int64_t entry_stride_rows, int sink, int recent,
+                       int block_size, const int32_t* lengths, int length, int append, const void* cur_k,
+                       const void* cur_v, float softmax_scale, void* res_k, void* res_v, int64_t* res_map,
+                       int res_slots, int res_map_pages, unsigned long long* res_stats, void* out, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr) return TW_EINVAL;
   if (G <= 0 || R <= 0 || R > 8 || plan_pages == nullptr || plan_counts == nullptr || plan_stride < 1) return TW_EINVAL;
   if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16) return TW_EUNSUPPORTED;
-  if (D != tw::kTileD || block_size != tw::kTileRows) return TW_EUNSUPPORTED;
+  if (D != kTileD || block_size != kTileRows) return TW_EUNSUPPORTED;
   if (sink < 0 || recent <= 0 || entry_stride_rows < 2 || entry_stride_rows > (1ll << 30)) return TW_EINVAL;
-  if (max_rows < sink + recent) return TW_EINVAL;  // every window's sink, recent and decode rows fit
+  if (max_rows < sink + recent) return TW_EINVAL;
   if ((cur_k == nullptr) != (cur_v == nullptr)) return TW_EINVAL;
+  if (lengths == nullptr && (length < 0 || length + 1 > entry_stride_rows)) return TW_EINVAL;
+  if (res_map != nullptr && (res_k == nullptr || res_v == nullptr || res_slots < 1 || res_map_pages < 1))
+    return TW_EINVAL;
   const uintptr_t align = 16;
   if ((reinterpret_cast<uintptr_t>(q) % align) || (reinterpret_cast<uintptr_t>(k_base) % align) ||
       (reinterpret_cast<uintptr_t>(v_base) % align) || (reinterpret_cast<uintptr_t>(cur_k) % align) ||
-      (reinterpret_cast<uintptr_t>(cur_v) % align))
+      (reinterpret_cast<uintptr_t>(cur_v) % align) || (reinterpret_cast<uintptr_t>(res_k) % align) ||
+      (reinterpret_cast<uintptr_t>(res_v) % align))
     return TW_EINVAL;
   size_t ml_off, o_off, total;
-  tw::workspace_layout(G, R, D, max_rows, &ml_off, &o_off, &total);
+  workspace_layout(G, R, D, max_rows, &ml_off, &o_off, &total);
   if (workspace == nullptr || workspace_bytes < total) return TW_ENOMEM;
-  tw::AttnArgs a{};
+  AttnArgs a{};
   a.q = q;
   a.k = k_base;
   a.v = v_base;
@@ -1838,29 +1917,90 @@ extern "C" int tw_decode_attention_pages_ragged(const void* q, const void* k_bas
   a.sink = sink;
   a.recent = recent;
   a.bs = block_size;
-  a.length = 0;
-  a.append_position = -1;
   a.cur_k = cur_k;
   a.cur_v = cur_v;
   if (cur_k != nullptr && append) {
     a.k_append = const_cast<void*>(k_base);
     a.v_append = const_cast<void*>(v_base);
   }
-  a.lengths = lengths;
-  a.ragged_append = append ? 1 : 0;
   a.Hk = 1;
   a.window_left = -1;
-  a.scale_log2 = softmax_scale * tw::kLog2e;
+  a.scale_log2 = softmax_scale * kLog2e;
   a.out = out;
   a.counters = static_cast<unsigned int*>(workspace);
   a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ml_off);
   a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
   a.max_rows = max_rows;
   a.phase = 3;
-  tw::plan_tile_chunks(G, max_rows, &a.iters, &a.max_chunks);
-  a.t_per_chunk = a.iters * tw::kTileNW * tw::kTileTW;
-  // page slots are read from tile ceil(sink / 16) on (every group past its sink window)
-  a.t_sink_tiles = (sink + tw::kTileRows - 1) / tw::kTileRows;
-  return dtype == TW_DTYPE_F16 ? tw::launch_tiles<tw::F16>(a, static_cast<hipStream_t>(stream))
-                               : tw::launch_tiles<tw::BF16>(a, static_cast<hipStream_t>(stream));
+  a.res_k = res_k;
+  a.res_v = res_v;
+  a.res_map = res_map;
+  a.res_slots = res_slots;
+  a.res_map_pages = res_map_pages;
+  a.res_stats = res_stats;
+  plan_tile_chunks(G, max_rows, &a.iters, &a.max_chunks);
+  a.t_per_chunk = a.iters * kTileNW * kTileTW;
+  if (lengths != nullptr) {
+    a.lengths = lengths;
+    a.ragged_append = append ? 1 : 0;
+    a.length = 0;
+    a.append_position = -1;
+    // page slots are read from tile ceil(sink / 16) on (every group past its sink window)
+    a.t_sink_tiles = (sink + kTileRows - 1) / kTileRows;
+  } else {
+    a.length = length;
+    a.append_position = append ? length : -1;
+    const int sink_end = sink < length ? sink : length;
+    const int hist_recent = recent - 1 > 0 ? recent - 1 : 0;
+    const int recent_start = length - hist_recent > sink_end ? length - hist_recent : sink_end;
+    const int has_dec = (cur_k != nullptr || append) ? 1 : 0;
+    const int run = (length - recent_start) + has_dec;
+    a.t_sink_tiles = (sink_end + kTileRows - 1) / kTileRows;
+    a.t_sink_end = sink_end;
+    a.t_recent_start = recent_start;
+    a.t_n_recent = length - recent_start;
+    a.t_has_dec = has_dec;
+    a.t_run = run;
+    a.t_run_tiles = (run + kTileRows - 1) / kTileRows;
+    const int64_t capacity = static_cast<int64_t>(a.max_chunks) * a.t_per_chunk;
+    int64_t cap = (max_rows - sink_end - run) / kTileRows;
+    const int64_t room = capacity - a.t_sink_tiles - a.t_run_tiles;
+    cap = cap < room ? cap : room;
+    cap = cap < plan_stride ? cap : plan_stride;
+    a.t_nu_cap = static_cast<int>(cap < 0 ? 0 : cap);
+  }
+  return dtype == TW_DTYPE_F16 ? launch_tiles<F16>(a, static_cast<hipStream_t>(stream))
+                               : launch_tiles<BF16>(a, static_cast<hipStream_t>(stream));
 }
+
+}  // namespace
+}  // namespace tw
+
+extern "C" int tw_decode_attention_pages_resident(
+    const void* q, const void* k_base, const void* v_base, int dtype, int G, int R, int D, const int32_t* plan_pages,
+    const uint8_t* plan_masks, const int32_t* plan_counts, int64_t plan_stride, int max_rows,
+    int64_t entry_stride_rows, int sink, int recent, int block_size, const int32_t* lengths, int length, int append,
+    const void* cur_k, const void* cur_v, float softmax_scale, void* res_k, void* res_v, int64_t* res_map,
+    int res_slots, int res_map_pages, unsigned long long* res_stats, void* out, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  if (res_map == nullptr) return TW_EINVAL;
+  return tw::pages_tiles_launch(q, k_base, v_base, dtype, G, R, D, plan_pages, plan_masks, plan_counts, plan_stride,
+                                max_rows, entry_stride_rows, sink, recent, block_size, lengths, length, append, cur_k,
+                                cur_v, softmax_scale, res_k, res_v, res_map, res_slots, res_map_pages, res_stats, out,
+                                workspace, workspace_bytes, stream);
+}
+
+extern "C" int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const void* v_base, int dtype,
+                                                int G, int R, int D, const int32_t* plan_pages,
+                                                const uint8_t* plan_masks, const int32_t* plan_counts,
+                                                int64_t plan_stride, int max_rows, int64_t entry_stride_rows, int sink,
+                                                int recent, int block_size, const int32_t* lengths, int append,
+                                                const void* cur_k, const void* cur_v, float softmax_scale, void* out,
+                                                void* workspace, size_t workspace_bytes, void* stream) {
+  if (lengths == nullptr) return TW_EINVAL;
+  return tw::pages_tiles_launch(q, k_base, v_base, dtype, G, R, D, plan_pages, plan_masks, plan_counts, plan_stride,
+                                max_rows, entry_stride_rows, sink, recent, block_size, lengths, 0, append, cur_k,
+                                cur_v, softmax_scale, nullptr, nullptr, nullptr, 0, 0, nullptr, out, workspace,
+                                workspace_bytes, stream);
+}
+

@@ -47,6 +47,9 @@ _HIP_SIGNATURES = {
                                      i32, vp, szt, vp]),
     "tw_decode_attention_pages_ragged": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32,
                                                i32, vp, i32, vp, vp, f32, vp, vp, szt, vp]),
+    "tw_decode_attention_pages_resident": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32,
+                                                 i32, i32, vp, i32, i32, vp, vp, f32, vp, vp, vp, i32, i32, vp, vp,
+                                                 vp, szt, vp]),
     "tw_int4_dequantize": (i32, [vp, vp, vp, i32, i64, i32, vp, vp]),
     "tw_quest_score": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp]),
     "tw_topk_sorted": (i32, [vp, i32, i32, i64, i32, vp, vp]),

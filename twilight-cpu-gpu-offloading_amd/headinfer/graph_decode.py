@@ -125,12 +125,20 @@ class GraphDecoder:
             kernels.quest_select_ragged(qg.float(), c._page_min[e0:e0 + G, :self.P], c._page_max[e0:e0 + G, :self.P],
                                         self.lengths, self.k, sink=c.sink_tokens, recent=c.recent_tokens,
                                         block_size=c.block_size, plan_pages=pp, plan_masks=pm, plan_counts=pc)
-            kernels.decode_attention_pages_ragged(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp, pc,
-                                                  self.lengths, plan_masks=pm, max_pages=self.width,
-                                                  sink=c.sink_tokens, recent=c.recent_tokens,
-                                                  block_size=c.block_size, append=True, cur_k=k.contiguous(),
-                                                  cur_v=v.contiguous(), softmax_scale=float(attn.scaling),
-                                                  out=self.attn[li])
+            if c.previous_token_resident_cache:
+                kernels.decode_attention_pages_resident(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp,
+                                                        pc, c.resident_pages().view(e0, G), lengths=self.lengths,
+                                                        plan_masks=pm, max_pages=self.width, sink=c.sink_tokens,
+                                                        recent=c.recent_tokens, block_size=c.block_size, append=True,
+                                                        cur_k=k.contiguous(), cur_v=v.contiguous(),
+                                                        softmax_scale=float(attn.scaling), out=self.attn[li])
+            else:
+                kernels.decode_attention_pages_ragged(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp,
+                                                      pc, self.lengths, plan_masks=pm, max_pages=self.width,
+                                                      sink=c.sink_tokens, recent=c.recent_tokens,
+                                                      block_size=c.block_size, append=True, cur_k=k.contiguous(),
+                                                      cur_v=v.contiguous(), softmax_scale=float(attn.scaling),
+                                                      out=self.attn[li])
             kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
                                                 block_size=c.block_size, page_min=c._page_min, page_max=c._page_max)
             h = h + attn.o_proj(self.attn[li].view(1, Hq * D))

@@ -803,6 +803,105 @@ def decode_attention_pages_ragged(
     return out
 
 
+class ResidentPages:
+    """HBM resident page cache of G groups (one layer's entries) for a slab
+    in host memory: K/V buffers [G, 2, slots, 16, D], the page map [G, pages]
+    int64 (-1 = never stored) and stats [G, 2] (hit pages, union pages)."""
+
+    def __init__(self, groups: int, slots: int, pages: int, head_dim: int, dtype: torch.dtype,
+                 device: torch.device) -> None:
+        self.k = torch.empty((groups, 2, slots, 16, head_dim), dtype=dtype, device=device)
+        self.v = torch.empty_like(self.k)
+        self.map = torch.full((groups, pages), -1, dtype=torch.int64, device=device)
+        self.stats = torch.zeros((groups, 2), dtype=torch.int64, device=device)
+        self.slots, self.pages = slots, pages
+
+    def view(self, g0: int, n: int) -> "ResidentPages":
+        out = ResidentPages.__new__(ResidentPages)
+        out.k, out.v = self.k[g0:g0 + n], self.v[g0:g0 + n]
+        out.map, out.stats = self.map[g0:g0 + n], self.stats[g0:g0 + n]
+        out.slots, out.pages = self.slots, self.pages
+        return out
+
+
+def decode_attention_pages_resident(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    plan_pages: torch.Tensor,
+    plan_counts: torch.Tensor,
+    resident: ResidentPages,
+    *,
+    lengths: Optional[torch.Tensor] = None,
+    length: int = 0,
+    plan_masks: Optional[torch.Tensor] = None,
+    max_pages: int,
+    sink: int,
+    recent: int,
+    block_size: int = 16,
+    append: bool = True,
+    cur_k: Optional[torch.Tensor] = None,
+    cur_v: Optional[torch.Tensor] = None,
+    softmax_scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """decode_attention_pages (lengths None: one `length`) or its ragged form
+    (lengths [G] int32 on the device), with union pages kept in an HBM
+    resident page cache: pages the previous step stored are read from HBM,
+    the rest from the slab, and every union page read is stored for the next
+    step.  16-bit K/V, D = 128, block_size 16.  Returns [G, R, D]."""
+    if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("q must be [G, R, D] fp16/bf16")
+    G, R, D = q.shape
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or k_cache.shape != v_cache.shape \
+            or k_cache.ndim != 3 or k_cache.shape[0] != G or k_cache.shape[2] != D \
+            or k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1 or k_cache.stride(1) != D \
+            or k_cache.stride(0) % D:
+        raise ValueError("K/V cache must be row-contiguous [G, Lmax, D] in q's dtype")
+    if plan_pages.dtype != torch.int32 or plan_pages.ndim != 2 or plan_pages.shape[0] != G \
+            or plan_pages.stride(1) != 1:
+        raise ValueError("plan_pages must be [G, stride] int32")
+    if plan_masks is not None and (plan_masks.dtype != torch.uint8 or plan_masks.shape != plan_pages.shape
+                                   or plan_masks.stride() != plan_pages.stride()):
+        raise ValueError("plan_masks must match plan_pages")
+    if plan_counts.dtype != torch.int32 or tuple(plan_counts.shape) != (G,):
+        raise ValueError("plan_counts must be [G] int32")
+    if lengths is not None and (lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,)
+                                or not lengths.is_contiguous()):
+        raise ValueError("lengths must be contiguous [G] int32")
+    rk, rv, rm, rs = resident.k, resident.v, resident.map, resident.stats
+    if rk.dtype != q.dtype or tuple(rk.shape) != (G, 2, resident.slots, 16, D) or not rk.is_contiguous() \
+            or rv.shape != rk.shape or not rv.is_contiguous() or rm.dtype != torch.int64 \
+            or tuple(rm.shape) != (G, resident.pages) or not rm.is_contiguous() \
+            or tuple(rs.shape) != (G, 2) or not rs.is_contiguous():
+        raise ValueError("resident buffers do not match the launch")
+    if not 0 <= max_pages <= plan_pages.shape[1]:
+        raise ValueError("max_pages must be within the plan width")
+    if (cur_k is None) != (cur_v is None):
+        raise ValueError("cur_k and cur_v go together")
+    if cur_k is not None and (cur_k.shape != (G, D) or cur_k.dtype != q.dtype or cur_v.shape != cur_k.shape
+                              or cur_v.dtype != q.dtype):
+        raise ValueError("cur_k/cur_v must be [G, D] in q's dtype")
+    dev = _require_device(q, plan_pages, plan_masks, plan_counts, lengths, cur_k, cur_v, rk, rv, rm, rs,
+                          what="decode_attention_pages_resident")
+    kp, vp = _slab_source(k_cache, v_cache)
+    _require_contiguous(q, cur_k, cur_v, what="decode_attention_pages_resident")
+    if out is None:
+        out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    max_rows = sink + max_pages * block_size + recent
+    nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
+    ws = WORKSPACE.get(dev, "decode_attention", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_decode_attention_pages_resident(
+            ptr(q), kp, vp, _dt(q), G, R, D, ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
+            plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink, recent, block_size, ptr(lengths),
+            int(length), int(bool(append)), ptr(cur_k), ptr(cur_v), scale, ptr(rk), ptr(rv), ptr(rm),
+            resident.slots, resident.pages, ptr(rs), ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
+            "decode_attention_pages_resident")
+    return out
+
+
 def decode_attention_varlen(
     q: torch.Tensor,
     k: torch.Tensor,

@@ -88,6 +88,7 @@ class QuestTopKOffloadedCache(_CacheBase):
         kv_residency: str = "host",
         budget_pages: Optional[int] = None,
         update_metadata_on_decode: bool = False,
+        previous_token_resident_cache: bool = False,
     ) -> None:
         super().__init__()
         device = torch.device(device)
@@ -143,6 +144,13 @@ class QuestTopKOffloadedCache(_CacheBase):
         # also writes the new row's metadata (pages completed during decode
         # become candidates).
         self.update_metadata_on_decode = bool(update_metadata_on_decode)
+        # The reference's previous-token resident cache (twilight_offload_cache.py:2457-2608): union pages
+        # stay in an HBM page cache and only the pages the previous step did not read cross the host link.
+        self.previous_token_resident_cache = bool(previous_token_resident_cache)
+        if self.previous_token_resident_cache and (kv_residency != "host" or block_size != 16 or head_dim != 128
+                                                   or dtype == torch.float32):
+            raise ValueError("the resident page cache serves a host slab of 16-bit K/V, head_dim 128, 16-row pages")
+        self._resident: Optional[kernels.ResidentPages] = None
 
         self._bookkeeping = SequentialCacheState(num_cache_entries, max_cache_len)
         self._logical_lengths = self._bookkeeping.logical_lengths
@@ -298,6 +306,7 @@ class QuestTopKOffloadedCache(_CacheBase):
             "layer_batched_selection": self.layer_batched_selection,
             "layer_flat_ragged_execution": self.layer_flat_ragged_execution,
             "update_metadata_on_decode": self.update_metadata_on_decode,
+            "previous_token_resident_cache": self.previous_token_resident_cache,
             "logical_lengths": list(self._logical_lengths),
             "seen_tokens": self._seen_tokens,
             "prompt_length": self._prompt_length,
@@ -663,6 +672,31 @@ class QuestTopKOffloadedCache(_CacheBase):
         return self._flat_keys[:total], self._flat_values[:total], cu, T, lengths
 
     # ------------------------------------------------------------ fast path
+    def resident_pages(self) -> "kernels.ResidentPages":
+        """The HBM resident page cache of every entry (allocated on first use):
+        slots for the widest union plan the budget allows, a map over every
+        page the metadata can hold."""
+        if self._resident is None:
+            if self._page_min is None:
+                raise RuntimeError("prompt metadata is missing")
+            G_all, D = self.geometry.num_entries, self.geometry.head_dim
+            pages = max(1, int(self._page_min.shape[1]))
+            budget = (self.budget_pages if self.budget_pages is not None else
+                      max(1, math.ceil(self.max_selected_history_fraction * max(1, (self.geometry.max_cache_len
+                                                                                    - self.sink_tokens)
+                                                                                   // self.block_size))))
+            slots = max(1, min(pages, self.num_query_heads_per_kv * budget))
+            self._resident = kernels.ResidentPages(G_all, slots, pages, D, self.dtype, self.device)
+        return self._resident
+
+    def resident_stats(self) -> Dict[str, int]:
+        """Pages served from the HBM resident cache vs. all union pages read
+        (cumulative; synchronizes the device)."""
+        if self._resident is None:
+            return {"resident_hit_pages": 0, "union_pages": 0}
+        st = self._resident.stats.sum(dim=0).tolist()
+        return {"resident_hit_pages": int(st[0]), "union_pages": int(st[1])}
+
     def decode_layer(self, *, queries: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
                      entries: Sequence[int], softmax_scale: Optional[float] = None,
                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -703,11 +737,19 @@ class QuestTopKOffloadedCache(_CacheBase):
                                  plan_masks=plan_masks, plan_counts=plan_counts)
         self._phase_end("selector", start)
         start = self._phase_start()
-        result = kernels.decode_attention_pages(
-            queries.contiguous(), slab_k, slab_v, plan_pages, plan_counts, plan_masks=plan_masks,
-            max_pages=width if k > 0 else 0, sink=self.sink_tokens, recent=self.recent_tokens,
-            block_size=self.block_size, length=old_length, append_position=old_length,
-            cur_k=key_states.contiguous(), cur_v=value_states.contiguous(), softmax_scale=softmax_scale, out=out)
+        if self.previous_token_resident_cache:
+            result = kernels.decode_attention_pages_resident(
+                queries.contiguous(), slab_k, slab_v, plan_pages, plan_counts, self.resident_pages().view(e0, G),
+                length=old_length, plan_masks=plan_masks, max_pages=width if k > 0 else 0, sink=self.sink_tokens,
+                recent=self.recent_tokens, block_size=self.block_size, append=True, cur_k=key_states.contiguous(),
+                cur_v=value_states.contiguous(), softmax_scale=softmax_scale, out=out)
+        else:
+            result = kernels.decode_attention_pages(
+                queries.contiguous(), slab_k, slab_v, plan_pages, plan_counts, plan_masks=plan_masks,
+                max_pages=width if k > 0 else 0, sink=self.sink_tokens, recent=self.recent_tokens,
+                block_size=self.block_size, length=old_length, append_position=old_length,
+                cur_k=key_states.contiguous(), cur_v=value_states.contiguous(), softmax_scale=softmax_scale,
+                out=out)
         self._phase_end("attention", start)
         self._update_decode_metadata(entries, old_length)
         for e in entries:
