@@ -416,6 +416,26 @@ int tw_append_kv(const void* new_k, const void* new_v, int n_entries, int D, int
                  void* dst_k, void* dst_v, int64_t entry_stride_rows, int first_entry,
                  int64_t position, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Element-wise steps of the graph-captured decode token around the sparse
+ * path (16-bit activations).  No counterpart in the reference's path: they
+ * stand for the HF modules the reference runs unpatched, with their rounding
+ * steps (each element-wise op in fp32, rounded to the activation dtype).
+ *   tw_add_rms_norm: h = h + delta (delta nullable), out = weight *
+ *     (h * rsqrt(mean(h^2) + eps)) -- the decoder layer's residual add and
+ *     LlamaRMSNorm; h [rows][H] updated in place.
+ *   tw_rope_qk: apply_rotary_pos_emb of q [Hq][D] and k [Hk][D] in place at
+ *     the position *position (device int64) of the cos/sin tables
+ *     [positions][D]; q32 (nullable) [Hq][D] receives q in fp32.
+ *   tw_silu_mul: out[i] = silu(gate_up[i]) * gate_up[I + i] (LlamaMLP's
+ *     act_fn(gate_proj(x)) * up_proj(x) over a fused gate/up projection).
+ * ---------------------------------------------------------------------- */
+int tw_add_rms_norm(void* h, const void* delta, const void* weight, float eps, void* out, int rows, int H,
+                    int dtype, void* stream);
+int tw_rope_qk(void* q, void* k, int Hq, int Hk, int D, const void* cos_table, const void* sin_table,
+               const int64_t* position, float* q32, int dtype, void* stream);
+int tw_silu_mul(const void* gate_up, void* out, int I, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -13,9 +13,16 @@ runner decodes, run_ruler_partial_h2d_tpot_case_v1.py:1302-1322).
 Nothing in the graph depends on a host-side length: the token id, the
 position and the cache length live in device memory and advance at the end
 of the graph, and the ragged kernels derive each group's window, candidate
-pages and decode row from the length.  The per-layer arithmetic is the HF
-modules' own (same ops, same operand shapes), so logits follow the eager
-patched model.  Quest selection with an absolute budget (``budget_pages``),
+pages and decode row from the length.  A layer is 13 launches: residual add
++ RMSNorm, one q/k/v GEMM, RoPE (which also writes q in fp32 for the Quest
+score), the Quest score and top-k, the page-tile attention and its merge,
+the metadata update, the output GEMM, residual add + RMSNorm, one gate/up
+GEMM, SiLU * up and the down GEMM.  The q/k/v and gate/up weights are
+concatenated once and the HF modules keep views into them, so the model's
+own forward (the prefill) uses the same storage.  The element-wise kernels
+repeat the HF modules' rounding steps; the fused GEMMs and the RMSNorm
+reduction order differ, so logits follow the eager patched model to bf16
+rounding.  Quest selection with an absolute budget (``budget_pages``),
 16-row pages, head_dim 128 and 16-bit K/V only (the page-tile kernel); the
 cache must be built with ``update_metadata_on_decode=True`` so pages
 completed during decode are scored.  While the decoder runs it owns the
@@ -32,19 +39,6 @@ import torch.nn.functional as F
 from . import kernels
 
 __all__ = ["GraphDecoder"]
-
-
-def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """LlamaRMSNorm / Qwen2RMSNorm: fp32 variance, scale in the input dtype."""
-    dtype = x.dtype
-    h = x.to(torch.float32)
-    h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
-    return weight * h.to(dtype)
-
-
-def _rotate_half(x: torch.Tensor) -> torch.Tensor:
-    half = x.shape[-1] // 2
-    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
 
 
 class GraphDecoder:
@@ -95,6 +89,33 @@ class GraphDecoder:
         dummy = torch.zeros((1, 1, self.D), dtype=cache.dtype, device=dev)
         cos, sin = inner.rotary_emb(dummy, torch.arange(npos, device=dev)[None])
         self.cos, self.sin = cos[0].contiguous(), sin[0].contiguous()
+        # fused projections: one q/k/v and one gate/up weight per layer, the HF modules keep views
+        self.wqkv, self.bqkv, self.wgu = [], [], []
+        with torch.no_grad():
+            for layer in self.layers:
+                at, mlp = layer.self_attn, layer.mlp
+                projs = (at.q_proj, at.k_proj, at.v_proj)
+                w = torch.cat([p.weight for p in projs]).contiguous()
+                b = torch.cat([p.bias for p in projs]).contiguous() if at.q_proj.bias is not None else None
+                o = 0
+                for p in projs:
+                    n = p.weight.shape[0]
+                    p.weight.data = w[o:o + n]
+                    if b is not None:
+                        p.bias.data = b[o:o + n]
+                    o += n
+                gu = torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight]).contiguous()
+                ni = mlp.gate_proj.weight.shape[0]
+                mlp.gate_proj.weight.data = gu[:ni]
+                mlp.up_proj.weight.data = gu[ni:]
+                self.wqkv.append(w)
+                self.bqkv.append(b)
+                self.wgu.append(gu)
+        self.I = self.wgu[0].shape[0] // 2
+        hidden = cfg.hidden_size
+        self.x = torch.empty((1, hidden), dtype=cache.dtype, device=dev)
+        self.q32 = torch.empty((self.Hq, self.D), dtype=torch.float32, device=dev)
+        self.m = torch.empty((1, self.I), dtype=cache.dtype, device=dev)
         # per-layer buffers
         self.plan = [(torch.zeros((self.G, self.width), dtype=torch.int32, device=dev),
                       torch.zeros((self.G, self.width), dtype=torch.uint8, device=dev),
@@ -108,45 +129,48 @@ class GraphDecoder:
         c = self.cache
         G, R, D, Hq = self.G, self.R, self.D, self.Hq
         inner = self.model.model
-        h = F.embedding(self.token, inner.embed_tokens.weight)          # [1, hidden]
-        cos = self.cos.index_select(0, self.position)                   # [1, D]
-        sin = self.sin.index_select(0, self.position)
+        h = F.embedding(self.token, inner.embed_tokens.weight)          # [1, hidden], the residual stream
+        x = self.x
+        delta: Optional[torch.Tensor] = None
         for li, layer in enumerate(self.layers):
             attn = layer.self_attn
-            x = _rms_norm(h, layer.input_layernorm.weight, layer.input_layernorm.variance_epsilon)
-            q = attn.q_proj(x).view(Hq, D)
-            k = attn.k_proj(x).view(G, D)
-            v = attn.v_proj(x).view(G, D)
-            q = (q * cos) + (_rotate_half(q) * sin)
-            k = (k * cos) + (_rotate_half(k) * sin)
-            qg = q.view(G, R, D).contiguous()
+            norm = layer.input_layernorm
+            kernels.add_rms_norm(h, delta, norm.weight, norm.variance_epsilon, x)
+            qkv = F.linear(x, self.wqkv[li], self.bqkv[li])[0]
+            q = qkv[:Hq * D].view(Hq, D)
+            k = qkv[Hq * D:(Hq + G) * D].view(G, D)
+            v = qkv[(Hq + G) * D:].view(G, D)
+            kernels.rope_qk(q, k, self.cos, self.sin, self.position, self.q32)
+            qg = q.view(G, R, D)
             e0 = li * G
             pp, pm, pc = self.plan[li]
-            kernels.quest_select_ragged(qg.float(), c._page_min[e0:e0 + G, :self.P], c._page_max[e0:e0 + G, :self.P],
-                                        self.lengths, self.k, sink=c.sink_tokens, recent=c.recent_tokens,
-                                        block_size=c.block_size, plan_pages=pp, plan_masks=pm, plan_counts=pc)
+            kernels.quest_select_ragged(self.q32.view(G, R, D), c._page_min[e0:e0 + G, :self.P],
+                                        c._page_max[e0:e0 + G, :self.P], self.lengths, self.k, sink=c.sink_tokens,
+                                        recent=c.recent_tokens, block_size=c.block_size, plan_pages=pp,
+                                        plan_masks=pm, plan_counts=pc)
             if c.previous_token_resident_cache:
                 kernels.decode_attention_pages_resident(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp,
                                                         pc, c.resident_pages().view(e0, G), lengths=self.lengths,
                                                         plan_masks=pm, max_pages=self.width, sink=c.sink_tokens,
                                                         recent=c.recent_tokens, block_size=c.block_size, append=True,
-                                                        cur_k=k.contiguous(), cur_v=v.contiguous(),
-                                                        softmax_scale=float(attn.scaling), out=self.attn[li])
+                                                        cur_k=k, cur_v=v, softmax_scale=float(attn.scaling),
+                                                        out=self.attn[li])
             else:
                 kernels.decode_attention_pages_ragged(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp,
                                                       pc, self.lengths, plan_masks=pm, max_pages=self.width,
                                                       sink=c.sink_tokens, recent=c.recent_tokens,
-                                                      block_size=c.block_size, append=True, cur_k=k.contiguous(),
-                                                      cur_v=v.contiguous(), softmax_scale=float(attn.scaling),
-                                                      out=self.attn[li])
+                                                      block_size=c.block_size, append=True, cur_k=k, cur_v=v,
+                                                      softmax_scale=float(attn.scaling), out=self.attn[li])
             kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
                                                 block_size=c.block_size, page_min=c._page_min, page_max=c._page_max)
-            h = h + attn.o_proj(self.attn[li].view(1, Hq * D))
-            x = _rms_norm(h, layer.post_attention_layernorm.weight, layer.post_attention_layernorm.variance_epsilon)
-            mlp = layer.mlp
-            h = h + mlp.down_proj(mlp.act_fn(mlp.gate_proj(x)) * mlp.up_proj(x))
-        h = _rms_norm(h, inner.norm.weight, inner.norm.variance_epsilon)
-        logits = self.model.lm_head(h)
+            o = attn.o_proj(self.attn[li].view(1, Hq * D))
+            norm = layer.post_attention_layernorm
+            kernels.add_rms_norm(h, o, norm.weight, norm.variance_epsilon, x)
+            gu = F.linear(x, self.wgu[li])
+            kernels.silu_mul(gu, self.m)
+            delta = layer.mlp.down_proj(self.m)
+        kernels.add_rms_norm(h, delta, inner.norm.weight, inner.norm.variance_epsilon, x)
+        logits = self.model.lm_head(x)
         if self.logits is None:
             self.logits = torch.empty_like(logits)
         self.logits.copy_(logits)

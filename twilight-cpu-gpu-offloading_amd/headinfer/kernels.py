@@ -1157,3 +1157,58 @@ def host_gather_kv(k: torch.Tensor, v: torch.Tensor, rows: torch.Tensor, out_k: 
                                           int(threads or torch.get_num_threads()))
     if rc:
         raise ValueError("row index out of bounds")
+
+
+# ------------------------------------------------- decode-step element-wise
+def add_rms_norm(h: torch.Tensor, delta: Optional[torch.Tensor], weight: torch.Tensor, eps: float,
+                 out: torch.Tensor) -> torch.Tensor:
+    """h += delta (when given), out = weight * rms_norm(h): the decoder layer's
+    residual add and LlamaRMSNorm in one launch.  h/delta/out [rows, H]
+    contiguous fp16/bf16, weight [H]."""
+    if h.dtype not in (torch.float16, torch.bfloat16) or h.ndim != 2 or not h.is_contiguous():
+        raise ValueError("h must be contiguous [rows, H] fp16/bf16")
+    rows, H = h.shape
+    for t in (delta, out):
+        if t is not None and (t.shape != h.shape or t.dtype != h.dtype or not t.is_contiguous()):
+            raise ValueError("delta/out must match h")
+    if weight.shape != (H,) or weight.dtype != h.dtype or not weight.is_contiguous():
+        raise ValueError("weight must be [H] in h's dtype")
+    dev = _require_device(h, delta, weight, out, what="add_rms_norm")
+    with torch.cuda.device(dev):
+        check(hip().tw_add_rms_norm(ptr(h), ptr(delta), ptr(weight), float(eps), ptr(out), rows, H, _dt(h),
+                                    stream_handle(dev)), "add_rms_norm")
+    return out
+
+
+def rope_qk(q: torch.Tensor, k: torch.Tensor, cos_table: torch.Tensor, sin_table: torch.Tensor,
+            position: torch.Tensor, q32: Optional[torch.Tensor] = None) -> None:
+    """apply_rotary_pos_emb of q [Hq, D] and k [Hk, D] in place at the device
+    position (int64 [1]) of the cos/sin tables [positions, D]; q32 [Hq, D]
+    fp32 receives the rotated q."""
+    if q.ndim != 2 or k.ndim != 2 or q.shape[1] != k.shape[1] or q.dtype != k.dtype \
+            or q.dtype not in (torch.float16, torch.bfloat16) or not q.is_contiguous() or not k.is_contiguous():
+        raise ValueError("q [Hq, D] and k [Hk, D] must be contiguous fp16/bf16")
+    D = q.shape[1]
+    if cos_table.dtype != q.dtype or sin_table.shape != cos_table.shape or cos_table.ndim != 2 \
+            or cos_table.shape[1] != D or not cos_table.is_contiguous() or not sin_table.is_contiguous():
+        raise ValueError("cos/sin tables must be contiguous [positions, D] in q's dtype")
+    if position.dtype != torch.int64 or position.numel() != 1:
+        raise ValueError("position must be one int64")
+    if q32 is not None and (q32.dtype != torch.float32 or q32.shape != q.shape or not q32.is_contiguous()):
+        raise ValueError("q32 must be contiguous fp32 like q")
+    dev = _require_device(q, k, cos_table, sin_table, position, q32, what="rope_qk")
+    with torch.cuda.device(dev):
+        check(hip().tw_rope_qk(ptr(q), ptr(k), q.shape[0], k.shape[0], D, ptr(cos_table), ptr(sin_table),
+                               ptr(position), ptr(q32), _dt(q), stream_handle(dev)), "rope_qk")
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out = silu(gate_up[..., :I]) * gate_up[..., I:] for one row."""
+    if gate_up.dtype not in (torch.float16, torch.bfloat16) or not gate_up.is_contiguous() \
+            or gate_up.numel() % 2 or out.dtype != gate_up.dtype or not out.is_contiguous() \
+            or out.numel() * 2 != gate_up.numel():
+        raise ValueError("gate_up [2I] and out [I] must be contiguous fp16/bf16")
+    dev = _require_device(gate_up, out, what="silu_mul")
+    with torch.cuda.device(dev):
+        check(hip().tw_silu_mul(ptr(gate_up), ptr(out), out.numel(), _dt(out), stream_handle(dev)), "silu_mul")
+    return out
