@@ -162,3 +162,57 @@ def test_graph_decoder_matches_eager(dev, residency, resident):
         a = graph_cache._key_cache[e, :L].float().cpu()
         b = eager_cache._key_cache[e, :L].float().cpu()
         assert torch.allclose(a, b, atol=2e-2, rtol=2e-2), e
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_step_ops_match_hf_modules(dev, dtype):
+    """The graph decoder's fused element-wise kernels against the HF modules
+    they stand for, run on the CPU in the same dtype: RoPE bit for bit;
+    residual add + RMSNorm and SiLU * up within one unit in the last place
+    (reduction order and exp may differ)."""
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm, apply_rotary_pos_emb
+
+    from headinfer import kernels
+
+    g = torch.Generator().manual_seed(7)
+    H, Hq, Hk, D, I = 4096, 32, 8, 128, 14336
+    # residual add + RMSNorm
+    h = (torch.randn((1, H), generator=g) * 3).to(dtype)
+    delta = torch.randn((1, H), generator=g).to(dtype)
+    norm = LlamaRMSNorm(H, eps=1e-5)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(H, generator=g))
+    norm = norm.to(dtype)
+    ref_h = h + delta
+    with torch.no_grad():
+        ref = norm(ref_h)
+    hd, out = h.to(dev), torch.empty((1, H), dtype=dtype, device=dev)
+    kernels.add_rms_norm(hd, delta.to(dev), norm.weight.to(dev), 1e-5, out)
+    torch.cuda.synchronize()
+    assert torch.equal(hd.cpu().view(torch.int16), ref_h.view(torch.int16))
+    ulp = (out.cpu().view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+    assert int(ulp.max()) <= 1 and float((ulp == 0).float().mean()) > 0.95
+    # RoPE at a device position
+    q = torch.randn((Hq, D), generator=g).to(dtype)
+    k = torch.randn((Hk, D), generator=g).to(dtype)
+    pos = 777
+    inv = 1.0 / (500000.0 ** (torch.arange(0, D, 2).float() / D))
+    ang = torch.outer(torch.arange(1024).float(), inv)
+    emb = torch.cat([ang, ang], dim=-1)
+    cos, sin = emb.cos().to(dtype), emb.sin().to(dtype)
+    rq, rk = apply_rotary_pos_emb(q[None, :, None], k[None, :, None], cos[pos:pos + 1][None], sin[pos:pos + 1][None])
+    qd, kd = q.to(dev), k.to(dev)
+    q32 = torch.empty((Hq, D), dtype=torch.float32, device=dev)
+    kernels.rope_qk(qd, kd, cos.to(dev), sin.to(dev), torch.tensor([pos], device=dev), q32)
+    torch.cuda.synchronize()
+    assert torch.equal(qd.cpu().view(torch.int16), rq[0, :, 0].contiguous().view(torch.int16))
+    assert torch.equal(kd.cpu().view(torch.int16), rk[0, :, 0].contiguous().view(torch.int16))
+    assert torch.equal(q32.cpu(), rq[0, :, 0].float())
+    # SiLU * up
+    gu = (torch.randn((1, 2 * I), generator=g) * 2).to(dtype)
+    ref = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]
+    m = torch.empty((1, I), dtype=dtype, device=dev)
+    kernels.silu_mul(gu.to(dev), m)
+    torch.cuda.synchronize()
+    ulp = (m.cpu().view(torch.int16).int() - ref.view(torch.int16).int()).abs()
+    assert int(ulp.max()) <= 1 and float((ulp == 0).float().mean()) > 0.95
