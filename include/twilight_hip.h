@@ -423,7 +423,8 @@ int tw_append_kv(const void* new_k, const void* new_v, int n_entries, int D, int
  * steps (each element-wise op in fp32, rounded to the activation dtype).
  *   tw_add_rms_norm: h = h + delta (delta nullable), out = weight *
  *     (h * rsqrt(mean(h^2) + eps)) -- the decoder layer's residual add and
- *     LlamaRMSNorm; h [rows][H] updated in place.
+ *     LlamaRMSNorm; h [rows][H] updated in place.  H % 8 == 0, H <= 8192,
+ *     16-byte aligned rows.
  *   tw_rope_qk: apply_rotary_pos_emb of q [Hq][D] and k [Hk][D] in place at
  *     the position *position (device int64) of the cos/sin tables
  *     [positions][D]; q32 (nullable) [Hq][D] receives q in fp32.
@@ -435,6 +436,10 @@ int tw_add_rms_norm(void* h, const void* delta, const void* weight, float eps, v
 int tw_rope_qk(void* q, void* k, int Hq, int Hk, int D, const void* cos_table, const void* sin_table,
                const int64_t* position, float* q32, int dtype, void* stream);
 int tw_silu_mul(const void* gate_up, void* out, int I, int dtype, void* stream);
+/* tw_gemv: y [N] = x [K] . W[n][:] (+ bias [N], nullable) for one token,
+ * W [N][K] row-major (nn.Linear's weight), fp32 accumulation, output in the
+ * 16-bit dtype.  K % 8 == 0, K <= 32768, 16-byte aligned W and x. */
+int tw_gemv(const void* W, const void* x, const void* bias, void* y, int N, int K, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -208,6 +208,17 @@ def test_decode_step_ops_match_hf_modules(dev, dtype):
     assert torch.equal(qd.cpu().view(torch.int16), rq[0, :, 0].contiguous().view(torch.int16))
     assert torch.equal(kd.cpu().view(torch.int16), rk[0, :, 0].contiguous().view(torch.int16))
     assert torch.equal(q32.cpu(), rq[0, :, 0].float())
+    # one-token GEMV (nn.Linear) against an fp32 matmul of the same operands
+    for N, Kd, with_bias in ((6144, 4096, True), (4096, 14336, False), (1000, 256, True)):
+        W = (torch.randn((N, Kd), generator=g) * 0.02).to(dtype)
+        xv = torch.randn((1, Kd), generator=g).to(dtype)
+        b = torch.randn(N, generator=g).to(dtype) if with_bias else None
+        ref = xv.float() @ W.float().T + (b.float() if b is not None else 0.0)
+        y = torch.empty((1, N), dtype=dtype, device=dev)
+        kernels.gemv(xv.to(dev), W.to(dev), None if b is None else b.to(dev), y)
+        torch.cuda.synchronize()
+        err = (y.cpu().float() - ref).abs()
+        assert bool((err <= 1e-2 * ref.abs() + 2e-3).all()), (N, Kd, float(err.max()))
     # SiLU * up
     gu = (torch.randn((1, 2 * I), generator=g) * 2).to(dtype)
     ref = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]

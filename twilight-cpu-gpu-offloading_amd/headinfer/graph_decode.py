@@ -14,15 +14,15 @@ Nothing in the graph depends on a host-side length: the token id, the
 position and the cache length live in device memory and advance at the end
 of the graph, and the ragged kernels derive each group's window, candidate
 pages and decode row from the length.  A layer is 13 launches: residual add
-+ RMSNorm, one q/k/v GEMM, RoPE (which also writes q in fp32 for the Quest
++ RMSNorm, one q/k/v GEMV, RoPE (which also writes q in fp32 for the Quest
 score), the Quest score and top-k, the page-tile attention and its merge,
-the metadata update, the output GEMM, residual add + RMSNorm, one gate/up
-GEMM, SiLU * up and the down GEMM.  The q/k/v and gate/up weights are
-concatenated once and the HF modules keep views into them, so the model's
-own forward (the prefill) uses the same storage.  The element-wise kernels
-repeat the HF modules' rounding steps; the fused GEMMs and the RMSNorm
-reduction order differ, so logits follow the eager patched model to bf16
-rounding.  Quest selection with an absolute budget (``budget_pages``),
+the metadata update, the output GEMV, residual add + RMSNorm, one gate/up
+GEMV, SiLU * up and the down GEMV (tw_gemv: one token, memory-bound, fp32
+accumulation).  The q/k/v and gate/up weights are concatenated once and the
+HF modules keep views into them, so the model's own forward (the prefill)
+uses the same storage.  The element-wise kernels repeat the HF modules'
+rounding steps; the GEMV and RMSNorm reduction orders differ from hipBLASLt
+and torch, so logits follow the eager patched model to bf16 rounding.  Quest selection with an absolute budget (``budget_pages``),
 16-row pages, head_dim 128 and 16-bit K/V only (the page-tile kernel); the
 cache must be built with ``update_metadata_on_decode=True`` so pages
 completed during decode are scored.  While the decoder runs it owns the
@@ -114,6 +114,11 @@ class GraphDecoder:
         self.I = self.wgu[0].shape[0] // 2
         hidden = cfg.hidden_size
         self.x = torch.empty((1, hidden), dtype=cache.dtype, device=dev)
+        self.qkv = torch.empty((1, self.wqkv[0].shape[0]), dtype=cache.dtype, device=dev)
+        self.o = torch.empty((1, hidden), dtype=cache.dtype, device=dev)
+        self.gu = torch.empty((1, self.wgu[0].shape[0]), dtype=cache.dtype, device=dev)
+        self.dn = torch.empty((1, hidden), dtype=cache.dtype, device=dev)
+        self.vocab = model.lm_head.weight.shape[0]
         self.q32 = torch.empty((self.Hq, self.D), dtype=torch.float32, device=dev)
         self.m = torch.empty((1, self.I), dtype=cache.dtype, device=dev)
         # per-layer buffers
@@ -136,7 +141,7 @@ class GraphDecoder:
             attn = layer.self_attn
             norm = layer.input_layernorm
             kernels.add_rms_norm(h, delta, norm.weight, norm.variance_epsilon, x)
-            qkv = F.linear(x, self.wqkv[li], self.bqkv[li])[0]
+            qkv = kernels.gemv(x, self.wqkv[li], self.bqkv[li], self.qkv)[0]
             q = qkv[:Hq * D].view(Hq, D)
             k = qkv[Hq * D:(Hq + G) * D].view(G, D)
             v = qkv[(Hq + G) * D:].view(G, D)
@@ -163,17 +168,16 @@ class GraphDecoder:
                                                       softmax_scale=float(attn.scaling), out=self.attn[li])
             kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
                                                 block_size=c.block_size, page_min=c._page_min, page_max=c._page_max)
-            o = attn.o_proj(self.attn[li].view(1, Hq * D))
+            o = kernels.gemv(self.attn[li].view(1, Hq * D), attn.o_proj.weight, attn.o_proj.bias, self.o)
             norm = layer.post_attention_layernorm
             kernels.add_rms_norm(h, o, norm.weight, norm.variance_epsilon, x)
-            gu = F.linear(x, self.wgu[li])
+            gu = kernels.gemv(x, self.wgu[li], None, self.gu)
             kernels.silu_mul(gu, self.m)
-            delta = layer.mlp.down_proj(self.m)
+            delta = kernels.gemv(self.m, layer.mlp.down_proj.weight, layer.mlp.down_proj.bias, self.dn)
         kernels.add_rms_norm(h, delta, inner.norm.weight, inner.norm.variance_epsilon, x)
-        logits = self.model.lm_head(x)
         if self.logits is None:
-            self.logits = torch.empty_like(logits)
-        self.logits.copy_(logits)
+            self.logits = torch.empty((1, self.vocab), dtype=self.cache.dtype, device=self.dev)
+        logits = kernels.gemv(x, self.model.lm_head.weight, self.model.lm_head.bias, self.logits)
         if self.fixed_token is None:
             self.token.copy_(logits.argmax(dim=-1))
         self.position.add_(1)

@@ -1212,3 +1212,21 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     with torch.cuda.device(dev):
         check(hip().tw_silu_mul(ptr(gate_up), ptr(out), out.numel(), _dt(out), stream_handle(dev)), "silu_mul")
     return out
+
+
+def gemv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], out: torch.Tensor) -> torch.Tensor:
+    """out [1, N] = x [1, K] @ weight [N, K]^T (+ bias): nn.Linear for one
+    token, memory-bound (fp32 accumulation)."""
+    if weight.ndim != 2 or not weight.is_contiguous() or weight.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("weight must be contiguous [N, K] fp16/bf16")
+    N, K = weight.shape
+    if x.dtype != weight.dtype or x.numel() != K or not x.is_contiguous():
+        raise ValueError("x must be contiguous [K] in the weight's dtype")
+    if out.dtype != weight.dtype or out.numel() != N or not out.is_contiguous():
+        raise ValueError("out must be contiguous [N] in the weight's dtype")
+    if bias is not None and (bias.dtype != weight.dtype or bias.numel() != N or not bias.is_contiguous()):
+        raise ValueError("bias must be contiguous [N]")
+    dev = _require_device(x, weight, bias, out, what="gemv")
+    with torch.cuda.device(dev):
+        check(hip().tw_gemv(ptr(weight), ptr(x), ptr(bias), ptr(out), N, K, _dt(weight), stream_handle(dev)), "gemv")
+    return out
