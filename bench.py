@@ -260,9 +260,7 @@ class TwilightWorkload:
 
         kernels.decode_attention_rows(self.q[layer], self.kc[layer], self.vc[layer], self.rows[layer],
                                       self.row_counts[layer], self.max_rows, cur_k=self.cur_k[layer],
-                                      cur_v=self.cur_v[layer], out=self.out[layer])
-        kernels.append_kv(self.cur_k[layer], self.cur_v[layer], self.kc[layer], self.vc[layer], first_entry=0,
-                          position=self.L)
+                                      cur_v=self.cur_v[layer], out=self.out[layer], append_position=self.L)
 
     def step(self) -> None:
         for layer in range(self.layers):
@@ -648,8 +646,6 @@ def run_twilight(args, dev) -> int:
     g_step = graph_of(w.step)
     g_sel = graph_of(lambda: [w.select(i) for i in range(w.layers)])
     g_att = graph_of(lambda: [w.attend(i) for i in range(w.layers)])
-    # the split-K kernel alone (phase 1; its partials are merged by phase 2)
-    g_att1 = graph_of(lambda: [w.attend(i, phase=1) for i in range(w.layers)])
     wall, _ = _timed_steps(g_step, args.steps, args.warmup)
     reps = max(20, args.steps // 2)
     t_sel = time_graph(g_sel, reps) / w.layers

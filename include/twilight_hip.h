@@ -351,6 +351,18 @@ int tw_decode_attention(const void* q, const void* k_base, const void* v_base, i
                         const int32_t* cu_seqlens_k, int Hk, int window_left, int max_rows,
                         const void* cur_k, const void* cur_v, float softmax_scale, void* out,
                         void* workspace, size_t workspace_bytes, void* stream);
+/* tw_decode_attention over a row list with the decode token's append fused:
+ * the first block of every group also writes cur_k/cur_v[g] to row
+ * append_position of entry g (0 <= append_position < entry_stride_rows;
+ * the row list must not name it).  Replaces the Twilight decode step's GQA
+ * decode attention over the union rows (mp.py:239-279) followed by the
+ * batched new-KV append (twilight_offload_cache.py:551-794). */
+int tw_decode_attention_rows_append(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
+                                    int D, const int32_t* rows, const uint8_t* row_masks, const int32_t* row_counts,
+                                    int64_t rows_stride, int64_t entry_stride_rows, int max_rows,
+                                    const void* cur_k, const void* cur_v, int64_t append_position,
+                                    float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
+                                    void* stream);
 
 /* ------------------------------------------------------------------------
  * Head-wise K/V row gather into the attention layout.

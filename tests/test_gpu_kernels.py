@@ -318,6 +318,42 @@ def test_decode_attention_rows(K, dev, dtype, G, R, D, L, n_rows, masked, cur):
 
 
 @pytest.mark.parametrize(
+    "dtype,G,R,D,L,n_rows",
+    [
+        ("bf16", 8, 4, 128, 32768, 9500),   # the Twilight 32K union
+        ("f16", 3, 7, 64, 3000, 400),
+        ("f32", 2, 3, 128, 2000, 1000),
+        ("bf16", 2, 3, 4, 32, 9),
+    ],
+)
+def test_decode_attention_rows_append(K, dev, dtype, G, R, D, L, n_rows):
+    """The fused append writes cur_k/cur_v to the row and nothing else, and the
+    attention output is bit-identical to the launch without it."""
+    _say(f"[attention rows append] {dtype} G={G} R={R} D={D} rows={n_rows}")
+    g0 = torch.Generator().manual_seed(L + 7 * n_rows)
+    Lmax = L + 3
+    kc = randn((G, Lmax, D), dtype, seed=11).to(dev)
+    vc = randn((G, Lmax, D), dtype, seed=12).to(dev)
+    q = randn((G, R, D), dtype, seed=13).to(dev)
+    rows = torch.stack([torch.randperm(L, generator=g0)[:n_rows].sort().values for _ in range(G)]).to(torch.int32)
+    counts = torch.tensor([max(1, n_rows - 3 * g) for g in range(G)], dtype=torch.int32)
+    ck = randn((G, D), dtype, seed=14).to(dev)
+    cv = randn((G, D), dtype, seed=15).to(dev)
+    rows, counts = rows.to(dev), counts.to(dev)
+    plain = K.decode_attention_rows(q, kc, vc, rows, counts, n_rows, cur_k=ck, cur_v=cv)
+    k0, v0 = kc.clone(), vc.clone()
+    fused = K.decode_attention_rows(q, kc, vc, rows, counts, n_rows, cur_k=ck, cur_v=cv, append_position=L)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, plain)
+    k0[:, L], v0[:, L] = ck, cv
+    assert torch.equal(kc, k0) and torch.equal(vc, v0)
+    with pytest.raises(ValueError):
+        K.decode_attention_rows(q, kc, vc, rows, counts, n_rows, append_position=L)
+    with pytest.raises(ValueError):
+        K.decode_attention_rows(q, kc, vc, rows, counts, n_rows, cur_k=ck, cur_v=cv, append_position=Lmax)
+
+
+@pytest.mark.parametrize(
     "dtype,G,R,D,L,k,sink,recent,bs,masked",
     [
         ("f16", 8, 4, 128, 32768, 128, 64, 256, 16, True),   # the 32K Quest layer

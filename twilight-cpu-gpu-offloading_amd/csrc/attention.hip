@@ -507,7 +507,7 @@ __global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(
     return;
   }
   if (chunk >= n_chunks) return;
-  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
+  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
 
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
@@ -823,7 +823,7 @@ __global__ __launch_bounds__(kBlock, 2) void decode_attn_mfma(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
+  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
 
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
@@ -1409,7 +1409,7 @@ __global__ __launch_bounds__(kBlock) void decode_attn_generic(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if (MODE == kModePages && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
+  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
   const S* qg = static_cast<const S*>(a.q) + static_cast<int64_t>(g) * R * D;
@@ -1709,12 +1709,15 @@ extern "C" size_t tw_decode_attention_workspace_size(int G, int R, int D, int ma
   return total;
 }
 
-extern "C" int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
-                                   int D, const int32_t* rows, const uint8_t* row_masks, const int32_t* row_counts,
-                                   int64_t rows_stride, int64_t entry_stride_rows, const int32_t* cu_seqlens_k,
-                                   int Hk, int window_left, int max_rows, const void* cur_k, const void* cur_v,
-                                   float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
+namespace {
+// Rows / varlen launch shared by tw_decode_attention and
+// tw_decode_attention_rows_append (append_position >= 0: chunk 0 of every
+// group writes cur_k/cur_v[g] to that row of its entry).
+int rows_launch(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R, int D,
+                const int32_t* rows, const uint8_t* row_masks, const int32_t* row_counts, int64_t rows_stride,
+                int64_t entry_stride_rows, const int32_t* cu_seqlens_k, int Hk, int window_left, int max_rows,
+                const void* cur_k, const void* cur_v, int64_t append_position, float softmax_scale, void* out,
+                void* workspace, size_t workspace_bytes, void* stream) {
   if (q == nullptr || out == nullptr || G <= 0 || R <= 0 || R > 8 || D <= 0 || D > 512 || (D % 2) != 0 ||
       max_rows < 0)
     return TW_EINVAL;
@@ -1763,8 +1766,40 @@ extern "C" int tw_decode_attention(const void* q, const void* k_base, const void
   a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ml_off);
   a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
   a.max_rows = max_rows;
+  a.append_position = -1;
+  if (append_position >= 0) {
+    a.k_append = const_cast<void*>(k_base);
+    a.v_append = const_cast<void*>(v_base);
+    a.append_position = static_cast<int>(append_position);
+  }
   tw::plan_chunks(dtype, G, R, D, max_rows + (cur_k != nullptr ? 1 : 0), &a.iters, &a.max_chunks);
   return tw::launch_dtype(dtype, a, static_cast<hipStream_t>(stream));
+}
+}  // namespace
+
+extern "C" int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
+                                   int D, const int32_t* rows, const uint8_t* row_masks, const int32_t* row_counts,
+                                   int64_t rows_stride, int64_t entry_stride_rows, const int32_t* cu_seqlens_k,
+                                   int Hk, int window_left, int max_rows, const void* cur_k, const void* cur_v,
+                                   float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  return rows_launch(q, k_base, v_base, dtype, G, R, D, rows, row_masks, row_counts, rows_stride, entry_stride_rows,
+                     cu_seqlens_k, Hk, window_left, max_rows, cur_k, cur_v, -1, softmax_scale, out, workspace,
+                     workspace_bytes, stream);
+}
+
+extern "C" int tw_decode_attention_rows_append(const void* q, const void* k_base, const void* v_base, int dtype,
+                                               int G, int R, int D, const int32_t* rows, const uint8_t* row_masks,
+                                               const int32_t* row_counts, int64_t rows_stride,
+                                               int64_t entry_stride_rows, int max_rows, const void* cur_k,
+                                               const void* cur_v, int64_t append_position, float softmax_scale,
+                                               void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (rows == nullptr || cur_k == nullptr || cur_v == nullptr || append_position < 0 ||
+      append_position >= entry_stride_rows || append_position > INT32_MAX)
+    return TW_EINVAL;
+  return rows_launch(q, k_base, v_base, dtype, G, R, D, rows, row_masks, row_counts, rows_stride, entry_stride_rows,
+                     nullptr, 0, -1, max_rows, cur_k, cur_v, append_position, softmax_scale, out, workspace,
+                     workspace_bytes, stream);
 }
 
 extern "C" int tw_decode_attention_pages(const void* q, const void* k_base, const void* v_base, int dtype, int G,

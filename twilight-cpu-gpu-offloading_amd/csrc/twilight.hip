@@ -337,17 +337,6 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, unsigned long long
   __syncthreads();
   return t;
 }
-__device__ __forceinline__ float block_max_f32(float v, float* red) {
-  v = wave_max_f32(v);
-  const int wave = static_cast<int>(threadIdx.x) / kWave;
-  if (lane_id() == 0) red[wave] = v;
-  __syncthreads();
-  float t = red[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) t = fmaxf(t, red[w]);
-  __syncthreads();
-  return t;
-}
 
 // ceil(p24 * z / 2^24) without 128-bit arithmetic (p24 <= 2^24, z < 2^56).
 __device__ __forceinline__ uint64_t top_p_threshold(uint32_t p24, uint64_t z) {
@@ -360,10 +349,11 @@ __device__ __forceinline__ uint64_t top_p_threshold(uint32_t p24, uint64_t z) {
 
 // The smallest count c of top keys (key desc, index asc) whose masses sum to
 // >= need; marks them in *taken (bit j = key j of this thread).  Keys are
-// KPT contiguous per thread (indices KPT*t + j).
+// KPT contiguous per thread (indices KPT*t + j).  kmin0/kmax0: the smallest
+// and largest key of the row; the caller has cleared the histograms.
 template <int KPT>
 __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)[KPT], int N, uint64_t need,
-                              TopShared& sh, uint32_t* taken_out) {
+                              uint32_t kmin0, uint32_t kmax0, TopShared& sh, uint32_t* taken_out) {
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid / kWave;
@@ -374,24 +364,73 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
   int count = 0;  // keys taken so far (block-uniform)
   int ccount = N;
   for (int level = 0;; ++level) {
-    uint32_t cmax = 0u, cmin = 0xffffffffu;
+    if (ccount <= kBlock) {
+      // exact: rank the candidates (key desc, index asc) and walk their
+      // masses in rank order; slot t's rank goes to sel.selbits[t]
+      int total;
+      const int first = block_excl_scan(__popc(cand), sh.sel.scan, &total);
+      int slot = first;
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const bool c = (cand >> j) & 1u;
-      cmax = (c && key[j] > cmax) ? key[j] : cmax;
-      cmin = (c && key[j] < cmin) ? key[j] : cmin;
-    }
-    cmax = wave_max_u32(cmax);
-    cmin = wave_min_u32(cmin);
-    if (lane == 0) {
-      sh.sel.red_max[wave] = cmax;
-      sh.sel.red_min[wave] = cmin;
-    }
-    __syncthreads();
+      for (int j = 0; j < KPT; ++j) {
+        if ((cand >> j) & 1u) {
+          sh.sel.ckey[slot] = key[j];
+          sh.sel.cidx[slot] = i0 + j;
+          sh.cmass[slot] = mass[j];
+          ++slot;
+        }
+      }
+      if (tid == 0) sh.ires[0] = total;  // default: every candidate
+      __syncthreads();
+      if (tid < total) {
+        const uint32_t mk = sh.sel.ckey[tid];
+        const int mi = sh.sel.cidx[tid];
+        uint64_t before = 0;
+        int rank = 0;
+        for (int m = 0; m < total; ++m) {
+          const uint32_t km = sh.sel.ckey[m];
+          const int im = sh.sel.cidx[m];
+          const bool ahead = km > mk || (km == mk && im < mi);
+          before += ahead ? sh.cmass[m] : 0ull;
+          rank += ahead ? 1 : 0;
+        }
+        sh.sel.selbits[tid] = static_cast<uint32_t>(rank);
+        if (before < need && need <= before + sh.cmass[tid]) sh.ires[0] = rank + 1;
+      }
+      __syncthreads();
+      const int needed = sh.ires[0];
+      slot = first;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      cmax = sh.sel.red_max[w] > cmax ? sh.sel.red_max[w] : cmax;
-      cmin = sh.sel.red_min[w] < cmin ? sh.sel.red_min[w] : cmin;
+      for (int j = 0; j < KPT; ++j) {
+        if ((cand >> j) & 1u) {
+          taken |= static_cast<int>(sh.sel.selbits[slot]) < needed ? (1u << j) : 0u;
+          ++slot;
+        }
+      }
+      count += needed;
+      break;
+    }
+    uint32_t cmax = kmax0, cmin = kmin0;
+    if (level > 0) {
+      cmax = 0u;
+      cmin = 0xffffffffu;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const bool c = (cand >> j) & 1u;
+        cmax = (c && key[j] > cmax) ? key[j] : cmax;
+        cmin = (c && key[j] < cmin) ? key[j] : cmin;
+      }
+      cmax = wave_max_u32(cmax);
+      cmin = wave_min_u32(cmin);
+      if (lane == 0) {
+        sh.sel.red_max[wave] = cmax;
+        sh.sel.red_min[wave] = cmin;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        cmax = sh.sel.red_max[w] > cmax ? sh.sel.red_max[w] : cmax;
+        cmin = sh.sel.red_min[w] < cmin ? sh.sel.red_min[w] : cmin;
+      }
     }
     if (cmax == cmin) {
       // equal keys carry equal masses: take ceil(need / m), lowest index first
@@ -418,55 +457,6 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
       count += needed < total ? needed : total;
       break;
     }
-    if (ccount <= kBlock) {
-      // exact: rank the candidates and walk their masses in rank order
-      int total;
-      int slot = block_excl_scan(__popc(cand), sh.sel.scan, &total);
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) {
-        if ((cand >> j) & 1u) {
-          sh.sel.ckey[slot] = key[j];
-          sh.sel.cidx[slot] = i0 + j;
-          sh.cmass[slot] = mass[j];
-          ++slot;
-        }
-      }
-      if (tid == 0) sh.ires[0] = total;  // default: every candidate
-      __syncthreads();
-      int my_rank = -1;
-      if (tid < total) {
-        const uint32_t mk = sh.sel.ckey[tid];
-        const int mi = sh.sel.cidx[tid];
-        uint64_t before = 0;
-        int rank = 0;
-        for (int m = 0; m < total; ++m) {
-          const uint32_t km = sh.sel.ckey[m];
-          const int im = sh.sel.cidx[m];
-          const bool ahead = km > mk || (km == mk && im < mi);
-          before += ahead ? sh.cmass[m] : 0ull;
-          rank += ahead ? 1 : 0;
-        }
-        my_rank = rank;
-        if (before < need && need <= before + sh.cmass[tid]) sh.ires[0] = rank + 1;
-      }
-      __syncthreads();
-      const int needed = sh.ires[0];
-      for (int w = tid; w < kMaxSelPages / 32; w += kBlock) sh.sel.selbits[w] = 0u;
-      __syncthreads();
-      if (tid < total && my_rank < needed) {
-        const int mi = sh.sel.cidx[tid];
-        atomicOr(&sh.sel.selbits[mi >> 5], 1u << (mi & 31));
-      }
-      __syncthreads();
-#pragma unroll
-      for (int j = 0; j < KPT; ++j) {
-        const int i = i0 + j;
-        const bool c = (cand >> j) & 1u;
-        taken |= (c && ((sh.sel.selbits[(i >> 5) & (kMaxSelPages / 32 - 1)] >> (i & 31)) & 1u)) ? (1u << j) : 0u;
-      }
-      count += needed;
-      break;
-    }
     BinFn fn;
     const float vmin = key_value(cmin);
     const float vmax = key_value(cmax);
@@ -479,11 +469,13 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
     fn.shift = hi >= 7 ? hi - 7 : 0;
     const int nb = fn.linear ? kLinBins : 256;
     const int bpt = nb / kBlock;
-    for (int b = tid; b < kLinBins + 64; b += kBlock) {
-      sh.sel.hist[b] = 0u;
-      sh.bin_mass[b] = 0ull;
+    if (level > 0) {
+      for (int b = tid; b < kLinBins + 64; b += kBlock) {
+        sh.sel.hist[b] = 0u;
+        sh.bin_mass[b] = 0ull;
+      }
+      __syncthreads();
     }
-    __syncthreads();
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
       if ((cand >> j) & 1u) {
@@ -605,9 +597,23 @@ __device__ __forceinline__ uint32_t range_bits(int lo, int a, int b) {
   return below_e & ~below_s;
 }
 
+// Dynamic LDS of the selection kernels: the union bitmap (one bit per
+// position, padded to 16 bytes), then a staging area shared by the logits
+// load (N floats) and the union compaction (2 * kBlock words = 16384
+// positions of rows per window).
+constexpr int kUnionWindowWords = 2 * kBlock;
+__host__ __device__ __forceinline__ int union_words(int length) { return (length + 31) / 32; }
+__host__ __device__ __forceinline__ int stage_offset_words(int length) { return (union_words(length) + 4 + 3) & ~3; }
+__host__ __device__ __forceinline__ int stage_elems(int N, int length) {
+  const int w = union_words(length);
+  const int rows = (w < kUnionWindowWords ? w : kUnionWindowWords) * 32;
+  const int n = (N + 3) & ~3;
+  return n > rows ? n : rows;
+}
+
 // The last block of group g: token union of the R selections plus the sink
 // and recent windows, compacted ascending into the group's row list.
-__device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, int* scan) {
+__device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, int32_t* stage, int* scan) {
   const int tid = threadIdx.x;
   const int length = s.length;
   const int sink_end = s.sink < length ? s.sink : length;
@@ -671,21 +677,38 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
     }
   }
   __syncthreads();
-  // compaction: thread t owns a contiguous run of words
-  const int wpt = (words + kBlock - 1) / kBlock;
-  const int w0 = tid * wpt;
-  int cnt = 0;
-  for (int w = w0; w < w0 + wpt && w < words; ++w) cnt += __popc(bits[w]);
-  int total;
-  int slot = block_excl_scan(cnt, scan, &total);
+  // compaction in windows of 2 * kBlock words: thread t ranks the positions
+  // of words w0 + 2t and w0 + 2t + 1 into the LDS stage, then consecutive
+  // threads copy consecutive rows out, four rows per thread in flight.
   int32_t* rows = s.rows + static_cast<int64_t>(g) * s.rows_stride;
-  for (int w = w0; w < w0 + wpt && w < words; ++w) {
-    uint32_t v = bits[w];
-    while (v != 0u) {
-      const int b = __ffs(static_cast<int>(v)) - 1;
-      v &= v - 1u;
-      rows[slot++] = 32 * w + b;
+  int total = 0;
+  for (int w0 = 0; w0 < words; w0 += kUnionWindowWords) {
+    const int w = w0 + 2 * tid;
+    uint32_t v0 = w < words ? bits[w] : 0u;
+    uint32_t v1 = w + 1 < words ? bits[w + 1] : 0u;
+    int n_win;
+    int slot = block_excl_scan(__popc(v0) + __popc(v1), scan, &n_win);
+    while (v0 != 0u) {
+      const int b = __ffs(static_cast<int>(v0)) - 1;
+      v0 &= v0 - 1u;
+      stage[slot++] = 32 * w + b;
     }
+    while (v1 != 0u) {
+      const int b = __ffs(static_cast<int>(v1)) - 1;
+      v1 &= v1 - 1u;
+      stage[slot++] = 32 * (w + 1) + b;
+    }
+    __syncthreads();
+    for (int i = tid; i < n_win; i += 4 * kBlock) {
+      int32_t r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) r[u] = i + u * kBlock < n_win ? stage[i + u * kBlock] : 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (i + u * kBlock < n_win) rows[total + i + u * kBlock] = r[u];
+    }
+    total += n_win;
+    __syncthreads();  // the next window reuses the stage
   }
   const int count = total + (s.append_position >= 0 ? 1 : 0);
   if (tid == 0) {
@@ -694,19 +717,59 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
   }
 }
 
+// The row's logits through the LDS stage (16-byte loads, consecutive threads
+// reading consecutive chunks), then KPT contiguous keys per thread; the
+// largest logit and the smallest and largest key of the row in one block
+// reduction.
 template <int KPT>
-__device__ __forceinline__ void load_logits(const float* row, int N, uint32_t (&key)[KPT], float& lmax,
-                                            float* fred) {
-  const int i0 = KPT * static_cast<int>(threadIdx.x);
+__device__ __forceinline__ void load_logits(const float* row, int N, float* stage, uint32_t (&key)[KPT],
+                                            float& lmax, uint32_t& kmin, uint32_t& kmax, TopShared& sh) {
+  const int tid = static_cast<int>(threadIdx.x);
+  if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    float4* s4 = reinterpret_cast<float4*>(stage);
+    const int n4 = N >> 2;
+#pragma unroll
+    for (int j = 0; j < KPT / 4; ++j) {
+      const int i = j * kBlock + tid;
+      if (i < n4) s4[i] = r4[i];
+    }
+  } else {
+    for (int i = tid; i < N; i += kBlock) stage[i] = row[i];
+  }
+  __syncthreads();
+  const int i0 = KPT * tid;
   float mx = -INFINITY;
+  uint32_t kmx = 0u, kmn = 0xffffffffu;
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
     const int i = i0 + j;
-    const float v = row[i < N ? i : N - 1];
+    const float v = stage[i < N ? i : N - 1];
     key[j] = score_key(v);
     mx = (i < N && v > mx) ? v : mx;
+    kmx = (i < N && key[j] > kmx) ? key[j] : kmx;
+    kmn = (i < N && key[j] < kmn) ? key[j] : kmn;
   }
-  lmax = block_max_f32(mx, fred);
+  mx = wave_max_f32(mx);
+  kmx = wave_max_u32(kmx);
+  kmn = wave_min_u32(kmn);
+  const int wave = tid / kWave;
+  if (lane_id() == 0) {
+    sh.fred[wave] = mx;
+    sh.sel.red_max[wave] = kmx;
+    sh.sel.red_min[wave] = kmn;
+  }
+  __syncthreads();
+  lmax = sh.fred[0];
+  kmax = sh.sel.red_max[0];
+  kmin = sh.sel.red_min[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    lmax = fmaxf(lmax, sh.fred[w]);
+    kmax = sh.sel.red_max[w] > kmax ? sh.sel.red_max[w] : kmax;
+    kmin = sh.sel.red_min[w] < kmin ? sh.sel.red_min[w] : kmin;
+  }
+  __syncthreads();
 }
 
 // Publish this row's selection bits (bit n = candidate n selected).
@@ -730,12 +793,19 @@ template <int KPT>
 __global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
   __shared__ __align__(16) TopShared sh;
   extern __shared__ __align__(16) uint32_t union_bits[];
+  float* stage = reinterpret_cast<float*>(union_bits + stage_offset_words(s.length));
   const int row = blockIdx.x;
   const int g = row / s.R;
   const int N = s.N;
+  // the first pass's histograms, cleared before load_logits' barrier
+  for (int b = threadIdx.x; b < kLinBins + 64; b += kBlock) {
+    sh.sel.hist[b] = 0u;
+    sh.bin_mass[b] = 0ull;
+  }
   uint32_t key[KPT];
   float lmax;
-  load_logits<KPT>(s.logits + static_cast<int64_t>(row) * N, N, key, lmax, sh.fred);
+  uint32_t kmin, kmax;
+  load_logits<KPT>(s.logits + static_cast<int64_t>(row) * N, N, stage, key, lmax, kmin, kmax, sh);
   uint64_t mass[KPT];
   uint64_t local = 0;
   const int i0 = KPT * static_cast<int>(threadIdx.x);
@@ -753,14 +823,14 @@ __global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
     need = 1;
   }
   uint32_t taken;
-  int desired = block_top_mass<KPT>(key, mass, N, need, sh, &taken);
+  int desired = block_top_mass<KPT>(key, mass, N, need, kmin, kmax, sh, &taken);
   desired = desired < 1 ? 1 : (desired > N ? N : desired);
   if (threadIdx.x == 0) s.desired[row] = desired;
   if (s.matched) return;
   if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = desired;
   publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
-  build_token_union(s, g, union_bits, sh.sel.scan);
+  build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan);
 }
 
 // Stage B (matched budgets): allocation from the group's desired counts, the
@@ -779,9 +849,11 @@ __global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) 
     matched_counts(d, s.R, s.target_total, N, c);
     sh.ires[1] = c[r];
   }
+  float* stage = reinterpret_cast<float*>(union_bits + stage_offset_words(s.length));
   uint32_t key[KPT];
   float lmax;
-  load_logits<KPT>(s.logits + static_cast<int64_t>(row) * N, N, key, lmax, sh.fred);  // (barriers inside)
+  uint32_t kmin, kmax;
+  load_logits<KPT>(s.logits + static_cast<int64_t>(row) * N, N, stage, key, lmax, kmin, kmax, sh);  // (barriers)
   int k = sh.ires[1];
   k = k < 1 ? 1 : (k > N ? N : k);
   if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = k;
@@ -790,7 +862,7 @@ __global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) 
   block_topk<KPT>(key, N, k, sh.sel, [&](int, int idx) { taken |= 1u << (idx - i0); });
   publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
-  build_token_union(s, g, union_bits, sh.sel.scan);
+  build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan);
 }
 
 // --------------------------------------------------------------- launch
@@ -846,7 +918,7 @@ int launch_qk_positions(const QkArgs& a, const int64_t* positions, int N, float*
 
 template <int KPT>
 int launch_select_kpt(const SelectArgs& s, hipStream_t stream) {
-  const size_t lds = static_cast<size_t>((s.length + 31) / 32) * 4 + 16;
+  const size_t lds = (static_cast<size_t>(stage_offset_words(s.length)) + stage_elems(s.N, s.length)) * 4;
   if (lds + sizeof(TopShared) > 160 * 1024) return TW_EUNSUPPORTED;
   if (lds + sizeof(TopShared) > 64 * 1024) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(twilight_topp_kernel<KPT>),

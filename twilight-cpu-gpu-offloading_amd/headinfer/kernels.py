@@ -609,11 +609,14 @@ def decode_attention_rows(
     cur_v: Optional[torch.Tensor] = None,
     softmax_scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
+    append_position: Optional[int] = None,
 ) -> torch.Tensor:
     """Sparse GQA decode attention reading K/V rows by position straight from
     the cache.  q [G,R,D]; k_cache/v_cache [G, Lmax, D] (the layer's entries,
     HBM or mapped pinned host); rows [G, stride] int32 positions; row_counts
-    [G] int32; cur_k/cur_v [G, D] extra decode token.  Returns [G,R,D]."""
+    [G] int32; cur_k/cur_v [G, D] extra decode token.  With append_position
+    (and cur_k/cur_v) the same launch also writes the decode token to that
+    row of every entry; the row list must not name it.  Returns [G,R,D]."""
     if q.ndim != 3 or q.dtype not in _KEY_DTYPES:
         raise ValueError("q must be [G, R, D]")
     G, R, D = q.shape
@@ -639,6 +642,17 @@ def decode_attention_rows(
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
+    if append_position is not None:
+        if cur_k is None:
+            raise ValueError("append_position needs cur_k/cur_v")
+        if not 0 <= int(append_position) < k_cache.shape[1]:
+            raise ValueError(f"append_position {append_position} outside the cache rows [0, {k_cache.shape[1]})")
+        with torch.cuda.device(dev):
+            check(hip().tw_decode_attention_rows_append(
+                ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D, ptr(rows), ptr(row_masks),
+                ptr(row_counts), rows.stride(0), k_cache.stride(0) // D, max_rows, ptr(cur_k), ptr(cur_v),
+                int(append_position), scale, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)), "decode_attention")
+        return out
     with torch.cuda.device(dev):
         check(hip().tw_decode_attention(ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D, ptr(rows),
                                         ptr(row_masks), ptr(row_counts), rows.stride(0), k_cache.stride(0) // D,

@@ -568,12 +568,17 @@ class QuestTopKOffloadedCache(_CacheBase):
         self._pack_rows_k = self._gpu_pack_keys.view(-1, D)
         self._pack_rows_v = self._gpu_pack_values.view(-1, D)
 
-    def _append(self, entries: Sequence[int], cur_k: torch.Tensor, cur_v: torch.Tensor, position: int) -> None:
+    def _append(self, entries: Sequence[int], cur_k: torch.Tensor, cur_v: torch.Tensor, position: int,
+                written: bool = False) -> None:
         """The decode tokens [G, D] into slab row `position` of their entries
         (the per-step append of quest_offload_cache.py:633-638), written by a
-        kernel on this stream -- through the mapped address for a host slab."""
+        kernel on this stream -- through the mapped address for a host slab.
+        written: the attention launch already stored the rows (fused append);
+        only the bookkeeping and the metadata update remain."""
         start = self._phase_start()
-        if self._consecutive(entries):
+        if written:
+            pass
+        elif self._consecutive(entries):
             kernels.append_kv(cur_k, cur_v, self._key_cache, self._value_cache, first_entry=entries[0],
                               position=position)
         else:

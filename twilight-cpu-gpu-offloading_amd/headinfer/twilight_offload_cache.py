@@ -430,7 +430,7 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         """One decoder layer's Twilight decode with no host sync: both
         selection stages and the GQA union on the device (Quest B0, INT4 QK,
         top-p, union rows), then the split-K attention reading the union rows
-        and the decode token straight from the slab, then the append.
+        and the decode token straight from the slab, with the append fused.
 
         queries [G, R, D] in the cache dtype; key_states/value_states [G, D];
         entries consecutive.  Returns [G, R, D]."""
@@ -452,12 +452,14 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         e0 = entries[0]
         cur_k, cur_v = key_states.contiguous(), value_states.contiguous()
         start = self._phase_start()
+        # the union rows are below old_length, so the decode token's row is
+        # written by the attention launch itself
         result = kernels.decode_attention_rows(queries.contiguous(), self._key_cache[e0:e0 + G],
                                                self._value_cache[e0:e0 + G], state["rows"], state["counts"],
                                                state["max_count"], cur_k=cur_k, cur_v=cur_v,
-                                               softmax_scale=softmax_scale, out=out)
+                                               softmax_scale=softmax_scale, out=out, append_position=old_length)
         self._phase_end("attention", start)
-        self._append(entries, cur_k, cur_v, old_length)
+        self._append(entries, cur_k, cur_v, old_length, written=True)
         for e in entries:
             self._last_query_head_lengths[e] = None
         return result
