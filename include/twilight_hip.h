@@ -452,6 +452,27 @@ int tw_silu_mul(const void* gate_up, void* out, int I, int dtype, void* stream);
  * W [N][K] row-major (nn.Linear's weight), fp32 accumulation, output in the
  * 16-bit dtype.  K % 8 == 0, K <= 32768, 16-byte aligned W and x. */
 int tw_gemv(const void* W, const void* x, const void* bias, void* y, int N, int K, int dtype, void* stream);
+/* The GEMV with the decoder layer's residual add + RMSNorm as its input:
+ * x = RMSNorm(h_in + delta) as tw_add_rms_norm computes it (every block
+ * normalises the row itself; delta nullable), h_out = h_in + delta (written
+ * when delta is given; a buffer other than h_in and delta), then
+ * y = x . W[n] (+ bias) as tw_gemv.  K % 8 == 0, K <= 8192.
+ *   tw_rms_norm_gemv: y [N].
+ *   tw_rms_norm_gemv_rope: W is the concatenated q/k/v projection
+ *     [(Hq + Hk + Hv) * D][K]; y [N] gets q and k rotated at *position as
+ *     tw_rope_qk does (q also to q32 [Hq][D], nullable).
+ *   tw_rms_norm_gemv_silu: W is the concatenated gate/up projection [2I][K];
+ *     y [I] = silu(gate) * up as tw_silu_mul does.
+ * Same bits as the separate launches.  No counterpart in the reference's
+ * path (the HF decoder layer's modules, run unpatched by the reference). */
+int tw_rms_norm_gemv(const void* h_in, const void* delta, const void* norm_weight, float eps, void* h_out,
+                     const void* W, const void* bias, void* y, int N, int K, int dtype, void* stream);
+int tw_rms_norm_gemv_rope(const void* h_in, const void* delta, const void* norm_weight, float eps, void* h_out,
+                          const void* W, const void* bias, void* y, int N, int K, int Hq, int Hk, int D,
+                          const void* cos_table, const void* sin_table, const int64_t* position, float* q32,
+                          int dtype, void* stream);
+int tw_rms_norm_gemv_silu(const void* h_in, const void* delta, const void* norm_weight, float eps, void* h_out,
+                          const void* W, const void* bias, void* y, int N, int K, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -227,3 +227,89 @@ def test_decode_step_ops_match_hf_modules(dev, dtype):
     torch.cuda.synchronize()
     ulp = (m.cpu().view(torch.int16).int() - ref.view(torch.int16).int()).abs()
     assert int(ulp.max()) <= 1 and float((ulp == 0).float().mean()) > 0.95
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rms_norm_gemv_matches_separate_launches(dev, dtype):
+    """The GEMV with the residual add + RMSNorm fused before it and RoPE or
+    SiLU * up fused after it: the same bits as add_rms_norm, gemv, rope_qk and
+    silu_mul launched one by one, and h_out = the updated residual."""
+    from headinfer import kernels
+
+    g = torch.Generator().manual_seed(11)
+
+    def rnd(shape, s=1.0):
+        return (torch.randn(shape, generator=g) * s).to(dtype).to(dev)
+
+    D = 128
+    pos = torch.tensor([321], device=dev)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2).float() / D))
+    emb = torch.cat([torch.outer(torch.arange(512).float(), inv)] * 2, dim=-1)
+    cos, sin = emb.cos().to(dtype).to(dev), emb.sin().to(dtype).to(dev)
+    for K, Hq, Hk, I, with_delta, with_bias in ((4096, 8, 2, 1024, True, True), (2048, 4, 4, 8200, False, False),
+                                                 (8192, 2, 1, 9000, True, False), (1000, 3, 1, 300, True, True)):
+        _say(f"[rms_norm_gemv] {dtype} K={K} Hq={Hq} Hk={Hk} I={I} delta={with_delta} bias={with_bias}")
+        h, w_norm = rnd((1, K), 3.0), (1 + 0.1 * torch.randn(K, generator=g)).to(dtype).to(dev)
+        delta = rnd((1, K)) if with_delta else None
+        Nqkv = (Hq + 2 * Hk) * D
+        Wqkv, Wgu = rnd((Nqkv, K), 0.02), rnd((2 * I, K), 0.02)
+        bqkv = rnd(Nqkv) if with_bias else None
+        bgu = rnd(2 * I) if with_bias else None
+        # separate launches
+        h_ref = h.clone()
+        x = torch.empty_like(h)
+        kernels.add_rms_norm(h_ref, delta, w_norm, 1e-5, x)
+        qkv_ref = kernels.gemv(x, Wqkv, bqkv, torch.empty((1, Nqkv), dtype=dtype, device=dev))
+        q_ref32 = torch.empty((Hq, D), dtype=torch.float32, device=dev)
+        kernels.rope_qk(qkv_ref[0, :Hq * D].view(Hq, D), qkv_ref[0, Hq * D:(Hq + Hk) * D].view(Hk, D), cos, sin, pos,
+                        q_ref32)
+        gu = kernels.gemv(x, Wgu, bgu, torch.empty((1, 2 * I), dtype=dtype, device=dev))
+        m_ref = kernels.silu_mul(gu, torch.empty((1, I), dtype=dtype, device=dev))
+        Wlm = rnd((17000, K), 0.02)   # wide launch shape
+        lm_ref = kernels.gemv(x, Wlm, None, torch.empty((1, 17000), dtype=dtype, device=dev))
+        # fused
+        h_out = torch.full_like(h, 7.0) if with_delta else None
+        qkv = torch.empty((1, Nqkv), dtype=dtype, device=dev)
+        q32 = torch.empty((Hq, D), dtype=torch.float32, device=dev)
+        kernels.rms_norm_gemv(h, delta, w_norm, 1e-5, h_out, Wqkv, bqkv, qkv, epilogue="rope",
+                              rope=(Hq, Hk, cos, sin, pos), q32=q32)
+        m = kernels.rms_norm_gemv(h, delta, w_norm, 1e-5, h_out, Wgu, bgu, torch.empty((1, I), dtype=dtype,
+                                                                                          device=dev),
+                                  epilogue="silu")
+        lm = kernels.rms_norm_gemv(h, delta, w_norm, 1e-5, h_out, Wlm, None, torch.empty((1, 17000), dtype=dtype,
+                                                                                            device=dev))
+        torch.cuda.synchronize()
+        assert torch.equal(qkv, qkv_ref) and torch.equal(q32, q_ref32)
+        assert torch.equal(m, m_ref) and torch.equal(lm, lm_ref)
+        if with_delta:
+            assert torch.equal(h_out, h_ref)
+    with pytest.raises(ValueError):
+        kernels.rms_norm_gemv(h, delta, w_norm, 1e-5, h, Wlm, None, lm)   # h_out aliasing h
+
+
+def test_graph_decoder_fused_equals_unfused(dev):
+    """GraphDecoder with the norms, RoPE and SiLU fused into the GEMVs == the
+    same decoder with them as launches of their own, bit for bit."""
+    from headinfer import mp
+    from headinfer.graph_decode import GraphDecoder
+    from headinfer.quest_offload_cache import QuestTopKOffloadedCache
+
+    steps = 4
+    _, gpu = _models(dev)
+    mp.mp_headinfer(gpu)
+    kw = dict(max_cache_len=T_PROMPT + steps + 2, sink_tokens=64, recent_tokens=256, block_size=16,
+              kv_residency="hbm", budget_pages=8, update_metadata_on_decode=True)
+    caches = [QuestTopKOffloadedCache.from_llama_model(gpu, **kw) for _ in range(2)]
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, 1000, (1, T_PROMPT), generator=g).to(dev)
+    with torch.no_grad():
+        for c in caches:
+            gpu(input_ids=ids, past_key_values=c, use_cache=True, logits_to_keep=1)
+        decs = [GraphDecoder(gpu, caches[0], max_new_tokens=steps, fuse=True),
+                GraphDecoder(gpu, caches[1], max_new_tokens=steps, fuse=False)]
+        for step in range(steps):
+            a = decs[0].step().clone()
+            b = decs[1].step().clone()
+            torch.cuda.synchronize()
+            assert torch.equal(a, b), step
+            assert torch.equal(decs[0].token, decs[1].token), step

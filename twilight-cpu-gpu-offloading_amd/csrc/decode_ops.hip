@@ -1,6 +1,7 @@
 // Element-wise steps of one decode token around the sparse path, fused for
 // the graph-captured decode step: residual add + RMSNorm, RoPE of q and k,
-// and the SiLU gate of the MLP.  Each reproduces the rounding steps of the
+// and the SiLU gate of the MLP, standalone or fused into the one-token GEMV
+// that consumes or produces them.  Each reproduces the rounding steps of the
 // HF modules it stands for on 16-bit activations (LlamaRMSNorm,
 // apply_rotary_pos_emb, LlamaMLP's act_fn(gate) * up): every element-wise
 // torch op on bf16/fp16 computes in fp32 and rounds its result to the input
@@ -21,19 +22,22 @@ constexpr int kNormBlock = 256;
 // the block's waves.  H % 8 == 0, H <= kNormBlock * 8 * kNormVec.
 constexpr int kNormVec = 4;
 
-template <typename DT>
-__global__ __launch_bounds__(kNormBlock) void add_rms_norm_kernel(typename DT::storage* __restrict__ h,
-                                                                  const typename DT::storage* __restrict__ delta,
-                                                                  const typename DT::storage* __restrict__ w,
-                                                                  float eps, typename DT::storage* __restrict__ out,
-                                                                  int H) {
+// The residual add + RMSNorm of one row by a block of kNormBlock threads:
+// a = bf16(h + delta) (a = h without delta) is stored to h_store (nullable),
+// and put(i, chunk) receives the 16-byte chunk i of bf16(w * bf16(a * r)).
+// Thread t owns chunks t + c * kNormBlock; the sum of squares runs over its
+// chunks in order, then a wave reduction, then the waves in order, so every
+// block computing the same row gets the same bits.
+template <typename DT, typename Put>
+__device__ __forceinline__ void rms_norm_row(const typename DT::storage* __restrict__ h,
+                                             const typename DT::storage* __restrict__ delta,
+                                             const typename DT::storage* __restrict__ w, float eps, int H,
+                                             typename DT::storage* h_store, float* s_part, Put put) {
   using S = typename DT::storage;
-  __shared__ float s_part[kNormBlock / kWave];
-  const int64_t row = blockIdx.x;
-  uint4* hr = reinterpret_cast<uint4*>(h + row * H);
-  const uint4* dr = delta != nullptr ? reinterpret_cast<const uint4*>(delta + row * H) : nullptr;
+  const uint4* hr = reinterpret_cast<const uint4*>(h);
+  const uint4* dr = reinterpret_cast<const uint4*>(delta);
   const uint4* wr = reinterpret_cast<const uint4*>(w);
-  uint4* orow = reinterpret_cast<uint4*>(out + row * H);
+  uint4* hs = reinterpret_cast<uint4*>(h_store);
   const int nv = H / 8;
   uint4 hv[kNormVec], dv[kNormVec], wv[kNormVec];
 #pragma unroll
@@ -67,7 +71,7 @@ __global__ __launch_bounds__(kNormBlock) void add_rms_norm_kernel(typename DT::s
     if (in) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc += x[c][e] * x[c][e];
-      if (dr != nullptr) hr[threadIdx.x + c * kNormBlock] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      if (hs != nullptr) hs[threadIdx.x + c * kNormBlock] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
     }
   }
   acc = wave_sum_f32(acc);
@@ -90,8 +94,26 @@ __global__ __launch_bounds__(kNormBlock) void add_rms_norm_kernel(typename DT::s
       const float ob = to_f32(DT{}, static_cast<S>(ww[e] >> 16)) * yb;
       ow[e] = static_cast<uint32_t>(from_f32(DT{}, oa)) | (static_cast<uint32_t>(from_f32(DT{}, ob)) << 16);
     }
-    orow[threadIdx.x + c * kNormBlock] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+    put(threadIdx.x + c * kNormBlock, make_uint4(ow[0], ow[1], ow[2], ow[3]));
   }
+}
+
+// h = bf16(h + delta) (when delta is given); out = bf16(w * bf16(h * r)),
+// r = rsqrt(mean(h^2) + eps) in fp32.  One block per row; each thread holds
+// up to kNormVec 8-element chunks of the row in registers (16-byte loads, all
+// issued before any store).  H % 8 == 0, H <= kNormBlock * 8 * kNormVec.
+template <typename DT>
+__global__ __launch_bounds__(kNormBlock) void add_rms_norm_kernel(typename DT::storage* __restrict__ h,
+                                                                  const typename DT::storage* __restrict__ delta,
+                                                                  const typename DT::storage* __restrict__ w,
+                                                                  float eps, typename DT::storage* __restrict__ out,
+                                                                  int H) {
+  __shared__ float s_part[kNormBlock / kWave];
+  const int64_t row = blockIdx.x;
+  uint4* orow = reinterpret_cast<uint4*>(out + row * H);
+  rms_norm_row<DT>(h + row * H, delta != nullptr ? delta + row * H : nullptr, w, eps, H,
+                   delta != nullptr ? h + row * H : nullptr, s_part,
+                   [&](int i, const uint4& v) { orow[i] = v; });
 }
 
 // In place on q [Hq][D] and k [Hk][D] at the position *pos: x' = bf16(bf16(x
@@ -174,53 +196,201 @@ __device__ __forceinline__ float dot8(const uint4& w, const uint4& x, float acc)
   return Dot2<DT>::dot(w.w, x.w, acc);
 }
 
-template <typename DT, int RPW>
-__global__ __launch_bounds__(kGemvBlock) void gemv_kernel(const typename DT::storage* __restrict__ W,
-                                                          const typename DT::storage* __restrict__ x,
-                                                          const typename DT::storage* __restrict__ bias,
-                                                          typename DT::storage* __restrict__ y, int N, int K) {
+// Prologue: x given, or x = RMSNorm(h_in + delta) computed by every block
+// (block 0 stores h_in + delta to h_out).  Epilogue: y[n] = bf16(x . W[n] +
+// bias[n]); or RoPE pairs -- the wave's rows are (head * D + i, head * D + i +
+// D/2) of a concatenated q/k/v projection, rotated as tw_rope_qk for the q and
+// k heads (q also to q32); or SiLU pairs -- rows (i, I + i) of a concatenated
+// gate/up projection, y[i] = bf16(bf16(silu(gate)) * up).
+constexpr int kProX = 0, kProNorm = 1;
+constexpr int kEpiPlain = 0, kEpiRope = 1, kEpiSilu = 2;
+
+template <typename S>
+struct GemvArgs {
+  const S* W;
+  const S* bias;
+  int N, K;
+  const S* x;          // kProX
+  const S* h_in;       // kProNorm
+  const S* delta;
+  const S* norm_w;
+  float eps;
+  S* h_out;
+  S* y;
+  int Hq, Hk, D;       // kEpiRope
+  const S* cos_t;
+  const S* sin_t;
+  const int64_t* pos;
+  float* q32;
+};
+
+template <typename DT, int RPW, int PRO, int EPI>
+__global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::storage> a) {
+  static_assert(EPI == kEpiPlain || RPW % 2 == 0, "paired epilogues take rows two by two");
   extern __shared__ __align__(16) uint4 xs[];
+  __shared__ float s_part[kGemvBlock / kWave];
+  const int K = a.K;
   const int kc = K / 8;  // 16-byte chunks per row
-  const uint4* x4 = reinterpret_cast<const uint4*>(x);
-  for (int i = threadIdx.x; i < kc; i += kGemvBlock) xs[i] = x4[i];
-  __syncthreads();
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
-  const int n0 = (blockIdx.x * (kGemvBlock / kWave) + wave) * RPW;
-  if (n0 >= N) return;
-  const uint4* w4 = reinterpret_cast<const uint4*>(W);
+  const int unit0 = (blockIdx.x * (kGemvBlock / kWave) + wave) * (EPI == kEpiPlain ? RPW : RPW / 2);
+  const int units = EPI == kEpiPlain ? a.N : a.N / 2;
+  // the wave's rows
+  int rows[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    if (EPI == kEpiPlain) {
+      const int n = unit0 + r;
+      rows[r] = n < a.N ? n : a.N - 1;
+    } else {
+      int p = unit0 + r / 2;
+      p = p < units ? p : units - 1;
+      int na, nb;
+      if (EPI == kEpiRope) {
+        const int half = a.D / 2;
+        const int head = p / half;
+        na = head * a.D + (p - head * half);
+        nb = na + half;
+      } else {
+        na = p;
+        nb = p + units;
+      }
+      rows[r] = (r & 1) ? nb : na;
+    }
+  }
+  const uint4* w4 = reinterpret_cast<const uint4*>(a.W);
   const uint4* rowp[RPW];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) rowp[r] = w4 + static_cast<int64_t>(n0 + r < N ? n0 + r : n0) * kc;
+  for (int r = 0; r < RPW; ++r) rowp[r] = w4 + static_cast<int64_t>(rows[r]) * kc;
+  // the first weight chunks are in flight while x is prepared
+  int c = lane;
+  uint4 wa[RPW], wb[RPW];
+  const bool two = c + kWave < kc;
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    wa[r] = rowp[r][c < kc ? c : 0];
+    wb[r] = rowp[r][two ? c + kWave : 0];
+  }
+  if (PRO == kProNorm) {
+    rms_norm_row<DT>(a.h_in, a.delta, a.norm_w, a.eps, K,
+                     (blockIdx.x == 0 && a.delta != nullptr) ? a.h_out : nullptr, s_part,
+                     [&](int i, const uint4& v) { xs[i] = v; });
+  } else {
+    const uint4* x4 = reinterpret_cast<const uint4*>(a.x);
+    for (int i = threadIdx.x; i < kc; i += kGemvBlock) xs[i] = x4[i];
+  }
+  __syncthreads();
+  if (unit0 >= units) return;
   float acc[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-  int c = lane;
-  for (; c + kWave < kc; c += 2 * kWave) {
-    uint4 wa[RPW], wb[RPW];
+  while (true) {
+    if (!two && c < kc) {
+      const uint4 xa = xs[c];
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      wa[r] = rowp[r][c];
-      wb[r] = rowp[r][c + kWave];
+      for (int r = 0; r < RPW; ++r) acc[r] = dot8<DT>(wa[r], xa, acc[r]);
+      break;
     }
+    if (c >= kc) break;
     const uint4 xa = xs[c];
     const uint4 xb = xs[c + kWave];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) acc[r] = dot8<DT>(wb[r], xb, dot8<DT>(wa[r], xa, acc[r]));
-  }
-  if (c < kc) {
-    const uint4 xa = xs[c];
+    c += 2 * kWave;
+    if (c >= kc) break;
+    const bool nxt2 = c + kWave < kc;
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = dot8<DT>(rowp[r][c], xa, acc[r]);
-  }
+    for (int r = 0; r < RPW; ++r) {
+      wa[r] = rowp[r][c];
+      wb[r] = rowp[r][nxt2 ? c + kWave : 0];
+    }
+    if (!nxt2) {
+      const uint4 xl = xs[c];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const float v = wave_sum_f32(acc[r]);
-    if (lane == 0 && n0 + r < N) {
-      const float b = bias != nullptr ? to_f32(DT{}, bias[n0 + r]) : 0.0f;
-      y[n0 + r] = from_f32(DT{}, v + b);
+      for (int r = 0; r < RPW; ++r) acc[r] = dot8<DT>(wa[r], xl, acc[r]);
+      break;
     }
   }
+  float v[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    v[r] = wave_sum_f32(acc[r]);
+    v[r] = v[r] + (a.bias != nullptr ? to_f32(DT{}, a.bias[rows[r]]) : 0.0f);
+  }
+  if (lane != 0) return;
+  if (EPI == kEpiPlain) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+      if (unit0 + r < a.N) a.y[unit0 + r] = from_f32(DT{}, v[r]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < RPW / 2; ++q) {
+      const int p = unit0 + q;
+      if (p >= units) continue;
+      const float va = round_to<DT>(v[2 * q]);
+      const float vb = round_to<DT>(v[2 * q + 1]);
+      if (EPI == kEpiSilu) {
+        const float g = round_to<DT>(va / (1.0f + expf(-va)));
+        a.y[p] = from_f32(DT{}, g * vb);
+      } else {
+        const int half = a.D / 2;
+        const int head = p / half;
+        const int i = p - head * half;
+        const int na = rows[2 * q], nb = rows[2 * q + 1];
+        float ya = va, yb = vb;
+        if (head < a.Hq + a.Hk) {
+          const int64_t t = *a.pos * a.D;
+          const float ci = to_f32(DT{}, a.cos_t[t + i]), si = to_f32(DT{}, a.sin_t[t + i]);
+          const float cj = to_f32(DT{}, a.cos_t[t + i + half]), sj = to_f32(DT{}, a.sin_t[t + i + half]);
+          ya = round_to<DT>(round_to<DT>(va * ci) + round_to<DT>(-vb * si));
+          yb = round_to<DT>(round_to<DT>(vb * cj) + round_to<DT>(va * sj));
+          if (head < a.Hq && a.q32 != nullptr) {
+            a.q32[static_cast<int64_t>(head) * a.D + i] = ya;
+            a.q32[static_cast<int64_t>(head) * a.D + i + half] = yb;
+          }
+        }
+        a.y[na] = from_f32(DT{}, ya);
+        a.y[nb] = from_f32(DT{}, yb);
+      }
+    }
+  }
+}
+
+template <typename DT, int PRO, int EPI>
+int launch_gemv(const GemvArgs<typename DT::storage>& a, hipStream_t st) {
+  const size_t lds = static_cast<size_t>(a.K) * 2;
+  const int waves = kGemvBlock / kWave;
+  const bool wide = a.N >= 16384;
+  const int rpw = wide ? 4 : 2;
+  const int units_per_block = waves * (EPI == kEpiPlain ? rpw : rpw / 2);
+  const int units = EPI == kEpiPlain ? a.N : a.N / 2;
+  const dim3 grid((units + units_per_block - 1) / units_per_block);
+  if (wide)
+    hipLaunchKernelGGL((gemv_kernel<DT, 4, PRO, EPI>), grid, dim3(kGemvBlock), lds, st, a);
+  else
+    hipLaunchKernelGGL((gemv_kernel<DT, 2, PRO, EPI>), grid, dim3(kGemvBlock), lds, st, a);
+  return tw_host::check_launch();
+}
+
+template <int PRO, int EPI>
+int launch_gemv_dtype(GemvArgs<uint16_t> a, int dtype, hipStream_t st) {
+  if (dtype == TW_DTYPE_BF16) return launch_gemv<BF16, PRO, EPI>(a, st);
+  if (dtype == TW_DTYPE_F16) return launch_gemv<F16, PRO, EPI>(a, st);
+  return TW_EUNSUPPORTED;
+}
+
+bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) != 0; }
+
+// Shared checks of the norm-prologue entry points.
+int check_norm_gemv(const void* h_in, const void* delta, const void* norm_w, const void* h_out, const void* W,
+                    const void* y, int N, int K) {
+  if (h_in == nullptr || norm_w == nullptr || W == nullptr || y == nullptr || N <= 0 || K <= 0)
+    return TW_EINVAL;
+  if (delta != nullptr && (h_out == nullptr || h_out == h_in || h_out == delta)) return TW_EINVAL;
+  if ((K % 8) != 0 || K > kNormBlock * 8 * kNormVec) return TW_EUNSUPPORTED;
+  if (misaligned(h_in) || misaligned(delta) || misaligned(norm_w) || misaligned(h_out) || misaligned(W))
+    return TW_EINVAL;
+  return TW_OK;
 }
 
 }  // namespace
@@ -230,36 +400,71 @@ extern "C" int tw_gemv(const void* W, const void* x, const void* bias, void* y, 
                        void* stream) {
   if (W == nullptr || x == nullptr || y == nullptr || N <= 0 || K <= 0 || (K % 8) != 0 || K > 32768)
     return TW_EINVAL;
-  const uintptr_t align = 16;
-  if ((reinterpret_cast<uintptr_t>(W) % align) || (reinterpret_cast<uintptr_t>(x) % align)) return TW_EINVAL;
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  const size_t lds = static_cast<size_t>(K) * 2;
-  const int waves = tw::kGemvBlock / tw::kWave;
-  const bool wide = N >= 16384;
-  const int rows_per_block = waves * (wide ? 4 : 2);
-  const dim3 grid((N + rows_per_block - 1) / rows_per_block);
-  if (dtype == TW_DTYPE_BF16) {
-    if (wide)
-      hipLaunchKernelGGL((tw::gemv_kernel<tw::BF16, 4>), grid, dim3(tw::kGemvBlock), lds, st,
-                         static_cast<const uint16_t*>(W), static_cast<const uint16_t*>(x),
-                         static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), N, K);
-    else
-      hipLaunchKernelGGL((tw::gemv_kernel<tw::BF16, 2>), grid, dim3(tw::kGemvBlock), lds, st,
-                         static_cast<const uint16_t*>(W), static_cast<const uint16_t*>(x),
-                         static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), N, K);
-  } else if (dtype == TW_DTYPE_F16) {
-    if (wide)
-      hipLaunchKernelGGL((tw::gemv_kernel<tw::F16, 4>), grid, dim3(tw::kGemvBlock), lds, st,
-                         static_cast<const uint16_t*>(W), static_cast<const uint16_t*>(x),
-                         static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), N, K);
-    else
-      hipLaunchKernelGGL((tw::gemv_kernel<tw::F16, 2>), grid, dim3(tw::kGemvBlock), lds, st,
-                         static_cast<const uint16_t*>(W), static_cast<const uint16_t*>(x),
-                         static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y), N, K);
-  } else {
-    return TW_EUNSUPPORTED;
-  }
-  return tw_host::check_launch();
+  if (tw::misaligned(W) || tw::misaligned(x)) return TW_EINVAL;
+  tw::GemvArgs<uint16_t> a{};
+  a.W = static_cast<const uint16_t*>(W);
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.N = N;
+  a.K = K;
+  a.x = static_cast<const uint16_t*>(x);
+  a.y = static_cast<uint16_t*>(y);
+  return tw::launch_gemv_dtype<tw::kProX, tw::kEpiPlain>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+namespace {
+tw::GemvArgs<uint16_t> norm_gemv_args(const void* h_in, const void* delta, const void* norm_w, float eps,
+                                      void* h_out, const void* W, const void* bias, void* y, int N, int K) {
+  tw::GemvArgs<uint16_t> a{};
+  a.W = static_cast<const uint16_t*>(W);
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.N = N;
+  a.K = K;
+  a.h_in = static_cast<const uint16_t*>(h_in);
+  a.delta = static_cast<const uint16_t*>(delta);
+  a.norm_w = static_cast<const uint16_t*>(norm_w);
+  a.eps = eps;
+  a.h_out = static_cast<uint16_t*>(h_out);
+  a.y = static_cast<uint16_t*>(y);
+  return a;
+}
+}  // namespace
+
+extern "C" int tw_rms_norm_gemv(const void* h_in, const void* delta, const void* norm_weight, float eps, void* h_out,
+                                const void* W, const void* bias, void* y, int N, int K, int dtype, void* stream) {
+  const int rc = tw::check_norm_gemv(h_in, delta, norm_weight, h_out, W, y, N, K);
+  if (rc != TW_OK) return rc;
+  return tw::launch_gemv_dtype<tw::kProNorm, tw::kEpiPlain>(
+      norm_gemv_args(h_in, delta, norm_weight, eps, h_out, W, bias, y, N, K), dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tw_rms_norm_gemv_rope(const void* h_in, const void* delta, const void* norm_weight, float eps,
+                                     void* h_out, const void* W, const void* bias, void* y, int N, int K, int Hq,
+                                     int Hk, int D, const void* cos_table, const void* sin_table,
+                                     const int64_t* position, float* q32, int dtype, void* stream) {
+  const int rc = tw::check_norm_gemv(h_in, delta, norm_weight, h_out, W, y, N, K);
+  if (rc != TW_OK) return rc;
+  if (Hq <= 0 || Hk < 0 || D <= 0 || (D % 2) != 0 || (N % D) != 0 || N / D < Hq + Hk || cos_table == nullptr ||
+      sin_table == nullptr || position == nullptr)
+    return TW_EINVAL;
+  tw::GemvArgs<uint16_t> a = norm_gemv_args(h_in, delta, norm_weight, eps, h_out, W, bias, y, N, K);
+  a.Hq = Hq;
+  a.Hk = Hk;
+  a.D = D;
+  a.cos_t = static_cast<const uint16_t*>(cos_table);
+  a.sin_t = static_cast<const uint16_t*>(sin_table);
+  a.pos = position;
+  a.q32 = q32;
+  return tw::launch_gemv_dtype<tw::kProNorm, tw::kEpiRope>(a, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tw_rms_norm_gemv_silu(const void* h_in, const void* delta, const void* norm_weight, float eps,
+                                     void* h_out, const void* W, const void* bias, void* y, int N, int K, int dtype,
+                                     void* stream) {
+  const int rc = tw::check_norm_gemv(h_in, delta, norm_weight, h_out, W, y, N, K);
+  if (rc != TW_OK) return rc;
+  if ((N % 2) != 0) return TW_EINVAL;
+  return tw::launch_gemv_dtype<tw::kProNorm, tw::kEpiSilu>(
+      norm_gemv_args(h_in, delta, norm_weight, eps, h_out, W, bias, y, N, K), dtype, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int tw_add_rms_norm(void* h, const void* delta, const void* weight, float eps, void* out, int rows, int H,

@@ -54,6 +54,10 @@ _HIP_SIGNATURES = {
     "tw_rope_qk": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "tw_silu_mul": (i32, [vp, vp, i32, i32, vp]),
     "tw_gemv": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
+    "tw_rms_norm_gemv": (i32, [vp, vp, vp, f32, vp, vp, vp, vp, i32, i32, i32, vp]),
+    "tw_rms_norm_gemv_rope": (i32, [vp, vp, vp, f32, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32,
+                                    vp]),
+    "tw_rms_norm_gemv_silu": (i32, [vp, vp, vp, f32, vp, vp, vp, vp, i32, i32, i32, vp]),
     "tw_int4_dequantize": (i32, [vp, vp, vp, i32, i64, i32, vp, vp]),
     "tw_quest_score": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp]),
     "tw_topk_sorted": (i32, [vp, i32, i32, i64, i32, vp, vp]),

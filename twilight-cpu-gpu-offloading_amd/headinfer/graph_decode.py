@@ -13,16 +13,20 @@ runner decodes, run_ruler_partial_h2d_tpot_case_v1.py:1302-1322).
 Nothing in the graph depends on a host-side length: the token id, the
 position and the cache length live in device memory and advance at the end
 of the graph, and the ragged kernels derive each group's window, candidate
-pages and decode row from the length.  A layer is 13 launches: residual add
-+ RMSNorm, one q/k/v GEMV, RoPE (which also writes q in fp32 for the Quest
-score), the Quest score and top-k, the page-tile attention and its merge,
-the metadata update, the output GEMV, residual add + RMSNorm, one gate/up
-GEMV, SiLU * up and the down GEMV (tw_gemv: one token, memory-bound, fp32
-accumulation).  The q/k/v and gate/up weights are concatenated once and the
-HF modules keep views into them, so the model's own forward (the prefill)
-uses the same storage.  The element-wise kernels repeat the HF modules'
-rounding steps; the GEMV and RMSNorm reduction orders differ from hipBLASLt
-and torch, so logits follow the eager patched model to bf16 rounding.  Quest selection with an absolute budget (``budget_pages``),
+pages and decode row from the length.  A layer is 9 launches: the q/k/v
+GEMV with the residual add + RMSNorm before it and RoPE after it (q also in
+fp32 for the Quest score), the Quest score and top-k, the page-tile
+attention and its merge, the metadata update, the output GEMV, the gate/up
+GEMV with the residual add + RMSNorm before it and SiLU * up after it, and
+the down GEMV (one token, memory-bound, fp32 accumulation).  The residual
+stream alternates between two buffers, since every GEMV block normalises
+the row itself while block 0 stores the sum.  With fuse=False the norms,
+RoPE and SiLU run as launches of their own (13 per layer) -- the same bits.
+The q/k/v and gate/up weights are concatenated once and the HF modules keep
+views into them, so the model's own forward (the prefill) uses the same
+storage.  The element-wise steps repeat the HF modules' rounding steps; the
+GEMV and RMSNorm reduction orders differ from hipBLASLt and torch, so logits
+follow the eager patched model to bf16 rounding.  Quest selection with an absolute budget (``budget_pages``),
 16-row pages, head_dim 128 and 16-bit K/V only (the page-tile kernel); the
 cache must be built with ``update_metadata_on_decode=True`` so pages
 completed during decode are scored.  While the decoder runs it owns the
@@ -44,7 +48,8 @@ __all__ = ["GraphDecoder"]
 class GraphDecoder:
     """One captured graph per model: ``step()`` decodes one token."""
 
-    def __init__(self, model: torch.nn.Module, cache, *, max_new_tokens: int, fixed_token: Optional[int] = None):
+    def __init__(self, model: torch.nn.Module, cache, *, max_new_tokens: int, fixed_token: Optional[int] = None,
+                 fuse: bool = True):
         if not getattr(cache, "update_metadata_on_decode", False):
             raise ValueError("GraphDecoder needs a cache built with update_metadata_on_decode=True")
         if cache.budget_pages is None:
@@ -77,6 +82,7 @@ class GraphDecoder:
         self.steps_done = 0
         self.max_new_tokens = max_new_tokens
         self.fixed_token = fixed_token
+        self.fuse = fuse
         self.P = min(int(cache._page_min.shape[1]), 8192)
         self.k = min(int(cache.budget_pages), self.P)
         self.width = max(1, min(self.P, self.R * self.k))
@@ -90,7 +96,7 @@ class GraphDecoder:
         cos, sin = inner.rotary_emb(dummy, torch.arange(npos, device=dev)[None])
         self.cos, self.sin = cos[0].contiguous(), sin[0].contiguous()
         # fused projections: one q/k/v and one gate/up weight per layer, the HF modules keep views
-        self.wqkv, self.bqkv, self.wgu = [], [], []
+        self.wqkv, self.bqkv, self.wgu, self.bgu = [], [], [], []
         with torch.no_grad():
             for layer in self.layers:
                 at, mlp = layer.self_attn, layer.mlp
@@ -108,9 +114,15 @@ class GraphDecoder:
                 ni = mlp.gate_proj.weight.shape[0]
                 mlp.gate_proj.weight.data = gu[:ni]
                 mlp.up_proj.weight.data = gu[ni:]
+                bgu = None
+                if mlp.gate_proj.bias is not None:
+                    bgu = torch.cat([mlp.gate_proj.bias, mlp.up_proj.bias]).contiguous()
+                    mlp.gate_proj.bias.data = bgu[:ni]
+                    mlp.up_proj.bias.data = bgu[ni:]
                 self.wqkv.append(w)
                 self.bqkv.append(b)
                 self.wgu.append(gu)
+                self.bgu.append(bgu)
         self.I = self.wgu[0].shape[0] // 2
         hidden = cfg.hidden_size
         self.x = torch.empty((1, hidden), dtype=cache.dtype, device=dev)
@@ -121,6 +133,7 @@ class GraphDecoder:
         self.vocab = model.lm_head.weight.shape[0]
         self.q32 = torch.empty((self.Hq, self.D), dtype=torch.float32, device=dev)
         self.m = torch.empty((1, self.I), dtype=cache.dtype, device=dev)
+        self.hbuf = [torch.empty((1, hidden), dtype=cache.dtype, device=dev) for _ in range(2)]
         # per-layer buffers
         self.plan = [(torch.zeros((self.G, self.width), dtype=torch.int32, device=dev),
                       torch.zeros((self.G, self.width), dtype=torch.uint8, device=dev),
@@ -137,15 +150,35 @@ class GraphDecoder:
         h = F.embedding(self.token, inner.embed_tokens.weight)          # [1, hidden], the residual stream
         x = self.x
         delta: Optional[torch.Tensor] = None
+        flip = 0
+
+        def norm_into(norm, weight, bias, out, epilogue, **kw) -> None:
+            # fused: h_out = h + delta goes to the buffer h is not in
+            nonlocal h, flip
+            h_out = None
+            if delta is not None:
+                h_out = self.hbuf[flip]
+                flip ^= 1
+            kernels.rms_norm_gemv(h, delta, norm.weight, norm.variance_epsilon, h_out, weight, bias, out,
+                                  epilogue=epilogue, **kw)
+            if h_out is not None:
+                h = h_out
+
         for li, layer in enumerate(self.layers):
             attn = layer.self_attn
             norm = layer.input_layernorm
-            kernels.add_rms_norm(h, delta, norm.weight, norm.variance_epsilon, x)
-            qkv = kernels.gemv(x, self.wqkv[li], self.bqkv[li], self.qkv)[0]
+            if self.fuse:
+                norm_into(norm, self.wqkv[li], self.bqkv[li], self.qkv, "rope",
+                          rope=(Hq, G, self.cos, self.sin, self.position), q32=self.q32)
+                qkv = self.qkv[0]
+            else:
+                kernels.add_rms_norm(h, delta, norm.weight, norm.variance_epsilon, x)
+                qkv = kernels.gemv(x, self.wqkv[li], self.bqkv[li], self.qkv)[0]
             q = qkv[:Hq * D].view(Hq, D)
             k = qkv[Hq * D:(Hq + G) * D].view(G, D)
             v = qkv[(Hq + G) * D:].view(G, D)
-            kernels.rope_qk(q, k, self.cos, self.sin, self.position, self.q32)
+            if not self.fuse:
+                kernels.rope_qk(q, k, self.cos, self.sin, self.position, self.q32)
             qg = q.view(G, R, D)
             e0 = li * G
             pp, pm, pc = self.plan[li]
@@ -170,14 +203,22 @@ class GraphDecoder:
                                                 block_size=c.block_size, page_min=c._page_min, page_max=c._page_max)
             o = kernels.gemv(self.attn[li].view(1, Hq * D), attn.o_proj.weight, attn.o_proj.bias, self.o)
             norm = layer.post_attention_layernorm
-            kernels.add_rms_norm(h, o, norm.weight, norm.variance_epsilon, x)
-            gu = kernels.gemv(x, self.wgu[li], None, self.gu)
-            kernels.silu_mul(gu, self.m)
+            delta = o
+            if self.fuse:
+                norm_into(norm, self.wgu[li], self.bgu[li], self.m, "silu")
+            else:
+                kernels.add_rms_norm(h, o, norm.weight, norm.variance_epsilon, x)
+                gu = kernels.gemv(x, self.wgu[li], self.bgu[li], self.gu)
+                kernels.silu_mul(gu, self.m)
             delta = kernels.gemv(self.m, layer.mlp.down_proj.weight, layer.mlp.down_proj.bias, self.dn)
-        kernels.add_rms_norm(h, delta, inner.norm.weight, inner.norm.variance_epsilon, x)
         if self.logits is None:
             self.logits = torch.empty((1, self.vocab), dtype=self.cache.dtype, device=self.dev)
-        logits = kernels.gemv(x, self.model.lm_head.weight, self.model.lm_head.bias, self.logits)
+        if self.fuse:
+            norm_into(inner.norm, self.model.lm_head.weight, self.model.lm_head.bias, self.logits, "plain")
+            logits = self.logits
+        else:
+            kernels.add_rms_norm(h, delta, inner.norm.weight, inner.norm.variance_epsilon, x)
+            logits = kernels.gemv(x, self.model.lm_head.weight, self.model.lm_head.bias, self.logits)
         if self.fixed_token is None:
             self.token.copy_(logits.argmax(dim=-1))
         self.position.add_(1)

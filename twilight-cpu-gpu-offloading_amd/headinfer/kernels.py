@@ -1244,3 +1244,62 @@ def gemv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], ou
     with torch.cuda.device(dev):
         check(hip().tw_gemv(ptr(weight), ptr(x), ptr(bias), ptr(out), N, K, _dt(weight), stream_handle(dev)), "gemv")
     return out
+
+
+def rms_norm_gemv(h: torch.Tensor, delta: Optional[torch.Tensor], norm_weight: torch.Tensor, eps: float,
+                  h_out: Optional[torch.Tensor], weight: torch.Tensor, bias: Optional[torch.Tensor],
+                  out: torch.Tensor, *, epilogue: str = "plain", rope: Optional[tuple] = None,
+                  q32: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One-token nn.Linear whose input is the decoder layer's residual add +
+    RMSNorm, in one launch: x = norm_weight * rms_norm(h + delta), h_out =
+    h + delta (written when delta is given; a buffer other than h and delta),
+    out = x @ weight^T (+ bias).  The same bits as add_rms_norm then gemv.
+
+    epilogue "plain": out [N]; "rope": weight is the concatenated q/k/v
+    projection and out [N] gets q and k rotated as rope_qk does, rope =
+    (Hq, Hk, cos_table, sin_table, position) and q32 [Hq, D] fp32 (nullable)
+    the rotated q; "silu": weight is the concatenated gate/up projection
+    [2I, K] and out [I] = silu(gate) * up as silu_mul does."""
+    if weight.ndim != 2 or not weight.is_contiguous() or weight.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("weight must be contiguous [N, K] fp16/bf16")
+    N, K = weight.shape
+    for name, t in (("h", h), ("delta", delta), ("h_out", h_out), ("norm_weight", norm_weight)):
+        if t is not None and (t.dtype != weight.dtype or t.numel() != K or not t.is_contiguous()):
+            raise ValueError(f"{name} must be contiguous [K] in the weight's dtype")
+    if delta is not None and (h_out is None or h_out.data_ptr() in (h.data_ptr(), delta.data_ptr())):
+        raise ValueError("h_out must be a buffer other than h and delta")
+    if bias is not None and (bias.dtype != weight.dtype or bias.numel() != N or not bias.is_contiguous()):
+        raise ValueError("bias must be contiguous [N]")
+    n_out = N // 2 if epilogue == "silu" else N
+    if out.dtype != weight.dtype or out.numel() != n_out or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous [{n_out}] in the weight's dtype")
+    dev = _require_device(h, delta, norm_weight, h_out, weight, bias, out, q32, what="rms_norm_gemv")
+    args = (ptr(h), ptr(delta), ptr(norm_weight), float(eps), ptr(h_out), ptr(weight), ptr(bias), ptr(out), N, K)
+    with torch.cuda.device(dev):
+        if epilogue == "plain":
+            check(hip().tw_rms_norm_gemv(*args, _dt(weight), stream_handle(dev)), "rms_norm_gemv")
+        elif epilogue == "silu":
+            if N % 2:
+                raise ValueError("the gate/up weight needs an even row count")
+            check(hip().tw_rms_norm_gemv_silu(*args, _dt(weight), stream_handle(dev)), "rms_norm_gemv")
+        elif epilogue == "rope":
+            if rope is None:
+                raise ValueError("the rope epilogue needs rope=(Hq, Hk, cos_table, sin_table, position)")
+            Hq, Hk, cos_table, sin_table, position = rope
+            D = cos_table.shape[1]
+            if N % D or N // D < Hq + Hk:
+                raise ValueError("the q/k/v weight rows must hold Hq + Hk (+ Hv) heads of head_dim rows")
+            if cos_table.dtype != weight.dtype or sin_table.shape != cos_table.shape or cos_table.ndim != 2 \
+                    or not cos_table.is_contiguous() or not sin_table.is_contiguous():
+                raise ValueError("cos/sin tables must be contiguous [positions, D] in the weight's dtype")
+            if position.dtype != torch.int64 or position.numel() != 1:
+                raise ValueError("position must be one int64")
+            if q32 is not None and (q32.dtype != torch.float32 or q32.numel() != Hq * D or not q32.is_contiguous()):
+                raise ValueError("q32 must be contiguous fp32 [Hq, D]")
+            _require_device(cos_table, sin_table, position, what="rms_norm_gemv")
+            check(hip().tw_rms_norm_gemv_rope(*args, int(Hq), int(Hk), int(D), ptr(cos_table), ptr(sin_table),
+                                              ptr(position), ptr(q32), _dt(weight), stream_handle(dev)),
+                  "rms_norm_gemv")
+        else:
+            raise ValueError(f"unknown epilogue {epilogue!r}")
+    return out
