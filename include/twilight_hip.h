@@ -312,14 +312,19 @@ int tw_decode_attention_pages_phase(const void* q, const void* k_base, const voi
  * attended); lengths[g] must be below entry_stride_rows (larger values are
  * clamped).  Workspace as tw_decode_attention_workspace_size(G, R, D,
  * max_rows).  Batches the reference's batch-1 GQA decode attention
- * (mp.py:239-279) over requests. */
+ * (mp.py:239-279) over requests.  page_min/page_max (nullable, append != 0):
+ * the decode-time metadata update of tw_update_page_metadata_ragged fused
+ * in -- when the appended row L_g completes page p ((L_g - sink + 1) % 16 ==
+ * 0, p < meta_pages), page_min/page_max[g * page_entry_stride + p * D ..]
+ * (16-bit, 4-byte aligned) get that page's min/max. */
 int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
                                      int D, const int32_t* plan_pages, const uint8_t* plan_masks,
                                      const int32_t* plan_counts, int64_t plan_stride, int max_rows,
                                      int64_t entry_stride_rows, int sink, int recent, int block_size,
                                      const int32_t* lengths, int append, const void* cur_k, const void* cur_v,
-                                     float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
-                                     void* stream);
+                                     float softmax_scale, void* page_min, void* page_max,
+                                     int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
+                                     size_t workspace_bytes, void* stream);
 /* Page-tile attention with a resident page cache in HBM, for slabs in host
  * memory.  Replaces the previous-token resident cache of the Twilight cache
  * (previous_token_resident_cache, twilight_offload_cache.py:2457-2608,
@@ -334,8 +339,9 @@ int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const vo
  * accumulates (hit pages, union pages).  lengths (device, per group) or,
  * when NULL, `length` for every group gives the window and the decode token
  * row, which is appended there from cur_k/cur_v when append != 0 -- the
- * semantics of tw_decode_attention_pages_ragged.  Union indexes at or above
- * res_slots are read from the slab and not stored. */
+ * semantics of tw_decode_attention_pages_ragged, as is the fused page
+ * metadata update (page_min/page_max).  Union indexes at or above res_slots
+ * are read from the slab and not stored. */
 int tw_decode_attention_pages_resident(const void* q, const void* k_base, const void* v_base, int dtype, int G,
                                        int R, int D, const int32_t* plan_pages, const uint8_t* plan_masks,
                                        const int32_t* plan_counts, int64_t plan_stride, int max_rows,
@@ -343,7 +349,8 @@ int tw_decode_attention_pages_resident(const void* q, const void* k_base, const 
                                        const int32_t* lengths, int length, int append, const void* cur_k,
                                        const void* cur_v, float softmax_scale, void* res_k, void* res_v,
                                        int64_t* res_map, int res_slots, int res_map_pages,
-                                       unsigned long long* res_stats, void* out, void* workspace,
+                                       unsigned long long* res_stats, void* page_min, void* page_max,
+                                       int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
                                        size_t workspace_bytes, void* stream);
 int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G,
                         int R, int D, const int32_t* rows, const uint8_t* row_masks,

@@ -289,12 +289,13 @@ def test_rms_norm_gemv_matches_separate_launches(dev, dtype):
 
 def test_graph_decoder_fused_equals_unfused(dev):
     """GraphDecoder with the norms, RoPE and SiLU fused into the GEMVs == the
-    same decoder with them as launches of their own, bit for bit."""
+    same decoder with them as launches of their own, bit for bit (the steps
+    cross a page completion, so the fused metadata update is exercised)."""
     from headinfer import mp
     from headinfer.graph_decode import GraphDecoder
     from headinfer.quest_offload_cache import QuestTopKOffloadedCache
 
-    steps = 4
+    steps = 10
     _, gpu = _models(dev)
     mp.mp_headinfer(gpu)
     kw = dict(max_cache_len=T_PROMPT + steps + 2, sink_tokens=64, recent_tokens=256, block_size=16,
@@ -313,3 +314,8 @@ def test_graph_decoder_fused_equals_unfused(dev):
             torch.cuda.synchronize()
             assert torch.equal(a, b), step
             assert torch.equal(decs[0].token, decs[1].token), step
+    assert torch.equal(caches[0]._page_min, caches[1]._page_min)
+    assert torch.equal(caches[0]._page_max, caches[1]._page_max)
+    n = T_PROMPT + steps   # rows beyond are never written
+    assert torch.equal(caches[0]._key_cache[:, :n], caches[1]._key_cache[:, :n])
+    assert torch.equal(caches[0]._value_cache[:, :n], caches[1]._value_cache[:, :n])

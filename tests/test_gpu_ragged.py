@@ -316,3 +316,57 @@ def test_resident_page_cache_bit_exact(K, dev, ragged):
     assert same_bits(kh, kh2) and same_bits(vh, vh2)   # the appends landed alike
     hits, union = res.stats.sum(dim=0).tolist()
     assert union > 0 and 0 < hits < union, (hits, union)
+
+
+@pytest.mark.parametrize("resident", [False, True])
+def test_attention_fused_page_metadata(K, dev, resident):
+    """The ragged page-tile attention with the page-metadata update fused in:
+    40 decode steps from lengths of different page phases (one appended row
+    holds a NaN) leave page_min/page_max equal to a rebuild over the final
+    rows, and every step's output equals the launch without the update."""
+    _say(f"[fused page metadata] resident={resident}")
+    dtype, R, k, steps = "bf16", 4, 16, 40
+    lengths0 = [100, 143, 200, 300]
+    G = len(lengths0)
+    Lmax = max(lengths0) + steps + 16
+    keys = randn((G, Lmax, D), dtype, seed=131)
+    vals = randn((G, Lmax, D), dtype, seed=132)
+    kd, vd = keys.to(dev), vals.to(dev)
+    kd2, vd2 = keys.to(dev), vals.to(dev)
+    pmin, pmax = _metadata(keys, lengths0, dtype, dev)
+    P = pmin.shape[1]
+    width = min(P, R * k)
+    res = K.ResidentPages(G, width, P, D, keys.dtype, dev) if resident else None
+    lengths = torch.tensor(lengths0, dtype=torch.int32, device=dev)
+    g = torch.Generator().manual_seed(133)
+    for step in range(steps):
+        q = torch.randn((G, R, D), generator=g).to(torch.bfloat16)
+        ck, cv = randn((G, D), dtype, seed=400 + step), randn((G, D), dtype, seed=500 + step)
+        if step == 11:
+            ck[0, 5] = float("nan")
+        pp = torch.zeros((G, width), dtype=torch.int32, device=dev)
+        pm = torch.zeros((G, width), dtype=torch.uint8, device=dev)
+        pc = torch.zeros((G,), dtype=torch.int32, device=dev)
+        K.quest_select_ragged(q.float().to(dev), pmin, pmax, lengths, k, sink=SINK, recent=RECENT, block_size=BS,
+                              plan_pages=pp, plan_masks=pm, plan_counts=pc)
+        kw = dict(plan_masks=pm, max_pages=width, sink=SINK, recent=RECENT, block_size=BS, append=True,
+                  cur_k=ck.to(dev), cur_v=cv.to(dev))
+        if resident:
+            a = K.decode_attention_pages_resident(q.to(dev), kd, vd, pp, pc, res, lengths=lengths, page_min=pmin,
+                                                  page_max=pmax, **kw)
+        else:
+            a = K.decode_attention_pages_ragged(q.to(dev), kd, vd, pp, pc, lengths, page_min=pmin, page_max=pmax,
+                                                **kw)
+        b = K.decode_attention_pages_ragged(q.to(dev), kd2, vd2, pp, pc, lengths, **kw)
+        torch.cuda.synchronize()
+        assert same_bits(a, b), step
+        lengths += 1
+    assert same_bits(kd, kd2) and same_bits(vd, vd2)
+    for gi, L0 in enumerate(lengths0):
+        n = L0 + steps
+        omin, omax, _, _, _ = oracle.build_page_metadata(to_bits(kd[gi, :n].cpu()), dtype, SINK, BS, quant=False)
+        p = omin.shape[0]
+        assert same_bits(pmin[gi, :p], from_bits(omin, dtype)) and same_bits(pmax[gi, :p], from_bits(omax, dtype)), gi
+    with pytest.raises(ValueError):
+        K.decode_attention_pages_ragged(q.to(dev), kd, vd, pp, pc, lengths, page_min=pmin, page_max=pmax,
+                                        **dict(kw, append=False))

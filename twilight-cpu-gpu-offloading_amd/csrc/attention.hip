@@ -103,6 +103,14 @@ struct AttnArgs {
   int res_slots;
   int res_map_pages;
   unsigned long long* res_stats;
+  // Page metadata of the appended row (page-tile kernel, nullable): when the
+  // row completes page p of its entry (row - sink + 1 a multiple of 16),
+  // meta_min/meta_max [G][meta_stride] get that page's per-channel min/max
+  // at p * D (p < meta_pages).
+  void* meta_min;
+  void* meta_max;
+  int64_t meta_stride;
+  int meta_pages;
 };
 
 // 8 consecutive channels of one row.
@@ -230,6 +238,53 @@ __device__ __forceinline__ GroupRows group_rows(const AttnArgs& a, int g, int D)
 
 // Page-tile mode (decode_attn_tiles): chunks count 16-row tiles.
 constexpr int kModeTiles = 3;
+
+// The min/max of the 16-row page the appended row `position` of group g
+// completes, by wave 0 of the block: lane l owns channels 2l and 2l + 1 of
+// all 16 rows (one 4-byte load per row, all in flight together), compared as
+// order keys; a NaN in a channel makes that channel's min and max the
+// canonical NaN -- the page rule of the metadata build, so the result equals
+// a rebuild.  The appended row is read from cur_k when given.
+template <typename DT>
+__device__ __forceinline__ void complete_page_meta(const AttnArgs& a, int g, int position) {
+  using S = typename DT::storage;
+  constexpr int D = 128, BS = 16;
+  if (a.meta_min == nullptr || position < a.sink || threadIdx.x >= kWave) return;
+  const int j = position - a.sink;
+  if ((j + 1) % BS != 0 || j / BS >= a.meta_pages) return;
+  const int page = j / BS;
+  const int lane = static_cast<int>(threadIdx.x);
+  const S* kg = static_cast<const S*>(a.k) + static_cast<int64_t>(g) * a.entry_stride * D;
+  const S* cur = a.cur_k != nullptr ? static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * D : nullptr;
+  uint32_t v[BS];
+#pragma unroll
+  for (int i = 0; i < BS; ++i) {
+    const int t = a.sink + page * BS + i;
+    const S* row = (t == position && cur != nullptr) ? cur : kg + static_cast<int64_t>(t) * D;
+    v[i] = *reinterpret_cast<const uint32_t*>(row + 2 * lane);
+  }
+  uint32_t kmin[2] = {0xffffffffu, 0xffffffffu}, kmax[2] = {0u, 0u};
+  bool nan[2] = {false, false};
+#pragma unroll
+  for (int i = 0; i < BS; ++i) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const S x = static_cast<S>(h ? (v[i] >> 16) : (v[i] & 0xffffu));
+      const uint32_t k = order_key(DT{}, x);
+      nan[h] |= is_nan(DT{}, x);
+      kmin[h] = k < kmin[h] ? k : kmin[h];
+      kmax[h] = k > kmax[h] ? k : kmax[h];
+    }
+  }
+  const int64_t at = static_cast<int64_t>(g) * a.meta_stride + static_cast<int64_t>(page) * D + 2 * lane;
+  S* mn = static_cast<S*>(a.meta_min) + at;
+  S* mx = static_cast<S*>(a.meta_max) + at;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    mn[h] = nan[h] ? canonical_nan(DT{}) : from_order_key(DT{}, kmin[h]);
+    mx[h] = nan[h] ? canonical_nan(DT{}) : from_order_key(DT{}, kmax[h]);
+  }
+}
 constexpr int kTileRows = 16;
 
 // Window of group g in a page-tile launch: the host's (one length for every
@@ -1143,7 +1198,10 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if (chunk == 0) append_decode_token<S>(a, g, D, win.append_position);
+  if (chunk == 0) {
+    append_decode_token<S>(a, g, D, win.append_position);
+    complete_page_meta<DT>(a, g, win.append_position);
+  }
 
   const S* kg = static_cast<const S*>(a.k) + static_cast<int64_t>(g) * a.entry_stride * D;
   const S* vg = static_cast<const S*>(a.v) + static_cast<int64_t>(g) * a.entry_stride * D;
@@ -1916,9 +1974,15 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
                        int64_t plan_stride, int max_rows, int64_t entry_stride_rows, int sink, int recent,
                        int block_size, const int32_t* lengths, int length, int append, const void* cur_k,
                        const void* cur_v, float softmax_scale, void* res_k, void* res_v, int64_t* res_map,
-                       int res_slots, int res_map_pages, unsigned long long* res_stats, void* out, void* workspace,
+                       int res_slots, int res_map_pages, unsigned long long* res_stats, void* page_min,
+                       void* page_max, int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
                        size_t workspace_bytes, void* stream) {
   if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr) return TW_EINVAL;
+  if (page_min != nullptr &&
+      (page_max == nullptr || append == 0 || meta_pages < 1 ||
+       page_entry_stride < static_cast<int64_t>(meta_pages) * kTileD ||
+       (reinterpret_cast<uintptr_t>(page_min) % 4) || (reinterpret_cast<uintptr_t>(page_max) % 4)))
+    return TW_EINVAL;
   if (G <= 0 || R <= 0 || R > 8 || plan_pages == nullptr || plan_counts == nullptr || plan_stride < 1) return TW_EINVAL;
   if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16) return TW_EUNSUPPORTED;
   if (D != kTileD || block_size != kTileRows) return TW_EUNSUPPORTED;
@@ -1973,6 +2037,10 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
   a.res_slots = res_slots;
   a.res_map_pages = res_map_pages;
   a.res_stats = res_stats;
+  a.meta_min = page_min;
+  a.meta_max = page_max;
+  a.meta_stride = page_entry_stride;
+  a.meta_pages = meta_pages;
   plan_tile_chunks(G, max_rows, &a.iters, &a.max_chunks);
   a.t_per_chunk = a.iters * kTileNW * kTileTW;
   if (lengths != nullptr) {
@@ -2016,13 +2084,14 @@ extern "C" int tw_decode_attention_pages_resident(
     const uint8_t* plan_masks, const int32_t* plan_counts, int64_t plan_stride, int max_rows,
     int64_t entry_stride_rows, int sink, int recent, int block_size, const int32_t* lengths, int length, int append,
     const void* cur_k, const void* cur_v, float softmax_scale, void* res_k, void* res_v, int64_t* res_map,
-    int res_slots, int res_map_pages, unsigned long long* res_stats, void* out, void* workspace,
-    size_t workspace_bytes, void* stream) {
+    int res_slots, int res_map_pages, unsigned long long* res_stats, void* page_min, void* page_max,
+    int64_t page_entry_stride, int meta_pages, void* out, void* workspace, size_t workspace_bytes, void* stream) {
   if (res_map == nullptr) return TW_EINVAL;
   return tw::pages_tiles_launch(q, k_base, v_base, dtype, G, R, D, plan_pages, plan_masks, plan_counts, plan_stride,
                                 max_rows, entry_stride_rows, sink, recent, block_size, lengths, length, append, cur_k,
-                                cur_v, softmax_scale, res_k, res_v, res_map, res_slots, res_map_pages, res_stats, out,
-                                workspace, workspace_bytes, stream);
+                                cur_v, softmax_scale, res_k, res_v, res_map, res_slots, res_map_pages, res_stats,
+                                page_min, page_max, page_entry_stride, meta_pages, out, workspace, workspace_bytes,
+                                stream);
 }
 
 extern "C" int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const void* v_base, int dtype,
@@ -2030,12 +2099,14 @@ extern "C" int tw_decode_attention_pages_ragged(const void* q, const void* k_bas
                                                 const uint8_t* plan_masks, const int32_t* plan_counts,
                                                 int64_t plan_stride, int max_rows, int64_t entry_stride_rows, int sink,
                                                 int recent, int block_size, const int32_t* lengths, int append,
-                                                const void* cur_k, const void* cur_v, float softmax_scale, void* out,
-                                                void* workspace, size_t workspace_bytes, void* stream) {
+                                                const void* cur_k, const void* cur_v, float softmax_scale,
+                                                void* page_min, void* page_max, int64_t page_entry_stride,
+                                                int meta_pages, void* out, void* workspace, size_t workspace_bytes,
+                                                void* stream) {
   if (lengths == nullptr) return TW_EINVAL;
   return tw::pages_tiles_launch(q, k_base, v_base, dtype, G, R, D, plan_pages, plan_masks, plan_counts, plan_stride,
                                 max_rows, entry_stride_rows, sink, recent, block_size, lengths, 0, append, cur_k,
-                                cur_v, softmax_scale, nullptr, nullptr, nullptr, 0, 0, nullptr, out, workspace,
-                                workspace_bytes, stream);
+                                cur_v, softmax_scale, nullptr, nullptr, nullptr, 0, 0, nullptr, page_min, page_max,
+                                page_entry_stride, meta_pages, out, workspace, workspace_bytes, stream);
 }
 

@@ -166,8 +166,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const typename DT::storag
 // y[n] = x . W[n, :] (+ bias[n]) for one row x [K] and W [N][K] row-major
 // (nn.Linear's weight), the decode token's projections.  x is staged in LDS
 // once per block; wave w of a block owns rows (block * 4 + w) * RPW ..; lane
-// l reads the 16-byte chunks l, l + 64, ... of each of its rows, two chunks
-// of every row in flight per step, and accumulates them with
+// l reads the 16-byte chunks l, l + 64, ... of each of its rows, 16 / RPW
+// chunks of every row in flight per step, and accumulates them with
 // v_dot2_f32_{bf16,f16} in fp32; a wave reduction ends each row.
 constexpr int kGemvBlock = 256;
 
@@ -262,15 +262,22 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
   const uint4* rowp[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) rowp[r] = w4 + static_cast<int64_t>(rows[r]) * kc;
-  // the first weight chunks are in flight while x is prepared
+  // A step covers chunks c + u * kWave, u < U, of every row: U * RPW
+  // 16-byte loads per lane (8 KB per wave) are in flight before any is
+  // used; the first step's are issued while x is prepared.  Each lane sums
+  // its chunks in increasing order.
+  constexpr int U = 16 / RPW;
   int c = lane;
-  uint4 wa[RPW], wb[RPW];
-  const bool two = c + kWave < kc;
+  uint4 wv[U][RPW];
+  auto load_step = [&](int c0) {
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    wa[r] = rowp[r][c < kc ? c : 0];
-    wb[r] = rowp[r][two ? c + kWave : 0];
-  }
+    for (int u = 0; u < U; ++u) {
+      const int idx = c0 + u * kWave;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) wv[u][r] = rowp[r][idx < kc ? idx : 0];
+    }
+  };
+  load_step(c);
   if (PRO == kProNorm) {
     rms_norm_row<DT>(a.h_in, a.delta, a.norm_w, a.eps, K,
                      (blockIdx.x == 0 && a.delta != nullptr) ? a.h_out : nullptr, s_part,
@@ -285,31 +292,18 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
   while (true) {
-    if (!two && c < kc) {
-      const uint4 xa = xs[c];
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) acc[r] = dot8<DT>(wa[r], xa, acc[r]);
-      break;
+    for (int u = 0; u < U; ++u) {
+      const int idx = c + u * kWave;
+      if (idx < kc) {
+        const uint4 xv = xs[idx];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) acc[r] = dot8<DT>(wv[u][r], xv, acc[r]);
+      }
     }
+    c += U * kWave;
     if (c >= kc) break;
-    const uint4 xa = xs[c];
-    const uint4 xb = xs[c + kWave];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = dot8<DT>(wb[r], xb, dot8<DT>(wa[r], xa, acc[r]));
-    c += 2 * kWave;
-    if (c >= kc) break;
-    const bool nxt2 = c + kWave < kc;
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      wa[r] = rowp[r][c];
-      wb[r] = rowp[r][nxt2 ? c + kWave : 0];
-    }
-    if (!nxt2) {
-      const uint4 xl = xs[c];
-#pragma unroll
-      for (int r = 0; r < RPW; ++r) acc[r] = dot8<DT>(wa[r], xl, acc[r]);
-      break;
-    }
+    load_step(c);
   }
   float v[RPW];
 #pragma unroll

@@ -13,15 +13,17 @@ runner decodes, run_ruler_partial_h2d_tpot_case_v1.py:1302-1322).
 Nothing in the graph depends on a host-side length: the token id, the
 position and the cache length live in device memory and advance at the end
 of the graph, and the ragged kernels derive each group's window, candidate
-pages and decode row from the length.  A layer is 9 launches: the q/k/v
+pages and decode row from the length.  A layer is 8 launches: the q/k/v
 GEMV with the residual add + RMSNorm before it and RoPE after it (q also in
 fp32 for the Quest score), the Quest score and top-k, the page-tile
-attention and its merge, the metadata update, the output GEMV, the gate/up
-GEMV with the residual add + RMSNorm before it and SiLU * up after it, and
-the down GEMV (one token, memory-bound, fp32 accumulation).  The residual
-stream alternates between two buffers, since every GEMV block normalises
-the row itself while block 0 stores the sum.  With fuse=False the norms,
-RoPE and SiLU run as launches of their own (13 per layer) -- the same bits.
+attention (which also appends the decode token and updates the min/max of
+a page it completes) and its merge, the output GEMV, the gate/up GEMV with
+the residual add + RMSNorm before it and SiLU * up after it, and the down
+GEMV (one token, memory-bound, fp32 accumulation).  The residual stream
+alternates between two buffers, since every GEMV block normalises the row
+itself while block 0 stores the sum.  With fuse=False the norms, RoPE, SiLU
+and the metadata update run as launches of their own (13 per layer) -- the
+same bits.
 The q/k/v and gate/up weights are concatenated once and the HF modules keep
 views into them, so the model's own forward (the prefill) uses the same
 storage.  The element-wise steps repeat the HF modules' rounding steps; the
@@ -186,21 +188,25 @@ class GraphDecoder:
                                         c._page_max[e0:e0 + G, :self.P], self.lengths, self.k, sink=c.sink_tokens,
                                         recent=c.recent_tokens, block_size=c.block_size, plan_pages=pp,
                                         plan_masks=pm, plan_counts=pc)
+            # the attention also appends the decode token and, when it completes a page, that page's min/max
+            meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G]) if self.fuse else {}
             if c.previous_token_resident_cache:
                 kernels.decode_attention_pages_resident(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp,
                                                         pc, c.resident_pages().view(e0, G), lengths=self.lengths,
                                                         plan_masks=pm, max_pages=self.width, sink=c.sink_tokens,
                                                         recent=c.recent_tokens, block_size=c.block_size, append=True,
                                                         cur_k=k, cur_v=v, softmax_scale=float(attn.scaling),
-                                                        out=self.attn[li])
+                                                        out=self.attn[li], **meta)
             else:
                 kernels.decode_attention_pages_ragged(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp,
                                                       pc, self.lengths, plan_masks=pm, max_pages=self.width,
                                                       sink=c.sink_tokens, recent=c.recent_tokens,
                                                       block_size=c.block_size, append=True, cur_k=k, cur_v=v,
-                                                      softmax_scale=float(attn.scaling), out=self.attn[li])
-            kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
-                                                block_size=c.block_size, page_min=c._page_min, page_max=c._page_max)
+                                                      softmax_scale=float(attn.scaling), out=self.attn[li], **meta)
+            if not self.fuse:
+                kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
+                                                    block_size=c.block_size, page_min=c._page_min,
+                                                    page_max=c._page_max)
             o = kernels.gemv(self.attn[li].view(1, Hq * D), attn.o_proj.weight, attn.o_proj.bias, self.o)
             norm = layer.post_attention_layernorm
             delta = o

@@ -747,6 +747,22 @@ def decode_attention_pages(
     return out
 
 
+def _page_meta_args(page_min: Optional[torch.Tensor], page_max: Optional[torch.Tensor], G: int, D: int,
+                    append: bool) -> tuple:
+    """(ptr min, ptr max, entry stride, pages) of the fused page-metadata
+    update; page_min/page_max [G, pages, D] views with contiguous pages."""
+    if page_min is None and page_max is None:
+        return None, None, 0, 0
+    if page_min is None or page_max is None:
+        raise ValueError("page_min and page_max go together")
+    if not append:
+        raise ValueError("the page metadata update follows the appended row (append=True)")
+    if page_min.ndim != 3 or page_min.shape[0] != G or page_min.shape[2] != D or page_min.stride(2) != 1 \
+            or page_min.stride(1) != D or page_max.shape != page_min.shape or page_max.stride() != page_min.stride():
+        raise ValueError("page_min/page_max must be [G, pages, D] with contiguous pages")
+    return ptr(page_min), ptr(page_max), page_min.stride(0), page_min.shape[1]
+
+
 def decode_attention_pages_ragged(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -765,13 +781,17 @@ def decode_attention_pages_ragged(
     cur_v: Optional[torch.Tensor] = None,
     softmax_scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
+    page_min: Optional[torch.Tensor] = None,
+    page_max: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """decode_attention_pages over G groups of different lengths (lengths [G]
     int32 on the device): group g's window follows from its own length and
     its decode token is cur_k/cur_v[g] (appended at row lengths[g] when
     `append`), or the cache row lengths[g] (`append`, no cur_k), or none.
     16-bit K/V, D = 128, block_size 16.  k_cache/v_cache [G, Lmax, D] (HBM or
-    pinned host).  Returns [G, R, D]."""
+    pinned host).  With page_min/page_max [G, pages, D] the launch also does
+    update_page_metadata_ragged's min/max of a page the appended row
+    completes.  Returns [G, R, D]."""
     if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("q must be [G, R, D] fp16/bf16")
     G, R, D = q.shape
@@ -797,8 +817,9 @@ def decode_attention_pages_ragged(
     if cur_k is not None and (cur_k.shape != (G, D) or cur_k.dtype != q.dtype or cur_v.shape != cur_k.shape
                               or cur_v.dtype != q.dtype):
         raise ValueError("cur_k/cur_v must be [G, D] in q's dtype")
-    dev = _require_device(q, plan_pages, plan_masks, plan_counts, lengths, cur_k, cur_v,
+    dev = _require_device(q, plan_pages, plan_masks, plan_counts, lengths, cur_k, cur_v, page_min, page_max,
                           what="decode_attention_pages_ragged")
+    meta = _page_meta_args(page_min, page_max, G, D, append)
     kp, vp = _slab_source(k_cache, v_cache)
     _require_contiguous(q, cur_k, cur_v, what="decode_attention_pages_ragged")
     if out is None:
@@ -812,7 +833,7 @@ def decode_attention_pages_ragged(
                                                      ptr(plan_masks), ptr(plan_counts), plan_pages.stride(0),
                                                      max_rows, k_cache.stride(0) // D, sink, recent, block_size,
                                                      ptr(lengths), int(bool(append)), ptr(cur_k), ptr(cur_v), scale,
-                                                     ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
+                                                     *meta, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
               "decode_attention_pages_ragged")
     return out
 
@@ -858,12 +879,15 @@ def decode_attention_pages_resident(
     cur_v: Optional[torch.Tensor] = None,
     softmax_scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
+    page_min: Optional[torch.Tensor] = None,
+    page_max: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """decode_attention_pages (lengths None: one `length`) or its ragged form
     (lengths [G] int32 on the device), with union pages kept in an HBM
     resident page cache: pages the previous step stored are read from HBM,
     the rest from the slab, and every union page read is stored for the next
-    step.  16-bit K/V, D = 128, block_size 16.  Returns [G, R, D]."""
+    step.  16-bit K/V, D = 128, block_size 16.  page_min/page_max as in
+    decode_attention_pages_ragged.  Returns [G, R, D]."""
     if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("q must be [G, R, D] fp16/bf16")
     G, R, D = q.shape
@@ -896,8 +920,9 @@ def decode_attention_pages_resident(
     if cur_k is not None and (cur_k.shape != (G, D) or cur_k.dtype != q.dtype or cur_v.shape != cur_k.shape
                               or cur_v.dtype != q.dtype):
         raise ValueError("cur_k/cur_v must be [G, D] in q's dtype")
-    dev = _require_device(q, plan_pages, plan_masks, plan_counts, lengths, cur_k, cur_v, rk, rv, rm, rs,
-                          what="decode_attention_pages_resident")
+    dev = _require_device(q, plan_pages, plan_masks, plan_counts, lengths, cur_k, cur_v, rk, rv, rm, rs, page_min,
+                          page_max, what="decode_attention_pages_resident")
+    meta = _page_meta_args(page_min, page_max, G, D, append)
     kp, vp = _slab_source(k_cache, v_cache)
     _require_contiguous(q, cur_k, cur_v, what="decode_attention_pages_resident")
     if out is None:
@@ -911,7 +936,7 @@ def decode_attention_pages_resident(
             ptr(q), kp, vp, _dt(q), G, R, D, ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
             plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink, recent, block_size, ptr(lengths),
             int(length), int(bool(append)), ptr(cur_k), ptr(cur_v), scale, ptr(rk), ptr(rv), ptr(rm),
-            resident.slots, resident.pages, ptr(rs), ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
+            resident.slots, resident.pages, ptr(rs), *meta, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
             "decode_attention_pages_resident")
     return out
 
