@@ -22,81 +22,91 @@ constexpr int kNormBlock = 256;
 // the block's waves.  H % 8 == 0, H <= kNormBlock * 8 * kNormVec.
 constexpr int kNormVec = 4;
 
-// The residual add + RMSNorm of one row by a block of kNormBlock threads:
-// a = bf16(h + delta) (a = h without delta) is stored to h_store (nullable),
-// and put(i, chunk) receives the 16-byte chunk i of bf16(w * bf16(a * r)).
-// Thread t owns chunks t + c * kNormBlock; the sum of squares runs over its
-// chunks in order, then a wave reduction, then the waves in order, so every
-// block computing the same row gets the same bits.
-template <typename DT, typename Put>
-__device__ __forceinline__ void rms_norm_row(const typename DT::storage* __restrict__ h,
-                                             const typename DT::storage* __restrict__ delta,
-                                             const typename DT::storage* __restrict__ w, float eps, int H,
-                                             typename DT::storage* h_store, float* s_part, Put put) {
+// The residual add + RMSNorm of one row by a block of kNormBlock threads,
+// in two calls so that other loads can be issued between them: load() reads
+// the thread's chunks of h, delta and w; finish() stores a = bf16(h + delta)
+// (a = h without delta) to h_store (nullable) and passes the 16-byte chunk i
+// of bf16(w * bf16(a * r)) to put(i, chunk).  Thread t owns chunks t + c *
+// kNormBlock, c < NV; the sum of squares runs over its chunks in order, then
+// a wave reduction, then the waves in order, so every block computing the
+// same row gets the same bits, whatever NV covers the row.
+template <typename DT, int NV>
+struct NormRow {
   using S = typename DT::storage;
-  const uint4* hr = reinterpret_cast<const uint4*>(h);
-  const uint4* dr = reinterpret_cast<const uint4*>(delta);
-  const uint4* wr = reinterpret_cast<const uint4*>(w);
-  uint4* hs = reinterpret_cast<uint4*>(h_store);
-  const int nv = H / 8;
-  uint4 hv[kNormVec], dv[kNormVec], wv[kNormVec];
+  uint4 hv[NV], dv[NV], wv[NV];
+  bool has_delta;
+
+  __device__ __forceinline__ void load(const S* __restrict__ h, const S* __restrict__ delta,
+                                       const S* __restrict__ w, int H) {
+    const uint4* hr = reinterpret_cast<const uint4*>(h);
+    const uint4* dr = reinterpret_cast<const uint4*>(delta);
+    const uint4* wr = reinterpret_cast<const uint4*>(w);
+    const int nv = H / 8;
+    has_delta = dr != nullptr;
 #pragma unroll
-  for (int c = 0; c < kNormVec; ++c) {
-    const int i = threadIdx.x + c * kNormBlock;
-    const int j = i < nv ? i : 0;
-    hv[c] = hr[j];
-    dv[c] = dr != nullptr ? dr[j] : make_uint4(0u, 0u, 0u, 0u);
-    wv[c] = wr[j];
+    for (int c = 0; c < NV; ++c) {
+      const int i = threadIdx.x + c * kNormBlock;
+      const int j = i < nv ? i : 0;
+      hv[c] = hr[j];
+      dv[c] = dr != nullptr ? dr[j] : make_uint4(0u, 0u, 0u, 0u);
+      wv[c] = wr[j];
+    }
   }
-  float x[kNormVec][8];
-  float acc = 0.0f;
+
+  template <typename Put>
+  __device__ __forceinline__ void finish(float eps, int H, S* h_store, float* s_part, Put put) {
+    uint4* hs = reinterpret_cast<uint4*>(h_store);
+    const int nv = H / 8;
+    float x[NV][8];
+    float acc = 0.0f;
 #pragma unroll
-  for (int c = 0; c < kNormVec; ++c) {
-    const uint32_t hw[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
-    const uint32_t dw[4] = {dv[c].x, dv[c].y, dv[c].z, dv[c].w};
-    uint32_t ow[4];
+    for (int c = 0; c < NV; ++c) {
+      const uint32_t hw[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
+      const uint32_t dw[4] = {dv[c].x, dv[c].y, dv[c].z, dv[c].w};
+      uint32_t ow[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float a = to_f32(DT{}, static_cast<S>(hw[e] & 0xffffu));
-      float b = to_f32(DT{}, static_cast<S>(hw[e] >> 16));
-      if (dr != nullptr) {
-        a = round_to<DT>(a + to_f32(DT{}, static_cast<S>(dw[e] & 0xffffu)));
-        b = round_to<DT>(b + to_f32(DT{}, static_cast<S>(dw[e] >> 16)));
+      for (int e = 0; e < 4; ++e) {
+        float a = to_f32(DT{}, static_cast<S>(hw[e] & 0xffffu));
+        float b = to_f32(DT{}, static_cast<S>(hw[e] >> 16));
+        if (has_delta) {
+          a = round_to<DT>(a + to_f32(DT{}, static_cast<S>(dw[e] & 0xffffu)));
+          b = round_to<DT>(b + to_f32(DT{}, static_cast<S>(dw[e] >> 16)));
+        }
+        x[c][2 * e] = a;
+        x[c][2 * e + 1] = b;
+        ow[e] = static_cast<uint32_t>(from_f32(DT{}, a)) | (static_cast<uint32_t>(from_f32(DT{}, b)) << 16);
       }
-      x[c][2 * e] = a;
-      x[c][2 * e + 1] = b;
-      ow[e] = static_cast<uint32_t>(from_f32(DT{}, a)) | (static_cast<uint32_t>(from_f32(DT{}, b)) << 16);
-    }
-    const bool in = threadIdx.x + c * kNormBlock < nv;
-    if (in) {
+      const bool in = threadIdx.x + c * kNormBlock < nv;
+      if (in) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += x[c][e] * x[c][e];
-      if (hs != nullptr) hs[threadIdx.x + c * kNormBlock] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+        for (int e = 0; e < 8; ++e) acc += x[c][e] * x[c][e];
+        if (hs != nullptr) hs[threadIdx.x + c * kNormBlock] = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      }
+    }
+    acc = wave_sum_f32(acc);
+    if (lane_id() == 0) s_part[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormBlock / kWave; ++i) total += s_part[i];
+    const float r = 1.0f / sqrtf(total / static_cast<float>(H) + eps);
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+      if (threadIdx.x + c * kNormBlock >= nv) continue;
+      const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float ya = round_to<DT>(x[c][2 * e] * r);
+        const float yb = round_to<DT>(x[c][2 * e + 1] * r);
+        const float oa = to_f32(DT{}, static_cast<S>(ww[e] & 0xffffu)) * ya;
+        const float ob = to_f32(DT{}, static_cast<S>(ww[e] >> 16)) * yb;
+        ow[e] = static_cast<uint32_t>(from_f32(DT{}, oa)) | (static_cast<uint32_t>(from_f32(DT{}, ob)) << 16);
+      }
+      put(threadIdx.x + c * kNormBlock, make_uint4(ow[0], ow[1], ow[2], ow[3]));
     }
   }
-  acc = wave_sum_f32(acc);
-  if (lane_id() == 0) s_part[threadIdx.x / kWave] = acc;
-  __syncthreads();
-  float total = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kNormBlock / kWave; ++i) total += s_part[i];
-  const float r = 1.0f / sqrtf(total / static_cast<float>(H) + eps);
-#pragma unroll
-  for (int c = 0; c < kNormVec; ++c) {
-    if (threadIdx.x + c * kNormBlock >= nv) continue;
-    const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
-    uint32_t ow[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float ya = round_to<DT>(x[c][2 * e] * r);
-      const float yb = round_to<DT>(x[c][2 * e + 1] * r);
-      const float oa = to_f32(DT{}, static_cast<S>(ww[e] & 0xffffu)) * ya;
-      const float ob = to_f32(DT{}, static_cast<S>(ww[e] >> 16)) * yb;
-      ow[e] = static_cast<uint32_t>(from_f32(DT{}, oa)) | (static_cast<uint32_t>(from_f32(DT{}, ob)) << 16);
-    }
-    put(threadIdx.x + c * kNormBlock, make_uint4(ow[0], ow[1], ow[2], ow[3]));
-  }
-}
+};
 
 // h = bf16(h + delta) (when delta is given); out = bf16(w * bf16(h * r)),
 // r = rsqrt(mean(h^2) + eps) in fp32.  One block per row; each thread holds
@@ -111,9 +121,9 @@ __global__ __launch_bounds__(kNormBlock) void add_rms_norm_kernel(typename DT::s
   __shared__ float s_part[kNormBlock / kWave];
   const int64_t row = blockIdx.x;
   uint4* orow = reinterpret_cast<uint4*>(out + row * H);
-  rms_norm_row<DT>(h + row * H, delta != nullptr ? delta + row * H : nullptr, w, eps, H,
-                   delta != nullptr ? h + row * H : nullptr, s_part,
-                   [&](int i, const uint4& v) { orow[i] = v; });
+  NormRow<DT, kNormVec> nr;
+  nr.load(h + row * H, delta != nullptr ? delta + row * H : nullptr, w, H);
+  nr.finish(eps, H, delta != nullptr ? h + row * H : nullptr, s_part, [&](int i, const uint4& v) { orow[i] = v; });
 }
 
 // In place on q [Hq][D] and k [Hk][D] at the position *pos: x' = bf16(bf16(x
@@ -224,7 +234,10 @@ struct GemvArgs {
   float* q32;
 };
 
-template <typename DT, int RPW, int PRO, int EPI>
+// NV: 16-byte chunks of x per thread held in registers while the first
+// weight loads are issued (x of up to NV * 2048 elements; longer x is staged
+// after them).
+template <typename DT, int RPW, int PRO, int EPI, int NV>
 __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::storage> a) {
   static_assert(EPI == kEpiPlain || RPW % 2 == 0, "paired epilogues take rows two by two");
   extern __shared__ __align__(16) uint4 xs[];
@@ -264,8 +277,9 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
   for (int r = 0; r < RPW; ++r) rowp[r] = w4 + static_cast<int64_t>(rows[r]) * kc;
   // A step covers chunks c + u * kWave, u < U, of every row: U * RPW
   // 16-byte loads per lane (8 KB per wave) are in flight before any is
-  // used; the first step's are issued while x is prepared.  Each lane sums
-  // its chunks in increasing order.
+  // used; the first step's are issued right after x's (or the norm's
+  // inputs'), so x is ready while they arrive.  Each lane sums its chunks in
+  // increasing order.
   constexpr int U = 16 / RPW;
   int c = lane;
   uint4 wv[U][RPW];
@@ -277,13 +291,30 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
       for (int r = 0; r < RPW; ++r) wv[u][r] = rowp[r][idx < kc ? idx : 0];
     }
   };
+  NormRow<DT, NV> nr;
+  uint4 xr[NV];
+  const uint4* x4 = reinterpret_cast<const uint4*>(a.x);
+  const bool x_in_regs = kc <= NV * kGemvBlock;
+  if (PRO == kProNorm) {
+    nr.load(a.h_in, a.delta, a.norm_w, K);
+  } else if (x_in_regs) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int i = static_cast<int>(threadIdx.x) + v * kGemvBlock;
+      xr[v] = x4[i < kc ? i : 0];
+    }
+  }
   load_step(c);
   if (PRO == kProNorm) {
-    rms_norm_row<DT>(a.h_in, a.delta, a.norm_w, a.eps, K,
-                     (blockIdx.x == 0 && a.delta != nullptr) ? a.h_out : nullptr, s_part,
-                     [&](int i, const uint4& v) { xs[i] = v; });
+    nr.finish(a.eps, K, (blockIdx.x == 0 && a.delta != nullptr) ? a.h_out : nullptr, s_part,
+              [&](int i, const uint4& v) { xs[i] = v; });
+  } else if (x_in_regs) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int i = static_cast<int>(threadIdx.x) + v * kGemvBlock;
+      if (i < kc) xs[i] = xr[v];
+    }
   } else {
-    const uint4* x4 = reinterpret_cast<const uint4*>(a.x);
     for (int i = threadIdx.x; i < kc; i += kGemvBlock) xs[i] = x4[i];
   }
   __syncthreads();
@@ -350,8 +381,8 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
   }
 }
 
-template <typename DT, int PRO, int EPI>
-int launch_gemv(const GemvArgs<typename DT::storage>& a, hipStream_t st) {
+template <typename DT, int PRO, int EPI, int NV>
+void launch_gemv_nv(const GemvArgs<typename DT::storage>& a, hipStream_t st) {
   const size_t lds = static_cast<size_t>(a.K) * 2;
   const int waves = kGemvBlock / kWave;
   const bool wide = a.N >= 16384;
@@ -360,9 +391,20 @@ int launch_gemv(const GemvArgs<typename DT::storage>& a, hipStream_t st) {
   const int units = EPI == kEpiPlain ? a.N : a.N / 2;
   const dim3 grid((units + units_per_block - 1) / units_per_block);
   if (wide)
-    hipLaunchKernelGGL((gemv_kernel<DT, 4, PRO, EPI>), grid, dim3(kGemvBlock), lds, st, a);
+    hipLaunchKernelGGL((gemv_kernel<DT, 4, PRO, EPI, NV>), grid, dim3(kGemvBlock), lds, st, a);
   else
-    hipLaunchKernelGGL((gemv_kernel<DT, 2, PRO, EPI>), grid, dim3(kGemvBlock), lds, st, a);
+    hipLaunchKernelGGL((gemv_kernel<DT, 2, PRO, EPI, NV>), grid, dim3(kGemvBlock), lds, st, a);
+}
+
+// x of up to 4096 elements in two register chunks per thread, else four
+// (the norm prologue takes K <= 8192; plain x longer than 8192 is staged
+// after the first weight loads).
+template <typename DT, int PRO, int EPI>
+int launch_gemv(const GemvArgs<typename DT::storage>& a, hipStream_t st) {
+  if (a.K <= 2 * 8 * kGemvBlock)
+    launch_gemv_nv<DT, PRO, EPI, 2>(a, st);
+  else
+    launch_gemv_nv<DT, PRO, EPI, 4>(a, st);
   return tw_host::check_launch();
 }
 
