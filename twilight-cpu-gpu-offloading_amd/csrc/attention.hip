@@ -1256,13 +1256,13 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       const int kr = krow < ts[tt].cnt ? krow : 0;
       const S* kp = krow == ts[tt].dec ? kdec : kt + tb + kr * D;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kf[tt][s] = *reinterpret_cast<const uint4*>(kp + 32 * s + 8 * quarter);
+      for (int s = 0; s < 4; ++s) kf[tt][s] = load_stream(kp + 32 * s + 8 * quarter);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * rg + j;
         const int vr = r < ts[tt].cnt ? r : 0;
         const S* vp = r == ts[tt].dec ? vdec : vt + tb + vr * D;
-        vf[tt][j] = *reinterpret_cast<const uint4*>(vp + c8);
+        vf[tt][j] = load_stream(vp + c8);
       }
     }
     // ---- q.k on the matrix cores; scores in log2 units ----

@@ -181,16 +181,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const typename DT::storag
 // v_dot2_f32_{bf16,f16} in fp32; a wave reduction ends each row.
 constexpr int kGemvBlock = 256;
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// A 16-byte load with the streaming (nontemporal) hint: data read once, such
-// as a projection weight per decode token, is not kept in the caches, which
-// lets the stream run closer to the HBM rate.
-__device__ __forceinline__ uint4 load_stream(const uint4* p) {
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
 template <typename DT>
 struct Dot2;
 template <>

@@ -219,6 +219,15 @@ __device__ __forceinline__ float2 fetch_f32x2(const float* p) {
   return make_float2(__uint_as_float(static_cast<uint32_t>(v)), __uint_as_float(static_cast<uint32_t>(v >> 32)));
 }
 
+// A 16-byte load with the streaming (nontemporal) hint, for data read once
+// per step (projection weights, K/V rows): it is not kept in the caches,
+// which lets a stream run closer to the HBM rate.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Returns true in every thread of the block that arrives last.  All of the
 // block's published data must have been written with publish_* before the
 // call.
