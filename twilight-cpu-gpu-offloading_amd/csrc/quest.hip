@@ -143,7 +143,8 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
       const int rem = i - which * np * quads;
       const int page = rem / quads;
       const int qd = rem - page * quads;
-      const uint4 v = reinterpret_cast<const uint4*>(which ? mx : mn)[static_cast<int64_t>(page) * quads + qd];
+      const uint4 v =
+          load_stream(reinterpret_cast<const uint4*>(which ? mx : mn) + static_cast<int64_t>(page) * quads + qd);
       *reinterpret_cast<uint4*>(lds + (which * kTilePages + page) * pitch + qd * 16) = v;
     }
   } else {
