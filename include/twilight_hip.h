@@ -480,12 +480,6 @@ int tw_rms_norm_gemv_rope(const void* h_in, const void* delta, const void* norm_
                           int dtype, void* stream);
 int tw_rms_norm_gemv_silu(const void* h_in, const void* delta, const void* norm_weight, float eps, void* h_out,
                           const void* W, const void* bias, void* y, int N, int K, int dtype, void* stream);
-/* Reads `bytes` at p (16-byte aligned) and discards the data, with `blocks`
- * blocks of 512 threads: run on a second stream while the decode step's
- * latency-bound sparse attention leaves the HBM idle, it brings the next
- * projection weights into the Infinity Cache.  nontemporal != 0 reads with
- * the streaming hint.  No counterpart in the reference. */
-int tw_prefetch(const void* p, size_t bytes, int blocks, int nontemporal, void* stream);
 
 #ifdef __cplusplus
 }

@@ -429,54 +429,8 @@ int check_norm_gemv(const void* h_in, const void* delta, const void* norm_w, con
   return TW_OK;
 }
 
-// Reads bytes [0, n16 * 16) of p and discards them, to bring a weight into
-// the device's last-level (Infinity) cache while the HBM is otherwise idle.
-// Consecutive threads read consecutive 16-byte chunks, kPrefetchUnroll
-// chunks per thread in flight; the XOR of the data reaches memory only when
-// it equals a value no caller passes as `key`, which keeps the loads alive.
-constexpr int kPrefetchBlock = 512;
-constexpr int kPrefetchUnroll = 16;
-
-template <bool NT>
-__global__ __launch_bounds__(kPrefetchBlock) void prefetch_kernel(const u32x4* __restrict__ p, int64_t n16,
-                                                                  uint32_t key, uint32_t* __restrict__ sink) {
-  uint32_t acc = 0u;
-  const int64_t step = static_cast<int64_t>(gridDim.x) * kPrefetchBlock * kPrefetchUnroll;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kPrefetchBlock * kPrefetchUnroll + threadIdx.x;
-       base < n16; base += step) {
-    u32x4 v[kPrefetchUnroll];
-#pragma unroll
-    for (int u = 0; u < kPrefetchUnroll; ++u) {
-      const int64_t i = base + static_cast<int64_t>(u) * kPrefetchBlock;
-      const u32x4* q = p + (i < n16 ? i : 0);
-      if constexpr (NT)
-        v[u] = __builtin_nontemporal_load(q);
-      else
-        v[u] = *q;
-    }
-#pragma unroll
-    for (int u = 0; u < kPrefetchUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-  }
-  if (acc == key && sink != nullptr) *sink = acc;
-}
-
 }  // namespace
 }  // namespace tw
-
-extern "C" int tw_prefetch(const void* p, size_t bytes, int blocks, int nontemporal, void* stream) {
-  if (p == nullptr || blocks <= 0 || (reinterpret_cast<uintptr_t>(p) % 16) != 0) return TW_EINVAL;
-  const int64_t n16 = static_cast<int64_t>(bytes / 16);
-  if (n16 == 0) return TW_OK;
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  // key 0 with a null sink: the store never happens
-  if (nontemporal)
-    hipLaunchKernelGGL(tw::prefetch_kernel<true>, dim3(blocks), dim3(tw::kPrefetchBlock), 0, st,
-                       static_cast<const tw::u32x4*>(p), n16, 0u, nullptr);
-  else
-    hipLaunchKernelGGL(tw::prefetch_kernel<false>, dim3(blocks), dim3(tw::kPrefetchBlock), 0, st,
-                       static_cast<const tw::u32x4*>(p), n16, 0u, nullptr);
-  return tw_host::check_launch();
-}
 
 extern "C" int tw_gemv(const void* W, const void* x, const void* bias, void* y, int N, int K, int dtype,
                        void* stream) {

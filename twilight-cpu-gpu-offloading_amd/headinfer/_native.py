@@ -54,7 +54,6 @@ _HIP_SIGNATURES = {
     "tw_rope_qk": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "tw_silu_mul": (i32, [vp, vp, i32, i32, vp]),
     "tw_gemv": (i32, [vp, vp, vp, vp, i32, i32, i32, vp]),
-    "tw_prefetch": (i32, [vp, szt, i32, i32, vp]),
     "tw_rms_norm_gemv": (i32, [vp, vp, vp, f32, vp, vp, vp, vp, i32, i32, i32, vp]),
     "tw_rms_norm_gemv_rope": (i32, [vp, vp, vp, f32, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, vp, vp, vp, i32,
                                     vp]),

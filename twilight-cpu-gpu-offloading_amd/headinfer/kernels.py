@@ -1329,15 +1329,3 @@ def rms_norm_gemv(h: torch.Tensor, delta: Optional[torch.Tensor], norm_weight: t
             raise ValueError(f"unknown epilogue {epilogue!r}")
     return out
 
-
-def prefetch(t: torch.Tensor, *, blocks: int = 64, nontemporal: bool = False, nbytes: Optional[int] = None) -> None:
-    """Read (and discard) the first nbytes (default all) of the contiguous
-    tensor t on the current stream: brings a weight into the Infinity Cache
-    ahead of its GEMV."""
-    if not t.is_contiguous():
-        raise ValueError("prefetch needs a contiguous tensor")
-    total = t.numel() * t.element_size()
-    n = total if nbytes is None else max(0, min(int(nbytes), total))
-    dev = _require_device(t, what="prefetch")
-    with torch.cuda.device(dev):
-        check(hip().tw_prefetch(t.data_ptr(), n, int(blocks), int(bool(nontemporal)), stream_handle(dev)), "prefetch")
