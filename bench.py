@@ -58,6 +58,8 @@ def parse_args(argv=None):
                          "multireq: 8 requests of 16K-128K context, Qwen2.5-7B-like GQA, KV heads half in HBM "
                          "and half in host memory, 256 decode steps with append and metadata update")
     ap.add_argument("--decode-tokens", type=int, default=32, help="decode tokens per TPOT run (D1..Dn)")
+    ap.add_argument("--tpot-only", default=None,
+                    help="tpot32k: run this variant only (e.g. sparse_graph, for a profile of its kernels)")
     ap.add_argument("--kv-residency", choices=("hbm", "host"), default="hbm",
                     help="tpot32k: KV slab in HBM or in pinned host memory (read zero-copy)")
     ap.add_argument("--context", type=int, default=None, help="context length (workload default if omitted)")
@@ -859,6 +861,10 @@ def run_tpot(args, dev) -> int:
     if residency == "host":  # the HBM resident page cache (previous_token_resident_cache) serves host slabs
         variants[1:1] = [("sparse_graph_resident", args.budget_pages, True, True)]
         variants[4:4] = [("sparse_hf_eager_resident", args.budget_pages, False, True)]
+    if args.tpot_only is not None:
+        variants = [v for v in variants if v[0] == args.tpot_only]
+        if not variants:
+            raise SystemExit(f"--tpot-only: no variant named {args.tpot_only!r}")
     for label, pages, graph, resident in variants:
         print(f"[bench] tpot {label}: prefill + {n_dec} decode tokens", file=sys.stderr, flush=True)
         cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + n_dec + 8,
@@ -872,6 +878,8 @@ def run_tpot(args, dev) -> int:
         del cache
         torch.cuda.empty_cache()
     head = "sparse_graph_resident" if residency == "host" else "sparse_graph"
+    if head not in runs:
+        head = next(iter(runs))
     sp = runs[head]
     result = {
         "metric": METRIC, "value": sp["tpot_p50_ms"], "unit": "ms/token (p50 TPOT)", "n_gpus": 1,
@@ -885,8 +893,9 @@ def run_tpot(args, dev) -> int:
                    "page_size": 16, "budget_pages": args.budget_pages, "sink": 64, "recent": 256},
         "tpot_variant": head,
         "tpot": runs,
-        "sparse_vs_dense_speedup": round(runs["dense_graph"]["tpot_p50_ms"] / sp["tpot_p50_ms"], 3),
     }
+    if "dense_graph" in runs:
+        result["sparse_vs_dense_speedup"] = round(runs["dense_graph"]["tpot_p50_ms"] / sp["tpot_p50_ms"], 3)
     print(json.dumps(result), flush=True)
     return 0
 
