@@ -111,6 +111,8 @@ struct AttnArgs {
   void* meta_max;
   int64_t meta_stride;
   int meta_pages;
+  // page-tile kernel: K and V are device memory (read with the streaming hint)
+  int kv_stream;
 };
 
 // 8 consecutive channels of one row.
@@ -1137,7 +1139,10 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
   return s;
 }
 
-template <typename DT, int RMAX, int NW, int TW, bool RES>
+// NT: the slab is device memory, so its K/V rows are read with the
+// streaming hint (pinned host memory read over the host link keeps plain
+// loads, which measured faster there).
+template <typename DT, int RMAX, int NW, int TW, bool RES, bool NT>
 __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   using S = typename DT::storage;
   using H = Half8<DT>;
@@ -1256,13 +1261,15 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       const int kr = krow < ts[tt].cnt ? krow : 0;
       const S* kp = krow == ts[tt].dec ? kdec : kt + tb + kr * D;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kf[tt][s] = load_stream(kp + 32 * s + 8 * quarter);
+      for (int s = 0; s < 4; ++s)
+        kf[tt][s] = NT ? load_stream(kp + 32 * s + 8 * quarter)
+                       : *reinterpret_cast<const uint4*>(kp + 32 * s + 8 * quarter);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * rg + j;
         const int vr = r < ts[tt].cnt ? r : 0;
         const S* vp = r == ts[tt].dec ? vdec : vt + tb + vr * D;
-        vf[tt][j] = load_stream(vp + c8);
+        vf[tt][j] = NT ? load_stream(vp + c8) : *reinterpret_cast<const uint4*>(vp + c8);
       }
     }
     // ---- q.k on the matrix cores; scores in log2 units ----
@@ -1628,15 +1635,21 @@ int launch_tiles(const AttnArgs& a, hipStream_t stream) {
   if (phase & 1) {
     const dim3 grid(a.G * a.max_chunks);
     const dim3 block(kTileNW * kWave);
+    // the resident page cache serves slabs in host memory: plain loads
     if (a.res_map != nullptr) {
       if (a.R <= 4)
-        hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, true, false>), grid, block, 0, stream, a);
       else
-        hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, true, false>), grid, block, 0, stream, a);
+    } else if (a.kv_stream) {
+      if (a.R <= 4)
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, false, true>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, false, true>), grid, block, 0, stream, a);
     } else if (a.R <= 4) {
-      hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, false>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, false, false>), grid, block, 0, stream, a);
     } else {
-      hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, false>), grid, block, 0, stream, a);
+      hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, false, false>), grid, block, 0, stream, a);
     }
     const int rc = tw_host::check_launch();
     if (rc != TW_OK) return rc;
@@ -1957,6 +1970,7 @@ extern "C" int tw_decode_attention_pages_phase(const void* q, const void* k_base
     cap = cap < room ? cap : room;
     cap = cap < plan_stride ? cap : plan_stride;
     a.t_nu_cap = static_cast<int>(cap < 0 ? 0 : cap);
+    a.kv_stream = tw_host::device_memory(k_base) && tw_host::device_memory(v_base);
     return dtype == TW_DTYPE_F16 ? tw::launch_tiles<tw::F16>(a, static_cast<hipStream_t>(stream))
                                  : tw::launch_tiles<tw::BF16>(a, static_cast<hipStream_t>(stream));
   }
@@ -2072,6 +2086,7 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
     cap = cap < plan_stride ? cap : plan_stride;
     a.t_nu_cap = static_cast<int>(cap < 0 ? 0 : cap);
   }
+  a.kv_stream = tw_host::device_memory(k_base) && tw_host::device_memory(v_base);
   return dtype == TW_DTYPE_F16 ? launch_tiles<F16>(a, static_cast<hipStream_t>(stream))
                                : launch_tiles<BF16>(a, static_cast<hipStream_t>(stream));
 }

@@ -20,6 +20,15 @@ int check_launch() {
   return TW_OK;
 }
 
+bool device_memory(const void* p) {
+  hipPointerAttribute_t attr;
+  if (p == nullptr || hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();  // an unknown pointer is not an error of the launch that follows
+    return false;
+  }
+  return attr.type == hipMemoryTypeDevice;
+}
+
 }  // namespace tw_host
 
 extern "C" const char* tw_status_string(int status) {

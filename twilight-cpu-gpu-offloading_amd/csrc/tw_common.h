@@ -251,4 +251,7 @@ __device__ __forceinline__ bool arrive_last(unsigned int* counter, unsigned int 
 namespace tw_host {
 int record_hip_error(hipError_t err);
 int check_launch();
+// True when p is device memory (HBM); false for pinned host memory mapped
+// into the device's address space, or a pointer the runtime does not know.
+bool device_memory(const void* p);
 }  // namespace tw_host
