@@ -841,6 +841,7 @@ def run_tpot(args, dev) -> int:
 
     from headinfer import mp
     from headinfer.quest_offload_cache import QuestTopKOffloadedCache
+    from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache
     from transformers import LlamaForCausalLM
 
     ctx = args.context or 32768
@@ -857,7 +858,8 @@ def run_tpot(args, dev) -> int:
     ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(5))
     runs = {}
     variants = [("sparse_graph", args.budget_pages, True, False), ("dense_graph", 1 << 20, True, False),
-                ("sparse_hf_eager", args.budget_pages, False, False), ("dense_hf_eager", 1 << 20, False, False)]
+                ("sparse_hf_eager", args.budget_pages, False, False), ("dense_hf_eager", 1 << 20, False, False),
+                ("twilight_hf_eager", None, False, False)]
     if residency == "host":  # the HBM resident page cache (previous_token_resident_cache) serves host slabs
         variants[1:1] = [("sparse_graph_resident", args.budget_pages, True, True)]
         variants[4:4] = [("sparse_hf_eager_resident", args.budget_pages, False, True)]
@@ -867,10 +869,16 @@ def run_tpot(args, dev) -> int:
             raise SystemExit(f"--tpot-only: no variant named {args.tpot_only!r}")
     for label, pages, graph, resident in variants:
         print(f"[bench] tpot {label}: prefill + {n_dec} decode tokens", file=sys.stderr, flush=True)
-        cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + n_dec + 8,
-                                                         kv_residency=residency, budget_pages=pages,
-                                                         update_metadata_on_decode=graph,
-                                                         previous_token_resident_cache=resident)
+        if label.startswith("twilight"):
+            # the reference runner's path: Quest B0 = 4096 tokens, INT4 QK, top-p 0.95
+            cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(
+                model, max_cache_len=ctx + n_dec + 8, kv_residency=residency, candidate_token_budget=4096,
+                top_p=0.95, budget_mode="dynamic")
+        else:
+            cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + n_dec + 8,
+                                                             kv_residency=residency, budget_pages=pages,
+                                                             update_metadata_on_decode=graph,
+                                                             previous_token_resident_cache=resident)
         runs[label] = tpot_run(model, ids, dev, cache, n_dec, graph=graph)
         if resident:
             st = cache.resident_stats()

@@ -247,6 +247,21 @@ int tw_twilight_select(const float* logits, int G, int R, int N, const int32_t* 
                        uint32_t* head_bits, int32_t* rows, int32_t* row_counts, int64_t rows_stride, int sink,
                        int recent, int block_size, int length, int append_position, void* workspace,
                        size_t workspace_bytes, void* stream);
+/* tw_twilight_select (dynamic budgets, no decode row in the union) over
+ * groups of different lengths: group g has lengths[g] tokens (int32,
+ * device; <= max_length, rows_stride > max_length), ragged_pages =
+ * min(whole pages between sink and recent, page_capacity) candidate pages,
+ * and min(that, b0_pages) B0 pages per head in sel_pages (the slots beyond
+ * are -1, as tw_quest_select_ragged leaves them), so min(..) * block_size
+ * valid candidates in its logits rows (N apart).  A group with no candidate
+ * page keeps its sink and recent windows only (desired 0).  Batches the
+ * reference's per-request top-p and GQA union (twilight_offload_cache.py
+ * :1265-1311,1517-1614) for the graph-captured decode step. */
+int tw_twilight_select_ragged(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,
+                              float top_p, int32_t* desired, int32_t* allocated, uint32_t* head_bits,
+                              int32_t* rows, int32_t* row_counts, int64_t rows_stride, int sink, int recent,
+                              int block_size, const int32_t* lengths, int max_length, int page_capacity,
+                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Sparse GQA decode attention, split-K over selected rows, one query
@@ -360,16 +375,18 @@ int tw_decode_attention(const void* q, const void* k_base, const void* v_base, i
                         void* workspace, size_t workspace_bytes, void* stream);
 /* tw_decode_attention over a row list with the decode token's append fused:
  * the first block of every group also writes cur_k/cur_v[g] to row
- * append_position of entry g (0 <= append_position < entry_stride_rows;
- * the row list must not name it).  Replaces the Twilight decode step's GQA
- * decode attention over the union rows (mp.py:239-279) followed by the
- * batched new-KV append (twilight_offload_cache.py:551-794). */
+ * append_position of entry g (0 <= append_position < entry_stride_rows), or,
+ * when append_rows (int32 [G], device) is given, to row append_rows[g]
+ * (rows outside the entry are skipped); the row list must not name it.
+ * Replaces the Twilight decode step's GQA decode attention over the union
+ * rows (mp.py:239-279) followed by the batched new-KV append
+ * (twilight_offload_cache.py:551-794). */
 int tw_decode_attention_rows_append(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
                                     int D, const int32_t* rows, const uint8_t* row_masks, const int32_t* row_counts,
                                     int64_t rows_stride, int64_t entry_stride_rows, int max_rows,
                                     const void* cur_k, const void* cur_v, int64_t append_position,
-                                    float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
-                                    void* stream);
+                                    const int32_t* append_rows, float softmax_scale, void* out, void* workspace,
+                                    size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Head-wise K/V row gather into the attention layout.

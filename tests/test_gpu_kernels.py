@@ -347,6 +347,17 @@ def test_decode_attention_rows_append(K, dev, dtype, G, R, D, L, n_rows):
     assert torch.equal(fused, plain)
     k0[:, L], v0[:, L] = ck, cv
     assert torch.equal(kc, k0) and torch.equal(vc, v0)
+    # per-group rows from the device (one beyond the entry: skipped)
+    at = torch.tensor([L + 1 + (g % 2) for g in range(G)], dtype=torch.int32)
+    at[-1] = Lmax + 5
+    ragged = K.decode_attention_rows(q, kc, vc, rows, counts, n_rows, cur_k=ck, cur_v=cv,
+                                     append_position=at.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(ragged, plain)
+    for g in range(G):
+        if int(at[g]) < Lmax:
+            k0[g, int(at[g])], v0[g, int(at[g])] = ck[g], cv[g]
+    assert torch.equal(kc, k0) and torch.equal(vc, v0)
     with pytest.raises(ValueError):
         K.decode_attention_rows(q, kc, vc, rows, counts, n_rows, append_position=L)
     with pytest.raises(ValueError):

@@ -370,3 +370,74 @@ def test_attention_fused_page_metadata(K, dev, resident):
     with pytest.raises(ValueError):
         K.decode_attention_pages_ragged(q.to(dev), kd, vd, pp, pc, lengths, page_min=pmin, page_max=pmax,
                                         **dict(kw, append=False))
+
+
+def test_twilight_select_ragged_matches_per_group(K, dev):
+    """Ragged Twilight stage 2 (INT4 QK over the ragged stage-1 plan, then
+    top-p and the GQA union with per-group lengths) == the per-group calls,
+    bit for bit: desired counts, head bitmaps, union rows.  One group has no
+    candidate page, one fewer candidate pages than B0."""
+    _say("[ragged twilight select]")
+    dtype, R, b0, top_p = "bf16", 4, 64, 0.9
+    lengths0 = [200, 1000, 1500, 5000, 9000]
+    G = len(lengths0)
+    Lmax = max(lengths0) + 16
+    kd = randn((G, Lmax, D), dtype, seed=141).to(dev)
+    q = randn((G, R, D), "f32", seed=142).to(dev)
+    P_cap = (Lmax - SINK) // BS
+    pmin = torch.zeros((G, P_cap, D), dtype=kd.dtype, device=dev)
+    pmax = torch.zeros_like(pmin)
+    packed = torch.zeros((G, Lmax, D // 2), dtype=torch.uint8, device=dev)
+    scale = torch.zeros((G, Lmax), dtype=kd.dtype, device=dev)
+    minimum = torch.zeros_like(scale)
+    for g, L in enumerate(lengths0):
+        K.build_page_metadata(kd[g, :L], sink=SINK, block_size=BS, page_min=pmin[g], page_max=pmax[g],
+                              packed=packed[g], scale=scale[g], minimum=minimum[g])
+    lengths = torch.tensor(lengths0, dtype=torch.int32, device=dev)
+    width = min(P_cap, R * b0)
+    sel = torch.empty((G, R, b0), dtype=torch.int32, device=dev)
+    pp = torch.empty((G, width), dtype=torch.int32, device=dev)
+    pm = torch.empty((G, width), dtype=torch.uint8, device=dev)
+    pc = torch.empty((G,), dtype=torch.int32, device=dev)
+    K.quest_select_ragged(q, pmin, pmax, lengths, b0, sink=SINK, recent=RECENT, block_size=BS, sel_pages=sel,
+                          plan_pages=pp, plan_masks=pm, plan_counts=pc)
+    logits = K.twilight_qk(q, packed, scale, minimum, pp, pm, pc, b0, sink=SINK, block_size=BS)
+    N = b0 * BS
+    rows = torch.full((G, Lmax + 1), -7, dtype=torch.int32, device=dev)
+    counts = torch.empty((G,), dtype=torch.int32, device=dev)
+    desired = torch.empty((G, R), dtype=torch.int32, device=dev)
+    hb = torch.empty((G, R, (N + 31) // 32), dtype=torch.int32, device=dev)
+    K.twilight_select_ragged(logits, sel, lengths, top_p=top_p, rows=rows, row_counts=counts,
+                             max_length=max(lengths0), page_capacity=P_cap, sink=SINK, recent=RECENT,
+                             block_size=BS, desired=desired, head_bits=hb)
+    torch.cuda.synchronize()
+    for g, L in enumerate(lengths0):
+        P = min(_cand(L), P_cap)
+        kg = min(b0, P)
+        n = int(counts[g])
+        if kg == 0:
+            sink_end, recent_start, _ = oracle.selection_window(L, SINK, RECENT)
+            want = torch.cat([torch.arange(sink_end), torch.arange(recent_start, L)]).to(torch.int32)
+            assert n == want.numel() and torch.equal(rows[g, :n].cpu(), want), g
+            assert bool((desired[g] == 0).all()) and bool((hb[g] == 0).all()), g
+            continue
+        w1 = min(P, R * kg)
+        s1 = torch.empty((1, R, kg), dtype=torch.int32, device=dev)
+        p1 = torch.empty((1, w1), dtype=torch.int32, device=dev)
+        m1 = torch.empty((1, w1), dtype=torch.uint8, device=dev)
+        c1 = torch.empty((1,), dtype=torch.int32, device=dev)
+        K.quest_select(q[g:g + 1].contiguous(), pmin[g:g + 1, :P], pmax[g:g + 1, :P], kg, sel_pages=s1,
+                       plan_pages=p1, plan_masks=m1, plan_counts=c1)
+        lg1 = K.twilight_qk(q[g:g + 1].contiguous(), packed[g:g + 1], scale[g:g + 1], minimum[g:g + 1], p1, m1, c1,
+                            kg, sink=SINK, block_size=BS)
+        r1 = torch.empty((1, L + 1), dtype=torch.int32, device=dev)
+        n1 = torch.empty((1,), dtype=torch.int32, device=dev)
+        d1 = torch.empty((1, R), dtype=torch.int32, device=dev)
+        words1 = (kg * BS + 31) // 32
+        h1 = torch.empty((1, R, words1), dtype=torch.int32, device=dev)
+        K.twilight_select(lg1, s1, top_p=top_p, budget_mode="dynamic", rows=r1, row_counts=n1, desired=d1,
+                          head_bits=h1, sink=SINK, recent=RECENT, block_size=BS, length=L)
+        torch.cuda.synchronize()
+        assert torch.equal(desired[g].cpu(), d1[0].cpu()), g
+        assert torch.equal(hb[g, :, :words1].cpu(), h1[0].cpu()) and bool((hb[g, :, words1:] == 0).all()), g
+        assert n == int(n1[0]) and torch.equal(rows[g, :n].cpu(), r1[0, :n].cpu()), g

@@ -241,6 +241,15 @@ __device__ __forceinline__ GroupRows group_rows(const AttnArgs& a, int g, int D)
 // Page-tile mode (decode_attn_tiles): chunks count 16-row tiles.
 constexpr int kModeTiles = 3;
 
+// The row the decode token of group g is appended at: append_position, or in
+// rows mode with per-group lengths, lengths[g] (out of range: none).
+template <int MODE>
+__device__ __forceinline__ int decode_row_position(const AttnArgs& a, int g) {
+  if (MODE != kModeRows || a.lengths == nullptr) return a.append_position;
+  const int p = a.lengths[g];
+  return (p >= 0 && p < a.entry_stride) ? p : -1;
+}
+
 // The min/max of the 16-row page the appended row `position` of group g
 // completes, by wave 0 of the block: lane l owns channels 2l and 2l + 1 of
 // all 16 rows (one 4-byte load per row, all in flight together), compared as
@@ -564,7 +573,8 @@ __global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(
     return;
   }
   if (chunk >= n_chunks) return;
-  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
+  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0)
+    append_decode_token<S>(a, g, D, decode_row_position<MODE>(a, g));
 
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
@@ -880,7 +890,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_attn_mfma(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
+  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0)
+    append_decode_token<S>(a, g, D, decode_row_position<MODE>(a, g));
 
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
@@ -1474,7 +1485,8 @@ __global__ __launch_bounds__(kBlock) void decode_attn_generic(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0) append_decode_token<S>(a, g, D, a.append_position);
+  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0)
+    append_decode_token<S>(a, g, D, decode_row_position<MODE>(a, g));
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
   const S* qg = static_cast<const S*>(a.q) + static_cast<int64_t>(g) * R * D;
@@ -1787,8 +1799,8 @@ namespace {
 int rows_launch(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R, int D,
                 const int32_t* rows, const uint8_t* row_masks, const int32_t* row_counts, int64_t rows_stride,
                 int64_t entry_stride_rows, const int32_t* cu_seqlens_k, int Hk, int window_left, int max_rows,
-                const void* cur_k, const void* cur_v, int64_t append_position, float softmax_scale, void* out,
-                void* workspace, size_t workspace_bytes, void* stream) {
+                const void* cur_k, const void* cur_v, int64_t append_position, const int32_t* append_rows,
+                float softmax_scale, void* out, void* workspace, size_t workspace_bytes, void* stream) {
   if (q == nullptr || out == nullptr || G <= 0 || R <= 0 || R > 8 || D <= 0 || D > 512 || (D % 2) != 0 ||
       max_rows < 0)
     return TW_EINVAL;
@@ -1842,6 +1854,7 @@ int rows_launch(const void* q, const void* k_base, const void* v_base, int dtype
     a.k_append = const_cast<void*>(k_base);
     a.v_append = const_cast<void*>(v_base);
     a.append_position = static_cast<int>(append_position);
+    a.lengths = append_rows;  // rows mode: per-group append rows
   }
   tw::plan_chunks(dtype, G, R, D, max_rows + (cur_k != nullptr ? 1 : 0), &a.iters, &a.max_chunks);
   return tw::launch_dtype(dtype, a, static_cast<hipStream_t>(stream));
@@ -1855,22 +1868,24 @@ extern "C" int tw_decode_attention(const void* q, const void* k_base, const void
                                    float softmax_scale, void* out, void* workspace, size_t workspace_bytes,
                                    void* stream) {
   return rows_launch(q, k_base, v_base, dtype, G, R, D, rows, row_masks, row_counts, rows_stride, entry_stride_rows,
-                     cu_seqlens_k, Hk, window_left, max_rows, cur_k, cur_v, -1, softmax_scale, out, workspace,
-                     workspace_bytes, stream);
+                     cu_seqlens_k, Hk, window_left, max_rows, cur_k, cur_v, -1, nullptr, softmax_scale, out,
+                     workspace, workspace_bytes, stream);
 }
 
 extern "C" int tw_decode_attention_rows_append(const void* q, const void* k_base, const void* v_base, int dtype,
                                                int G, int R, int D, const int32_t* rows, const uint8_t* row_masks,
                                                const int32_t* row_counts, int64_t rows_stride,
                                                int64_t entry_stride_rows, int max_rows, const void* cur_k,
-                                               const void* cur_v, int64_t append_position, float softmax_scale,
-                                               void* out, void* workspace, size_t workspace_bytes, void* stream) {
-  if (rows == nullptr || cur_k == nullptr || cur_v == nullptr || append_position < 0 ||
-      append_position >= entry_stride_rows || append_position > INT32_MAX)
+                                               const void* cur_v, int64_t append_position,
+                                               const int32_t* append_rows, float softmax_scale, void* out,
+                                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (rows == nullptr || cur_k == nullptr || cur_v == nullptr) return TW_EINVAL;
+  if (append_rows == nullptr &&
+      (append_position < 0 || append_position >= entry_stride_rows || append_position > INT32_MAX))
     return TW_EINVAL;
   return rows_launch(q, k_base, v_base, dtype, G, R, D, rows, row_masks, row_counts, rows_stride, entry_stride_rows,
-                     nullptr, 0, -1, max_rows, cur_k, cur_v, append_position, softmax_scale, out, workspace,
-                     workspace_bytes, stream);
+                     nullptr, 0, -1, max_rows, cur_k, cur_v, append_rows != nullptr ? 0 : append_position,
+                     append_rows, softmax_scale, out, workspace, workspace_bytes, stream);
 }
 
 extern "C" int tw_decode_attention_pages(const void* q, const void* k_base, const void* v_base, int dtype, int G,

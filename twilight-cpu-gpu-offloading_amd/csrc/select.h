@@ -229,5 +229,17 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
   }
 }
 
+// Candidate pages of a group with `length` tokens: the whole pages between
+// the sink and the recent window (quest_offload_cache.py:326-346), at most
+// P_max.
+__device__ __forceinline__ int ragged_pages(int length, int sink, int recent, int bs, int P_max) {
+  length = length < 0 ? 0 : length;
+  const int sink_end = sink < length ? sink : length;
+  const int hist_recent = recent - 1 > 0 ? recent - 1 : 0;
+  const int recent_start = (length - hist_recent) > sink_end ? (length - hist_recent) : sink_end;
+  const int cand = (recent_start - sink_end) / bs;
+  return cand < P_max ? cand : P_max;
+}
+
 }  // namespace sel
 }  // namespace tw

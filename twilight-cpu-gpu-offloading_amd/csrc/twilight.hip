@@ -299,7 +299,27 @@ struct SelectArgs {
   int64_t rows_stride;
   int sink, recent, bs, length, append_position;
   unsigned int* counters;     // [G]
+  // Ragged groups (nullable, dynamic budgets): group g has lengths[g] tokens
+  // (< rows_stride; `length` then bounds them all), so ragged_pages(lengths[g],
+  // .., p_max) candidate pages and at most that many (<= b0) B0 pages per head.
+  const int32_t* lengths;
+  int p_max;
 };
+
+// Tokens of group g (ragged: its own length, clamped to the launch bound).
+__device__ __forceinline__ int group_length(const SelectArgs& s, int g) {
+  if (s.lengths == nullptr) return s.length;
+  const int L = s.lengths[g];
+  return L < 0 ? 0 : (L > s.length ? s.length : L);
+}
+// Valid candidates of group g's rows: B0 pages x bs (ragged: fewer when the
+// group has fewer candidate pages).
+__device__ __forceinline__ int group_candidates(const SelectArgs& s, int g) {
+  if (s.lengths == nullptr) return s.N;
+  const int P = ragged_pages(group_length(s, g), s.sink, s.recent, s.bs, s.p_max);
+  const int k = P < s.b0 ? P : s.b0;
+  return k * s.bs;
+}
 
 struct TopShared {
   SelShared sel;
@@ -615,7 +635,7 @@ __host__ __device__ __forceinline__ int stage_elems(int N, int length) {
 // and recent windows, compacted ascending into the group's row list.
 __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, int32_t* stage, int* scan) {
   const int tid = threadIdx.x;
-  const int length = s.length;
+  const int length = group_length(s, g);
   const int sink_end = s.sink < length ? s.sink : length;
   const int hist_recent = s.recent - 1 > 0 ? s.recent - 1 : 0;
   const int recent_start = (length - hist_recent) > sink_end ? (length - hist_recent) : sink_end;
@@ -796,16 +816,27 @@ __global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
   float* stage = reinterpret_cast<float*>(union_bits + stage_offset_words(s.length));
   const int row = blockIdx.x;
   const int g = row / s.R;
-  const int N = s.N;
+  const int N = group_candidates(s, g);  // valid candidates; logits rows are s.N apart
   // the first pass's histograms, cleared before load_logits' barrier
   for (int b = threadIdx.x; b < kLinBins + 64; b += kBlock) {
     sh.sel.hist[b] = 0u;
     sh.bin_mass[b] = 0ull;
   }
+  if (N == 0) {
+    // a ragged group with no candidate page: sink and recent windows only
+    if (threadIdx.x == 0) {
+      s.desired[row] = 0;
+      if (s.allocated != nullptr) s.allocated[row] = 0;
+    }
+    publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, 0u, sh);
+    if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
+    build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan);
+    return;
+  }
   uint32_t key[KPT];
   float lmax;
   uint32_t kmin, kmax;
-  load_logits<KPT>(s.logits + static_cast<int64_t>(row) * N, N, stage, key, lmax, kmin, kmax, sh);
+  load_logits<KPT>(s.logits + static_cast<int64_t>(row) * s.N, N, stage, key, lmax, kmin, kmax, sh);
   uint64_t mass[KPT];
   uint64_t local = 0;
   const int i0 = KPT * static_cast<int>(threadIdx.x);
@@ -999,11 +1030,12 @@ extern "C" size_t tw_twilight_select_workspace_size(int G, int R, int N) {
   return tw::counter_bytes(G) + static_cast<size_t>(G) * R * words * 4 + static_cast<size_t>(G) * R * 4;
 }
 
-extern "C" int tw_twilight_select(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,
-                                  float top_p, int budget_mode, int target_total, int32_t* desired,
-                                  int32_t* allocated, uint32_t* head_bits, int32_t* rows, int32_t* row_counts,
-                                  int64_t rows_stride, int sink, int recent, int block_size, int length,
-                                  int append_position, void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+int select_launch(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages, float top_p,
+                  int budget_mode, int target_total, int32_t* desired, int32_t* allocated, uint32_t* head_bits,
+                  int32_t* rows, int32_t* row_counts, int64_t rows_stride, int sink, int recent, int block_size,
+                  int length, const int32_t* lengths, int p_max, int append_position, void* workspace,
+                  size_t workspace_bytes, void* stream) {
   if (logits == nullptr || sel_pages == nullptr || rows == nullptr || row_counts == nullptr) return TW_EINVAL;
   if (G <= 0 || R <= 0 || R > 8 || N <= 0 || b0_pages <= 0 || N != b0_pages * block_size) return TW_EINVAL;
   if (N > tw::sel::kMaxSelPages) return TW_EUNSUPPORTED;
@@ -1040,5 +1072,30 @@ extern "C" int tw_twilight_select(const float* logits, int G, int R, int N, cons
   s.bs = block_size;
   s.length = length;
   s.append_position = append_position;
+  s.lengths = lengths;
+  s.p_max = p_max;
   return tw::launch_select(s, static_cast<hipStream_t>(stream));
+}
+}  // namespace
+
+extern "C" int tw_twilight_select(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,
+                                  float top_p, int budget_mode, int target_total, int32_t* desired,
+                                  int32_t* allocated, uint32_t* head_bits, int32_t* rows, int32_t* row_counts,
+                                  int64_t rows_stride, int sink, int recent, int block_size, int length,
+                                  int append_position, void* workspace, size_t workspace_bytes, void* stream) {
+  return select_launch(logits, G, R, N, sel_pages, b0_pages, top_p, budget_mode, target_total, desired, allocated,
+                       head_bits, rows, row_counts, rows_stride, sink, recent, block_size, length, nullptr, 0,
+                       append_position, workspace, workspace_bytes, stream);
+}
+
+extern "C" int tw_twilight_select_ragged(const float* logits, int G, int R, int N, const int32_t* sel_pages,
+                                         int b0_pages, float top_p, int32_t* desired, int32_t* allocated,
+                                         uint32_t* head_bits, int32_t* rows, int32_t* row_counts,
+                                         int64_t rows_stride, int sink, int recent, int block_size,
+                                         const int32_t* lengths, int max_length, int page_capacity,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (lengths == nullptr || max_length < 0 || page_capacity < 0) return TW_EINVAL;
+  return select_launch(logits, G, R, N, sel_pages, b0_pages, top_p, 0, 0, desired, allocated, head_bits, rows,
+                       row_counts, rows_stride, sink, recent, block_size, max_length, lengths, page_capacity, -1,
+                       workspace, workspace_bytes, stream);
 }

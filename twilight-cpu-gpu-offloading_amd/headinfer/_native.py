@@ -68,7 +68,7 @@ _HIP_SIGNATURES = {
     "tw_decode_attention": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i64, vp, i32, i32, i32, vp, vp,
                                   f32, vp, vp, szt, vp]),
     "tw_decode_attention_rows_append": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i64, i32, vp, vp,
-                                              i64, f32, vp, vp, szt, vp]),
+                                              i64, vp, f32, vp, vp, szt, vp]),
     "tw_decode_attention_pages": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32, i32, i32,
                                         i32, vp, vp, f32, vp, vp, szt, vp]),
     "tw_twilight_qk": (i32, [vp, i32, i32, i32, vp, vp, vp, i32, i64, i64, vp, vp, vp, i64, i32, i32, i32, f32, vp, vp]),
@@ -76,6 +76,8 @@ _HIP_SIGNATURES = {
     "tw_twilight_select_workspace_size": (szt, [i32, i32, i32]),
     "tw_twilight_select": (i32, [vp, i32, i32, i32, vp, i32, f32, i32, i32, vp, vp, vp, vp, vp, i64, i32, i32, i32,
                                  i32, i32, vp, szt, vp]),
+    "tw_twilight_select_ragged": (i32, [vp, i32, i32, i32, vp, i32, f32, vp, vp, vp, vp, vp, i64, i32, i32, i32, vp,
+                                        i32, i32, vp, szt, vp]),
     "tw_decode_attention_pages_phase": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32,
                                               i32, i32, i32, vp, vp, f32, vp, vp, szt, i32, vp]),
     "tw_gather_rows": (i32, [vp, vp, i64, vp, vp, i64, i32, i32, vp, vp, vp, vp]),

@@ -595,6 +595,61 @@ def twilight_select(
                                        stream_handle(dev)), "twilight_select")
 
 
+def twilight_select_ragged(
+    logits: torch.Tensor,
+    sel_pages: torch.Tensor,
+    lengths: torch.Tensor,
+    *,
+    top_p: float,
+    rows: torch.Tensor,
+    row_counts: torch.Tensor,
+    max_length: int,
+    page_capacity: int,
+    sink: int,
+    recent: int,
+    block_size: int,
+    desired: Optional[torch.Tensor] = None,
+    head_bits: Optional[torch.Tensor] = None,
+) -> None:
+    """twilight_select with dynamic budgets over groups of different lengths
+    (lengths [G] int32 on the device, each <= max_length < rows.shape[1]):
+    group g keeps min(ragged candidate pages, page_capacity, b0) B0 pages per
+    head (sel_pages from quest_select_ragged, -1 beyond), and its union has
+    no decode row (the attention takes cur_k/cur_v)."""
+    if logits.dtype != torch.float32 or logits.ndim != 3 or not logits.is_contiguous():
+        raise ValueError("logits must be contiguous [G, R, N] fp32")
+    G, R, N = logits.shape
+    if sel_pages.dtype != torch.int32 or sel_pages.ndim != 3 or sel_pages.shape[:2] != (G, R) \
+            or not sel_pages.is_contiguous():
+        raise ValueError("sel_pages must be contiguous [G, R, b0] int32")
+    b0 = sel_pages.shape[2]
+    if b0 * block_size != N:
+        raise ValueError("logits must hold b0_pages * block_size candidates per head")
+    if lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,) or not lengths.is_contiguous():
+        raise ValueError("lengths must be contiguous [G] int32")
+    if rows.dtype != torch.int32 or rows.ndim != 2 or rows.shape[0] != G or rows.stride(1) != 1 \
+            or rows.shape[1] <= max_length:
+        raise ValueError("rows must be [G, > max_length] int32")
+    if row_counts.dtype != torch.int32 or tuple(row_counts.shape) != (G,):
+        raise ValueError("row_counts must be [G] int32")
+    if desired is not None and (desired.dtype != torch.int32 or tuple(desired.shape) != (G, R)
+                                or not desired.is_contiguous()):
+        raise ValueError("desired must be contiguous [G, R] int32")
+    if head_bits is not None and (head_bits.dtype != torch.int32 or tuple(head_bits.shape) != (G, R, (N + 31) // 32)
+                                  or not head_bits.is_contiguous()):
+        raise ValueError("head_bits must be contiguous [G, R, ceil(N/32)] int32")
+    dev = _require_device(logits, sel_pages, lengths, rows, row_counts, desired, head_bits,
+                          what="twilight_select_ragged")
+    nbytes = hip().tw_twilight_select_workspace_size(G, R, N)
+    ws = WORKSPACE.get(dev, "twilight_select", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_twilight_select_ragged(ptr(logits), G, R, N, ptr(sel_pages), b0, float(top_p), ptr(desired),
+                                              None, ptr(head_bits), ptr(rows), ptr(row_counts), rows.stride(0),
+                                              sink, recent, block_size, ptr(lengths), int(max_length),
+                                              int(page_capacity), ptr(ws), ws.numel(), stream_handle(dev)),
+              "twilight_select_ragged")
+
+
 # --------------------------------------------------------------- attention
 def decode_attention_rows(
     q: torch.Tensor,
@@ -616,7 +671,9 @@ def decode_attention_rows(
     HBM or mapped pinned host); rows [G, stride] int32 positions; row_counts
     [G] int32; cur_k/cur_v [G, D] extra decode token.  With append_position
     (and cur_k/cur_v) the same launch also writes the decode token to that
-    row of every entry; the row list must not name it.  Returns [G,R,D]."""
+    row of every entry -- an int, or an int32 [G] device tensor of per-group
+    rows (rows outside the entry are skipped); the row list must not name
+    it.  Returns [G,R,D]."""
     if q.ndim != 3 or q.dtype not in _KEY_DTYPES:
         raise ValueError("q must be [G, R, D]")
     G, R, D = q.shape
@@ -645,13 +702,21 @@ def decode_attention_rows(
     if append_position is not None:
         if cur_k is None:
             raise ValueError("append_position needs cur_k/cur_v")
-        if not 0 <= int(append_position) < k_cache.shape[1]:
-            raise ValueError(f"append_position {append_position} outside the cache rows [0, {k_cache.shape[1]})")
+        rows_dev = None
+        if isinstance(append_position, torch.Tensor):
+            if append_position.dtype != torch.int32 or tuple(append_position.shape) != (G,) \
+                    or not append_position.is_contiguous() or append_position.device != q.device:
+                raise ValueError("per-group append rows must be contiguous [G] int32 on q's device")
+            rows_dev, pos = append_position, 0
+        else:
+            pos = int(append_position)
+            if not 0 <= pos < k_cache.shape[1]:
+                raise ValueError(f"append_position {pos} outside the cache rows [0, {k_cache.shape[1]})")
         with torch.cuda.device(dev):
             check(hip().tw_decode_attention_rows_append(
                 ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D, ptr(rows), ptr(row_masks),
                 ptr(row_counts), rows.stride(0), k_cache.stride(0) // D, max_rows, ptr(cur_k), ptr(cur_v),
-                int(append_position), scale, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)), "decode_attention")
+                pos, ptr(rows_dev), scale, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)), "decode_attention")
         return out
     with torch.cuda.device(dev):
         check(hip().tw_decode_attention(ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D, ptr(rows),
