@@ -859,7 +859,7 @@ def run_tpot(args, dev) -> int:
     runs = {}
     variants = [("sparse_graph", args.budget_pages, True, False), ("dense_graph", 1 << 20, True, False),
                 ("sparse_hf_eager", args.budget_pages, False, False), ("dense_hf_eager", 1 << 20, False, False),
-                ("twilight_hf_eager", None, False, False)]
+                ("twilight_graph", None, True, False), ("twilight_hf_eager", None, False, False)]
     if residency == "host":  # the HBM resident page cache (previous_token_resident_cache) serves host slabs
         variants[1:1] = [("sparse_graph_resident", args.budget_pages, True, True)]
         variants[4:4] = [("sparse_hf_eager_resident", args.budget_pages, False, True)]
@@ -873,7 +873,7 @@ def run_tpot(args, dev) -> int:
             # the reference runner's path: Quest B0 = 4096 tokens, INT4 QK, top-p 0.95
             cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(
                 model, max_cache_len=ctx + n_dec + 8, kv_residency=residency, candidate_token_budget=4096,
-                top_p=0.95, budget_mode="dynamic")
+                top_p=0.95, budget_mode="dynamic", update_metadata_on_decode=graph)
         else:
             cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + n_dec + 8,
                                                              kv_residency=residency, budget_pages=pages,

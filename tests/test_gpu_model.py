@@ -319,3 +319,44 @@ def test_graph_decoder_fused_equals_unfused(dev):
     n = T_PROMPT + steps   # rows beyond are never written
     assert torch.equal(caches[0]._key_cache[:, :n], caches[1]._key_cache[:, :n])
     assert torch.equal(caches[0]._value_cache[:, :n], caches[1]._value_cache[:, :n])
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+def test_graph_decoder_twilight_matches_eager(dev, fuse):
+    """GraphDecoder over a Twilight cache (Quest B0, INT4 QK, top-p and the
+    GQA union from device-side lengths, the union attention with the append,
+    the INT4 + page metadata update) == the eager patched model with the same
+    cache policy, token by token; the steps cross a page completion."""
+    from headinfer import mp
+    from headinfer.graph_decode import GraphDecoder
+    from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache
+
+    _say(f"[graph decoder twilight] fuse={fuse}")
+    steps = 10
+    _, gpu = _models(dev)
+    mp.mp_headinfer(gpu)
+    kw = dict(max_cache_len=T_PROMPT + steps + 2, sink_tokens=64, recent_tokens=256, block_size=16,
+              kv_residency="hbm", candidate_token_budget=128, top_p=0.9, budget_mode="dynamic",
+              update_metadata_on_decode=True)
+    eager_cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(gpu, **kw)
+    graph_cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(gpu, **kw)
+    g = torch.Generator().manual_seed(9)
+    ids = torch.randint(0, 1000, (1, T_PROMPT), generator=g).to(dev)
+    tok = torch.ones((1, 1), dtype=torch.long, device=dev)
+    with torch.no_grad():
+        gpu(input_ids=ids, past_key_values=eager_cache, use_cache=True, logits_to_keep=1)
+        gpu(input_ids=ids, past_key_values=graph_cache, use_cache=True, logits_to_keep=1)
+        dec = GraphDecoder(gpu, graph_cache, max_new_tokens=steps, fixed_token=1, fuse=fuse)
+        for step in range(steps):
+            ref = gpu(input_ids=tok, past_key_values=eager_cache, use_cache=True).logits[0, -1].float()
+            got = dec.step()[0].float()
+            torch.cuda.synchronize()
+            err = (got - ref).abs().max().item()
+            assert err <= 0.02 * ref.abs().max().item() + 1e-3, (step, err)
+    dec.sync_cache()
+    L = T_PROMPT + steps
+    assert graph_cache.get_seq_length() == eager_cache.get_seq_length() == L
+    for e in range(graph_cache.geometry.num_entries):
+        a = graph_cache._key_cache[e, :L].float().cpu()
+        b = eager_cache._key_cache[e, :L].float().cpu()
+        assert torch.allclose(a, b, atol=2e-2, rtol=2e-2), e

@@ -1,4 +1,5 @@
-"""Graph-captured decode of a patched Llama / Qwen2 model over a Quest cache.
+"""Graph-captured decode of a patched Llama / Qwen2 model over a Quest or a
+Twilight cache.
 
 After the prompt went through the ``mp_headinfer``-patched model (which fills
 the cache's slab and page metadata), ``GraphDecoder`` runs every decode token
@@ -24,19 +25,24 @@ alternates between two buffers, since every GEMV block normalises the row
 itself while block 0 stores the sum.  With fuse=False the norms, RoPE, SiLU
 and the metadata update run as launches of their own (13 per layer) -- the
 same bits.
+Over a Twilight cache (dynamic top-p budgets) the sparse path of a layer is
+the ragged Quest B0 selection, the INT4 QK, the top-p and GQA union, the
+union attention with the append and the INT4 + page metadata update of the
+appended row, all from the device-side lengths.
 The q/k/v and gate/up weights are concatenated once and the HF modules keep
 views into them, so the model's own forward (the prefill) uses the same
 storage.  The element-wise steps repeat the HF modules' rounding steps; the
 GEMV and RMSNorm reduction orders differ from hipBLASLt and torch, so logits
-follow the eager patched model to bf16 rounding.  Quest selection with an absolute budget (``budget_pages``),
-16-row pages, head_dim 128 and 16-bit K/V only (the page-tile kernel); the
-cache must be built with ``update_metadata_on_decode=True`` so pages
-completed during decode are scored.  While the decoder runs it owns the
+follow the eager patched model to bf16 rounding.  Quest selection needs an
+absolute budget (``budget_pages``); both caches need 16-row pages, head_dim
+128 and 16-bit K/V, and must be built with ``update_metadata_on_decode=True``
+so pages completed during decode are scored.  While the decoder runs it owns the
 cache; ``sync_cache()`` brings the cache's host-side lengths up to date.
 """
 
 from __future__ import annotations
 
+import math
 from typing import Optional
 
 import torch
@@ -54,10 +60,19 @@ class GraphDecoder:
                  fuse: bool = True):
         if not getattr(cache, "update_metadata_on_decode", False):
             raise ValueError("GraphDecoder needs a cache built with update_metadata_on_decode=True")
-        if cache.budget_pages is None:
-            raise ValueError("GraphDecoder needs an absolute Quest budget (budget_pages)")
-        if type(cache).__name__ != "QuestTopKOffloadedCache":
-            raise ValueError("GraphDecoder runs Quest selection; use a QuestTopKOffloadedCache")
+        kind = type(cache).__name__
+        if kind == "TwilightMatchedBudgetOffloadedCache":
+            self.twilight = True
+            if cache.budget_mode != "dynamic":
+                raise ValueError("GraphDecoder runs Twilight with dynamic (top-p) budgets")
+            if cache.previous_token_resident_cache:
+                raise ValueError("GraphDecoder runs the Twilight union attention without the resident cache")
+        elif kind == "QuestTopKOffloadedCache":
+            self.twilight = False
+            if cache.budget_pages is None:
+                raise ValueError("GraphDecoder needs an absolute Quest budget (budget_pages)")
+        else:
+            raise ValueError("GraphDecoder runs a QuestTopKOffloadedCache or a TwilightMatchedBudgetOffloadedCache")
         inner = model.model
         cfg = model.config
         self.model, self.cache = model, cache
@@ -86,7 +101,11 @@ class GraphDecoder:
         self.fixed_token = fixed_token
         self.fuse = fuse
         self.P = min(int(cache._page_min.shape[1]), 8192)
-        self.k = min(int(cache.budget_pages), self.P)
+        if self.twilight:
+            # stage 1 keeps B0 pages per head (fewer for a short group), stage 2 top-p over their tokens
+            self.k = min(max(1, math.ceil(cache.candidate_token_budget / cache.block_size)), self.P)
+        else:
+            self.k = min(int(cache.budget_pages), self.P)
         self.width = max(1, min(self.P, self.R * self.k))
         # device state: token, position, per-group length
         self.token = torch.full((1,), 1 if fixed_token is None else int(fixed_token), dtype=torch.long, device=dev)
@@ -141,6 +160,15 @@ class GraphDecoder:
                       torch.zeros((self.G, self.width), dtype=torch.uint8, device=dev),
                       torch.zeros((self.G,), dtype=torch.int32, device=dev)) for _ in self.layers]
         self.attn = [torch.empty((self.G, self.R, self.D), dtype=cache.dtype, device=dev) for _ in self.layers]
+        if self.twilight:
+            # stage-2 buffers, reused layer after layer: B0 pages, INT4 logits, union rows
+            self.max_length = L0 + max_new_tokens
+            n_cand = self.k * cache.block_size
+            self.tw_sel = torch.zeros((self.G, self.R, self.k), dtype=torch.int32, device=dev)
+            self.tw_logits = torch.zeros((self.G, self.R, n_cand), dtype=torch.float32, device=dev)
+            self.tw_rows = torch.zeros((self.G, self.max_length + 1), dtype=torch.int32, device=dev)
+            self.tw_counts = torch.zeros((self.G,), dtype=torch.int32, device=dev)
+            self.tw_max_rows = min(self.max_length, cache.sink_tokens + self.R * n_cand + cache.recent_tokens)
         self.logits: Optional[torch.Tensor] = None
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
@@ -184,6 +212,19 @@ class GraphDecoder:
             qg = q.view(G, R, D)
             e0 = li * G
             pp, pm, pc = self.plan[li]
+            if self.twilight:
+                self._twilight_attention(li, attn, qg, k, v, pp, pm, pc)
+                o = kernels.gemv(self.attn[li].view(1, Hq * D), attn.o_proj.weight, attn.o_proj.bias, self.o)
+                norm = layer.post_attention_layernorm
+                delta = o
+                if self.fuse:
+                    norm_into(norm, self.wgu[li], self.bgu[li], self.m, "silu")
+                else:
+                    kernels.add_rms_norm(h, o, norm.weight, norm.variance_epsilon, x)
+                    gu = kernels.gemv(x, self.wgu[li], self.bgu[li], self.gu)
+                    kernels.silu_mul(gu, self.m)
+                delta = kernels.gemv(self.m, layer.mlp.down_proj.weight, layer.mlp.down_proj.bias, self.dn)
+                continue
             kernels.quest_select_ragged(self.q32.view(G, R, D), c._page_min[e0:e0 + G, :self.P],
                                         c._page_max[e0:e0 + G, :self.P], self.lengths, self.k, sink=c.sink_tokens,
                                         recent=c.recent_tokens, block_size=c.block_size, plan_pages=pp,
@@ -229,6 +270,32 @@ class GraphDecoder:
             self.token.copy_(logits.argmax(dim=-1))
         self.position.add_(1)
         self.lengths.add_(1)
+
+    def _twilight_attention(self, li: int, attn, qg, k, v, pp, pm, pc) -> None:
+        """Twilight stages 1-2 (Quest B0, INT4 QK, top-p + GQA union) and the
+        union attention with the append, then the INT4 row and page metadata
+        of the appended row, all from the device-side lengths."""
+        c = self.cache
+        G, R, D = self.G, self.R, self.D
+        e0 = li * G
+        q32 = self.q32.view(G, R, D)
+        kernels.quest_select_ragged(q32, c._page_min[e0:e0 + G, :self.P], c._page_max[e0:e0 + G, :self.P],
+                                    self.lengths, self.k, sink=c.sink_tokens, recent=c.recent_tokens,
+                                    block_size=c.block_size, sel_pages=self.tw_sel, plan_pages=pp, plan_masks=pm,
+                                    plan_counts=pc)
+        kernels.twilight_qk(q32, c._packed[e0:e0 + G], c._qscale[e0:e0 + G], c._qmin[e0:e0 + G], pp, pm, pc, self.k,
+                            sink=c.sink_tokens, block_size=c.block_size, out=self.tw_logits)
+        kernels.twilight_select_ragged(self.tw_logits, self.tw_sel, self.lengths, top_p=c.top_p, rows=self.tw_rows,
+                                       row_counts=self.tw_counts, max_length=self.max_length,
+                                       page_capacity=self.P, sink=c.sink_tokens, recent=c.recent_tokens,
+                                       block_size=c.block_size)
+        kernels.decode_attention_rows(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], self.tw_rows,
+                                      self.tw_counts, self.tw_max_rows, cur_k=k, cur_v=v,
+                                      softmax_scale=float(attn.scaling), out=self.attn[li],
+                                      append_position=self.lengths)
+        kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
+                                            block_size=c.block_size, page_min=c._page_min, page_max=c._page_max,
+                                            packed=c._packed, scale=c._qscale, minimum=c._qmin)
 
     def capture(self) -> None:
         """Capture the step graph.  The step runs once eagerly first (its
