@@ -378,15 +378,22 @@ int tw_decode_attention(const void* q, const void* k_base, const void* v_base, i
  * append_position of entry g (0 <= append_position < entry_stride_rows), or,
  * when append_rows (int32 [G], device) is given, to row append_rows[g]
  * (rows outside the entry are skipped); the row list must not name it.
- * Replaces the Twilight decode step's GQA decode attention over the union
- * rows (mp.py:239-279) followed by the batched new-KV append
- * (twilight_offload_cache.py:551-794). */
+ * Optional (16-bit keys, D = 128): the decode-time metadata update of
+ * tw_update_page_metadata for the appended row -- its INT4 code, scale and
+ * minimum into packed / quant_scale / quant_min (row g * quant_entry_stride
+ * + row) and, when it completes page p ((row - sink + 1) % 16 == 0,
+ * p < meta_pages), that page's min/max into page_min / page_max (g *
+ * page_entry_stride + p * 128).  Replaces the Twilight decode step's GQA
+ * decode attention over the union rows (mp.py:239-279) followed by the
+ * batched new-KV append (twilight_offload_cache.py:551-794). */
 int tw_decode_attention_rows_append(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
                                     int D, const int32_t* rows, const uint8_t* row_masks, const int32_t* row_counts,
                                     int64_t rows_stride, int64_t entry_stride_rows, int max_rows,
                                     const void* cur_k, const void* cur_v, int64_t append_position,
-                                    const int32_t* append_rows, float softmax_scale, void* out, void* workspace,
-                                    size_t workspace_bytes, void* stream);
+                                    const int32_t* append_rows, float softmax_scale, int sink, void* page_min,
+                                    void* page_max, int64_t page_entry_stride, int meta_pages, uint8_t* packed,
+                                    void* quant_scale, void* quant_min, int64_t quant_entry_stride, void* out,
+                                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Head-wise K/V row gather into the attention layout.

@@ -441,3 +441,55 @@ def test_twilight_select_ragged_matches_per_group(K, dev):
         assert torch.equal(desired[g].cpu(), d1[0].cpu()), g
         assert torch.equal(hb[g, :, :words1].cpu(), h1[0].cpu()) and bool((hb[g, :, words1:] == 0).all()), g
         assert n == int(n1[0]) and torch.equal(rows[g, :n].cpu(), r1[0, :n].cpu()), g
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_rows_append_fused_metadata(K, dev, dtype):
+    """The rows-mode attention with the append and the INT4 + page metadata
+    update fused: 40 steps from lengths of different page phases (one
+    appended row holds a NaN) leave the metadata equal to a rebuild, and the
+    outputs equal the launch without the update."""
+    _say(f"[rows append metadata] {dtype}")
+    R, steps = 4, 40
+    lengths0 = [100, 143, 200, 300]
+    G = len(lengths0)
+    Lmax = max(lengths0) + steps + 16
+    keys = randn((G, Lmax, D), dtype, seed=151)
+    kd, vd = keys.to(dev), randn((G, Lmax, D), dtype, seed=152).to(dev)
+    kd2, vd2 = kd.clone(), vd.clone()
+    P = (Lmax - SINK) // BS
+    pmin = torch.zeros((G, P, D), dtype=keys.dtype, device=dev)
+    pmax = torch.zeros_like(pmin)
+    packed = torch.zeros((G, Lmax, D // 2), dtype=torch.uint8, device=dev)
+    scale = torch.zeros((G, Lmax), dtype=keys.dtype, device=dev)
+    minimum = torch.zeros_like(scale)
+    for g, L in enumerate(lengths0):
+        K.build_page_metadata(kd[g, :L], sink=SINK, block_size=BS, page_min=pmin[g], page_max=pmax[g],
+                              packed=packed[g], scale=scale[g], minimum=minimum[g])
+    lengths = torch.tensor(lengths0, dtype=torch.int32, device=dev)
+    meta = dict(sink=SINK, page_min=pmin, page_max=pmax, packed=packed, scale=scale, minimum=minimum)
+    gen = torch.Generator().manual_seed(153)
+    for step in range(steps):
+        q = randn((G, R, D), dtype, seed=600 + step).to(dev)
+        ck, cv = randn((G, D), dtype, seed=700 + step), randn((G, D), dtype, seed=800 + step)
+        if step == 9:
+            ck[1, 17] = float("nan")
+        ck, cv = ck.to(dev), cv.to(dev)
+        n = 50
+        rows = torch.stack([torch.randperm(min(lengths0) + step, generator=gen)[:n].sort().values
+                            for _ in range(G)]).to(torch.int32).to(dev)
+        counts = torch.full((G,), n, dtype=torch.int32, device=dev)
+        a = K.decode_attention_rows(q, kd, vd, rows, counts, n, cur_k=ck, cur_v=cv, append_position=lengths,
+                                    metadata=meta)
+        b = K.decode_attention_rows(q, kd2, vd2, rows, counts, n, cur_k=ck, cur_v=cv, append_position=lengths)
+        torch.cuda.synchronize()
+        assert same_bits(a, b), step
+        lengths += 1
+    assert same_bits(kd, kd2) and same_bits(vd, vd2)
+    for g, L0 in enumerate(lengths0):
+        n = L0 + steps
+        omin, omax, opk, osc, omn = oracle.build_page_metadata(to_bits(kd[g, :n].cpu()), dtype, SINK, BS)
+        p = omin.shape[0]
+        assert same_bits(pmin[g, :p], from_bits(omin, dtype)) and same_bits(pmax[g, :p], from_bits(omax, dtype)), g
+        assert np.array_equal(packed[g, :n].cpu().numpy(), opk), g
+        assert same_bits(scale[g, :n], from_bits(osc, dtype)) and same_bits(minimum[g, :n], from_bits(omn, dtype)), g

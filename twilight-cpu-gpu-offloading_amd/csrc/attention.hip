@@ -113,6 +113,14 @@ struct AttnArgs {
   int meta_pages;
   // page-tile kernel: K and V are device memory (read with the streaming hint)
   int kv_stream;
+  // Rows mode with the append (16-bit, D = 128, nullable): the appended
+  // row's INT4 code, scale and minimum at row (g * meta_qstride + row) of
+  // meta_packed ([.][D/2] bytes) / meta_qscale / meta_qmin; the page it
+  // completes as meta_min / meta_max above.
+  uint8_t* meta_packed;
+  void* meta_qscale;
+  void* meta_qmin;
+  int64_t meta_qstride;
 };
 
 // 8 consecutive channels of one row.
@@ -241,6 +249,19 @@ __device__ __forceinline__ GroupRows group_rows(const AttnArgs& a, int g, int D)
 // Page-tile mode (decode_attn_tiles): chunks count 16-row tiles.
 constexpr int kModeTiles = 3;
 
+// Host side: the metadata the rows-mode append updates (complete_row_meta).
+struct RowMeta {
+  int sink;
+  void* page_min;
+  void* page_max;
+  int64_t page_stride;
+  int pages;
+  uint8_t* packed;
+  void* qscale;
+  void* qmin;
+  int64_t qstride;
+};
+
 // The row the decode token of group g is appended at: append_position, or in
 // rows mode with per-group lengths, lengths[g] (out of range: none).
 template <int MODE>
@@ -294,6 +315,45 @@ __device__ __forceinline__ void complete_page_meta(const AttnArgs& a, int g, int
   for (int h = 0; h < 2; ++h) {
     mn[h] = nan[h] ? canonical_nan(DT{}) : from_order_key(DT{}, kmin[h]);
     mx[h] = nan[h] ? canonical_nan(DT{}) : from_order_key(DT{}, kmax[h]);
+  }
+}
+
+// Rows mode: the metadata update of the appended row `position` of group g
+// by wave 0 of the block (16-bit keys, D = 128, read from cur_k): its INT4
+// code -- row min/max as order keys reduced over the wavefront, scale and
+// codes as the metadata build computes them -- and the page it completes.
+template <typename DT>
+__device__ __forceinline__ void complete_row_meta(const AttnArgs& a, int g, int position) {
+  if constexpr (sizeof(typename DT::storage) != 2) {
+    return;
+  } else {
+    using S = typename DT::storage;
+    if (position < 0 || threadIdx.x >= kWave || a.cur_k == nullptr) return;
+    if (a.meta_packed != nullptr) {
+      const int lane = static_cast<int>(threadIdx.x);
+      const S* cur = static_cast<const S*>(a.cur_k) + static_cast<int64_t>(g) * 128;
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(cur + 2 * lane);
+      const S x0 = static_cast<S>(w & 0xffffu), x1 = static_cast<S>(w >> 16);
+      const uint32_t k0 = order_key(DT{}, x0), k1 = order_key(DT{}, x1);
+      const uint32_t kmin = wave_min_u32(k0 < k1 ? k0 : k1);
+      const uint32_t kmax = wave_max_u32(k0 > k1 ? k0 : k1);
+      const bool any_nan = __ballot(is_nan(DT{}, x0) || is_nan(DT{}, x1)) != 0ull;
+      const S mn = any_nan ? canonical_nan(DT{}) : from_order_key(DT{}, kmin);
+      const S mx = any_nan ? canonical_nan(DT{}) : from_order_key(DT{}, kmax);
+      const float mnf = to_f32(DT{}, mn);
+      const float mxf = to_f32(DT{}, mx);
+      const S sc = from_f32(DT{}, int4_scale<DT>(mnf, mxf));
+      const float sf = to_f32(DT{}, sc);
+      const uint32_t lo = int4_code(to_f32(DT{}, x0), mnf, sf);
+      const uint32_t hi = int4_code(to_f32(DT{}, x1), mnf, sf);
+      const int64_t row = static_cast<int64_t>(g) * a.meta_qstride + position;
+      a.meta_packed[row * 64 + lane] = static_cast<uint8_t>(lo | (hi << 4));
+      if (lane == 0) {
+        static_cast<S*>(a.meta_qscale)[row] = sc;
+        static_cast<S*>(a.meta_qmin)[row] = mn;
+      }
+    }
+    complete_page_meta<DT>(a, g, position);
   }
 }
 constexpr int kTileRows = 16;
@@ -573,8 +633,10 @@ __global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(
     return;
   }
   if (chunk >= n_chunks) return;
-  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0)
+  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0) {
     append_decode_token<S>(a, g, D, decode_row_position<MODE>(a, g));
+    if (MODE == kModeRows) complete_row_meta<DT>(a, g, decode_row_position<MODE>(a, g));
+  }
 
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
@@ -890,8 +952,10 @@ __global__ __launch_bounds__(kBlock, 2) void decode_attn_mfma(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0)
+  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0) {
     append_decode_token<S>(a, g, D, decode_row_position<MODE>(a, g));
+    if (MODE == kModeRows) complete_row_meta<DT>(a, g, decode_row_position<MODE>(a, g));
+  }
 
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
@@ -1485,8 +1549,10 @@ __global__ __launch_bounds__(kBlock) void decode_attn_generic(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
-  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0)
+  if ((MODE == kModePages || MODE == kModeRows) && chunk == 0) {
     append_decode_token<S>(a, g, D, decode_row_position<MODE>(a, g));
+    if (MODE == kModeRows) complete_row_meta<DT>(a, g, decode_row_position<MODE>(a, g));
+  }
   const S* kbase = static_cast<const S*>(a.k);
   const S* vbase = static_cast<const S*>(a.v);
   const S* qg = static_cast<const S*>(a.q) + static_cast<int64_t>(g) * R * D;
@@ -1800,7 +1866,8 @@ int rows_launch(const void* q, const void* k_base, const void* v_base, int dtype
                 const int32_t* rows, const uint8_t* row_masks, const int32_t* row_counts, int64_t rows_stride,
                 int64_t entry_stride_rows, const int32_t* cu_seqlens_k, int Hk, int window_left, int max_rows,
                 const void* cur_k, const void* cur_v, int64_t append_position, const int32_t* append_rows,
-                float softmax_scale, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+                float softmax_scale, void* out, void* workspace, size_t workspace_bytes, void* stream,
+                const tw::RowMeta* meta = nullptr) {
   if (q == nullptr || out == nullptr || G <= 0 || R <= 0 || R > 8 || D <= 0 || D > 512 || (D % 2) != 0 ||
       max_rows < 0)
     return TW_EINVAL;
@@ -1855,6 +1922,17 @@ int rows_launch(const void* q, const void* k_base, const void* v_base, int dtype
     a.v_append = const_cast<void*>(v_base);
     a.append_position = static_cast<int>(append_position);
     a.lengths = append_rows;  // rows mode: per-group append rows
+    if (meta != nullptr) {
+      a.sink = meta->sink;
+      a.meta_min = meta->page_min;
+      a.meta_max = meta->page_max;
+      a.meta_stride = meta->page_stride;
+      a.meta_pages = meta->pages;
+      a.meta_packed = meta->packed;
+      a.meta_qscale = meta->qscale;
+      a.meta_qmin = meta->qmin;
+      a.meta_qstride = meta->qstride;
+    }
   }
   tw::plan_chunks(dtype, G, R, D, max_rows + (cur_k != nullptr ? 1 : 0), &a.iters, &a.max_chunks);
   return tw::launch_dtype(dtype, a, static_cast<hipStream_t>(stream));
@@ -1872,20 +1950,33 @@ extern "C" int tw_decode_attention(const void* q, const void* k_base, const void
                      workspace, workspace_bytes, stream);
 }
 
-extern "C" int tw_decode_attention_rows_append(const void* q, const void* k_base, const void* v_base, int dtype,
-                                               int G, int R, int D, const int32_t* rows, const uint8_t* row_masks,
-                                               const int32_t* row_counts, int64_t rows_stride,
-                                               int64_t entry_stride_rows, int max_rows, const void* cur_k,
-                                               const void* cur_v, int64_t append_position,
-                                               const int32_t* append_rows, float softmax_scale, void* out,
-                                               void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int tw_decode_attention_rows_append(
+    const void* q, const void* k_base, const void* v_base, int dtype, int G, int R, int D, const int32_t* rows,
+    const uint8_t* row_masks, const int32_t* row_counts, int64_t rows_stride, int64_t entry_stride_rows,
+    int max_rows, const void* cur_k, const void* cur_v, int64_t append_position, const int32_t* append_rows,
+    float softmax_scale, int sink, void* page_min, void* page_max, int64_t page_entry_stride, int meta_pages,
+    uint8_t* packed, void* quant_scale, void* quant_min, int64_t quant_entry_stride, void* out, void* workspace,
+    size_t workspace_bytes, void* stream) {
   if (rows == nullptr || cur_k == nullptr || cur_v == nullptr) return TW_EINVAL;
   if (append_rows == nullptr &&
       (append_position < 0 || append_position >= entry_stride_rows || append_position > INT32_MAX))
     return TW_EINVAL;
+  const bool meta = page_min != nullptr || packed != nullptr;
+  if (meta) {
+    if (dtype == TW_DTYPE_F32 || D != 128 || sink < 0) return TW_EUNSUPPORTED;
+    if (page_min != nullptr && (page_max == nullptr || meta_pages < 1 || page_entry_stride < 128ll * meta_pages))
+      return TW_EINVAL;
+    if (packed != nullptr && (quant_scale == nullptr || quant_min == nullptr || quant_entry_stride < entry_stride_rows))
+      return TW_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(cur_k) % 4) || (reinterpret_cast<uintptr_t>(page_min) % 4) ||
+        (reinterpret_cast<uintptr_t>(page_max) % 4))
+      return TW_EINVAL;
+  }
+  tw::RowMeta m{sink, page_min, page_max, page_entry_stride, meta_pages, packed, quant_scale, quant_min,
+                quant_entry_stride};
   return rows_launch(q, k_base, v_base, dtype, G, R, D, rows, row_masks, row_counts, rows_stride, entry_stride_rows,
                      nullptr, 0, -1, max_rows, cur_k, cur_v, append_rows != nullptr ? 0 : append_position,
-                     append_rows, softmax_scale, out, workspace, workspace_bytes, stream);
+                     append_rows, softmax_scale, out, workspace, workspace_bytes, stream, meta ? &m : nullptr);
 }
 
 extern "C" int tw_decode_attention_pages(const void* q, const void* k_base, const void* v_base, int dtype, int G,

@@ -32,24 +32,6 @@ __device__ __forceinline__ void load_pair(const float* p, float& a, float& b) {
   b = w.y;
 }
 
-// INT4 code of one value (twilight_offload_cache.py:32-35): round half to
-// even of (f32(k) - f32(min)) / f32(scale), clamped to [0, 15]; NaN -> 0.
-__device__ __forceinline__ uint32_t int4_code(float k, float mn, float sf) {
-  float c = rintf((k - mn) / sf);
-  c = c < 0.0f ? 0.0f : c;
-  c = c > 15.0f ? 15.0f : c;
-  return (c == c) ? static_cast<uint32_t>(c) : 0u;
-}
-
-// Per-row scale (twilight_offload_cache.py:31): the max - min difference is
-// rounded to the key dtype, clamped below at 1e-9 in fp32 (NaN stays NaN),
-// divided by 15 and rounded back to the key dtype.
-template <typename DT>
-__device__ __forceinline__ float int4_scale(float mnf, float mxf) {
-  float diff = round_to<DT>(mxf - mnf);
-  if (diff < 1e-9f) diff = 1e-9f;
-  return diff / 15.0f;
-}
 
 template <typename DT>
 __device__ __forceinline__ void process_row(const typename DT::storage* __restrict__ row, int D, int nchunk,

@@ -68,7 +68,8 @@ _HIP_SIGNATURES = {
     "tw_decode_attention": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i64, vp, i32, i32, i32, vp, vp,
                                   f32, vp, vp, szt, vp]),
     "tw_decode_attention_rows_append": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i64, i32, vp, vp,
-                                              i64, vp, f32, vp, vp, szt, vp]),
+                                              i64, vp, f32, i32, vp, vp, i64, i32, vp, vp, vp, i64, vp, vp, szt,
+                                              vp]),
     "tw_decode_attention_pages": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32, i32, i32,
                                         i32, vp, vp, f32, vp, vp, szt, vp]),
     "tw_twilight_qk": (i32, [vp, i32, i32, i32, vp, vp, vp, i32, i64, i64, vp, vp, vp, i64, i32, i32, i32, f32, vp, vp]),

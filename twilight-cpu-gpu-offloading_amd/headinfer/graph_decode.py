@@ -289,13 +289,18 @@ class GraphDecoder:
                                        row_counts=self.tw_counts, max_length=self.max_length,
                                        page_capacity=self.P, sink=c.sink_tokens, recent=c.recent_tokens,
                                        block_size=c.block_size)
+        # the attention also appends the decode token and (fused) updates its INT4 row and page metadata
+        meta = dict(sink=c.sink_tokens, page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G],
+                    packed=c._packed[e0:e0 + G], scale=c._qscale[e0:e0 + G], minimum=c._qmin[e0:e0 + G])
         kernels.decode_attention_rows(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], self.tw_rows,
                                       self.tw_counts, self.tw_max_rows, cur_k=k, cur_v=v,
                                       softmax_scale=float(attn.scaling), out=self.attn[li],
-                                      append_position=self.lengths)
-        kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
-                                            block_size=c.block_size, page_min=c._page_min, page_max=c._page_max,
-                                            packed=c._packed, scale=c._qscale, minimum=c._qmin)
+                                      append_position=self.lengths, metadata=meta if self.fuse else None)
+        if not self.fuse:
+            kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
+                                                block_size=c.block_size, page_min=c._page_min,
+                                                page_max=c._page_max, packed=c._packed, scale=c._qscale,
+                                                minimum=c._qmin)
 
     def capture(self) -> None:
         """Capture the step graph.  The step runs once eagerly first (its

@@ -665,6 +665,7 @@ def decode_attention_rows(
     softmax_scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
     append_position: Optional[int] = None,
+    metadata: Optional[dict] = None,
 ) -> torch.Tensor:
     """Sparse GQA decode attention reading K/V rows by position straight from
     the cache.  q [G,R,D]; k_cache/v_cache [G, Lmax, D] (the layer's entries,
@@ -673,7 +674,10 @@ def decode_attention_rows(
     (and cur_k/cur_v) the same launch also writes the decode token to that
     row of every entry -- an int, or an int32 [G] device tensor of per-group
     rows (rows outside the entry are skipped); the row list must not name
-    it.  Returns [G,R,D]."""
+    it.  metadata (with the append; 16-bit K, D = 128): dict(sink=,
+    page_min=, page_max= [G, pages, D], packed= [G, T, D/2], scale=,
+    minimum= [G, T]) -- the launch also does update_page_metadata for the
+    appended row (either pair may be left out).  Returns [G,R,D]."""
     if q.ndim != 3 or q.dtype not in _KEY_DTYPES:
         raise ValueError("q must be [G, R, D]")
     G, R, D = q.shape
@@ -712,11 +716,28 @@ def decode_attention_rows(
             pos = int(append_position)
             if not 0 <= pos < k_cache.shape[1]:
                 raise ValueError(f"append_position {pos} outside the cache rows [0, {k_cache.shape[1]})")
+        md = dict(metadata or {})
+        pmn, pmx, pk, qs, qm = (md.get(n) for n in ("page_min", "page_max", "packed", "scale", "minimum"))
+        if pmn is not None and (pmx is None or pmn.ndim != 3 or pmn.shape[0] != G or pmn.shape[2] != D
+                                or pmn.stride(2) != 1 or pmn.stride(1) != D or pmx.shape != pmn.shape
+                                or pmx.stride() != pmn.stride() or pmn.dtype != q.dtype):
+            raise ValueError("page_min/page_max must be [G, pages, D] with contiguous pages in q's dtype")
+        if pk is not None and (qs is None or qm is None or pk.dtype != torch.uint8 or pk.ndim != 3
+                               or pk.shape[0] != G or pk.shape[2] != D // 2 or pk.stride(2) != 1
+                               or pk.stride(1) != D // 2 or qs.ndim != 2 or qs.shape[0] != G or qs.stride(1) != 1
+                               or qm.stride() != qs.stride() or qs.dtype != q.dtype or qm.dtype != q.dtype
+                               or pk.stride(0) // (D // 2) != qs.stride(0)):
+            raise ValueError("packed [G, T, D/2] uint8 and scale/minimum [G, T] must match")
+        if pmn is not None or pk is not None:
+            _require_device(pmn, pmx, pk, qs, qm, what="decode_attention")
         with torch.cuda.device(dev):
             check(hip().tw_decode_attention_rows_append(
                 ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D, ptr(rows), ptr(row_masks),
                 ptr(row_counts), rows.stride(0), k_cache.stride(0) // D, max_rows, ptr(cur_k), ptr(cur_v),
-                pos, ptr(rows_dev), scale, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)), "decode_attention")
+                pos, ptr(rows_dev), scale, int(md.get("sink", 0)), ptr(pmn), ptr(pmx),
+                0 if pmn is None else pmn.stride(0), 0 if pmn is None else pmn.shape[1], ptr(pk), ptr(qs), ptr(qm),
+                0 if qs is None else qs.stride(0), ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
+                "decode_attention")
         return out
     with torch.cuda.device(dev):
         check(hip().tw_decode_attention(ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D, ptr(rows),
