@@ -90,6 +90,12 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
   int mode = 0;  // 0: take every candidate, 1: exact rank, 2: equal keys by index
   for (int level = 0;; ++level) {
     if (ccount == need) break;
+    // after a pass, few candidates go straight to the exact rank (it orders
+    // equal keys by index too), with no bounds reduction
+    if (level > 0 && ccount <= static_cast<uint32_t>(kBlock)) {
+      mode = 1;
+      break;
+    }
     uint32_t cmax = 0u, cmin = 0xffffffffu;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
@@ -179,9 +185,12 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
   }
   int total;
   if (mode == 1) {
-    // exact rank of at most kBlock candidates
+    // exact rank of at most kBlock candidates; slot t's rank goes to
+    // selbits[t] and back to the thread that owns slot t
+    static_assert(kMaxSelPages / 32 >= kBlock, "one rank per candidate slot");
     const int mine = __popc(cand);
-    int slot = block_excl_scan(mine, sh.scan, &total);
+    const int first = block_excl_scan(mine, sh.scan, &total);
+    int slot = first;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
       if ((cand >> j) & 1u) {
@@ -190,7 +199,6 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
         ++slot;
       }
     }
-    for (int w = tid; w < kMaxSelPages / 32; w += kBlock) sh.selbits[w] = 0u;
     __syncthreads();
     if (tid < static_cast<int>(ccount)) {
       const uint32_t mk = sh.ckey[tid];
@@ -201,14 +209,16 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
         const int im = sh.cidx[m];
         rank += (km > mk || (km == mk && im < mi)) ? 1u : 0u;
       }
-      if (rank < need) atomicOr(&sh.selbits[mi >> 5], 1u << (mi & 31));
+      sh.selbits[tid] = rank;
     }
     __syncthreads();
+    slot = first;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      const int i = i0 + j;
-      const bool c = (cand >> j) & 1u;
-      taken |= (c && ((sh.selbits[(i >> 5) & (kMaxSelPages / 32 - 1)] >> (i & 31)) & 1u)) ? (1u << j) : 0u;
+      if ((cand >> j) & 1u) {
+        taken |= sh.selbits[slot] < need ? (1u << j) : 0u;
+        ++slot;
+      }
     }
   } else if (mode == 2) {
     int before = block_excl_scan(__popc(cand), sh.scan, &total);
