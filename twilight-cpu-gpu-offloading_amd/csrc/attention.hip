@@ -495,6 +495,26 @@ __global__ __launch_bounds__(kBlock) void merge_vec_kernel(AttnArgs a, int rows_
   const int R = a.R;
   const int g = blockIdx.x / R;
   const int r = blockIdx.x - g * R;
+  const int t = threadIdx.x;
+  const int q = t % NQ;
+  const int cl = t / NQ;
+  const int wave = t / kWave;
+  __shared__ float s_red[kWaves];
+  __shared__ float4 s_o[NL][NQ];
+  __shared__ float s_l[NL];
+  // The partial loads go out against the launch's chunk bound, in the same
+  // round trip as the group's own chunk count; chunks past that count hold
+  // stale or unwritten data and are replaced by zeros (selects, not products).
+  const int64_t base = static_cast<int64_t>(g) * a.max_chunks;
+  float4 ov[MAXJ];
+  float2 mlv[MAXJ];
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const int c = cl + NL * j;
+    const int64_t pc = base + (c < a.max_chunks ? c : a.max_chunks - 1);
+    ov[j] = *reinterpret_cast<const float4*>(a.part_o + (pc * R + r) * D + 4 * q);
+    mlv[j] = *reinterpret_cast<const float2*>(a.part_ml + (pc * R + r) * 2);
+  }
   // rows_per_block: rows of a chunk, or tiles of a chunk in page-tile mode
   int n_chunks;
   if constexpr (MODE == kModeTiles) {
@@ -506,24 +526,13 @@ __global__ __launch_bounds__(kBlock) void merge_vec_kernel(AttnArgs a, int rows_
     n_chunks = (gr.n_rows + rows_per_block - 1) / rows_per_block;
   }
   if (n_chunks <= 1) return;
-  const int t = threadIdx.x;
-  const int q = t % NQ;
-  const int cl = t / NQ;
-  const int wave = t / kWave;
-  __shared__ float s_red[kWaves];
-  __shared__ float4 s_o[NL][NQ];
-  __shared__ float s_l[NL];
-  const int64_t base = static_cast<int64_t>(g) * a.max_chunks;
-  float4 ov[MAXJ];
   float mv[MAXJ], lv[MAXJ];
 #pragma unroll
   for (int j = 0; j < MAXJ; ++j) {
-    const int c = cl + NL * j;
-    const int64_t pc = base + (c < n_chunks ? c : n_chunks - 1);
-    ov[j] = *reinterpret_cast<const float4*>(a.part_o + (pc * R + r) * D + 4 * q);
-    const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + (pc * R + r) * 2);
-    mv[j] = c < n_chunks ? ml.x : -INFINITY;
-    lv[j] = ml.y;
+    const bool ok = cl + NL * j < n_chunks;
+    mv[j] = ok ? mlv[j].x : -INFINITY;
+    lv[j] = ok ? mlv[j].y : 0.0f;
+    ov[j] = ok ? ov[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
   float m = -INFINITY;
 #pragma unroll
@@ -1245,18 +1254,18 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   const int64_t plan_base = static_cast<int64_t>(g) * a.plan_stride;
   const int slot_last = static_cast<int>(a.plan_stride - 1);
   const int per_chunk = NW * TW * a.iters;
-  int page[TW];
-  uint32_t pmask[TW];
-  auto load_slots = [&](int t0) {
+  int page[TW], page_nx[TW];
+  uint32_t pmask[TW], pmask_nx[TW];
+  auto load_slots = [&](int t0, int (&pg)[TW], uint32_t (&pm)[TW]) {
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
       int u = t0 + tt - a.t_sink_tiles;
       u = u < 0 ? 0 : (u > slot_last ? slot_last : u);
-      page[tt] = a.plan_pages[plan_base + u];
-      pmask[tt] = a.plan_masks != nullptr ? static_cast<uint32_t>(a.plan_masks[plan_base + u]) : 0xffu;
+      pg[tt] = a.plan_pages[plan_base + u];
+      pm[tt] = a.plan_masks != nullptr ? static_cast<uint32_t>(a.plan_masks[plan_base + u]) : 0xffu;
     }
   };
-  load_slots((chunk * a.iters * NW + wave) * TW);
+  load_slots((chunk * a.iters * NW + wave) * TW, page, pmask);
   uint4 qf[4];
   {
     const S* qh = static_cast<const S*>(a.q) + (static_cast<int64_t>(g) * R + (krow < R ? krow : 0)) * D + 8 * quarter;
@@ -1308,7 +1317,13 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
 
   for (int it = 0; it < a.iters; ++it) {
     const int t0 = ((chunk * a.iters + it) * NW + wave) * TW;
-    if (it > 0) load_slots(t0);
+    if (it > 0) {
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt) {
+        page[tt] = page_nx[tt];
+        pmask[tt] = pmask_nx[tt];
+      }
+    }
     if (t0 >= n_tiles) break;
     // ---- round trip 2: K fragments and V rows of the batch ----
     TileSrc ts[TW];
@@ -1347,6 +1362,8 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
         vf[tt][j] = NT ? load_stream(vp + c8) : *reinterpret_cast<const uint4*>(vp + c8);
       }
     }
+    // the next batch's page slots ride in the same round trip
+    if (it + 1 < a.iters) load_slots(t0 + NW * TW, page_nx, pmask_nx);
     // ---- q.k on the matrix cores; scores in log2 units ----
     float sc[TW][4];
 #pragma unroll

@@ -115,19 +115,58 @@ struct ScoreArgs {
 };
 
 
-// Stage a tile of pages (min then max) into LDS with a padded pitch.
+// Stage a tile of pages (min then max) into LDS with a padded pitch, and the
+// group's queries to q_lds.  On the vector path every global load of the
+// tile is issued before the first LDS store, so a block waits for one memory
+// round trip rather than one per loop trip.
 template <typename DT>
-__device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, int np, uint8_t* lds, int pitch) {
+__device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, int np, uint8_t* lds, int pitch,
+                                           float* q_lds) {
   using S = typename DT::storage;
   const int row_bytes = a.D * static_cast<int>(sizeof(S));
   const int words = row_bytes / 4;  // D even -> row_bytes % 4 == 0
   const S* mn = static_cast<const S*>(a.pmin) + g * a.group_stride + static_cast<int64_t>(p0) * a.D;
   const S* mx = static_cast<const S*>(a.pmax) + g * a.group_stride + static_cast<int64_t>(p0) * a.D;
+  const float* qg = a.q + static_cast<int64_t>(g) * a.R * a.D;
+  const int nq = a.R * a.D;
+  const int nthreads = static_cast<int>(blockDim.x);
+  const int tid = static_cast<int>(threadIdx.x);
   const bool vec4 =
       (words % 4) == 0 && ((reinterpret_cast<uintptr_t>(mn) | reinterpret_cast<uintptr_t>(mx)) % 16) == 0;
   if (vec4) {
+    constexpr int kPer = 8;  // 16-byte loads per thread: 64 pages x 2 x 256 B over 512 threads is 4
     const int quads = words / 4;
-    for (int i = threadIdx.x; i < 2 * np * quads; i += blockDim.x) {
+    const int total = 2 * np * quads;
+    if (total <= kPer * nthreads) {
+      uint4 v[kPer];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int i = tid + j * nthreads;
+        if (i < total) {
+          const int which = i / (np * quads);
+          const int rem = i - which * np * quads;
+          v[j] = load_stream(reinterpret_cast<const uint4*>(which ? mx : mn) + rem);
+        }
+      }
+      for (int i = tid; i < nq; i += nthreads) q_lds[i] = qg[i];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int i = tid + j * nthreads;
+        if (i < total) {
+          const int which = i / (np * quads);
+          const int rem = i - which * np * quads;
+          const int page = rem / quads;
+          const int qd = rem - page * quads;
+          *reinterpret_cast<uint4*>(lds + (which * kTilePages + page) * pitch + qd * 16) = v[j];
+        }
+      }
+      return;
+    }
+  }
+  for (int i = tid; i < nq; i += nthreads) q_lds[i] = qg[i];
+  if (vec4) {
+    const int quads = words / 4;
+    for (int i = tid; i < 2 * np * quads; i += nthreads) {
       const int which = i / (np * quads);
       const int rem = i - which * np * quads;
       const int page = rem / quads;
@@ -138,7 +177,7 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
     }
   } else {
     const int total = 2 * np * words;
-    for (int i = threadIdx.x; i < total; i += blockDim.x) {
+    for (int i = tid; i < total; i += nthreads) {
       const int which = i / (np * words);
       const int rem = i - which * np * words;
       const int page = rem / words;
@@ -154,17 +193,20 @@ template <typename DT, int DFIX>
 __device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
   using S = typename DT::storage;
   const int p0 = tile * kTilePages;
-  const int P = a.lengths != nullptr ? ragged_pages(a.lengths[g], a.sink, a.recent, a.bs, a.P) : a.P;
+  if (p0 >= a.P) return;  // block-uniform
+  // A ragged group's length is read in the same round trip as the tile: the
+  // tile is staged up to the buffer's P pages (in bounds), and only the
+  // scores of the group's own pages are written.
+  // (an unconditional load: without lengths it reads the first query word
+  // and ignores it)
+  const int length = *(a.lengths != nullptr ? a.lengths + g : reinterpret_cast<const int32_t*>(a.q));
+  const int np_cap = (a.P - p0) < kTilePages ? (a.P - p0) : kTilePages;
+  const int pitch = a.D * static_cast<int>(sizeof(S)) + 16;  // 16-byte aligned rows, padded
+  float* q_lds = reinterpret_cast<float*>(lds + 2 * kTilePages * pitch);
+  stage_tile<DT>(a, g, p0, np_cap, lds, pitch, q_lds);
+  const int P = a.lengths != nullptr ? ragged_pages(length, a.sink, a.recent, a.bs, a.P) : a.P;
   if (p0 >= P) return;  // block-uniform
   const int np = (P - p0) < kTilePages ? (P - p0) : kTilePages;
-  const int pitch = a.D * static_cast<int>(sizeof(S)) + 16;  // 16-byte aligned rows, padded
-  // The group's queries go to LDS in the same round trip as the tile.
-  float* q_lds = reinterpret_cast<float*>(lds + 2 * kTilePages * pitch);
-  {
-    const float* qg = a.q + static_cast<int64_t>(g) * a.R * a.D;
-    for (int i = threadIdx.x; i < a.R * a.D; i += blockDim.x) q_lds[i] = qg[i];
-  }
-  stage_tile<DT>(a, g, p0, np, lds, pitch);
   __syncthreads();
   const int es = static_cast<int>(sizeof(S));
   const int wave = wave_uniform(static_cast<int>(threadIdx.x) / kWave);
@@ -357,8 +399,9 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
   extern __shared__ __align__(16) uint8_t dyn[];  // union scratch
   const int row = blockIdx.x;
   const int g = row / s.R;
-  const int P = s.lengths != nullptr ? ragged_pages(s.lengths[g], s.sink, s.recent, s.bs, s.P) : s.P;
-  const int k = s.k < P ? s.k : P;
+  // unconditional length load (the first score word when not ragged; relaxed
+  // atomic so that it is not sunk into a branch), overlapping the key loads
+  const int length = fetch_i32(s.lengths != nullptr ? s.lengths + g : reinterpret_cast<const int32_t*>(s.scores));
   const float* vals = s.scores + static_cast<int64_t>(row) * s.score_stride;
   // ---- keys: one batched round trip ----
   uint32_t key[KPT];
@@ -379,13 +422,17 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
         key[4 * q4 + 3] = score_key(v.w);
       }
     } else {
+      // (clamped to the buffer's P: keys past a ragged row's end are never
+      // candidates)
 #pragma unroll
       for (int j = 0; j < KPT; ++j) {
         const int i = i0 + j;
-        key[j] = score_key(vals[i < P ? i : (P > 0 ? P - 1 : 0)]);
+        key[j] = score_key(vals[i < s.P ? i : s.P - 1]);
       }
     }
   }
+  const int P = s.lengths != nullptr ? ragged_pages(length, s.sink, s.recent, s.bs, s.P) : s.P;
+  const int k = s.k < P ? s.k : P;
   int32_t* ws_row = s.sel_ws != nullptr ? s.sel_ws + static_cast<int64_t>(row) * s.k : nullptr;
   int32_t* out32 = s.sel_out != nullptr ? s.sel_out + static_cast<int64_t>(row) * s.k : nullptr;
   int64_t* out64 = s.sel_out64 != nullptr ? s.sel_out64 + static_cast<int64_t>(row) * s.k : nullptr;

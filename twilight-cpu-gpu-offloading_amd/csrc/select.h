@@ -30,6 +30,7 @@ struct SelShared {
   uint32_t red_max[kWaves];
   uint32_t red_min[kWaves];
   int scan[kWaves];
+  unsigned long long tmask;
   int bnd;
   uint32_t bnd_above;
   uint32_t bnd_count;
@@ -87,7 +88,9 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
   for (int j = 0; j < KPT; ++j) cand |= (i0 + j < P) ? (1u << j) : 0u;
   uint32_t need = static_cast<uint32_t>(k);
   uint32_t ccount = static_cast<uint32_t>(P);
-  int mode = 0;  // 0: take every candidate, 1: exact rank, 2: equal keys by index
+  // 0: take every candidate, 1: exact rank, 2: equal keys, lowest indices
+  int mode = 0;
+  uint4* hist4 = reinterpret_cast<uint4*>(sh.hist);
   for (int level = 0;; ++level) {
     if (ccount == need) break;
     // after a pass, few candidates go straight to the exact rank (it orders
@@ -109,6 +112,9 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
       sh.red_max[wave] = cmax;
       sh.red_min[wave] = cmin;
     }
+    // the histogram is cleared in the same barrier interval: the previous
+    // pass's reads of it ended at its last barrier
+    for (int b = tid; b < (kLinBins + 64) / 4; b += kBlock) hist4[b] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
@@ -135,18 +141,30 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
                 range > 0.0f && __builtin_isfinite(fn.scale);
     const int hi = 31 - __clz(static_cast<int>(cmax ^ cmin));
     fn.shift = hi >= 7 ? hi - 7 : 0;
-    const int nb = fn.linear ? kLinBins : 256;
-    const int bpt = nb / kBlock;  // bins owned by a thread
-    for (int b = tid; b < (kLinBins + 64) / 4; b += kBlock)
-      reinterpret_cast<uint4*>(sh.hist)[b] = make_uint4(0u, 0u, 0u, 0u);
-    __syncthreads();
+    int bin[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      if ((cand >> j) & 1u) atomicAdd(&sh.hist[fn(key[j])], 1u);
+      bin[j] = fn(key[j]);
+      if ((cand >> j) & 1u) atomicAdd(&sh.hist[bin[j]], 1u);
     }
     __syncthreads();
+    // thread t owns bins 8t .. 8t + 7 (linear) or bin t (digit)
+    constexpr int kBpt = kLinBins / kBlock;
+    static_assert(kBpt == 8, "two 16-byte histogram reads per thread");
+    uint32_t hv[kBpt];
+    if (fn.linear) {
+      const uint4 h0 = hist4[2 * tid];
+      const uint4 h1 = hist4[2 * tid + 1];
+      hv[0] = h0.x; hv[1] = h0.y; hv[2] = h0.z; hv[3] = h0.w;
+      hv[4] = h1.x; hv[5] = h1.y; hv[6] = h1.z; hv[7] = h1.w;
+    } else {
+      hv[0] = sh.hist[tid];
+#pragma unroll
+      for (int b = 1; b < kBpt; ++b) hv[b] = 0u;
+    }
     uint32_t tot = 0u;
-    for (int b = 0; b < bpt; ++b) tot += sh.hist[bpt * tid + b];
+#pragma unroll
+    for (int b = 0; b < kBpt; ++b) tot += hv[b];
     // suffix sums over threads (bins descending)
     const uint32_t wincl = wave_suffix_sum_u32(tot);
     if (lane == 0) sh.scan[wave] = static_cast<int>(wincl);
@@ -156,18 +174,18 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
     for (int w = 0; w < kWaves; ++w) incl += w > wave ? static_cast<uint32_t>(sh.scan[w]) : 0u;
     if (incl - tot < need && need <= incl) {
       uint32_t acc = incl - tot;
-      int bin = bpt * tid;
+      int bsel = 0;
       uint32_t cnt = 0u;
-      for (int b = bpt - 1; b >= 0; --b) {
-        const uint32_t c = sh.hist[bpt * tid + b];
-        if (need <= acc + c) {
-          bin = bpt * tid + b;
-          cnt = c;
-          break;
-        }
-        acc += c;
+      bool found = false;
+#pragma unroll
+      for (int b = kBpt - 1; b >= 0; --b) {
+        const bool hit = !found && need <= acc + hv[b];
+        bsel = hit ? b : bsel;
+        cnt = hit ? hv[b] : cnt;
+        acc += (found || hit) ? 0u : hv[b];
+        found = found || hit;
       }
-      sh.bnd = bin;
+      sh.bnd = fn.linear ? kBpt * tid + bsel : tid;
       sh.bnd_above = acc;
       sh.bnd_count = cnt;
     }
@@ -178,18 +196,16 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
       const bool c = (cand >> j) & 1u;
-      const int b = fn(key[j]);
-      taken |= (c && b > bnd) ? (1u << j) : 0u;
-      cand &= (c && b == bnd) ? 0xffffffffu : ~(1u << j);
+      taken |= (c && bin[j] > bnd) ? (1u << j) : 0u;
+      cand &= (c && bin[j] == bnd) ? 0xffffffffu : ~(1u << j);
     }
   }
   int total;
-  if (mode == 1) {
+  if (mode == 1 && ccount > static_cast<uint32_t>(kWave)) {
     // exact rank of at most kBlock candidates; slot t's rank goes to
     // selbits[t] and back to the thread that owns slot t
     static_assert(kMaxSelPages / 32 >= kBlock, "one rank per candidate slot");
-    const int mine = __popc(cand);
-    const int first = block_excl_scan(mine, sh.scan, &total);
+    const int first = block_excl_scan(__popc(cand), sh.scan, &total);
     int slot = first;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
@@ -220,22 +236,58 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
         ++slot;
       }
     }
-  } else if (mode == 2) {
-    int before = block_excl_scan(__popc(cand), sh.scan, &total);
+    cand = 0u;
+    mode = 0;
+  }
+  if (mode == 0) {
+    taken |= cand;
+    cand = 0u;
+  }
+  // One scan gives both the taken keys (low half) and the candidates (high
+  // half) in earlier threads; candidate c (in index order) is taken when
+  // its rank is below need (mode 1: tmask bit c) or c < need (mode 2).
+  const int pre = block_excl_scan(__popc(taken) | (__popc(cand) << 16), sh.scan, &total);
+  const int a_before = pre & 0xffff;
+  const int c_before = pre >> 16;
+  uint64_t tmask = 0ull;
+  if (mode == 1) {
+    // at most one wavefront of candidates: staged in index order, ranked by
+    // (key desc, index asc) in wavefront 0
+    int slot = c_before;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      if ((cand >> j) & 1u) {
-        taken |= (static_cast<uint32_t>(before) < need) ? (1u << j) : 0u;
-        ++before;
-      }
+      if ((cand >> j) & 1u) sh.ckey[slot++] = key[j];
     }
-  } else {
-    taken |= cand;
+    __syncthreads();
+    if (wave == 0) {
+      const int n = static_cast<int>(ccount);
+      const uint32_t mk = lane < n ? sh.ckey[lane] : 0u;
+      uint32_t rank = 0u;
+      for (int m = 0; m < n; ++m) {
+        const uint32_t km = readlane_u32(mk, m);
+        rank += (km > mk || (km == mk && m < lane)) ? 1u : 0u;
+      }
+      const uint64_t t = __ballot(lane < n && rank < need);
+      if (lane == 0) sh.tmask = t;
+    }
+    __syncthreads();
+    tmask = sh.tmask;
   }
-  int slot = block_excl_scan(__popc(taken), sh.scan, &total);
+  int out = a_before;
+  if (mode == 1) {
+    out += c_before > 0 ? __popcll(tmask & (~0ull >> (64 - c_before))) : 0;
+  } else {
+    out += c_before < static_cast<int>(need) ? c_before : static_cast<int>(need);
+  }
+  int cpos = c_before;
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
-    if ((taken >> j) & 1u) emit(slot++, i0 + j);
+    bool take = (taken >> j) & 1u;
+    if ((cand >> j) & 1u) {
+      take = mode == 1 ? ((tmask >> cpos) & 1ull) != 0ull : cpos < static_cast<int>(need);
+      ++cpos;
+    }
+    if (take) emit(out++, i0 + j);
   }
 }
 
