@@ -44,6 +44,7 @@ namespace {
 using namespace sel;
 
 constexpr int kTilePages = 64;
+constexpr int kScoreBlock = 512;  // score kernel: 8 wavefronts, two per head
 constexpr int kMaxD = 256;
 
 // ------------------------------------------------------------------ scores
@@ -129,7 +130,7 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
   const S* mx = static_cast<const S*>(a.pmax) + g * a.group_stride + static_cast<int64_t>(p0) * a.D;
   const float* qg = a.q + static_cast<int64_t>(g) * a.R * a.D;
   const int nq = a.R * a.D;
-  const int nthreads = static_cast<int>(blockDim.x);
+  constexpr int nthreads = kScoreBlock;
   const int tid = static_cast<int>(threadIdx.x);
   const bool vec4 =
       (words % 4) == 0 && ((reinterpret_cast<uintptr_t>(mn) | reinterpret_cast<uintptr_t>(mx)) % 16) == 0;
@@ -188,6 +189,116 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
   }
 }
 
+// Scores of one tile for D = DFIX and at most 4 heads, in two phases:
+// channels [0, DFIX/2) of every page are stored and scored while the loads
+// of channels [DFIX/2, DFIX) are still in flight.  Each accumulator takes
+// its 32-channel chunks in the same order as the one-phase path (c = 0, 1
+// here, then c = 2, 3), so the scores are identical.
+template <typename DT, int DFIX>
+__device__ void score_tile_split(const ScoreArgs& a, int g, int p0, int np_cap, int length, uint8_t* lds) {
+  using S = typename DT::storage;
+  constexpr int es = static_cast<int>(sizeof(S));
+  constexpr int kQuads = DFIX * es / 16;  // 16-byte quads per row
+  constexpr int kHq = kQuads / 2;
+  constexpr int kPerHalf = (2 * kTilePages * kHq + kScoreBlock - 1) / kScoreBlock;
+  constexpr int kChunks = DFIX / 32;
+  constexpr int pitch = DFIX * es + 16;
+  static_assert(4 * DFIX <= kScoreBlock, "one query value per thread");
+  static_assert(kChunks % 2 == 0 && kHq * 16 == (DFIX / 2) * es, "channel halves are whole chunks and quads");
+  const int tid = static_cast<int>(threadIdx.x);
+  const S* mn = static_cast<const S*>(a.pmin) + g * a.group_stride + static_cast<int64_t>(p0) * DFIX;
+  const S* mx = static_cast<const S*>(a.pmax) + g * a.group_stride + static_cast<int64_t>(p0) * DFIX;
+  float* q_lds = reinterpret_cast<float*>(lds + 2 * kTilePages * pitch);
+  // Loads are unconditional (indices clamped into the tile), so they issue
+  // back to back and each store waits only for its own load.
+  const int nq = a.R * DFIX;
+  const float qv0 = a.q[static_cast<int64_t>(g) * a.R * DFIX + (tid < nq ? tid : nq - 1)];
+  const int total_h = 2 * np_cap * kHq;
+  uint4 va[kPerHalf], vb[kPerHalf];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int j = 0; j < kPerHalf; ++j) {
+      int i = tid + j * kScoreBlock;
+      i = i < total_h ? i : total_h - 1;
+      const bool which = i >= np_cap * kHq;
+      const int rem = i - (which ? np_cap * kHq : 0);
+      const int page = rem / kHq;
+      const int qd = rem % kHq + h * kHq;
+      const uint4 v = load_stream(reinterpret_cast<const uint4*>(which ? mx : mn) + page * kQuads + qd);
+      if (h == 0) va[j] = v; else vb[j] = v;
+    }
+    // the first half's loads go out first (and so arrive first)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  auto store_half = [&](int h, const uint4 (&v)[kPerHalf]) {
+#pragma unroll
+    for (int j = 0; j < kPerHalf; ++j) {
+      // clamped like the loads: a thread past the tile stores the last
+      // quad's value to the last quad's place again
+      int i = tid + j * kScoreBlock;
+      i = i < total_h ? i : total_h - 1;
+      const bool which = i >= np_cap * kHq;
+      const int rem = i - (which ? np_cap * kHq : 0);
+      const int page = rem / kHq;
+      const int qd = rem % kHq + h * kHq;
+      *reinterpret_cast<uint4*>(lds + ((which ? kTilePages : 0) + page) * pitch + qd * 16) = v[j];
+    }
+  };
+  // (unconditional, so the query load is not sunk behind the tile loads;
+  // threads past R*D repeat the last value)
+  q_lds[tid < nq ? tid : nq - 1] = qv0;
+  store_half(0, va);
+  const int P = a.lengths != nullptr ? ragged_pages(length, a.sink, a.recent, a.bs, a.P) : a.P;
+  if (p0 >= P) return;  // block-uniform
+  const int np = (P - p0) < kTilePages ? (P - p0) : kTilePages;
+  __syncthreads();
+  const int wave = wave_uniform(tid / kWave);
+  const int lane = lane_id();
+  const int half = wave / 4;
+  const int r = wave % 4;
+  const bool active = r < a.R;
+  const float* qh = q_lds + r * DFIX;
+  const uint8_t* min_row = lds + lane * pitch;
+  const uint8_t* max_row = lds + (kTilePages + lane) * pitch;
+  float acc[16];
+#pragma unroll
+  for (int l = 0; l < 16; ++l) acc[l] = 0.0f;
+  auto chunks = [&](int c_begin, int c_end) {
+#pragma unroll
+    for (int c = c_begin; c < c_end; ++c) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int d0 = 32 * c + 16 * half + 8 * e;
+        float qv[8], x[8];
+        *reinterpret_cast<float4*>(qv) = *reinterpret_cast<const float4*>(qh + d0);
+        *reinterpret_cast<float4*>(qv + 4) = *reinterpret_cast<const float4*>(qh + d0 + 4);
+        select8(min_row + d0 * es, max_row + d0 * es, qv, x, DT{});
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[8 * e + i] = acc[8 * e + i] + x[i] * qv[i];
+      }
+    }
+  };
+  if (active) chunks(0, kChunks / 2);
+  store_half(1, vb);
+  __syncthreads();
+  if (active) chunks(kChunks / 2, kChunks);
+#pragma unroll
+  for (int w = 1; w < 16; w <<= 1) {
+#pragma unroll
+    for (int l = 0; l < 16; l += 2 * w) acc[l] = acc[l] + acc[l + w];
+  }
+  __shared__ float s_half[4][kWave];
+  if (half == 1) s_half[r][lane] = acc[0];
+  __syncthreads();
+  if (half == 0 && active && lane < np) {
+    const float sc = acc[0] + s_half[r][lane];
+    const int64_t row = static_cast<int64_t>(g) * a.R + r;
+    a.scores[row * a.score_stride + p0 + lane] = sc;
+    if (a.scores_out != nullptr) a.scores_out[row * a.P + p0 + lane] = sc;
+  }
+}
+
 // Scores of one tile of kTilePages pages of group g for all R heads.
 template <typename DT, int DFIX>
 __device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
@@ -201,6 +312,14 @@ __device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
   // and ignores it)
   const int length = *(a.lengths != nullptr ? a.lengths + g : reinterpret_cast<const int32_t*>(a.q));
   const int np_cap = (a.P - p0) < kTilePages ? (a.P - p0) : kTilePages;
+  if constexpr (DFIX > 0) {
+    const uintptr_t base = reinterpret_cast<uintptr_t>(static_cast<const S*>(a.pmin) + g * a.group_stride) |
+                           reinterpret_cast<uintptr_t>(static_cast<const S*>(a.pmax) + g * a.group_stride);
+    if (a.R <= 4 && (base % 16) == 0) {
+      score_tile_split<DT, DFIX>(a, g, p0, np_cap, length, lds);
+      return;
+    }
+  }
   const int pitch = a.D * static_cast<int>(sizeof(S)) + 16;  // 16-byte aligned rows, padded
   float* q_lds = reinterpret_cast<float*>(lds + 2 * kTilePages * pitch);
   stage_tile<DT>(a, g, p0, np_cap, lds, pitch, q_lds);
@@ -276,8 +395,6 @@ __device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
     __syncthreads();
   }
 }
-
-constexpr int kScoreBlock = 512;  // 8 wavefronts: two per head
 
 template <typename DT, int DFIX>
 __global__ __launch_bounds__(kScoreBlock) void quest_score_kernel(ScoreArgs a) {
@@ -437,11 +554,37 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
   int32_t* out32 = s.sel_out != nullptr ? s.sel_out + static_cast<int64_t>(row) * s.k : nullptr;
   int64_t* out64 = s.sel_out64 != nullptr ? s.sel_out64 + static_cast<int64_t>(row) * s.k : nullptr;
   if (k > 0) {
-    block_topk<KPT>(key, P, k, sh, [&](int slot, int idx) {
-      if (ws_row != nullptr) publish_i32(ws_row + slot, idx);
-      if (out32 != nullptr) out32[slot] = idx;
-      if (out64 != nullptr) out64[slot] = idx;
-    });
+    uint32_t take;
+    int slot;
+    block_topk<KPT>(key, P, k, sh, &take, &slot);
+    const int i0 = KPT * static_cast<int>(threadIdx.x);
+    constexpr int kStage = kLinBins + 64;
+    if (k <= kStage) {
+      // the selection goes through LDS (the histogram is free now) and out
+      // with coalesced stores
+      int32_t* st = reinterpret_cast<int32_t*>(sh.hist);
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        if ((take >> j) & 1u) st[slot++] = i0 + j;
+      }
+      __syncthreads();
+      for (int i = threadIdx.x; i < k; i += kBlock) {
+        const int idx = st[i];
+        if (ws_row != nullptr) publish_i32(ws_row + i, idx);
+        if (out32 != nullptr) out32[i] = idx;
+        if (out64 != nullptr) out64[i] = idx;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        if ((take >> j) & 1u) {
+          if (ws_row != nullptr) publish_i32(ws_row + slot, i0 + j);
+          if (out32 != nullptr) out32[slot] = i0 + j;
+          if (out64 != nullptr) out64[slot] = i0 + j;
+          ++slot;
+        }
+      }
+    }
   }
   for (int slot = k + static_cast<int>(threadIdx.x); slot < s.k; slot += kBlock) {
     if (out32 != nullptr) out32[slot] = -1;

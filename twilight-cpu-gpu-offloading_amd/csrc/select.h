@@ -75,10 +75,11 @@ struct BinFn {
 };
 
 // Top-k of one row held as KPT contiguous keys per thread (indices
-// KPT*t .. KPT*t + KPT - 1).  emit(slot, index) is called once per selected
-// index, slot = rank in ascending index order.
-template <int KPT, typename Emit>
-__device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& sh, Emit emit) {
+// KPT*t .. KPT*t + KPT - 1).  On return, bit j of *take marks index
+// KPT*t + j as selected, and *first is the rank (in ascending index order)
+// of this thread's first selected index among all selected ones.
+template <int KPT>
+__device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& sh, uint32_t* take, int* first) {
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid / kWave;
@@ -282,13 +283,13 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
   int cpos = c_before;
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
-    bool take = (taken >> j) & 1u;
-    if ((cand >> j) & 1u) {
-      take = mode == 1 ? ((tmask >> cpos) & 1ull) != 0ull : cpos < static_cast<int>(need);
-      ++cpos;
-    }
-    if (take) emit(out++, i0 + j);
+    const bool c = (cand >> j) & 1u;
+    const bool t = mode == 1 ? ((tmask >> cpos) & 1ull) != 0ull : cpos < static_cast<int>(need);
+    taken |= (c && t) ? (1u << j) : 0u;
+    cpos += c ? 1 : 0;
   }
+  *take = taken;
+  *first = out;
 }
 
 // Candidate pages of a group with `length` tokens: the whole pages between

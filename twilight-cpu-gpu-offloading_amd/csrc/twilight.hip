@@ -888,9 +888,9 @@ __global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) 
   int k = sh.ires[1];
   k = k < 1 ? 1 : (k > N ? N : k);
   if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = k;
-  const int i0 = KPT * static_cast<int>(threadIdx.x);
   uint32_t taken = 0u;
-  block_topk<KPT>(key, N, k, sh.sel, [&](int, int idx) { taken |= 1u << (idx - i0); });
+  int first_slot;  // (the selection is published as a bitmap)
+  block_topk<KPT>(key, N, k, sh.sel, &taken, &first_slot);
   publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
   build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan);
