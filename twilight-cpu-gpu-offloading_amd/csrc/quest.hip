@@ -437,6 +437,11 @@ __device__ void write_union_plan(const SelectArgs& s, int g, int P, const uint8_
                                  uint8_t* umask, int* scan) {
   const int tid = threadIdx.x;
   const uint8_t all = static_cast<uint8_t>((1u << s.R) - 1u);
+  // Without a row plan (rows, row counts) the union goes straight to the
+  // page plan in global memory; the row plan reads it back from LDS.
+  const bool direct = s.rows == nullptr && s.row_counts == nullptr;
+  int32_t* pp = s.plan_pages != nullptr ? s.plan_pages + static_cast<int64_t>(g) * s.plan_stride : nullptr;
+  uint8_t* pm = s.plan_masks != nullptr ? s.plan_masks + static_cast<int64_t>(g) * s.plan_stride : nullptr;
   int nu = 0;
   for (int base = 0; base < P; base += kBlock * 8) {
     const int p0 = base + 8 * tid;
@@ -451,23 +456,27 @@ __device__ void write_union_plan(const SelectArgs& s, int g, int P, const uint8_
     for (int b = 0; b < 8; ++b) {
       const uint32_t m = ((b < 4 ? w.x : w.y) >> (8 * (b & 3))) & 255u;
       if (m != 0u) {
-        upage[slot] = p0 + b;
-        umask[slot] = static_cast<uint8_t>(m);
+        if (direct) {
+          if (pp != nullptr) pp[slot] = p0 + b;
+          if (pm != nullptr) pm[slot] = static_cast<uint8_t>(m);
+        } else {
+          upage[slot] = p0 + b;
+          umask[slot] = static_cast<uint8_t>(m);
+        }
         ++slot;
       }
     }
     nu += total;
   }
+  if (tid == 0 && s.plan_counts != nullptr) s.plan_counts[g] = nu;
+  if (direct) return;
   __syncthreads();
-  if (s.plan_pages != nullptr) {
-    int32_t* pp = s.plan_pages + static_cast<int64_t>(g) * s.plan_stride;
-    uint8_t* pm = s.plan_masks != nullptr ? s.plan_masks + static_cast<int64_t>(g) * s.plan_stride : nullptr;
+  if (pp != nullptr) {
     for (int i = tid; i < nu; i += kBlock) {
       pp[i] = upage[i];
       if (pm != nullptr) pm[i] = umask[i];
     }
   }
-  if (tid == 0 && s.plan_counts != nullptr) s.plan_counts[g] = nu;
   const int length = s.length;
   const int bs = s.bs;
   const int sink_end = s.sink < length ? s.sink : length;
@@ -598,11 +607,34 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
   uint8_t* page_mask = dyn;
   int32_t* upage = reinterpret_cast<int32_t*>(dyn + mask_bytes);
   uint8_t* umask = reinterpret_cast<uint8_t*>(upage + P);
-  for (int i = threadIdx.x; i < mask_bytes / 4; i += kBlock) reinterpret_cast<uint32_t*>(page_mask)[i] = 0u;
-  __syncthreads();
   const int32_t* sel_g = s.sel_ws + static_cast<int64_t>(g) * s.R * s.k;
   const int n_sel = s.R * k;
-  for (int i = threadIdx.x; i < n_sel; i += kBlock) {
+  // the first kPre selections per thread are fetched before the mask is
+  // cleared (one round trip, overlapping the clear and its barrier)
+  constexpr int kPre = 4;
+  int pre[kPre];
+  if (n_sel > 0) {
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      int i = static_cast<int>(threadIdx.x) + u * kBlock;
+      i = i < n_sel ? i : n_sel - 1;
+      const int hr = i / k;
+      pre[u] = fetch_i32(sel_g + hr * s.k + (i - hr * k));
+    }
+  }
+  for (int i = threadIdx.x; i < mask_bytes / 4; i += kBlock) reinterpret_cast<uint32_t*>(page_mask)[i] = 0u;
+  __syncthreads();
+  if (n_sel > 0) {
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      const int i = static_cast<int>(threadIdx.x) + u * kBlock;
+      if (i < n_sel) {
+        const int hr = i / k;
+        atomicOr(reinterpret_cast<uint32_t*>(page_mask) + (pre[u] >> 2), (1u << hr) << (8 * (pre[u] & 3)));
+      }
+    }
+  }
+  for (int i = static_cast<int>(threadIdx.x) + kPre * kBlock; i < n_sel; i += kBlock) {
     const int hr = i / k;
     const int id = fetch_i32(sel_g + hr * s.k + (i - hr * k));
     atomicOr(reinterpret_cast<uint32_t*>(page_mask) + (id >> 2), (1u << hr) << (8 * (id & 3)));
