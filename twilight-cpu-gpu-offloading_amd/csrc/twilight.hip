@@ -323,7 +323,7 @@ __device__ __forceinline__ int group_candidates(const SelectArgs& s, int g) {
 
 struct TopShared {
   SelShared sel;
-  unsigned long long bin_mass[kLinBins + 64];
+  __align__(16) unsigned long long bin_mass[kLinBins + 64];
   unsigned long long red64[kWaves];
   unsigned long long cmass[kBlock];
   float fred[kWaves];
@@ -384,6 +384,61 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
   int count = 0;  // keys taken so far (block-uniform)
   int ccount = N;
   for (int level = 0;; ++level) {
+    if (ccount <= kWave) {
+      // exact, one wavefront: the candidates are staged in index order, lane
+      // c ranks candidate c (key desc, index asc) and sums the masses ahead
+      // of it with register reads; the boundary is the lane whose own mass
+      // crosses need
+      int total;
+      const int first = block_excl_scan(__popc(cand), sh.sel.scan, &total);
+      int slot = first;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        if ((cand >> j) & 1u) {
+          sh.sel.ckey[slot] = key[j];
+          sh.cmass[slot] = mass[j];
+          ++slot;
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+        const bool live = lane < total;
+        const uint32_t mk = live ? sh.sel.ckey[lane] : 0u;
+        const uint64_t mm = live ? sh.cmass[lane] : 0ull;
+        const uint32_t mlo = static_cast<uint32_t>(mm), mhi = static_cast<uint32_t>(mm >> 32);
+        uint64_t before = 0;
+        int rank = 0;
+        for (int m = 0; m < total; ++m) {
+          const uint32_t km = readlane_u32(mk, m);
+          const uint64_t am = (static_cast<uint64_t>(readlane_u32(mhi, m)) << 32) | readlane_u32(mlo, m);
+          const bool ahead = km > mk || (km == mk && m < lane);
+          before += ahead ? am : 0ull;
+          rank += ahead ? 1 : 0;
+        }
+        const bool cross = live && before < need && need <= before + mm;
+        const uint64_t cb = __ballot(cross);
+        // default: every candidate (their masses fall short of need)
+        const int needed = cb != 0ull ? static_cast<int>(readlane_u32(static_cast<uint32_t>(rank), first_lane(cb))) + 1
+                                      : total;
+        const uint64_t tm = __ballot(live && rank < needed);
+        if (lane == 0) {
+          sh.sel.tmask = tm;
+          sh.ires[0] = needed;
+        }
+      }
+      __syncthreads();
+      const uint64_t tm = sh.sel.tmask;
+      const int needed = sh.ires[0];
+      int cpos = first;
+#pragma unroll
+      for (int j = 0; j < KPT; ++j) {
+        const bool c = (cand >> j) & 1u;
+        taken |= (c && ((tm >> cpos) & 1ull)) ? (1u << j) : 0u;
+        cpos += c ? 1 : 0;
+      }
+      count += needed;
+      break;
+    }
     if (ccount <= kBlock) {
       // exact: rank the candidates (key desc, index asc) and walk their
       // masses in rank order; slot t's rank goes to sel.selbits[t]
@@ -487,8 +542,6 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
                 range > 0.0f && __builtin_isfinite(fn.scale);
     const int hi = 31 - __clz(static_cast<int>(cmax ^ cmin));
     fn.shift = hi >= 7 ? hi - 7 : 0;
-    const int nb = fn.linear ? kLinBins : 256;
-    const int bpt = nb / kBlock;
     if (level > 0) {
       for (int b = tid; b < kLinBins + 64; b += kBlock) {
         sh.sel.hist[b] = 0u;
@@ -496,20 +549,48 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
       }
       __syncthreads();
     }
+    int bin[KPT];
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
+      bin[j] = fn(key[j]);
       if ((cand >> j) & 1u) {
-        const int b = fn(key[j]);
-        atomicAdd(&sh.sel.hist[b], 1u);
-        if (mass[j] != 0) atomicAdd(&sh.bin_mass[b], static_cast<unsigned long long>(mass[j]));
+        atomicAdd(&sh.sel.hist[bin[j]], 1u);
+        if (mass[j] != 0) atomicAdd(&sh.bin_mass[bin[j]], static_cast<unsigned long long>(mass[j]));
       }
     }
     __syncthreads();
+    // thread t owns bins 8t .. 8t + 7 (linear) or bin t (digit), read once
+    // into registers
+    constexpr int kBpt = kLinBins / kBlock;
+    static_assert(kBpt == 8, "eight bins per thread");
+    uint32_t hc[kBpt];
+    uint64_t hm[kBpt];
+    if (fn.linear) {
+      const uint4 c0 = reinterpret_cast<const uint4*>(sh.sel.hist)[2 * tid];
+      const uint4 c1 = reinterpret_cast<const uint4*>(sh.sel.hist)[2 * tid + 1];
+      hc[0] = c0.x; hc[1] = c0.y; hc[2] = c0.z; hc[3] = c0.w;
+      hc[4] = c1.x; hc[5] = c1.y; hc[6] = c1.z; hc[7] = c1.w;
+#pragma unroll
+      for (int q = 0; q < kBpt / 2; ++q) {
+        const ulonglong2 m2 = reinterpret_cast<const ulonglong2*>(sh.bin_mass)[kBpt / 2 * tid + q];
+        hm[2 * q] = m2.x;
+        hm[2 * q + 1] = m2.y;
+      }
+    } else {
+      hc[0] = sh.sel.hist[tid];
+      hm[0] = sh.bin_mass[tid];
+#pragma unroll
+      for (int b = 1; b < kBpt; ++b) {
+        hc[b] = 0u;
+        hm[b] = 0ull;
+      }
+    }
     uint64_t tmass = 0;
     uint32_t tcnt = 0;
-    for (int b = 0; b < bpt; ++b) {
-      tmass += sh.bin_mass[bpt * tid + b];
-      tcnt += sh.sel.hist[bpt * tid + b];
+#pragma unroll
+    for (int b = 0; b < kBpt; ++b) {
+      tmass += hm[b];
+      tcnt += hc[b];
     }
     // suffix sums over threads (bins descending): masses and counts
     const uint64_t wm = wave_suffix_u64(tmass);
@@ -529,20 +610,22 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
     if (incl - tmass < need && need <= incl) {
       uint64_t acc = incl - tmass;
       uint32_t acc_c = incl_c - tcnt;
-      int bin = bpt * tid;
-      for (int b = bpt - 1; b >= 0; --b) {
-        const uint64_t mb = sh.bin_mass[bpt * tid + b];
-        if (need <= acc + mb) {
-          bin = bpt * tid + b;
-          break;
-        }
-        acc += mb;
-        acc_c += sh.sel.hist[bpt * tid + b];
+      int bsel = 0;
+      uint32_t cnt = 0u;
+      bool found = false;
+#pragma unroll
+      for (int b = kBpt - 1; b >= 0; --b) {
+        const bool hit = !found && need <= acc + hm[b];
+        bsel = hit ? b : bsel;
+        cnt = hit ? hc[b] : cnt;
+        acc += (found || hit) ? 0ull : hm[b];
+        acc_c += (found || hit) ? 0u : hc[b];
+        found = found || hit;
       }
-      sh.sel.bnd = bin;
+      sh.sel.bnd = fn.linear ? kBpt * tid + bsel : tid;
       sh.lres[0] = acc;
       sh.sel.bnd_above = acc_c;
-      sh.sel.bnd_count = sh.sel.hist[bin];
+      sh.sel.bnd_count = cnt;
     }
     __syncthreads();
     const int bnd = sh.sel.bnd;
@@ -553,9 +636,8 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
       const bool c = (cand >> j) & 1u;
-      const int b = fn(key[j]);
-      taken |= (c && b > bnd) ? (1u << j) : 0u;
-      cand &= (c && b == bnd) ? 0xffffffffu : ~(1u << j);
+      taken |= (c && bin[j] > bnd) ? (1u << j) : 0u;
+      cand &= (c && bin[j] == bnd) ? 0xffffffffu : ~(1u << j);
     }
   }
   *taken_out = taken;
@@ -620,42 +702,91 @@ __device__ __forceinline__ uint32_t range_bits(int lo, int a, int b) {
 // Dynamic LDS of the selection kernels: the union bitmap (one bit per
 // position, padded to 16 bytes), then a staging area shared by the logits
 // load (N floats) and the union compaction (2 * kBlock words = 16384
-// positions of rows per window).
+// positions of rows per window, then 64 dummy slots).
 constexpr int kUnionWindowWords = 2 * kBlock;
 __host__ __device__ __forceinline__ int union_words(int length) { return (length + 31) / 32; }
 __host__ __device__ __forceinline__ int stage_offset_words(int length) { return (union_words(length) + 4 + 3) & ~3; }
 __host__ __device__ __forceinline__ int stage_elems(int N, int length) {
-  const int w = union_words(length);
-  const int rows = (w < kUnionWindowWords ? w : kUnionWindowWords) * 32;
+  (void)length;
+  const int rows = kUnionWindowWords * 32 + kWave;  // a full window and the dummy slots
   const int n = (N + 3) & ~3;
   return n > rows ? n : rows;
 }
 
+// Rows of the set bits of cb (cw words) in ascending bit order, written to
+// rows[total ...]; pos(c) is the token position of bit c.  Windows of
+// 2 * kBlock words: thread t holds words w0 + 2t and w0 + 2t + 1 and the
+// block scan gives it its first row.  Every wavefront then walks its 64
+// threads: at step k all lanes take lane k's two words, lane j keeps bit j
+// and, if set, puts its position in the LDS stage at lane k's first row plus
+// the set bits below j (mbcnt); clear lanes write a dummy slot past the
+// window, so the 64 steps have no branch.  The window's rows leave with
+// full, contiguous stores.  Returns the new total.
+template <typename PosFn>
+__device__ int expand_bits(const uint32_t* cb, int cw, int32_t* stage, int32_t* rows, int total, int* scan,
+                           PosFn pos) {
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const bool lo_half = lane < 32;
+  const int sh = lane & 31;
+  const int dummy = kUnionWindowWords * 32 + lane;
+  for (int w0 = 0; w0 < cw; w0 += kUnionWindowWords) {
+    const int w = w0 + 2 * tid;
+    const uint32_t v0 = w < cw ? cb[w] : 0u;
+    const uint32_t v1 = w + 1 < cw ? cb[w + 1] : 0u;
+    int n_win;
+    const int first = block_excl_scan(__popc(v0) + __popc(v1), scan, &n_win);
+    const int c_wave = 32 * (w0 + 2 * kWave * wave) + lane;
+#pragma unroll
+    for (int k = 0; k < kWave; ++k) {
+      const uint32_t a = readlane_u32(v0, k);
+      const uint32_t b = readlane_u32(v1, k);
+      const int base = static_cast<int>(readlane_u32(static_cast<uint32_t>(first), k));
+      const uint32_t rank = __builtin_amdgcn_mbcnt_hi(b, __builtin_amdgcn_mbcnt_lo(a, 0u));
+      const uint32_t mine = ((lo_half ? a : b) >> sh) & 1u;
+      stage[mine ? base + static_cast<int>(rank) : dummy] = pos(c_wave + 64 * k);
+    }
+    __syncthreads();
+    for (int i = tid; i < n_win; i += 4 * kBlock) {
+      int32_t r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) r[u] = i + u * kBlock < n_win ? stage[i + u * kBlock] : 0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (i + u * kBlock < n_win) rows[total + i + u * kBlock] = r[u];
+    }
+    total += n_win;
+    __syncthreads();  // the next window reuses the stage
+  }
+  return total;
+}
+
 // The last block of group g: token union of the R selections plus the sink
 // and recent windows, compacted ascending into the group's row list.
-__device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, int32_t* stage, int* scan) {
+// scratch_a (kLinBins + 64 words) and scratch_b (2 * (kLinBins + 64) words)
+// are free block-shared memory.
+__device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, int32_t* stage, int* scan,
+                                  uint32_t* scratch_a, int32_t* scratch_b) {
   const int tid = threadIdx.x;
   const int length = group_length(s, g);
   const int sink_end = s.sink < length ? s.sink : length;
   const int hist_recent = s.recent - 1 > 0 ? s.recent - 1 : 0;
   const int recent_start = (length - hist_recent) > sink_end ? (length - hist_recent) : sink_end;
   const int words = (length + 31) / 32;
-  for (int w = tid; w < words; w += kBlock) {
-    const int lo = 32 * w;
-    bits[w] = range_bits(lo, 0, sink_end) | range_bits(lo, recent_start, length);
-  }
-  __syncthreads();
+  int32_t* rows = s.rows + static_cast<int64_t>(g) * s.rows_stride;
   // Page by page: the bs candidates of head r's page pi are bits
   // [pi*bs, pi*bs + bs) of its selection and positions sink + page*bs + [0, bs)
   // of the union, so one page moves as one shifted bit field.  Four pages per
-  // thread are fetched before any is used (one round trip per 1024 pages).
+  // thread are fetched before any is used (one round trip per 1024 pages);
+  // the first batch is in flight while the path is chosen.
   const int n_words = s.words_n;
   const int bs = s.bs;
   const int total_pages = s.R * s.b0;
-  for (int base = 0; base < total_pages; base += 4 * kBlock) {
-    int page[4], n0[4];
-    uint32_t lo[4], hi[4];
-    bool act[4];
+  int page[4], n0[4];
+  uint32_t lo[4], hi[4];
+  bool act[4];
+  auto fetch = [&](int base) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int idx = base + j * kBlock + tid;
@@ -663,7 +794,8 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
       const int ii = act[j] ? idx : 0;
       const int r = ii / s.b0;
       const int pi = ii - r * s.b0;
-      page[j] = s.sel_pages[(static_cast<int64_t>(g) * s.R + r) * s.b0 + pi];
+      page[j] = __hip_atomic_load(s.sel_pages + (static_cast<int64_t>(g) * s.R + r) * s.b0 + pi, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
       n0[j] = pi * bs;
       const uint32_t* sb = s.selbits + (static_cast<int64_t>(g) * s.R + r) * n_words;
       const int w0 = n0[j] >> 5;
@@ -671,14 +803,94 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
       lo[j] = __hip_atomic_load(sb + w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       hi[j] = __hip_atomic_load(sb + (w1 < n_words ? w1 : w0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  };
+  auto page_mask = [&](int j) -> uint32_t {
+    const uint64_t both = (static_cast<uint64_t>(hi[j]) << 32) | lo[j];
+    return static_cast<uint32_t>(both >> (n0[j] & 31)) & (bs == 32 ? 0xffffffffu : ((1u << bs) - 1u));
+  };
+  if (total_pages > 0) fetch(0);
+
+  // ---- page path: pages of a power-of-two size <= 32, one fetch batch, every
+  // selected page between the sink and the recent window.  The union pages
+  // are ranked through a page bitmap, their masks packed at bit u * bs of a
+  // compact array (union page u), and only that array is expanded.
+  const int n_pages = recent_start > s.sink ? (recent_start - s.sink) / bs : 0;  // pages below the recent window
+  const int pbw = (n_pages + 31) / 32;
+  const bool pow2 = bs > 0 && (bs & (bs - 1)) == 0 && bs <= 32;
+  if (pow2 && total_pages <= 4 * kBlock && 2 * pbw <= kLinBins + 64 && total_pages <= 2 * (kLinBins + 64)) {
+    uint32_t m[4];
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      m[j] = act[j] ? page_mask(j) : 0u;
+      // a selected page outside [sink, recent_start) would overlap a window
+      bad = bad || (m[j] != 0u && (page[j] < 0 || page[j] >= n_pages));
+    }
+    uint32_t* pb = scratch_a;
+    int* pfx = reinterpret_cast<int*>(scratch_a + pbw);
+    int32_t* upage = scratch_b;
+    const int lbs = __ffs(bs) - 1;
+    const int cw_max = ((total_pages < n_pages ? total_pages : n_pages) * bs + 31) / 32;
+    for (int w = tid; w < pbw; w += kBlock) pb[w] = 0u;
+    for (int w = tid; w < cw_max; w += kBlock) bits[w] = 0u;
+    if (__syncthreads_or(bad ? 1 : 0) == 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (m[j] != 0u) atomicOr(&pb[page[j] >> 5], 1u << (page[j] & 31));
+      __syncthreads();
+      int U = 0;
+      for (int w0 = 0; w0 < pbw; w0 += kBlock) {
+        const int w = w0 + tid;
+        int tot;
+        const int ex = block_excl_scan(w < pbw ? __popc(pb[w]) : 0, scan, &tot);
+        if (w < pbw) pfx[w] = U + ex;
+        U += tot;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (m[j] != 0u) {
+          const int p = page[j];
+          const int u = pfx[p >> 5] + __popc(pb[p >> 5] & ((1u << (p & 31)) - 1u));
+          atomicOr(&bits[(u << lbs) >> 5], m[j] << ((u << lbs) & 31));
+          upage[u] = p;
+        }
+      }
+      // sink rows, then the union pages, then the recent window
+      for (int i = tid; i < sink_end; i += kBlock) rows[i] = i;
+      __syncthreads();
+      const int sink = s.sink;
+      const int u_last = U > 0 ? U - 1 : 0;
+      int total = expand_bits(bits, ((U << lbs) + 31) / 32, stage, rows, sink_end, scan, [&](int c) {
+        const int u = c >> lbs;
+        return sink + (upage[u < u_last ? u : u_last] << lbs) + (c & (bs - 1));
+      });
+      const int n_recent = length - recent_start;
+      for (int i = tid; i < n_recent; i += kBlock) rows[total + i] = recent_start + i;
+      total += n_recent;
+      const int count = total + (s.append_position >= 0 ? 1 : 0);
+      if (tid == 0) {
+        if (s.append_position >= 0) rows[total] = s.append_position;
+        s.row_counts[g] = count;
+      }
+      return;
+    }
+  }
+
+  // ---- bitmap path: one bit per position of [0, length)
+  for (int w = tid; w < words; w += kBlock) {
+    const int lo_pos = 32 * w;
+    bits[w] = range_bits(lo_pos, 0, sink_end) | range_bits(lo_pos, recent_start, length);
+  }
+  __syncthreads();
+  for (int base = 0; base < total_pages; base += 4 * kBlock) {
+    if (base > 0) fetch(base);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (!act[j]) continue;
       const int64_t pos0 = static_cast<int64_t>(s.sink) + static_cast<int64_t>(page[j]) * bs;
       if (bs <= 32) {
-        const uint64_t both = (static_cast<uint64_t>(hi[j]) << 32) | lo[j];
-        const uint32_t m = static_cast<uint32_t>(both >> (n0[j] & 31)) &
-                           (bs == 32 ? 0xffffffffu : ((1u << bs) - 1u));
+        const uint32_t m = page_mask(j);
         if (m == 0u || pos0 < 0 || pos0 + bs > length) continue;
         const uint64_t field = static_cast<uint64_t>(m) << (pos0 & 31);
         atomicOr(&bits[pos0 >> 5], static_cast<uint32_t>(field));
@@ -697,39 +909,7 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
     }
   }
   __syncthreads();
-  // compaction in windows of 2 * kBlock words: thread t ranks the positions
-  // of words w0 + 2t and w0 + 2t + 1 into the LDS stage, then consecutive
-  // threads copy consecutive rows out, four rows per thread in flight.
-  int32_t* rows = s.rows + static_cast<int64_t>(g) * s.rows_stride;
-  int total = 0;
-  for (int w0 = 0; w0 < words; w0 += kUnionWindowWords) {
-    const int w = w0 + 2 * tid;
-    uint32_t v0 = w < words ? bits[w] : 0u;
-    uint32_t v1 = w + 1 < words ? bits[w + 1] : 0u;
-    int n_win;
-    int slot = block_excl_scan(__popc(v0) + __popc(v1), scan, &n_win);
-    while (v0 != 0u) {
-      const int b = __ffs(static_cast<int>(v0)) - 1;
-      v0 &= v0 - 1u;
-      stage[slot++] = 32 * w + b;
-    }
-    while (v1 != 0u) {
-      const int b = __ffs(static_cast<int>(v1)) - 1;
-      v1 &= v1 - 1u;
-      stage[slot++] = 32 * (w + 1) + b;
-    }
-    __syncthreads();
-    for (int i = tid; i < n_win; i += 4 * kBlock) {
-      int32_t r[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) r[u] = i + u * kBlock < n_win ? stage[i + u * kBlock] : 0;
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (i + u * kBlock < n_win) rows[total + i + u * kBlock] = r[u];
-    }
-    total += n_win;
-    __syncthreads();  // the next window reuses the stage
-  }
+  const int total = expand_bits(bits, words, stage, rows, 0, scan, [](int c) { return c; });
   const int count = total + (s.append_position >= 0 ? 1 : 0);
   if (tid == 0) {
     if (s.append_position >= 0) rows[total] = s.append_position;
@@ -830,7 +1010,8 @@ __global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
     }
     publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, 0u, sh);
     if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
-    build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan);
+    build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
+                      reinterpret_cast<int32_t*>(sh.bin_mass));
     return;
   }
   uint32_t key[KPT];
@@ -861,7 +1042,8 @@ __global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
   if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = desired;
   publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
-  build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan);
+  build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
+                      reinterpret_cast<int32_t*>(sh.bin_mass));
 }
 
 // Stage B (matched budgets): allocation from the group's desired counts, the
@@ -893,7 +1075,8 @@ __global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) 
   block_topk<KPT>(key, N, k, sh.sel, &taken, &first_slot);
   publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
-  build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan);
+  build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
+                      reinterpret_cast<int32_t*>(sh.bin_mass));
 }
 
 // --------------------------------------------------------------- launch
