@@ -20,6 +20,8 @@
 //     selection finds the boundary, as the top-k does for counts.
 #pragma clang fp contract(off)
 
+#include <type_traits>
+
 #include "select.h"
 
 namespace tw {
@@ -708,7 +710,7 @@ __host__ __device__ __forceinline__ int union_words(int length) { return (length
 __host__ __device__ __forceinline__ int stage_offset_words(int length) { return (union_words(length) + 4 + 3) & ~3; }
 __host__ __device__ __forceinline__ int stage_elems(int N, int length) {
   (void)length;
-  const int rows = kUnionWindowWords * 32 + kWave;  // a full window and the dummy slots
+  const int rows = kUnionWindowWords * 32 + kWave + 4;  // a full window, the dummy slots, an alignment shift
   const int n = (N + 3) & ~3;
   return n > rows ? n : rows;
 }
@@ -812,12 +814,16 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
 
   // ---- page path: pages of a power-of-two size <= 32, one fetch batch, every
   // selected page between the sink and the recent window.  The union pages
-  // are ranked through a page bitmap, their masks packed at bit u * bs of a
-  // compact array (union page u), and only that array is expanded.
+  // are ranked through a page bitmap (union page u = rank of its page id) and
+  // their head masks ORed into umask[u]; a scan over the union pages gives
+  // each page its first row, and one thread per union page writes its set
+  // offsets (through the LDS stage: at most one window of rows).
   const int n_pages = recent_start > s.sink ? (recent_start - s.sink) / bs : 0;  // pages below the recent window
   const int pbw = (n_pages + 31) / 32;
   const bool pow2 = bs > 0 && (bs & (bs - 1)) == 0 && bs <= 32;
-  if (pow2 && total_pages <= 4 * kBlock && 2 * pbw <= kLinBins + 64 && total_pages <= 2 * (kLinBins + 64)) {
+  constexpr int kScratchB = 2 * (kLinBins + 64);
+  if (pow2 && total_pages <= 4 * kBlock && 2 * pbw <= kLinBins + 64 && 3 * total_pages <= kScratchB &&
+      total_pages * bs <= kUnionWindowWords * 32) {
     uint32_t m[4];
     bool bad = false;
 #pragma unroll
@@ -828,11 +834,12 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
     }
     uint32_t* pb = scratch_a;
     int* pfx = reinterpret_cast<int*>(scratch_a + pbw);
+    const int u_cap = total_pages < n_pages ? total_pages : n_pages;
     int32_t* upage = scratch_b;
-    const int lbs = __ffs(bs) - 1;
-    const int cw_max = ((total_pages < n_pages ? total_pages : n_pages) * bs + 31) / 32;
+    uint32_t* umask = reinterpret_cast<uint32_t*>(scratch_b + u_cap);
+    int32_t* ubase = scratch_b + 2 * u_cap;
     for (int w = tid; w < pbw; w += kBlock) pb[w] = 0u;
-    for (int w = tid; w < cw_max; w += kBlock) bits[w] = 0u;
+    for (int u = tid; u < u_cap; u += kBlock) umask[u] = 0u;
     if (__syncthreads_or(bad ? 1 : 0) == 0) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -852,19 +859,85 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
         if (m[j] != 0u) {
           const int p = page[j];
           const int u = pfx[p >> 5] + __popc(pb[p >> 5] & ((1u << (p & 31)) - 1u));
-          atomicOr(&bits[(u << lbs) >> 5], m[j] << ((u << lbs) & 31));
+          atomicOr(&umask[u], m[j]);
           upage[u] = p;
         }
       }
-      // sink rows, then the union pages, then the recent window
+      // sink rows meanwhile
       for (int i = tid; i < sink_end; i += kBlock) rows[i] = i;
       __syncthreads();
+      // first row of every union page: thread t sums union pages 4t .. 4t + 3
+      int union_rows;
+      {
+        int c[4], sum = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int u = 4 * tid + q;
+          c[q] = u < U ? __popc(umask[u]) : 0;
+          sum += c[q];
+        }
+        int acc = block_excl_scan(sum, scan, &union_rows);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int u = 4 * tid + q;
+          if (u < U) ubase[u] = acc;
+          acc += c[q];
+        }
+      }
+      __syncthreads();
+      // one thread per union page puts its set offsets, ascending, into the
+      // LDS stage (scattered LDS stores are cheap; scattered global stores
+      // are not), then the rows leave with full, contiguous stores
+      const int lbs = __ffs(bs) - 1;
       const int sink = s.sink;
-      const int u_last = U > 0 ? U - 1 : 0;
-      int total = expand_bits(bits, ((U << lbs) + 31) / 32, stage, rows, sink_end, scan, [&](int c) {
-        const int u = c >> lbs;
-        return sink + (upage[u < u_last ? u : u_last] << lbs) + (c & (bs - 1));
-      });
+      // Branch-free: offsets are written in ascending order at the running
+      // count k, so an unset offset's value is overwritten by the next set
+      // one; offsets past the page's highest set bit go to a dummy slot.
+      int32_t* urows = rows + sink_end;
+      // the stage is shifted so that stage row i and urows[i] agree modulo
+      // 16 bytes (vector copies below); the dummy slots follow the window
+      const int lead = static_cast<int>((4u - ((reinterpret_cast<uintptr_t>(urows) >> 2) & 3u)) & 3u);
+      int32_t* st = stage + ((4 - lead) & 3);
+      const int dummy = kUnionWindowWords * 32 + lane_id();
+      auto put_pages = [&](auto bs_c) {
+        constexpr int kBs = decltype(bs_c)::value;
+        for (int u = tid; u < U; u += kBlock) {
+          const uint32_t mu = umask[u];  // non-zero: u is a union page
+          const int hb = 31 - __clz(static_cast<int>(mu));
+          const int b0 = ubase[u];
+          const int v0 = sink + (upage[u] << lbs);
+          int k = b0;
+#pragma unroll
+          for (int o = 0; o < (kBs > 0 ? kBs : 32); ++o) {
+            if (kBs > 0 || o < bs) st[o <= hb ? k : dummy] = v0 + o;
+            k += static_cast<int>((mu >> o) & 1u);
+          }
+        }
+      };
+      if (bs == 16)
+        put_pages(std::integral_constant<int, 16>{});
+      else
+        put_pages(std::integral_constant<int, 0>{});
+      __syncthreads();
+      // rows [0, lead) and the tail one by one, the rest as 16-byte copies,
+      // four per thread in flight
+      const int n4 = union_rows > lead ? (union_rows - lead) >> 2 : 0;
+      const int4* src4 = reinterpret_cast<const int4*>(st + lead);
+      int4* dst4 = reinterpret_cast<int4*>(urows + lead);
+      for (int i = tid; i < n4; i += 4 * kBlock) {
+        int4 r[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r[q] = src4[i + q * kBlock < n4 ? i + q * kBlock : i];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (i + q * kBlock < n4) dst4[i + q * kBlock] = r[q];
+      }
+      if (tid < lead && tid < union_rows) urows[tid] = st[tid];
+      {
+        const int i = lead + 4 * n4 + tid;
+        if (tid < 4 && i < union_rows) urows[i] = st[i];
+      }
+      int total = sink_end + union_rows;
       const int n_recent = length - recent_start;
       for (int i = tid; i < n_recent; i += kBlock) rows[total + i] = recent_start + i;
       total += n_recent;
