@@ -162,3 +162,46 @@ def test_twilight_logits_close_to_fp64(K, dev):
             want = deq[pos] @ q[g, r].double().numpy() / math.sqrt(D)
             got = logits[g, r].cpu().numpy().astype(np.float64)
             assert np.max(np.abs(got - want)) <= 1e-4 * (1.0 + np.max(np.abs(want)))
+
+
+@pytest.mark.parametrize("bs,b0", [(16, 24), (8, 40)])
+def test_twilight_union_pages_reaching_recent_window(K, dev, bs, b0):
+    """Selections on pages that reach into the recent window (the page path of
+    the union hands over to the token bitmap): the union counts a position
+    the recent window also holds once, as np.unique over the oracle's
+    top-p selections does."""
+    G, R, L, sink, recent, top_p = 2, 4, 2048, 16, 64, 0.9
+    _say(f"[twilight union overlap] bs={bs} b0={b0}")
+    N = b0 * bs
+    rng = np.random.default_rng(11 + bs)
+    n_pages = (L - sink) // bs
+    pages = np.empty((G, R, b0), np.int32)
+    for g in range(G):
+        for r in range(R):
+            pages[g, r] = np.sort(rng.choice(n_pages, b0, replace=False))
+        # head 0's last page: the last whole page, inside the recent window
+        pages[g, 0] = np.append(np.sort(rng.choice(n_pages - 1, b0 - 1, replace=False)), n_pages - 1)
+    logits = (rng.standard_normal((G, R, N)) * 3.0).astype(np.float32)
+    rows = torch.full((G, L + 1), -5, dtype=torch.int32, device=dev)
+    counts = torch.zeros((G,), dtype=torch.int32, device=dev)
+    desired = torch.zeros((G, R), dtype=torch.int32, device=dev)
+    K.twilight_select(torch.from_numpy(logits).to(dev), torch.from_numpy(pages).to(dev), top_p=top_p,
+                      budget_mode="dynamic", rows=rows, row_counts=counts, desired=desired, sink=sink,
+                      recent=recent, block_size=bs, length=L, append_position=L)
+    torch.cuda.synchronize()
+    sink_end, recent_start, _ = oracle.selection_window(L, sink, recent)
+    offs = np.arange(bs)
+    for g in range(G):
+        assert pages[g, 0, -1] * bs + sink + bs > recent_start, "the case must reach the recent window"
+        sel = []
+        for r in range(R):
+            d = oracle.top_p_count(logits[g, r], top_p)[0]
+            assert int(desired[g, r]) == d, f"group {g} head {r}: desired"
+            idx = oracle.topk_sorted(logits[g, r][None], d)[0]
+            cand = (sink + pages[g, r][:, None] * bs + offs).reshape(-1)
+            sel.append(cand[idx])
+        union = np.unique(np.concatenate([np.arange(sink_end), *sel, np.arange(recent_start, L)]))
+        n = int(counts[g])
+        assert n == len(union) + 1, f"group {g}: union size {n - 1} vs {len(union)}"
+        got = rows[g, :n].cpu().numpy()
+        assert np.array_equal(got[:-1], union) and got[-1] == L
