@@ -1045,19 +1045,23 @@ __device__ __forceinline__ void load_logits(const float* row, int N, float* stag
   __syncthreads();
 }
 
-// Publish this row's selection bits (bit n = candidate n selected).
+// Publish this row's selection bits (bit n = candidate n selected): the
+// 32 / KPT consecutive threads of a word OR their shifted bits together
+// (lane shuffles within the wavefront) and the first of them stores the
+// word; words past the block's keys are zero.
 template <int KPT>
 __device__ __forceinline__ void publish_selection(uint32_t* row_bits, int words, uint32_t taken, TopShared& sh) {
-  const int i0 = KPT * static_cast<int>(threadIdx.x);
-  for (int w = threadIdx.x; w < words; w += kBlock) sh.sel.selbits[w] = 0u;
-  __syncthreads();
+  (void)sh;
+  const int tid = static_cast<int>(threadIdx.x);
+  static_assert(KPT <= 32 && (32 % KPT) == 0, "whole threads per word");
+  constexpr int kLpw = 32 / KPT;  // threads per word
+  uint32_t w = KPT == 32 ? taken : (taken << ((tid % kLpw) * KPT));
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    if ((taken >> j) & 1u) atomicOr(&sh.sel.selbits[(i0 + j) >> 5], 1u << ((i0 + j) & 31));
-  }
-  __syncthreads();
-  for (int w = threadIdx.x; w < words; w += kBlock)
-    __hip_atomic_store(row_bits + w, sh.sel.selbits[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int o = 1; o < kLpw; o <<= 1) w |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), o));
+  if (tid % kLpw == 0 && tid / kLpw < words)
+    __hip_atomic_store(row_bits + tid / kLpw, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int i = kBlock / kLpw + tid; i < words; i += kBlock)
+    __hip_atomic_store(row_bits + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Stage A: the top-p count of every (group, head) row; in dynamic mode also
