@@ -990,38 +990,52 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
   }
 }
 
-// The row's logits through the LDS stage (16-byte loads, consecutive threads
-// reading consecutive chunks), then KPT contiguous keys per thread; the
-// largest logit and the smallest and largest key of the row in one block
-// reduction.
+// The row's logits as KPT contiguous keys per thread (16-byte loads of the
+// thread's own logits; rows that are not 16-byte aligned go through the LDS
+// stage); the largest logit and the smallest and largest key of the row in
+// one block reduction.
 template <int KPT>
 __device__ __forceinline__ void load_logits(const float* row, int N, float* stage, uint32_t (&key)[KPT],
                                             float& lmax, uint32_t& kmin, uint32_t& kmax, TopShared& sh) {
   const int tid = static_cast<int>(threadIdx.x);
-  if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
-    const float4* r4 = reinterpret_cast<const float4*>(row);
-    float4* s4 = reinterpret_cast<float4*>(stage);
-    const int n4 = N >> 2;
-#pragma unroll
-    for (int j = 0; j < KPT / 4; ++j) {
-      const int i = j * kBlock + tid;
-      if (i < n4) s4[i] = r4[i];
-    }
-  } else {
-    for (int i = tid; i < N; i += kBlock) stage[i] = row[i];
-  }
-  __syncthreads();
   const int i0 = KPT * tid;
   float mx = -INFINITY;
   uint32_t kmx = 0u, kmn = 0xffffffffu;
+  if (N > 0 && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
+    // the thread's KPT contiguous logits straight from memory, 16 bytes a load
+    // (indices past the row read its last float4 and are masked below)
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    const int last4 = (N >> 2) - 1;
+    float v[KPT];
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    const int i = i0 + j;
-    const float v = stage[i < N ? i : N - 1];
-    key[j] = score_key(v);
-    mx = (i < N && v > mx) ? v : mx;
-    kmx = (i < N && key[j] > kmx) ? key[j] : kmx;
-    kmn = (i < N && key[j] < kmn) ? key[j] : kmn;
+    for (int j = 0; j < KPT / 4; ++j) {
+      const int i4 = (i0 >> 2) + j;
+      const float4 t = r4[i4 < last4 ? i4 : last4];
+      v[4 * j] = t.x;
+      v[4 * j + 1] = t.y;
+      v[4 * j + 2] = t.z;
+      v[4 * j + 3] = t.w;
+    }
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int i = i0 + j;
+      key[j] = score_key(v[j]);
+      mx = (i < N && v[j] > mx) ? v[j] : mx;
+      kmx = (i < N && key[j] > kmx) ? key[j] : kmx;
+      kmn = (i < N && key[j] < kmn) ? key[j] : kmn;
+    }
+  } else {
+    for (int i = tid; i < N; i += kBlock) stage[i] = row[i];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int i = i0 + j;
+      const float v = stage[i < N ? i : N - 1];
+      key[j] = score_key(v);
+      mx = (i < N && v > mx) ? v : mx;
+      kmx = (i < N && key[j] > kmx) ? key[j] : kmx;
+      kmn = (i < N && key[j] < kmn) ? key[j] : kmn;
+    }
   }
   mx = wave_max_f32(mx);
   kmx = wave_max_u32(kmx);
