@@ -305,7 +305,8 @@ float or_det_exp(float x) {
 /* INT4 QK estimate of one query head (twilight_fused_qk.py:12-55,
  * twilight_offload_cache.py:1197-1261) in this build's defined order:
  *   k_d = f32(code_d) * f32(scale) + f32(min)            (dequantize, :40-47)
- *   acc_j = sum_{i<8} k_{8j+i} * q_{8j+i}, sequential from +0 (j = 0..ceil(D/8)-1,
+ *   acc_j = sum_{i<8} k_{8j+i} * q_{8j+i}, sequential fused multiply-adds from +0
+ *   (j = 0..ceil(D/8)-1,
  *   the one chunk of D < 8 channels is partial)
  *   dot = adjacent-pair tree over the acc_j
  *   logit = dot * qk_scale   (qk_scale = fp32(1/sqrt(D)))
@@ -324,7 +325,7 @@ void or_int4_qk(const float* q, int D, const uint8_t* packed, const void* scale,
         const uint32_t b = packed[t * (D / 2) + d / 2];
         const uint32_t code = (d & 1) ? (b >> 4) & 15u : b & 15u;
         const float k = (float)code * s + m;
-        a = a + k * q[d];
+        a = fmaf(k, q[d], a);
       }
       acc[j] = a;
     }

@@ -311,12 +311,19 @@ def _int4_qk_crafted(values: dict[int, float], q_of: dict[int, float]) -> float:
 
 def test_int4_qk_defined_order():
     """logit = qk_scale * tree(chunk sums), chunk j = sum_{i<8} k_{8j+i} q_{8j+i}
-    sequentially.  With terms 1, 2^24, -2^24 the result depends on the order."""
+    as sequential fused multiply-adds.  With terms 1, 2^24, -2^24 the result
+    depends on the order."""
     big = float(2 ** 24)
-    # inside one chunk, sequential: (1 + 0) + 2^24 -> 2^24, then - 2^24 = 0 (a pairwise sum gives 1)
+    # inside one chunk, sequential: fma(1, 2^24, 1) = 2^24 + 1 rounds to 2^24 (ties to even),
+    # then fma(1, -2^24, 2^24) = 0 (a pairwise sum gives 1)
     assert _int4_qk_crafted({0: 1, 2: 1, 3: 1}, {0: 1.0, 2: big, 3: -big}) == 0.0
     # across chunks 0, 2, 3: tree (c0 + c1) + (c2 + c3) = 1 (a sequential sum over chunks gives 0)
     assert _int4_qk_crafted({0: 1, 16: 1, 24: 1}, {0: 1.0, 16: big, 24: -big}) == 1.0
+    # fused, not a rounded product then a sum: after -3, fma(3, 1 + 2^-23, -3) is 3 * 2^-23
+    # exactly, while fl(3 * (1 + 2^-23)) - 3 is a multiple of 2^-22
+    u = 1.0 + 2.0 ** -23
+    qv = {0: -1.0, 1: u}
+    assert _int4_qk_crafted({0: 3, 1: 3}, qv) == float(np.float32(3 * 2.0 ** -23))
 
 
 @pytest.mark.parametrize("dtype,D", [("bf16", 128), ("f16", 64), ("f32", 256)])

@@ -10,7 +10,8 @@
 // Orders this build defines (the reference's are unpinned: cuBLAS / tl.sum
 // reductions, argsort ties, fp32 cumsum rounding):
 //   * logit = dot * qk_scale, dot = adjacent-pair tree over D/8 chunk sums,
-//     chunk sum = sum_{i<8} k_{8j+i} q_{8j+i} sequentially, k = code*scale+min;
+//     chunk sum = sum_{i<8} k_{8j+i} q_{8j+i} as sequential fused multiply-adds
+//     from +0, k = code*scale+min (a multiply, then an add);
 //   * candidate order = ascending token position (B0 pages ascending);
 //   * top-p: masses E_i = floor(det_exp(l_i - max l) * 2^40), exact integer
 //     sums; desired = smallest c whose c largest logits (ties to the lower
@@ -79,12 +80,12 @@ struct Int4Row {
       for (int j = 0; j < 8; ++j) q[j] = j < CPL ? qr[j] : 0.0f;
     }
   }
-  // Sequential sum of the lane's CPL products, then the adjacent-pair tree
+  // Sequential fused multiply-adds over the lane's CPL channels, then the adjacent-pair tree
   // over the row's LPR lane sums (every lane of the row gets the result).
   __device__ static __forceinline__ float dot(const float (&k)[8], const float (&q)[8]) {
     float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) acc = acc + k[j] * q[j];
+    for (int j = 0; j < CPL; ++j) acc = __builtin_fmaf(k[j], q[j], acc);
     if constexpr (LPR >= 2) acc = acc + dpp_f32<kDppQuadXor1>(acc);
     if constexpr (LPR >= 4) acc = acc + dpp_f32<kDppQuadXor2>(acc);
     if constexpr (LPR >= 8) acc = acc + dpp_f32<kDppRowHalfMirror>(acc);
