@@ -232,6 +232,10 @@ int tw_int4_qk_positions(const float* q, int G, int R, int D, const uint8_t* pac
  *   budget_mode 1 (matched): allocated = matched_budget_counts(desired,
  *   target_total) per group, and each head keeps its top-allocated
  *   candidates (ties to the lower n).  R <= target_total <= R*N.
+ *   budget_mode 2 (given): allocated [G][R] is an input (counts clamped to
+ *   [1, N]); each head keeps its top-allocated candidates, desired is not
+ *   computed.  For callers that allocate one budget across more heads than
+ *   one call takes (R > 8 split into sub-groups).
  *   allocated (nullable) [G][R] the kept counts.
  *   head_bits (nullable) [G][R][ceil(N/32)]: bit n of head r's row is set
  *   when the head keeps candidate n (its own selection before the union).
@@ -404,13 +408,15 @@ int tw_decode_attention_rows_append(const void* q, const void* k_base, const voi
  *   src_k/src_v: row r at + r*D (HBM, or the device alias of mapped pinned
  *   host memory returned by tw_host_device_pointer).
  *   src_rows [n] int64 source rows (absolute, i.e. entry*Lmax + pos);
- *   dst_rows (nullable) [n] int64 destination rows (NULL: dst row = i).
- *   Rows outside [0, src_row_limit) are not read; the call then still
- *   completes and sets *error_flag (device int32, nullable) to 1.
+ *   dst_rows (nullable) [n] int64 destination rows (NULL: dst row = i, and
+ *   n must not exceed dst_row_limit); dst_k/dst_v hold dst_row_limit rows.
+ *   A pair whose source row is outside [0, src_row_limit) or whose
+ *   destination row is outside [0, dst_row_limit) is not copied; the call
+ *   then still completes and sets *error_flag (device int32, nullable) to 1.
  * Bit-exact copies.
  * ---------------------------------------------------------------------- */
 int tw_gather_rows(const void* src_k, const void* src_v, int64_t src_row_limit,
-                   const int64_t* src_rows, const int64_t* dst_rows, int64_t n, int D,
+                   const int64_t* src_rows, const int64_t* dst_rows, int64_t n, int64_t dst_row_limit, int D,
                    int elem_bytes, void* dst_k, void* dst_v, int32_t* error_flag, void* stream);
 
 /* Group-union gather of the GQA group path: replaces the per-layer union

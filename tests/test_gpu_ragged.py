@@ -1,8 +1,9 @@
 """GPU parity of the ragged (multi-request) entry points.
 
 Groups of one launch have different lengths, read from a device array:
-quest_select_ragged must equal quest_select run group by group with each
-group's own length (bit-exact page ids and union plan), the ragged page-tile
+quest_select_ragged and the ragged Twilight stage 2 must equal the oracle at
+each group's own length (bit-exact page ids, union plan, logits, counts and
+union rows), the ragged page-tile
 attention must match float64 attention over each group's own window, and the
 ragged metadata update must equal a rebuild.  A decode step made of these
 launches plus the device-side length increment is captured in a HIP graph
@@ -61,8 +62,21 @@ def _cand(L):
 LENGTHS = [40, 400, 1000, 5000, 20000, 33000]
 
 
+def _oracle_plan(sel_heads: np.ndarray):
+    """Union plan of a group from its heads' page lists: ascending union
+    pages and the bitmask of the heads that chose each."""
+    union = np.unique(sel_heads.reshape(-1))
+    masks = np.zeros(union.shape[0], np.uint8)
+    for r in range(sel_heads.shape[0]):
+        masks[np.searchsorted(union, sel_heads[r])] |= np.uint8(1 << r)
+    return union, masks
+
+
 @pytest.mark.parametrize("dtype,R", [("bf16", 7), ("f16", 4)])
-def test_quest_select_ragged_matches_per_group(K, dev, dtype, R):
+def test_quest_select_ragged_matches_oracle(K, dev, dtype, R):
+    """Each group of the ragged launch == the oracle's Quest score + top-k at
+    that group's own length (bit-exact page ids), and its union plan == the
+    set union of its heads' pages with the heads' bitmask."""
     _say(f"[ragged select] {dtype} R={R}")
     G, k = len(LENGTHS), 128
     Lmax = max(LENGTHS) + 16
@@ -76,10 +90,10 @@ def test_quest_select_ragged_matches_per_group(K, dev, dtype, R):
     pp = torch.empty((G, width), dtype=torch.int32, device=dev)
     pm = torch.empty((G, width), dtype=torch.uint8, device=dev)
     pc = torch.empty((G,), dtype=torch.int32, device=dev)
-    qd = q.to(dev)
-    K.quest_select_ragged(qd, pmin, pmax, lengths, k, sink=SINK, recent=RECENT, block_size=BS, sel_pages=sel,
+    K.quest_select_ragged(q.to(dev), pmin, pmax, lengths, k, sink=SINK, recent=RECENT, block_size=BS, sel_pages=sel,
                           plan_pages=pp, plan_masks=pm, plan_counts=pc)
     torch.cuda.synchronize()
+    pmin_h, pmax_h = to_bits(pmin), to_bits(pmax)
     for g, L in enumerate(LENGTHS):
         P = _cand(L)
         kg = min(k, P)
@@ -87,18 +101,13 @@ def test_quest_select_ragged_matches_per_group(K, dev, dtype, R):
         if P == 0:
             assert int(pc[g]) == 0
             continue
-        w = min(P, R * kg)
-        s1 = torch.empty((1, R, kg), dtype=torch.int32, device=dev)
-        p1 = torch.empty((1, w), dtype=torch.int32, device=dev)
-        m1 = torch.empty((1, w), dtype=torch.uint8, device=dev)
-        c1 = torch.empty((1,), dtype=torch.int32, device=dev)
-        K.quest_select(qd[g:g + 1].contiguous(), pmin[g:g + 1, :P], pmax[g:g + 1, :P], kg, sel_pages=s1,
-                       plan_pages=p1, plan_masks=m1, plan_counts=c1)
-        torch.cuda.synchronize()
-        n = int(c1[0])
-        assert int(pc[g]) == n, g
-        assert torch.equal(sel[g, :, :kg].cpu(), s1[0].cpu()), g
-        assert torch.equal(pp[g, :n].cpu(), p1[0, :n].cpu()) and torch.equal(pm[g, :n].cpu(), m1[0, :n].cpu()), g
+        sc = oracle.quest_score(q[g:g + 1].numpy(), pmin_h[g:g + 1, :P], pmax_h[g:g + 1, :P], dtype)[0]
+        want = oracle.topk_sorted(sc, kg)
+        assert np.array_equal(sel[g, :, :kg].cpu().numpy(), want), g
+        union, masks = _oracle_plan(want)
+        n = int(pc[g])
+        assert n == union.shape[0], g
+        assert np.array_equal(pp[g, :n].cpu().numpy(), union) and np.array_equal(pm[g, :n].cpu().numpy(), masks), g
 
 
 def _rows(L, pages, masks, R, decode):
@@ -372,10 +381,11 @@ def test_attention_fused_page_metadata(K, dev, resident):
                                         **dict(kw, append=False))
 
 
-def test_twilight_select_ragged_matches_per_group(K, dev):
+def test_twilight_select_ragged_matches_oracle(K, dev):
     """Ragged Twilight stage 2 (INT4 QK over the ragged stage-1 plan, then
-    top-p and the GQA union with per-group lengths) == the per-group calls,
-    bit for bit: desired counts, head bitmaps, union rows.  One group has no
+    top-p and the GQA union with per-group lengths) == oracle.twilight_layer
+    at each group's own length, bit for bit: B0 pages, logits, desired counts,
+    each head's kept candidates and the union rows.  One group has no
     candidate page, one fewer candidate pages than B0."""
     _say("[ragged twilight select]")
     dtype, R, b0, top_p = "bf16", 4, 64, 0.9
@@ -411,6 +421,7 @@ def test_twilight_select_ragged_matches_per_group(K, dev):
                              max_length=max(lengths0), page_capacity=P_cap, sink=SINK, recent=RECENT,
                              block_size=BS, desired=desired, head_bits=hb)
     torch.cuda.synchronize()
+    keys_h = kd.cpu()
     for g, L in enumerate(lengths0):
         P = min(_cand(L), P_cap)
         kg = min(b0, P)
@@ -421,26 +432,20 @@ def test_twilight_select_ragged_matches_per_group(K, dev):
             assert n == want.numel() and torch.equal(rows[g, :n].cpu(), want), g
             assert bool((desired[g] == 0).all()) and bool((hb[g] == 0).all()), g
             continue
-        w1 = min(P, R * kg)
-        s1 = torch.empty((1, R, kg), dtype=torch.int32, device=dev)
-        p1 = torch.empty((1, w1), dtype=torch.int32, device=dev)
-        m1 = torch.empty((1, w1), dtype=torch.uint8, device=dev)
-        c1 = torch.empty((1,), dtype=torch.int32, device=dev)
-        K.quest_select(q[g:g + 1].contiguous(), pmin[g:g + 1, :P], pmax[g:g + 1, :P], kg, sel_pages=s1,
-                       plan_pages=p1, plan_masks=m1, plan_counts=c1)
-        lg1 = K.twilight_qk(q[g:g + 1].contiguous(), packed[g:g + 1], scale[g:g + 1], minimum[g:g + 1], p1, m1, c1,
-                            kg, sink=SINK, block_size=BS)
-        r1 = torch.empty((1, L + 1), dtype=torch.int32, device=dev)
-        n1 = torch.empty((1,), dtype=torch.int32, device=dev)
-        d1 = torch.empty((1, R), dtype=torch.int32, device=dev)
-        words1 = (kg * BS + 31) // 32
-        h1 = torch.empty((1, R, words1), dtype=torch.int32, device=dev)
-        K.twilight_select(lg1, s1, top_p=top_p, budget_mode="dynamic", rows=r1, row_counts=n1, desired=d1,
-                          head_bits=h1, sink=SINK, recent=RECENT, block_size=BS, length=L)
-        torch.cuda.synchronize()
-        assert torch.equal(desired[g].cpu(), d1[0].cpu()), g
-        assert torch.equal(hb[g, :, :words1].cpu(), h1[0].cpu()) and bool((hb[g, :, words1:] == 0).all()), g
-        assert n == int(n1[0]) and torch.equal(rows[g, :n].cpu(), r1[0, :n].cpu()), g
+        omin, omax, opk, osc, omn = oracle.build_page_metadata(to_bits(keys_h[g, :L]), dtype, SINK, BS)
+        ref = oracle.twilight_layer(q[g].cpu().numpy(), omin[:P], omax[:P], opk, osc, omn, dtype, length=L, sink=SINK,
+                                    recent=RECENT, block_size=BS, b0_pages=kg, top_p=top_p)
+        nk = kg * BS
+        assert np.array_equal(sel[g, :, :kg].cpu().numpy(), ref["pages"]), g
+        assert np.array_equal(logits[g, :, :nk].cpu().numpy().view(np.uint32),
+                              ref["logits"].astype(np.float32).view(np.uint32)), g
+        assert np.array_equal(desired[g].cpu().numpy(), ref["desired"]), g
+        bits = ((hb[g].cpu().numpy().astype(np.int64) & 0xFFFFFFFF)[:, :, None] >> np.arange(32)) & 1
+        keep = bits.reshape(R, -1)[:, :nk].astype(bool)
+        for r in range(R):
+            assert np.array_equal(np.sort(ref["candidates"][r][keep[r]]), ref["selected"][r]), (g, r)
+        assert bool((hb[g, :, (nk + 31) // 32:] == 0).all()), g
+        assert n == len(ref["union"]) and np.array_equal(rows[g, :n].cpu().numpy(), ref["union"]), g
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])

@@ -20,8 +20,9 @@ template <typename V>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ src_k, const V* __restrict__ src_v,
                                                           int64_t src_row_limit, const int64_t* __restrict__ src_rows,
                                                           const int64_t* __restrict__ dst_rows, int64_t n,
-                                                          int vec_per_row, V* __restrict__ dst_k,
-                                                          V* __restrict__ dst_v, int32_t* error_flag) {
+                                                          int64_t dst_row_limit, int vec_per_row,
+                                                          V* __restrict__ dst_k, V* __restrict__ dst_v,
+                                                          int32_t* error_flag) {
   const int64_t total = n * vec_per_row;
   for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
        t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -33,6 +34,10 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const V* __restrict__ 
       continue;
     }
     const int64_t dr = dst_rows != nullptr ? dst_rows[i] : i;
+    if (dr < 0 || dr >= dst_row_limit) {
+      if (c == 0 && error_flag != nullptr) *error_flag = 1;
+      continue;
+    }
     dst_k[dr * vec_per_row + c] = src_k[sr * vec_per_row + c];
     dst_v[dr * vec_per_row + c] = src_v[sr * vec_per_row + c];
   }
@@ -181,14 +186,14 @@ int vec_width(int64_t row_bytes, std::initializer_list<const void*> ptrs) {
 
 template <typename V>
 int launch_gather(const void* sk, const void* sv, int64_t limit, const int64_t* sr, const int64_t* dr, int64_t n,
-                  int64_t row_bytes, void* dk, void* dv, int32_t* err, hipStream_t stream) {
+                  int64_t dst_limit, int64_t row_bytes, void* dk, void* dv, int32_t* err, hipStream_t stream) {
   const int vpr = static_cast<int>(row_bytes / sizeof(V));
   const int64_t total = n * vpr;
   int64_t blocks = (total + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   hipLaunchKernelGGL(gather_rows_kernel<V>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
-                     static_cast<const V*>(sk), static_cast<const V*>(sv), limit, sr, dr, n, vpr, static_cast<V*>(dk),
-                     static_cast<V*>(dv), err);
+                     static_cast<const V*>(sk), static_cast<const V*>(sv), limit, sr, dr, n, dst_limit, vpr,
+                     static_cast<V*>(dk), static_cast<V*>(dv), err);
   return tw_host::check_launch();
 }
 
@@ -207,21 +212,24 @@ int launch_append(const void* nk, const void* nv, int n, int64_t row_bytes, void
 }  // namespace tw
 
 extern "C" int tw_gather_rows(const void* src_k, const void* src_v, int64_t src_row_limit, const int64_t* src_rows,
-                              const int64_t* dst_rows, int64_t n, int D, int elem_bytes, void* dst_k, void* dst_v,
-                              int32_t* error_flag, void* stream) {
-  if (n < 0 || D <= 0 || !(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8))
+                              const int64_t* dst_rows, int64_t n, int64_t dst_row_limit, int D, int elem_bytes,
+                              void* dst_k, void* dst_v, int32_t* error_flag, void* stream) {
+  if (n < 0 || D <= 0 || dst_row_limit < 0 ||
+      !(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8))
     return TW_EINVAL;
   if (n == 0) return TW_OK;
+  // without dst_rows the destination rows are 0 .. n-1
+  if (dst_rows == nullptr && n > dst_row_limit) return TW_EINVAL;
   if (src_k == nullptr || src_v == nullptr || src_rows == nullptr || dst_k == nullptr || dst_v == nullptr)
     return TW_EINVAL;
   const int64_t row_bytes = static_cast<int64_t>(D) * elem_bytes;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (tw::vec_width(row_bytes, {src_k, src_v, dst_k, dst_v})) {
-    case 16: return tw::launch_gather<uint4>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, row_bytes, dst_k, dst_v, error_flag, s);
-    case 8: return tw::launch_gather<uint2>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, row_bytes, dst_k, dst_v, error_flag, s);
-    case 4: return tw::launch_gather<uint32_t>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, row_bytes, dst_k, dst_v, error_flag, s);
-    case 2: return tw::launch_gather<uint16_t>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, row_bytes, dst_k, dst_v, error_flag, s);
-    default: return tw::launch_gather<uint8_t>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, row_bytes, dst_k, dst_v, error_flag, s);
+    case 16: return tw::launch_gather<uint4>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, dst_row_limit, row_bytes, dst_k, dst_v, error_flag, s);
+    case 8: return tw::launch_gather<uint2>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, dst_row_limit, row_bytes, dst_k, dst_v, error_flag, s);
+    case 4: return tw::launch_gather<uint32_t>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, dst_row_limit, row_bytes, dst_k, dst_v, error_flag, s);
+    case 2: return tw::launch_gather<uint16_t>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, dst_row_limit, row_bytes, dst_k, dst_v, error_flag, s);
+    default: return tw::launch_gather<uint8_t>(src_k, src_v, src_row_limit, src_rows, dst_rows, n, dst_row_limit, row_bytes, dst_k, dst_v, error_flag, s);
   }
 }
 

@@ -290,6 +290,7 @@ struct SelectArgs {
   int G, R, N;
   uint32_t p24;               // round(top_p * 2^24)
   bool matched;
+  bool given;                 // matched kernel only, with allocated[] as its input
   int target_total;           // matched: fixed_pages * bs * R
   const int32_t* sel_pages;   // [G][R][b0] B0 pages per head, ascending
   int b0;
@@ -1149,10 +1150,14 @@ __global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) 
   const int r = row - g * s.R;
   const int N = s.N;
   if (threadIdx.x == 0) {
-    int d[8], c[8];
-    for (int i = 0; i < s.R; ++i) d[i] = s.desired[static_cast<int64_t>(g) * s.R + i];
-    matched_counts(d, s.R, s.target_total, N, c);
-    sh.ires[1] = c[r];
+    if (s.given) {
+      sh.ires[1] = s.allocated[row];
+    } else {
+      int d[8], c[8];
+      for (int i = 0; i < s.R; ++i) d[i] = s.desired[static_cast<int64_t>(g) * s.R + i];
+      matched_counts(d, s.R, s.target_total, N, c);
+      sh.ires[1] = c[r];
+    }
   }
   float* stage = reinterpret_cast<float*>(union_bits + stage_offset_words(s.length));
   uint32_t key[KPT];
@@ -1161,7 +1166,7 @@ __global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) 
   load_logits<KPT>(s.logits + static_cast<int64_t>(row) * N, N, stage, key, lmax, kmin, kmax, sh);  // (barriers)
   int k = sh.ires[1];
   k = k < 1 ? 1 : (k > N ? N : k);
-  if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = k;
+  if (threadIdx.x == 0 && s.allocated != nullptr && !s.given) s.allocated[row] = k;
   uint32_t taken = 0u;
   int first_slot;  // (the selection is published as a bitmap)
   block_topk<KPT>(key, N, k, sh.sel, &taken, &first_slot);
@@ -1234,9 +1239,11 @@ int launch_select_kpt(const SelectArgs& s, hipStream_t stream) {
       return tw_host::check_launch();
   }
   const dim3 grid(s.G * s.R);
-  hipLaunchKernelGGL(twilight_topp_kernel<KPT>, grid, dim3(kBlock), lds, stream, s);
-  int rc = tw_host::check_launch();
-  if (rc != TW_OK || !s.matched) return rc;
+  if (!s.given) {
+    hipLaunchKernelGGL(twilight_topp_kernel<KPT>, grid, dim3(kBlock), lds, stream, s);
+    const int rc = tw_host::check_launch();
+    if (rc != TW_OK || !s.matched) return rc;
+  }
   hipLaunchKernelGGL(twilight_matched_kernel<KPT>, grid, dim3(kBlock), lds, stream, s);
   return tw_host::check_launch();
 }
@@ -1314,7 +1321,8 @@ int select_launch(const float* logits, int G, int R, int N, const int32_t* sel_p
   if (logits == nullptr || sel_pages == nullptr || rows == nullptr || row_counts == nullptr) return TW_EINVAL;
   if (G <= 0 || R <= 0 || R > 8 || N <= 0 || b0_pages <= 0 || N != b0_pages * block_size) return TW_EINVAL;
   if (N > tw::sel::kMaxSelPages) return TW_EUNSUPPORTED;
-  if (!(top_p > 0.0f) || !(top_p <= 1.0f) || (budget_mode != 0 && budget_mode != 1)) return TW_EINVAL;
+  if (!(top_p > 0.0f) || !(top_p <= 1.0f) || budget_mode < 0 || budget_mode > 2) return TW_EINVAL;
+  if (budget_mode == 2 && allocated == nullptr) return TW_EINVAL;
   if (sink < 0 || recent <= 0 || block_size <= 0 || length < 0) return TW_EINVAL;
   if (budget_mode == 1 && (target_total < R || target_total > static_cast<int64_t>(R) * N)) return TW_EINVAL;
   // every union row fits: sink + recent + R*N selected + the decode row
@@ -1328,7 +1336,8 @@ int select_launch(const float* logits, int G, int R, int N, const int32_t* sel_p
   s.R = R;
   s.N = N;
   s.p24 = static_cast<uint32_t>(__builtin_rintf(top_p * 16777216.0f));
-  s.matched = budget_mode == 1;
+  s.matched = budget_mode >= 1;
+  s.given = budget_mode == 2;
   s.target_total = target_total;
   s.sel_pages = sel_pages;
   s.b0 = b0_pages;

@@ -81,7 +81,7 @@ _HIP_SIGNATURES = {
                                         i32, i32, vp, szt, vp]),
     "tw_decode_attention_pages_phase": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32,
                                               i32, i32, i32, vp, vp, f32, vp, vp, szt, i32, vp]),
-    "tw_gather_rows": (i32, [vp, vp, i64, vp, vp, i64, i32, i32, vp, vp, vp, vp]),
+    "tw_gather_rows": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, i32, vp, vp, vp, vp]),
     "tw_gather_union": (i32, [vp, vp, i64, i64, i64, vp, i64, vp, i32, i32, vp, vp, i32, i32, i64, vp, vp, vp, vp,
                               vp]),
     "tw_gather_heads": (i32, [vp, vp, i64, i64, i64, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i64,

@@ -52,10 +52,17 @@ def _require_contiguous(*tensors: Optional[torch.Tensor], what: str) -> None:
 
 class _Workspace:
     """Per-device, per-purpose scratch buffers.  Allocated zeroed once; the
-    kernels return their arrival counters to zero after every launch."""
+    kernels return their arrival counters to zero after every launch.
+
+    A buffer that a larger request outgrows is kept, never freed: a captured
+    HIP graph holds its raw address, and replaying that graph after the
+    replacement must still write into memory nobody else owns (with counters
+    still at zero).  Sizes double, so the retired buffers together are
+    smaller than the live one."""
 
     def __init__(self) -> None:
         self._buffers: dict[tuple, torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
 
     def get(self, device: torch.device, name: str, nbytes: int) -> torch.Tensor:
         key = (device, name)
@@ -64,13 +71,20 @@ class _Workspace:
             size = max(nbytes, 1 << 16)
             if buf is not None:
                 size = max(size, 2 * buf.numel())
-            # Enqueue the replacement after any pending use of the old buffer.
+                self._retired.append(buf)
             buf = torch.zeros(size, dtype=torch.uint8, device=device)
             self._buffers[key] = buf
         return buf
 
 
 WORKSPACE = _Workspace()
+
+
+def head_chunks(R: int, width: int = 8) -> list[tuple[int, int]]:
+    """[r0, r1) ranges splitting R query heads into ceil(R / width) nearly
+    equal sub-groups of at most `width` heads (the kernels' per-group limit)."""
+    n = -(-R // width)
+    return [(R * i // n, R * (i + 1) // n) for i in range(n)]
 
 
 # --------------------------------------------------------------- metadata
@@ -561,9 +575,14 @@ def twilight_select(
     the stage-1 pages; rows [G, >=length+1] int32 and row_counts [G] int32
     receive the union (ascending, then append_position if >= 0); desired /
     allocated [G,R] int32 (optional) the counts; head_bits [G,R,ceil(N/32)]
-    int32 (optional) each head's kept candidates as a bitmap."""
-    if budget_mode not in ("dynamic", "matched"):
-        raise ValueError("budget_mode must be 'dynamic' or 'matched'")
+    int32 (optional) each head's kept candidates as a bitmap.  budget_mode
+    "given" takes allocated [G,R] as an input (every head keeps its
+    top-allocated candidates; desired is not computed)."""
+    modes = {"dynamic": 0, "matched": 1, "given": 2}
+    if budget_mode not in modes:
+        raise ValueError("budget_mode must be 'dynamic', 'matched' or 'given'")
+    if budget_mode == "given" and allocated is None:
+        raise ValueError("budget_mode 'given' needs the allocated counts")
     if logits.dtype != torch.float32 or logits.ndim != 3 or not logits.is_contiguous():
         raise ValueError("logits must be contiguous [G, R, N] fp32")
     G, R, N = logits.shape
@@ -589,7 +608,7 @@ def twilight_select(
     ws = WORKSPACE.get(dev, "twilight_select", nbytes)
     with torch.cuda.device(dev):
         check(hip().tw_twilight_select(ptr(logits), G, R, N, ptr(sel_pages), b0, float(top_p),
-                                       1 if budget_mode == "matched" else 0, int(target_total), ptr(desired),
+                                       modes[budget_mode], int(target_total), ptr(desired),
                                        ptr(allocated), ptr(head_bits), ptr(rows), ptr(row_counts), rows.stride(0), sink, recent,
                                        block_size, length, append_position, ptr(ws), ws.numel(),
                                        stream_handle(dev)), "twilight_select")
@@ -677,10 +696,24 @@ def decode_attention_rows(
     it.  metadata (with the append; 16-bit K, D = 128): dict(sink=,
     page_min=, page_max= [G, pages, D], packed= [G, T, D/2], scale=,
     minimum= [G, T]) -- the launch also does update_page_metadata for the
-    appended row (either pair may be left out).  Returns [G,R,D]."""
+    appended row (either pair may be left out).  Returns [G,R,D].
+
+    More than 8 query heads per group run as sub-groups of at most 8 heads
+    over the same rows (every head sees every row unless row_masks, which
+    then limits R to 8); each sub-group's launch writes the same decode row."""
     if q.ndim != 3 or q.dtype not in _KEY_DTYPES:
         raise ValueError("q must be [G, R, D]")
     G, R, D = q.shape
+    if R > 8:
+        if row_masks is not None:
+            raise ValueError("row_masks take at most 8 query heads per group")
+        if out is None:
+            out = torch.empty_like(q)
+        for r0, r1 in head_chunks(R):
+            out[:, r0:r1] = decode_attention_rows(
+                q[:, r0:r1].contiguous(), k_cache, v_cache, rows, row_counts, max_rows, cur_k=cur_k, cur_v=cur_v,
+                softmax_scale=softmax_scale, append_position=append_position, metadata=metadata)
+        return out
     if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or k_cache.shape != v_cache.shape:
         raise ValueError("K/V cache must match q's dtype and each other")
     if k_cache.ndim != 3 or k_cache.shape[0] != G or k_cache.shape[2] != D or k_cache.stride() != v_cache.stride():
@@ -1057,6 +1090,15 @@ def decode_attention_varlen(
     G = B * Hk
     if out is None:
         out = torch.empty_like(q)
+    if R > 8:
+        # sub-groups of at most 8 query heads per KV head over the same keys
+        qv, ov = q.view(B, Hk, R, D), out.view(B, Hk, R, D)
+        for r0, r1 in head_chunks(R):
+            res = decode_attention_varlen(qv[:, :, r0:r1].reshape(B, Hk * (r1 - r0), D).contiguous(), k, v,
+                                          cu_seqlens_k, max_seqlen_k, softmax_scale=softmax_scale,
+                                          window_left=window_left)
+            ov[:, :, r0:r1] = res.view(B, Hk, r1 - r0, D)
+        return out
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
     max_rows = int(max_seqlen_k)
     if window_left >= 0:
@@ -1104,13 +1146,21 @@ def gather_rows(
     """dst[dst_rows[i]] = src[src_rows[i]] for K and V (bit-exact).
 
     src_k/src_v: [rows, D] on the device, or pinned host tensors (read
-    zero-copy through their mapped device address).  src_rows/dst_rows: int64
-    device tensors.  Out-of-range source rows are skipped and flagged in
-    error_flag (int32 device scalar)."""
+    zero-copy through their mapped device address).  dst_k/dst_v: matching
+    contiguous [..., D] buffers of capacity numel // D rows.  src_rows/dst_rows:
+    int64 device tensors (without dst_rows, row i goes to row i, and
+    len(src_rows) must fit the destination).  A pair with an out-of-range
+    source or destination row is skipped and flagged in error_flag (int32
+    device scalar)."""
     if src_k.shape != src_v.shape or src_k.dtype != src_v.dtype or src_k.ndim != 2:
         raise ValueError("src_k/src_v must be matching [rows, D]")
     if dst_k.dtype != src_k.dtype or dst_v.dtype != src_k.dtype or dst_k.shape[-1] != src_k.shape[-1]:
         raise ValueError("destination must match the source dtype and row width")
+    if dst_k.shape != dst_v.shape:
+        raise ValueError("dst_k/dst_v must match")
+    dst_capacity = dst_k.numel() // src_k.shape[1]
+    if dst_rows is None and src_rows.numel() > dst_capacity:
+        raise ValueError(f"{src_rows.numel()} rows do not fit a destination of {dst_capacity} rows")
     _require_contiguous(src_k, src_v, dst_k, dst_v, src_rows, dst_rows, what="gather_rows")
     if src_rows.dtype != torch.int64 or (dst_rows is not None and (dst_rows.dtype != torch.int64
                                                                    or dst_rows.shape != src_rows.shape)):
@@ -1122,8 +1172,8 @@ def gather_rows(
         sk, sv = host_device_pointer(src_k), host_device_pointer(src_v)
     D = src_k.shape[1]
     with torch.cuda.device(dev):
-        check(hip().tw_gather_rows(sk, sv, src_k.shape[0], ptr(src_rows), ptr(dst_rows), src_rows.numel(), D,
-                                   src_k.element_size(), ptr(dst_k), ptr(dst_v), ptr(error_flag),
+        check(hip().tw_gather_rows(sk, sv, src_k.shape[0], ptr(src_rows), ptr(dst_rows), src_rows.numel(),
+                                   dst_capacity, D, src_k.element_size(), ptr(dst_k), ptr(dst_v), ptr(error_flag),
                                    stream_handle(dev)), "gather_rows")
 
 

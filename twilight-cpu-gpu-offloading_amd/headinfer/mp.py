@@ -134,7 +134,7 @@ def _decode(self, cache, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> t
     groupwise = bool(getattr(cache, "gqa_groupwise_execution", False))
     flat = bool(getattr(cache, "layer_flat_ragged_execution", False))
     per_head_ref = bool(getattr(cache, "per_head_varlen_attention_reference", False))
-    if not (groupwise or flat or per_head_ref) and R <= 8:
+    if not (groupwise or flat or per_head_ref):
         out = cache.decode_layer(queries=q[0, :, 0].reshape(G, R, D).contiguous(),
                                  key_states=k[0, :, 0].contiguous(), value_states=v[0, :, 0].contiguous(),
                                  entries=entries, softmax_scale=scale)

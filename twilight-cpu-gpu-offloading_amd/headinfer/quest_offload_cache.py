@@ -108,8 +108,6 @@ class QuestTopKOffloadedCache(_CacheBase):
             raise ValueError("max_selected_history_fraction must be in (0, 1]")
         if num_query_heads_per_kv <= 0:
             raise ValueError("num_query_heads_per_kv must be positive")
-        if num_query_heads_per_kv > 8:
-            raise ValueError("at most 8 query heads per KV head are supported")
         if layer_flat_ragged_execution and not layer_batched_selection:
             raise ValueError("layer-flat ragged execution requires layer-batched selection")
         if sparse_gather_stabilized and not layer_flat_ragged_execution:
@@ -148,8 +146,9 @@ class QuestTopKOffloadedCache(_CacheBase):
         # stay in an HBM page cache and only the pages the previous step did not read cross the host link.
         self.previous_token_resident_cache = bool(previous_token_resident_cache)
         if self.previous_token_resident_cache and (kv_residency != "host" or block_size != 16 or head_dim != 128
-                                                   or dtype == torch.float32):
-            raise ValueError("the resident page cache serves a host slab of 16-bit K/V, head_dim 128, 16-row pages")
+                                                   or dtype == torch.float32 or num_query_heads_per_kv > 8):
+            raise ValueError("the resident page cache serves a host slab of 16-bit K/V, head_dim 128, 16-row pages "
+                             "and at most 8 query heads per KV head")
         self._resident: Optional[kernels.ResidentPages] = None
 
         self._bookkeeping = SequentialCacheState(num_cache_entries, max_cache_len)
@@ -180,6 +179,10 @@ class QuestTopKOffloadedCache(_CacheBase):
         self._layer_flat_group_count: Optional[int] = None
 
         self.eviction_stream = torch.cuda.Stream(device=device)
+        # Set by a gather kernel that met a row outside the slab or its
+        # destination (the row is skipped); synchronize() raises on it, so the
+        # decode path itself needs no host sync to report a bad index.
+        self._gather_error = torch.zeros(1, dtype=torch.int32, device=device)
         self._host_write_done: list[Optional[torch.cuda.Event]] = [None] * E
         self._page_min: Optional[torch.Tensor] = None   # [E, prompt_pages, D]
         self._page_max: Optional[torch.Tensor] = None
@@ -272,6 +275,9 @@ class QuestTopKOffloadedCache(_CacheBase):
     def synchronize(self) -> None:
         self._stream().synchronize()
         self.eviction_stream.synchronize()
+        if int(self._gather_error.item()):
+            self._gather_error.zero_()
+            raise RuntimeError("a K/V gather met a row index outside the slab or its destination")
 
     def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
         return self._logical_lengths[0 if layer_idx is None else layer_idx]
@@ -547,7 +553,7 @@ class QuestTopKOffloadedCache(_CacheBase):
         kernels.gather_heads(self._key_rows, self._value_rows, sel, cur_k, cur_v, self._pack_rows_k,
                              self._pack_rows_v, entry_row0=self.geometry.row(layer_idx, 0), entry_row_step=0,
                              sink=self.sink_tokens, recent=self.recent_tokens, block_size=self.block_size,
-                             length=old_length, num_heads=R, dst_strides=(0, 1, R))
+                             length=old_length, num_heads=R, dst_strides=(0, 1, R), error_flag=self._gather_error)
         self._phase_end("gather", start)
         self._append([layer_idx], cur_k, cur_v, old_length)
         self._last_query_head_lengths[layer_idx] = (total,) * R
@@ -657,14 +663,15 @@ class QuestTopKOffloadedCache(_CacheBase):
                                  entry_row0=self.geometry.row(entries[0], 0),
                                  entry_row_step=self.geometry.max_cache_len, sink=self.sink_tokens,
                                  recent=self.recent_tokens, block_size=self.block_size, length=old_length,
-                                 num_heads=R, dst_strides=(R * T, T, 1))
+                                 num_heads=R, dst_strides=(R * T, T, 1), error_flag=self._gather_error)
         else:
             for g, entry in enumerate(entries):
                 kernels.gather_heads(self._key_rows, self._value_rows, None if sel is None else sel[g:g + 1],
                                      cur_k[g:g + 1], cur_v[g:g + 1], fk[g * R * T:], fv[g * R * T:],
                                      entry_row0=self.geometry.row(entry, 0), entry_row_step=0,
                                      sink=self.sink_tokens, recent=self.recent_tokens, block_size=self.block_size,
-                                     length=old_length, num_heads=R, dst_strides=(0, T, 1))
+                                     length=old_length, num_heads=R, dst_strides=(0, T, 1),
+                                     error_flag=self._gather_error)
         self._phase_end("gather", start)
         self._append(entries, cur_k, cur_v, old_length)
         cu = torch.arange(0, G * R + 1, dtype=torch.int32, device=self.device) * T
@@ -731,6 +738,29 @@ class QuestTopKOffloadedCache(_CacheBase):
         e0 = entries[0]
         slab_k = self._key_cache[e0:e0 + G]
         slab_v = self._value_cache[e0:e0 + G]
+        if R > 8:
+            # sub-groups of at most 8 heads, each with its own union plan: a
+            # head attends to its own pages either way, so the output equals
+            # one plan over all R heads; every sub-group writes the same row
+            if out is None:
+                out = torch.empty_like(queries)
+            for r0, r1 in kernels.head_chunks(R):
+                out[:, r0:r1] = self._decode_pages(queries[:, r0:r1].contiguous(), key_states, value_states, e0,
+                                                   slab_k, slab_v, old_length, cand, k, softmax_scale, None)
+        else:
+            out = self._decode_pages(queries, key_states, value_states, e0, slab_k, slab_v, old_length, cand, k,
+                                     softmax_scale, out)
+        self._update_decode_metadata(entries, old_length)
+        for e in entries:
+            self._last_query_head_lengths[e] = None
+        return out
+
+    def _decode_pages(self, queries: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor, e0: int,
+                      slab_k: torch.Tensor, slab_v: torch.Tensor, old_length: int, cand: int, k: int,
+                      softmax_scale: Optional[float], out: Optional[torch.Tensor]) -> torch.Tensor:
+        """Selection plan + page attention of decode_layer for <= 8 heads."""
+        G, R, _ = queries.shape
+        entries = list(range(e0, e0 + G))
         width = max(1, min(cand, R * k))
         plan_pages = torch.empty((G, width), dtype=torch.int32, device=self.device)
         plan_masks = torch.empty((G, width), dtype=torch.uint8, device=self.device)
@@ -756,7 +786,4 @@ class QuestTopKOffloadedCache(_CacheBase):
                 cur_k=key_states.contiguous(), cur_v=value_states.contiguous(), softmax_scale=softmax_scale,
                 out=out)
         self._phase_end("attention", start)
-        self._update_decode_metadata(entries, old_length)
-        for e in entries:
-            self._last_query_head_lengths[e] = None
         return result

@@ -127,16 +127,6 @@ def matched_budget_counts_tensor(desired: torch.Tensor, target_total: int, capac
 
 
 # ------------------------------------------------------------------- cache
-_BACKEND_CHOICES = {
-    "qk_backend": {"pytorch", "triton", "triton_prepare"},
-    "resident_mapping_backend": {"torch", "native", "native_compact", "gpu_bitmap"},
-    "resident_hit_copy_backend": {"torch", "triton"},
-    "resident_snapshot_backend": {"torch", "triton"},
-    "resident_position_snapshot_backend": {"clone", "triton"},
-    "new_kv_d2h_granularity": {"token", "layer"},
-}
-
-
 class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
     """Quest B0 + INT4 QK + top-p with matched or dynamic budgets."""
 
@@ -183,35 +173,132 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         post_selection_groups_per_chunk: int = 1,
         **kwargs: Any,
     ) -> None:
+        # Validation follows twilight_offload_cache.py:183-381 condition by
+        # condition, in the same order and with the same messages, so a
+        # configuration fails here exactly when it fails in the reference.
         if candidate_token_budget <= 0:
             raise ValueError("candidate_token_budget must be positive")
         if not 0.0 < top_p <= 1.0:
             raise ValueError("top_p must be in (0, 1]")
         if not 0.0 < matched_budget_fraction <= 1.0:
             raise ValueError("matched_budget_fraction must be in (0, 1]")
-        if budget_mode not in ("matched", "dynamic"):
+        if budget_mode not in {"matched", "dynamic"}:
             raise ValueError("budget_mode must be 'matched' or 'dynamic'")
-        choices = dict(qk_backend=qk_backend, resident_mapping_backend=resident_mapping_backend,
-                       resident_hit_copy_backend=resident_hit_copy_backend,
-                       resident_snapshot_backend=resident_snapshot_backend,
-                       resident_position_snapshot_backend=resident_position_snapshot_backend,
-                       new_kv_d2h_granularity=new_kv_d2h_granularity)
-        for name, value in choices.items():
-            if value not in _BACKEND_CHOICES[name]:
-                raise ValueError(f"unknown {name.replace('_', ' ')} {value!r}")
-        if qk_backend != "pytorch" and not kwargs.get("layer_batched_selection", False):
+        num_query_heads_per_kv = int(kwargs["num_query_heads_per_kv"])
+        layer_batched_selection = bool(kwargs.get("layer_batched_selection", False))
+        if qk_backend not in {"pytorch", "triton", "triton_prepare"}:
+            raise ValueError("unknown Twilight QK backend")
+        if qk_backend != "pytorch" and not layer_batched_selection:
             raise ValueError("fused QK requires layer-batched selection")
         if exact_scan_graph and exact_top_p_graph:
             raise ValueError("select one exact Top-p graph scope")
-        if resident_zero_copy and not previous_token_resident_cache:
-            raise ValueError("resident zero-copy requires resident cache")
         if resident_precompute_gpu_mapping and not resident_zero_copy:
             raise ValueError("precomputed GPU mapping requires mapped resident fast path")
-        if gather_h2d_chunks < 0:
-            raise ValueError("gather_h2d_chunks must be non-negative")
-        if post_selection_groups_per_chunk <= 0:
-            raise ValueError("post_selection_groups_per_chunk must be positive")
+        if any((vram_alias_history_staging, vram_lazy_gpu_pack, vram_ondemand_attention_capacity,
+                vram_tight_resident_capacity)) and not resident_zero_copy:
+            raise ValueError("VRAM audit options require the mapped resident fast path")
+        if resident_zero_copy and not previous_token_resident_cache:
+            raise ValueError("resident zero-copy requires resident cache")
+        if resident_mapping_backend not in {"torch", "native", "native_compact", "gpu_bitmap"}:
+            raise ValueError("unknown resident mapping backend")
+        if resident_mapping_backend != "torch" and not previous_token_resident_cache:
+            raise ValueError("native resident mapping requires resident cache")
+        if resident_hit_copy_backend not in {"torch", "triton"}:
+            raise ValueError("unknown resident hit copy backend")
+        if resident_hit_copy_backend != "torch" and not previous_token_resident_cache:
+            raise ValueError("Triton resident hit copy requires resident cache")
+        if resident_mapping_backend in {"native_compact", "gpu_bitmap"} and resident_hit_copy_backend != "triton":
+            raise ValueError("compact hit indices require Triton hit copy")
+        if resident_snapshot_backend not in {"torch", "triton", "contiguous"}:
+            raise ValueError("unknown resident snapshot backend")
+        if resident_snapshot_backend != "torch" and not previous_token_resident_cache:
+            raise ValueError("alternate resident snapshot requires resident cache")
+        if resident_snapshot_backend == "contiguous" and (
+                resident_mapping_backend not in {"native_compact", "gpu_bitmap"}
+                or resident_hit_copy_backend != "triton"):
+            raise ValueError("contiguous snapshot requires native_compact mapping and Triton hit copy")
+        if resident_position_snapshot_backend not in {"clone", "reference"}:
+            raise ValueError("unknown resident position snapshot backend")
+        if resident_position_snapshot_backend == "reference" and (
+                resident_snapshot_backend != "contiguous" or not gpu_compact_gqa_union):
+            raise ValueError("reference position snapshot requires contiguous resident and GPU union")
+        if resident_zero_copy and not (resident_mapping_backend == "gpu_bitmap"
+                                       and resident_snapshot_backend == "contiguous"
+                                       and resident_position_snapshot_backend == "reference"
+                                       and gpu_compact_gqa_union):
+            raise ValueError("resident zero-copy requires GPU bitmap mapping and contiguous GPU union")
+        if resident_pack_hit_indices and (resident_snapshot_backend != "contiguous"
+                                          or resident_mapping_backend != "native_compact"):
+            raise ValueError("packed hit indices require contiguous resident and native_compact mapping")
+        if new_kv_d2h_granularity not in {"layer", "token"}:
+            raise ValueError("new KV D2H granularity must be 'layer' or 'token'")
+        if gpu_compact_gqa_union and not gqa_groupwise_execution:
+            raise ValueError("GPU compact union requires GQA group execution")
+        if gpu_union_validate_cpu and not gpu_compact_gqa_union:
+            raise ValueError("GPU union CPU validation requires GPU compact union")
+        if int(post_selection_groups_per_chunk) <= 0:
+            raise ValueError("post-selection groups per chunk must be positive")
+        if post_selection_pipeline and not (gpu_compact_gqa_union and gqa_groupwise_execution and cpu_flat_gather
+                                            and direct_attention_layout and gather_h2d_chunks > 0
+                                            and not cpu_native_gather and not cpu_run_gather
+                                            and not previous_token_resident_cache):
+            raise ValueError("post-selection pipeline requires the current GPU-union GQA flat/direct/chunk path "
+                             "without native/run gather or resident reuse")
+        if cpu_run_gather and (not (cpu_flat_gather and direct_attention_layout and gqa_groupwise_execution
+                                    and gather_h2d_chunks > 0) or cpu_native_gather):
+            raise ValueError("run gather requires flat/direct/GQA chunk pipeline without native gather")
+        if fused_quest_score and not layer_batched_selection:
+            raise ValueError("fused Quest score requires layer-batched selection")
+        if int(gather_h2d_chunks) < 0:
+            raise ValueError("gather_h2d_chunks must be nonnegative")
+        if gather_h2d_chunks and not (cpu_flat_gather and direct_attention_layout and gqa_groupwise_execution):
+            raise ValueError("chunk pipeline requires flat gather, direct layout and GQA execution")
+        if gather_h2d_chunks and cpu_native_gather:
+            raise ValueError("chunk pipeline pilot uses PyTorch gather only")
+        if early_gpu_metadata and not gqa_groupwise_execution:
+            raise ValueError("early GPU metadata requires GQA group execution")
+        if (cpu_native_gather or direct_attention_layout) and not (cpu_flat_gather and gqa_groupwise_execution):
+            raise ValueError("native gather/direct layout requires flat gather and GQA group execution")
+        if cpu_flat_gather and not gqa_groupwise_execution:
+            raise ValueError("cpu_flat_gather requires GQA group execution")
+        if previous_token_resident_cache and not (gqa_groupwise_execution and cpu_flat_gather
+                                                  and direct_attention_layout and gather_h2d_chunks > 0
+                                                  and not cpu_native_gather and not cpu_run_gather):
+            raise ValueError("previous-token resident cache requires the current GQA flat/direct/chunk path "
+                             "without native/run gather")
+        layer_flat_ragged_execution = bool(kwargs.get("layer_flat_ragged_execution", False))
+        if gqa_groupwise_execution and not layer_batched_selection:
+            raise ValueError("GQA group-wise execution requires layer-batched selection")
+        if gqa_groupwise_execution and layer_flat_ragged_execution:
+            raise ValueError("GQA group-wise and per-Query-head flat execution are exclusive")
+        # The Quest base selects with the matched fraction, and sizes its
+        # per-head packs for the largest Twilight selection
+        # (twilight_offload_cache.py:353-370).
+        kwargs["budget_fraction"] = matched_budget_fraction
+        if budget_mode == "dynamic":
+            max_cache_len = int(kwargs["max_cache_len"])
+            sink_tokens = int(kwargs.get("sink_tokens", 64))
+            block_size = int(kwargs.get("block_size", 16))
+            max_pages = math.ceil(max(0, max_cache_len - sink_tokens) / block_size)
+            required_pages = min(max_pages, math.ceil(candidate_token_budget / block_size))
+            kwargs["max_selected_history_fraction"] = required_pages / max_pages if max_pages else 1.0
+        else:
+            kwargs["max_selected_history_fraction"] = min(1.0, matched_budget_fraction * num_query_heads_per_kv)
         super().__init__(**kwargs)
+        if cpu_bitmap_union and not gqa_groupwise_execution:
+            raise ValueError("cpu_bitmap_union requires GQA group execution")
+        # The reference's host natives behind the CPU variants; the union,
+        # gather and attention of this cache run on the device, so these are
+        # held for callers that use them directly.
+        if cpu_run_gather:
+            from .cpu_kv_run_gather import CpuKVRunGather
+            self._cpu_run_gather = CpuKVRunGather()
+        if cpu_native_gather:
+            from .cpu_kv_gather import CpuKVGather
+            self._cpu_kv_gather = CpuKVGather()
+        if cpu_bitmap_union:
+            from .cpu_token_union import CpuTokenUnion
+            self._cpu_token_union = CpuTokenUnion(self.geometry.max_cache_len)
         self.candidate_token_budget = int(candidate_token_budget)
         self.top_p = float(top_p)
         self.matched_budget_fraction = float(matched_budget_fraction)
@@ -219,8 +306,37 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         self.gqa_groupwise_execution = bool(gqa_groupwise_execution)
         self.detailed_selection_profile = bool(detailed_selection_profile)
         self.qk_backend = qk_backend
+        self.exact_scan_graph = bool(exact_scan_graph)
+        self.exact_top_p_graph = bool(exact_top_p_graph)
+        self.cpu_flat_gather = bool(cpu_flat_gather)
+        self.cpu_bitmap_union = bool(cpu_bitmap_union)
+        self.cpu_native_gather = bool(cpu_native_gather)
+        self.direct_attention_layout = bool(direct_attention_layout)
+        self.early_gpu_metadata = bool(early_gpu_metadata)
+        self.gather_h2d_chunks = int(gather_h2d_chunks)
+        self.reuse_quant_metadata = bool(reuse_quant_metadata)
+        self.fused_final_indices = bool(fused_final_indices)
+        self.fused_quest_score = bool(fused_quest_score)
+        self.skip_unused_host_views = bool(skip_unused_host_views)
+        self.cpu_run_gather = bool(cpu_run_gather)
+        self.resident_zero_copy = bool(resident_zero_copy)
+        self.resident_precompute_gpu_mapping = bool(resident_precompute_gpu_mapping)
+        self.resident_mapping_backend = resident_mapping_backend
+        self.resident_hit_copy_backend = resident_hit_copy_backend
+        self.resident_snapshot_backend = resident_snapshot_backend
+        self.resident_position_snapshot_backend = resident_position_snapshot_backend
+        self.resident_pack_hit_indices = bool(resident_pack_hit_indices)
+        self.gpu_union_validate_cpu = bool(gpu_union_validate_cpu)
+        self.batched_new_kv_d2h = bool(batched_new_kv_d2h)
+        self.new_kv_d2h_granularity = new_kv_d2h_granularity
+        self.post_selection_pipeline = bool(post_selection_pipeline)
+        self.post_selection_groups_per_chunk = int(post_selection_groups_per_chunk)
         self._variant_flags = dict(
-            choices, exact_scan_graph=exact_scan_graph, exact_top_p_graph=exact_top_p_graph,
+            qk_backend=qk_backend, resident_mapping_backend=resident_mapping_backend,
+            resident_hit_copy_backend=resident_hit_copy_backend, resident_snapshot_backend=resident_snapshot_backend,
+            resident_position_snapshot_backend=resident_position_snapshot_backend,
+            new_kv_d2h_granularity=new_kv_d2h_granularity, exact_scan_graph=exact_scan_graph,
+            exact_top_p_graph=exact_top_p_graph,
             cpu_flat_gather=cpu_flat_gather, cpu_bitmap_union=cpu_bitmap_union, cpu_native_gather=cpu_native_gather,
             direct_attention_layout=direct_attention_layout, early_gpu_metadata=early_gpu_metadata,
             gather_h2d_chunks=gather_h2d_chunks, reuse_quant_metadata=reuse_quant_metadata,
@@ -314,6 +430,9 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
             state.update(desired=None, allocated=None, head_bits=None, pages=None)
             return state
         pmin, pmax = self._metadata(entries, cand)
+        if R > 8:
+            state.update(self._select_heads_split(entries, q, old_length, pmin, pmax, b0, fixed))
+            return state
         N = b0 * self.block_size
         sel = torch.empty((G, R, b0), dtype=torch.int32, device=self.device)
         width = min(cand, R * b0)
@@ -340,6 +459,82 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         self._phase_end("twilight_top_p_union", start)
         state.update(desired=desired, allocated=allocated, head_bits=head_bits, pages=sel, logits=logits)
         return state
+
+    def _select_heads_split(self, entries: Sequence[int], q: torch.Tensor, old_length: int, pmin: torch.Tensor,
+                            pmax: torch.Tensor, b0: int, fixed: int) -> dict:
+        """Both stages for more than 8 query heads per KV head: the kernels
+        take at most 8 heads per group, so the heads run in sub-groups of at
+        most 8.  Each head's B0 pages, logits and top-p count depend on that
+        head alone, so they are the same as in one call.  Matched budgets are
+        shared by all R heads of a group (twilight_offload_cache.py:50-86):
+        the desired counts of every sub-group are gathered, allocated over the
+        R heads with matched_budget_counts, and each sub-group then keeps its
+        heads' given allocations.  The group's union is the sorted union of
+        the sub-groups' unions (each holds the sink and recent windows)."""
+        G, R = q.shape[0], q.shape[1]
+        bs, dev = self.block_size, self.device
+        N = b0 * bs
+        bounds = kernels.head_chunks(R)
+        n_sub = len(bounds)
+        packed, qscale, qmin = self._quant(entries)
+        sel = torch.empty((G, R, b0), dtype=torch.int32, device=dev)
+        logits = torch.empty((G, R, N), dtype=torch.float32, device=dev)
+        desired = torch.empty((G, R), dtype=torch.int32, device=dev)
+        allocated = torch.empty((G, R), dtype=torch.int32, device=dev)
+        head_bits = torch.empty((G, R, (N + 31) // 32), dtype=torch.int32, device=dev)
+        sub_rows, sub_counts = [], []
+        for r0, r1 in bounds:
+            qs = q[:, r0:r1].contiguous()
+            width = min(pmin.shape[1], (r1 - r0) * b0)
+            sel_s = torch.empty((G, r1 - r0, b0), dtype=torch.int32, device=dev)
+            plan_pages = torch.empty((G, width), dtype=torch.int32, device=dev)
+            plan_masks = torch.empty((G, width), dtype=torch.uint8, device=dev)
+            plan_counts = torch.empty((G,), dtype=torch.int32, device=dev)
+            kernels.quest_select(qs, pmin, pmax, b0, sel_pages=sel_s, plan_pages=plan_pages, plan_masks=plan_masks,
+                                 plan_counts=plan_counts)
+            lg = kernels.twilight_qk(qs, packed, qscale, qmin, plan_pages, plan_masks, plan_counts, b0,
+                                     sink=self.sink_tokens, block_size=bs)
+            sel[:, r0:r1] = sel_s
+            logits[:, r0:r1] = lg
+            rows_s = torch.empty((G, old_length + 1), dtype=torch.int32, device=dev)
+            counts_s = torch.empty((G,), dtype=torch.int32, device=dev)
+            des_s = torch.empty((G, r1 - r0), dtype=torch.int32, device=dev)
+            bits_s = torch.empty((G, r1 - r0, (N + 31) // 32), dtype=torch.int32, device=dev)
+            kernels.twilight_select(lg, sel_s, top_p=self.top_p, budget_mode="dynamic", rows=rows_s,
+                                    row_counts=counts_s, desired=des_s, head_bits=bits_s, sink=self.sink_tokens,
+                                    recent=self.recent_tokens, block_size=bs, length=old_length)
+            desired[:, r0:r1] = des_s
+            head_bits[:, r0:r1] = bits_s
+            sub_rows.append(rows_s)
+            sub_counts.append(counts_s)
+        if self.budget_mode == "matched":
+            des_host = desired.cpu().tolist()
+            alloc = [matched_budget_counts(d, fixed * bs * R, [N] * R) for d in des_host]
+            allocated.copy_(torch.tensor(alloc, dtype=torch.int32))
+            sub_rows, sub_counts = [], []
+            for r0, r1 in bounds:
+                rows_s = torch.empty((G, old_length + 1), dtype=torch.int32, device=dev)
+                counts_s = torch.empty((G,), dtype=torch.int32, device=dev)
+                bits_s = torch.empty((G, r1 - r0, (N + 31) // 32), dtype=torch.int32, device=dev)
+                kernels.twilight_select(logits[:, r0:r1].contiguous(), sel[:, r0:r1].contiguous(), top_p=self.top_p,
+                                        budget_mode="given", rows=rows_s, row_counts=counts_s,
+                                        allocated=allocated[:, r0:r1].contiguous(), head_bits=bits_s,
+                                        sink=self.sink_tokens, recent=self.recent_tokens, block_size=bs,
+                                        length=old_length)
+                head_bits[:, r0:r1] = bits_s
+                sub_rows.append(rows_s)
+                sub_counts.append(counts_s)
+        else:
+            allocated.copy_(desired)
+        rows = torch.empty((G, old_length + 1), dtype=torch.int32, device=dev)
+        counts = torch.empty((G,), dtype=torch.int32, device=dev)
+        counts_host = torch.stack(sub_counts).cpu()
+        for g in range(G):
+            merged = torch.unique(torch.cat([sub_rows[i][g, :int(counts_host[i, g])] for i in range(n_sub)]))
+            rows[g, :merged.numel()] = merged
+            counts[g] = merged.numel()
+        return dict(desired=desired, allocated=allocated, head_bits=head_bits, pages=sel, logits=logits, rows=rows,
+                    counts=counts)
 
     def _quant(self, entries: Sequence[int]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         assert self._packed is not None and self._qscale is not None and self._qmin is not None
@@ -407,7 +602,8 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
             kernels.gather_union(self._key_rows, self._value_rows, state["rows"], state["counts"], cur_k, cur_v,
                                  self._flat_union_keys.view(-1, D), self._flat_union_values.view(-1, D), cu,
                                  entry_row0=self.geometry.row(entries[0], 0),
-                                 entry_row_step=self.geometry.max_cache_len, max_count=state["max_count"])
+                                 entry_row_step=self.geometry.max_cache_len, max_count=state["max_count"],
+                                 error_flag=self._gather_error)
         else:
             raise ValueError("GQA group execution needs the consecutive entries of one layer")
         self._phase_end("gather", start)
@@ -517,7 +713,8 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         src = torch.cat([p + row0 for p in positions])
         dst = torch.cat([torch.arange(n, device=self.device, dtype=torch.int64) * R + r
                          for r, n in enumerate(lengths)])
-        kernels.gather_rows(self._key_rows, self._value_rows, src, self._pack_rows_k, self._pack_rows_v, dst)
+        kernels.gather_rows(self._key_rows, self._value_rows, src, self._pack_rows_k, self._pack_rows_v, dst,
+                            error_flag=self._gather_error)
         cur_k = key_states[0, 0].contiguous()
         cur_v = value_states[0, 0].contiguous()
         for r, n in enumerate(lengths):
@@ -562,7 +759,8 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
             self._flat_values = torch.empty_like(self._flat_keys)
         assert self._flat_values is not None
         fk, fv = self._flat_keys.view(-1, D), self._flat_values.view(-1, D)
-        kernels.gather_rows(self._key_rows, self._value_rows, torch.cat(srcs), fk, fv, torch.cat(dsts))
+        kernels.gather_rows(self._key_rows, self._value_rows, torch.cat(srcs), fk, fv, torch.cat(dsts),
+                            error_flag=self._gather_error)
         cur_k = torch.cat([k[0, 0] for k in key_states], dim=0).contiguous()
         cur_v = torch.cat([v[0, 0] for v in value_states], dim=0).contiguous()
         rows = torch.tensor(tok_rows, device=dev)
