@@ -160,6 +160,24 @@ int tw_quest_select(const float* q, const void* page_min, const void* page_max, 
                     int64_t rows_stride, int sink, int recent, int block_size, int length,
                     int append_position, void* workspace, size_t workspace_bytes, void* stream);
 
+/* tw_quest_select with no workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc.  No counterpart in the reference.  The
+ * workspace is a static device array of tw_quest_select_static_capacity()
+ * bytes (16 MiB) that each GPU holds until the process ends; a call whose
+ * tw_quest_select_workspace_size(G, R, P) exceeds it returns TW_ENOMEM.  The
+ * first call on a device takes the array's address and enqueues a zero fill
+ * (a kernel, capture-safe) ahead of its own kernels; nothing is allocated.
+ * Every call on one GPU shares the array: calls that overlap in time on one
+ * GPU race (issue them on one stream).  Outputs and validation are those of
+ * tw_quest_select. */
+size_t tw_quest_select_static_capacity(void);
+int tw_quest_select_static(const float* q, const void* page_min, const void* page_max, int dtype, int G, int R,
+                           int P, int D, int64_t page_group_stride, int k, float* scores, int32_t* sel_pages,
+                           int32_t* plan_pages, uint8_t* plan_masks, int32_t* plan_counts, int64_t plan_stride,
+                           int32_t* rows, uint8_t* row_masks, int32_t* row_counts, int64_t rows_stride, int sink,
+                           int recent, int block_size, int length, int append_position, void* stream);
+
 /* Ragged groups: tw_quest_select's score, top-k and union plan for G groups
  * of different lengths in one launch pair (e.g. the KV heads of several
  * requests at one layer).  lengths [G] (int32, device) gives each group's

@@ -36,6 +36,8 @@
 //    expanded row plan (sink ++ union page rows ++ recent ++ decode row).
 #pragma clang fp contract(off)
 
+#include <mutex>
+
 #include "select.h"
 
 namespace tw {
@@ -853,4 +855,92 @@ extern "C" int tw_quest_select_ragged(const float* q, const void* page_min, cons
   const int rc = tw::dispatch_score(dtype, a, st);
   if (rc != TW_OK) return rc;
   return tw::launch_select(s, G * R, true, st);
+}
+
+// ---------------------------------------------------------------------------
+// tw_quest_select_static: tw_quest_select for callers that cannot allocate
+// (code under graph capture, serving loops that forbid hipMalloc).  The
+// workspace -- arrival counters, scores, selections -- lives in `scratch`, a
+// file-scope device array of kStaticScratchBytes that every GPU the library
+// runs on holds until the process ends.  In host code `scratch` names a
+// host-side stand-in, not device memory: its device address is taken with
+// hipGetSymbolAddress once per device (the first call on that device, with
+// that device current) and only that address is ever passed to kernels.
+// Calls on one device share the array: two calls that overlap in time on one
+// GPU race.
+namespace {
+
+constexpr size_t kStaticScratchBytes = size_t{16} << 20;  // 16 MiB
+constexpr int kMaxStaticDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxStaticDevices] = {};
+bool g_scratch_zeroed[kMaxStaticDevices] = {};
+
+// Zero every byte of the array on its first use on a device: the arrival
+// counters must start at zero (the selection kernels leave them zero after
+// every call).  A kernel, not a memset node, so a captured graph replays it
+// correctly.
+__global__ __launch_bounds__(256) void zero_scratch_kernel(uint4* p, size_t n16) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n16;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The device address of `scratch` on the current device, set up on the first
+// call there.  Until a zero fill has been enqueued outside graph capture, every
+// call enqueues one on `stream` ahead of its kernels (a fill captured into a
+// graph runs only when the graph replays).
+int static_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return tw_host::record_hip_error(err);
+  if (dev < 0 || dev >= kMaxStaticDevices) return TW_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return tw_host::record_hip_error(err);
+    if (p == nullptr) return TW_EHIP;
+    g_scratch_ptr[dev] = p;
+  }
+  if (!g_scratch_zeroed[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    err = hipStreamIsCapturing(stream, &cs);
+    if (err != hipSuccess) return tw_host::record_hip_error(err);
+    hipLaunchKernelGGL(zero_scratch_kernel, dim3(1024), dim3(256), 0, stream,
+                       static_cast<uint4*>(g_scratch_ptr[dev]), kStaticScratchBytes / 16);
+    const int rc = tw_host::check_launch();
+    if (rc != TW_OK) return rc;
+    g_scratch_zeroed[dev] = cs == hipStreamCaptureStatusNone;
+  }
+  *out = g_scratch_ptr[dev];
+  return TW_OK;
+}
+
+}  // namespace
+
+extern "C" size_t tw_quest_select_static_capacity(void) { return kStaticScratchBytes; }
+
+extern "C" int tw_quest_select_static(const float* q, const void* page_min, const void* page_max, int dtype, int G,
+                                      int R, int P, int D, int64_t page_group_stride, int k, float* scores,
+                                      int32_t* sel_pages, int32_t* plan_pages, uint8_t* plan_masks,
+                                      int32_t* plan_counts, int64_t plan_stride, int32_t* rows, uint8_t* row_masks,
+                                      int32_t* row_counts, int64_t rows_stride, int sink, int recent,
+                                      int block_size, int length, int append_position, void* stream) {
+  const size_t need = tw_quest_select_workspace_size(G, R, P);
+  if (need == 0) return TW_EINVAL;
+  if (need > kStaticScratchBytes) return TW_ENOMEM;  // beyond the static array: use tw_quest_select
+  void* ws = nullptr;
+  const int rc = static_scratch(static_cast<hipStream_t>(stream), &ws);
+  if (rc != TW_OK) return rc;
+  return tw_quest_select(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, k, scores, sel_pages,
+                         plan_pages, plan_masks, plan_counts, plan_stride, rows, row_masks, row_counts, rows_stride,
+                         sink, recent, block_size, length, append_position, ws, kStaticScratchBytes, stream);
 }

@@ -64,6 +64,9 @@ _HIP_SIGNATURES = {
     "tw_quest_select_workspace_size": (szt, [i32, i32, i32]),
     "tw_quest_select": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, i32, vp, vp, vp, vp, vp, i64, vp, vp, vp, i64,
                               i32, i32, i32, i32, i32, vp, szt, vp]),
+    "tw_quest_select_static_capacity": (szt, []),
+    "tw_quest_select_static": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, i32, vp, vp, vp, vp, vp, i64, vp, vp,
+                                     vp, i64, i32, i32, i32, i32, i32, vp]),
     "tw_decode_attention_workspace_size": (szt, [i32, i32, i32, i32]),
     "tw_decode_attention": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i64, vp, i32, i32, i32, vp, vp,
                                   f32, vp, vp, szt, vp]),
