@@ -30,6 +30,7 @@ __all__ = [
     "from_f32",
     "build_page_metadata",
     "int4_dequantize",
+    "qfix",
     "quest_score",
     "topk_sorted",
     "quest_row_plan",
@@ -77,6 +78,8 @@ def lib() -> ctypes.CDLL:
         L.or_quest_row_plan.argtypes = [vp, i32, i32, i32, i32, i32, i32, i32, i32, vp, vp]
         L.or_det_exp.restype = ctypes.c_float
         L.or_det_exp.argtypes = [ctypes.c_float]
+        L.or_qfix.restype = i32
+        L.or_qfix.argtypes = [vp, i32, vp, vp, vp]
         L.or_int4_qk.restype = None
         L.or_int4_qk.argtypes = [vp, i32, vp, vp, vp, i32, vp, i32, ctypes.c_float, vp]
         L.or_top_p_count.restype = i32
@@ -259,9 +262,22 @@ def det_exp(x: float) -> float:
     return float(lib().or_det_exp(float(np.float32(x))))
 
 
+def qfix(q: np.ndarray) -> tuple[np.ndarray, int, int, bool]:
+    """Fixed-point form of a query head: (Q [D] int32, sum Q, shift, finite)
+    with q~ = Q * 2^shift (see or_qfix)."""
+    q = np.ascontiguousarray(q, np.float32)
+    Q = np.zeros(q.shape[0], np.int32)
+    qs = ctypes.c_int32()
+    ok = ctypes.c_int()
+    shift = lib().or_qfix(_ptr(q), q.shape[0], _ptr(Q), ctypes.byref(qs), ctypes.byref(ok))
+    return Q, int(qs.value), int(shift), bool(ok.value)
+
+
 def int4_qk(q: np.ndarray, packed: np.ndarray, scale: np.ndarray, minimum: np.ndarray, dtype: str,
             rows: np.ndarray, qk_scale: float) -> np.ndarray:
-    """INT4 QK estimate of one query head q [D] over candidate rows."""
+    """INT4 QK estimate of one query head q [D] over candidate rows: the
+    exact integer dot of the codes with q's fixed-point form, then
+    qk_scale * (scale * dot + min * sum q~) in fp32 (see or_int4_qk)."""
     q = np.ascontiguousarray(q, np.float32)
     packed = np.ascontiguousarray(packed, np.uint8)
     rows = np.ascontiguousarray(rows, np.int64)

@@ -302,36 +302,71 @@ float or_det_exp(float x) {
   return ldexpf(p, (int)n);
 }
 
+/* Fixed-point form of one query head for the INT4 QK estimate:
+ * M = max_d |q_d|, E the exponent of M (M = f * 2^E, f in [0.5, 1)), and
+ * Q_d = round_half_even(q_d * 2^(22 - E)), so |Q_d| <= 2^22.  Returns the
+ * shift E - 22 that scales an integer dot product back, with *qs = sum_d Q_d;
+ * *ok = 0 when a q_d is not finite (the estimate is then NaN); M = 0 gives
+ * Q = 0 and shift 0. */
+int or_qfix(const float* q, int D, int32_t* Q, int32_t* qs, int* ok) {
+  float M = 0.0f;
+  *ok = 1;
+  for (int d = 0; d < D; ++d) {
+    if (!isfinite(q[d])) *ok = 0;
+    const float a = fabsf(q[d]);
+    M = a > M ? a : M;
+  }
+  int32_t sum = 0;
+  if (!*ok || M == 0.0f) {
+    for (int d = 0; d < D; ++d) Q[d] = 0;
+    *qs = 0;
+    return 0;
+  }
+  int E = 0;
+  (void)frexpf(M, &E);
+  for (int d = 0; d < D; ++d) {
+    Q[d] = (int32_t)rintf(ldexpf(q[d], 22 - E));
+    sum += Q[d];
+  }
+  *qs = sum;
+  return E - 22;
+}
+
 /* INT4 QK estimate of one query head (twilight_fused_qk.py:12-55,
- * twilight_offload_cache.py:1197-1261) in this build's defined order:
- *   k_d = f32(code_d) * f32(scale) + f32(min)            (dequantize, :40-47)
- *   acc_j = sum_{i<8} k_{8j+i} * q_{8j+i}, sequential fused multiply-adds from +0
- *   (j = 0..ceil(D/8)-1,
- *   the one chunk of D < 8 channels is partial)
- *   dot = adjacent-pair tree over the acc_j
- *   logit = dot * qk_scale   (qk_scale = fp32(1/sqrt(D)))
- * rows[n] selects the packed row of candidate n.  D = 4 .. 256, a power of two. */
+ * twilight_offload_cache.py:1197-1261) in this build's defined arithmetic.
+ * The reference dequantizes k_d = f32(code_d) * f32(scale) + f32(min)
+ * (:40-47) and reduces k . q in an unpinned fp32 order (cuBLAS / tl.sum).
+ * Here the dot product is exact: with q in the fixed-point form of or_qfix,
+ *   S = sum_d code_d * Q_d                      (exact integer, int64)
+ *   dotc = ldexp(f32(S), shift), qsum = ldexp(f32(sum_d Q_d), shift)
+ *   logit = qk_scale * ((scale * dotc) + (min * qsum))   (each op rounded)
+ * which is sum_d (code_d * scale + min) * q~_d for q~ = Q * 2^shift, with
+ * one rounding per fp32 operation.  rows[n] selects the packed row of
+ * candidate n (low nibble = even channel).  D = 4 .. 256, a power of two. */
 void or_int4_qk(const float* q, int D, const uint8_t* packed, const void* scale, const void* minimum, int dt,
                 const int64_t* rows, int N, float qk_scale, float* out) {
-  float acc[64];
+  int32_t Q[256];
+  int32_t qs = 0;
+  int ok = 1;
+  const int shift = or_qfix(q, D, Q, &qs, &ok);
+  const float qsum = ldexpf((float)qs, shift);
   for (int n = 0; n < N; ++n) {
     const int64_t t = rows[n];
-    const float s = load_f(scale, t, dt), m = load_f(minimum, t, dt);
-    const int chunks = (D + 7) / 8; /* the last chunk is partial when D < 8 */
-    for (int j = 0; j < chunks; ++j) {
-      float a = 0.0f;
-      for (int i = 0; i < 8 && 8 * j + i < D; ++i) {
-        const int d = 8 * j + i;
-        const uint32_t b = packed[t * (D / 2) + d / 2];
-        const uint32_t code = (d & 1) ? (b >> 4) & 15u : b & 15u;
-        const float k = (float)code * s + m;
-        a = fmaf(k, q[d], a);
-      }
-      acc[j] = a;
+    if (!ok) {
+      out[n] = u2f(0x7fc00000u);
+      continue;
     }
-    for (int w = 1; w < chunks; w <<= 1)
-      for (int j = 0; j + w < chunks; j += 2 * w) acc[j] = acc[j] + acc[j + w];
-    out[n] = acc[0] * qk_scale;
+    const float s = load_f(scale, t, dt), m = load_f(minimum, t, dt);
+    int64_t S = 0;
+    for (int d = 0; d < D; ++d) {
+      const uint32_t b = packed[t * (D / 2) + d / 2];
+      const uint32_t code = (d & 1) ? (b >> 4) & 15u : b & 15u;
+      S += (int64_t)code * Q[d];
+    }
+    const float dotc = ldexpf((float)S, shift);
+    const float a = s * dotc;
+    const float c = m * qsum;
+    out[n] = qk_scale * (a + c);
   }
 }
 

@@ -293,10 +293,9 @@ def test_top_p_count_closed_forms():
     assert oracle.top_p_threshold(3, 1.0) == 3
 
 
-def _int4_qk_crafted(values: dict[int, float], q_of: dict[int, float]) -> float:
-    """One candidate whose dequantized channel d is values[d] exactly
-    (scale 1, minimum 0, codes = values), against q."""
-    D = 64
+def _int4_qk_crafted(values: dict[int, int], q_of: dict[int, float], scale: float = 1.0,
+                     minimum: float = 0.0, D: int = 64) -> float:
+    """One candidate with codes `values` (others 0), fp32 scale/minimum, against q."""
     codes = np.zeros(D, np.int64)
     for d, v in values.items():
         codes[d] = int(v)
@@ -304,29 +303,41 @@ def _int4_qk_crafted(values: dict[int, float], q_of: dict[int, float]) -> float:
     q = np.zeros(D, np.float32)
     for d, v in q_of.items():
         q[d] = v
-    one = np.float32([1.0])
-    zero = np.float32([0.0])
-    return float(oracle.int4_qk(q, packed, one, zero, "f32", np.zeros(1, np.int64), 1.0)[0])
+    return float(oracle.int4_qk(q, packed, np.float32([scale]), np.float32([minimum]), "f32",
+                                np.zeros(1, np.int64), 1.0)[0])
 
 
-def test_int4_qk_defined_order():
-    """logit = qk_scale * tree(chunk sums), chunk j = sum_{i<8} k_{8j+i} q_{8j+i}
-    as sequential fused multiply-adds.  With terms 1, 2^24, -2^24 the result
-    depends on the order."""
-    big = float(2 ** 24)
-    # inside one chunk, sequential: fma(1, 2^24, 1) = 2^24 + 1 rounds to 2^24 (ties to even),
-    # then fma(1, -2^24, 2^24) = 0 (a pairwise sum gives 1)
-    assert _int4_qk_crafted({0: 1, 2: 1, 3: 1}, {0: 1.0, 2: big, 3: -big}) == 0.0
-    # across chunks 0, 2, 3: tree (c0 + c1) + (c2 + c3) = 1 (a sequential sum over chunks gives 0)
-    assert _int4_qk_crafted({0: 1, 16: 1, 24: 1}, {0: 1.0, 16: big, 24: -big}) == 1.0
-    # fused, not a rounded product then a sum: after -3, fma(3, 1 + 2^-23, -3) is 3 * 2^-23
-    # exactly, while fl(3 * (1 + 2^-23)) - 3 is a multiple of 2^-22
-    u = 1.0 + 2.0 ** -23
-    qv = {0: -1.0, 1: u}
-    assert _int4_qk_crafted({0: 3, 1: 3}, qv) == float(np.float32(3 * 2.0 ** -23))
+def test_qfix_closed_forms():
+    """q~ = Q * 2^(E - 22), E the frexp exponent of max |q|, Q rounded half to even."""
+    Q, qs, shift, ok = oracle.qfix(np.float32([1.0, -0.5, 0.0, 2.0 ** -30]))
+    assert ok and shift == 1 - 22 and Q.tolist() == [2 ** 21, -(2 ** 20), 0, 0] and qs == 2 ** 21 - 2 ** 20
+    Q, _, shift, _ = oracle.qfix(np.float32([3.0, 2.5 * 2.0 ** -20, 3.5 * 2.0 ** -20]))   # E = 2: x 2^20
+    assert shift == -20 and Q.tolist() == [3 * 2 ** 20, 2, 4]                             # 2.5 -> 2, 3.5 -> 4
+    Q, qs, shift, ok = oracle.qfix(np.zeros(8, np.float32))
+    assert ok and qs == 0 and shift == 0 and not Q.any()
+    assert not oracle.qfix(np.float32([1.0, np.nan]))[3] and not oracle.qfix(np.float32([np.inf, 0.0]))[3]
 
 
-@pytest.mark.parametrize("dtype,D", [("bf16", 128), ("f16", 64), ("f32", 256)])
+def test_int4_qk_defined_arithmetic():
+    """logit = qk_scale * ((scale * ldexp(S, shift)) + (min * ldexp(sum Q, shift))),
+    S = sum code * Q exact.  Each case separates the definition from a
+    plausible variant."""
+    # S = 15 * 128 * 2^21 > 2^31: an int32 accumulator would wrap
+    assert _int4_qk_crafted({d: 15 for d in range(128)}, {d: 1.0 for d in range(128)}, D=128) == 1920.0
+    # Q rounds half to even: q_1 * 2^21 = 2.5 -> 2 (half away from zero gives 3)
+    assert _int4_qk_crafted({1: 1}, {0: 1.0, 1: 2.5 * 2.0 ** -21}) == 2 * 2.0 ** -21
+    # the exponent is frexp's (max |q| = 1 -> E = 1, q x 2^21): q_1 = 1.25 * 2^-22 -> Q_1 = 1,
+    # i.e. 2^-21 (scaling by 2^22 would give 2^-22)
+    assert _int4_qk_crafted({1: 1}, {0: 1.0, 1: 1.25 * 2.0 ** -22}) == 2.0 ** -21
+    # two rounded products then a rounded sum (a fused multiply-add gives 2^-22 + 2^-43)
+    got = _int4_qk_crafted({0: 1, 1: 1}, {0: 1.0, 1: 2.0 ** -21}, scale=1.0 + 2.0 ** -22, minimum=-1.0)
+    assert got == 2.0 ** -22
+    # a non-finite query gives NaN, an all-zero query the minimum times zero
+    assert math.isnan(_int4_qk_crafted({0: 3}, {0: float("inf")}))
+    assert _int4_qk_crafted({0: 3}, {}, scale=2.0, minimum=5.0) == 0.0
+
+
+@pytest.mark.parametrize("dtype,D", [("bf16", 128), ("f16", 64), ("f32", 256), ("bf16", 4)])
 def test_int4_qk_close_to_float64_and_one_hot_exact(dtype, D):
     x = (RNG.standard_normal((300, D)) * 2).astype(np.float32)
     keys = oracle.from_f32(x, dtype)
@@ -338,8 +349,10 @@ def test_int4_qk_close_to_float64_and_one_hot_exact(dtype, D):
     got = oracle.int4_qk(q, packed, scale, minimum, dtype, rows, float(qs))
     want = deq[rows] @ q.astype(np.float64) * float(qs)
     mag = np.abs(deq[rows]) @ np.abs(q.astype(np.float64)) * float(qs)
-    assert np.all(np.abs(got - want) <= 2e-6 * mag + 1e-30)
-    for d in (0, D // 2 + 3, D - 1):
+    # q~ differs from q by at most 2^(E-23) <= 2^-22 max|q| per channel
+    qerr = np.abs(deq[rows]).sum(axis=1) * float(np.abs(q).max()) * 2.0 ** -22 * float(qs)
+    assert np.all(np.abs(got - want) <= qerr + 4e-7 * mag + 1e-30)
+    for d in (0, D // 2 + 1, D - 1):
         e = np.zeros(D, np.float32)
         e[d] = 1.0
         got = oracle.int4_qk(e, packed, scale, minimum, dtype, rows, float(qs))

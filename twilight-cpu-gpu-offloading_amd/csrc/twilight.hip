@@ -9,9 +9,9 @@
 //
 // Orders this build defines (the reference's are unpinned: cuBLAS / tl.sum
 // reductions, argsort ties, fp32 cumsum rounding):
-//   * logit = dot * qk_scale, dot = adjacent-pair tree over D/8 chunk sums,
-//     chunk sum = sum_{i<8} k_{8j+i} q_{8j+i} as sequential fused multiply-adds
-//     from +0, k = code*scale+min (a multiply, then an add);
+//   * logit = qk_scale * ((scale * dot) + (min * qsum)) with dot the exact
+//     integer sum of code * Q over q's fixed-point form Q (22 fraction bits
+//     below max |q|), scaled back by a power of two (see the INT4 QK section);
 //   * candidate order = ascending token position (B0 pages ascending);
 //   * top-p: masses E_i = floor(det_exp(l_i - max l) * 2^40), exact integer
 //     sums; desired = smallest c whose c largest logits (ties to the lower
@@ -33,6 +33,20 @@ using namespace sel;
 constexpr int kQkPagesPerBlock = 16;
 
 // ------------------------------------------------------------ INT4 QK
+// The estimate is exact integer arithmetic followed by three fp32 steps.  A
+// query head is first put in fixed point: M = max_d |q_d|, E the exponent of
+// M (M = f * 2^E, f in [0.5, 1)), Q_d = rint(q_d * 2^(22 - E)), so
+// |Q_d| <= 2^22 (a NaN or infinite q_d makes the head's logits NaN, M = 0
+// gives Q = 0).  Then for every candidate row
+//   S = sum_d code_d * Q_d                                  (exact, 64-bit)
+//   logit = qk_scale * ((scale * ldexp(S, E - 22)) + (min * ldexp(sum_d Q_d, E - 22)))
+// Q_d is split into three byte slices, Q = h * 2^16 + m * 2^8 + l with h
+// signed (|h| <= 64) and m, l unsigned, and every slice meets the codes in
+// v_dot4 instructions: the codes of 8 channels are one 32-bit word whose even
+// channels (w & 0x0f0f0f0f) and odd channels ((w >> 4) & 0x0f0f0f0f) are four
+// bytes each, dotted with the matching bytes of a slice.  The sums are
+// integers, so neither the lane layout nor the summation order changes a bit
+// of the result.
 struct QkArgs {
   const float* q;             // [G][R][D]
   const uint8_t* packed;      // entry g row t at + (g*qstride + t)*D/2
@@ -50,185 +64,434 @@ struct QkArgs {
   float* logits;              // [G][R][b0*bs]
 };
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+// Sums / maxima over aligned groups of N lanes (N = 1..16, a power of two);
+// every lane of a group receives the result.
+template <int N>
+__device__ __forceinline__ int group_sum_i32(int x) {
+  if constexpr (N >= 2) x += static_cast<int>(dpp_u32<kDppQuadXor1>(static_cast<uint32_t>(x)));
+  if constexpr (N >= 4) x += static_cast<int>(dpp_u32<kDppQuadXor2>(static_cast<uint32_t>(x)));
+  if constexpr (N >= 8) x += static_cast<int>(dpp_u32<kDppRowHalfMirror>(static_cast<uint32_t>(x)));
+  if constexpr (N >= 16) x += static_cast<int>(dpp_u32<kDppRowMirror>(static_cast<uint32_t>(x)));
+  return x;
+}
+template <int N>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t x) {
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  if constexpr (N >= 2) x = mx(x, dpp_u32<kDppQuadXor1>(x));
+  if constexpr (N >= 4) x = mx(x, dpp_u32<kDppQuadXor2>(x));
+  if constexpr (N >= 8) x = mx(x, dpp_u32<kDppRowHalfMirror>(x));
+  if constexpr (N >= 16) x = mx(x, dpp_u32<kDppRowMirror>(x));
+  if constexpr (N >= 32) x = mx(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), 16)));
+  if constexpr (N >= 64) x = mx(x, static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), 32)));
+  return x;
+}
+template <int N>
+__device__ __forceinline__ int group_sum_wide_i32(int x) {
+  x = group_sum_i32<(N < 16 ? N : 16)>(x);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32);
+  return x;
 }
 
-// One INT4 row shared by LPR lanes, CPL channels (CPL/2 code bytes) each:
-// CPL = min(D, 8), so D = 4 .. 256 (a power of two) maps to 1 .. 32 lanes.
-template <int DIM>
-struct Int4Row {
-  static constexpr int CPL = DIM < 8 ? DIM : 8;
+// Lane layout of one INT4 row: LPR lanes per row, each owning CPL consecutive
+// channels, i.e. CPL / 2 code bytes in WPL 32-bit words (a half word when
+// CPL = 4).
+template <int DIM, int CPLMAX>
+struct QkLane {
+  static constexpr int CPL = DIM < CPLMAX ? DIM : CPLMAX;
   static constexpr int LPR = DIM / CPL;
-  static constexpr int RPI = kWave / LPR;  // rows per wavefront instruction
-  static_assert(CPL >= 2 && LPR * CPL == DIM && (LPR & (LPR - 1)) == 0, "unsupported head dim");
+  static constexpr int RPW = kWave / LPR;  // rows per wavefront instruction
+  static constexpr int WPL = CPL >= 8 ? CPL / 8 : 1;
+  static_assert(CPL >= 4 && LPR * CPL == DIM && (LPR & (LPR - 1)) == 0 && LPR <= 16, "unsupported head dim");
 
-  __device__ static __forceinline__ uint32_t codes(const uint8_t* row, int c0) {
-    if constexpr (CPL == 8) return *reinterpret_cast<const uint32_t*>(row + c0 / 2);
-    else if constexpr (CPL == 4) return *reinterpret_cast<const uint16_t*>(row + c0 / 2);
-    else return row[c0 / 2];
-  }
-  __device__ static __forceinline__ void query(const float* qr, float (&q)[8]) {
-    if constexpr (CPL == 8) {
-      const float4 x = reinterpret_cast<const float4*>(qr)[0];
-      const float4 y = reinterpret_cast<const float4*>(qr)[1];
-      q[0] = x.x; q[1] = x.y; q[2] = x.z; q[3] = x.w;
-      q[4] = y.x; q[5] = y.y; q[6] = y.z; q[7] = y.w;
+  __device__ static __forceinline__ void codes(const uint8_t* row, int c0, uint32_t (&w)[4]) {
+    const uint8_t* p = row + c0 / 2;
+    if constexpr (CPL == 32) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p);
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else if constexpr (CPL == 16) {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      w[0] = v.x; w[1] = v.y; w[2] = 0u; w[3] = 0u;
+    } else if constexpr (CPL == 8) {
+      w[0] = *reinterpret_cast<const uint32_t*>(p); w[1] = 0u; w[2] = 0u; w[3] = 0u;
     } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) q[j] = j < CPL ? qr[j] : 0.0f;
+      w[0] = *reinterpret_cast<const uint16_t*>(p); w[1] = 0u; w[2] = 0u; w[3] = 0u;
     }
-  }
-  // Sequential fused multiply-adds over the lane's CPL channels, then the adjacent-pair tree
-  // over the row's LPR lane sums (every lane of the row gets the result).
-  __device__ static __forceinline__ float dot(const float (&k)[8], const float (&q)[8]) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) acc = __builtin_fmaf(k[j], q[j], acc);
-    if constexpr (LPR >= 2) acc = acc + dpp_f32<kDppQuadXor1>(acc);
-    if constexpr (LPR >= 4) acc = acc + dpp_f32<kDppQuadXor2>(acc);
-    if constexpr (LPR >= 8) acc = acc + dpp_f32<kDppRowHalfMirror>(acc);
-    if constexpr (LPR >= 16) acc = acc + dpp_f32<kDppRowMirror>(acc);
-    if constexpr (LPR >= 32) acc = acc + __shfl_xor(acc, 16);
-    return acc;
-  }
-  __device__ static __forceinline__ void dequant(uint32_t w, float s, float m, float (&k)[8]) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) k[j] = j < CPL ? static_cast<float>((w >> (4 * j)) & 15u) * s + m : 0.0f;
   }
 };
 
-template <typename DT, int DIM, int RMAX>
+// One query head in fixed point, as the byte slices of the lane's CPL
+// channels laid out like its code words: [word][0] even channels, [1] odd.
+template <int CPL, int LPR>
+struct QFix {
+  static constexpr int WPL = CPL >= 8 ? CPL / 8 : 1;
+  uint32_t hs[WPL][2], ms[WPL][2], ls[WPL][2];
+  int shift;
+  float qsum;  // ldexp(sum_d Q_d, shift), the same in every lane
+  bool ok;
+
+  // qr: the head's D channels; c0: the lane's first channel.  Every lane of
+  // a row group must call it (group reductions).
+  __device__ __forceinline__ void init(const float* qr, int c0) {
+    float v[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; i += 4) *reinterpret_cast<float4*>(v + i) = *reinterpret_cast<const float4*>(qr + c0 + i);
+    uint32_t mx = 0u, bad = 0u;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const uint32_t u = f32_as_u32(v[i]) & 0x7fffffffu;
+      bad |= u >= 0x7f800000u ? 1u : 0u;
+      mx = u > mx ? u : mx;
+    }
+    mx = group_max_u32<LPR>(mx);
+    bad = group_max_u32<LPR>(bad);
+    ok = bad == 0u;
+    const float M = u32_as_f32(mx);
+    int E = 22;
+    if (ok && M != 0.0f) (void)frexpf(M, &E);
+    shift = (ok && M != 0.0f) ? E - 22 : 0;
+    int q_int[CPL];
+    int part = 0;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      q_int[i] = (ok && M != 0.0f) ? static_cast<int>(rintf(ldexpf(v[i], 22 - E))) : 0;
+      part += q_int[i];
+    }
+    qsum = ldexpf(static_cast<float>(group_sum_i32<LPR>(part)), shift);
+#pragma unroll
+    for (int w = 0; w < WPL; ++w) {
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+        uint32_t h = 0u, m = 0u, l = 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = 8 * w + 2 * j + par;
+          if (i < CPL) {
+            const int Q = q_int[i];
+            h |= (static_cast<uint32_t>(Q >> 16) & 255u) << (8 * j);
+            m |= (static_cast<uint32_t>(Q >> 8) & 255u) << (8 * j);
+            l |= (static_cast<uint32_t>(Q) & 255u) << (8 * j);
+          }
+        }
+        hs[w][par] = h;
+        ms[w][par] = m;
+        ls[w][par] = l;
+      }
+    }
+  }
+
+  // The head's slices for the lane's channels from a block's staged form
+  // (stage_qfix): [head][slice][parity][DIM / 8 words].
+  template <int DIM>
+  __device__ __forceinline__ void load(const uint32_t* st, const int* st_shift, const float* st_qsum,
+                                       const int* st_ok, int r, int c0) {
+    constexpr int K = DIM >= 8 ? DIM / 8 : 1;
+    const uint32_t* base = st + r * 6 * K + c0 / 8;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+#pragma unroll
+      for (int w = 0; w < WPL; ++w) {
+        hs[w][par] = base[(0 * 2 + par) * K + w];
+        ms[w][par] = base[(1 * 2 + par) * K + w];
+        ls[w][par] = base[(2 * 2 + par) * K + w];
+      }
+    }
+    shift = st_shift[r];
+    qsum = st_qsum[r];
+    ok = st_ok[r] != 0;
+  }
+
+  // sum_d code_d * Q_d of one row (every lane of the group gets it).
+  __device__ __forceinline__ int64_t dot(const uint32_t (&w)[4]) const {
+    int th = 0;
+    uint32_t tm = 0u, tl = 0u;
+#pragma unroll
+    for (int k = 0; k < WPL; ++k) {
+      const uint32_t lo = w[k] & 0x0f0f0f0fu;
+      const uint32_t hi = (w[k] >> 4) & 0x0f0f0f0fu;
+      th = __builtin_amdgcn_sdot4(static_cast<int>(lo), static_cast<int>(hs[k][0]), th, false);
+      th = __builtin_amdgcn_sdot4(static_cast<int>(hi), static_cast<int>(hs[k][1]), th, false);
+      tm = __builtin_amdgcn_udot4(lo, ms[k][0], tm, false);
+      tm = __builtin_amdgcn_udot4(hi, ms[k][1], tm, false);
+      tl = __builtin_amdgcn_udot4(lo, ls[k][0], tl, false);
+      tl = __builtin_amdgcn_udot4(hi, ls[k][1], tl, false);
+    }
+    // per lane |th| <= 32*15*64, so th * 256 + tm stays far inside int32, and
+    // so do the group sums for D <= 256
+    const int t = group_sum_i32<LPR>(th * 256 + static_cast<int>(tm));
+    const int l = group_sum_i32<LPR>(static_cast<int>(tl));
+    return static_cast<int64_t>(t) * 256 + l;
+  }
+
+  __device__ __forceinline__ float logit(int64_t S, float s, float m, float qk_scale) const {
+    if (!ok) return u32_as_f32(0x7fc00000u);
+    // |S| < 2^34: exact in double, so one double -> float conversion is the
+    // single round-to-nearest-even of S
+    const float dotc = ldexpf(static_cast<float>(static_cast<double>(S)), shift);
+    const float a = s * dotc;
+    const float c = m * qsum;
+    return qk_scale * (a + c);
+  }
+};
+
+constexpr int kQkRows = 256;  // candidate rows per block
+
+// Stage the fixed-point form of the group's R query heads in LDS, once per
+// block: thread t converts VPT consecutive channels of head t / LH (LH =
+// DIM / VPT lanes per head, an aligned group inside one wavefront, so the
+// head's max |q| and sum Q are group reductions).  st: [RMAX][3][2][DIM/8]
+// words (slice h, m, l; even / odd channels), byte j of word k holding
+// channel 8k + 2j + parity.  The caller synchronizes before reading.
+template <int DIM, int RMAX>
+struct QStage {
+  static constexpr int TOT = RMAX * DIM;
+  static constexpr int VPT = TOT > kBlock ? TOT / kBlock : 1;  // channels per thread
+  static constexpr int LH = DIM / VPT;                         // lanes per head
+  static constexpr int K = DIM >= 8 ? DIM / 8 : 1;
+  static_assert(LH <= kWave && (kWave % LH) == 0 && VPT <= 8 && (VPT & (VPT - 1)) == 0, "head layout");
+  float v[VPT];
+  // the thread's channels (issued first, so the load overlaps the block's
+  // other round-trip-1 loads)
+  __device__ __forceinline__ void load(const float* qg, int R) {
+    const int t = static_cast<int>(threadIdx.x);
+    const int r = t / LH;
+    const int d0 = (t - r * LH) * VPT;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) v[i] = qg[static_cast<int64_t>(r < R ? r : 0) * DIM + d0 + i];
+  }
+};
+
+template <int DIM, int RMAX>
+__device__ __forceinline__ void stage_qfix(const QStage<DIM, RMAX>& qv, int R, uint32_t* st, int* st_shift,
+                                           float* st_qsum, int* st_ok) {
+  using QS = QStage<DIM, RMAX>;
+  constexpr int VPT = QS::VPT, LH = QS::LH, K = QS::K;
+  const int t = static_cast<int>(threadIdx.x);
+  const int r = t / LH;
+  const int d0 = (t - r * LH) * VPT;
+  const bool act = r < R;
+  const float* v = qv.v;
+  uint32_t mx = 0u, bad = 0u;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const uint32_t u = f32_as_u32(v[i]) & 0x7fffffffu;
+    bad |= u >= 0x7f800000u ? 1u : 0u;
+    mx = u > mx ? u : mx;
+  }
+  mx = group_max_u32<LH>(mx);
+  bad = group_max_u32<LH>(bad);
+  const bool ok = bad == 0u;
+  const float M = u32_as_f32(mx);
+  const bool nz = ok && M != 0.0f;
+  int E = 22;
+  if (nz) (void)frexpf(M, &E);
+  int part = 0;
+  int Q[VPT];
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    Q[i] = nz ? static_cast<int>(rintf(ldexpf(v[i], 22 - E))) : 0;
+    part += Q[i];
+  }
+  const int qs = group_sum_wide_i32<LH>(part);
+  if (act) {
+    uint8_t* sb = reinterpret_cast<uint8_t*>(st);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int d = d0 + i;
+      const int k = d / 8, par = d & 1, j = (d % 8) / 2;
+#pragma unroll
+      for (int sl = 0; sl < 3; ++sl) {
+        const int sh = 16 - 8 * sl;
+        sb[((r * 3 + sl) * 2 + par) * K * 4 + k * 4 + j] = static_cast<uint8_t>((Q[i] >> sh) & 255);
+      }
+    }
+    if (d0 == 0) {
+      st_shift[r] = nz ? E - 22 : 0;
+      st_qsum[r] = ldexpf(static_cast<float>(qs), nz ? E - 22 : 0);
+      st_ok[r] = ok ? 1 : 0;
+    }
+  }
+}
+
+// Union-plan INT4 QK: block = kQkRows consecutive rows of group g's union
+// pages (page u holds rows u*bs .. u*bs + bs - 1).  Round trip 1 loads the
+// plan count, the block's pages and masks, the masks of every earlier union
+// page (for the logit slots) and the queries; round trip 2 the rows' codes,
+// scales and minima.  A head's logit slot for union page u is the number of
+// earlier union pages it chose (its B0 pages are ascending).  The block's
+// logits go through LDS and leave as one coalesced store per (row, head).
+template <typename DT, int DIM, int RMAX, int CPLMAX>
 __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
   using S = typename DT::storage;
-  using Row = Int4Row<DIM>;
-  constexpr int LPR = Row::LPR;
-  constexpr int RPI = Row::RPI;
-  const int chunks = static_cast<int>((a.plan_stride + kQkPagesPerBlock - 1) / kQkPagesPerBlock);
-  const int g = blockIdx.x / chunks;
-  const int chunk = blockIdx.x - g * chunks;
-  int nu = a.plan_counts[g];
-  nu = nu < 0 ? 0 : (nu > a.plan_stride ? static_cast<int>(a.plan_stride) : nu);
-  const int u0 = chunk * kQkPagesPerBlock;
-  if (u0 >= nu) return;
-  const int np = (nu - u0) < kQkPagesPerBlock ? (nu - u0) : kQkPagesPerBlock;
-  const int R = a.R;
-  const int tid = threadIdx.x;
+  using L = QkLane<DIM, CPLMAX>;
+  using QF = QFix<L::CPL, L::LPR>;
+  constexpr int RPB = kWaves * L::RPW;
+  constexpr int PASSES = (kQkRows + RPB - 1) / RPB;
+  constexpr int NC = RMAX / 2;  // packed head counters (two 16-bit fields each)
+  constexpr int KW = DIM >= 8 ? DIM / 8 : 1;
+  static_assert(RMAX == 4 || RMAX == 8, "4 or 8 head slots");
+  static_assert(kQkRows == kBlock, "one block page per thread");
+  const int bs = a.bs;
+  const int row_blocks = static_cast<int>((a.plan_stride * bs + kQkRows - 1) / kQkRows);
+  const int g = blockIdx.x / row_blocks;
+  const int rb = blockIdx.x - g * row_blocks;
+  const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
   const int wave = tid / kWave;
+  const int R = a.R;
+  const int row0 = rb * kQkRows;
+  const int u_first = row0 / bs;
+  const int u_cap = static_cast<int>(a.plan_stride) - 1;
 
-  __shared__ int s_base[8];                    // candidate slots before page u0, per head
-  __shared__ int s_page[kQkPagesPerBlock];
-  __shared__ uint32_t s_mask[kQkPagesPerBlock];
-  __shared__ int s_slot[kQkPagesPerBlock][8];
-  if (tid < 8) s_base[tid] = 0;
-  __syncthreads();
-  // slot of a page for head r = number of earlier union pages head r chose
+  __shared__ int s_page[kQkRows];
+  __shared__ int s_mask[kQkRows];
+  __shared__ int s_slot[kQkRows][RMAX];
+  __shared__ uint32_t s_cnt[kWaves][NC];
+  __shared__ float s_log[kQkRows][RMAX];
+  __shared__ __align__(16) uint32_t s_q[RMAX * 6 * KW];
+  __shared__ int s_qshift[RMAX];
+  __shared__ float s_qsum[RMAX];
+  __shared__ int s_qok[RMAX];
+
+  // ---- round trip 1 (all loads independent): queries, plan count, the
+  // block's pages and masks, the masks of every earlier union page ----
+  QStage<DIM, RMAX> qst;
+  qst.load(a.q + static_cast<int64_t>(g) * R * DIM, R);
+  int nu = a.plan_counts[g];
+  const uint8_t* pm = a.plan_masks + static_cast<int64_t>(g) * a.plan_stride;
+  uint32_t cnt[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) cnt[c] = 0u;
+  for (int ub = 0; ub < u_first; ub += 4 * kBlock) {
+    uint32_t m4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int u = ub + j * kBlock + tid;
+      const uint32_t m = pm[u < u_first ? u : 0];
+      m4[j] = u < u_first ? m : 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) cnt[c] += ((m4[j] >> (2 * c)) & 1u) | (((m4[j] >> (2 * c + 1)) & 1u) << 16);
+    }
+  }
+  int my_page, my_mask;
   {
-    const uint8_t* pm = a.plan_masks + static_cast<int64_t>(g) * a.plan_stride;
-    int cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int ub = 0; ub < u0; ub += 4 * kBlock) {
-      uint32_t m4[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int u = ub + j * kBlock + tid;
-        m4[j] = pm[u < u0 ? u : 0];
-        m4[j] = u < u0 ? m4[j] : 0u;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) cnt[r] += (m4[j] >> r) & 1u;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int w = wave_sum_i32(cnt[r]);
-      if (lane == 0 && w != 0) atomicAdd(&s_base[r], w);
-    }
-    if (tid < np) {
-      s_page[tid] = a.plan_pages[static_cast<int64_t>(g) * a.plan_stride + u0 + tid];
-      s_mask[tid] = pm[u0 + tid];
-    }
+    const int u = u_first + tid < u_cap ? u_first + tid : u_cap;
+    my_page = a.plan_pages[static_cast<int64_t>(g) * a.plan_stride + u];
+    my_mask = pm[u];
+  }
+  nu = nu < 0 ? 0 : (nu > a.plan_stride ? static_cast<int>(a.plan_stride) : nu);
+  const int total_rows = nu * bs;
+  if (row0 >= total_rows) return;  // block-uniform, before any barrier
+  const int nrows = (total_rows - row0) < kQkRows ? (total_rows - row0) : kQkRows;
+  const int npg = (row0 + nrows - 1) / bs - u_first + 1;
+  s_page[tid] = my_page;
+  s_mask[tid] = tid < npg ? my_mask : 0;
+  if constexpr (DIM < 8) {
+    // the heads stage their bytes below; the unused bytes of a D < 8 word stay zero
+    for (int i = tid; i < RMAX * 6 * KW; i += kBlock) s_q[i] = 0u;
   }
   __syncthreads();
-  if (tid < 8) {
-    int run = s_base[tid];
-    for (int i = 0; i < np; ++i) {
-      s_slot[i][tid] = run;
-      run += (s_mask[i] >> tid) & 1u;
-    }
-  }
-  // queries of the group: CPL channels per lane, RMAX heads
-  const int c0 = (lane % LPR) * Row::CPL;
-  const int rig = lane / LPR;
-  float qv[RMAX][8];
-  {
-    const float* qg = a.q + static_cast<int64_t>(g) * R * DIM;
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r) Row::query(qg + static_cast<int64_t>(r < R ? r : R - 1) * DIM + c0, qv[r]);
-  }
-  __syncthreads();
-  const int n_rows = np * a.bs;
-  const int64_t N = static_cast<int64_t>(a.b0) * a.bs;
+  // ---- round trip 2: the block's INT4 rows (needs only the page ids) ----
+  const int c0 = (lane % L::LPR) * L::CPL;
+  const int64_t N = static_cast<int64_t>(a.b0) * bs;
   const uint8_t* pk = a.packed + static_cast<int64_t>(g) * a.qstride * (DIM / 2);
   const S* sc = static_cast<const S*>(a.scale) + static_cast<int64_t>(g) * a.qstride;
   const S* mn = static_cast<const S*>(a.minimum) + static_cast<int64_t>(g) * a.qstride;
-  // Rows in batches of QB wavefront steps: every load of a batch is issued
-  // before the first is used.
-  constexpr int QB = 8;
-  for (int base = wave * RPI; base < n_rows; base += kWaves * RPI * QB) {
-    uint32_t w[QB];
-    S sv[QB], mv[QB];
-    int pis[QB], is[QB];
-    bool oks[QB];
+  uint32_t w[PASSES][4];
+  S sv[PASSES], mv[PASSES];
 #pragma unroll
-    for (int b = 0; b < QB; ++b) {
-      const int row = base + b * kWaves * RPI + rig;
-      const bool ok = row < n_rows;
-      const int rr = ok ? row : n_rows - 1;
-      const int pi = rr / a.bs;
-      const int i = rr - pi * a.bs;
-      int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[pi]) * a.bs + i;
-      const bool in_range = t >= 0 && t < a.qrows;
-      t = in_range ? t : 0;
-      w[b] = Row::codes(pk + t * (DIM / 2), c0);
-      sv[b] = sc[t];
-      mv[b] = mn[t];
-      pis[b] = pi;
-      is[b] = i;
-      oks[b] = ok && in_range;
-    }
+  for (int i = 0; i < PASSES; ++i) {
+    const int lr = i * RPB + wave * L::RPW + lane / L::LPR;  // row within the block
+    const int row = row0 + (lr < nrows ? lr : 0);
+    const int p = row / bs - u_first;
+    int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[p]) * bs + (row - (row / bs) * bs);
+    t = (t >= 0 && t < a.qrows) ? t : 0;
+    L::codes(pk + t * (DIM / 2), c0, w[i]);
+    sv[i] = sc[t];
+    mv[i] = mn[t];
+  }
+  // ---- while they are in flight: q in fixed point, the logit slots ----
+  stage_qfix<DIM, RMAX>(qst, R, s_q, s_qshift, s_qsum, s_qok);
 #pragma unroll
-    for (int b = 0; b < QB; ++b) {
-      float k[8];
-      Row::dequant(w[b], to_f32(DT{}, sv[b]), to_f32(DT{}, mv[b]), k);
-      const uint32_t pmask = s_mask[pis[b]];
+  for (int c = 0; c < NC; ++c) cnt[c] = static_cast<uint32_t>(wave_sum_i32(static_cast<int>(cnt[c])));
+  if (lane == 0) {
 #pragma unroll
-      for (int r = 0; r < RMAX; ++r) {
-        const float acc = Row::dot(k, qv[r]);
-        const int slot = s_slot[pis[b]][r < 8 ? r : 7];
-        if (oks[b] && (lane % LPR) == 0 && r < R && ((pmask >> r) & 1u) && slot < a.b0) {
-          const int64_t n = static_cast<int64_t>(slot) * a.bs + is[b];
-          a.logits[(static_cast<int64_t>(g) * R + r) * N + n] = acc * a.qk_scale;
-        }
+    for (int c = 0; c < NC; ++c) s_cnt[wave][c] = cnt[c];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // a head's slot for union page u = the earlier union pages it chose:
+    // four block pages per lane, exclusive scan of the packed counts
+    constexpr int PPL = kQkRows / kWave;
+    int mk[PPL];
+#pragma unroll
+    for (int j = 0; j < PPL; ++j) mk[j] = s_mask[PPL * lane + j];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      uint32_t before = 0u;
+#pragma unroll
+      for (int v = 0; v < kWaves; ++v) before += s_cnt[v][c];
+      uint32_t e[PPL], tot = 0u;
+#pragma unroll
+      for (int j = 0; j < PPL; ++j) {
+        e[j] = ((mk[j] >> (2 * c)) & 1) | (((mk[j] >> (2 * c + 1)) & 1) << 16);
+        tot += e[j];
       }
+      before += wave_prefix_sum_u32(tot) - tot;
+#pragma unroll
+      for (int j = 0; j < PPL; ++j) {
+        s_slot[PPL * lane + j][2 * c] = static_cast<int>(before & 0xffffu);
+        s_slot[PPL * lane + j][2 * c + 1] = static_cast<int>(before >> 16);
+        before += e[j];
+      }
+    }
+  }
+  QF qf[RMAX];
+#pragma unroll
+  for (int r = 0; r < RMAX; ++r) qf[r].template load<DIM>(s_q, s_qshift, s_qsum, s_qok, r < R ? r : 0, c0);
+  // ---- dot products ----
+#pragma unroll
+  for (int i = 0; i < PASSES; ++i) {
+    const int lr = i * RPB + wave * L::RPW + lane / L::LPR;
+    const float s = to_f32(DT{}, sv[i]), m = to_f32(DT{}, mv[i]);
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+      if (r >= R) break;
+      const float lg = qf[r].logit(qf[r].dot(w[i]), s, m, a.qk_scale);
+      if (lr < kQkRows && (lane % L::LPR) == 0) s_log[lr][r] = lg;
+    }
+  }
+  __syncthreads();
+  // ---- out: row lr of head r to logits[g][r][slot * bs + lr's place in its
+  // page]; candidates beyond the INT4 rows are skipped ----
+  if (tid < nrows) {
+    const int lr = tid;
+    const int row = row0 + lr;
+    const int p = row / bs - u_first;
+    const int i = row - (row / bs) * bs;
+    const int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[p]) * bs + i;
+    const int m = (t >= 0 && t < a.qrows) ? s_mask[p] : 0;
+    for (int r = 0; r < R; ++r) {
+      const int slot = s_slot[p][r];
+      if (((m >> r) & 1) && slot < a.b0)
+        a.logits[(static_cast<int64_t>(g) * R + r) * N + static_cast<int64_t>(slot) * bs + i] = s_log[lr][r];
     }
   }
 }
 
 // INT4 QK at explicit candidate positions, one query head per block row
 // (the fused_affine_int4_qk call surface): positions[g][r][n] index entry g's
-// INT4 rows.  Same dequantization and reduction order as twilight_qk_kernel;
-// with materialize, the dequantized fp32 rows are written instead.
-template <typename DT, int DIM>
+// INT4 rows.  The estimate of twilight_qk_kernel; with materialize, the
+// dequantized rows k_d = f32(code_d) * f32(scale) + f32(min) instead.
+template <typename DT, int DIM, int CPLMAX>
 __global__ __launch_bounds__(kBlock) void int4_qk_positions_kernel(QkArgs a, const int64_t* positions, int N,
                                                                    float* out, bool materialize) {
   using S = typename DT::storage;
-  using Row = Int4Row<DIM>;
-  constexpr int LPR = Row::LPR;
-  constexpr int RPI = Row::RPI;
+  using L = QkLane<DIM, CPLMAX>;
+  using QF = QFix<L::CPL, L::LPR>;
   constexpr int ROWS = 64;  // candidates per block
   const int tiles = (N + ROWS - 1) / ROWS;
   const int row = blockIdx.x / tiles;  // g*R + r
@@ -236,30 +499,34 @@ __global__ __launch_bounds__(kBlock) void int4_qk_positions_kernel(QkArgs a, con
   const int g = row / a.R;
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) / kWave;
-  const int c0 = (lane % LPR) * Row::CPL;
-  float qv[8];
-  Row::query(a.q + static_cast<int64_t>(row) * DIM + c0, qv);
+  const int c0 = (lane % L::LPR) * L::CPL;
+  QF qf;
+  qf.init(a.q + static_cast<int64_t>(row) * DIM, c0);
   const uint8_t* pk = a.packed + static_cast<int64_t>(g) * a.qstride * (DIM / 2);
   const S* sc = static_cast<const S*>(a.scale) + static_cast<int64_t>(g) * a.qstride;
   const S* mn = static_cast<const S*>(a.minimum) + static_cast<int64_t>(g) * a.qstride;
-  for (int i0 = tile * ROWS + wave * RPI; i0 < (tile + 1) * ROWS; i0 += kWaves * RPI) {
-    const int n = i0 + lane / LPR;
+  for (int i0 = tile * ROWS + wave * L::RPW; i0 < (tile + 1) * ROWS; i0 += kWaves * L::RPW) {
+    const int n = i0 + lane / L::LPR;
     const bool ok = n < N && n < (tile + 1) * ROWS;
     int64_t t = positions[static_cast<int64_t>(row) * N + (n < N ? n : N - 1)];
     const bool in_range = t >= 0 && t < a.qrows;
     t = in_range ? t : 0;
-    float k[8];
-    Row::dequant(Row::codes(pk + t * (DIM / 2), c0), to_f32(DT{}, sc[t]), to_f32(DT{}, mn[t]), k);
+    uint32_t w[4];
+    L::codes(pk + t * (DIM / 2), c0, w);
+    const float s = to_f32(DT{}, sc[t]), m = to_f32(DT{}, mn[t]);
     if (materialize) {
       if (ok) {
         float* o = out + (static_cast<int64_t>(row) * N + n) * DIM + c0;
 #pragma unroll
-        for (int j = 0; j < Row::CPL; ++j) o[j] = in_range ? k[j] : 0.0f;
+        for (int j = 0; j < L::CPL; ++j) {
+          const float k = static_cast<float>((w[j / 8] >> (4 * (j % 8))) & 15u) * s + m;
+          o[j] = in_range ? k : 0.0f;
+        }
       }
       continue;
     }
-    const float acc = Row::dot(k, qv);
-    if (ok && in_range && (lane % LPR) == 0) out[static_cast<int64_t>(row) * N + n] = acc * a.qk_scale;
+    const float lg = qf.logit(qf.dot(w), s, m, a.qk_scale);
+    if (ok && in_range && (lane % L::LPR) == 0) out[static_cast<int64_t>(row) * N + n] = lg;
   }
 }
 
@@ -1179,12 +1446,12 @@ __global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) 
 // --------------------------------------------------------------- launch
 template <typename DT, int DIM>
 int launch_qk_r(const QkArgs& a, hipStream_t stream) {
-  const int chunks = static_cast<int>((a.plan_stride + kQkPagesPerBlock - 1) / kQkPagesPerBlock);
-  const dim3 grid(a.G * chunks);
+  const int row_blocks = static_cast<int>((a.plan_stride * a.bs + kQkRows - 1) / kQkRows);
+  const dim3 grid(a.G * row_blocks);
   if (a.R <= 4) {
-    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 4>), grid, dim3(kBlock), 0, stream, a);
+    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 4, 32>), grid, dim3(kBlock), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 8>), grid, dim3(kBlock), 0, stream, a);
+    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 8, 16>), grid, dim3(kBlock), 0, stream, a);
   }
   return tw_host::check_launch();
 }
@@ -1207,7 +1474,7 @@ template <typename DT, int DIM>
 void launch_qk_positions_d(const QkArgs& a, const int64_t* positions, int N, float* out, bool materialize,
                            hipStream_t stream) {
   const dim3 grid(a.G * a.R * ((N + 63) / 64));
-  hipLaunchKernelGGL((int4_qk_positions_kernel<DT, DIM>), grid, dim3(kBlock), 0, stream, a, positions, N, out,
+  hipLaunchKernelGGL((int4_qk_positions_kernel<DT, DIM, 32>), grid, dim3(kBlock), 0, stream, a, positions, N, out,
                      materialize);
 }
 
@@ -1272,7 +1539,9 @@ extern "C" int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t
       quant_entry_stride <= 0 || quant_rows <= 0 || quant_rows > quant_entry_stride)
     return TW_EINVAL;
   if (D < 4 || D > 256 || (D & (D - 1)) != 0) return TW_EUNSUPPORTED;
-  if ((reinterpret_cast<uintptr_t>(q) % 16) || (reinterpret_cast<uintptr_t>(packed) % 4)) return TW_EINVAL;
+  // each lane reads min(D, 32) / 2 code bytes of a row with one load
+  const uintptr_t pk_align = D >= 32 ? 16 : static_cast<uintptr_t>(D / 2);
+  if ((reinterpret_cast<uintptr_t>(q) % 16) || (reinterpret_cast<uintptr_t>(packed) % pk_align)) return TW_EINVAL;
   tw::QkArgs a{q, packed, scale, minimum, quant_entry_stride, quant_rows, G, R, D, plan_pages, plan_masks, plan_counts,
                plan_stride, b0_pages, sink, block_size, qk_scale, logits};
   const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1294,7 +1563,8 @@ extern "C" int tw_int4_qk_positions(const float* q, int G, int R, int D, const u
   if (N == 0) return TW_OK;
   if (positions == nullptr) return TW_EINVAL;
   if (D < 4 || D > 256 || (D & (D - 1)) != 0) return TW_EUNSUPPORTED;
-  if ((reinterpret_cast<uintptr_t>(q) % 16) || (reinterpret_cast<uintptr_t>(packed) % 4)) return TW_EINVAL;
+  const uintptr_t pk_align = D >= 32 ? 16 : static_cast<uintptr_t>(D / 2);
+  if ((reinterpret_cast<uintptr_t>(q) % 16) || (reinterpret_cast<uintptr_t>(packed) % pk_align)) return TW_EINVAL;
   tw::QkArgs a{q, packed, scale, minimum, quant_entry_stride, quant_rows, G, R, D, nullptr, nullptr, nullptr, 0,
                0, 0, 1, qk_scale, nullptr};
   const hipStream_t s = static_cast<hipStream_t>(stream);
