@@ -299,11 +299,8 @@ class OffloadWorkload(QuestWorkload):
         del self.kc, self.vc
         torch.cuda.empty_cache()
         G, D = self.G, self.D
-        self.stage_k = torch.empty((G, self.max_rows, D), dtype=hk.dtype, pin_memory=True)
-        self.stage_v = torch.empty_like(self.stage_k)
         self.dev_k = torch.empty((G, self.max_rows, D), dtype=hk.dtype, device=dev)
         self.dev_v = torch.empty_like(self.dev_k)
-        self.rows_h = torch.zeros((G, self.max_rows), dtype=torch.int32, pin_memory=True)
         self.rmask_h = torch.zeros((G, self.max_rows), dtype=torch.uint8, pin_memory=True)
         self.counts_h = torch.zeros((G,), dtype=torch.int32, pin_memory=True)
         self.rows_d = torch.zeros((G, self.max_rows), dtype=torch.int32, device=dev)
@@ -319,46 +316,71 @@ class OffloadWorkload(QuestWorkload):
                                        block_size=self.BS, length=self.L, append_position=self.L,
                                        cur_k=self.cur_k[layer], cur_v=self.cur_v[layer], out=self.out[layer])
 
-    def attend_dma(self, layer: int) -> int:
-        """The reference's host path: page ids to the host, CPU gather of each
-        group's union rows into pinned staging, one H2D copy per group and
-        plane, attention over the staged rows.  Returns the rows moved."""
+    def attend_dma(self, layer: int, groups_per_chunk: int = 2) -> int:
+        """The DMA alternative to zero-copy (the reference's post-selection
+        pipeline, twilight_offload_cache.py:2053-2455): the layer's union
+        plans come to the host in one copy, then chunk by chunk the CPU
+        gathers the union rows from the pinned slab into pinned staging and a
+        side stream copies them to HBM, while the next chunk is gathered; each
+        chunk's attention over its staged rows starts behind its copy.
+        Returns the rows moved."""
+        import numpy as np
         import torch
 
         from headinfer import kernels
+        from headinfer.dma_pipeline import HostGatherPipeline
 
-        counts = self.plan_counts[layer].cpu()
-        pages = self.plan_pages[layer].cpu()
-        masks = self.plan_masks[layer].cpu()
-        G, R, BS, L = self.G, self.R, self.BS, self.L
+        plan = torch.cat([self.plan_counts[layer].view(-1, 1), self.plan_pages[layer],
+                          self.plan_masks[layer].to(torch.int32)], dim=1).cpu().numpy()
+        G, R, BS, L, D = self.G, self.R, self.BS, self.L, self.D
+        W = self.plan_pages.shape[2]
         sink_end = min(self.SINK, L)
         recent_start = max(sink_end, L - (self.RECENT - 1))
-        all_heads = (1 << R) - 1
-        moved = 0
-        for g in range(G):
-            nu = int(counts[g])
-            pg = pages[g, :nu].long()
-            pos = torch.cat([torch.arange(sink_end), (self.SINK + pg[:, None] * BS + torch.arange(BS)).reshape(-1),
-                             torch.arange(recent_start, L)])
-            n = pos.numel()
-            kernels.host_gather_kv(self.hk[layer, g], self.hv[layer, g], pos, self.stage_k[g, :n], self.stage_v[g, :n])
-            self.dev_k[g, :n].copy_(self.stage_k[g, :n], non_blocking=True)
-            self.dev_v[g, :n].copy_(self.stage_v[g, :n], non_blocking=True)
-            self.rows_h[g, :n] = torch.arange(n, dtype=torch.int32)
-            self.rmask_h[g, :n] = torch.cat([torch.full((sink_end,), all_heads),
-                                             masks[g, :nu].long().repeat_interleave(BS),
-                                             torch.full((L - recent_start,), all_heads)]).to(torch.uint8)
-            self.counts_h[g] = n
-            moved += n
-        self.rows_d.copy_(self.rows_h, non_blocking=True)
-        self.rmask_d.copy_(self.rmask_h, non_blocking=True)
-        self.counts_d.copy_(self.counts_h, non_blocking=True)
-        kernels.decode_attention_rows(self.q[layer], self.dev_k, self.dev_v, self.rows_d, self.counts_d,
-                                      self.max_rows, row_masks=self.rmask_d, cur_k=self.cur_k[layer],
-                                      cur_v=self.cur_v[layer], out=self.out[layer])
+        n_fixed = sink_end + (L - recent_start)
+        if getattr(self, "dma", None) is None:
+            self.dma = HostGatherPipeline(self.dev, D, self.hk.dtype, groups_per_chunk * self.max_rows)
+            self.rows_d.copy_(torch.arange(self.max_rows, dtype=torch.int32).expand(G, -1))
+            head = np.full(sink_end, (1 << R) - 1, np.uint8)
+            tail = np.full(L - recent_start, (1 << R) - 1, np.uint8)
+            self._dma_fixed = (np.arange(sink_end, dtype=np.int64), np.arange(recent_start, L, dtype=np.int64),
+                               head, tail)
+        sink_pos, recent_pos, head, tail = self._dma_fixed
+        counts = plan[:, 0]
+        n = counts * BS + n_fixed
+        offs = np.arange(BS, dtype=np.int64)
+        rmask = np.zeros((G, self.max_rows), np.uint8)
+        dst_k = self.dev_k.view(-1, D)
+        dst_v = self.dev_v.view(-1, D)
+        chunks = []
+        for c0 in range(0, G, groups_per_chunk):
+            ids = []
+            for g in range(c0, min(G, c0 + groups_per_chunk)):
+                nu = int(counts[g])
+                body = (self.SINK + plan[g, 1:1 + nu].astype(np.int64)[:, None] * BS + offs).reshape(-1)
+                base = g * self.Lmax
+                ids.append(np.concatenate([sink_pos, body, recent_pos]) + base)
+                pad = self.max_rows - int(n[g])  # staged groups sit max_rows apart
+                if pad:
+                    ids.append(np.full(pad, base, np.int64))
+                rmask[g, :n[g]] = np.concatenate([head, np.repeat(plan[g, 1 + W:1 + W + nu].astype(np.uint8), BS),
+                                                  tail])
+            ids = np.concatenate(ids)
+            a = c0 * self.max_rows
+            chunks.append((ids, dst_k[a:a + ids.shape[0]], dst_v[a:a + ids.shape[0]]))
+        self.counts_d.copy_(torch.from_numpy(n.astype(np.int32)), non_blocking=False)
+        self.rmask_d.copy_(torch.from_numpy(rmask), non_blocking=False)
+
+        def attend(c: int) -> None:
+            g0, g1 = c * groups_per_chunk, min(G, (c + 1) * groups_per_chunk)
+            kernels.decode_attention_rows(self.q[layer, g0:g1], self.dev_k[g0:g1], self.dev_v[g0:g1],
+                                          self.rows_d[g0:g1], self.counts_d[g0:g1], self.max_rows,
+                                          row_masks=self.rmask_d[g0:g1], cur_k=self.cur_k[layer, g0:g1],
+                                          cur_v=self.cur_v[layer, g0:g1], out=self.out[layer, g0:g1])
+
+        self.dma.run(self.hk[layer].view(-1, D), self.hv[layer].view(-1, D), chunks, on_chunk=attend)
         kernels.append_kv(self.cur_k[layer], self.cur_v[layer], self.hk[layer], self.hv[layer], first_entry=0,
                           position=self.L)
-        return moved
+        return int(n.sum())
 
     def host_bytes_per_layer(self) -> float:
         fixed = min(self.SINK, self.L) + (self.RECENT - 1)
@@ -739,10 +761,31 @@ def run_offload(args, dev) -> int:
     layer_s = wall / w.layers
     host_bytes = w.host_bytes_per_layer()
     by = w.bytes_per_layer()
-    # the reference's host path for comparison: eager, a host sync per layer
+    # the DMA alternative for comparison: eager (the page ids go to the host
+    # once per layer), side-stream copies overlapped with the CPU gather and
+    # each group's attention; checked against float64 like the zero-copy path
     w.step()
     torch.cuda.synchronize()
     dma_layers = min(w.layers, 8)
+    w.select(0)
+    w.attend_dma(0)
+    torch.cuda.synchronize()
+    for g in range(w.G):
+        nu = int(w.plan_counts[0, g])
+        pages = w.plan_pages[0, g, :nu].long().cpu()
+        pm = w.plan_masks[0, g, :nu].cpu()
+        rows = torch.cat([torch.arange(sink_end), (w.SINK + pages[:, None] * w.BS + torch.arange(w.BS)).reshape(-1),
+                          torch.arange(recent_start, w.L)])
+        masks = torch.cat([torch.full((sink_end,), (1 << w.R) - 1), pm.long().repeat_interleave(w.BS),
+                           torch.full((w.L - recent_start,), (1 << w.R) - 1)])
+        e = _attention_check(w.q[0, g].cpu(), w.hk[0, g], w.hv[0, g], rows, masks, w.cur_k[0, g].cpu(),
+                             w.cur_v[0, g].cpu(), w.out[0, g].cpu())
+        ok &= e != float("inf")
+        err = max(err, e)
+    for layer in range(dma_layers):  # warm: first CPU touch of each layer's slab rows
+        w.select(layer)
+        w.attend_dma(layer)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for layer in range(dma_layers):
         w.select(layer)

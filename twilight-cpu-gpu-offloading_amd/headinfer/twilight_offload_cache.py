@@ -362,6 +362,7 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         self._capture_budget_trace = False
         self._flat_union_keys: Optional[torch.Tensor] = None
         self._flat_union_values: Optional[torch.Tensor] = None
+        self._dma = None  # HostGatherPipeline of post_selection_pipeline (host slabs)
 
     # ------------------------------------------------------------ metadata
     def _build_metadata(self, entry: int, key_states: torch.Tensor) -> None:
@@ -598,7 +599,10 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         cur_v = torch.cat([v[0, 0] for v in value_states], dim=0).contiguous()
         cu = torch.empty((G + 1,), dtype=torch.int32, device=self.device)
         start = self._phase_start()
-        if self._consecutive(entries):
+        if self.post_selection_pipeline and self.kv_residency == "host":
+            cu_host = self._pipelined_union_gather(entries, state, cur_k, cur_v)
+            cu.copy_(cu_host.to(torch.int32), non_blocking=True)
+        elif self._consecutive(entries):
             kernels.gather_union(self._key_rows, self._value_rows, state["rows"], state["counts"], cur_k, cur_v,
                                  self._flat_union_keys.view(-1, D), self._flat_union_values.view(-1, D), cu,
                                  entry_row0=self.geometry.row(entries[0], 0),
@@ -608,7 +612,8 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
             raise ValueError("GQA group execution needs the consecutive entries of one layer")
         self._phase_end("gather", start)
         self._append(entries, cur_k, cur_v, old_length)
-        cu_host = cu.cpu()
+        if not (self.post_selection_pipeline and self.kv_residency == "host"):
+            cu_host = cu.cpu()
         lengths = tuple(int(cu_host[g + 1] - cu_host[g]) for g in range(G))
         total = int(cu_host[-1])
         for g, entry in enumerate(entries):
@@ -773,6 +778,43 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
             self._last_query_head_lengths[entry] = tuple(lengths[g * R:(g + 1) * R])
         cu = torch.tensor([0, *torch.tensor(lengths).cumsum(0).tolist()], dtype=torch.int32, device=dev)
         return self._flat_keys[:off], self._flat_values[:off], cu, max(lengths), tuple(lengths)
+
+    def _pipelined_union_gather(self, entries: Sequence[int], state: dict, cur_k: torch.Tensor,
+                                cur_v: torch.Tensor) -> torch.Tensor:
+        """The union rows of every group through the side-stream DMA pipeline
+        (the reference's post_selection_pipeline, twilight_offload_cache.py:
+        2053-2455): the union row lists come to the host once, then every
+        chunk of post_selection_groups_per_chunk groups is gathered on the CPU
+        from the pinned slab and copied to the flat attention layout on the
+        pipeline's stream while the next chunk is gathered.  Each group's gap
+        row takes its decode token on the device afterwards.  Returns the
+        cu_seqlens on the host."""
+        import numpy as np
+
+        from .dma_pipeline import HostGatherPipeline
+
+        G, D = len(entries), self.geometry.head_dim
+        counts = state["counts"].cpu().numpy().astype(np.int64)
+        rows = state["rows"][:, :max(1, int(counts.max()) if G else 1)].cpu().numpy().astype(np.int64)
+        cu = np.concatenate([[0], np.cumsum(counts + 1)])
+        per = max(1, self.post_selection_groups_per_chunk)
+        fk = self._flat_union_keys.view(-1, D)
+        fv = self._flat_union_values.view(-1, D)
+        chunks = []
+        for c0 in range(0, G, per):
+            gs = range(c0, min(G, c0 + per))
+            # each group's rows, then a placeholder for its decode token's row
+            ids = np.concatenate([np.append(self.geometry.row(entries[g], 0) + rows[g, :counts[g]], 0) for g in gs])
+            a, b = int(cu[c0]), int(cu[gs[-1] + 1])
+            chunks.append((ids, fk[a:b], fv[a:b]))
+        need = max(int(c[0].shape[0]) for c in chunks) if chunks else 1
+        if self._dma is None or self._dma.max_rows < need:
+            self._dma = HostGatherPipeline(self.device, D, self.dtype, need)
+        self._dma.run(self._key_rows, self._value_rows, chunks)
+        gap = torch.from_numpy(cu[1:] - 1).to(self.device)
+        fk.index_copy_(0, gap, cur_k)
+        fv.index_copy_(0, gap, cur_v)
+        return torch.from_numpy(cu)
 
     # ----------------------------------------------------------------- traces
     def enable_budget_trace(self, enabled: bool = True) -> None:
