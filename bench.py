@@ -67,6 +67,8 @@ def parse_args(argv=None):
                     help="Twilight budgets (twilight32k)")
     ap.add_argument("--budget-pages", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--quest-only", action="store_true",
+                    help="default workload: only the Quest 32K leg (no Twilight / host-offload / TPOT summaries)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget (s)")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="also run one 256 MiB device copy (reference kernel for PMC byte counters)")
@@ -457,13 +459,25 @@ def check_parity(w: QuestWorkload) -> dict:
     return {"ok": ok, "attention_max_abs_err": err}
 
 
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w: QuestWorkload, seconds: float) -> dict:
+    """The torch-CPU port of the reference's Quest layer step, on this box's
+    host cores: with every core of the process's affinity (the headline) and
+    with 6 threads (the reference's formal runs), median over a bounded sample,
+    with the time split into score + top-k, row gather and attention."""
     import torch
 
     from oracle.cpu_baseline import quest_layer_step
 
-    threads = min(16, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(threads)
     L = w.L
     q = w.q[0].cpu()
     kc = w.kc[0, :, :L].cpu()
@@ -471,23 +485,37 @@ def cpu_baseline(w: QuestWorkload, seconds: float) -> dict:
     pmin = w.pmin[0, :, : w.P].cpu()
     pmax = w.pmax[0, :, : w.P].cpu()
     ck, cv = w.cur_k[0].cpu(), w.cur_v[0].cpu()
+    threads0 = torch.get_num_threads()
 
-    def run():
-        return quest_layer_step(q, kc, vc, pmin, pmax, ck, cv, length=L, budget=w.k, sink=w.SINK,
-                                recent=w.RECENT, block_size=w.BS)
+    def sample(threads: int, budget_s: float) -> dict:
+        torch.set_num_threads(threads)
+        phases: dict = {}
 
-    run()
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < seconds and len(times) < 200):
-        t0 = time.perf_counter()
+        def run(ph=None):
+            return quest_layer_step(q, kc, vc, pmin, pmax, ck, cv, length=L, budget=w.k, sink=w.SINK,
+                                    recent=w.RECENT, block_size=w.BS, phases=ph)
+
         run()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    med = times[len(times) // 2]
-    return {"value": round(med * 1e6, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"median of {len(times)} single-layer steps (layer 0, all 8 KV heads, torch CPU: "
-                      "where/sum score, topk, expand, index_select, SDPA math)"}
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
+            t0 = time.perf_counter()
+            run(phases)
+            times.append(time.perf_counter() - t0)
+        times.sort()
+        n = len(times)
+        return {"us_per_layer": round(times[n // 2] * 1e6, 1), "steps": n,
+                "phases_us": {k: round(v / n * 1e6, 1) for k, v in phases.items()}}
+
+    n_aff = len(os.sched_getaffinity(0))
+    full = sample(n_aff, seconds)
+    six = sample(6, seconds / 2)
+    torch.set_num_threads(threads0)
+    return {"value": full["us_per_layer"], "unit": "us/layer", "cores": n_aff, "kind": "port",
+            "sample": f"median of {full['steps']} single-layer steps (layer 0, all 8 KV heads, 32K context, torch "
+                      "CPU: where/sum score, topk, expand, index_select, SDPA math)",
+            "cpu_model": _cpu_model(), "phases_us": full["phases_us"],
+            "threads_6": {"value": six["us_per_layer"], "phases_us": six["phases_us"], "steps": six["steps"]}}
 
 
 def main(argv=None) -> int:
@@ -605,8 +633,28 @@ def main(argv=None) -> int:
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    ok = parity["ok"]
+    if not args.quest_only:
+        # the rest of the metric in the same line: the Twilight 32K layer, the
+        # 64K host-offload layer (zero-copy and side-stream DMA) and p50 TPOT
+        del w, g_step, g_sel, g_att, g_att1
+        torch.cuda.empty_cache()
+        leg_args = argparse.Namespace(**vars(args))
+        leg_args.steps, leg_args.warmup, leg_args.no_cpu_baseline = 50, 5, True
+        leg_args.context = None
+        print("[bench] leg: twilight32k", file=sys.stderr, flush=True)
+        tw = twilight_leg(leg_args, dev)
+        result["twilight32k"] = {"layer_us": tw["layer_us"], "GBps": tw["value"], "kernels": tw["kernels"],
+                                 "rows_per_group": tw["rows_per_group"], "parity_ok": tw["parity"]["ok"]}
+        print("[bench] leg: offload64k", file=sys.stderr, flush=True)
+        off = offload_leg(leg_args, dev)
+        result["offload64k"] = {"layer_us": off["layer_us"], "host_link": off["host_link"],
+                                "parity_ok": off["parity"]["ok"]}
+        print("[bench] leg: tpot32k", file=sys.stderr, flush=True)
+        result["tpot32k"] = tpot_leg(leg_args, dev)
+        ok = ok and tw["parity"]["ok"] and off["parity"]["ok"]
     print(json.dumps(result), flush=True)
-    return 0 if parity["ok"] else 1
+    return 0 if ok else 1
 
 
 def _timed_steps(step_graph, steps: int, warmup: int) -> tuple[float, float]:
@@ -644,6 +692,12 @@ def _attention_check(q, keys, vals, rows, masks, cur_k, cur_v, out) -> float:
 
 
 def run_twilight(args, dev) -> int:
+    result = twilight_leg(args, dev)
+    print(json.dumps(result), flush=True)
+    return 0 if result["parity"]["ok"] else 1
+
+
+def twilight_leg(args, dev) -> dict:
     """Twilight at 32K: one decode step of 32 layers x (Quest B0 + INT4 QK +
     top-p + GQA union, then sparse attention over the union and the append)."""
     import torch
@@ -724,14 +778,21 @@ def run_twilight(args, dev) -> int:
                                   "sample": f"median of {len(times)} single-layer steps (layer 0, 8 KV heads, torch "
                                             "CPU: score, topk, INT4 dequant + matmul, argsort/softmax/cumsum top-p, "
                                             "union, index_select, SDPA)"}
-    print(json.dumps(result), flush=True)
-    return 0 if ok else 1
+    del w
+    torch.cuda.empty_cache()
+    return result
 
 
 def run_offload(args, dev) -> int:
+    result = offload_leg(args, dev)
+    print(json.dumps(result), flush=True)
+    return 0 if result["parity"]["ok"] else 1
+
+
+def offload_leg(args, dev) -> dict:
     """64K layer with the KV in pinned host memory: the attention reads the
-    selected pages zero-copy over the host link; the reference's host-gather +
-    DMA path is timed beside it."""
+    selected pages zero-copy over the host link; the side-stream DMA path is
+    timed beside it."""
     import torch
 
     ctx = args.context or 65536
@@ -823,8 +884,9 @@ def run_offload(args, dev) -> int:
         "rows_per_group": round(host_bytes / (2 * w.D * 2) / w.G, 1),
         "parity": {"ok": ok, "attention_max_abs_err": err},
     }
-    print(json.dumps(result), flush=True)
-    return 0 if ok else 1
+    del w
+    torch.cuda.empty_cache()
+    return result
 
 
 # rocprofv3 FETCH_SIZE / WRITE_SIZE of each kernel, calibrated against a copy
@@ -839,7 +901,7 @@ def llama3_8b_config(layers: int = 32):
                        rope_theta=500000.0, rms_norm_eps=1e-5, tie_word_embeddings=False)
 
 
-def tpot_run(model, ids, dev, cache, decode_tokens: int, graph: bool = False) -> dict:
+def tpot_run(model, ids, dev, cache, decode_tokens: int, graph: bool = False, dense: bool = False) -> dict:
     """Prefill `ids` into `cache` through the patched model, then decode
     `decode_tokens` tokens of the fixed id 1 -- through the HF forward, or
     (graph) as replays of one captured decode graph (headinfer.graph_decode;
@@ -855,7 +917,8 @@ def tpot_run(model, ids, dev, cache, decode_tokens: int, graph: bool = False) ->
         torch.cuda.synchronize()
         prefill_s = time.perf_counter() - t0
         tok = torch.ones((1, 1), dtype=torch.long, device=dev)
-        dec = GraphDecoder(model, cache, max_new_tokens=decode_tokens, fixed_token=1) if graph else None
+        dec = GraphDecoder(model, cache, max_new_tokens=decode_tokens, fixed_token=1,
+                           dense=dense) if graph else None
         times = []
         for _ in range(decode_tokens):
             torch.cuda.synchronize()
@@ -878,8 +941,9 @@ def run_tpot(args, dev) -> int:
     Quest cache (budget 128 pages = 2048 tokens per query head, sink 64,
     recent 256, page 16).  A random 32K-token prompt is prefilled (dense
     causal attention), then tokens of the fixed id 1 are decoded; TPOT is the
-    synchronized wall time per token, p50 over D2..Dn.  The same harness with
-    a budget covering every page is the dense-attention comparison."""
+    synchronized wall time per token, p50 over D2..Dn.  The dense comparison
+    is the graph decoder with no score or top-k: every whole page before the
+    recent window through the same attention kernels."""
     import torch
 
     from headinfer import mp
@@ -900,8 +964,10 @@ def run_tpot(args, dev) -> int:
     mp.mp_headinfer(model)
     ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(5))
     runs = {}
-    variants = [("sparse_graph", args.budget_pages, True, False), ("dense_graph", 1 << 20, True, False),
-                ("sparse_hf_eager", args.budget_pages, False, False), ("dense_hf_eager", 1 << 20, False, False),
+    # dense_graph: no score or top-k, every whole page through the same
+    # attention; allpages_hf_eager: the HF forward with a budget covering every page
+    variants = [("sparse_graph", args.budget_pages, True, False), ("dense_graph", args.budget_pages, True, False),
+                ("sparse_hf_eager", args.budget_pages, False, False), ("allpages_hf_eager", 1 << 20, False, False),
                 ("twilight_graph", None, True, False), ("twilight_hf_eager", None, False, False)]
     if residency == "host":  # the HBM resident page cache (previous_token_resident_cache) serves host slabs
         variants[1:1] = [("sparse_graph_resident", args.budget_pages, True, True)]
@@ -922,7 +988,7 @@ def run_tpot(args, dev) -> int:
                                                              kv_residency=residency, budget_pages=pages,
                                                              update_metadata_on_decode=graph,
                                                              previous_token_resident_cache=resident)
-        runs[label] = tpot_run(model, ids, dev, cache, n_dec, graph=graph)
+        runs[label] = tpot_run(model, ids, dev, cache, n_dec, graph=graph, dense=label == "dense_graph")
         if resident:
             st = cache.resident_stats()
             runs[label]["resident_hit_ratio"] = round(st["resident_hit_pages"] / max(1, st["union_pages"]), 4)
@@ -949,6 +1015,88 @@ def run_tpot(args, dev) -> int:
         result["sparse_vs_dense_speedup"] = round(runs["dense_graph"]["tpot_p50_ms"] / sp["tpot_p50_ms"], 3)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def _graph_tpot(dec, n: int) -> dict:
+    """Synchronized wall time of n graph-decoded tokens (D1 includes the
+    capture); p50 and mean over D2..Dn (run_ruler_partial_h2d_tpot_case_v1.py:
+    1302-1322,1897-1906)."""
+    import torch
+
+    times = []
+    with torch.no_grad():
+        for _ in range(n):
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            dec.step()
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t1)
+    steady = sorted(times[1:])
+    return {"tpot_p50_ms": round(steady[len(steady) // 2] * 1e3, 3),
+            "tpot_mean_ms": round(sum(steady) / len(steady) * 1e3, 3), "decode_tokens": n}
+
+
+def tpot_leg(args, dev) -> dict:
+    """p50 TPOT at 32K context with the KV in HBM, every decode token one
+    replay of a captured graph: a Llama-3-8B-shaped model (random-init bf16
+    weights) patched by mp_headinfer, a random 32K-token prompt prefilled once
+    per cache, then tokens of the fixed id 1.  Three decoders: sparse Quest
+    (budget 128 pages per query head), the dense comparator on the same
+    prefilled cache (no score or top-k: every whole page before the recent
+    window through the same attention), and Twilight (Quest B0 4096 tokens,
+    INT4 QK, top-p 0.95, dynamic budgets)."""
+    import torch
+
+    from headinfer import mp
+    from headinfer.graph_decode import GraphDecoder
+    from headinfer.quest_offload_cache import QuestTopKOffloadedCache
+    from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache
+    from transformers import LlamaForCausalLM
+
+    ctx = 32768
+    n_dec = max(4, args.decode_tokens)
+    cfg = llama3_8b_config(32)
+    print("[bench] tpot: Llama-3-8B-shaped model, random init", file=sys.stderr, flush=True)
+    torch.manual_seed(4)
+    with torch.device(dev):
+        model = LlamaForCausalLM._from_config(cfg, dtype=torch.bfloat16)
+    model.eval()
+    mp.mp_headinfer(model)
+    ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(5)).to(dev)
+    out = {}
+    with torch.no_grad():
+        cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + 2 * n_dec + 8,
+                                                         kv_residency="hbm", budget_pages=args.budget_pages,
+                                                         update_metadata_on_decode=True)
+        print("[bench] tpot: prefill (Quest cache)", file=sys.stderr, flush=True)
+        model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        torch.cuda.synchronize()
+        dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1)
+        out["sparse_graph"] = _graph_tpot(dec, n_dec)
+        dec.sync_cache()
+        del dec
+        dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1, dense=True)
+        out["dense_graph"] = _graph_tpot(dec, n_dec)
+        del dec, cache
+        torch.cuda.empty_cache()
+        cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(
+            model, max_cache_len=ctx + n_dec + 8, kv_residency="hbm", candidate_token_budget=4096, top_p=0.95,
+            budget_mode="dynamic", update_metadata_on_decode=True)
+        print("[bench] tpot: prefill (Twilight cache)", file=sys.stderr, flush=True)
+        model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        torch.cuda.synchronize()
+        dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1)
+        out["twilight_graph"] = _graph_tpot(dec, n_dec)
+        del dec, cache
+    del model
+    torch.cuda.empty_cache()
+    dense = out["dense_graph"]["tpot_p50_ms"]
+    return {"context": ctx, "kv": "hbm", "p50_ms": {k: v["tpot_p50_ms"] for k, v in out.items()},
+            "mean_ms": {k: v["tpot_mean_ms"] for k, v in out.items()}, "decode_tokens": n_dec,
+            "dense_over_sparse": round(dense / out["sparse_graph"]["tpot_p50_ms"], 3),
+            "dense_over_twilight": round(dense / out["twilight_graph"]["tpot_p50_ms"], 3),
+            "model": "Llama-3-8B-shaped (32 layers, 32 q / 8 kv heads, head_dim 128), random-init bf16",
+            "budget_pages": args.budget_pages}
 
 
 class MultiRequestWorkload:

@@ -18,6 +18,8 @@ decoder layer of the Quest per-head path:
 from __future__ import annotations
 
 import math
+import time
+from typing import Optional
 
 import torch
 import torch.nn.functional as F
@@ -25,11 +27,15 @@ import torch.nn.functional as F
 
 def quest_layer_step(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_min: torch.Tensor,
                      page_max: torch.Tensor, cur_k: torch.Tensor, cur_v: torch.Tensor, *, length: int, budget: int,
-                     sink: int, recent: int, block_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+                     sink: int, recent: int, block_size: int,
+                     phases: Optional[dict] = None) -> tuple[torch.Tensor, torch.Tensor]:
     """One layer: q [G,R,D]; k_cache/v_cache [G,>=L,D]; page_min/page_max
-    [G,P,D] (the P scored pages); cur_k/cur_v [G,D].
+    [G,P,D] (the P scored pages); cur_k/cur_v [G,D].  phases (optional)
+    accumulates seconds per phase: "score_select", "gather", "attention".
 
     Returns (out [G,R,D] in q's dtype, selected pages [G,R,budget] int64)."""
+    clock = time.perf_counter
+    t0 = clock()
     G, R, D = q.shape
     sink_end = min(sink, length)
     recent_start = max(sink_end, length - max(0, recent - 1))
@@ -39,6 +45,8 @@ def quest_layer_step(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
     extrema = torch.where(qf.unsqueeze(1) > 0, pmax, pmin)
     scores = (extrema.float() * qf.unsqueeze(1)).sum(dim=-1)
     chosen = torch.topk(scores, k=budget, dim=-1, largest=True, sorted=False).indices.sort(dim=-1).values
+    t_sel = clock() - t0
+    t_gather = t_attn = 0.0
     sink_idx = torch.arange(sink_end, dtype=torch.long)
     recent_idx = torch.arange(recent_start, length, dtype=torch.long)
     offsets = torch.arange(block_size, dtype=torch.long)
@@ -48,12 +56,19 @@ def quest_layer_step(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
         for r in range(R):
             pages = chosen[g * R + r]
             blocks = (sink + pages.unsqueeze(1) * block_size + offsets.unsqueeze(0)).reshape(-1)
+            t1 = clock()
             pos = torch.cat((sink_idx, blocks, recent_idx))
             keys = torch.cat((k_cache[g].index_select(0, pos), cur_k[g : g + 1]))
             vals = torch.cat((v_cache[g].index_select(0, pos), cur_v[g : g + 1]))
+            t2 = clock()
             o = F.scaled_dot_product_attention(q[g, r].view(1, 1, 1, D).float(), keys.view(1, 1, -1, D).float(),
                                                vals.view(1, 1, -1, D).float(), is_causal=False, scale=scale)
             out[g, r] = o.view(D).to(q.dtype)
+            t_gather += t2 - t1
+            t_attn += clock() - t2
+    if phases is not None:
+        for name, t in (("score_select", t_sel), ("gather", t_gather), ("attention", t_attn)):
+            phases[name] = phases.get(name, 0.0) + t
     return out, chosen.view(G, R, budget)
 
 

@@ -360,3 +360,34 @@ def test_graph_decoder_twilight_matches_eager(dev, fuse):
         a = graph_cache._key_cache[e, :L].float().cpu()
         b = eager_cache._key_cache[e, :L].float().cpu()
         assert torch.allclose(a, b, atol=2e-2, rtol=2e-2), e
+
+
+def test_graph_decoder_dense_equals_all_pages_budget(dev):
+    """The dense comparator (no score or top-k, every page through the page-tile
+    attention) == the sparse decoder whose budget covers every page, bit for
+    bit: same rows, same tile order, same kernels after the selection."""
+    from headinfer import mp
+    from headinfer.graph_decode import GraphDecoder
+    from headinfer.quest_offload_cache import QuestTopKOffloadedCache
+
+    steps = 6
+    _, gpu = _models(dev)
+    mp.mp_headinfer(gpu)
+    kw = dict(max_cache_len=T_PROMPT + steps + 2, sink_tokens=64, recent_tokens=256, block_size=16,
+              kv_residency="hbm", update_metadata_on_decode=True)
+    caches = [QuestTopKOffloadedCache.from_llama_model(gpu, budget_pages=1000, **kw),
+              QuestTopKOffloadedCache.from_llama_model(gpu, **kw)]
+    g = torch.Generator().manual_seed(6)
+    ids = torch.randint(0, 1000, (1, T_PROMPT), generator=g).to(dev)
+    with torch.no_grad():
+        for c in caches:
+            gpu(input_ids=ids, past_key_values=c, use_cache=True, logits_to_keep=1)
+        decs = [GraphDecoder(gpu, caches[0], max_new_tokens=steps),
+                GraphDecoder(gpu, caches[1], max_new_tokens=steps, dense=True)]
+        for step in range(steps):
+            a = decs[0].step().clone()
+            b = decs[1].step().clone()
+            torch.cuda.synchronize()
+            assert torch.equal(a, b), step
+    n = T_PROMPT + steps
+    assert torch.equal(caches[0]._key_cache[:, :n], caches[1]._key_cache[:, :n])

@@ -57,7 +57,7 @@ class GraphDecoder:
     """One captured graph per model: ``step()`` decodes one token."""
 
     def __init__(self, model: torch.nn.Module, cache, *, max_new_tokens: int, fixed_token: Optional[int] = None,
-                 fuse: bool = True):
+                 fuse: bool = True, dense: bool = False):
         if not getattr(cache, "update_metadata_on_decode", False):
             raise ValueError("GraphDecoder needs a cache built with update_metadata_on_decode=True")
         kind = type(cache).__name__
@@ -69,10 +69,19 @@ class GraphDecoder:
                 raise ValueError("GraphDecoder runs the Twilight union attention without the resident cache")
         elif kind == "QuestTopKOffloadedCache":
             self.twilight = False
-            if cache.budget_pages is None:
+            if cache.budget_pages is None and not dense:
                 raise ValueError("GraphDecoder needs an absolute Quest budget (budget_pages)")
+            if dense and cache.previous_token_resident_cache:
+                raise ValueError("the dense comparator reads the slab directly (no resident cache)")
         else:
             raise ValueError("GraphDecoder runs a QuestTopKOffloadedCache or a TwilightMatchedBudgetOffloadedCache")
+        if dense and self.twilight:
+            raise ValueError("the dense comparator runs over a Quest cache")
+        # dense: no selection at all -- every whole page between the sink and
+        # the recent window is attended through the same page-tile kernel (the
+        # plan is every page, ascending), i.e. all rows but the <= bs - 1 rows
+        # of the partial page before the recent window
+        self.dense = bool(dense)
         inner = model.model
         cfg = model.config
         self.model, self.cache = model, cache
@@ -105,7 +114,7 @@ class GraphDecoder:
             # stage 1 keeps B0 pages per head (fewer for a short group), stage 2 top-p over their tokens
             self.k = min(max(1, math.ceil(cache.candidate_token_budget / cache.block_size)), self.P)
         else:
-            self.k = min(int(cache.budget_pages), self.P)
+            self.k = self.P if self.dense else min(int(cache.budget_pages), self.P)
         self.width = max(1, min(self.P, self.R * self.k))
         # device state: token, position, per-group length
         self.token = torch.full((1,), 1 if fixed_token is None else int(fixed_token), dtype=torch.long, device=dev)
@@ -160,6 +169,10 @@ class GraphDecoder:
                       torch.zeros((self.G, self.width), dtype=torch.uint8, device=dev),
                       torch.zeros((self.G,), dtype=torch.int32, device=dev)) for _ in self.layers]
         self.attn = [torch.empty((self.G, self.R, self.D), dtype=cache.dtype, device=dev) for _ in self.layers]
+        if self.dense:
+            self.dense_pages = torch.arange(self.width, dtype=torch.int32, device=dev).expand(self.G, -1).contiguous()
+            self.dense_masks = torch.full((self.G, self.width), (1 << self.R) - 1, dtype=torch.uint8, device=dev)
+            self.dense_counts = torch.zeros((self.G,), dtype=torch.int32, device=dev)
         if self.twilight:
             # stage-2 buffers, reused layer after layer: B0 pages, INT4 logits, union rows
             self.max_length = L0 + max_new_tokens
@@ -194,6 +207,12 @@ class GraphDecoder:
             if h_out is not None:
                 h = h_out
 
+        if self.dense:
+            # every whole page between the sink and the recent window, per group
+            L = self.lengths
+            sink_end = L.clamp(max=c.sink_tokens)
+            recent_start = torch.maximum(sink_end, L - max(0, c.recent_tokens - 1))
+            self.dense_counts.copy_(((recent_start - sink_end) // c.block_size).clamp(0, self.width))
         for li, layer in enumerate(self.layers):
             attn = layer.self_attn
             norm = layer.input_layernorm
@@ -225,12 +244,16 @@ class GraphDecoder:
                     kernels.silu_mul(gu, self.m)
                 delta = kernels.gemv(self.m, layer.mlp.down_proj.weight, layer.mlp.down_proj.bias, self.dn)
                 continue
-            kernels.quest_select_ragged(self.q32.view(G, R, D), c._page_min[e0:e0 + G, :self.P],
-                                        c._page_max[e0:e0 + G, :self.P], self.lengths, self.k, sink=c.sink_tokens,
-                                        recent=c.recent_tokens, block_size=c.block_size, plan_pages=pp,
-                                        plan_masks=pm, plan_counts=pc)
-            # the attention also appends the decode token and, when it completes a page, that page's min/max
-            meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G]) if self.fuse else {}
+            if self.dense:
+                pp, pm, pc = self.dense_pages, self.dense_masks, self.dense_counts
+                meta = {}
+            else:
+                kernels.quest_select_ragged(self.q32.view(G, R, D), c._page_min[e0:e0 + G, :self.P],
+                                            c._page_max[e0:e0 + G, :self.P], self.lengths, self.k,
+                                            sink=c.sink_tokens, recent=c.recent_tokens, block_size=c.block_size,
+                                            plan_pages=pp, plan_masks=pm, plan_counts=pc)
+                # the attention also appends the decode token and, when it completes a page, that page's min/max
+                meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G]) if self.fuse else {}
             if c.previous_token_resident_cache:
                 kernels.decode_attention_pages_resident(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp,
                                                         pc, c.resident_pages().view(e0, G), lengths=self.lengths,
@@ -244,7 +267,7 @@ class GraphDecoder:
                                                       sink=c.sink_tokens, recent=c.recent_tokens,
                                                       block_size=c.block_size, append=True, cur_k=k, cur_v=v,
                                                       softmax_scale=float(attn.scaling), out=self.attn[li], **meta)
-            if not self.fuse:
+            if not self.fuse and not self.dense:
                 kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
                                                     block_size=c.block_size, page_min=c._page_min,
                                                     page_max=c._page_max)
