@@ -121,9 +121,15 @@ int tw_quest_score(const float* q, const void* page_min, const void* page_max, i
  * scores [rows][P] fp32 (row stride score_row_stride) -> out [rows][k] int64
  * ascending page ids.  Ties go to the lowest index, NaN ranks highest, -0
  * equals +0.  1 <= k <= P.
+ * Rows of P > 8192 scores first keep the top min(k, n) of every 8192-score
+ * segment (an extra launch) and select among those: they need a workspace of
+ * tw_topk_sorted_workspace_size(rows, P) bytes (0, and workspace may be
+ * NULL, when P <= 8192) and (P / 8192) * k + min(k, P % 8192) <= 8192,
+ * else TW_EUNSUPPORTED.
  * ---------------------------------------------------------------------- */
+size_t tw_topk_sorted_workspace_size(int rows, int P);
 int tw_topk_sorted(const float* scores, int rows, int P, int64_t score_row_stride, int k,
-                   int64_t* out, void* stream);
+                   int64_t* out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Quest selection for one decoder layer: score, top-k and the GQA union
@@ -132,7 +138,11 @@ int tw_topk_sorted(const float* scores, int rows, int P, int64_t score_row_strid
  * prepare_layer_selection (quest_offload_cache.py:299-401) followed by
  * _selected_positions (:403-511) for the G entries of a layer, and the
  * Twilight stage-1 B0 selection (twilight_offload_cache.py:1128-1166).
- *   q [G][R][D] fp32; metadata as in tw_quest_score; P <= 8192 pages scored.
+ *   q [G][R][D] fp32; metadata as in tw_quest_score; P pages scored.  Above
+ *   8192 pages a segment pass (one more launch, as tw_topk_sorted) keeps each
+ *   8192-page segment's top k first, so (P / 8192) * k + min(k, P % 8192)
+ *   <= 8192 and, with a plan, the union's page bitmap (P / 4 + 8 * min(P, R*k)
+ *   bytes) within the 160 KB of LDS, else TW_EUNSUPPORTED.
  *   scores (nullable) [G][R][P] fp32 copy of the scores.
  *   sel_pages (nullable) [G][R][k] int32 ascending page ids per head
  *   (torch.topk(sorted=False) then sort, quest_offload_cache.py:373-374;

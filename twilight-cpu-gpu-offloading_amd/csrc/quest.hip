@@ -34,6 +34,18 @@
 //    into a page mask and writes the union plan: the ascending union pages
 //    with the bitmask of heads that selected each, and optionally the
 //    expanded row plan (sink ++ union page rows ++ recent ++ decode row).
+//
+// Rows longer than a block holds (P > kMaxSelPages pages, contexts past
+// 131K tokens at 16-token pages) take one more launch first: a block per
+// (row, segment of kMaxSelPages pages) keeps its segment's top
+// min(k, segment length) pages.  The row's top k under (key desc, index
+// asc) lies inside the union of its segments' top k -- a page beaten by k
+// pages of its own segment is beaten by them in the whole row -- so the
+// selection then runs over the compacted row (segment s's winners at
+// [s*k, s*k + k_s), ascending page order within and across segments) and
+// maps each compacted index back to its page.  The compaction keeps the
+// index order, so ties still go to the lowest page.  The union of such rows
+// goes through a page bitmap (one bit per page) instead of a byte per page.
 #pragma clang fp contract(off)
 
 #include <mutex>
@@ -429,7 +441,16 @@ struct SelectArgs {
   // Ragged groups (nullable): group g selects min(k, its candidate pages)
   // among ragged_pages(lengths[g]) <= P; selection slots beyond that get -1.
   const int32_t* lengths;
+  // Compacted long rows (nullable): scores holds each row's segment winners,
+  // map[row * score_stride + i] the page of compacted key i and widths[row]
+  // the row's key count.  keys_max bounds the keys of any row.
+  const int32_t* map;
+  const int32_t* widths;
+  int keys_max;
 };
+
+template <typename M>
+__device__ void emit_union_plan(const SelectArgs& s, int g, int nu, const int32_t* upage, const M* umask);
 
 // Union plan of group g: page_mask (LDS, byte per page, zero padded to a
 // multiple of 8) -> ascending union pages and their head masks, then the
@@ -470,13 +491,27 @@ __device__ void write_union_plan(const SelectArgs& s, int g, int P, const uint8_
     }
     nu += total;
   }
-  if (tid == 0 && s.plan_counts != nullptr) s.plan_counts[g] = nu;
-  if (direct) return;
+  if (direct) {
+    if (tid == 0 && s.plan_counts != nullptr) s.plan_counts[g] = nu;
+    return;
+  }
   __syncthreads();
+  emit_union_plan(s, g, nu, upage, umask);
+}
+
+// The union plan of group g from its nu union pages in LDS (ascending pages
+// upage[u], head masks umask[u]): the page plan and the optional row plan.
+template <typename M>
+__device__ void emit_union_plan(const SelectArgs& s, int g, int nu, const int32_t* upage, const M* umask) {
+  const int tid = threadIdx.x;
+  const uint8_t all = static_cast<uint8_t>((1u << s.R) - 1u);
+  int32_t* pp = s.plan_pages != nullptr ? s.plan_pages + static_cast<int64_t>(g) * s.plan_stride : nullptr;
+  uint8_t* pm = s.plan_masks != nullptr ? s.plan_masks + static_cast<int64_t>(g) * s.plan_stride : nullptr;
+  if (tid == 0 && s.plan_counts != nullptr) s.plan_counts[g] = nu;
   if (pp != nullptr) {
     for (int i = tid; i < nu; i += kBlock) {
       pp[i] = upage[i];
-      if (pm != nullptr) pm[i] = umask[i];
+      if (pm != nullptr) pm[i] = static_cast<uint8_t>(umask[i]);
     }
   }
   const int length = s.length;
@@ -501,7 +536,7 @@ __device__ void write_union_plan(const SelectArgs& s, int g, int P, const uint8_
         const int j = i - sink_end;
         const int u = pow2 ? (j >> sh) : j / bs;
         pos = s.sink + upage[u] * bs + (j - u * bs);
-        m = umask[u];
+        m = static_cast<uint8_t>(umask[u]);
       } else if (i < recent_end) {
         pos = recent_start + (i - page_end);
       } else {
@@ -519,6 +554,141 @@ __device__ __forceinline__ int32_t fetch_i32(const int32_t* p) {
 }
 __device__ __forceinline__ void publish_i32(int32_t* p, int32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------- long rows
+// Key count of a row of P pages after the segment pass.
+__host__ __device__ __forceinline__ int long_row_width(int P, int k) {
+  const int full = P / kMaxSelPages;
+  const int rem = P - full * kMaxSelPages;
+  return full * k + (k < rem ? k : rem);
+}
+
+struct SegArgs {
+  const float* scores;     // row r at + r * score_stride
+  int64_t score_stride;
+  int vec_last4;           // vector loads: last readable float4 start of a row
+  int P, k, nseg, R;
+  float* cscore;           // [rows][kMaxSelPages] segment winners' scores
+  int32_t* cidx;           // [rows][kMaxSelPages] their pages
+  int32_t* cwidth;         // [rows]
+  const int32_t* lengths;  // nullable: ragged groups (group = row / R)
+  int sink, recent, bs;
+};
+
+// Block = (row, segment): the segment's top min(k, its pages), in ascending
+// page order, at [segment * k, ...) of the compacted row.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void segment_topk_kernel(SegArgs a) {
+  __shared__ __align__(16) SelShared sh;
+  constexpr int KPT = kMaxSelPages / kBlock;
+  const int row = blockIdx.x / a.nseg;
+  const int sg = blockIdx.x - row * a.nseg;
+  const int length = fetch_i32(a.lengths != nullptr ? a.lengths + row / a.R : reinterpret_cast<const int32_t*>(a.scores));
+  const float* vals = a.scores + static_cast<int64_t>(row) * a.score_stride;
+  const int lo = sg * kMaxSelPages;
+  const int i0 = KPT * static_cast<int>(threadIdx.x);
+  uint32_t key[KPT];
+  if (VEC) {
+#pragma unroll
+    for (int q4 = 0; q4 < KPT / 4; ++q4) {
+      int at = lo + i0 + 4 * q4;
+      at = at < a.vec_last4 ? at : a.vec_last4;
+      const float4 v = *reinterpret_cast<const float4*>(vals + at);
+      key[4 * q4] = score_key(v.x);
+      key[4 * q4 + 1] = score_key(v.y);
+      key[4 * q4 + 2] = score_key(v.z);
+      key[4 * q4 + 3] = score_key(v.w);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int i = lo + i0 + j;
+      key[j] = score_key(vals[i < a.P ? i : a.P - 1]);
+    }
+  }
+  const int P = a.lengths != nullptr ? ragged_pages(length, a.sink, a.recent, a.bs, a.P) : a.P;
+  int n = P - lo;
+  n = n < 0 ? 0 : (n > kMaxSelPages ? kMaxSelPages : n);
+  const int ks = a.k < n ? a.k : n;
+  if (sg == 0 && threadIdx.x == 0) a.cwidth[row] = long_row_width(P, a.k);
+  if (ks == 0) return;  // block-uniform
+  uint32_t take;
+  int slot;
+  block_topk<KPT>(key, n, ks, sh, &take, &slot);
+  float* cs = a.cscore + static_cast<int64_t>(row) * kMaxSelPages + static_cast<int64_t>(sg) * a.k;
+  int32_t* ci = a.cidx + static_cast<int64_t>(row) * kMaxSelPages + static_cast<int64_t>(sg) * a.k;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    if ((take >> j) & 1u) {
+      cs[slot] = key_value(key[j]);
+      ci[slot] = lo + i0 + j;
+      ++slot;
+    }
+  }
+}
+
+// LDS of the bitmap union: page bits and word prefixes (P / 32 words each),
+// then at most min(P, R * k) union pages and 32-bit head masks.
+__host__ __device__ __forceinline__ size_t bitmap_union_lds_bytes(int P, int R, int k) {
+  const int64_t nw = (static_cast<int64_t>(P) + 31) / 32;
+  const int64_t rk = static_cast<int64_t>(R) * k;
+  const int64_t u_cap = rk < P ? rk : P;
+  return static_cast<size_t>(8 * nw + 8 * u_cap + 16);
+}
+
+// Union plan of group g over pages [0, P) through a page bitmap: selected
+// pages set their bits, a block scan of the words' popcounts ranks the union
+// pages (union page u = rank of its page), and every selection ORs its
+// head's bit into the mask of its union page.  k: pages per head.
+__device__ void union_plan_bitmap(const SelectArgs& s, int g, int P, int k, uint8_t* dyn, int* scan) {
+  const int tid = threadIdx.x;
+  const int nw = (P + 31) / 32;
+  const int n_sel = s.R * k;
+  const int u_cap = n_sel < P ? n_sel : P;
+  uint32_t* bits = reinterpret_cast<uint32_t*>(dyn);
+  int* pfx = reinterpret_cast<int*>(bits + nw);
+  int32_t* upage = pfx + nw;
+  uint32_t* umask = reinterpret_cast<uint32_t*>(upage + u_cap);
+  const int32_t* sel_g = s.sel_ws + static_cast<int64_t>(g) * s.R * s.k;
+  for (int w = tid; w < nw; w += kBlock) bits[w] = 0u;
+  for (int u = tid; u < u_cap; u += kBlock) umask[u] = 0u;
+  __syncthreads();
+  for (int i = tid; i < n_sel; i += kBlock) {
+    const int hr = i / k;
+    const int p = fetch_i32(sel_g + hr * s.k + (i - hr * k));
+    atomicOr(&bits[p >> 5], 1u << (p & 31));
+  }
+  __syncthreads();
+  constexpr int kWpt = 8;
+  int U = 0;
+  for (int base = 0; base < nw; base += kBlock * kWpt) {
+    const int w0 = base + kWpt * tid;
+    int c[kWpt], sum = 0;
+#pragma unroll
+    for (int j = 0; j < kWpt; ++j) {
+      c[j] = w0 + j < nw ? __popc(bits[w0 + j]) : 0;
+      sum += c[j];
+    }
+    int tot;
+    int acc = U + block_excl_scan(sum, scan, &tot);
+#pragma unroll
+    for (int j = 0; j < kWpt; ++j) {
+      if (w0 + j < nw) pfx[w0 + j] = acc;
+      acc += c[j];
+    }
+    U += tot;
+  }
+  __syncthreads();
+  for (int i = tid; i < n_sel; i += kBlock) {
+    const int hr = i / k;
+    const int p = fetch_i32(sel_g + hr * s.k + (i - hr * k));
+    const int u = pfx[p >> 5] + __popc(bits[p >> 5] & ((1u << (p & 31)) - 1u));
+    atomicOr(&umask[u], 1u << hr);
+    upage[u] = p;
+  }
+  __syncthreads();
+  emit_union_plan(s, g, U, upage, umask);
 }
 
 template <int KPT, bool VEC>
@@ -560,14 +730,16 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
     }
   }
   const int P = s.lengths != nullptr ? ragged_pages(length, s.sink, s.recent, s.bs, s.P) : s.P;
-  const int k = s.k < P ? s.k : P;
+  const int n_keys = s.widths != nullptr ? fetch_i32(s.widths + row) : P;  // compacted long rows
+  const int k = s.k < n_keys ? s.k : n_keys;
+  const int32_t* map_row = s.map != nullptr ? s.map + static_cast<int64_t>(row) * s.score_stride : nullptr;
   int32_t* ws_row = s.sel_ws != nullptr ? s.sel_ws + static_cast<int64_t>(row) * s.k : nullptr;
   int32_t* out32 = s.sel_out != nullptr ? s.sel_out + static_cast<int64_t>(row) * s.k : nullptr;
   int64_t* out64 = s.sel_out64 != nullptr ? s.sel_out64 + static_cast<int64_t>(row) * s.k : nullptr;
   if (k > 0) {
     uint32_t take;
     int slot;
-    block_topk<KPT>(key, P, k, sh, &take, &slot);
+    block_topk<KPT>(key, n_keys, k, sh, &take, &slot);
     const int i0 = KPT * static_cast<int>(threadIdx.x);
     constexpr int kStage = kLinBins + 64;
     if (k <= kStage) {
@@ -580,7 +752,7 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
       }
       __syncthreads();
       for (int i = threadIdx.x; i < k; i += kBlock) {
-        const int idx = st[i];
+        const int idx = map_row != nullptr ? map_row[st[i]] : st[i];
         if (ws_row != nullptr) publish_i32(ws_row + i, idx);
         if (out32 != nullptr) out32[i] = idx;
         if (out64 != nullptr) out64[i] = idx;
@@ -589,9 +761,10 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
 #pragma unroll
       for (int j = 0; j < KPT; ++j) {
         if ((take >> j) & 1u) {
-          if (ws_row != nullptr) publish_i32(ws_row + slot, i0 + j);
-          if (out32 != nullptr) out32[slot] = i0 + j;
-          if (out64 != nullptr) out64[slot] = i0 + j;
+          const int idx = map_row != nullptr ? map_row[i0 + j] : i0 + j;
+          if (ws_row != nullptr) publish_i32(ws_row + slot, idx);
+          if (out32 != nullptr) out32[slot] = idx;
+          if (out64 != nullptr) out64[slot] = idx;
           ++slot;
         }
       }
@@ -605,6 +778,10 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.flag)) return;
 
   // ---- last block of group g: union of the R selections ----
+  if (s.map != nullptr) {
+    union_plan_bitmap(s, g, P, k, dyn, sh.scan);
+    return;
+  }
   const int mask_bytes = ((P + 7) / 8) * 8;
   uint8_t* page_mask = dyn;
   int32_t* upage = reinterpret_cast<int32_t*>(dyn + mask_bytes);
@@ -647,22 +824,82 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
 
 size_t union_lds_bytes(int P) { return static_cast<size_t>((P + 7) / 8) * 8 + static_cast<size_t>(P) * 5 + 16; }
 
+constexpr size_t kMaxLds = 160 * 1024;  // gfx950: LDS per CU
+
+size_t select_lds_bytes(const SelectArgs& s) {
+  if (!s.want_union) return 0;
+  return s.map != nullptr ? bitmap_union_lds_bytes(s.P, s.R, s.k) : union_lds_bytes(s.P);
+}
+
 template <int KPT>
 int launch_select_kpt(const SelectArgs& s, int n_rows, bool vec, hipStream_t stream) {
-  const size_t lds = s.want_union ? union_lds_bytes(s.P) : 0;
-  if (vec) {
-    hipLaunchKernelGGL((quest_select_kernel<KPT, true>), dim3(n_rows), dim3(kBlock), lds, stream, s);
-  } else {
-    hipLaunchKernelGGL((quest_select_kernel<KPT, false>), dim3(n_rows), dim3(kBlock), lds, stream, s);
-  }
+  const size_t lds = select_lds_bytes(s);
+  if (lds > kMaxLds) return TW_EUNSUPPORTED;
+  auto kern = vec ? quest_select_kernel<KPT, true> : quest_select_kernel<KPT, false>;
+  if (lds + sizeof(SelShared) > 64 * 1024)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              static_cast<int>(lds));
+  hipLaunchKernelGGL(kern, dim3(n_rows), dim3(kBlock), lds, stream, s);
   return tw_host::check_launch();
 }
 
 int launch_select(const SelectArgs& s, int n_rows, bool vec, hipStream_t stream) {
-  if (s.P <= 4 * kBlock) return launch_select_kpt<4>(s, n_rows, vec, stream);
-  if (s.P <= 8 * kBlock) return launch_select_kpt<8>(s, n_rows, vec, stream);
-  if (s.P <= 16 * kBlock) return launch_select_kpt<16>(s, n_rows, vec, stream);
+  const int keys = s.keys_max > 0 ? s.keys_max : s.P;
+  if (keys <= 4 * kBlock) return launch_select_kpt<4>(s, n_rows, vec, stream);
+  if (keys <= 8 * kBlock) return launch_select_kpt<8>(s, n_rows, vec, stream);
+  if (keys <= 16 * kBlock) return launch_select_kpt<16>(s, n_rows, vec, stream);
   return launch_select_kpt<32>(s, n_rows, vec, stream);
+}
+
+// Workspace of the segment pass: compacted scores and pages per row, then
+// the row widths (256-byte aligned pieces).
+size_t align256(size_t n) { return (n + 255) & ~static_cast<size_t>(255); }
+size_t long_row_bytes(int64_t rows, int P) {
+  if (P <= kMaxSelPages) return 0;
+  return 2 * align256(static_cast<size_t>(rows) * kMaxSelPages * 4) + align256(static_cast<size_t>(rows) * 4);
+}
+
+// Validity of a long-row selection: the compacted row fits a block and the
+// union's bitmap fits the LDS (want_union).
+int check_long_rows(int P, int R, int k, bool want_union) {
+  if (P <= kMaxSelPages) return TW_OK;
+  if (long_row_width(P, k) > kMaxSelPages) return TW_EUNSUPPORTED;
+  if (want_union && bitmap_union_lds_bytes(P, R, k) > kMaxLds) return TW_EUNSUPPORTED;
+  return TW_OK;
+}
+
+// Runs the segment pass over s's rows (scores at s.scores / s.score_stride)
+// into the long-row workspace `lw`, and points s at the compacted rows.
+int prepare_long_rows(SelectArgs& s, int n_rows, bool vec, uint8_t* lw, hipStream_t stream) {
+  SegArgs a{};
+  a.scores = s.scores;
+  a.score_stride = s.score_stride;
+  a.vec_last4 = s.vec_last4;
+  a.P = s.P;
+  a.k = s.k;
+  a.nseg = (s.P + kMaxSelPages - 1) / kMaxSelPages;
+  a.R = s.R;
+  a.cscore = reinterpret_cast<float*>(lw);
+  a.cidx = reinterpret_cast<int32_t*>(lw + align256(static_cast<size_t>(n_rows) * kMaxSelPages * 4));
+  a.cwidth = reinterpret_cast<int32_t*>(lw + 2 * align256(static_cast<size_t>(n_rows) * kMaxSelPages * 4));
+  a.lengths = s.lengths;
+  a.sink = s.sink;
+  a.recent = s.recent;
+  a.bs = s.bs;
+  const dim3 grid(static_cast<unsigned>(n_rows) * a.nseg);
+  if (vec)
+    hipLaunchKernelGGL(segment_topk_kernel<true>, grid, dim3(kBlock), 0, stream, a);
+  else
+    hipLaunchKernelGGL(segment_topk_kernel<false>, grid, dim3(kBlock), 0, stream, a);
+  const int rc = tw_host::check_launch();
+  if (rc != TW_OK) return rc;
+  s.scores = a.cscore;
+  s.score_stride = kMaxSelPages;
+  s.vec_last4 = kMaxSelPages - 4;
+  s.map = a.cidx;
+  s.widths = a.cwidth;
+  s.keys_max = long_row_width(s.P, s.k);
+  return TW_OK;
 }
 
 template <typename DT>
@@ -712,12 +949,22 @@ extern "C" int tw_quest_score(const float* q, const void* page_min, const void* 
   return tw::dispatch_score(dtype, a, static_cast<hipStream_t>(stream));
 }
 
+extern "C" size_t tw_topk_sorted_workspace_size(int rows, int P) {
+  if (rows <= 0 || P <= 0) return 0;
+  return tw::long_row_bytes(rows, P);
+}
+
 extern "C" int tw_topk_sorted(const float* scores, int rows, int P, int64_t score_row_stride, int k,
-                              int64_t* out, void* stream) {
+                              int64_t* out, void* workspace, size_t workspace_bytes, void* stream) {
   if (scores == nullptr || out == nullptr || rows < 0 || P <= 0 || k <= 0 || k > P) return TW_EINVAL;
   if (score_row_stride < P) return TW_EINVAL;
-  if (P > tw::kMaxSelPages) return TW_EUNSUPPORTED;
+  {
+    const int rc = tw::check_long_rows(P, 1, k, false);
+    if (rc != TW_OK) return rc;
+  }
   if (rows == 0) return TW_OK;
+  if (P > tw::kMaxSelPages && (workspace == nullptr || workspace_bytes < tw_topk_sorted_workspace_size(rows, P)))
+    return TW_ENOMEM;
   tw::SelectArgs s{};
   s.scores = scores;
   s.score_stride = score_row_stride;
@@ -731,15 +978,47 @@ extern "C" int tw_topk_sorted(const float* scores, int rows, int P, int64_t scor
   // of a row ends exactly at its last score.
   const bool vec = (score_row_stride % 4) == 0 && (P % 4) == 0 && (reinterpret_cast<uintptr_t>(scores) % 16) == 0;
   s.vec_last4 = P - 4;
-  return tw::launch_select(s, rows, vec, static_cast<hipStream_t>(stream));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (P > tw::kMaxSelPages) {
+    const int rc = tw::prepare_long_rows(s, rows, vec, static_cast<uint8_t*>(workspace), st);
+    if (rc != TW_OK) return rc;
+    return tw::launch_select(s, rows, true, st);
+  }
+  return tw::launch_select(s, rows, vec, st);
 }
 
 extern "C" size_t tw_quest_select_workspace_size(int G, int R, int P) {
   // arrival counters | scores [G][R][P rounded up to 4] | selections [G][R][<= P]
+  // | (P > 8192) the segment pass's compacted rows
   if (G <= 0 || R <= 0 || P <= 0) return 0;
-  return tw::counter_bytes(G) + static_cast<size_t>(G) * R * tw::padded(P) * sizeof(float) +
-         static_cast<size_t>(G) * R * P * sizeof(int32_t);
+  return tw::counter_bytes(G) + tw::align256(static_cast<size_t>(G) * R * tw::padded(P) * sizeof(float)) +
+         tw::align256(static_cast<size_t>(G) * R * P * sizeof(int32_t)) +
+         tw::long_row_bytes(static_cast<int64_t>(G) * R, P);
 }
+
+namespace tw {
+namespace {
+// Workspace pieces of the selection (layout of tw_quest_select_workspace_size).
+struct SelectWorkspace {
+  unsigned int* counters;
+  float* scores;
+  int32_t* sel;
+  uint8_t* long_rows;
+};
+SelectWorkspace carve(void* workspace, int G, int R, int P) {
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  SelectWorkspace w{};
+  w.counters = reinterpret_cast<unsigned int*>(ws);
+  ws += counter_bytes(G);
+  w.scores = reinterpret_cast<float*>(ws);
+  ws += align256(static_cast<size_t>(G) * R * padded(P) * sizeof(float));
+  w.sel = reinterpret_cast<int32_t*>(ws);
+  ws += align256(static_cast<size_t>(G) * R * P * sizeof(int32_t));
+  w.long_rows = ws;
+  return w;
+}
+}  // namespace
+}  // namespace tw
 
 extern "C" int tw_quest_select(const float* q, const void* page_min, const void* page_max, int dtype, int G,
                                int R, int P, int D, int64_t page_group_stride, int k, float* scores,
@@ -749,10 +1028,13 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
                                int append_position, void* workspace, size_t workspace_bytes, void* stream) {
   if (!tw::check_score_args(q, page_min, page_max, G, R, P, D, page_group_stride)) return TW_EINVAL;
   if (k <= 0 || k > P) return TW_EINVAL;
-  if (P > tw::kMaxSelPages) return TW_EUNSUPPORTED;
   const bool row_plan = rows != nullptr || row_counts != nullptr;
   const bool page_plan = plan_pages != nullptr || plan_counts != nullptr;
   if ((row_plan || page_plan) && R > 8) return TW_EINVAL;
+  {
+    const int rc = tw::check_long_rows(P, R, k, row_plan || page_plan);
+    if (rc != TW_OK) return rc;
+  }
   if ((plan_masks != nullptr && plan_pages == nullptr) || (row_masks != nullptr && rows == nullptr)) return TW_EINVAL;
   if (plan_pages != nullptr && plan_stride < (static_cast<int64_t>(R) * k < P ? static_cast<int64_t>(R) * k : P))
     return TW_EINVAL;
@@ -772,10 +1054,10 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
     }
   }
   if (workspace == nullptr || workspace_bytes < tw_quest_select_workspace_size(G, R, P)) return TW_ENOMEM;
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
-  unsigned int* counters = reinterpret_cast<unsigned int*>(ws);
-  float* score_ws = reinterpret_cast<float*>(ws + tw::counter_bytes(G));
-  int32_t* sel_ws = reinterpret_cast<int32_t*>(score_ws + static_cast<int64_t>(G) * R * tw::padded(P));
+  const tw::SelectWorkspace w = tw::carve(workspace, G, R, P);
+  unsigned int* counters = w.counters;
+  float* score_ws = w.scores;
+  int32_t* sel_ws = w.sel;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   tw::ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P, D, score_ws, tw::padded(P), scores};
   tw::SelectArgs s{};
@@ -803,8 +1085,12 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
   s.length = length;
   s.append_position = append_position;
   s.counters = counters;
-  const int rc = tw::dispatch_score(dtype, a, st);
+  int rc = tw::dispatch_score(dtype, a, st);
   if (rc != TW_OK) return rc;
+  if (P > tw::kMaxSelPages) {
+    rc = tw::prepare_long_rows(s, G * R, true, w.long_rows, st);
+    if (rc != TW_OK) return rc;
+  }
   return tw::launch_select(s, G * R, true, st);
 }
 
@@ -816,18 +1102,21 @@ extern "C" int tw_quest_select_ragged(const float* q, const void* page_min, cons
   if (!tw::check_score_args(q, page_min, page_max, G, R, P_max, D, page_group_stride)) return TW_EINVAL;
   if (lengths == nullptr || k <= 0 || k > P_max) return TW_EINVAL;
   if (sink < 0 || recent <= 0 || block_size <= 0) return TW_EINVAL;
-  if (P_max > tw::kMaxSelPages) return TW_EUNSUPPORTED;
   const bool page_plan = plan_pages != nullptr || plan_counts != nullptr;
   if (page_plan && (R > 8 || plan_pages == nullptr || plan_counts == nullptr)) return TW_EINVAL;
+  {
+    const int rc = tw::check_long_rows(P_max, R, k, page_plan);
+    if (rc != TW_OK) return rc;
+  }
   if (plan_masks != nullptr && plan_pages == nullptr) return TW_EINVAL;
   if (plan_pages != nullptr &&
       plan_stride < (static_cast<int64_t>(R) * k < P_max ? static_cast<int64_t>(R) * k : P_max))
     return TW_EINVAL;
   if (workspace == nullptr || workspace_bytes < tw_quest_select_workspace_size(G, R, P_max)) return TW_ENOMEM;
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
-  unsigned int* counters = reinterpret_cast<unsigned int*>(ws);
-  float* score_ws = reinterpret_cast<float*>(ws + tw::counter_bytes(G));
-  int32_t* sel_ws = reinterpret_cast<int32_t*>(score_ws + static_cast<int64_t>(G) * R * tw::padded(P_max));
+  const tw::SelectWorkspace w = tw::carve(workspace, G, R, P_max);
+  unsigned int* counters = w.counters;
+  float* score_ws = w.scores;
+  int32_t* sel_ws = w.sel;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   tw::ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P_max, D, score_ws, tw::padded(P_max), nullptr,
                   lengths, sink, recent, block_size};
@@ -852,8 +1141,12 @@ extern "C" int tw_quest_select_ragged(const float* q, const void* page_min, cons
   s.append_position = -1;
   s.counters = counters;
   s.lengths = lengths;
-  const int rc = tw::dispatch_score(dtype, a, st);
+  int rc = tw::dispatch_score(dtype, a, st);
   if (rc != TW_OK) return rc;
+  if (P_max > tw::kMaxSelPages) {
+    rc = tw::prepare_long_rows(s, G * R, true, w.long_rows, st);
+    if (rc != TW_OK) return rc;
+  }
   return tw::launch_select(s, G * R, true, st);
 }
 

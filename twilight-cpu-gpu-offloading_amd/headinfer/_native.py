@@ -60,7 +60,8 @@ _HIP_SIGNATURES = {
     "tw_rms_norm_gemv_silu": (i32, [vp, vp, vp, f32, vp, vp, vp, vp, i32, i32, i32, vp]),
     "tw_int4_dequantize": (i32, [vp, vp, vp, i32, i64, i32, vp, vp]),
     "tw_quest_score": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp]),
-    "tw_topk_sorted": (i32, [vp, i32, i32, i64, i32, vp, vp]),
+    "tw_topk_sorted_workspace_size": (szt, [i32, i32]),
+    "tw_topk_sorted": (i32, [vp, i32, i32, i64, i32, vp, vp, szt, vp]),
     "tw_quest_select_workspace_size": (szt, [i32, i32, i32]),
     "tw_quest_select": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, i32, vp, vp, vp, vp, vp, i64, vp, vp, vp, i64,
                               i32, i32, i32, i32, i32, vp, szt, vp]),

@@ -109,7 +109,7 @@ class GraphDecoder:
         self.max_new_tokens = max_new_tokens
         self.fixed_token = fixed_token
         self.fuse = fuse
-        self.P = min(int(cache._page_min.shape[1]), 8192)
+        self.P = int(cache._page_min.shape[1])
         if self.twilight:
             # stage 1 keeps B0 pages per head (fewer for a short group), stage 2 top-p over their tokens
             self.k = min(max(1, math.ceil(cache.candidate_token_budget / cache.block_size)), self.P)

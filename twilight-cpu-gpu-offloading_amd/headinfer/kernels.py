@@ -353,9 +353,11 @@ def topk_sorted(scores: torch.Tensor, k: int) -> torch.Tensor:
     if flat.stride(1) != 1:
         flat = flat.contiguous()
     out = torch.empty((flat.shape[0], k), dtype=torch.int64, device=dev)
+    nbytes = hip().tw_topk_sorted_workspace_size(flat.shape[0], P)
+    ws = WORKSPACE.get(dev, "topk_sorted", nbytes) if nbytes else None
     with torch.cuda.device(dev):
-        check(hip().tw_topk_sorted(ptr(flat), flat.shape[0], P, flat.stride(0), k, ptr(out), stream_handle(dev)),
-              "topk_sorted")
+        check(hip().tw_topk_sorted(ptr(flat), flat.shape[0], P, flat.stride(0), k, ptr(out), ptr(ws),
+                                   0 if ws is None else ws.numel(), stream_handle(dev)), "topk_sorted")
     return out.view(*scores.shape[:-1], k)
 
 
