@@ -449,24 +449,24 @@ struct SelectArgs {
   int keys_max;
 };
 
-template <typename M>
+template <int NT, typename M>
 __device__ void emit_union_plan(const SelectArgs& s, int g, int nu, const int32_t* upage, const M* umask);
 
 // Union plan of group g: page_mask (LDS, byte per page, zero padded to a
 // multiple of 8) -> ascending union pages and their head masks, then the
-// optional row plan.  Thread t owns pages [8t, 8t + 8) of each 2048-page
+// optional row plan.  Thread t owns pages [8t, 8t + 8) of each 8 NT-page
 // stretch.
+template <int NT>
 __device__ void write_union_plan(const SelectArgs& s, int g, int P, const uint8_t* page_mask, int32_t* upage,
                                  uint8_t* umask, int* scan) {
   const int tid = threadIdx.x;
-  const uint8_t all = static_cast<uint8_t>((1u << s.R) - 1u);
   // Without a row plan (rows, row counts) the union goes straight to the
   // page plan in global memory; the row plan reads it back from LDS.
   const bool direct = s.rows == nullptr && s.row_counts == nullptr;
   int32_t* pp = s.plan_pages != nullptr ? s.plan_pages + static_cast<int64_t>(g) * s.plan_stride : nullptr;
   uint8_t* pm = s.plan_masks != nullptr ? s.plan_masks + static_cast<int64_t>(g) * s.plan_stride : nullptr;
   int nu = 0;
-  for (int base = 0; base < P; base += kBlock * 8) {
+  for (int base = 0; base < P; base += NT * 8) {
     const int p0 = base + 8 * tid;
     uint2 w = make_uint2(0u, 0u);
     if (p0 < P) w = reinterpret_cast<const uint2*>(page_mask)[p0 >> 3];
@@ -474,7 +474,7 @@ __device__ void write_union_plan(const SelectArgs& s, int g, int P, const uint8_
 #pragma unroll
     for (int b = 0; b < 4; ++b) cnt += (((w.x >> (8 * b)) & 255u) != 0u) + (((w.y >> (8 * b)) & 255u) != 0u);
     int total;
-    int slot = nu + block_excl_scan(cnt, scan, &total);
+    int slot = nu + block_excl_scan<NT>(cnt, scan, &total);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
       const uint32_t m = ((b < 4 ? w.x : w.y) >> (8 * (b & 3))) & 255u;
@@ -496,12 +496,12 @@ __device__ void write_union_plan(const SelectArgs& s, int g, int P, const uint8_
     return;
   }
   __syncthreads();
-  emit_union_plan(s, g, nu, upage, umask);
+  emit_union_plan<NT>(s, g, nu, upage, umask);
 }
 
 // The union plan of group g from its nu union pages in LDS (ascending pages
 // upage[u], head masks umask[u]): the page plan and the optional row plan.
-template <typename M>
+template <int NT, typename M>
 __device__ void emit_union_plan(const SelectArgs& s, int g, int nu, const int32_t* upage, const M* umask) {
   const int tid = threadIdx.x;
   const uint8_t all = static_cast<uint8_t>((1u << s.R) - 1u);
@@ -509,7 +509,7 @@ __device__ void emit_union_plan(const SelectArgs& s, int g, int nu, const int32_
   uint8_t* pm = s.plan_masks != nullptr ? s.plan_masks + static_cast<int64_t>(g) * s.plan_stride : nullptr;
   if (tid == 0 && s.plan_counts != nullptr) s.plan_counts[g] = nu;
   if (pp != nullptr) {
-    for (int i = tid; i < nu; i += kBlock) {
+    for (int i = tid; i < nu; i += NT) {
       pp[i] = upage[i];
       if (pm != nullptr) pm[i] = static_cast<uint8_t>(umask[i]);
     }
@@ -527,7 +527,7 @@ __device__ void emit_union_plan(const SelectArgs& s, int g, int nu, const int32_
     const int sh = pow2 ? __ffs(bs) - 1 : 0;
     int32_t* rows = s.rows + static_cast<int64_t>(g) * s.rows_stride;
     uint8_t* masks = s.row_masks != nullptr ? s.row_masks + static_cast<int64_t>(g) * s.rows_stride : nullptr;
-    for (int i = tid; i < count; i += kBlock) {
+    for (int i = tid; i < count; i += NT) {
       int pos;
       uint8_t m = all;
       if (i < sink_end) {
@@ -641,6 +641,7 @@ __host__ __device__ __forceinline__ size_t bitmap_union_lds_bytes(int P, int R, 
 // pages set their bits, a block scan of the words' popcounts ranks the union
 // pages (union page u = rank of its page), and every selection ORs its
 // head's bit into the mask of its union page.  k: pages per head.
+template <int NT>
 __device__ void union_plan_bitmap(const SelectArgs& s, int g, int P, int k, uint8_t* dyn, int* scan) {
   const int tid = threadIdx.x;
   const int nw = (P + 31) / 32;
@@ -651,10 +652,10 @@ __device__ void union_plan_bitmap(const SelectArgs& s, int g, int P, int k, uint
   int32_t* upage = pfx + nw;
   uint32_t* umask = reinterpret_cast<uint32_t*>(upage + u_cap);
   const int32_t* sel_g = s.sel_ws + static_cast<int64_t>(g) * s.R * s.k;
-  for (int w = tid; w < nw; w += kBlock) bits[w] = 0u;
-  for (int u = tid; u < u_cap; u += kBlock) umask[u] = 0u;
+  for (int w = tid; w < nw; w += NT) bits[w] = 0u;
+  for (int u = tid; u < u_cap; u += NT) umask[u] = 0u;
   __syncthreads();
-  for (int i = tid; i < n_sel; i += kBlock) {
+  for (int i = tid; i < n_sel; i += NT) {
     const int hr = i / k;
     const int p = fetch_i32(sel_g + hr * s.k + (i - hr * k));
     atomicOr(&bits[p >> 5], 1u << (p & 31));
@@ -662,7 +663,7 @@ __device__ void union_plan_bitmap(const SelectArgs& s, int g, int P, int k, uint
   __syncthreads();
   constexpr int kWpt = 8;
   int U = 0;
-  for (int base = 0; base < nw; base += kBlock * kWpt) {
+  for (int base = 0; base < nw; base += NT * kWpt) {
     const int w0 = base + kWpt * tid;
     int c[kWpt], sum = 0;
 #pragma unroll
@@ -671,7 +672,7 @@ __device__ void union_plan_bitmap(const SelectArgs& s, int g, int P, int k, uint
       sum += c[j];
     }
     int tot;
-    int acc = U + block_excl_scan(sum, scan, &tot);
+    int acc = U + block_excl_scan<NT>(sum, scan, &tot);
 #pragma unroll
     for (int j = 0; j < kWpt; ++j) {
       if (w0 + j < nw) pfx[w0 + j] = acc;
@@ -680,7 +681,7 @@ __device__ void union_plan_bitmap(const SelectArgs& s, int g, int P, int k, uint
     U += tot;
   }
   __syncthreads();
-  for (int i = tid; i < n_sel; i += kBlock) {
+  for (int i = tid; i < n_sel; i += NT) {
     const int hr = i / k;
     const int p = fetch_i32(sel_g + hr * s.k + (i - hr * k));
     const int u = pfx[p >> 5] + __popc(bits[p >> 5] & ((1u << (p & 31)) - 1u));
@@ -688,12 +689,12 @@ __device__ void union_plan_bitmap(const SelectArgs& s, int g, int P, int k, uint
     upage[u] = p;
   }
   __syncthreads();
-  emit_union_plan(s, g, U, upage, umask);
+  emit_union_plan<NT>(s, g, U, upage, umask);
 }
 
-template <int KPT, bool VEC>
-__global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
-  __shared__ __align__(16) SelShared sh;
+template <int KPT, bool VEC, int NT>
+__global__ __launch_bounds__(NT) void quest_select_kernel(SelectArgs s) {
+  __shared__ __align__(16) SelSharedT<NT> sh;
   extern __shared__ __align__(16) uint8_t dyn[];  // union scratch
   const int row = blockIdx.x;
   const int g = row / s.R;
@@ -707,17 +708,28 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
     const int i0 = KPT * static_cast<int>(threadIdx.x);
     if (VEC) {
       // Rows are 16-byte aligned and readable up to vec_last4 + 3: a float4
-      // start clamped to vec_last4 stays inside the row.
+      // start clamped to vec_last4 (a float2 start to vec_last4 + 2, a float
+      // to vec_last4 + 3) stays inside the row and below P covers the
+      // thread's own keys.
       const int last4 = s.vec_last4;
+      if constexpr (KPT >= 4) {
 #pragma unroll
-      for (int q4 = 0; q4 < KPT / 4; ++q4) {
-        int at = i0 + 4 * q4;
-        at = at < last4 ? at : last4;
-        const float4 v = *reinterpret_cast<const float4*>(vals + at);
-        key[4 * q4] = score_key(v.x);
-        key[4 * q4 + 1] = score_key(v.y);
-        key[4 * q4 + 2] = score_key(v.z);
-        key[4 * q4 + 3] = score_key(v.w);
+        for (int q4 = 0; q4 < KPT / 4; ++q4) {
+          int at = i0 + 4 * q4;
+          at = at < last4 ? at : last4;
+          const float4 v = *reinterpret_cast<const float4*>(vals + at);
+          key[4 * q4] = score_key(v.x);
+          key[4 * q4 + 1] = score_key(v.y);
+          key[4 * q4 + 2] = score_key(v.z);
+          key[4 * q4 + 3] = score_key(v.w);
+        }
+      } else if constexpr (KPT == 2) {
+        const int at = i0 < last4 + 2 ? i0 : last4 + 2;
+        const float2 v = *reinterpret_cast<const float2*>(vals + at);
+        key[0] = score_key(v.x);
+        key[1] = score_key(v.y);
+      } else {
+        key[0] = score_key(vals[i0 < last4 + 3 ? i0 : last4 + 3]);
       }
     } else {
       // (clamped to the buffer's P: keys past a ragged row's end are never
@@ -751,7 +763,7 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
         if ((take >> j) & 1u) st[slot++] = i0 + j;
       }
       __syncthreads();
-      for (int i = threadIdx.x; i < k; i += kBlock) {
+      for (int i = threadIdx.x; i < k; i += NT) {
         const int idx = map_row != nullptr ? map_row[st[i]] : st[i];
         if (ws_row != nullptr) publish_i32(ws_row + i, idx);
         if (out32 != nullptr) out32[i] = idx;
@@ -770,7 +782,7 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
       }
     }
   }
-  for (int slot = k + static_cast<int>(threadIdx.x); slot < s.k; slot += kBlock) {
+  for (int slot = k + static_cast<int>(threadIdx.x); slot < s.k; slot += NT) {
     if (out32 != nullptr) out32[slot] = -1;
     if (out64 != nullptr) out64[slot] = -1;
   }
@@ -779,7 +791,7 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
 
   // ---- last block of group g: union of the R selections ----
   if (s.map != nullptr) {
-    union_plan_bitmap(s, g, P, k, dyn, sh.scan);
+    union_plan_bitmap<NT>(s, g, P, k, dyn, sh.scan);
     return;
   }
   const int mask_bytes = ((P + 7) / 8) * 8;
@@ -795,31 +807,31 @@ __global__ __launch_bounds__(kBlock) void quest_select_kernel(SelectArgs s) {
   if (n_sel > 0) {
 #pragma unroll
     for (int u = 0; u < kPre; ++u) {
-      int i = static_cast<int>(threadIdx.x) + u * kBlock;
+      int i = static_cast<int>(threadIdx.x) + u * NT;
       i = i < n_sel ? i : n_sel - 1;
       const int hr = i / k;
       pre[u] = fetch_i32(sel_g + hr * s.k + (i - hr * k));
     }
   }
-  for (int i = threadIdx.x; i < mask_bytes / 4; i += kBlock) reinterpret_cast<uint32_t*>(page_mask)[i] = 0u;
+  for (int i = threadIdx.x; i < mask_bytes / 4; i += NT) reinterpret_cast<uint32_t*>(page_mask)[i] = 0u;
   __syncthreads();
   if (n_sel > 0) {
 #pragma unroll
     for (int u = 0; u < kPre; ++u) {
-      const int i = static_cast<int>(threadIdx.x) + u * kBlock;
+      const int i = static_cast<int>(threadIdx.x) + u * NT;
       if (i < n_sel) {
         const int hr = i / k;
         atomicOr(reinterpret_cast<uint32_t*>(page_mask) + (pre[u] >> 2), (1u << hr) << (8 * (pre[u] & 3)));
       }
     }
   }
-  for (int i = static_cast<int>(threadIdx.x) + kPre * kBlock; i < n_sel; i += kBlock) {
+  for (int i = static_cast<int>(threadIdx.x) + kPre * NT; i < n_sel; i += NT) {
     const int hr = i / k;
     const int id = fetch_i32(sel_g + hr * s.k + (i - hr * k));
     atomicOr(reinterpret_cast<uint32_t*>(page_mask) + (id >> 2), (1u << hr) << (8 * (id & 3)));
   }
   __syncthreads();
-  write_union_plan(s, g, P, page_mask, upage, umask, sh.scan);
+  write_union_plan<NT>(s, g, P, page_mask, upage, umask, sh.scan);
 }
 
 size_t union_lds_bytes(int P) { return static_cast<size_t>((P + 7) / 8) * 8 + static_cast<size_t>(P) * 5 + 16; }
@@ -831,24 +843,46 @@ size_t select_lds_bytes(const SelectArgs& s) {
   return s.map != nullptr ? bitmap_union_lds_bytes(s.P, s.R, s.k) : union_lds_bytes(s.P);
 }
 
+// Threads of a selection block (one row per block).  512 measured best at
+// 2028 pages: 1024 threads paid more in 16-wave barriers than they saved.
+#ifndef TW_SELECT_THREADS
+#define TW_SELECT_THREADS 512
+#endif
+constexpr int kSelectThreads = TW_SELECT_THREADS;
+
 template <int KPT>
 int launch_select_kpt(const SelectArgs& s, int n_rows, bool vec, hipStream_t stream) {
+  constexpr int NT = kSelectThreads;
   const size_t lds = select_lds_bytes(s);
   if (lds > kMaxLds) return TW_EUNSUPPORTED;
-  auto kern = vec ? quest_select_kernel<KPT, true> : quest_select_kernel<KPT, false>;
-  if (lds + sizeof(SelShared) > 64 * 1024)
+  auto kern = vec ? quest_select_kernel<KPT, true, NT> : quest_select_kernel<KPT, false, NT>;
+  if (lds + sizeof(SelSharedT<NT>) > 64 * 1024)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               static_cast<int>(lds));
-  hipLaunchKernelGGL(kern, dim3(n_rows), dim3(kBlock), lds, stream, s);
+  hipLaunchKernelGGL(kern, dim3(n_rows), dim3(NT), lds, stream, s);
   return tw_host::check_launch();
 }
 
 int launch_select(const SelectArgs& s, int n_rows, bool vec, hipStream_t stream) {
+  constexpr int NT = kSelectThreads;
   const int keys = s.keys_max > 0 ? s.keys_max : s.P;
-  if (keys <= 4 * kBlock) return launch_select_kpt<4>(s, n_rows, vec, stream);
-  if (keys <= 8 * kBlock) return launch_select_kpt<8>(s, n_rows, vec, stream);
-  if (keys <= 16 * kBlock) return launch_select_kpt<16>(s, n_rows, vec, stream);
-  return launch_select_kpt<32>(s, n_rows, vec, stream);
+  if constexpr (NT >= 1024) {
+    if (keys <= NT) return launch_select_kpt<1>(s, n_rows, vec, stream);
+  }
+  if constexpr (NT >= 512) {
+    if (keys <= 2 * NT) return launch_select_kpt<2>(s, n_rows, vec, stream);
+  }
+  if (keys <= 4 * NT) return launch_select_kpt<4>(s, n_rows, vec, stream);
+  if constexpr (8 * NT >= kMaxSelPages) {
+    return launch_select_kpt<8>(s, n_rows, vec, stream);
+  } else if constexpr (16 * NT >= kMaxSelPages) {
+    if (keys <= 8 * NT) return launch_select_kpt<8>(s, n_rows, vec, stream);
+    return launch_select_kpt<16>(s, n_rows, vec, stream);
+  } else {
+    if (keys <= 8 * NT) return launch_select_kpt<8>(s, n_rows, vec, stream);
+    if (keys <= 16 * NT) return launch_select_kpt<16>(s, n_rows, vec, stream);
+    return launch_select_kpt<32>(s, n_rows, vec, stream);
+  }
 }
 
 // Workspace of the segment pass: compacted scores and pages per row, then

@@ -1,15 +1,16 @@
 // Block-wide exact top-k over register-resident keys, shared by the Quest
 // page selection and the Twilight token selection.
 //
-// A block of 256 threads holds one row of scores as KPT contiguous order keys
-// per thread (score_key: NaN highest, -0 == +0).  A pass histograms the
-// remaining candidates into bins that are monotone in the key -- 2048 bins
-// linear in the score value over the candidates' range when that range is
-// finite, else the next 8-bit digit below the candidates' common key prefix
-// -- finds the bin holding the k-th largest, takes every candidate above it
-// and keeps the bin's keys as the next candidates.  At most 256 candidates
-// are ranked exactly by (key desc, index asc); equal candidates are taken
-// lowest index first.  The winners are reported in ascending index order.
+// A block of NT threads (256 or more) holds one row of scores as KPT
+// contiguous order keys per thread (score_key: NaN highest, -0 == +0).  A
+// pass histograms the remaining candidates into bins that are monotone in
+// the key -- 2048 bins linear in the score value over the candidates' range
+// when that range is finite, else the next 8-bit digit below the candidates'
+// common key prefix -- finds the bin holding the k-th largest, takes every
+// candidate above it and keeps the bin's keys as the next candidates.  At
+// most 256 candidates (kExactMax, whatever NT) are ranked exactly by (key
+// desc, index asc); equal candidates are taken lowest index first.  The
+// winners are reported in ascending index order.
 #pragma once
 
 #include "tw_common.h"
@@ -17,30 +18,39 @@
 namespace tw {
 namespace sel {
 
-constexpr int kBlock = 256;
+constexpr int kBlock = 256;  // threads of a selection block unless a kernel says otherwise
 constexpr int kWaves = kBlock / kWave;
 constexpr int kMaxSelPages = 8192;  // longest row
 constexpr int kLinBins = 2048;
+constexpr int kExactMax = 256;      // at most this many candidates are ranked pairwise
 
-struct SelShared {
+// Block-shared state of a selection block of NT threads (NT a multiple of
+// 256: the linear bins split evenly over the threads).
+template <int NT>
+struct SelSharedT {
+  static constexpr int kW = NT / kWave;
+  static_assert(NT % 256 == 0 && NT <= kLinBins, "whole bins per thread");
   uint32_t hist[kLinBins + 64];
-  uint32_t ckey[kBlock];
-  int32_t cidx[kBlock];
+  uint32_t ckey[kExactMax];
+  int32_t cidx[kExactMax];
   uint32_t selbits[kMaxSelPages / 32];
-  uint32_t red_max[kWaves];
-  uint32_t red_min[kWaves];
-  int scan[kWaves];
+  uint32_t red_max[kW];
+  uint32_t red_min[kW];
+  int scan[kW];
   unsigned long long tmask;
   int bnd;
   uint32_t bnd_above;
   uint32_t bnd_count;
   int flag;
 };
+using SelShared = SelSharedT<kBlock>;
 
 __device__ __forceinline__ float key_value(uint32_t key) { return __uint_as_float(from_order_key32(key)); }
 
-// Exclusive prefix of v over the block's threads (thread order); *total gets
-// the block sum.  Two barriers, so consecutive calls never race on scan[].
+// Exclusive prefix of v over the block's NT threads (thread order); *total
+// gets the block sum.  scan: NT / 64 ints.  Two barriers, so consecutive
+// calls never race on scan[].
+template <int NT>
 __device__ __forceinline__ int block_excl_scan(int v, int* scan, int* total) {
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) / kWave;
@@ -49,7 +59,7 @@ __device__ __forceinline__ int block_excl_scan(int v, int* scan, int* total) {
   __syncthreads();
   int before = 0, sum = 0;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < NT / kWave; ++w) {
     const int t = scan[w];
     before += w < wave ? t : 0;
     sum += t;
@@ -78,8 +88,10 @@ struct BinFn {
 // KPT*t .. KPT*t + KPT - 1).  On return, bit j of *take marks index
 // KPT*t + j as selected, and *first is the rank (in ascending index order)
 // of this thread's first selected index among all selected ones.
-template <int KPT>
-__device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& sh, uint32_t* take, int* first) {
+template <int KPT, int NT>
+__device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelSharedT<NT>& sh, uint32_t* take,
+                           int* first) {
+  constexpr int kW = NT / kWave;
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid / kWave;
@@ -96,7 +108,7 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
     if (ccount == need) break;
     // after a pass, few candidates go straight to the exact rank (it orders
     // equal keys by index too), with no bounds reduction
-    if (level > 0 && ccount <= static_cast<uint32_t>(kBlock)) {
+    if (level > 0 && ccount <= static_cast<uint32_t>(kExactMax)) {
       mode = 1;
       break;
     }
@@ -115,10 +127,10 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
     }
     // the histogram is cleared in the same barrier interval: the previous
     // pass's reads of it ended at its last barrier
-    for (int b = tid; b < (kLinBins + 64) / 4; b += kBlock) hist4[b] = make_uint4(0u, 0u, 0u, 0u);
+    for (int b = tid; b < (kLinBins + 64) / 4; b += NT) hist4[b] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kW; ++w) {
       cmax = sh.red_max[w] > cmax ? sh.red_max[w] : cmax;
       cmin = sh.red_min[w] < cmin ? sh.red_min[w] : cmin;
     }
@@ -126,7 +138,7 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
       mode = 2;
       break;
     }
-    if (ccount <= static_cast<uint32_t>(kBlock)) {
+    if (ccount <= static_cast<uint32_t>(kExactMax)) {
       mode = 1;
       break;
     }
@@ -149,15 +161,21 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
       if ((cand >> j) & 1u) atomicAdd(&sh.hist[bin[j]], 1u);
     }
     __syncthreads();
-    // thread t owns bins 8t .. 8t + 7 (linear) or bin t (digit)
-    constexpr int kBpt = kLinBins / kBlock;
-    static_assert(kBpt == 8, "two 16-byte histogram reads per thread");
+    // thread t owns bins kBpt t .. kBpt t + kBpt - 1 (linear) or bin t (digit)
+    constexpr int kBpt = kLinBins / NT;
+    static_assert(kBpt == 2 || kBpt == 4 || kBpt == 8, "16-byte or 8-byte histogram reads");
     uint32_t hv[kBpt];
     if (fn.linear) {
-      const uint4 h0 = hist4[2 * tid];
-      const uint4 h1 = hist4[2 * tid + 1];
-      hv[0] = h0.x; hv[1] = h0.y; hv[2] = h0.z; hv[3] = h0.w;
-      hv[4] = h1.x; hv[5] = h1.y; hv[6] = h1.z; hv[7] = h1.w;
+      if constexpr (kBpt == 2) {
+        const uint2 h0 = reinterpret_cast<const uint2*>(sh.hist)[tid];
+        hv[0] = h0.x; hv[1] = h0.y;
+      } else {
+#pragma unroll
+        for (int q = 0; q < kBpt / 4; ++q) {
+          const uint4 h = hist4[kBpt / 4 * tid + q];
+          hv[4 * q] = h.x; hv[4 * q + 1] = h.y; hv[4 * q + 2] = h.z; hv[4 * q + 3] = h.w;
+        }
+      }
     } else {
       hv[0] = sh.hist[tid];
 #pragma unroll
@@ -172,7 +190,7 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
     __syncthreads();
     uint32_t incl = wincl;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) incl += w > wave ? static_cast<uint32_t>(sh.scan[w]) : 0u;
+    for (int w = 0; w < kW; ++w) incl += w > wave ? static_cast<uint32_t>(sh.scan[w]) : 0u;
     if (incl - tot < need && need <= incl) {
       uint32_t acc = incl - tot;
       int bsel = 0;
@@ -203,10 +221,10 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
   }
   int total;
   if (mode == 1 && ccount > static_cast<uint32_t>(kWave)) {
-    // exact rank of at most kBlock candidates; slot t's rank goes to
+    // exact rank of at most kExactMax candidates; slot t's rank goes to
     // selbits[t] and back to the thread that owns slot t
-    static_assert(kMaxSelPages / 32 >= kBlock, "one rank per candidate slot");
-    const int first = block_excl_scan(__popc(cand), sh.scan, &total);
+    static_assert(kMaxSelPages / 32 >= kExactMax, "one rank per candidate slot");
+    const int first = block_excl_scan<NT>(__popc(cand), sh.scan, &total);
     int slot = first;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
@@ -247,7 +265,7 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelShared& 
   // One scan gives both the taken keys (low half) and the candidates (high
   // half) in earlier threads; candidate c (in index order) is taken when
   // its rank is below need (mode 1: tmask bit c) or c < need (mode 2).
-  const int pre = block_excl_scan(__popc(taken) | (__popc(cand) << 16), sh.scan, &total);
+  const int pre = block_excl_scan<NT>(__popc(taken) | (__popc(cand) << 16), sh.scan, &total);
   const int a_before = pre & 0xffff;
   const int c_before = pre >> 16;
   uint64_t tmask = 0ull;

@@ -592,12 +592,15 @@ __device__ __forceinline__ int group_candidates(const SelectArgs& s, int g) {
   return k * s.bs;
 }
 
+// Block-shared state of a top-p block of NT threads.
+template <int NT>
 struct TopShared {
-  SelShared sel;
+  static constexpr int kW = NT / kWave;
+  SelSharedT<NT> sel;
   __align__(16) unsigned long long bin_mass[kLinBins + 64];
-  unsigned long long red64[kWaves];
-  unsigned long long cmass[kBlock];
-  float fred[kWaves];
+  unsigned long long red64[kW];
+  unsigned long long cmass[kExactMax];
+  float fred[kW];
   int ires[4];
   unsigned long long lres[2];
 };
@@ -617,6 +620,7 @@ __device__ __forceinline__ uint64_t wave_suffix_u64(uint64_t v) {
   }
   return v;
 }
+template <int NT>
 __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, unsigned long long* red) {
   const uint64_t s = wave_suffix_u64(v);  // lane 0 holds the wave sum
   const int wave = static_cast<int>(threadIdx.x) / kWave;
@@ -624,7 +628,7 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, unsigned long long
   __syncthreads();
   uint64_t t = 0;
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) t += red[w];
+  for (int w = 0; w < NT / kWave; ++w) t += red[w];
   __syncthreads();
   return t;
 }
@@ -642,9 +646,10 @@ __device__ __forceinline__ uint64_t top_p_threshold(uint32_t p24, uint64_t z) {
 // >= need; marks them in *taken (bit j = key j of this thread).  Keys are
 // KPT contiguous per thread (indices KPT*t + j).  kmin0/kmax0: the smallest
 // and largest key of the row; the caller has cleared the histograms.
-template <int KPT>
+template <int KPT, int NT>
 __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)[KPT], int N, uint64_t need,
-                              uint32_t kmin0, uint32_t kmax0, TopShared& sh, uint32_t* taken_out) {
+                              uint32_t kmin0, uint32_t kmax0, TopShared<NT>& sh, uint32_t* taken_out) {
+  constexpr int kW = NT / kWave;
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int wave = tid / kWave;
@@ -661,7 +666,7 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
       // of it with register reads; the boundary is the lane whose own mass
       // crosses need
       int total;
-      const int first = block_excl_scan(__popc(cand), sh.sel.scan, &total);
+      const int first = block_excl_scan<NT>(__popc(cand), sh.sel.scan, &total);
       int slot = first;
 #pragma unroll
       for (int j = 0; j < KPT; ++j) {
@@ -710,11 +715,11 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
       count += needed;
       break;
     }
-    if (ccount <= kBlock) {
+    if (ccount <= kExactMax) {
       // exact: rank the candidates (key desc, index asc) and walk their
       // masses in rank order; slot t's rank goes to sel.selbits[t]
       int total;
-      const int first = block_excl_scan(__popc(cand), sh.sel.scan, &total);
+      const int first = block_excl_scan<NT>(__popc(cand), sh.sel.scan, &total);
       int slot = first;
 #pragma unroll
       for (int j = 0; j < KPT; ++j) {
@@ -773,7 +778,7 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
       }
       __syncthreads();
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < kW; ++w) {
         cmax = sh.sel.red_max[w] > cmax ? sh.sel.red_max[w] : cmax;
         cmin = sh.sel.red_min[w] < cmin ? sh.sel.red_min[w] : cmin;
       }
@@ -789,10 +794,10 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
       __syncthreads();
       uint64_t mm = 0;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) mm = sh.red64[w] > mm ? sh.red64[w] : mm;
+      for (int w = 0; w < kW; ++w) mm = sh.red64[w] > mm ? sh.red64[w] : mm;
       const int needed = mm == 0 ? ccount : static_cast<int>((need + mm - 1) / mm);
       int total;
-      int before = block_excl_scan(__popc(cand), sh.sel.scan, &total);
+      int before = block_excl_scan<NT>(__popc(cand), sh.sel.scan, &total);
 #pragma unroll
       for (int j = 0; j < KPT; ++j) {
         if ((cand >> j) & 1u) {
@@ -814,7 +819,7 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
     const int hi = 31 - __clz(static_cast<int>(cmax ^ cmin));
     fn.shift = hi >= 7 ? hi - 7 : 0;
     if (level > 0) {
-      for (int b = tid; b < kLinBins + 64; b += kBlock) {
+      for (int b = tid; b < kLinBins + 64; b += NT) {
         sh.sel.hist[b] = 0u;
         sh.bin_mass[b] = 0ull;
       }
@@ -830,17 +835,23 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
       }
     }
     __syncthreads();
-    // thread t owns bins 8t .. 8t + 7 (linear) or bin t (digit), read once
-    // into registers
-    constexpr int kBpt = kLinBins / kBlock;
-    static_assert(kBpt == 8, "eight bins per thread");
+    // thread t owns bins kBpt t .. kBpt t + kBpt - 1 (linear) or bin t
+    // (digit), read once into registers
+    constexpr int kBpt = kLinBins / NT;
+    static_assert(kBpt == 2 || kBpt == 4 || kBpt == 8, "whole 8-byte or 16-byte bin reads per thread");
     uint32_t hc[kBpt];
     uint64_t hm[kBpt];
     if (fn.linear) {
-      const uint4 c0 = reinterpret_cast<const uint4*>(sh.sel.hist)[2 * tid];
-      const uint4 c1 = reinterpret_cast<const uint4*>(sh.sel.hist)[2 * tid + 1];
-      hc[0] = c0.x; hc[1] = c0.y; hc[2] = c0.z; hc[3] = c0.w;
-      hc[4] = c1.x; hc[5] = c1.y; hc[6] = c1.z; hc[7] = c1.w;
+      if constexpr (kBpt == 2) {
+        const uint2 c0 = reinterpret_cast<const uint2*>(sh.sel.hist)[tid];
+        hc[0] = c0.x; hc[1] = c0.y;
+      } else {
+#pragma unroll
+        for (int q = 0; q < kBpt / 4; ++q) {
+          const uint4 c = reinterpret_cast<const uint4*>(sh.sel.hist)[kBpt / 4 * tid + q];
+          hc[4 * q] = c.x; hc[4 * q + 1] = c.y; hc[4 * q + 2] = c.z; hc[4 * q + 3] = c.w;
+        }
+      }
 #pragma unroll
       for (int q = 0; q < kBpt / 2; ++q) {
         const ulonglong2 m2 = reinterpret_cast<const ulonglong2*>(sh.bin_mass)[kBpt / 2 * tid + q];
@@ -874,7 +885,7 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
     uint64_t incl = wm;
     uint32_t incl_c = wc;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kW; ++w) {
       incl += w > wave ? sh.red64[w] : 0ull;
       incl_c += w > wave ? static_cast<uint32_t>(sh.sel.scan[w]) : 0u;
     }
@@ -973,8 +984,9 @@ __device__ __forceinline__ uint32_t range_bits(int lo, int a, int b) {
 // Dynamic LDS of the selection kernels: the union bitmap (one bit per
 // position, padded to 16 bytes), then a staging area shared by the logits
 // load (N floats) and the union compaction (2 * kBlock words = 16384
-// positions of rows per window, then 64 dummy slots).
-constexpr int kUnionWindowWords = 2 * kBlock;
+// positions of rows per window, then 64 dummy slots).  Whatever the block
+// size, a window is 512 words and its first 256 threads hold two each.
+constexpr int kUnionWindowWords = 512;
 __host__ __device__ __forceinline__ int union_words(int length) { return (length + 31) / 32; }
 __host__ __device__ __forceinline__ int stage_offset_words(int length) { return (union_words(length) + 4 + 3) & ~3; }
 __host__ __device__ __forceinline__ int stage_elems(int N, int length) {
@@ -993,7 +1005,7 @@ __host__ __device__ __forceinline__ int stage_elems(int N, int length) {
 // the set bits below j (mbcnt); clear lanes write a dummy slot past the
 // window, so the 64 steps have no branch.  The window's rows leave with
 // full, contiguous stores.  Returns the new total.
-template <typename PosFn>
+template <int NT, typename PosFn>
 __device__ int expand_bits(const uint32_t* cb, int cw, int32_t* stage, int32_t* rows, int total, int* scan,
                            PosFn pos) {
   const int tid = threadIdx.x;
@@ -1004,10 +1016,11 @@ __device__ int expand_bits(const uint32_t* cb, int cw, int32_t* stage, int32_t* 
   const int dummy = kUnionWindowWords * 32 + lane;
   for (int w0 = 0; w0 < cw; w0 += kUnionWindowWords) {
     const int w = w0 + 2 * tid;
-    const uint32_t v0 = w < cw ? cb[w] : 0u;
-    const uint32_t v1 = w + 1 < cw ? cb[w + 1] : 0u;
+    const bool holds = 2 * tid < kUnionWindowWords;
+    const uint32_t v0 = holds && w < cw ? cb[w] : 0u;
+    const uint32_t v1 = holds && w + 1 < cw ? cb[w + 1] : 0u;
     int n_win;
-    const int first = block_excl_scan(__popc(v0) + __popc(v1), scan, &n_win);
+    const int first = block_excl_scan<NT>(__popc(v0) + __popc(v1), scan, &n_win);
     const int c_wave = 32 * (w0 + 2 * kWave * wave) + lane;
 #pragma unroll
     for (int k = 0; k < kWave; ++k) {
@@ -1019,13 +1032,13 @@ __device__ int expand_bits(const uint32_t* cb, int cw, int32_t* stage, int32_t* 
       stage[mine ? base + static_cast<int>(rank) : dummy] = pos(c_wave + 64 * k);
     }
     __syncthreads();
-    for (int i = tid; i < n_win; i += 4 * kBlock) {
+    for (int i = tid; i < n_win; i += 4 * NT) {
       int32_t r[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) r[u] = i + u * kBlock < n_win ? stage[i + u * kBlock] : 0;
+      for (int u = 0; u < 4; ++u) r[u] = i + u * NT < n_win ? stage[i + u * NT] : 0;
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        if (i + u * kBlock < n_win) rows[total + i + u * kBlock] = r[u];
+        if (i + u * NT < n_win) rows[total + i + u * NT] = r[u];
     }
     total += n_win;
     __syncthreads();  // the next window reuses the stage
@@ -1037,6 +1050,7 @@ __device__ int expand_bits(const uint32_t* cb, int cw, int32_t* stage, int32_t* 
 // and recent windows, compacted ascending into the group's row list.
 // scratch_a (kLinBins + 64 words) and scratch_b (2 * (kLinBins + 64) words)
 // are free block-shared memory.
+template <int NT>
 __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, int32_t* stage, int* scan,
                                   uint32_t* scratch_a, int32_t* scratch_b) {
   const int tid = threadIdx.x;
@@ -1060,7 +1074,7 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
   auto fetch = [&](int base) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int idx = base + j * kBlock + tid;
+      const int idx = base + j * NT + tid;
       act[j] = idx < total_pages;
       const int ii = act[j] ? idx : 0;
       const int r = ii / s.b0;
@@ -1091,7 +1105,7 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
   const int pbw = (n_pages + 31) / 32;
   const bool pow2 = bs > 0 && (bs & (bs - 1)) == 0 && bs <= 32;
   constexpr int kScratchB = 2 * (kLinBins + 64);
-  if (pow2 && total_pages <= 4 * kBlock && 2 * pbw <= kLinBins + 64 && 3 * total_pages <= kScratchB &&
+  if (pow2 && total_pages <= 4 * NT && 2 * pbw <= kLinBins + 64 && 3 * total_pages <= kScratchB &&
       total_pages * bs <= kUnionWindowWords * 32) {
     uint32_t m[4];
     bool bad = false;
@@ -1107,18 +1121,18 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
     int32_t* upage = scratch_b;
     uint32_t* umask = reinterpret_cast<uint32_t*>(scratch_b + u_cap);
     int32_t* ubase = scratch_b + 2 * u_cap;
-    for (int w = tid; w < pbw; w += kBlock) pb[w] = 0u;
-    for (int u = tid; u < u_cap; u += kBlock) umask[u] = 0u;
+    for (int w = tid; w < pbw; w += NT) pb[w] = 0u;
+    for (int u = tid; u < u_cap; u += NT) umask[u] = 0u;
     if (__syncthreads_or(bad ? 1 : 0) == 0) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (m[j] != 0u) atomicOr(&pb[page[j] >> 5], 1u << (page[j] & 31));
       __syncthreads();
       int U = 0;
-      for (int w0 = 0; w0 < pbw; w0 += kBlock) {
+      for (int w0 = 0; w0 < pbw; w0 += NT) {
         const int w = w0 + tid;
         int tot;
-        const int ex = block_excl_scan(w < pbw ? __popc(pb[w]) : 0, scan, &tot);
+        const int ex = block_excl_scan<NT>(w < pbw ? __popc(pb[w]) : 0, scan, &tot);
         if (w < pbw) pfx[w] = U + ex;
         U += tot;
       }
@@ -1133,7 +1147,7 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
         }
       }
       // sink rows meanwhile
-      for (int i = tid; i < sink_end; i += kBlock) rows[i] = i;
+      for (int i = tid; i < sink_end; i += NT) rows[i] = i;
       __syncthreads();
       // first row of every union page: thread t sums union pages 4t .. 4t + 3
       int union_rows;
@@ -1145,7 +1159,7 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
           c[q] = u < U ? __popc(umask[u]) : 0;
           sum += c[q];
         }
-        int acc = block_excl_scan(sum, scan, &union_rows);
+        int acc = block_excl_scan<NT>(sum, scan, &union_rows);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int u = 4 * tid + q;
@@ -1170,7 +1184,7 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
       const int dummy = kUnionWindowWords * 32 + lane_id();
       auto put_pages = [&](auto bs_c) {
         constexpr int kBs = decltype(bs_c)::value;
-        for (int u = tid; u < U; u += kBlock) {
+        for (int u = tid; u < U; u += NT) {
           const uint32_t mu = umask[u];  // non-zero: u is a union page
           const int hb = 31 - __clz(static_cast<int>(mu));
           const int b0 = ubase[u];
@@ -1193,13 +1207,13 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
       const int n4 = union_rows > lead ? (union_rows - lead) >> 2 : 0;
       const int4* src4 = reinterpret_cast<const int4*>(st + lead);
       int4* dst4 = reinterpret_cast<int4*>(urows + lead);
-      for (int i = tid; i < n4; i += 4 * kBlock) {
+      for (int i = tid; i < n4; i += 4 * NT) {
         int4 r[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) r[q] = src4[i + q * kBlock < n4 ? i + q * kBlock : i];
+        for (int q = 0; q < 4; ++q) r[q] = src4[i + q * NT < n4 ? i + q * NT : i];
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          if (i + q * kBlock < n4) dst4[i + q * kBlock] = r[q];
+          if (i + q * NT < n4) dst4[i + q * NT] = r[q];
       }
       if (tid < lead && tid < union_rows) urows[tid] = st[tid];
       {
@@ -1208,7 +1222,7 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
       }
       int total = sink_end + union_rows;
       const int n_recent = length - recent_start;
-      for (int i = tid; i < n_recent; i += kBlock) rows[total + i] = recent_start + i;
+      for (int i = tid; i < n_recent; i += NT) rows[total + i] = recent_start + i;
       total += n_recent;
       const int count = total + (s.append_position >= 0 ? 1 : 0);
       if (tid == 0) {
@@ -1220,12 +1234,12 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
   }
 
   // ---- bitmap path: one bit per position of [0, length)
-  for (int w = tid; w < words; w += kBlock) {
+  for (int w = tid; w < words; w += NT) {
     const int lo_pos = 32 * w;
     bits[w] = range_bits(lo_pos, 0, sink_end) | range_bits(lo_pos, recent_start, length);
   }
   __syncthreads();
-  for (int base = 0; base < total_pages; base += 4 * kBlock) {
+  for (int base = 0; base < total_pages; base += 4 * NT) {
     if (base > 0) fetch(base);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1239,7 +1253,7 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
         if (static_cast<uint32_t>(field >> 32) != 0u) atomicOr(&bits[(pos0 >> 5) + 1], static_cast<uint32_t>(field >> 32));
       } else {
         // pages wider than a word: bit by bit
-        const int r = (base + j * kBlock + tid) / s.b0;
+        const int r = (base + j * NT + tid) / s.b0;
         const uint32_t* sb = s.selbits + (static_cast<int64_t>(g) * s.R + r) * n_words;
         for (int i = 0; i < bs; ++i) {
           const int n = n0[j] + i;
@@ -1251,7 +1265,7 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
     }
   }
   __syncthreads();
-  const int total = expand_bits(bits, words, stage, rows, 0, scan, [](int c) { return c; });
+  const int total = expand_bits<NT>(bits, words, stage, rows, 0, scan, [](int c) { return c; });
   const int count = total + (s.append_position >= 0 ? 1 : 0);
   if (tid == 0) {
     if (s.append_position >= 0) rows[total] = s.append_position;
@@ -1263,9 +1277,9 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
 // thread's own logits; rows that are not 16-byte aligned go through the LDS
 // stage); the largest logit and the smallest and largest key of the row in
 // one block reduction.
-template <int KPT>
+template <int KPT, int NT>
 __device__ __forceinline__ void load_logits(const float* row, int N, float* stage, uint32_t (&key)[KPT],
-                                            float& lmax, uint32_t& kmin, uint32_t& kmax, TopShared& sh) {
+                                            float& lmax, uint32_t& kmin, uint32_t& kmax, TopShared<NT>& sh) {
   const int tid = static_cast<int>(threadIdx.x);
   const int i0 = KPT * tid;
   float mx = -INFINITY;
@@ -1273,17 +1287,28 @@ __device__ __forceinline__ void load_logits(const float* row, int N, float* stag
   if (N > 0 && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
     // the thread's KPT contiguous logits straight from memory, 16 bytes a load
     // (indices past the row read its last float4 and are masked below)
-    const float4* r4 = reinterpret_cast<const float4*>(row);
-    const int last4 = (N >> 2) - 1;
     float v[KPT];
+    if constexpr (KPT >= 4) {
+      const float4* r4 = reinterpret_cast<const float4*>(row);
+      const int last4 = (N >> 2) - 1;
 #pragma unroll
-    for (int j = 0; j < KPT / 4; ++j) {
-      const int i4 = (i0 >> 2) + j;
-      const float4 t = r4[i4 < last4 ? i4 : last4];
-      v[4 * j] = t.x;
-      v[4 * j + 1] = t.y;
-      v[4 * j + 2] = t.z;
-      v[4 * j + 3] = t.w;
+      for (int j = 0; j < KPT / 4; ++j) {
+        const int i4 = (i0 >> 2) + j;
+        const float4 t = r4[i4 < last4 ? i4 : last4];
+        v[4 * j] = t.x;
+        v[4 * j + 1] = t.y;
+        v[4 * j + 2] = t.z;
+        v[4 * j + 3] = t.w;
+      }
+    } else if constexpr (KPT == 2) {
+      const float2* r2 = reinterpret_cast<const float2*>(row);
+      const int last2 = (N >> 1) - 1;
+      const int i2 = i0 >> 1;
+      const float2 t = r2[i2 < last2 ? i2 : last2];
+      v[0] = t.x;
+      v[1] = t.y;
+    } else {
+      v[0] = row[i0 < N - 1 ? i0 : N - 1];
     }
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
@@ -1294,7 +1319,7 @@ __device__ __forceinline__ void load_logits(const float* row, int N, float* stag
       kmn = (i < N && key[j] < kmn) ? key[j] : kmn;
     }
   } else {
-    for (int i = tid; i < N; i += kBlock) stage[i] = row[i];
+    for (int i = tid; i < N; i += NT) stage[i] = row[i];
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
@@ -1320,7 +1345,7 @@ __device__ __forceinline__ void load_logits(const float* row, int N, float* stag
   kmax = sh.sel.red_max[0];
   kmin = sh.sel.red_min[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) {
+  for (int w = 1; w < NT / kWave; ++w) {
     lmax = fmaxf(lmax, sh.fred[w]);
     kmax = sh.sel.red_max[w] > kmax ? sh.sel.red_max[w] : kmax;
     kmin = sh.sel.red_min[w] < kmin ? sh.sel.red_min[w] : kmin;
@@ -1332,8 +1357,8 @@ __device__ __forceinline__ void load_logits(const float* row, int N, float* stag
 // 32 / KPT consecutive threads of a word OR their shifted bits together
 // (lane shuffles within the wavefront) and the first of them stores the
 // word; words past the block's keys are zero.
-template <int KPT>
-__device__ __forceinline__ void publish_selection(uint32_t* row_bits, int words, uint32_t taken, TopShared& sh) {
+template <int KPT, int NT>
+__device__ __forceinline__ void publish_selection(uint32_t* row_bits, int words, uint32_t taken, TopShared<NT>& sh) {
   (void)sh;
   const int tid = static_cast<int>(threadIdx.x);
   static_assert(KPT <= 32 && (32 % KPT) == 0, "whole threads per word");
@@ -1343,22 +1368,22 @@ __device__ __forceinline__ void publish_selection(uint32_t* row_bits, int words,
   for (int o = 1; o < kLpw; o <<= 1) w |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), o));
   if (tid % kLpw == 0 && tid / kLpw < words)
     __hip_atomic_store(row_bits + tid / kLpw, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int i = kBlock / kLpw + tid; i < words; i += kBlock)
+  for (int i = NT / kLpw + tid; i < words; i += NT)
     __hip_atomic_store(row_bits + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Stage A: the top-p count of every (group, head) row; in dynamic mode also
 // the selection and the group's token union.
-template <int KPT>
-__global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
-  __shared__ __align__(16) TopShared sh;
+template <int KPT, int NT>
+__global__ __launch_bounds__(NT) void twilight_topp_kernel(SelectArgs s) {
+  __shared__ __align__(16) TopShared<NT> sh;
   extern __shared__ __align__(16) uint32_t union_bits[];
   float* stage = reinterpret_cast<float*>(union_bits + stage_offset_words(s.length));
   const int row = blockIdx.x;
   const int g = row / s.R;
   const int N = group_candidates(s, g);  // valid candidates; logits rows are s.N apart
   // the first pass's histograms, cleared before load_logits' barrier
-  for (int b = threadIdx.x; b < kLinBins + 64; b += kBlock) {
+  for (int b = threadIdx.x; b < kLinBins + 64; b += NT) {
     sh.sel.hist[b] = 0u;
     sh.bin_mass[b] = 0ull;
   }
@@ -1370,7 +1395,7 @@ __global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
     }
     publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, 0u, sh);
     if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
-    build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
+    build_token_union<NT>(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
                       reinterpret_cast<int32_t*>(sh.bin_mass));
     return;
   }
@@ -1386,7 +1411,7 @@ __global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
     mass[j] = (i0 + j < N) ? mass_of(key_value(key[j]), lmax) : 0ull;
     local += mass[j];
   }
-  const uint64_t z = block_sum_u64(local, sh.red64);
+  const uint64_t z = block_sum_u64<NT>(local, sh.red64);
   uint64_t need = top_p_threshold(s.p24, z);
   if (need == 0) {
     // no mass at all (non-finite logits): one key, the largest, as on the CPU
@@ -1402,15 +1427,15 @@ __global__ __launch_bounds__(kBlock) void twilight_topp_kernel(SelectArgs s) {
   if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = desired;
   publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
-  build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
+  build_token_union<NT>(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
                       reinterpret_cast<int32_t*>(sh.bin_mass));
 }
 
 // Stage B (matched budgets): allocation from the group's desired counts, the
 // top-allocated selection of each head and the group's token union.
-template <int KPT>
-__global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) {
-  __shared__ __align__(16) TopShared sh;
+template <int KPT, int NT>
+__global__ __launch_bounds__(NT) void twilight_matched_kernel(SelectArgs s) {
+  __shared__ __align__(16) TopShared<NT> sh;
   extern __shared__ __align__(16) uint32_t union_bits[];
   const int row = blockIdx.x;
   const int g = row / s.R;
@@ -1439,7 +1464,7 @@ __global__ __launch_bounds__(kBlock) void twilight_matched_kernel(SelectArgs s) 
   block_topk<KPT>(key, N, k, sh.sel, &taken, &first_slot);
   publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
-  build_token_union(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
+  build_token_union<NT>(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
                       reinterpret_cast<int32_t*>(sh.bin_mass));
 }
 
@@ -1494,32 +1519,55 @@ int launch_qk_positions(const QkArgs& a, const int64_t* positions, int N, float*
   return tw_host::check_launch();
 }
 
+// Threads of a top-p block (one (group, head) row per block).  512 measured
+// best at 4096 candidates: two wavefronts per SIMD hide part of each other's
+// instruction latency, while 1024 threads paid more in 16-wave barriers.
+#ifndef TW_TOPP_THREADS
+#define TW_TOPP_THREADS 512
+#endif
+constexpr int kToppThreads = TW_TOPP_THREADS;
+
 template <int KPT>
 int launch_select_kpt(const SelectArgs& s, hipStream_t stream) {
+  constexpr int NT = kToppThreads;
   const size_t lds = (static_cast<size_t>(stage_offset_words(s.length)) + stage_elems(s.N, s.length)) * 4;
-  if (lds + sizeof(TopShared) > 160 * 1024) return TW_EUNSUPPORTED;
-  if (lds + sizeof(TopShared) > 64 * 1024) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(twilight_topp_kernel<KPT>),
+  if (lds + sizeof(TopShared<NT>) > 160 * 1024) return TW_EUNSUPPORTED;
+  if (lds + sizeof(TopShared<NT>) > 64 * 1024) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(twilight_topp_kernel<KPT, NT>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess ||
-        hipFuncSetAttribute(reinterpret_cast<const void*>(twilight_matched_kernel<KPT>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(twilight_matched_kernel<KPT, NT>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
       return tw_host::check_launch();
   }
   const dim3 grid(s.G * s.R);
   if (!s.given) {
-    hipLaunchKernelGGL(twilight_topp_kernel<KPT>, grid, dim3(kBlock), lds, stream, s);
+    hipLaunchKernelGGL((twilight_topp_kernel<KPT, NT>), grid, dim3(NT), lds, stream, s);
     const int rc = tw_host::check_launch();
     if (rc != TW_OK || !s.matched) return rc;
   }
-  hipLaunchKernelGGL(twilight_matched_kernel<KPT>, grid, dim3(kBlock), lds, stream, s);
+  hipLaunchKernelGGL((twilight_matched_kernel<KPT, NT>), grid, dim3(NT), lds, stream, s);
   return tw_host::check_launch();
 }
 
 int launch_select(const SelectArgs& s, hipStream_t stream) {
-  if (s.N <= 4 * kBlock) return launch_select_kpt<4>(s, stream);
-  if (s.N <= 8 * kBlock) return launch_select_kpt<8>(s, stream);
-  if (s.N <= 16 * kBlock) return launch_select_kpt<16>(s, stream);
-  return launch_select_kpt<32>(s, stream);
+  constexpr int NT = kToppThreads;
+  if constexpr (NT >= 1024) {
+    if (s.N <= NT) return launch_select_kpt<1>(s, stream);
+  }
+  if constexpr (NT >= 512) {
+    if (s.N <= 2 * NT) return launch_select_kpt<2>(s, stream);
+  }
+  if (s.N <= 4 * NT) return launch_select_kpt<4>(s, stream);
+  if constexpr (8 * NT >= kMaxSelPages) {
+    return launch_select_kpt<8>(s, stream);
+  } else if constexpr (16 * NT >= kMaxSelPages) {
+    if (s.N <= 8 * NT) return launch_select_kpt<8>(s, stream);
+    return launch_select_kpt<16>(s, stream);
+  } else {
+    if (s.N <= 8 * NT) return launch_select_kpt<8>(s, stream);
+    if (s.N <= 16 * NT) return launch_select_kpt<16>(s, stream);
+    return launch_select_kpt<32>(s, stream);
+  }
 }
 
 size_t counter_bytes(int G) { return ((static_cast<size_t>(G) * 4 + 255) / 256) * 256; }
