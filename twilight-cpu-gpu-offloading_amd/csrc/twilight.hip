@@ -120,6 +120,19 @@ struct QkLane {
   }
 };
 
+// The logit of a candidate from its exact integer dot S (see above): one
+// rounding of S to fp32, the power-of-two scale, then three fp32 operations.
+__device__ __forceinline__ float qk_logit(int64_t S, int shift, float qsum, bool ok, float s, float m,
+                                          float qk_scale) {
+  if (!ok) return u32_as_f32(0x7fc00000u);
+  // |S| < 2^34: exact in double, so one double -> float conversion is the
+  // single round-to-nearest-even of S
+  const float dotc = ldexpf(static_cast<float>(static_cast<double>(S)), shift);
+  const float a = s * dotc;
+  const float c = m * qsum;
+  return qk_scale * (a + c);
+}
+
 // One query head in fixed point, as the byte slices of the lane's CPL
 // channels laid out like its code words: [word][0] even channels, [1] odd.
 template <int CPL, int LPR>
@@ -224,13 +237,7 @@ struct QFix {
   }
 
   __device__ __forceinline__ float logit(int64_t S, float s, float m, float qk_scale) const {
-    if (!ok) return u32_as_f32(0x7fc00000u);
-    // |S| < 2^34: exact in double, so one double -> float conversion is the
-    // single round-to-nearest-even of S
-    const float dotc = ldexpf(static_cast<float>(static_cast<double>(S)), shift);
-    const float a = s * dotc;
-    const float c = m * qsum;
-    return qk_scale * (a + c);
+    return qk_logit(S, shift, qsum, ok, s, m, qk_scale);
   }
 };
 
@@ -261,7 +268,11 @@ struct QStage {
   }
 };
 
-template <int DIM, int RMAX>
+// BALANCED: the slices are signed digits h, m, l in [-128, 127] with
+// Q = h * 2^16 + m * 2^8 + l (for the matrix cores' signed int8 operands);
+// otherwise h = Q >> 16 signed and m, l the unsigned bytes below it.  Both
+// represent the same Q, so the integer dot is the same.
+template <int DIM, int RMAX, bool BALANCED = false>
 __device__ __forceinline__ void stage_qfix(const QStage<DIM, RMAX>& qv, int R, uint32_t* st, int* st_shift,
                                            float* st_qsum, int* st_ok) {
   using QS = QStage<DIM, RMAX>;
@@ -299,11 +310,21 @@ __device__ __forceinline__ void stage_qfix(const QStage<DIM, RMAX>& qv, int R, u
     for (int i = 0; i < VPT; ++i) {
       const int d = d0 + i;
       const int k = d / 8, par = d & 1, j = (d % 8) / 2;
-#pragma unroll
-      for (int sl = 0; sl < 3; ++sl) {
-        const int sh = 16 - 8 * sl;
-        sb[((r * 3 + sl) * 2 + par) * K * 4 + k * 4 + j] = static_cast<uint8_t>((Q[i] >> sh) & 255);
+      int dig[3];
+      if constexpr (BALANCED) {
+        const int l = ((Q[i] + 128) & 255) - 128;
+        const int q1 = (Q[i] - l) >> 8;
+        const int m = ((q1 + 128) & 255) - 128;
+        dig[0] = (q1 - m) >> 8;
+        dig[1] = m;
+        dig[2] = l;
+      } else {
+        dig[0] = Q[i] >> 16;
+        dig[1] = Q[i] >> 8;
+        dig[2] = Q[i];
       }
+#pragma unroll
+      for (int sl = 0; sl < 3; ++sl) sb[((r * 3 + sl) * 2 + par) * K * 4 + k * 4 + j] = static_cast<uint8_t>(dig[sl] & 255);
     }
     if (d0 == 0) {
       st_shift[r] = nz ? E - 22 : 0;
@@ -320,12 +341,23 @@ __device__ __forceinline__ void stage_qfix(const QStage<DIM, RMAX>& qv, int R, u
 // scales and minima.  A head's logit slot for union page u is the number of
 // earlier union pages it chose (its B0 pages are ascending).  The block's
 // logits go through LDS and leave as one coalesced store per (row, head).
-template <typename DT, int DIM, int RMAX, int CPLMAX>
+//
+// MF (D = 128): the dots run on the matrix cores, v_mfma_i32_16x16x64_i8
+// per 16 rows and 64 channels.  A row m = 4 h + t holds slice t of head h
+// (balanced signed digits; row 4 h + 3 is zero) and B column n the codes of
+// candidate row n, so lane group G of the product holds head G's three slice
+// dots of row lane % 16 in its own registers and forms S there.  Both
+// operands give a lane the same 16 channels of a 64-channel step, in the
+// same byte order (even channels of a code word, then odd), so the sum over
+// k pairs every q digit with its code whatever order the hardware uses
+// inside a lane group.  Slices of 128 channels stay far inside int32.
+template <typename DT, int DIM, int RMAX, int CPLMAX, bool MF = false>
 __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
   using S = typename DT::storage;
   using L = QkLane<DIM, CPLMAX>;
   using QF = QFix<L::CPL, L::LPR>;
-  constexpr int RPB = kWaves * L::RPW;
+  static_assert(!MF || DIM == 128, "the matrix-core path takes 128 channels");
+  constexpr int RPB = MF ? kWaves * 16 : kWaves * L::RPW;
   constexpr int PASSES = (kQkRows + RPB - 1) / RPB;
   constexpr int NC = RMAX / 2;  // packed head counters (two 16-bit fields each)
   constexpr int KW = DIM >= 8 ? DIM / 8 : 1;
@@ -404,17 +436,24 @@ __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
   S sv[PASSES], mv[PASSES];
 #pragma unroll
   for (int i = 0; i < PASSES; ++i) {
-    const int lr = i * RPB + wave * L::RPW + lane / L::LPR;  // row within the block
+    // row within the block: MF, tile i of the wavefront's 16-row tiles, row
+    // lane % 16, lane group lane / 16 reading code bytes [16 G, 16 G + 16)
+    const int lr = MF ? i * RPB + wave * 16 + (lane % 16) : i * RPB + wave * L::RPW + lane / L::LPR;
     const int row = row0 + (lr < nrows ? lr : 0);
     const int p = row / bs - u_first;
     int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[p]) * bs + (row - (row / bs) * bs);
     t = (t >= 0 && t < a.qrows) ? t : 0;
-    L::codes(pk + t * (DIM / 2), c0, w[i]);
+    if constexpr (MF) {
+      const uint4 v = *reinterpret_cast<const uint4*>(pk + t * (DIM / 2) + 16 * (lane / 16));
+      w[i][0] = v.x; w[i][1] = v.y; w[i][2] = v.z; w[i][3] = v.w;
+    } else {
+      L::codes(pk + t * (DIM / 2), c0, w[i]);
+    }
     sv[i] = sc[t];
     mv[i] = mn[t];
   }
   // ---- while they are in flight: q in fixed point, the logit slots ----
-  stage_qfix<DIM, RMAX>(qst, R, s_q, s_qshift, s_qsum, s_qok);
+  stage_qfix<DIM, RMAX, MF>(qst, R, s_q, s_qshift, s_qsum, s_qok);
 #pragma unroll
   for (int c = 0; c < NC; ++c) cnt[c] = static_cast<uint32_t>(wave_sum_i32(static_cast<int>(cnt[c])));
   if (lane == 0) {
@@ -449,19 +488,71 @@ __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
       }
     }
   }
-  QF qf[RMAX];
+  if constexpr (MF) {
+    // ---- A operands: head tile h, step sp: lane group G holds channels
+    // 32 G + 16 sp + [0, 16), i.e. code words k0 = 4 G + 2 sp and k0 + 1,
+    // as [even, odd] channel bytes of each word, like B below ----
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    constexpr int HT = RMAX / 4;
+    const int G = lane / 16;
+    const int mrow = lane % 16;
+    v4i av[HT][2];
 #pragma unroll
-  for (int r = 0; r < RMAX; ++r) qf[r].template load<DIM>(s_q, s_qshift, s_qsum, s_qok, r < R ? r : 0, c0);
-  // ---- dot products ----
+    for (int h = 0; h < HT; ++h) {
+      const int r = 4 * h + mrow / 4;
+      const int t = mrow % 4;
+      const bool live = t < 3 && r < R;
+      const uint32_t* st = s_q + (r < R ? r : 0) * 6 * KW + (t < 3 ? t : 0) * 2 * KW;
 #pragma unroll
-  for (int i = 0; i < PASSES; ++i) {
-    const int lr = i * RPB + wave * L::RPW + lane / L::LPR;
-    const float s = to_f32(DT{}, sv[i]), m = to_f32(DT{}, mv[i]);
+      for (int sp = 0; sp < 2; ++sp) {
+        const int k0 = 4 * G + 2 * sp;
+        av[h][sp][0] = live ? static_cast<int>(st[k0]) : 0;            // even channels of word k0
+        av[h][sp][1] = live ? static_cast<int>(st[KW + k0]) : 0;       // odd channels of word k0
+        av[h][sp][2] = live ? static_cast<int>(st[k0 + 1]) : 0;
+        av[h][sp][3] = live ? static_cast<int>(st[KW + k0 + 1]) : 0;
+      }
+    }
+    // ---- dot products: lane (G, n) of tile i gets head 4 h + G of row n ----
 #pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-      if (r >= R) break;
-      const float lg = qf[r].logit(qf[r].dot(w[i]), s, m, a.qk_scale);
-      if (lr < kQkRows && (lane % L::LPR) == 0) s_log[lr][r] = lg;
+    for (int i = 0; i < PASSES; ++i) {
+      const int lr = i * RPB + wave * 16 + mrow;
+      const float sf = to_f32(DT{}, sv[i]), mf = to_f32(DT{}, mv[i]);
+      v4i b0, b1;
+      b0[0] = static_cast<int>(w[i][0] & 0x0f0f0f0fu);
+      b0[1] = static_cast<int>((w[i][0] >> 4) & 0x0f0f0f0fu);
+      b0[2] = static_cast<int>(w[i][1] & 0x0f0f0f0fu);
+      b0[3] = static_cast<int>((w[i][1] >> 4) & 0x0f0f0f0fu);
+      b1[0] = static_cast<int>(w[i][2] & 0x0f0f0f0fu);
+      b1[1] = static_cast<int>((w[i][2] >> 4) & 0x0f0f0f0fu);
+      b1[2] = static_cast<int>(w[i][3] & 0x0f0f0f0fu);
+      b1[3] = static_cast<int>((w[i][3] >> 4) & 0x0f0f0f0fu);
+#pragma unroll
+      for (int h = 0; h < HT; ++h) {
+        v4i c = {0, 0, 0, 0};
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[h][0], b0, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[h][1], b1, c, 0, 0, 0);
+        const int r = 4 * h + G;
+        const int64_t S = (static_cast<int64_t>(c[0]) << 16) + (static_cast<int64_t>(c[1]) << 8) + c[2];
+        const int rr = r < R ? r : 0;
+        const float lg = qk_logit(S, s_qshift[rr], s_qsum[rr], s_qok[rr] != 0, sf, mf, a.qk_scale);
+        if (r < R && lr < kQkRows) s_log[lr][r] = lg;
+      }
+    }
+  } else {
+    QF qf[RMAX];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) qf[r].template load<DIM>(s_q, s_qshift, s_qsum, s_qok, r < R ? r : 0, c0);
+    // ---- dot products ----
+#pragma unroll
+    for (int i = 0; i < PASSES; ++i) {
+      const int lr = i * RPB + wave * L::RPW + lane / L::LPR;
+      const float s = to_f32(DT{}, sv[i]), m = to_f32(DT{}, mv[i]);
+#pragma unroll
+      for (int r = 0; r < RMAX; ++r) {
+        if (r >= R) break;
+        const float lg = qf[r].logit(qf[r].dot(w[i]), s, m, a.qk_scale);
+        if (lr < kQkRows && (lane % L::LPR) == 0) s_log[lr][r] = lg;
+      }
     }
   }
   __syncthreads();
@@ -1473,10 +1564,11 @@ template <typename DT, int DIM>
 int launch_qk_r(const QkArgs& a, hipStream_t stream) {
   const int row_blocks = static_cast<int>((a.plan_stride * a.bs + kQkRows - 1) / kQkRows);
   const dim3 grid(a.G * row_blocks);
+  constexpr bool kMf = DIM == 128;  // matrix cores at 128 channels
   if (a.R <= 4) {
-    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 4, 32>), grid, dim3(kBlock), 0, stream, a);
+    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 4, 32, kMf>), grid, dim3(kBlock), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 8, 16>), grid, dim3(kBlock), 0, stream, a);
+    hipLaunchKernelGGL((twilight_qk_kernel<DT, DIM, 8, 16, kMf>), grid, dim3(kBlock), 0, stream, a);
   }
   return tw_host::check_launch();
 }
