@@ -243,6 +243,11 @@ class TwilightWorkload:
         self.desired = torch.zeros((layers, G, R), dtype=i32, device=dev)
         self.max_rows = min(L, sink_end + R * self.N + (L - recent_start))
         self.out = torch.empty_like(self.q)
+        # dynamic budgets: the kept rows as row masks of the B0 union pages,
+        # attended page by page (the same rows as the union row list)
+        self.page_rows = budget_mode == "dynamic"
+        self.slot_u = torch.zeros((layers, G, R, self.b0), dtype=i32, device=dev)
+        self.prows = torch.zeros((layers, G, self.width), dtype=i32, device=dev)
         torch.cuda.synchronize(dev)
 
     def select(self, layer: int) -> None:
@@ -251,9 +256,15 @@ class TwilightWorkload:
         kernels.quest_select(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P], self.b0,
                              sel_pages=self.sel[layer], plan_pages=self.plan_pages[layer],
                              plan_masks=self.plan_masks[layer], plan_counts=self.plan_counts[layer])
+        pr = dict(slot_u=self.slot_u[layer], page_rows=self.prows[layer]) if self.page_rows else {}
         kernels.twilight_qk(self.qf[layer], self.packed[layer], self.scale[layer], self.minimum[layer],
                             self.plan_pages[layer], self.plan_masks[layer], self.plan_counts[layer], self.b0,
-                            sink=self.SINK, block_size=self.BS, out=self.logits[layer])
+                            sink=self.SINK, block_size=self.BS, out=self.logits[layer], **pr)
+        if self.page_rows:
+            kernels.twilight_select_pages(self.logits[layer], self.sel[layer], self.slot_u[layer], self.prows[layer],
+                                          top_p=self.TOP_P, sink=self.SINK, recent=self.RECENT, block_size=self.BS,
+                                          length=self.L, desired=self.desired[layer])
+            return
         kernels.twilight_select(self.logits[layer], self.sel[layer], top_p=self.TOP_P, budget_mode=self.mode,
                                 target_total=self.fixed * self.BS * self.R, rows=self.rows[layer],
                                 row_counts=self.row_counts[layer], desired=self.desired[layer], sink=self.SINK,
@@ -262,9 +273,35 @@ class TwilightWorkload:
     def attend(self, layer: int) -> None:
         from headinfer import kernels
 
+        if self.page_rows:
+            kernels.decode_attention_page_rows(self.q[layer], self.kc[layer], self.vc[layer], self.plan_pages[layer],
+                                               self.plan_counts[layer], self.prows[layer], max_pages=self.width,
+                                               sink=self.SINK, recent=self.RECENT, block_size=self.BS, length=self.L,
+                                               append=True, cur_k=self.cur_k[layer], cur_v=self.cur_v[layer],
+                                               out=self.out[layer])
+            return
         kernels.decode_attention_rows(self.q[layer], self.kc[layer], self.vc[layer], self.rows[layer],
                                       self.row_counts[layer], self.max_rows, cur_k=self.cur_k[layer],
                                       cur_v=self.cur_v[layer], out=self.out[layer], append_position=self.L)
+
+    def kept_rows(self, layer: int, g: int):
+        """Token positions group g attends at `layer` (without the decode
+        token), ascending."""
+        import torch
+
+        if not self.page_rows:
+            n = int(self.row_counts[layer, g])
+            return self.rows[layer, g, :n].long()
+        sink_end = min(self.SINK, self.L)
+        recent_start = max(sink_end, self.L - (self.RECENT - 1))
+        nu = int(self.plan_counts[layer, g])
+        pages = self.plan_pages[layer, g, :nu].long()
+        masks = self.prows[layer, g, :nu].long() & 0xFFFFFFFF
+        bits = (masks[:, None] >> torch.arange(self.BS, device=masks.device)) & 1
+        pos = self.SINK + pages[:, None] * self.BS + torch.arange(self.BS, device=masks.device)
+        dev = masks.device
+        return torch.cat([torch.arange(sink_end, device=dev), pos[bits.bool()],
+                          torch.arange(recent_start, self.L, device=dev)])
 
     def step(self) -> None:
         for layer in range(self.layers):
@@ -275,7 +312,10 @@ class TwilightWorkload:
         G, R, D, P, N = self.G, self.R, self.D, self.P, self.N
         e = 2
         cand_rows = self.plan_counts.double().sum().item() * self.BS / self.layers   # union of the B0 candidates
-        rows = self.row_counts.double().sum().item() / self.layers                  # attended union rows
+        if self.page_rows:                                                          # attended union rows
+            rows = sum(self.kept_rows(layer, g).numel() for layer in range(self.layers) for g in range(G)) / self.layers
+        else:
+            rows = self.row_counts.double().sum().item() / self.layers
         select = (2 * P * D * e * G + G * R * P * 4 * 2 + G * R * self.b0 * 4 + cand_rows * (D // 2 + 2 * e)
                   + G * R * N * 4 * 2 + G * R * D * 4)
         attention = rows * 2 * D * e + 2 * G * R * D * e + 4 * G * D * e
@@ -713,8 +753,8 @@ def twilight_leg(args, dev) -> dict:
     sink_end = min(w.SINK, w.L)
     recent_start = max(sink_end, w.L - (w.RECENT - 1))
     for g in range(w.G):
-        n = int(w.row_counts[0, g])
-        rows = w.rows[0, g, :n].long()
+        rows = w.kept_rows(0, g)
+        n = rows.numel()
         ok &= bool((rows[1:] > rows[:-1]).all()) and int(rows[0]) == 0 and int(rows[-1]) == w.L - 1
         ok &= n >= sink_end + (w.L - recent_start) and bool((w.desired[0, g] >= 1).all())
         e = _attention_check(w.q[0, g], w.kc[0, g, : w.L], w.vc[0, g, : w.L], rows, None, w.cur_k[0, g],
@@ -741,7 +781,9 @@ def twilight_leg(args, dev) -> dict:
         "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "twilight-32k-hbm: Llama-3-8B-shaped layer x 32, Quest B0 4096 tokens, INT4 QK, "
-                               f"top-p {w.TOP_P} ({w.mode} budgets), union attention, KV in HBM",
+                               f"top-p {w.TOP_P} ({w.mode} budgets), union attention "
+                               f"({'over the B0 union pages row masks' if w.page_rows else 'over the union row list'}), "
+                               "KV in HBM",
                    "layers": w.layers, "context": w.L, "kv_heads": w.G, "q_per_kv": w.R, "head_dim": w.D,
                    "page_size": w.BS, "b0_pages": w.b0, "top_p": w.TOP_P, "budget_mode": w.mode},
         "layer_us": round(layer_s * 1e6, 3),

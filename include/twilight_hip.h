@@ -220,16 +220,22 @@ int tw_quest_select_ragged(const float* q, const void* page_min, const void* pag
  *   D/2 + d/2] (low nibble = even channel), scale/minimum [G][
  *   quant_entry_stride] in dtype (tw_build_page_metadata's quantized keys);
  *   quant_rows valid rows per entry (candidates beyond it are skipped).
- *   logits [G][R][b0_pages*block_size] fp32 = qk_scale * (q . k~), k~_d =
- *   code_d*scale + min, reduced as 8-channel sequential sums combined by an
- *   adjacent-pair tree.  D = 4 .. 256, a power of two (8 channels per lane
- *   chunk, D channels when D < 8); R <= 8.
+ *   logits [G][R][b0_pages*block_size] fp32, the estimate of qk_scale * (q .
+ *   k~) with k~_d = code_d*scale + min, defined exactly: Q_d = rint(q_d *
+ *   2^(22-E)) with E the frexp exponent of max |q|, S = sum_d code_d * Q_d
+ *   (exact integer), logit = qk_scale * ((scale * ldexp(S, E-22)) + (min *
+ *   ldexp(sum_d Q_d, E-22))) in fp32 (a non-finite q gives NaN).  D = 4 ..
+ *   256, a power of two; R <= 8.
+ *   slot_u / page_rows (both or neither): for tw_twilight_select_pages,
+ *   slot_u [G][R][b0_pages] int32 gets the union index of each head's B0
+ *   slot and page_rows[g*plan_stride + u] is cleared for every union page.
  * ---------------------------------------------------------------------- */
 int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t* packed, const void* scale,
                    const void* minimum, int dtype, int64_t quant_entry_stride, int64_t quant_rows,
                    const int32_t* plan_pages,
                    const uint8_t* plan_masks, const int32_t* plan_counts, int64_t plan_stride, int b0_pages,
-                   int sink, int block_size, float qk_scale, float* logits, void* stream);
+                   int sink, int block_size, float qk_scale, float* logits, int32_t* slot_u, uint32_t* page_rows,
+                   void* stream);
 
 /* INT4 QK at explicit positions: the fused_affine_int4_qk call surface
  * (twilight_fused_qk.py:34-55).  q [G][R][D] fp32; positions [G][R][N] int64
@@ -294,6 +300,25 @@ int tw_twilight_select_ragged(const float* logits, int G, int R, int N, const in
                               int32_t* rows, int32_t* row_counts, int64_t rows_stride, int sink, int recent,
                               int block_size, const int32_t* lengths, int max_length, int page_capacity,
                               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Twilight top-p with dynamic budgets, the kept rows published per union
+ * page instead of as a row list (the union attention then walks the B0
+ * union pages with these row masks, tw_decode_attention_page_rows).  Same
+ * selection as tw_twilight_select(_ragged): every kept candidate n = slot *
+ * block_size + i of head r sets bit i of page_rows[g*page_rows_stride +
+ * slot_u[g][r][slot]] (slot_u and the cleared page_rows from tw_twilight_qk
+ * with the same plan stride).  desired [G][R] as tw_twilight_select.
+ * lengths (nullable): ragged groups as tw_twilight_select_ragged, each
+ * clamped to `length` (its max_length; page_capacity bounds their candidate
+ * pages); else every group has `length` tokens.  block_size <= 32 and a multiple of the candidates each
+ * thread holds (true for 16-token pages); workspace as tw_twilight_select.
+ * No counterpart in the reference, which builds the union row list
+ * (twilight_offload_cache.py:1517-1614); the row set is the same. */
+int tw_twilight_select_pages(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,
+                             float top_p, const int32_t* slot_u, uint32_t* page_rows, int64_t page_rows_stride,
+                             int32_t* desired, int sink, int recent, int block_size, int length,
+                             const int32_t* lengths, int page_capacity, void* workspace, size_t workspace_bytes,
+                             void* stream);
 
 /* ------------------------------------------------------------------------
  * Sparse GQA decode attention, split-K over selected rows, one query
@@ -372,6 +397,29 @@ int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const vo
                                      float softmax_scale, void* page_min, void* page_max,
                                      int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
                                      size_t workspace_bytes, void* stream);
+
+/* The Twilight union attention over page rows: the page-tile attention of
+ * tw_decode_attention_pages(_ragged) where plan_pages / plan_counts are the
+ * B0 union (tw_quest_select with k = b0_pages) and page_rows[g*plan_stride +
+ * u] (tw_twilight_select_pages) says which rows of union page u are kept.
+ * Every head attends every kept row (the GQA union of
+ * twilight_offload_cache.py:1517-1614 with mp.py:239-279), the sink and
+ * recent windows and the decode token; rows not kept are neither read nor
+ * attended.  lengths (nullable) or length, append, cur_k / cur_v, the page
+ * metadata of a completed page (page_min/page_max) and, with packed / qscale /
+ * qmin [G][quant_entry_stride] (16-bit K), the appended row's INT4 code, as
+ * tw_decode_attention_pages_ragged and tw_decode_attention_rows_append do.
+ * D = 128, 16-row pages, 16-bit K/V, R <= 8; workspace as tw_decode_attention
+ * for max_rows. */
+int tw_decode_attention_page_rows(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
+                                  int D, const int32_t* plan_pages, const int32_t* plan_counts,
+                                  const uint32_t* page_rows, int64_t plan_stride, int max_rows,
+                                  int64_t entry_stride_rows, int sink, int recent, int block_size,
+                                  const int32_t* lengths, int length, int append, const void* cur_k,
+                                  const void* cur_v, float softmax_scale, void* page_min, void* page_max,
+                                  int64_t page_entry_stride, int meta_pages, uint8_t* packed, void* qscale,
+                                  void* qmin, int64_t quant_entry_stride, void* out, void* workspace,
+                                  size_t workspace_bytes, void* stream);
 /* Page-tile attention with a resident page cache in HBM, for slabs in host
  * memory.  Replaces the previous-token resident cache of the Twilight cache
  * (previous_token_resident_cache, twilight_offload_cache.py:2457-2608,

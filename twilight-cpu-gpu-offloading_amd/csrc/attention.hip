@@ -121,6 +121,10 @@ struct AttnArgs {
   void* meta_qscale;
   void* meta_qmin;
   int64_t meta_qstride;
+  // Page-tile kernel, Twilight union (nullable): page_rows[g][u] (plan_stride
+  // apart) has bit i set when row i of union page u is kept; every head
+  // attends the kept rows, and rows not kept are neither read nor attended.
+  const uint32_t* page_rows;
 };
 
 // 8 consecutive channels of one row.
@@ -1187,15 +1191,18 @@ struct TileSrc {
   int cnt;       // rows of the tile that exist (0..16)
   int dec;       // index of the decode token in the tile, or -1
   uint32_t hm;   // heads that see the tile's cache rows
+  uint32_t rm;   // rows of the tile that are attended (bit i = row i)
+  int r0;        // a row that is attended (the address of the rows that are not)
   int u;         // union-plan index of a page tile, -1 for sink / recent tiles
   int page;      // its page id
 };
 
 __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w, int t, int nu, int page,
-                                            uint32_t pmask) {
+                                            uint32_t pmask, uint32_t prow) {
   TileSrc s;
   s.dec = -1;
   s.hm = 0xffu;
+  s.rm = 0xffffu;
   s.u = -1;
   s.page = page;
   const int ts = w.sink_tiles;
@@ -1206,7 +1213,11 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
   } else if (t < ts + nu) {
     s.pos0 = a.sink + static_cast<int64_t>(page) * kTileRows;
     s.hm = pmask;
-    s.cnt = (s.pos0 >= 0 && s.pos0 + kTileRows <= a.entry_stride) ? kTileRows : 0;
+    if (a.page_rows != nullptr) {
+      s.hm = 0xffu;  // the GQA union: every head attends every kept row
+      s.rm = prow & 0xffffu;
+    }
+    s.cnt = (s.pos0 >= 0 && s.pos0 + kTileRows <= a.entry_stride && s.rm != 0u) ? kTileRows : 0;
     s.u = s.cnt > 0 ? t - ts : -1;
   } else {
     const int j0 = kTileRows * (t - ts - nu);
@@ -1220,6 +1231,7 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
     s.cnt = 0;
     s.pos0 = 0;
   }
+  s.r0 = s.rm != 0u ? __builtin_ctz(s.rm) : 0;
   return s;
 }
 
@@ -1255,17 +1267,18 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   const int slot_last = static_cast<int>(a.plan_stride - 1);
   const int per_chunk = NW * TW * a.iters;
   int page[TW], page_nx[TW];
-  uint32_t pmask[TW], pmask_nx[TW];
-  auto load_slots = [&](int t0, int (&pg)[TW], uint32_t (&pm)[TW]) {
+  uint32_t pmask[TW], pmask_nx[TW], prow[TW], prow_nx[TW];
+  auto load_slots = [&](int t0, int (&pg)[TW], uint32_t (&pm)[TW], uint32_t (&pr)[TW]) {
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
       int u = t0 + tt - a.t_sink_tiles;
       u = u < 0 ? 0 : (u > slot_last ? slot_last : u);
       pg[tt] = a.plan_pages[plan_base + u];
       pm[tt] = a.plan_masks != nullptr ? static_cast<uint32_t>(a.plan_masks[plan_base + u]) : 0xffu;
+      pr[tt] = a.page_rows != nullptr ? a.page_rows[plan_base + u] : 0xffffu;
     }
   };
-  load_slots((chunk * a.iters * NW + wave) * TW, page, pmask);
+  load_slots((chunk * a.iters * NW + wave) * TW, page, pmask, prow);
   uint4 qf[4];
   {
     const S* qh = static_cast<const S*>(a.q) + (static_cast<int64_t>(g) * R + (krow < R ? krow : 0)) * D + 8 * quarter;
@@ -1289,7 +1302,10 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   if (chunk >= n_chunks) return;
   if (chunk == 0) {
     append_decode_token<S>(a, g, D, win.append_position);
-    complete_page_meta<DT>(a, g, win.append_position);
+    if (a.meta_packed != nullptr)
+      complete_row_meta<DT>(a, g, win.append_position);  // the row's INT4 code, then its page
+    else
+      complete_page_meta<DT>(a, g, win.append_position);
   }
 
   const S* kg = static_cast<const S*>(a.k) + static_cast<int64_t>(g) * a.entry_stride * D;
@@ -1322,6 +1338,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       for (int tt = 0; tt < TW; ++tt) {
         page[tt] = page_nx[tt];
         pmask[tt] = pmask_nx[tt];
+        prow[tt] = prow_nx[tt];
       }
     }
     if (t0 >= n_tiles) break;
@@ -1334,7 +1351,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     int hit_slot[TW];
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
-      ts[tt] = tile_src(a, win, t0 + tt, nu, page[tt], pmask[tt]);
+      ts[tt] = tile_src(a, win, t0 + tt, nu, page[tt], pmask[tt], prow[tt]);
       hit_slot[tt] = -1;
       if (res && ts[tt].u >= 0 && ts[tt].page >= 0 && ts[tt].page < a.res_map_pages) {
         const int64_t m = a.res_map[static_cast<int64_t>(g) * a.res_map_pages + ts[tt].page];
@@ -1348,7 +1365,9 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       const int64_t tb = hit ? (res_prev + static_cast<int64_t>(hit_slot[tt]) * kTileRows) * D : ts[tt].pos0 * D;
       const S* kt = hit ? static_cast<const S*>(a.res_k) : kg;
       const S* vt = hit ? static_cast<const S*>(a.res_v) : vg;
-      const int kr = krow < ts[tt].cnt ? krow : 0;
+      // rows outside the tile or not kept read a kept row (the same lines,
+      // no extra traffic) and are masked below
+      const int kr = (krow < ts[tt].cnt && ((ts[tt].rm >> krow) & 1u)) ? krow : ts[tt].r0;
       const S* kp = krow == ts[tt].dec ? kdec : kt + tb + kr * D;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
@@ -1357,13 +1376,13 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * rg + j;
-        const int vr = r < ts[tt].cnt ? r : 0;
+        const int vr = (r < ts[tt].cnt && ((ts[tt].rm >> r) & 1u)) ? r : ts[tt].r0;
         const S* vp = r == ts[tt].dec ? vdec : vt + tb + vr * D;
         vf[tt][j] = NT ? load_stream(vp + c8) : *reinterpret_cast<const uint4*>(vp + c8);
       }
     }
     // the next batch's page slots ride in the same round trip
-    if (it + 1 < a.iters) load_slots(t0 + NW * TW, page_nx, pmask_nx);
+    if (it + 1 < a.iters) load_slots(t0 + NW * TW, page_nx, pmask_nx, prow_nx);
     // ---- q.k on the matrix cores; scores in log2 units ----
     float sc[TW][4];
 #pragma unroll
@@ -1371,7 +1390,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) H::mfma(qf[s], kf[tt][s], acc);
-      const bool ok = krow < ts[tt].cnt;
+      const bool ok = krow < ts[tt].cnt && ((ts[tt].rm >> krow) & 1u);
       const uint32_t hm = krow == ts[tt].dec ? 0xffu : ts[tt].hm;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -2113,8 +2132,14 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
                        const void* cur_v, float softmax_scale, void* res_k, void* res_v, int64_t* res_map,
                        int res_slots, int res_map_pages, unsigned long long* res_stats, void* page_min,
                        void* page_max, int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
-                       size_t workspace_bytes, void* stream) {
+                       size_t workspace_bytes, void* stream, const uint32_t* page_rows = nullptr,
+                       uint8_t* packed = nullptr, void* qscale = nullptr, void* qmin = nullptr,
+                       int64_t quant_entry_stride = 0) {
   if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr) return TW_EINVAL;
+  if (page_rows != nullptr && res_map != nullptr) return TW_EINVAL;  // the resident cache keeps whole pages
+  if (packed != nullptr &&
+      (qscale == nullptr || qmin == nullptr || cur_k == nullptr || append == 0 || quant_entry_stride < entry_stride_rows))
+    return TW_EINVAL;
   if (page_min != nullptr &&
       (page_max == nullptr || append == 0 || meta_pages < 1 ||
        page_entry_stride < static_cast<int64_t>(meta_pages) * kTileD ||
@@ -2178,6 +2203,11 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
   a.meta_max = page_max;
   a.meta_stride = page_entry_stride;
   a.meta_pages = meta_pages;
+  a.page_rows = page_rows;
+  a.meta_packed = packed;
+  a.meta_qscale = qscale;
+  a.meta_qmin = qmin;
+  a.meta_qstride = quant_entry_stride;
   plan_tile_chunks(G, max_rows, &a.iters, &a.max_chunks);
   a.t_per_chunk = a.iters * kTileNW * kTileTW;
   if (lengths != nullptr) {
@@ -2248,3 +2278,19 @@ extern "C" int tw_decode_attention_pages_ragged(const void* q, const void* k_bas
                                 page_entry_stride, meta_pages, out, workspace, workspace_bytes, stream);
 }
 
+extern "C" int tw_decode_attention_page_rows(const void* q, const void* k_base, const void* v_base, int dtype, int G,
+                                             int R, int D, const int32_t* plan_pages, const int32_t* plan_counts,
+                                             const uint32_t* page_rows, int64_t plan_stride, int max_rows,
+                                             int64_t entry_stride_rows, int sink, int recent, int block_size,
+                                             const int32_t* lengths, int length, int append, const void* cur_k,
+                                             const void* cur_v, float softmax_scale, void* page_min, void* page_max,
+                                             int64_t page_entry_stride, int meta_pages, uint8_t* packed, void* qscale,
+                                             void* qmin, int64_t quant_entry_stride, void* out, void* workspace,
+                                             size_t workspace_bytes, void* stream) {
+  if (page_rows == nullptr) return TW_EINVAL;
+  return tw::pages_tiles_launch(q, k_base, v_base, dtype, G, R, D, plan_pages, nullptr, plan_counts, plan_stride,
+                                max_rows, entry_stride_rows, sink, recent, block_size, lengths, length, append, cur_k,
+                                cur_v, softmax_scale, nullptr, nullptr, nullptr, 0, 0, nullptr, page_min, page_max,
+                                page_entry_stride, meta_pages, out, workspace, workspace_bytes, stream, page_rows,
+                                packed, qscale, qmin, quant_entry_stride);
+}

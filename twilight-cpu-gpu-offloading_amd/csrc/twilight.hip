@@ -62,6 +62,11 @@ struct QkArgs {
   int b0, sink, bs;
   float qk_scale;
   float* logits;              // [G][R][b0*bs]
+  // Page-row outputs (nullable): slot_u[g][r][slot] = the union index of
+  // head r's B0 slot, and page_rows[g][u] (plan_stride apart) cleared for
+  // every union page, for the top-p's row bits.
+  int32_t* slot_u;
+  uint32_t* page_rows;
 };
 
 // Sums / maxima over aligned groups of N lanes (N = 1..16, a power of two);
@@ -556,6 +561,17 @@ __global__ __launch_bounds__(kBlock) void twilight_qk_kernel(QkArgs a) {
     }
   }
   __syncthreads();
+  // ---- page-row outputs: each union page's slot map and a cleared row mask ----
+  if (a.slot_u != nullptr) {
+    for (int idx = tid; idx < npg * R; idx += kBlock) {
+      const int p = idx / R;
+      const int r = idx - p * R;
+      const int slot = s_slot[p][r];
+      if (((s_mask[p] >> r) & 1) && slot < a.b0)
+        a.slot_u[(static_cast<int64_t>(g) * R + r) * a.b0 + slot] = u_first + p;
+    }
+  }
+  if (a.page_rows != nullptr && tid < npg) a.page_rows[static_cast<int64_t>(g) * a.plan_stride + u_first + tid] = 0u;
   // ---- out: row lr of head r to logits[g][r][slot * bs + lr's place in its
   // page]; candidates beyond the INT4 rows are skipped ----
   if (tid < nrows) {
@@ -666,6 +682,12 @@ struct SelectArgs {
   // .., p_max) candidate pages and at most that many (<= b0) B0 pages per head.
   const int32_t* lengths;
   int p_max;
+  // Page-row output (nullable, dynamic budgets): each kept candidate's row
+  // bit ORed into page_rows[g][slot_u[g][r][slot]] (page_rows_stride apart),
+  // instead of the published bitmaps and the group's union rows.
+  const int32_t* slot_u;
+  uint32_t* page_rows;
+  int64_t page_rows_stride;
 };
 
 // Tokens of group g (ragged: its own length, clamped to the launch bound).
@@ -1484,6 +1506,7 @@ __global__ __launch_bounds__(NT) void twilight_topp_kernel(SelectArgs s) {
       s.desired[row] = 0;
       if (s.allocated != nullptr) s.allocated[row] = 0;
     }
+    if (s.page_rows != nullptr) return;  // no row of this head is kept
     publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, 0u, sh);
     if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
     build_token_union<NT>(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
@@ -1516,6 +1539,17 @@ __global__ __launch_bounds__(NT) void twilight_topp_kernel(SelectArgs s) {
   if (threadIdx.x == 0) s.desired[row] = desired;
   if (s.matched) return;
   if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = desired;
+  if (s.page_rows != nullptr) {
+    // the thread's KPT candidates lie in one B0 slot (bs % KPT == 0, checked
+    // on the host): one OR of their row bits into that union page's mask
+    if (taken != 0u) {
+      const int c0 = KPT * static_cast<int>(threadIdx.x);
+      const int slot = c0 / s.bs;
+      const int u = s.slot_u[static_cast<int64_t>(row) * s.b0 + slot];
+      atomicOr(s.page_rows + static_cast<int64_t>(g) * s.page_rows_stride + u, taken << (c0 - slot * s.bs));
+    }
+    return;
+  }
   publish_selection<KPT>(s.selbits + static_cast<int64_t>(row) * s.words_n, s.words_n, taken, sh);
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
   build_token_union<NT>(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
@@ -1641,6 +1675,17 @@ int launch_select_kpt(const SelectArgs& s, hipStream_t stream) {
   return tw_host::check_launch();
 }
 
+// Candidates per thread of the top-p launch for N candidates per head (the
+// KPT launch_select picks).
+int candidates_per_thread(int N) {
+  constexpr int NT = kToppThreads;
+  int kpt = 1;
+  while (kpt * NT < N && kpt < 32) kpt *= 2;
+  if (NT < 1024 && kpt < 2) kpt = 2;
+  if (NT < 512 && kpt < 4) kpt = 4;
+  return kpt;
+}
+
 int launch_select(const SelectArgs& s, hipStream_t stream) {
   constexpr int NT = kToppThreads;
   if constexpr (NT >= 1024) {
@@ -1671,10 +1716,12 @@ extern "C" int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t
                               const void* minimum, int dtype, int64_t quant_entry_stride, int64_t quant_rows,
                               const int32_t* plan_pages,
                               const uint8_t* plan_masks, const int32_t* plan_counts, int64_t plan_stride,
-                              int b0_pages, int sink, int block_size, float qk_scale, float* logits, void* stream) {
+                              int b0_pages, int sink, int block_size, float qk_scale, float* logits,
+                              int32_t* slot_u, uint32_t* page_rows, void* stream) {
   if (q == nullptr || packed == nullptr || scale == nullptr || minimum == nullptr || plan_pages == nullptr ||
       plan_masks == nullptr || plan_counts == nullptr || logits == nullptr)
     return TW_EINVAL;
+  if ((slot_u == nullptr) != (page_rows == nullptr)) return TW_EINVAL;
   if (G <= 0 || R <= 0 || R > 8 || b0_pages <= 0 || sink < 0 || block_size <= 0 || plan_stride < 1 ||
       quant_entry_stride <= 0 || quant_rows <= 0 || quant_rows > quant_entry_stride)
     return TW_EINVAL;
@@ -1683,7 +1730,7 @@ extern "C" int tw_twilight_qk(const float* q, int G, int R, int D, const uint8_t
   const uintptr_t pk_align = D >= 32 ? 16 : static_cast<uintptr_t>(D / 2);
   if ((reinterpret_cast<uintptr_t>(q) % 16) || (reinterpret_cast<uintptr_t>(packed) % pk_align)) return TW_EINVAL;
   tw::QkArgs a{q, packed, scale, minimum, quant_entry_stride, quant_rows, G, R, D, plan_pages, plan_masks, plan_counts,
-               plan_stride, b0_pages, sink, block_size, qk_scale, logits};
+               plan_stride, b0_pages, sink, block_size, qk_scale, logits, slot_u, page_rows};
   const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case TW_DTYPE_F16: return tw::launch_qk<tw::F16>(a, s);
@@ -1706,7 +1753,7 @@ extern "C" int tw_int4_qk_positions(const float* q, int G, int R, int D, const u
   const uintptr_t pk_align = D >= 32 ? 16 : static_cast<uintptr_t>(D / 2);
   if ((reinterpret_cast<uintptr_t>(q) % 16) || (reinterpret_cast<uintptr_t>(packed) % pk_align)) return TW_EINVAL;
   tw::QkArgs a{q, packed, scale, minimum, quant_entry_stride, quant_rows, G, R, D, nullptr, nullptr, nullptr, 0,
-               0, 0, 1, qk_scale, nullptr};
+               0, 0, 1, qk_scale, nullptr, nullptr, nullptr};
   const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case TW_DTYPE_F16: return tw::launch_qk_positions<tw::F16>(a, positions, N, out, materialize != 0, s);
@@ -1727,8 +1774,11 @@ int select_launch(const float* logits, int G, int R, int N, const int32_t* sel_p
                   int budget_mode, int target_total, int32_t* desired, int32_t* allocated, uint32_t* head_bits,
                   int32_t* rows, int32_t* row_counts, int64_t rows_stride, int sink, int recent, int block_size,
                   int length, const int32_t* lengths, int p_max, int append_position, void* workspace,
-                  size_t workspace_bytes, void* stream) {
-  if (logits == nullptr || sel_pages == nullptr || rows == nullptr || row_counts == nullptr) return TW_EINVAL;
+                  size_t workspace_bytes, void* stream, const int32_t* slot_u = nullptr,
+                  uint32_t* page_rows = nullptr, int64_t page_rows_stride = 0) {
+  const bool pr = page_rows != nullptr;
+  if (logits == nullptr || sel_pages == nullptr || (!pr && (rows == nullptr || row_counts == nullptr)))
+    return TW_EINVAL;
   if (G <= 0 || R <= 0 || R > 8 || N <= 0 || b0_pages <= 0 || N != b0_pages * block_size) return TW_EINVAL;
   if (N > tw::sel::kMaxSelPages) return TW_EUNSUPPORTED;
   if (!(top_p > 0.0f) || !(top_p <= 1.0f) || budget_mode < 0 || budget_mode > 2) return TW_EINVAL;
@@ -1736,7 +1786,13 @@ int select_launch(const float* logits, int G, int R, int N, const int32_t* sel_p
   if (sink < 0 || recent <= 0 || block_size <= 0 || length < 0) return TW_EINVAL;
   if (budget_mode == 1 && (target_total < R || target_total > static_cast<int64_t>(R) * N)) return TW_EINVAL;
   // every union row fits: sink + recent + R*N selected + the decode row
-  if (rows_stride < static_cast<int64_t>(length) + 1) return TW_EINVAL;
+  if (!pr && rows_stride < static_cast<int64_t>(length) + 1) return TW_EINVAL;
+  if (pr) {
+    // dynamic budgets only; a thread's candidates in one page's row mask
+    const int kpt = tw::candidates_per_thread(N);
+    if (slot_u == nullptr || budget_mode != 0 || block_size > 32 || block_size % kpt != 0 || page_rows_stride < 1)
+      return TW_EINVAL;
+  }
   if (workspace == nullptr || workspace_bytes < tw_twilight_select_workspace_size(G, R, N)) return TW_ENOMEM;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const int words = (N + 31) / 32;
@@ -1768,6 +1824,9 @@ int select_launch(const float* logits, int G, int R, int N, const int32_t* sel_p
   s.append_position = append_position;
   s.lengths = lengths;
   s.p_max = p_max;
+  s.slot_u = slot_u;
+  s.page_rows = page_rows;
+  s.page_rows_stride = page_rows_stride;
   return tw::launch_select(s, static_cast<hipStream_t>(stream));
 }
 }  // namespace
@@ -1792,4 +1851,15 @@ extern "C" int tw_twilight_select_ragged(const float* logits, int G, int R, int 
   return select_launch(logits, G, R, N, sel_pages, b0_pages, top_p, 0, 0, desired, allocated, head_bits, rows,
                        row_counts, rows_stride, sink, recent, block_size, max_length, lengths, page_capacity, -1,
                        workspace, workspace_bytes, stream);
+}
+
+extern "C" int tw_twilight_select_pages(const float* logits, int G, int R, int N, const int32_t* sel_pages,
+                                        int b0_pages, float top_p, const int32_t* slot_u, uint32_t* page_rows,
+                                        int64_t page_rows_stride, int32_t* desired, int sink, int recent,
+                                        int block_size, int length, const int32_t* lengths, int page_capacity,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  if (page_rows == nullptr || length < 0 || page_capacity < 0) return TW_EINVAL;
+  return select_launch(logits, G, R, N, sel_pages, b0_pages, top_p, 0, 0, desired, nullptr, nullptr, nullptr,
+                       nullptr, 0, sink, recent, block_size, length, lengths, lengths != nullptr ? page_capacity : 0,
+                       -1, workspace, workspace_bytes, stream, slot_u, page_rows, page_rows_stride);
 }

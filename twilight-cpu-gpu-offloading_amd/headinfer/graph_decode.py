@@ -182,6 +182,12 @@ class GraphDecoder:
             self.tw_rows = torch.zeros((self.G, self.max_length + 1), dtype=torch.int32, device=dev)
             self.tw_counts = torch.zeros((self.G,), dtype=torch.int32, device=dev)
             self.tw_max_rows = min(self.max_length, cache.sink_tokens + self.R * n_cand + cache.recent_tokens)
+            # 16-row pages at D = 128, 16-bit K/V, R <= 8: the kept rows as row
+            # masks of the B0 union pages, attended page by page
+            self.page_rows = (cache.block_size == 16 and self.D == 128 and self.R <= 8
+                              and cache.dtype in (torch.float16, torch.bfloat16))
+            self.tw_slot_u = torch.zeros((self.G, self.R, self.k), dtype=torch.int32, device=dev)
+            self.tw_prows = torch.zeros((self.G, self.width), dtype=torch.int32, device=dev)
         self.logits: Optional[torch.Tensor] = None
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
@@ -306,8 +312,38 @@ class GraphDecoder:
                                     self.lengths, self.k, sink=c.sink_tokens, recent=c.recent_tokens,
                                     block_size=c.block_size, sel_pages=self.tw_sel, plan_pages=pp, plan_masks=pm,
                                     plan_counts=pc)
-        kernels.twilight_qk(q32, c._packed[e0:e0 + G], c._qscale[e0:e0 + G], c._qmin[e0:e0 + G], pp, pm, pc, self.k,
-                            sink=c.sink_tokens, block_size=c.block_size, out=self.tw_logits)
+        if self.page_rows:
+            kernels.twilight_qk(q32, c._packed[e0:e0 + G], c._qscale[e0:e0 + G], c._qmin[e0:e0 + G], pp, pm, pc,
+                                self.k, sink=c.sink_tokens, block_size=c.block_size, out=self.tw_logits,
+                                slot_u=self.tw_slot_u, page_rows=self.tw_prows)
+            kernels.twilight_select_pages(self.tw_logits, self.tw_sel, self.tw_slot_u, self.tw_prows, top_p=c.top_p,
+                                          sink=c.sink_tokens, recent=c.recent_tokens, block_size=c.block_size,
+                                          length=self.max_length, lengths=self.lengths, page_capacity=self.P)
+            # the attention also appends the decode token and (fused) its INT4 row and page metadata
+            meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G],
+                        packed=c._packed[e0:e0 + G], scale=c._qscale[e0:e0 + G],
+                        minimum=c._qmin[e0:e0 + G]) if self.fuse else {}
+            kernels.decode_attention_page_rows(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp, pc,
+                                               self.tw_prows, max_pages=self.width, sink=c.sink_tokens,
+                                               recent=c.recent_tokens, block_size=c.block_size, lengths=self.lengths,
+                                               append=True, cur_k=k, cur_v=v, softmax_scale=float(attn.scaling),
+                                               out=self.attn[li], **meta)
+        else:
+            kernels.twilight_qk(q32, c._packed[e0:e0 + G], c._qscale[e0:e0 + G], c._qmin[e0:e0 + G], pp, pm, pc,
+                                self.k, sink=c.sink_tokens, block_size=c.block_size, out=self.tw_logits)
+            self._twilight_rows_attention(li, attn, qg, k, v)
+        if not self.fuse:
+            kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
+                                                block_size=c.block_size, page_min=c._page_min,
+                                                page_max=c._page_max, packed=c._packed, scale=c._qscale,
+                                                minimum=c._qmin)
+
+    def _twilight_rows_attention(self, li: int, attn, qg, k, v) -> None:
+        """Top-p + the GQA union as a row list, then the rows-mode attention
+        with the append (shapes the page-row path does not take)."""
+        c = self.cache
+        G = self.G
+        e0 = li * G
         kernels.twilight_select_ragged(self.tw_logits, self.tw_sel, self.lengths, top_p=c.top_p, rows=self.tw_rows,
                                        row_counts=self.tw_counts, max_length=self.max_length,
                                        page_capacity=self.P, sink=c.sink_tokens, recent=c.recent_tokens,
@@ -319,11 +355,6 @@ class GraphDecoder:
                                       self.tw_counts, self.tw_max_rows, cur_k=k, cur_v=v,
                                       softmax_scale=float(attn.scaling), out=self.attn[li],
                                       append_position=self.lengths, metadata=meta if self.fuse else None)
-        if not self.fuse:
-            kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
-                                                block_size=c.block_size, page_min=c._page_min,
-                                                page_max=c._page_max, packed=c._packed, scale=c._qscale,
-                                                minimum=c._qmin)
 
     def capture(self) -> None:
         """Capture the step graph.  The step runs once eagerly first (its

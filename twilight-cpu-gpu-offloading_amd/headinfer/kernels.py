@@ -490,13 +490,18 @@ def twilight_qk(
     block_size: int,
     qk_scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
+    slot_u: Optional[torch.Tensor] = None,
+    page_rows: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """INT4 QK estimate of every head over its B0 candidates (one launch).
 
     q [G,R,D] fp32; packed [G, >=T, D/2] uint8 with scale/minimum [G, >=T]
     (build_page_metadata's INT4 outputs); the stage-1 union plan of
     quest_select with k = b0_pages.  Returns logits [G, R, b0_pages*bs] fp32
-    in candidate order (each head's pages ascending, block_size rows each)."""
+    in candidate order (each head's pages ascending, block_size rows each).
+    slot_u [G, R, b0_pages] int32 and page_rows [G, plan stride] int32 (both
+    or neither): the union index of every head's B0 slot, and cleared row
+    masks of the union pages, for twilight_select_pages."""
     if q.ndim != 3 or q.dtype != torch.float32 or not q.is_contiguous():
         raise ValueError("q must be contiguous [G, R, D] fp32")
     G, R, D = q.shape
@@ -520,10 +525,20 @@ def twilight_qk(
     elif out.dtype != torch.float32 or tuple(out.shape) != (G, R, N) or not out.is_contiguous():
         raise ValueError("out must be contiguous [G, R, b0_pages*block_size] fp32")
     qs = float(torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32)) if qk_scale is None else float(qk_scale)
+    if (slot_u is None) != (page_rows is None):
+        raise ValueError("slot_u and page_rows go together")
+    if slot_u is not None:
+        if slot_u.dtype != torch.int32 or tuple(slot_u.shape) != (G, R, b0_pages) or not slot_u.is_contiguous():
+            raise ValueError("slot_u must be contiguous [G, R, b0_pages] int32")
+        if page_rows.dtype != torch.int32 or tuple(page_rows.shape) != tuple(plan_pages.shape) \
+                or page_rows.stride() != plan_pages.stride():
+            raise ValueError("page_rows must be int32 shaped and strided like plan_pages")
+        _require_device(slot_u, page_rows, what="twilight_qk")
     with torch.cuda.device(dev):
         check(hip().tw_twilight_qk(ptr(q), G, R, D, ptr(packed), ptr(scale), ptr(minimum), _dt(scale), qe,
                                    packed.shape[1], ptr(plan_pages), ptr(plan_masks), ptr(plan_counts), plan_pages.stride(0),
-                                   b0_pages, sink, block_size, qs, ptr(out), stream_handle(dev)), "twilight_qk")
+                                   b0_pages, sink, block_size, qs, ptr(out), ptr(slot_u), ptr(page_rows),
+                                   stream_handle(dev)), "twilight_qk")
     return out
 
 
@@ -669,6 +684,55 @@ def twilight_select_ragged(
                                               sink, recent, block_size, ptr(lengths), int(max_length),
                                               int(page_capacity), ptr(ws), ws.numel(), stream_handle(dev)),
               "twilight_select_ragged")
+
+
+def twilight_select_pages(
+    logits: torch.Tensor,
+    sel_pages: torch.Tensor,
+    slot_u: torch.Tensor,
+    page_rows: torch.Tensor,
+    *,
+    top_p: float,
+    sink: int,
+    recent: int,
+    block_size: int,
+    length: int = 0,
+    lengths: Optional[torch.Tensor] = None,
+    page_capacity: int = 0,
+    desired: Optional[torch.Tensor] = None,
+) -> None:
+    """Top-p with dynamic budgets, each kept row published as a bit of its
+    union page's row mask (page_rows, cleared by twilight_qk with the same
+    slot_u) instead of a union row list.  lengths [G] int32 (device) for
+    ragged groups, each clamped to `length` (their bound, as max_length of
+    twilight_select_ragged); else every group has `length` tokens."""
+    if logits.dtype != torch.float32 or logits.ndim != 3 or not logits.is_contiguous():
+        raise ValueError("logits must be contiguous [G, R, N] fp32")
+    G, R, N = logits.shape
+    if sel_pages.dtype != torch.int32 or sel_pages.ndim != 3 or sel_pages.shape[:2] != (G, R) \
+            or not sel_pages.is_contiguous():
+        raise ValueError("sel_pages must be contiguous [G, R, b0] int32")
+    b0 = sel_pages.shape[2]
+    if b0 * block_size != N:
+        raise ValueError("logits must hold b0_pages * block_size candidates per head")
+    if slot_u.dtype != torch.int32 or tuple(slot_u.shape) != (G, R, b0) or not slot_u.is_contiguous():
+        raise ValueError("slot_u must be contiguous [G, R, b0] int32")
+    if page_rows.dtype != torch.int32 or page_rows.ndim != 2 or page_rows.shape[0] != G or page_rows.stride(1) != 1:
+        raise ValueError("page_rows must be [G, stride] int32")
+    if lengths is not None and (lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,)
+                                or not lengths.is_contiguous()):
+        raise ValueError("lengths must be contiguous [G] int32")
+    if desired is not None and (desired.dtype != torch.int32 or tuple(desired.shape) != (G, R)
+                                or not desired.is_contiguous()):
+        raise ValueError("desired must be contiguous [G, R] int32")
+    dev = _require_device(logits, sel_pages, slot_u, page_rows, lengths, desired, what="twilight_select_pages")
+    nbytes = hip().tw_twilight_select_workspace_size(G, R, N)
+    ws = WORKSPACE.get(dev, "twilight_select", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_twilight_select_pages(ptr(logits), G, R, N, ptr(sel_pages), b0, float(top_p), ptr(slot_u),
+                                             ptr(page_rows), page_rows.stride(0), ptr(desired), sink, recent,
+                                             block_size, int(length), ptr(lengths), int(page_capacity), ptr(ws),
+                                             ws.numel(), stream_handle(dev)), "twilight_select_pages")
 
 
 # --------------------------------------------------------------- attention
@@ -956,6 +1020,95 @@ def decode_attention_pages_ragged(
                                                      ptr(lengths), int(bool(append)), ptr(cur_k), ptr(cur_v), scale,
                                                      *meta, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
               "decode_attention_pages_ragged")
+    return out
+
+
+def decode_attention_page_rows(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    plan_pages: torch.Tensor,
+    plan_counts: torch.Tensor,
+    page_rows: torch.Tensor,
+    *,
+    max_pages: int,
+    sink: int,
+    recent: int,
+    block_size: int = 16,
+    lengths: Optional[torch.Tensor] = None,
+    length: int = 0,
+    append: bool = True,
+    cur_k: Optional[torch.Tensor] = None,
+    cur_v: Optional[torch.Tensor] = None,
+    softmax_scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+    page_min: Optional[torch.Tensor] = None,
+    page_max: Optional[torch.Tensor] = None,
+    packed: Optional[torch.Tensor] = None,
+    scale: Optional[torch.Tensor] = None,
+    minimum: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """The Twilight union attention over page rows: every head attends the
+    kept rows of the B0 union pages (page_rows from twilight_select_pages,
+    int32 shaped like plan_pages), the sink and recent windows and the decode
+    token.  lengths [G] int32 (device) for ragged groups, else every group has
+    `length` tokens.  append / cur_k / cur_v / page_min / page_max as
+    decode_attention_pages_ragged; packed [G, T, D/2] with scale / minimum
+    [G, T] (16-bit) also get the appended row's INT4 code.  16-bit K/V,
+    D = 128, block_size 16.  Returns [G, R, D]."""
+    if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("q must be [G, R, D] fp16/bf16")
+    G, R, D = q.shape
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or k_cache.shape != v_cache.shape \
+            or k_cache.ndim != 3 or k_cache.shape[0] != G or k_cache.shape[2] != D \
+            or k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1 or k_cache.stride(1) != D \
+            or k_cache.stride(0) % D:
+        raise ValueError("K/V cache must be row-contiguous [G, Lmax, D] in q's dtype")
+    if plan_pages.dtype != torch.int32 or plan_pages.ndim != 2 or plan_pages.shape[0] != G \
+            or plan_pages.stride(1) != 1:
+        raise ValueError("plan_pages must be [G, stride] int32")
+    if page_rows.dtype != torch.int32 or page_rows.shape != plan_pages.shape or page_rows.stride() != plan_pages.stride():
+        raise ValueError("page_rows must be int32 shaped and strided like plan_pages")
+    if plan_counts.dtype != torch.int32 or tuple(plan_counts.shape) != (G,):
+        raise ValueError("plan_counts must be [G] int32")
+    if lengths is not None and (lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,)
+                                or not lengths.is_contiguous()):
+        raise ValueError("lengths must be contiguous [G] int32")
+    if lengths is None and not 0 <= int(length) < k_cache.shape[1]:
+        raise ValueError("length must leave the decode row inside the cache")
+    if not 0 <= max_pages <= plan_pages.shape[1]:
+        raise ValueError("max_pages must be within the plan width")
+    if (cur_k is None) != (cur_v is None):
+        raise ValueError("cur_k and cur_v go together")
+    if cur_k is not None and (cur_k.shape != (G, D) or cur_k.dtype != q.dtype or cur_v.shape != cur_k.shape
+                              or cur_v.dtype != q.dtype):
+        raise ValueError("cur_k/cur_v must be [G, D] in q's dtype")
+    if packed is not None and (scale is None or minimum is None or cur_k is None or not append
+                               or packed.dtype != torch.uint8 or packed.ndim != 3 or packed.shape[0] != G
+                               or packed.shape[2] != D // 2 or packed.stride(2) != 1 or packed.stride(1) != D // 2
+                               or scale.ndim != 2 or scale.shape[0] != G or scale.stride(1) != 1
+                               or minimum.stride() != scale.stride() or scale.dtype != q.dtype
+                               or minimum.dtype != q.dtype or packed.stride(0) // (D // 2) != scale.stride(0)):
+        raise ValueError("packed [G, T, D/2] uint8 and scale/minimum [G, T] must match (with cur_k and append)")
+    dev = _require_device(q, plan_pages, plan_counts, page_rows, lengths, cur_k, cur_v, page_min, page_max, packed,
+                          scale, minimum, what="decode_attention_page_rows")
+    meta = _page_meta_args(page_min, page_max, G, D, append)
+    kp, vp = _slab_source(k_cache, v_cache)
+    _require_contiguous(q, cur_k, cur_v, what="decode_attention_page_rows")
+    if out is None:
+        out = torch.empty_like(q)
+    sc = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    max_rows = sink + max_pages * block_size + recent
+    nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
+    ws = WORKSPACE.get(dev, "decode_attention", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_decode_attention_page_rows(ptr(q), kp, vp, _dt(q), G, R, D, ptr(plan_pages), ptr(plan_counts),
+                                                  ptr(page_rows), plan_pages.stride(0), max_rows,
+                                                  k_cache.stride(0) // D, sink, recent, block_size, ptr(lengths),
+                                                  int(length), int(bool(append)), ptr(cur_k), ptr(cur_v), sc, *meta,
+                                                  ptr(packed), ptr(scale), ptr(minimum),
+                                                  0 if scale is None else scale.stride(0), ptr(out), ptr(ws),
+                                                  ws.numel(), stream_handle(dev)), "decode_attention_page_rows")
     return out
 
 
