@@ -67,6 +67,8 @@ def parse_args(argv=None):
                     help="Twilight budgets (twilight32k)")
     ap.add_argument("--budget-pages", type=int, default=128)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-host-tpot", action="store_true",
+                    help="default workload: leave out the 64K pinned-host TPOT leg")
     ap.add_argument("--quest-only", action="store_true",
                     help="default workload: only the Quest 32K leg (no Twilight / host-offload / TPOT summaries)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample budget (s)")
@@ -691,7 +693,13 @@ def main(argv=None) -> int:
         result["offload64k"] = {"layer_us": off["layer_us"], "host_link": off["host_link"],
                                 "parity_ok": off["parity"]["ok"]}
         print("[bench] leg: tpot32k", file=sys.stderr, flush=True)
-        result["tpot32k"] = tpot_leg(leg_args, dev)
+        model = tpot_model(dev)
+        result["tpot32k"] = tpot_leg(leg_args, dev, model)
+        if not args.no_host_tpot:
+            print("[bench] leg: tpot64k host", file=sys.stderr, flush=True)
+            result["tpot64k_host"] = tpot_leg(leg_args, dev, model, ctx=65536, kv="host", n_dec=16)
+        del model
+        torch.cuda.empty_cache()
         ok = ok and tw["parity"]["ok"] and off["parity"]["ok"]
     print(json.dumps(result), flush=True)
     return 0 if ok else 1
@@ -1078,41 +1086,59 @@ def _graph_tpot(dec, n: int) -> dict:
             "tpot_mean_ms": round(sum(steady) / len(steady) * 1e3, 3), "decode_tokens": n}
 
 
-def tpot_leg(args, dev) -> dict:
-    """p50 TPOT at 32K context with the KV in HBM, every decode token one
-    replay of a captured graph: a Llama-3-8B-shaped model (random-init bf16
-    weights) patched by mp_headinfer, a random 32K-token prompt prefilled once
-    per cache, then tokens of the fixed id 1.  Three decoders: sparse Quest
-    (budget 128 pages per query head), the dense comparator on the same
-    prefilled cache (no score or top-k: every whole page before the recent
-    window through the same attention), and Twilight (Quest B0 4096 tokens,
-    INT4 QK, top-p 0.95, dynamic budgets)."""
+def tpot_model(dev):
+    """The Llama-3-8B-shaped model (random-init bf16 weights) patched by
+    mp_headinfer, shared by the TPOT legs."""
     import torch
 
     from headinfer import mp
-    from headinfer.graph_decode import GraphDecoder
-    from headinfer.quest_offload_cache import QuestTopKOffloadedCache
-    from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache
     from transformers import LlamaForCausalLM
 
-    ctx = 32768
-    n_dec = max(4, args.decode_tokens)
-    cfg = llama3_8b_config(32)
     print("[bench] tpot: Llama-3-8B-shaped model, random init", file=sys.stderr, flush=True)
     torch.manual_seed(4)
     with torch.device(dev):
-        model = LlamaForCausalLM._from_config(cfg, dtype=torch.bfloat16)
+        model = LlamaForCausalLM._from_config(llama3_8b_config(32), dtype=torch.bfloat16)
     model.eval()
     mp.mp_headinfer(model)
-    ids = torch.randint(0, cfg.vocab_size, (1, ctx), generator=torch.Generator().manual_seed(5)).to(dev)
+    return model
+
+
+def tpot_leg(args, dev, model=None, ctx: int = 32768, kv: str = "hbm", n_dec: int = 0) -> dict:
+    """p50 TPOT with every decode token one replay of a captured graph: the
+    Llama-3-8B-shaped model, a random ctx-token prompt prefilled once per
+    cache, then tokens of the fixed id 1.  Decoders: sparse Quest (budget 128
+    pages per query head), the dense comparator on the same prefilled cache
+    (no score or top-k: every whole page before the recent window through the
+    same attention), Twilight (Quest B0 4096 tokens, INT4 QK, top-p 0.95,
+    dynamic budgets), and with the KV in pinned host memory also sparse Quest
+    with the HBM resident page cache (previous_token_resident_cache)."""
+    import torch
+
+    from headinfer.graph_decode import GraphDecoder
+    from headinfer.quest_offload_cache import QuestTopKOffloadedCache
+    from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache
+
+    own = model is None
+    if own:
+        model = tpot_model(dev)
+    n_dec = n_dec or max(4, args.decode_tokens)
+    vocab = model.config.vocab_size
+    ids = torch.randint(0, vocab, (1, ctx), generator=torch.Generator().manual_seed(5)).to(dev)
     out = {}
-    with torch.no_grad():
-        cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + 2 * n_dec + 8,
-                                                         kv_residency="hbm", budget_pages=args.budget_pages,
-                                                         update_metadata_on_decode=True)
-        print("[bench] tpot: prefill (Quest cache)", file=sys.stderr, flush=True)
+    prefill_s = {}
+
+    def prefill(cache, label):
+        print(f"[bench] tpot {ctx // 1024}k {kv}: prefill ({label})", file=sys.stderr, flush=True)
+        t0 = time.perf_counter()
         model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
         torch.cuda.synchronize()
+        prefill_s[label] = round(time.perf_counter() - t0, 2)
+
+    with torch.no_grad():
+        cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + 2 * n_dec + 8,
+                                                         kv_residency=kv, budget_pages=args.budget_pages,
+                                                         update_metadata_on_decode=True)
+        prefill(cache, "quest")
         dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1)
         out["sparse_graph"] = _graph_tpot(dec, n_dec)
         dec.sync_cache()
@@ -1121,24 +1147,39 @@ def tpot_leg(args, dev) -> dict:
         out["dense_graph"] = _graph_tpot(dec, n_dec)
         del dec, cache
         torch.cuda.empty_cache()
+        if kv == "host":
+            cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + n_dec + 8, kv_residency=kv,
+                                                             budget_pages=args.budget_pages,
+                                                             update_metadata_on_decode=True,
+                                                             previous_token_resident_cache=True)
+            prefill(cache, "quest, resident page cache")
+            dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1)
+            out["sparse_graph_resident"] = _graph_tpot(dec, n_dec)
+            st = cache.resident_stats()
+            out["sparse_graph_resident"]["resident_hit_ratio"] = round(
+                st["resident_hit_pages"] / max(1, st["union_pages"]), 4)
+            del dec, cache
+            torch.cuda.empty_cache()
         cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(
-            model, max_cache_len=ctx + n_dec + 8, kv_residency="hbm", candidate_token_budget=4096, top_p=0.95,
+            model, max_cache_len=ctx + n_dec + 8, kv_residency=kv, candidate_token_budget=4096, top_p=0.95,
             budget_mode="dynamic", update_metadata_on_decode=True)
-        print("[bench] tpot: prefill (Twilight cache)", file=sys.stderr, flush=True)
-        model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
-        torch.cuda.synchronize()
+        prefill(cache, "twilight")
         dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1)
         out["twilight_graph"] = _graph_tpot(dec, n_dec)
         del dec, cache
-    del model
+    if own:
+        del model
     torch.cuda.empty_cache()
     dense = out["dense_graph"]["tpot_p50_ms"]
-    return {"context": ctx, "kv": "hbm", "p50_ms": {k: v["tpot_p50_ms"] for k, v in out.items()},
-            "mean_ms": {k: v["tpot_mean_ms"] for k, v in out.items()}, "decode_tokens": n_dec,
-            "dense_over_sparse": round(dense / out["sparse_graph"]["tpot_p50_ms"], 3),
-            "dense_over_twilight": round(dense / out["twilight_graph"]["tpot_p50_ms"], 3),
-            "model": "Llama-3-8B-shaped (32 layers, 32 q / 8 kv heads, head_dim 128), random-init bf16",
-            "budget_pages": args.budget_pages}
+    res = {"context": ctx, "kv": kv, "p50_ms": {k: v["tpot_p50_ms"] for k, v in out.items()},
+           "mean_ms": {k: v["tpot_mean_ms"] for k, v in out.items()}, "decode_tokens": n_dec,
+           "dense_over": {k: round(dense / v["tpot_p50_ms"], 3) for k, v in out.items() if k != "dense_graph"},
+           "prefill_s": prefill_s,
+           "model": "Llama-3-8B-shaped (32 layers, 32 q / 8 kv heads, head_dim 128), random-init bf16",
+           "budget_pages": args.budget_pages}
+    if "sparse_graph_resident" in out:
+        res["resident_hit_ratio"] = out["sparse_graph_resident"]["resident_hit_ratio"]
+    return res
 
 
 class MultiRequestWorkload:
