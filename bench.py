@@ -66,6 +66,8 @@ def parse_args(argv=None):
     ap.add_argument("--budget-mode", choices=("dynamic", "matched"), default="dynamic",
                     help="Twilight budgets (twilight32k)")
     ap.add_argument("--budget-pages", type=int, default=128)
+    ap.add_argument("--requests", type=int, default=1,
+                    help="quest32k: decode this many requests of the same context per launch (8 KV groups each)")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-host-tpot", action="store_true",
                     help="default workload: leave out the 64K pinned-host TPOT leg")
@@ -85,12 +87,16 @@ class QuestWorkload:
     SINK, RECENT, BS = 64, 256, 16
     PLANTED, OUTLIERS = 16, 4
 
-    def __init__(self, dev, layers: int, context: int, budget_pages: int, seed: int = 1):
+    def __init__(self, dev, layers: int, context: int, budget_pages: int, seed: int = 1, requests: int = 1):
         import torch
 
         from headinfer import kernels
 
         self.dev, self.layers, self.L = dev, layers, context
+        # a batch of requests at one context length: every request's KV groups
+        # side by side in the same launches
+        self.requests = requests
+        self.G = type(self).G * requests
         G, R, D, L = self.G, self.R, self.D, context
         self.dtype = torch.float16
         self.Lmax = L + 1  # room for the decode token's row
@@ -587,7 +593,7 @@ def main(argv=None) -> int:
         return run_multireq(args, dev)
     args.context = args.context or 32768
     print(f"[bench] building inputs: layers={args.layers} context={args.context}", file=sys.stderr, flush=True)
-    w = QuestWorkload(dev, args.layers, args.context, args.budget_pages)
+    w = QuestWorkload(dev, args.layers, args.context, args.budget_pages, requests=args.requests)
 
     print("[bench] eager step + parity", file=sys.stderr, flush=True)
     w.step()
@@ -660,6 +666,7 @@ def main(argv=None) -> int:
                         "append), all KV in HBM",
             "layers": w.layers, "context": w.L, "kv_heads": w.G, "q_per_kv": w.R, "head_dim": w.D,
             "page_size": w.BS, "budget_pages": w.k, "scored_pages": w.P, "sink": w.SINK, "recent": w.RECENT,
+            "requests": w.requests,
         },
         "layer_us": round(layer_s * 1e6, 3),
         "layer_us_event": round(step_event / w.layers * 1e6, 3),

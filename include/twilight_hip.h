@@ -255,7 +255,8 @@ int tw_int4_qk_positions(const float* q, int G, int R, int D, const uint8_t* pac
  * inline twilight_offload_cache.py:1274-1310), matched_budget_counts
  * (twilight_offload_cache.py:50-86, per group, every head's capacity N) and
  * the GPU GQA union (twilight_offload_cache.py:1517-1614).
- *   logits [G][R][N] from tw_twilight_qk, N = b0_pages*block_size <= 8192;
+ *   logits [G][R][N] from tw_twilight_qk, N = b0_pages*block_size <=
+ *   tw_twilight_max_candidates() (16384);
  *   sel_pages [G][R][b0_pages] the stage-1 pages (ascending) that map
  *   candidate n of head r to position sink + sel_pages[n/bs]*bs + n%bs.
  *   desired (nullable) [G][R]: the exact top-p count -- masses E_n =
@@ -280,6 +281,13 @@ int tw_int4_qk_positions(const float* q, int G, int R, int D, const uint8_t* pac
  *   before the first call (the library leaves its counters zero).
  * ---------------------------------------------------------------------- */
 size_t tw_twilight_select_workspace_size(int G, int R, int N);
+/* Largest candidate count per head (N = b0_pages * block_size) the Twilight
+ * selection entry points take (16384: a 512-thread block, 32 candidates per
+ * thread); beyond it they return TW_EUNSUPPORTED.  The reference has no such
+ * limit (twilight_offload_cache.py:183-381 checks only that the budget is
+ * positive); TwilightOffloadCache refuses, at construction, a budget the
+ * longest cache would take past it. */
+int tw_twilight_max_candidates(void);
 int tw_twilight_select(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,
                        float top_p, int budget_mode, int target_total, int32_t* desired, int32_t* allocated,
                        uint32_t* head_bits, int32_t* rows, int32_t* row_counts, int64_t rows_stride, int sink,
@@ -310,8 +318,9 @@ int tw_twilight_select_ragged(const float* logits, int G, int R, int N, const in
  * with the same plan stride).  desired [G][R] as tw_twilight_select.
  * lengths (nullable): ragged groups as tw_twilight_select_ragged, each
  * clamped to `length` (its max_length; page_capacity bounds their candidate
- * pages); else every group has `length` tokens.  block_size <= 32 and a multiple of the candidates each
- * thread holds (true for 16-token pages); workspace as tw_twilight_select.
+ * pages); else every group has `length` tokens.  block_size <= 32, and it
+ * divides or is divided by the candidates each thread holds (2 to 32, a power
+ * of two: true for power-of-two page sizes); workspace as tw_twilight_select.
  * No counterpart in the reference, which builds the union row list
  * (twilight_offload_cache.py:1517-1614); the row set is the same. */
 int tw_twilight_select_pages(const float* logits, int G, int R, int N, const int32_t* sel_pages, int b0_pages,

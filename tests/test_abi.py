@@ -58,6 +58,7 @@ def test_invalid_arguments_rejected_without_launch():
     assert lib.tw_quest_score(None, None, None, 0, 1, 1, 1, 128, 128, None, None) == _native.TW_EINVAL
     assert lib.tw_topk_sorted(None, 1, 10, 10, 3, None, None, 0, None) == _native.TW_EINVAL
     assert lib.tw_topk_sorted_workspace_size(4, 8192) == 0 and lib.tw_topk_sorted_workspace_size(4, 8193) > 0
+    assert lib.tw_twilight_max_candidates() == 16384
     assert lib.tw_build_page_metadata(None, 0, 1, 16, 3, 0, 0, 16, None, None, 0, None, None, None, 0,
                                       None) == _native.TW_EINVAL
     assert lib.tw_decode_attention(None, None, None, 0, 1, 1, 128, None, None, None, 0, 0, None, 1, -1, 0, None,

@@ -122,6 +122,27 @@ def test_twilight_accepts_what_the_reference_accepts(kw):
         _twilight()(**BASE, **kw)
 
 
+def test_twilight_candidate_budget_limit():
+    """Past tw_twilight_max_candidates() candidate tokens per head the
+    selection cannot run, so the constructor refuses such a budget when the
+    cache is long enough to reach it (and only then)."""
+    from headinfer import kernels
+
+    cap = kernels.twilight_max_candidates()
+    assert cap == 16384
+    long_cache = dict(BASE, max_cache_len=64 + cap + 2 * 16 + 256)
+    for budget in (cap + 1, cap + 16, 4 * cap):
+        with pytest.raises(ValueError, match="the Twilight selection takes at most 16384"):
+            _twilight()(**long_cache, candidate_token_budget=budget)
+    if torch.cuda.is_available():
+        return
+    # the widest selection fits: a budget of exactly the cap, or a cache too
+    # short to give that many candidate pages
+    for kw in (dict(long_cache, candidate_token_budget=cap), dict(BASE, candidate_token_budget=4 * cap)):
+        with pytest.raises(ValueError, match="an operational ROCm device is required"):
+            _twilight()(**kw)
+
+
 def test_quest_accepts_more_than_eight_query_heads_per_kv():
     """The reference has no limit on query heads per KV head
     (quest_offload_cache.py:26-60); a 16-head group passes validation."""

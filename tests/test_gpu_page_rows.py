@@ -177,7 +177,8 @@ def _run_case(K, dev, G, R, lengths, b0, top_p, ragged, seed):
         _say(f"[page rows] G={G} R={R} ragged={ragged} rep {rep} ok, kept {[int(c) for c in counts_h]}")
 
 
-@pytest.mark.parametrize("G,R,L,b0,top_p", [(4, 4, 4096, 64, 0.95), (2, 8, 3000, 40, 0.8), (3, 2, 8192, 256, 0.99)])
+@pytest.mark.parametrize("G,R,L,b0,top_p", [(4, 4, 4096, 64, 0.95), (2, 8, 3000, 40, 0.8), (3, 2, 8192, 256, 0.99),
+                                             (2, 4, 20000, 1024, 0.95)])   # 16384 candidates: two pages per thread
 def test_page_rows_match_row_list(K, dev, G, R, L, b0, top_p):
     _run_case(K, dev, G, R, [L] * G, b0, top_p, ragged=False, seed=L + G)
 

@@ -45,6 +45,10 @@ CASES = [
     ("f16", 2, 4, 128, 32768, 64, 256, 16, 512, 0.99, "dynamic", 0, 0.5),
     ("f16", 4, 2, 128, 2500, 64, 256, 12, 30, 1.0, "dynamic", 0, 8.0),          # top_p = 1, page size 12
     ("bf16", 2, 1, 64, 1200, 4, 16, 4, 100, 0.3, "matched", 25, 1.0),          # one head per group
+    # past 8192 candidates: 32 per thread of the 512-thread top-p block
+    ("f16", 2, 4, 128, 32768, 64, 256, 16, 1024, 0.95, "dynamic", 0, 1.0),    # N = 16384, the limit
+    ("bf16", 2, 4, 128, 32768, 64, 256, 16, 1024, 0.9, "matched", 300, 3.0),
+    ("bf16", 3, 2, 128, 20000, 64, 256, 16, 700, 0.99, "dynamic", 0, 0.5),    # N = 11200
 ]
 
 
@@ -205,3 +209,24 @@ def test_twilight_union_pages_reaching_recent_window(K, dev, bs, b0):
         assert n == len(union) + 1, f"group {g}: union size {n - 1} vs {len(union)}"
         got = rows[g, :n].cpu().numpy()
         assert np.array_equal(got[:-1], union) and got[-1] == L
+
+
+def test_twilight_candidates_past_the_limit_rejected(K, dev):
+    """N = b0 * block_size above twilight_max_candidates() is refused before any
+    launch (TW_EUNSUPPORTED), by every selection entry point."""
+    cap = K.twilight_max_candidates()
+    G, R, bs = 1, 2, 16
+    b0 = cap // bs + 1
+    logits = torch.zeros((G, R, b0 * bs), dtype=torch.float32, device=dev)
+    sel = torch.arange(b0, dtype=torch.int32, device=dev).repeat(G, R, 1).contiguous()
+    L = 64 + b0 * bs + 256
+    rows = torch.zeros((G, L + 1), dtype=torch.int32, device=dev)
+    counts = torch.zeros((G,), dtype=torch.int32, device=dev)
+    with pytest.raises(RuntimeError, match="twilight_select"):
+        K.twilight_select(logits, sel, top_p=0.9, budget_mode="dynamic", rows=rows, row_counts=counts, sink=64,
+                          recent=256, block_size=bs, length=L)
+    slot_u = torch.zeros((G, R, b0), dtype=torch.int32, device=dev)
+    prows = torch.zeros((G, R * b0), dtype=torch.int32, device=dev)
+    with pytest.raises(RuntimeError, match="twilight_select_pages"):
+        K.twilight_select_pages(logits, sel, slot_u, prows, top_p=0.9, sink=64, recent=256, block_size=bs, length=L)
+    torch.cuda.synchronize()

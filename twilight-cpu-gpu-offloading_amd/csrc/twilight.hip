@@ -1540,13 +1540,19 @@ __global__ __launch_bounds__(NT) void twilight_topp_kernel(SelectArgs s) {
   if (s.matched) return;
   if (threadIdx.x == 0 && s.allocated != nullptr) s.allocated[row] = desired;
   if (s.page_rows != nullptr) {
-    // the thread's KPT candidates lie in one B0 slot (bs % KPT == 0, checked
-    // on the host): one OR of their row bits into that union page's mask
-    if (taken != 0u) {
-      const int c0 = KPT * static_cast<int>(threadIdx.x);
-      const int slot = c0 / s.bs;
-      const int u = s.slot_u[static_cast<int64_t>(row) * s.b0 + slot];
-      atomicOr(s.page_rows + static_cast<int64_t>(g) * s.page_rows_stride + u, taken << (c0 - slot * s.bs));
+    // the thread's KPT candidates lie in one B0 slot (bs % KPT == 0) or
+    // cover KPT / bs whole slots (KPT % bs == 0), as the host checks: one OR
+    // of their row bits into each such union page's mask
+    const int c0 = KPT * static_cast<int>(threadIdx.x);
+    const int span = KPT < s.bs ? KPT : s.bs;
+    const uint32_t low = span >= 32 ? 0xffffffffu : ((1u << span) - 1u);
+    for (int j = 0; j < KPT; j += span) {
+      const uint32_t m = (taken >> j) & low;
+      if (m != 0u) {  // set bits are candidates < N, so the slot is < b0
+        const int slot = (c0 + j) / s.bs;
+        const int u = s.slot_u[static_cast<int64_t>(row) * s.b0 + slot];
+        atomicOr(s.page_rows + static_cast<int64_t>(g) * s.page_rows_stride + u, m << (c0 + j - slot * s.bs));
+      }
     }
     return;
   }
@@ -1652,6 +1658,9 @@ int launch_qk_positions(const QkArgs& a, const int64_t* positions, int N, float*
 #define TW_TOPP_THREADS 512
 #endif
 constexpr int kToppThreads = TW_TOPP_THREADS;
+// Candidates per head a top-p block holds: 32 per thread (one 32-bit
+// selection mask each).
+constexpr int kMaxCandidates = 32 * kToppThreads;
 
 template <int KPT>
 int launch_select_kpt(const SelectArgs& s, hipStream_t stream) {
@@ -1695,16 +1704,9 @@ int launch_select(const SelectArgs& s, hipStream_t stream) {
     if (s.N <= 2 * NT) return launch_select_kpt<2>(s, stream);
   }
   if (s.N <= 4 * NT) return launch_select_kpt<4>(s, stream);
-  if constexpr (8 * NT >= kMaxSelPages) {
-    return launch_select_kpt<8>(s, stream);
-  } else if constexpr (16 * NT >= kMaxSelPages) {
-    if (s.N <= 8 * NT) return launch_select_kpt<8>(s, stream);
-    return launch_select_kpt<16>(s, stream);
-  } else {
-    if (s.N <= 8 * NT) return launch_select_kpt<8>(s, stream);
-    if (s.N <= 16 * NT) return launch_select_kpt<16>(s, stream);
-    return launch_select_kpt<32>(s, stream);
-  }
+  if (s.N <= 8 * NT) return launch_select_kpt<8>(s, stream);
+  if (s.N <= 16 * NT) return launch_select_kpt<16>(s, stream);
+  return launch_select_kpt<32>(s, stream);  // N <= kMaxCandidates, checked by the caller
 }
 
 size_t counter_bytes(int G) { return ((static_cast<size_t>(G) * 4 + 255) / 256) * 256; }
@@ -1763,6 +1765,8 @@ extern "C" int tw_int4_qk_positions(const float* q, int G, int R, int D, const u
   }
 }
 
+extern "C" int tw_twilight_max_candidates(void) { return tw::kMaxCandidates; }
+
 extern "C" size_t tw_twilight_select_workspace_size(int G, int R, int N) {
   if (G <= 0 || R <= 0 || N <= 0) return 0;
   const size_t words = static_cast<size_t>((N + 31) / 32);
@@ -1780,7 +1784,7 @@ int select_launch(const float* logits, int G, int R, int N, const int32_t* sel_p
   if (logits == nullptr || sel_pages == nullptr || (!pr && (rows == nullptr || row_counts == nullptr)))
     return TW_EINVAL;
   if (G <= 0 || R <= 0 || R > 8 || N <= 0 || b0_pages <= 0 || N != b0_pages * block_size) return TW_EINVAL;
-  if (N > tw::sel::kMaxSelPages) return TW_EUNSUPPORTED;
+  if (N > tw::kMaxCandidates) return TW_EUNSUPPORTED;
   if (!(top_p > 0.0f) || !(top_p <= 1.0f) || budget_mode < 0 || budget_mode > 2) return TW_EINVAL;
   if (budget_mode == 2 && allocated == nullptr) return TW_EINVAL;
   if (sink < 0 || recent <= 0 || block_size <= 0 || length < 0) return TW_EINVAL;
@@ -1790,7 +1794,8 @@ int select_launch(const float* logits, int G, int R, int N, const int32_t* sel_p
   if (pr) {
     // dynamic budgets only; a thread's candidates in one page's row mask
     const int kpt = tw::candidates_per_thread(N);
-    if (slot_u == nullptr || budget_mode != 0 || block_size > 32 || block_size % kpt != 0 || page_rows_stride < 1)
+    if (slot_u == nullptr || budget_mode != 0 || block_size > 32 || (block_size % kpt != 0 && kpt % block_size != 0) ||
+        page_rows_stride < 1)
       return TW_EINVAL;
   }
   if (workspace == nullptr || workspace_bytes < tw_twilight_select_workspace_size(G, R, N)) return TW_ENOMEM;

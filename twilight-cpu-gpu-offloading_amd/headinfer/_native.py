@@ -85,6 +85,7 @@ _HIP_SIGNATURES = {
                                             vp]),
     "tw_int4_qk_positions": (i32, [vp, i32, i32, i32, vp, vp, vp, i32, i64, i64, vp, i32, f32, i32, vp, vp]),
     "tw_twilight_select_workspace_size": (szt, [i32, i32, i32]),
+    "tw_twilight_max_candidates": (i32, []),
     "tw_twilight_select": (i32, [vp, i32, i32, i32, vp, i32, f32, i32, i32, vp, vp, vp, vp, vp, i64, i32, i32, i32,
                                  i32, i32, vp, szt, vp]),
     "tw_twilight_select_ragged": (i32, [vp, i32, i32, i32, vp, i32, f32, vp, vp, vp, vp, vp, i64, i32, i32, i32, vp,

@@ -569,6 +569,12 @@ def fused_affine_int4_qk(q: torch.Tensor, packed: torch.Tensor, scale: torch.Ten
     return out
 
 
+def twilight_max_candidates() -> int:
+    """Largest candidate count per head (B0 pages x page size) the Twilight
+    selection takes (tw_twilight_max_candidates)."""
+    return int(hip().tw_twilight_max_candidates())
+
+
 def twilight_select(
     logits: torch.Tensor,
     sel_pages: torch.Tensor,

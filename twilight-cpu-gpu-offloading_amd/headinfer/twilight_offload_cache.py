@@ -284,6 +284,19 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
             kwargs["max_selected_history_fraction"] = required_pages / max_pages if max_pages else 1.0
         else:
             kwargs["max_selected_history_fraction"] = min(1.0, matched_budget_fraction * num_query_heads_per_kv)
+        # The one limit the reference does not have: a top-p block holds at
+        # most kernels.twilight_max_candidates() candidate tokens per head
+        # (B0 pages x page size).  A budget the longest cache would take past
+        # it is refused here rather than at the first decode step.
+        block_size = int(kwargs.get("block_size", 16))
+        _, _, eligible = _window(int(kwargs["max_cache_len"]), int(kwargs.get("sink_tokens", 64)),
+                                 int(kwargs.get("recent_tokens", 256)))
+        widest = min(eligible // block_size, max(1, math.ceil(candidate_token_budget / block_size))) * block_size
+        if widest > kernels.twilight_max_candidates():
+            raise ValueError(
+                f"candidate_token_budget {candidate_token_budget} gives {widest} candidate tokens per head at "
+                f"max_cache_len {kwargs['max_cache_len']}; the Twilight selection takes at most "
+                f"{kernels.twilight_max_candidates()}")
         super().__init__(**kwargs)
         if cpu_bitmap_union and not gqa_groupwise_execution:
             raise ValueError("cpu_bitmap_union requires GQA group execution")
