@@ -66,6 +66,9 @@ def parse_args(argv=None):
     ap.add_argument("--budget-mode", choices=("dynamic", "matched"), default="dynamic",
                     help="Twilight budgets (twilight32k)")
     ap.add_argument("--budget-pages", type=int, default=128)
+    ap.add_argument("--union", choices=("bits", "plan"), default="bits",
+                    help="quest32k: the GQA union as per-head selection bitmaps ranked by the attention (bits) "
+                         "or as a union plan built after the top-k (plan)")
     ap.add_argument("--requests", type=int, default=1,
                     help="quest32k: decode this many requests of the same context per launch (8 KV groups each)")
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
@@ -87,12 +90,16 @@ class QuestWorkload:
     SINK, RECENT, BS = 64, 256, 16
     PLANTED, OUTLIERS = 16, 4
 
-    def __init__(self, dev, layers: int, context: int, budget_pages: int, seed: int = 1, requests: int = 1):
+    def __init__(self, dev, layers: int, context: int, budget_pages: int, seed: int = 1, requests: int = 1,
+                 union: str = "bits"):
         import torch
 
         from headinfer import kernels
 
         self.dev, self.layers, self.L = dev, layers, context
+        # "bits": per-head selection bitmaps ranked by the attention; "plan":
+        # the union plan built by the top-k's last block of each group
+        self.union = union
         # a batch of requests at one context length: every request's KV groups
         # side by side in the same launches
         self.requests = requests
@@ -138,6 +145,9 @@ class QuestWorkload:
         self.plan_masks = torch.zeros((layers, G, self.max_pages), dtype=torch.uint8, device=dev)
         self.plan_counts = torch.zeros((layers, G), dtype=i32, device=dev)
         self.sel = torch.zeros((layers, G, R, self.k), dtype=i32, device=dev)
+        self.bits = torch.zeros((layers, G, R, kernels.sel_bits_words(self.P)), dtype=i32, device=dev)
+        if self.union == "bits" and self.P > 8192:
+            self.union = "plan"  # longer rows select through the segment pass and a plan
         self.out = torch.empty_like(self.q)
         torch.cuda.synchronize(dev)
 
@@ -145,9 +155,43 @@ class QuestWorkload:
     def select(self, layer: int) -> None:
         from headinfer import kernels
 
+        if self.union == "bits":
+            kernels.quest_select_bits(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P],
+                                      self.k, self.bits[layer])
+            return
         kernels.quest_select(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P], self.k,
                              sel_pages=self.sel[layer], plan_pages=self.plan_pages[layer],
                              plan_masks=self.plan_masks[layer], plan_counts=self.plan_counts[layer])
+
+    def union_of(self, layer: int, g: int):
+        """(ascending union pages, head masks) of group g at `layer` from the
+        selection the step produced."""
+        import numpy as np
+
+        if self.union == "bits":
+            w = self.bits[layer, g].cpu().numpy().view(np.uint32)
+            p = np.arange(self.P)
+            hb = ((w[:, p >> 5] >> (p & 31).astype(np.uint32)) & 1).astype(np.int64)  # [R, P]
+            pages = np.flatnonzero(hb.any(axis=0))
+            masks = (hb[:, pages] << np.arange(self.R)[:, None]).sum(axis=0)
+            return pages, masks
+        nu = int(self.plan_counts[layer, g])
+        return (self.plan_pages[layer, g, :nu].long().cpu().numpy(),
+                self.plan_masks[layer, g, :nu].long().cpu().numpy())
+
+    def union_counts(self):
+        """Union pages per (layer, group)."""
+        import torch
+
+        if self.union == "bits":
+            b = self.bits.view(torch.int32).cpu()
+            words = b[..., 0::2].long() & 0xffffffff | (b[..., 1::2].long() << 32)
+            u = words[:, :, 0]
+            for r in range(1, self.R):
+                u = u | words[:, :, r]
+            return torch.tensor([[sum(bin(int(x) & 0xffffffffffffffff).count("1") for x in u[l, g])
+                                  for g in range(self.G)] for l in range(self.layers)], dtype=torch.float64)
+        return self.plan_counts.double().cpu()
 
     def append(self, layer: int) -> None:
         from headinfer import kernels
@@ -158,6 +202,13 @@ class QuestWorkload:
     def attend(self, layer: int, phase: int = 3) -> None:
         from headinfer import kernels
 
+        if self.union == "bits":
+            kernels.decode_attention_pages_bits(self.q[layer], self.kc[layer], self.vc[layer], self.bits[layer], self.P,
+                                                max_pages=self.max_pages, sink=self.SINK, recent=self.RECENT,
+                                                block_size=self.BS, length=self.L, append=True,
+                                                cur_k=self.cur_k[layer], cur_v=self.cur_v[layer],
+                                                out=self.out[layer], phase=phase)
+            return
         kernels.decode_attention_pages(self.q[layer], self.kc[layer], self.vc[layer], self.plan_pages[layer],
                                        self.plan_counts[layer], plan_masks=self.plan_masks[layer],
                                        max_pages=self.max_pages, sink=self.SINK, recent=self.RECENT,
@@ -178,7 +229,7 @@ class QuestWorkload:
         G, R, D, P, k = self.G, self.R, self.D, self.P, self.k
         e = 2
         fixed = min(self.SINK, self.L) + (self.RECENT - 1) + 1  # sink + recent + the decode token
-        rows = (self.plan_counts.double().sum().item() * self.BS + G * fixed) / self.layers
+        rows = (self.union_counts().sum().item() * self.BS + G * fixed) / self.layers
         select = 2 * P * D * e * G + G * R * P * 4 * 2 + G * R * k * 4 + G * R * D * 4
         # K/V rows (the decode token's come from registers), q, out, and the
         # append of the decode token (read + write)
@@ -340,7 +391,7 @@ class OffloadWorkload(QuestWorkload):
     def __init__(self, dev, layers: int, context: int, budget_pages: int, seed: int = 3):
         import torch
 
-        super().__init__(dev, layers, context, budget_pages, seed=seed)
+        super().__init__(dev, layers, context, budget_pages, seed=seed, union="plan")  # the DMA leg reads the plan
         hk = torch.empty(self.kc.shape, dtype=self.kc.dtype, pin_memory=True)
         hv = torch.empty(self.vc.shape, dtype=self.vc.dtype, pin_memory=True)
         hk.copy_(self.kc)
@@ -474,7 +525,13 @@ def check_parity(w: QuestWorkload) -> dict:
     import numpy as np
     import torch
 
+    from headinfer import kernels
+
     G, R, D = w.G, w.R, w.D
+    if w.union == "bits":
+        # the per-head page lists of the same selection, for the set checks
+        kernels.quest_select(w.qf[0], w.pmin[0, :, : w.P], w.pmax[0, :, : w.P], w.k, sel_pages=w.sel[0])
+        torch.cuda.synchronize()
     sel = w.sel[0].cpu().numpy()
     ok = bool((np.diff(sel, axis=-1) > 0).all() and sel.min() >= 0 and sel.max() < w.P)
     kc = w.kc[0].float()
@@ -483,10 +540,11 @@ def check_parity(w: QuestWorkload) -> dict:
     sink_end = min(w.SINK, w.L)
     recent_start = max(sink_end, w.L - (w.RECENT - 1))
     for g in range(G):
-        nu = int(w.plan_counts[0, g])
-        pages = w.plan_pages[0, g, :nu].long().cpu()
-        pmask = w.plan_masks[0, g, :nu].long().cpu()
-        # union plan == union of the per-head selections, masks == heads that chose each page
+        pages_np, masks_np = w.union_of(0, g)
+        nu = pages_np.shape[0]
+        pages = torch.from_numpy(pages_np).long()
+        pmask = torch.from_numpy(masks_np).long()
+        # union == union of the per-head selections, masks == heads that chose each page
         ok &= bool(np.array_equal(pages.numpy(), np.unique(sel[g])))
         ok &= all(int(pmask[u]) == sum(1 << r for r in range(R) if int(pages[u]) in sel[g, r]) for u in range(nu))
         bs = w.BS
@@ -593,7 +651,7 @@ def main(argv=None) -> int:
         return run_multireq(args, dev)
     args.context = args.context or 32768
     print(f"[bench] building inputs: layers={args.layers} context={args.context}", file=sys.stderr, flush=True)
-    w = QuestWorkload(dev, args.layers, args.context, args.budget_pages, requests=args.requests)
+    w = QuestWorkload(dev, args.layers, args.context, args.budget_pages, requests=args.requests, union=args.union)
 
     print("[bench] eager step + parity", file=sys.stderr, flush=True)
     w.step()
@@ -673,7 +731,8 @@ def main(argv=None) -> int:
         "layer_bytes": int(layer_bytes),
         "step_roofline_frac": round(value / HBM_PEAK_GBS, 4),
         "rows_per_group": round(by["rows_per_group"], 1),
-        "union_pages_per_group": round(w.plan_counts.double().mean().item(), 1),
+        "union_pages_per_group": round(w.union_counts().mean().item(), 1),
+        "union_form": w.union,
         "kernels": kern,
         "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom), "kernel": dom},

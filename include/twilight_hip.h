@@ -206,6 +206,26 @@ int tw_quest_select_ragged(const float* q, const void* page_min, const void* pag
                            int64_t plan_stride, int sink, int recent, int block_size, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* Quest selection as per-head page bitmaps, for the fused decode path.  The
+ * score and top-k of tw_quest_select (same orders and ties; lengths
+ * (nullable, device [G] int32) selects per group as tw_quest_select_ragged
+ * does), but instead of a union plan -- built by one block per group after
+ * its heads' top-k -- every head's selection is written as a bitmap: bit p
+ * of sel_bits[(g*R + r)*bits_stride + p/32] (32-bit words) is set when head
+ * r of group g selected page p.  2*ceil(P/64) words per row are written;
+ * bits_stride is even and sel_bits 8-byte aligned, so a row reads as 64-bit
+ * words.  tw_decode_attention_pages_bits ranks the union from these rows.
+ * Replaces prepare_layer_selection's page ids and the GQA union of the
+ * decode branches (quest_offload_cache.py:299-401, mp.py:239-279): the set
+ * of pages is the same, only the form differs.  P <= 8192 (longer rows:
+ * tw_quest_select), k in [1, P].  scores, sel_pages (nullable) as in
+ * tw_quest_select (ragged: each group's own pages and k_g slots, the rest
+ * -1).  Workspace: tw_quest_select_workspace_size(G, R, P). */
+int tw_quest_select_bits(const float* q, const void* page_min, const void* page_max, int dtype, int G, int R,
+                         int P, int D, int64_t page_group_stride, const int32_t* lengths, int k, float* scores,
+                         int32_t* sel_pages, uint32_t* sel_bits, int64_t bits_stride, int sink, int recent,
+                         int block_size, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Twilight stage 2, INT4 QK estimate over the B0 candidates of every head.
  * Replaces fused_affine_int4_qk (twilight_fused_qk.py:12-55) with the
@@ -407,6 +427,25 @@ int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const vo
                                      int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
+/* The page-tile attention of tw_decode_attention_pages(_ragged) with the
+ * union taken from selection bitmaps (tw_quest_select_bits) instead of a
+ * union plan: group g's union pages are the pages p < P whose bit is set in
+ * any of its R rows sel_bits[(g*R + r)*bits_stride ..], in ascending order,
+ * each attended by the heads whose bit is set (the plan's head masks).  The
+ * same tiles in the same order as the plan path, so the output is the same.
+ * lengths (nullable, device) or length, append, cur_k/cur_v and the fused
+ * page metadata update (page_min/page_max) as tw_decode_attention_page_rows;
+ * phase as tw_decode_attention_pages_phase.  P <= 8192 (128 words a row),
+ * bits_stride even, sel_bits 8-byte aligned; D = 128, 16-row pages, 16-bit
+ * K/V, R <= 8; max_rows bounds every group's rows (sink_end + union pages *
+ * 16 + recent rows + 1); workspace as tw_decode_attention for max_rows. */
+int tw_decode_attention_pages_bits(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R,
+                                   int D, const uint32_t* sel_bits, int64_t bits_stride, int P, int max_rows,
+                                   int64_t entry_stride_rows, int sink, int recent, int block_size,
+                                   const int32_t* lengths, int length, int append, const void* cur_k,
+                                   const void* cur_v, float softmax_scale, void* page_min, void* page_max,
+                                   int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
+                                   size_t workspace_bytes, int phase, void* stream);
 /* The Twilight union attention over page rows: the page-tile attention of
  * tw_decode_attention_pages(_ragged) where plan_pages / plan_counts are the
  * B0 union (tw_quest_select with k = b0_pages) and page_rows[g*plan_stride +

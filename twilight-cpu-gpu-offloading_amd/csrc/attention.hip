@@ -72,7 +72,7 @@ struct AttnArgs {
   void* v_append;
   float* part_ml;           // [G][max_chunks][R][2]  (m, l)
   float* part_o;            // [G][max_chunks][R][D]
-  unsigned int* counters;   // [G]
+  int32_t* union_sizes;    // [G] bitmap mode: each group's union pages, from the split-K kernel to the merge
   int max_chunks;
   int iters;                // row batches per block
   int max_rows;             // bound on every group's row count
@@ -125,6 +125,13 @@ struct AttnArgs {
   // apart) has bit i set when row i of union page u is kept; every head
   // attends the kept rows, and rows not kept are neither read nor attended.
   const uint32_t* page_rows;
+  // Page-tile kernel, selection bitmaps instead of a union plan (nullable):
+  // bit p of sel_bits + (g*R + r) * bits_stride (32-bit words) is set when
+  // head r of group g selected page p; bits_w64 64-bit words per row.  The
+  // union pages are the OR of the R rows, ranked in ascending page order.
+  const uint32_t* sel_bits;
+  int64_t bits_stride;
+  int bits_w64;
 };
 
 // 8 consecutive channels of one row.
@@ -406,9 +413,11 @@ __device__ __forceinline__ TileWin tile_window(const AttnArgs& a, int g) {
   return w;
 }
 
-// Union pages of group g that a page-tile launch covers.
+// Union pages of group g that a page-tile launch covers: the union plan's
+// count, or with selection bitmaps the size the split-K kernel ranked
+// (written by the group's chunk-0 block for the merge launch).
 __device__ __forceinline__ int tile_pages(const AttnArgs& a, int g, const TileWin& w) {
-  int nu = a.plan_counts[g];
+  int nu = a.sel_bits != nullptr ? a.union_sizes[g] : a.plan_counts[g];
   nu = nu < 0 ? 0 : nu;
   return nu > w.nu_cap ? w.nu_cap : nu;
 }
@@ -1186,6 +1195,46 @@ __global__ __launch_bounds__(kBlock, 2) void decode_attn_mfma(AttnArgs a) {
 // One wavefront batch is TW tiles; a wave's first batch needs no rescale.
 constexpr int kTileD = 128;
 
+// Union pages from selection bitmaps.  Each lane holds NWL consecutive
+// 64-bit words of every head's row (lane l: words NWL*l ..), uw their OR,
+// and incl / cnt the wavefront's inclusive prefix and own count of union
+// pages.  The union page of rank u (wave-uniform, below the union size) is
+// the (u - exclusive prefix)-th set bit of the first lane whose inclusive
+// prefix exceeds u; every lane tests one bit position of that word, so the
+// bit is found with one popcount and a ballot.  *hm gets the heads that
+// selected the page.
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t x, int l) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(x)), l));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(x >> 32)), l));
+  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+}
+
+template <int RMAX, int NWL>
+__device__ __forceinline__ void bits_page(int u, int incl, int cnt, const uint64_t (&uw)[NWL],
+                                          const uint64_t (&hw)[RMAX][NWL], int* page, uint32_t* hm) {
+  const int lane = lane_id();
+  const int L = __ffsll(static_cast<long long>(__ballot(incl > u))) - 1;
+  int j = u - (__builtin_amdgcn_readlane(incl, L) - __builtin_amdgcn_readlane(cnt, L));
+  int wsel = 0;
+  uint64_t word = readlane_u64(uw[0], L);
+  if constexpr (NWL == 2) {
+    const int c0 = __popcll(word);
+    wsel = j >= c0 ? 1 : 0;
+    j -= wsel ? c0 : 0;
+    word = wsel ? readlane_u64(uw[1], L) : word;
+  }
+  const bool hit = ((word >> lane) & 1ull) != 0ull && __popcll(word & lanemask_lt()) == j;
+  const int b = __ffsll(static_cast<long long>(__ballot(hit))) - 1;
+  *page = 64 * (NWL * L + wsel) + b;
+  uint32_t m = 0u;
+#pragma unroll
+  for (int h = 0; h < RMAX; ++h) {
+    const uint64_t x = (NWL == 2 && wsel) ? hw[h][NWL - 1] : hw[h][0];
+    m |= static_cast<uint32_t>((readlane_u64(x, L) >> b) & 1ull) << h;
+  }
+  *hm = m;
+}
+
 struct TileSrc {
   int64_t pos0;  // position of the tile's row 0 in the entry (cache rows)
   int cnt;       // rows of the tile that exist (0..16)
@@ -1238,7 +1287,9 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
 // NT: the slab is device memory, so its K/V rows are read with the
 // streaming hint (pinned host memory read over the host link keeps plain
 // loads, which measured faster there).
-template <typename DT, int RMAX, int NW, int TW, bool RES, bool NT>
+// NWL > 0: the union comes from selection bitmaps (NWL 64-bit words per
+// lane) instead of a union plan.
+template <typename DT, int RMAX, int NW, int TW, bool RES, bool NT, int NWL>
 __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   using S = typename DT::storage;
   using H = Half8<DT>;
@@ -1278,7 +1329,30 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       pr[tt] = a.page_rows != nullptr ? a.page_rows[plan_base + u] : 0xffffu;
     }
   };
-  load_slots((chunk * a.iters * NW + wave) * TW, page, pmask, prow);
+  // bitmap mode: every head's words of this lane, their OR and the prefix
+  constexpr int kNwl = NWL > 0 ? NWL : 1;
+  uint64_t hw[RMAX][kNwl], uw[kNwl];
+  int b_cnt = 0, b_incl = 0;
+  if constexpr (NWL > 0) {
+    const uint32_t* brow = a.sel_bits + static_cast<int64_t>(g) * R * a.bits_stride;
+#pragma unroll
+    for (int w = 0; w < NWL; ++w) {
+      const int wi = NWL * lane + w;
+      const int wc = wi < a.bits_w64 ? wi : a.bits_w64 - 1;
+      uw[w] = 0ull;
+#pragma unroll
+      for (int h = 0; h < RMAX; ++h) {
+        const int hc = h < R ? h : R - 1;
+        const uint64_t v = *reinterpret_cast<const uint64_t*>(brow + hc * a.bits_stride + 2 * wc);
+        hw[h][w] = (h < R && wi < a.bits_w64) ? v : 0ull;
+        uw[w] |= hw[h][w];
+      }
+      b_cnt += __popcll(uw[w]);
+    }
+    b_incl = wave_prefix_sum_i32(b_cnt);
+  } else {
+    load_slots((chunk * a.iters * NW + wave) * TW, page, pmask, prow);
+  }
   uint4 qf[4];
   {
     const S* qh = static_cast<const S*>(a.q) + (static_cast<int64_t>(g) * R + (krow < R ? krow : 0)) * D + 8 * quarter;
@@ -1289,7 +1363,14 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     }
   }
   const TileWin win = tile_window(a, g);
-  const int nu = tile_pages(a, g, win);
+  int nu;
+  if constexpr (NWL > 0) {
+    nu = __builtin_amdgcn_readlane(b_incl, kWave - 1);
+    nu = nu > win.nu_cap ? win.nu_cap : nu;
+    if (chunk == 0 && threadIdx.x == 0) a.union_sizes[g] = nu;
+  } else {
+    nu = tile_pages(a, g, win);
+  }
   const int n_tiles = win.sink_tiles + nu + win.run_tiles;
   const int n_chunks = (n_tiles + per_chunk - 1) / per_chunk;
   if (n_tiles == 0) {
@@ -1333,7 +1414,16 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
 
   for (int it = 0; it < a.iters; ++it) {
     const int t0 = ((chunk * a.iters + it) * NW + wave) * TW;
-    if (it > 0) {
+    if constexpr (NWL > 0) {
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt) {
+        const int u = t0 + tt - win.sink_tiles;  // wave-uniform
+        page[tt] = 0;
+        pmask[tt] = 0u;
+        prow[tt] = 0xffffu;
+        if (u >= 0 && u < nu) bits_page<RMAX, kNwl>(u, b_incl, b_cnt, uw, hw, &page[tt], &pmask[tt]);
+      }
+    } else if (it > 0) {
 #pragma unroll
       for (int tt = 0; tt < TW; ++tt) {
         page[tt] = page_nx[tt];
@@ -1382,7 +1472,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       }
     }
     // the next batch's page slots ride in the same round trip
-    if (it + 1 < a.iters) load_slots(t0 + NW * TW, page_nx, pmask_nx, prow_nx);
+    if (NWL == 0 && it + 1 < a.iters) load_slots(t0 + NW * TW, page_nx, pmask_nx, prow_nx);
     // ---- q.k on the matrix cores; scores in log2 units ----
     float sc[TW][4];
 #pragma unroll
@@ -1743,27 +1833,39 @@ void plan_tile_chunks(int G, int max_rows_total, int* iters, int* chunks) {
   *chunks = ch < 1 ? 1 : ch;
 }
 
+template <typename DT, int RMAX, bool RES, bool NT>
+void launch_tiles_nwl(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  const int nwl = a.sel_bits == nullptr ? 0 : (a.bits_w64 <= kWave ? 1 : 2);
+  if (nwl == 0)
+    hipLaunchKernelGGL((decode_attn_tiles<DT, RMAX, kTileNW, kTileTW, RES, NT, 0>), grid, block, 0, stream, a);
+  else if (nwl == 1)
+    hipLaunchKernelGGL((decode_attn_tiles<DT, RMAX, kTileNW, kTileTW, RES, NT, 1>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((decode_attn_tiles<DT, RMAX, kTileNW, kTileTW, RES, NT, 2>), grid, block, 0, stream, a);
+}
+
 template <typename DT>
 int launch_tiles(const AttnArgs& a, hipStream_t stream) {
   const int phase = a.phase == 0 ? 3 : a.phase;
   if (phase & 1) {
     const dim3 grid(a.G * a.max_chunks);
     const dim3 block(kTileNW * kWave);
-    // the resident page cache serves slabs in host memory: plain loads
+    // the resident page cache serves slabs in host memory: plain loads (and
+    // takes a union plan)
     if (a.res_map != nullptr) {
       if (a.R <= 4)
-        hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, true, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, true, false, 0>), grid, block, 0, stream, a);
       else
-        hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, true, false>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, true, false, 0>), grid, block, 0, stream, a);
     } else if (a.kv_stream) {
       if (a.R <= 4)
-        hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, false, true>), grid, block, 0, stream, a);
+        launch_tiles_nwl<DT, 4, false, true>(a, grid, block, stream);
       else
-        hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, false, true>), grid, block, 0, stream, a);
+        launch_tiles_nwl<DT, 8, false, true>(a, grid, block, stream);
     } else if (a.R <= 4) {
-      hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, false, false>), grid, block, 0, stream, a);
+      launch_tiles_nwl<DT, 4, false, false>(a, grid, block, stream);
     } else {
-      hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, false, false>), grid, block, 0, stream, a);
+      launch_tiles_nwl<DT, 8, false, false>(a, grid, block, stream);
     }
     const int rc = tw_host::check_launch();
     if (rc != TW_OK) return rc;
@@ -1858,7 +1960,7 @@ int launch_dtype(int dtype, const AttnArgs& a, hipStream_t s) {
 
 size_t counter_bytes(int G) { return ((static_cast<size_t>(G) * 4 + 255) / 256) * 256; }
 
-// Workspace layout: counters | part_ml | part_o, sized for the largest chunk
+// Workspace layout: union sizes | part_ml | part_o, sized for the largest chunk
 // count any dtype can produce for max_rows (+1 decode token).
 void workspace_layout(int G, int R, int D, int max_rows, size_t* ml_off, size_t* o_off, size_t* total) {
   // The chunk count is not monotonic in the row bound (more rows can mean
@@ -1948,7 +2050,7 @@ int rows_launch(const void* q, const void* k_base, const void* v_base, int dtype
   a.cur_v = cur_v;
   a.scale_log2 = softmax_scale * tw::kLog2e;
   a.out = out;
-  a.counters = static_cast<unsigned int*>(workspace);
+  a.union_sizes = static_cast<int32_t*>(workspace);
   a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ml_off);
   a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
   a.max_rows = max_rows;
@@ -2082,7 +2184,7 @@ extern "C" int tw_decode_attention_pages_phase(const void* q, const void* k_base
   a.window_left = -1;
   a.scale_log2 = softmax_scale * tw::kLog2e;
   a.out = out;
-  a.counters = static_cast<unsigned int*>(workspace);
+  a.union_sizes = static_cast<int32_t*>(workspace);
   a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ml_off);
   a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
   a.max_rows = max_rows;
@@ -2134,7 +2236,8 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
                        void* page_max, int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
                        size_t workspace_bytes, void* stream, const uint32_t* page_rows = nullptr,
                        uint8_t* packed = nullptr, void* qscale = nullptr, void* qmin = nullptr,
-                       int64_t quant_entry_stride = 0) {
+                       int64_t quant_entry_stride = 0, const uint32_t* sel_bits = nullptr, int64_t bits_stride = 0,
+                       int bits_pages = 0, int phase = 3) {
   if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr) return TW_EINVAL;
   if (page_rows != nullptr && res_map != nullptr) return TW_EINVAL;  // the resident cache keeps whole pages
   if (packed != nullptr &&
@@ -2145,7 +2248,18 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
        page_entry_stride < static_cast<int64_t>(meta_pages) * kTileD ||
        (reinterpret_cast<uintptr_t>(page_min) % 4) || (reinterpret_cast<uintptr_t>(page_max) % 4)))
     return TW_EINVAL;
-  if (G <= 0 || R <= 0 || R > 8 || plan_pages == nullptr || plan_counts == nullptr || plan_stride < 1) return TW_EINVAL;
+  if (G <= 0 || R <= 0 || R > 8 || phase < 1 || phase > 3) return TW_EINVAL;
+  if (sel_bits != nullptr) {
+    // selection bitmaps of bits_pages pages: at most 128 64-bit words a row
+    // (two per lane), 8-byte aligned rows
+    if (bits_pages < 1 || bits_pages > 128 * 64 || page_rows != nullptr || res_map != nullptr) return TW_EINVAL;
+    if (bits_stride < 2 * ((bits_pages + 63) / 64) || (bits_stride % 2) != 0 ||
+        (reinterpret_cast<uintptr_t>(sel_bits) % 8) != 0)
+      return TW_EINVAL;
+    plan_stride = bits_pages;  // the union has at most this many pages
+  } else if (plan_pages == nullptr || plan_counts == nullptr || plan_stride < 1) {
+    return TW_EINVAL;
+  }
   if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16) return TW_EUNSUPPORTED;
   if (D != kTileD || block_size != kTileRows) return TW_EUNSUPPORTED;
   if (sink < 0 || recent <= 0 || entry_stride_rows < 2 || entry_stride_rows > (1ll << 30)) return TW_EINVAL;
@@ -2188,11 +2302,10 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
   a.window_left = -1;
   a.scale_log2 = softmax_scale * kLog2e;
   a.out = out;
-  a.counters = static_cast<unsigned int*>(workspace);
+  a.union_sizes = static_cast<int32_t*>(workspace);
   a.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + ml_off);
   a.part_o = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + o_off);
   a.max_rows = max_rows;
-  a.phase = 3;
   a.res_k = res_k;
   a.res_v = res_v;
   a.res_map = res_map;
@@ -2208,6 +2321,10 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
   a.meta_qscale = qscale;
   a.meta_qmin = qmin;
   a.meta_qstride = quant_entry_stride;
+  a.sel_bits = sel_bits;
+  a.bits_stride = bits_stride;
+  a.bits_w64 = (bits_pages + 63) / 64;
+  a.phase = phase;
   plan_tile_chunks(G, max_rows, &a.iters, &a.max_chunks);
   a.t_per_chunk = a.iters * kTileNW * kTileTW;
   if (lengths != nullptr) {
@@ -2293,4 +2410,20 @@ extern "C" int tw_decode_attention_page_rows(const void* q, const void* k_base, 
                                 cur_v, softmax_scale, nullptr, nullptr, nullptr, 0, 0, nullptr, page_min, page_max,
                                 page_entry_stride, meta_pages, out, workspace, workspace_bytes, stream, page_rows,
                                 packed, qscale, qmin, quant_entry_stride);
+}
+
+extern "C" int tw_decode_attention_pages_bits(const void* q, const void* k_base, const void* v_base, int dtype, int G,
+                                              int R, int D, const uint32_t* sel_bits, int64_t bits_stride, int P,
+                                              int max_rows, int64_t entry_stride_rows, int sink, int recent,
+                                              int block_size, const int32_t* lengths, int length, int append,
+                                              const void* cur_k, const void* cur_v, float softmax_scale,
+                                              void* page_min, void* page_max, int64_t page_entry_stride,
+                                              int meta_pages, void* out, void* workspace, size_t workspace_bytes,
+                                              int phase, void* stream) {
+  if (sel_bits == nullptr) return TW_EINVAL;
+  return tw::pages_tiles_launch(q, k_base, v_base, dtype, G, R, D, nullptr, nullptr, nullptr, 0, max_rows,
+                                entry_stride_rows, sink, recent, block_size, lengths, length, append, cur_k, cur_v,
+                                softmax_scale, nullptr, nullptr, nullptr, 0, 0, nullptr, page_min, page_max,
+                                page_entry_stride, meta_pages, out, workspace, workspace_bytes, stream, nullptr,
+                                nullptr, nullptr, nullptr, 0, sel_bits, bits_stride, P, phase);
 }

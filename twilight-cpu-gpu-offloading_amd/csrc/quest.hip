@@ -447,6 +447,12 @@ struct SelectArgs {
   const int32_t* map;
   const int32_t* widths;
   int keys_max;
+  // Selection bitmaps (nullable): bit p of row (g, r) at bits + (g*R + r) *
+  // bits_stride (32-bit words) is set when head r of group g selected page
+  // p; bits_words words per row are written (2 * ceil(P / 64)).
+  uint32_t* bits;
+  int64_t bits_stride;
+  int bits_words;
 };
 
 template <int NT, typename M>
@@ -748,8 +754,8 @@ __global__ __launch_bounds__(NT) void quest_select_kernel(SelectArgs s) {
   int32_t* ws_row = s.sel_ws != nullptr ? s.sel_ws + static_cast<int64_t>(row) * s.k : nullptr;
   int32_t* out32 = s.sel_out != nullptr ? s.sel_out + static_cast<int64_t>(row) * s.k : nullptr;
   int64_t* out64 = s.sel_out64 != nullptr ? s.sel_out64 + static_cast<int64_t>(row) * s.k : nullptr;
+  uint32_t take = 0u;
   if (k > 0) {
-    uint32_t take;
     int slot;
     block_topk<KPT>(key, n_keys, k, sh, &take, &slot);
     const int i0 = KPT * static_cast<int>(threadIdx.x);
@@ -785,6 +791,19 @@ __global__ __launch_bounds__(NT) void quest_select_kernel(SelectArgs s) {
   for (int slot = k + static_cast<int>(threadIdx.x); slot < s.k; slot += NT) {
     if (out32 != nullptr) out32[slot] = -1;
     if (out64 != nullptr) out64[slot] = -1;
+  }
+  if (s.bits != nullptr) {
+    // Thread t's KPT keys are pages KPT*t .. KPT*t + KPT - 1, so its take
+    // bits are one aligned run of a 32-bit word: the 32 / KPT threads of a
+    // word OR their shifted runs together and the first of them stores it.
+    static_assert(KPT <= 32 && (32 % KPT) == 0, "a thread's run lies in one word");
+    constexpr int kTpw = 32 / KPT;
+    const int t = static_cast<int>(threadIdx.x);
+    uint32_t w = take << ((KPT * t) & 31);
+#pragma unroll
+    for (int o = 1; o < kTpw; o <<= 1) w |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(w), o));
+    const int wi = (KPT * t) >> 5;
+    if ((t % kTpw) == 0 && wi < s.bits_words) s.bits[static_cast<int64_t>(row) * s.bits_stride + wi] = w;
   }
   if (!s.want_union) return;
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.flag)) return;
@@ -1181,6 +1200,47 @@ extern "C" int tw_quest_select_ragged(const float* q, const void* page_min, cons
     rc = tw::prepare_long_rows(s, G * R, true, w.long_rows, st);
     if (rc != TW_OK) return rc;
   }
+  return tw::launch_select(s, G * R, true, st);
+}
+
+extern "C" int tw_quest_select_bits(const float* q, const void* page_min, const void* page_max, int dtype, int G,
+                                    int R, int P, int D, int64_t page_group_stride, const int32_t* lengths, int k,
+                                    float* scores, int32_t* sel_pages, uint32_t* sel_bits, int64_t bits_stride,
+                                    int sink, int recent, int block_size, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  if (!tw::check_score_args(q, page_min, page_max, G, R, P, D, page_group_stride)) return TW_EINVAL;
+  if (k <= 0 || k > P || sel_bits == nullptr) return TW_EINVAL;
+  if (P > tw::kMaxSelPages) return TW_EUNSUPPORTED;  // long rows select through the segment pass and a plan
+  const int words = 2 * ((P + 63) / 64);
+  if (bits_stride < words || (bits_stride % 2) != 0 || (reinterpret_cast<uintptr_t>(sel_bits) % 8) != 0)
+    return TW_EINVAL;
+  if (lengths != nullptr && (sink < 0 || recent <= 0 || block_size <= 0)) return TW_EINVAL;
+  if (workspace == nullptr || workspace_bytes < tw_quest_select_workspace_size(G, R, P)) return TW_ENOMEM;
+  const tw::SelectWorkspace w = tw::carve(workspace, G, R, P);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  tw::ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P, D, w.scores, tw::padded(P), scores,
+                  lengths, sink, recent, block_size};
+  tw::SelectArgs s{};
+  s.scores = w.scores;
+  s.score_stride = tw::padded(P);
+  s.vec_last4 = static_cast<int>(tw::padded(P)) - 4;
+  s.G = G;
+  s.R = R;
+  s.P = P;
+  s.k = k;
+  s.sel_out = sel_pages;
+  s.want_union = false;
+  s.sink = sink;
+  s.recent = recent;
+  s.bs = block_size;
+  s.append_position = -1;
+  s.counters = w.counters;
+  s.lengths = lengths;
+  s.bits = sel_bits;
+  s.bits_stride = bits_stride;
+  s.bits_words = words;
+  const int rc = tw::dispatch_score(dtype, a, st);
+  if (rc != TW_OK) return rc;
   return tw::launch_select(s, G * R, true, st);
 }
 

@@ -45,6 +45,10 @@ _HIP_SIGNATURES = {
                                              vp, i64, vp]),
     "tw_quest_select_ragged": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, i32, vp, vp, vp, vp, i64, i32, i32,
                                      i32, vp, szt, vp]),
+    "tw_quest_select_bits": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, i32, vp, vp, vp, i64, i32, i32, i32,
+                                   vp, szt, vp]),
+    "tw_decode_attention_pages_bits": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32, i64, i32, i32, i32,
+                                             vp, i32, i32, vp, vp, f32, vp, vp, i64, i32, vp, vp, szt, i32, vp]),
     "tw_decode_attention_pages_ragged": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32,
                                                i32, vp, i32, vp, vp, f32, vp, vp, i64, i32, vp, vp, szt, vp]),
     "tw_decode_attention_pages_resident": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32,

@@ -475,6 +475,58 @@ def quest_select_ragged(
                                            ptr(ws), ws.numel(), stream_handle(dev)), "quest_select_ragged")
 
 
+def sel_bits_words(P: int) -> int:
+    """32-bit words of one selection-bitmap row over P pages (whole 64-bit
+    words)."""
+    return 2 * ((P + 63) // 64)
+
+
+def quest_select_bits(
+    q: torch.Tensor,
+    page_min: torch.Tensor,
+    page_max: torch.Tensor,
+    k: int,
+    sel_bits: torch.Tensor,
+    *,
+    lengths: Optional[torch.Tensor] = None,
+    scores: Optional[torch.Tensor] = None,
+    sel_pages: Optional[torch.Tensor] = None,
+    sink: int = 0,
+    recent: int = 1,
+    block_size: int = 1,
+) -> None:
+    """Quest score + top-k with each head's selection written as a page
+    bitmap (two launches, no union plan): bit p of sel_bits[g, r] (int32
+    words, [G, R, >= sel_bits_words(P)]) is set when head r of group g chose
+    page p.  lengths ([G] int32, device, optional) selects per group as
+    quest_select_ragged.  P <= 8192."""
+    _check_score_inputs(q, page_min, page_max, "quest_select_bits")
+    dev = _require_device(q, page_min, page_max, lengths, scores, sel_pages, sel_bits, what="quest_select_bits")
+    G, R, D = q.shape
+    P = page_min.shape[1]
+    if not 1 <= k <= P:
+        raise ValueError("k must be in [1, P]")
+    if P > 8192:
+        raise ValueError("quest_select_bits takes at most 8192 pages (use quest_select)")
+    if sel_bits.dtype != torch.int32 or sel_bits.ndim != 3 or tuple(sel_bits.shape[:2]) != (G, R) \
+            or sel_bits.shape[2] < sel_bits_words(P) or sel_bits.stride(2) != 1 \
+            or sel_bits.stride(0) != R * sel_bits.stride(1) or sel_bits.stride(1) % 2 or sel_bits.data_ptr() % 8:
+        raise ValueError("sel_bits must be [G, R, >= sel_bits_words(P)] int32 with 8-byte aligned rows")
+    for t, dt, shape in ((scores, torch.float32, (G, R, P)), (sel_pages, torch.int32, (G, R, k))):
+        if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
+            raise ValueError("quest_select_bits output has the wrong dtype/shape")
+    if lengths is not None and (lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,)
+                                or not lengths.is_contiguous()):
+        raise ValueError("lengths must be contiguous [G] int32")
+    nbytes = hip().tw_quest_select_workspace_size(G, R, P)
+    ws = WORKSPACE.get(dev, "quest_select", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_quest_select_bits(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
+                                         page_min.stride(0), ptr(lengths), k, ptr(scores), ptr(sel_pages),
+                                         ptr(sel_bits), sel_bits.stride(1), sink, recent, block_size, ptr(ws),
+                                         ws.numel(), stream_handle(dev)), "quest_select_bits")
+
+
 # ---------------------------------------------------------------- Twilight
 def twilight_qk(
     q: torch.Tensor,
@@ -1026,6 +1078,81 @@ def decode_attention_pages_ragged(
                                                      ptr(lengths), int(bool(append)), ptr(cur_k), ptr(cur_v), scale,
                                                      *meta, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
               "decode_attention_pages_ragged")
+    return out
+
+
+def decode_attention_pages_bits(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    sel_bits: torch.Tensor,
+    P: int,
+    *,
+    max_pages: int,
+    sink: int,
+    recent: int,
+    block_size: int = 16,
+    lengths: Optional[torch.Tensor] = None,
+    length: int = 0,
+    append: bool = True,
+    cur_k: Optional[torch.Tensor] = None,
+    cur_v: Optional[torch.Tensor] = None,
+    softmax_scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+    page_min: Optional[torch.Tensor] = None,
+    page_max: Optional[torch.Tensor] = None,
+    phase: int = 3,
+) -> torch.Tensor:
+    """decode_attention_pages(_ragged) with the union taken from the
+    selection bitmaps of quest_select_bits ([G, R, words] int32 over P
+    pages): the same tiles, in the same order, as the union plan gives.
+    lengths ([G] int32, device) or length; the decode token is cur_k/cur_v
+    (appended at the group's length when `append`).  max_pages bounds the
+    union (R * k).  16-bit K/V, D = 128, block_size 16.  Returns [G, R, D]."""
+    if phase not in (1, 2, 3):
+        raise ValueError("phase must be 1, 2 or 3")
+    if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("q must be [G, R, D] fp16/bf16")
+    G, R, D = q.shape
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or k_cache.shape != v_cache.shape \
+            or k_cache.ndim != 3 or k_cache.shape[0] != G or k_cache.shape[2] != D \
+            or k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1 or k_cache.stride(1) != D \
+            or k_cache.stride(0) % D:
+        raise ValueError("K/V cache must be row-contiguous [G, Lmax, D] in q's dtype")
+    if not 1 <= P <= 8192:
+        raise ValueError("P must be in [1, 8192]")
+    if sel_bits.dtype != torch.int32 or sel_bits.ndim != 3 or tuple(sel_bits.shape[:2]) != (G, R) \
+            or sel_bits.shape[2] < sel_bits_words(P) or sel_bits.stride(2) != 1 \
+            or sel_bits.stride(0) != R * sel_bits.stride(1) or sel_bits.stride(1) % 2 or sel_bits.data_ptr() % 8:
+        raise ValueError("sel_bits must be [G, R, >= sel_bits_words(P)] int32 with 8-byte aligned rows")
+    if lengths is not None and (lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,)
+                                or not lengths.is_contiguous()):
+        raise ValueError("lengths must be contiguous [G] int32")
+    if (cur_k is None) != (cur_v is None):
+        raise ValueError("cur_k and cur_v go together")
+    if cur_k is not None and (cur_k.shape != (G, D) or cur_k.dtype != q.dtype or cur_v.shape != cur_k.shape
+                              or cur_v.dtype != q.dtype):
+        raise ValueError("cur_k/cur_v must be [G, D] in q's dtype")
+    if lengths is None and not 0 <= length < k_cache.shape[1]:
+        raise ValueError("length outside the cache")
+    dev = _require_device(q, sel_bits, lengths, cur_k, cur_v, page_min, page_max,
+                          what="decode_attention_pages_bits")
+    meta = _page_meta_args(page_min, page_max, G, D, append)
+    kp, vp = _slab_source(k_cache, v_cache)
+    _require_contiguous(q, cur_k, cur_v, what="decode_attention_pages_bits")
+    if out is None:
+        out = torch.empty_like(q)
+    scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    max_rows = sink + max(0, max_pages) * block_size + recent
+    nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
+    ws = WORKSPACE.get(dev, "decode_attention", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_decode_attention_pages_bits(ptr(q), kp, vp, _dt(q), G, R, D, ptr(sel_bits),
+                                                   sel_bits.stride(1), P, max_rows, k_cache.stride(0) // D, sink,
+                                                   recent, block_size, ptr(lengths), int(length),
+                                                   int(bool(append)), ptr(cur_k), ptr(cur_v), scale, *meta,
+                                                   ptr(out), ptr(ws), ws.numel(), int(phase), stream_handle(dev)),
+              "decode_attention_pages_bits")
     return out
 
 
