@@ -215,3 +215,57 @@ def test_decode_attention_pages_bits_equals_plan(K, dev, label, dtype, R, length
     got = outs[1].float().numpy().astype(np.float64)
     err = np.abs(got - ref)
     assert np.all(err <= 2e-3 + 1e-2 * np.abs(ref)), f"max abs err {err.max():.3e}"
+
+
+def _crafted_metadata(kind: str, G: int, P: int, dtype: str):
+    """Page min/max whose scores defeat the top-k's one-pass fast path:
+    hundreds of tied top scores, a NaN score, one flat row, or a few
+    distinct values (boundary bins far fuller than 64 keys)."""
+    lo = randn((G, P, D), dtype, seed=231)
+    hi = randn((G, P, D), dtype, seed=232)
+    pmin, pmax = torch.minimum(lo, hi), torch.maximum(lo, hi)
+    if kind == "ties":
+        # 300 copies of one strong page: the 128 best scores are all equal
+        pmin[:, 5:305] = pmin[:, 4:5] * 4
+        pmax[:, 5:305] = pmax[:, 4:5] * 4
+    elif kind == "nan":
+        pmax[:, 17, 3] = float("nan")
+    elif kind == "flat":
+        pmin[:] = pmin[:, :1]
+        pmax[:] = pmax[:, :1]
+    elif kind == "few":
+        pmin[:, :] = pmin[:, torch.arange(P) % 5]
+        pmax[:, :] = pmax[:, torch.arange(P) % 5]
+    return pmin.contiguous(), pmax.contiguous()
+
+
+@pytest.mark.parametrize("kind", ["ties", "nan", "flat", "few"])
+def test_quest_select_fast_path_fallbacks(K, dev, kind):
+    """Rows whose first histogram pass cannot finish the selection still
+    select the oracle's pages (ties to the lowest page, NaN highest), through
+    quest_select_bits and through quest_select's plan path."""
+    _say(f"[select fallbacks] {kind}")
+    G, R, P, k, dtype = 2, 4, 2028, 128, "f16"
+    pmin, pmax = _crafted_metadata(kind, G, P, dtype)
+    q = randn((G, R, D), "f32", seed=233)
+    bits = _bits_tensor(K, G, R, P, dev)
+    sel_b = torch.empty((G, R, k), dtype=torch.int32, device=dev)
+    sel_p = torch.empty_like(sel_b)
+    pp = torch.empty((G, min(P, R * k)), dtype=torch.int32, device=dev)
+    pc = torch.empty((G,), dtype=torch.int32, device=dev)
+    qd, dmin, dmax = q.to(dev), pmin.to(dev), pmax.to(dev)
+    K.quest_select_bits(qd, dmin, dmax, k, bits, sel_pages=sel_b)
+    K.quest_select(qd, dmin, dmax, k, sel_pages=sel_p, plan_pages=pp, plan_counts=pc)
+    torch.cuda.synchronize()
+    rows = _bit_rows(bits, P)
+    sc = oracle.quest_score(q.numpy(), to_bits(pmin), to_bits(pmax), dtype)
+    for g in range(G):
+        want = oracle.topk_sorted(sc[g], k)
+        assert np.array_equal(sel_b[g].cpu().numpy(), want), g
+        assert np.array_equal(sel_p[g].cpu().numpy(), want), g
+        for r in range(R):
+            expect = np.zeros(P, bool)
+            expect[want[r]] = True
+            assert np.array_equal(rows[g, r], expect), (g, r)
+        union = np.unique(want)
+        assert int(pc[g]) == union.shape[0] and np.array_equal(pp[g, :union.shape[0]].cpu().numpy(), union), g

@@ -1329,7 +1329,17 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       pr[tt] = a.page_rows != nullptr ? a.page_rows[plan_base + u] : 0xffffu;
     }
   };
+  uint4 qf[4];
+  {
+    const S* qh = static_cast<const S*>(a.q) + (static_cast<int64_t>(g) * R + (krow < R ? krow : 0)) * D + 8 * quarter;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint4 t = *reinterpret_cast<const uint4*>(qh + 32 * s);
+      qf[s] = krow < R ? t : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
   // bitmap mode: every head's words of this lane, their OR and the prefix
+  // (the query loads above are already in flight)
   constexpr int kNwl = NWL > 0 ? NWL : 1;
   uint64_t hw[RMAX][kNwl], uw[kNwl];
   int b_cnt = 0, b_incl = 0;
@@ -1340,11 +1350,14 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       const int wi = NWL * lane + w;
       const int wc = wi < a.bits_w64 ? wi : a.bits_w64 - 1;
       uw[w] = 0ull;
+      // Slots h >= R repeat row R - 1: the OR is unchanged and their mask
+      // bits are never read.  No uniform condition guards a load, so the
+      // compiler cannot sink them into branches that wait one by one.
 #pragma unroll
       for (int h = 0; h < RMAX; ++h) {
         const int hc = h < R ? h : R - 1;
         const uint64_t v = *reinterpret_cast<const uint64_t*>(brow + hc * a.bits_stride + 2 * wc);
-        hw[h][w] = (h < R && wi < a.bits_w64) ? v : 0ull;
+        hw[h][w] = wi < a.bits_w64 ? v : 0ull;
         uw[w] |= hw[h][w];
       }
       b_cnt += __popcll(uw[w]);
@@ -1352,15 +1365,6 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     b_incl = wave_prefix_sum_i32(b_cnt);
   } else {
     load_slots((chunk * a.iters * NW + wave) * TW, page, pmask, prow);
-  }
-  uint4 qf[4];
-  {
-    const S* qh = static_cast<const S*>(a.q) + (static_cast<int64_t>(g) * R + (krow < R ? krow : 0)) * D + 8 * quarter;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const uint4 t = *reinterpret_cast<const uint4*>(qh + 32 * s);
-      qf[s] = krow < R ? t : make_uint4(0u, 0u, 0u, 0u);
-    }
   }
   const TileWin win = tile_window(a, g);
   int nu;

@@ -127,6 +127,9 @@ struct ScoreArgs {
   // Ragged groups (nullable): group g scores ragged_pages(lengths[g]) <= P pages.
   const int32_t* lengths;
   int sink, recent, bs;
+  // Per-tile key range (nullable): tile_mm[(g*R + r) * tiles + tile] =
+  // (max, min) of score_key over the tile's scored pages, for the top-k.
+  uint2* tile_mm;
 };
 
 
@@ -201,6 +204,16 @@ __device__ __forceinline__ void stage_tile(const ScoreArgs& a, int g, int p0, in
       reinterpret_cast<uint32_t*>(lds + (which * kTilePages + page) * pitch)[w] = v;
     }
   }
+}
+
+// The (max, min) score key of one head's pages in a tile (lane = page, ok:
+// the page is scored), stored for the selection's first histogram pass.
+__device__ __forceinline__ void tile_key_range(const ScoreArgs& a, int64_t row, int p0, bool ok, float sc) {
+  const uint32_t key = score_key(sc);
+  const uint32_t kmax = wave_max_u32(ok ? key : 0u);
+  const uint32_t kmin = wave_min_u32(ok ? key : 0xffffffffu);
+  const int tiles = (a.P + kTilePages - 1) / kTilePages;
+  if (lane_id() == 0) a.tile_mm[row * tiles + p0 / kTilePages] = make_uint2(kmax, kmin);
 }
 
 // Scores of one tile for D = DFIX and at most 4 heads, in two phases:
@@ -305,11 +318,14 @@ __device__ void score_tile_split(const ScoreArgs& a, int g, int p0, int np_cap, 
   __shared__ float s_half[4][kWave];
   if (half == 1) s_half[r][lane] = acc[0];
   __syncthreads();
-  if (half == 0 && active && lane < np) {
+  if (half == 0 && active) {
     const float sc = acc[0] + s_half[r][lane];
     const int64_t row = static_cast<int64_t>(g) * a.R + r;
-    a.scores[row * a.score_stride + p0 + lane] = sc;
-    if (a.scores_out != nullptr) a.scores_out[row * a.P + p0 + lane] = sc;
+    if (lane < np) {
+      a.scores[row * a.score_stride + p0 + lane] = sc;
+      if (a.scores_out != nullptr) a.scores_out[row * a.P + p0 + lane] = sc;
+    }
+    if (a.tile_mm != nullptr) tile_key_range(a, row, p0, lane < np, sc);
   }
 }
 
@@ -400,11 +416,14 @@ __device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
     }
     if (half == 1) s_half[hw][lane] = part;
     __syncthreads();
-    if (half == 0 && r < a.R && lane < np) {
+    if (half == 0 && r < a.R) {
       const float sc = part + s_half[hw][lane];
       const int64_t row = static_cast<int64_t>(g) * a.R + r;
-      a.scores[row * a.score_stride + p0 + lane] = sc;
-      if (a.scores_out != nullptr) a.scores_out[row * a.P + p0 + lane] = sc;
+      if (lane < np) {
+        a.scores[row * a.score_stride + p0 + lane] = sc;
+        if (a.scores_out != nullptr) a.scores_out[row * a.P + p0 + lane] = sc;
+      }
+      if (a.tile_mm != nullptr) tile_key_range(a, row, p0, lane < np, sc);
     }
     __syncthreads();
   }
@@ -453,6 +472,9 @@ struct SelectArgs {
   uint32_t* bits;
   int64_t bits_stride;
   int bits_words;
+  // Per-tile key ranges from the score kernel (nullable; rows of
+  // ceil(P / 64) tiles): the top-k takes its one-pass fast path.
+  const uint2* tile_mm;
 };
 
 template <int NT, typename M>
@@ -704,6 +726,13 @@ __global__ __launch_bounds__(NT) void quest_select_kernel(SelectArgs s) {
   extern __shared__ __align__(16) uint8_t dyn[];  // union scratch
   const int row = blockIdx.x;
   const int g = row / s.R;
+  // the fast top-k's histogram is cleared before the first load goes out, so
+  // its barrier does not wait for the loads
+  const bool fast = s.tile_mm != nullptr && s.map == nullptr;
+  if (fast) {
+    topk_fast_clear(sh);
+    __syncthreads();
+  }
   // unconditional length load (the first score word when not ragged; relaxed
   // atomic so that it is not sunk into a branch), overlapping the key loads
   const int length = fetch_i32(s.lengths != nullptr ? s.lengths + g : reinterpret_cast<const int32_t*>(s.scores));
@@ -747,6 +776,16 @@ __global__ __launch_bounds__(NT) void quest_select_kernel(SelectArgs s) {
       }
     }
   }
+  // the row's per-tile key ranges ride in the same round trip (two tiles a
+  // lane: rows of at most 128 tiles)
+  uint2 tr0 = make_uint2(0u, 0u), tr1 = make_uint2(0u, 0u);
+  const int tiles = (s.P + 63) / 64;
+  if (fast) {
+    const uint2* tm = s.tile_mm + static_cast<int64_t>(row) * tiles;
+    const int l = lane_id();
+    tr0 = tm[l < tiles ? l : tiles - 1];
+    tr1 = tm[l + kWave < tiles ? l + kWave : tiles - 1];
+  }
   const int P = s.lengths != nullptr ? ragged_pages(length, s.sink, s.recent, s.bs, s.P) : s.P;
   const int n_keys = s.widths != nullptr ? fetch_i32(s.widths + row) : P;  // compacted long rows
   const int k = s.k < n_keys ? s.k : n_keys;
@@ -755,12 +794,28 @@ __global__ __launch_bounds__(NT) void quest_select_kernel(SelectArgs s) {
   int32_t* out32 = s.sel_out != nullptr ? s.sel_out + static_cast<int64_t>(row) * s.k : nullptr;
   int64_t* out64 = s.sel_out64 != nullptr ? s.sel_out64 + static_cast<int64_t>(row) * s.k : nullptr;
   uint32_t take = 0u;
+  const bool want_list = ws_row != nullptr || out32 != nullptr || out64 != nullptr;
   if (k > 0) {
-    int slot;
-    block_topk<KPT>(key, n_keys, k, sh, &take, &slot);
+    int slot = 0;
+    bool done = false;
+    if (fast) {
+      // key range of the row's scored tiles
+      const int tg = (n_keys + 63) / 64;
+      const int l = lane_id();
+      const uint32_t kmax = wave_max_u32(max(l < tg ? tr0.x : 0u, l + kWave < tg ? tr1.x : 0u));
+      const uint32_t kmin = wave_min_u32(min(l < tg ? tr0.y : 0xffffffffu, l + kWave < tg ? tr1.y : 0xffffffffu));
+      done = block_topk_fast<KPT>(key, n_keys, k, kmin, kmax, sh, &take);
+      if (done && want_list) {
+        int total;
+        slot = block_excl_scan<NT>(__popc(take), sh.scan, &total);
+      }
+    }
+    if (!done) block_topk<KPT>(key, n_keys, k, sh, &take, &slot);
     const int i0 = KPT * static_cast<int>(threadIdx.x);
     constexpr int kStage = kLinBins + 64;
-    if (k <= kStage) {
+    if (!want_list) {
+      // bitmaps only
+    } else if (k <= kStage) {
       // the selection goes through LDS (the histogram is free now) and out
       // with coalesced stores
       int32_t* st = reinterpret_cast<int32_t*>(sh.hist);
@@ -989,6 +1044,9 @@ bool check_score_args(const float* q, const void* pmin, const void* pmax, int G,
 }
 
 int64_t padded(int P) { return (static_cast<int64_t>(P) + 3) & ~static_cast<int64_t>(3); }
+size_t tile_range_bytes(int G, int R, int P) {
+  return align256(static_cast<size_t>(G) * R * ((P + kTilePages - 1) / kTilePages) * sizeof(uint2));
+}
 size_t counter_bytes(int G) { return ((static_cast<size_t>(G) * 4 + 255) / 256) * 256; }
 
 }  // namespace
@@ -1042,10 +1100,11 @@ extern "C" int tw_topk_sorted(const float* scores, int rows, int P, int64_t scor
 
 extern "C" size_t tw_quest_select_workspace_size(int G, int R, int P) {
   // arrival counters | scores [G][R][P rounded up to 4] | selections [G][R][<= P]
-  // | (P > 8192) the segment pass's compacted rows
+  // | per-tile key ranges [G][R][ceil(P / 64)] | (P > 8192) the segment
+  // pass's compacted rows
   if (G <= 0 || R <= 0 || P <= 0) return 0;
   return tw::counter_bytes(G) + tw::align256(static_cast<size_t>(G) * R * tw::padded(P) * sizeof(float)) +
-         tw::align256(static_cast<size_t>(G) * R * P * sizeof(int32_t)) +
+         tw::align256(static_cast<size_t>(G) * R * P * sizeof(int32_t)) + tw::tile_range_bytes(G, R, P) +
          tw::long_row_bytes(static_cast<int64_t>(G) * R, P);
 }
 
@@ -1056,6 +1115,7 @@ struct SelectWorkspace {
   unsigned int* counters;
   float* scores;
   int32_t* sel;
+  uint2* tile_mm;
   uint8_t* long_rows;
 };
 SelectWorkspace carve(void* workspace, int G, int R, int P) {
@@ -1067,6 +1127,8 @@ SelectWorkspace carve(void* workspace, int G, int R, int P) {
   ws += align256(static_cast<size_t>(G) * R * padded(P) * sizeof(float));
   w.sel = reinterpret_cast<int32_t*>(ws);
   ws += align256(static_cast<size_t>(G) * R * P * sizeof(int32_t));
+  w.tile_mm = reinterpret_cast<uint2*>(ws);
+  ws += tile_range_bytes(G, R, P);
   w.long_rows = ws;
   return w;
 }
@@ -1138,6 +1200,8 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
   s.length = length;
   s.append_position = append_position;
   s.counters = counters;
+  a.tile_mm = w.tile_mm;
+  s.tile_mm = w.tile_mm;
   int rc = tw::dispatch_score(dtype, a, st);
   if (rc != TW_OK) return rc;
   if (P > tw::kMaxSelPages) {
@@ -1194,6 +1258,8 @@ extern "C" int tw_quest_select_ragged(const float* q, const void* page_min, cons
   s.append_position = -1;
   s.counters = counters;
   s.lengths = lengths;
+  a.tile_mm = w.tile_mm;
+  s.tile_mm = w.tile_mm;
   int rc = tw::dispatch_score(dtype, a, st);
   if (rc != TW_OK) return rc;
   if (P_max > tw::kMaxSelPages) {
@@ -1239,6 +1305,8 @@ extern "C" int tw_quest_select_bits(const float* q, const void* page_min, const 
   s.bits = sel_bits;
   s.bits_stride = bits_stride;
   s.bits_words = words;
+  a.tile_mm = w.tile_mm;
+  s.tile_mm = w.tile_mm;
   const int rc = tw::dispatch_score(dtype, a, st);
   if (rc != TW_OK) return rc;
   return tw::launch_select(s, G * R, true, st);

@@ -23,6 +23,9 @@ constexpr int kWaves = kBlock / kWave;
 constexpr int kMaxSelPages = 8192;  // longest row
 constexpr int kLinBins = 2048;
 constexpr int kExactMax = 256;      // at most this many candidates are ranked pairwise
+// Bins of the fast path's single pass: 8 per lane keep each wavefront's
+// in-lane boundary search short; the boundary bin then holds a few keys.
+constexpr int kFastBins = 512;
 
 // Block-shared state of a selection block of NT threads (NT a multiple of
 // 256: the linear bins split evenly over the threads).
@@ -42,6 +45,8 @@ struct SelSharedT {
   uint32_t bnd_above;
   uint32_t bnd_count;
   int flag;
+  uint2 cpair[kWave];  // fast path: boundary candidates (key, index)
+  uint32_t ncand;      // fast path: staging slots handed out
 };
 using SelShared = SelSharedT<kBlock>;
 
@@ -308,6 +313,138 @@ __device__ void block_topk(const uint32_t (&key)[KPT], int P, int k, SelSharedT<
   }
   *take = taken;
   *first = out;
+}
+
+// Clears the fast path's histogram and staging counter.  The caller puts a
+// barrier between this and block_topk_fast (at kernel entry, ahead of the
+// key loads, so the barrier does not wait for them).
+template <int NT>
+__device__ __forceinline__ void topk_fast_clear(SelSharedT<NT>& sh) {
+  uint4* hist4 = reinterpret_cast<uint4*>(sh.hist);
+  for (int b = threadIdx.x; b < kFastBins / 4; b += NT) hist4[b] = make_uint4(0u, 0u, 0u, 0u);
+  if (threadIdx.x == 0) sh.ncand = 0u;
+}
+
+// Fast path of block_topk for a row whose key range [kmin, kmax] is known
+// before the keys are looked at (the score kernel reduces it per tile).  One
+// pass of kFastBins bins linear in the value over that range (histogram cleared
+// by topk_fast_clear), every wavefront then scans the bins itself (8 per
+// lane, a wavefront suffix sum, no barrier) and finds the bin holding the
+// k-th largest; at most 64 keys of that bin are staged through an LDS slot
+// counter and every wavefront ranks them by (key desc, index asc) with
+// readlane, four at a time.  Two barriers after the clear.  Returns false --
+// block-uniformly, the caller then runs block_topk -- when the range is not
+// finite and positive or the boundary bin holds more than 64 keys.  On true,
+// bit j of *take marks index KPT*t + j as selected: the same set block_topk
+// selects.
+template <int KPT, int NT>
+__device__ bool block_topk_fast(const uint32_t (&key)[KPT], int P, int k, uint32_t kmin, uint32_t kmax,
+                                SelSharedT<NT>& sh, uint32_t* take) {
+  constexpr int kBins = kFastBins;
+  constexpr int kBpl = kBins / kWave;  // bins per lane
+  static_assert(kBpl % 4 == 0, "16-byte bin reads");
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int i0 = KPT * tid;
+  if (k >= P) {
+    uint32_t t = 0u;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) t |= (i0 + j < P) ? (1u << j) : 0u;
+    *take = t;
+    return true;
+  }
+  const float vmin = key_value(kmin);
+  const float vmax = key_value(kmax);
+  const float range = vmax - vmin;
+  const float scale = static_cast<float>(kBins) / range;
+  if (!(__builtin_isfinite(vmin) && __builtin_isfinite(vmax) && __builtin_isfinite(range) && range > 0.0f &&
+        __builtin_isfinite(scale)))
+    return false;
+  int bin[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int b = static_cast<int>((key_value(key[j]) - vmin) * scale);
+    bin[j] = (i0 + j < P) ? (b < kBins - 1 ? b : kBins - 1) : -1;
+    if (bin[j] >= 0) atomicAdd(&sh.hist[bin[j]], 1u);
+  }
+  __syncthreads();
+  // lane l: bins kBpl*l ..; the suffix over lanes counts the bins above
+  const uint4* hist4 = reinterpret_cast<const uint4*>(sh.hist);
+  uint32_t hv[kBpl];
+#pragma unroll
+  for (int q = 0; q < kBpl / 4; ++q) {
+    const uint4 h = hist4[kBpl / 4 * lane + q];
+    hv[4 * q] = h.x;
+    hv[4 * q + 1] = h.y;
+    hv[4 * q + 2] = h.z;
+    hv[4 * q + 3] = h.w;
+  }
+  uint32_t tot = 0u;
+#pragma unroll
+  for (int b = 0; b < kBpl; ++b) tot += hv[b];
+  const uint32_t incl = wave_suffix_sum_u32(tot);
+  const uint32_t need = static_cast<uint32_t>(k);
+  // lanes 0 .. L have incl >= need (incl does not grow with the lane)
+  const uint64_t bl = __ballot(incl >= need);
+  const int L = 63 - __clzll(static_cast<long long>(bl));
+  uint32_t acc = incl - tot;
+  int bsel = 0;
+  uint32_t cnt = 0u;
+  bool found = false;
+#pragma unroll
+  for (int b = kBpl - 1; b >= 0; --b) {
+    const bool hit = !found && need <= acc + hv[b];
+    bsel = hit ? b : bsel;
+    cnt = hit ? hv[b] : cnt;
+    acc += (found || hit) ? 0u : hv[b];
+    found = found || hit;
+  }
+  const int bnd = kBpl * L + static_cast<int>(readlane_u32(static_cast<uint32_t>(bsel), L));
+  const uint32_t above = readlane_u32(acc, L);
+  const uint32_t ccount = readlane_u32(cnt, L);
+  if (ccount > static_cast<uint32_t>(kWave)) {
+    __syncthreads();  // every wavefront is done with the bins before block_topk reuses them
+    return false;
+  }
+  const uint32_t need2 = need - above;  // 1 .. ccount
+  uint32_t t = 0u;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) t |= (bin[j] > bnd) ? (1u << j) : 0u;
+  if (need2 == ccount) {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) t |= (bin[j] == bnd) ? (1u << j) : 0u;
+    *take = t;
+    return true;
+  }
+  uint32_t cslot[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    cslot[j] = 0u;
+    if (bin[j] == bnd) {
+      cslot[j] = atomicAdd(&sh.ncand, 1u);
+      sh.cpair[cslot[j]] = make_uint2(key[j], static_cast<uint32_t>(i0 + j));
+    }
+  }
+  __syncthreads();
+  // every wavefront ranks the staged candidates (lane m holds candidate m)
+  // with readlane, so no barrier hands the ranks back; slots past ccount
+  // hold (0, ~0u), which never outranks a candidate
+  const uint2 c = static_cast<uint32_t>(lane) < ccount ? sh.cpair[lane] : make_uint2(0u, 0xffffffffu);
+  uint32_t rank = 0u;
+  const int n4 = (static_cast<int>(ccount) + 3) & ~3;
+  for (int m = 0; m < n4; m += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t km = readlane_u32(c.x, m + u);
+      const uint32_t im = readlane_u32(c.y, m + u);
+      rank += (km > c.x || (km == c.x && im < c.y)) ? 1u : 0u;
+    }
+  }
+  const uint64_t tm = __ballot(static_cast<uint32_t>(lane) < ccount && rank < need2);
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) t |= (bin[j] == bnd && ((tm >> cslot[j]) & 1ull)) ? (1u << j) : 0u;
+  *take = t;
+  return true;
 }
 
 // Candidate pages of a group with `length` tokens: the whole pages between

@@ -169,6 +169,13 @@ class GraphDecoder:
                       torch.zeros((self.G, self.width), dtype=torch.uint8, device=dev),
                       torch.zeros((self.G,), dtype=torch.int32, device=dev)) for _ in self.layers]
         self.attn = [torch.empty((self.G, self.R, self.D), dtype=cache.dtype, device=dev) for _ in self.layers]
+        # sparse Quest over an HBM or host slab (no resident page cache): each
+        # head's selection as a page bitmap, ranked by the attention
+        self.use_bits = (not self.twilight and not self.dense and not cache.previous_token_resident_cache
+                         and self.P <= 8192 and self.R <= 8)
+        if self.use_bits:
+            self.bits = torch.zeros((len(self.layers), self.G, self.R, kernels.sel_bits_words(self.P)),
+                                    dtype=torch.int32, device=dev)
         if self.dense:
             self.dense_pages = torch.arange(self.width, dtype=torch.int32, device=dev).expand(self.G, -1).contiguous()
             self.dense_masks = torch.full((self.G, self.width), (1 << self.R) - 1, dtype=torch.uint8, device=dev)
@@ -250,7 +257,18 @@ class GraphDecoder:
                     kernels.silu_mul(gu, self.m)
                 delta = kernels.gemv(self.m, layer.mlp.down_proj.weight, layer.mlp.down_proj.bias, self.dn)
                 continue
-            if self.dense:
+            if self.use_bits:
+                bits = self.bits[li]
+                kernels.quest_select_bits(self.q32.view(G, R, D), c._page_min[e0:e0 + G, :self.P],
+                                          c._page_max[e0:e0 + G, :self.P], self.k, bits, lengths=self.lengths,
+                                          sink=c.sink_tokens, recent=c.recent_tokens, block_size=c.block_size)
+                meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G]) if self.fuse else {}
+                kernels.decode_attention_pages_bits(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], bits,
+                                                    self.P, max_pages=self.width, sink=c.sink_tokens,
+                                                    recent=c.recent_tokens, block_size=c.block_size,
+                                                    lengths=self.lengths, append=True, cur_k=k, cur_v=v,
+                                                    softmax_scale=float(attn.scaling), out=self.attn[li], **meta)
+            elif self.dense:
                 pp, pm, pc = self.dense_pages, self.dense_masks, self.dense_counts
                 meta = {}
             else:
@@ -260,7 +278,9 @@ class GraphDecoder:
                                             plan_pages=pp, plan_masks=pm, plan_counts=pc)
                 # the attention also appends the decode token and, when it completes a page, that page's min/max
                 meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G]) if self.fuse else {}
-            if c.previous_token_resident_cache:
+            if self.use_bits:
+                pass
+            elif c.previous_token_resident_cache:
                 kernels.decode_attention_pages_resident(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], pp,
                                                         pc, c.resident_pages().view(e0, G), lengths=self.lengths,
                                                         plan_masks=pm, max_pages=self.width, sink=c.sink_tokens,

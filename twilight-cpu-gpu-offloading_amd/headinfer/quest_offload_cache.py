@@ -762,6 +762,21 @@ class QuestTopKOffloadedCache(_CacheBase):
         G, R, _ = queries.shape
         entries = list(range(e0, e0 + G))
         width = max(1, min(cand, R * k))
+        if k > 0 and cand <= 8192 and not self.previous_token_resident_cache:
+            # each head's selection as a page bitmap, ranked by the attention
+            # (no union plan to build between the two launches)
+            bits = torch.empty((G, R, kernels.sel_bits_words(cand)), dtype=torch.int32, device=self.device)
+            start = self._phase_start()
+            pmin, pmax = self._metadata(entries, cand)
+            kernels.quest_select_bits(queries.float().contiguous(), pmin, pmax, k, bits)
+            self._phase_end("selector", start)
+            start = self._phase_start()
+            result = kernels.decode_attention_pages_bits(
+                queries.contiguous(), slab_k, slab_v, bits, cand, max_pages=width, sink=self.sink_tokens,
+                recent=self.recent_tokens, block_size=self.block_size, length=old_length, append=True,
+                cur_k=key_states.contiguous(), cur_v=value_states.contiguous(), softmax_scale=softmax_scale, out=out)
+            self._phase_end("attention", start)
+            return result
         plan_pages = torch.empty((G, width), dtype=torch.int32, device=self.device)
         plan_masks = torch.empty((G, width), dtype=torch.uint8, device=self.device)
         plan_counts = torch.zeros((G,), dtype=torch.int32, device=self.device)
