@@ -66,6 +66,9 @@ def parse_args(argv=None):
     ap.add_argument("--budget-mode", choices=("dynamic", "matched"), default="dynamic",
                     help="Twilight budgets (twilight32k)")
     ap.add_argument("--budget-pages", type=int, default=128)
+    ap.add_argument("--twilight-path", choices=("fused", "pages", "rows"), default="fused",
+                    help="Twilight selection + union form: fused (score + one per-head launch, union record), "
+                         "pages (B0 plan, INT4 QK, top-p into B0 union page row masks) or rows (union row list)")
     ap.add_argument("--union", choices=("bits", "plan"), default="bits",
                     help="quest32k: the GQA union as per-head selection bitmaps ranked by the attention (bits) "
                          "or as a union plan built after the top-k (plan)")
@@ -247,7 +250,8 @@ class TwilightWorkload:
     SINK, RECENT, BS = 64, 256, 16
     B0_TOKENS, TOP_P, ALPHA, ZIPF = 4096, 0.95, 4.0, 1.1
 
-    def __init__(self, dev, layers: int, context: int, budget_mode: str = "dynamic", seed: int = 2):
+    def __init__(self, dev, layers: int, context: int, budget_mode: str = "dynamic", seed: int = 2,
+                 path: str = "fused"):
         import torch
 
         from headinfer import kernels
@@ -304,14 +308,26 @@ class TwilightWorkload:
         self.out = torch.empty_like(self.q)
         # dynamic budgets: the kept rows as row masks of the B0 union pages,
         # attended page by page (the same rows as the union row list)
-        self.page_rows = budget_mode == "dynamic"
+        self.page_rows = budget_mode == "dynamic" and path == "pages"
         self.slot_u = torch.zeros((layers, G, R, self.b0), dtype=i32, device=dev)
         self.prows = torch.zeros((layers, G, self.width), dtype=i32, device=dev)
+        # dynamic budgets, fused: two selection launches (score; per-head B0 +
+        # INT4 QK + top-p) writing each group's union record
+        self.fused = budget_mode == "dynamic" and path == "fused"
+        self.path = path if budget_mode == "dynamic" else "rows"
+        words = (kernels.union_record_words(self.P) + 3) & ~3
+        self.rec = torch.zeros((layers, G, words), dtype=i32, device=dev)
         torch.cuda.synchronize(dev)
 
     def select(self, layer: int) -> None:
         from headinfer import kernels
 
+        if self.fused:
+            kernels.twilight_select_fused(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P],
+                                          self.packed[layer], self.scale[layer], self.minimum[layer], self.b0,
+                                          self.rec[layer], top_p=self.TOP_P, sink=self.SINK, recent=self.RECENT,
+                                          block_size=self.BS, length=self.L, desired=self.desired[layer])
+            return
         kernels.quest_select(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P], self.b0,
                              sel_pages=self.sel[layer], plan_pages=self.plan_pages[layer],
                              plan_masks=self.plan_masks[layer], plan_counts=self.plan_counts[layer])
@@ -332,6 +348,12 @@ class TwilightWorkload:
     def attend(self, layer: int) -> None:
         from headinfer import kernels
 
+        if self.fused:
+            kernels.decode_attention_union(self.q[layer], self.kc[layer], self.vc[layer], self.rec[layer], self.P,
+                                           max_pages=self.width, sink=self.SINK, recent=self.RECENT,
+                                           block_size=self.BS, length=self.L, append=True, cur_k=self.cur_k[layer],
+                                           cur_v=self.cur_v[layer], out=self.out[layer])
+            return
         if self.page_rows:
             kernels.decode_attention_page_rows(self.q[layer], self.kc[layer], self.vc[layer], self.plan_pages[layer],
                                                self.plan_counts[layer], self.prows[layer], max_pages=self.width,
@@ -348,11 +370,21 @@ class TwilightWorkload:
         token), ascending."""
         import torch
 
+        sink_end = min(self.SINK, self.L)
+        recent_start = max(sink_end, self.L - (self.RECENT - 1))
+        if self.fused:
+            rec = self.rec[layer, g].long() & 0xFFFFFFFF
+            off = ((2 * ((self.P + 63) // 64)) + 3) & ~3
+            dev = rec.device
+            pages = torch.arange(self.P, device=dev)
+            masks = (rec[off + (pages >> 1)] >> (16 * (pages & 1))) & 0xFFFF
+            bits = (masks[:, None] >> torch.arange(self.BS, device=dev)) & 1
+            pos = self.SINK + pages[:, None] * self.BS + torch.arange(self.BS, device=dev)
+            return torch.cat([torch.arange(sink_end, device=dev), pos[bits.bool()],
+                              torch.arange(recent_start, self.L, device=dev)])
         if not self.page_rows:
             n = int(self.row_counts[layer, g])
             return self.rows[layer, g, :n].long()
-        sink_end = min(self.SINK, self.L)
-        recent_start = max(sink_end, self.L - (self.RECENT - 1))
         nu = int(self.plan_counts[layer, g])
         pages = self.plan_pages[layer, g, :nu].long()
         masks = self.prows[layer, g, :nu].long() & 0xFFFFFFFF
@@ -370,13 +402,20 @@ class TwilightWorkload:
     def bytes_per_layer(self) -> dict:
         G, R, D, P, N = self.G, self.R, self.D, self.P, self.N
         e = 2
-        cand_rows = self.plan_counts.double().sum().item() * self.BS / self.layers   # union of the B0 candidates
-        if self.page_rows:                                                          # attended union rows
+        if self.page_rows or self.fused:                                            # attended union rows
             rows = sum(self.kept_rows(layer, g).numel() for layer in range(self.layers) for g in range(G)) / self.layers
         else:
             rows = self.row_counts.double().sum().item() / self.layers
-        select = (2 * P * D * e * G + G * R * P * 4 * 2 + G * R * self.b0 * 4 + cand_rows * (D // 2 + 2 * e)
-                  + G * R * N * 4 * 2 + G * R * D * 4)
+        if self.fused:
+            # page min/max, scores out and back, every head's own B0 candidates'
+            # INT4 rows (codes + scale + min), q, the union records
+            cand_rows = G * R * N
+            select = (2 * P * D * e * G + G * R * P * 4 * 2 + cand_rows * (D // 2 + 2 * e) + G * R * D * 4
+                      + G * self.rec.shape[2] * 4)
+        else:
+            cand_rows = self.plan_counts.double().sum().item() * self.BS / self.layers   # union of the B0 candidates
+            select = (2 * P * D * e * G + G * R * P * 4 * 2 + G * R * self.b0 * 4 + cand_rows * (D // 2 + 2 * e)
+                      + G * R * N * 4 * 2 + G * R * D * 4)
         attention = rows * 2 * D * e + 2 * G * R * D * e + 4 * G * D * e
         return {"select": select, "attention": attention, "rows_per_group": rows / G,
                 "candidate_rows_per_group": cand_rows / G}
@@ -811,6 +850,10 @@ def run_twilight(args, dev) -> int:
     return 0 if result["parity"]["ok"] else 1
 
 
+_TW_PATHS = {"fused": "score + per-head B0/INT4 QK/top-p launch into a union record, attention over its row masks",
+             "pages": "over the B0 union pages row masks", "rows": "over the union row list"}
+
+
 def twilight_leg(args, dev) -> dict:
     """Twilight at 32K: one decode step of 32 layers x (Quest B0 + INT4 QK +
     top-p + GQA union, then sparse attention over the union and the append)."""
@@ -818,7 +861,7 @@ def twilight_leg(args, dev) -> dict:
 
     ctx = args.context or 32768
     print(f"[bench] twilight inputs: layers={args.layers} context={ctx}", file=sys.stderr, flush=True)
-    w = TwilightWorkload(dev, args.layers, ctx, args.budget_mode)
+    w = TwilightWorkload(dev, args.layers, ctx, args.budget_mode, path=args.twilight_path)
     w.step()
     torch.cuda.synchronize()
     # structure + attention of layer 0: union ascending, sink and recent present, within bounds
@@ -856,7 +899,7 @@ def twilight_leg(args, dev) -> dict:
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "twilight-32k-hbm: Llama-3-8B-shaped layer x 32, Quest B0 4096 tokens, INT4 QK, "
                                f"top-p {w.TOP_P} ({w.mode} budgets), union attention "
-                               f"({'over the B0 union pages row masks' if w.page_rows else 'over the union row list'}), "
+                               f"({_TW_PATHS[w.path]}), "
                                "KV in HBM",
                    "layers": w.layers, "context": w.L, "kv_heads": w.G, "q_per_kv": w.R, "head_dim": w.D,
                    "page_size": w.BS, "b0_pages": w.b0, "top_p": w.TOP_P, "budget_mode": w.mode},

@@ -349,6 +349,52 @@ int tw_twilight_select_pages(const float* logits, int G, int R, int N, const int
                              const int32_t* lengths, int page_capacity, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* Words (32-bit) of one KV group's Twilight union record over P scored
+ * pages (the output of tw_twilight_select_fused, the input of
+ * tw_decode_attention_union): a page bitmap of 2*ceil(P/64) words (bit p of
+ * word p/32: some head keeps a row of page p), then, from the next multiple
+ * of 4 words, each page's kept rows as a 16-bit mask, two pages per word
+ * (page p in bits 16*(p&1) .. of word p/2), padded to 16 bytes. */
+int tw_twilight_union_record_words(int P);
+
+/* Workspace bytes of tw_twilight_select_fused. */
+size_t tw_twilight_select_fused_workspace_size(int G, int R, int P, int b0_pages);
+
+/* The whole Twilight selection of a layer in two launches, dynamic budgets:
+ * the Quest score (page min/max upper bound, as tw_quest_select), then
+ * ceil(b0_pages/32) blocks per (group, head), each of which picks the head's
+ * B0 pages (the top b0_pages scores, ties to the lowest page) and estimates
+ * the INT4 QK of 32 of them (the logits of tw_twilight_qk, bit for bit); the
+ * last of them to finish keeps the top-p rows (the desired count and set of
+ * tw_twilight_select in dynamic mode) and ORs them into the group's union
+ * record (union_rec + g*rec_stride, tw_twilight_union_record_words(P) <=
+ * rec_stride, a multiple of 4; 16-byte aligned), which the score launch
+ * clears first.  No union plan or row list is built.
+ *   q [G][R][128] fp32; page_min/page_max as tw_quest_select (P pages,
+ *   16-bit); packed / qscale / qmin the INT4 keys of tw_build_page_metadata
+ *   (quant_entry_stride rows apart, quant_rows >= length valid rows, packed
+ *   16-byte aligned); qk_scale the logit scale (1/sqrt(D) in the reference);
+ *   lengths (nullable, device [G] int32): group g has min(lengths[g],
+ *   length) tokens, so its own candidate pages P_g <= P and min(b0_pages,
+ *   P_g) B0 pages; else every group has `length` tokens and P candidate
+ *   pages.  Outputs: desired [G][R] (the top-p counts, 0 for a group with no
+ *   candidate); sel_pages [G][R][b0_pages] (nullable; ascending, -1 past a
+ *   ragged group's pages); logits [G][R][b0_pages*16] (nullable).
+ * D = 128, block_size 16, R <= 8, P <= 8192, b0_pages*16 <= 8192.
+ * Workspace: tw_twilight_select_fused_workspace_size(G, R, P, b0_pages)
+ * bytes, zeroed before its first use (its arrival counters return to zero
+ * after every launch).  Replaces
+ * prepare_layer_selection's stages 1-2 and the GPU GQA union of the
+ * dynamic-budget path (twilight_offload_cache.py:996-1614); the union is
+ * the reference's token set, held as page row masks. */
+int tw_twilight_select_fused(const float* q, const void* page_min, const void* page_max, int dtype, int G, int R,
+                             int P, int D, int64_t page_group_stride, const uint8_t* packed, const void* qscale,
+                             const void* qmin, int64_t quant_entry_stride, int64_t quant_rows, int b0_pages,
+                             float top_p, float qk_scale, int sink, int recent, int block_size,
+                             const int32_t* lengths, int length, int32_t* sel_pages, float* logits, int32_t* desired,
+                             uint32_t* union_rec, int64_t rec_stride, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* ------------------------------------------------------------------------
  * Sparse GQA decode attention, split-K over selected rows, one query
  * token per group.  Replaces _flash_attention_varlen_forward
@@ -446,6 +492,28 @@ int tw_decode_attention_pages_bits(const void* q, const void* k_base, const void
                                    const void* cur_v, float softmax_scale, void* page_min, void* page_max,
                                    int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
                                    size_t workspace_bytes, int phase, void* stream);
+
+/* The Twilight union attention from a union record (tw_twilight_select_
+ * fused): the page-tile attention over the sink rows, the kept rows of every
+ * union page (the pages whose bitmap bit is set, ascending; every head
+ * attends every kept row, the rows no head keeps are neither read nor
+ * attended), the recent rows and the decode token.  The block stages the
+ * group's row masks in LDS in the same round trip as the bitmap.  lengths /
+ * length, append, cur_k/cur_v, page_min/page_max and packed/qscale/qmin (the
+ * appended row's INT4 code) as tw_decode_attention_page_rows; phase as
+ * tw_decode_attention_pages_phase.  P <= 8192, rec_stride >=
+ * tw_twilight_union_record_words(P) and a multiple of 4, union_rec 16-byte
+ * aligned; D = 128, 16-row pages, 16-bit K/V, R <= 8; max_rows bounds every
+ * group's rows; workspace as tw_decode_attention for max_rows.  The
+ * reference attends the GQA-group union rows (mp.py:239-279); the rows are
+ * the same set. */
+int tw_decode_attention_union(const void* q, const void* k_base, const void* v_base, int dtype, int G, int R, int D,
+                              const uint32_t* union_rec, int64_t rec_stride, int P, int max_rows,
+                              int64_t entry_stride_rows, int sink, int recent, int block_size, const int32_t* lengths,
+                              int length, int append, const void* cur_k, const void* cur_v, float softmax_scale,
+                              void* page_min, void* page_max, int64_t page_entry_stride, int meta_pages,
+                              uint8_t* packed, void* qscale, void* qmin, int64_t quant_entry_stride, void* out,
+                              void* workspace, size_t workspace_bytes, int phase, void* stream);
 /* The Twilight union attention over page rows: the page-tile attention of
  * tw_decode_attention_pages(_ragged) where plan_pages / plan_counts are the
  * B0 union (tw_quest_select with k = b0_pages) and page_rows[g*plan_stride +

@@ -1,0 +1,216 @@
+"""The fused Twilight selection (twilight_select_fused) and the union-record
+attention (decode_attention_union) against the oracle.
+
+Per group, oracle.twilight_layer at the group's own length gives the B0 pages,
+the INT4 QK logits, the top-p counts and each head's kept positions.  The
+fused selection must reproduce the first three bit for bit, and its union
+record must hold exactly the union of the heads' kept rows: one bitmap bit
+per page that has a kept row, that page's rows in its 16-bit mask, nothing
+else.  The attention over the record is held to 2e-3 abs + 1e-2 rel of
+float64 over the oracle's rows plus the decode token, and the appended row
+with its INT4 code and page metadata must equal the page-row path's bit for
+bit.  Every case runs twice with new queries on a record that starts as
+garbage, so a bit the score launch failed to clear would show."""
+
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import to_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*args):
+    print(*args, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def K():
+    from headinfer import kernels
+
+    return kernels
+
+
+def _close(got, ref, what):
+    got = np.asarray(got, dtype=np.float64)
+    err = np.abs(got - ref)
+    assert np.all(err <= 2e-3 + 1e-2 * np.abs(ref)), f"{what}: max abs err {err.max():.3e}"
+
+
+def _record_of(kept_pos, P, sink, bs):
+    """The union record's bitmap words and per-page masks the kept token
+    positions (between the sink and the recent window) give."""
+    masks = np.zeros(P, np.int64)
+    for p in kept_pos:
+        page, i = divmod(int(p) - sink, bs)
+        assert 0 <= page < P
+        masks[page] |= 1 << i
+    return masks
+
+
+def _decode_record(rec, P):
+    """(bitmap as a bool array over P pages + the bits past P, masks [P])."""
+    rec = rec.astype(np.int64) & 0xFFFFFFFF
+    nb = 2 * ((P + 63) // 64)
+    off = (nb + 3) & ~3
+    bits = np.array([(rec[p >> 5] >> (p & 31)) & 1 for p in range(32 * nb)], bool)
+    masks = np.array([(rec[off + (p >> 1)] >> (16 * (p & 1))) & 0xFFFF for p in range(P)], np.int64)
+    return bits, masks
+
+
+class _Setup:
+    def __init__(self, K, dev, G, R, Lmax, lengths, dtype=torch.bfloat16, seed=0, sink=64, recent=256, bs=16):
+        self.G, self.R, self.D, self.bs, self.sink, self.recent = G, R, 128, bs, sink, recent
+        D = self.D
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.k = (torch.randn((G, Lmax, D), generator=g, device=dev) * 1.5).to(dtype)
+        self.v = torch.randn((G, Lmax, D), generator=g, device=dev).to(dtype)
+        self.P = (Lmax - sink) // bs
+        self.pmin = torch.zeros((G, self.P, D), dtype=dtype, device=dev)
+        self.pmax = torch.zeros_like(self.pmin)
+        self.packed = torch.zeros((G, Lmax, D // 2), dtype=torch.uint8, device=dev)
+        self.qscale = torch.zeros((G, Lmax), dtype=dtype, device=dev)
+        self.qmin = torch.zeros_like(self.qscale)
+        for gi, L in enumerate(lengths):
+            p = max(0, (L - sink) // bs)
+            K.build_page_metadata(self.k[gi:gi + 1, :L], sink=sink, block_size=bs,
+                                  page_min=self.pmin[gi:gi + 1, :p], page_max=self.pmax[gi:gi + 1, :p],
+                                  packed=self.packed[gi:gi + 1, :L], scale=self.qscale[gi:gi + 1, :L],
+                                  minimum=self.qmin[gi:gi + 1, :L])
+
+
+def _run_case(K, dev, G, R, lengths, b0, top_p, ragged, seed):
+    st = _Setup(K, dev, G, R, max(lengths) + 8, lengths, seed=seed)
+    D, bs, sink, recent = st.D, st.bs, st.sink, st.recent
+    L = lengths[0]
+    # one length: the launch scores the pages wholly between its sink and recent windows
+    P = st.P if ragged else oracle.selection_window(L, sink, recent)[2] // bs
+    lens = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    words = K.union_record_words(P)
+    rec = torch.full((G, (words + 3) & ~3), -1, dtype=torch.int32, device=dev)   # garbage: the score launch clears it
+    sel = torch.zeros((G, R, b0), dtype=torch.int32, device=dev)
+    logits = torch.zeros((G, R, b0 * bs), dtype=torch.float32, device=dev)
+    desired = torch.zeros((G, R), dtype=torch.int32, device=dev)
+    # the page-row path on a second slab copy, for the appended row and its metadata
+    width = min(P, R * b0)
+    ppB = torch.zeros((G, width), dtype=torch.int32, device=dev)
+    pmB = torch.zeros((G, width), dtype=torch.uint8, device=dev)
+    pcB = torch.zeros((G,), dtype=torch.int32, device=dev)
+    selB = torch.zeros((G, R, b0), dtype=torch.int32, device=dev)
+    logB = torch.zeros((G, R, b0 * bs), dtype=torch.float32, device=dev)
+    slot_u = torch.zeros((G, R, b0), dtype=torch.int32, device=dev)
+    prB = torch.zeros((G, width), dtype=torch.int32, device=dev)
+    dB = torch.zeros((G, R), dtype=torch.int32, device=dev)
+    kA, vA, kB, vB = st.k.clone(), st.v.clone(), st.k.clone(), st.v.clone()
+    metaA = [t.clone() for t in (st.pmin, st.pmax, st.packed, st.qscale, st.qmin)]
+    metaB = [t.clone() for t in (st.pmin, st.pmax, st.packed, st.qscale, st.qmin)]
+    gen = torch.Generator(device=dev).manual_seed(seed + 1)
+    for rep in range(2):
+        q = (torch.randn((G, R, D), generator=gen, device=dev) * 2).to(torch.bfloat16)
+        cur_k = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+        cur_v = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+        qf = q.float()
+        _say(f"[fused] G={G} R={R} lengths={lengths[:3]}.. b0={b0} ragged={ragged} rep {rep}: select")
+        K.twilight_select_fused(qf, metaA[0][:, :P], metaA[1][:, :P], metaA[2], metaA[3], metaA[4], b0, rec,
+                                top_p=top_p, sink=sink, recent=recent, block_size=bs,
+                                length=max(lengths) if ragged else L, lengths=lens if ragged else None,
+                                desired=desired, sel_pages=sel, logits=logits)
+        torch.cuda.synchronize()
+        rec_h = rec.cpu().numpy()
+        sel_h, log_h, des_h = sel.cpu().numpy(), logits.cpu().numpy(), desired.cpu().numpy()
+        kept_all = []
+        for gi in range(G):
+            Lg = lengths[gi] if ragged else L
+            sink_end, recent_start, span = oracle.selection_window(Lg, sink, recent)
+            Pg = min(span // bs, P)
+            bits, masks = _decode_record(rec_h[gi], P)
+            b0g = min(b0, Pg)
+            if b0g == 0:
+                assert np.all(des_h[gi] == 0) and np.all(sel_h[gi] == -1), gi
+                assert not bits.any() and not masks.any(), gi
+                kept_all.append(np.concatenate([np.arange(sink_end), np.arange(recent_start, Lg)]).astype(np.int64))
+                continue
+            ref = oracle.twilight_layer(qf[gi].cpu().numpy(), to_bits(st.pmin[gi, :Pg]), to_bits(st.pmax[gi, :Pg]),
+                                        st.packed[gi].cpu().numpy(), to_bits(st.qscale[gi]), to_bits(st.qmin[gi]),
+                                        "bf16", length=Lg, sink=sink, recent=recent, block_size=bs, b0_pages=b0g,
+                                        top_p=top_p)
+            assert np.array_equal(sel_h[gi, :, :b0g], ref["pages"]), (rep, gi)
+            assert np.all(sel_h[gi, :, b0g:] == -1), (rep, gi)
+            Ng = b0g * bs
+            assert np.array_equal(log_h[gi, :, :Ng].view(np.uint32), ref["logits"].astype(np.float32).view(np.uint32)), \
+                (rep, gi)
+            assert np.array_equal(des_h[gi], ref["desired"]), (rep, gi, des_h[gi], ref["desired"])
+            sel_pos = np.unique(np.concatenate(ref["selected"]))
+            want = _record_of(sel_pos, P, sink, bs)
+            assert np.array_equal(masks, want), (rep, gi)
+            assert np.array_equal(bits[:P], want != 0) and not bits[P:].any(), (rep, gi)
+            kept_all.append(ref["union"].astype(np.int64))
+        # ---- attention over the record (A) and over page rows (B) ----
+        max_pages = min(P, R * b0)
+        outA = K.decode_attention_union(q, kA, vA, rec, P, max_pages=max_pages, sink=sink, recent=recent,
+                                        block_size=bs, lengths=lens if ragged else None, length=L, append=True,
+                                        cur_k=cur_k, cur_v=cur_v, page_min=metaA[0], page_max=metaA[1],
+                                        packed=metaA[2], scale=metaA[3], minimum=metaA[4])
+        if ragged:
+            K.quest_select_ragged(qf, metaB[0][:, :P], metaB[1][:, :P], lens, b0, sink=sink, recent=recent,
+                                  block_size=bs, sel_pages=selB, plan_pages=ppB, plan_masks=pmB, plan_counts=pcB)
+        else:
+            K.quest_select(qf, metaB[0][:, :P], metaB[1][:, :P], b0, sel_pages=selB, plan_pages=ppB,
+                           plan_masks=pmB, plan_counts=pcB)
+        K.twilight_qk(qf, metaB[2], metaB[3], metaB[4], ppB, pmB, pcB, b0, sink=sink, block_size=bs, out=logB,
+                      slot_u=slot_u, page_rows=prB)
+        K.twilight_select_pages(logB, selB, slot_u, prB, top_p=top_p, sink=sink, recent=recent, block_size=bs,
+                                length=max(lengths) if ragged else L, lengths=lens if ragged else None,
+                                page_capacity=P, desired=dB)
+        outB = K.decode_attention_page_rows(q, kB, vB, ppB, pcB, prB, max_pages=width, sink=sink, recent=recent,
+                                            block_size=bs, lengths=lens if ragged else None, length=L, append=True,
+                                            cur_k=cur_k, cur_v=cur_v, page_min=metaB[0], page_max=metaB[1],
+                                            packed=metaB[2], scale=metaB[3], minimum=metaB[4])
+        torch.cuda.synchronize()
+        assert torch.equal(desired, dB), rep
+        ref_o = np.zeros((G, R, D))
+        for gi in range(G):
+            kept = kept_all[gi]
+            keys = torch.cat([st.k[gi, kept].float(), cur_k[gi:gi + 1].float()]).cpu().numpy()
+            vals = torch.cat([st.v[gi, kept].float(), cur_v[gi:gi + 1].float()]).cpu().numpy()
+            ref_o[gi] = oracle.decode_attention(qf[gi].cpu().numpy(), keys, vals, 1.0 / math.sqrt(D))
+        _close(outA.float().cpu().numpy(), ref_o, f"union-record attention rep {rep}")
+        _close(outB.float().cpu().numpy(), ref_o, f"page-row attention rep {rep}")
+        assert torch.equal(kA.view(torch.int16), kB.view(torch.int16)) and torch.equal(vA.view(torch.int16),
+                                                                                         vB.view(torch.int16))
+        for a, b in zip(metaA, metaB):
+            assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), rep
+        # the next repetition reads the slab with this step's row (the oracle too)
+        st.k.copy_(kA)
+        st.v.copy_(vA)
+        for t, a in zip((st.pmin, st.pmax, st.packed, st.qscale, st.qmin), metaA):
+            t.copy_(a)
+        _say(f"[fused] rep {rep} ok, desired {des_h[0].tolist()}, union pages "
+             f"{[int(_decode_record(rec_h[gi], P)[0].sum()) for gi in range(G)]}")
+
+
+@pytest.mark.parametrize("G,R,L,b0,top_p", [
+    (4, 4, 4096, 64, 0.95),
+    (2, 8, 3000, 40, 0.8),
+    (3, 2, 8192, 256, 0.99),
+    (2, 4, 20000, 512, 0.95),     # 8192 candidates: 16 a thread
+    (2, 4, 40000, 256, 0.95),     # 2480 scored pages: 8 keys a thread in the B0 top-k
+    (8, 4, 32768, 256, 0.95),     # the 32K Twilight layer's shape
+])
+def test_fused_selection_matches_oracle(K, dev, G, R, L, b0, top_p):
+    _run_case(K, dev, G, R, [L] * G, b0, top_p, ragged=False, seed=L + G)
+
+
+def test_fused_selection_matches_oracle_ragged(K, dev):
+    # a group with no whole page between its windows, one with fewer pages
+    # than b0, longer ones, and one past 4096 pages (16 keys a thread)
+    lengths = [300, 1000, 4000, 4097, 7000, 70000]
+    _run_case(K, dev, len(lengths), 4, lengths, 64, 0.95, ragged=True, seed=11)

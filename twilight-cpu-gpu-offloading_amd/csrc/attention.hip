@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "tw_common.h"
+#include "union_record.h"
 
 namespace tw {
 namespace {
@@ -132,6 +133,14 @@ struct AttnArgs {
   const uint32_t* sel_bits;
   int64_t bits_stride;
   int bits_w64;
+  // Page-tile kernel, Twilight union record (union_record.h) instead
+  // (union_rec set): sel_bits + g * bits_stride is group g's record, its one
+  // bitmap row the union pages and its row masks, from 32-bit word mask_off
+  // on (mask_w4 16-byte units), the kept rows of each; every head attends
+  // every kept row.
+  int union_rec;
+  int mask_off;
+  int mask_w4;
 };
 
 // 8 consecutive channels of one row.
@@ -1247,7 +1256,7 @@ struct TileSrc {
 };
 
 __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w, int t, int nu, int page,
-                                            uint32_t pmask, uint32_t prow) {
+                                            uint32_t pmask, uint32_t prow, bool row_masks) {
   TileSrc s;
   s.dec = -1;
   s.hm = 0xffu;
@@ -1262,7 +1271,7 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
   } else if (t < ts + nu) {
     s.pos0 = a.sink + static_cast<int64_t>(page) * kTileRows;
     s.hm = pmask;
-    if (a.page_rows != nullptr) {
+    if (row_masks) {
       s.hm = 0xffu;  // the GQA union: every head attends every kept row
       s.rm = prow & 0xffffu;
     }
@@ -1289,7 +1298,9 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
 // loads, which measured faster there).
 // NWL > 0: the union comes from selection bitmaps (NWL 64-bit words per
 // lane) instead of a union plan.
-template <typename DT, int RMAX, int NW, int TW, bool RES, bool NT, int NWL>
+// MK (with NWL > 0): the union comes from a Twilight union record (one
+// bitmap row, row masks staged in LDS by the block).
+template <typename DT, int RMAX, int NW, int TW, bool RES, bool NT, int NWL, bool MK = false>
 __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   using S = typename DT::storage;
   using H = Half8<DT>;
@@ -1343,24 +1354,52 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   constexpr int kNwl = NWL > 0 ? NWL : 1;
   uint64_t hw[RMAX][kNwl], uw[kNwl];
   int b_cnt = 0, b_incl = 0;
+  // union record: the group's row masks (up to 4096 NWL pages) staged in
+  // LDS by the whole block, loaded in this round trip
+  constexpr int kMw4 = MK ? 512 * (NWL > 0 ? NWL : 1) : 1;
+  __shared__ __align__(16) uint4 s_mw[kMw4];
   if constexpr (NWL > 0) {
-    const uint32_t* brow = a.sel_bits + static_cast<int64_t>(g) * R * a.bits_stride;
+    const uint32_t* brow = a.sel_bits + static_cast<int64_t>(g) * (MK ? 1 : R) * a.bits_stride;
 #pragma unroll
     for (int w = 0; w < NWL; ++w) {
       const int wi = NWL * lane + w;
       const int wc = wi < a.bits_w64 ? wi : a.bits_w64 - 1;
       uw[w] = 0ull;
-      // Slots h >= R repeat row R - 1: the OR is unchanged and their mask
-      // bits are never read.  No uniform condition guards a load, so the
-      // compiler cannot sink them into branches that wait one by one.
+      if constexpr (MK) {
+        const uint64_t v = *reinterpret_cast<const uint64_t*>(brow + 2 * wc);
+        uw[w] = wi < a.bits_w64 ? v : 0ull;
 #pragma unroll
-      for (int h = 0; h < RMAX; ++h) {
-        const int hc = h < R ? h : R - 1;
-        const uint64_t v = *reinterpret_cast<const uint64_t*>(brow + hc * a.bits_stride + 2 * wc);
-        hw[h][w] = wi < a.bits_w64 ? v : 0ull;
-        uw[w] |= hw[h][w];
+        for (int h = 0; h < RMAX; ++h) hw[h][w] = uw[w];
+      } else {
+        // Slots h >= R repeat row R - 1: the OR is unchanged and their mask
+        // bits are never read.  No uniform condition guards a load, so the
+        // compiler cannot sink them into branches that wait one by one.
+#pragma unroll
+        for (int h = 0; h < RMAX; ++h) {
+          const int hc = h < R ? h : R - 1;
+          const uint64_t v = *reinterpret_cast<const uint64_t*>(brow + hc * a.bits_stride + 2 * wc);
+          hw[h][w] = wi < a.bits_w64 ? v : 0ull;
+          uw[w] |= hw[h][w];
+        }
       }
       b_cnt += __popcll(uw[w]);
+    }
+    if constexpr (MK) {
+      constexpr int kPer = kMw4 / (NW * kWave);
+      static_assert(kPer * NW * kWave == kMw4, "whole mask units per thread");
+      const uint4* src = reinterpret_cast<const uint4*>(brow + a.mask_off);
+      const int last = a.mask_w4 - 1;
+      uint4 mv[kPer];
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int i = static_cast<int>(threadIdx.x) + j * NW * kWave;
+        mv[j] = src[i < last ? i : last];
+      }
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int i = static_cast<int>(threadIdx.x) + j * NW * kWave;
+        s_mw[i] = i <= last ? mv[j] : make_uint4(0u, 0u, 0u, 0u);
+      }
     }
     b_incl = wave_prefix_sum_i32(b_cnt);
   } else {
@@ -1385,6 +1424,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     return;
   }
   if (chunk >= n_chunks) return;
+  if constexpr (MK) __syncthreads();  // the staged row masks (every exit above is block-uniform)
   if (chunk == 0) {
     append_decode_token<S>(a, g, D, win.append_position);
     if (a.meta_packed != nullptr)
@@ -1425,7 +1465,11 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
         page[tt] = 0;
         pmask[tt] = 0u;
         prow[tt] = 0xffffu;
-        if (u >= 0 && u < nu) bits_page<RMAX, kNwl>(u, b_incl, b_cnt, uw, hw, &page[tt], &pmask[tt]);
+        if (u >= 0 && u < nu) {
+          bits_page<RMAX, kNwl>(u, b_incl, b_cnt, uw, hw, &page[tt], &pmask[tt]);
+          if constexpr (MK)
+            prow[tt] = (reinterpret_cast<const uint32_t*>(s_mw)[page[tt] >> 1] >> (16 * (page[tt] & 1))) & 0xffffu;
+        }
       }
     } else if (it > 0) {
 #pragma unroll
@@ -1445,7 +1489,7 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     int hit_slot[TW];
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
-      ts[tt] = tile_src(a, win, t0 + tt, nu, page[tt], pmask[tt], prow[tt]);
+      ts[tt] = tile_src(a, win, t0 + tt, nu, page[tt], pmask[tt], prow[tt], MK || a.page_rows != nullptr);
       hit_slot[tt] = -1;
       if (res && ts[tt].u >= 0 && ts[tt].page >= 0 && ts[tt].page < a.res_map_pages) {
         const int64_t m = a.res_map[static_cast<int64_t>(g) * a.res_map_pages + ts[tt].page];
@@ -1840,7 +1884,11 @@ void plan_tile_chunks(int G, int max_rows_total, int* iters, int* chunks) {
 template <typename DT, int RMAX, bool RES, bool NT>
 void launch_tiles_nwl(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
   const int nwl = a.sel_bits == nullptr ? 0 : (a.bits_w64 <= kWave ? 1 : 2);
-  if (nwl == 0)
+  if (a.union_rec && nwl == 1)
+    hipLaunchKernelGGL((decode_attn_tiles<DT, RMAX, kTileNW, kTileTW, RES, NT, 1, true>), grid, block, 0, stream, a);
+  else if (a.union_rec)
+    hipLaunchKernelGGL((decode_attn_tiles<DT, RMAX, kTileNW, kTileTW, RES, NT, 2, true>), grid, block, 0, stream, a);
+  else if (nwl == 0)
     hipLaunchKernelGGL((decode_attn_tiles<DT, RMAX, kTileNW, kTileTW, RES, NT, 0>), grid, block, 0, stream, a);
   else if (nwl == 1)
     hipLaunchKernelGGL((decode_attn_tiles<DT, RMAX, kTileNW, kTileTW, RES, NT, 1>), grid, block, 0, stream, a);
@@ -2241,7 +2289,7 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
                        size_t workspace_bytes, void* stream, const uint32_t* page_rows = nullptr,
                        uint8_t* packed = nullptr, void* qscale = nullptr, void* qmin = nullptr,
                        int64_t quant_entry_stride = 0, const uint32_t* sel_bits = nullptr, int64_t bits_stride = 0,
-                       int bits_pages = 0, int phase = 3) {
+                       int bits_pages = 0, int phase = 3, int union_rec = 0) {
   if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr) return TW_EINVAL;
   if (page_rows != nullptr && res_map != nullptr) return TW_EINVAL;  // the resident cache keeps whole pages
   if (packed != nullptr &&
@@ -2259,6 +2307,9 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
     if (bits_pages < 1 || bits_pages > 128 * 64 || page_rows != nullptr || res_map != nullptr) return TW_EINVAL;
     if (bits_stride < 2 * ((bits_pages + 63) / 64) || (bits_stride % 2) != 0 ||
         (reinterpret_cast<uintptr_t>(sel_bits) % 8) != 0)
+      return TW_EINVAL;
+    if (union_rec && (bits_stride < union_record_words(bits_pages) || (bits_stride % 4) != 0 ||
+                      (reinterpret_cast<uintptr_t>(sel_bits) % 16) != 0))
       return TW_EINVAL;
     plan_stride = bits_pages;  // the union has at most this many pages
   } else if (plan_pages == nullptr || plan_counts == nullptr || plan_stride < 1) {
@@ -2328,6 +2379,9 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
   a.sel_bits = sel_bits;
   a.bits_stride = bits_stride;
   a.bits_w64 = (bits_pages + 63) / 64;
+  a.union_rec = union_rec;
+  a.mask_off = union_rec ? union_mask_offset(bits_pages) : 0;
+  a.mask_w4 = union_rec ? union_mask_words(bits_pages) / 4 : 0;
   a.phase = phase;
   plan_tile_chunks(G, max_rows, &a.iters, &a.max_chunks);
   a.t_per_chunk = a.iters * kTileNW * kTileTW;
@@ -2430,4 +2484,20 @@ extern "C" int tw_decode_attention_pages_bits(const void* q, const void* k_base,
                                 softmax_scale, nullptr, nullptr, nullptr, 0, 0, nullptr, page_min, page_max,
                                 page_entry_stride, meta_pages, out, workspace, workspace_bytes, stream, nullptr,
                                 nullptr, nullptr, nullptr, 0, sel_bits, bits_stride, P, phase);
+}
+
+extern "C" int tw_decode_attention_union(const void* q, const void* k_base, const void* v_base, int dtype, int G,
+                                         int R, int D, const uint32_t* union_rec, int64_t rec_stride, int P,
+                                         int max_rows, int64_t entry_stride_rows, int sink, int recent,
+                                         int block_size, const int32_t* lengths, int length, int append,
+                                         const void* cur_k, const void* cur_v, float softmax_scale, void* page_min,
+                                         void* page_max, int64_t page_entry_stride, int meta_pages, uint8_t* packed,
+                                         void* qscale, void* qmin, int64_t quant_entry_stride, void* out,
+                                         void* workspace, size_t workspace_bytes, int phase, void* stream) {
+  if (union_rec == nullptr) return TW_EINVAL;
+  return tw::pages_tiles_launch(q, k_base, v_base, dtype, G, R, D, nullptr, nullptr, nullptr, 0, max_rows,
+                                entry_stride_rows, sink, recent, block_size, lengths, length, append, cur_k, cur_v,
+                                softmax_scale, nullptr, nullptr, nullptr, 0, 0, nullptr, page_min, page_max,
+                                page_entry_stride, meta_pages, out, workspace, workspace_bytes, stream, nullptr,
+                                packed, qscale, qmin, quant_entry_stride, union_rec, rec_stride, P, phase, 1);
 }

@@ -51,6 +51,7 @@
 #include <mutex>
 
 #include "select.h"
+#include "union_record.h"
 
 namespace tw {
 namespace {
@@ -130,6 +131,14 @@ struct ScoreArgs {
   // Per-tile key range (nullable): tile_mm[(g*R + r) * tiles + tile] =
   // (max, min) of score_key over the tile's scored pages, for the top-k.
   uint2* tile_mm;
+  // Union records to clear (nullable): group g's at rec + g * rec_stride;
+  // the block of a tile zeroes the tile's bitmap word and row-mask words.
+  uint32_t* rec;
+  int64_t rec_stride;
+  // Arrival counters the launch after this one uses (nullable): block 0
+  // zeroes n_counters of them.
+  unsigned int* zero_counters;
+  int n_counters;
 };
 
 
@@ -335,6 +344,20 @@ __device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
   using S = typename DT::storage;
   const int p0 = tile * kTilePages;
   if (p0 >= a.P) return;  // block-uniform
+  if (a.zero_counters != nullptr && g == 0 && tile == 0) {
+    for (int i = static_cast<int>(threadIdx.x); i < a.n_counters; i += kScoreBlock) a.zero_counters[i] = 0u;
+  }
+  if (a.rec != nullptr) {
+    // every tile of the launch (a ragged group's too): words 2 tile and
+    // 2 tile + 1 of the bitmap, mask words [32 tile, 32 tile + 32)
+    uint32_t* rec = a.rec + g * a.rec_stride;
+    const int t = static_cast<int>(threadIdx.x);
+    const int mw = (p0 >> 1) + t - 2;
+    if (t < 2)
+      rec[2 * tile + t] = 0u;
+    else if (t < 2 + kTilePages / 2 && mw < union_mask_words(a.P))
+      rec[union_mask_offset(a.P) + mw] = 0u;
+  }
   // A ragged group's length is read in the same round trip as the tile: the
   // tile is staged up to the buffer's P pages (in bounds), and only the
   // scores of the group's own pages are written.
@@ -1311,6 +1334,33 @@ extern "C" int tw_quest_select_bits(const float* q, const void* page_min, const 
   if (rc != TW_OK) return rc;
   return tw::launch_select(s, G * R, true, st);
 }
+
+namespace tw {
+
+int fused_quest_score(const float* q, const void* page_min, const void* page_max, int dtype, int G, int R, int P,
+                      int D, int64_t page_group_stride, const int32_t* lengths, int sink, int recent, int block_size,
+                      void* workspace, size_t workspace_bytes, uint32_t* rec, int64_t rec_stride,
+                      unsigned int* counters, int n_counters, FusedScores* out, hipStream_t stream) {
+  if (!check_score_args(q, page_min, page_max, G, R, P, D, page_group_stride) || out == nullptr) return TW_EINVAL;
+  if (P > kMaxSelPages) return TW_EUNSUPPORTED;
+  if (rec != nullptr && rec_stride < union_record_words(P)) return TW_EINVAL;
+  if (workspace == nullptr || workspace_bytes < tw_quest_select_workspace_size(G, R, P)) return TW_ENOMEM;
+  const SelectWorkspace w = carve(workspace, G, R, P);
+  ScoreArgs a{q, page_min, page_max, page_group_stride, G, R, P, D, w.scores, padded(P), nullptr,
+              lengths, sink, recent, block_size};
+  a.tile_mm = w.tile_mm;
+  a.rec = rec;
+  a.rec_stride = rec_stride;
+  a.zero_counters = counters;
+  a.n_counters = counters != nullptr ? n_counters : 0;
+  out->scores = w.scores;
+  out->score_stride = padded(P);
+  out->vec_last4 = static_cast<int>(padded(P)) - 4;
+  out->tile_mm = w.tile_mm;
+  return dispatch_score(dtype, a, stream);
+}
+
+}  // namespace tw
 
 // ---------------------------------------------------------------------------
 // tw_quest_select_static: tw_quest_select for callers that cannot allocate

@@ -45,7 +45,10 @@ struct SelSharedT {
   uint32_t bnd_above;
   uint32_t bnd_count;
   int flag;
-  uint2 cpair[kWave];  // fast path: boundary candidates (key, index)
+  // fast path: boundary candidates as (key << 32) | ~index, so that one
+  // unsigned compare orders them by (key desc, index asc); unused slots are
+  // 0, which never outranks a candidate
+  unsigned long long cpair[kWave];
   uint32_t ncand;      // fast path: staging slots handed out
 };
 using SelShared = SelSharedT<kBlock>;
@@ -322,7 +325,27 @@ template <int NT>
 __device__ __forceinline__ void topk_fast_clear(SelSharedT<NT>& sh) {
   uint4* hist4 = reinterpret_cast<uint4*>(sh.hist);
   for (int b = threadIdx.x; b < kFastBins / 4; b += NT) hist4[b] = make_uint4(0u, 0u, 0u, 0u);
+  if (threadIdx.x < kWave) sh.cpair[threadIdx.x] = 0ull;
   if (threadIdx.x == 0) sh.ncand = 0u;
+}
+
+// Packed rank key of a candidate (see cpair).
+__device__ __forceinline__ unsigned long long rank_key(uint32_t key, int index) {
+  return (static_cast<unsigned long long>(key) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(index));
+}
+
+// Staging slots for the candidates of a thread whose bits are set in sel
+// (bit j = its j-th key): one LDS atomic per wavefront hands out a run of
+// slots (the wavefront's total) and each thread takes its part of the run
+// in lane order.  Returns the thread's first slot.
+__device__ __forceinline__ uint32_t stage_slots(uint32_t sel, uint32_t* counter) {
+  const uint32_t n = static_cast<uint32_t>(__popc(sel));
+  const uint32_t incl = static_cast<uint32_t>(wave_prefix_sum_i32(static_cast<int>(n)));
+  const uint32_t total = readlane_u32(incl, kWave - 1);
+  uint32_t base = 0u;
+  if (lane_id() == kWave - 1 && total != 0u) base = atomicAdd(counter, total);
+  base = readlane_u32(base, kWave - 1);
+  return base + incl - n;
 }
 
 // Fast path of block_topk for a row whose key range [kmin, kmax] is known
@@ -416,33 +439,36 @@ __device__ bool block_topk_fast(const uint32_t (&key)[KPT], int P, int k, uint32
     *take = t;
     return true;
   }
-  uint32_t cslot[KPT];
+  uint32_t inbin = 0u;
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    cslot[j] = 0u;
-    if (bin[j] == bnd) {
-      cslot[j] = atomicAdd(&sh.ncand, 1u);
-      sh.cpair[cslot[j]] = make_uint2(key[j], static_cast<uint32_t>(i0 + j));
+  for (int j = 0; j < KPT; ++j) inbin |= (bin[j] == bnd) ? (1u << j) : 0u;
+  uint32_t cslot[KPT];
+  {
+    uint32_t slot = stage_slots(inbin, &sh.ncand);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      cslot[j] = slot;
+      if ((inbin >> j) & 1u) sh.cpair[slot] = rank_key(key[j], i0 + j);
+      slot += (inbin >> j) & 1u;
     }
   }
   __syncthreads();
   // every wavefront ranks the staged candidates (lane m holds candidate m)
-  // with readlane, so no barrier hands the ranks back; slots past ccount
-  // hold (0, ~0u), which never outranks a candidate
-  const uint2 c = static_cast<uint32_t>(lane) < ccount ? sh.cpair[lane] : make_uint2(0u, 0xffffffffu);
+  // against all of them, read from LDS by every lane at once (broadcast
+  // reads, four in flight): one 64-bit compare each, no branch (the slots
+  // past ccount are 0 and never count), and no barrier hands the ranks back
+  const unsigned long long c = sh.cpair[lane];
   uint32_t rank = 0u;
-  const int n4 = (static_cast<int>(ccount) + 3) & ~3;
-  for (int m = 0; m < n4; m += 4) {
+  for (int m = 0; m < static_cast<int>(ccount); m += 4) {
+    unsigned long long o[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint32_t km = readlane_u32(c.x, m + u);
-      const uint32_t im = readlane_u32(c.y, m + u);
-      rank += (km > c.x || (km == c.x && im < c.y)) ? 1u : 0u;
-    }
+    for (int u = 0; u < 4; ++u) o[u] = sh.cpair[m + u];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rank += o[u] > c ? 1u : 0u;
   }
   const uint64_t tm = __ballot(static_cast<uint32_t>(lane) < ccount && rank < need2);
 #pragma unroll
-  for (int j = 0; j < KPT; ++j) t |= (bin[j] == bnd && ((tm >> cslot[j]) & 1ull)) ? (1u << j) : 0u;
+  for (int j = 0; j < KPT; ++j) t |= (((inbin >> j) & 1u) && ((tm >> cslot[j]) & 1ull)) ? (1u << j) : 0u;
   *take = t;
   return true;
 }

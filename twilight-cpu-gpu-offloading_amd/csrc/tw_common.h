@@ -176,6 +176,27 @@ __device__ __forceinline__ uint32_t wave_prefix_sum_u32(uint32_t v) {
   const int l = lane_id();
   return v + (l >= 16 ? t0 : 0u) + (l >= 32 ? t1 : 0u) + (l >= 48 ? t2 : 0u);
 }
+// Inclusive prefix sum of 64-bit values over lanes: the same DPP row scan on
+// the two 32-bit halves with the carry of the low half, then the row totals.
+__device__ __forceinline__ uint64_t wave_prefix_sum_u64(uint64_t v) {
+  uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);
+  auto step = [&](uint32_t slo, uint32_t shi) {
+    const uint32_t n = lo + slo;
+    hi += shi + (n < lo ? 1u : 0u);
+    lo = n;
+  };
+  step(dpp_shr_zero<1>(lo), dpp_shr_zero<1>(hi));
+  step(dpp_shr_zero<2>(lo), dpp_shr_zero<2>(hi));
+  step(dpp_shr_zero<4>(lo), dpp_shr_zero<4>(hi));
+  step(dpp_shr_zero<8>(lo), dpp_shr_zero<8>(hi));
+  uint64_t r = (static_cast<uint64_t>(hi) << 32) | lo;
+  const uint64_t t0 = (static_cast<uint64_t>(readlane_u32(hi, 15)) << 32) | readlane_u32(lo, 15);
+  const uint64_t t1 = (static_cast<uint64_t>(readlane_u32(hi, 31)) << 32) | readlane_u32(lo, 31);
+  const uint64_t t2 = (static_cast<uint64_t>(readlane_u32(hi, 47)) << 32) | readlane_u32(lo, 47);
+  const int l = lane_id();
+  r += (l >= 16 ? t0 : 0ull) + (l >= 32 ? t1 : 0ull) + (l >= 48 ? t2 : 0ull);
+  return r;
+}
 __device__ __forceinline__ int wave_prefix_sum_i32(int v) {
   return static_cast<int>(wave_prefix_sum_u32(static_cast<uint32_t>(v)));
 }

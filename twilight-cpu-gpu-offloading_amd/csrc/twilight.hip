@@ -24,6 +24,7 @@
 #include <type_traits>
 
 #include "select.h"
+#include "union_record.h"
 
 namespace tw {
 namespace {
@@ -1386,6 +1387,166 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
   }
 }
 
+// Fast path of block_top_mass for a row whose key range [kmin, kmax] is
+// known, with the top-p threshold found on the way: one pass of kFastBins
+// bins linear in the value over that range accumulates each bin's count and
+// integer mass (the caller has cleared both and the staging counter); every
+// wavefront then reads all bins (8 per lane), takes the total mass Z and the
+// threshold need = ceil(p24 * Z / 2^24) from them, and finds the bin where
+// the mass of the bins above it falls short of need and with it reaches it.
+// At most 64 keys of that bin are staged and every wavefront ranks them by
+// (key desc, index asc) with readlane, summing the masses ranked ahead of
+// each: the key whose own mass crosses the rest of need ends the selection.
+// Two barriers.  Returns false -- block-uniformly, with the bins dirty --
+// when the range is not finite and positive, need is 0 (no mass or p24 = 0)
+// or the boundary bin holds more than 64 keys; on true, *taken and *count
+// are what block_top_mass gives for that need.
+template <int KPT, int NT>
+__device__ bool block_top_p_fast(const uint32_t (&key)[KPT], const uint64_t (&mass)[KPT], int N, uint32_t p24,
+                                 uint32_t kmin, uint32_t kmax, TopShared<NT>& sh, uint32_t* taken_out,
+                                 int* count_out) {
+  constexpr int kBins = kFastBins;
+  constexpr int kBpl = kBins / kWave;  // bins per lane
+  static_assert(kBpl == 8, "two 16-byte count reads and four mass reads per lane");
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = lane_id();
+  const int i0 = KPT * tid;
+  const float vmin = key_value(kmin);
+  const float vmax = key_value(kmax);
+  const float range = vmax - vmin;
+  const float scale = static_cast<float>(kBins) / range;
+  if (!(__builtin_isfinite(vmin) && __builtin_isfinite(vmax) && __builtin_isfinite(range) && range > 0.0f &&
+        __builtin_isfinite(scale)))
+    return false;
+  int bin[KPT];
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int b = static_cast<int>((key_value(key[j]) - vmin) * scale);
+    bin[j] = (i0 + j < N) ? (b < kBins - 1 ? b : kBins - 1) : -1;
+    if (bin[j] >= 0) {
+      atomicAdd(&sh.sel.hist[bin[j]], 1u);
+      if (mass[j] != 0) atomicAdd(&sh.bin_mass[bin[j]], static_cast<unsigned long long>(mass[j]));
+    }
+  }
+  __syncthreads();
+  uint32_t hc[kBpl];
+  uint64_t hm[kBpl];
+  {
+    const uint4* c4 = reinterpret_cast<const uint4*>(sh.sel.hist) + 2 * lane;
+    const uint4 a0 = c4[0], a1 = c4[1];
+    hc[0] = a0.x; hc[1] = a0.y; hc[2] = a0.z; hc[3] = a0.w;
+    hc[4] = a1.x; hc[5] = a1.y; hc[6] = a1.z; hc[7] = a1.w;
+    const ulonglong2* m2 = reinterpret_cast<const ulonglong2*>(sh.bin_mass) + 4 * lane;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const ulonglong2 v = m2[q];
+      hm[2 * q] = v.x;
+      hm[2 * q + 1] = v.y;
+    }
+  }
+  uint64_t tm = 0;
+  uint32_t tc = 0u;
+#pragma unroll
+  for (int b = 0; b < kBpl; ++b) {
+    tm += hm[b];
+    tc += hc[b];
+  }
+  const uint64_t pm = wave_prefix_sum_u64(tm);
+  const uint64_t z = (static_cast<uint64_t>(readlane_u32(static_cast<uint32_t>(pm >> 32), kWave - 1)) << 32) |
+                     readlane_u32(static_cast<uint32_t>(pm), kWave - 1);
+  const uint64_t sm = z - pm + tm;  // mass of the bins of lanes >= this one
+  const uint32_t sc = wave_suffix_sum_u32(tc);
+  const uint64_t need = top_p_threshold(p24, z);
+  if (need == 0) {
+    __syncthreads();  // every wavefront is done with the bins
+    return false;
+  }
+  // lanes 0 .. L have a suffix mass >= need
+  const uint64_t bl = __ballot(sm >= need);
+  const int L = 63 - __clzll(static_cast<long long>(bl));
+  uint64_t acc = sm - tm;     // mass of the bins above this lane's
+  uint32_t cacc = sc - tc;    // and their keys
+  int bsel = 0;
+  uint32_t cnt = 0u;
+  uint64_t bmass = 0;
+  bool found = false;
+#pragma unroll
+  for (int b = kBpl - 1; b >= 0; --b) {
+    const bool hit = !found && need <= acc + hm[b];
+    bsel = hit ? b : bsel;
+    cnt = hit ? hc[b] : cnt;
+    bmass = hit ? hm[b] : bmass;
+    acc += (found || hit) ? 0ull : hm[b];
+    cacc += (found || hit) ? 0u : hc[b];
+    found = found || hit;
+  }
+  const int bnd = kBpl * L + static_cast<int>(readlane_u32(static_cast<uint32_t>(bsel), L));
+  const uint64_t above = (static_cast<uint64_t>(readlane_u32(static_cast<uint32_t>(acc >> 32), L)) << 32) |
+                         readlane_u32(static_cast<uint32_t>(acc), L);
+  const uint32_t c_above = readlane_u32(cacc, L);
+  const uint32_t ccount = readlane_u32(cnt, L);
+  if (ccount > static_cast<uint32_t>(kWave)) {
+    __syncthreads();
+    return false;
+  }
+  const uint64_t need2 = need - above;  // 1 .. the bin's mass
+  uint32_t t = 0u;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) t |= (bin[j] > bnd) ? (1u << j) : 0u;
+  uint32_t inbin = 0u;
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) inbin |= (bin[j] == bnd) ? (1u << j) : 0u;
+  uint32_t cslot[KPT];
+  {
+    uint32_t slot = stage_slots(inbin, &sh.sel.ncand);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      cslot[j] = slot;
+      if ((inbin >> j) & 1u) {
+        sh.sel.cpair[slot] = rank_key(key[j], i0 + j);
+        sh.cmass[slot] = mass[j];
+      }
+      slot += (inbin >> j) & 1u;
+    }
+  }
+  __syncthreads();
+  // every wavefront ranks the staged keys (lane m holds key m) against all
+  // of them, read from LDS by every lane at once (broadcast reads, four in
+  // flight): one 64-bit compare each, no branch (slots past ccount hold
+  // key 0, which never outranks a key, so their stale masses never count)
+  const bool live = static_cast<uint32_t>(lane) < ccount;
+  const unsigned long long c = sh.sel.cpair[lane];
+  const uint64_t cm = live ? static_cast<uint64_t>(sh.cmass[lane]) : 0ull;
+  uint64_t before = 0;
+  uint32_t rank = 0u;
+  for (int m = 0; m < static_cast<int>(ccount); m += 4) {
+    unsigned long long o[4];
+    uint64_t om[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      o[u] = sh.sel.cpair[m + u];
+      om[u] = sh.cmass[m + u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool ahead = o[u] > c;
+      before += ahead ? om[u] : 0ull;
+      rank += ahead ? 1u : 0u;
+    }
+  }
+  const bool cross = live && before < need2 && need2 <= before + cm;
+  const uint64_t cb = __ballot(cross);
+  // (need2 <= the bin's mass, so some key crosses; all of them otherwise)
+  const uint32_t needed = cb != 0ull ? readlane_u32(rank, first_lane(cb)) + 1u : ccount;
+  const uint64_t tmk = __ballot(live && rank < needed);
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) t |= (((inbin >> j) & 1u) && ((tmk >> cslot[j]) & 1ull)) ? (1u << j) : 0u;
+  *taken_out = t;
+  *count_out = static_cast<int>(c_above + needed);
+  (void)bmass;
+  return true;
+}
+
 // The row's logits as KPT contiguous keys per thread (16-byte loads of the
 // thread's own logits; rows that are not 16-byte aligned go through the LDS
 // stage); the largest logit and the smallest and largest key of the row in
@@ -1597,6 +1758,320 @@ __global__ __launch_bounds__(NT) void twilight_matched_kernel(SelectArgs s) {
   if (!arrive_last(s.counters + g, static_cast<unsigned int>(s.R), &sh.sel.flag)) return;
   build_token_union<NT>(s, g, union_bits, reinterpret_cast<int32_t*>(stage), sh.sel.scan, sh.sel.hist,
                       reinterpret_cast<int32_t*>(sh.bin_mass));
+}
+
+// ------------------------------------------------ fused per-head selection
+// The Twilight selection of every (group, head) row after the score kernel,
+// in one launch: `parts` blocks per row, each of which
+//   1. picks the head's B0 pages (the top b0 of its page scores: block top-k
+//      with the one-pass fast path over the score kernel's tile key ranges),
+//      ascending, in LDS -- every part block of a row finds the same pages
+//      (the top-k is deterministic), so no block waits for another's;
+//   2. estimates the INT4 QK of its kPartPages of those pages (candidate n =
+//      row n % 16 of the (n / 16)-th B0 page): one 16-row page per
+//      matrix-core tile, v_mfma_i32_16x16x64_i8 with the head's three
+//      balanced fixed-point digits as A rows 0..2 and the page's codes as B
+//      columns, so lanes 0..15 hold S of rows 0..15 (the integers
+//      twilight_qk_kernel forms, hence the same logits), and publishes the
+//      logits to the workspace;
+// and the part block that arrives last (arrival counter per row, the
+// device-coherent handoff of arrive_last) reads the row's logits back and
+//   3. runs the top-p with dynamic budgets (the exact integer-mass rule of
+//      twilight_topp_kernel);
+//   4. ORs each page's kept rows into its 16-bit mask and the page's bit into
+//      the group's page bitmap (global atomics into the union record the
+//      score kernel cleared; a page whose rows no head keeps is not in the
+//      union).
+// The part blocks spread the INT4 rows' reads over parts x G x R CUs; the
+// top-k each repeats reads 4 bytes a page from L2.  D = 128, 16-row pages,
+// 16-bit keys.
+constexpr int kHeadThreads = 512;
+constexpr int kPartPages = 32;  // B0 pages a part block estimates: 4 per wavefront
+
+struct HeadArgs {
+  const float* scores;   // FusedScores
+  int64_t score_stride;
+  int vec_last4;
+  const uint2* tile_mm;
+  int G, R, P, b0;       // P: scored pages of the launch; b0: B0 pages per head
+  int parts;             // part blocks per row: ceil(b0 / kPartPages)
+  const int32_t* lengths;  // nullable: group g has min(lengths[g], length) tokens
+  int length;
+  int sink, recent;
+  const float* q;        // [G][R][128]
+  const uint8_t* packed; // entry g row t at + (g * qstride + t) * 64
+  const void* scale;
+  const void* minimum;
+  int64_t qstride, qrows;
+  float qk_scale;
+  uint32_t p24;
+  unsigned int* counters;  // [G * R] arrival counters (zero between launches)
+  float* ws_logits;        // [G * R][b0 * 16] the rows' logits, handed to the last block
+  int32_t* sel_pages;    // nullable [G][R][b0]: B0 pages ascending, -1 past a ragged group's
+  float* logits;         // nullable [G][R][b0 * 16]
+  int32_t* desired;      // [G][R]
+  uint32_t* rec;         // union records, rec_stride words apart
+  int64_t rec_stride;
+};
+
+template <typename DT, int KPA, int KPB>
+__global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a) {
+  constexpr int NT = kHeadThreads;
+  constexpr int BS = 16;
+  constexpr int kSlots = KPB * NT / BS;  // B0 pages a row holds
+  constexpr int KW = 16;                 // code words of a 128-channel row
+  constexpr int kWv = NT / kWave;        // wavefronts
+  constexpr int BT = kPartPages / kWv;   // pages per wavefront
+  using S = typename DT::storage;
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  static_assert(KPA % 4 == 0 && (KPB == 8 || KPB == 16) && BT * kWv == kPartPages, "block shape");
+  __shared__ __align__(16) TopShared<NT> sh;
+  __shared__ int s_page[kSlots];
+  __shared__ __align__(16) uint32_t s_q[4 * 6 * KW];
+  __shared__ int s_qshift[4];
+  __shared__ float s_qsum[4];
+  __shared__ int s_qok[4];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const int row = blockIdx.x / a.parts;
+  const int part = blockIdx.x - row * a.parts;
+  const int g = row / a.R;
+  topk_fast_clear(sh.sel);
+  __syncthreads();
+  // ---- round trip 1: length, the row's keys and tile ranges, q ----
+  int length = __hip_atomic_load(a.lengths != nullptr ? a.lengths + g : reinterpret_cast<const int32_t*>(a.q),
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t key[KPA];
+  {
+    const float* vals = a.scores + static_cast<int64_t>(row) * a.score_stride;
+    const int i0 = KPA * tid;
+#pragma unroll
+    for (int q4 = 0; q4 < KPA / 4; ++q4) {
+      int at = i0 + 4 * q4;
+      at = at < a.vec_last4 ? at : a.vec_last4;
+      const float4 v = *reinterpret_cast<const float4*>(vals + at);
+      key[4 * q4] = score_key(v.x);
+      key[4 * q4 + 1] = score_key(v.y);
+      key[4 * q4 + 2] = score_key(v.z);
+      key[4 * q4 + 3] = score_key(v.w);
+    }
+  }
+  const int tiles = (a.P + 63) / 64;
+  uint2 tr0, tr1;
+  {
+    const uint2* tm = a.tile_mm + static_cast<int64_t>(row) * tiles;
+    tr0 = tm[lane < tiles ? lane : tiles - 1];
+    tr1 = tm[lane + kWave < tiles ? lane + kWave : tiles - 1];
+  }
+  QStage<128, 4> qst;
+  qst.load(a.q + static_cast<int64_t>(row) * 128, 1);
+  length = a.lengths != nullptr ? (length < 0 ? 0 : (length > a.length ? a.length : length)) : a.length;
+  const int P = a.lengths != nullptr ? ragged_pages(length, a.sink, a.recent, BS, a.P) : a.P;
+  const int b0 = a.b0 < P ? a.b0 : P;  // block-uniform
+  const int N = b0 * BS;
+  // the head's query in fixed point (the first wavefront; barriers below)
+  stage_qfix<128, 4, true>(qst, 1, s_q, s_qshift, s_qsum, s_qok);
+
+  // ---- 1. the B0 pages ----
+  uint32_t take = 0u;
+  if (b0 > 0) {
+    const int tg = (P + 63) / 64;
+    const uint32_t kmax = wave_max_u32(max(lane < tg ? tr0.x : 0u, lane + kWave < tg ? tr1.x : 0u));
+    const uint32_t kmin =
+        wave_min_u32(min(lane < tg ? tr0.y : 0xffffffffu, lane + kWave < tg ? tr1.y : 0xffffffffu));
+    if (!block_topk_fast<KPA>(key, P, b0, kmin, kmax, sh.sel, &take)) {
+      int first;
+      block_topk<KPA>(key, P, b0, sh.sel, &take, &first);
+    }
+  }
+  {
+    int total;
+    int slot = block_excl_scan<NT>(__popc(take), sh.sel.scan, &total);
+#pragma unroll
+    for (int j = 0; j < KPA; ++j) {
+      if ((take >> j) & 1u) s_page[slot++] = KPA * tid + j;
+    }
+  }
+  // the top-p's histograms and staging counter start at zero (the top-k is
+  // done with them)
+  for (int b = tid; b < kLinBins + 64; b += NT) {
+    sh.sel.hist[b] = 0u;
+    sh.bin_mass[b] = 0ull;
+  }
+  if (tid == 0) sh.sel.ncand = 0u;
+  if (tid < kWave) sh.sel.cpair[tid] = 0ull;
+  __syncthreads();
+  if (part == 0 && a.sel_pages != nullptr) {
+    for (int i = tid; i < a.b0; i += NT) a.sel_pages[static_cast<int64_t>(row) * a.b0 + i] = i < b0 ? s_page[i] : -1;
+  }
+  if (N == 0) {
+    if (part == 0 && tid == 0) a.desired[row] = 0;
+    return;  // every part block of the row: no candidate, no arrival
+  }
+
+  // ---- 2. INT4 QK of the part's pages, one page per matrix-core tile ----
+  float* wl = a.ws_logits + static_cast<int64_t>(row) * a.b0 * BS;
+  {
+    const int G4 = lane / 16;
+    const int mrow = lane % 16;
+    v4i av[2];
+    {
+      // A row m < 3 = slice m of the head (balanced digits), rows 3..15 zero;
+      // lane group G4 holds channel words 4 G4 + 2 sp and + 1 as [even, odd]
+      const bool live = mrow < 3;
+      const uint32_t* st = s_q + (live ? mrow : 0) * 2 * KW;
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp) {
+        const int k0 = 4 * G4 + 2 * sp;
+        av[sp][0] = live ? static_cast<int>(st[k0]) : 0;
+        av[sp][1] = live ? static_cast<int>(st[KW + k0]) : 0;
+        av[sp][2] = live ? static_cast<int>(st[k0 + 1]) : 0;
+        av[sp][3] = live ? static_cast<int>(st[KW + k0 + 1]) : 0;
+      }
+    }
+    const int qshift = s_qshift[0];
+    const float qsum = s_qsum[0];
+    const bool qok = s_qok[0] != 0;
+    const uint8_t* pk = a.packed + static_cast<int64_t>(g) * a.qstride * 64;
+    const S* sc = static_cast<const S*>(a.scale) + static_cast<int64_t>(g) * a.qstride;
+    const S* mn = static_cast<const S*>(a.minimum) + static_cast<int64_t>(g) * a.qstride;
+    uint4 cw[BT];
+    S sv[BT], mv[BT];
+    // pages part * kPartPages + wave + kWv * j (clamped into the B0 pages)
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      int s = part * kPartPages + wave + kWv * j;
+      s = s < b0 ? s : b0 - 1;
+      int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[s]) * BS + mrow;
+      t = (t >= 0 && t < a.qrows) ? t : 0;
+      cw[j] = *reinterpret_cast<const uint4*>(pk + t * 64 + 16 * G4);
+      sv[j] = sc[t];
+      mv[j] = mn[t];
+    }
+#pragma unroll
+    for (int j = 0; j < BT; ++j) {
+      const int s = part * kPartPages + wave + kWv * j;
+      v4i b0v, b1v;
+      b0v[0] = static_cast<int>(cw[j].x & 0x0f0f0f0fu);
+      b0v[1] = static_cast<int>((cw[j].x >> 4) & 0x0f0f0f0fu);
+      b0v[2] = static_cast<int>(cw[j].y & 0x0f0f0f0fu);
+      b0v[3] = static_cast<int>((cw[j].y >> 4) & 0x0f0f0f0fu);
+      b1v[0] = static_cast<int>(cw[j].z & 0x0f0f0f0fu);
+      b1v[1] = static_cast<int>((cw[j].z >> 4) & 0x0f0f0f0fu);
+      b1v[2] = static_cast<int>(cw[j].w & 0x0f0f0f0fu);
+      b1v[3] = static_cast<int>((cw[j].w >> 4) & 0x0f0f0f0fu);
+      v4i c = {0, 0, 0, 0};
+      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[0], b0v, c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[1], b1v, c, 0, 0, 0);
+      if (lane < 16 && s < b0) {
+        const int64_t Sd = (static_cast<int64_t>(c[0]) << 16) + (static_cast<int64_t>(c[1]) << 8) + c[2];
+        publish_f32(wl + s * BS + lane,
+                    qk_logit(Sd, qshift, qsum, qok, to_f32(DT{}, sv[j]), to_f32(DT{}, mv[j]), a.qk_scale));
+      }
+    }
+  }
+  if (!arrive_last(a.counters + row, static_cast<unsigned int>(a.parts), &sh.sel.flag)) return;
+
+  // ---- 3. the last part block: top-p over the row's logits ----
+  uint32_t lkey[KPB];
+  float lmax;
+  uint32_t kmin, kmax;
+  {
+    const int i0 = KPB * tid;
+    float v[KPB];
+#pragma unroll
+    for (int j = 0; j < KPB; j += 2) {
+      const int i = i0 + j < N ? i0 + j : 0;
+      const float2 t = fetch_f32x2(wl + i);
+      v[j] = t.x;
+      v[j + 1] = t.y;
+    }
+    float mx = -INFINITY;
+    uint32_t kmx = 0u, kmn = 0xffffffffu;
+#pragma unroll
+    for (int j = 0; j < KPB; ++j) {
+      const bool ok = i0 + j < N;
+      lkey[j] = score_key(v[j]);
+      mx = (ok && v[j] > mx) ? v[j] : mx;
+      kmx = (ok && lkey[j] > kmx) ? lkey[j] : kmx;
+      kmn = (ok && lkey[j] < kmn) ? lkey[j] : kmn;
+    }
+    if (a.logits != nullptr) {
+      float* lo = a.logits + static_cast<int64_t>(row) * a.b0 * BS;
+#pragma unroll
+      for (int j = 0; j < KPB; ++j)
+        if (i0 + j < N) lo[i0 + j] = v[j];
+    }
+    mx = wave_max_f32(mx);
+    kmx = wave_max_u32(kmx);
+    kmn = wave_min_u32(kmn);
+    if (lane == 0) {
+      sh.fred[wave] = mx;
+      sh.sel.red_max[wave] = kmx;
+      sh.sel.red_min[wave] = kmn;
+    }
+    __syncthreads();
+    lmax = sh.fred[0];
+    kmax = sh.sel.red_max[0];
+    kmin = sh.sel.red_min[0];
+#pragma unroll
+    for (int w = 1; w < kWv; ++w) {
+      lmax = fmaxf(lmax, sh.fred[w]);
+      kmax = sh.sel.red_max[w] > kmax ? sh.sel.red_max[w] : kmax;
+      kmin = sh.sel.red_min[w] < kmin ? sh.sel.red_min[w] : kmin;
+    }
+    __syncthreads();
+  }
+  uint64_t mass[KPB];
+  uint64_t local = 0;
+  const int c0 = KPB * tid;
+#pragma unroll
+  for (int j = 0; j < KPB; ++j) {
+    mass[j] = (c0 + j < N) ? mass_of(key_value(lkey[j]), lmax) : 0ull;
+    local += mass[j];
+  }
+  uint32_t taken;
+  int desired;
+  if (!block_top_p_fast<KPB>(lkey, mass, N, a.p24, kmin, kmax, sh, &taken, &desired)) {
+    // the general search, on cleared bins
+    for (int b = tid; b < kLinBins + 64; b += NT) {
+      sh.sel.hist[b] = 0u;
+      sh.bin_mass[b] = 0ull;
+    }
+    const uint64_t z = block_sum_u64<NT>(local, sh.red64);  // (its barriers order the clear)
+    uint64_t need = top_p_threshold(a.p24, z);
+    if (need == 0) {
+      // no mass at all (non-finite logits): one key, the largest
+#pragma unroll
+      for (int j = 0; j < KPB; ++j) mass[j] = (c0 + j < N) ? 1ull : 0ull;
+      need = 1;
+    }
+    desired = block_top_mass<KPB>(lkey, mass, N, need, kmin, kmax, sh, &taken);
+  }
+  desired = desired < 1 ? 1 : (desired > N ? N : desired);
+  if (tid == 0) a.desired[row] = desired;
+
+  // ---- 4. publish: row masks and the page bitmap of the union record ----
+  uint32_t* rec = a.rec + static_cast<int64_t>(g) * a.rec_stride;
+  uint32_t* masks = rec + union_mask_offset(a.P);
+  if constexpr (KPB == 8) {
+    // two threads per page: the even one ORs both halves
+    uint32_t m = (taken & 0xffu) << (8 * (tid & 1));
+    m |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 1));
+    if ((tid & 1) == 0 && m != 0u) {
+      const int p = s_page[tid >> 1];
+      atomicOr(masks + (p >> 1), m << (16 * (p & 1)));
+      atomicOr(rec + (p >> 5), 1u << (p & 31));
+    }
+  } else {
+    const uint32_t m = taken & 0xffffu;
+    if (m != 0u) {
+      const int p = s_page[tid];
+      atomicOr(masks + (p >> 1), m << (16 * (p & 1)));
+      atomicOr(rec + (p >> 5), 1u << (p & 31));
+    }
+  }
 }
 
 // --------------------------------------------------------------- launch
@@ -1867,4 +2342,103 @@ extern "C" int tw_twilight_select_pages(const float* logits, int G, int R, int N
   return select_launch(logits, G, R, N, sel_pages, b0_pages, top_p, 0, 0, desired, nullptr, nullptr, nullptr,
                        nullptr, 0, sink, recent, block_size, length, lengths, lengths != nullptr ? page_capacity : 0,
                        -1, workspace, workspace_bytes, stream, slot_u, page_rows, page_rows_stride);
+}
+
+namespace tw {
+namespace {
+
+template <typename DT, int KPA, int KPB>
+int launch_head_kpb(const HeadArgs& h, hipStream_t stream) {
+  hipLaunchKernelGGL((twilight_head_kernel<DT, KPA, KPB>), dim3(h.G * h.R * h.parts), dim3(kHeadThreads), 0, stream,
+                     h);
+  return tw_host::check_launch();
+}
+
+template <typename DT>
+int launch_head(const HeadArgs& h, hipStream_t stream) {
+  const bool wide = h.b0 * 16 > 8 * kHeadThreads;
+  if (h.P <= 4 * kHeadThreads)
+    return wide ? launch_head_kpb<DT, 4, 16>(h, stream) : launch_head_kpb<DT, 4, 8>(h, stream);
+  if (h.P <= 8 * kHeadThreads)
+    return wide ? launch_head_kpb<DT, 8, 16>(h, stream) : launch_head_kpb<DT, 8, 8>(h, stream);
+  return wide ? launch_head_kpb<DT, 16, 16>(h, stream) : launch_head_kpb<DT, 16, 8>(h, stream);
+}
+
+}  // namespace
+}  // namespace tw
+
+extern "C" int tw_twilight_union_record_words(int P) {
+  return P > 0 ? static_cast<int>(tw::union_record_words(P)) : 0;
+}
+
+extern "C" size_t tw_twilight_select_fused_workspace_size(int G, int R, int P, int b0_pages) {
+  // the Quest score's workspace | arrival counters [G*R] (zeroed by the score
+  // launch) | logits [G*R][b0*16]
+  if (G <= 0 || R <= 0 || P <= 0 || b0_pages <= 0) return 0;
+  const size_t rows = static_cast<size_t>(G) * R;
+  return tw_quest_select_workspace_size(G, R, P) + ((rows * 4 + 255) / 256) * 256 +
+         rows * static_cast<size_t>(b0_pages) * 16 * sizeof(float);
+}
+
+extern "C" int tw_twilight_select_fused(const float* q, const void* page_min, const void* page_max, int dtype,
+                                        int G, int R, int P, int D, int64_t page_group_stride, const uint8_t* packed,
+                                        const void* qscale, const void* qmin, int64_t quant_entry_stride,
+                                        int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
+                                        int recent, int block_size, const int32_t* lengths, int length,
+                                        int32_t* sel_pages, float* logits, int32_t* desired, uint32_t* union_rec,
+                                        int64_t rec_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  if (q == nullptr || page_min == nullptr || page_max == nullptr || packed == nullptr || qscale == nullptr ||
+      qmin == nullptr || desired == nullptr || union_rec == nullptr)
+    return TW_EINVAL;
+  if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16) return TW_EUNSUPPORTED;
+  if (D != 128 || block_size != 16) return TW_EUNSUPPORTED;
+  if (G <= 0 || R <= 0 || R > 8 || P <= 0 || b0_pages <= 0 || b0_pages > P) return TW_EINVAL;
+  if (P > 16 * tw::kHeadThreads || b0_pages * 16 > 16 * tw::kHeadThreads) return TW_EUNSUPPORTED;
+  if (!(top_p > 0.0f) || !(top_p <= 1.0f) || sink < 0 || recent <= 0 || length < 0) return TW_EINVAL;
+  // every candidate row (below the group's recent window) has its INT4 code
+  if (quant_entry_stride < quant_rows || quant_rows < length || (G > 1 && quant_entry_stride <= 0)) return TW_EINVAL;
+  if (rec_stride < tw::union_record_words(P) || (rec_stride % 4) != 0 ||
+      (reinterpret_cast<uintptr_t>(union_rec) % 16) != 0)
+    return TW_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(packed) % 16) != 0) return TW_EINVAL;
+  if (workspace == nullptr || workspace_bytes < tw_twilight_select_fused_workspace_size(G, R, P, b0_pages))
+    return TW_ENOMEM;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t score_ws = tw_quest_select_workspace_size(G, R, P);
+  uint8_t* tail = static_cast<uint8_t*>(workspace) + score_ws;
+  tw::FusedScores fs{};
+  int rc = tw::fused_quest_score(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, lengths, sink, recent,
+                                 block_size, workspace, score_ws, union_rec, rec_stride,
+                                 reinterpret_cast<unsigned int*>(tail), G * R, &fs, st);
+  if (rc != TW_OK) return rc;
+  tw::HeadArgs h{};
+  h.scores = fs.scores;
+  h.score_stride = fs.score_stride;
+  h.vec_last4 = fs.vec_last4;
+  h.tile_mm = fs.tile_mm;
+  h.G = G;
+  h.R = R;
+  h.P = P;
+  h.b0 = b0_pages;
+  h.parts = (b0_pages + tw::kPartPages - 1) / tw::kPartPages;
+  h.counters = reinterpret_cast<unsigned int*>(tail);
+  h.ws_logits = reinterpret_cast<float*>(tail + ((static_cast<size_t>(G) * R * 4 + 255) / 256) * 256);
+  h.lengths = lengths;
+  h.length = length;
+  h.sink = sink;
+  h.recent = recent;
+  h.q = q;
+  h.packed = packed;
+  h.scale = qscale;
+  h.minimum = qmin;
+  h.qstride = quant_entry_stride;
+  h.qrows = quant_rows;
+  h.qk_scale = qk_scale;
+  h.p24 = static_cast<uint32_t>(__builtin_rintf(top_p * 16777216.0f));
+  h.sel_pages = sel_pages;
+  h.logits = logits;
+  h.desired = desired;
+  h.rec = union_rec;
+  h.rec_stride = rec_stride;
+  return dtype == TW_DTYPE_F16 ? tw::launch_head<tw::F16>(h, st) : tw::launch_head<tw::BF16>(h, st);
 }

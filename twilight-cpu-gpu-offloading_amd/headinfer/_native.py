@@ -87,6 +87,13 @@ _HIP_SIGNATURES = {
     "tw_decode_attention_page_rows": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32, i32, i32,
                                             vp, i32, i32, vp, vp, f32, vp, vp, i64, i32, vp, vp, vp, i64, vp, vp, szt,
                                             vp]),
+    "tw_twilight_union_record_words": (i32, [i32]),
+    "tw_twilight_select_fused_workspace_size": (szt, [i32, i32, i32, i32]),
+    "tw_twilight_select_fused": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64, i32, f32, f32,
+                                       i32, i32, i32, vp, i32, vp, vp, vp, vp, i64, vp, szt, vp]),
+    "tw_decode_attention_union": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32, i64, i32, i32, i32, vp,
+                                        i32, i32, vp, vp, f32, vp, vp, i64, i32, vp, vp, vp, i64, vp, vp, szt, i32,
+                                        vp]),
     "tw_int4_qk_positions": (i32, [vp, i32, i32, i32, vp, vp, vp, i32, i64, i64, vp, i32, f32, i32, vp, vp]),
     "tw_twilight_select_workspace_size": (szt, [i32, i32, i32]),
     "tw_twilight_max_candidates": (i32, []),

@@ -793,6 +793,92 @@ def twilight_select_pages(
                                              ws.numel(), stream_handle(dev)), "twilight_select_pages")
 
 
+def union_record_words(P: int) -> int:
+    """int32 words of one KV group's Twilight union record over P scored
+    pages: a page bitmap (whole 64-bit words), then 16-bit row masks two
+    pages a word (16-byte padded)."""
+    bits = 2 * ((P + 63) // 64)
+    return ((bits + 3) & ~3) + ((((P + 1) // 2) + 3) & ~3)
+
+
+def _check_int4_keys(packed: torch.Tensor, scale: torch.Tensor, minimum: torch.Tensor, G: int, D: int,
+                     what: str) -> int:
+    if packed.dtype != torch.uint8 or packed.ndim != 3 or packed.shape[0] != G or packed.shape[2] != D // 2:
+        raise ValueError(f"{what}: packed must be [G, T, D/2] uint8")
+    if packed.stride(2) != 1 or packed.stride(1) != D // 2 or packed.stride(0) % (D // 2):
+        raise ValueError(f"{what}: packed rows must be contiguous")
+    qe = packed.stride(0) // (D // 2)
+    if scale.dtype not in _KEY_DTYPES or minimum.dtype != scale.dtype or scale.ndim != 2 or scale.shape[0] != G:
+        raise ValueError(f"{what}: scale/minimum must be [G, T] in one key dtype")
+    if scale.stride(1) != 1 or minimum.stride(1) != 1 or scale.stride(0) != qe or minimum.stride(0) != qe:
+        raise ValueError(f"{what}: scale/minimum must share the packed entry stride")
+    return qe
+
+
+def twilight_select_fused(
+    q: torch.Tensor,
+    page_min: torch.Tensor,
+    page_max: torch.Tensor,
+    packed: torch.Tensor,
+    scale: torch.Tensor,
+    minimum: torch.Tensor,
+    b0_pages: int,
+    union_rec: torch.Tensor,
+    *,
+    top_p: float,
+    sink: int,
+    recent: int,
+    block_size: int = 16,
+    length: int = 0,
+    lengths: Optional[torch.Tensor] = None,
+    qk_scale: Optional[float] = None,
+    desired: Optional[torch.Tensor] = None,
+    sel_pages: Optional[torch.Tensor] = None,
+    logits: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """The Twilight selection of a layer with dynamic budgets in two launches
+    (Quest score; one block per head: B0 top-k, INT4 QK, top-p, publish),
+    written to each group's union record: union_rec [G, >= union_record_words
+    (P)] int32 (row stride a multiple of 4, 16-byte aligned).  q [G, R, 128]
+    fp32; page_min/page_max [G, >= P, 128] over the P scored pages (16-bit);
+    packed/scale/minimum the INT4 keys.  lengths [G] int32 (device) for ragged
+    groups, each clamped to `length`; else every group has `length` tokens.
+    Returns desired [G, R] int32 (the top-p counts); sel_pages [G, R,
+    b0_pages] and logits [G, R, b0_pages * 16] are optional outputs."""
+    _check_score_inputs(q, page_min, page_max, "twilight_select_fused")
+    G, R, D = q.shape
+    P = page_min.shape[1]
+    qe = _check_int4_keys(packed, scale, minimum, G, D, "twilight_select_fused")
+    if not 1 <= b0_pages <= P:
+        raise ValueError("b0_pages must be in [1, P]")
+    if union_rec.dtype != torch.int32 or union_rec.ndim != 2 or union_rec.shape[0] != G \
+            or union_rec.shape[1] < union_record_words(P) or union_rec.stride(1) != 1 or union_rec.stride(0) % 4 \
+            or union_rec.data_ptr() % 16:
+        raise ValueError("union_rec must be [G, >= union_record_words(P)] int32, rows 16-byte aligned")
+    if lengths is not None and (lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,)
+                                or not lengths.is_contiguous()):
+        raise ValueError("lengths must be contiguous [G] int32")
+    dev = _require_device(q, page_min, page_max, packed, scale, minimum, union_rec, lengths, desired, sel_pages,
+                          logits, what="twilight_select_fused")
+    if desired is None:
+        desired = torch.empty((G, R), dtype=torch.int32, device=dev)
+    for t, dt, shape in ((desired, torch.int32, (G, R)), (sel_pages, torch.int32, (G, R, b0_pages)),
+                         (logits, torch.float32, (G, R, b0_pages * block_size))):
+        if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
+            raise ValueError("twilight_select_fused output has the wrong dtype/shape")
+    qs = float(torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32)) if qk_scale is None else float(qk_scale)
+    nbytes = hip().tw_twilight_select_fused_workspace_size(G, R, P, int(b0_pages))
+    ws = WORKSPACE.get(dev, "twilight_fused", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_twilight_select_fused(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
+                                             page_min.stride(0), ptr(packed), ptr(scale), ptr(minimum), qe,
+                                             packed.shape[1], int(b0_pages), float(top_p), qs, sink, recent,
+                                             block_size, ptr(lengths), int(length), ptr(sel_pages), ptr(logits),
+                                             ptr(desired), ptr(union_rec), union_rec.stride(0), ptr(ws), ws.numel(),
+                                             stream_handle(dev)), "twilight_select_fused")
+    return desired
+
+
 # --------------------------------------------------------------- attention
 def decode_attention_rows(
     q: torch.Tensor,
@@ -1242,6 +1328,90 @@ def decode_attention_page_rows(
                                                   ptr(packed), ptr(scale), ptr(minimum),
                                                   0 if scale is None else scale.stride(0), ptr(out), ptr(ws),
                                                   ws.numel(), stream_handle(dev)), "decode_attention_page_rows")
+    return out
+
+
+def decode_attention_union(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    union_rec: torch.Tensor,
+    P: int,
+    *,
+    max_pages: int,
+    sink: int,
+    recent: int,
+    block_size: int = 16,
+    lengths: Optional[torch.Tensor] = None,
+    length: int = 0,
+    append: bool = True,
+    cur_k: Optional[torch.Tensor] = None,
+    cur_v: Optional[torch.Tensor] = None,
+    softmax_scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+    page_min: Optional[torch.Tensor] = None,
+    page_max: Optional[torch.Tensor] = None,
+    packed: Optional[torch.Tensor] = None,
+    scale: Optional[torch.Tensor] = None,
+    minimum: Optional[torch.Tensor] = None,
+    phase: int = 3,
+) -> torch.Tensor:
+    """The Twilight union attention from the union records of
+    twilight_select_fused over P pages: every head attends the kept rows of
+    the union pages, the sink and recent windows and the decode token.
+    max_pages bounds a group's union pages (min(P, R * b0_pages)); the other
+    arguments as decode_attention_page_rows.  Returns [G, R, D]."""
+    if phase not in (1, 2, 3):
+        raise ValueError("phase must be 1, 2 or 3")
+    if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("q must be [G, R, D] fp16/bf16")
+    G, R, D = q.shape
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype or k_cache.shape != v_cache.shape \
+            or k_cache.ndim != 3 or k_cache.shape[0] != G or k_cache.shape[2] != D \
+            or k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1 or k_cache.stride(1) != D \
+            or k_cache.stride(0) % D:
+        raise ValueError("K/V cache must be row-contiguous [G, Lmax, D] in q's dtype")
+    if not 1 <= P <= 8192:
+        raise ValueError("P must be in [1, 8192]")
+    if union_rec.dtype != torch.int32 or union_rec.ndim != 2 or union_rec.shape[0] != G \
+            or union_rec.shape[1] < union_record_words(P) or union_rec.stride(1) != 1 or union_rec.stride(0) % 4 \
+            or union_rec.data_ptr() % 16:
+        raise ValueError("union_rec must be [G, >= union_record_words(P)] int32, rows 16-byte aligned")
+    if lengths is not None and (lengths.dtype != torch.int32 or tuple(lengths.shape) != (G,)
+                                or not lengths.is_contiguous()):
+        raise ValueError("lengths must be contiguous [G] int32")
+    if lengths is None and not 0 <= int(length) < k_cache.shape[1]:
+        raise ValueError("length must leave the decode row inside the cache")
+    if (cur_k is None) != (cur_v is None):
+        raise ValueError("cur_k and cur_v go together")
+    if cur_k is not None and (cur_k.shape != (G, D) or cur_k.dtype != q.dtype or cur_v.shape != cur_k.shape
+                              or cur_v.dtype != q.dtype):
+        raise ValueError("cur_k/cur_v must be [G, D] in q's dtype")
+    if packed is not None and (scale is None or minimum is None or cur_k is None or not append
+                               or packed.dtype != torch.uint8 or packed.ndim != 3 or packed.shape[0] != G
+                               or packed.shape[2] != D // 2 or packed.stride(2) != 1 or packed.stride(1) != D // 2
+                               or scale.ndim != 2 or scale.shape[0] != G or scale.stride(1) != 1
+                               or minimum.stride() != scale.stride() or scale.dtype != q.dtype
+                               or minimum.dtype != q.dtype or packed.stride(0) // (D // 2) != scale.stride(0)):
+        raise ValueError("packed [G, T, D/2] uint8 and scale/minimum [G, T] must match (with cur_k and append)")
+    dev = _require_device(q, union_rec, lengths, cur_k, cur_v, page_min, page_max, packed, scale, minimum,
+                          what="decode_attention_union")
+    meta = _page_meta_args(page_min, page_max, G, D, append)
+    kp, vp = _slab_source(k_cache, v_cache)
+    _require_contiguous(q, cur_k, cur_v, what="decode_attention_union")
+    if out is None:
+        out = torch.empty_like(q)
+    sc = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
+    max_rows = sink + max(0, max_pages) * block_size + recent
+    nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
+    ws = WORKSPACE.get(dev, "decode_attention", nbytes)
+    with torch.cuda.device(dev):
+        check(hip().tw_decode_attention_union(ptr(q), kp, vp, _dt(q), G, R, D, ptr(union_rec), union_rec.stride(0),
+                                              P, max_rows, k_cache.stride(0) // D, sink, recent, block_size,
+                                              ptr(lengths), int(length), int(bool(append)), ptr(cur_k), ptr(cur_v),
+                                              sc, *meta, ptr(packed), ptr(scale), ptr(minimum),
+                                              0 if scale is None else scale.stride(0), ptr(out), ptr(ws), ws.numel(),
+                                              int(phase), stream_handle(dev)), "decode_attention_union")
     return out
 
 
