@@ -195,6 +195,12 @@ class GraphDecoder:
                               and cache.dtype in (torch.float16, torch.bfloat16))
             self.tw_slot_u = torch.zeros((self.G, self.R, self.k), dtype=torch.int32, device=dev)
             self.tw_prows = torch.zeros((self.G, self.width), dtype=torch.int32, device=dev)
+            # the fused selection (score; B0 + INT4 QK + top-p per head) into a
+            # union record per KV group, read by the union attention
+            self.fused = self.page_rows and self.P <= 8192 and n_cand <= 8192
+            words = (kernels.union_record_words(self.P) + 3) & ~3
+            self.tw_rec = torch.zeros((self.G, words), dtype=torch.int32, device=dev)
+            self.tw_desired = torch.zeros((self.G, self.R), dtype=torch.int32, device=dev)
         self.logits: Optional[torch.Tensor] = None
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
@@ -328,6 +334,27 @@ class GraphDecoder:
         G, R, D = self.G, self.R, self.D
         e0 = li * G
         q32 = self.q32.view(G, R, D)
+        if self.fused:
+            kernels.twilight_select_fused(q32, c._page_min[e0:e0 + G, :self.P], c._page_max[e0:e0 + G, :self.P],
+                                          c._packed[e0:e0 + G], c._qscale[e0:e0 + G], c._qmin[e0:e0 + G], self.k,
+                                          self.tw_rec, top_p=c.top_p, sink=c.sink_tokens, recent=c.recent_tokens,
+                                          block_size=c.block_size, length=self.max_length, lengths=self.lengths,
+                                          desired=self.tw_desired)
+            # the attention also appends the decode token and (fused) its INT4 row and page metadata
+            meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G],
+                        packed=c._packed[e0:e0 + G], scale=c._qscale[e0:e0 + G],
+                        minimum=c._qmin[e0:e0 + G]) if self.fuse else {}
+            kernels.decode_attention_union(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], self.tw_rec,
+                                           self.P, max_pages=self.width, sink=c.sink_tokens,
+                                           recent=c.recent_tokens, block_size=c.block_size, lengths=self.lengths,
+                                           append=True, cur_k=k, cur_v=v, softmax_scale=float(attn.scaling),
+                                           out=self.attn[li], **meta)
+            if not self.fuse:
+                kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
+                                                    block_size=c.block_size, page_min=c._page_min,
+                                                    page_max=c._page_max, packed=c._packed, scale=c._qscale,
+                                                    minimum=c._qmin)
+            return
         kernels.quest_select_ragged(q32, c._page_min[e0:e0 + G, :self.P], c._page_max[e0:e0 + G, :self.P],
                                     self.lengths, self.k, sink=c.sink_tokens, recent=c.recent_tokens,
                                     block_size=c.block_size, sel_pages=self.tw_sel, plan_pages=pp, plan_masks=pm,
