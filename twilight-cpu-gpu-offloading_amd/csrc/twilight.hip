@@ -1407,7 +1407,7 @@ __device__ bool block_top_p_fast(const uint32_t (&key)[KPT], const uint64_t (&ma
                                  int* count_out) {
   constexpr int kBins = kFastBins;
   constexpr int kBpl = kBins / kWave;  // bins per lane
-  static_assert(kBpl == 8, "two 16-byte count reads and four mass reads per lane");
+  static_assert(kBpl % 8 == 0, "whole 16-byte count and mass reads per lane");
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
   const int i0 = KPT * tid;
@@ -1432,13 +1432,18 @@ __device__ bool block_top_p_fast(const uint32_t (&key)[KPT], const uint64_t (&ma
   uint32_t hc[kBpl];
   uint64_t hm[kBpl];
   {
-    const uint4* c4 = reinterpret_cast<const uint4*>(sh.sel.hist) + 2 * lane;
-    const uint4 a0 = c4[0], a1 = c4[1];
-    hc[0] = a0.x; hc[1] = a0.y; hc[2] = a0.z; hc[3] = a0.w;
-    hc[4] = a1.x; hc[5] = a1.y; hc[6] = a1.z; hc[7] = a1.w;
-    const ulonglong2* m2 = reinterpret_cast<const ulonglong2*>(sh.bin_mass) + 4 * lane;
+    const uint4* c4 = reinterpret_cast<const uint4*>(sh.sel.hist) + (kBpl / 4) * lane;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kBpl / 4; ++q) {
+      const uint4 v = c4[q];
+      hc[4 * q] = v.x;
+      hc[4 * q + 1] = v.y;
+      hc[4 * q + 2] = v.z;
+      hc[4 * q + 3] = v.w;
+    }
+    const ulonglong2* m2 = reinterpret_cast<const ulonglong2*>(sh.bin_mass) + (kBpl / 2) * lane;
+#pragma unroll
+    for (int q = 0; q < kBpl / 2; ++q) {
       const ulonglong2 v = m2[q];
       hm[2 * q] = v.x;
       hm[2 * q + 1] = v.y;
@@ -1807,6 +1812,7 @@ struct HeadArgs {
   uint32_t p24;
   unsigned int* counters;  // [G * R] arrival counters (zero between launches)
   float* ws_logits;        // [G * R][b0 * 16] the rows' logits, handed to the last block
+  uint32_t* ws_range;      // [G * R][parts * 8][4] each wavefront's (max logit, max key, min key, 0)
   int32_t* sel_pages;    // nullable [G][R][b0]: B0 pages ascending, -1 past a ragged group's
   float* logits;         // nullable [G][R][b0 * 16]
   int32_t* desired;      // [G][R]
@@ -1938,6 +1944,8 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a)
     const S* mn = static_cast<const S*>(a.minimum) + static_cast<int64_t>(g) * a.qstride;
     uint4 cw[BT];
     S sv[BT], mv[BT];
+    float wmax = -INFINITY;
+    uint32_t wkmax = 0u, wkmin = 0xffffffffu;
     // pages part * kPartPages + wave + kWv * j (clamped into the B0 pages)
 #pragma unroll
     for (int j = 0; j < BT; ++j) {
@@ -1966,9 +1974,25 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a)
       c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[1], b1v, c, 0, 0, 0);
       if (lane < 16 && s < b0) {
         const int64_t Sd = (static_cast<int64_t>(c[0]) << 16) + (static_cast<int64_t>(c[1]) << 8) + c[2];
-        publish_f32(wl + s * BS + lane,
-                    qk_logit(Sd, qshift, qsum, qok, to_f32(DT{}, sv[j]), to_f32(DT{}, mv[j]), a.qk_scale));
+        const float lg = qk_logit(Sd, qshift, qsum, qok, to_f32(DT{}, sv[j]), to_f32(DT{}, mv[j]), a.qk_scale);
+        publish_f32(wl + s * BS + lane, lg);
+        const uint32_t k = score_key(lg);
+        wmax = lg > wmax ? lg : wmax;
+        wkmax = k > wkmax ? k : wkmax;
+        wkmin = k < wkmin ? k : wkmin;
       }
+    }
+    // the wavefront's largest logit and key range, for the last block
+    wmax = wave_max_f32(wmax);
+    wkmax = wave_max_u32(wkmax);
+    wkmin = wave_min_u32(wkmin);
+    if (lane == 0) {
+      uint32_t* wr = a.ws_range + (static_cast<int64_t>(row) * a.parts * kWv + part * kWv + wave) * 4;
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(wr),
+                         static_cast<uint64_t>(__float_as_uint(wmax)) | (static_cast<uint64_t>(wkmax) << 32),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(wr + 2), static_cast<uint64_t>(wkmin), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (!arrive_last(a.counters + row, static_cast<unsigned int>(a.parts), &sh.sel.flag)) return;
@@ -1978,6 +2002,8 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a)
   float lmax;
   uint32_t kmin, kmax;
   {
+    // the row's logits and every part wavefront's range, one round trip; each
+    // wavefront reduces the ranges itself (no barrier)
     const int i0 = KPB * tid;
     float v[KPB];
 #pragma unroll
@@ -1987,41 +2013,38 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a)
       v[j] = t.x;
       v[j + 1] = t.y;
     }
-    float mx = -INFINITY;
-    uint32_t kmx = 0u, kmn = 0xffffffffu;
+    const int n_rng = a.parts * kWv;  // <= 128
+    const uint32_t* rr = a.ws_range + static_cast<int64_t>(row) * n_rng * 4;
+    uint64_t r0[2], r1[2];
 #pragma unroll
-    for (int j = 0; j < KPB; ++j) {
-      const bool ok = i0 + j < N;
-      lkey[j] = score_key(v[j]);
-      mx = (ok && v[j] > mx) ? v[j] : mx;
-      kmx = (ok && lkey[j] > kmx) ? lkey[j] : kmx;
-      kmn = (ok && lkey[j] < kmn) ? lkey[j] : kmn;
+    for (int h = 0; h < 2; ++h) {
+      const int e = lane + kWave * h < n_rng ? lane + kWave * h : n_rng - 1;
+      r0[h] = __hip_atomic_load(reinterpret_cast<const uint64_t*>(rr + 4 * e), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+      r1[h] = __hip_atomic_load(reinterpret_cast<const uint64_t*>(rr + 4 * e + 2), __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
     }
+#pragma unroll
+    for (int j = 0; j < KPB; ++j) lkey[j] = score_key(v[j]);
     if (a.logits != nullptr) {
       float* lo = a.logits + static_cast<int64_t>(row) * a.b0 * BS;
 #pragma unroll
       for (int j = 0; j < KPB; ++j)
         if (i0 + j < N) lo[i0 + j] = v[j];
     }
-    mx = wave_max_f32(mx);
-    kmx = wave_max_u32(kmx);
-    kmn = wave_min_u32(kmn);
-    if (lane == 0) {
-      sh.fred[wave] = mx;
-      sh.sel.red_max[wave] = kmx;
-      sh.sel.red_min[wave] = kmn;
-    }
-    __syncthreads();
-    lmax = sh.fred[0];
-    kmax = sh.sel.red_max[0];
-    kmin = sh.sel.red_min[0];
+    float mx = -INFINITY;
+    uint32_t kmx = 0u, kmn = 0xffffffffu;
 #pragma unroll
-    for (int w = 1; w < kWv; ++w) {
-      lmax = fmaxf(lmax, sh.fred[w]);
-      kmax = sh.sel.red_max[w] > kmax ? sh.sel.red_max[w] : kmax;
-      kmin = sh.sel.red_min[w] < kmin ? sh.sel.red_min[w] : kmin;
+    for (int h = 0; h < 2; ++h) {
+      const float m = __uint_as_float(static_cast<uint32_t>(r0[h]));
+      const uint32_t kx = static_cast<uint32_t>(r0[h] >> 32), kn = static_cast<uint32_t>(r1[h]);
+      mx = m > mx ? m : mx;
+      kmx = kx > kmx ? kx : kmx;
+      kmn = kn < kmn ? kn : kmn;
     }
-    __syncthreads();
+    lmax = wave_max_f32(mx);
+    kmax = wave_max_u32(kmx);
+    kmin = wave_min_u32(kmn);
   }
   uint64_t mass[KPB];
   uint64_t local = 0;
@@ -2373,11 +2396,12 @@ extern "C" int tw_twilight_union_record_words(int P) {
 
 extern "C" size_t tw_twilight_select_fused_workspace_size(int G, int R, int P, int b0_pages) {
   // the Quest score's workspace | arrival counters [G*R] (zeroed by the score
-  // launch) | logits [G*R][b0*16]
+  // launch) | logits [G*R][b0*16] | wavefront ranges [G*R][parts*8][4]
   if (G <= 0 || R <= 0 || P <= 0 || b0_pages <= 0) return 0;
   const size_t rows = static_cast<size_t>(G) * R;
+  const size_t parts = static_cast<size_t>((b0_pages + tw::kPartPages - 1) / tw::kPartPages);
   return tw_quest_select_workspace_size(G, R, P) + ((rows * 4 + 255) / 256) * 256 +
-         rows * static_cast<size_t>(b0_pages) * 16 * sizeof(float);
+         ((rows * static_cast<size_t>(b0_pages) * 16 * sizeof(float) + 255) / 256) * 256 + rows * parts * 8 * 16;
 }
 
 extern "C" int tw_twilight_select_fused(const float* q, const void* page_min, const void* page_max, int dtype,
@@ -2422,7 +2446,10 @@ extern "C" int tw_twilight_select_fused(const float* q, const void* page_min, co
   h.b0 = b0_pages;
   h.parts = (b0_pages + tw::kPartPages - 1) / tw::kPartPages;
   h.counters = reinterpret_cast<unsigned int*>(tail);
-  h.ws_logits = reinterpret_cast<float*>(tail + ((static_cast<size_t>(G) * R * 4 + 255) / 256) * 256);
+  const size_t cnt_bytes = ((static_cast<size_t>(G) * R * 4 + 255) / 256) * 256;
+  const size_t log_bytes = ((static_cast<size_t>(G) * R * b0_pages * 16 * sizeof(float) + 255) / 256) * 256;
+  h.ws_logits = reinterpret_cast<float*>(tail + cnt_bytes);
+  h.ws_range = reinterpret_cast<uint32_t*>(tail + cnt_bytes + log_bytes);
   h.lengths = lengths;
   h.length = length;
   h.sink = sink;
