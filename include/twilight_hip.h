@@ -372,8 +372,8 @@ size_t tw_twilight_select_fused_workspace_size(int G, int R, int P, int b0_pages
  * clears first.  No union plan or row list is built.
  *   q [G][R][128] fp32; page_min/page_max as tw_quest_select (P pages,
  *   16-bit); packed / qscale / qmin the INT4 keys of tw_build_page_metadata
- *   (quant_entry_stride rows apart, quant_rows >= length valid rows, packed
- *   16-byte aligned); qk_scale the logit scale (1/sqrt(D) in the reference);
+ *   (quant_entry_stride rows apart, quant_rows >= sink + 16*P valid rows,
+ *   packed 16-byte aligned); qk_scale the logit scale (1/sqrt(D) in the reference);
  *   lengths (nullable, device [G] int32): group g has min(lengths[g],
  *   length) tokens, so its own candidate pages P_g <= P and min(b0_pages,
  *   P_g) B0 pages; else every group has `length` tokens and P candidate

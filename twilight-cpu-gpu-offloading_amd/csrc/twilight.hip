@@ -2419,8 +2419,10 @@ extern "C" int tw_twilight_select_fused(const float* q, const void* page_min, co
   if (G <= 0 || R <= 0 || R > 8 || P <= 0 || b0_pages <= 0 || b0_pages > P) return TW_EINVAL;
   if (P > 16 * tw::kHeadThreads || b0_pages * 16 > 16 * tw::kHeadThreads) return TW_EUNSUPPORTED;
   if (!(top_p > 0.0f) || !(top_p <= 1.0f) || sink < 0 || recent <= 0 || length < 0) return TW_EINVAL;
-  // every candidate row (below the group's recent window) has its INT4 code
-  if (quant_entry_stride < quant_rows || quant_rows < length || (G > 1 && quant_entry_stride <= 0)) return TW_EINVAL;
+  // every candidate row (a page below P, so a row below sink + 16 P) has its INT4 code
+  if (quant_entry_stride < quant_rows || quant_rows < static_cast<int64_t>(sink) + 16ll * P ||
+      (G > 1 && quant_entry_stride <= 0))
+    return TW_EINVAL;
   if (rec_stride < tw::union_record_words(P) || (rec_stride % 4) != 0 ||
       (reinterpret_cast<uintptr_t>(union_rec) % 16) != 0)
     return TW_EINVAL;

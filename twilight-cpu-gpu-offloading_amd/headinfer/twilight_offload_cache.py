@@ -373,6 +373,9 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         self._group_union_trace: list[dict[str, Any]] = []
         self._budget_trace: list[dict[str, Any]] = []
         self._capture_budget_trace = False
+        # decode_layer with dynamic budgets runs the fused selection (union
+        # record) when the shapes allow; False keeps the union-row path
+        self.fused_decode = True
         self._flat_union_keys: Optional[torch.Tensor] = None
         self._flat_union_values: Optional[torch.Tensor] = None
         self._dma = None  # HostGatherPipeline of post_selection_pipeline (host slabs)
@@ -661,6 +664,9 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         self._seen_tokens = self._bookkeeping.seen_tokens
         old_length = self._logical_lengths[entries[0]] - 1
         self._wait_host_writes(entries)
+        fused = self._decode_layer_fused(queries, key_states, value_states, entries, old_length, softmax_scale, out)
+        if fused is not None:
+            return fused
         state = self._select_layer(entries, queries.float().contiguous(), old_length)
         self._trace_layer(state)
         e0 = entries[0]
@@ -672,6 +678,50 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
                                                self._value_cache[e0:e0 + G], state["rows"], state["counts"],
                                                state["max_count"], cur_k=cur_k, cur_v=cur_v,
                                                softmax_scale=softmax_scale, out=out, append_position=old_length)
+        self._phase_end("attention", start)
+        self._append(entries, cur_k, cur_v, old_length, written=True)
+        for e in entries:
+            self._last_query_head_lengths[e] = None
+        return result
+
+    def _decode_layer_fused(self, queries: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
+                            entries: Sequence[int], old_length: int, softmax_scale: Optional[float],
+                            out: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        """decode_layer with dynamic budgets in two selection launches: the
+        Quest score, then per (group, head) the B0 top-k, INT4 QK and top-p
+        into the group's union record, and the attention over its kept rows
+        (the same token set as the union row list).  None when the layer
+        takes the general path: other budget modes or shapes, or traces that
+        record the row list."""
+        G, R, D = queries.shape
+        if (not self.fused_decode or self.budget_mode != "dynamic" or R > 8 or D != 128 or self.block_size != 16
+                or self.dtype not in (torch.float16, torch.bfloat16) or self._capture_selection_trace
+                or self._capture_budget_trace or self._page_min is None or self._packed is None):
+            return None
+        sink_end, recent_start, cand, fixed, b0 = self._twilight_budgets(old_length)
+        if cand == 0 or fixed == 0 or b0 == 0 or cand > 8192 or b0 * self.block_size > 8192:
+            return None
+        pmin, pmax = self._metadata(entries, cand)
+        packed, qscale, qmin = self._quant(entries)
+        if packed.shape[1] < self.sink_tokens + cand * self.block_size:
+            return None
+        words = (kernels.union_record_words(cand) + 3) & ~3
+        rec = torch.empty((G, words), dtype=torch.int32, device=self.device)
+        desired = torch.empty((G, R), dtype=torch.int32, device=self.device)
+        start = self._phase_start()
+        kernels.twilight_select_fused(queries.float().contiguous(), pmin, pmax, packed, qscale, qmin, b0, rec,
+                                      top_p=self.top_p, sink=self.sink_tokens, recent=self.recent_tokens,
+                                      block_size=self.block_size, length=old_length, desired=desired)
+        self._phase_end("twilight_fused_selection", start)
+        e0 = entries[0]
+        cur_k, cur_v = key_states.contiguous(), value_states.contiguous()
+        start = self._phase_start()
+        result = kernels.decode_attention_union(queries.contiguous(), self._key_cache[e0:e0 + G],
+                                                self._value_cache[e0:e0 + G], rec, cand,
+                                                max_pages=min(cand, R * b0), sink=self.sink_tokens,
+                                                recent=self.recent_tokens, block_size=self.block_size,
+                                                length=old_length, append=True, cur_k=cur_k, cur_v=cur_v,
+                                                softmax_scale=softmax_scale, out=out)
         self._phase_end("attention", start)
         self._append(entries, cur_k, cur_v, old_length, written=True)
         for e in entries:
