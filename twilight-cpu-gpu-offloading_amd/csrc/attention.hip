@@ -1300,6 +1300,10 @@ __device__ __forceinline__ TileSrc tile_src(const AttnArgs& a, const TileWin& w,
 // lane) instead of a union plan.
 // MK (with NWL > 0): the union comes from a Twilight union record (one
 // bitmap row, row masks staged in LDS by the block).
+// Key rows are loaded like value rows (four whole 256-byte rows per load,
+// 1 KB contiguous) and turned into matrix-core fragments through LDS.  Loads
+// shaped as the fragments (16 rows x 64 B each) read pinned host memory at
+// ~41 GB/s against ~51 GB/s for whole rows, and HBM slower too.
 template <typename DT, int RMAX, int NW, int TW, bool RES, bool NT, int NWL, bool MK = false>
 __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   using S = typename DT::storage;
@@ -1323,6 +1327,9 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   __shared__ float s_l[NW][RMAX];
   __shared__ __align__(16) uint32_t s_p[NW][TW][8][RMAX];
   __shared__ __align__(16) float s_o[NW][RMAX][D];
+  // each wavefront's key tiles, 16-byte unit c of row r at [r][c ^ r] (whole
+  // rows written and fragment columns read without bank conflicts)
+  __shared__ __align__(16) uint4 s_k[NW][TW][kTileRows][D / 8];
 
   // ---- round trip 1: plan count, the first batch's page slots, q ----
   const int64_t plan_base = static_cast<int64_t>(g) * a.plan_stride;
@@ -1505,22 +1512,35 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       const S* vt = hit ? static_cast<const S*>(a.res_v) : vg;
       // rows outside the tile or not kept read a kept row (the same lines,
       // no extra traffic) and are masked below
-      const int kr = (krow < ts[tt].cnt && ((ts[tt].rm >> krow) & 1u)) ? krow : ts[tt].r0;
-      const S* kp = krow == ts[tt].dec ? kdec : kt + tb + kr * D;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        kf[tt][s] = NT ? load_stream(kp + 32 * s + 8 * quarter)
-                       : *reinterpret_cast<const uint4*>(kp + 32 * s + 8 * quarter);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * rg + j;
         const int vr = (r < ts[tt].cnt && ((ts[tt].rm >> r) & 1u)) ? r : ts[tt].r0;
-        const S* vp = r == ts[tt].dec ? vdec : vt + tb + vr * D;
-        vf[tt][j] = NT ? load_stream(vp + c8) : *reinterpret_cast<const uint4*>(vp + c8);
+        const int64_t ro = tb + static_cast<int64_t>(vr) * D + c8;
+        const S* vp = r == ts[tt].dec ? vdec + c8 : vt + ro;
+        vf[tt][j] = NT ? load_stream(vp) : *reinterpret_cast<const uint4*>(vp);
+        // key row r, channels c8..c8+7, until the LDS pass below
+        const S* kp = r == ts[tt].dec ? kdec + c8 : kt + ro;
+        kf[tt][j] = NT ? load_stream(kp) : *reinterpret_cast<const uint4*>(kp);
       }
     }
     // the next batch's page slots ride in the same round trip
     if (NWL == 0 && it + 1 < a.iters) load_slots(t0 + NW * TW, page_nx, pmask_nx, prow_nx);
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * rg + j;
+        s_k[wave][tt][r][(lane & 15) ^ r] = kf[tt][j];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's key rows are in LDS
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[tt][s] = s_k[wave][tt][krow][(4 * s + quarter) ^ krow];
+    }
     // ---- q.k on the matrix cores; scores in log2 units ----
     float sc[TW][4];
 #pragma unroll
