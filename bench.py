@@ -311,10 +311,11 @@ class TwilightWorkload:
         self.page_rows = budget_mode == "dynamic" and path == "pages"
         self.slot_u = torch.zeros((layers, G, R, self.b0), dtype=i32, device=dev)
         self.prows = torch.zeros((layers, G, self.width), dtype=i32, device=dev)
-        # dynamic budgets, fused: two selection launches (score; per-head B0 +
-        # INT4 QK + top-p) writing each group's union record
-        self.fused = budget_mode == "dynamic" and path == "fused"
-        self.path = path if budget_mode == "dynamic" else "rows"
+        # fused: two selection launches (score; per-head B0 + INT4 QK + top-p)
+        # writing each group's union record, and with matched budgets a third
+        # (allocation and each head's top-allocated rows)
+        self.fused = path == "fused"
+        self.path = path if budget_mode == "dynamic" or path == "fused" else "rows"
         words = (kernels.union_record_words(self.P) + 3) & ~3
         self.rec = torch.zeros((layers, G, words), dtype=i32, device=dev)
         torch.cuda.synchronize(dev)
@@ -326,7 +327,9 @@ class TwilightWorkload:
             kernels.twilight_select_fused(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P],
                                           self.packed[layer], self.scale[layer], self.minimum[layer], self.b0,
                                           self.rec[layer], top_p=self.TOP_P, sink=self.SINK, recent=self.RECENT,
-                                          block_size=self.BS, length=self.L, desired=self.desired[layer])
+                                          block_size=self.BS, length=self.L, desired=self.desired[layer],
+                                          budget_mode=self.mode,
+                                          target_total=self.fixed * self.BS * self.R if self.mode == "matched" else 0)
             return
         kernels.quest_select(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P], self.b0,
                              sel_pages=self.sel[layer], plan_pages=self.plan_pages[layer],
@@ -412,6 +415,8 @@ class TwilightWorkload:
             cand_rows = G * R * N
             select = (2 * P * D * e * G + G * R * P * 4 * 2 + cand_rows * (D // 2 + 2 * e) + G * R * D * 4
                       + G * self.rec.shape[2] * 4)
+            if self.mode == "matched":  # the allocation launch reads the logits back
+                select += G * R * N * 4
         else:
             cand_rows = self.plan_counts.double().sum().item() * self.BS / self.layers   # union of the B0 candidates
             select = (2 * P * D * e * G + G * R * P * 4 * 2 + G * R * self.b0 * 4 + cand_rows * (D // 2 + 2 * e)
@@ -850,7 +855,8 @@ def run_twilight(args, dev) -> int:
     return 0 if result["parity"]["ok"] else 1
 
 
-_TW_PATHS = {"fused": "score + per-head B0/INT4 QK/top-p launch into a union record, attention over its row masks",
+_TW_PATHS = {"fused": "score + per-head B0/INT4 QK/top-p launch (+ the matched allocation launch) into a union "
+                      "record, attention over its row masks",
              "pages": "over the B0 union pages row masks", "rows": "over the union row list"}
 
 

@@ -395,6 +395,28 @@ int tw_twilight_select_fused(const float* q, const void* page_min, const void* p
                              uint32_t* union_rec, int64_t rec_stride, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* tw_twilight_select_fused with matched budgets, in three launches: the
+ * score, the per-head B0 + INT4 QK + top-p launch (desired counts, no
+ * record), then one block per (group, head) that forms the group's
+ * allocation (matched_budget_counts of the desired counts towards
+ * target_total, twilight_offload_cache.py:50-86, the same as
+ * tw_twilight_select in matched mode), keeps the head's top-allocated
+ * candidates by logit (ties to the lower candidate) and ORs their rows into
+ * the union record.  Every group has `length` tokens (no ragged lengths);
+ * sel_pages is required (the last launch reads it); R <= target_total <=
+ * R*b0_pages*16.  Outputs as tw_twilight_select_fused plus allocated [G][R]
+ * (nullable).  Workspace: tw_twilight_select_fused_workspace_size.
+ * Replaces prepare_layer_selection's stages 1-2, the matched reallocation
+ * and the GPU GQA union of the matched path (twilight_offload_cache.py:
+ * 996-1614). */
+int tw_twilight_select_fused_matched(const float* q, const void* page_min, const void* page_max, int dtype, int G,
+                                     int R, int P, int D, int64_t page_group_stride, const uint8_t* packed,
+                                     const void* qscale, const void* qmin, int64_t quant_entry_stride,
+                                     int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
+                                     int recent, int block_size, int length, int target_total, int32_t* sel_pages,
+                                     float* logits, int32_t* desired, int32_t* allocated, uint32_t* union_rec,
+                                     int64_t rec_stride, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Sparse GQA decode attention, split-K over selected rows, one query
  * token per group.  Replaces _flash_attention_varlen_forward

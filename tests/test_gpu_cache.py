@@ -370,17 +370,20 @@ def test_twilight_decode_metadata_update(H, dev):
     assert late > 0
 
 
-@pytest.mark.parametrize("residency,dtype,fused", [("hbm", "f16", True), ("host", "bf16", True),
-                                                   ("hbm", "bf16", False)])
-def test_twilight_decode_layer(H, dev, residency, dtype, fused):
-    """decode_layer with dynamic budgets: every head of a group attends the
-    oracle's group union ++ the decode token (float64 reference), through the
-    fused selection (union record) or the union-row path, and the decode
-    tokens land in the slab."""
+@pytest.mark.parametrize("residency,dtype,fused,mode", [("hbm", "f16", True, "dynamic"), ("host", "bf16", True, "dynamic"),
+                                                        ("hbm", "bf16", False, "dynamic"),
+                                                        ("hbm", "bf16", True, "matched"),
+                                                        ("host", "f16", True, "matched"),
+                                                        ("hbm", "f16", False, "matched")])
+def test_twilight_decode_layer(H, dev, residency, dtype, fused, mode):
+    """decode_layer: every head of a group attends the oracle's group union ++
+    the decode token (float64 reference), with dynamic or matched budgets,
+    through the fused selection (union record) or the union-row path, and the
+    decode tokens land in the slab."""
     G, R, D, T, steps = 4, 4, 128, 3000, 3
-    _say(f"[twilight decode_layer] {residency} {dtype} fused={fused}")
-    cache = _twilight_cache(H, dev, E=G, T=T, D=D, R=R, dtype=dtype, residency=residency, mode="dynamic",
-                            candidate_token_budget=512, top_p=0.9)
+    _say(f"[twilight decode_layer] {residency} {dtype} fused={fused} {mode}")
+    cache = _twilight_cache(H, dev, E=G, T=T, D=D, R=R, dtype=dtype, residency=residency, mode=mode,
+                            candidate_token_budget=512, top_p=0.9, matched_budget_fraction=0.05)
     cache.fused_decode = fused
     model = _Model(G, T, D, dtype, seed=51, scale=2.0)
     model.prefill(cache, dev)

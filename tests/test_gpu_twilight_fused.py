@@ -214,3 +214,67 @@ def test_fused_selection_matches_oracle_ragged(K, dev):
     # than b0, longer ones, and one past 4096 pages (16 keys a thread)
     lengths = [300, 1000, 4000, 4097, 7000, 70000]
     _run_case(K, dev, len(lengths), 4, lengths, 64, 0.95, ragged=True, seed=11)
+
+
+@pytest.mark.parametrize("G,R,L,b0,top_p,fixed", [
+    (4, 4, 4096, 64, 0.95, 12),
+    (2, 8, 3000, 40, 0.8, 40),       # fixed == b0: every head allocated all of its candidates
+    (3, 7, 9000, 100, 1.0, 30),      # seven heads, top-p 1
+    (2, 4, 20000, 512, 0.95, 62),    # 8192 candidates: 16 a thread
+    (8, 4, 32768, 256, 0.95, 102),   # the 32K Twilight layer, matched_budget_fraction 0.05
+])
+def test_fused_matched_selection_matches_oracle(K, dev, G, R, L, b0, top_p, fixed):
+    """Matched budgets through the fused selection: B0 pages, logits and top-p
+    counts bit for bit, the allocation (largest remainder towards fixed * 16 *
+    R) equal to the oracle's, the record equal to the union of each head's
+    top-allocated rows, and the attention over the record within 2e-3 abs +
+    1e-2 rel of float64 over the oracle's union plus the decode token."""
+    st = _Setup(K, dev, G, R, L + 8, [L] * G, seed=L + R)
+    D, bs, sink, recent = st.D, st.bs, st.sink, st.recent
+    P = oracle.selection_window(L, sink, recent)[2] // bs
+    words = K.union_record_words(P)
+    rec = torch.full((G, (words + 3) & ~3), -1, dtype=torch.int32, device=dev)   # garbage: the score launch clears it
+    sel = torch.zeros((G, R, b0), dtype=torch.int32, device=dev)
+    logits = torch.zeros((G, R, b0 * bs), dtype=torch.float32, device=dev)
+    desired = torch.zeros((G, R), dtype=torch.int32, device=dev)
+    allocated = torch.zeros((G, R), dtype=torch.int32, device=dev)
+    k, v = st.k.clone(), st.v.clone()
+    gen = torch.Generator(device=dev).manual_seed(L + 7)
+    for rep in range(2):
+        q = (torch.randn((G, R, D), generator=gen, device=dev) * 2).to(torch.bfloat16)
+        cur_k = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+        cur_v = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+        qf = q.float()
+        _say(f"[fused matched] G={G} R={R} L={L} b0={b0} fixed={fixed} rep {rep}")
+        K.twilight_select_fused(qf, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec,
+                                top_p=top_p, sink=sink, recent=recent, block_size=bs, length=L, desired=desired,
+                                sel_pages=sel, logits=logits, budget_mode="matched", target_total=fixed * bs * R,
+                                allocated=allocated)
+        out = K.decode_attention_union(q, k, v, rec, P, max_pages=min(P, R * b0), sink=sink, recent=recent,
+                                       block_size=bs, length=L, append=True, cur_k=cur_k, cur_v=cur_v)
+        torch.cuda.synchronize()
+        rec_h, sel_h, log_h = rec.cpu().numpy(), sel.cpu().numpy(), logits.cpu().numpy()
+        des_h, all_h = desired.cpu().numpy(), allocated.cpu().numpy()
+        ref_o = np.zeros((G, R, D))
+        for gi in range(G):
+            ref = oracle.twilight_layer(qf[gi].cpu().numpy(), to_bits(st.pmin[gi, :P]), to_bits(st.pmax[gi, :P]),
+                                        st.packed[gi].cpu().numpy(), to_bits(st.qscale[gi]), to_bits(st.qmin[gi]),
+                                        "bf16", length=L, sink=sink, recent=recent, block_size=bs, b0_pages=b0,
+                                        top_p=top_p, budget_mode="matched", fixed_pages=fixed)
+            assert np.array_equal(sel_h[gi], ref["pages"]), (rep, gi)
+            assert np.array_equal(log_h[gi].view(np.uint32), ref["logits"].astype(np.float32).view(np.uint32)), \
+                (rep, gi)
+            assert np.array_equal(des_h[gi], ref["desired"]), (rep, gi, des_h[gi], ref["desired"])
+            assert np.array_equal(all_h[gi], ref["allocated"]), (rep, gi, all_h[gi], ref["allocated"])
+            assert all_h[gi].sum() == fixed * bs * R, (rep, gi)
+            bits, masks = _decode_record(rec_h[gi], P)
+            want = _record_of(np.unique(np.concatenate(ref["selected"])), P, sink, bs)
+            assert np.array_equal(masks, want), (rep, gi)
+            assert np.array_equal(bits[:P], want != 0) and not bits[P:].any(), (rep, gi)
+            kept = ref["union"].astype(np.int64)
+            keys = torch.cat([st.k[gi, kept].float(), cur_k[gi:gi + 1].float()]).cpu().numpy()
+            vals = torch.cat([st.v[gi, kept].float(), cur_v[gi:gi + 1].float()]).cpu().numpy()
+            ref_o[gi] = oracle.decode_attention(qf[gi].cpu().numpy(), keys, vals, 1.0 / math.sqrt(D))
+        _close(out.float().cpu().numpy(), ref_o, f"matched union-record attention rep {rep}")
+        assert torch.equal(k[:, L].view(torch.int16), cur_k.view(torch.int16))
+        _say(f"[fused matched] rep {rep} ok, desired {des_h[0].tolist()} allocated {all_h[0].tolist()}")

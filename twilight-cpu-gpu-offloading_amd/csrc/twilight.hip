@@ -1818,7 +1818,35 @@ struct HeadArgs {
   int32_t* desired;      // [G][R]
   uint32_t* rec;         // union records, rec_stride words apart
   int64_t rec_stride;
+  int matched;           // matched budgets: stop after the top-p count (the record is
+                         // written by twilight_matched_rec_kernel)
 };
+
+// ORs the kept candidates of a row (bit j of taken: candidate KPB t + j, row
+// n % 16 of B0 page s_page[n / 16]) into its group's union record: the
+// page's 16-bit row mask and its bit in the page bitmap.
+template <int KPB>
+__device__ __forceinline__ void or_into_record(uint32_t taken, const int* s_page, uint32_t* rec, int P) {
+  const int tid = static_cast<int>(threadIdx.x);
+  uint32_t* masks = rec + union_mask_offset(P);
+  if constexpr (KPB == 8) {
+    // two threads per page: the even one ORs both halves
+    uint32_t m = (taken & 0xffu) << (8 * (tid & 1));
+    m |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 1));
+    if ((tid & 1) == 0 && m != 0u) {
+      const int p = s_page[tid >> 1];
+      atomicOr(masks + (p >> 1), m << (16 * (p & 1)));
+      atomicOr(rec + (p >> 5), 1u << (p & 31));
+    }
+  } else {
+    const uint32_t m = taken & 0xffffu;
+    if (m != 0u) {
+      const int p = s_page[tid];
+      atomicOr(masks + (p >> 1), m << (16 * (p & 1)));
+      atomicOr(rec + (p >> 5), 1u << (p & 31));
+    }
+  }
+}
 
 template <typename DT, int KPA, int KPB>
 __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a) {
@@ -2074,27 +2102,91 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a)
   }
   desired = desired < 1 ? 1 : (desired > N ? N : desired);
   if (tid == 0) a.desired[row] = desired;
+  if (a.matched) return;
 
   // ---- 4. publish: row masks and the page bitmap of the union record ----
-  uint32_t* rec = a.rec + static_cast<int64_t>(g) * a.rec_stride;
-  uint32_t* masks = rec + union_mask_offset(a.P);
-  if constexpr (KPB == 8) {
-    // two threads per page: the even one ORs both halves
-    uint32_t m = (taken & 0xffu) << (8 * (tid & 1));
-    m |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), 1));
-    if ((tid & 1) == 0 && m != 0u) {
-      const int p = s_page[tid >> 1];
-      atomicOr(masks + (p >> 1), m << (16 * (p & 1)));
-      atomicOr(rec + (p >> 5), 1u << (p & 31));
-    }
-  } else {
-    const uint32_t m = taken & 0xffffu;
-    if (m != 0u) {
-      const int p = s_page[tid];
-      atomicOr(masks + (p >> 1), m << (16 * (p & 1)));
-      atomicOr(rec + (p >> 5), 1u << (p & 31));
-    }
+  or_into_record<KPB>(taken, s_page, a.rec + static_cast<int64_t>(g) * a.rec_stride, a.P);
+}
+
+// Matched budgets over the fused selection: one block per (group, head)
+// after twilight_head_kernel (matched) has written every head's top-p count
+// and left its logits, B0 pages and wavefront key ranges in the workspace.
+// Every block of a group forms the same allocation (matched_counts), takes
+// its head's top-allocated logits (key desc, candidate index asc: the
+// selection twilight_matched_kernel makes) and ORs their rows into the
+// union record the score kernel cleared.  Uniform lengths only.
+struct MatchedRecArgs {
+  const float* ws_logits;     // [G * R][b0 * 16]
+  const uint32_t* ws_range;   // [G * R][parts * 8][4] (max logit, max key, min key, 0)
+  const int32_t* sel_pages;   // [G][R][b0] ascending
+  const int32_t* desired;     // [G][R] top-p counts
+  int32_t* allocated;         // nullable [G][R]
+  int G, R, P, b0, parts, target_total;
+  uint32_t* rec;
+  int64_t rec_stride;
+};
+
+template <int KPB>
+__global__ __launch_bounds__(kHeadThreads) void twilight_matched_rec_kernel(MatchedRecArgs a) {
+  constexpr int NT = kHeadThreads;
+  constexpr int BS = 16;
+  constexpr int kSlots = KPB * NT / BS;
+  constexpr int kWv = NT / kWave;
+  __shared__ __align__(16) TopShared<NT> sh;
+  __shared__ int s_page[kSlots];
+  __shared__ int s_k;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = lane_id();
+  const int row = blockIdx.x;
+  const int g = row / a.R;
+  const int r = row - g * a.R;
+  const int N = a.b0 * BS;
+  topk_fast_clear(sh.sel);
+  // ---- one round trip: the group's counts, the row's pages, logits and ranges ----
+  if (tid == 0) {
+    int d[8], c[8];
+    for (int i = 0; i < a.R; ++i) d[i] = a.desired[static_cast<int64_t>(g) * a.R + i];
+    matched_counts(d, a.R, a.target_total, N, c);
+    const int k = c[r] < 1 ? 1 : (c[r] > N ? N : c[r]);
+    s_k = k;
+    if (a.allocated != nullptr) a.allocated[row] = k;
   }
+  for (int i = tid; i < a.b0; i += NT) s_page[i] = a.sel_pages[static_cast<int64_t>(row) * a.b0 + i];
+  uint32_t lkey[KPB];
+  uint32_t kmin, kmax;
+  {
+    const float* wl = a.ws_logits + static_cast<int64_t>(row) * N;
+    const int i0 = KPB * tid;
+#pragma unroll
+    for (int j = 0; j < KPB; j += 4) {
+      const int i = i0 + j < N ? i0 + j : 0;
+      const float4 t = *reinterpret_cast<const float4*>(wl + i);
+      lkey[j] = score_key(t.x);
+      lkey[j + 1] = score_key(t.y);
+      lkey[j + 2] = score_key(t.z);
+      lkey[j + 3] = score_key(t.w);
+    }
+    const int n_rng = a.parts * kWv;  // <= 128
+    const uint32_t* rr = a.ws_range + static_cast<int64_t>(row) * n_rng * 4;
+    uint32_t kmx = 0u, kmn = 0xffffffffu;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = lane + kWave * h < n_rng ? lane + kWave * h : n_rng - 1;
+      const uint4 t = *reinterpret_cast<const uint4*>(rr + 4 * e);
+      kmx = t.y > kmx ? t.y : kmx;
+      kmn = t.z < kmn ? t.z : kmn;
+    }
+    kmax = wave_max_u32(kmx);
+    kmin = wave_min_u32(kmn);
+  }
+  __syncthreads();  // s_k, s_page and the cleared histogram
+  const int k = s_k;
+  uint32_t taken = 0u;
+  if (!block_topk_fast<KPB>(lkey, N, k, kmin, kmax, sh.sel, &taken)) {
+    int first;
+    block_topk<KPB>(lkey, N, k, sh.sel, &taken, &first);
+  }
+  or_into_record<KPB>(taken, s_page, a.rec + static_cast<int64_t>(g) * a.rec_stride, a.P);
 }
 
 // --------------------------------------------------------------- launch
@@ -2404,15 +2496,22 @@ extern "C" size_t tw_twilight_select_fused_workspace_size(int G, int R, int P, i
          ((rows * static_cast<size_t>(b0_pages) * 16 * sizeof(float) + 255) / 256) * 256 + rows * parts * 8 * 16;
 }
 
-extern "C" int tw_twilight_select_fused(const float* q, const void* page_min, const void* page_max, int dtype,
-                                        int G, int R, int P, int D, int64_t page_group_stride, const uint8_t* packed,
-                                        const void* qscale, const void* qmin, int64_t quant_entry_stride,
-                                        int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
-                                        int recent, int block_size, const int32_t* lengths, int length,
-                                        int32_t* sel_pages, float* logits, int32_t* desired, uint32_t* union_rec,
-                                        int64_t rec_stride, void* workspace, size_t workspace_bytes, void* stream) {
+namespace tw {
+namespace {
+
+// tw_twilight_select_fused (matched false) and tw_twilight_select_fused_matched.
+int select_fused(const float* q, const void* page_min, const void* page_max, int dtype, int G, int R, int P, int D,
+                 int64_t page_group_stride, const uint8_t* packed, const void* qscale, const void* qmin,
+                 int64_t quant_entry_stride, int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
+                 int recent, int block_size, const int32_t* lengths, int length, int32_t* sel_pages, float* logits,
+                 int32_t* desired, uint32_t* union_rec, int64_t rec_stride, void* workspace, size_t workspace_bytes,
+                 bool matched, int target_total, int32_t* allocated, void* stream) {
   if (q == nullptr || page_min == nullptr || page_max == nullptr || packed == nullptr || qscale == nullptr ||
       qmin == nullptr || desired == nullptr || union_rec == nullptr)
+    return TW_EINVAL;
+  // matched: uniform lengths, the B0 pages as an output the second launch reads
+  if (matched && (lengths != nullptr || sel_pages == nullptr || target_total < R ||
+                  static_cast<int64_t>(target_total) > static_cast<int64_t>(R) * b0_pages * 16))
     return TW_EINVAL;
   if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16) return TW_EUNSUPPORTED;
   if (D != 128 || block_size != 16) return TW_EUNSUPPORTED;
@@ -2469,5 +2568,57 @@ extern "C" int tw_twilight_select_fused(const float* q, const void* page_min, co
   h.desired = desired;
   h.rec = union_rec;
   h.rec_stride = rec_stride;
-  return dtype == TW_DTYPE_F16 ? tw::launch_head<tw::F16>(h, st) : tw::launch_head<tw::BF16>(h, st);
+  h.matched = matched ? 1 : 0;
+  rc = dtype == TW_DTYPE_F16 ? tw::launch_head<tw::F16>(h, st) : tw::launch_head<tw::BF16>(h, st);
+  if (rc != TW_OK || !matched) return rc;
+  tw::MatchedRecArgs m{};
+  m.ws_logits = h.ws_logits;
+  m.ws_range = h.ws_range;
+  m.sel_pages = sel_pages;
+  m.desired = desired;
+  m.allocated = allocated;
+  m.G = G;
+  m.R = R;
+  m.P = P;
+  m.b0 = b0_pages;
+  m.parts = h.parts;
+  m.target_total = target_total;
+  m.rec = union_rec;
+  m.rec_stride = rec_stride;
+  if (b0_pages * 16 > 8 * tw::kHeadThreads)
+    hipLaunchKernelGGL((tw::twilight_matched_rec_kernel<16>), dim3(G * R), dim3(tw::kHeadThreads), 0, st, m);
+  else
+    hipLaunchKernelGGL((tw::twilight_matched_rec_kernel<8>), dim3(G * R), dim3(tw::kHeadThreads), 0, st, m);
+  return tw_host::check_launch();
+}
+
+}  // namespace
+}  // namespace tw
+
+extern "C" int tw_twilight_select_fused(const float* q, const void* page_min, const void* page_max, int dtype,
+                                        int G, int R, int P, int D, int64_t page_group_stride, const uint8_t* packed,
+                                        const void* qscale, const void* qmin, int64_t quant_entry_stride,
+                                        int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
+                                        int recent, int block_size, const int32_t* lengths, int length,
+                                        int32_t* sel_pages, float* logits, int32_t* desired, uint32_t* union_rec,
+                                        int64_t rec_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  return tw::select_fused(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, packed, qscale, qmin,
+                          quant_entry_stride, quant_rows, b0_pages, top_p, qk_scale, sink, recent, block_size,
+                          lengths, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
+                          workspace_bytes, false, 0, nullptr, stream);
+}
+
+extern "C" int tw_twilight_select_fused_matched(const float* q, const void* page_min, const void* page_max,
+                                                int dtype, int G, int R, int P, int D, int64_t page_group_stride,
+                                                const uint8_t* packed, const void* qscale, const void* qmin,
+                                                int64_t quant_entry_stride, int64_t quant_rows, int b0_pages,
+                                                float top_p, float qk_scale, int sink, int recent, int block_size,
+                                                int length, int target_total, int32_t* sel_pages, float* logits,
+                                                int32_t* desired, int32_t* allocated, uint32_t* union_rec,
+                                                int64_t rec_stride, void* workspace, size_t workspace_bytes,
+                                                void* stream) {
+  return tw::select_fused(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, packed, qscale, qmin,
+                          quant_entry_stride, quant_rows, b0_pages, top_p, qk_scale, sink, recent, block_size,
+                          nullptr, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
+                          workspace_bytes, true, target_total, allocated, stream);
 }

@@ -91,6 +91,9 @@ _HIP_SIGNATURES = {
     "tw_twilight_select_fused_workspace_size": (szt, [i32, i32, i32, i32]),
     "tw_twilight_select_fused": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64, i32, f32, f32,
                                        i32, i32, i32, vp, i32, vp, vp, vp, vp, i64, vp, szt, vp]),
+    "tw_twilight_select_fused_matched": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64, i32,
+                                               f32, f32, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, szt,
+                                               vp]),
     "tw_decode_attention_union": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32, i64, i32, i32, i32, vp,
                                         i32, i32, vp, vp, f32, vp, vp, i64, i32, vp, vp, vp, i64, vp, vp, szt, i32,
                                         vp]),

@@ -835,16 +835,26 @@ def twilight_select_fused(
     desired: Optional[torch.Tensor] = None,
     sel_pages: Optional[torch.Tensor] = None,
     logits: Optional[torch.Tensor] = None,
+    budget_mode: str = "dynamic",
+    target_total: int = 0,
+    allocated: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """The Twilight selection of a layer with dynamic budgets in two launches
-    (Quest score; one block per head: B0 top-k, INT4 QK, top-p, publish),
-    written to each group's union record: union_rec [G, >= union_record_words
-    (P)] int32 (row stride a multiple of 4, 16-byte aligned).  q [G, R, 128]
-    fp32; page_min/page_max [G, >= P, 128] over the P scored pages (16-bit);
-    packed/scale/minimum the INT4 keys.  lengths [G] int32 (device) for ragged
-    groups, each clamped to `length`; else every group has `length` tokens.
-    Returns desired [G, R] int32 (the top-p counts); sel_pages [G, R,
-    b0_pages] and logits [G, R, b0_pages * 16] are optional outputs."""
+    """The Twilight selection of a layer in two launches with dynamic budgets
+    (Quest score; one block per head: B0 top-k, INT4 QK, top-p, publish), or
+    three with matched budgets (the head launch stops at the top-p counts;
+    one block per head then forms the group's allocation towards
+    target_total and keeps the head's top-allocated logits), written to each
+    group's union record: union_rec [G, >= union_record_words(P)] int32 (row
+    stride a multiple of 4, 16-byte aligned).  q [G, R, 128] fp32;
+    page_min/page_max [G, >= P, 128] over the P scored pages (16-bit);
+    packed/scale/minimum the INT4 keys.  lengths [G] int32 (device, dynamic
+    budgets only) for ragged groups, each clamped to `length`; else every
+    group has `length` tokens.  Returns desired [G, R] int32 (the top-p
+    counts); sel_pages [G, R, b0_pages], logits [G, R, b0_pages * 16] and
+    (matched) allocated [G, R] are optional outputs."""
+    if budget_mode not in ("dynamic", "matched"):
+        raise ValueError("budget_mode must be 'dynamic' or 'matched'")
+    matched = budget_mode == "matched"
     _check_score_inputs(q, page_min, page_max, "twilight_select_fused")
     G, R, D = q.shape
     P = page_min.shape[1]
@@ -859,23 +869,40 @@ def twilight_select_fused(
                                 or not lengths.is_contiguous()):
         raise ValueError("lengths must be contiguous [G] int32")
     dev = _require_device(q, page_min, page_max, packed, scale, minimum, union_rec, lengths, desired, sel_pages,
-                          logits, what="twilight_select_fused")
+                          logits, allocated, what="twilight_select_fused")
     if desired is None:
         desired = torch.empty((G, R), dtype=torch.int32, device=dev)
+    if matched:
+        if lengths is not None:
+            raise ValueError("twilight_select_fused: matched budgets take one length for every group")
+        if not R <= target_total <= R * b0_pages * block_size:
+            raise ValueError("target_total must be in [R, R * b0_pages * block_size]")
+        if sel_pages is None:  # the last launch reads the B0 pages
+            sel_pages = torch.empty((G, R, b0_pages), dtype=torch.int32, device=dev)
+    elif allocated is not None:
+        raise ValueError("allocated is an output of matched budgets")
     for t, dt, shape in ((desired, torch.int32, (G, R)), (sel_pages, torch.int32, (G, R, b0_pages)),
-                         (logits, torch.float32, (G, R, b0_pages * block_size))):
+                         (logits, torch.float32, (G, R, b0_pages * block_size)), (allocated, torch.int32, (G, R))):
         if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
             raise ValueError("twilight_select_fused output has the wrong dtype/shape")
     qs = float(torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32)) if qk_scale is None else float(qk_scale)
     nbytes = hip().tw_twilight_select_fused_workspace_size(G, R, P, int(b0_pages))
     ws = WORKSPACE.get(dev, "twilight_fused", nbytes)
     with torch.cuda.device(dev):
-        check(hip().tw_twilight_select_fused(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
-                                             page_min.stride(0), ptr(packed), ptr(scale), ptr(minimum), qe,
-                                             packed.shape[1], int(b0_pages), float(top_p), qs, sink, recent,
-                                             block_size, ptr(lengths), int(length), ptr(sel_pages), ptr(logits),
-                                             ptr(desired), ptr(union_rec), union_rec.stride(0), ptr(ws), ws.numel(),
-                                             stream_handle(dev)), "twilight_select_fused")
+        if matched:
+            check(hip().tw_twilight_select_fused_matched(
+                ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D, page_min.stride(0), ptr(packed),
+                ptr(scale), ptr(minimum), qe, packed.shape[1], int(b0_pages), float(top_p), qs, sink, recent,
+                block_size, int(length), int(target_total), ptr(sel_pages), ptr(logits), ptr(desired),
+                ptr(allocated), ptr(union_rec), union_rec.stride(0), ptr(ws), ws.numel(), stream_handle(dev)),
+                "twilight_select_fused_matched")
+        else:
+            check(hip().tw_twilight_select_fused(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
+                                                 page_min.stride(0), ptr(packed), ptr(scale), ptr(minimum), qe,
+                                                 packed.shape[1], int(b0_pages), float(top_p), qs, sink, recent,
+                                                 block_size, ptr(lengths), int(length), ptr(sel_pages), ptr(logits),
+                                                 ptr(desired), ptr(union_rec), union_rec.stride(0), ptr(ws),
+                                                 ws.numel(), stream_handle(dev)), "twilight_select_fused")
     return desired
 
 

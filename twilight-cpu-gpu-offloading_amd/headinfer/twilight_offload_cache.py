@@ -687,19 +687,23 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
     def _decode_layer_fused(self, queries: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
                             entries: Sequence[int], old_length: int, softmax_scale: Optional[float],
                             out: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
-        """decode_layer with dynamic budgets in two selection launches: the
-        Quest score, then per (group, head) the B0 top-k, INT4 QK and top-p
-        into the group's union record, and the attention over its kept rows
-        (the same token set as the union row list).  None when the layer
-        takes the general path: other budget modes or shapes, or traces that
-        record the row list."""
+        """decode_layer through the fused selection: the Quest score, then per
+        (group, head) the B0 top-k, INT4 QK and top-p into the group's union
+        record (matched budgets: the top-p counts, then the group's
+        allocation and each head's top-allocated rows in one more launch),
+        and the attention over the record's kept rows (the same token set as
+        the union row list).  None when the layer takes the general path:
+        other shapes, or traces that record the row list."""
         G, R, D = queries.shape
-        if (not self.fused_decode or self.budget_mode != "dynamic" or R > 8 or D != 128 or self.block_size != 16
+        if (not self.fused_decode or R > 8 or D != 128 or self.block_size != 16
                 or self.dtype not in (torch.float16, torch.bfloat16) or self._capture_selection_trace
                 or self._capture_budget_trace or self._page_min is None or self._packed is None):
             return None
         sink_end, recent_start, cand, fixed, b0 = self._twilight_budgets(old_length)
         if cand == 0 or fixed == 0 or b0 == 0 or cand > 8192 or b0 * self.block_size > 8192:
+            return None
+        matched = self.budget_mode == "matched"
+        if matched and fixed > b0:  # a target past every candidate: the general path reports it
             return None
         pmin, pmax = self._metadata(entries, cand)
         packed, qscale, qmin = self._quant(entries)
@@ -711,7 +715,9 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         start = self._phase_start()
         kernels.twilight_select_fused(queries.float().contiguous(), pmin, pmax, packed, qscale, qmin, b0, rec,
                                       top_p=self.top_p, sink=self.sink_tokens, recent=self.recent_tokens,
-                                      block_size=self.block_size, length=old_length, desired=desired)
+                                      block_size=self.block_size, length=old_length, desired=desired,
+                                      budget_mode=self.budget_mode,
+                                      target_total=fixed * self.block_size * R if matched else 0)
         self._phase_end("twilight_fused_selection", start)
         e0 = entries[0]
         cur_k, cur_v = key_states.contiguous(), value_states.contiguous()
