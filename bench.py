@@ -798,6 +798,14 @@ def main(argv=None) -> int:
         tw = twilight_leg(leg_args, dev)
         result["twilight32k"] = {"layer_us": tw["layer_us"], "GBps": tw["value"], "kernels": tw["kernels"],
                                  "rows_per_group": tw["rows_per_group"], "parity_ok": tw["parity"]["ok"]}
+        # the same layer with matched budgets, the reference cache's default budget mode
+        print("[bench] leg: twilight32k matched", file=sys.stderr, flush=True)
+        m_args = argparse.Namespace(**vars(leg_args))
+        m_args.budget_mode, m_args.twilight_path = "matched", "fused"
+        twm = twilight_leg(m_args, dev)
+        result["twilight32k_matched"] = {"layer_us": twm["layer_us"], "GBps": twm["value"],
+                                         "kernels": twm["kernels"], "rows_per_group": twm["rows_per_group"],
+                                         "parity_ok": twm["parity"]["ok"]}
         print("[bench] leg: offload64k", file=sys.stderr, flush=True)
         off = offload_leg(leg_args, dev)
         result["offload64k"] = {"layer_us": off["layer_us"], "host_link": off["host_link"],
@@ -810,7 +818,7 @@ def main(argv=None) -> int:
             result["tpot64k_host"] = tpot_leg(leg_args, dev, model, ctx=65536, kv="host", n_dec=16)
         del model
         torch.cuda.empty_cache()
-        ok = ok and tw["parity"]["ok"] and off["parity"]["ok"]
+        ok = ok and tw["parity"]["ok"] and twm["parity"]["ok"] and off["parity"]["ok"]
     print(json.dumps(result), flush=True)
     return 0 if ok else 1
 
