@@ -503,20 +503,24 @@ __global__ __launch_bounds__(512) void merge_kernel(AttnArgs a, int rows_per_blo
   }
 }
 
-// Split-K combine for D in {64, 128, 256}: one block per (group, head), thread
-// t = (chunk lane t / (D/4), channel quad t % (D/4)).  Every chunk lane loads
-// its chunks' (m, l) and 16-byte o slices in one batch (at most 32 loads per
-// thread for D <= 128, one memory round trip), the block finds the max m,
-// weights its chunks by exp2(m_c - M) and the chunk lanes are summed in LDS.
-template <typename DT, int MODE, int D>
+// Split-K combine for D in {64, 128, 256}: CS blocks per (group, head), each
+// over D / CS channels, thread t = (chunk lane t / (D/4/CS), channel quad
+// t % (D/4/CS)).  Every chunk lane loads its chunks' (m, l) and 16-byte o
+// slices in one batch (at most 32 loads per thread for D <= 128 at CS = 1, 8
+// at CS = 4; one memory round trip), the block finds the max m (every slice
+// block of a head the same), weights its chunks by exp2(m_c - M) and the
+// chunk lanes are summed in LDS.
+template <typename DT, int MODE, int D, int CS = 1>
 __global__ __launch_bounds__(kBlock) void merge_vec_kernel(AttnArgs a, int rows_per_block) {
   using S = typename DT::storage;
-  constexpr int NQ = D / 4;                        // channel quads
+  constexpr int NQ = D / 4 / CS;                   // channel quads of the block's slice
   constexpr int NL = kBlock / NQ;                  // chunk lanes
   constexpr int MAXJ = (kMaxChunks + NL - 1) / NL; // chunks per lane
   const int R = a.R;
-  const int g = blockIdx.x / R;
-  const int r = blockIdx.x - g * R;
+  const int gr = blockIdx.x / CS;
+  const int c0 = (blockIdx.x - gr * CS) * (D / CS);  // first channel of the slice
+  const int g = gr / R;
+  const int r = gr - g * R;
   const int t = threadIdx.x;
   const int q = t % NQ;
   const int cl = t / NQ;
@@ -534,7 +538,7 @@ __global__ __launch_bounds__(kBlock) void merge_vec_kernel(AttnArgs a, int rows_
   for (int j = 0; j < MAXJ; ++j) {
     const int c = cl + NL * j;
     const int64_t pc = base + (c < a.max_chunks ? c : a.max_chunks - 1);
-    ov[j] = *reinterpret_cast<const float4*>(a.part_o + (pc * R + r) * D + 4 * q);
+    ov[j] = *reinterpret_cast<const float4*>(a.part_o + (pc * R + r) * D + c0 + 4 * q);
     mlv[j] = *reinterpret_cast<const float2*>(a.part_ml + (pc * R + r) * 2);
   }
   // rows_per_block: rows of a chunk, or tiles of a chunk in page-tile mode
@@ -591,7 +595,7 @@ __global__ __launch_bounds__(kBlock) void merge_vec_kernel(AttnArgs a, int rows_
       L += s_l[k];
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    S* out = static_cast<S*>(a.out) + (static_cast<int64_t>(g) * R + r) * D + 4 * q;
+    S* out = static_cast<S*>(a.out) + (static_cast<int64_t>(g) * R + r) * D + c0 + 4 * q;
     out[0] = from_f32(DT{}, L > 0.0f ? O.x * inv : 0.0f);
     out[1] = from_f32(DT{}, L > 0.0f ? O.y * inv : 0.0f);
     out[2] = from_f32(DT{}, L > 0.0f ? O.z * inv : 0.0f);
@@ -1882,6 +1886,11 @@ void plan_chunks(int dtype, int G, int R, int D, int max_rows_total, int* iters,
 #ifndef TW_TILE_TW
 #define TW_TILE_TW 2
 #endif
+// blocks per (group, head) of the page-tile merge, each over D / TW_MERGE_CS
+// channels (4: the merge 4.0 -> 3.45 us at 32K, each thread 8 loads instead of 32)
+#ifndef TW_MERGE_CS
+#define TW_MERGE_CS 4
+#endif
 constexpr int kTileNW = TW_TILE_NW;
 constexpr int kTileTW = TW_TILE_TW;
 
@@ -1943,7 +1952,8 @@ int launch_tiles(const AttnArgs& a, hipStream_t stream) {
     if (rc != TW_OK) return rc;
   }
   if (!(phase & 2) || a.max_chunks <= 1) return TW_OK;
-  hipLaunchKernelGGL((merge_vec_kernel<DT, kModeTiles, kTileD>), dim3(a.G * a.R), dim3(kBlock), 0, stream, a,
+  hipLaunchKernelGGL((merge_vec_kernel<DT, kModeTiles, kTileD, TW_MERGE_CS>), dim3(a.G * a.R * TW_MERGE_CS),
+                     dim3(kBlock), 0, stream, a,
                      kTileNW * kTileTW * a.iters);
   return tw_host::check_launch();
 }
