@@ -1886,8 +1886,9 @@ void plan_chunks(int dtype, int G, int R, int D, int max_rows_total, int* iters,
 #ifndef TW_TILE_TW
 #define TW_TILE_TW 2
 #endif
-// blocks per (group, head) of the page-tile merge, each over D / TW_MERGE_CS
-// channels (4: the merge 4.0 -> 3.45 us at 32K, each thread 8 loads instead of 32)
+// blocks per (group, head) of the split-K merge at D = 128, each over
+// D / TW_MERGE_CS channels (4: the page-tile merge 4.0 -> 3.45 us at 32K, each
+// thread 8 loads instead of 32)
 #ifndef TW_MERGE_CS
 #define TW_MERGE_CS 4
 #endif
@@ -1995,7 +1996,8 @@ int launch_one(const AttnArgs& a, hipStream_t stream) {
   threads = threads < a.max_chunks ? ((a.max_chunks + kWave - 1) / kWave) * kWave : threads;
   const int rpb = rows_per_batch(DT::code, a.D, a.R) * a.iters;
   if constexpr (D == 64 || D == 128 || D == 256) {
-    hipLaunchKernelGGL((merge_vec_kernel<DT, MODE, D>), dim3(a.G * a.R), dim3(kBlock), 0, stream, a, rpb);
+    constexpr int CS = D == 128 ? TW_MERGE_CS : 1;  // channel slices (a 64-lane serial sum past 4)
+    hipLaunchKernelGGL((merge_vec_kernel<DT, MODE, D, CS>), dim3(a.G * a.R * CS), dim3(kBlock), 0, stream, a, rpb);
     return tw_host::check_launch();
   }
   if (a.max_chunks <= 64) {
