@@ -165,7 +165,35 @@ def check(status: int, what: str) -> None:
 
 def stream_handle(device: torch.device | None = None) -> int:
     """The hipStream_t of torch's current stream on ``device``."""
-    return torch.cuda.current_stream(device).cuda_stream
+    index = torch.cuda.current_device() if device is None or device.index is None else device.index
+    return _raw_stream(index)
+
+
+def _raw_stream_of(index: int) -> int:
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+# torch's current raw stream without building a Stream object (a few
+# microseconds a call on the eager decode path)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or _raw_stream_of
+
+
+class _NoGuard:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_GUARD = _NoGuard()
+
+
+def on_device(device: torch.device):
+    """torch.cuda.device(device), or nothing to do when it is already current."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _NO_GUARD
+    return torch.cuda.device(device)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -16,7 +16,7 @@ from typing import Optional
 import torch
 
 from . import _native
-from ._native import check, hip, ptr, stream_handle
+from ._native import check, hip, on_device, ptr, stream_handle
 
 _KEY_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
@@ -145,7 +145,7 @@ def build_page_metadata(
         raise ValueError("INT4 outputs must be given together")
     if page_min is None and packed is None:
         return
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_build_page_metadata(ptr(keys), keys.stride(0), E, T, D, _dt(keys), sink, block_size,
                                            ptr(page_min), ptr(page_max), pe, ptr(packed), ptr(scale), ptr(minimum),
                                            qe, stream_handle(dev)), "build_page_metadata")
@@ -210,7 +210,7 @@ def update_page_metadata(
     dev = _require_device(page_min, page_max, packed, scale, minimum, what="update_page_metadata")
     kp = ptr(keys) if keys.is_cuda else host_device_pointer(keys)
     kp += e0 * keys.stride(0) * keys.element_size()
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_update_page_metadata(kp, keys.stride(0), n_entries, position, D, _dt(keys), sink,
                                             block_size, pmin_p, pmax_p, pe, pk_p, sc_p, mn_p, qe,
                                             stream_handle(dev)), "update_page_metadata")
@@ -271,7 +271,7 @@ def update_page_metadata_ragged(
     dev = _require_device(positions, page_min, page_max, packed, scale, minimum, what="update_page_metadata_ragged")
     kp = ptr(keys) if keys.is_cuda else host_device_pointer(keys)
     kp += e0 * keys.stride(0) * keys.element_size()
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_update_page_metadata_ragged(kp, keys.stride(0), n, ptr(positions), max_position, D,
                                                    _dt(keys), sink, block_size, pmin_p, pmax_p, max_pages, pe, pk_p,
                                                    sc_p, mn_p, qe, stream_handle(dev)), "update_page_metadata_ragged")
@@ -301,7 +301,7 @@ def affine_int4_dequantize(packed: torch.Tensor, scale: torch.Tensor, minimum: t
     D = packed.shape[-1] * 2
     N = scale.numel()
     out = torch.empty((*packed.shape[:-1], D), dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_int4_dequantize(ptr(packed), ptr(scale), ptr(minimum), _dt(scale), N, D, ptr(out),
                                        stream_handle(dev)), "affine_int4_dequantize")
     return out
@@ -334,7 +334,7 @@ def fused_quest_score(q: torch.Tensor, page_min: torch.Tensor, page_max: torch.T
     out = torch.empty((G, R, P), dtype=torch.float32, device=dev)
     if P == 0:
         return out
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_quest_score(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
                                    page_min.stride(0), ptr(out), stream_handle(dev)), "fused_quest_score")
     return out
@@ -355,7 +355,7 @@ def topk_sorted(scores: torch.Tensor, k: int) -> torch.Tensor:
     out = torch.empty((flat.shape[0], k), dtype=torch.int64, device=dev)
     nbytes = hip().tw_topk_sorted_workspace_size(flat.shape[0], P)
     ws = WORKSPACE.get(dev, "topk_sorted", nbytes) if nbytes else None
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_topk_sorted(ptr(flat), flat.shape[0], P, flat.stride(0), k, ptr(out), ptr(ws),
                                    0 if ws is None else ws.numel(), stream_handle(dev)), "topk_sorted")
     return out.view(*scores.shape[:-1], k)
@@ -418,7 +418,7 @@ def quest_select(
             raise ValueError("plan_masks must match plan_pages")
     nbytes = hip().tw_quest_select_workspace_size(G, R, P)
     ws = WORKSPACE.get(dev, "quest_select", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_quest_select(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
                                     page_min.stride(0), k, ptr(scores), ptr(sel_pages), ptr(plan_pages),
                                     ptr(plan_masks), ptr(plan_counts), plan_stride, ptr(rows), ptr(row_masks),
@@ -468,7 +468,7 @@ def quest_select_ragged(
             raise ValueError("plan_masks must match plan_pages")
     nbytes = hip().tw_quest_select_workspace_size(G, R, P)
     ws = WORKSPACE.get(dev, "quest_select", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_quest_select_ragged(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
                                            page_min.stride(0), ptr(lengths), k, ptr(sel_pages), ptr(plan_pages),
                                            ptr(plan_masks), ptr(plan_counts), plan_stride, sink, recent, block_size,
@@ -520,7 +520,7 @@ def quest_select_bits(
         raise ValueError("lengths must be contiguous [G] int32")
     nbytes = hip().tw_quest_select_workspace_size(G, R, P)
     ws = WORKSPACE.get(dev, "quest_select", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_quest_select_bits(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
                                          page_min.stride(0), ptr(lengths), k, ptr(scores), ptr(sel_pages),
                                          ptr(sel_bits), sel_bits.stride(1), sink, recent, block_size, ptr(ws),
@@ -586,7 +586,7 @@ def twilight_qk(
                 or page_rows.stride() != plan_pages.stride():
             raise ValueError("page_rows must be int32 shaped and strided like plan_pages")
         _require_device(slot_u, page_rows, what="twilight_qk")
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_twilight_qk(ptr(q), G, R, D, ptr(packed), ptr(scale), ptr(minimum), _dt(scale), qe,
                                    packed.shape[1], ptr(plan_pages), ptr(plan_masks), ptr(plan_counts), plan_pages.stride(0),
                                    b0_pages, sink, block_size, qs, ptr(out), ptr(slot_u), ptr(page_rows),
@@ -614,7 +614,7 @@ def fused_affine_int4_qk(q: torch.Tensor, packed: torch.Tensor, scale: torch.Ten
     _require_contiguous(q, packed, scale, minimum, positions, what="fused_affine_int4_qk")
     dev = _require_device(q, packed, scale, minimum, positions, what="fused_affine_int4_qk")
     out = torch.empty((g, r, n, d) if materialize else (g, r, n), device=dev, dtype=torch.float32)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_int4_qk_positions(ptr(q), g, r, d, ptr(packed), ptr(scale), ptr(minimum), _dt(scale), h, h,
                                          ptr(positions), n, 1.0, int(bool(materialize)), ptr(out),
                                          stream_handle(dev)), "fused_affine_int4_qk")
@@ -681,7 +681,7 @@ def twilight_select(
                           what="twilight_select")
     nbytes = hip().tw_twilight_select_workspace_size(G, R, N)
     ws = WORKSPACE.get(dev, "twilight_select", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_twilight_select(ptr(logits), G, R, N, ptr(sel_pages), b0, float(top_p),
                                        modes[budget_mode], int(target_total), ptr(desired),
                                        ptr(allocated), ptr(head_bits), ptr(rows), ptr(row_counts), rows.stride(0), sink, recent,
@@ -736,7 +736,7 @@ def twilight_select_ragged(
                           what="twilight_select_ragged")
     nbytes = hip().tw_twilight_select_workspace_size(G, R, N)
     ws = WORKSPACE.get(dev, "twilight_select", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_twilight_select_ragged(ptr(logits), G, R, N, ptr(sel_pages), b0, float(top_p), ptr(desired),
                                               None, ptr(head_bits), ptr(rows), ptr(row_counts), rows.stride(0),
                                               sink, recent, block_size, ptr(lengths), int(max_length),
@@ -786,7 +786,7 @@ def twilight_select_pages(
     dev = _require_device(logits, sel_pages, slot_u, page_rows, lengths, desired, what="twilight_select_pages")
     nbytes = hip().tw_twilight_select_workspace_size(G, R, N)
     ws = WORKSPACE.get(dev, "twilight_select", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_twilight_select_pages(ptr(logits), G, R, N, ptr(sel_pages), b0, float(top_p), ptr(slot_u),
                                              ptr(page_rows), page_rows.stride(0), ptr(desired), sink, recent,
                                              block_size, int(length), ptr(lengths), int(page_capacity), ptr(ws),
@@ -888,7 +888,7 @@ def twilight_select_fused(
     qs = float(torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32)) if qk_scale is None else float(qk_scale)
     nbytes = hip().tw_twilight_select_fused_workspace_size(G, R, P, int(b0_pages))
     ws = WORKSPACE.get(dev, "twilight_fused", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         if matched:
             check(hip().tw_twilight_select_fused_matched(
                 ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D, page_min.stride(0), ptr(packed),
@@ -1000,7 +1000,7 @@ def decode_attention_rows(
             raise ValueError("packed [G, T, D/2] uint8 and scale/minimum [G, T] must match")
         if pmn is not None or pk is not None:
             _require_device(pmn, pmx, pk, qs, qm, what="decode_attention")
-        with torch.cuda.device(dev):
+        with on_device(dev):
             check(hip().tw_decode_attention_rows_append(
                 ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D, ptr(rows), ptr(row_masks),
                 ptr(row_counts), rows.stride(0), k_cache.stride(0) // D, max_rows, ptr(cur_k), ptr(cur_v),
@@ -1009,7 +1009,7 @@ def decode_attention_rows(
                 0 if qs is None else qs.stride(0), ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
                 "decode_attention")
         return out
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_decode_attention(ptr(q), k_cache.data_ptr(), v_cache.data_ptr(), _dt(q), G, R, D, ptr(rows),
                                         ptr(row_masks), ptr(row_counts), rows.stride(0), k_cache.stride(0) // D,
                                         None, 0, -1, max_rows, ptr(cur_k), ptr(cur_v), scale, ptr(out), ptr(ws),
@@ -1093,7 +1093,7 @@ def decode_attention_pages(
     max_rows += 0 if cur_k is None else 1
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_decode_attention_pages_phase(ptr(q), kp, vp, _dt(q), G, R, D,
                                                     ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
                                                     plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink,
@@ -1184,7 +1184,7 @@ def decode_attention_pages_ragged(
     max_rows = sink + max_pages * block_size + recent
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_decode_attention_pages_ragged(ptr(q), kp, vp, _dt(q), G, R, D, ptr(plan_pages),
                                                      ptr(plan_masks), ptr(plan_counts), plan_pages.stride(0),
                                                      max_rows, k_cache.stride(0) // D, sink, recent, block_size,
@@ -1259,7 +1259,7 @@ def decode_attention_pages_bits(
     max_rows = sink + max(0, max_pages) * block_size + recent
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_decode_attention_pages_bits(ptr(q), kp, vp, _dt(q), G, R, D, ptr(sel_bits),
                                                    sel_bits.stride(1), P, max_rows, k_cache.stride(0) // D, sink,
                                                    recent, block_size, ptr(lengths), int(length),
@@ -1347,7 +1347,7 @@ def decode_attention_page_rows(
     max_rows = sink + max_pages * block_size + recent
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_decode_attention_page_rows(ptr(q), kp, vp, _dt(q), G, R, D, ptr(plan_pages), ptr(plan_counts),
                                                   ptr(page_rows), plan_pages.stride(0), max_rows,
                                                   k_cache.stride(0) // D, sink, recent, block_size, ptr(lengths),
@@ -1432,7 +1432,7 @@ def decode_attention_union(
     max_rows = sink + max(0, max_pages) * block_size + recent
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_decode_attention_union(ptr(q), kp, vp, _dt(q), G, R, D, ptr(union_rec), union_rec.stride(0),
                                               P, max_rows, k_cache.stride(0) // D, sink, recent, block_size,
                                               ptr(lengths), int(length), int(bool(append)), ptr(cur_k), ptr(cur_v),
@@ -1535,7 +1535,7 @@ def decode_attention_pages_resident(
     max_rows = sink + max_pages * block_size + recent
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_decode_attention_pages_resident(
             ptr(q), kp, vp, _dt(q), G, R, D, ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
             plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink, recent, block_size, ptr(lengths),
@@ -1590,7 +1590,7 @@ def decode_attention_varlen(
         max_rows = min(max_rows, window_left + 1)
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_decode_attention(ptr(q), k.data_ptr(), v.data_ptr(), _dt(q), G, R, D, None, None, None, 0, 0,
                                         ptr(cu_seqlens_k), Hk, int(window_left), max_rows, None, None, scale,
                                         ptr(out), ptr(ws), ws.numel(), stream_handle(dev)), "decode_attention_varlen")
@@ -1656,7 +1656,7 @@ def gather_rows(
     else:
         sk, sv = host_device_pointer(src_k), host_device_pointer(src_v)
     D = src_k.shape[1]
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_gather_rows(sk, sv, src_k.shape[0], ptr(src_rows), ptr(dst_rows), src_rows.numel(),
                                    dst_capacity, D, src_k.element_size(), ptr(dst_k), ptr(dst_v), ptr(error_flag),
                                    stream_handle(dev)), "gather_rows")
@@ -1712,7 +1712,7 @@ def gather_union(
     dev = _require_device(rows, row_counts, cur_k, cur_v, dst_k, dst_v, cu_seqlens, error_flag,
                           what="gather_union")
     sk, sv = _slab_source(src_k, src_v)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_gather_union(sk, sv, src_k.shape[0], entry_row0, entry_row_step, ptr(rows), rows.stride(0),
                                     ptr(row_counts), G, max_count, ptr(cur_k), ptr(cur_v), D, src_k.element_size(),
                                     dst_k.shape[0], ptr(dst_k), ptr(dst_v), ptr(cu_seqlens), ptr(error_flag),
@@ -1758,7 +1758,7 @@ def gather_heads(
     dev = _require_device(sel_pages, cur_k, cur_v, dst_k, dst_v, error_flag, what="gather_heads")
     sk, sv = _slab_source(src_k, src_v)
     sg, sr, st = dst_strides
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_gather_heads(sk, sv, src_k.shape[0], entry_row0, entry_row_step, ptr(sel_pages), G, R, k,
                                     sink, recent, block_size, length, ptr(cur_k), ptr(cur_v), D,
                                     src_k.element_size(), sg, sr, st, dst_k.shape[0], ptr(dst_k), ptr(dst_v),
@@ -1790,7 +1790,7 @@ def append_kv(
         dk, dv = dst_k.data_ptr(), dst_v.data_ptr()
     else:
         dk, dv = host_device_pointer(dst_k), host_device_pointer(dst_v)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_append_kv(ptr(new_k), ptr(new_v), n, D, new_k.element_size(), dk, dv, dst_k.shape[1],
                                  first_entry, position, stream_handle(dev)), "append_kv")
 
@@ -1834,7 +1834,7 @@ def add_rms_norm(h: torch.Tensor, delta: Optional[torch.Tensor], weight: torch.T
     if weight.shape != (H,) or weight.dtype != h.dtype or not weight.is_contiguous():
         raise ValueError("weight must be [H] in h's dtype")
     dev = _require_device(h, delta, weight, out, what="add_rms_norm")
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_add_rms_norm(ptr(h), ptr(delta), ptr(weight), float(eps), ptr(out), rows, H, _dt(h),
                                     stream_handle(dev)), "add_rms_norm")
     return out
@@ -1857,7 +1857,7 @@ def rope_qk(q: torch.Tensor, k: torch.Tensor, cos_table: torch.Tensor, sin_table
     if q32 is not None and (q32.dtype != torch.float32 or q32.shape != q.shape or not q32.is_contiguous()):
         raise ValueError("q32 must be contiguous fp32 like q")
     dev = _require_device(q, k, cos_table, sin_table, position, q32, what="rope_qk")
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_rope_qk(ptr(q), ptr(k), q.shape[0], k.shape[0], D, ptr(cos_table), ptr(sin_table),
                                ptr(position), ptr(q32), _dt(q), stream_handle(dev)), "rope_qk")
 
@@ -1869,7 +1869,7 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
             or out.numel() * 2 != gate_up.numel():
         raise ValueError("gate_up [2I] and out [I] must be contiguous fp16/bf16")
     dev = _require_device(gate_up, out, what="silu_mul")
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_silu_mul(ptr(gate_up), ptr(out), out.numel(), _dt(out), stream_handle(dev)), "silu_mul")
     return out
 
@@ -1887,7 +1887,7 @@ def gemv(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], ou
     if bias is not None and (bias.dtype != weight.dtype or bias.numel() != N or not bias.is_contiguous()):
         raise ValueError("bias must be contiguous [N]")
     dev = _require_device(x, weight, bias, out, what="gemv")
-    with torch.cuda.device(dev):
+    with on_device(dev):
         check(hip().tw_gemv(ptr(weight), ptr(x), ptr(bias), ptr(out), N, K, _dt(weight), stream_handle(dev)), "gemv")
     return out
 
@@ -1921,7 +1921,7 @@ def rms_norm_gemv(h: torch.Tensor, delta: Optional[torch.Tensor], norm_weight: t
         raise ValueError(f"out must be contiguous [{n_out}] in the weight's dtype")
     dev = _require_device(h, delta, norm_weight, h_out, weight, bias, out, q32, what="rms_norm_gemv")
     args = (ptr(h), ptr(delta), ptr(norm_weight), float(eps), ptr(h_out), ptr(weight), ptr(bias), ptr(out), N, K)
-    with torch.cuda.device(dev):
+    with on_device(dev):
         if epilogue == "plain":
             check(hip().tw_rms_norm_gemv(*args, _dt(weight), stream_handle(dev)), "rms_norm_gemv")
         elif epilogue == "silu":
