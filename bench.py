@@ -1233,8 +1233,9 @@ def tpot_leg(args, dev, model=None, ctx: int = 32768, kv: str = "hbm", n_dec: in
     pages per query head), the dense comparator on the same prefilled cache
     (no score or top-k: every whole page before the recent window through the
     same attention), Twilight (Quest B0 4096 tokens, INT4 QK, top-p 0.95,
-    dynamic budgets), and with the KV in pinned host memory also sparse Quest
-    with the HBM resident page cache (previous_token_resident_cache)."""
+    dynamic budgets, then matched budgets on the same cache), and with the KV
+    in pinned host memory also sparse Quest with the HBM resident page cache
+    (previous_token_resident_cache)."""
     import torch
 
     from headinfer.graph_decode import GraphDecoder
@@ -1284,11 +1285,18 @@ def tpot_leg(args, dev, model=None, ctx: int = 32768, kv: str = "hbm", n_dec: in
             del dec, cache
             torch.cuda.empty_cache()
         cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(
-            model, max_cache_len=ctx + n_dec + 8, kv_residency=kv, candidate_token_budget=4096, top_p=0.95,
+            model, max_cache_len=ctx + 2 * n_dec + 8, kv_residency=kv, candidate_token_budget=4096, top_p=0.95,
             budget_mode="dynamic", update_metadata_on_decode=True)
         prefill(cache, "twilight")
         dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1)
         out["twilight_graph"] = _graph_tpot(dec, n_dec)
+        dec.sync_cache()
+        del dec
+        # the reference cache's default budgets (matched, 5% of the eligible
+        # pages), decoding on from the same cache
+        cache.budget_mode = "matched"
+        dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1)
+        out["twilight_matched_graph"] = _graph_tpot(dec, n_dec)
         del dec, cache
     if own:
         del model

@@ -402,9 +402,14 @@ int tw_twilight_select_fused(const float* q, const void* page_min, const void* p
  * target_total, twilight_offload_cache.py:50-86, the same as
  * tw_twilight_select in matched mode), keeps the head's top-allocated
  * candidates by logit (ties to the lower candidate) and ORs their rows into
- * the union record.  Every group has `length` tokens (no ragged lengths);
- * sel_pages is required (the last launch reads it); R <= target_total <=
- * R*b0_pages*16.  Outputs as tw_twilight_select_fused plus allocated [G][R]
+ * the union record.  lengths null: every group has `length` tokens and
+ * target_total rows (R <= target_total <= R*b0_pages*16); lengths (device,
+ * [G] int32): group g has min(lengths[g], length) tokens, its own candidate
+ * and B0 pages (as tw_twilight_select_fused), and target fixed_g*16*R with
+ * fixed_g = min(candidates_g, max(1, ceil(matched_fraction * eligible_g /
+ * 16))) (twilight_offload_cache.py:1019-1083; at most every candidate),
+ * 0 < matched_fraction <= 1.  sel_pages is required (the last launch reads
+ * it).  Outputs as tw_twilight_select_fused plus allocated [G][R]
  * (nullable).  Workspace: tw_twilight_select_fused_workspace_size.
  * Replaces prepare_layer_selection's stages 1-2, the matched reallocation
  * and the GPU GQA union of the matched path (twilight_offload_cache.py:
@@ -413,9 +418,10 @@ int tw_twilight_select_fused_matched(const float* q, const void* page_min, const
                                      int R, int P, int D, int64_t page_group_stride, const uint8_t* packed,
                                      const void* qscale, const void* qmin, int64_t quant_entry_stride,
                                      int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
-                                     int recent, int block_size, int length, int target_total, int32_t* sel_pages,
-                                     float* logits, int32_t* desired, int32_t* allocated, uint32_t* union_rec,
-                                     int64_t rec_stride, void* workspace, size_t workspace_bytes, void* stream);
+                                     int recent, int block_size, const int32_t* lengths, int length,
+                                     int target_total, double matched_fraction, int32_t* sel_pages, float* logits,
+                                     int32_t* desired, int32_t* allocated, uint32_t* union_rec, int64_t rec_stride,
+                                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Sparse GQA decode attention, split-K over selected rows, one query

@@ -321,8 +321,8 @@ def test_graph_decoder_fused_equals_unfused(dev):
     assert torch.equal(caches[0]._value_cache[:, :n], caches[1]._value_cache[:, :n])
 
 
-@pytest.mark.parametrize("fuse", [True, False])
-def test_graph_decoder_twilight_matches_eager(dev, fuse):
+@pytest.mark.parametrize("fuse,mode", [(True, "dynamic"), (False, "dynamic"), (True, "matched")])
+def test_graph_decoder_twilight_matches_eager(dev, fuse, mode):
     """GraphDecoder over a Twilight cache (Quest B0, INT4 QK, top-p and the
     GQA union from device-side lengths, the union attention with the append,
     the INT4 + page metadata update) == the eager patched model with the same
@@ -331,12 +331,12 @@ def test_graph_decoder_twilight_matches_eager(dev, fuse):
     from headinfer.graph_decode import GraphDecoder
     from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache
 
-    _say(f"[graph decoder twilight] fuse={fuse}")
+    _say(f"[graph decoder twilight] fuse={fuse} {mode}")
     steps = 10
     _, gpu = _models(dev)
     mp.mp_headinfer(gpu)
     kw = dict(max_cache_len=T_PROMPT + steps + 2, sink_tokens=64, recent_tokens=256, block_size=16,
-              kv_residency="hbm", candidate_token_budget=128, top_p=0.9, budget_mode="dynamic",
+              kv_residency="hbm", candidate_token_budget=128, top_p=0.9, budget_mode=mode,
               update_metadata_on_decode=True)
     eager_cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(gpu, **kw)
     graph_cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(gpu, **kw)

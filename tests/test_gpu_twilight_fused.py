@@ -278,3 +278,71 @@ def test_fused_matched_selection_matches_oracle(K, dev, G, R, L, b0, top_p, fixe
         _close(out.float().cpu().numpy(), ref_o, f"matched union-record attention rep {rep}")
         assert torch.equal(k[:, L].view(torch.int16), cur_k.view(torch.int16))
         _say(f"[fused matched] rep {rep} ok, desired {des_h[0].tolist()} allocated {all_h[0].tolist()}")
+
+
+def test_fused_matched_selection_ragged(K, dev):
+    """Matched budgets with device lengths (the graph-captured decode): each
+    group's candidate and B0 pages and its target (fixed = min(candidates,
+    max(1, ceil(0.05 * eligible / 16))) pages x 16 x R) come from its own
+    length; B0 pages, logits, counts, allocation and record against the
+    oracle at that length, the attention against float64.  A group with no
+    whole page between its windows keeps nothing."""
+    lengths = [300, 3000, 4097, 9000, 20000]
+    G, R, b0, top_p, frac = len(lengths), 4, 64, 0.9, 0.05
+    st = _Setup(K, dev, G, R, max(lengths) + 8, lengths, seed=23)
+    D, bs, sink, recent = st.D, st.bs, st.sink, st.recent
+    P = st.P
+    lens = torch.tensor(lengths, dtype=torch.int32, device=dev)
+    words = K.union_record_words(P)
+    rec = torch.full((G, (words + 3) & ~3), -1, dtype=torch.int32, device=dev)
+    sel = torch.zeros((G, R, b0), dtype=torch.int32, device=dev)
+    logits = torch.zeros((G, R, b0 * bs), dtype=torch.float32, device=dev)
+    desired = torch.zeros((G, R), dtype=torch.int32, device=dev)
+    allocated = torch.full((G, R), -7, dtype=torch.int32, device=dev)
+    k, v = st.k.clone(), st.v.clone()
+    gen = torch.Generator(device=dev).manual_seed(29)
+    q = (torch.randn((G, R, D), generator=gen, device=dev) * 2).to(torch.bfloat16)
+    cur_k = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+    cur_v = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+    qf = q.float()
+    _say(f"[fused matched ragged] lengths={lengths}")
+    K.twilight_select_fused(qf, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec, top_p=top_p,
+                            sink=sink, recent=recent, block_size=bs, length=max(lengths), lengths=lens,
+                            desired=desired, sel_pages=sel, logits=logits, budget_mode="matched",
+                            matched_fraction=frac, allocated=allocated)
+    out = K.decode_attention_union(q, k, v, rec, P, max_pages=min(P, R * b0), sink=sink, recent=recent,
+                                   block_size=bs, lengths=lens, length=max(lengths), append=True, cur_k=cur_k,
+                                   cur_v=cur_v)
+    torch.cuda.synchronize()
+    rec_h, sel_h, log_h = rec.cpu().numpy(), sel.cpu().numpy(), logits.cpu().numpy()
+    des_h, all_h = desired.cpu().numpy(), allocated.cpu().numpy()
+    ref_o = np.zeros((G, R, D))
+    for gi, Lg in enumerate(lengths):
+        sink_end, recent_start, eligible = oracle.selection_window(Lg, sink, recent)
+        cand = min(eligible // bs, P)
+        bits, masks = _decode_record(rec_h[gi], P)
+        if cand == 0:
+            assert np.all(des_h[gi] == 0) and not bits.any() and not masks.any(), gi
+            kept = np.concatenate([np.arange(sink_end), np.arange(recent_start, Lg)]).astype(np.int64)
+        else:
+            b0g = min(b0, cand)
+            fixed = min(cand, max(1, math.ceil(frac * eligible / bs)))
+            ref = oracle.twilight_layer(qf[gi].cpu().numpy(), to_bits(st.pmin[gi, :cand]),
+                                        to_bits(st.pmax[gi, :cand]), st.packed[gi].cpu().numpy(),
+                                        to_bits(st.qscale[gi]), to_bits(st.qmin[gi]), "bf16", length=Lg, sink=sink,
+                                        recent=recent, block_size=bs, b0_pages=b0g, top_p=top_p,
+                                        budget_mode="matched", fixed_pages=fixed)
+            Ng = b0g * bs
+            assert np.array_equal(sel_h[gi, :, :b0g], ref["pages"]) and np.all(sel_h[gi, :, b0g:] == -1), gi
+            assert np.array_equal(log_h[gi, :, :Ng].view(np.uint32),
+                                  ref["logits"].astype(np.float32).view(np.uint32)), gi
+            assert np.array_equal(des_h[gi], ref["desired"]), (gi, des_h[gi], ref["desired"])
+            assert np.array_equal(all_h[gi], ref["allocated"]), (gi, all_h[gi], ref["allocated"])
+            want = _record_of(np.unique(np.concatenate(ref["selected"])), P, sink, bs)
+            assert np.array_equal(masks, want) and np.array_equal(bits[:P], want != 0) and not bits[P:].any(), gi
+            kept = ref["union"].astype(np.int64)
+        keys = torch.cat([st.k[gi, kept].float(), cur_k[gi:gi + 1].float()]).cpu().numpy()
+        vals = torch.cat([st.v[gi, kept].float(), cur_v[gi:gi + 1].float()]).cpu().numpy()
+        ref_o[gi] = oracle.decode_attention(qf[gi].cpu().numpy(), keys, vals, 1.0 / math.sqrt(D))
+    _close(out.float().cpu().numpy(), ref_o, "matched ragged union-record attention")
+    _say(f"[fused matched ragged] ok, allocated {all_h.tolist()}")

@@ -2114,7 +2114,10 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a)
 // Every block of a group forms the same allocation (matched_counts), takes
 // its head's top-allocated logits (key desc, candidate index asc: the
 // selection twilight_matched_kernel makes) and ORs their rows into the
-// union record the score kernel cleared.  Uniform lengths only.
+// union record the score kernel cleared.  With lengths (device), group g's
+// candidate pages, B0 pages and target come from its own length, as the
+// cache forms them on the host: fixed = min(candidates, max(1, ceil(frac *
+// eligible / 16))) pages, target = fixed * 16 * R (at most every candidate).
 struct MatchedRecArgs {
   const float* ws_logits;     // [G * R][b0 * 16]
   const uint32_t* ws_range;   // [G * R][parts * 8][4] (max logit, max key, min key, 0)
@@ -2122,6 +2125,9 @@ struct MatchedRecArgs {
   const int32_t* desired;     // [G][R] top-p counts
   int32_t* allocated;         // nullable [G][R]
   int G, R, P, b0, parts, target_total;
+  const int32_t* lengths;     // nullable [G]: group g has min(lengths[g], length) tokens
+  int length, sink, recent;
+  double frac;                // matched_budget_fraction (with lengths)
   uint32_t* rec;
   int64_t rec_stride;
 };
@@ -2140,13 +2146,29 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_matched_rec_kernel(Matc
   const int row = blockIdx.x;
   const int g = row / a.R;
   const int r = row - g * a.R;
-  const int N = a.b0 * BS;
+  int N = a.b0 * BS;
+  int target = a.target_total;
+  if (a.lengths != nullptr) {
+    int L = a.lengths[g];
+    L = L < 0 ? 0 : (L > a.length ? a.length : L);
+    const int Pg = ragged_pages(L, a.sink, a.recent, BS, a.P);
+    N = (a.b0 < Pg ? a.b0 : Pg) * BS;
+    const int sink_end = a.sink < L ? a.sink : L;
+    const int hist_recent = a.recent - 1 > 0 ? a.recent - 1 : 0;
+    const int recent_start = L - hist_recent > sink_end ? L - hist_recent : sink_end;
+    const double f = ceil(a.frac * static_cast<double>(recent_start - sink_end) / static_cast<double>(BS));
+    int fixed = f < 1.0 ? 1 : (f > static_cast<double>(Pg) ? Pg : static_cast<int>(f));
+    fixed = fixed < Pg ? fixed : Pg;
+    target = fixed * BS * a.R;
+    target = target < a.R * N ? target : a.R * N;
+  }
+  if (N == 0) return;  // block-uniform: no candidate, nothing kept
   topk_fast_clear(sh.sel);
   // ---- one round trip: the group's counts, the row's pages, logits and ranges ----
   if (tid == 0) {
     int d[8], c[8];
     for (int i = 0; i < a.R; ++i) d[i] = a.desired[static_cast<int64_t>(g) * a.R + i];
-    matched_counts(d, a.R, a.target_total, N, c);
+    matched_counts(d, a.R, target, N, c);
     const int k = c[r] < 1 ? 1 : (c[r] > N ? N : c[r]);
     s_k = k;
     if (a.allocated != nullptr) a.allocated[row] = k;
@@ -2155,7 +2177,7 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_matched_rec_kernel(Matc
   uint32_t lkey[KPB];
   uint32_t kmin, kmax;
   {
-    const float* wl = a.ws_logits + static_cast<int64_t>(row) * N;
+    const float* wl = a.ws_logits + static_cast<int64_t>(row) * a.b0 * BS;
     const int i0 = KPB * tid;
 #pragma unroll
     for (int j = 0; j < KPB; j += 4) {
@@ -2505,13 +2527,16 @@ int select_fused(const float* q, const void* page_min, const void* page_max, int
                  int64_t quant_entry_stride, int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
                  int recent, int block_size, const int32_t* lengths, int length, int32_t* sel_pages, float* logits,
                  int32_t* desired, uint32_t* union_rec, int64_t rec_stride, void* workspace, size_t workspace_bytes,
-                 bool matched, int target_total, int32_t* allocated, void* stream) {
+                 bool matched, int target_total, double matched_fraction, int32_t* allocated, void* stream) {
   if (q == nullptr || page_min == nullptr || page_max == nullptr || packed == nullptr || qscale == nullptr ||
       qmin == nullptr || desired == nullptr || union_rec == nullptr)
     return TW_EINVAL;
-  // matched: uniform lengths, the B0 pages as an output the second launch reads
-  if (matched && (lengths != nullptr || sel_pages == nullptr || target_total < R ||
-                  static_cast<int64_t>(target_total) > static_cast<int64_t>(R) * b0_pages * 16))
+  // matched: the B0 pages as an output the last launch reads; a target for
+  // one length, or the matched fraction for device lengths
+  if (matched && (sel_pages == nullptr ||
+                  (lengths == nullptr && (target_total < R || static_cast<int64_t>(target_total) >
+                                                                  static_cast<int64_t>(R) * b0_pages * 16)) ||
+                  (lengths != nullptr && !(matched_fraction > 0.0 && matched_fraction <= 1.0))))
     return TW_EINVAL;
   if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16) return TW_EUNSUPPORTED;
   if (D != 128 || block_size != 16) return TW_EUNSUPPORTED;
@@ -2583,6 +2608,11 @@ int select_fused(const float* q, const void* page_min, const void* page_max, int
   m.b0 = b0_pages;
   m.parts = h.parts;
   m.target_total = target_total;
+  m.lengths = lengths;
+  m.length = length;
+  m.sink = sink;
+  m.recent = recent;
+  m.frac = matched_fraction;
   m.rec = union_rec;
   m.rec_stride = rec_stride;
   if (b0_pages * 16 > 8 * tw::kHeadThreads)
@@ -2605,7 +2635,7 @@ extern "C" int tw_twilight_select_fused(const float* q, const void* page_min, co
   return tw::select_fused(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, packed, qscale, qmin,
                           quant_entry_stride, quant_rows, b0_pages, top_p, qk_scale, sink, recent, block_size,
                           lengths, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
-                          workspace_bytes, false, 0, nullptr, stream);
+                          workspace_bytes, false, 0, 0.0, nullptr, stream);
 }
 
 extern "C" int tw_twilight_select_fused_matched(const float* q, const void* page_min, const void* page_max,
@@ -2613,12 +2643,13 @@ extern "C" int tw_twilight_select_fused_matched(const float* q, const void* page
                                                 const uint8_t* packed, const void* qscale, const void* qmin,
                                                 int64_t quant_entry_stride, int64_t quant_rows, int b0_pages,
                                                 float top_p, float qk_scale, int sink, int recent, int block_size,
-                                                int length, int target_total, int32_t* sel_pages, float* logits,
+                                                const int32_t* lengths, int length, int target_total,
+                                                double matched_fraction, int32_t* sel_pages, float* logits,
                                                 int32_t* desired, int32_t* allocated, uint32_t* union_rec,
                                                 int64_t rec_stride, void* workspace, size_t workspace_bytes,
                                                 void* stream) {
   return tw::select_fused(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, packed, qscale, qmin,
                           quant_entry_stride, quant_rows, b0_pages, top_p, qk_scale, sink, recent, block_size,
-                          nullptr, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
-                          workspace_bytes, true, target_total, allocated, stream);
+                          lengths, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
+                          workspace_bytes, true, target_total, matched_fraction, allocated, stream);
 }

@@ -33,6 +33,7 @@ vp = ctypes.c_void_p
 i32 = ctypes.c_int
 i64 = ctypes.c_int64
 f32 = ctypes.c_float
+f64 = ctypes.c_double
 szt = ctypes.c_size_t
 
 _HIP_SIGNATURES = {
@@ -92,8 +93,8 @@ _HIP_SIGNATURES = {
     "tw_twilight_select_fused": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64, i32, f32, f32,
                                        i32, i32, i32, vp, i32, vp, vp, vp, vp, i64, vp, szt, vp]),
     "tw_twilight_select_fused_matched": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64, i32,
-                                               f32, f32, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i64, vp, szt,
-                                               vp]),
+                                               f32, f32, i32, i32, i32, vp, i32, i32, f64, vp, vp, vp, vp, vp, i64,
+                                               vp, szt, vp]),
     "tw_decode_attention_union": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32, i64, i32, i32, i32, vp,
                                         i32, i32, vp, vp, f32, vp, vp, i64, i32, vp, vp, vp, i64, vp, vp, szt, i32,
                                         vp]),

@@ -25,10 +25,11 @@ alternates between two buffers, since every GEMV block normalises the row
 itself while block 0 stores the sum.  With fuse=False the norms, RoPE, SiLU
 and the metadata update run as launches of their own (13 per layer) -- the
 same bits.
-Over a Twilight cache (dynamic top-p budgets) the sparse path of a layer is
-the ragged Quest B0 selection, the INT4 QK, the top-p and GQA union, the
-union attention with the append and the INT4 + page metadata update of the
-appended row, all from the device-side lengths.
+Over a Twilight cache the sparse path of a layer is the ragged Quest B0
+selection, the INT4 QK, the top-p (with matched budgets, the allocation
+and each head's top-allocated rows) and the GQA union, the union attention
+with the append and the INT4 + page metadata update of the appended row,
+all from the device-side lengths.
 The q/k/v and gate/up weights are concatenated once and the HF modules keep
 views into them, so the model's own forward (the prefill) uses the same
 storage.  The element-wise steps repeat the HF modules' rounding steps; the
@@ -63,8 +64,6 @@ class GraphDecoder:
         kind = type(cache).__name__
         if kind == "TwilightMatchedBudgetOffloadedCache":
             self.twilight = True
-            if cache.budget_mode != "dynamic":
-                raise ValueError("GraphDecoder runs Twilight with dynamic (top-p) budgets")
             if cache.previous_token_resident_cache:
                 raise ValueError("GraphDecoder runs the Twilight union attention without the resident cache")
         elif kind == "QuestTopKOffloadedCache":
@@ -198,6 +197,22 @@ class GraphDecoder:
             # the fused selection (score; B0 + INT4 QK + top-p per head) into a
             # union record per KV group, read by the union attention
             self.fused = self.page_rows and self.P <= 8192 and n_cand <= 8192
+            if cache.budget_mode == "matched":
+                if not self.fused:
+                    raise ValueError("GraphDecoder runs matched Twilight budgets through the fused selection "
+                                     "(16-row pages, head_dim 128, R <= 8, <= 8192 candidate pages)")
+                # the matched target grows with the length while B0 stops at k
+                # pages: past that the reference's allocation raises, so refuse
+                # a decode that would reach it
+                L = self.max_length
+                sink_end = min(cache.sink_tokens, L)
+                recent_start = max(sink_end, L - max(0, cache.recent_tokens - 1))
+                eligible = recent_start - sink_end
+                cand = min(eligible // cache.block_size, self.P)
+                fixed = min(cand, max(1, math.ceil(cache.matched_budget_fraction * eligible / cache.block_size)))
+                if fixed > min(cand, self.k):
+                    raise ValueError("matched budget past the B0 candidates before max_new_tokens "
+                                     f"({fixed} > {min(cand, self.k)} pages)")
             words = (kernels.union_record_words(self.P) + 3) & ~3
             self.tw_rec = torch.zeros((self.G, words), dtype=torch.int32, device=dev)
             self.tw_desired = torch.zeros((self.G, self.R), dtype=torch.int32, device=dev)
@@ -339,7 +354,8 @@ class GraphDecoder:
                                           c._packed[e0:e0 + G], c._qscale[e0:e0 + G], c._qmin[e0:e0 + G], self.k,
                                           self.tw_rec, top_p=c.top_p, sink=c.sink_tokens, recent=c.recent_tokens,
                                           block_size=c.block_size, length=self.max_length, lengths=self.lengths,
-                                          desired=self.tw_desired)
+                                          desired=self.tw_desired, sel_pages=self.tw_sel, budget_mode=c.budget_mode,
+                                          matched_fraction=c.matched_budget_fraction)
             # the attention also appends the decode token and (fused) its INT4 row and page metadata
             meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G],
                         packed=c._packed[e0:e0 + G], scale=c._qscale[e0:e0 + G],

@@ -838,6 +838,7 @@ def twilight_select_fused(
     budget_mode: str = "dynamic",
     target_total: int = 0,
     allocated: Optional[torch.Tensor] = None,
+    matched_fraction: float = 0.0,
 ) -> torch.Tensor:
     """The Twilight selection of a layer in two launches with dynamic budgets
     (Quest score; one block per head: B0 top-k, INT4 QK, top-p, publish), or
@@ -847,11 +848,13 @@ def twilight_select_fused(
     group's union record: union_rec [G, >= union_record_words(P)] int32 (row
     stride a multiple of 4, 16-byte aligned).  q [G, R, 128] fp32;
     page_min/page_max [G, >= P, 128] over the P scored pages (16-bit);
-    packed/scale/minimum the INT4 keys.  lengths [G] int32 (device, dynamic
-    budgets only) for ragged groups, each clamped to `length`; else every
-    group has `length` tokens.  Returns desired [G, R] int32 (the top-p
-    counts); sel_pages [G, R, b0_pages], logits [G, R, b0_pages * 16] and
-    (matched) allocated [G, R] are optional outputs."""
+    packed/scale/minimum the INT4 keys.  lengths [G] int32 (device) for
+    ragged groups, each clamped to `length`; else every group has `length`
+    tokens.  Matched budgets take target_total rows per group for one
+    length, or with lengths each group's own target from matched_fraction
+    (the cache's fixed pages x 16 x R).  Returns desired [G, R] int32 (the
+    top-p counts); sel_pages [G, R, b0_pages], logits [G, R, b0_pages * 16]
+    and (matched) allocated [G, R] are optional outputs."""
     if budget_mode not in ("dynamic", "matched"):
         raise ValueError("budget_mode must be 'dynamic' or 'matched'")
     matched = budget_mode == "matched"
@@ -874,8 +877,9 @@ def twilight_select_fused(
         desired = torch.empty((G, R), dtype=torch.int32, device=dev)
     if matched:
         if lengths is not None:
-            raise ValueError("twilight_select_fused: matched budgets take one length for every group")
-        if not R <= target_total <= R * b0_pages * block_size:
+            if not 0.0 < matched_fraction <= 1.0:
+                raise ValueError("matched budgets over device lengths take 0 < matched_fraction <= 1")
+        elif not R <= target_total <= R * b0_pages * block_size:
             raise ValueError("target_total must be in [R, R * b0_pages * block_size]")
         if sel_pages is None:  # the last launch reads the B0 pages
             sel_pages = torch.empty((G, R, b0_pages), dtype=torch.int32, device=dev)
@@ -893,8 +897,9 @@ def twilight_select_fused(
             check(hip().tw_twilight_select_fused_matched(
                 ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D, page_min.stride(0), ptr(packed),
                 ptr(scale), ptr(minimum), qe, packed.shape[1], int(b0_pages), float(top_p), qs, sink, recent,
-                block_size, int(length), int(target_total), ptr(sel_pages), ptr(logits), ptr(desired),
-                ptr(allocated), ptr(union_rec), union_rec.stride(0), ptr(ws), ws.numel(), stream_handle(dev)),
+                block_size, ptr(lengths), int(length), int(target_total), float(matched_fraction), ptr(sel_pages),
+                ptr(logits), ptr(desired), ptr(allocated), ptr(union_rec), union_rec.stride(0), ptr(ws), ws.numel(),
+                stream_handle(dev)),
                 "twilight_select_fused_matched")
         else:
             check(hip().tw_twilight_select_fused(ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D,
