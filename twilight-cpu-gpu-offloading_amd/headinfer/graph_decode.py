@@ -354,7 +354,8 @@ class GraphDecoder:
                                           c._packed[e0:e0 + G], c._qscale[e0:e0 + G], c._qmin[e0:e0 + G], self.k,
                                           self.tw_rec, top_p=c.top_p, sink=c.sink_tokens, recent=c.recent_tokens,
                                           block_size=c.block_size, length=self.max_length, lengths=self.lengths,
-                                          desired=self.tw_desired, sel_pages=self.tw_sel, budget_mode=c.budget_mode,
+                                          desired=self.tw_desired, budget_mode=c.budget_mode,
+                                          sel_pages=self.tw_sel if c.budget_mode == "matched" else None,
                                           matched_fraction=c.matched_budget_fraction)
             # the attention also appends the decode token and (fused) its INT4 row and page metadata
             meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G],
