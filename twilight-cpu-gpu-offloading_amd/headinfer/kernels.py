@@ -10,6 +10,7 @@ for the zero-copy host path, in pinned host memory).
 
 from __future__ import annotations
 
+import functools
 import math
 from typing import Optional
 
@@ -576,7 +577,7 @@ def twilight_qk(
         out = torch.empty((G, R, N), dtype=torch.float32, device=dev)
     elif out.dtype != torch.float32 or tuple(out.shape) != (G, R, N) or not out.is_contiguous():
         raise ValueError("out must be contiguous [G, R, b0_pages*block_size] fp32")
-    qs = float(torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32)) if qk_scale is None else float(qk_scale)
+    qs = _default_qk_scale(D) if qk_scale is None else float(qk_scale)
     if (slot_u is None) != (page_rows is None):
         raise ValueError("slot_u and page_rows go together")
     if slot_u is not None:
@@ -793,6 +794,12 @@ def twilight_select_pages(
                                              ws.numel(), stream_handle(dev)), "twilight_select_pages")
 
 
+@functools.lru_cache(maxsize=None)
+def _default_qk_scale(D: int) -> float:
+    """1/sqrt(D) rounded to fp32 (the logit scale of the reference's INT4 QK)."""
+    return float(torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32))
+
+
 def union_record_words(P: int) -> int:
     """int32 words of one KV group's Twilight union record over P scored
     pages: a page bitmap (whole 64-bit words), then 16-bit row masks two
@@ -889,7 +896,7 @@ def twilight_select_fused(
                          (logits, torch.float32, (G, R, b0_pages * block_size)), (allocated, torch.int32, (G, R))):
         if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
             raise ValueError("twilight_select_fused output has the wrong dtype/shape")
-    qs = float(torch.tensor(1.0 / math.sqrt(D), dtype=torch.float32)) if qk_scale is None else float(qk_scale)
+    qs = _default_qk_scale(D) if qk_scale is None else float(qk_scale)
     nbytes = hip().tw_twilight_select_fused_workspace_size(G, R, P, int(b0_pages))
     ws = WORKSPACE.get(dev, "twilight_fused", nbytes)
     with on_device(dev):
