@@ -376,6 +376,7 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         # decode_layer with dynamic budgets runs the fused selection (union
         # record) when the shapes allow; False keeps the union-row path
         self.fused_decode = True
+        self._fused_bufs: Optional[tuple[torch.Tensor, torch.Tensor]] = None
         self._flat_union_keys: Optional[torch.Tensor] = None
         self._flat_union_values: Optional[torch.Tensor] = None
         self._dma = None  # HostGatherPipeline of post_selection_pipeline (host slabs)
@@ -709,9 +710,14 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         packed, qscale, qmin = self._quant(entries)
         if packed.shape[1] < self.sink_tokens + cand * self.block_size:
             return None
-        words = (kernels.union_record_words(cand) + 3) & ~3
-        rec = torch.empty((G, words), dtype=torch.int32, device=self.device)
-        desired = torch.empty((G, R), dtype=torch.int32, device=self.device)
+        # one record row per group, sized for every page of the metadata (the
+        # entry points take any row stride that is a multiple of 4 words), and
+        # the counts: allocated once, reused by every layer in stream order
+        if self._fused_bufs is None or self._fused_bufs[0].shape[0] != G or self._fused_bufs[1].shape[1] != R:
+            words = (kernels.union_record_words(int(self._page_min.shape[1])) + 3) & ~3
+            self._fused_bufs = (torch.empty((G, words), dtype=torch.int32, device=self.device),
+                                torch.empty((G, R), dtype=torch.int32, device=self.device))
+        rec, desired = self._fused_bufs
         start = self._phase_start()
         kernels.twilight_select_fused(queries.float().contiguous(), pmin, pmax, packed, qscale, qmin, b0, rec,
                                       top_p=self.top_p, sink=self.sink_tokens, recent=self.recent_tokens,
