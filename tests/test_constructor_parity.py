@@ -143,6 +143,20 @@ def test_twilight_candidate_budget_limit():
             _twilight()(**kw)
 
 
+def test_twilight_bad_windows_fail_in_the_quest_base():
+    """Matched budgets with block_size 0 (or a negative sink, or no recent
+    window) pass the Twilight checks and reach the Quest base, which refuses
+    them with its ValueError (quest_offload_cache.py:47-53): the device check
+    first, then the window check.  The candidate-budget limit must not divide
+    by the block size ahead of it."""
+    on_gpu = torch.cuda.is_available()
+    want = "invalid sink/recent/block configuration" if on_gpu else "an operational ROCm device is required"
+    dev = "cuda:0" if on_gpu else "cuda"
+    for bad in (dict(block_size=0), dict(block_size=-16), dict(sink_tokens=-1), dict(recent_tokens=0)):
+        with pytest.raises(ValueError, match=want):
+            _twilight()(**dict(BASE, device=dev), budget_mode="matched", **bad)
+
+
 def test_quest_accepts_more_than_eight_query_heads_per_kv():
     """The reference has no limit on query heads per KV head
     (quest_offload_cache.py:26-60); a 16-head group passes validation."""

@@ -323,6 +323,7 @@ def test_fused_matched_selection_ragged(K, dev):
         bits, masks = _decode_record(rec_h[gi], P)
         if cand == 0:
             assert np.all(des_h[gi] == 0) and not bits.any() and not masks.any(), gi
+            assert np.all(all_h[gi] == 0), (gi, all_h[gi])   # allocated was -7: written, not left
             kept = np.concatenate([np.arange(sink_end), np.arange(recent_start, Lg)]).astype(np.int64)
         else:
             b0g = min(b0, cand)

@@ -110,3 +110,12 @@ def test_cpu_token_union_matches_unique_and_rejects_outside():
         union([], 5001)
     with pytest.raises(ValueError, match="CPU int64"):
         union([torch.tensor([1], dtype=torch.int32)], 10)
+    # lists are checked one at a time, dtype then range (cpu_token_union.py:15-20):
+    # an out-of-range int64 list ahead of a float list is the range error, and
+    # the reverse order is the dtype error
+    with pytest.raises(ValueError, match="outside history"):
+        union([torch.tensor([12]), torch.tensor([1.0])], 10)
+    with pytest.raises(ValueError, match="CPU int64"):
+        union([torch.tensor([1.0]), torch.tensor([12])], 10)
+    with pytest.raises(ValueError, match="outside history"):
+        union([torch.tensor([0])], 0)

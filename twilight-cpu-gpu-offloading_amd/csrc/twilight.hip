@@ -2162,7 +2162,10 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_matched_rec_kernel(Matc
     target = fixed * BS * a.R;
     target = target < a.R * N ? target : a.R * N;
   }
-  if (N == 0) return;  // block-uniform: no candidate, nothing kept
+  if (N == 0) {  // block-uniform: no candidate, nothing kept, nothing allocated
+    if (tid == 0 && a.allocated != nullptr) a.allocated[row] = 0;
+    return;
+  }
   topk_fast_clear(sh.sel);
   // ---- one round trip: the group's counts, the row's pages, logits and ranges ----
   if (tid == 0) {

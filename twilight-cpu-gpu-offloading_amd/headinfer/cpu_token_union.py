@@ -28,15 +28,18 @@ class CpuTokenUnion:
     def __call__(self, positions: list[torch.Tensor], length: int) -> torch.Tensor:
         if not 0 <= length <= self.members.size:
             raise ValueError("invalid union length")
+        # one list at a time, dtype then range, as the reference checks them
+        # (cpu_token_union.py:15-20): the first bad list decides the error
         lists = []
         for selected in positions:
             if selected.device.type != "cpu" or selected.dtype != torch.int64:
                 raise ValueError("union expects CPU int64 indices")
-            lists.append(selected.contiguous().reshape(-1))
+            flat = selected.contiguous().reshape(-1)
+            if flat.numel() and (int(flat.min()) < 0 or int(flat.max()) >= length):
+                raise ValueError("selected position outside history")
+            lists.append(flat)
         out = torch.empty(length, dtype=torch.int64)
         if length == 0:
-            if any(t.numel() for t in lists):
-                raise ValueError("selected position outside history")
             return out
         n = len(lists)
         ptrs = (ctypes.c_void_p * max(n, 1))(*[t.data_ptr() for t in lists])

@@ -886,6 +886,19 @@ def twilight_select_fused(
         if lengths is not None:
             if not 0.0 < matched_fraction <= 1.0:
                 raise ValueError("matched budgets over device lengths take 0 < matched_fraction <= 1")
+            # each group's target is fixed(L_g) x 16 x R with fixed growing with
+            # L_g, and its capacity min(b0, candidate pages) x 16 per head: past
+            # b0 the reference's allocation raises (twilight_offload_cache.py:58-59),
+            # so a launch whose longest group (at most `length`) would get there
+            # is refused instead of clamped on the device
+            sink_end = min(sink, length)
+            recent_start = max(sink_end, length - max(0, recent - 1))
+            eligible = recent_start - sink_end
+            cand = min(eligible // block_size, P)
+            fixed = min(cand, max(1, math.ceil(matched_fraction * eligible / block_size)))
+            if cand > 0 and fixed > min(cand, b0_pages):
+                raise ValueError(f"target_total is infeasible: the matched budget at length {length} is {fixed} "
+                                 f"pages a head, past the {min(cand, b0_pages)} B0 pages")
         elif not R <= target_total <= R * b0_pages * block_size:
             raise ValueError("target_total must be in [R, R * b0_pages * block_size]")
         if sel_pages is None:  # the last launch reads the B0 pages

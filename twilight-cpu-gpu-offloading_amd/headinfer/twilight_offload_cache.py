@@ -287,11 +287,16 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         # The one limit the reference does not have: a top-p block holds at
         # most kernels.twilight_max_candidates() candidate tokens per head
         # (B0 pages x page size).  A budget the longest cache would take past
-        # it is refused here rather than at the first decode step.
+        # it is refused here rather than at the first decode step.  Windows the
+        # Quest base refuses (quest_offload_cache.py:52) reach it unchecked, so
+        # they fail with its error, as in the reference.
         block_size = int(kwargs.get("block_size", 16))
-        _, _, eligible = _window(int(kwargs["max_cache_len"]), int(kwargs.get("sink_tokens", 64)),
-                                 int(kwargs.get("recent_tokens", 256)))
-        widest = min(eligible // block_size, max(1, math.ceil(candidate_token_budget / block_size))) * block_size
+        sink_tokens = int(kwargs.get("sink_tokens", 64))
+        recent_tokens = int(kwargs.get("recent_tokens", 256))
+        widest = 0
+        if block_size > 0 and sink_tokens >= 0 and recent_tokens > 0:
+            _, _, eligible = _window(int(kwargs["max_cache_len"]), sink_tokens, recent_tokens)
+            widest = min(eligible // block_size, max(1, math.ceil(candidate_token_budget / block_size))) * block_size
         if widest > kernels.twilight_max_candidates():
             raise ValueError(
                 f"candidate_token_budget {candidate_token_budget} gives {widest} candidate tokens per head at "
