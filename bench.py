@@ -94,12 +94,16 @@ class QuestWorkload:
     PLANTED, OUTLIERS = 16, 4
 
     def __init__(self, dev, layers: int, context: int, budget_pages: int, seed: int = 1, requests: int = 1,
-                 union: str = "bits"):
+                 union: str = "bits", planted: int | None = None, outliers: int | None = None):
         import torch
 
         from headinfer import kernels
 
         self.dev, self.layers, self.L = dev, layers, context
+        # the 32K layer's structure by default; the 4K layer has 4 planted
+        # pages and no outlier channels
+        self.PLANTED = type(self).PLANTED if planted is None else planted
+        self.OUTLIERS = type(self).OUTLIERS if outliers is None else outliers
         # "bits": per-head selection bitmaps ranked by the attention; "plan":
         # the union plan built by the top-k's last block of each group
         self.union = union
@@ -195,6 +199,20 @@ class QuestWorkload:
             return torch.tensor([[sum(bin(int(x) & 0xffffffffffffffff).count("1") for x in u[l, g])
                                   for g in range(self.G)] for l in range(self.layers)], dtype=torch.float64)
         return self.plan_counts.double().cpu()
+
+    def selection_of(self, layer: int):
+        """Every head's selected pages at `layer` (ascending arrays, [G][R]),
+        read from what the timed step wrote: the selection bitmaps, or the
+        per-head page lists of the plan form."""
+        import numpy as np
+
+        if self.union == "bits":
+            w = self.bits[layer].cpu().numpy().view(np.uint32)
+            p = np.arange(self.P)
+            hb = ((w[:, :, p >> 5] >> (p & 31).astype(np.uint32)) & 1).astype(bool)   # [G, R, P]
+            return [[np.flatnonzero(hb[g, r]) for r in range(self.R)] for g in range(self.G)]
+        sel = self.sel[layer].long().cpu().numpy()
+        return [[sel[g, r] for r in range(self.R)] for g in range(self.G)]
 
     def append(self, layer: int) -> None:
         from headinfer import kernels
@@ -348,14 +366,14 @@ class TwilightWorkload:
                                 row_counts=self.row_counts[layer], desired=self.desired[layer], sink=self.SINK,
                                 recent=self.RECENT, block_size=self.BS, length=self.L)
 
-    def attend(self, layer: int) -> None:
+    def attend(self, layer: int, phase: int = 3) -> None:
         from headinfer import kernels
 
         if self.fused:
             kernels.decode_attention_union(self.q[layer], self.kc[layer], self.vc[layer], self.rec[layer], self.P,
                                            max_pages=self.width, sink=self.SINK, recent=self.RECENT,
                                            block_size=self.BS, length=self.L, append=True, cur_k=self.cur_k[layer],
-                                           cur_v=self.cur_v[layer], out=self.out[layer])
+                                           cur_v=self.cur_v[layer], out=self.out[layer], phase=phase)
             return
         if self.page_rows:
             kernels.decode_attention_page_rows(self.q[layer], self.kc[layer], self.vc[layer], self.plan_pages[layer],
@@ -402,7 +420,29 @@ class TwilightWorkload:
             self.select(layer)
             self.attend(layer)
 
+    def candidate_union_rows(self) -> float:
+        """Sum over groups of |C_g|, the union of the group's per-head B0
+        candidate rows (mean over layers), measured: the B0 pages are the
+        Quest top-b0 of each head, the same pages the selection launches
+        take, listed here by a separate top-k outside any timed region."""
+        import numpy as np
+
+        from headinfer import kernels
+
+        total = 0
+        for layer in range(self.layers):
+            kernels.quest_select(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P],
+                                 self.b0, sel_pages=self.sel[layer])
+            sel = self.sel[layer].cpu().numpy()
+            total += sum(np.unique(sel[g]).size for g in range(self.G)) * self.BS
+        return total / self.layers
+
     def bytes_per_layer(self) -> dict:
+        """Algorithmic HBM bytes per layer (mean over layers) by stage, as the
+        scope's measurement defines them: page min/max once per group, the
+        scores written and read back, the INT4 rows (codes, scale, minimum)
+        of Sum_g |C_g| candidates (the union of the heads' candidate sets),
+        the attended K/V rows, q and the output."""
         G, R, D, P, N = self.G, self.R, self.D, self.P, self.N
         e = 2
         if self.page_rows or self.fused:                                            # attended union rows
@@ -410,20 +450,22 @@ class TwilightWorkload:
         else:
             rows = self.row_counts.double().sum().item() / self.layers
         if self.fused:
-            # page min/max, scores out and back, every head's own B0 candidates'
-            # INT4 rows (codes + scale + min), q, the union records
-            cand_rows = G * R * N
-            select = (2 * P * D * e * G + G * R * P * 4 * 2 + cand_rows * (D // 2 + 2 * e) + G * R * D * 4
-                      + G * self.rec.shape[2] * 4)
-            if self.mode == "matched":  # the allocation launch reads the logits back
-                select += G * R * N * 4
+            cand_rows = self.candidate_union_rows()
         else:
             cand_rows = self.plan_counts.double().sum().item() * self.BS / self.layers   # union of the B0 candidates
-            select = (2 * P * D * e * G + G * R * P * 4 * 2 + G * R * self.b0 * 4 + cand_rows * (D // 2 + 2 * e)
-                      + G * R * N * 4 * 2 + G * R * D * 4)
+        int4 = cand_rows * (D // 2 + 2 * e)
+        score = 2 * P * D * e * G + G * R * P * 4 + G * R * D * 4      # metadata + q in, scores out
+        if self.fused:
+            # the head launch: the scores back, the INT4 rows, the union records
+            head = G * R * P * 4 + int4 + G * self.rec.shape[2] * 4
+            if self.mode == "matched":  # the allocation launch reads the logits back
+                head += G * R * N * 4
+        else:
+            head = G * R * P * 4 + G * R * self.b0 * 4 + int4 + G * R * N * 4 * 2
         attention = rows * 2 * D * e + 2 * G * R * D * e + 4 * G * D * e
-        return {"select": select, "attention": attention, "rows_per_group": rows / G,
-                "candidate_rows_per_group": cand_rows / G}
+        return {"select": score + head, "score": score, "head": head, "attention": attention,
+                "rows_per_group": rows / G, "candidate_rows_per_group": cand_rows / G,
+                "per_head_candidate_rows_per_group": R * N}
 
 
 class OffloadWorkload(QuestWorkload):
@@ -619,11 +661,72 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def _bits(t):
+    """A 16-bit float tensor's storage as uint16 (the oracle's input form)."""
+    import numpy as np
+    import torch
+
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _sampled(run, budget_s: float, cap: int) -> tuple[float, int]:
+    """Median seconds of run() over a bounded sample (at least 3 calls, then
+    until budget_s or cap calls), after one untimed call."""
+    run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < cap):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def quest_oracle_check(w: QuestWorkload, layer: int = 0) -> dict:
+    """The checker of the CPU-baseline leg: every head's pages the timed step
+    selected at `layer` against oracle.topk_sorted(oracle.quest_score(...))
+    (bit for bit, quest_offload_cache.py:362-374), and each head's attention
+    output within 2e-3 abs + 1e-2 rel of float64 over sink ++ the oracle's
+    pages ++ recent ++ the decode token."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    G, R, D, P, L = w.G, w.R, w.D, w.P, w.L
+    q = w.qf[layer].cpu().numpy()
+    sc = oracle.quest_score(q, _bits(w.pmin[layer, :, :P]), _bits(w.pmax[layer, :, :P]), "f16")
+    want = oracle.topk_sorted(sc.reshape(G * R, P), w.k).reshape(G, R, w.k)
+    got = w.selection_of(layer)
+    match = all(np.array_equal(got[g][r], want[g, r]) for g in range(G) for r in range(R))
+    sink_end, recent_start, _ = oracle.selection_window(L, w.SINK, w.RECENT)
+    kc, vc = w.kc[layer].cpu().float(), w.vc[layer].cpu().float()
+    out = w.out[layer].float().cpu().numpy()
+    err, att_ok = 0.0, True
+    for g in range(G):
+        for r in range(R):
+            pages = torch.from_numpy(want[g, r]).long()
+            rows = torch.cat([torch.arange(sink_end), (w.SINK + pages[:, None] * w.BS + torch.arange(w.BS)).reshape(-1),
+                              torch.arange(recent_start, L)])
+            keys = torch.cat([kc[g, rows], w.cur_k[layer, g:g + 1].cpu().float()]).numpy()
+            vals = torch.cat([vc[g, rows], w.cur_v[layer, g:g + 1].cpu().float()]).numpy()
+            ref = oracle.decode_attention(q[g, r:r + 1], keys, vals, 1.0 / math.sqrt(D))[0]
+            e = np.abs(out[g, r].astype(np.float64) - ref)
+            att_ok &= bool(np.all(e <= 2e-3 + 1e-2 * np.abs(ref)))
+            err = max(err, float(e.max()))
+    return {"ok": bool(match and att_ok), "selection_match": bool(match), "heads": G * R, "layer": layer,
+            "attention_max_abs_err": err,
+            "checker": "oracle.quest_score + oracle.topk_sorted (pages, bit for bit); float64 attention over "
+                       "the oracle's rows"}
+
+
 def cpu_baseline(w: QuestWorkload, seconds: float) -> dict:
     """The torch-CPU port of the reference's Quest layer step, on this box's
     host cores: with every core of the process's affinity (the headline) and
     with 6 threads (the reference's formal runs), median over a bounded sample,
-    with the time split into score + top-k, row gather and attention."""
+    with the time split into score + top-k, row gather and attention.  The
+    leg also checks layer 0 of the timed step against the oracle."""
     import torch
 
     from oracle.cpu_baseline import quest_layer_step
@@ -640,32 +743,107 @@ def cpu_baseline(w: QuestWorkload, seconds: float) -> dict:
     def sample(threads: int, budget_s: float) -> dict:
         torch.set_num_threads(threads)
         phases: dict = {}
+        calls = [0]
 
-        def run(ph=None):
+        def run():
+            calls[0] += 1
             return quest_layer_step(q, kc, vc, pmin, pmax, ck, cv, length=L, budget=w.k, sink=w.SINK,
-                                    recent=w.RECENT, block_size=w.BS, phases=ph)
+                                    recent=w.RECENT, block_size=w.BS, phases=phases)
 
-        run()
-        times = []
-        t_start = time.perf_counter()
-        while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
-            t0 = time.perf_counter()
-            run(phases)
-            times.append(time.perf_counter() - t0)
-        times.sort()
-        n = len(times)
-        return {"us_per_layer": round(times[n // 2] * 1e6, 1), "steps": n,
-                "phases_us": {k: round(v / n * 1e6, 1) for k, v in phases.items()}}
+        med, n = _sampled(run, budget_s, 200)
+        return {"us_per_layer": round(med * 1e6, 1), "steps": n,
+                "phases_us": {k: round(v / calls[0] * 1e6, 1) for k, v in phases.items()}}
 
     n_aff = len(os.sched_getaffinity(0))
     full = sample(n_aff, seconds)
     six = sample(6, seconds / 2)
     torch.set_num_threads(threads0)
     return {"value": full["us_per_layer"], "unit": "us/layer", "cores": n_aff, "kind": "port",
-            "sample": f"median of {full['steps']} single-layer steps (layer 0, all 8 KV heads, 32K context, torch "
-                      "CPU: where/sum score, topk, expand, index_select, SDPA math)",
+            "sample": f"median of {full['steps']} single-layer steps (layer 0, all {w.G} KV heads, {L // 1024}K "
+                      f"context, k = {w.k} pages, torch CPU: where/sum score, topk, expand, index_select, SDPA math)",
             "cpu_model": _cpu_model(), "phases_us": full["phases_us"],
-            "threads_6": {"value": six["us_per_layer"], "phases_us": six["phases_us"], "steps": six["steps"]}}
+            "threads_6": {"value": six["us_per_layer"], "phases_us": six["phases_us"], "steps": six["steps"]},
+            "oracle_check": quest_oracle_check(w, 0)}
+
+
+def twilight_oracle_check(w: "TwilightWorkload", layer: int = 0) -> dict:
+    """The checker of the Twilight CPU-baseline leg: for every group of
+    `layer`, the rows the timed step kept (its union record) == the union of
+    oracle.twilight_layer, the top-p counts equal, and the union attention
+    within 2e-3 abs + 1e-2 rel of float64 over the oracle's rows plus the
+    decode token (twilight_offload_cache.py:1144-1354)."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    G, D, P, L = w.G, w.D, w.P, w.L
+    union_ok = counts_ok = att_ok = True
+    err = 0.0
+    out = w.out[layer].float().cpu().numpy()
+    des = w.desired[layer].cpu().numpy()
+    kc, vc = w.kc[layer].cpu().float(), w.vc[layer].cpu().float()
+    for g in range(G):
+        ref = oracle.twilight_layer(w.qf[layer, g].cpu().numpy(), _bits(w.pmin[layer, g, :P]),
+                                    _bits(w.pmax[layer, g, :P]), w.packed[layer, g].cpu().numpy(),
+                                    _bits(w.scale[layer, g]), _bits(w.minimum[layer, g]), "bf16", length=L,
+                                    sink=w.SINK, recent=w.RECENT, block_size=w.BS, b0_pages=w.b0, top_p=w.TOP_P,
+                                    budget_mode=w.mode, fixed_pages=w.fixed)
+        counts_ok &= bool(np.array_equal(des[g], ref["desired"]))
+        union_ok &= bool(np.array_equal(w.kept_rows(layer, g).cpu().numpy(), ref["union"]))
+        rows = torch.from_numpy(ref["union"].astype(np.int64))
+        keys = torch.cat([kc[g, rows], w.cur_k[layer, g:g + 1].cpu().float()]).numpy()
+        vals = torch.cat([vc[g, rows], w.cur_v[layer, g:g + 1].cpu().float()]).numpy()
+        ref_o = oracle.decode_attention(w.qf[layer, g].cpu().numpy(), keys, vals, 1.0 / math.sqrt(D))
+        e = np.abs(out[g].astype(np.float64) - ref_o)
+        att_ok &= bool(np.all(e <= 2e-3 + 1e-2 * np.abs(ref_o)))
+        err = max(err, float(e.max()))
+    return {"ok": bool(union_ok and counts_ok and att_ok), "union_match": union_ok, "top_p_counts_match": counts_ok,
+            "groups": G, "layer": layer, "attention_max_abs_err": err,
+            "checker": "oracle.twilight_layer (B0 pages, INT4 QK, exact top-p, allocation, union); float64 "
+                       "attention over the oracle's rows"}
+
+
+def twilight_cpu_baseline(w: "TwilightWorkload", seconds: float) -> dict:
+    """The torch-CPU port of the reference's Twilight layer step
+    (oracle/cpu_baseline.py twilight_layer_step, dynamic or matched budgets
+    as the workload) on layer 0's inputs, with every core of the process's
+    affinity and with 6 threads, median over a bounded sample, with the time
+    split into phases; plus the oracle check of the timed step's layer 0."""
+    import torch
+
+    from oracle.cpu_baseline import twilight_layer_step
+
+    L = w.L
+    cpu = [t.cpu() for t in (w.q[0], w.kc[0, :, :L], w.vc[0, :, :L], w.pmin[0, :, : w.P], w.pmax[0, :, : w.P],
+                             w.packed[0], w.scale[0], w.minimum[0], w.cur_k[0], w.cur_v[0])]
+    threads0 = torch.get_num_threads()
+
+    def sample(threads: int, budget_s: float) -> dict:
+        torch.set_num_threads(threads)
+        phases: dict = {}
+        calls = [0]
+
+        def run():
+            calls[0] += 1
+            twilight_layer_step(*cpu, length=L, b0_pages=w.b0, top_p=w.TOP_P, sink=w.SINK, recent=w.RECENT,
+                                block_size=w.BS, budget_mode=w.mode, fixed_pages=w.fixed, phases=phases)
+
+        med, n = _sampled(run, budget_s, 100)
+        return {"us_per_layer": round(med * 1e6, 1), "steps": n,
+                "phases_us": {k: round(v / calls[0] * 1e6, 1) for k, v in phases.items()}}
+
+    n_aff = len(os.sched_getaffinity(0))
+    full = sample(n_aff, seconds)
+    six = sample(6, seconds / 2)
+    torch.set_num_threads(threads0)
+    return {"value": full["us_per_layer"], "unit": "us/layer", "cores": n_aff, "kind": "port",
+            "sample": f"median of {full['steps']} single-layer steps (layer 0, {w.G} KV heads, {L // 1024}K "
+                      f"context, B0 {w.N} tokens, top-p {w.TOP_P}, {w.mode} budgets; torch CPU: score, topk, "
+                      "INT4 dequant + matmul, argsort/softmax/cumsum top-p, union, index_select, SDPA)",
+            "cpu_model": _cpu_model(), "phases_us": full["phases_us"],
+            "threads_6": {"value": six["us_per_layer"], "phases_us": six["phases_us"], "steps": six["steps"]},
+            "oracle_check": twilight_oracle_check(w, 0)}
 
 
 def main(argv=None) -> int:
@@ -783,33 +961,48 @@ def main(argv=None) -> int:
         "parity": parity,
     }
     if not args.no_cpu_baseline:
-        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        print("[bench] CPU baseline + oracle check", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+        parity["oracle"] = result["cpu_baseline"]["oracle_check"]
+        parity["ok"] = parity["ok"] and parity["oracle"]["ok"]
     ok = parity["ok"]
     if not args.quest_only:
-        # the rest of the metric in the same line: the Twilight 32K layer, the
-        # 64K host-offload layer (zero-copy and side-stream DMA) and p50 TPOT
+        # the rest of the metric in the same line: the 4K layer, the Twilight
+        # 32K layer (dynamic and matched budgets), the 64K host-offload layer
+        # (zero-copy and side-stream DMA), p50 TPOT and the multi-request run
         del w, g_step, g_sel, g_att, g_att1
         torch.cuda.empty_cache()
         leg_args = argparse.Namespace(**vars(args))
-        leg_args.steps, leg_args.warmup, leg_args.no_cpu_baseline = 50, 5, True
+        leg_args.steps, leg_args.warmup = 50, 5
+        leg_args.cpu_seconds = args.cpu_seconds / 2
         leg_args.context = None
+        print("[bench] leg: quest4k", file=sys.stderr, flush=True)
+        q4 = quest4k_leg(leg_args, dev)
+        result["quest4k"] = q4
         print("[bench] leg: twilight32k", file=sys.stderr, flush=True)
         tw = twilight_leg(leg_args, dev)
-        result["twilight32k"] = {"layer_us": tw["layer_us"], "GBps": tw["value"], "kernels": tw["kernels"],
-                                 "rows_per_group": tw["rows_per_group"], "parity_ok": tw["parity"]["ok"]}
+        result["twilight32k"] = _leg_summary(tw)
         # the same layer with matched budgets, the reference cache's default budget mode
         print("[bench] leg: twilight32k matched", file=sys.stderr, flush=True)
         m_args = argparse.Namespace(**vars(leg_args))
         m_args.budget_mode, m_args.twilight_path = "matched", "fused"
         twm = twilight_leg(m_args, dev)
-        result["twilight32k_matched"] = {"layer_us": twm["layer_us"], "GBps": twm["value"],
-                                         "kernels": twm["kernels"], "rows_per_group": twm["rows_per_group"],
-                                         "parity_ok": twm["parity"]["ok"]}
+        result["twilight32k_matched"] = _leg_summary(twm)
+        print("[bench] leg: multireq", file=sys.stderr, flush=True)
+        mr = multireq_leg(leg_args, dev)
+        result["multireq"] = {k: mr[k] for k in ("value", "unit", "ms_per_step", "layer_us", "hbm_GBps",
+                                                 "host_link_GBps", "host_link_frac_pcie_gen5_x16",
+                                                 "rows_per_group", "steps")}
+        result["multireq"]["contexts"] = mr["config"]["contexts"]
+        result["multireq"]["parity_ok"] = mr["parity"]["ok"]
+        _release_pinned()
         print("[bench] leg: offload64k", file=sys.stderr, flush=True)
-        off = offload_leg(leg_args, dev)
+        off_args = argparse.Namespace(**vars(leg_args))
+        off_args.no_cpu_baseline = True
+        off = offload_leg(off_args, dev)
         result["offload64k"] = {"layer_us": off["layer_us"], "host_link": off["host_link"],
                                 "parity_ok": off["parity"]["ok"]}
+        _release_pinned()
         print("[bench] leg: tpot32k", file=sys.stderr, flush=True)
         model = tpot_model(dev)
         result["tpot32k"] = tpot_leg(leg_args, dev, model)
@@ -818,9 +1011,64 @@ def main(argv=None) -> int:
             result["tpot64k_host"] = tpot_leg(leg_args, dev, model, ctx=65536, kv="host", n_dec=16)
         del model
         torch.cuda.empty_cache()
-        ok = ok and tw["parity"]["ok"] and twm["parity"]["ok"] and off["parity"]["ok"]
+        ok = (ok and q4["parity_ok"] and tw["parity"]["ok"] and twm["parity"]["ok"] and off["parity"]["ok"]
+              and mr["parity"]["ok"])
     print(json.dumps(result), flush=True)
     return 0 if ok else 1
+
+
+def _release_pinned() -> None:
+    """Return the pinned host blocks a finished leg freed to the system
+    (torch keeps freed pinned memory cached; the next leg's slab is tens of
+    GB)."""
+    import gc
+
+    import torch
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
+
+
+def _leg_summary(leg: dict) -> dict:
+    out = {k: leg[k] for k in ("layer_us", "kernels", "rows_per_group", "candidate_rows_per_group", "roofline")}
+    out["GBps"] = leg["value"]
+    out["parity_ok"] = leg["parity"]["ok"]
+    if "cpu_baseline" in leg:
+        out["cpu_baseline"] = leg["cpu_baseline"]
+    return out
+
+
+def quest4k_leg(args, dev) -> dict:
+    """The 4K fp16 layer (8 KV heads x 4 query heads, k = 16 pages, 4 planted
+    pages, no outlier channels, seed 0): the configuration the reference's
+    torch-CPU path is quoted on, timed on the host cores (the CPU baseline
+    and its oracle check) and on the GPU through the same launches as the
+    32K layer."""
+    import torch
+
+    w = QuestWorkload(dev, args.layers, 4096, 16, seed=0, planted=4, outliers=0)
+    w.step()
+    torch.cuda.synchronize()
+    par = check_parity(w)
+    g_step = graph_of(w.step)
+    wall, _ = _timed_steps(g_step, args.steps, args.warmup)
+    w.step()
+    torch.cuda.synchronize()
+    by = w.bytes_per_layer()
+    layer_s = wall / w.layers
+    res = {"layer_us": round(layer_s * 1e6, 3), "GBps": round((by["select"] + by["attention"]) / layer_s / 1e9, 1),
+           "context": w.L, "budget_pages": w.k, "scored_pages": w.P, "rows_per_group": round(by["rows_per_group"], 1),
+           "dtype": "f16"}
+    ok = par["ok"]
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+        ok = ok and res["cpu_baseline"]["oracle_check"]["ok"]
+    res["parity_ok"] = ok
+    del w, g_step
+    torch.cuda.empty_cache()
+    return res
 
 
 def _timed_steps(step_graph, steps: int, warmup: int) -> tuple[float, float]:
@@ -873,6 +1121,8 @@ def twilight_leg(args, dev) -> dict:
     top-p + GQA union, then sparse attention over the union and the append)."""
     import torch
 
+    from headinfer import kernels
+
     ctx = args.context or 32768
     print(f"[bench] twilight inputs: layers={args.layers} context={ctx}", file=sys.stderr, flush=True)
     w = TwilightWorkload(dev, args.layers, ctx, args.budget_mode, path=args.twilight_path)
@@ -895,18 +1145,45 @@ def twilight_leg(args, dev) -> dict:
     g_step = graph_of(w.step)
     g_sel = graph_of(lambda: [w.select(i) for i in range(w.layers)])
     g_att = graph_of(lambda: [w.attend(i) for i in range(w.layers)])
+    g_att1 = graph_of(lambda: [w.attend(i, phase=1) for i in range(w.layers)]) if w.fused else None
+    # the score kernel alone (the fused selection's first launch), for the
+    # head launch's share of the selection
+    scores = torch.empty((w.G, w.R, w.P), dtype=torch.float32, device=dev)
+    g_score = graph_of(lambda: [kernels.fused_quest_score(w.qf[i], w.pmin[i, :, : w.P], w.pmax[i, :, : w.P],
+                                                          out=scores) for i in range(w.layers)])
     wall, _ = _timed_steps(g_step, args.steps, args.warmup)
     reps = max(20, args.steps // 2)
     t_sel = time_graph(g_sel, reps) / w.layers
     t_att = time_graph(g_att, reps) / w.layers
+    t_att1 = time_graph(g_att1, reps) / w.layers if g_att1 is not None else t_att
+    t_score = time_graph(g_score, reps) / w.layers
+    w.step()  # leave a complete step's outputs after the partial replays
+    torch.cuda.synchronize()
     by = w.bytes_per_layer()
     layer_s = wall / w.layers
     value = (by["select"] + by["attention"]) / layer_s / 1e9
+    t_head = max(t_sel - t_score, 1e-9)
     kern = {"twilight_select": {"us": round(t_sel * 1e6, 2), "bytes": int(by["select"]),
                                 "GBps": round(by["select"] / t_sel / 1e9, 1)},
-            "decode_attention": {"us": round(t_att * 1e6, 2), "bytes": int(by["attention"]),
-                                 "GBps": round(by["attention"] / t_att / 1e9, 1)}}
-    dom = "decode_attention" if t_att >= t_sel else "twilight_select"
+            "quest_score": {"us": round(t_score * 1e6, 2), "bytes": int(by["score"]),
+                            "GBps": round(by["score"] / t_score / 1e9, 1), "kernel": "quest_score_kernel"},
+            "twilight_head": {"us": round(t_head * 1e6, 2), "bytes": int(by["head"]),
+                              "GBps": round(by["head"] / t_head / 1e9, 1),
+                              "kernel": "twilight_head_kernel" + (" + twilight_matched_rec_kernel"
+                                                                  if w.mode == "matched" else ""),
+                              "us_from": "selection graph - score graph"},
+            "decode_attention": {"us": round(t_att1 * 1e6, 2), "bytes": int(by["attention"]),
+                                 "GBps": round(by["attention"] / t_att1 / 1e9, 1),
+                                 "kernel": "decode_attn_tiles over the union record (split-K, fused append)"},
+            "attention_merge": {"us": round((t_att - t_att1) * 1e6, 2), "kernel": "merge_vec_kernel"}}
+    if not w.fused:
+        for name in ("quest_score", "twilight_head", "attention_merge"):
+            kern.pop(name)
+    # the longest single kernel of the layer
+    dom = "decode_attention"
+    if w.fused and kern["twilight_head"]["us"] > kern["decode_attention"]["us"]:
+        dom = "twilight_head"
+    traffic = measured_traffic(dom, TWILIGHT_PROFILE) if w.fused and w.mode == "dynamic" else None
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
@@ -922,35 +1199,14 @@ def twilight_leg(args, dev) -> dict:
         "candidate_rows_per_group": round(by["candidate_rows_per_group"], 1),
         "kernels": kern,
         "roofline": {"bound": "hbm", "achieved": kern[dom]["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(kern[dom]["GBps"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom},
+                     "frac": round(kern[dom]["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom},
         "parity": {"ok": ok, "attention_max_abs_err": err},
     }
     if not args.no_cpu_baseline:
-        from oracle.cpu_baseline import twilight_layer_step
-
-        threads = min(16, len(os.sched_getaffinity(0)))
-        torch.set_num_threads(threads)
-        L = w.L
-        cpu = [t.cpu() for t in (w.q[0], w.kc[0, :, :L], w.vc[0, :, :L], w.pmin[0, :, : w.P], w.pmax[0, :, : w.P],
-                                 w.packed[0], w.scale[0], w.minimum[0], w.cur_k[0], w.cur_v[0])]
-
-        def run():
-            twilight_layer_step(*cpu, length=L, b0_pages=w.b0, top_p=w.TOP_P, sink=w.SINK, recent=w.RECENT,
-                                block_size=w.BS)
-
-        run()
-        times = []
-        t0 = time.perf_counter()
-        while len(times) < 3 or (time.perf_counter() - t0 < args.cpu_seconds and len(times) < 100):
-            t1 = time.perf_counter()
-            run()
-            times.append(time.perf_counter() - t1)
-        times.sort()
-        result["cpu_baseline"] = {"value": round(times[len(times) // 2] * 1e6, 1), "unit": "us/layer",
-                                  "cores": threads, "kind": "port",
-                                  "sample": f"median of {len(times)} single-layer steps (layer 0, 8 KV heads, torch "
-                                            "CPU: score, topk, INT4 dequant + matmul, argsort/softmax/cumsum top-p, "
-                                            "union, index_select, SDPA)"}
+        print(f"[bench] twilight {w.mode}: CPU baseline + oracle check", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = twilight_cpu_baseline(w, args.cpu_seconds)
+        result["parity"]["oracle"] = result["cpu_baseline"]["oracle_check"]
+        result["parity"]["ok"] = ok and result["parity"]["oracle"]["ok"]
     del w
     torch.cuda.empty_cache()
     return result
@@ -1425,6 +1681,12 @@ class MultiRequestWorkload:
 
 
 def run_multireq(args, dev) -> int:
+    result = multireq_leg(args, dev)
+    print(json.dumps(result), flush=True)
+    return 0 if result["parity"]["ok"] else 1
+
+
+def multireq_leg(args, dev) -> dict:
     """Multi-request decode: 256 steps of 8 requests x 28 layers, each layer
     one ragged Quest select + one ragged page-tile attention (decode-token
     append fused) + one ragged metadata update per residency set, the step
@@ -1476,8 +1738,9 @@ def run_multireq(args, dev) -> int:
         "setup_s": round(setup_s, 1),
         "parity": {"ok": ok, "attention_max_abs_err": err},
     }
-    print(json.dumps(result), flush=True)
-    return 0 if ok else 1
+    del w, g_step
+    torch.cuda.empty_cache()
+    return result
 
 
 def multireq_check(w) -> tuple[bool, float]:
@@ -1529,14 +1792,16 @@ def multireq_check(w) -> tuple[bool, float]:
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "pmc_traffic_quest32k.md"
-TRAFFIC_KERNEL = {"decode_attention": "decode_attn_tiles", "quest_select": "quest_score_kernel"}
+TWILIGHT_PROFILE = ROOT / "profiles" / "pmc_twilight32k.md"
+TRAFFIC_KERNEL = {"decode_attention": "decode_attn_tiles", "quest_select": "quest_score_kernel",
+                  "twilight_head": "twilight_head_kernel"}
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of the named kernel from the committed PMC
-    summary, or None when it is absent."""
+def measured_traffic(kernel: str, profile: Path = TRAFFIC_PROFILE):
+    """HBM bytes per launch of the named kernel from a committed PMC summary
+    (calibrated FETCH_SIZE + WRITE_SIZE), or None when it is absent."""
     try:
-        text = TRAFFIC_PROFILE.read_text()
+        text = profile.read_text()
     except OSError:
         return None
     for line in text.splitlines():

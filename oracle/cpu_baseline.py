@@ -75,15 +75,26 @@ def quest_layer_step(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
 def twilight_layer_step(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, page_min: torch.Tensor,
                         page_max: torch.Tensor, packed: torch.Tensor, scale: torch.Tensor, minimum: torch.Tensor,
                         cur_k: torch.Tensor, cur_v: torch.Tensor, *, length: int, b0_pages: int, top_p: float,
-                        sink: int, recent: int, block_size: int) -> torch.Tensor:
-    """One layer of the Twilight dynamic path on host tensors, in the
-    reference's op order (twilight_offload_cache.py:1128-1614): Quest B0 pages,
-    candidate expansion, INT4 dequantize + fp32 matmul / sqrt(D), argsort +
-    softmax + cumsum + searchsorted top-p, the per-group token union, then
-    index_select and SDPA over the union plus the decode token.
+                        sink: int, recent: int, block_size: int, budget_mode: str = "dynamic",
+                        fixed_pages: int = 0, phases: Optional[dict] = None) -> tuple[torch.Tensor, list]:
+    """One layer of the Twilight path on host tensors, in the reference's op
+    order (twilight_offload_cache.py:1128-1614): Quest B0 pages, candidate
+    expansion, INT4 dequantize + fp32 matmul / sqrt(D), argsort + softmax +
+    cumsum + searchsorted top-p, with matched budgets the largest-remainder
+    allocation towards fixed_pages x block_size x R (:1346-1354, :50-86),
+    the per-group token union, then index_select and SDPA over the union plus
+    the decode token.
 
     q [G,R,D]; k_cache/v_cache [G,>=L,D]; page metadata [G,P,D]; packed
-    [G,T,D/2] u8, scale/minimum [G,T]; cur_k/cur_v [G,D].  Returns [G,R,D]."""
+    [G,T,D/2] u8, scale/minimum [G,T]; cur_k/cur_v [G,D].  phases (optional)
+    accumulates seconds per phase: "score_select" (Quest B0), "int4_qk",
+    "top_p" (with the allocation), "union", "gather", "attention".  Returns
+    (out [G,R,D], the union of each group as an ascending int64 tensor)."""
+    from .oracle import matched_budget_counts
+
+    clock = time.perf_counter
+    t = {name: 0.0 for name in ("score_select", "int4_qk", "top_p", "union", "gather", "attention")}
+    t0 = clock()
     G, R, D = q.shape
     sink_end = min(sink, length)
     recent_start = max(sink_end, length - max(0, recent - 1))
@@ -94,26 +105,53 @@ def twilight_layer_step(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     pages = torch.topk(scores, k=b0_pages, dim=-1, sorted=False).indices.view(G, R, b0_pages)
     offsets = torch.arange(block_size)
     cand = (sink + pages.unsqueeze(-1) * block_size + offsets).reshape(G, R, -1)   # [G,R,N]
+    t["score_select"] += clock() - t0
     out = torch.empty_like(q)
+    unions = []
     scale_qk = 1.0 / math.sqrt(D)
+    threshold = torch.tensor(top_p)
     for g in range(G):
+        t1 = clock()
         low = (packed[g] & 0x0F)
         high = (packed[g] >> 4) & 0x0F
-        selected = [torch.arange(sink_end), torch.arange(recent_start, length)]
+        logits = []
         for r in range(R):
             pos = cand[g, r]
             codes = torch.stack((low[pos], high[pos]), dim=-1).flatten(-2).float()
             k_hat = codes * scale[g, pos].float().unsqueeze(-1) + minimum[g, pos].float().unsqueeze(-1)
-            logits = (k_hat @ qf[g, r]) * scale_qk
-            order = torch.argsort(logits, descending=True)
-            cum = torch.cumsum(torch.softmax(logits[order], dim=0), dim=0)
-            desired = min(int(torch.searchsorted(cum, torch.tensor(top_p), right=False)) + 1, pos.numel())
-            selected.append(pos[order[:desired]])
+            logits.append((k_hat @ qf[g, r]) * scale_qk)
+        t2 = clock()
+        orders, desired = [], []
+        for r in range(R):
+            order = torch.argsort(logits[r], descending=True)
+            cum = torch.cumsum(torch.softmax(logits[r][order], dim=0), dim=0)
+            desired.append(min(int(torch.searchsorted(cum, threshold, right=False)) + 1, order.numel()))
+            orders.append(order)
+        if budget_mode == "matched":
+            n = cand.shape[2]
+            allocated = matched_budget_counts(desired, fixed_pages * block_size * R, [n] * R)
+        else:
+            allocated = desired
+        t3 = clock()
+        selected = [torch.arange(sink_end), torch.arange(recent_start, length)]
+        selected += [cand[g, r][orders[r][:allocated[r]]] for r in range(R)]
         union = torch.unique(torch.cat(selected), sorted=True)
+        t4 = clock()
         keys = torch.cat((k_cache[g].index_select(0, union), cur_k[g:g + 1])).float()
         vals = torch.cat((v_cache[g].index_select(0, union), cur_v[g:g + 1])).float()
+        t5 = clock()
         o = F.scaled_dot_product_attention(qf[g].view(1, R, 1, D), keys.view(1, 1, -1, D).expand(1, R, -1, D),
                                            vals.view(1, 1, -1, D).expand(1, R, -1, D), is_causal=False,
                                            scale=scale_qk)
         out[g] = o.view(R, D).to(q.dtype)
-    return out
+        t6 = clock()
+        t["int4_qk"] += t2 - t1
+        t["top_p"] += t3 - t2
+        t["union"] += t4 - t3
+        t["gather"] += t5 - t4
+        t["attention"] += t6 - t5
+        unions.append(union)
+    if phases is not None:
+        for name, v in t.items():
+            phases[name] = phases.get(name, 0.0) + v
+    return out, unions

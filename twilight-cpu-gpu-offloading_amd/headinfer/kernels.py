@@ -325,14 +325,19 @@ def _check_score_inputs(q, page_min, page_max, what):
         raise ValueError(f"{what}: head_dim must be even and <= 256")
 
 
-def fused_quest_score(q: torch.Tensor, page_min: torch.Tensor, page_max: torch.Tensor) -> torch.Tensor:
+def fused_quest_score(q: torch.Tensor, page_min: torch.Tensor, page_max: torch.Tensor, *,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Quest upper-bound page score in the reference's explicit order
-    (twilight_fused_quest.py:35-46).  q [G,R,D] fp32, lo/hi [G,P,D]."""
+    (twilight_fused_quest.py:35-46).  q [G,R,D] fp32, lo/hi [G,P,D]; out
+    (optional) a contiguous [G,R,P] fp32 tensor to write."""
     _check_score_inputs(q, page_min, page_max, "fused_quest_score")
-    dev = _require_device(q, page_min, page_max, what="fused_quest_score")
+    dev = _require_device(q, page_min, page_max, out, what="fused_quest_score")
     G, R, D = q.shape
     P = page_min.shape[1]
-    out = torch.empty((G, R, P), dtype=torch.float32, device=dev)
+    if out is None:
+        out = torch.empty((G, R, P), dtype=torch.float32, device=dev)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (G, R, P) or not out.is_contiguous():
+        raise ValueError("fused_quest_score out must be a contiguous [G, R, P] float32 tensor")
     if P == 0:
         return out
     with on_device(dev):
