@@ -23,6 +23,7 @@
 
 #include <type_traits>
 
+#include "score_order.h"
 #include "select.h"
 #include "union_record.h"
 
@@ -1765,54 +1766,300 @@ __global__ __launch_bounds__(NT) void twilight_matched_kernel(SelectArgs s) {
                       reinterpret_cast<int32_t*>(sh.bin_mass));
 }
 
-// ------------------------------------------------ fused per-head selection
-// The Twilight selection of every (group, head) row after the score kernel,
-// in one launch: `parts` blocks per row, each of which
-//   1. picks the head's B0 pages (the top b0 of its page scores: block top-k
-//      with the one-pass fast path over the score kernel's tile key ranges),
-//      ascending, in LDS -- every part block of a row finds the same pages
-//      (the top-k is deterministic), so no block waits for another's;
-//   2. estimates the INT4 QK of its kPartPages of those pages (candidate n =
-//      row n % 16 of the (n / 16)-th B0 page): one 16-row page per
-//      matrix-core tile, v_mfma_i32_16x16x64_i8 with the head's three
-//      balanced fixed-point digits as A rows 0..2 and the page's codes as B
-//      columns, so lanes 0..15 hold S of rows 0..15 (the integers
-//      twilight_qk_kernel forms, hence the same logits), and publishes the
-//      logits to the workspace;
-// and the part block that arrives last (arrival counter per row, the
-// device-coherent handoff of arrive_last) reads the row's logits back and
+// ------------------------------------------------ fused Twilight selection
+// Two launches (three with matched budgets) select a whole layer.
+//
+// twilight_score_qk_kernel: block = (group g, tile of kSqTile pages), 512
+// threads, over every page the launch scores.  It
+//   1. scores the tile's pages for the group's R heads in the Quest order of
+//      quest_score_kernel (32 accumulators over channels d mod 32, chunk by
+//      chunk, then the adjacent-pair tree; every product an unfused fp32
+//      multiply of the page's max or min by q_d), so the scores are the same
+//      bits, and stores each head's per-tile key range for the top-k;
+//   2. estimates the INT4 QK of every row of those pages for all R heads on
+//      the matrix cores: v_mfma_i32_16x16x64_i8 with A row 4 h + t holding
+//      slice t of head h's balanced fixed-point digits (rows 4 h + 3 zero; two
+//      A tiles for R > 4) and B column n the codes of row n of one 16-row
+//      page, so lane group h of the product holds head h's three slice dots
+//      of row lane % 16 and forms the exact integer S in-lane (the integers
+//      twilight_qk_kernel forms, hence the same logits); the logits go to a
+//      per-head array indexed by row within the scored span.
+// The INT4 rows are read once for all R heads, from every CU at once, while
+// the B0 pages are still unknown: the scored span's rows rather than only
+// the union of the heads' B0 candidates, so that no launch waits on a top-k
+// before it reads them.  It also clears the group's union record.
+//
+// twilight_topp_head_kernel: block = one (group, head) row, 512 threads.  It
+//   1. picks the head's B0 pages (the top b0 page scores: block top-k with the
+//      one-pass fast path over the tile key ranges, the digit search when the
+//      fast path gives up), ascending;
+//   2. gathers the logits of those pages' rows (candidate n = row n % 16 of
+//      the (n / 16)-th B0 page) and their max and key range (one block
+//      reduction);
 //   3. runs the top-p with dynamic budgets (the exact integer-mass rule of
 //      twilight_topp_kernel);
 //   4. ORs each page's kept rows into its 16-bit mask and the page's bit into
-//      the group's page bitmap (global atomics into the union record the
-//      score kernel cleared; a page whose rows no head keeps is not in the
-//      union).
-// The part blocks spread the INT4 rows' reads over parts x G x R CUs; the
-// top-k each repeats reads 4 bytes a page from L2.  D = 128, 16-row pages,
-// 16-bit keys.
+//      the group's page bitmap (global atomics into the cleared record; a
+//      page whose rows no head keeps is not in the union).
+// With matched budgets it stops after the top-p count and leaves the
+// candidates' logits and key ranges for twilight_matched_rec_kernel.
+// D = 128, 16-row pages, 16-bit keys.
 constexpr int kHeadThreads = 512;
-constexpr int kPartPages = 32;  // B0 pages a part block estimates: 4 per wavefront
+constexpr int kSqTile = 64;       // pages per block of the score + QK launch
+constexpr int kSqThreads = 512;   // 8 wavefronts: two per head for the score, 8 pages each for the QK
 
-struct HeadArgs {
-  const float* scores;   // FusedScores
-  int64_t score_stride;
-  int vec_last4;
-  const uint2* tile_mm;
-  int G, R, P, b0;       // P: scored pages of the launch; b0: B0 pages per head
-  int parts;             // part blocks per row: ceil(b0 / kPartPages)
-  const int32_t* lengths;  // nullable: group g has min(lengths[g], length) tokens
-  int length;
+struct ScoreQkArgs {
+  const float* q;          // [G][R][128]
+  const void* pmin;        // group g page p at + g * group_stride + p * 128
+  const void* pmax;
+  int64_t group_stride;
+  int G, R, P;             // P: pages the launch scores (every group's P_g <= P)
+  const int32_t* lengths;  // nullable: group g has lengths[g] tokens (its P_g from the windows)
   int sink, recent;
-  const float* q;        // [G][R][128]
-  const uint8_t* packed; // entry g row t at + (g * qstride + t) * 64
+  const uint8_t* packed;   // entry g row t at + (g * qstride + t) * 64
   const void* scale;
   const void* minimum;
   int64_t qstride, qrows;
   float qk_scale;
+  float* scores;           // [G * R][score_stride]
+  int64_t score_stride;
+  uint2* tile_mm;          // [G * R][tiles] (max, min) score key of a tile's pages
+  float* logits;           // [G * R][logit_stride]: row sink + 16 p + i at 16 p + i
+  int64_t logit_stride;
+  uint32_t* rec;           // union records to clear, rec_stride words apart
+  int64_t rec_stride;
+  unsigned int* zero_counters;  // nullable: block 0 zeroes n_counters of them
+  int n_counters;
+};
+
+template <typename DT, int RMAX>
+__global__ __launch_bounds__(kSqThreads) void twilight_score_qk_kernel(ScoreQkArgs a) {
+  using S = typename DT::storage;
+  constexpr int D = 128;
+  constexpr int BS = 16;
+  constexpr int KW = D / 8;                      // code words of a row
+  constexpr int kWv = kSqThreads / kWave;        // wavefronts
+  constexpr int kPitch = D * 2 + 16;             // padded LDS row of page extrema (bytes)
+  constexpr int kQuads = D * 2 / 16;             // 16-byte quads of a row of extrema
+  constexpr int kMetaPer = 2 * kSqTile * kQuads / kSqThreads;
+  constexpr int kPg = kSqTile / kWv;             // 16-row pages a wavefront estimates
+  constexpr int HT = RMAX / 4;                   // A tiles of four heads
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  static_assert(RMAX == 4 || RMAX == 8, "4 or 8 head slots");
+  static_assert(kMetaPer * kSqThreads == 2 * kSqTile * kQuads && kPg * kWv == kSqTile, "tile shape");
+  __shared__ __align__(16) uint8_t s_meta[2 * kSqTile * kPitch];
+  __shared__ __align__(16) float s_qv[RMAX * D];
+  __shared__ float s_half[RMAX][kWave];
+  __shared__ __align__(16) uint32_t s_q[RMAX * 6 * KW];
+  __shared__ int s_qshift[RMAX];
+  __shared__ float s_qsum[RMAX];
+  __shared__ int s_qok[RMAX];
+  const int tiles = (a.P + kSqTile - 1) / kSqTile;
+  const int g = blockIdx.x / tiles;
+  const int tile = blockIdx.x - g * tiles;
+  const int p0 = tile * kSqTile;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = lane_id();
+  const int wave = wave_uniform(tid / kWave);
+  const int R = a.R;
+  const int np_cap = (a.P - p0) < kSqTile ? (a.P - p0) : kSqTile;
+
+  // ---- round trip 1: the length, q, the tile's extrema and INT4 rows ----
+  // (every load unconditional, indices clamped, so they issue back to back)
+  const int length = *(a.lengths != nullptr ? a.lengths + g : reinterpret_cast<const int32_t*>(a.q));
+  const int nq = R * D;
+  const float* qg = a.q + static_cast<int64_t>(g) * nq;
+  const float qv0 = qg[tid < nq ? tid : nq - 1];
+  const float qv1 = qg[tid + kSqThreads < nq ? tid + kSqThreads : nq - 1];
+  QStage<D, RMAX> qst;
+  qst.load(qg, R);
+  const S* mn = static_cast<const S*>(a.pmin) + g * a.group_stride + static_cast<int64_t>(p0) * D;
+  const S* mx = static_cast<const S*>(a.pmax) + g * a.group_stride + static_cast<int64_t>(p0) * D;
+  const int meta_last = 2 * np_cap * kQuads - 1;
+  uint4 mv[kMetaPer];
+#pragma unroll
+  for (int j = 0; j < kMetaPer; ++j) {
+    int i = tid + j * kSqThreads;
+    i = i < meta_last ? i : meta_last;
+    const bool hi = i >= np_cap * kQuads;
+    const int rem = i - (hi ? np_cap * kQuads : 0);
+    mv[j] = load_stream(reinterpret_cast<const uint4*>(hi ? mx : mn) + rem);
+  }
+  const int G4 = lane / 16;
+  const int n = lane % 16;
+  const uint8_t* pk = a.packed + static_cast<int64_t>(g) * a.qstride * (D / 2);
+  const S* scl = static_cast<const S*>(a.scale) + static_cast<int64_t>(g) * a.qstride;
+  const S* mnq = static_cast<const S*>(a.minimum) + static_cast<int64_t>(g) * a.qstride;
+  uint4 cw[kPg];
+  S sv[kPg], mq[kPg];
+#pragma unroll
+  for (int i = 0; i < kPg; ++i) {
+    const int pl = wave + kWv * i;
+    int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(p0 + (pl < np_cap ? pl : np_cap - 1)) * BS + n;
+    t = (t >= 0 && t < a.qrows) ? t : 0;
+    cw[i] = load_stream(pk + t * (D / 2) + 16 * G4);
+    sv[i] = scl[t];
+    mq[i] = mnq[t];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // ---- the launch's bookkeeping: the group's union record, the counters ----
+  if (a.zero_counters != nullptr && g == 0 && tile == 0) {
+    for (int i = tid; i < a.n_counters; i += kSqThreads) a.zero_counters[i] = 0u;
+  }
+  if (a.rec != nullptr) {
+    // bitmap words 2 tile and 2 tile + 1, mask words [32 tile, 32 tile + 32)
+    uint32_t* rec = a.rec + g * a.rec_stride;
+    const int mw = (p0 >> 1) + tid - 2;
+    if (tid < 2)
+      rec[2 * tile + tid] = 0u;
+    else if (tid < 2 + kSqTile / 2 && mw < union_mask_words(a.P))
+      rec[union_mask_offset(a.P) + mw] = 0u;
+  }
+  // ---- extrema and q to LDS, q in fixed point ----
+#pragma unroll
+  for (int j = 0; j < kMetaPer; ++j) {
+    int i = tid + j * kSqThreads;
+    i = i < meta_last ? i : meta_last;
+    const bool hi = i >= np_cap * kQuads;
+    const int rem = i - (hi ? np_cap * kQuads : 0);
+    const int page = rem / kQuads;
+    const int qd = rem - page * kQuads;
+    *reinterpret_cast<uint4*>(s_meta + ((hi ? kSqTile : 0) + page) * kPitch + qd * 16) = mv[j];
+  }
+  s_qv[tid < nq ? tid : nq - 1] = qv0;
+  if (RMAX > 4) s_qv[tid + kSqThreads < nq ? tid + kSqThreads : nq - 1] = qv1;
+  stage_qfix<D, RMAX, true>(qst, R, s_q, s_qshift, s_qsum, s_qok);
+  const int P = a.lengths != nullptr ? ragged_pages(length, a.sink, a.recent, BS, a.P) : a.P;
+  const int np = (P - p0) < kSqTile ? (P - p0) : kSqTile;  // <= 0: a ragged group's tile past its pages
+  __syncthreads();
+
+  // ---- 1. scores: wavefronts w and w + 4 sum halves of head w (+4), lane = page ----
+  const int half = wave / 4;
+  const int hw = wave % 4;
+  {
+    const uint8_t* min_row = s_meta + lane * kPitch;
+    const uint8_t* max_row = s_meta + (kSqTile + lane) * kPitch;
+    float part[HT];
+#pragma unroll
+    for (int h = 0; h < HT; ++h) {
+      const int r = 4 * h + hw;
+      part[h] = 0.0f;
+      if (r < R) {
+        const float* qh = s_qv + r * D;
+        float acc[16];
+#pragma unroll
+        for (int l = 0; l < 16; ++l) acc[l] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int d0 = 32 * c + 16 * half + 8 * e;
+            float qv[8], x[8];
+            *reinterpret_cast<float4*>(qv) = *reinterpret_cast<const float4*>(qh + d0);
+            *reinterpret_cast<float4*>(qv + 4) = *reinterpret_cast<const float4*>(qh + d0 + 4);
+            select8(min_row + d0 * 2, max_row + d0 * 2, qv, x, DT{});
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[8 * e + i] = acc[8 * e + i] + x[i] * qv[i];
+          }
+        }
+#pragma unroll
+        for (int w = 1; w < 16; w <<= 1) {
+#pragma unroll
+          for (int l = 0; l < 16; l += 2 * w) acc[l] = acc[l] + acc[l + w];
+        }
+        part[h] = acc[0];
+      }
+      if (half == 1) s_half[r < RMAX ? r : RMAX - 1][lane] = part[h];
+    }
+    __syncthreads();
+    if (half == 0 && np > 0) {
+#pragma unroll
+      for (int h = 0; h < HT; ++h) {
+        const int r = 4 * h + hw;
+        if (r >= R) continue;
+        const float sc = part[h] + s_half[r][lane];
+        const int64_t row = static_cast<int64_t>(g) * R + r;
+        if (lane < np) a.scores[row * a.score_stride + p0 + lane] = sc;
+        const uint32_t key = score_key(sc);
+        const uint32_t kmax = wave_max_u32(lane < np ? key : 0u);
+        const uint32_t kmin = wave_min_u32(lane < np ? key : 0xffffffffu);
+        if (lane == 0) a.tile_mm[row * tiles + tile] = make_uint2(kmax, kmin);
+      }
+    }
+  }
+
+  // ---- 2. INT4 QK of the tile's rows for every head ----
+  v4i av[HT][2];
+  {
+    const int mrow = lane % 16;
+#pragma unroll
+    for (int h = 0; h < HT; ++h) {
+      const int r = 4 * h + mrow / 4;
+      const int t = mrow % 4;
+      const bool live = t < 3 && r < R;
+      const uint32_t* st = s_q + (r < R ? r : 0) * 6 * KW + (t < 3 ? t : 0) * 2 * KW;
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp) {
+        const int k0 = 4 * G4 + 2 * sp;
+        av[h][sp][0] = live ? static_cast<int>(st[k0]) : 0;
+        av[h][sp][1] = live ? static_cast<int>(st[KW + k0]) : 0;
+        av[h][sp][2] = live ? static_cast<int>(st[k0 + 1]) : 0;
+        av[h][sp][3] = live ? static_cast<int>(st[KW + k0 + 1]) : 0;
+      }
+    }
+  }
+  float* lbase[HT];
+  int qshift[HT];
+  float qsum[HT];
+  bool qok[HT];
+#pragma unroll
+  for (int h = 0; h < HT; ++h) {
+    const int r = 4 * h + G4 < R ? 4 * h + G4 : R - 1;
+    lbase[h] = a.logits + (static_cast<int64_t>(g) * R + r) * a.logit_stride + static_cast<int64_t>(p0) * BS + n;
+    qshift[h] = s_qshift[r];
+    qsum[h] = s_qsum[r];
+    qok[h] = s_qok[r] != 0;
+  }
+#pragma unroll
+  for (int i = 0; i < kPg; ++i) {
+    const int pl = wave + kWv * i;
+    v4i b0v, b1v;
+    b0v[0] = static_cast<int>(cw[i].x & 0x0f0f0f0fu);
+    b0v[1] = static_cast<int>((cw[i].x >> 4) & 0x0f0f0f0fu);
+    b0v[2] = static_cast<int>(cw[i].y & 0x0f0f0f0fu);
+    b0v[3] = static_cast<int>((cw[i].y >> 4) & 0x0f0f0f0fu);
+    b1v[0] = static_cast<int>(cw[i].z & 0x0f0f0f0fu);
+    b1v[1] = static_cast<int>((cw[i].z >> 4) & 0x0f0f0f0fu);
+    b1v[2] = static_cast<int>(cw[i].w & 0x0f0f0f0fu);
+    b1v[3] = static_cast<int>((cw[i].w >> 4) & 0x0f0f0f0fu);
+    const float sf = to_f32(DT{}, sv[i]), mf = to_f32(DT{}, mq[i]);
+#pragma unroll
+    for (int h = 0; h < HT; ++h) {
+      v4i c = {0, 0, 0, 0};
+      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[h][0], b0v, c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[h][1], b1v, c, 0, 0, 0);
+      const int64_t Sd = (static_cast<int64_t>(c[0]) << 16) + (static_cast<int64_t>(c[1]) << 8) + c[2];
+      const float lg = qk_logit(Sd, qshift[h], qsum[h], qok[h], sf, mf, a.qk_scale);
+      if (4 * h + G4 < R && pl < np) lbase[h][pl * BS] = lg;
+    }
+  }
+}
+
+struct HeadArgs {
+  const float* scores;   // score_qk's page scores
+  int64_t score_stride;
+  int vec_last4;
+  const uint2* tile_mm;
+  int G, R, P, b0;       // P: scored pages of the launch; b0: B0 pages per head
+  int parts;             // range entries per row over kWave (1: one per wavefront)
+  const int32_t* lengths;  // nullable: group g has min(lengths[g], length) tokens
+  int length;
+  int sink, recent;
+  const float* qk_logits;  // score_qk's logits, [G * R][logit_stride]
+  int64_t logit_stride;
   uint32_t p24;
-  unsigned int* counters;  // [G * R] arrival counters (zero between launches)
-  float* ws_logits;        // [G * R][b0 * 16] the rows' logits, handed to the last block
-  uint32_t* ws_range;      // [G * R][parts * 8][4] each wavefront's (max logit, max key, min key, 0)
+  float* ws_logits;        // matched: [G * R][b0 * 16] the candidates' logits
+  uint32_t* ws_range;      // matched: [G * R][8][4] each wavefront's (max logit, max key, min key, 0)
   int32_t* sel_pages;    // nullable [G][R][b0]: B0 pages ascending, -1 past a ragged group's
   float* logits;         // nullable [G][R][b0 * 16]
   int32_t* desired;      // [G][R]
@@ -1848,33 +2095,26 @@ __device__ __forceinline__ void or_into_record(uint32_t taken, const int* s_page
   }
 }
 
-template <typename DT, int KPA, int KPB>
-__global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a) {
+template <int KPA, int KPB>
+__global__ __launch_bounds__(kHeadThreads) void twilight_topp_head_kernel(HeadArgs a) {
   constexpr int NT = kHeadThreads;
   constexpr int BS = 16;
   constexpr int kSlots = KPB * NT / BS;  // B0 pages a row holds
-  constexpr int KW = 16;                 // code words of a 128-channel row
   constexpr int kWv = NT / kWave;        // wavefronts
-  constexpr int BT = kPartPages / kWv;   // pages per wavefront
-  using S = typename DT::storage;
-  typedef int v4i __attribute__((ext_vector_type(4)));
-  static_assert(KPA % 4 == 0 && (KPB == 8 || KPB == 16) && BT * kWv == kPartPages, "block shape");
+  static_assert(KPA % 4 == 0 && (KPB == 8 || KPB == 16), "block shape");
   __shared__ __align__(16) TopShared<NT> sh;
   __shared__ int s_page[kSlots];
-  __shared__ __align__(16) uint32_t s_q[4 * 6 * KW];
-  __shared__ int s_qshift[4];
-  __shared__ float s_qsum[4];
-  __shared__ int s_qok[4];
+  __shared__ float s_rmax[kWv];
+  __shared__ uint32_t s_rkx[kWv], s_rkn[kWv];
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
   const int wave = tid / kWave;
-  const int row = blockIdx.x / a.parts;
-  const int part = blockIdx.x - row * a.parts;
+  const int row = blockIdx.x;
   const int g = row / a.R;
   topk_fast_clear(sh.sel);
   __syncthreads();
-  // ---- round trip 1: length, the row's keys and tile ranges, q ----
-  int length = __hip_atomic_load(a.lengths != nullptr ? a.lengths + g : reinterpret_cast<const int32_t*>(a.q),
+  // ---- round trip 1: length, the row's keys and tile ranges ----
+  int length = __hip_atomic_load(a.lengths != nullptr ? a.lengths + g : reinterpret_cast<const int32_t*>(a.scores),
                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   uint32_t key[KPA];
   {
@@ -1891,26 +2131,23 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a)
       key[4 * q4 + 3] = score_key(v.w);
     }
   }
-  const int tiles = (a.P + 63) / 64;
+  const int tiles = (a.P + kSqTile - 1) / kSqTile;
   uint2 tr0, tr1;
   {
     const uint2* tm = a.tile_mm + static_cast<int64_t>(row) * tiles;
     tr0 = tm[lane < tiles ? lane : tiles - 1];
     tr1 = tm[lane + kWave < tiles ? lane + kWave : tiles - 1];
   }
-  QStage<128, 4> qst;
-  qst.load(a.q + static_cast<int64_t>(row) * 128, 1);
+
   length = a.lengths != nullptr ? (length < 0 ? 0 : (length > a.length ? a.length : length)) : a.length;
   const int P = a.lengths != nullptr ? ragged_pages(length, a.sink, a.recent, BS, a.P) : a.P;
   const int b0 = a.b0 < P ? a.b0 : P;  // block-uniform
   const int N = b0 * BS;
-  // the head's query in fixed point (the first wavefront; barriers below)
-  stage_qfix<128, 4, true>(qst, 1, s_q, s_qshift, s_qsum, s_qok);
 
   // ---- 1. the B0 pages ----
   uint32_t take = 0u;
   if (b0 > 0) {
-    const int tg = (P + 63) / 64;
+    const int tg = (P + kSqTile - 1) / kSqTile;
     const uint32_t kmax = wave_max_u32(max(lane < tg ? tr0.x : 0u, lane + kWave < tg ? tr1.x : 0u));
     const uint32_t kmin =
         wave_min_u32(min(lane < tg ? tr0.y : 0xffffffffu, lane + kWave < tg ? tr1.y : 0xffffffffu));
@@ -1936,147 +2173,80 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a)
   if (tid == 0) sh.sel.ncand = 0u;
   if (tid < kWave) sh.sel.cpair[tid] = 0ull;
   __syncthreads();
-  if (part == 0 && a.sel_pages != nullptr) {
+  if (a.sel_pages != nullptr) {
     for (int i = tid; i < a.b0; i += NT) a.sel_pages[static_cast<int64_t>(row) * a.b0 + i] = i < b0 ? s_page[i] : -1;
   }
   if (N == 0) {
-    if (part == 0 && tid == 0) a.desired[row] = 0;
-    return;  // every part block of the row: no candidate, no arrival
+    if (tid == 0) a.desired[row] = 0;
+    return;  // block-uniform: no candidate
   }
 
-  // ---- 2. INT4 QK of the part's pages, one page per matrix-core tile ----
-  float* wl = a.ws_logits + static_cast<int64_t>(row) * a.b0 * BS;
+  // ---- 2. round trip 2: the candidates' logits (KPB consecutive rows of one
+  // B0 page a thread), their max and key range ----
+  const int c0 = KPB * tid;
+  float v[KPB];
   {
-    const int G4 = lane / 16;
-    const int mrow = lane % 16;
-    v4i av[2];
-    {
-      // A row m < 3 = slice m of the head (balanced digits), rows 3..15 zero;
-      // lane group G4 holds channel words 4 G4 + 2 sp and + 1 as [even, odd]
-      const bool live = mrow < 3;
-      const uint32_t* st = s_q + (live ? mrow : 0) * 2 * KW;
+    const int slot = c0 < N ? c0 / BS : 0;
+    const float* src = a.qk_logits + static_cast<int64_t>(row) * a.logit_stride +
+                       static_cast<int64_t>(s_page[slot]) * BS + (c0 % BS);
 #pragma unroll
-      for (int sp = 0; sp < 2; ++sp) {
-        const int k0 = 4 * G4 + 2 * sp;
-        av[sp][0] = live ? static_cast<int>(st[k0]) : 0;
-        av[sp][1] = live ? static_cast<int>(st[KW + k0]) : 0;
-        av[sp][2] = live ? static_cast<int>(st[k0 + 1]) : 0;
-        av[sp][3] = live ? static_cast<int>(st[KW + k0 + 1]) : 0;
-      }
-    }
-    const int qshift = s_qshift[0];
-    const float qsum = s_qsum[0];
-    const bool qok = s_qok[0] != 0;
-    const uint8_t* pk = a.packed + static_cast<int64_t>(g) * a.qstride * 64;
-    const S* sc = static_cast<const S*>(a.scale) + static_cast<int64_t>(g) * a.qstride;
-    const S* mn = static_cast<const S*>(a.minimum) + static_cast<int64_t>(g) * a.qstride;
-    uint4 cw[BT];
-    S sv[BT], mv[BT];
-    float wmax = -INFINITY;
-    uint32_t wkmax = 0u, wkmin = 0xffffffffu;
-    // pages part * kPartPages + wave + kWv * j (clamped into the B0 pages)
-#pragma unroll
-    for (int j = 0; j < BT; ++j) {
-      int s = part * kPartPages + wave + kWv * j;
-      s = s < b0 ? s : b0 - 1;
-      int64_t t = static_cast<int64_t>(a.sink) + static_cast<int64_t>(s_page[s]) * BS + mrow;
-      t = (t >= 0 && t < a.qrows) ? t : 0;
-      cw[j] = *reinterpret_cast<const uint4*>(pk + t * 64 + 16 * G4);
-      sv[j] = sc[t];
-      mv[j] = mn[t];
-    }
-#pragma unroll
-    for (int j = 0; j < BT; ++j) {
-      const int s = part * kPartPages + wave + kWv * j;
-      v4i b0v, b1v;
-      b0v[0] = static_cast<int>(cw[j].x & 0x0f0f0f0fu);
-      b0v[1] = static_cast<int>((cw[j].x >> 4) & 0x0f0f0f0fu);
-      b0v[2] = static_cast<int>(cw[j].y & 0x0f0f0f0fu);
-      b0v[3] = static_cast<int>((cw[j].y >> 4) & 0x0f0f0f0fu);
-      b1v[0] = static_cast<int>(cw[j].z & 0x0f0f0f0fu);
-      b1v[1] = static_cast<int>((cw[j].z >> 4) & 0x0f0f0f0fu);
-      b1v[2] = static_cast<int>(cw[j].w & 0x0f0f0f0fu);
-      b1v[3] = static_cast<int>((cw[j].w >> 4) & 0x0f0f0f0fu);
-      v4i c = {0, 0, 0, 0};
-      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[0], b0v, c, 0, 0, 0);
-      c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[1], b1v, c, 0, 0, 0);
-      if (lane < 16 && s < b0) {
-        const int64_t Sd = (static_cast<int64_t>(c[0]) << 16) + (static_cast<int64_t>(c[1]) << 8) + c[2];
-        const float lg = qk_logit(Sd, qshift, qsum, qok, to_f32(DT{}, sv[j]), to_f32(DT{}, mv[j]), a.qk_scale);
-        publish_f32(wl + s * BS + lane, lg);
-        const uint32_t k = score_key(lg);
-        wmax = lg > wmax ? lg : wmax;
-        wkmax = k > wkmax ? k : wkmax;
-        wkmin = k < wkmin ? k : wkmin;
-      }
-    }
-    // the wavefront's largest logit and key range, for the last block
-    wmax = wave_max_f32(wmax);
-    wkmax = wave_max_u32(wkmax);
-    wkmin = wave_min_u32(wkmin);
-    if (lane == 0) {
-      uint32_t* wr = a.ws_range + (static_cast<int64_t>(row) * a.parts * kWv + part * kWv + wave) * 4;
-      __hip_atomic_store(reinterpret_cast<uint64_t*>(wr),
-                         static_cast<uint64_t>(__float_as_uint(wmax)) | (static_cast<uint64_t>(wkmax) << 32),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(reinterpret_cast<uint64_t*>(wr + 2), static_cast<uint64_t>(wkmin), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  if (!arrive_last(a.counters + row, static_cast<unsigned int>(a.parts), &sh.sel.flag)) return;
-
-  // ---- 3. the last part block: top-p over the row's logits ----
-  uint32_t lkey[KPB];
-  float lmax;
-  uint32_t kmin, kmax;
-  {
-    // the row's logits and every part wavefront's range, one round trip; each
-    // wavefront reduces the ranges itself (no barrier)
-    const int i0 = KPB * tid;
-    float v[KPB];
-#pragma unroll
-    for (int j = 0; j < KPB; j += 2) {
-      const int i = i0 + j < N ? i0 + j : 0;
-      const float2 t = fetch_f32x2(wl + i);
+    for (int j = 0; j < KPB; j += 4) {
+      const float4 t = *reinterpret_cast<const float4*>(src + j);
       v[j] = t.x;
       v[j + 1] = t.y;
+      v[j + 2] = t.z;
+      v[j + 3] = t.w;
     }
-    const int n_rng = a.parts * kWv;  // <= 128
-    const uint32_t* rr = a.ws_range + static_cast<int64_t>(row) * n_rng * 4;
-    uint64_t r0[2], r1[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int e = lane + kWave * h < n_rng ? lane + kWave * h : n_rng - 1;
-      r0[h] = __hip_atomic_load(reinterpret_cast<const uint64_t*>(rr + 4 * e), __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_AGENT);
-      r1[h] = __hip_atomic_load(reinterpret_cast<const uint64_t*>(rr + 4 * e + 2), __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_AGENT);
-    }
-#pragma unroll
-    for (int j = 0; j < KPB; ++j) lkey[j] = score_key(v[j]);
-    if (a.logits != nullptr) {
-      float* lo = a.logits + static_cast<int64_t>(row) * a.b0 * BS;
-#pragma unroll
-      for (int j = 0; j < KPB; ++j)
-        if (i0 + j < N) lo[i0 + j] = v[j];
-    }
-    float mx = -INFINITY;
-    uint32_t kmx = 0u, kmn = 0xffffffffu;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float m = __uint_as_float(static_cast<uint32_t>(r0[h]));
-      const uint32_t kx = static_cast<uint32_t>(r0[h] >> 32), kn = static_cast<uint32_t>(r1[h]);
-      mx = m > mx ? m : mx;
-      kmx = kx > kmx ? kx : kmx;
-      kmn = kn < kmn ? kn : kmn;
-    }
-    lmax = wave_max_f32(mx);
-    kmax = wave_max_u32(kmx);
-    kmin = wave_min_u32(kmn);
   }
+  uint32_t lkey[KPB];
+  float wmx = -INFINITY;
+  uint32_t wkx = 0u, wkn = 0xffffffffu;
+#pragma unroll
+  for (int j = 0; j < KPB; ++j) {
+    lkey[j] = score_key(v[j]);
+    const bool ok = c0 + j < N;
+    wmx = (ok && v[j] > wmx) ? v[j] : wmx;
+    wkx = (ok && lkey[j] > wkx) ? lkey[j] : wkx;
+    wkn = (ok && lkey[j] < wkn) ? lkey[j] : wkn;
+  }
+  if (a.logits != nullptr) {
+    float* lo = a.logits + static_cast<int64_t>(row) * a.b0 * BS;
+#pragma unroll
+    for (int j = 0; j < KPB; ++j)
+      if (c0 + j < N) lo[c0 + j] = v[j];
+  }
+  wmx = wave_max_f32(wmx);
+  wkx = wave_max_u32(wkx);
+  wkn = wave_min_u32(wkn);
+  if (lane == 0) {
+    s_rmax[wave] = wmx;
+    s_rkx[wave] = wkx;
+    s_rkn[wave] = wkn;
+  }
+  if (a.matched) {
+    // the allocation launch reads the candidates' logits and the wavefronts' ranges back
+    float* wl = a.ws_logits + static_cast<int64_t>(row) * a.b0 * BS;
+#pragma unroll
+    for (int j = 0; j < KPB; j += 4) {
+      if (c0 + j < N) *reinterpret_cast<float4*>(wl + c0 + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+    }
+    if (lane == 0)
+      *reinterpret_cast<uint4*>(a.ws_range + (static_cast<int64_t>(row) * kWv + wave) * 4) =
+          make_uint4(__float_as_uint(wmx), wkx, wkn, 0u);
+  }
+  __syncthreads();
+  float lmax = s_rmax[0];
+  uint32_t kmax = s_rkx[0], kmin = s_rkn[0];
+#pragma unroll
+  for (int w = 1; w < kWv; ++w) {
+    lmax = s_rmax[w] > lmax ? s_rmax[w] : lmax;
+    kmax = s_rkx[w] > kmax ? s_rkx[w] : kmax;
+    kmin = s_rkn[w] < kmin ? s_rkn[w] : kmin;
+  }
+
+  // ---- 3. top-p over the row's logits ----
   uint64_t mass[KPB];
   uint64_t local = 0;
-  const int c0 = KPB * tid;
 #pragma unroll
   for (int j = 0; j < KPB; ++j) {
     mass[j] = (c0 + j < N) ? mass_of(key_value(lkey[j]), lmax) : 0ull;
@@ -2109,8 +2279,9 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_head_kernel(HeadArgs a)
 }
 
 // Matched budgets over the fused selection: one block per (group, head)
-// after twilight_head_kernel (matched) has written every head's top-p count
-// and left its logits, B0 pages and wavefront key ranges in the workspace.
+// after twilight_topp_head_kernel (matched) has written every head's top-p
+// count and left its candidates' logits, B0 pages and wavefront key ranges in
+// the workspace.
 // Every block of a group forms the same allocation (matched_counts), takes
 // its head's top-allocated logits (key desc, candidate index asc: the
 // selection twilight_matched_kernel makes) and ORs their rows into the
@@ -2487,21 +2658,64 @@ extern "C" int tw_twilight_select_pages(const float* logits, int G, int R, int N
 namespace tw {
 namespace {
 
-template <typename DT, int KPA, int KPB>
+template <int KPA, int KPB>
 int launch_head_kpb(const HeadArgs& h, hipStream_t stream) {
-  hipLaunchKernelGGL((twilight_head_kernel<DT, KPA, KPB>), dim3(h.G * h.R * h.parts), dim3(kHeadThreads), 0, stream,
-                     h);
+  hipLaunchKernelGGL((twilight_topp_head_kernel<KPA, KPB>), dim3(h.G * h.R), dim3(kHeadThreads), 0, stream, h);
   return tw_host::check_launch();
 }
 
-template <typename DT>
 int launch_head(const HeadArgs& h, hipStream_t stream) {
   const bool wide = h.b0 * 16 > 8 * kHeadThreads;
-  if (h.P <= 4 * kHeadThreads)
-    return wide ? launch_head_kpb<DT, 4, 16>(h, stream) : launch_head_kpb<DT, 4, 8>(h, stream);
-  if (h.P <= 8 * kHeadThreads)
-    return wide ? launch_head_kpb<DT, 8, 16>(h, stream) : launch_head_kpb<DT, 8, 8>(h, stream);
-  return wide ? launch_head_kpb<DT, 16, 16>(h, stream) : launch_head_kpb<DT, 16, 8>(h, stream);
+  if (h.P <= 4 * kHeadThreads) return wide ? launch_head_kpb<4, 16>(h, stream) : launch_head_kpb<4, 8>(h, stream);
+  if (h.P <= 8 * kHeadThreads) return wide ? launch_head_kpb<8, 16>(h, stream) : launch_head_kpb<8, 8>(h, stream);
+  return wide ? launch_head_kpb<16, 16>(h, stream) : launch_head_kpb<16, 8>(h, stream);
+}
+
+template <typename DT>
+int launch_score_qk(const ScoreQkArgs& s, hipStream_t stream) {
+  const dim3 grid(s.G * ((s.P + kSqTile - 1) / kSqTile));
+  if (s.R <= 4)
+    hipLaunchKernelGGL((twilight_score_qk_kernel<DT, 4>), grid, dim3(kSqThreads), 0, stream, s);
+  else
+    hipLaunchKernelGGL((twilight_score_qk_kernel<DT, 8>), grid, dim3(kSqThreads), 0, stream, s);
+  return tw_host::check_launch();
+}
+
+// Workspace of the fused selection, 256-byte aligned pieces: page scores
+// [G * R][P rounded up to 4] | tile key ranges [G * R][ceil(P / 64)] | row
+// logits [G * R][16 P] | (matched) the candidates' logits [G * R][16 b0] and
+// the head launch's wavefront ranges [G * R][8][4].
+struct FusedWorkspace {
+  float* scores;
+  int64_t score_stride;
+  uint2* tile_mm;
+  float* qk_logits;
+  int64_t logit_stride;
+  float* cand_logits;
+  uint32_t* ranges;
+  size_t bytes;
+};
+
+FusedWorkspace fused_layout(void* base, int G, int R, int P, int b0_pages) {
+  auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t rows = static_cast<size_t>(G) * R;
+  FusedWorkspace w{};
+  w.score_stride = (static_cast<int64_t>(P) + 3) & ~static_cast<int64_t>(3);
+  w.logit_stride = static_cast<int64_t>(P) * 16;
+  uint8_t* p = static_cast<uint8_t*>(base);
+  size_t off = 0;
+  w.scores = reinterpret_cast<float*>(p + off);
+  off += al(rows * w.score_stride * sizeof(float));
+  w.tile_mm = reinterpret_cast<uint2*>(p + off);
+  off += al(rows * ((P + kSqTile - 1) / kSqTile) * sizeof(uint2));
+  w.qk_logits = reinterpret_cast<float*>(p + off);
+  off += al(rows * w.logit_stride * sizeof(float));
+  w.cand_logits = reinterpret_cast<float*>(p + off);
+  off += al(rows * static_cast<size_t>(b0_pages) * 16 * sizeof(float));
+  w.ranges = reinterpret_cast<uint32_t*>(p + off);
+  off += al(rows * (kHeadThreads / kWave) * 4 * sizeof(uint32_t));
+  w.bytes = off;
+  return w;
 }
 
 }  // namespace
@@ -2512,13 +2726,8 @@ extern "C" int tw_twilight_union_record_words(int P) {
 }
 
 extern "C" size_t tw_twilight_select_fused_workspace_size(int G, int R, int P, int b0_pages) {
-  // the Quest score's workspace | arrival counters [G*R] (zeroed by the score
-  // launch) | logits [G*R][b0*16] | wavefront ranges [G*R][parts*8][4]
   if (G <= 0 || R <= 0 || P <= 0 || b0_pages <= 0) return 0;
-  const size_t rows = static_cast<size_t>(G) * R;
-  const size_t parts = static_cast<size_t>((b0_pages + tw::kPartPages - 1) / tw::kPartPages);
-  return tw_quest_select_workspace_size(G, R, P) + ((rows * 4 + 255) / 256) * 256 +
-         ((rows * static_cast<size_t>(b0_pages) * 16 * sizeof(float) + 255) / 256) * 256 + rows * parts * 8 * 16;
+  return tw::fused_layout(nullptr, G, R, P, b0_pages).bytes;
 }
 
 namespace tw {
@@ -2557,39 +2766,51 @@ int select_fused(const float* q, const void* page_min, const void* page_max, int
   if (workspace == nullptr || workspace_bytes < tw_twilight_select_fused_workspace_size(G, R, P, b0_pages))
     return TW_ENOMEM;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  const size_t score_ws = tw_quest_select_workspace_size(G, R, P);
-  uint8_t* tail = static_cast<uint8_t*>(workspace) + score_ws;
-  tw::FusedScores fs{};
-  int rc = tw::fused_quest_score(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, lengths, sink, recent,
-                                 block_size, workspace, score_ws, union_rec, rec_stride,
-                                 reinterpret_cast<unsigned int*>(tail), G * R, &fs, st);
+  const FusedWorkspace w = fused_layout(workspace, G, R, P, b0_pages);
+  ScoreQkArgs sq{};
+  sq.q = q;
+  sq.pmin = page_min;
+  sq.pmax = page_max;
+  sq.group_stride = page_group_stride;
+  sq.G = G;
+  sq.R = R;
+  sq.P = P;
+  sq.lengths = lengths;
+  sq.sink = sink;
+  sq.recent = recent;
+  sq.packed = packed;
+  sq.scale = qscale;
+  sq.minimum = qmin;
+  sq.qstride = quant_entry_stride;
+  sq.qrows = quant_rows;
+  sq.qk_scale = qk_scale;
+  sq.scores = w.scores;
+  sq.score_stride = w.score_stride;
+  sq.tile_mm = w.tile_mm;
+  sq.logits = w.qk_logits;
+  sq.logit_stride = w.logit_stride;
+  sq.rec = union_rec;
+  sq.rec_stride = rec_stride;
+  int rc = dtype == TW_DTYPE_F16 ? launch_score_qk<F16>(sq, st) : launch_score_qk<BF16>(sq, st);
   if (rc != TW_OK) return rc;
-  tw::HeadArgs h{};
-  h.scores = fs.scores;
-  h.score_stride = fs.score_stride;
-  h.vec_last4 = fs.vec_last4;
-  h.tile_mm = fs.tile_mm;
+  HeadArgs h{};
+  h.scores = w.scores;
+  h.score_stride = w.score_stride;
+  h.vec_last4 = static_cast<int>(w.score_stride) - 4;
+  h.tile_mm = w.tile_mm;
   h.G = G;
   h.R = R;
   h.P = P;
   h.b0 = b0_pages;
-  h.parts = (b0_pages + tw::kPartPages - 1) / tw::kPartPages;
-  h.counters = reinterpret_cast<unsigned int*>(tail);
-  const size_t cnt_bytes = ((static_cast<size_t>(G) * R * 4 + 255) / 256) * 256;
-  const size_t log_bytes = ((static_cast<size_t>(G) * R * b0_pages * 16 * sizeof(float) + 255) / 256) * 256;
-  h.ws_logits = reinterpret_cast<float*>(tail + cnt_bytes);
-  h.ws_range = reinterpret_cast<uint32_t*>(tail + cnt_bytes + log_bytes);
+  h.parts = 1;
+  h.qk_logits = w.qk_logits;
+  h.logit_stride = w.logit_stride;
+  h.ws_logits = w.cand_logits;
+  h.ws_range = w.ranges;
   h.lengths = lengths;
   h.length = length;
   h.sink = sink;
   h.recent = recent;
-  h.q = q;
-  h.packed = packed;
-  h.scale = qscale;
-  h.minimum = qmin;
-  h.qstride = quant_entry_stride;
-  h.qrows = quant_rows;
-  h.qk_scale = qk_scale;
   h.p24 = static_cast<uint32_t>(__builtin_rintf(top_p * 16777216.0f));
   h.sel_pages = sel_pages;
   h.logits = logits;
@@ -2597,7 +2818,7 @@ int select_fused(const float* q, const void* page_min, const void* page_max, int
   h.rec = union_rec;
   h.rec_stride = rec_stride;
   h.matched = matched ? 1 : 0;
-  rc = dtype == TW_DTYPE_F16 ? tw::launch_head<tw::F16>(h, st) : tw::launch_head<tw::BF16>(h, st);
+  rc = launch_head(h, st);
   if (rc != TW_OK || !matched) return rc;
   tw::MatchedRecArgs m{};
   m.ws_logits = h.ws_logits;
