@@ -338,7 +338,7 @@ class TwilightWorkload:
         self.rec = torch.zeros((layers, G, words), dtype=i32, device=dev)
         torch.cuda.synchronize(dev)
 
-    def select(self, layer: int) -> None:
+    def select(self, layer: int, phase: int = 3) -> None:
         from headinfer import kernels
 
         if self.fused:
@@ -347,7 +347,8 @@ class TwilightWorkload:
                                           self.rec[layer], top_p=self.TOP_P, sink=self.SINK, recent=self.RECENT,
                                           block_size=self.BS, length=self.L, desired=self.desired[layer],
                                           budget_mode=self.mode,
-                                          target_total=self.fixed * self.BS * self.R if self.mode == "matched" else 0)
+                                          target_total=self.fixed * self.BS * self.R if self.mode == "matched" else 0,
+                                          phase=phase)
             return
         kernels.quest_select(self.qf[layer], self.pmin[layer, :, : self.P], self.pmax[layer, :, : self.P], self.b0,
                              sel_pages=self.sel[layer], plan_pages=self.plan_pages[layer],
@@ -440,9 +441,11 @@ class TwilightWorkload:
     def bytes_per_layer(self) -> dict:
         """Algorithmic HBM bytes per layer (mean over layers) by stage, as the
         scope's measurement defines them: page min/max once per group, the
-        scores written and read back, the INT4 rows (codes, scale, minimum)
-        of Sum_g |C_g| candidates (the union of the heads' candidate sets),
-        the attended K/V rows, q and the output."""
+        scores and the candidates' logits written and read back, the INT4
+        rows (codes, scale, minimum) of Sum_g |C_g| candidates (the union of
+        the heads' candidate sets), the attended K/V rows, q and the output.
+        The fused selection reads the INT4 rows of every scored page (more
+        than Sum_g |C_g|); that excess is traffic, not algorithmic bytes."""
         G, R, D, P, N = self.G, self.R, self.D, self.P, self.N
         e = 2
         if self.page_rows or self.fused:                                            # attended union rows
@@ -456,10 +459,13 @@ class TwilightWorkload:
         int4 = cand_rows * (D // 2 + 2 * e)
         score = 2 * P * D * e * G + G * R * P * 4 + G * R * D * 4      # metadata + q in, scores out
         if self.fused:
-            # the head launch: the scores back, the INT4 rows, the union records
-            head = G * R * P * 4 + int4 + G * self.rec.shape[2] * 4
+            # the score + QK launch also reads the candidates' INT4 rows and
+            # writes their logits; the head launch reads the scores and those
+            # logits back and ORs the union records
+            score += int4 + G * R * N * 4
+            head = G * R * P * 4 + G * R * N * 4 + G * self.rec.shape[2] * 4
             if self.mode == "matched":  # the allocation launch reads the logits back
-                head += G * R * N * 4
+                head += G * R * N * 4 * 2
         else:
             head = G * R * P * 4 + G * R * self.b0 * 4 + int4 + G * R * N * 4 * 2
         attention = rows * 2 * D * e + 2 * G * R * D * e + 4 * G * D * e
@@ -1142,21 +1148,25 @@ def twilight_leg(args, dev) -> dict:
                              w.cur_v[0, g], w.out[0, g])
         ok &= e != float("inf")
         err = max(err, e)
+    if getattr(args, "calibration_copy", False):
+        # a 256 MiB device copy of known size, for scaling the counters of a profiled run
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
+        del src
     g_step = graph_of(w.step)
     g_sel = graph_of(lambda: [w.select(i) for i in range(w.layers)])
     g_att = graph_of(lambda: [w.attend(i) for i in range(w.layers)])
     g_att1 = graph_of(lambda: [w.attend(i, phase=1) for i in range(w.layers)]) if w.fused else None
-    # the score kernel alone (the fused selection's first launch), for the
-    # head launch's share of the selection
-    scores = torch.empty((w.G, w.R, w.P), dtype=torch.float32, device=dev)
-    g_score = graph_of(lambda: [kernels.fused_quest_score(w.qf[i], w.pmin[i, :, : w.P], w.pmax[i, :, : w.P],
-                                                          out=scores) for i in range(w.layers)])
+    # the fused selection's first launch alone (score + INT4 QK of every
+    # scored row), for the per-head launch's share of the selection
+    g_score = graph_of(lambda: [w.select(i, phase=1) for i in range(w.layers)]) if w.fused else None
     wall, _ = _timed_steps(g_step, args.steps, args.warmup)
     reps = max(20, args.steps // 2)
     t_sel = time_graph(g_sel, reps) / w.layers
     t_att = time_graph(g_att, reps) / w.layers
     t_att1 = time_graph(g_att1, reps) / w.layers if g_att1 is not None else t_att
-    t_score = time_graph(g_score, reps) / w.layers
+    t_score = time_graph(g_score, reps) / w.layers if g_score is not None else 0.0
     w.step()  # leave a complete step's outputs after the partial replays
     torch.cuda.synchronize()
     by = w.bytes_per_layer()
@@ -1165,25 +1175,30 @@ def twilight_leg(args, dev) -> dict:
     t_head = max(t_sel - t_score, 1e-9)
     kern = {"twilight_select": {"us": round(t_sel * 1e6, 2), "bytes": int(by["select"]),
                                 "GBps": round(by["select"] / t_sel / 1e9, 1)},
-            "quest_score": {"us": round(t_score * 1e6, 2), "bytes": int(by["score"]),
-                            "GBps": round(by["score"] / t_score / 1e9, 1), "kernel": "quest_score_kernel"},
+            "score_qk": {"us": round(t_score * 1e6, 2), "bytes": int(by["score"]),
+                         "GBps": round(by["score"] / max(t_score, 1e-9) / 1e9, 1),
+                         "kernel": "twilight_score_qk_kernel (Quest score + INT4 QK of every scored row)"},
             "twilight_head": {"us": round(t_head * 1e6, 2), "bytes": int(by["head"]),
                               "GBps": round(by["head"] / t_head / 1e9, 1),
-                              "kernel": "twilight_head_kernel" + (" + twilight_matched_rec_kernel"
-                                                                  if w.mode == "matched" else ""),
-                              "us_from": "selection graph - score graph"},
+                              "kernel": "twilight_topp_head_kernel" + (" + twilight_matched_rec_kernel"
+                                                                       if w.mode == "matched" else ""),
+                              "us_from": "selection graph - score + QK graph"},
             "decode_attention": {"us": round(t_att1 * 1e6, 2), "bytes": int(by["attention"]),
                                  "GBps": round(by["attention"] / t_att1 / 1e9, 1),
                                  "kernel": "decode_attn_tiles over the union record (split-K, fused append)"},
             "attention_merge": {"us": round((t_att - t_att1) * 1e6, 2), "kernel": "merge_vec_kernel"}}
     if not w.fused:
-        for name in ("quest_score", "twilight_head", "attention_merge"):
+        for name in ("score_qk", "twilight_head", "attention_merge"):
             kern.pop(name)
-    # the longest single kernel of the layer
+    # the longest single kernel of the layer (with matched budgets the head
+    # entry is two launches, the top-p counts and the allocation)
     dom = "decode_attention"
-    if w.fused and kern["twilight_head"]["us"] > kern["decode_attention"]["us"]:
-        dom = "twilight_head"
-    traffic = measured_traffic(dom, TWILIGHT_PROFILE) if w.fused and w.mode == "dynamic" else None
+    if w.fused:
+        for name in ("score_qk", "twilight_head") if w.mode == "dynamic" else ("score_qk",):
+            if kern[name]["us"] > kern[dom]["us"]:
+                dom = name
+    traffic = (measured_traffic(dom, TWILIGHT_PROFILE if w.mode == "dynamic" else TWILIGHT_MATCHED_PROFILE)
+               if w.fused else None)
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True, "scaling": "weak",
@@ -1793,8 +1808,9 @@ def multireq_check(w) -> tuple[bool, float]:
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "pmc_traffic_quest32k.md"
 TWILIGHT_PROFILE = ROOT / "profiles" / "pmc_twilight32k.md"
+TWILIGHT_MATCHED_PROFILE = ROOT / "profiles" / "kernel_trace_twilight32k_matched.md"
 TRAFFIC_KERNEL = {"decode_attention": "decode_attn_tiles", "quest_select": "quest_score_kernel",
-                  "twilight_head": "twilight_head_kernel"}
+                  "twilight_head": "twilight_topp_head_kernel", "score_qk": "twilight_score_qk_kernel"}
 
 
 def measured_traffic(kernel: str, profile: Path = TRAFFIC_PROFILE):

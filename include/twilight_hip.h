@@ -361,15 +361,17 @@ int tw_twilight_union_record_words(int P);
 size_t tw_twilight_select_fused_workspace_size(int G, int R, int P, int b0_pages);
 
 /* The whole Twilight selection of a layer in two launches, dynamic budgets:
- * the Quest score (page min/max upper bound, as tw_quest_select), then
- * ceil(b0_pages/32) blocks per (group, head), each of which picks the head's
- * B0 pages (the top b0_pages scores, ties to the lowest page) and estimates
- * the INT4 QK of 32 of them (the logits of tw_twilight_qk, bit for bit); the
- * last of them to finish keeps the top-p rows (the desired count and set of
- * tw_twilight_select in dynamic mode) and ORs them into the group's union
- * record (union_rec + g*rec_stride, tw_twilight_union_record_words(P) <=
- * rec_stride, a multiple of 4; 16-byte aligned), which the score launch
- * clears first.  No union plan or row list is built.
+ * a score + INT4 QK launch (one block per KV group and 64-page tile: the
+ * Quest score of the tile's pages for the R heads, bit for bit as
+ * tw_quest_select, and the INT4 QK estimate of every row of those pages for
+ * the R heads, the logits of tw_twilight_qk bit for bit), then one block
+ * per (group, head) that picks the head's B0 pages (the top b0_pages
+ * scores, ties to the lowest page), gathers their rows' logits, keeps the
+ * top-p rows (the desired count and set of tw_twilight_select in dynamic
+ * mode) and ORs them into the group's union record (union_rec +
+ * g*rec_stride, tw_twilight_union_record_words(P) <= rec_stride, a multiple
+ * of 4; 16-byte aligned), which the first launch clears.  No union plan or
+ * row list is built.
  *   q [G][R][128] fp32; page_min/page_max as tw_quest_select (P pages,
  *   16-bit); packed / qscale / qmin the INT4 keys of tw_build_page_metadata
  *   (quant_entry_stride rows apart, quant_rows >= sink + 16*P valid rows,
@@ -382,8 +384,8 @@ size_t tw_twilight_select_fused_workspace_size(int G, int R, int P, int b0_pages
  *   ragged group's pages); logits [G][R][b0_pages*16] (nullable).
  * D = 128, block_size 16, R <= 8, P <= 8192, b0_pages*16 <= 8192.
  * Workspace: tw_twilight_select_fused_workspace_size(G, R, P, b0_pages)
- * bytes, zeroed before its first use (its arrival counters return to zero
- * after every launch).  Replaces
+ * bytes (scores, per-tile key ranges, the rows' logits; no state carries
+ * over between calls).  Replaces
  * prepare_layer_selection's stages 1-2 and the GPU GQA union of the
  * dynamic-budget path (twilight_offload_cache.py:996-1614); the union is
  * the reference's token set, held as page row masks. */
@@ -395,8 +397,23 @@ int tw_twilight_select_fused(const float* q, const void* page_min, const void* p
                              uint32_t* union_rec, int64_t rec_stride, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* tw_twilight_select_fused with its launches chosen, for timing one of them
+ * in isolation: phase 1 runs the score + INT4 QK launch only (its
+ * workspace outputs and the cleared records; desired and the other outputs
+ * are left as they were), phase 3 the whole selection.  No counterpart in
+ * the reference: the measurement's per-kernel split of
+ * prepare_layer_selection (twilight_offload_cache.py:996-1614). */
+int tw_twilight_select_fused_phase(const float* q, const void* page_min, const void* page_max, int dtype, int G,
+                                   int R, int P, int D, int64_t page_group_stride, const uint8_t* packed,
+                                   const void* qscale, const void* qmin, int64_t quant_entry_stride,
+                                   int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
+                                   int recent, int block_size, const int32_t* lengths, int length,
+                                   int32_t* sel_pages, float* logits, int32_t* desired, uint32_t* union_rec,
+                                   int64_t rec_stride, void* workspace, size_t workspace_bytes, int phase,
+                                   void* stream);
+
 /* tw_twilight_select_fused with matched budgets, in three launches: the
- * score, the per-head B0 + INT4 QK + top-p launch (desired counts, no
+ * score + INT4 QK launch, the per-head B0 + top-p launch (desired counts, no
  * record), then one block per (group, head) that forms the group's
  * allocation (matched_budget_counts of the desired counts towards
  * target_total, twilight_offload_cache.py:50-86, the same as

@@ -347,3 +347,38 @@ def test_fused_matched_selection_ragged(K, dev):
         ref_o[gi] = oracle.decode_attention(qf[gi].cpu().numpy(), keys, vals, 1.0 / math.sqrt(D))
     _close(out.float().cpu().numpy(), ref_o, "matched ragged union-record attention")
     _say(f"[fused matched ragged] ok, allocated {all_h.tolist()}")
+
+
+def test_fused_selection_phase_one(K, dev):
+    """phase 1 runs the score + INT4 QK launch alone (for timing it): the
+    union records come back cleared and the counts untouched; the whole
+    selection after it is the oracle's."""
+    G, R, L, b0 = 2, 4, 5000, 48
+    st = _Setup(K, dev, G, R, L + 8, [L] * G, seed=31)
+    P = oracle.selection_window(L, st.sink, st.recent)[2] // st.bs
+    words = K.union_record_words(P)
+    rec = torch.full((G, (words + 3) & ~3), -1, dtype=torch.int32, device=dev)
+    desired = torch.full((G, R), -5, dtype=torch.int32, device=dev)
+    q = (torch.randn((G, R, 128), generator=torch.Generator(device=dev).manual_seed(32), device=dev) * 2).to(
+        torch.bfloat16).float()
+    args = (q, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec)
+    kw = dict(top_p=0.95, sink=st.sink, recent=st.recent, block_size=st.bs, length=L, desired=desired)
+    _say(f"[fused phase] G={G} R={R} L={L} b0={b0}")
+    K.twilight_select_fused(*args, phase=1, **kw)
+    torch.cuda.synchronize()
+    for gi in range(G):   # the bitmap and the row masks (not the padding between them)
+        bits, masks = _decode_record(rec[gi].cpu().numpy(), P)
+        assert not bits.any() and not masks.any(), gi
+    assert bool((desired == -5).all())
+    K.twilight_select_fused(*args, **kw)
+    torch.cuda.synchronize()
+    for gi in range(G):
+        ref = oracle.twilight_layer(q[gi].cpu().numpy(), to_bits(st.pmin[gi, :P]), to_bits(st.pmax[gi, :P]),
+                                    st.packed[gi].cpu().numpy(), to_bits(st.qscale[gi]), to_bits(st.qmin[gi]), "bf16",
+                                    length=L, sink=st.sink, recent=st.recent, block_size=st.bs, b0_pages=b0,
+                                    top_p=0.95)
+        assert np.array_equal(desired[gi].cpu().numpy(), ref["desired"])
+        bits, masks = _decode_record(rec[gi].cpu().numpy(), P)
+        assert np.array_equal(masks, _record_of(np.unique(np.concatenate(ref["selected"])), P, st.sink, st.bs))
+    with pytest.raises(ValueError, match="phase"):
+        K.twilight_select_fused(*args, phase=2, **kw)

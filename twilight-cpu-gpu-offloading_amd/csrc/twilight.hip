@@ -2739,7 +2739,9 @@ int select_fused(const float* q, const void* page_min, const void* page_max, int
                  int64_t quant_entry_stride, int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
                  int recent, int block_size, const int32_t* lengths, int length, int32_t* sel_pages, float* logits,
                  int32_t* desired, uint32_t* union_rec, int64_t rec_stride, void* workspace, size_t workspace_bytes,
-                 bool matched, int target_total, double matched_fraction, int32_t* allocated, void* stream) {
+                 bool matched, int target_total, double matched_fraction, int32_t* allocated, void* stream,
+                 int phase = 3) {
+  if (phase != 1 && phase != 3) return TW_EINVAL;
   if (q == nullptr || page_min == nullptr || page_max == nullptr || packed == nullptr || qscale == nullptr ||
       qmin == nullptr || desired == nullptr || union_rec == nullptr)
     return TW_EINVAL;
@@ -2792,7 +2794,7 @@ int select_fused(const float* q, const void* page_min, const void* page_max, int
   sq.rec = union_rec;
   sq.rec_stride = rec_stride;
   int rc = dtype == TW_DTYPE_F16 ? launch_score_qk<F16>(sq, st) : launch_score_qk<BF16>(sq, st);
-  if (rc != TW_OK) return rc;
+  if (rc != TW_OK || phase == 1) return rc;
   HeadArgs h{};
   h.scores = w.scores;
   h.score_stride = w.score_stride;
@@ -2860,6 +2862,20 @@ extern "C" int tw_twilight_select_fused(const float* q, const void* page_min, co
                           quant_entry_stride, quant_rows, b0_pages, top_p, qk_scale, sink, recent, block_size,
                           lengths, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
                           workspace_bytes, false, 0, 0.0, nullptr, stream);
+}
+
+extern "C" int tw_twilight_select_fused_phase(const float* q, const void* page_min, const void* page_max, int dtype,
+                                              int G, int R, int P, int D, int64_t page_group_stride,
+                                              const uint8_t* packed, const void* qscale, const void* qmin,
+                                              int64_t quant_entry_stride, int64_t quant_rows, int b0_pages,
+                                              float top_p, float qk_scale, int sink, int recent, int block_size,
+                                              const int32_t* lengths, int length, int32_t* sel_pages, float* logits,
+                                              int32_t* desired, uint32_t* union_rec, int64_t rec_stride,
+                                              void* workspace, size_t workspace_bytes, int phase, void* stream) {
+  return tw::select_fused(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, packed, qscale, qmin,
+                          quant_entry_stride, quant_rows, b0_pages, top_p, qk_scale, sink, recent, block_size,
+                          lengths, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
+                          workspace_bytes, false, 0, 0.0, nullptr, stream, phase);
 }
 
 extern "C" int tw_twilight_select_fused_matched(const float* q, const void* page_min, const void* page_max,

@@ -92,6 +92,8 @@ _HIP_SIGNATURES = {
     "tw_twilight_select_fused_workspace_size": (szt, [i32, i32, i32, i32]),
     "tw_twilight_select_fused": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64, i32, f32, f32,
                                        i32, i32, i32, vp, i32, vp, vp, vp, vp, i64, vp, szt, vp]),
+    "tw_twilight_select_fused_phase": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64, i32, f32,
+                                             f32, i32, i32, i32, vp, i32, vp, vp, vp, vp, i64, vp, szt, i32, vp]),
     "tw_twilight_select_fused_matched": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64, i32,
                                                f32, f32, i32, i32, i32, vp, i32, i32, f64, vp, vp, vp, vp, vp, i64,
                                                vp, szt, vp]),

@@ -851,12 +851,13 @@ def twilight_select_fused(
     target_total: int = 0,
     allocated: Optional[torch.Tensor] = None,
     matched_fraction: float = 0.0,
+    phase: int = 3,
 ) -> torch.Tensor:
     """The Twilight selection of a layer in two launches with dynamic budgets
-    (Quest score; one block per head: B0 top-k, INT4 QK, top-p, publish), or
-    three with matched budgets (the head launch stops at the top-p counts;
-    one block per head then forms the group's allocation towards
-    target_total and keeps the head's top-allocated logits), written to each
+    (Quest score + INT4 QK of every scored row; one block per head: B0 top-k,
+    top-p, publish), or three with matched budgets (the head launch stops at
+    the top-p counts; one block per head then forms the group's allocation
+    towards target_total and keeps the head's top-allocated logits), written to each
     group's union record: union_rec [G, >= union_record_words(P)] int32 (row
     stride a multiple of 4, 16-byte aligned).  q [G, R, 128] fp32;
     page_min/page_max [G, >= P, 128] over the P scored pages (16-bit);
@@ -866,7 +867,10 @@ def twilight_select_fused(
     length, or with lengths each group's own target from matched_fraction
     (the cache's fixed pages x 16 x R).  Returns desired [G, R] int32 (the
     top-p counts); sel_pages [G, R, b0_pages], logits [G, R, b0_pages * 16]
-    and (matched) allocated [G, R] are optional outputs."""
+    and (matched) allocated [G, R] are optional outputs.  phase 1 runs the
+    first launch alone (for timing it; the outputs are left as they were)."""
+    if phase not in (1, 3):
+        raise ValueError("phase must be 1 (score + INT4 QK launch) or 3 (the selection)")
     if budget_mode not in ("dynamic", "matched"):
         raise ValueError("budget_mode must be 'dynamic' or 'matched'")
     matched = budget_mode == "matched"
@@ -918,7 +922,13 @@ def twilight_select_fused(
     nbytes = hip().tw_twilight_select_fused_workspace_size(G, R, P, int(b0_pages))
     ws = WORKSPACE.get(dev, "twilight_fused", nbytes)
     with on_device(dev):
-        if matched:
+        if phase == 1:
+            check(hip().tw_twilight_select_fused_phase(
+                ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D, page_min.stride(0), ptr(packed),
+                ptr(scale), ptr(minimum), qe, packed.shape[1], int(b0_pages), float(top_p), qs, sink, recent,
+                block_size, ptr(lengths), int(length), ptr(sel_pages), ptr(logits), ptr(desired), ptr(union_rec),
+                union_rec.stride(0), ptr(ws), ws.numel(), 1, stream_handle(dev)), "twilight_select_fused_phase")
+        elif matched:
             check(hip().tw_twilight_select_fused_matched(
                 ptr(q), ptr(page_min), ptr(page_max), _dt(page_min), G, R, P, D, page_min.stride(0), ptr(packed),
                 ptr(scale), ptr(minimum), qe, packed.shape[1], int(b0_pages), float(top_p), qs, sink, recent,
