@@ -33,11 +33,11 @@ def _say(*args):
     sys.stdout.flush()
 
 
-def _models(dev, seed=0):
+def _models(dev, seed=0, q_heads=8):
     from transformers import LlamaConfig, LlamaForCausalLM
 
     def cfg():
-        return LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=8,
+        return LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=q_heads,
                            num_key_value_heads=2, head_dim=128, vocab_size=1000, max_position_embeddings=4096,
                            rope_theta=500000.0)
 
@@ -321,19 +321,22 @@ def test_graph_decoder_fused_equals_unfused(dev):
     assert torch.equal(caches[0]._value_cache[:, :n], caches[1]._value_cache[:, :n])
 
 
-@pytest.mark.parametrize("fuse,mode", [(True, "dynamic"), (False, "dynamic"), (True, "matched")])
-def test_graph_decoder_twilight_matches_eager(dev, fuse, mode):
+@pytest.mark.parametrize("fuse,mode,q_heads", [(True, "dynamic", 8), (False, "dynamic", 8), (True, "matched", 8),
+                                               (True, "dynamic", 32)])
+def test_graph_decoder_twilight_matches_eager(dev, fuse, mode, q_heads):
     """GraphDecoder over a Twilight cache (Quest B0, INT4 QK, top-p and the
     GQA union from device-side lengths, the union attention with the append,
     the INT4 + page metadata update) == the eager patched model with the same
-    cache policy, token by token; the steps cross a page completion."""
+    cache policy, token by token; the steps cross a page completion.  32
+    query heads over 2 KV heads (16 per group) run the fused selection and
+    the union attention as sub-groups of 8."""
     from headinfer import mp
     from headinfer.graph_decode import GraphDecoder
     from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache
 
-    _say(f"[graph decoder twilight] fuse={fuse} {mode}")
+    _say(f"[graph decoder twilight] fuse={fuse} {mode} q_heads={q_heads}")
     steps = 10
-    _, gpu = _models(dev)
+    _, gpu = _models(dev, q_heads=q_heads)
     mp.mp_headinfer(gpu)
     kw = dict(max_cache_len=T_PROMPT + steps + 2, sink_tokens=64, recent_tokens=256, block_size=16,
               kv_residency="hbm", candidate_token_budget=128, top_p=0.9, budget_mode=mode,

@@ -382,3 +382,56 @@ def test_fused_selection_phase_one(K, dev):
         assert np.array_equal(masks, _record_of(np.unique(np.concatenate(ref["selected"])), P, st.sink, st.bs))
     with pytest.raises(ValueError, match="phase"):
         K.twilight_select_fused(*args, phase=2, **kw)
+
+
+@pytest.mark.parametrize("R", [12, 16])
+def test_fused_selection_wide_group(K, dev, R):
+    """More than 8 query heads per KV head through the fused selection and the
+    union attention: sub-groups of at most 8 heads, their records ORed into
+    the group's.  B0 pages, logits, top-p counts and the record against
+    oracle.twilight_layer over all R heads; matched budgets are refused (they
+    allocate over every head at once)."""
+    G, L, b0 = 2, 6000, 64
+    st = _Setup(K, dev, G, R, L + 8, [L] * G, seed=40 + R)
+    D, bs, sink, recent = st.D, st.bs, st.sink, st.recent
+    P = oracle.selection_window(L, sink, recent)[2] // bs
+    words = K.union_record_words(P)
+    rec = torch.full((G, (words + 3) & ~3), -1, dtype=torch.int32, device=dev)
+    sel = torch.zeros((G, R, b0), dtype=torch.int32, device=dev)
+    logits = torch.zeros((G, R, b0 * bs), dtype=torch.float32, device=dev)
+    desired = torch.zeros((G, R), dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(R)
+    q = (torch.randn((G, R, D), generator=gen, device=dev) * 2).to(torch.bfloat16)
+    cur_k = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+    cur_v = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+    qf = q.float()
+    _say(f"[fused wide] G={G} R={R} L={L} b0={b0}")
+    K.twilight_select_fused(qf, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec, top_p=0.9,
+                            sink=sink, recent=recent, block_size=bs, length=L, desired=desired, sel_pages=sel,
+                            logits=logits)
+    k, v = st.k.clone(), st.v.clone()
+    out = K.decode_attention_union(q, k, v, rec, P, max_pages=min(P, R * b0), sink=sink, recent=recent,
+                                   block_size=bs, length=L, append=True, cur_k=cur_k, cur_v=cur_v)
+    torch.cuda.synchronize()
+    rec_h, sel_h, log_h, des_h = rec.cpu().numpy(), sel.cpu().numpy(), logits.cpu().numpy(), desired.cpu().numpy()
+    ref_o = np.zeros((G, R, D))
+    for gi in range(G):
+        ref = oracle.twilight_layer(qf[gi].cpu().numpy(), to_bits(st.pmin[gi, :P]), to_bits(st.pmax[gi, :P]),
+                                    st.packed[gi].cpu().numpy(), to_bits(st.qscale[gi]), to_bits(st.qmin[gi]), "bf16",
+                                    length=L, sink=sink, recent=recent, block_size=bs, b0_pages=b0, top_p=0.9)
+        assert np.array_equal(sel_h[gi], ref["pages"]), gi
+        assert np.array_equal(log_h[gi].view(np.uint32), ref["logits"].astype(np.float32).view(np.uint32)), gi
+        assert np.array_equal(des_h[gi], ref["desired"]), (gi, des_h[gi], ref["desired"])
+        bits, masks = _decode_record(rec_h[gi], P)
+        want = _record_of(np.unique(np.concatenate(ref["selected"])), P, sink, bs)
+        assert np.array_equal(masks, want) and np.array_equal(bits[:P], want != 0) and not bits[P:].any(), gi
+        kept = ref["union"].astype(np.int64)
+        keys = torch.cat([st.k[gi, kept].float(), cur_k[gi:gi + 1].float()]).cpu().numpy()
+        vals = torch.cat([st.v[gi, kept].float(), cur_v[gi:gi + 1].float()]).cpu().numpy()
+        ref_o[gi] = oracle.decode_attention(qf[gi].cpu().numpy(), keys, vals, 1.0 / math.sqrt(D))
+    _close(out.float().cpu().numpy(), ref_o, f"wide union-record attention R={R}")
+    assert torch.equal(k[:, L].view(torch.int16), cur_k.view(torch.int16))
+    with pytest.raises(ValueError, match="at most 8 query heads"):
+        K.twilight_select_fused(qf, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec,
+                                top_p=0.9, sink=sink, recent=recent, block_size=bs, length=L, sel_pages=sel,
+                                budget_mode="matched", target_total=12 * bs * R)

@@ -114,10 +114,14 @@ def test_twilight_gqa_group_union_wide_group(H, dev, R, mode):
     _close(out, ref_out)
 
 
-def test_twilight_decode_layer_wide_group(H, dev):
+@pytest.mark.parametrize("mode", ["matched", "dynamic"])
+def test_twilight_decode_layer_wide_group(H, dev, mode):
+    """decode_layer with 16 query heads per KV head: matched budgets take the
+    general path (budgets over all 16 heads on the host), dynamic budgets the
+    fused selection in two sub-groups of 8 whose records are ORed."""
     G, R, D, T = 2, 16, 128, 1500
-    _say("[wide twilight decode_layer]")
-    cache = _twilight_cache(H, dev, E=G, T=T, D=D, R=R, dtype="f16", residency="hbm", mode="matched",
+    _say(f"[wide twilight decode_layer] {mode}")
+    cache = _twilight_cache(H, dev, E=G, T=T, D=D, R=R, dtype="f16", residency="hbm", mode=mode,
                             candidate_token_budget=256, top_p=0.9, matched_budget_fraction=0.05,
                             layer_batched_selection=True)
     model = _Model(G, T, D, "f16", seed=107, scale=2.0)

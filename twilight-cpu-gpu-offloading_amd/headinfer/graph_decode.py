@@ -91,8 +91,12 @@ class GraphDecoder:
         self.layers = list(inner.layers)
         if cache.block_size != 16 or self.D != 128 or cache.dtype not in (torch.float16, torch.bfloat16):
             raise ValueError("GraphDecoder needs 16-row pages, head_dim 128 and a 16-bit cache")
-        if self.R > 8:
-            raise ValueError("at most 8 query heads per KV head")
+        if self.R > 8 and not (self.twilight and cache.budget_mode == "dynamic"):
+            # the Twilight fused selection and union attention run wider groups
+            # as sub-groups of 8 under dynamic budgets; the Quest page-tile and
+            # matched-budget launches take at most 8 heads a group
+            raise ValueError("GraphDecoder takes at most 8 query heads per KV head, except over a Twilight cache "
+                             "with dynamic budgets")
         if cache.geometry.num_entries != len(self.layers) * self.G:
             raise ValueError("cache entries do not match the model's layers x KV heads")
         lengths = set(cache._logical_lengths)
@@ -194,13 +198,16 @@ class GraphDecoder:
                               and cache.dtype in (torch.float16, torch.bfloat16))
             self.tw_slot_u = torch.zeros((self.G, self.R, self.k), dtype=torch.int32, device=dev)
             self.tw_prows = torch.zeros((self.G, self.width), dtype=torch.int32, device=dev)
-            # the fused selection (score; B0 + INT4 QK + top-p per head) into a
-            # union record per KV group, read by the union attention
-            self.fused = self.page_rows and self.P <= 8192 and n_cand <= 8192
+            # the fused selection (score + INT4 QK; B0 + top-p per head) into a
+            # union record per KV group, read by the union attention; more
+            # than 8 query heads per KV head as sub-groups (dynamic budgets)
+            self.fused = (cache.block_size == 16 and self.D == 128 and cache.dtype in (torch.float16, torch.bfloat16)
+                          and (self.R <= 8 or cache.budget_mode == "dynamic") and self.P <= 8192
+                          and n_cand <= 8192)
             if cache.budget_mode == "matched":
                 if not self.fused:
                     raise ValueError("GraphDecoder runs matched Twilight budgets through the fused selection "
-                                     "(16-row pages, head_dim 128, R <= 8, <= 8192 candidate pages)")
+                                     "(16-row pages, head_dim 128, 16-bit K/V, R <= 8, <= 8192 candidate pages)")
                 # the matched target grows with the length while B0 stops at k
                 # pages: past that the reference's allocation raises, so refuse
                 # a decode that would reach it

@@ -891,6 +891,42 @@ def twilight_select_fused(
                           logits, allocated, what="twilight_select_fused")
     if desired is None:
         desired = torch.empty((G, R), dtype=torch.int32, device=dev)
+    if R > 8:
+        # Sub-groups of at most 8 query heads: a dynamic budget is each head's
+        # own, so the group's kept rows are the union of the sub-groups' --
+        # the first writes the record, the others their own records ORed into
+        # it.  Matched budgets allocate over every head of the group at once.
+        if matched:
+            raise ValueError("matched budgets over the fused selection take at most 8 query heads per KV head")
+        if phase != 3:
+            raise ValueError("phase 1 takes at most 8 query heads per KV head")
+        for t, dt, shape in ((desired, torch.int32, (G, R)), (sel_pages, torch.int32, (G, R, b0_pages)),
+                             (logits, torch.float32, (G, R, b0_pages * block_size))):
+            if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
+                raise ValueError("twilight_select_fused output has the wrong dtype/shape")
+        other = None
+        for i, (r0, r1) in enumerate(head_chunks(R)):
+            Rc = r1 - r0
+            rec = union_rec
+            if i > 0:
+                if other is None:
+                    other = torch.empty((G, union_rec.stride(0)), dtype=torch.int32, device=dev)
+                rec = other[:, :union_rec.shape[1]]
+            d = torch.empty((G, Rc), dtype=torch.int32, device=dev)
+            sp = None if sel_pages is None else torch.empty((G, Rc, b0_pages), dtype=torch.int32, device=dev)
+            lg = None if logits is None else torch.empty((G, Rc, b0_pages * block_size), dtype=torch.float32,
+                                                          device=dev)
+            twilight_select_fused(q[:, r0:r1].contiguous(), page_min, page_max, packed, scale, minimum, b0_pages,
+                                  rec, top_p=top_p, sink=sink, recent=recent, block_size=block_size, length=length,
+                                  lengths=lengths, qk_scale=qk_scale, desired=d, sel_pages=sp, logits=lg)
+            if i > 0:
+                union_rec.bitwise_or_(rec)
+            desired[:, r0:r1] = d
+            if sp is not None:
+                sel_pages[:, r0:r1] = sp
+            if lg is not None:
+                logits[:, r0:r1] = lg
+        return desired
     if matched:
         if lengths is not None:
             if not 0.0 < matched_fraction <= 1.0:
@@ -1427,7 +1463,9 @@ def decode_attention_union(
     twilight_select_fused over P pages: every head attends the kept rows of
     the union pages, the sink and recent windows and the decode token.
     max_pages bounds a group's union pages (min(P, R * b0_pages)); the other
-    arguments as decode_attention_page_rows.  Returns [G, R, D]."""
+    arguments as decode_attention_page_rows.  More than 8 query heads per
+    group run as sub-groups of at most 8 over the same record.  Returns
+    [G, R, D]."""
     if phase not in (1, 2, 3):
         raise ValueError("phase must be 1, 2 or 3")
     if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
@@ -1468,6 +1506,19 @@ def decode_attention_union(
     _require_contiguous(q, cur_k, cur_v, what="decode_attention_union")
     if out is None:
         out = torch.empty_like(q)
+    if R > 8:
+        # sub-groups of at most 8 heads over the same record (every head
+        # attends every kept row); each launch writes the same decode row and
+        # completes the same metadata
+        if phase != 3:
+            raise ValueError("phases 1 and 2 take at most 8 query heads per KV head")
+        for r0, r1 in head_chunks(R):
+            out[:, r0:r1] = decode_attention_union(
+                q[:, r0:r1].contiguous(), k_cache, v_cache, union_rec, P, max_pages=max_pages, sink=sink,
+                recent=recent, block_size=block_size, lengths=lengths, length=length, append=append, cur_k=cur_k,
+                cur_v=cur_v, softmax_scale=softmax_scale, page_min=page_min, page_max=page_max, packed=packed,
+                scale=scale, minimum=minimum)
+        return out
     sc = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
     max_rows = sink + max(0, max_pages) * block_size + recent
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)

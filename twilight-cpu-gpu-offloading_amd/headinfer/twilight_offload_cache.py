@@ -8,16 +8,25 @@ defaults (candidate_token_budget 8192, top_p 0.95, matched_budget_fraction
 0.05, budget_mode "matched"), prepare_layer_selection,
 update_layer_gqa_group_ragged, the traces and state_snapshot.
 
-The whole selection of a decoder layer is four launches on the device --
-tw_quest_select (B0 pages + union plan), tw_twilight_qk (INT4 estimate of
-every head's candidates, each INT4 row read once for the group),
-tw_twilight_select (exact top-p counts, budgets, per-head selection, the
-group's token union) -- and the union gather reads the selected rows from
-the slab (HBM or zero-copy host) into the varlen attention layout.  The
-reference's many execution variants (qk_backend, CPU union / gather
-flavours, graphs, pipelines, resident caches) choose between
-implementations of the same selection; they are accepted and validated like
-the reference does, recorded in state_snapshot, and all run this one path.
+decode_layer selects a decoder layer in two launches on the device with
+dynamic budgets -- tw_twilight_select_fused: the Quest score and the INT4
+estimate of every scored row for the group's heads, then one block per head
+for the B0 pages, the exact top-p and the group's union record -- and three
+with matched budgets (the allocation and each head's top-allocated rows in
+one more launch); the attention then reads the record's rows from the slab
+(HBM or zero-copy host) with the decode token's append fused.  Under a
+selection or budget trace (which records the row list), for shapes outside
+the fused kernels, or with matched budgets over more than 8 query heads per
+KV head, the general path runs instead: tw_quest_select (B0 pages + union
+plan), tw_twilight_qk, tw_twilight_select (counts, budgets, per-head
+selection, the token union as a row list), then the row attention; both
+attend the same rows.  The update APIs (update_layer_gqa_group_ragged and the
+per-entry update) take the general path and gather the selected rows into
+the varlen attention layout.  The reference's many execution variants
+(qk_backend, CPU union / gather flavours, graphs, pipelines, resident caches)
+choose between implementations of the same selection; they are accepted and
+validated like the reference does, recorded in state_snapshot, and run these
+paths.
 """
 
 from __future__ import annotations
@@ -693,15 +702,19 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
     def _decode_layer_fused(self, queries: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
                             entries: Sequence[int], old_length: int, softmax_scale: Optional[float],
                             out: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
-        """decode_layer through the fused selection: the Quest score, then per
-        (group, head) the B0 top-k, INT4 QK and top-p into the group's union
-        record (matched budgets: the top-p counts, then the group's
-        allocation and each head's top-allocated rows in one more launch),
-        and the attention over the record's kept rows (the same token set as
-        the union row list).  None when the layer takes the general path:
-        other shapes, or traces that record the row list."""
+        """decode_layer through the fused selection: the Quest score and the
+        INT4 QK of every scored row, then per (group, head) the B0 top-k and
+        top-p into the group's union record (matched budgets: the top-p
+        counts, then the group's allocation and each head's top-allocated
+        rows in one more launch), and the attention over the record's kept
+        rows (the same token set as the union row list).  More than 8 query
+        heads per KV head run as sub-groups with dynamic budgets.  None when
+        the layer takes the general path: other shapes, matched budgets over
+        more than 8 heads, or traces that record the row list."""
         G, R, D = queries.shape
-        if (not self.fused_decode or R > 8 or D != 128 or self.block_size != 16
+        # more than 8 query heads per KV head run as sub-groups, which dynamic
+        # budgets (each head's own) allow; matched budgets allocate over all R
+        if (not self.fused_decode or (R > 8 and self.budget_mode == "matched") or D != 128 or self.block_size != 16
                 or self.dtype not in (torch.float16, torch.bfloat16) or self._capture_selection_trace
                 or self._capture_budget_trace or self._page_min is None or self._packed is None):
             return None
