@@ -11,9 +11,12 @@
  *     and never synchronizes it, unless the comment says otherwise;
  *   - takes caller-allocated outputs.  Entry points that need scratch take a
  *     `workspace` pointer whose size is given by the matching *_workspace_size
- *     query; its arrival counters must be zero before the first call (the
- *     library leaves them zero after every call, so a workspace is reusable,
- *     but two calls sharing one workspace must not overlap in time).
+ *     query; its arrival counters (a fixed 64 KiB region at its start, one
+ *     counter per KV group, at most 16384 groups) must be zero before the
+ *     first call -- a zeroed buffer -- and the library leaves them zero after
+ *     every call and never puts other data there, so a workspace is reusable
+ *     by any later call whatever its sizes, but two calls sharing one
+ *     workspace must not overlap in time.
  *
  * dtype codes: TW_DTYPE_F16, TW_DTYPE_BF16, TW_DTYPE_F32 (key/value/metadata
  * storage); queries for scoring are always fp32, as in the reference.

@@ -1,8 +1,9 @@
 """tw_quest_select_static (the entry point that allocates nothing) against
 tw_quest_select on the same inputs: scores, page ids, union plan and row plan
-bit for bit, on two calls in a row (the second smaller, so it runs on the
-first call's leftover scratch), then replayed from a captured graph with
-eager work between the replays."""
+bit for bit, on calls in a row (the second smaller, so it runs on the first
+call's leftover scratch; the third with more groups, so more arrival counters
+than the first call zeroed), then replayed from a captured graph with eager
+work between the replays."""
 
 from __future__ import annotations
 
@@ -77,9 +78,11 @@ def _same(a: dict, b: dict) -> bool:
     return ok
 
 
-CASES = [  # (G, R, D, dtype, length, k): the 32K layer, then a smaller one on the leftover scratch
+CASES = [  # (G, R, D, dtype, length, k): the 32K layer, then a smaller one on the leftover scratch,
+    # then one with more groups than the first call's zeroed arrival counters cover
     (8, 4, 128, "f16", 32768, 128),
     (3, 2, 64, "bf16", 3000, 20),
+    (96, 2, 64, "f16", 3000, 20),
 ]
 
 

@@ -1036,7 +1036,7 @@ int64_t padded(int P) { return (static_cast<int64_t>(P) + 3) & ~static_cast<int6
 size_t tile_range_bytes(int G, int R, int P) {
   return align256(static_cast<size_t>(G) * R * ((P + kTilePages - 1) / kTilePages) * sizeof(uint2));
 }
-size_t counter_bytes(int G) { return ((static_cast<size_t>(G) * 4 + 255) / 256) * 256; }
+size_t counter_bytes(int) { return kCounterRegionBytes; }
 
 }  // namespace
 }  // namespace tw
@@ -1088,7 +1088,7 @@ extern "C" int tw_topk_sorted(const float* scores, int rows, int P, int64_t scor
 }
 
 extern "C" size_t tw_quest_select_workspace_size(int G, int R, int P) {
-  // arrival counters | scores [G][R][P rounded up to 4] | selections [G][R][<= P]
+  // arrival counters (the fixed 64 KiB region) | scores [G][R][P rounded up to 4] | selections [G][R][<= P]
   // | per-tile key ranges [G][R][ceil(P / 64)] | (P > 8192) the segment
   // pass's compacted rows
   if (G <= 0 || R <= 0 || P <= 0) return 0;
@@ -1157,6 +1157,7 @@ extern "C" int tw_quest_select(const float* q, const void* page_min, const void*
       if (rows_stride < max_count) return TW_EINVAL;
     }
   }
+  if (G > tw::kMaxCounterGroups) return TW_EUNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < tw_quest_select_workspace_size(G, R, P)) return TW_ENOMEM;
   const tw::SelectWorkspace w = tw::carve(workspace, G, R, P);
   unsigned int* counters = w.counters;
@@ -1218,6 +1219,7 @@ extern "C" int tw_quest_select_ragged(const float* q, const void* page_min, cons
   if (plan_pages != nullptr &&
       plan_stride < (static_cast<int64_t>(R) * k < P_max ? static_cast<int64_t>(R) * k : P_max))
     return TW_EINVAL;
+  if (G > tw::kMaxCounterGroups) return TW_EUNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < tw_quest_select_workspace_size(G, R, P_max)) return TW_ENOMEM;
   const tw::SelectWorkspace w = tw::carve(workspace, G, R, P_max);
   unsigned int* counters = w.counters;
@@ -1352,12 +1354,12 @@ namespace {
 
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxStaticDevices] = {};
-bool g_scratch_zeroed[kMaxStaticDevices] = {};
+size_t g_scratch_zeroed[kMaxStaticDevices] = {};  // bytes from the start known to be zero
 
-// Zero every byte of the array on its first use on a device: the arrival
-// counters must start at zero (the selection kernels leave them zero after
-// every call).  A kernel, not a memset node, so a captured graph replays it
-// correctly.
+// Zero the arrival counters at the start of the array (the only part of the
+// workspace that must start at zero; the selection kernels leave them zero
+// after every call).  A kernel, not a memset node, so a captured graph
+// replays it correctly.
 __global__ __launch_bounds__(256) void zero_scratch_kernel(uint4* p, size_t n16) {
   for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n16;
        i += static_cast<size_t>(gridDim.x) * blockDim.x)
@@ -1365,10 +1367,12 @@ __global__ __launch_bounds__(256) void zero_scratch_kernel(uint4* p, size_t n16)
 }
 
 // The device address of `scratch` on the current device, set up on the first
-// call there.  Until a zero fill has been enqueued outside graph capture, every
-// call enqueues one on `stream` ahead of its kernels (a fill captured into a
-// graph runs only when the graph replays).
-int static_scratch(hipStream_t stream, void** out) {
+// call there, with its first `zero_bytes` (the call's arrival counters, a
+// multiple of 256) known to be zero: a call that needs more of them zeroed
+// than a fill outside graph capture has covered enqueues one on `stream`
+// ahead of its kernels (a fill captured into a graph runs at every replay,
+// so only the counters' few bytes are filled).
+int static_scratch(hipStream_t stream, size_t zero_bytes, void** out) {
   int dev = -1;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess) return tw_host::record_hip_error(err);
@@ -1381,15 +1385,17 @@ int static_scratch(hipStream_t stream, void** out) {
     if (p == nullptr) return TW_EHIP;
     g_scratch_ptr[dev] = p;
   }
-  if (!g_scratch_zeroed[dev]) {
+  if (zero_bytes > g_scratch_zeroed[dev]) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     err = hipStreamIsCapturing(stream, &cs);
     if (err != hipSuccess) return tw_host::record_hip_error(err);
-    hipLaunchKernelGGL(zero_scratch_kernel, dim3(1024), dim3(256), 0, stream,
-                       static_cast<uint4*>(g_scratch_ptr[dev]), kStaticScratchBytes / 16);
+    const size_t n16 = zero_bytes / 16;
+    const int blocks = static_cast<int>((n16 + 255) / 256 < 1024 ? (n16 + 255) / 256 : 1024);
+    hipLaunchKernelGGL(zero_scratch_kernel, dim3(blocks), dim3(256), 0, stream,
+                       static_cast<uint4*>(g_scratch_ptr[dev]), n16);
     const int rc = tw_host::check_launch();
     if (rc != TW_OK) return rc;
-    g_scratch_zeroed[dev] = cs == hipStreamCaptureStatusNone;
+    if (cs == hipStreamCaptureStatusNone) g_scratch_zeroed[dev] = zero_bytes;
   }
   *out = g_scratch_ptr[dev];
   return TW_OK;
@@ -1409,7 +1415,7 @@ extern "C" int tw_quest_select_static(const float* q, const void* page_min, cons
   if (need == 0) return TW_EINVAL;
   if (need > kStaticScratchBytes) return TW_ENOMEM;  // beyond the static array: use tw_quest_select
   void* ws = nullptr;
-  const int rc = static_scratch(static_cast<hipStream_t>(stream), &ws);
+  const int rc = static_scratch(static_cast<hipStream_t>(stream), tw::counter_bytes(G), &ws);
   if (rc != TW_OK) return rc;
   return tw_quest_select(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, k, scores, sel_pages,
                          plan_pages, plan_masks, plan_counts, plan_stride, rows, row_masks, row_counts, rows_stride,

@@ -16,6 +16,14 @@ namespace tw {
 
 constexpr int kWave = 64;
 
+// Arrival counters (one 32-bit counter per KV group) sit in a fixed region at
+// the start of every selection workspace, [0, kCounterRegionBytes); the
+// workspace's data starts after it.  The kernels return every counter they
+// use to zero, so with the buffer zeroed once, no later call -- whatever its
+// group count or sizes -- finds data of an earlier call on its counters.
+constexpr int kMaxCounterGroups = 16384;
+constexpr size_t kCounterRegionBytes = static_cast<size_t>(kMaxCounterGroups) * 4;  // 64 KiB
+
 // ---------------------------------------------------------------- dtypes
 // Storage types: 16-bit formats are carried as raw uint16_t bit patterns so the
 // conversions below (and therefore every rounding step) are explicit.

@@ -2495,7 +2495,7 @@ int launch_select(const SelectArgs& s, hipStream_t stream) {
   return launch_select_kpt<32>(s, stream);  // N <= kMaxCandidates, checked by the caller
 }
 
-size_t counter_bytes(int G) { return ((static_cast<size_t>(G) * 4 + 255) / 256) * 256; }
+size_t counter_bytes(int) { return kCounterRegionBytes; }
 
 }  // namespace
 }  // namespace tw
@@ -2584,6 +2584,7 @@ int select_launch(const float* logits, int G, int R, int N, const int32_t* sel_p
         page_rows_stride < 1)
       return TW_EINVAL;
   }
+  if (G > tw::kMaxCounterGroups) return TW_EUNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < tw_twilight_select_workspace_size(G, R, N)) return TW_ENOMEM;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const int words = (N + 31) / 32;
