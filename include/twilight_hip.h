@@ -600,7 +600,19 @@ int tw_decode_attention_page_rows(const void* q, const void* k_base, const void*
  * row, which is appended there from cur_k/cur_v when append != 0 -- the
  * semantics of tw_decode_attention_pages_ragged, as is the fused page
  * metadata update (page_min/page_max).  Union indexes at or above res_slots
- * are read from the slab and not stored. */
+ * are read from the slab and not stored.
+ *   Resident windows (res_win_k nullable): res_win_k/res_win_v [G][sink +
+ * ring_rows][D] (16-byte aligned; ring_rows a power of two >= recent) keep
+ * each group's sink rows at [0, sink) and its latest ring_rows rows at sink
+ * + (row & (ring_rows - 1)), and res_win_state [G][2] int32 (zeroed before
+ * the first call, and again whenever the slab's rows change other than by
+ * these launches' appends) records the history length the ring serves and
+ * whether the sink rows are stored.  When the previous launch ran at
+ * length - 1 with a decode row, both windows are read from HBM; otherwise
+ * they are read from the slab and stored, so the next step reads them from
+ * HBM.  The decode row goes into its ring slot at every launch.  The
+ * reference's resident rows cover the sink and recent windows too
+ * (twilight_offload_cache.py:3323-3330). */
 int tw_decode_attention_pages_resident(const void* q, const void* k_base, const void* v_base, int dtype, int G,
                                        int R, int D, const int32_t* plan_pages, const uint8_t* plan_masks,
                                        const int32_t* plan_counts, int64_t plan_stride, int max_rows,
@@ -608,7 +620,8 @@ int tw_decode_attention_pages_resident(const void* q, const void* k_base, const 
                                        const int32_t* lengths, int length, int append, const void* cur_k,
                                        const void* cur_v, float softmax_scale, void* res_k, void* res_v,
                                        int64_t* res_map, int res_slots, int res_map_pages,
-                                       unsigned long long* res_stats, void* page_min, void* page_max,
+                                       unsigned long long* res_stats, void* res_win_k, void* res_win_v,
+                                       int32_t* res_win_state, int ring_rows, void* page_min, void* page_max,
                                        int64_t page_entry_stride, int meta_pages, void* out, void* workspace,
                                        size_t workspace_bytes, void* stream);
 int tw_decode_attention(const void* q, const void* k_base, const void* v_base, int dtype, int G,

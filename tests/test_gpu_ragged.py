@@ -327,6 +327,90 @@ def test_resident_page_cache_bit_exact(K, dev, ragged):
     assert union > 0 and 0 < hits < union, (hits, union)
 
 
+@pytest.mark.parametrize("ragged", [True, False])
+def test_resident_windows_serve_sink_and_recent(K, dev, ragged):
+    """Resident sink/recent windows: after each step the host slab's copies of
+    the next step's sink and recent rows are overwritten with noise, and the
+    next step still equals the plain launch over the intact slab bit for bit
+    (the windows come from HBM); the window buffers hold the slab's rows at
+    their slots and the state names the next length.  At step 4 the window
+    buffers are overwritten with noise and the state cleared instead: that
+    launch reads the slab and stores the windows again.  One ragged group
+    starts below the sink size and crosses it."""
+    _say(f"[resident windows] ragged={ragged}")
+    dtype, R, k, steps = "bf16", 4, 16, 7
+    lengths0 = [3000, 3000, 3000] if not ragged else [60, 2500, 3100, 4000]
+    G = len(lengths0)
+    Lmax = max(lengths0) + steps + 16
+    keys = randn((G, Lmax, D), dtype, seed=121)
+    vals = randn((G, Lmax, D), dtype, seed=122)
+    kh, vh = keys.clone().pin_memory(), vals.clone().pin_memory()      # resident run, noise planted
+    kh2, vh2 = keys.clone().pin_memory(), vals.clone().pin_memory()    # plain run, intact
+    pmin, pmax = _metadata(keys, lengths0, dtype, dev)
+    P = pmin.shape[1]
+    width = min(P, R * k)
+    res = K.ResidentPages(G, width, P, D, keys.dtype, dev, sink=SINK, recent=RECENT)
+    ring = res.ring
+    assert ring == 256 and tuple(res.win_k.shape) == (G, SINK + ring, D)
+    lengths = torch.tensor(lengths0, dtype=torch.int32, device=dev)
+    g = torch.Generator().manual_seed(123)
+    noise = torch.Generator().manual_seed(124)
+    base = torch.randn((G, R, D), generator=g)
+    for step in range(steps):
+        Ls = [L0 + step for L0 in lengths0]
+        kh.copy_(kh2)   # only this step's own window rows stay overwritten below
+        vh.copy_(vh2)
+        if step == 4:
+            res.win_k.copy_(torch.randn(res.win_k.shape, generator=noise).to(res.win_k.dtype))
+            res.win_v.copy_(torch.randn(res.win_v.shape, generator=noise).to(res.win_v.dtype))
+            res.win_state.zero_()
+        elif step > 0:
+            for gi, L in enumerate(Ls):
+                if L - 1 >= SINK:   # the previous launch stored the whole sink
+                    kh[gi, :SINK] = torch.randn((SINK, D), generator=noise).to(kh.dtype)
+                    vh[gi, :SINK] = torch.randn((SINK, D), generator=noise).to(vh.dtype)
+                r0 = oracle.selection_window(L, SINK, RECENT)[1]   # recent - 1 history rows
+                if r0 < L:
+                    kh[gi, r0:L] = torch.randn((L - r0, D), generator=noise).to(kh.dtype)
+                    vh[gi, r0:L] = torch.randn((L - r0, D), generator=noise).to(vh.dtype)
+        q = (base + 0.15 * torch.randn((G, R, D), generator=g)).to(torch.bfloat16)
+        ck, cv = randn((G, D), dtype, seed=600 + step), randn((G, D), dtype, seed=700 + step)
+        pp = torch.zeros((G, width), dtype=torch.int32, device=dev)
+        pm = torch.zeros((G, width), dtype=torch.uint8, device=dev)
+        pc = torch.zeros((G,), dtype=torch.int32, device=dev)
+        K.quest_select_ragged(q.float().to(dev), pmin, pmax, lengths, k, sink=SINK, recent=RECENT, block_size=BS,
+                              plan_pages=pp, plan_masks=pm, plan_counts=pc)
+        kw = dict(plan_masks=pm, max_pages=width, sink=SINK, recent=RECENT, block_size=BS, append=True,
+                  cur_k=ck.to(dev), cur_v=cv.to(dev))
+        if ragged:
+            a = K.decode_attention_pages_resident(q.to(dev), kh, vh, pp, pc, res, lengths=lengths, **kw)
+            b = K.decode_attention_pages_ragged(q.to(dev), kh2, vh2, pp, pc, lengths, **kw)
+        else:
+            L = Ls[0]
+            a = K.decode_attention_pages_resident(q.to(dev), kh, vh, pp, pc, res, length=L, **kw)
+            b = K.decode_attention_pages(q.to(dev), kh2, vh2, pp, pc, plan_masks=pm, max_pages=width, sink=SINK,
+                                         recent=RECENT, block_size=BS, length=L, append_position=L,
+                                         cur_k=ck.to(dev), cur_v=cv.to(dev))
+        torch.cuda.synchronize()
+        assert same_bits(a, b), step
+        state = res.win_state.cpu()
+        for gi, L in enumerate(Ls):
+            assert same_bits(kh[gi, L], kh2[gi, L]) and same_bits(vh[gi, L], vh2[gi, L]), (step, gi)  # the append
+            se = min(SINK, L)
+            assert state[gi].tolist() == [L + 1, int(se == SINK)], (step, gi, state[gi].tolist())
+            if se == SINK:
+                assert same_bits(res.win_k[gi, :SINK], kh2[gi, :SINK]), (step, gi)
+                assert same_bits(res.win_v[gi, :SINK], vh2[gi, :SINK]), (step, gi)
+            rows = torch.arange(oracle.selection_window(L, SINK, RECENT)[1], L + 1)
+            slots = SINK + (rows & (ring - 1))
+            assert same_bits(res.win_k[gi, slots.to(dev)], kh2[gi, rows]), (step, gi)
+            assert same_bits(res.win_v[gi, slots.to(dev)], vh2[gi, rows]), (step, gi)
+        lengths += 1
+    with pytest.raises(ValueError):
+        K.decode_attention_pages_resident(q.to(dev), kh, vh, pp, pc, res, lengths=lengths,
+                                          **dict(kw, recent=RECENT * 2))
+
+
 @pytest.mark.parametrize("resident", [False, True])
 def test_attention_fused_page_metadata(K, dev, resident):
     """The ragged page-tile attention with the page-metadata update fused in:

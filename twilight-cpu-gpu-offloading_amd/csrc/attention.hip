@@ -104,6 +104,21 @@ struct AttnArgs {
   int res_slots;
   int res_map_pages;
   unsigned long long* res_stats;
+  // Resident windows (with the resident page cache, nullable): res_win_k /
+  // res_win_v [G][win_rows][D] keep group g's sink rows at [0, sink) and its
+  // latest ring_rows rows (a power of two >= recent) at sink + (row &
+  // (ring_rows - 1)); res_win_state [G][2] = (the history length the ring
+  // serves: it holds rows [length - ring_rows + 1, length); 1 when the sink
+  // rows are stored too).  A launch reads the windows from HBM only when the
+  // ring serves its length (the previous launch was at length - 1 with a
+  // decode row), stores the window rows it read from the slab otherwise, and
+  // stores its decode row into the ring every time.  The recent window holds
+  // recent - 1 history rows, so the decode row's slot is never one this
+  // launch reads.
+  void* res_win_k;
+  void* res_win_v;
+  int32_t* res_win_state;
+  int win_rows, ring_rows;
   // Page metadata of the appended row (page-tile kernel, nullable): when the
   // row completes page p of its entry (row - sink + 1 a multiple of 16),
   // meta_min/meta_max [G][meta_stride] get that page's per-channel min/max
@@ -1351,6 +1366,10 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       pr[tt] = a.page_rows != nullptr ? a.page_rows[plan_base + u] : 0xffffu;
     }
   };
+  // resident windows: their state rides in round trip 1 (an unconditional
+  // load, from q when there are none)
+  const bool win_res = RES && a.res_win_k != nullptr;
+  const int2 wstate = *reinterpret_cast<const int2*>(win_res ? a.res_win_state + 2 * g : static_cast<const int32_t*>(a.q));
   uint4 qf[4];
   {
     const S* qh = static_cast<const S*>(a.q) + (static_cast<int64_t>(g) * R + (krow < R ? krow : 0)) * D + 8 * quarter;
@@ -1454,6 +1473,12 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   const int64_t res_base = static_cast<int64_t>(g) * 2 * a.res_slots;
   const int64_t res_prev = (res_base + static_cast<int64_t>((win.length - 1) & 1) * a.res_slots) * kTileRows;
   const int64_t res_cur = (res_base + static_cast<int64_t>(win.length & 1) * a.res_slots) * kTileRows;
+  // the sink rows and the recent ring in HBM, when their state serves this
+  // launch's length (a state written by this launch never does)
+  const bool ring_ok = win_res && wstate.x == win.length;
+  const bool sink_ok = ring_ok && wstate.y != 0;
+  const int ring_mask = a.ring_rows - 1;
+  const int64_t win_base = static_cast<int64_t>(g) * a.win_rows * D;
 
   float m_run[RMAX];
   float o_acc[RMAX][8];
@@ -1511,16 +1536,22 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
       const bool hit = hit_slot[tt] >= 0;
-      const int64_t tb = hit ? (res_prev + static_cast<int64_t>(hit_slot[tt]) * kTileRows) * D : ts[tt].pos0 * D;
-      const S* kt = hit ? static_cast<const S*>(a.res_k) : kg;
-      const S* vt = hit ? static_cast<const S*>(a.res_v) : vg;
+      // (wave-uniform) a sink tile or a recent tile served by the HBM windows
+      const bool wsink = sink_ok && t0 + tt < win.sink_tiles;
+      const bool wring = ring_ok && t0 + tt >= win.sink_tiles + nu;
+      const int64_t tb =
+          hit ? (res_prev + static_cast<int64_t>(hit_slot[tt]) * kTileRows) * D : ts[tt].pos0 * D + (wsink ? win_base : 0);
+      const S* kt = hit ? static_cast<const S*>(a.res_k) : (wsink || wring ? static_cast<const S*>(a.res_win_k) : kg);
+      const S* vt = hit ? static_cast<const S*>(a.res_v) : (wsink || wring ? static_cast<const S*>(a.res_win_v) : vg);
       // rows outside the tile or not kept read a kept row (the same lines,
       // no extra traffic) and are masked below
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * rg + j;
         const int vr = (r < ts[tt].cnt && ((ts[tt].rm >> r) & 1u)) ? r : ts[tt].r0;
-        const int64_t ro = tb + static_cast<int64_t>(vr) * D + c8;
+        const int64_t ro =
+            wring ? win_base + (a.sink + ((ts[tt].pos0 + vr) & ring_mask)) * static_cast<int64_t>(D) + c8
+                  : tb + static_cast<int64_t>(vr) * D + c8;
         const S* vp = r == ts[tt].dec ? vdec + c8 : vt + ro;
         vf[tt][j] = NT ? load_stream(vp) : *reinterpret_cast<const uint4*>(vp);
         // key row r, channels c8..c8+7, until the LDS pass below
@@ -1637,6 +1668,42 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
             o_acc[h][2 * i] = H::dot2(pp[h], lo[i], o_acc[h][2 * i]);
             o_acc[h][2 * i + 1] = H::dot2(pp[h], hi[i], o_acc[h][2 * i + 1]);
           }
+        }
+      }
+    }
+    // ---- resident windows: the sink rows and recent rows read from the slab
+    // go to HBM, and the decode row to its ring slot every launch ----
+    if (win_res) {
+#pragma unroll
+      for (int tt = 0; tt < TW; ++tt) {
+        const int t = t0 + tt;  // wave-uniform
+        const bool sink_tile = t < win.sink_tiles;
+        const bool recent_tile = t >= win.sink_tiles + nu && t < n_tiles;
+        if (!(sink_tile && !sink_ok) && !recent_tile) continue;
+        S* wk = static_cast<S*>(a.res_win_k) + win_base;
+        S* wv = static_cast<S*>(a.res_win_v) + win_base;
+        auto win_row = [&](int r) -> int64_t {   // window row of tile row r
+          const int64_t pos = ts[tt].pos0 + r;
+          return sink_tile ? pos : a.sink + (pos & ring_mask);
+        };
+        auto store_row = [&](int r) -> bool {
+          return r < ts[tt].cnt && (sink_tile || !ring_ok || r == ts[tt].dec);
+        };
+        if (store_row(krow)) {
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4)
+            *reinterpret_cast<uint4*>(wk + win_row(krow) * D + 32 * s4 + 8 * quarter) = kf[tt][s4];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * rg + j;
+          if (store_row(r)) *reinterpret_cast<uint4*>(wv + win_row(r) * D + c8) = vf[tt][j];
+        }
+        if (t == n_tiles - 1 && lane == 0) {
+          // the group's last tile: the state the next launch checks
+          const int ring_len = win.length + win.has_dec;
+          const int sink_stored = win.sink_end == a.sink ? 1 : 0;
+          *reinterpret_cast<int2*>(a.res_win_state + 2 * g) = make_int2(ring_len, sink_stored);
         }
       }
     }
@@ -2321,7 +2388,8 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
                        size_t workspace_bytes, void* stream, const uint32_t* page_rows = nullptr,
                        uint8_t* packed = nullptr, void* qscale = nullptr, void* qmin = nullptr,
                        int64_t quant_entry_stride = 0, const uint32_t* sel_bits = nullptr, int64_t bits_stride = 0,
-                       int bits_pages = 0, int phase = 3, int union_rec = 0) {
+                       int bits_pages = 0, int phase = 3, int union_rec = 0, void* res_win_k = nullptr,
+                       void* res_win_v = nullptr, int32_t* res_win_state = nullptr, int ring_rows = 0) {
   if (q == nullptr || out == nullptr || k_base == nullptr || v_base == nullptr) return TW_EINVAL;
   if (page_rows != nullptr && res_map != nullptr) return TW_EINVAL;  // the resident cache keeps whole pages
   if (packed != nullptr &&
@@ -2354,6 +2422,13 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
   if ((cur_k == nullptr) != (cur_v == nullptr)) return TW_EINVAL;
   if (lengths == nullptr && (length < 0 || length + 1 > entry_stride_rows)) return TW_EINVAL;
   if (res_map != nullptr && (res_k == nullptr || res_v == nullptr || res_slots < 1 || res_map_pages < 1))
+    return TW_EINVAL;
+  // resident windows: with the page cache; a ring of a power of two rows
+  // holding the recent window and the decode row
+  if (res_win_k != nullptr &&
+      (res_map == nullptr || res_win_v == nullptr || res_win_state == nullptr || ring_rows < recent ||
+       (ring_rows & (ring_rows - 1)) != 0 || (reinterpret_cast<uintptr_t>(res_win_k) % 16) ||
+       (reinterpret_cast<uintptr_t>(res_win_v) % 16) || (reinterpret_cast<uintptr_t>(res_win_state) % 8)))
     return TW_EINVAL;
   const uintptr_t align = 16;
   if ((reinterpret_cast<uintptr_t>(q) % align) || (reinterpret_cast<uintptr_t>(k_base) % align) ||
@@ -2399,6 +2474,11 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
   a.res_slots = res_slots;
   a.res_map_pages = res_map_pages;
   a.res_stats = res_stats;
+  a.res_win_k = res_win_k;
+  a.res_win_v = res_win_v;
+  a.res_win_state = res_win_state;
+  a.ring_rows = ring_rows;
+  a.win_rows = sink + ring_rows;
   a.meta_min = page_min;
   a.meta_max = page_max;
   a.meta_stride = page_entry_stride;
@@ -2459,14 +2539,16 @@ extern "C" int tw_decode_attention_pages_resident(
     const uint8_t* plan_masks, const int32_t* plan_counts, int64_t plan_stride, int max_rows,
     int64_t entry_stride_rows, int sink, int recent, int block_size, const int32_t* lengths, int length, int append,
     const void* cur_k, const void* cur_v, float softmax_scale, void* res_k, void* res_v, int64_t* res_map,
-    int res_slots, int res_map_pages, unsigned long long* res_stats, void* page_min, void* page_max,
-    int64_t page_entry_stride, int meta_pages, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+    int res_slots, int res_map_pages, unsigned long long* res_stats, void* res_win_k, void* res_win_v,
+    int32_t* res_win_state, int ring_rows, void* page_min, void* page_max, int64_t page_entry_stride, int meta_pages,
+    void* out, void* workspace, size_t workspace_bytes, void* stream) {
   if (res_map == nullptr) return TW_EINVAL;
   return tw::pages_tiles_launch(q, k_base, v_base, dtype, G, R, D, plan_pages, plan_masks, plan_counts, plan_stride,
                                 max_rows, entry_stride_rows, sink, recent, block_size, lengths, length, append, cur_k,
                                 cur_v, softmax_scale, res_k, res_v, res_map, res_slots, res_map_pages, res_stats,
                                 page_min, page_max, page_entry_stride, meta_pages, out, workspace, workspace_bytes,
-                                stream);
+                                stream, nullptr, nullptr, nullptr, nullptr, 0, nullptr, 0, 0, 3, 0, res_win_k,
+                                res_win_v, res_win_state, ring_rows);
 }
 
 extern "C" int tw_decode_attention_pages_ragged(const void* q, const void* k_base, const void* v_base, int dtype,

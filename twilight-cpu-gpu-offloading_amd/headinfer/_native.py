@@ -54,7 +54,7 @@ _HIP_SIGNATURES = {
                                                i32, vp, i32, vp, vp, f32, vp, vp, i64, i32, vp, vp, szt, vp]),
     "tw_decode_attention_pages_resident": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, i64, i32, i64, i32,
                                                  i32, i32, vp, i32, i32, vp, vp, f32, vp, vp, vp, i32, i32, vp, vp,
-                                                 vp, i64, i32, vp, vp, szt, vp]),
+                                                 vp, vp, i32, vp, vp, i64, i32, vp, vp, szt, vp]),
     "tw_add_rms_norm": (i32, [vp, vp, vp, f32, vp, i32, i32, i32, vp]),
     "tw_rope_qk": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "tw_silu_mul": (i32, [vp, vp, i32, i32, vp]),

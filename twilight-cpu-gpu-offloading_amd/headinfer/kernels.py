@@ -1536,21 +1536,38 @@ def decode_attention_union(
 class ResidentPages:
     """HBM resident page cache of G groups (one layer's entries) for a slab
     in host memory: K/V buffers [G, 2, slots, 16, D], the page map [G, pages]
-    int64 (-1 = never stored) and stats [G, 2] (hit pages, union pages)."""
+    int64 (-1 = never stored) and stats [G, 2] (hit pages, union pages).
+    With sink/recent given, the resident windows too: win_k/win_v [G, sink +
+    ring, D] (the sink rows, then a ring of the latest `ring` rows, ring the
+    smallest power of two >= recent: recent - 1 history rows and the decode
+    row) and win_state [G, 2] int32 (zeroed:
+    nothing stored yet)."""
 
     def __init__(self, groups: int, slots: int, pages: int, head_dim: int, dtype: torch.dtype,
-                 device: torch.device) -> None:
+                 device: torch.device, sink: int = 0, recent: int = 0) -> None:
         self.k = torch.empty((groups, 2, slots, 16, head_dim), dtype=dtype, device=device)
         self.v = torch.empty_like(self.k)
         self.map = torch.full((groups, pages), -1, dtype=torch.int64, device=device)
         self.stats = torch.zeros((groups, 2), dtype=torch.int64, device=device)
         self.slots, self.pages = slots, pages
+        self.sink = sink
+        self.ring = 1 << (max(recent, 1) - 1).bit_length() if sink + recent > 0 else 0
+        self.win_k = self.win_v = self.win_state = None
+        if self.ring > 0:
+            self.win_k = torch.empty((groups, sink + self.ring, head_dim), dtype=dtype, device=device)
+            self.win_v = torch.empty_like(self.win_k)
+            self.win_state = torch.zeros((groups, 2), dtype=torch.int32, device=device)
 
     def view(self, g0: int, n: int) -> "ResidentPages":
         out = ResidentPages.__new__(ResidentPages)
         out.k, out.v = self.k[g0:g0 + n], self.v[g0:g0 + n]
         out.map, out.stats = self.map[g0:g0 + n], self.stats[g0:g0 + n]
         out.slots, out.pages = self.slots, self.pages
+        out.sink, out.ring = self.sink, self.ring
+        out.win_k = out.win_v = out.win_state = None
+        if self.win_k is not None:
+            out.win_k, out.win_v = self.win_k[g0:g0 + n], self.win_v[g0:g0 + n]
+            out.win_state = self.win_state[g0:g0 + n]
         return out
 
 
@@ -1581,8 +1598,11 @@ def decode_attention_pages_resident(
     (lengths [G] int32 on the device), with union pages kept in an HBM
     resident page cache: pages the previous step stored are read from HBM,
     the rest from the slab, and every union page read is stored for the next
-    step.  16-bit K/V, D = 128, block_size 16.  page_min/page_max as in
-    decode_attention_pages_ragged.  Returns [G, R, D]."""
+    step.  With resident windows (a ResidentPages built with sink/recent),
+    the sink rows and the recent window come from HBM once stored, and the
+    decode row joins the ring every step.  16-bit K/V, D = 128, block_size
+    16.  page_min/page_max as in decode_attention_pages_ragged.  Returns
+    [G, R, D]."""
     if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("q must be [G, R, D] fp16/bf16")
     G, R, D = q.shape
@@ -1608,6 +1628,12 @@ def decode_attention_pages_resident(
             or tuple(rm.shape) != (G, resident.pages) or not rm.is_contiguous() \
             or tuple(rs.shape) != (G, 2) or not rs.is_contiguous():
         raise ValueError("resident buffers do not match the launch")
+    wk, wv, wst = resident.win_k, resident.win_v, resident.win_state
+    if wk is not None and (resident.sink != sink or resident.ring < recent or wk.dtype != q.dtype
+                           or tuple(wk.shape) != (G, sink + resident.ring, D) or not wk.is_contiguous()
+                           or wv.shape != wk.shape or not wv.is_contiguous() or wst.dtype != torch.int32
+                           or tuple(wst.shape) != (G, 2) or not wst.is_contiguous()):
+        raise ValueError("resident windows do not match the launch (sink, recent, dtype, shape)")
     if not 0 <= max_pages <= plan_pages.shape[1]:
         raise ValueError("max_pages must be within the plan width")
     if (cur_k is None) != (cur_v is None):
@@ -1631,7 +1657,8 @@ def decode_attention_pages_resident(
             ptr(q), kp, vp, _dt(q), G, R, D, ptr(plan_pages), ptr(plan_masks), ptr(plan_counts),
             plan_pages.stride(0), max_rows, k_cache.stride(0) // D, sink, recent, block_size, ptr(lengths),
             int(length), int(bool(append)), ptr(cur_k), ptr(cur_v), scale, ptr(rk), ptr(rv), ptr(rm),
-            resident.slots, resident.pages, ptr(rs), *meta, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
+            resident.slots, resident.pages, ptr(rs), ptr(wk), ptr(wv), ptr(wst), resident.ring if wk is not None else 0,
+            *meta, ptr(out), ptr(ws), ws.numel(), stream_handle(dev)),
             "decode_attention_pages_resident")
     return out
 

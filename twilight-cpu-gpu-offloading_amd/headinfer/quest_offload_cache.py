@@ -687,7 +687,7 @@ class QuestTopKOffloadedCache(_CacheBase):
     def resident_pages(self) -> "kernels.ResidentPages":
         """The HBM resident page cache of every entry (allocated on first use):
         slots for the widest union plan the budget allows, a map over every
-        page the metadata can hold."""
+        page the metadata can hold, and the resident sink and recent windows."""
         if self._resident is None:
             if self._page_min is None:
                 raise RuntimeError("prompt metadata is missing")
@@ -698,7 +698,8 @@ class QuestTopKOffloadedCache(_CacheBase):
                                                                                     - self.sink_tokens)
                                                                                    // self.block_size))))
             slots = max(1, min(pages, self.num_query_heads_per_kv * budget))
-            self._resident = kernels.ResidentPages(G_all, slots, pages, D, self.dtype, self.device)
+            self._resident = kernels.ResidentPages(G_all, slots, pages, D, self.dtype, self.device,
+                                                   sink=self.sink_tokens, recent=self.recent_tokens)
         return self._resident
 
     def resident_stats(self) -> Dict[str, int]:
