@@ -442,6 +442,32 @@ int tw_twilight_select_fused_matched(const float* q, const void* page_min, const
                                      int target_total, double matched_fraction, int32_t* sel_pages, float* logits,
                                      int32_t* desired, int32_t* allocated, uint32_t* union_rec, int64_t rec_stride,
                                      void* workspace, size_t workspace_bytes, void* stream);
+/* tw_twilight_select_fused_matched for a KV group of more than 8 query heads,
+ * run as sub-groups of at most 8 (R here) that share one allocation over all
+ * heads_all <= 64 heads of the group, in two parts per sub-group.  Part 1:
+ * the score + INT4 QK launch and the head launch, the sub-group's top-p counts
+ * into desired [G][R] (and its B0 pages, logits and key ranges into sel_pages
+ * and the workspace; union_rec cleared).  Part 2, once the caller has placed
+ * every sub-group's counts in desired_all [G][heads_all] (this sub-group's at
+ * columns head0 .. head0 + R - 1): the allocation over all heads_all heads
+ * (matched_budget_counts towards target_total, or with lengths fixed_g * 16 *
+ * heads_all; twilight_offload_cache.py:50-86, 1019-1083) and this
+ * sub-group's top-allocated rows ORed into union_rec, with the same
+ * workspace, sel_pages and union_rec as its part 1.  The group's union is
+ * the OR of its sub-groups' records.  Other arguments as
+ * tw_twilight_select_fused_matched.  Replaces the matched path of
+ * prepare_layer_selection for wide GQA groups (twilight_offload_cache.py:
+ * 996-1614), which has no head limit. */
+int tw_twilight_select_fused_matched_part(const float* q, const void* page_min, const void* page_max, int dtype,
+                                          int G, int R, int P, int D, int64_t page_group_stride,
+                                          const uint8_t* packed, const void* qscale, const void* qmin,
+                                          int64_t quant_entry_stride, int64_t quant_rows, int b0_pages, float top_p,
+                                          float qk_scale, int sink, int recent, int block_size,
+                                          const int32_t* lengths, int length, int target_total,
+                                          double matched_fraction, int32_t* sel_pages, float* logits,
+                                          int32_t* desired, int32_t* allocated, uint32_t* union_rec,
+                                          int64_t rec_stride, int part, const int32_t* desired_all, int heads_all,
+                                          int head0, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Sparse GQA decode attention, split-K over selected rows, one query

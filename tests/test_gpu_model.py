@@ -322,14 +322,15 @@ def test_graph_decoder_fused_equals_unfused(dev):
 
 
 @pytest.mark.parametrize("fuse,mode,q_heads", [(True, "dynamic", 8), (False, "dynamic", 8), (True, "matched", 8),
-                                               (True, "dynamic", 32)])
+                                               (True, "dynamic", 32), (True, "matched", 32)])
 def test_graph_decoder_twilight_matches_eager(dev, fuse, mode, q_heads):
     """GraphDecoder over a Twilight cache (Quest B0, INT4 QK, top-p and the
     GQA union from device-side lengths, the union attention with the append,
     the INT4 + page metadata update) == the eager patched model with the same
     cache policy, token by token; the steps cross a page completion.  32
     query heads over 2 KV heads (16 per group) run the fused selection and
-    the union attention as sub-groups of 8."""
+    the union attention as sub-groups of 8 (matched: one allocation over the
+    16 heads)."""
     from headinfer import mp
     from headinfer.graph_decode import GraphDecoder
     from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache

@@ -389,8 +389,8 @@ def test_fused_selection_wide_group(K, dev, R):
     """More than 8 query heads per KV head through the fused selection and the
     union attention: sub-groups of at most 8 heads, their records ORed into
     the group's.  B0 pages, logits, top-p counts and the record against
-    oracle.twilight_layer over all R heads; matched budgets are refused (they
-    allocate over every head at once)."""
+    oracle.twilight_layer over all R heads (matched budgets:
+    test_fused_matched_wide_group)."""
     G, L, b0 = 2, 6000, 64
     st = _Setup(K, dev, G, R, L + 8, [L] * G, seed=40 + R)
     D, bs, sink, recent = st.D, st.bs, st.sink, st.recent
@@ -431,7 +431,87 @@ def test_fused_selection_wide_group(K, dev, R):
         ref_o[gi] = oracle.decode_attention(qf[gi].cpu().numpy(), keys, vals, 1.0 / math.sqrt(D))
     _close(out.float().cpu().numpy(), ref_o, f"wide union-record attention R={R}")
     assert torch.equal(k[:, L].view(torch.int16), cur_k.view(torch.int16))
-    with pytest.raises(ValueError, match="at most 8 query heads"):
-        K.twilight_select_fused(qf, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec,
-                                top_p=0.9, sink=sink, recent=recent, block_size=bs, length=L, sel_pages=sel,
-                                budget_mode="matched", target_total=12 * bs * R)
+
+
+@pytest.mark.parametrize("R,ragged", [(12, False), (16, False), (40, False), (12, True)])
+def test_fused_matched_wide_group(K, dev, R, ragged):
+    """Matched budgets over more than 8 query heads per KV head: the
+    sub-groups' score + QK and head launches, then each sub-group's
+    allocation + top-allocated launch over all R heads' counts.  B0 pages,
+    logits, counts, the allocation (largest remainder over all R heads,
+    summing to the group's target) and the ORed record against
+    oracle.twilight_layer over all R heads; with device lengths each group's
+    target from its own length (one group below the first whole page).  More
+    than 64 heads are refused."""
+    lengths = [300, 5000, 9000] if ragged else [6000, 6000]
+    G, b0, top_p, frac = len(lengths), 64, 0.9, 0.05
+    L = max(lengths)
+    st = _Setup(K, dev, G, R, L + 8, lengths, seed=60 + R)
+    D, bs, sink, recent = st.D, st.bs, st.sink, st.recent
+    P = st.P if ragged else oracle.selection_window(L, sink, recent)[2] // bs
+    words = K.union_record_words(P)
+    rec = torch.full((G, (words + 3) & ~3), -1, dtype=torch.int32, device=dev)
+    sel = torch.zeros((G, R, b0), dtype=torch.int32, device=dev)
+    logits = torch.zeros((G, R, b0 * bs), dtype=torch.float32, device=dev)
+    desired = torch.zeros((G, R), dtype=torch.int32, device=dev)
+    allocated = torch.full((G, R), -7, dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(R + 3)
+    q = (torch.randn((G, R, D), generator=gen, device=dev) * 2).to(torch.bfloat16)
+    cur_k = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+    cur_v = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+    qf = q.float()
+    kw = dict(top_p=top_p, sink=sink, recent=recent, block_size=bs, desired=desired, sel_pages=sel, logits=logits,
+              budget_mode="matched", allocated=allocated)
+    fixed_one = 24
+    if ragged:
+        lens = torch.tensor(lengths, dtype=torch.int32, device=dev)
+        kw.update(length=L, lengths=lens, matched_fraction=frac)
+    else:
+        lens = None
+        kw.update(length=L, target_total=fixed_one * bs * R)
+    _say(f"[fused matched wide] G={G} R={R} lengths={lengths} b0={b0}")
+    K.twilight_select_fused(qf, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec, **kw)
+    k, v = st.k.clone(), st.v.clone()
+    akw = dict(lengths=lens, length=L) if ragged else dict(length=L)
+    out = K.decode_attention_union(q, k, v, rec, P, max_pages=min(P, R * b0), sink=sink, recent=recent,
+                                   block_size=bs, append=True, cur_k=cur_k, cur_v=cur_v, **akw)
+    torch.cuda.synchronize()
+    rec_h, sel_h, log_h = rec.cpu().numpy(), sel.cpu().numpy(), logits.cpu().numpy()
+    des_h, all_h = desired.cpu().numpy(), allocated.cpu().numpy()
+    ref_o = np.zeros((G, R, D))
+    for gi, Lg in enumerate(lengths):
+        sink_end, recent_start, eligible = oracle.selection_window(Lg, sink, recent)
+        cand = min(eligible // bs, P)
+        bits, masks = _decode_record(rec_h[gi], P)
+        if cand == 0:
+            assert np.all(des_h[gi] == 0) and np.all(all_h[gi] == 0) and not bits.any() and not masks.any(), gi
+            kept = np.concatenate([np.arange(sink_end), np.arange(recent_start, Lg)]).astype(np.int64)
+        else:
+            b0g = min(b0, cand)
+            fixed = min(cand, max(1, math.ceil(frac * eligible / bs))) if ragged else fixed_one
+            ref = oracle.twilight_layer(qf[gi].cpu().numpy(), to_bits(st.pmin[gi, :cand]),
+                                        to_bits(st.pmax[gi, :cand]), st.packed[gi].cpu().numpy(),
+                                        to_bits(st.qscale[gi]), to_bits(st.qmin[gi]), "bf16", length=Lg, sink=sink,
+                                        recent=recent, block_size=bs, b0_pages=b0g, top_p=top_p,
+                                        budget_mode="matched", fixed_pages=fixed)
+            Ng = b0g * bs
+            assert np.array_equal(sel_h[gi, :, :b0g], ref["pages"]), gi
+            assert np.array_equal(log_h[gi, :, :Ng].view(np.uint32),
+                                  ref["logits"].astype(np.float32).view(np.uint32)), gi
+            assert np.array_equal(des_h[gi], ref["desired"]), (gi, des_h[gi], ref["desired"])
+            assert np.array_equal(all_h[gi], ref["allocated"]), (gi, all_h[gi], ref["allocated"])
+            assert all_h[gi].sum() == fixed * bs * R, gi
+            want = _record_of(np.unique(np.concatenate(ref["selected"])), P, sink, bs)
+            assert np.array_equal(masks, want) and np.array_equal(bits[:P], want != 0) and not bits[P:].any(), gi
+            kept = ref["union"].astype(np.int64)
+        keys = torch.cat([st.k[gi, kept].float(), cur_k[gi:gi + 1].float()]).cpu().numpy()
+        vals = torch.cat([st.v[gi, kept].float(), cur_v[gi:gi + 1].float()]).cpu().numpy()
+        ref_o[gi] = oracle.decode_attention(qf[gi].cpu().numpy(), keys, vals, 1.0 / math.sqrt(D))
+    _close(out.float().cpu().numpy(), ref_o, f"matched wide union-record attention R={R}")
+    _say(f"[fused matched wide] ok, allocated {all_h[-1].tolist()}")
+    if R == 12 and not ragged:
+        q65 = torch.zeros((G, 65, D), dtype=torch.float32, device=dev)
+        with pytest.raises(ValueError, match="at most 64 query heads"):
+            K.twilight_select_fused(q65, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec,
+                                    top_p=top_p, sink=sink, recent=recent, block_size=bs, length=L,
+                                    budget_mode="matched", target_total=65 * bs)

@@ -116,9 +116,10 @@ def test_twilight_gqa_group_union_wide_group(H, dev, R, mode):
 
 @pytest.mark.parametrize("mode", ["matched", "dynamic"])
 def test_twilight_decode_layer_wide_group(H, dev, mode):
-    """decode_layer with 16 query heads per KV head: matched budgets take the
-    general path (budgets over all 16 heads on the host), dynamic budgets the
-    fused selection in two sub-groups of 8 whose records are ORed."""
+    """decode_layer with 16 query heads per KV head through the fused
+    selection in two sub-groups of 8 whose records are ORed: dynamic budgets
+    each head's own, matched budgets one allocation over all 16 heads (each
+    sub-group's last launch reads every head's top-p count)."""
     G, R, D, T = 2, 16, 128, 1500
     _say(f"[wide twilight decode_layer] {mode}")
     cache = _twilight_cache(H, dev, E=G, T=T, D=D, R=R, dtype="f16", residency="hbm", mode=mode,
@@ -142,3 +143,4 @@ def test_twilight_decode_layer_wide_group(H, dev, mode):
     _close(out, ref_out)
     torch.cuda.synchronize()
     assert _same(cache._key_cache[0, T], nk[0])
+    assert cache._fused_bufs is not None   # the fused selection ran, not the general path

@@ -1046,45 +1046,60 @@ __device__ int block_top_mass(const uint32_t (&key)[KPT], const uint64_t (&mass)
 // to desired in float64, floors first, then +1 by (fractional remainder desc,
 // desired desc, index asc); any excess is taken from the heads with the
 // smallest (desired, index).  capacity: the candidate count of every head.
-__device__ void matched_counts(const int* desired, int R, int target, int capacity, int* counts) {
-  double raw[8];
-  double total = 0.0;
-  for (int i = 0; i < R; ++i) total = total + static_cast<double>(desired[i]);
+// One wavefront forms it, lane i for head i of R <= 64 (every lane active,
+// desired[i] >= 1 read by lane i), and every lane gets its own head's count
+// (0 past R).  The serial +1 loop is taken in batches with the same outcome:
+// a head with a positive remainder is picked at most once (its remainder is
+// then 0), and once the best remaining key has remainder 0 every key has, so
+// that head takes +1 until it reaches capacity or the target; the excess is
+// taken from the same smallest head until it keeps one.  At most 3R rounds.
+__device__ int wave_matched_counts(const int32_t* desired, int R, int target, int capacity) {
+  const int lane = lane_id();
+  const bool live = lane < R;
+  const int d = live ? desired[lane] : 0;
+  // the counts are integers below 2^53, so their float64 sum is exact in any order
+  const double total = static_cast<double>(static_cast<int64_t>(wave_sum_i32(d)));
   const int remaining = target - R;
-  int sum = 0;
-  for (int i = 0; i < R; ++i) {
-    raw[i] = static_cast<double>(remaining) * static_cast<double>(desired[i]) / total;
-    const double fl = floor(raw[i]);
-    const int extra = fl < static_cast<double>(capacity - 1) ? static_cast<int>(fl) : capacity - 1;
-    counts[i] = 1 + extra;
-    sum += counts[i];
+  double raw = live ? static_cast<double>(remaining) * static_cast<double>(d) / total : 0.0;
+  int cnt = 0;
+  if (live) {
+    const double fl = floor(raw);
+    cnt = 1 + (fl < static_cast<double>(capacity - 1) ? static_cast<int>(fl) : capacity - 1);
   }
-  while (sum < target) {
-    int best = -1;
-    for (int i = 0; i < R; ++i) {
-      if (counts[i] >= capacity) continue;
-      if (best < 0) {
-        best = i;
-        continue;
-      }
-      const double fi = raw[i] - floor(raw[i]), fb = raw[best] - floor(raw[best]);
-      if (fi > fb || (fi == fb && desired[i] > desired[best])) best = i;
+  int sum = wave_sum_i32(cnt);
+  while (sum < target) {  // wave-uniform
+    const double fl = floor(raw);
+    // remainders are >= +0, so their bits order them; +1 keeps a 0 remainder
+    // of an eligible head above the ineligible heads' key 0
+    const uint64_t key = (live && cnt < capacity) ? static_cast<uint64_t>(__double_as_longlong(raw - fl)) + 1ull : 0ull;
+    const uint32_t khi = static_cast<uint32_t>(key >> 32), klo = static_cast<uint32_t>(key);
+    const uint32_t mhi = wave_max_u32(khi);
+    const uint32_t mlo = wave_max_u32(khi == mhi ? klo : 0u);
+    if (mhi == 0u && mlo == 0u) break;  // every head at capacity
+    const bool top = khi == mhi && klo == mlo;
+    const uint32_t md = wave_max_u32(top ? static_cast<uint32_t>(d) : 0u);
+    const int best = first_lane(__ballot(top && static_cast<uint32_t>(d) == md));
+    const bool positive = mhi != 0u || mlo > 1u;  // the best remainder is above 0
+    const int cb = static_cast<int>(readlane_u32(static_cast<uint32_t>(cnt), best));
+    const int room = target - sum < capacity - cb ? target - sum : capacity - cb;
+    const int add = positive ? 1 : room;
+    if (lane == best) {
+      cnt += add;
+      raw = fl;
     }
-    if (best < 0) break;
-    counts[best] += 1;
-    raw[best] = floor(raw[best]);
-    ++sum;
+    sum += add;
   }
   while (sum > target) {
-    int worst = -1;
-    for (int i = 0; i < R; ++i) {
-      if (counts[i] <= 1) continue;
-      if (worst < 0 || desired[i] < desired[worst]) worst = i;
-    }
-    if (worst < 0) break;
-    counts[worst] -= 1;
-    --sum;
+    const uint32_t key = (live && cnt > 1) ? static_cast<uint32_t>(d) : 0xffffffffu;
+    const uint32_t mk = wave_min_u32(key);
+    if (mk == 0xffffffffu) break;  // every head keeps one
+    const int worst = first_lane(__ballot(key == mk));
+    const int cw = static_cast<int>(readlane_u32(static_cast<uint32_t>(cnt), worst));
+    const int sub = sum - target < cw - 1 ? sum - target : cw - 1;
+    if (lane == worst) cnt -= sub;
+    sum -= sub;
   }
+  return cnt;
 }
 
 // Bits of [a, b) within the 32-position word starting at lo.
@@ -1739,15 +1754,12 @@ __global__ __launch_bounds__(NT) void twilight_matched_kernel(SelectArgs s) {
   const int g = row / s.R;
   const int r = row - g * s.R;
   const int N = s.N;
-  if (threadIdx.x == 0) {
-    if (s.given) {
-      sh.ires[1] = s.allocated[row];
-    } else {
-      int d[8], c[8];
-      for (int i = 0; i < s.R; ++i) d[i] = s.desired[static_cast<int64_t>(g) * s.R + i];
-      matched_counts(d, s.R, s.target_total, N, c);
-      sh.ires[1] = c[r];
-    }
+  if (s.given) {
+    if (threadIdx.x == 0) sh.ires[1] = s.allocated[row];
+  } else if (threadIdx.x < kWave) {  // the first wavefront, whole
+    const int c = wave_matched_counts(s.desired + static_cast<int64_t>(g) * s.R, s.R, s.target_total, N);
+    const int cr = static_cast<int>(readlane_u32(static_cast<uint32_t>(c), r));
+    if (threadIdx.x == 0) sh.ires[1] = cr;
   }
   float* stage = reinterpret_cast<float*>(union_bits + stage_offset_words(s.length));
   uint32_t key[KPT];
@@ -2282,7 +2294,7 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_topp_head_kernel(HeadAr
 // after twilight_topp_head_kernel (matched) has written every head's top-p
 // count and left its candidates' logits, B0 pages and wavefront key ranges in
 // the workspace.
-// Every block of a group forms the same allocation (matched_counts), takes
+// Every block of a group forms the same allocation (wave_matched_counts), takes
 // its head's top-allocated logits (key desc, candidate index asc: the
 // selection twilight_matched_kernel makes) and ORs their rows into the
 // union record the score kernel cleared.  With lengths (device), group g's
@@ -2293,9 +2305,11 @@ struct MatchedRecArgs {
   const float* ws_logits;     // [G * R][b0 * 16]
   const uint32_t* ws_range;   // [G * R][parts * 8][4] (max logit, max key, min key, 0)
   const int32_t* sel_pages;   // [G][R][b0] ascending
-  const int32_t* desired;     // [G][R] top-p counts
+  const int32_t* desired;     // [G][desired_stride]: the top-p counts of every head of the group
+  int64_t desired_stride;
   int32_t* allocated;         // nullable [G][R]
   int G, R, P, b0, parts, target_total;
+  int heads_all, head0;       // the group's heads (<= 64); this launch's are head0 .. head0 + R - 1
   const int32_t* lengths;     // nullable [G]: group g has min(lengths[g], length) tokens
   int length, sink, recent;
   double frac;                // matched_budget_fraction (with lengths)
@@ -2330,8 +2344,8 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_matched_rec_kernel(Matc
     const double f = ceil(a.frac * static_cast<double>(recent_start - sink_end) / static_cast<double>(BS));
     int fixed = f < 1.0 ? 1 : (f > static_cast<double>(Pg) ? Pg : static_cast<int>(f));
     fixed = fixed < Pg ? fixed : Pg;
-    target = fixed * BS * a.R;
-    target = target < a.R * N ? target : a.R * N;
+    target = fixed * BS * a.heads_all;
+    target = target < a.heads_all * N ? target : a.heads_all * N;
   }
   if (N == 0) {  // block-uniform: no candidate, nothing kept, nothing allocated
     if (tid == 0 && a.allocated != nullptr) a.allocated[row] = 0;
@@ -2339,14 +2353,6 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_matched_rec_kernel(Matc
   }
   topk_fast_clear(sh.sel);
   // ---- one round trip: the group's counts, the row's pages, logits and ranges ----
-  if (tid == 0) {
-    int d[8], c[8];
-    for (int i = 0; i < a.R; ++i) d[i] = a.desired[static_cast<int64_t>(g) * a.R + i];
-    matched_counts(d, a.R, target, N, c);
-    const int k = c[r] < 1 ? 1 : (c[r] > N ? N : c[r]);
-    s_k = k;
-    if (a.allocated != nullptr) a.allocated[row] = k;
-  }
   for (int i = tid; i < a.b0; i += NT) s_page[i] = a.sel_pages[static_cast<int64_t>(row) * a.b0 + i];
   uint32_t lkey[KPB];
   uint32_t kmin, kmax;
@@ -2374,6 +2380,17 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_matched_rec_kernel(Matc
     }
     kmax = wave_max_u32(kmx);
     kmin = wave_min_u32(kmn);
+  }
+  // the allocation, by the first wavefront (whole) while the others' loads land
+  if (tid < kWave) {
+    const int c = wave_matched_counts(a.desired + static_cast<int64_t>(g) * a.desired_stride, a.heads_all, target,
+                                      N);
+    const int cr = static_cast<int>(readlane_u32(static_cast<uint32_t>(c), a.head0 + r));
+    const int k = cr < 1 ? 1 : (cr > N ? N : cr);
+    if (tid == 0) {
+      s_k = k;
+      if (a.allocated != nullptr) a.allocated[row] = k;
+    }
   }
   __syncthreads();  // s_k, s_page and the cleared histogram
   const int k = s_k;
@@ -2735,22 +2752,32 @@ namespace tw {
 namespace {
 
 // tw_twilight_select_fused (matched false) and tw_twilight_select_fused_matched.
+// phase 1: the score + INT4 QK launch; 2: it and the head launch; 3: the whole
+// selection; 4 (matched): the allocation + top-allocated launch alone, after
+// a phase-2 call with the same workspace.  desired_all (nullable, matched):
+// the top-p counts of all heads_all heads of each group ([G][heads_all]), of
+// which this call's R heads are head0 .. head0 + R - 1; null means this call's
+// own R counts.
 int select_fused(const float* q, const void* page_min, const void* page_max, int dtype, int G, int R, int P, int D,
                  int64_t page_group_stride, const uint8_t* packed, const void* qscale, const void* qmin,
                  int64_t quant_entry_stride, int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink,
                  int recent, int block_size, const int32_t* lengths, int length, int32_t* sel_pages, float* logits,
                  int32_t* desired, uint32_t* union_rec, int64_t rec_stride, void* workspace, size_t workspace_bytes,
                  bool matched, int target_total, double matched_fraction, int32_t* allocated, void* stream,
-                 int phase = 3) {
-  if (phase != 1 && phase != 3) return TW_EINVAL;
+                 int phase = 3, const int32_t* desired_all = nullptr, int heads_all = 0, int head0 = 0) {
+  if (phase < 1 || phase > 4 || (phase == 4 && !matched)) return TW_EINVAL;
   if (q == nullptr || page_min == nullptr || page_max == nullptr || packed == nullptr || qscale == nullptr ||
       qmin == nullptr || desired == nullptr || union_rec == nullptr)
     return TW_EINVAL;
+  const int32_t* dall = desired_all != nullptr ? desired_all : desired;
+  const int hall = desired_all != nullptr ? heads_all : R;
+  const int h0 = desired_all != nullptr ? head0 : 0;
   // matched: the B0 pages as an output the last launch reads; a target for
-  // one length, or the matched fraction for device lengths
-  if (matched && (sel_pages == nullptr ||
-                  (lengths == nullptr && (target_total < R || static_cast<int64_t>(target_total) >
-                                                                  static_cast<int64_t>(R) * b0_pages * 16)) ||
+  // one length (over all hall heads), or the matched fraction for device
+  // lengths; one wavefront allocates, a lane a head
+  if (matched && (sel_pages == nullptr || hall < R || hall > kWave || h0 < 0 || h0 + R > hall ||
+                  (lengths == nullptr && (target_total < hall || static_cast<int64_t>(target_total) >
+                                                                     static_cast<int64_t>(hall) * b0_pages * 16)) ||
                   (lengths != nullptr && !(matched_fraction > 0.0 && matched_fraction <= 1.0))))
     return TW_EINVAL;
   if (dtype != TW_DTYPE_F16 && dtype != TW_DTYPE_BF16) return TW_EUNSUPPORTED;
@@ -2770,70 +2797,76 @@ int select_fused(const float* q, const void* page_min, const void* page_max, int
     return TW_ENOMEM;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const FusedWorkspace w = fused_layout(workspace, G, R, P, b0_pages);
-  ScoreQkArgs sq{};
-  sq.q = q;
-  sq.pmin = page_min;
-  sq.pmax = page_max;
-  sq.group_stride = page_group_stride;
-  sq.G = G;
-  sq.R = R;
-  sq.P = P;
-  sq.lengths = lengths;
-  sq.sink = sink;
-  sq.recent = recent;
-  sq.packed = packed;
-  sq.scale = qscale;
-  sq.minimum = qmin;
-  sq.qstride = quant_entry_stride;
-  sq.qrows = quant_rows;
-  sq.qk_scale = qk_scale;
-  sq.scores = w.scores;
-  sq.score_stride = w.score_stride;
-  sq.tile_mm = w.tile_mm;
-  sq.logits = w.qk_logits;
-  sq.logit_stride = w.logit_stride;
-  sq.rec = union_rec;
-  sq.rec_stride = rec_stride;
-  int rc = dtype == TW_DTYPE_F16 ? launch_score_qk<F16>(sq, st) : launch_score_qk<BF16>(sq, st);
-  if (rc != TW_OK || phase == 1) return rc;
-  HeadArgs h{};
-  h.scores = w.scores;
-  h.score_stride = w.score_stride;
-  h.vec_last4 = static_cast<int>(w.score_stride) - 4;
-  h.tile_mm = w.tile_mm;
-  h.G = G;
-  h.R = R;
-  h.P = P;
-  h.b0 = b0_pages;
-  h.parts = 1;
-  h.qk_logits = w.qk_logits;
-  h.logit_stride = w.logit_stride;
-  h.ws_logits = w.cand_logits;
-  h.ws_range = w.ranges;
-  h.lengths = lengths;
-  h.length = length;
-  h.sink = sink;
-  h.recent = recent;
-  h.p24 = static_cast<uint32_t>(__builtin_rintf(top_p * 16777216.0f));
-  h.sel_pages = sel_pages;
-  h.logits = logits;
-  h.desired = desired;
-  h.rec = union_rec;
-  h.rec_stride = rec_stride;
-  h.matched = matched ? 1 : 0;
-  rc = launch_head(h, st);
-  if (rc != TW_OK || !matched) return rc;
+  int rc = TW_OK;
+  if (phase != 4) {
+    ScoreQkArgs sq{};
+    sq.q = q;
+    sq.pmin = page_min;
+    sq.pmax = page_max;
+    sq.group_stride = page_group_stride;
+    sq.G = G;
+    sq.R = R;
+    sq.P = P;
+    sq.lengths = lengths;
+    sq.sink = sink;
+    sq.recent = recent;
+    sq.packed = packed;
+    sq.scale = qscale;
+    sq.minimum = qmin;
+    sq.qstride = quant_entry_stride;
+    sq.qrows = quant_rows;
+    sq.qk_scale = qk_scale;
+    sq.scores = w.scores;
+    sq.score_stride = w.score_stride;
+    sq.tile_mm = w.tile_mm;
+    sq.logits = w.qk_logits;
+    sq.logit_stride = w.logit_stride;
+    sq.rec = union_rec;
+    sq.rec_stride = rec_stride;
+    rc = dtype == TW_DTYPE_F16 ? launch_score_qk<F16>(sq, st) : launch_score_qk<BF16>(sq, st);
+    if (rc != TW_OK || phase == 1) return rc;
+    HeadArgs h{};
+    h.scores = w.scores;
+    h.score_stride = w.score_stride;
+    h.vec_last4 = static_cast<int>(w.score_stride) - 4;
+    h.tile_mm = w.tile_mm;
+    h.G = G;
+    h.R = R;
+    h.P = P;
+    h.b0 = b0_pages;
+    h.parts = 1;
+    h.qk_logits = w.qk_logits;
+    h.logit_stride = w.logit_stride;
+    h.ws_logits = w.cand_logits;
+    h.ws_range = w.ranges;
+    h.lengths = lengths;
+    h.length = length;
+    h.sink = sink;
+    h.recent = recent;
+    h.p24 = static_cast<uint32_t>(__builtin_rintf(top_p * 16777216.0f));
+    h.sel_pages = sel_pages;
+    h.logits = logits;
+    h.desired = desired;
+    h.rec = union_rec;
+    h.rec_stride = rec_stride;
+    h.matched = matched ? 1 : 0;
+    rc = launch_head(h, st);
+    if (rc != TW_OK || !matched || phase == 2) return rc;
+  }
   tw::MatchedRecArgs m{};
-  m.ws_logits = h.ws_logits;
-  m.ws_range = h.ws_range;
+  m.ws_logits = w.cand_logits;
+  m.ws_range = w.ranges;
   m.sel_pages = sel_pages;
-  m.desired = desired;
+  m.desired = dall;
+  m.desired_stride = hall;
+  m.heads_all = hall;
+  m.head0 = h0;
   m.allocated = allocated;
   m.G = G;
   m.R = R;
   m.P = P;
   m.b0 = b0_pages;
-  m.parts = h.parts;
+  m.parts = 1;
   m.target_total = target_total;
   m.lengths = lengths;
   m.length = length;
@@ -2873,6 +2906,7 @@ extern "C" int tw_twilight_select_fused_phase(const float* q, const void* page_m
                                               const int32_t* lengths, int length, int32_t* sel_pages, float* logits,
                                               int32_t* desired, uint32_t* union_rec, int64_t rec_stride,
                                               void* workspace, size_t workspace_bytes, int phase, void* stream) {
+  if (phase != 1 && phase != 3) return TW_EINVAL;
   return tw::select_fused(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, packed, qscale, qmin,
                           quant_entry_stride, quant_rows, b0_pages, top_p, qk_scale, sink, recent, block_size,
                           lengths, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
@@ -2893,4 +2927,20 @@ extern "C" int tw_twilight_select_fused_matched(const float* q, const void* page
                           quant_entry_stride, quant_rows, b0_pages, top_p, qk_scale, sink, recent, block_size,
                           lengths, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
                           workspace_bytes, true, target_total, matched_fraction, allocated, stream);
+}
+
+extern "C" int tw_twilight_select_fused_matched_part(
+    const float* q, const void* page_min, const void* page_max, int dtype, int G, int R, int P, int D,
+    int64_t page_group_stride, const uint8_t* packed, const void* qscale, const void* qmin,
+    int64_t quant_entry_stride, int64_t quant_rows, int b0_pages, float top_p, float qk_scale, int sink, int recent,
+    int block_size, const int32_t* lengths, int length, int target_total, double matched_fraction,
+    int32_t* sel_pages, float* logits, int32_t* desired, int32_t* allocated, uint32_t* union_rec, int64_t rec_stride,
+    int part, const int32_t* desired_all, int heads_all, int head0, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  if ((part != 1 && part != 2) || desired_all == nullptr) return TW_EINVAL;
+  return tw::select_fused(q, page_min, page_max, dtype, G, R, P, D, page_group_stride, packed, qscale, qmin,
+                          quant_entry_stride, quant_rows, b0_pages, top_p, qk_scale, sink, recent, block_size,
+                          lengths, length, sel_pages, logits, desired, union_rec, rec_stride, workspace,
+                          workspace_bytes, true, target_total, matched_fraction, allocated, stream,
+                          part == 1 ? 2 : 4, desired_all, heads_all, head0);
 }

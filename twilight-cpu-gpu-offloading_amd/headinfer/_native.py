@@ -97,6 +97,9 @@ _HIP_SIGNATURES = {
     "tw_twilight_select_fused_matched": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64, i32,
                                                f32, f32, i32, i32, i32, vp, i32, i32, f64, vp, vp, vp, vp, vp, i64,
                                                vp, szt, vp]),
+    "tw_twilight_select_fused_matched_part": (i32, [vp, vp, vp, i32, i32, i32, i32, i32, i64, vp, vp, vp, i64, i64,
+                                                    i32, f32, f32, i32, i32, i32, vp, i32, i32, f64, vp, vp, vp, vp,
+                                                    vp, i64, i32, vp, i32, i32, vp, szt, vp]),
     "tw_decode_attention_union": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32, i64, i32, i32, i32, vp,
                                         i32, i32, vp, vp, f32, vp, vp, i64, i32, vp, vp, vp, i64, vp, vp, szt, i32,
                                         vp]),

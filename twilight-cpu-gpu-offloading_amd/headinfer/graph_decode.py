@@ -91,12 +91,12 @@ class GraphDecoder:
         self.layers = list(inner.layers)
         if cache.block_size != 16 or self.D != 128 or cache.dtype not in (torch.float16, torch.bfloat16):
             raise ValueError("GraphDecoder needs 16-row pages, head_dim 128 and a 16-bit cache")
-        if self.R > 8 and not (self.twilight and cache.budget_mode == "dynamic"):
+        if self.R > 8 and not (self.twilight and (cache.budget_mode == "dynamic" or self.R <= 64)):
             # the Twilight fused selection and union attention run wider groups
-            # as sub-groups of 8 under dynamic budgets; the Quest page-tile and
-            # matched-budget launches take at most 8 heads a group
+            # as sub-groups of 8 (matched budgets: up to 64 heads sharing one
+            # allocation); the Quest page-tile launches take at most 8 heads a group
             raise ValueError("GraphDecoder takes at most 8 query heads per KV head, except over a Twilight cache "
-                             "with dynamic budgets")
+                             "(dynamic budgets, or matched budgets up to 64 heads)")
         if cache.geometry.num_entries != len(self.layers) * self.G:
             raise ValueError("cache entries do not match the model's layers x KV heads")
         lengths = set(cache._logical_lengths)
@@ -200,14 +200,15 @@ class GraphDecoder:
             self.tw_prows = torch.zeros((self.G, self.width), dtype=torch.int32, device=dev)
             # the fused selection (score + INT4 QK; B0 + top-p per head) into a
             # union record per KV group, read by the union attention; more
-            # than 8 query heads per KV head as sub-groups (dynamic budgets)
+            # than 8 query heads per KV head as sub-groups (matched budgets:
+            # up to 64 heads, one allocation over all of them)
             self.fused = (cache.block_size == 16 and self.D == 128 and cache.dtype in (torch.float16, torch.bfloat16)
-                          and (self.R <= 8 or cache.budget_mode == "dynamic") and self.P <= 8192
+                          and (self.R <= 64 or cache.budget_mode == "dynamic") and self.P <= 8192
                           and n_cand <= 8192)
             if cache.budget_mode == "matched":
                 if not self.fused:
                     raise ValueError("GraphDecoder runs matched Twilight budgets through the fused selection "
-                                     "(16-row pages, head_dim 128, 16-bit K/V, R <= 8, <= 8192 candidate pages)")
+                                     "(16-row pages, head_dim 128, 16-bit K/V, R <= 64, <= 8192 candidate pages)")
                 # the matched target grows with the length while B0 stops at k
                 # pages: past that the reference's allocation raises, so refuse
                 # a decode that would reach it

@@ -868,7 +868,9 @@ def twilight_select_fused(
     (the cache's fixed pages x 16 x R).  Returns desired [G, R] int32 (the
     top-p counts); sel_pages [G, R, b0_pages], logits [G, R, b0_pages * 16]
     and (matched) allocated [G, R] are optional outputs.  phase 1 runs the
-    first launch alone (for timing it; the outputs are left as they were)."""
+    first launch alone (for timing it; the outputs are left as they were).
+    More than 8 query heads per KV head run as sub-groups of at most 8; with
+    matched budgets (at most 64 heads) they share one allocation over all R."""
     if phase not in (1, 3):
         raise ValueError("phase must be 1 (score + INT4 QK launch) or 3 (the selection)")
     if budget_mode not in ("dynamic", "matched"):
@@ -891,42 +893,6 @@ def twilight_select_fused(
                           logits, allocated, what="twilight_select_fused")
     if desired is None:
         desired = torch.empty((G, R), dtype=torch.int32, device=dev)
-    if R > 8:
-        # Sub-groups of at most 8 query heads: a dynamic budget is each head's
-        # own, so the group's kept rows are the union of the sub-groups' --
-        # the first writes the record, the others their own records ORed into
-        # it.  Matched budgets allocate over every head of the group at once.
-        if matched:
-            raise ValueError("matched budgets over the fused selection take at most 8 query heads per KV head")
-        if phase != 3:
-            raise ValueError("phase 1 takes at most 8 query heads per KV head")
-        for t, dt, shape in ((desired, torch.int32, (G, R)), (sel_pages, torch.int32, (G, R, b0_pages)),
-                             (logits, torch.float32, (G, R, b0_pages * block_size))):
-            if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
-                raise ValueError("twilight_select_fused output has the wrong dtype/shape")
-        other = None
-        for i, (r0, r1) in enumerate(head_chunks(R)):
-            Rc = r1 - r0
-            rec = union_rec
-            if i > 0:
-                if other is None:
-                    other = torch.empty((G, union_rec.stride(0)), dtype=torch.int32, device=dev)
-                rec = other[:, :union_rec.shape[1]]
-            d = torch.empty((G, Rc), dtype=torch.int32, device=dev)
-            sp = None if sel_pages is None else torch.empty((G, Rc, b0_pages), dtype=torch.int32, device=dev)
-            lg = None if logits is None else torch.empty((G, Rc, b0_pages * block_size), dtype=torch.float32,
-                                                          device=dev)
-            twilight_select_fused(q[:, r0:r1].contiguous(), page_min, page_max, packed, scale, minimum, b0_pages,
-                                  rec, top_p=top_p, sink=sink, recent=recent, block_size=block_size, length=length,
-                                  lengths=lengths, qk_scale=qk_scale, desired=d, sel_pages=sp, logits=lg)
-            if i > 0:
-                union_rec.bitwise_or_(rec)
-            desired[:, r0:r1] = d
-            if sp is not None:
-                sel_pages[:, r0:r1] = sp
-            if lg is not None:
-                logits[:, r0:r1] = lg
-        return desired
     if matched:
         if lengths is not None:
             if not 0.0 < matched_fraction <= 1.0:
@@ -954,6 +920,13 @@ def twilight_select_fused(
                          (logits, torch.float32, (G, R, b0_pages * block_size)), (allocated, torch.int32, (G, R))):
         if t is not None and (t.dtype != dt or tuple(t.shape) != shape or not t.is_contiguous()):
             raise ValueError("twilight_select_fused output has the wrong dtype/shape")
+    if R > 8:
+        return _twilight_select_fused_wide(q, page_min, page_max, packed, scale, minimum, b0_pages, union_rec,
+                                           top_p=top_p, sink=sink, recent=recent, block_size=block_size,
+                                           length=length, lengths=lengths, qk_scale=qk_scale, desired=desired,
+                                           sel_pages=sel_pages, logits=logits, budget_mode=budget_mode,
+                                           target_total=target_total, allocated=allocated,
+                                           matched_fraction=matched_fraction, phase=phase, dev=dev, qe=qe)
     qs = _default_qk_scale(D) if qk_scale is None else float(qk_scale)
     nbytes = hip().tw_twilight_select_fused_workspace_size(G, R, P, int(b0_pages))
     ws = WORKSPACE.get(dev, "twilight_fused", nbytes)
@@ -979,6 +952,93 @@ def twilight_select_fused(
                                                  block_size, ptr(lengths), int(length), ptr(sel_pages), ptr(logits),
                                                  ptr(desired), ptr(union_rec), union_rec.stride(0), ptr(ws),
                                                  ws.numel(), stream_handle(dev)), "twilight_select_fused")
+    return desired
+
+
+def _twilight_select_fused_wide(q, page_min, page_max, packed, scale, minimum, b0_pages, union_rec, *, top_p, sink,
+                                recent, block_size, length, lengths, qk_scale, desired, sel_pages, logits,
+                                budget_mode, target_total, allocated, matched_fraction, phase, dev, qe):
+    """twilight_select_fused for more than 8 query heads per KV head, as
+    sub-groups of at most 8 (the outputs checked by the caller).  Dynamic
+    budgets are each head's own, so the group's kept rows are the union of
+    the sub-groups': the first sub-group writes union_rec, the others their
+    own records ORed into it.  Matched budgets allocate over every head of the
+    group: each sub-group's score + QK and head launches first (its top-p
+    counts into its columns of desired), then each sub-group's allocation +
+    top-allocated launch reads all of desired (tw_twilight_select_fused_matched_part)."""
+    G, R, D = q.shape
+    P = page_min.shape[1]
+    matched = budget_mode == "matched"
+    if phase != 3:
+        raise ValueError("phase 1 takes at most 8 query heads per KV head")
+    if matched and R > 64:
+        raise ValueError("matched budgets over the fused selection take at most 64 query heads per KV head")
+    chunks = head_chunks(R)
+    extra = None
+    if len(chunks) > 1:
+        n_extra = len(chunks) - 1 if matched else 1
+        extra = torch.empty((n_extra, G, union_rec.stride(0)), dtype=torch.int32, device=dev)
+
+    def record(i):
+        if i == 0:
+            return union_rec
+        return extra[i - 1 if matched else 0, :, :union_rec.shape[1]]
+
+    if not matched:
+        for i, (r0, r1) in enumerate(chunks):
+            Rc = r1 - r0
+            rec = record(i)
+            d = torch.empty((G, Rc), dtype=torch.int32, device=dev)
+            sp = None if sel_pages is None else torch.empty((G, Rc, b0_pages), dtype=torch.int32, device=dev)
+            lg = None if logits is None else torch.empty((G, Rc, b0_pages * block_size), dtype=torch.float32,
+                                                          device=dev)
+            twilight_select_fused(q[:, r0:r1].contiguous(), page_min, page_max, packed, scale, minimum, b0_pages,
+                                  rec, top_p=top_p, sink=sink, recent=recent, block_size=block_size, length=length,
+                                  lengths=lengths, qk_scale=qk_scale, desired=d, sel_pages=sp, logits=lg)
+            if i > 0:
+                union_rec.bitwise_or_(rec)
+            desired[:, r0:r1] = d
+            if sp is not None:
+                sel_pages[:, r0:r1] = sp
+            if lg is not None:
+                logits[:, r0:r1] = lg
+        return desired
+    qs = _default_qk_scale(D) if qk_scale is None else float(qk_scale)
+    subs = []
+    with on_device(dev):
+        for part in (1, 2):
+            for i, (r0, r1) in enumerate(chunks):
+                Rc = r1 - r0
+                if part == 1:
+                    nbytes = hip().tw_twilight_select_fused_workspace_size(G, Rc, P, int(b0_pages))
+                    subs.append(dict(
+                        q=q[:, r0:r1].contiguous(), ws=WORKSPACE.get(dev, f"twilight_fused_sub{i}", nbytes),
+                        d=torch.empty((G, Rc), dtype=torch.int32, device=dev),
+                        sp=torch.empty((G, Rc, b0_pages), dtype=torch.int32, device=dev),
+                        lg=None if logits is None else torch.empty((G, Rc, b0_pages * block_size),
+                                                                   dtype=torch.float32, device=dev),
+                        al=None if allocated is None else torch.empty((G, Rc), dtype=torch.int32, device=dev)))
+                t = subs[i]
+                rec = record(i)
+                check(hip().tw_twilight_select_fused_matched_part(
+                    ptr(t["q"]), ptr(page_min), ptr(page_max), _dt(page_min), G, Rc, P, D, page_min.stride(0),
+                    ptr(packed), ptr(scale), ptr(minimum), qe, packed.shape[1], int(b0_pages), float(top_p), qs,
+                    sink, recent, block_size, ptr(lengths), int(length), int(target_total), float(matched_fraction),
+                    ptr(t["sp"]), ptr(t["lg"]), ptr(t["d"]), ptr(t["al"]), ptr(rec), union_rec.stride(0), part,
+                    ptr(desired), R, r0, ptr(t["ws"]), t["ws"].numel(), stream_handle(dev)),
+                    "twilight_select_fused_matched_part")
+                if part == 1:
+                    desired[:, r0:r1] = t["d"]
+    for i, (r0, r1) in enumerate(chunks):
+        t = subs[i]
+        if i > 0:
+            union_rec.bitwise_or_(record(i))
+        if sel_pages is not None:
+            sel_pages[:, r0:r1] = t["sp"]
+        if logits is not None:
+            logits[:, r0:r1] = t["lg"]
+        if allocated is not None:
+            allocated[:, r0:r1] = t["al"]
     return desired
 
 

@@ -708,13 +708,14 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         counts, then the group's allocation and each head's top-allocated
         rows in one more launch), and the attention over the record's kept
         rows (the same token set as the union row list).  More than 8 query
-        heads per KV head run as sub-groups with dynamic budgets.  None when
-        the layer takes the general path: other shapes, matched budgets over
-        more than 8 heads, or traces that record the row list."""
+        heads per KV head run as sub-groups (with matched budgets, up to 64
+        heads sharing one allocation).  None when the layer takes the general
+        path: other shapes, matched budgets over more than 64 heads, or traces
+        that record the row list."""
         G, R, D = queries.shape
-        # more than 8 query heads per KV head run as sub-groups, which dynamic
-        # budgets (each head's own) allow; matched budgets allocate over all R
-        if (not self.fused_decode or (R > 8 and self.budget_mode == "matched") or D != 128 or self.block_size != 16
+        # more than 8 query heads per KV head run as sub-groups; one wavefront
+        # forms a matched allocation, a lane a head
+        if (not self.fused_decode or (R > 64 and self.budget_mode == "matched") or D != 128 or self.block_size != 16
                 or self.dtype not in (torch.float16, torch.bfloat16) or self._capture_selection_trace
                 or self._capture_budget_trace or self._page_min is None or self._packed is None):
             return None
