@@ -336,7 +336,7 @@ def matched_budget_counts(desired, target_total, capacities):
 def twilight_layer(q: np.ndarray, page_min: np.ndarray, page_max: np.ndarray, packed: np.ndarray,
                    scale: np.ndarray, minimum: np.ndarray, dtype: str, *, length: int, sink: int, recent: int,
                    block_size: int, b0_pages: int, top_p: float, budget_mode: str = "dynamic",
-                   fixed_pages: int = 0, qk_scale: float | None = None):
+                   fixed_pages: int = 0, qk_scale: float | None = None, target_total: int | None = None):
     """Twilight selection of one KV group (prepare_layer_selection,
     twilight_offload_cache.py:996-1614) in this build's defined orders.
 
@@ -358,7 +358,8 @@ def twilight_layer(q: np.ndarray, page_min: np.ndarray, page_max: np.ndarray, pa
     if budget_mode == "dynamic":
         allocated = desired.copy()
     else:
-        target = fixed_pages * block_size * R
+        # the cache's target (fixed pages x page size x R) unless one is given
+        target = fixed_pages * block_size * R if target_total is None else int(target_total)
         allocated = np.array(matched_budget_counts(list(map(int, desired)), target, [N] * R))
     selected = []
     for r in range(R):

@@ -433,16 +433,18 @@ def test_fused_selection_wide_group(K, dev, R):
     assert torch.equal(k[:, L].view(torch.int16), cur_k.view(torch.int16))
 
 
-@pytest.mark.parametrize("R,ragged", [(12, False), (16, False), (40, False), (12, True)])
-def test_fused_matched_wide_group(K, dev, R, ragged):
+@pytest.mark.parametrize("R,ragged,target", [(12, False, "fixed"), (16, False, "fixed"), (40, False, "fixed"),
+                                             (12, True, "fixed"), (12, False, "capacity"), (16, False, "tiny")])
+def test_fused_matched_wide_group(K, dev, R, ragged, target):
     """Matched budgets over more than 8 query heads per KV head: the
     sub-groups' score + QK and head launches, then each sub-group's
     allocation + top-allocated launch over all R heads' counts.  B0 pages,
     logits, counts, the allocation (largest remainder over all R heads,
     summing to the group's target) and the ORed record against
     oracle.twilight_layer over all R heads; with device lengths each group's
-    target from its own length (one group below the first whole page).  More
-    than 64 heads are refused."""
+    target from its own length (one group below the first whole page).  The
+    targets also reach every candidate (heads filled to capacity) and R + 1
+    (one head above one).  More than 64 heads are refused."""
     lengths = [300, 5000, 9000] if ragged else [6000, 6000]
     G, b0, top_p, frac = len(lengths), 64, 0.9, 0.05
     L = max(lengths)
@@ -468,8 +470,9 @@ def test_fused_matched_wide_group(K, dev, R, ragged):
         kw.update(length=L, lengths=lens, matched_fraction=frac)
     else:
         lens = None
-        kw.update(length=L, target_total=fixed_one * bs * R)
-    _say(f"[fused matched wide] G={G} R={R} lengths={lengths} b0={b0}")
+        total = {"fixed": fixed_one * bs * R, "capacity": b0 * bs * R, "tiny": R + 1}[target]
+        kw.update(length=L, target_total=total)
+    _say(f"[fused matched wide] G={G} R={R} lengths={lengths} b0={b0} target={target}")
     K.twilight_select_fused(qf, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec, **kw)
     k, v = st.k.clone(), st.v.clone()
     akw = dict(lengths=lens, length=L) if ragged else dict(length=L)
@@ -493,14 +496,15 @@ def test_fused_matched_wide_group(K, dev, R, ragged):
                                         to_bits(st.pmax[gi, :cand]), st.packed[gi].cpu().numpy(),
                                         to_bits(st.qscale[gi]), to_bits(st.qmin[gi]), "bf16", length=Lg, sink=sink,
                                         recent=recent, block_size=bs, b0_pages=b0g, top_p=top_p,
-                                        budget_mode="matched", fixed_pages=fixed)
+                                        budget_mode="matched", fixed_pages=fixed,
+                                        target_total=None if ragged else total)
             Ng = b0g * bs
             assert np.array_equal(sel_h[gi, :, :b0g], ref["pages"]), gi
             assert np.array_equal(log_h[gi, :, :Ng].view(np.uint32),
                                   ref["logits"].astype(np.float32).view(np.uint32)), gi
             assert np.array_equal(des_h[gi], ref["desired"]), (gi, des_h[gi], ref["desired"])
             assert np.array_equal(all_h[gi], ref["allocated"]), (gi, all_h[gi], ref["allocated"])
-            assert all_h[gi].sum() == fixed * bs * R, gi
+            assert all_h[gi].sum() == (fixed * bs * R if ragged else total), gi
             want = _record_of(np.unique(np.concatenate(ref["selected"])), P, sink, bs)
             assert np.array_equal(masks, want) and np.array_equal(bits[:P], want != 0) and not bits[P:].any(), gi
             kept = ref["union"].astype(np.int64)
