@@ -83,3 +83,21 @@ def test_constructors_require_a_rocm_device():
         TwilightMatchedBudgetOffloadedCache(**kw)
     with pytest.raises(ValueError):
         TwilightMatchedBudgetOffloadedCache(top_p=1.5, **kw)
+
+
+@pytest.mark.parametrize("sink,recent,ring", [(64, 256, 256), (64, 257, 512), (0, 1, 1), (16, 0, 1), (4, 100, 128)])
+def test_resident_window_sizes(sink, recent, ring):
+    """The resident windows hold the sink rows and a ring of the smallest
+    power of two >= recent rows (the recent window's recent - 1 history rows
+    plus the decode row), state zeroed; a view slices every buffer by group."""
+    from headinfer.kernels import ResidentPages
+
+    res = ResidentPages(6, 4, 10, 128, torch.bfloat16, torch.device("cpu"), sink=sink, recent=recent)
+    assert res.ring == ring and res.sink == sink
+    assert tuple(res.win_k.shape) == (6, sink + ring, 128) and res.win_v.shape == res.win_k.shape
+    assert res.win_state.dtype == torch.int32 and not res.win_state.any()
+    v = res.view(2, 3)
+    assert tuple(v.win_k.shape) == (3, sink + ring, 128) and v.win_k.is_contiguous()
+    assert v.win_state.data_ptr() == res.win_state[2].data_ptr() and v.ring == ring
+    plain = ResidentPages(6, 4, 10, 128, torch.bfloat16, torch.device("cpu"))
+    assert plain.win_k is None and plain.view(0, 2).win_state is None
