@@ -327,8 +327,8 @@ def test_resident_page_cache_bit_exact(K, dev, ragged):
     assert union > 0 and 0 < hits < union, (hits, union)
 
 
-@pytest.mark.parametrize("ragged", [True, False])
-def test_resident_windows_serve_sink_and_recent(K, dev, ragged):
+@pytest.mark.parametrize("ragged,recent", [(True, RECENT), (False, RECENT), (True, 100)])
+def test_resident_windows_serve_sink_and_recent(K, dev, ragged, recent):
     """Resident sink/recent windows: after each step the host slab's copies of
     the next step's sink and recent rows are overwritten with noise, and the
     next step still equals the plain launch over the intact slab bit for bit
@@ -336,8 +336,9 @@ def test_resident_windows_serve_sink_and_recent(K, dev, ragged):
     their slots and the state names the next length.  At step 4 the window
     buffers are overwritten with noise and the state cleared instead: that
     launch reads the slab and stores the windows again.  One ragged group
-    starts below the sink size and crosses it."""
-    _say(f"[resident windows] ragged={ragged}")
+    starts below the sink size and crosses it; a recent window of 100 rows
+    takes a ring of 128."""
+    _say(f"[resident windows] ragged={ragged} recent={recent}")
     dtype, R, k, steps = "bf16", 4, 16, 7
     lengths0 = [3000, 3000, 3000] if not ragged else [60, 2500, 3100, 4000]
     G = len(lengths0)
@@ -349,9 +350,9 @@ def test_resident_windows_serve_sink_and_recent(K, dev, ragged):
     pmin, pmax = _metadata(keys, lengths0, dtype, dev)
     P = pmin.shape[1]
     width = min(P, R * k)
-    res = K.ResidentPages(G, width, P, D, keys.dtype, dev, sink=SINK, recent=RECENT)
+    res = K.ResidentPages(G, width, P, D, keys.dtype, dev, sink=SINK, recent=recent)
     ring = res.ring
-    assert ring == 256 and tuple(res.win_k.shape) == (G, SINK + ring, D)
+    assert ring == (256 if recent == 256 else 128) and tuple(res.win_k.shape) == (G, SINK + ring, D)
     lengths = torch.tensor(lengths0, dtype=torch.int32, device=dev)
     g = torch.Generator().manual_seed(123)
     noise = torch.Generator().manual_seed(124)
@@ -369,7 +370,7 @@ def test_resident_windows_serve_sink_and_recent(K, dev, ragged):
                 if L - 1 >= SINK:   # the previous launch stored the whole sink
                     kh[gi, :SINK] = torch.randn((SINK, D), generator=noise).to(kh.dtype)
                     vh[gi, :SINK] = torch.randn((SINK, D), generator=noise).to(vh.dtype)
-                r0 = oracle.selection_window(L, SINK, RECENT)[1]   # recent - 1 history rows
+                r0 = oracle.selection_window(L, SINK, recent)[1]   # recent - 1 history rows
                 if r0 < L:
                     kh[gi, r0:L] = torch.randn((L - r0, D), generator=noise).to(kh.dtype)
                     vh[gi, r0:L] = torch.randn((L - r0, D), generator=noise).to(vh.dtype)
@@ -378,9 +379,9 @@ def test_resident_windows_serve_sink_and_recent(K, dev, ragged):
         pp = torch.zeros((G, width), dtype=torch.int32, device=dev)
         pm = torch.zeros((G, width), dtype=torch.uint8, device=dev)
         pc = torch.zeros((G,), dtype=torch.int32, device=dev)
-        K.quest_select_ragged(q.float().to(dev), pmin, pmax, lengths, k, sink=SINK, recent=RECENT, block_size=BS,
+        K.quest_select_ragged(q.float().to(dev), pmin, pmax, lengths, k, sink=SINK, recent=recent, block_size=BS,
                               plan_pages=pp, plan_masks=pm, plan_counts=pc)
-        kw = dict(plan_masks=pm, max_pages=width, sink=SINK, recent=RECENT, block_size=BS, append=True,
+        kw = dict(plan_masks=pm, max_pages=width, sink=SINK, recent=recent, block_size=BS, append=True,
                   cur_k=ck.to(dev), cur_v=cv.to(dev))
         if ragged:
             a = K.decode_attention_pages_resident(q.to(dev), kh, vh, pp, pc, res, lengths=lengths, **kw)
@@ -389,7 +390,7 @@ def test_resident_windows_serve_sink_and_recent(K, dev, ragged):
             L = Ls[0]
             a = K.decode_attention_pages_resident(q.to(dev), kh, vh, pp, pc, res, length=L, **kw)
             b = K.decode_attention_pages(q.to(dev), kh2, vh2, pp, pc, plan_masks=pm, max_pages=width, sink=SINK,
-                                         recent=RECENT, block_size=BS, length=L, append_position=L,
+                                         recent=recent, block_size=BS, length=L, append_position=L,
                                          cur_k=ck.to(dev), cur_v=cv.to(dev))
         torch.cuda.synchronize()
         assert same_bits(a, b), step
@@ -401,14 +402,14 @@ def test_resident_windows_serve_sink_and_recent(K, dev, ragged):
             if se == SINK:
                 assert same_bits(res.win_k[gi, :SINK], kh2[gi, :SINK]), (step, gi)
                 assert same_bits(res.win_v[gi, :SINK], vh2[gi, :SINK]), (step, gi)
-            rows = torch.arange(oracle.selection_window(L, SINK, RECENT)[1], L + 1)
+            rows = torch.arange(oracle.selection_window(L, SINK, recent)[1], L + 1)
             slots = SINK + (rows & (ring - 1))
             assert same_bits(res.win_k[gi, slots.to(dev)], kh2[gi, rows]), (step, gi)
             assert same_bits(res.win_v[gi, slots.to(dev)], vh2[gi, rows]), (step, gi)
         lengths += 1
     with pytest.raises(ValueError):
         K.decode_attention_pages_resident(q.to(dev), kh, vh, pp, pc, res, lengths=lengths,
-                                          **dict(kw, recent=RECENT * 2))
+                                          **dict(kw, recent=ring + 1))
 
 
 @pytest.mark.parametrize("resident", [False, True])
