@@ -588,6 +588,32 @@ int tw_decode_attention_union(const void* q, const void* k_base, const void* v_b
                               void* page_min, void* page_max, int64_t page_entry_stride, int meta_pages,
                               uint8_t* packed, void* qscale, void* qmin, int64_t quant_entry_stride, void* out,
                               void* workspace, size_t workspace_bytes, int phase, void* stream);
+/* tw_decode_attention_union with the previous-token resident cache of the
+ * Twilight cache (previous_token_resident_cache, twilight_offload_cache.py:
+ * 2457-2608, 3323-3470; hit/miss mapping resident_gpu_mapping.py:14-144),
+ * for slabs in host memory: the reference keeps the previous token's union
+ * rows on the GPU and reads only the new rows from the host.  Here every
+ * group keeps the rows of its last union in res_k/res_v [G][2][res_slots][16]
+ * [D] (16-bit, HBM; two buffers alternating with the length's parity, a page
+ * a slot at its union index, res_slots <= 65535), and res_map [G]
+ * [res_map_pages] (int64, initialised to -1) = (length << 32) | (the page's
+ * kept rows << 16) | slot: a kept row that the previous step kept too is
+ * read from HBM, every other kept row from the slab, and every union page
+ * read is stored for the next step.  res_stats [G][2] (nullable) accumulates
+ * (hit rows, union rows).  The resident sink and recent windows (res_win_k,
+ * res_win_v, res_win_state, ring_rows) as tw_decode_attention_pages_
+ * resident.  Other arguments as tw_decode_attention_union. */
+int tw_decode_attention_union_resident(const void* q, const void* k_base, const void* v_base, int dtype, int G,
+                                       int R, int D, const uint32_t* union_rec, int64_t rec_stride, int P,
+                                       int max_rows, int64_t entry_stride_rows, int sink, int recent,
+                                       int block_size, const int32_t* lengths, int length, int append,
+                                       const void* cur_k, const void* cur_v, float softmax_scale, void* res_k,
+                                       void* res_v, int64_t* res_map, int res_slots, int res_map_pages,
+                                       unsigned long long* res_stats, void* res_win_k, void* res_win_v,
+                                       int32_t* res_win_state, int ring_rows, void* page_min, void* page_max,
+                                       int64_t page_entry_stride, int meta_pages, uint8_t* packed, void* qscale,
+                                       void* qmin, int64_t quant_entry_stride, void* out, void* workspace,
+                                       size_t workspace_bytes, int phase, void* stream);
 /* The Twilight union attention over page rows: the page-tile attention of
  * tw_decode_attention_pages(_ragged) where plan_pages / plan_counts are the
  * B0 union (tw_quest_select with k = b0_pages) and page_rows[g*plan_stride +

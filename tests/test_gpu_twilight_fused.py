@@ -519,3 +519,78 @@ def test_fused_matched_wide_group(K, dev, R, ragged, target):
             K.twilight_select_fused(q65, st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec,
                                     top_p=top_p, sink=sink, recent=recent, block_size=bs, length=L,
                                     budget_mode="matched", target_total=65 * bs)
+
+
+@pytest.mark.parametrize("lengths0", [[5000, 5000, 5000], [3000, 5000, 9000]])
+def test_union_attention_resident_cache(K, dev, lengths0):
+    """The union-record attention over a host slab with the row-granular
+    resident cache (and its sink/recent windows) == the same launch over an
+    intact slab without it, bit for bit, over 6 decode steps with drifting
+    queries (the fused selection rerun every step from device lengths),
+    although before each step the resident run's slab copies of the rows the
+    previous step kept are overwritten with noise: a row kept again is read
+    from HBM.  At every step the buffer of the step's parity holds the slab's
+    kept rows at their union slots; kept rows the previous step also kept are
+    counted as hits, and some are."""
+    from helpers import same_bits
+
+    G, R, b0, steps, top_p = len(lengths0), 4, 64, 6, 0.9
+    Lmax = max(lengths0) + steps + 8
+    st = _Setup(K, dev, G, R, Lmax, lengths0, seed=71)
+    D, bs, sink, recent, P = st.D, st.bs, st.sink, st.recent, st.P
+    kh, vh = st.k.cpu().pin_memory(), st.v.cpu().pin_memory()        # resident run
+    kh2, vh2 = st.k.cpu().pin_memory(), st.v.cpu().pin_memory()      # plain run
+    width = min(P, R * b0)
+    res = K.ResidentPages(G, width, P, D, torch.bfloat16, dev, sink=sink, recent=recent)
+    lens = torch.tensor(lengths0, dtype=torch.int32, device=dev)
+    words = K.union_record_words(P)
+    rec = torch.zeros((G, (words + 3) & ~3), dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(72)
+    noise = torch.Generator().manual_seed(73)
+    base = torch.randn((G, R, D), generator=gen, device=dev) * 2
+    prev_kept = [None] * G
+    _say(f"[union resident] lengths={lengths0}")
+    for step in range(steps):
+        Ls = [L0 + step for L0 in lengths0]
+        # the resident run's slab copies of the rows the previous step kept
+        # turn to noise: a row kept again must come from HBM
+        kh.copy_(kh2)
+        vh.copy_(vh2)
+        for gi in range(G):
+            if prev_kept[gi] is not None and len(prev_kept[gi]):
+                n = len(prev_kept[gi])
+                kh[gi, prev_kept[gi]] = torch.randn((n, D), generator=noise).to(kh.dtype)
+                vh[gi, prev_kept[gi]] = torch.randn((n, D), generator=noise).to(vh.dtype)
+        q = (base + 0.3 * torch.randn((G, R, D), generator=gen, device=dev)).to(torch.bfloat16)
+        cur_k = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+        cur_v = torch.randn((G, D), generator=gen, device=dev).to(torch.bfloat16)
+        K.twilight_select_fused(q.float(), st.pmin[:, :P], st.pmax[:, :P], st.packed, st.qscale, st.qmin, b0, rec,
+                                top_p=top_p, sink=sink, recent=recent, block_size=bs, length=Lmax - 8,
+                                lengths=lens)
+        kw = dict(max_pages=width, sink=sink, recent=recent, block_size=bs, lengths=lens, length=Lmax - 8,
+                  append=True, cur_k=cur_k, cur_v=cur_v)
+        a = K.decode_attention_union(q, kh, vh, rec, P, resident=res, **kw)
+        b = K.decode_attention_union(q, kh2, vh2, rec, P, **kw)
+        torch.cuda.synchronize()
+        assert same_bits(a, b), step
+        rec_h = rec.cpu().numpy()
+        for gi, L in enumerate(Ls):
+            assert same_bits(kh[gi, L], kh2[gi, L]) and same_bits(vh[gi, L], vh2[gi, L]), (step, gi)  # the append
+            bits, masks = _decode_record(rec_h[gi], P)
+            pages = np.flatnonzero(bits[:P])
+            par = L & 1
+            kept = []
+            for u, p in enumerate(pages[:width]):
+                rows = [r for r in range(bs) if (masks[p] >> r) & 1]
+                pos = torch.tensor([sink + int(p) * bs + r for r in rows])
+                kept.append(pos)
+                assert same_bits(res.k[gi, par, u, rows], kh2[gi, pos]), (step, gi, u)
+                assert same_bits(res.v[gi, par, u, rows], vh2[gi, pos]), (step, gi, u)
+            prev_kept[gi] = torch.cat(kept) if kept else None
+        lens += 1
+    hits, union = res.stats.sum(dim=0).tolist()
+    _say(f"[union resident] hit rows {hits} of {union}")
+    assert union > 0 and 0 < hits < union, (hits, union)
+    with pytest.raises(ValueError, match="at most 8 query heads"):
+        K.decode_attention_union(torch.zeros((G, 12, D), dtype=torch.bfloat16, device=dev), kh, vh, rec, P,
+                                 resident=res, **kw)

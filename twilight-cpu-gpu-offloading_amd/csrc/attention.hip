@@ -98,6 +98,10 @@ struct AttnArgs {
   // buffers alternating with the length's parity), and res_map [G]
   // [res_map_pages] = (length << 32) | slot of the step that last stored
   // each page.  res_stats [G][2] accumulates (hit pages, union pages).
+  // Over a union record (Twilight) the cache is row-granular: res_map =
+  // (length << 32) | (the page's kept rows << 16) | slot, a kept row is read
+  // from HBM when the previous step kept it too, and res_stats counts rows
+  // (hit rows, union rows).
   void* res_k;
   void* res_v;
   int64_t* res_map;
@@ -1523,14 +1527,19 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
     // resident page cache: a page stored by the previous step (epoch
     // length - 1) is read from HBM instead of the slab
     int hit_slot[TW];
+    uint32_t hit_rows[TW];  // rows of the tile the previous step stored (row-granular over a record)
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
       ts[tt] = tile_src(a, win, t0 + tt, nu, page[tt], pmask[tt], prow[tt], MK || a.page_rows != nullptr);
       hit_slot[tt] = -1;
+      hit_rows[tt] = 0u;
       if (res && ts[tt].u >= 0 && ts[tt].page >= 0 && ts[tt].page < a.res_map_pages) {
         const int64_t m = a.res_map[static_cast<int64_t>(g) * a.res_map_pages + ts[tt].page];
-        const int slot = static_cast<int>(m & 0xffffffffll);
-        if ((m >> 32) == static_cast<int64_t>(win.length) - 1 && slot >= 0 && slot < a.res_slots) hit_slot[tt] = slot;
+        const int slot = static_cast<int>(MK ? (m & 0xffffll) : (m & 0xffffffffll));
+        if ((m >> 32) == static_cast<int64_t>(win.length) - 1 && slot >= 0 && slot < a.res_slots) {
+          hit_slot[tt] = slot;
+          hit_rows[tt] = MK ? static_cast<uint32_t>((m >> 16) & 0xffffll) : 0xffffu;
+        }
       }
     }
 #pragma unroll
@@ -1539,19 +1548,23 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
       // (wave-uniform) a sink tile or a recent tile served by the HBM windows
       const bool wsink = sink_ok && t0 + tt < win.sink_tiles;
       const bool wring = ring_ok && t0 + tt >= win.sink_tiles + nu;
-      const int64_t tb =
-          hit ? (res_prev + static_cast<int64_t>(hit_slot[tt]) * kTileRows) * D : ts[tt].pos0 * D + (wsink ? win_base : 0);
-      const S* kt = hit ? static_cast<const S*>(a.res_k) : (wsink || wring ? static_cast<const S*>(a.res_win_k) : kg);
-      const S* vt = hit ? static_cast<const S*>(a.res_v) : (wsink || wring ? static_cast<const S*>(a.res_win_v) : vg);
+      const int64_t tb_res = (res_prev + static_cast<int64_t>(hit ? hit_slot[tt] : 0) * kTileRows) * D;
+      const int64_t tb_src = ts[tt].pos0 * D + (wsink ? win_base : 0);
+      const S* ks = wsink || wring ? static_cast<const S*>(a.res_win_k) : kg;
+      const S* vs = wsink || wring ? static_cast<const S*>(a.res_win_v) : vg;
       // rows outside the tile or not kept read a kept row (the same lines,
       // no extra traffic) and are masked below
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * rg + j;
         const int vr = (r < ts[tt].cnt && ((ts[tt].rm >> r) & 1u)) ? r : ts[tt].r0;
+        // a row the previous step stored comes from this step's HBM copy
+        const bool rh = hit && ((hit_rows[tt] >> vr) & 1u);
         const int64_t ro =
             wring ? win_base + (a.sink + ((ts[tt].pos0 + vr) & ring_mask)) * static_cast<int64_t>(D) + c8
-                  : tb + static_cast<int64_t>(vr) * D + c8;
+                  : (rh ? tb_res : tb_src) + static_cast<int64_t>(vr) * D + c8;
+        const S* kt = rh ? static_cast<const S*>(a.res_k) : ks;
+        const S* vt = rh ? static_cast<const S*>(a.res_v) : vs;
         const S* vp = r == ts[tt].dec ? vdec + c8 : vt + ro;
         vf[tt][j] = NT ? load_stream(vp) : *reinterpret_cast<const uint4*>(vp);
         // key row r, channels c8..c8+7, until the LDS pass below
@@ -1721,12 +1734,21 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4*>(dv + (4 * rg + j) * D + c8) = vf[tt][j];
         if (lane == 0) {
+          // (over a record the rows the tile keeps are what this step stored)
+          const uint32_t kept = ts[tt].rm & 0xffffu;
           if (ts[tt].page >= 0 && ts[tt].page < a.res_map_pages)
             a.res_map[static_cast<int64_t>(g) * a.res_map_pages + ts[tt].page] =
-                (static_cast<int64_t>(win.length) << 32) | static_cast<int64_t>(ts[tt].u);
+                (static_cast<int64_t>(win.length) << 32) |
+                (MK ? (static_cast<int64_t>(kept) << 16) : 0ll) | static_cast<int64_t>(ts[tt].u);
           if (a.res_stats != nullptr) {
-            atomicAdd(a.res_stats + 2 * g + 1, 1ull);
-            if (hit_slot[tt] >= 0) atomicAdd(a.res_stats + 2 * g, 1ull);
+            if constexpr (MK) {
+              atomicAdd(a.res_stats + 2 * g + 1, static_cast<unsigned long long>(__popc(kept)));
+              if (hit_slot[tt] >= 0)
+                atomicAdd(a.res_stats + 2 * g, static_cast<unsigned long long>(__popc(kept & hit_rows[tt])));
+            } else {
+              atomicAdd(a.res_stats + 2 * g + 1, 1ull);
+              if (hit_slot[tt] >= 0) atomicAdd(a.res_stats + 2 * g, 1ull);
+            }
           }
         }
       }
@@ -1999,9 +2021,19 @@ int launch_tiles(const AttnArgs& a, hipStream_t stream) {
   if (phase & 1) {
     const dim3 grid(a.G * a.max_chunks);
     const dim3 block(kTileNW * kWave);
-    // the resident page cache serves slabs in host memory: plain loads (and
-    // takes a union plan)
-    if (a.res_map != nullptr) {
+    // the resident page cache serves slabs in host memory: plain loads, over
+    // a union plan (whole pages) or a union record (kept rows)
+    if (a.res_map != nullptr && a.union_rec) {
+      const bool one = a.bits_w64 <= kWave;
+      if (a.R <= 4 && one)
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, true, false, 1, true>), grid, block, 0, stream, a);
+      else if (a.R <= 4)
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, true, false, 2, true>), grid, block, 0, stream, a);
+      else if (one)
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, true, false, 1, true>), grid, block, 0, stream, a);
+      else
+        hipLaunchKernelGGL((decode_attn_tiles<DT, 8, kTileNW, kTileTW, true, false, 2, true>), grid, block, 0, stream, a);
+    } else if (a.res_map != nullptr) {
       if (a.R <= 4)
         hipLaunchKernelGGL((decode_attn_tiles<DT, 4, kTileNW, kTileTW, true, false, 0>), grid, block, 0, stream, a);
       else
@@ -2404,7 +2436,10 @@ int pages_tiles_launch(const void* q, const void* k_base, const void* v_base, in
   if (sel_bits != nullptr) {
     // selection bitmaps of bits_pages pages: at most 128 64-bit words a row
     // (two per lane), 8-byte aligned rows
-    if (bits_pages < 1 || bits_pages > 128 * 64 || page_rows != nullptr || res_map != nullptr) return TW_EINVAL;
+    // (the resident cache takes a union record, whose slots fit 16 bits)
+    if (bits_pages < 1 || bits_pages > 128 * 64 || page_rows != nullptr ||
+        (res_map != nullptr && (!union_rec || res_slots > 0xffff)))
+      return TW_EINVAL;
     if (bits_stride < 2 * ((bits_pages + 63) / 64) || (bits_stride % 2) != 0 ||
         (reinterpret_cast<uintptr_t>(sel_bits) % 8) != 0)
       return TW_EINVAL;
@@ -2614,4 +2649,21 @@ extern "C" int tw_decode_attention_union(const void* q, const void* k_base, cons
                                 softmax_scale, nullptr, nullptr, nullptr, 0, 0, nullptr, page_min, page_max,
                                 page_entry_stride, meta_pages, out, workspace, workspace_bytes, stream, nullptr,
                                 packed, qscale, qmin, quant_entry_stride, union_rec, rec_stride, P, phase, 1);
+}
+
+extern "C" int tw_decode_attention_union_resident(
+    const void* q, const void* k_base, const void* v_base, int dtype, int G, int R, int D, const uint32_t* union_rec,
+    int64_t rec_stride, int P, int max_rows, int64_t entry_stride_rows, int sink, int recent, int block_size,
+    const int32_t* lengths, int length, int append, const void* cur_k, const void* cur_v, float softmax_scale,
+    void* res_k, void* res_v, int64_t* res_map, int res_slots, int res_map_pages, unsigned long long* res_stats,
+    void* res_win_k, void* res_win_v, int32_t* res_win_state, int ring_rows, void* page_min, void* page_max,
+    int64_t page_entry_stride, int meta_pages, uint8_t* packed, void* qscale, void* qmin,
+    int64_t quant_entry_stride, void* out, void* workspace, size_t workspace_bytes, int phase, void* stream) {
+  if (union_rec == nullptr || res_map == nullptr) return TW_EINVAL;
+  return tw::pages_tiles_launch(q, k_base, v_base, dtype, G, R, D, nullptr, nullptr, nullptr, 0, max_rows,
+                                entry_stride_rows, sink, recent, block_size, lengths, length, append, cur_k, cur_v,
+                                softmax_scale, res_k, res_v, res_map, res_slots, res_map_pages, res_stats, page_min,
+                                page_max, page_entry_stride, meta_pages, out, workspace, workspace_bytes, stream,
+                                nullptr, packed, qscale, qmin, quant_entry_stride, union_rec, rec_stride, P, phase, 1,
+                                res_win_k, res_win_v, res_win_state, ring_rows);
 }

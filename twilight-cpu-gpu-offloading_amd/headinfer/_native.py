@@ -103,6 +103,10 @@ _HIP_SIGNATURES = {
     "tw_decode_attention_union": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32, i64, i32, i32, i32, vp,
                                         i32, i32, vp, vp, f32, vp, vp, i64, i32, vp, vp, vp, i64, vp, vp, szt, i32,
                                         vp]),
+    "tw_decode_attention_union_resident": (i32, [vp, vp, vp, i32, i32, i32, i32, vp, i64, i32, i32, i64, i32, i32,
+                                                 i32, vp, i32, i32, vp, vp, f32, vp, vp, vp, i32, i32, vp, vp, vp,
+                                                 vp, i32, vp, vp, i64, i32, vp, vp, vp, i64, vp, vp, szt, i32,
+                                                 vp]),
     "tw_int4_qk_positions": (i32, [vp, i32, i32, i32, vp, vp, vp, i32, i64, i64, vp, i32, f32, i32, vp, vp]),
     "tw_twilight_select_workspace_size": (szt, [i32, i32, i32]),
     "tw_twilight_max_candidates": (i32, []),

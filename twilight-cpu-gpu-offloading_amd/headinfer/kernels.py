@@ -1518,14 +1518,18 @@ def decode_attention_union(
     scale: Optional[torch.Tensor] = None,
     minimum: Optional[torch.Tensor] = None,
     phase: int = 3,
+    resident: Optional["ResidentPages"] = None,
 ) -> torch.Tensor:
     """The Twilight union attention from the union records of
     twilight_select_fused over P pages: every head attends the kept rows of
     the union pages, the sink and recent windows and the decode token.
     max_pages bounds a group's union pages (min(P, R * b0_pages)); the other
     arguments as decode_attention_page_rows.  More than 8 query heads per
-    group run as sub-groups of at most 8 over the same record.  Returns
-    [G, R, D]."""
+    group run as sub-groups of at most 8 over the same record.  resident
+    (R <= 8; a ResidentPages over this launch's groups, slots <= 65535): the
+    previous-token resident cache, row by row -- a kept row the previous
+    step kept too is read from HBM -- with its sink/recent windows, and its
+    stats counting (hit rows, union rows).  Returns [G, R, D]."""
     if phase not in (1, 2, 3):
         raise ValueError("phase must be 1, 2 or 3")
     if q.ndim != 3 or q.dtype not in (torch.float16, torch.bfloat16):
@@ -1559,7 +1563,15 @@ def decode_attention_union(
                                or minimum.stride() != scale.stride() or scale.dtype != q.dtype
                                or minimum.dtype != q.dtype or packed.stride(0) // (D // 2) != scale.stride(0)):
         raise ValueError("packed [G, T, D/2] uint8 and scale/minimum [G, T] must match (with cur_k and append)")
-    dev = _require_device(q, union_rec, lengths, cur_k, cur_v, page_min, page_max, packed, scale, minimum,
+    if resident is not None:
+        if R > 8:
+            raise ValueError("the resident cache takes at most 8 query heads per KV head")
+        if resident.slots > 0xffff:
+            raise ValueError("the resident cache over a union record takes at most 65535 slots")
+        _check_resident(resident, q, G, D, sink, recent)
+    res = () if resident is None else (resident.k, resident.v, resident.map, resident.stats, resident.win_k,
+                                       resident.win_v, resident.win_state)
+    dev = _require_device(q, union_rec, lengths, cur_k, cur_v, page_min, page_max, packed, scale, minimum, *res,
                           what="decode_attention_union")
     meta = _page_meta_args(page_min, page_max, G, D, append)
     kp, vp = _slab_source(k_cache, v_cache)
@@ -1584,12 +1596,23 @@ def decode_attention_union(
     nbytes = hip().tw_decode_attention_workspace_size(G, R, D, max_rows)
     ws = WORKSPACE.get(dev, "decode_attention", nbytes)
     with on_device(dev):
-        check(hip().tw_decode_attention_union(ptr(q), kp, vp, _dt(q), G, R, D, ptr(union_rec), union_rec.stride(0),
-                                              P, max_rows, k_cache.stride(0) // D, sink, recent, block_size,
-                                              ptr(lengths), int(length), int(bool(append)), ptr(cur_k), ptr(cur_v),
-                                              sc, *meta, ptr(packed), ptr(scale), ptr(minimum),
-                                              0 if scale is None else scale.stride(0), ptr(out), ptr(ws), ws.numel(),
-                                              int(phase), stream_handle(dev)), "decode_attention_union")
+        if resident is None:
+            check(hip().tw_decode_attention_union(
+                ptr(q), kp, vp, _dt(q), G, R, D, ptr(union_rec), union_rec.stride(0), P, max_rows,
+                k_cache.stride(0) // D, sink, recent, block_size, ptr(lengths), int(length), int(bool(append)),
+                ptr(cur_k), ptr(cur_v), sc, *meta, ptr(packed), ptr(scale), ptr(minimum),
+                0 if scale is None else scale.stride(0), ptr(out), ptr(ws), ws.numel(), int(phase),
+                stream_handle(dev)), "decode_attention_union")
+        else:
+            wk = resident.win_k
+            check(hip().tw_decode_attention_union_resident(
+                ptr(q), kp, vp, _dt(q), G, R, D, ptr(union_rec), union_rec.stride(0), P, max_rows,
+                k_cache.stride(0) // D, sink, recent, block_size, ptr(lengths), int(length), int(bool(append)),
+                ptr(cur_k), ptr(cur_v), sc, ptr(resident.k), ptr(resident.v), ptr(resident.map), resident.slots,
+                resident.pages, ptr(resident.stats), ptr(wk), ptr(resident.win_v), ptr(resident.win_state),
+                resident.ring if wk is not None else 0, *meta, ptr(packed), ptr(scale), ptr(minimum),
+                0 if scale is None else scale.stride(0), ptr(out), ptr(ws), ws.numel(), int(phase),
+                stream_handle(dev)), "decode_attention_union_resident")
     return out
 
 
@@ -1629,6 +1652,21 @@ class ResidentPages:
             out.win_k, out.win_v = self.win_k[g0:g0 + n], self.win_v[g0:g0 + n]
             out.win_state = self.win_state[g0:g0 + n]
         return out
+
+
+def _check_resident(resident: "ResidentPages", q: torch.Tensor, G: int, D: int, sink: int, recent: int) -> None:
+    rk, rv, rm, rs = resident.k, resident.v, resident.map, resident.stats
+    if rk.dtype != q.dtype or tuple(rk.shape) != (G, 2, resident.slots, 16, D) or not rk.is_contiguous() \
+            or rv.shape != rk.shape or not rv.is_contiguous() or rm.dtype != torch.int64 \
+            or tuple(rm.shape) != (G, resident.pages) or not rm.is_contiguous() \
+            or tuple(rs.shape) != (G, 2) or not rs.is_contiguous():
+        raise ValueError("resident buffers do not match the launch")
+    wk, wv, wst = resident.win_k, resident.win_v, resident.win_state
+    if wk is not None and (resident.sink != sink or resident.ring < recent or wk.dtype != q.dtype
+                           or tuple(wk.shape) != (G, sink + resident.ring, D) or not wk.is_contiguous()
+                           or wv.shape != wk.shape or not wv.is_contiguous() or wst.dtype != torch.int32
+                           or tuple(wst.shape) != (G, 2) or not wst.is_contiguous()):
+        raise ValueError("resident windows do not match the launch (sink, recent, dtype, shape)")
 
 
 def decode_attention_pages_resident(
@@ -1683,17 +1721,8 @@ def decode_attention_pages_resident(
                                 or not lengths.is_contiguous()):
         raise ValueError("lengths must be contiguous [G] int32")
     rk, rv, rm, rs = resident.k, resident.v, resident.map, resident.stats
-    if rk.dtype != q.dtype or tuple(rk.shape) != (G, 2, resident.slots, 16, D) or not rk.is_contiguous() \
-            or rv.shape != rk.shape or not rv.is_contiguous() or rm.dtype != torch.int64 \
-            or tuple(rm.shape) != (G, resident.pages) or not rm.is_contiguous() \
-            or tuple(rs.shape) != (G, 2) or not rs.is_contiguous():
-        raise ValueError("resident buffers do not match the launch")
+    _check_resident(resident, q, G, D, sink, recent)
     wk, wv, wst = resident.win_k, resident.win_v, resident.win_state
-    if wk is not None and (resident.sink != sink or resident.ring < recent or wk.dtype != q.dtype
-                           or tuple(wk.shape) != (G, sink + resident.ring, D) or not wk.is_contiguous()
-                           or wv.shape != wk.shape or not wv.is_contiguous() or wst.dtype != torch.int32
-                           or tuple(wst.shape) != (G, 2) or not wst.is_contiguous()):
-        raise ValueError("resident windows do not match the launch (sink, recent, dtype, shape)")
     if not 0 <= max_pages <= plan_pages.shape[1]:
         raise ValueError("max_pages must be within the plan width")
     if (cur_k is None) != (cur_v is None):
