@@ -410,6 +410,43 @@ def test_twilight_decode_layer(H, dev, residency, dtype, fused, mode):
         assert _same(cache._key_cache[e, :n], model.keys[e]) and _same(cache._value_cache[e, :n], model.vals[e])
 
 
+@pytest.mark.parametrize("mode", ["dynamic", "matched"])
+def test_twilight_decode_layer_resident_cache(H, dev, mode):
+    """previous_token_resident_cache on a Twilight cache with a host slab
+    (with the execution flags the reference requires for it): decode_layer
+    == the same cache without it, bit for bit, over 4 steps of drifting
+    queries, while kept rows of the previous step come from the HBM resident
+    cache (counted: some rows hit) and the slabs receive the same appends."""
+    G, R, D, T, steps = 4, 4, 128, 3000, 4
+    _say(f"[twilight resident decode_layer] {mode}")
+    kw = dict(candidate_token_budget=512, top_p=0.9, matched_budget_fraction=0.05)
+    flags = dict(previous_token_resident_cache=True, layer_batched_selection=True, gqa_groupwise_execution=True,
+                 cpu_flat_gather=True, direct_attention_layout=True, gather_h2d_chunks=1)
+    res_cache = _twilight_cache(H, dev, E=G, T=T, D=D, R=R, dtype="bf16", residency="host", mode=mode, **kw, **flags)
+    plain = _twilight_cache(H, dev, E=G, T=T, D=D, R=R, dtype="bf16", residency="host", mode=mode, **kw)
+    assert res_cache._resident_active and not plain._resident_active
+    model = _Model(G, T, D, "bf16", seed=61, scale=2.0)
+    model.prefill(res_cache, dev)
+    model.prefill(plain, dev)
+    g = torch.Generator().manual_seed(62)
+    base = torch.randn(G, R, D, generator=g) * 2
+    for step in range(steps):
+        q = (base + 0.3 * torch.randn(G, R, D, generator=g)).to(torch.bfloat16).to(dev)
+        new = [model.new_token(D) for _ in range(G)]
+        nk = torch.stack([k for k, _ in new]).to(dev)
+        nv = torch.stack([v for _, v in new]).to(dev)
+        a = res_cache.decode_layer(queries=q, key_states=nk, value_states=nv, entries=list(range(G)))
+        b = plain.decode_layer(queries=q, key_states=nk, value_states=nv, entries=list(range(G)))
+        torch.cuda.synchronize()
+        assert _same(a, b), step
+    n = T + steps
+    assert _same(res_cache._key_cache[:, :n], plain._key_cache[:, :n])
+    assert _same(res_cache._value_cache[:, :n], plain._value_cache[:, :n])
+    st = res_cache.resident_stats()
+    _say(f"[twilight resident decode_layer] {st}")
+    assert 0 < st["resident_hit_pages"] < st["union_pages"], st
+
+
 def test_twilight_per_head_update_and_flat(H, dev):
     """Per-entry update() and update_layer_flat_ragged give every head its own
     Twilight selection (the oracle's per-head selected positions)."""

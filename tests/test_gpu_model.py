@@ -321,29 +321,36 @@ def test_graph_decoder_fused_equals_unfused(dev):
     assert torch.equal(caches[0]._value_cache[:, :n], caches[1]._value_cache[:, :n])
 
 
-@pytest.mark.parametrize("fuse,mode,q_heads", [(True, "dynamic", 8), (False, "dynamic", 8), (True, "matched", 8),
-                                               (True, "dynamic", 32), (True, "matched", 32)])
-def test_graph_decoder_twilight_matches_eager(dev, fuse, mode, q_heads):
+@pytest.mark.parametrize("fuse,mode,q_heads,resident", [(True, "dynamic", 8, False), (False, "dynamic", 8, False),
+                                                        (True, "matched", 8, False), (True, "dynamic", 32, False),
+                                                        (True, "matched", 32, False), (True, "dynamic", 8, True)])
+def test_graph_decoder_twilight_matches_eager(dev, fuse, mode, q_heads, resident):
     """GraphDecoder over a Twilight cache (Quest B0, INT4 QK, top-p and the
     GQA union from device-side lengths, the union attention with the append,
     the INT4 + page metadata update) == the eager patched model with the same
     cache policy, token by token; the steps cross a page completion.  32
     query heads over 2 KV heads (16 per group) run the fused selection and
     the union attention as sub-groups of 8 (matched: one allocation over the
-    16 heads)."""
+    16 heads).  resident: both caches over a host slab, the graph's with the
+    previous-token resident cache (the union rows and windows in HBM)."""
     from headinfer import mp
     from headinfer.graph_decode import GraphDecoder
     from headinfer.twilight_offload_cache import TwilightMatchedBudgetOffloadedCache
 
-    _say(f"[graph decoder twilight] fuse={fuse} {mode} q_heads={q_heads}")
+    _say(f"[graph decoder twilight] fuse={fuse} {mode} q_heads={q_heads} resident={resident}")
     steps = 10
     _, gpu = _models(dev, q_heads=q_heads)
     mp.mp_headinfer(gpu)
     kw = dict(max_cache_len=T_PROMPT + steps + 2, sink_tokens=64, recent_tokens=256, block_size=16,
               kv_residency="hbm", candidate_token_budget=128, top_p=0.9, budget_mode=mode,
               update_metadata_on_decode=True)
+    if resident:
+        kw["kv_residency"] = "host"
     eager_cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(gpu, **kw)
-    graph_cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(gpu, **kw)
+    flags = dict(previous_token_resident_cache=True, layer_batched_selection=True, gqa_groupwise_execution=True,
+                 cpu_flat_gather=True, direct_attention_layout=True, gather_h2d_chunks=1) if resident else {}
+    graph_cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(gpu, **kw, **flags)
+    assert graph_cache._resident_active == resident
     g = torch.Generator().manual_seed(9)
     ids = torch.randint(0, 1000, (1, T_PROMPT), generator=g).to(dev)
     tok = torch.ones((1, 1), dtype=torch.long, device=dev)

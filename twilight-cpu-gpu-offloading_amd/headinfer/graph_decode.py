@@ -63,9 +63,8 @@ class GraphDecoder:
             raise ValueError("GraphDecoder needs a cache built with update_metadata_on_decode=True")
         kind = type(cache).__name__
         if kind == "TwilightMatchedBudgetOffloadedCache":
+            # (its resident cache, when active, rides in the fused union attention)
             self.twilight = True
-            if cache.previous_token_resident_cache:
-                raise ValueError("GraphDecoder runs the Twilight union attention without the resident cache")
         elif kind == "QuestTopKOffloadedCache":
             self.twilight = False
             if cache.budget_pages is None and not dense:
@@ -369,11 +368,12 @@ class GraphDecoder:
             meta = dict(page_min=c._page_min[e0:e0 + G], page_max=c._page_max[e0:e0 + G],
                         packed=c._packed[e0:e0 + G], scale=c._qscale[e0:e0 + G],
                         minimum=c._qmin[e0:e0 + G]) if self.fuse else {}
+            resident = c.resident_pages().view(e0, G) if c._resident_active else None
             kernels.decode_attention_union(qg, c._key_cache[e0:e0 + G], c._value_cache[e0:e0 + G], self.tw_rec,
                                            self.P, max_pages=self.width, sink=c.sink_tokens,
                                            recent=c.recent_tokens, block_size=c.block_size, lengths=self.lengths,
                                            append=True, cur_k=k, cur_v=v, softmax_scale=float(attn.scaling),
-                                           out=self.attn[li], **meta)
+                                           out=self.attn[li], resident=resident, **meta)
             if not self.fuse:
                 kernels.update_page_metadata_ragged(c._key_cache, self.lengths, first_entry=e0, sink=c.sink_tokens,
                                                     block_size=c.block_size, page_min=c._page_min,

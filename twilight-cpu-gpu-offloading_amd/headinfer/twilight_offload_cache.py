@@ -328,6 +328,18 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
             self._cpu_token_union = CpuTokenUnion(self.geometry.max_cache_len)
         self.candidate_token_budget = int(candidate_token_budget)
         self.top_p = float(top_p)
+        # The previous-token resident cache (twilight_offload_cache.py:2457-2608,
+        # 3323-3470): with a host slab, the fused decode keeps each group's last
+        # union rows in HBM, row by row, with the sink and recent windows, and
+        # reads only the other rows over the host link.  An HBM slab needs no
+        # such cache, and the fused shapes bound it (16-bit K/V, head_dim 128,
+        # 16-row pages, at most 8 query heads per KV head); elsewhere the flag
+        # is validated and recorded only.
+        self.previous_token_resident_cache = bool(previous_token_resident_cache)
+        self._resident_active = (self.previous_token_resident_cache and self.kv_residency == "host"
+                                 and self.block_size == 16 and self.geometry.head_dim == 128
+                                 and self.dtype in (torch.float16, torch.bfloat16)
+                                 and self.num_query_heads_per_kv <= 8)
         self.matched_budget_fraction = float(matched_budget_fraction)
         self.budget_mode = budget_mode
         self.gqa_groupwise_execution = bool(gqa_groupwise_execution)
@@ -431,6 +443,22 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         self._phase_end("metadata_update", start)
 
     # --------------------------------------------------------------- budgets
+    def resident_pages(self) -> "kernels.ResidentPages":
+        """The HBM resident cache of every entry (allocated on first use):
+        slots for the widest union the B0 budget allows (R x B0 pages), a map
+        over every page the metadata can hold, and the sink and recent
+        windows."""
+        if self._resident is None:
+            if self._page_min is None:
+                raise RuntimeError("prompt metadata is missing")
+            pages = max(1, int(self._page_min.shape[1]))
+            b0 = max(1, math.ceil(self.candidate_token_budget / self.block_size))
+            slots = max(1, min(pages, self.num_query_heads_per_kv * b0, 0xffff))
+            self._resident = kernels.ResidentPages(self.geometry.num_entries, slots, pages, self.geometry.head_dim,
+                                                   self.dtype, self.device, sink=self.sink_tokens,
+                                                   recent=self.recent_tokens)
+        return self._resident
+
     def _twilight_budgets(self, old_length: int) -> tuple[int, int, int, int, int]:
         """(sink_end, recent_start, candidate_pages, fixed_pages, b0_pages) of
         twilight_offload_cache.py:1019-1083."""
@@ -747,12 +775,13 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         e0 = entries[0]
         cur_k, cur_v = key_states.contiguous(), value_states.contiguous()
         start = self._phase_start()
+        resident = self.resident_pages().view(e0, G) if self._resident_active else None
         result = kernels.decode_attention_union(queries.contiguous(), self._key_cache[e0:e0 + G],
                                                 self._value_cache[e0:e0 + G], rec, cand,
                                                 max_pages=min(cand, R * b0), sink=self.sink_tokens,
                                                 recent=self.recent_tokens, block_size=self.block_size,
                                                 length=old_length, append=True, cur_k=cur_k, cur_v=cur_v,
-                                                softmax_scale=softmax_scale, out=out)
+                                                softmax_scale=softmax_scale, out=out, resident=resident)
         self._phase_end("attention", start)
         self._append(entries, cur_k, cur_v, old_length, written=True)
         for e in entries:
