@@ -1416,6 +1416,7 @@ def run_tpot(args, dev) -> int:
     if residency == "host":  # the HBM resident page cache (previous_token_resident_cache) serves host slabs
         variants[1:1] = [("sparse_graph_resident", args.budget_pages, True, True)]
         variants[4:4] = [("sparse_hf_eager_resident", args.budget_pages, False, True)]
+        variants.append(("twilight_graph_resident", None, True, True))
     if args.tpot_only is not None:
         variants = [v for v in variants if v[0] == args.tpot_only]
         if not variants:
@@ -1424,9 +1425,13 @@ def run_tpot(args, dev) -> int:
         print(f"[bench] tpot {label}: prefill + {n_dec} decode tokens", file=sys.stderr, flush=True)
         if label.startswith("twilight"):
             # the reference runner's path: Quest B0 = 4096 tokens, INT4 QK, top-p 0.95
+            # (resident: with the execution flags the reference requires for its resident cache)
+            flags = dict(previous_token_resident_cache=True, layer_batched_selection=True,
+                         gqa_groupwise_execution=True, cpu_flat_gather=True, direct_attention_layout=True,
+                         gather_h2d_chunks=1) if resident else {}
             cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(
                 model, max_cache_len=ctx + n_dec + 8, kv_residency=residency, candidate_token_budget=4096,
-                top_p=0.95, budget_mode="dynamic", update_metadata_on_decode=graph)
+                top_p=0.95, budget_mode="dynamic", update_metadata_on_decode=graph, **flags)
         else:
             cache = QuestTopKOffloadedCache.from_llama_model(model, max_cache_len=ctx + n_dec + 8,
                                                              kv_residency=residency, budget_pages=pages,
@@ -1505,8 +1510,8 @@ def tpot_leg(args, dev, model=None, ctx: int = 32768, kv: str = "hbm", n_dec: in
     (no score or top-k: every whole page before the recent window through the
     same attention), Twilight (Quest B0 4096 tokens, INT4 QK, top-p 0.95,
     dynamic budgets, then matched budgets on the same cache), and with the KV
-    in pinned host memory also sparse Quest with the HBM resident page cache
-    (previous_token_resident_cache)."""
+    in pinned host memory also sparse Quest and Twilight with the HBM resident
+    cache (previous_token_resident_cache)."""
     import torch
 
     from headinfer.graph_decode import GraphDecoder
@@ -1569,6 +1574,23 @@ def tpot_leg(args, dev, model=None, ctx: int = 32768, kv: str = "hbm", n_dec: in
         dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1)
         out["twilight_matched_graph"] = _graph_tpot(dec, n_dec)
         del dec, cache
+        if kv == "host":
+            # the Twilight cache's previous-token resident cache (the union rows
+            # and the sink/recent windows in HBM), with the execution flags the
+            # reference requires for it, on a cache of its own
+            torch.cuda.empty_cache()
+            cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(
+                model, max_cache_len=ctx + n_dec + 8, kv_residency=kv, candidate_token_budget=4096, top_p=0.95,
+                budget_mode="dynamic", update_metadata_on_decode=True, previous_token_resident_cache=True,
+                layer_batched_selection=True, gqa_groupwise_execution=True, cpu_flat_gather=True,
+                direct_attention_layout=True, gather_h2d_chunks=1)
+            prefill(cache, "twilight, resident cache")
+            dec = GraphDecoder(model, cache, max_new_tokens=n_dec, fixed_token=1)
+            out["twilight_graph_resident"] = _graph_tpot(dec, n_dec)
+            st = cache.resident_stats()
+            out["twilight_graph_resident"]["resident_hit_ratio"] = round(
+                st["resident_hit_pages"] / max(1, st["union_pages"]), 4)
+            del dec, cache
     if own:
         del model
     torch.cuda.empty_cache()
@@ -1581,6 +1603,8 @@ def tpot_leg(args, dev, model=None, ctx: int = 32768, kv: str = "hbm", n_dec: in
            "budget_pages": args.budget_pages}
     if "sparse_graph_resident" in out:
         res["resident_hit_ratio"] = out["sparse_graph_resident"]["resident_hit_ratio"]
+    if "twilight_graph_resident" in out:
+        res["twilight_resident_hit_row_ratio"] = out["twilight_graph_resident"]["resident_hit_ratio"]
     return res
 
 
