@@ -739,6 +739,26 @@ int tw_gather_union(const void* src_k, const void* src_v, int64_t src_row_limit,
                     int G, int max_count, const void* cur_k, const void* cur_v, int D, int elem_bytes,
                     int64_t dst_capacity, void* dst_k, void* dst_v, int32_t* cu_seqlens, int32_t* error_flag,
                     void* stream);
+/* tw_gather_union with the previous-token resident cache of the GQA-group
+ * path (previous_token_resident_cache, twilight_offload_cache.py:2457-2608,
+ * 3323-3470; hit/miss mapping resident_gpu_mapping.py:14-144, which maps the
+ * current union onto the previous one and copies hits from the previous
+ * snapshot): res_map [G][map_stride] (int64, initialised to -1; map_stride
+ * above every position) holds (epoch << 32) | index of the step that last
+ * packed each position, prev_k/prev_v [prev_capacity][D] that step's packed
+ * output and prev_cu [G + 1] its cu_seqlens.  A union row whose entry names
+ * epoch - 1 is copied from prev_k/prev_v (HBM) instead of the slab; the
+ * entries of this step's rows then name epoch (this step's history length,
+ * >= 1) and their index in dst.  res_stats [2] (nullable) accumulates (rows
+ * copied from the previous step, union rows).  Other arguments as
+ * tw_gather_union. */
+int tw_gather_union_resident(const void* src_k, const void* src_v, int64_t src_row_limit, int64_t entry_row0,
+                             int64_t entry_row_step, const int32_t* rows, int64_t rows_stride,
+                             const int32_t* row_counts, int G, int max_count, const void* cur_k, const void* cur_v,
+                             int D, int elem_bytes, int64_t dst_capacity, void* dst_k, void* dst_v,
+                             int32_t* cu_seqlens, int32_t* error_flag, int64_t* res_map, int64_t map_stride,
+                             int epoch, const void* prev_k, const void* prev_v, const int32_t* prev_cu,
+                             int64_t prev_capacity, unsigned long long* res_stats, void* stream);
 
 /* Per-query-head gather of the Quest paths: replaces the per-head CPU
  * index_select + H2D + current-token write of update (quest_offload_cache.py:

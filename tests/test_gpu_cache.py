@@ -326,6 +326,67 @@ def test_twilight_gqa_group_union(H, dev, residency, dtype, mode):
         assert _same(cache._key_cache[e, :T + 2], model.keys[e])
 
 
+@pytest.mark.parametrize("mode", ["matched", "dynamic"])
+def test_twilight_gqa_group_union_resident_cache(H, dev, mode):
+    """update_layer_gqa_group_ragged with previous_token_resident_cache (the
+    reference's path for it): K/V == slab[oracle union] ++ decode token at
+    every step, although before each step the cache's host slab copies of the
+    previous step's union rows are overwritten with noise -- a row packed
+    again must come from the HBM copy of the previous step; rows are counted
+    as hits, some are, and the slab gets every append."""
+    layers, G, R, D, T, steps = 2, 4, 4, 128, 3000, 4
+    E = layers * G
+    dtype = "bf16"
+    _say(f"[twilight gqa resident] {mode}")
+    cache = _twilight_cache(H, dev, E=E, T=T, D=D, R=R, dtype=dtype, residency="host", mode=mode,
+                            candidate_token_budget=512, top_p=0.9, matched_budget_fraction=0.05,
+                            layer_batched_selection=True, gqa_groupwise_execution=True, cpu_flat_gather=True,
+                            direct_attention_layout=True, gather_h2d_chunks=1, previous_token_resident_cache=True)
+    model = _Model(E, T, D, dtype, seed=33, scale=2.0)
+    model.prefill(cache, dev)
+    g = torch.Generator().manual_seed(34)
+    noise = torch.Generator().manual_seed(35)
+    bases = [torch.randn(1, R, 1, D, generator=g) * 2 for _ in range(E)]
+    prev_union = [None] * E
+    for step in range(steps):
+        torch.cuda.synchronize()
+        for e in range(E):   # the slab back to the model's rows, then the previous union to noise
+            n = T + step
+            cache._key_cache[e, :n] = model.keys[e][:n]
+            cache._value_cache[e, :n] = model.vals[e][:n]
+            if prev_union[e] is not None:
+                m = len(prev_union[e])
+                cache._key_cache[e, prev_union[e]] = torch.randn((m, D), generator=noise).to(torch.bfloat16)
+                cache._value_cache[e, prev_union[e]] = torch.randn((m, D), generator=noise).to(torch.bfloat16)
+        for layer in range(layers):
+            entries = list(range(layer * G, layer * G + G))
+            qs = [(bases[e] + 0.3 * torch.randn(1, R, 1, D, generator=g)).to(TORCH_DT[dtype]) for e in entries]
+            new = [model.new_token(D) for _ in entries]
+            cache.prepare_layer_selection(entries=entries, queries=[q.to(dev) for q in qs])
+            K, V, cu, max_k, lengths = cache.update_layer_gqa_group_ragged(
+                key_states=[k[None, None, None].to(dev) for k, _ in new],
+                value_states=[v[None, None, None].to(dev) for _, v in new],
+                queries=[q.to(dev) for q in qs], entries=entries)
+            cu_h = cu.cpu().numpy()
+            assert cu_h[0] == 0 and list(np.diff(cu_h)) == list(lengths) and max_k == max(lengths)
+            for gi, e in enumerate(entries):
+                ref = _twilight_expected(model, e, qs[gi][0, :, 0].float().numpy(), T + step, cache)
+                s, n = int(cu_h[gi]), len(ref["union"])
+                assert lengths[gi] == n + 1, (gi, lengths[gi], n)
+                assert _same(K[s:s + n, 0], model.keys[e][ref["union"]]), (step, e)
+                assert _same(V[s:s + n, 0], model.vals[e][ref["union"]]), (step, e)
+                assert _same(K[s + n, 0], new[gi][0]) and _same(V[s + n, 0], new[gi][1])
+                model.append(e, *new[gi])
+                prev_union[e] = torch.as_tensor(np.asarray(ref["union"]), dtype=torch.long)
+            torch.cuda.synchronize()
+            for gi, e in enumerate(entries):   # the append landed in the slab
+                assert _same(cache._key_cache[e, T + step], new[gi][0]), (step, e)
+                assert _same(cache._value_cache[e, T + step], new[gi][1]), (step, e)
+    st = cache.resident_stats()
+    _say(f"[twilight gqa resident] {st}")
+    assert 0 < st["resident_hit_pages"] < st["union_pages"], st
+
+
 def test_twilight_decode_metadata_update(H, dev):
     """Twilight with update_metadata_on_decode: decode rows get INT4 codes and
     completed pages get min/max, so the union over pages completed during

@@ -126,6 +126,102 @@ __global__ __launch_bounds__(256) void gather_union_kernel(const V* __restrict__
   }
 }
 
+// gather_union_kernel with the previous-token resident cache of the GQA-group
+// path: res_map [G][map_stride] (int64, position-indexed, initialised to -1)
+// holds (epoch << 32) | flat index of the step that last gathered each
+// position, and prev_k/prev_v (with prev_cu [G + 1]) that step's flat output.
+// A union row whose entry names epoch - 1 (the previous step) is copied from
+// there (HBM) instead of from the slab; after the block's copies, its rows'
+// entries name this step (each position is one row of one block, so no other
+// block reads them in this launch).  res_stats [2] (nullable) accumulates
+// (rows copied from the previous step, union rows).
+template <typename V>
+__global__ __launch_bounds__(256) void gather_union_resident_kernel(
+    const V* __restrict__ src_k, const V* __restrict__ src_v, int64_t src_row_limit, int64_t entry_row0,
+    int64_t entry_row_step, const int32_t* __restrict__ rows, int64_t rows_stride, const int32_t* __restrict__ counts,
+    int G, int max_count, const V* __restrict__ cur_k, const V* __restrict__ cur_v, int vec_per_row,
+    int64_t dst_capacity, V* __restrict__ dst_k, V* __restrict__ dst_v, int32_t* cu_seqlens, int32_t* error_flag,
+    int chunks, int rows_per_block, int64_t* res_map, int64_t map_stride, int epoch, const V* __restrict__ prev_k,
+    const V* __restrict__ prev_v, const int32_t* __restrict__ prev_cu, int64_t prev_capacity,
+    unsigned long long* res_stats) {
+  const int g = blockIdx.x / chunks;
+  const int chunk = blockIdx.x - g * chunks;
+  __shared__ int64_t s_off;
+  __shared__ int s_count;
+  __shared__ int64_t s_prev;
+  __shared__ unsigned int s_hits, s_rows;
+  if (threadIdx.x == 0) {
+    int64_t off = 0;
+    for (int h = 0; h < g; ++h) {
+      int c = counts[h];
+      c = c < 0 ? 0 : (c > max_count ? max_count : c);
+      off += c + 1;
+    }
+    int c = counts[g];
+    s_count = c < 0 ? 0 : (c > max_count ? max_count : c);
+    s_off = off;
+    s_prev = prev_cu[g];
+    s_hits = 0u;
+    s_rows = 0u;
+    if (blockIdx.x == 0) {
+      int64_t run = 0;
+      cu_seqlens[0] = 0;
+      for (int h = 0; h < G; ++h) {
+        int ch = counts[h];
+        ch = ch < 0 ? 0 : (ch > max_count ? max_count : ch);
+        run += ch + 1;
+        cu_seqlens[h + 1] = static_cast<int32_t>(run);
+      }
+    }
+  }
+  __syncthreads();
+  const int count = s_count;
+  const int64_t off = s_off;
+  const int64_t prev0 = s_prev;
+  const int first = chunk * rows_per_block;
+  const int last = (first + rows_per_block) < (count + 1) ? (first + rows_per_block) : (count + 1);
+  const int64_t row0 = entry_row0 + static_cast<int64_t>(g) * entry_row_step;
+  int64_t* gmap = res_map + static_cast<int64_t>(g) * map_stride;
+  for (int t = first * vec_per_row + static_cast<int>(threadIdx.x); t < last * vec_per_row; t += blockDim.x) {
+    const int i = t / vec_per_row;
+    const int c = t - i * vec_per_row;
+    const int64_t dr = off + i;
+    if (dr >= dst_capacity) {
+      if (error_flag != nullptr) *error_flag = 1;
+      continue;
+    }
+    if (i == count) {  // the decode token
+      dst_k[dr * vec_per_row + c] = cur_k[static_cast<int64_t>(g) * vec_per_row + c];
+      dst_v[dr * vec_per_row + c] = cur_v[static_cast<int64_t>(g) * vec_per_row + c];
+      continue;
+    }
+    const int pos = rows[static_cast<int64_t>(g) * rows_stride + i];
+    const int64_t sr = row0 + pos;
+    if (sr < 0 || sr >= src_row_limit || pos >= map_stride) {
+      if (error_flag != nullptr) *error_flag = 1;
+      continue;
+    }
+    const int64_t m = gmap[pos];
+    const int64_t pr = prev0 + (m & 0xffffffffll);
+    const bool hit = (m >> 32) == static_cast<int64_t>(epoch) - 1 && pr < prev_capacity;
+    if (c == 0) {
+      atomicAdd(&s_rows, 1u);
+      if (hit) atomicAdd(&s_hits, 1u);
+    }
+    dst_k[dr * vec_per_row + c] = hit ? prev_k[pr * vec_per_row + c] : src_k[sr * vec_per_row + c];
+    dst_v[dr * vec_per_row + c] = hit ? prev_v[pr * vec_per_row + c] : src_v[sr * vec_per_row + c];
+  }
+  __syncthreads();  // every map entry of the block's rows has been read
+  for (int i = first + static_cast<int>(threadIdx.x); i < last && i < count; i += blockDim.x) {
+    const int pos = rows[static_cast<int64_t>(g) * rows_stride + i];
+    if (pos >= 0 && pos < map_stride) gmap[pos] = (static_cast<int64_t>(epoch) << 32) | static_cast<int64_t>(i);
+  }
+  if (threadIdx.x == 0 && res_stats != nullptr && s_rows > 0u) {
+    atomicAdd(res_stats, static_cast<unsigned long long>(s_hits));
+    atomicAdd(res_stats + 1, static_cast<unsigned long long>(s_rows));
+  }
+}
+
 // Per-query-head layout of the Quest paths: head r of group g sees
 // [0, sink_end) ++ its own pages sel[g][r][0..k) (ascending) expanded to bs
 // rows ++ [recent_start, length), then the decode token; its row t goes to
@@ -280,6 +376,25 @@ int launch_union(const void* sk, const void* sv, int64_t limit, int64_t row0, in
 }
 
 template <typename V>
+int launch_union_resident(const void* sk, const void* sv, int64_t limit, int64_t row0, int64_t step,
+                          const int32_t* rows, int64_t rows_stride, const int32_t* counts, int G, int max_count,
+                          const void* ck, const void* cv, int64_t row_bytes, int64_t cap, void* dk, void* dv,
+                          int32_t* cu, int32_t* err, int64_t* res_map, int64_t map_stride, int epoch,
+                          const void* pk, const void* pv, const int32_t* prev_cu, int64_t prev_cap,
+                          unsigned long long* stats, hipStream_t stream) {
+  const int vpr = static_cast<int>(row_bytes / sizeof(V));
+  int rpb = static_cast<int>(16384 / row_bytes);
+  rpb = rpb < 1 ? 1 : rpb;
+  const int chunks = (max_count + 1 + rpb - 1) / rpb;
+  hipLaunchKernelGGL(gather_union_resident_kernel<V>, dim3(G * chunks), dim3(256), 0, stream,
+                     static_cast<const V*>(sk), static_cast<const V*>(sv), limit, row0, step, rows, rows_stride,
+                     counts, G, max_count, static_cast<const V*>(ck), static_cast<const V*>(cv), vpr, cap,
+                     static_cast<V*>(dk), static_cast<V*>(dv), cu, err, chunks, rpb, res_map, map_stride, epoch,
+                     static_cast<const V*>(pk), static_cast<const V*>(pv), prev_cu, prev_cap, stats);
+  return tw_host::check_launch();
+}
+
+template <typename V>
 int launch_heads(const void* sk, const void* sv, int64_t limit, int64_t row0, int64_t step, const int32_t* sel, int G,
                  int R, int k, int sink, int bs, int sink_end, int recent_start, int length, const void* ck,
                  const void* cv, int64_t row_bytes, int64_t gs, int64_t rs, int64_t ts, void* dk, void* dv,
@@ -323,6 +438,40 @@ extern "C" int tw_gather_union(const void* src_k, const void* src_v, int64_t src
     default: return TW_UNION(uint8_t);
   }
 #undef TW_UNION
+}
+
+extern "C" int tw_gather_union_resident(const void* src_k, const void* src_v, int64_t src_row_limit,
+                                        int64_t entry_row0, int64_t entry_row_step, const int32_t* rows,
+                                        int64_t rows_stride, const int32_t* row_counts, int G, int max_count,
+                                        const void* cur_k, const void* cur_v, int D, int elem_bytes,
+                                        int64_t dst_capacity, void* dst_k, void* dst_v, int32_t* cu_seqlens,
+                                        int32_t* error_flag, int64_t* res_map, int64_t map_stride, int epoch,
+                                        const void* prev_k, const void* prev_v, const int32_t* prev_cu,
+                                        int64_t prev_capacity, unsigned long long* res_stats, void* stream) {
+  if (G <= 0 || max_count < 0 || D <= 0 || rows_stride < max_count || dst_capacity <= 0 ||
+      !(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8))
+    return TW_EINVAL;
+  if (src_k == nullptr || src_v == nullptr || rows == nullptr || row_counts == nullptr || cur_k == nullptr ||
+      cur_v == nullptr || dst_k == nullptr || dst_v == nullptr || cu_seqlens == nullptr)
+    return TW_EINVAL;
+  if (res_map == nullptr || map_stride < 1 || epoch < 1 || prev_k == nullptr || prev_v == nullptr ||
+      prev_cu == nullptr || prev_capacity < 0)
+    return TW_EINVAL;
+  const int64_t row_bytes = static_cast<int64_t>(D) * elem_bytes;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+#define TW_UNION_RES(V)                                                                                           \
+  tw::launch_union_resident<V>(src_k, src_v, src_row_limit, entry_row0, entry_row_step, rows, rows_stride,        \
+                               row_counts, G, max_count, cur_k, cur_v, row_bytes, dst_capacity, dst_k, dst_v,      \
+                               cu_seqlens, error_flag, res_map, map_stride, epoch, prev_k, prev_v, prev_cu,        \
+                               prev_capacity, res_stats, s)
+  switch (tw::vec_width(row_bytes, {src_k, src_v, dst_k, dst_v, cur_k, cur_v, prev_k, prev_v})) {
+    case 16: return TW_UNION_RES(uint4);
+    case 8: return TW_UNION_RES(uint2);
+    case 4: return TW_UNION_RES(uint32_t);
+    case 2: return TW_UNION_RES(uint16_t);
+    default: return TW_UNION_RES(uint8_t);
+  }
+#undef TW_UNION_RES
 }
 
 extern "C" int tw_gather_heads(const void* src_k, const void* src_v, int64_t src_row_limit, int64_t entry_row0,

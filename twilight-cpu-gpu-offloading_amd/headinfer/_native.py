@@ -119,6 +119,8 @@ _HIP_SIGNATURES = {
     "tw_gather_rows": (i32, [vp, vp, i64, vp, vp, i64, i64, i32, i32, vp, vp, vp, vp]),
     "tw_gather_union": (i32, [vp, vp, i64, i64, i64, vp, i64, vp, i32, i32, vp, vp, i32, i32, i64, vp, vp, vp, vp,
                               vp]),
+    "tw_gather_union_resident": (i32, [vp, vp, i64, i64, i64, vp, i64, vp, i32, i32, vp, vp, i32, i32, i64, vp, vp,
+                                       vp, vp, vp, i64, i32, vp, vp, vp, i64, vp, vp]),
     "tw_gather_heads": (i32, [vp, vp, i64, i64, i64, vp, i32, i32, i32, i32, i32, i32, i32, vp, vp, i32, i32, i64,
                               i64, i64, i64, vp, vp, vp, vp]),
     "tw_host_device_pointer": (i32, [vp, ctypes.POINTER(ctypes.c_void_p)]),

@@ -1894,6 +1894,7 @@ def gather_union(
     entry_row_step: int,
     max_count: int,
     error_flag: Optional[torch.Tensor] = None,
+    resident: Optional[dict] = None,
 ) -> None:
     """Pack each group's union rows, then its decode token, back to back
     (the varlen K/V of the GQA group path) and write cu_seqlens [G+1].
@@ -1901,7 +1902,11 @@ def gather_union(
     src_k/src_v: the slab planes [rows, D] (HBM or pinned host); group g's
     source rows are entry_row0 + g*entry_row_step + rows[g, i]; rows [G,
     stride] int32 and row_counts [G] int32 on the device; cur_k/cur_v [G, D];
-    dst_k/dst_v [capacity, D]."""
+    dst_k/dst_v [capacity, D].  resident (the previous-token resident cache):
+    dict(map= [G, positions] int64 (-1 at first), epoch= this step's history
+    length, prev_k=, prev_v= the previous step's packed output, prev_cu= its
+    cu_seqlens, stats= [2] int64 or None): rows the previous step packed are
+    copied from there, and the map then names this step's rows."""
     if src_k.ndim != 2 or src_k.shape != src_v.shape or src_k.dtype != src_v.dtype:
         raise ValueError("src_k/src_v must be matching [rows, D]")
     D = src_k.shape[1]
@@ -1919,11 +1924,30 @@ def gather_union(
     dev = _require_device(rows, row_counts, cur_k, cur_v, dst_k, dst_v, cu_seqlens, error_flag,
                           what="gather_union")
     sk, sv = _slab_source(src_k, src_v)
+    if resident is not None:
+        rm, pk, pv, pcu, st = (resident["map"], resident["prev_k"], resident["prev_v"], resident["prev_cu"],
+                               resident.get("stats"))
+        if rm.dtype != torch.int64 or rm.ndim != 2 or rm.shape[0] != G or not rm.is_contiguous():
+            raise ValueError("the resident map must be contiguous [G, positions] int64")
+        if pk.shape != pv.shape or pk.ndim != 2 or pk.shape[1] != D or pk.dtype != src_k.dtype \
+                or pcu.dtype != torch.int32 or pcu.shape != (G + 1,) or int(resident["epoch"]) < 1:
+            raise ValueError("prev_k/prev_v [capacity, D] and prev_cu [G + 1] int32 must match, epoch >= 1")
+        if st is not None and (st.dtype != torch.int64 or st.shape != (2,)):
+            raise ValueError("resident stats must be [2] int64")
+        _require_contiguous(pk, pv, pcu, what="gather_union")
+        _require_device(rm, pk, pv, pcu, st, what="gather_union")
     with on_device(dev):
-        check(hip().tw_gather_union(sk, sv, src_k.shape[0], entry_row0, entry_row_step, ptr(rows), rows.stride(0),
-                                    ptr(row_counts), G, max_count, ptr(cur_k), ptr(cur_v), D, src_k.element_size(),
-                                    dst_k.shape[0], ptr(dst_k), ptr(dst_v), ptr(cu_seqlens), ptr(error_flag),
-                                    stream_handle(dev)), "gather_union")
+        if resident is None:
+            check(hip().tw_gather_union(sk, sv, src_k.shape[0], entry_row0, entry_row_step, ptr(rows),
+                                        rows.stride(0), ptr(row_counts), G, max_count, ptr(cur_k), ptr(cur_v), D,
+                                        src_k.element_size(), dst_k.shape[0], ptr(dst_k), ptr(dst_v),
+                                        ptr(cu_seqlens), ptr(error_flag), stream_handle(dev)), "gather_union")
+        else:
+            check(hip().tw_gather_union_resident(
+                sk, sv, src_k.shape[0], entry_row0, entry_row_step, ptr(rows), rows.stride(0), ptr(row_counts), G,
+                max_count, ptr(cur_k), ptr(cur_v), D, src_k.element_size(), dst_k.shape[0], ptr(dst_k),
+                ptr(dst_v), ptr(cu_seqlens), ptr(error_flag), ptr(rm), rm.shape[1], int(resident["epoch"]),
+                ptr(pk), ptr(pv), ptr(pcu), pk.shape[0], ptr(st), stream_handle(dev)), "gather_union_resident")
 
 
 def gather_heads(

@@ -340,6 +340,10 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
                                  and self.block_size == 16 and self.geometry.head_dim == 128
                                  and self.dtype in (torch.float16, torch.bfloat16)
                                  and self.num_query_heads_per_kv <= 8)
+        # ... and on the reference's own GQA-group path (update_layer_gqa_group_ragged),
+        # where it lives in the reference: each layer's previous packed union
+        # stays in HBM and rows it holds are copied from there
+        self._gqa_resident: dict[int, dict] = {}
         self.matched_budget_fraction = float(matched_budget_fraction)
         self.budget_mode = budget_mode
         self.gqa_groupwise_execution = bool(gqa_groupwise_execution)
@@ -657,16 +661,20 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
         cur_k = torch.cat([k[0, 0] for k in key_states], dim=0).contiguous()
         cur_v = torch.cat([v[0, 0] for v in value_states], dim=0).contiguous()
         cu = torch.empty((G + 1,), dtype=torch.int32, device=self.device)
+        flat_k, flat_v = self._flat_union_keys, self._flat_union_values
         start = self._phase_start()
         if self.post_selection_pipeline and self.kv_residency == "host":
             cu_host = self._pipelined_union_gather(entries, state, cur_k, cur_v)
             cu.copy_(cu_host.to(torch.int32), non_blocking=True)
         elif self._consecutive(entries):
+            resident = None
+            if self.previous_token_resident_cache and self.kv_residency == "host":
+                flat_k, flat_v, cu, resident = self._gqa_resident_buffers(entries, old_length)
             kernels.gather_union(self._key_rows, self._value_rows, state["rows"], state["counts"], cur_k, cur_v,
-                                 self._flat_union_keys.view(-1, D), self._flat_union_values.view(-1, D), cu,
+                                 flat_k.view(-1, D), flat_v.view(-1, D), cu,
                                  entry_row0=self.geometry.row(entries[0], 0),
                                  entry_row_step=self.geometry.max_cache_len, max_count=state["max_count"],
-                                 error_flag=self._gather_error)
+                                 error_flag=self._gather_error, resident=resident)
         else:
             raise ValueError("GQA group execution needs the consecutive entries of one layer")
         self._phase_end("gather", start)
@@ -681,7 +689,43 @@ class TwilightMatchedBudgetOffloadedCache(QuestTopKOffloadedCache):
             self.metrics["cache_update_calls"] += 1
             self.metrics["attention_valid_tokens_total"] += total
             self.metrics["gather_bytes"] += 2 * (total - G) * D * cur_k.element_size()
-        return self._flat_union_keys[:total], self._flat_union_values[:total], cu, max(lengths), lengths
+        return flat_k[:total], flat_v[:total], cu, max(lengths), lengths
+
+    def _gqa_resident_buffers(self, entries: Sequence[int], old_length: int):
+        """This layer's packed-union buffers of the resident GQA-group path: two
+        alternating by the length's parity (this step packs into one while the
+        previous step's stays readable), their cu_seqlens, the position map
+        and the stats; the gather's resident arguments."""
+        G, D = len(entries), self.geometry.head_dim
+        layer = entries[0] // G
+        st = self._gqa_resident.get(layer)
+        if st is None:
+            R = self.num_query_heads_per_kv
+            b0 = max(1, math.ceil(self.candidate_token_budget / self.block_size))
+            per_group = min(self.geometry.max_cache_len,
+                            self.sink_tokens + R * b0 * self.block_size + self.recent_tokens) + 1
+            cap = G * per_group
+            st = {"k": [torch.empty((cap, 1, D), dtype=self.dtype, device=self.device) for _ in range(2)],
+                  "v": [torch.empty((cap, 1, D), dtype=self.dtype, device=self.device) for _ in range(2)],
+                  "cu": [torch.zeros((G + 1,), dtype=torch.int32, device=self.device) for _ in range(2)],
+                  "map": torch.full((G, self.geometry.max_cache_len), -1, dtype=torch.int64, device=self.device),
+                  "stats": torch.zeros((2,), dtype=torch.int64, device=self.device)}
+            self._gqa_resident[layer] = st
+        par = old_length & 1
+        resident = dict(map=st["map"], epoch=old_length, prev_k=st["k"][1 - par].view(-1, D),
+                        prev_v=st["v"][1 - par].view(-1, D), prev_cu=st["cu"][1 - par], stats=st["stats"])
+        return st["k"][par], st["v"][par], st["cu"][par], resident
+
+    def resident_stats(self) -> dict[str, int]:
+        """Rows read from the HBM resident cache vs. all union rows, over the
+        fused decode and the GQA-group path (cumulative; synchronizes the
+        device).  The keys are the Quest cache's, whose counts are pages."""
+        out = super().resident_stats()
+        hits, rows = out["resident_hit_pages"], out["union_pages"]
+        for st in self._gqa_resident.values():
+            h, r = st["stats"].tolist()
+            hits, rows = hits + int(h), rows + int(r)
+        return {"resident_hit_pages": hits, "union_pages": rows}
 
     # ------------------------------------------------------------ fast path
     def decode_layer(self, *, queries: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
