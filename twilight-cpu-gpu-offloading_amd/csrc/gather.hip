@@ -197,7 +197,7 @@ __global__ __launch_bounds__(256) void gather_union_resident_kernel(
     }
     const int pos = rows[static_cast<int64_t>(g) * rows_stride + i];
     const int64_t sr = row0 + pos;
-    if (sr < 0 || sr >= src_row_limit || pos >= map_stride) {
+    if (sr < 0 || sr >= src_row_limit || pos < 0 || pos >= map_stride) {
       if (error_flag != nullptr) *error_flag = 1;
       continue;
     }
