@@ -1417,6 +1417,10 @@ def run_tpot(args, dev) -> int:
         variants[1:1] = [("sparse_graph_resident", args.budget_pages, True, True)]
         variants[4:4] = [("sparse_hf_eager_resident", args.budget_pages, False, True)]
         variants.append(("twilight_graph_resident", None, True, True))
+        # the reference's own decode path for its resident cache: the HF forward
+        # through update_layer_gqa_group_ragged (GQA-group packing + varlen attention)
+        variants.append(("twilight_gqa_hf_eager", None, False, False))
+        variants.append(("twilight_gqa_hf_eager_resident", None, False, True))
     if args.tpot_only is not None:
         variants = [v for v in variants if v[0] == args.tpot_only]
         if not variants:
@@ -1429,6 +1433,8 @@ def run_tpot(args, dev) -> int:
             flags = dict(previous_token_resident_cache=True, layer_batched_selection=True,
                          gqa_groupwise_execution=True, cpu_flat_gather=True, direct_attention_layout=True,
                          gather_h2d_chunks=1) if resident else {}
+            if "_gqa_" in label and not resident:
+                flags = dict(layer_batched_selection=True, gqa_groupwise_execution=True)
             cache = TwilightMatchedBudgetOffloadedCache.from_llama_model(
                 model, max_cache_len=ctx + n_dec + 8, kv_residency=residency, candidate_token_budget=4096,
                 top_p=0.95, budget_mode="dynamic", update_metadata_on_decode=graph, **flags)
