@@ -643,9 +643,11 @@ __global__ __launch_bounds__(kBlock) void int4_qk_positions_kernel(QkArgs a, con
 // Deterministic exp of x <= 0 (the definition the CPU oracle shares):
 // x < -28 -> 0; t = x*log2(e), n = rint(t), f = t - n, degree-6 Taylor
 // polynomial of 2^f in Horner form, scaled by 2^n.
+// Written without a branch (the argument is replaced by 0 where the result
+// is 0), so that a thread's several calls interleave.
 __device__ __forceinline__ float det_exp(float x) {
-  if (!(x >= -28.0f)) return 0.0f;
-  const float t = x * 1.44269504088896341f;
+  const bool ok = x >= -28.0f;  // false for NaN
+  const float t = (ok ? x : 0.0f) * 1.44269504088896341f;
   const float n = __builtin_rintf(t);
   const float f = t - n;
   float p = 1.54035303933816e-4f;
@@ -655,7 +657,7 @@ __device__ __forceinline__ float det_exp(float x) {
   p = p * f + 2.40226506959101e-1f;
   p = p * f + 6.93147180559945e-1f;
   p = p * f + 1.0f;
-  return __builtin_ldexpf(p, static_cast<int>(n));
+  return ok ? __builtin_ldexpf(p, static_cast<int>(n)) : 0.0f;
 }
 __device__ __forceinline__ uint64_t mass_of(float logit, float lmax) {
   return static_cast<uint64_t>(det_exp(logit - lmax) * 1099511627776.0f);  // * 2^40, truncated
@@ -718,6 +720,8 @@ struct TopShared {
   float fred[kW];
   int ires[4];
   unsigned long long lres[2];
+  int fp_i[4];                 // block_top_p_fast: the first wavefront's results
+  unsigned long long fp_l[2];
 };
 
 __device__ __forceinline__ uint64_t shfl_down_u64(uint64_t v, int o) {
@@ -1406,17 +1410,20 @@ __device__ void build_token_union(const SelectArgs& s, int g, uint32_t* bits, in
 // Fast path of block_top_mass for a row whose key range [kmin, kmax] is
 // known, with the top-p threshold found on the way: one pass of kFastBins
 // bins linear in the value over that range accumulates each bin's count and
-// integer mass (the caller has cleared both and the staging counter); every
-// wavefront then reads all bins (8 per lane), takes the total mass Z and the
-// threshold need = ceil(p24 * Z / 2^24) from them, and finds the bin where
-// the mass of the bins above it falls short of need and with it reaches it.
-// At most 64 keys of that bin are staged and every wavefront ranks them by
-// (key desc, index asc) with readlane, summing the masses ranked ahead of
-// each: the key whose own mass crosses the rest of need ends the selection.
-// Two barriers.  Returns false -- block-uniformly, with the bins dirty --
-// when the range is not finite and positive, need is 0 (no mass or p24 = 0)
-// or the boundary bin holds more than 64 keys; on true, *taken and *count
-// are what block_top_mass gives for that need.
+// integer mass (the caller has cleared both and the staging counter); the
+// first wavefront then reads all bins (8 per lane), takes the total mass Z
+// and the threshold need = ceil(p24 * Z / 2^24) from them, and finds the bin
+// where the mass of the bins above it falls short of need and with it
+// reaches it.  At most 64 keys of that bin are staged, and the first
+// wavefront ranks them by (key desc, index asc), summing the masses ranked
+// ahead of each: the key whose own mass crosses the rest of need ends the
+// selection.  Work that is the same for the whole row runs in one wavefront
+// (the others wait at the barrier that hands its result over), since the
+// block's wavefronts would otherwise issue it twice on each SIMD.  Four
+// barriers.  Returns false -- block-uniformly, with the bins dirty -- when the
+// range is not finite and positive, need is 0 (no mass or p24 = 0) or the
+// boundary bin holds more than 64 keys; on true, *taken and *count are what
+// block_top_mass gives for that need.
 template <int KPT, int NT>
 __device__ bool block_top_p_fast(const uint32_t (&key)[KPT], const uint64_t (&mass)[KPT], int N, uint32_t p24,
                                  uint32_t kmin, uint32_t kmax, TopShared<NT>& sh, uint32_t* taken_out,
@@ -1426,6 +1433,7 @@ __device__ bool block_top_p_fast(const uint32_t (&key)[KPT], const uint64_t (&ma
   static_assert(kBpl % 8 == 0, "whole 16-byte count and mass reads per lane");
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
+  const bool first_wave = tid < kWave;
   const int i0 = KPT * tid;
   const float vmin = key_value(kmin);
   const float vmax = key_value(kmax);
@@ -1439,77 +1447,90 @@ __device__ bool block_top_p_fast(const uint32_t (&key)[KPT], const uint64_t (&ma
   for (int j = 0; j < KPT; ++j) {
     const int b = static_cast<int>((key_value(key[j]) - vmin) * scale);
     bin[j] = (i0 + j < N) ? (b < kBins - 1 ? b : kBins - 1) : -1;
-    if (bin[j] >= 0) {
-      atomicAdd(&sh.sel.hist[bin[j]], 1u);
-      if (mass[j] != 0) atomicAdd(&sh.bin_mass[bin[j]], static_cast<unsigned long long>(mass[j]));
-    }
+  }
+  // no branch: keys past the row count into bin kBins, which nothing reads
+  // (the bins hold kLinBins + 64 > kBins entries)
+  static_assert(kBins < kLinBins + 64, "a spare bin");
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const int b = bin[j] >= 0 ? bin[j] : kBins;
+    atomicAdd(&sh.sel.hist[b], 1u);
+    atomicAdd(&sh.bin_mass[b], static_cast<unsigned long long>(mass[j]));
   }
   __syncthreads();
-  uint32_t hc[kBpl];
-  uint64_t hm[kBpl];
-  {
-    const uint4* c4 = reinterpret_cast<const uint4*>(sh.sel.hist) + (kBpl / 4) * lane;
+  if (first_wave) {
+    uint32_t hc[kBpl];
+    uint64_t hm[kBpl];
+    {
+      const uint4* c4 = reinterpret_cast<const uint4*>(sh.sel.hist) + (kBpl / 4) * lane;
 #pragma unroll
-    for (int q = 0; q < kBpl / 4; ++q) {
-      const uint4 v = c4[q];
-      hc[4 * q] = v.x;
-      hc[4 * q + 1] = v.y;
-      hc[4 * q + 2] = v.z;
-      hc[4 * q + 3] = v.w;
+      for (int q = 0; q < kBpl / 4; ++q) {
+        const uint4 v = c4[q];
+        hc[4 * q] = v.x;
+        hc[4 * q + 1] = v.y;
+        hc[4 * q + 2] = v.z;
+        hc[4 * q + 3] = v.w;
+      }
+      const ulonglong2* m2 = reinterpret_cast<const ulonglong2*>(sh.bin_mass) + (kBpl / 2) * lane;
+#pragma unroll
+      for (int q = 0; q < kBpl / 2; ++q) {
+        const ulonglong2 v = m2[q];
+        hm[2 * q] = v.x;
+        hm[2 * q + 1] = v.y;
+      }
     }
-    const ulonglong2* m2 = reinterpret_cast<const ulonglong2*>(sh.bin_mass) + (kBpl / 2) * lane;
+    uint64_t tm = 0;
+    uint32_t tc = 0u;
 #pragma unroll
-    for (int q = 0; q < kBpl / 2; ++q) {
-      const ulonglong2 v = m2[q];
-      hm[2 * q] = v.x;
-      hm[2 * q + 1] = v.y;
+    for (int b = 0; b < kBpl; ++b) {
+      tm += hm[b];
+      tc += hc[b];
+    }
+    const uint64_t pm = wave_prefix_sum_u64(tm);
+    const uint64_t z = (static_cast<uint64_t>(readlane_u32(static_cast<uint32_t>(pm >> 32), kWave - 1)) << 32) |
+                       readlane_u32(static_cast<uint32_t>(pm), kWave - 1);
+    const uint64_t sm = z - pm + tm;  // mass of the bins of lanes >= this one
+    const uint32_t sc = wave_suffix_sum_u32(tc);
+    const uint64_t need = top_p_threshold(p24, z);
+    // lanes 0 .. L have a suffix mass >= need (need == 0: any lane; unused)
+    const uint64_t bl = __ballot(sm >= need);
+    const int L = 63 - __clzll(static_cast<long long>(bl));
+    uint64_t acc = sm - tm;     // mass of the bins above this lane's
+    uint32_t cacc = sc - tc;    // and their keys
+    int bsel = 0;
+    uint32_t cnt = 0u;
+    bool found = false;
+#pragma unroll
+    for (int b = kBpl - 1; b >= 0; --b) {
+      const bool hit = !found && need <= acc + hm[b];
+      bsel = hit ? b : bsel;
+      cnt = hit ? hc[b] : cnt;
+      acc += (found || hit) ? 0ull : hm[b];
+      cacc += (found || hit) ? 0u : hc[b];
+      found = found || hit;
+    }
+    const int bnd = kBpl * L + static_cast<int>(readlane_u32(static_cast<uint32_t>(bsel), L));
+    const uint64_t above = (static_cast<uint64_t>(readlane_u32(static_cast<uint32_t>(acc >> 32), L)) << 32) |
+                           readlane_u32(static_cast<uint32_t>(acc), L);
+    // (lane reads ahead of the lane-0 branch: inside it, the compiler could
+    // compute the per-lane values for lane 0 alone)
+    const uint32_t c_above = readlane_u32(cacc, L);
+    const uint32_t ccount = readlane_u32(cnt, L);
+    if (lane == 0) {
+      sh.fp_l[0] = need;
+      sh.fp_l[1] = above;
+      sh.fp_i[0] = bnd;
+      sh.fp_i[1] = static_cast<int>(c_above);
+      sh.fp_i[2] = static_cast<int>(ccount);
     }
   }
-  uint64_t tm = 0;
-  uint32_t tc = 0u;
-#pragma unroll
-  for (int b = 0; b < kBpl; ++b) {
-    tm += hm[b];
-    tc += hc[b];
-  }
-  const uint64_t pm = wave_prefix_sum_u64(tm);
-  const uint64_t z = (static_cast<uint64_t>(readlane_u32(static_cast<uint32_t>(pm >> 32), kWave - 1)) << 32) |
-                     readlane_u32(static_cast<uint32_t>(pm), kWave - 1);
-  const uint64_t sm = z - pm + tm;  // mass of the bins of lanes >= this one
-  const uint32_t sc = wave_suffix_sum_u32(tc);
-  const uint64_t need = top_p_threshold(p24, z);
-  if (need == 0) {
-    __syncthreads();  // every wavefront is done with the bins
-    return false;
-  }
-  // lanes 0 .. L have a suffix mass >= need
-  const uint64_t bl = __ballot(sm >= need);
-  const int L = 63 - __clzll(static_cast<long long>(bl));
-  uint64_t acc = sm - tm;     // mass of the bins above this lane's
-  uint32_t cacc = sc - tc;    // and their keys
-  int bsel = 0;
-  uint32_t cnt = 0u;
-  uint64_t bmass = 0;
-  bool found = false;
-#pragma unroll
-  for (int b = kBpl - 1; b >= 0; --b) {
-    const bool hit = !found && need <= acc + hm[b];
-    bsel = hit ? b : bsel;
-    cnt = hit ? hc[b] : cnt;
-    bmass = hit ? hm[b] : bmass;
-    acc += (found || hit) ? 0ull : hm[b];
-    cacc += (found || hit) ? 0u : hc[b];
-    found = found || hit;
-  }
-  const int bnd = kBpl * L + static_cast<int>(readlane_u32(static_cast<uint32_t>(bsel), L));
-  const uint64_t above = (static_cast<uint64_t>(readlane_u32(static_cast<uint32_t>(acc >> 32), L)) << 32) |
-                         readlane_u32(static_cast<uint32_t>(acc), L);
-  const uint32_t c_above = readlane_u32(cacc, L);
-  const uint32_t ccount = readlane_u32(cnt, L);
-  if (ccount > static_cast<uint32_t>(kWave)) {
-    __syncthreads();
-    return false;
-  }
+  __syncthreads();  // (the first wavefront is also done with the bins)
+  const uint64_t need = sh.fp_l[0];
+  const uint64_t above = sh.fp_l[1];
+  const int bnd = sh.fp_i[0];
+  const uint32_t c_above = static_cast<uint32_t>(sh.fp_i[1]);
+  const uint32_t ccount = static_cast<uint32_t>(sh.fp_i[2]);
+  if (need == 0 || ccount > static_cast<uint32_t>(kWave)) return false;
   const uint64_t need2 = need - above;  // 1 .. the bin's mass
   uint32_t t = 0u;
 #pragma unroll
@@ -1531,40 +1552,48 @@ __device__ bool block_top_p_fast(const uint32_t (&key)[KPT], const uint64_t (&ma
     }
   }
   __syncthreads();
-  // every wavefront ranks the staged keys (lane m holds key m) against all
-  // of them, read from LDS by every lane at once (broadcast reads, four in
-  // flight): one 64-bit compare each, no branch (slots past ccount hold
-  // key 0, which never outranks a key, so their stale masses never count)
-  const bool live = static_cast<uint32_t>(lane) < ccount;
-  const unsigned long long c = sh.sel.cpair[lane];
-  const uint64_t cm = live ? static_cast<uint64_t>(sh.cmass[lane]) : 0ull;
-  uint64_t before = 0;
-  uint32_t rank = 0u;
-  for (int m = 0; m < static_cast<int>(ccount); m += 4) {
-    unsigned long long o[4];
-    uint64_t om[4];
+  if (first_wave) {
+    // lane m ranks staged key m against all of them, read from LDS by every
+    // lane at once (broadcast reads, four in flight): one 64-bit compare
+    // each, no branch (slots past ccount hold key 0, which never outranks a
+    // key, so their stale masses never count)
+    const bool live = static_cast<uint32_t>(lane) < ccount;
+    const unsigned long long c = sh.sel.cpair[lane];
+    const uint64_t cm = live ? static_cast<uint64_t>(sh.cmass[lane]) : 0ull;
+    uint64_t before = 0;
+    uint32_t rank = 0u;
+    for (int m = 0; m < static_cast<int>(ccount); m += 4) {
+      unsigned long long o[4];
+      uint64_t om[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      o[u] = sh.sel.cpair[m + u];
-      om[u] = sh.cmass[m + u];
+      for (int u = 0; u < 4; ++u) {
+        o[u] = sh.sel.cpair[m + u];
+        om[u] = sh.cmass[m + u];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool ahead = o[u] > c;
+        before += ahead ? om[u] : 0ull;
+        rank += ahead ? 1u : 0u;
+      }
     }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const bool ahead = o[u] > c;
-      before += ahead ? om[u] : 0ull;
-      rank += ahead ? 1u : 0u;
+    const bool cross = live && before < need2 && need2 <= before + cm;
+    const uint64_t cb = __ballot(cross);
+    // (need2 <= the bin's mass, so some key crosses; all of them otherwise)
+    const uint32_t needed = cb != 0ull ? readlane_u32(rank, first_lane(cb)) + 1u : ccount;
+    const uint64_t tmk = __ballot(live && rank < needed);
+    if (lane == 0) {
+      sh.fp_l[0] = tmk;
+      sh.fp_i[3] = static_cast<int>(needed);
     }
   }
-  const bool cross = live && before < need2 && need2 <= before + cm;
-  const uint64_t cb = __ballot(cross);
-  // (need2 <= the bin's mass, so some key crosses; all of them otherwise)
-  const uint32_t needed = cb != 0ull ? readlane_u32(rank, first_lane(cb)) + 1u : ccount;
-  const uint64_t tmk = __ballot(live && rank < needed);
+  __syncthreads();
+  const uint64_t tmk = sh.fp_l[0];
+  const uint32_t needed = static_cast<uint32_t>(sh.fp_i[3]);
 #pragma unroll
   for (int j = 0; j < KPT; ++j) t |= (((inbin >> j) & 1u) && ((tmk >> cslot[j]) & 1ull)) ? (1u << j) : 0u;
   *taken_out = t;
   *count_out = static_cast<int>(c_above + needed);
-  (void)bmass;
   return true;
 }
 
@@ -1704,7 +1733,7 @@ __global__ __launch_bounds__(NT) void twilight_topp_kernel(SelectArgs s) {
   const int i0 = KPT * static_cast<int>(threadIdx.x);
 #pragma unroll
   for (int j = 0; j < KPT; ++j) {
-    mass[j] = (i0 + j < N) ? mass_of(key_value(key[j]), lmax) : 0ull;
+    mass[j] = mass_of((i0 + j < N) ? key_value(key[j]) : -INFINITY, lmax);  // 0 past the row
     local += mass[j];
   }
   const uint64_t z = block_sum_u64<NT>(local, sh.red64);
@@ -2261,7 +2290,7 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_topp_head_kernel(HeadAr
   uint64_t local = 0;
 #pragma unroll
   for (int j = 0; j < KPB; ++j) {
-    mass[j] = (c0 + j < N) ? mass_of(key_value(lkey[j]), lmax) : 0ull;
+    mass[j] = mass_of((c0 + j < N) ? key_value(lkey[j]) : -INFINITY, lmax);  // 0 past the row
     local += mass[j];
   }
   uint32_t taken;
