@@ -29,7 +29,9 @@ constexpr int kNormVec = 4;
 // of bf16(w * bf16(a * r)) to put(i, chunk).  Thread t owns chunks t + c *
 // kNormBlock, c < NV; the sum of squares runs over its chunks in order, then
 // a wave reduction, then the waves in order, so every block computing the
-// same row gets the same bits, whatever NV covers the row.
+// same row gets the same bits, whatever NV covers the row.  In a block of
+// more than kNormBlock threads the first kNormBlock do the work and the rest
+// only meet the barrier in finish().
 template <typename DT, int NV>
 struct NormRow {
   using S = typename DT::storage;
@@ -45,7 +47,8 @@ struct NormRow {
     has_delta = dr != nullptr;
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
-      const int i = threadIdx.x + c * kNormBlock;
+      // (a thread past kNormBlock, in a larger block, reads chunk 0 and adds nothing)
+      const int i = threadIdx.x < kNormBlock ? static_cast<int>(threadIdx.x) + c * kNormBlock : nv;
       const int j = i < nv ? i : 0;
       hv[c] = hr[j];
       dv[c] = dr != nullptr ? dr[j] : make_uint4(0u, 0u, 0u, 0u);
@@ -76,7 +79,7 @@ struct NormRow {
         x[c][2 * e + 1] = b;
         ow[e] = static_cast<uint32_t>(from_f32(DT{}, a)) | (static_cast<uint32_t>(from_f32(DT{}, b)) << 16);
       }
-      const bool in = threadIdx.x + c * kNormBlock < nv;
+      const bool in = threadIdx.x < kNormBlock && threadIdx.x + c * kNormBlock < nv;
       if (in) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc += x[c][e] * x[c][e];
@@ -84,7 +87,7 @@ struct NormRow {
       }
     }
     acc = wave_sum_f32(acc);
-    if (lane_id() == 0) s_part[threadIdx.x / kWave] = acc;
+    if (lane_id() == 0 && threadIdx.x < kNormBlock) s_part[threadIdx.x / kWave] = acc;
     __syncthreads();
     float total = 0.0f;
 #pragma unroll
@@ -92,7 +95,7 @@ struct NormRow {
     const float r = 1.0f / sqrtf(total / static_cast<float>(H) + eps);
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
-      if (threadIdx.x + c * kNormBlock >= nv) continue;
+      if (threadIdx.x >= kNormBlock || threadIdx.x + c * kNormBlock >= nv) continue;
       const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
       uint32_t ow[4];
 #pragma unroll
@@ -175,10 +178,11 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const typename DT::storag
 
 // y[n] = x . W[n, :] (+ bias[n]) for one row x [K] and W [N][K] row-major
 // (nn.Linear's weight), the decode token's projections.  x is staged in LDS
-// once per block; wave w of a block owns rows (block * 4 + w) * RPW ..; lane
-// l reads the 16-byte chunks l, l + 64, ... of each of its rows, 16 / RPW
-// chunks of every row in flight per step, and accumulates them with
-// v_dot2_f32_{bf16,f16} in fp32; a wave reduction ends each row.
+// once per block; wave w of a block owns RPW rows; lane l reads the 16-byte
+// chunks l, l + 64, ... of each of its rows, 16 / RPW chunks of every row (8
+// with one row) in flight per step, and accumulates them in increasing order
+// with v_dot2_f32_{bf16,f16} in fp32; a wave reduction ends each row.  The
+// sums do not depend on RPW.
 constexpr int kGemvBlock = 256;
 
 template <typename DT>
@@ -208,10 +212,12 @@ __device__ __forceinline__ float dot8(const uint4& w, const uint4& x, float acc)
 
 // Prologue: x given, or x = RMSNorm(h_in + delta) computed by every block
 // (block 0 stores h_in + delta to h_out).  Epilogue: y[n] = bf16(x . W[n] +
-// bias[n]); or RoPE pairs -- the wave's rows are (head * D + i, head * D + i +
-// D/2) of a concatenated q/k/v projection, rotated as tw_rope_qk for the q and
-// k heads (q also to q32); or SiLU pairs -- rows (i, I + i) of a concatenated
-// gate/up projection, y[i] = bf16(bf16(silu(gate)) * up).
+// bias[n]); or RoPE pairs -- rows (head * D + i, head * D + i + D/2) of a
+// concatenated q/k/v projection, rotated as tw_rope_qk for the q and k heads
+// (q also to q32); or SiLU pairs -- rows (i, I + i) of a concatenated
+// gate/up projection, y[i] = bf16(bf16(silu(gate)) * up).  With one row a
+// wave, the two rows of a pair belong to waves 2j and 2j + 1 of a block and
+// meet in LDS.
 constexpr int kProX = 0, kProNorm = 1;
 constexpr int kEpiPlain = 0, kEpiRope = 1, kEpiSilu = 2;
 
@@ -237,17 +243,23 @@ struct GemvArgs {
 // NV: 16-byte chunks of x per thread held in registers while the first
 // weight loads are issued (x of up to NV * 2048 elements; longer x is staged
 // after them).
-template <typename DT, int RPW, int PRO, int EPI, int NV>
-__global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::storage> a) {
-  static_assert(EPI == kEpiPlain || RPW % 2 == 0, "paired epilogues take rows two by two");
+template <typename DT, int RPW, int PRO, int EPI, int NV, int NTB>
+__global__ __launch_bounds__(NTB) void gemv_kernel(GemvArgs<typename DT::storage> a) {
+  constexpr int kW = NTB / kWave;
+  static_assert(NTB % kNormBlock == 0, "the norm runs in the first kNormBlock threads");
+  constexpr bool kWavePairs = EPI != kEpiPlain && RPW == 1;  // a pair's rows in two waves
+  static_assert(EPI == kEpiPlain || RPW % 2 == 0 || RPW == 1, "paired epilogues: rows two by two, or wave pairs");
   extern __shared__ __align__(16) uint4 xs[];
-  __shared__ float s_part[kGemvBlock / kWave];
+  __shared__ float s_part[kW];
+  __shared__ float s_pair[kW];
   const int K = a.K;
   const int kc = K / 8;  // 16-byte chunks per row
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
-  const int unit0 = (blockIdx.x * (kGemvBlock / kWave) + wave) * (EPI == kEpiPlain ? RPW : RPW / 2);
+  // units: rows (plain) or row pairs; this wave's first unit
   const int units = EPI == kEpiPlain ? a.N : a.N / 2;
+  const int unit0 = kWavePairs ? blockIdx.x * (kW / 2) + wave / 2
+                               : (blockIdx.x * kW + wave) * (EPI == kEpiPlain ? RPW : RPW / 2);
   // the wave's rows
   int rows[RPW];
 #pragma unroll
@@ -256,7 +268,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
       const int n = unit0 + r;
       rows[r] = n < a.N ? n : a.N - 1;
     } else {
-      int p = unit0 + r / 2;
+      int p = kWavePairs ? unit0 : unit0 + r / 2;
       p = p < units ? p : units - 1;
       int na, nb;
       if (EPI == kEpiRope) {
@@ -268,7 +280,7 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
         na = p;
         nb = p + units;
       }
-      rows[r] = (r & 1) ? nb : na;
+      rows[r] = ((kWavePairs ? wave : r) & 1) ? nb : na;
     }
   }
   const uint4* w4 = reinterpret_cast<const uint4*>(a.W);
@@ -276,11 +288,11 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
 #pragma unroll
   for (int r = 0; r < RPW; ++r) rowp[r] = w4 + static_cast<int64_t>(rows[r]) * kc;
   // A step covers chunks c + u * kWave, u < U, of every row: U * RPW
-  // 16-byte loads per lane (8 KB per wave) are in flight before any is
-  // used; the first step's are issued right after x's (or the norm's
-  // inputs'), so x is ready while they arrive.  Each lane sums its chunks in
-  // increasing order.
-  constexpr int U = 16 / RPW;
+  // 16-byte loads per lane are in flight before any is used; the first
+  // step's are issued right after x's (or the norm's inputs'), so x is ready
+  // while they arrive.  Chunks past the row read its last chunk again (a
+  // line the step already reads).
+  constexpr int U = RPW == 1 ? 8 : 16 / RPW;
   int c = lane;
   uint4 wv[U][RPW];
   auto load_step = [&](int c0) {
@@ -288,37 +300,52 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
     for (int u = 0; u < U; ++u) {
       const int idx = c0 + u * kWave;
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) wv[u][r] = load_stream(rowp[r] + (idx < kc ? idx : 0));
+      for (int r = 0; r < RPW; ++r) wv[u][r] = load_stream(rowp[r] + (idx < kc ? idx : kc - 1));
     }
   };
   NormRow<DT, NV> nr;
   uint4 xr[NV];
   const uint4* x4 = reinterpret_cast<const uint4*>(a.x);
-  const bool x_in_regs = kc <= NV * kGemvBlock;
+  const bool x_in_regs = kc <= NV * NTB;
   if (PRO == kProNorm) {
     nr.load(a.h_in, a.delta, a.norm_w, K);
   } else if (x_in_regs) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      const int i = static_cast<int>(threadIdx.x) + v * kGemvBlock;
+      const int i = static_cast<int>(threadIdx.x) + v * NTB;
       xr[v] = x4[i < kc ? i : 0];
     }
   }
   load_step(c);
+  // RoPE: the position and the four table entries of the wave's (first)
+  // pair, read while the weights stream (every lane reads the same addresses)
+  float rc_i = 0.0f, rs_i = 0.0f, rc_j = 0.0f, rs_j = 0.0f;
+  if (EPI == kEpiRope) {
+    const int half = a.D / 2;
+    int p = unit0;
+    p = p < units ? p : units - 1;
+    const int i = p - (p / half) * half;
+    const int64_t t = *a.pos * a.D;
+    rc_i = to_f32(DT{}, a.cos_t[t + i]);
+    rs_i = to_f32(DT{}, a.sin_t[t + i]);
+    rc_j = to_f32(DT{}, a.cos_t[t + i + half]);
+    rs_j = to_f32(DT{}, a.sin_t[t + i + half]);
+  }
   if (PRO == kProNorm) {
     nr.finish(a.eps, K, (blockIdx.x == 0 && a.delta != nullptr) ? a.h_out : nullptr, s_part,
               [&](int i, const uint4& v) { xs[i] = v; });
   } else if (x_in_regs) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      const int i = static_cast<int>(threadIdx.x) + v * kGemvBlock;
+      const int i = static_cast<int>(threadIdx.x) + v * NTB;
       if (i < kc) xs[i] = xr[v];
     }
   } else {
-    for (int i = threadIdx.x; i < kc; i += kGemvBlock) xs[i] = x4[i];
+    for (int i = threadIdx.x; i < kc; i += NTB) xs[i] = x4[i];
   }
   __syncthreads();
-  if (unit0 >= units) return;
+  // (wave pairs meet at a barrier below: every wave goes on)
+  if (!kWavePairs && unit0 >= units) return;
   float acc[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
@@ -336,11 +363,18 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
     if (c >= kc) break;
     load_step(c);
   }
-  float v[RPW];
+  float v[RPW > 1 ? RPW : 2];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     v[r] = wave_sum_f32(acc[r]);
     v[r] = v[r] + (a.bias != nullptr ? to_f32(DT{}, a.bias[rows[r]]) : 0.0f);
+  }
+  if (kWavePairs) {
+    // the odd wave of a pair hands its row to the even one
+    if (lane == 0) s_pair[wave] = v[0];
+    __syncthreads();
+    if ((wave & 1) != 0 || unit0 >= units) return;
+    v[1] = s_pair[wave + 1];
   }
   if (lane != 0) return;
   if (EPI == kEpiPlain) {
@@ -348,8 +382,9 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
     for (int r = 0; r < RPW; ++r)
       if (unit0 + r < a.N) a.y[unit0 + r] = from_f32(DT{}, v[r]);
   } else {
+    constexpr int kPairs = kWavePairs ? 1 : RPW / 2;
 #pragma unroll
-    for (int q = 0; q < RPW / 2; ++q) {
+    for (int q = 0; q < kPairs; ++q) {
       const int p = unit0 + q;
       if (p >= units) continue;
       const float va = round_to<DT>(v[2 * q]);
@@ -361,12 +396,17 @@ __global__ __launch_bounds__(kGemvBlock) void gemv_kernel(GemvArgs<typename DT::
         const int half = a.D / 2;
         const int head = p / half;
         const int i = p - head * half;
-        const int na = rows[2 * q], nb = rows[2 * q + 1];
+        const int na = head * a.D + i, nb = na + half;
         float ya = va, yb = vb;
         if (head < a.Hq + a.Hk) {
-          const int64_t t = *a.pos * a.D;
-          const float ci = to_f32(DT{}, a.cos_t[t + i]), si = to_f32(DT{}, a.sin_t[t + i]);
-          const float cj = to_f32(DT{}, a.cos_t[t + i + half]), sj = to_f32(DT{}, a.sin_t[t + i + half]);
+          float ci = rc_i, si = rs_i, cj = rc_j, sj = rs_j;  // read for the wave's first pair
+          if (q > 0) {
+            const int64_t t = *a.pos * a.D;
+            ci = to_f32(DT{}, a.cos_t[t + i]);
+            si = to_f32(DT{}, a.sin_t[t + i]);
+            cj = to_f32(DT{}, a.cos_t[t + i + half]);
+            sj = to_f32(DT{}, a.sin_t[t + i + half]);
+          }
           ya = round_to<DT>(round_to<DT>(va * ci) + round_to<DT>(-vb * si));
           yb = round_to<DT>(round_to<DT>(vb * cj) + round_to<DT>(va * sj));
           if (head < a.Hq && a.q32 != nullptr) {
@@ -385,15 +425,21 @@ template <typename DT, int PRO, int EPI, int NV>
 void launch_gemv_nv(const GemvArgs<typename DT::storage>& a, hipStream_t st) {
   const size_t lds = static_cast<size_t>(a.K) * 2;
   const int waves = kGemvBlock / kWave;
-  const bool wide = a.N >= 16384;
-  const int rpw = wide ? 4 : 2;
-  const int units_per_block = waves * (EPI == kEpiPlain ? rpw : rpw / 2);
+  // a given x: one row a wave.  A norm prologue: every block normalises x
+  // itself, and that work grows with the block count, so those blocks hold
+  // two rows a wave (four from 16384 rows); measured on the decode shapes.
+  const int rpw = PRO != kProNorm ? 1 : (a.N >= 16384 ? 4 : 2);
+  const int units_per_block = EPI == kEpiPlain ? waves * rpw : (rpw == 1 ? waves / 2 : waves * rpw / 2);
   const int units = EPI == kEpiPlain ? a.N : a.N / 2;
   const dim3 grid((units + units_per_block - 1) / units_per_block);
-  if (wide)
-    hipLaunchKernelGGL((gemv_kernel<DT, 4, PRO, EPI, NV>), grid, dim3(kGemvBlock), lds, st, a);
-  else
-    hipLaunchKernelGGL((gemv_kernel<DT, 2, PRO, EPI, NV>), grid, dim3(kGemvBlock), lds, st, a);
+  if constexpr (PRO != kProNorm) {
+    hipLaunchKernelGGL((gemv_kernel<DT, 1, PRO, EPI, NV, kGemvBlock>), grid, dim3(kGemvBlock), lds, st, a);
+  } else {
+    if (rpw == 2)
+      hipLaunchKernelGGL((gemv_kernel<DT, 2, PRO, EPI, NV, kGemvBlock>), grid, dim3(kGemvBlock), lds, st, a);
+    else
+      hipLaunchKernelGGL((gemv_kernel<DT, 4, PRO, EPI, NV, kGemvBlock>), grid, dim3(kGemvBlock), lds, st, a);
+  }
 }
 
 // x of up to 4096 elements in two register chunks per thread, else four
