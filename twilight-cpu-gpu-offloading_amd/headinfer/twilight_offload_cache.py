@@ -13,11 +13,15 @@ dynamic budgets -- tw_twilight_select_fused: the Quest score and the INT4
 estimate of every scored row for the group's heads, then one block per head
 for the B0 pages, the exact top-p and the group's union record -- and three
 with matched budgets (the allocation and each head's top-allocated rows in
-one more launch); the attention then reads the record's rows from the slab
-(HBM or zero-copy host) with the decode token's append fused.  Under a
-selection or budget trace (which records the row list), for shapes outside
-the fused kernels, or with matched budgets over more than 8 query heads per
-KV head, the general path runs instead: tw_quest_select (B0 pages + union
+one more launch); more than 8 query heads per KV head run as sub-groups of at
+most 8 whose records are ORed (with matched budgets every sub-group's
+allocation launch reads the counts of all the group's heads).  The attention
+then reads the record's rows from the slab (HBM or zero-copy host) with the
+decode token's append fused.  Under a selection or budget trace (which
+records the row list), for shapes outside the fused kernels (D != 128, pages
+other than 16 rows, more than 8192 candidate pages or B0 tokens), or with
+matched budgets over more than 64 query heads per KV head, the general path
+runs instead: tw_quest_select (B0 pages + union
 plan), tw_twilight_qk, tw_twilight_select (counts, budgets, per-head
 selection, the token union as a row list), then the row attention; both
 attend the same rows.  The update APIs (update_layer_gqa_group_ragged and the
