@@ -1,8 +1,8 @@
 """The fallback branches of the fused Twilight kernels against the oracle.
 
-The fused selection (twilight_select_fused: twilight_head_kernel, and with
-matched budgets twilight_matched_rec_kernel) takes one-pass histogram fast
-paths that give up, block-uniformly, when
+The fused selection (twilight_select_fused: twilight_topp_head_kernel, and
+with matched budgets twilight_matched_rec_kernel) takes one-pass histogram
+fast paths that give up, block-uniformly, when
 
 * the B0 top-k's score keys span no finite positive range, or more than 64
   keys fall in the boundary bin (then block_topk, the digit search);
