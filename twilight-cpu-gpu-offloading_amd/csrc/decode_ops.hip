@@ -306,10 +306,12 @@ __global__ __launch_bounds__(NTB) void gemv_kernel(GemvArgs<typename DT::storage
   NormRow<DT, NV> nr;
   uint4 xr[NV];
   const uint4* x4 = reinterpret_cast<const uint4*>(a.x);
-  const bool x_in_regs = kc <= NV * NTB;
-  if (PRO == kProNorm) {
+  if constexpr (PRO == kProNorm) {
     nr.load(a.h_in, a.delta, a.norm_w, K);
-  } else if (x_in_regs) {
+  } else {
+    // the thread's first NV chunks of x, unconditionally (clamped indices):
+    // loaded under a condition the array went to scratch memory, and its
+    // store there waited for the loads before the weights' were issued
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int i = static_cast<int>(threadIdx.x) + v * NTB;
@@ -334,14 +336,14 @@ __global__ __launch_bounds__(NTB) void gemv_kernel(GemvArgs<typename DT::storage
   if (PRO == kProNorm) {
     nr.finish(a.eps, K, (blockIdx.x == 0 && a.delta != nullptr) ? a.h_out : nullptr, s_part,
               [&](int i, const uint4& v) { xs[i] = v; });
-  } else if (x_in_regs) {
+  } else {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const int i = static_cast<int>(threadIdx.x) + v * NTB;
       if (i < kc) xs[i] = xr[v];
     }
-  } else {
-    for (int i = threadIdx.x; i < kc; i += NTB) xs[i] = x4[i];
+    // x longer than NV chunks a thread: the rest after the weights' loads
+    for (int i = static_cast<int>(threadIdx.x) + NV * NTB; i < kc; i += NTB) xs[i] = x4[i];
   }
   __syncthreads();
   // (wave pairs meet at a barrier below: every wave goes on)
@@ -443,14 +445,17 @@ void launch_gemv_nv(const GemvArgs<typename DT::storage>& a, hipStream_t st) {
 }
 
 // x of up to 4096 elements in two register chunks per thread, else four
-// (the norm prologue takes K <= 8192; plain x longer than 8192 is staged
-// after the first weight loads).
+// (the norm prologue takes K <= 8192), else for a given x eight (16384
+// elements); a given x longer than that is staged past the register chunks
+// after the first weight loads.
 template <typename DT, int PRO, int EPI>
 int launch_gemv(const GemvArgs<typename DT::storage>& a, hipStream_t st) {
   if (a.K <= 2 * 8 * kGemvBlock)
     launch_gemv_nv<DT, PRO, EPI, 2>(a, st);
-  else
+  else if (PRO == kProNorm || a.K <= 4 * 8 * kGemvBlock)
     launch_gemv_nv<DT, PRO, EPI, 4>(a, st);
+  else if constexpr (PRO != kProNorm)
+    launch_gemv_nv<DT, PRO, EPI, 8>(a, st);
   return tw_host::check_launch();
 }
 
