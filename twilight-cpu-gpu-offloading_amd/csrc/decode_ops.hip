@@ -319,20 +319,6 @@ __global__ __launch_bounds__(NTB) void gemv_kernel(GemvArgs<typename DT::storage
     }
   }
   load_step(c);
-  // RoPE: the position and the four table entries of the wave's (first)
-  // pair, read while the weights stream (every lane reads the same addresses)
-  float rc_i = 0.0f, rs_i = 0.0f, rc_j = 0.0f, rs_j = 0.0f;
-  if (EPI == kEpiRope) {
-    const int half = a.D / 2;
-    int p = unit0;
-    p = p < units ? p : units - 1;
-    const int i = p - (p / half) * half;
-    const int64_t t = *a.pos * a.D;
-    rc_i = to_f32(DT{}, a.cos_t[t + i]);
-    rs_i = to_f32(DT{}, a.sin_t[t + i]);
-    rc_j = to_f32(DT{}, a.cos_t[t + i + half]);
-    rs_j = to_f32(DT{}, a.sin_t[t + i + half]);
-  }
   if (PRO == kProNorm) {
     nr.finish(a.eps, K, (blockIdx.x == 0 && a.delta != nullptr) ? a.h_out : nullptr, s_part,
               [&](int i, const uint4& v) { xs[i] = v; });
@@ -401,14 +387,9 @@ __global__ __launch_bounds__(NTB) void gemv_kernel(GemvArgs<typename DT::storage
         const int na = head * a.D + i, nb = na + half;
         float ya = va, yb = vb;
         if (head < a.Hq + a.Hk) {
-          float ci = rc_i, si = rs_i, cj = rc_j, sj = rs_j;  // read for the wave's first pair
-          if (q > 0) {
-            const int64_t t = *a.pos * a.D;
-            ci = to_f32(DT{}, a.cos_t[t + i]);
-            si = to_f32(DT{}, a.sin_t[t + i]);
-            cj = to_f32(DT{}, a.cos_t[t + i + half]);
-            sj = to_f32(DT{}, a.sin_t[t + i + half]);
-          }
+          const int64_t t = *a.pos * a.D;
+          const float ci = to_f32(DT{}, a.cos_t[t + i]), si = to_f32(DT{}, a.sin_t[t + i]);
+          const float cj = to_f32(DT{}, a.cos_t[t + i + half]), sj = to_f32(DT{}, a.sin_t[t + i + half]);
           ya = round_to<DT>(round_to<DT>(va * ci) + round_to<DT>(-vb * si));
           yb = round_to<DT>(round_to<DT>(vb * cj) + round_to<DT>(va * sj));
           if (head < a.Hq && a.q32 != nullptr) {
