@@ -690,7 +690,7 @@ def _sampled(run, budget_s: float, cap: int) -> tuple[float, int]:
 
 
 def quest_oracle_check(w: QuestWorkload, layer: int = 0) -> dict:
-    """The checker of the CPU-baseline leg: every head's pages the timed step
+    """Verification of the CPU-baseline leg: every head's pages the timed step
     selected at `layer` against oracle.topk_sorted(oracle.quest_score(...))
     (bit for bit, quest_offload_cache.py:362-374), and each head's attention
     output within 2e-3 abs + 1e-2 rel of float64 over sink ++ the oracle's
@@ -723,7 +723,7 @@ def quest_oracle_check(w: QuestWorkload, layer: int = 0) -> dict:
             err = max(err, float(e.max()))
     return {"ok": bool(match and att_ok), "selection_match": bool(match), "heads": G * R, "layer": layer,
             "attention_max_abs_err": err,
-            "checker": "oracle.quest_score + oracle.topk_sorted (pages, bit for bit); float64 attention over "
+            "verified_against": "oracle.quest_score + oracle.topk_sorted (pages, bit for bit); float64 attention over "
                        "the oracle's rows"}
 
 
@@ -773,7 +773,7 @@ def cpu_baseline(w: QuestWorkload, seconds: float) -> dict:
 
 
 def twilight_oracle_check(w: "TwilightWorkload", layer: int = 0) -> dict:
-    """The checker of the Twilight CPU-baseline leg: for every group of
+    """Verification of the Twilight CPU-baseline leg: for every group of
     `layer`, the rows the timed step kept (its union record) == the union of
     oracle.twilight_layer, the top-p counts equal, and the union attention
     within 2e-3 abs + 1e-2 rel of float64 over the oracle's rows plus the
@@ -806,7 +806,7 @@ def twilight_oracle_check(w: "TwilightWorkload", layer: int = 0) -> dict:
         err = max(err, float(e.max()))
     return {"ok": bool(union_ok and counts_ok and att_ok), "union_match": union_ok, "top_p_counts_match": counts_ok,
             "groups": G, "layer": layer, "attention_max_abs_err": err,
-            "checker": "oracle.twilight_layer (B0 pages, INT4 QK, exact top-p, allocation, union); float64 "
+            "verified_against": "oracle.twilight_layer (B0 pages, INT4 QK, exact top-p, allocation, union); float64 "
                        "attention over the oracle's rows"}
 
 

@@ -40,7 +40,7 @@ enum tw_status {
   TW_ERANGE = 2,      /* an index is outside its source (gather natives) */
   TW_ENOMEM = 3,      /* workspace too small */
   TW_EHIP = 4,        /* HIP runtime error; see tw_last_hip_error() */
-  TW_EUNSUPPORTED = 5 /* valid request this build does not implement */
+  TW_EUNSUPPORTED = 5 /* valid request this library does not implement */
 };
 
 enum tw_dtype { TW_DTYPE_F16 = 0, TW_DTYPE_BF16 = 1, TW_DTYPE_F32 = 2 };

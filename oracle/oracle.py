@@ -338,7 +338,7 @@ def twilight_layer(q: np.ndarray, page_min: np.ndarray, page_max: np.ndarray, pa
                    block_size: int, b0_pages: int, top_p: float, budget_mode: str = "dynamic",
                    fixed_pages: int = 0, qk_scale: float | None = None, target_total: int | None = None):
     """Twilight selection of one KV group (prepare_layer_selection,
-    twilight_offload_cache.py:996-1614) in this build's defined orders.
+    twilight_offload_cache.py:996-1614) in the orders twilight_oracle.c defines.
 
     q [R, D] fp32; page_min/page_max [P, D] (the P scored pages); packed
     [T, D/2], scale/minimum [T] (storage of dtype).  Returns a dict with the

@@ -1,7 +1,7 @@
 /*
  * twilight_oracle.c -- CPU restatement of the reference's sparse-decode KV
  * arithmetic.  TEST INFRASTRUCTURE ONLY: used by tests/, by smoke() and by
- * bench.py's cpu_baseline leg as the checker / CPU baseline.  Nothing in the
+ * bench.py's cpu_baseline leg, to verify results and as the CPU baseline.  Nothing in the
  * product links or calls it.
  *
  * Scalar, single-threaded, IEEE single precision (x86-64 SSE, built with
@@ -333,7 +333,7 @@ int or_qfix(const float* q, int D, int32_t* Q, int32_t* qs, int* ok) {
 }
 
 /* INT4 QK estimate of one query head (twilight_fused_qk.py:12-55,
- * twilight_offload_cache.py:1197-1261) in this build's defined arithmetic.
+ * twilight_offload_cache.py:1197-1261) in the arithmetic defined here.
  * The reference dequantizes k_d = f32(code_d) * f32(scale) + f32(min)
  * (:40-47) and reduces k . q in an unpinned fp32 order (cuBLAS / tl.sum).
  * Here the dot product is exact: with q in the fixed-point form of or_qfix,
@@ -371,7 +371,7 @@ void or_int4_qk(const float* q, int D, const uint8_t* packed, const void* scale,
 }
 
 /* Top-p count (twilight_exact_top_p_graph.py:19-32; inline
- * twilight_offload_cache.py:1274-1310) in this build's exact definition:
+ * twilight_offload_cache.py:1274-1310) in the exact definition used here:
  *   e_i = det_exp(l_i - max l), mass E_i = floor(e_i * 2^40) (int64),
  *   Z = sum E_i, T = ceil(P24 * Z / 2^24) with P24 = round(top_p * 2^24),
  *   desired = the smallest c >= 1 such that the c largest logits (ties to the

@@ -7,7 +7,7 @@
 // ExactTopPGraph (twilight_exact_top_p_graph.py:19-32, inline :1274-1310),
 // matched_budget_counts (:50-86) and the GPU GQA union (:1517-1614).
 //
-// Orders this build defines (the reference's are unpinned: cuBLAS / tl.sum
+// Orders defined here (the reference's are unpinned: cuBLAS / tl.sum
 // reductions, argsort ties, fp32 cumsum rounding):
 //   * logit = qk_scale * ((scale * dot) + (min * qsum)) with dot the exact
 //     integer sum of code * Q over q's fixed-point form Q (22 fraction bits
