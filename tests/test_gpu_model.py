@@ -209,7 +209,10 @@ def test_decode_step_ops_match_hf_modules(dev, dtype):
     assert torch.equal(kd.cpu().view(torch.int16), rk[0, :, 0].contiguous().view(torch.int16))
     assert torch.equal(q32.cpu(), rq[0, :, 0].float())
     # one-token GEMV (nn.Linear) against an fp32 matmul of the same operands
-    for N, Kd, with_bias in ((6144, 4096, True), (4096, 14336, False), (1000, 256, True)):
+    # (x held in registers as 2, 4 or 8 chunks a thread; past 16384 elements the
+    # rest staged after the weights' loads)
+    for N, Kd, with_bias in ((6144, 4096, True), (4096, 14336, False), (1000, 256, True), (300, 6000, True),
+                             (512, 20000, False)):
         W = (torch.randn((N, Kd), generator=g) * 0.02).to(dtype)
         xv = torch.randn((1, Kd), generator=g).to(dtype)
         b = torch.randn(N, generator=g).to(dtype) if with_bias else None
