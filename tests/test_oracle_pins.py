@@ -293,6 +293,50 @@ def test_top_p_count_closed_forms():
     assert oracle.top_p_threshold(3, 1.0) == 3
 
 
+def _fp32_top_p(logits: torch.Tensor, top_p: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """The reference's fp32 op sequence, restated with torch on the CPU
+    (twilight_offload_cache.py:1275-1309, twilight_exact_top_p_graph.py:19-32):
+    descending argsort, softmax of the sorted logits, one 1-D cumsum per head,
+    searchsorted(right=False) + 1 against top_p, clamped to the row."""
+    order = torch.argsort(logits, dim=-1, descending=True)
+    probs = torch.softmax(torch.gather(logits, -1, order), dim=-1)
+    cum = torch.stack([row.cumsum(dim=0) for row in probs.flatten(0, -2)]).view_as(probs)
+    thr = torch.full((*cum.shape[:-1], 1), top_p, dtype=cum.dtype)
+    desired = torch.searchsorted(cum.contiguous(), thr, right=False).squeeze(-1) + 1
+    return desired.clamp_max(logits.shape[-1]), order
+
+
+@pytest.mark.parametrize("N,spread,top_p", [(4096, 1.5, 0.95), (4096, 4.0, 0.95), (1024, 0.5, 0.9),
+                                            (4096, 2.5, 0.99), (256, 8.0, 0.95)])
+def test_top_p_count_against_reference_fp32_rule(N, spread, top_p):
+    """The exact integer-mass count against the reference's fp32 count on the
+    same logits.  They agree wherever fp32 rounding cannot decide; where they
+    differ, every cumulative probability between the two counts (float64) lies
+    within the fp32 rounding budget of top_p (N ulps at 1.0), and the kept
+    tokens are the same whenever the counts are."""
+    rows = 64
+    g = torch.Generator().manual_seed(N + int(10 * spread))
+    logits = torch.randn(rows, N, generator=g) * spread
+    logits[:, :N // 8] += 2.0 * spread * torch.rand(rows, N // 8, generator=g)  # a peaked head of the row
+    ref, order = _fp32_top_p(logits, top_p)
+    tol = N * 2.0 ** -24
+    agree = 0
+    for r in range(rows):
+        lg = logits[r].numpy()
+        d, _ = oracle.top_p_count(lg, top_p)
+        dr = int(ref[r])
+        if d == dr:
+            agree += 1
+            ours = sorted(range(N), key=lambda i: (-float(lg[i]), i))[:d]
+            assert set(ours) == set(order[r, :d].tolist())
+            continue
+        p64 = np.exp(lg.astype(np.float64) - float(lg.max()))
+        cum = np.cumsum(np.sort(p64)[::-1] / p64.sum())
+        for k in range(min(d, dr), max(d, dr)):
+            assert abs(cum[k - 1] - float(np.float32(top_p))) <= tol, (r, d, dr, k)
+    assert agree >= rows * 9 // 10, agree
+
+
 def _int4_qk_crafted(values: dict[int, int], q_of: dict[int, float], scale: float = 1.0,
                      minimum: float = 0.0, D: int = 64) -> float:
     """One candidate with codes `values` (others 0), fp32 scale/minimum, against q."""
