@@ -476,8 +476,8 @@ __global__ __launch_bounds__(512) void merge_kernel(AttnArgs a, int rows_per_blo
   using S = typename DT::storage;
   const int R = a.R;
   const int D = a.D;
-  const int g = blockIdx.x / R;
-  const int r = blockIdx.x - g * R;
+  const int g = static_cast<int>(blockIdx.x) % a.G;  // group-minor, as the split-K blocks
+  const int r = static_cast<int>(blockIdx.x) / a.G;
   const GroupRows gr = group_rows<MODE>(a, g, D);
   const int n_chunks = (gr.n_rows + rows_per_block - 1) / rows_per_block;
   if (n_chunks <= 1) return;
@@ -536,10 +536,11 @@ __global__ __launch_bounds__(kBlock) void merge_vec_kernel(AttnArgs a, int rows_
   constexpr int NL = kBlock / NQ;                  // chunk lanes
   constexpr int MAXJ = (kMaxChunks + NL - 1) / NL; // chunks per lane
   const int R = a.R;
-  const int gr = blockIdx.x / CS;
-  const int c0 = (blockIdx.x - gr * CS) * (D / CS);  // first channel of the slice
-  const int g = gr / R;
-  const int r = gr - g * R;
+  // group-minor like the split-K kernels' blocks: group g on XCD g % 8
+  const int g = static_cast<int>(blockIdx.x) % a.G;
+  const int hs = static_cast<int>(blockIdx.x) / a.G;  // (head, slice)
+  const int r = hs / CS;
+  const int c0 = (hs - r * CS) * (D / CS);  // first channel of the slice
   const int t = threadIdx.x;
   const int q = t % NQ;
   const int cl = t / NQ;
@@ -665,8 +666,8 @@ __global__ __launch_bounds__(kBlock, RMAX >= 8 ? 2 : 3) void decode_attn_kernel(
   static_assert(RW <= kWave, "one index lane per row");
 
   const int R = a.R;
-  const int g = blockIdx.x / a.max_chunks;
-  const int chunk = blockIdx.x - g * a.max_chunks;
+  const int g = static_cast<int>(blockIdx.x) % a.G;  // chunk-major (group g on XCD g % 8)
+  const int chunk = static_cast<int>(blockIdx.x) / a.G;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
   const int rig = lane / LPR;
@@ -981,8 +982,8 @@ __global__ __launch_bounds__(kBlock, 2) void decode_attn_mfma(AttnArgs a) {
   static_assert(RMAX <= 8, "at most 8 heads per group");
 
   const int R = a.R;
-  const int g = blockIdx.x / a.max_chunks;
-  const int chunk = blockIdx.x - g * a.max_chunks;
+  const int g = static_cast<int>(blockIdx.x) % a.G;  // chunk-major (group g on XCD g % 8)
+  const int chunk = static_cast<int>(blockIdx.x) / a.G;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
   const int krow = lane & 15;                // q.k: row of the tile / head of A
@@ -1337,8 +1338,12 @@ __global__ __launch_bounds__(NW * kWave, 2) void decode_attn_tiles(AttnArgs a) {
   static_assert(RMAX == 4 || RMAX == 8, "4 or 8 head slots");
 
   const int R = a.R;
-  const int g = blockIdx.x / a.max_chunks;
-  const int chunk = blockIdx.x - g * a.max_chunks;
+  // chunk-major: workgroups go to the XCDs round-robin, so with G a multiple
+  // of 8 every chunk of group g runs on XCD g % 8, where the group's
+  // selection blocks wrote its bitmaps and its merge blocks read the partials
+  // back, both through that XCD's L2
+  const int g = static_cast<int>(blockIdx.x) % a.G;
+  const int chunk = static_cast<int>(blockIdx.x) / a.G;
   const int wave = wave_uniform(static_cast<int>(threadIdx.x) / kWave);
   const int lane = lane_id();
   const int krow = lane & 15;
@@ -1817,8 +1822,8 @@ __global__ __launch_bounds__(kBlock) void decode_attn_generic(AttnArgs a) {
   constexpr int JMAX = 8;  // D <= 512
   const int R = a.R;
   const int D = a.D;
-  const int g = blockIdx.x / a.max_chunks;
-  const int chunk = blockIdx.x - g * a.max_chunks;
+  const int g = static_cast<int>(blockIdx.x) % a.G;  // chunk-major (group g on XCD g % 8)
+  const int chunk = static_cast<int>(blockIdx.x) / a.G;
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int lane = lane_id();
   __shared__ float s_m[kWaves * RMAX];

@@ -421,9 +421,10 @@ __device__ void score_tile(const ScoreArgs& a, int g, int tile, uint8_t* lds) {
 template <typename DT, int DFIX>
 __global__ __launch_bounds__(kScoreBlock) void quest_score_kernel(ScoreArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
-  const int tiles = (a.P + kTilePages - 1) / kTilePages;
-  const int g = blockIdx.x / tiles;
-  score_tile<DT, DFIX>(a, g, blockIdx.x - g * tiles, lds);
+  // group-minor: workgroups go to the XCDs round-robin, so with G a multiple
+  // of 8 group g's blocks of every launch of the layer share XCD g % 8 (and
+  // its L2)
+  score_tile<DT, DFIX>(a, static_cast<int>(blockIdx.x) % a.G, static_cast<int>(blockIdx.x) / a.G, lds);
 }
 
 // --------------------------------------------------------------- selection
@@ -713,8 +714,8 @@ template <int KPT, bool VEC, int NT>
 __global__ __launch_bounds__(NT) void quest_select_kernel(SelectArgs s) {
   __shared__ __align__(16) SelSharedT<NT> sh;
   extern __shared__ __align__(16) uint8_t dyn[];  // union scratch
-  const int row = blockIdx.x;
-  const int g = row / s.R;
+  const int g = static_cast<int>(blockIdx.x) % s.G;  // group-minor (XCD g % 8)
+  const int row = g * s.R + static_cast<int>(blockIdx.x) / s.G;
   // the fast top-k's histogram is cleared before the first load goes out, so
   // its barrier does not wait for the loads
   const bool fast = s.tile_mm != nullptr && s.map == nullptr;

@@ -1895,9 +1895,10 @@ __global__ __launch_bounds__(kSqThreads) void twilight_score_qk_kernel(ScoreQkAr
   __shared__ int s_qshift[RMAX];
   __shared__ float s_qsum[RMAX];
   __shared__ int s_qok[RMAX];
+  // group-minor: group g's blocks of every launch of the layer on XCD g % 8
   const int tiles = (a.P + kSqTile - 1) / kSqTile;
-  const int g = blockIdx.x / tiles;
-  const int tile = blockIdx.x - g * tiles;
+  const int g = static_cast<int>(blockIdx.x) % a.G;
+  const int tile = static_cast<int>(blockIdx.x) / a.G;
   const int p0 = tile * kSqTile;
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
@@ -2150,8 +2151,8 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_topp_head_kernel(HeadAr
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
   const int wave = tid / kWave;
-  const int row = blockIdx.x;
-  const int g = row / a.R;
+  const int g = static_cast<int>(blockIdx.x) % a.G;  // group-minor (XCD g % 8)
+  const int row = g * a.R + static_cast<int>(blockIdx.x) / a.G;
   topk_fast_clear(sh.sel);
   __syncthreads();
   // ---- round trip 1: length, the row's keys and tile ranges ----
@@ -2357,9 +2358,9 @@ __global__ __launch_bounds__(kHeadThreads) void twilight_matched_rec_kernel(Matc
   __shared__ int s_k;
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = lane_id();
-  const int row = blockIdx.x;
-  const int g = row / a.R;
-  const int r = row - g * a.R;
+  const int g = static_cast<int>(blockIdx.x) % a.G;  // group-minor (XCD g % 8)
+  const int r = static_cast<int>(blockIdx.x) / a.G;
+  const int row = g * a.R + r;
   int N = a.b0 * BS;
   int target = a.target_total;
   if (a.lengths != nullptr) {
