@@ -1973,12 +1973,14 @@ void plan_chunks(int dtype, int G, int R, int D, int max_rows_total, int* iters,
   *chunks = ch < 1 ? 1 : ch;
 }
 
-// Page-tile kernel shape: waves per block and tiles per wavefront batch.
+// Page-tile kernel shape: waves per block and tiles per wavefront batch (one
+// tile a wavefront: with a group's blocks on one XCD, twice the blocks of
+// half the rows balance its CUs better than two tiles a wavefront)
 #ifndef TW_TILE_NW
 #define TW_TILE_NW 4
 #endif
 #ifndef TW_TILE_TW
-#define TW_TILE_TW 2
+#define TW_TILE_TW 1
 #endif
 // blocks per (group, head) of the split-K merge at D = 128, each over
 // D / TW_MERGE_CS channels (4: the page-tile merge 4.0 -> 3.45 us at 32K, each
